@@ -1,0 +1,282 @@
+/*
+ * lgbm_hip.h — C-ABI of the MI355X (gfx950) GBDT tree-learner hot path.
+ *
+ * The library replaces the device half of the reference's compute seam,
+ * `trait Backend` (crates/lgbm-compute/src/lib.rs:1092-2782), for the numeric
+ * leaf-wise learner spine: the quantized gradient discretizer, the resident bin
+ * layout, ConstructHistogram, FixHistogram + compaction, the subtraction trick,
+ * FindBestThreshold, the cross-leaf ArgMax and DataPartition.  Every entry point
+ * below names the reference interface it replaces.
+ *
+ * Conventions
+ *  - All functions return an int status: LGBM_HIP_OK (0) or a negative code that
+ *    mirrors `ComputeError` (crates/lgbm-compute/src/error.rs).  A message with the
+ *    details is available from lgbm_hip_last_error().  Nothing aborts across the ABI.
+ *  - Host pointers are borrowed for the duration of the call only.  Outputs are
+ *    caller-allocated; capacities are implied by the documented sizes.
+ *  - A context owns every device allocation (bins, gradients, quantized gradients,
+ *    row permutation buffers, histogram slots, tree buffers).  A context is not
+ *    thread-safe (the reference backend is `!Sync`, lib.rs:3840-3846); all calls
+ *    on one context are synchronous at the API boundary.
+ *  - Histogram cells use the reference layout: feature f occupies
+ *    [slot_off[f], slot_off[f] + 2*num_bin[f]) of a leaf slot, grad at 2*bin,
+ *    hess at 2*bin+1 (crates/lgbm-compute/src/kernels/histogram.rs:64-68,
+ *    crates/lgbm-treelearner/src/learner.rs:4438-4446).
+ */
+#ifndef LGBM_HIP_H
+#define LGBM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (crates/lgbm-compute/src/error.rs) ---------------------- */
+#define LGBM_HIP_OK 0
+#define LGBM_HIP_ERR_LENGTH_MISMATCH (-1)       /* ComputeError::LengthMismatch      */
+#define LGBM_HIP_ERR_BIN_OUT_OF_RANGE (-2)      /* ComputeError::BinIndexOutOfRange  */
+#define LGBM_HIP_ERR_CAPABILITY (-3)            /* ComputeError::CapabilityUnavailable */
+#define LGBM_HIP_ERR_RUNTIME (-4)               /* ComputeError::Runtime             */
+#define LGBM_HIP_ERR_HIP (-5)                   /* a HIP runtime call failed          */
+#define LGBM_HIP_ERR_INVALID_ARGUMENT (-6)      /* null pointer / bad size            */
+#define LGBM_HIP_ERR_INVALID_LEAF_HESSIAN (-7)  /* TreeLearnerError::InvalidLeafHessian */
+
+/* MissingType (crates/lgbm-dataset/src/bin_mapper.rs; Tree decision_type bits 2-3) */
+#define LGBM_MISSING_NONE 0
+#define LGBM_MISSING_ZERO 1
+#define LGBM_MISSING_NAN 2
+
+/* `GainConfig` (crates/lgbm-compute/src/gain.rs:904-960), field for field. */
+typedef struct lgbm_gain_config {
+  int32_t min_data_in_leaf;
+  int32_t _pad0;
+  double min_sum_hessian_in_leaf;
+  double max_delta_step;
+  double lambda_l1;
+  double lambda_l2;
+  double min_gain_to_split;
+  double path_smooth;
+  double parent_output;
+  int32_t min_data_per_group;
+  int32_t max_cat_threshold;
+  double cat_l2;
+  double cat_smooth;
+  int32_t max_cat_to_onehot;
+  int32_t _pad1;
+} lgbm_gain_config;
+
+/* `SplitInfo` (crates/lgbm-compute/src/gain.rs:1019-1053).  gain == -inf is the
+ * "no split" sentinel (`SplitInfo::none`, gain.rs:1068-1084). */
+typedef struct lgbm_split_info {
+  uint32_t threshold;
+  int32_t left_count;
+  int32_t right_count;
+  int32_t default_left; /* bool */
+  double gain;
+  double left_sum_gradient;
+  double left_sum_hessian;
+  double right_sum_gradient;
+  double right_sum_hessian;
+  double left_output;
+  double right_output;
+} lgbm_split_info;
+
+/* `BatchedSplitFeature` (crates/lgbm-compute/src/kernels/split.rs:77-95). */
+typedef struct lgbm_batched_feature {
+  uint64_t slot_off;
+  uint32_t num_bin;
+  int32_t offset;
+  uint32_t default_bin;
+  uint32_t most_freq_bin;
+  int32_t skip_default_bin; /* bool */
+  int32_t na_as_missing;    /* bool */
+  int32_t run_forward;      /* bool */
+  int32_t _pad;
+} lgbm_batched_feature;
+
+/* The numeric `FeatureColumn` descriptors (crates/lgbm-treelearner/src/
+ * learner.rs:87-204) minus the bins themselves; `bin_upper_bound` values are
+ * passed as one concatenated array (feature f at sum_{f'<f} num_bin[f']). */
+typedef struct lgbm_feature_meta {
+  uint32_t num_bin;
+  int32_t offset; /* offset_for_most_freq_bin(most_freq_bin) (lgbm-treelearner/src/lib.rs:89-95) */
+  uint32_t min_bin;
+  uint32_t max_bin;
+  uint32_t default_bin;
+  uint32_t most_freq_bin;
+  int32_t missing_type; /* LGBM_MISSING_* */
+  int32_t real_feature_index;
+} lgbm_feature_meta;
+
+/* A grown tree (crates/lgbm-model/src/tree.rs: Tree fields written by
+ * `Tree::split`, tree.rs:614-700).  Caller-allocated arrays; capacities:
+ * node arrays num_leaves_cap-1, leaf arrays num_leaves_cap. */
+typedef struct lgbm_tree_out {
+  int32_t num_leaves; /* out */
+  int32_t _pad;
+  int32_t* split_feature;      /* real feature index per internal node */
+  uint32_t* threshold_in_bin;
+  double* threshold;           /* bin_upper_bound[threshold_in_bin] */
+  float* split_gain;           /* f32(gain + min_gain_to_split), learner.rs:3985 */
+  int8_t* decision_type;
+  int32_t* left_child;
+  int32_t* right_child;
+  double* internal_value;
+  int32_t* internal_count;
+  double* leaf_value;
+  double* leaf_weight;
+  int32_t* leaf_count;
+  int32_t* leaf_depth;
+  int32_t* leaf_parent;
+} lgbm_tree_out;
+
+/* `LeafPartitionLayout` (crates/lgbm-dataset/src/dataset.rs:88-97): the data
+ * partition a tree was grown over.  indices has num_data entries, leaf arrays
+ * num_leaves_cap entries. */
+typedef struct lgbm_layout_out {
+  uint32_t* indices;
+  int32_t* leaf_begin;
+  int32_t* leaf_count;
+} lgbm_layout_out;
+
+/* Leaf totals handed to a per-leaf op (`LeafSplits`, lgbm-treelearner/src/
+ * leaf_splits.rs:36-52). */
+typedef struct lgbm_leaf_sums {
+  double sum_gradient;
+  double sum_hessian;
+  int32_t num_data;
+  int32_t _pad;
+  double weight; /* parent_output for path smoothing */
+} lgbm_leaf_sums;
+
+typedef struct lgbm_hip_ctx lgbm_hip_ctx;
+
+/* ---- context ---------------------------------------------------------------- */
+
+/* Create a context on HIP device `device`.  Replaces constructing `GpuBackend`
+ * with its resident caches (lib.rs:3848-3934; dispatch arm
+ * crates/lgbm/src/booster.rs:1922-1932). */
+int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out);
+int lgbm_hip_ctx_destroy(lgbm_hip_ctx* ctx);
+/* Copy the last error message of `ctx` (or of the last failed create when ctx is
+ * NULL) into buf; always NUL-terminates when size > 0. */
+int lgbm_hip_last_error(const lgbm_hip_ctx* ctx, char* buf, size_t size);
+
+/* ---- resident data (lgbm-compute/src/lib.rs:1564-1620) ---------------------- */
+
+/* Upload the binned columns once per train.  Replaces
+ * `Backend::upload_resident_bins(&[&BinColumn])` (lib.rs:1564; GPU impl
+ * lib.rs:4368-4433) and `resident_bin_width` (lib.rs:3752).  `bins` is
+ * feature-major u8 ([f*num_data + row]); every bin must be < num_bin[f] (the
+ * once-per-train bin-range gate, learner.rs:1161-1187): a violation returns
+ * LGBM_HIP_ERR_BIN_OUT_OF_RANGE.  `bin_upper_bound` holds sum(num_bin) doubles
+ * (may be NULL: thresholds then record the bin index). */
+int lgbm_hip_upload_bins(lgbm_hip_ctx* ctx, const uint8_t* bins, int32_t num_features,
+                         int64_t num_data, const lgbm_feature_meta* meta,
+                         const double* bin_upper_bound);
+
+/* Upload per-row f32 gradients/hessians (`Backend::upload_resident_grad_hess`,
+ * lib.rs:1607).  n must equal the uploaded num_data. */
+int lgbm_hip_set_gradients(lgbm_hip_ctx* ctx, const float* grad, const float* hess, int64_t n);
+
+/* Quantize the resident gradients in place for `use_quantized_grad`:
+ * `GradientDiscretizer::discretize_dequantize_in_place` + the call site
+ * `quantize_grad_hess_in_place` (lgbm-treelearner/src/gradient_discretizer.rs:
+ * 126-188, lgbm-boosting/src/gbdt.rs:43-62).  `stochastic` selects xorshift64
+ * stochastic rounding seeded with `seed` (gbdt.rs:950 derives it per (iter,class)).
+ * Writes the packed int8 (grad, hess) pairs the histogram kernels consume and,
+ * when the out pointers are non-NULL, the dequantized f32 values and the scales
+ * {grad_scale, hess_scale}. */
+int lgbm_hip_quantize(lgbm_hip_ctx* ctx, int32_t num_grad_quant_bins, int32_t stochastic,
+                      uint64_t seed, float* dequant_grad_out, float* dequant_hess_out,
+                      double* scales_out);
+
+/* Read back the packed discretized buffer in the reference `discretize` layout:
+ * out[2*i] = hessian, out[2*i+1] = gradient (gradient_discretizer.rs:25-26,104-118). */
+int lgbm_hip_get_discretized(lgbm_hip_ctx* ctx, int8_t* out, int64_t n);
+
+/* ---- per-op seam (parity tests / fine-grained driver) ----------------------- */
+
+/* Exact integer histogram of the quantized gradients over `leaf_rows` (or all rows
+ * when leaf_rows is NULL): out[slot cell] as int64, [g0,h0,g1,h1,...] per feature.
+ * Replaces `construct_int_histogram` (gradient_discretizer.rs:235-250) per feature. */
+int lgbm_hip_build_int_histogram(lgbm_hip_ctx* ctx, const uint32_t* leaf_rows, int64_t n_rows,
+                                 int64_t* out);
+
+/* Build one leaf's f64 histogram from the quantized gradients, then FixHistogram
+ * on the RAW leaf sums and compaction: the device analog of
+ * `build_leaf_histogram_into` (learner.rs:2464-2566) =
+ * `Backend::build_resident_leaf` (lib.rs:1953-1972).  out has slot_len doubles.
+ * Requires a prior lgbm_hip_quantize. */
+int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* ctx, const uint32_t* leaf_rows, int64_t n_rows,
+                                  double sum_gradient, double sum_hessian, double* out);
+
+/* FindBestThreshold over a batch of features of one leaf histogram:
+ * `Backend::find_best_splits_batched` (lib.rs:1500-1548) whose per-feature body is
+ * `find_best_split_cpu_native` (kernels/split.rs:8970-9329).  `hist` is host
+ * memory of `hist_len` doubles; out has n_feats entries. */
+int lgbm_hip_find_best_splits(lgbm_hip_ctx* ctx, const double* hist, int64_t hist_len,
+                              const lgbm_batched_feature* feats, int32_t n_feats,
+                              const lgbm_gain_config* cfg, double sum_gradient,
+                              double sum_hessian, int32_t num_data, lgbm_split_info* out);
+
+/* Elementwise larger = parent - smaller (`Backend::subtract_histograms`,
+ * lib.rs:1314; kernels/subtract.rs:204-215). */
+int lgbm_hip_subtract_histograms(lgbm_hip_ctx* ctx, const double* parent, const double* child,
+                                 int64_t len, double* out);
+
+/* Stable DataPartition of `n` rows: returns the reordered local positions
+ * [left ascending | right ascending] and the left count.  Router of
+ * `DataPartition::split` / `split_fused_host_impl`
+ * (lgbm-treelearner/src/data_partition.rs:192-288,360-463) and
+ * `data_partition_cpu_native` (kernels/partition.rs:115). */
+int lgbm_hip_data_partition(lgbm_hip_ctx* ctx, const uint32_t* bins, int64_t n, uint32_t num_bin,
+                            uint32_t min_bin, uint32_t max_bin, uint32_t threshold,
+                            uint32_t most_freq_bin, int32_t na_as_missing, int32_t default_left,
+                            uint32_t* order_out, int64_t* left_count_out);
+
+/* ---- coarse seam: one whole tree per call ----------------------------------- */
+
+/* Grow one tree on device from the resident bins and the CURRENT quantized
+ * gradients: `Backend::grow_tree_on_device_with_cfg` (lib.rs:2688,2771;
+ * kernels/grow_driver.rs:1219), following the CPU learner `train_inner`
+ * (learner.rs:980-1562) decision for decision.  Quantized (integer-exact) path
+ * only: call lgbm_hip_quantize first.  `tree` arrays need num_leaves capacity;
+ * `layout` may be NULL (else indices has num_data entries). */
+int lgbm_hip_grow_tree(lgbm_hip_ctx* ctx, const lgbm_gain_config* cfg, int32_t num_leaves,
+                       int32_t max_depth, lgbm_tree_out* tree, lgbm_layout_out* layout);
+
+/* ---- boosting loop on device (binary objective) ----------------------------- */
+
+/* Upload f32 labels and reset the resident f64 score to `init_score`
+ * (`ScoreUpdater::new` + `add_constant`, lgbm-boosting/src/score_updater.rs:63-99). */
+int lgbm_hip_set_labels(lgbm_hip_ctx* ctx, const float* labels, int64_t n, double init_score);
+
+/* One binary-logloss boosting iteration with quantized gradients, all resident:
+ * `BinaryLogloss::get_gradients` (lgbm-objective/src/binary.rs:134-172) ->
+ * quantize (gbdt.rs:945-960, seed ((iter<<20) ^ 0x51702010)) -> grow tree ->
+ * `Tree::shrinkage` (tree.rs:1074) -> score update (score_updater.rs:133).
+ * `tree` (may be NULL) receives the shrunk tree. */
+int lgbm_hip_train_iter_binary(lgbm_hip_ctx* ctx, int32_t iter, const lgbm_gain_config* cfg,
+                               int32_t num_leaves, int32_t max_depth, double learning_rate,
+                               int32_t num_grad_quant_bins, int32_t stochastic,
+                               lgbm_tree_out* tree);
+
+/* Copy the resident f64 training score back to the host. */
+int lgbm_hip_get_scores(lgbm_hip_ctx* ctx, double* out, int64_t n);
+
+/* Per-kernel device time (ms, HIP events on the context stream) accumulated since
+ * the last reset, by kernel family: [0] histogram, [1] partition, [2] split scan,
+ * [3] quantize, [4] objective+score.  Also returns the algorithmic histogram bytes
+ * and launch count.  Enabling timing adds event records per launch. */
+int lgbm_hip_set_timing(lgbm_hip_ctx* ctx, int32_t enable);
+int lgbm_hip_get_timing(lgbm_hip_ctx* ctx, double* ms_out5, double* hist_bytes_out,
+                        int64_t* hist_launches_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LGBM_HIP_H */

@@ -1,0 +1,1237 @@
+// lgbm_oracle.cpp — CPU restatement of the reference learner spine.
+//
+// TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP path
+// and the timed CPU baseline in bench.py.  Only tests/, __graft_entry__.smoke()
+// and bench.py's cpu_baseline leg may load it; the product (lightgbm_rs_amd/)
+// never does.
+//
+// It restates, function by function, the reference CPU path of
+// BectorVoom/lightgbm_rs (paths relative to crates/):
+//   histogram fold      lgbm-compute/src/kernels/histogram.rs:207-233,
+//                       lgbm-compute/src/lib.rs:223-246,262-390,1422-1469
+//   discretizer         lgbm-treelearner/src/gradient_discretizer.rs:55-263
+//   quantize call site  lgbm-boosting/src/gbdt.rs:43-62,945-960
+//   FixHistogram        lgbm-treelearner/src/fix_histogram.rs:50-80
+//   compaction          lgbm-treelearner/src/learner.rs:4460-4492
+//   subtract            lgbm-compute/src/kernels/subtract.rs:204-215
+//   gain math           lgbm-compute/src/gain.rs:107-655
+//   FindBestThreshold   lgbm-compute/src/kernels/split.rs:8970-9329
+//   split_gt / arg_max  lgbm-treelearner/src/split_info.rs:28-35, learner.rs:4537
+//   DataPartition       lgbm-treelearner/src/data_partition.rs:99-288,360-463
+//   LeafSplits          lgbm-treelearner/src/leaf_splits.rs:75-173
+//   learner loop        lgbm-treelearner/src/learner.rs:980-2453,2708-3355,3895-4092
+//   Tree::split         lgbm-model/src/tree.rs:614-700, shrinkage :1074, add_bias :1161
+//   binary objective    lgbm-objective/src/binary.rs:134-220
+//   boosting loop       lgbm-boosting/src/gbdt.rs:612-640,691-1300 (binary spine)
+//
+// Numeric conventions follow the Rust source: no FP contraction anywhere (build
+// with -ffp-contract=off) except the explicit fma in GetLeafGainGivenOutput
+// (gain.rs:204-220); `as i8` / `as i32` casts saturate with NaN -> 0; f64::max is
+// NaN-ignoring (fmax).
+//
+// Parallelism (OpenMP) mirrors the reference CpuBackend's structure and is
+// bit-identical to the serial order: feature-group parallel histogram folds
+// (lib.rs:681-704), feature-parallel scans (lib.rs:728-748) and a block-parallel
+// two-buffer partition (data_partition.rs:489-615).
+
+#include "../include/lgbm_hip.h"
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <string>
+#include <vector>
+#include <algorithm>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+namespace {
+
+const double kEps = (double)1e-15f;  // K_EPSILON (lgbm-core/src/types.rs:31) widened
+const double kMinScore = -std::numeric_limits<double>::infinity();
+const double kZeroThreshold = (double)1e-35f;  // tree.rs MaybeRoundToZero
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+// Rust `f64 as i8` (saturating, NaN -> 0).
+inline int8_t sat_i8(double x) {
+  if (std::isnan(x)) return 0;
+  if (x >= 127.0) return 127;
+  if (x <= -128.0) return -128;
+  return (int8_t)(int)std::trunc(x);
+}
+// Rust `f64 as i32` (saturating, NaN -> 0).
+inline int32_t sat_i32(double x) {
+  if (std::isnan(x)) return 0;
+  if (x >= 2147483647.0) return 2147483647;
+  if (x <= -2147483648.0) return (int32_t)(-2147483647 - 1);
+  return (int32_t)std::trunc(x);
+}
+// `Common::RoundInt` as the reference writes it (split.rs:9069).
+inline int32_t round_int(double x) { return sat_i32(x + (double)0.5f); }
+
+inline double maybe_round_to_zero(double v) {
+  return (v >= -kZeroThreshold && v <= kZeroThreshold) ? 0.0 : v;
+}
+
+// ---------------------------------------------------------------------------
+// gain.rs
+// ---------------------------------------------------------------------------
+// threshold_l1 (gain.rs:107-116): Sign(s) * max(0, |s| - l1), Sign(0) == 0.
+inline double threshold_l1(double s, double l1) {
+  double reg = std::fmax(0.0, std::fabs(s) - l1);
+  double pos = s > 0.0 ? 1.0 : 0.0;
+  double neg = s < 0.0 ? 1.0 : 0.0;
+  return (pos - neg) * reg;
+}
+// get_leaf_gain (gain.rs:132-139)
+inline double get_leaf_gain(bool use_l1, double g, double h, double l1, double l2) {
+  if (use_l1) {
+    double s = threshold_l1(g, l1);
+    return (s * s) / (h + l2);
+  }
+  return (g * g) / (h + l2);
+}
+// get_split_gains (gain.rs:149-161)
+inline double get_split_gains(bool use_l1, double lg, double lh, double rg, double rh, double l1,
+                              double l2) {
+  return get_leaf_gain(use_l1, lg, lh, l1, l2) + get_leaf_gain(use_l1, rg, rh, l1, l2);
+}
+// get_leaf_gain_given_output (gain.rs:204-220): the fused multiply-add is part of the
+// reference arithmetic.
+inline double get_leaf_gain_given_output(bool use_l1, double g, double h, double l1, double l2,
+                                         double out) {
+  double gg = use_l1 ? threshold_l1(g, l1) : g;
+  return -std::fma(2.0 * gg, out, (h + l2) * out * out);
+}
+// calculate_splitted_leaf_output (gain.rs:232-249)
+inline double calc_leaf_output(bool use_l1, double g, double h, double l1, double l2) {
+  if (use_l1) return -threshold_l1(g, l1) / (h + l2);
+  return -g / (h + l2);
+}
+// calculate_splitted_leaf_output_full (gain.rs:494-535)
+inline double calc_leaf_output_full(bool use_l1, double g, double h, double l1, double l2,
+                                    double max_delta_step, bool use_smoothing, double path_smooth,
+                                    int32_t num_data, double parent_output) {
+  double base = calc_leaf_output(use_l1, g, h, l1, l2);
+  bool clamp = max_delta_step > 0.0 && std::fabs(base) > max_delta_step;
+  double pos = base > 0.0 ? 1.0 : 0.0;
+  double neg = base < 0.0 ? 1.0 : 0.0;
+  double clamped = clamp ? (pos - neg) * max_delta_step : base;
+  if (use_smoothing) {
+    double n_over_ps = (double)num_data / path_smooth;
+    return clamped * n_over_ps / (n_over_ps + 1.0) + parent_output / (n_over_ps + 1.0);
+  }
+  return clamped;
+}
+// get_leaf_gain_full (gain.rs:556-593)
+inline double get_leaf_gain_full(bool use_l1, double g, double h, double l1, double l2,
+                                 double max_delta_step, bool use_smoothing, double path_smooth,
+                                 int32_t num_data, double parent_output) {
+  if (max_delta_step > 0.0 || use_smoothing) {
+    double out = calc_leaf_output_full(use_l1, g, h, l1, l2, max_delta_step, use_smoothing,
+                                       path_smooth, num_data, parent_output);
+    return get_leaf_gain_given_output(use_l1, g, h, l1, l2, out);
+  }
+  return get_leaf_gain(use_l1, g, h, l1, l2);
+}
+// get_split_gains_full (gain.rs:604-655)
+inline double get_split_gains_full(bool use_l1, double lg, double lh, double rg, double rh,
+                                   double l1, double l2, double mds, bool sm, double ps,
+                                   int32_t lc, int32_t rc, double po) {
+  return get_leaf_gain_full(use_l1, lg, lh, l1, l2, mds, sm, ps, lc, po) +
+         get_leaf_gain_full(use_l1, rg, rh, l1, l2, mds, sm, ps, rc, po);
+}
+
+inline bool cfg_use_l1(const lgbm_gain_config& c) { return c.lambda_l1 > 0.0; }
+inline bool cfg_use_smoothing(const lgbm_gain_config& c) { return c.path_smooth > kEps; }
+
+lgbm_split_info split_none() {
+  lgbm_split_info s;
+  std::memset(&s, 0, sizeof(s));
+  s.gain = kMinScore;
+  s.default_left = 1;
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// find_best_split_cpu_native (kernels/split.rs:8970-9329)
+// ---------------------------------------------------------------------------
+int find_best_split(const double* hist, size_t hist_len, const lgbm_gain_config& cfg,
+                    uint32_t num_bin, int32_t offset, uint32_t default_bin,
+                    bool skip_default_bin, bool na_as_missing, bool run_forward,
+                    double sum_gradient, double sum_hessian, int32_t num_data,
+                    lgbm_split_info* out) {
+  if (num_bin == 0) return fail(LGBM_HIP_ERR_RUNTIME, "find_best_split: num_bin must be > 0");
+  if (hist_len != 2ull * num_bin) return fail(LGBM_HIP_ERR_LENGTH_MISMATCH, "hist length");
+  if (!(sum_hessian > 0.0))
+    return fail(LGBM_HIP_ERR_RUNTIME, "find_best_split: sum_hessian must be > 0");
+  const double two_eps = 2.0 * kEps;
+  const double sum_hessian_bumped = sum_hessian + two_eps;
+  const bool use_l1 = cfg_use_l1(cfg);
+  const bool use_smoothing = cfg_use_smoothing(cfg);
+  const double mds = cfg.max_delta_step;
+  const double po = cfg.parent_output;
+  const bool use_full = use_smoothing || mds > 0.0;
+  const double gain_shift =
+      get_leaf_gain_full(use_l1, sum_gradient, sum_hessian_bumped, cfg.lambda_l1, cfg.lambda_l2,
+                         mds, use_smoothing, cfg.path_smooth, num_data, po);
+  const double min_gain_shift = gain_shift + cfg.min_gain_to_split;
+  const int32_t nb = (int32_t)num_bin;
+  const int32_t rev_count = std::max(nb - 1 - (na_as_missing ? 1 : 0), 0);
+  const bool na_preamble = na_as_missing && offset == 1;
+  int32_t fwd_count = 0;
+  if (run_forward) {
+    int32_t base = std::max(nb - 1 - offset, 0);
+    fwd_count = na_preamble ? base + 1 : base;
+  }
+  const double l1 = cfg.lambda_l1, l2 = cfg.lambda_l2;
+  const double cnt_factor = (double)num_data / sum_hessian_bumped;
+  const double min_h = cfg.min_sum_hessian_in_leaf;
+  const int32_t min_d = cfg.min_data_in_leaf;
+
+  double best_lg = 0.0, best_lh = 0.0, best_gain = kMinScore;
+  int32_t best_lc = 0, best_thr = 0;
+  bool is_splittable = false, best_dl = true;
+
+  auto gain_of = [&](double lg, double lh, double rg, double rh, int32_t lc, int32_t rc) {
+    if (use_full)
+      return get_split_gains_full(use_l1, lg, lh, rg, rh, l1, l2, mds, use_smoothing,
+                                  cfg.path_smooth, lc, rc, po);
+    return get_split_gains(use_l1, lg, lh, rg, rh, l1, l2);
+  };
+
+  {  // REVERSE
+    double srg = 0.0, srh = kEps;
+    int32_t rc = 0;
+    const int32_t t_start = nb - 1 - offset - (na_as_missing ? 1 : 0);
+    bool done = false;
+    for (int32_t k = 0; k < rev_count; ++k) {
+      if (done) break;
+      const int32_t t = t_start - k;
+      const bool in_range = t >= (1 - offset);
+      const bool skip = skip_default_bin && (t + offset) == (int32_t)default_bin;
+      const bool active = in_range && !skip && !done;
+      if (active) {
+        double hg = hist[(size_t)t * 2], hh = hist[(size_t)t * 2 + 1];
+        srg += hg;
+        srh += hh;
+        rc += round_int(hh * cnt_factor);
+      }
+      const int32_t lc = num_data - rc;
+      const double slh = sum_hessian_bumped - srh;
+      const double slg = sum_gradient - srg;
+      const bool cont = rc < min_d || srh < min_h;
+      const bool brk = lc < min_d || slh < min_h;
+      done = done || (active && !cont && brk);
+      if (active && !cont && !done) {
+        double g = gain_of(slg, slh, srg, srh, lc, rc);
+        if (g > min_gain_shift) {
+          is_splittable = true;
+          if (g > best_gain) {
+            best_lc = lc;
+            best_lg = slg;
+            best_lh = slh;
+            best_thr = t - 1 + offset;
+            best_gain = g;
+            best_dl = true;
+          }
+        }
+      }
+    }
+  }
+  {  // FORWARD
+    double slg = 0.0, slh = kEps;
+    int32_t lc = 0;
+    int32_t fwd_start = 0;
+    if (na_preamble) {
+      slg = sum_gradient;
+      slh = sum_hessian_bumped - kEps;
+      lc = num_data;
+      for (int32_t i = 0; i < nb - offset; ++i) {
+        slg -= hist[(size_t)i * 2];
+        slh -= hist[(size_t)i * 2 + 1];
+        lc -= round_int(hist[(size_t)i * 2 + 1] * cnt_factor);
+      }
+      fwd_start = -1;
+    }
+    bool done = false;
+    for (int32_t k = 0; k < fwd_count; ++k) {
+      if (done) break;
+      const int32_t t = fwd_start + k;
+      const bool skip = skip_default_bin && (t + offset) == (int32_t)default_bin;
+      const bool active = !skip && !done;
+      if (active && t >= 0) {
+        double hg = hist[(size_t)t * 2], hh = hist[(size_t)t * 2 + 1];
+        slg += hg;
+        slh += hh;
+        lc += round_int(hh * cnt_factor);
+      }
+      const int32_t rc = num_data - lc;
+      const double srh = sum_hessian_bumped - slh;
+      const double srg = sum_gradient - slg;
+      const bool cont = lc < min_d || slh < min_h;
+      const bool brk = rc < min_d || srh < min_h;
+      done = done || (active && !cont && brk);
+      if (active && !cont && !done) {
+        double g = gain_of(slg, slh, srg, srh, lc, rc);
+        if (g > min_gain_shift) {
+          is_splittable = true;
+          if (g > best_gain) {
+            best_lc = lc;
+            best_lg = slg;
+            best_lh = slh;
+            best_thr = t + offset;
+            best_gain = g;
+            best_dl = false;
+          }
+        }
+      }
+    }
+  }
+  const int32_t best_rc = num_data - best_lc;
+  const double lo = calc_leaf_output_full(use_l1, best_lg, best_lh, l1, l2, mds, use_smoothing,
+                                          cfg.path_smooth, best_lc, po);
+  const double rsg = sum_gradient - best_lg;
+  const double rsh = sum_hessian_bumped - best_lh;
+  const double ro = calc_leaf_output_full(use_l1, rsg, rsh, l1, l2, mds, use_smoothing,
+                                          cfg.path_smooth, best_rc, po);
+  if (is_splittable && best_gain > kMinScore) {
+    out->threshold = (uint32_t)best_thr;
+    out->gain = best_gain - min_gain_shift;
+    out->left_count = best_lc;
+    out->right_count = num_data - best_lc;
+    out->left_sum_gradient = best_lg;
+    out->left_sum_hessian = best_lh - kEps;
+    out->right_sum_gradient = rsg;
+    out->right_sum_hessian = rsh - kEps;
+    out->left_output = lo;
+    out->right_output = ro;
+    out->default_left = best_dl ? 1 : 0;
+  } else {
+    *out = split_none();
+  }
+  return LGBM_HIP_OK;
+}
+
+// split_gt (split_info.rs:28-35)
+inline bool split_gt(const lgbm_split_info& a, int32_t af, const lgbm_split_info& b, int32_t bf) {
+  if (a.gain != b.gain) return a.gain > b.gain;
+  int32_t x = af == -1 ? std::numeric_limits<int32_t>::max() : af;
+  int32_t y = bf == -1 ? std::numeric_limits<int32_t>::max() : bf;
+  return x < y;
+}
+
+// fix_histogram (fix_histogram.rs:50-80)
+void fix_histogram(double* hist, uint32_t num_bin, uint32_t mfb, double sum_g, double sum_h) {
+  if (mfb == 0 || mfb >= num_bin) return;
+  double g = sum_g, h = sum_h;
+  for (uint32_t i = 0; i < num_bin; ++i) {
+    if (i != mfb) {
+      g -= hist[(size_t)i * 2];
+      h -= hist[(size_t)i * 2 + 1];
+    }
+  }
+  hist[(size_t)mfb * 2] = g;
+  hist[(size_t)mfb * 2 + 1] = h;
+}
+
+// compact_histogram (learner.rs:4460-4492)
+void compact_histogram(double* hist, uint32_t num_bin, int32_t offset) {
+  if (offset <= 0) return;
+  uint32_t off = (uint32_t)offset;
+  if (off >= num_bin) {
+    for (size_t i = 0; i < 2ull * num_bin; ++i) hist[i] = 0.0;
+    return;
+  }
+  for (uint32_t c = 0; c < num_bin - off; ++c) {
+    hist[(size_t)c * 2] = hist[(size_t)(c + off) * 2];
+    hist[(size_t)c * 2 + 1] = hist[(size_t)(c + off) * 2 + 1];
+  }
+  for (size_t i = (size_t)(num_bin - off) * 2; i < 2ull * num_bin; ++i) hist[i] = 0.0;
+}
+
+// ---------------------------------------------------------------------------
+// GradientDiscretizer (gradient_discretizer.rs)
+// ---------------------------------------------------------------------------
+struct Discretizer {
+  int32_t bins;
+  bool const_hess;
+  bool stochastic;
+  uint64_t rng;
+  double gs = 0, hs = 0, igs = 0, ihs = 0;
+
+  // next_u01 (gradient_discretizer.rs:255-263)
+  double next_u01() {
+    uint64_t x = rng;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    rng = x;
+    return (double)(x >> 11) / (double)(1ull << 53);
+  }
+  // compute_scales (:145-165)
+  void compute_scales(const float* g, const float* h, int64_t n) {
+    double mg = std::fabs((double)g[0]), mh = std::fabs((double)h[0]);
+    for (int64_t i = 0; i < n; ++i) {
+      mg = std::fmax(mg, std::fabs((double)g[i]));
+      mh = std::fmax(mh, std::fabs((double)h[i]));
+    }
+    double half = (double)(bins / 2);
+    gs = mg / half;
+    hs = const_hess ? mh : mh / (double)bins;
+    igs = 1.0 / gs;
+    ihs = 1.0 / hs;
+  }
+  // quantize_pair (:173-188)
+  void quantize_pair(float g, float h, int8_t* qg, int8_t* qh) {
+    double bg = 0.5, bh = 0.5;
+    if (stochastic) {
+      bg = next_u01();
+      bh = next_u01();
+    }
+    double x = (double)g * igs;
+    *qg = sat_i8(g >= 0.0f ? x + bg : x - bg);
+    *qh = const_hess ? (int8_t)1 : sat_i8((double)h * ihs + bh);
+  }
+};
+
+Discretizer make_discretizer(int32_t bins, bool const_hess, bool stochastic, uint64_t seed) {
+  Discretizer d;
+  d.bins = bins;
+  d.const_hess = const_hess;
+  d.stochastic = stochastic;
+  d.rng = stochastic ? (seed ^ 0x9E3779B97F4A7C15ull) : 0;  // new_stochastic (:78-84)
+  return d;
+}
+
+bool is_constant_hessian(const float* h, int64_t n) {  // gbdt.rs:54
+  for (int64_t i = 0; i < n; ++i)
+    if (!(h[i] == h[0])) return false;
+  return true;
+}
+
+// quantize_grad_hess_in_place (gbdt.rs:43-62) -> discretize_dequantize_in_place (:126-139)
+void quantize_in_place(float* g, float* h, int64_t n, int32_t bins, bool stochastic, uint64_t seed,
+                       int8_t* disc_out, double* scales) {
+  if (n == 0) return;
+  bool ch = is_constant_hessian(h, n);
+  Discretizer d = make_discretizer(bins, ch, stochastic, seed);
+  d.compute_scales(g, h, n);
+  for (int64_t i = 0; i < n; ++i) {
+    int8_t qg, qh;
+    d.quantize_pair(g[i], h[i], &qg, &qh);
+    if (disc_out) {
+      disc_out[2 * i] = qh;
+      disc_out[2 * i + 1] = qg;
+    }
+    g[i] = (float)((double)qg * d.gs);
+    h[i] = (float)((double)qh * d.hs);
+  }
+  if (scales) {
+    scales[0] = d.gs;
+    scales[1] = d.hs;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Bin columns (BinColumn, lib.rs:75-211): u8 / u16 / u32 feature-major storage.
+// ---------------------------------------------------------------------------
+struct Bins {
+  const void* data;
+  int width;  // 1, 2 or 4 bytes
+  int64_t n;
+  inline uint32_t at(int f, int64_t row) const {
+    size_t i = (size_t)f * (size_t)n + (size_t)row;
+    if (width == 1) return ((const uint8_t*)data)[i];
+    if (width == 2) return ((const uint16_t*)data)[i];
+    return ((const uint32_t*)data)[i];
+  }
+};
+
+// fold_one_feature (lib.rs:223-246): ascending leaf rows, f32 read -> f64 accumulate.
+template <typename T>
+void fold_feature_t(const T* col, const uint32_t* rows, int64_t nr, const float* og,
+                    const float* oh, double* h) {
+  for (int64_t k = 0; k < nr; ++k) {
+    size_t b = (size_t)col[rows[k]] * 2;
+    h[b] += (double)og[k];
+    h[b + 1] += (double)oh[k];
+  }
+}
+// fold_u8_x4 (lib.rs:484-519): four independent per-feature chains in one walk.
+void fold_u8_x4(const uint8_t* c0, const uint8_t* c1, const uint8_t* c2, const uint8_t* c3,
+                const uint32_t* rows, int64_t nr, const float* og, const float* oh, double* h0,
+                double* h1, double* h2, double* h3) {
+  for (int64_t k = 0; k < nr; ++k) {
+    uint32_t r = rows[k];
+    double g = (double)og[k], hh = (double)oh[k];
+    size_t b0 = (size_t)c0[r] * 2, b1 = (size_t)c1[r] * 2, b2 = (size_t)c2[r] * 2,
+           b3 = (size_t)c3[r] * 2;
+    h0[b0] += g;
+    h0[b0 + 1] += hh;
+    h1[b1] += g;
+    h1[b1 + 1] += hh;
+    h2[b2] += g;
+    h2[b2 + 1] += hh;
+    h3[b3] += g;
+    h3[b3 + 1] += hh;
+  }
+}
+
+void fold_feature(const Bins& bins, int f, const uint32_t* rows, int64_t nr, const float* og,
+                  const float* oh, double* h) {
+  size_t base = (size_t)f * (size_t)bins.n;
+  if (bins.width == 1)
+    fold_feature_t((const uint8_t*)bins.data + base, rows, nr, og, oh, h);
+  else if (bins.width == 2)
+    fold_feature_t((const uint16_t*)bins.data + base, rows, nr, og, oh, h);
+  else
+    fold_feature_t((const uint32_t*)bins.data + base, rows, nr, og, oh, h);
+}
+
+// build_histograms_into (lib.rs:262-390): zero, then fold every used feature;
+// features are grouped by 4 and the groups run in parallel for large leaves
+// (par_build_threshold, lib.rs:681-704).  Order within a feature is ascending rows
+// in every arm, so the result is thread-count independent.
+void build_histograms_into(const Bins& bins, const std::vector<uint32_t>& num_bin,
+                           const std::vector<size_t>& slot_off, const uint32_t* rows, int64_t nr,
+                           const float* og, const float* oh, const std::vector<char>* used,
+                           double* out, size_t slot_len) {
+  std::fill(out, out + slot_len, 0.0);
+  const int F = (int)num_bin.size();
+  std::vector<int> act;
+  for (int f = 0; f < F; ++f)
+    if (!used || (*used)[f]) act.push_back(f);
+  const int ng = ((int)act.size() + 3) / 4;
+  auto run_group = [&](int gi) {
+    int a = gi * 4;
+    int cnt = std::min(4, (int)act.size() - a);
+    if (cnt == 4 && bins.width == 1) {
+      const uint8_t* b = (const uint8_t*)bins.data;
+      size_t n = (size_t)bins.n;
+      fold_u8_x4(b + act[a] * n, b + act[a + 1] * n, b + act[a + 2] * n, b + act[a + 3] * n, rows,
+                 nr, og, oh, out + slot_off[act[a]], out + slot_off[act[a + 1]],
+                 out + slot_off[act[a + 2]], out + slot_off[act[a + 3]]);
+    } else {
+      for (int j = 0; j < cnt; ++j) fold_feature(bins, act[a + j], rows, nr, og, oh, out + slot_off[act[a + j]]);
+    }
+  };
+  const bool parallel = nr >= 64;  // par_build_threshold default (lib.rs:681-704)
+#pragma omp parallel for schedule(dynamic, 1) if (parallel && ng > 1)
+  for (int gi = 0; gi < ng; ++gi) run_group(gi);
+}
+
+// ---------------------------------------------------------------------------
+// Tree (lgbm-model/src/tree.rs)
+// ---------------------------------------------------------------------------
+struct Tree {
+  int32_t num_leaves = 1;
+  std::vector<int32_t> split_feature, left_child, right_child, internal_count, leaf_count,
+      leaf_depth, leaf_parent;
+  std::vector<uint32_t> threshold_in_bin;
+  std::vector<double> threshold, internal_value, leaf_value, leaf_weight;
+  std::vector<float> split_gain;
+  std::vector<int8_t> decision_type;
+
+  // root_tree (learner.rs:5398-5424)
+  static Tree root(double out, int32_t n) {
+    Tree t;
+    t.leaf_value = {out};
+    t.leaf_weight = {0.0};
+    t.leaf_count = {n};
+    t.leaf_depth = {0};
+    t.leaf_parent = {-1};
+    return t;
+  }
+  // Tree::split (tree.rs:614-700)
+  void split(int32_t leaf, int32_t real_feature, uint32_t thr_bin, double thr, double lv, double rv,
+             int32_t lc, int32_t rc, double lw, double rw, float gain, int8_t missing_type,
+             bool default_left) {
+    int32_t node = num_leaves - 1;
+    int32_t new_leaf = num_leaves;
+    int32_t parent = leaf_parent[leaf];
+    if (parent >= 0) {
+      if (right_child[parent] == ~leaf)
+        right_child[parent] = node;
+      else
+        left_child[parent] = node;
+    }
+    split_feature.push_back(real_feature);
+    split_gain.push_back(gain);
+    threshold_in_bin.push_back(thr_bin);
+    threshold.push_back(thr);
+    internal_value.push_back(leaf_value[leaf]);
+    internal_count.push_back(lc + rc);
+    left_child.push_back(~leaf);
+    right_child.push_back(~new_leaf);
+    int8_t dt = 0;
+    if (default_left) dt |= 2;  // kDefaultLeftMask
+    dt |= (int8_t)((missing_type & 3) << 2);
+    decision_type.push_back(dt);
+    leaf_value[leaf] = lv;
+    leaf_weight[leaf] = lw;
+    leaf_count[leaf] = lc;
+    leaf_value.push_back(rv);
+    leaf_weight.push_back(rw);
+    leaf_count.push_back(rc);
+    leaf_depth.push_back(leaf_depth[leaf] + 1);
+    leaf_depth[leaf] += 1;
+    leaf_parent[leaf] = node;
+    leaf_parent.push_back(node);
+    num_leaves += 1;
+  }
+  void shrinkage(double rate) {  // tree.rs:1074
+    for (auto& v : leaf_value) v = maybe_round_to_zero(v * rate);
+    for (auto& v : internal_value) v = maybe_round_to_zero(v * rate);
+  }
+  void add_bias(double val) {  // tree.rs:1161
+    for (auto& v : leaf_value) v = maybe_round_to_zero(v + val);
+    for (auto& v : internal_value) v = maybe_round_to_zero(v + val);
+  }
+  void to_out(lgbm_tree_out* o) const {
+    o->num_leaves = num_leaves;
+    for (int i = 0; i < num_leaves - 1; ++i) {
+      if (o->split_feature) o->split_feature[i] = split_feature[i];
+      if (o->threshold_in_bin) o->threshold_in_bin[i] = threshold_in_bin[i];
+      if (o->threshold) o->threshold[i] = threshold[i];
+      if (o->split_gain) o->split_gain[i] = split_gain[i];
+      if (o->decision_type) o->decision_type[i] = decision_type[i];
+      if (o->left_child) o->left_child[i] = left_child[i];
+      if (o->right_child) o->right_child[i] = right_child[i];
+      if (o->internal_value) o->internal_value[i] = internal_value[i];
+      if (o->internal_count) o->internal_count[i] = internal_count[i];
+    }
+    for (int i = 0; i < num_leaves; ++i) {
+      if (o->leaf_value) o->leaf_value[i] = leaf_value[i];
+      if (o->leaf_weight) o->leaf_weight[i] = leaf_weight[i];
+      if (o->leaf_count) o->leaf_count[i] = leaf_count[i];
+      if (o->leaf_depth) o->leaf_depth[i] = leaf_depth[i];
+      if (o->leaf_parent) o->leaf_parent[i] = leaf_parent[i];
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// DataPartition (data_partition.rs)
+// ---------------------------------------------------------------------------
+struct Router {  // split_fused_host_impl router (data_partition.rs:387-417)
+  int32_t min_b, max_b, th, na_bin;
+  bool default_to_right, na, default_left;
+  Router(uint32_t num_bin, uint32_t min_bin, uint32_t max_bin, uint32_t threshold, uint32_t mfb,
+         bool na_as_missing, bool dl) {
+    min_b = (int32_t)min_bin;
+    max_b = (int32_t)max_bin;
+    th = (int32_t)threshold + min_b;
+    if (mfb == 0) th -= 1;
+    default_to_right = (int32_t)mfb > (int32_t)threshold;
+    na_bin = (int32_t)num_bin - 1;
+    na = na_as_missing;
+    default_left = dl;
+  }
+  inline bool go_right(uint32_t b) const {
+    int32_t bin = (int32_t)b;
+    if (na && bin == na_bin) return !default_left;
+    if (bin < min_b || bin > max_b) return default_to_right;
+    return bin > th;
+  }
+};
+
+struct DataPartition {
+  int64_t n;
+  std::vector<uint32_t> indices, part_left, part_right;
+  std::vector<int32_t> leaf_begin, leaf_count;
+  DataPartition(int64_t num_data, int32_t num_leaves)
+      : n(num_data), indices(num_data), part_left(num_data), part_right(num_data),
+        leaf_begin(std::max(num_leaves, 1), 0), leaf_count(std::max(num_leaves, 1), 0) {
+    for (int64_t i = 0; i < num_data; ++i) indices[i] = (uint32_t)i;
+    leaf_count[0] = (int32_t)num_data;
+  }
+  // split (:192-288) with the two-buffer serial body (:418-463) or the block-parallel
+  // body (:489-615); both produce [left ascending | right ascending].
+  int split(int32_t leaf, int32_t right_leaf, const Bins& bins, int f, uint32_t num_bin,
+            uint32_t min_bin, uint32_t max_bin, uint32_t threshold, uint32_t mfb, bool na,
+            bool default_left) {
+    if (num_bin == 0) return fail(LGBM_HIP_ERR_RUNTIME, "data_partition: num_bin must be > 0");
+    if (threshold >= num_bin)
+      return fail(LGBM_HIP_ERR_RUNTIME, "data_partition: threshold >= num_bin");
+    Router r(num_bin, min_bin, max_bin, threshold, mfb, na, default_left);
+    const int64_t begin = leaf_begin[leaf], count = leaf_count[leaf];
+    uint32_t* idx = indices.data() + begin;
+    int64_t lc = 0, rc = 0;
+    const int64_t par_min = 65536;  // LGBM_PAR_PARTITION_MIN default
+#ifdef _OPENMP
+    const int nt = omp_get_max_threads();
+#else
+    const int nt = 1;
+#endif
+    if (count >= par_min && nt > 1) {
+      const int B = nt;
+      std::vector<int64_t> bl(B + 1, 0), br(B + 1, 0);
+      const int64_t blk = (count + B - 1) / B;
+#pragma omp parallel for schedule(static, 1)
+      for (int b = 0; b < B; ++b) {
+        int64_t s = b * blk, e = std::min(count, s + blk);
+        int64_t l = 0, rr = 0;
+        for (int64_t i = s; i < e; ++i) {
+          uint32_t row = idx[i];
+          bool gr = r.go_right(bins.at(f, row));
+          part_left[s + l] = row;
+          part_right[s + rr] = row;
+          l += gr ? 0 : 1;
+          rr += gr ? 1 : 0;
+        }
+        bl[b + 1] = l;
+        br[b + 1] = rr;
+      }
+      for (int b = 0; b < B; ++b) {
+        bl[b + 1] += bl[b];
+        br[b + 1] += br[b];
+      }
+      lc = bl[B];
+      rc = br[B];
+#pragma omp parallel for schedule(static, 1)
+      for (int b = 0; b < B; ++b) {
+        int64_t s = b * blk;
+        std::memcpy(idx + bl[b], part_left.data() + s, (size_t)(bl[b + 1] - bl[b]) * 4);
+        std::memcpy(idx + lc + br[b], part_right.data() + s, (size_t)(br[b + 1] - br[b]) * 4);
+      }
+    } else {
+      for (int64_t i = 0; i < count; ++i) {
+        uint32_t row = idx[i];
+        bool gr = r.go_right(bins.at(f, row));
+        part_right[rc] = row;
+        part_left[lc] = row;
+        rc += gr ? 1 : 0;
+        lc += gr ? 0 : 1;
+      }
+      std::memcpy(idx, part_left.data(), (size_t)lc * 4);
+      std::memcpy(idx + lc, part_right.data(), (size_t)rc * 4);
+    }
+    leaf_count[leaf] = (int32_t)lc;
+    leaf_begin[right_leaf] = (int32_t)(begin + lc);
+    leaf_count[right_leaf] = (int32_t)rc;
+    return LGBM_HIP_OK;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// LeafSplits (leaf_splits.rs)
+// ---------------------------------------------------------------------------
+struct LeafSplits {
+  int32_t n = 0;
+  double sg = 0, sh = 0, weight = 0;
+};
+double self_output(double sg, double sh, const lgbm_gain_config& c) {  // leaf_splits.rs:113-127
+  return calc_leaf_output_full(cfg_use_l1(c), sg, sh, c.lambda_l1, c.lambda_l2, c.max_delta_step,
+                               false, c.path_smooth, 0, 0.0);
+}
+
+// ---------------------------------------------------------------------------
+// SerialTreeLearner spine (learner.rs:980-1562)
+// ---------------------------------------------------------------------------
+struct Learner {
+  Bins bins;
+  int F;
+  std::vector<lgbm_feature_meta> meta;
+  std::vector<uint32_t> num_bin;
+  std::vector<size_t> slot_off;
+  std::vector<size_t> ub_off;
+  const double* ub = nullptr;
+  size_t slot_len = 0;
+  lgbm_gain_config cfg;
+  int32_t num_leaves, max_depth;
+
+  bool skip_default_bin(int f) const {
+    return meta[f].num_bin > 2 && meta[f].missing_type == LGBM_MISSING_ZERO;
+  }
+  bool na_as_missing(int f) const {
+    return meta[f].num_bin > 2 && meta[f].missing_type == LGBM_MISSING_NAN;
+  }
+  bool run_forward(int f) const {
+    return meta[f].num_bin > 2 && meta[f].missing_type != LGBM_MISSING_NONE;
+  }
+
+  // scan_leaf_histogram (learner.rs:2708-3355), spine features only.
+  void scan_leaf(int32_t leaf, const LeafSplits& ls, const double* buf,
+                 const std::vector<char>* parent_split, std::vector<lgbm_split_info>& best,
+                 std::vector<int32_t>& best_feat, std::vector<std::vector<char>>& splittable) {
+    if (!(ls.sh > 0.0) || ls.n <= 0) {
+      best[leaf] = split_none();
+      best_feat[leaf] = -1;
+      return;
+    }
+    lgbm_gain_config lc = cfg;
+    lc.parent_output = ls.weight;
+    std::vector<lgbm_split_info> res(F);
+    std::vector<char> scanned(F, 0);
+#pragma omp parallel for schedule(dynamic, 1) if (F >= 16)
+    for (int f = 0; f < F; ++f) {
+      if (parent_split && !(*parent_split)[f]) continue;
+      find_best_split(buf + slot_off[f], 2ull * num_bin[f], lc, num_bin[f], meta[f].offset,
+                      meta[f].default_bin, skip_default_bin(f), na_as_missing(f), run_forward(f),
+                      ls.sg, ls.sh, ls.n, &res[f]);
+      scanned[f] = 1;
+    }
+    std::vector<char> this_split(F, 0);
+    lgbm_split_info lb = split_none();
+    int32_t lbf = -1;
+    for (int f = 0; f < F; ++f) {
+      if (!scanned[f]) continue;
+      const lgbm_split_info& s = res[f];
+      this_split[f] = s.gain > kMinScore;
+      if (s.gain > kMinScore && split_gt(s, meta[f].real_feature_index, lb, lbf)) {
+        lb = s;
+        lbf = meta[f].real_feature_index;
+      }
+    }
+    best[leaf] = lb;
+    best_feat[leaf] = lbf;
+    splittable[leaf] = this_split;
+  }
+
+  // build_leaf_histogram_into (learner.rs:2464-2566)
+  void build_leaf(const DataPartition& dp, int32_t leaf, const LeafSplits& ls, const float* g,
+                  const float* h, const std::vector<char>* used, double* buf,
+                  std::vector<float>& og, std::vector<float>& oh) {
+    if (!(ls.sh > 0.0) || ls.n <= 0) {
+      std::fill(buf, buf + slot_len, 0.0);
+      return;
+    }
+    const uint32_t* rows = dp.indices.data() + dp.leaf_begin[leaf];
+    const int64_t nr = dp.leaf_count[leaf];
+    for (int64_t k = 0; k < nr; ++k) {
+      og[k] = g[rows[k]];
+      oh[k] = h[rows[k]];
+    }
+    build_histograms_into(bins, num_bin, slot_off, rows, nr, og.data(), oh.data(), used, buf,
+                          slot_len);
+    for (int f = 0; f < F; ++f) {
+      if (used && !(*used)[f]) continue;
+      fix_histogram(buf + slot_off[f], num_bin[f], meta[f].most_freq_bin, ls.sg, ls.sh);
+      compact_histogram(buf + slot_off[f], num_bin[f], meta[f].offset);
+    }
+  }
+
+  int train(const float* g, const float* h, Tree& tree, DataPartition& dp) {
+    const int64_t N = bins.n;
+    // bin-range gate (learner.rs:1161-1187)
+    for (int f = 0; f < F; ++f)
+      for (int64_t r = 0; r < N; ++r)
+        if (bins.at(f, r) >= num_bin[f])
+          return fail(LGBM_HIP_ERR_BIN_OUT_OF_RANGE, "bin index out of range");
+    if (num_leaves < 1) return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "num_leaves < 1");
+    std::vector<std::vector<double>> slot(num_leaves);
+    std::vector<float> og(N), oh(N);
+    // root LeafSplits::init (leaf_splits.rs:75-89): sequential ordered f64 fold.
+    LeafSplits smaller, larger;
+    {
+      double sg = 0.0, sh = 0.0;
+      for (int64_t i = 0; i < N; ++i) {
+        sg += (double)g[i];
+        sh += (double)h[i];
+      }
+      smaller.n = (int32_t)N;
+      smaller.sg = sg;
+      smaller.sh = sh;
+      smaller.weight = self_output(sg, sh, cfg);
+    }
+    if (!(smaller.sh > 0.0)) return fail(LGBM_HIP_ERR_INVALID_LEAF_HESSIAN, "root sum_hessian <= 0");
+    tree = Tree::root(smaller.weight, (int32_t)N);
+    std::vector<lgbm_split_info> best(num_leaves, split_none());
+    std::vector<int32_t> best_feat(num_leaves, -1);
+    std::vector<std::vector<char>> splittable(num_leaves, std::vector<char>(F, 1));
+    int32_t left_leaf = 0, right_leaf = -1;
+    for (int32_t it = 0; it < num_leaves - 1; ++it) {
+      // before_find_best_split (learner.rs:1808-1839)
+      bool did = true;
+      {
+        int32_t nl = dp.leaf_count[left_leaf];
+        if (max_depth > 0 && tree.leaf_depth[left_leaf] >= max_depth) {
+          best[left_leaf].gain = kMinScore;
+          if (right_leaf >= 0) best[right_leaf].gain = kMinScore;
+          did = false;
+        } else {
+          int32_t min2 = cfg.min_data_in_leaf * 2;
+          if (right_leaf >= 0) {
+            int32_t nr = dp.leaf_count[right_leaf];
+            if (nr < min2 && nl < min2) {
+              best[left_leaf].gain = kMinScore;
+              best[right_leaf].gain = kMinScore;
+              did = false;
+            }
+          } else if (nl < min2) {
+            best[left_leaf].gain = kMinScore;
+            did = false;
+          }
+        }
+      }
+      if (did) {
+        // find_best_splits (learner.rs:1851-2453)
+        int32_t sm, lg;
+        if (right_leaf < 0) {
+          sm = left_leaf;
+          lg = -1;
+        } else if (dp.leaf_count[left_leaf] < dp.leaf_count[right_leaf]) {
+          sm = left_leaf;
+          lg = right_leaf;
+        } else {
+          sm = right_leaf;
+          lg = left_leaf;
+        }
+        const bool use_subtract = right_leaf >= 0 && !slot[left_leaf].empty();
+        std::vector<char> parent_split;
+        if (use_subtract) parent_split = splittable[left_leaf];
+        std::vector<double> parent;
+        if (use_subtract) parent.swap(slot[left_leaf]);
+        const LeafSplits& s_ls = smaller;
+        const LeafSplits& l_ls = right_leaf < 0 ? smaller : larger;
+        std::vector<double> sbuf(slot_len, 0.0);
+        build_leaf(dp, sm, s_ls, g, h, use_subtract ? &parent_split : nullptr, sbuf.data(), og, oh);
+        std::vector<double> lbuf;
+        if (lg >= 0) {
+          lbuf.resize(slot_len);
+          if (use_subtract) {
+            for (size_t i = 0; i < slot_len; ++i) lbuf[i] = parent[i] - sbuf[i];
+          } else {
+            build_leaf(dp, lg, l_ls, g, h, nullptr, lbuf.data(), og, oh);
+          }
+        }
+        slot[sm].swap(sbuf);
+        if (lg >= 0) slot[lg].swap(lbuf);
+        const std::vector<char>* ps = use_subtract ? &parent_split : nullptr;
+        scan_leaf(sm, s_ls, slot[sm].data(), ps, best, best_feat, splittable);
+        if (lg >= 0) scan_leaf(lg, l_ls, slot[lg].data(), ps, best, best_feat, splittable);
+      }
+      // arg_max (learner.rs:4537)
+      int32_t bl = 0;
+      for (int32_t i = 1; i < num_leaves; ++i)
+        if (split_gt(best[i], best_feat[i], best[bl], best_feat[bl])) bl = i;
+      const lgbm_split_info b = best[bl];
+      if (b.gain <= 0.0) break;
+      // split_inner (learner.rs:3895-4092)
+      const int32_t fr = best_feat[bl];
+      int f = -1;
+      for (int j = 0; j < F; ++j)
+        if (meta[j].real_feature_index == fr) {
+          f = j;
+          break;
+        }
+      const int32_t new_left = bl, new_right = tree.num_leaves;
+      const lgbm_feature_meta& m = meta[f];
+      const uint32_t pmin = m.min_bin + (uint32_t)std::max(m.offset, 0);
+      int rc = dp.split(bl, new_right, bins, f, m.num_bin, pmin, m.max_bin, b.threshold,
+                        m.most_freq_bin, na_as_missing(f), b.default_left != 0);
+      if (rc != LGBM_HIP_OK) return rc;
+      const double thr_real =
+          ub ? ub[ub_off[f] + b.threshold] : (double)b.threshold;  // real_threshold (learner.rs:198-203)
+      const float gain_field = (float)(b.gain + cfg.min_gain_to_split);
+      const int32_t pl = dp.leaf_count[new_left], pr = dp.leaf_count[new_right];
+      tree.split(bl, fr, b.threshold, thr_real, b.left_output, b.right_output, pl, pr,
+                 b.left_sum_hessian, b.right_sum_hessian, gain_field, (int8_t)m.missing_type,
+                 b.default_left != 0);
+      if (pl < pr) {
+        smaller = {pl, b.left_sum_gradient, b.left_sum_hessian, b.left_output};
+        larger = {pr, b.right_sum_gradient, b.right_sum_hessian, b.right_output};
+      } else {
+        smaller = {pr, b.right_sum_gradient, b.right_sum_hessian, b.right_output};
+        larger = {pl, b.left_sum_gradient, b.left_sum_hessian, b.left_output};
+      }
+      best[bl] = split_none();
+      best_feat[bl] = -1;
+      best[new_left] = split_none();
+      best_feat[new_left] = -1;
+      best[new_right] = split_none();
+      best_feat[new_right] = -1;
+      left_leaf = new_left;
+      right_leaf = new_right;
+    }
+    return LGBM_HIP_OK;
+  }
+};
+
+int make_learner(Learner& L, const void* bins, int width, int32_t F, int64_t N,
+                 const lgbm_feature_meta* meta, const double* ub, const lgbm_gain_config* cfg,
+                 int32_t num_leaves, int32_t max_depth) {
+  if (!bins || !meta || !cfg || F <= 0 || N <= 0)
+    return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "null input or empty shape");
+  if (width != 1 && width != 2 && width != 4)
+    return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "bin width must be 1, 2 or 4");
+  L.bins = {bins, width, N};
+  L.F = F;
+  L.meta.assign(meta, meta + F);
+  L.num_bin.resize(F);
+  L.slot_off.resize(F);
+  L.ub_off.resize(F);
+  size_t acc = 0, uacc = 0;
+  for (int f = 0; f < F; ++f) {
+    L.num_bin[f] = meta[f].num_bin;
+    L.slot_off[f] = acc;
+    L.ub_off[f] = uacc;
+    acc += 2ull * meta[f].num_bin;
+    uacc += meta[f].num_bin;
+  }
+  L.slot_len = acc;
+  L.ub = ub;
+  L.cfg = *cfg;
+  L.num_leaves = num_leaves;
+  L.max_depth = max_depth;
+  return LGBM_HIP_OK;
+}
+
+// BinaryLogloss::get_gradients (lgbm-objective/src/binary.rs:134-172), sigmoid = 1,
+// balanced label weights.
+void binary_gradients(const double* score, const float* label, float* g, float* h, int64_t n,
+                      double sigmoid) {
+#pragma omp parallel for schedule(static) if (n > 65536)
+  for (int64_t i = 0; i < n; ++i) {
+    bool pos = label[i] > 0.0f;
+    double lv = pos ? 1.0 : -1.0;
+    double resp = -lv * sigmoid / (1.0 + std::exp(lv * sigmoid * score[i]));
+    double ar = std::fabs(resp);
+    g[i] = (float)(resp * 1.0);
+    h[i] = (float)(ar * (sigmoid - ar) * 1.0);
+  }
+}
+// BinaryLogloss::boost_from_score (binary.rs:178-192)
+double binary_boost_from_score(const float* label, int64_t n, double sigmoid) {
+  if (n == 0) return 0.0;
+  double suml = 0.0;
+  for (int64_t i = 0; i < n; ++i) suml += label[i] > 0.0f ? 1.0 : 0.0;
+  double pavg = suml / (double)n;
+  pavg = std::fmin(pavg, 1.0 - kEps);
+  pavg = std::fmax(pavg, kEps);
+  return std::log(pavg / (1.0 - pavg)) / sigmoid;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C API (test infrastructure)
+// ===========================================================================
+extern "C" {
+
+int oracle_last_error(char* buf, size_t size) {
+  if (size == 0) return 0;
+  std::snprintf(buf, size, "%s", g_err.c_str());
+  return 0;
+}
+
+int oracle_set_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+  return omp_get_max_threads();
+#else
+  (void)n;
+  return 1;
+#endif
+}
+
+// construct_histograms_cpu_native (kernels/histogram.rs:207-233): rows in order.
+int oracle_construct_histogram(const uint32_t* bins, const float* g, const float* h, int64_t n,
+                               uint32_t num_bin, double* out) {
+  for (int64_t i = 0; i < n; ++i)
+    if (bins[i] >= num_bin) return fail(LGBM_HIP_ERR_BIN_OUT_OF_RANGE, "bin >= num_bin");
+  std::fill(out, out + 2ull * num_bin, 0.0);
+  for (int64_t i = 0; i < n; ++i) {
+    size_t t = (size_t)bins[i] * 2;
+    out[t] += (double)g[i];
+    out[t + 1] += (double)h[i];
+  }
+  return LGBM_HIP_OK;
+}
+
+// construct_int_histogram (gradient_discretizer.rs:235-250)
+int oracle_construct_int_histogram(const uint32_t* binned, const int8_t* disc,
+                                   const uint32_t* rows, int64_t nr, uint32_t num_bin,
+                                   int64_t* out) {
+  std::fill(out, out + 2ull * num_bin, 0);
+  for (int64_t k = 0; k < nr; ++k) {
+    uint32_t r = rows[k];
+    size_t t = (size_t)binned[r] * 2;
+    out[t] += disc[2 * (size_t)r + 1];
+    out[t + 1] += disc[2 * (size_t)r];
+  }
+  return LGBM_HIP_OK;
+}
+
+// Discretizer entry: discretize (:104-118) when disc_out != NULL, and the in-place
+// dequantize write-back (:126-139).  constant-hessian inference per gbdt.rs:54 when
+// const_hess < 0, else forced.
+int oracle_quantize(float* g, float* h, int64_t n, int32_t bins, int32_t stochastic,
+                    uint64_t seed, int32_t const_hess, int8_t* disc_out, double* scales) {
+  if (n == 0) return LGBM_HIP_OK;
+  bool ch = const_hess < 0 ? is_constant_hessian(h, n) : const_hess != 0;
+  Discretizer d = make_discretizer(bins, ch, stochastic != 0, seed);
+  d.compute_scales(g, h, n);
+  for (int64_t i = 0; i < n; ++i) {
+    int8_t qg, qh;
+    d.quantize_pair(g[i], h[i], &qg, &qh);
+    if (disc_out) {
+      disc_out[2 * i] = qh;
+      disc_out[2 * i + 1] = qg;
+    }
+    g[i] = (float)((double)qg * d.gs);
+    h[i] = (float)((double)qh * d.hs);
+  }
+  if (scales) {
+    scales[0] = d.gs;
+    scales[1] = d.hs;
+  }
+  return LGBM_HIP_OK;
+}
+
+// xorshift64 stream (gradient_discretizer.rs:255-263) for RNG tests.
+int oracle_xorshift_u01(uint64_t state, int64_t n, double* out) {
+  Discretizer d;
+  d.rng = state;
+  for (int64_t i = 0; i < n; ++i) out[i] = d.next_u01();
+  return LGBM_HIP_OK;
+}
+
+int oracle_fix_histogram(double* hist, uint32_t num_bin, uint32_t mfb, double sg, double sh) {
+  fix_histogram(hist, num_bin, mfb, sg, sh);
+  return LGBM_HIP_OK;
+}
+int oracle_compact_histogram(double* hist, uint32_t num_bin, int32_t offset) {
+  compact_histogram(hist, num_bin, offset);
+  return LGBM_HIP_OK;
+}
+int oracle_subtract(const double* parent, const double* child, int64_t n, double* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = parent[i] - child[i];
+  return LGBM_HIP_OK;
+}
+
+int oracle_find_best_split(const double* hist, int64_t hist_len, const lgbm_gain_config* cfg,
+                           uint32_t num_bin, int32_t offset, uint32_t default_bin,
+                           int32_t skip_default_bin, int32_t na_as_missing, int32_t run_forward,
+                           double sum_gradient, double sum_hessian, int32_t num_data,
+                           lgbm_split_info* out) {
+  return find_best_split(hist, (size_t)hist_len, *cfg, num_bin, offset, default_bin,
+                         skip_default_bin != 0, na_as_missing != 0, run_forward != 0,
+                         sum_gradient, sum_hessian, num_data, out);
+}
+
+// The learner router over a row set: stable [left | right] order of local positions.
+int oracle_data_partition(const uint32_t* bins, int64_t n, uint32_t num_bin, uint32_t min_bin,
+                          uint32_t max_bin, uint32_t threshold, uint32_t mfb,
+                          int32_t na_as_missing, int32_t default_left, uint32_t* order,
+                          int64_t* left_count) {
+  if (num_bin == 0) return fail(LGBM_HIP_ERR_RUNTIME, "data_partition: num_bin must be > 0");
+  if (threshold >= num_bin) return fail(LGBM_HIP_ERR_RUNTIME, "threshold >= num_bin");
+  for (int64_t i = 0; i < n; ++i)
+    if (bins[i] >= num_bin) return fail(LGBM_HIP_ERR_BIN_OUT_OF_RANGE, "bin >= num_bin");
+  Router r(num_bin, min_bin, max_bin, threshold, mfb, na_as_missing != 0, default_left != 0);
+  int64_t k = 0;
+  for (int64_t i = 0; i < n; ++i)
+    if (!r.go_right(bins[i])) order[k++] = (uint32_t)i;
+  *left_count = k;
+  for (int64_t i = 0; i < n; ++i)
+    if (r.go_right(bins[i])) order[k++] = (uint32_t)i;
+  return LGBM_HIP_OK;
+}
+
+// One tree of the SerialTreeLearner spine over feature-major bins of `width` bytes.
+int oracle_train_tree(const void* bins, int32_t width, int32_t F, int64_t N,
+                      const lgbm_feature_meta* meta, const double* ub, const float* g,
+                      const float* h, const lgbm_gain_config* cfg, int32_t num_leaves,
+                      int32_t max_depth, lgbm_tree_out* tree_out, lgbm_layout_out* layout) {
+  Learner L;
+  int rc = make_learner(L, bins, width, F, N, meta, ub, cfg, num_leaves, max_depth);
+  if (rc) return rc;
+  Tree t;
+  DataPartition dp(N, num_leaves);
+  rc = L.train(g, h, t, dp);
+  if (rc) return rc;
+  if (tree_out) t.to_out(tree_out);
+  if (layout) {
+    if (layout->indices) std::memcpy(layout->indices, dp.indices.data(), (size_t)N * 4);
+    for (int i = 0; i < t.num_leaves; ++i) {
+      if (layout->leaf_begin) layout->leaf_begin[i] = dp.leaf_begin[i];
+      if (layout->leaf_count) layout->leaf_count[i] = dp.leaf_count[i];
+    }
+  }
+  return LGBM_HIP_OK;
+}
+
+int oracle_binary_gradients(const double* score, const float* label, float* g, float* h,
+                            int64_t n) {
+  binary_gradients(score, label, g, h, n, 1.0);
+  return LGBM_HIP_OK;
+}
+double oracle_binary_boost_from_score(const float* label, int64_t n) {
+  return binary_boost_from_score(label, n, 1.0);
+}
+
+// The binary boosting loop (gbdt.rs:691-1300 for K = 1, no bagging): gradients ->
+// optional quantization (seed per gbdt.rs:950) -> grow -> shrinkage -> score update
+// through the partition (learner.rs:4380-4395) -> add_bias on the first tree.
+// `scores` (n) receives the final training scores; trees_out (optional) is an array of
+// `iters` tree descriptors.  Returns the number of trees in *n_trees.
+int oracle_train_binary(const void* bins, int32_t width, int32_t F, int64_t N,
+                        const lgbm_feature_meta* meta, const double* ub, const float* label,
+                        const lgbm_gain_config* cfg, int32_t num_leaves, int32_t max_depth,
+                        int32_t iters, double lr, int32_t boost_from_average, int32_t quantized,
+                        int32_t quant_bins, int32_t stochastic, double* scores,
+                        lgbm_tree_out* trees_out, int32_t* n_trees) {
+  Learner L;
+  int rc = make_learner(L, bins, width, F, N, meta, ub, cfg, num_leaves, max_depth);
+  if (rc) return rc;
+  std::vector<double> score(N, 0.0);
+  double init = 0.0;
+  if (boost_from_average) {
+    init = binary_boost_from_score(label, N, 1.0);
+    if (std::fabs(init) > kEps)
+      for (int64_t i = 0; i < N; ++i) score[i] += init;
+  }
+  std::vector<float> g(N), h(N);
+  int32_t nt = 0;
+  for (int32_t it = 0; it < iters; ++it) {
+    binary_gradients(score.data(), label, g.data(), h.data(), N, 1.0);
+    if (quantized) {
+      uint64_t seed = ((uint64_t)it << 20) ^ 0ull ^ 0x51702010ull;
+      quantize_in_place(g.data(), h.data(), N, quant_bins, stochastic != 0, seed, nullptr, nullptr);
+    }
+    Tree t;
+    DataPartition dp(N, num_leaves);
+    rc = L.train(g.data(), h.data(), t, dp);
+    if (rc) return rc;
+    if (t.num_leaves <= 1) {
+      // No split anywhere this round: GBDT::TrainOneIter keeps the first iteration's
+      // constant tree (init score) and stops training (gbdt.rs:981-992, the C++
+      // should_continue / pop at gbdt.cpp:440-446).
+      if (it == 0) {
+        t = Tree::root(init, (int32_t)N);
+        if (trees_out) t.to_out(&trees_out[it]);
+        nt++;
+      }
+      break;
+    }
+    {
+      t.shrinkage(lr);
+      for (int32_t leaf = 0; leaf < t.num_leaves; ++leaf) {
+        const double v = t.leaf_value[leaf];
+        const uint32_t* rows = dp.indices.data() + dp.leaf_begin[leaf];
+        const int32_t c = dp.leaf_count[leaf];
+        for (int32_t k = 0; k < c; ++k) score[rows[k]] += v;
+      }
+      if (it == 0 && std::fabs(init) > kEps) t.add_bias(init);
+    }
+    if (trees_out) t.to_out(&trees_out[it]);
+    nt++;
+  }
+  if (scores) std::memcpy(scores, score.data(), (size_t)N * 8);
+  if (n_trees) *n_trees = nt;
+  return LGBM_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,226 @@
+"""Extract the reference's committed golden vectors into compact JSON fixtures.
+
+Run in the build container (where /root/reference exists):
+
+    python tests/golden/make_golden.py
+
+The reference's fixtures are data (inputs + expected outputs as raw IEEE bit
+patterns); this script only re-encodes them.  Sources (under
+/root/reference/crates/oracle-harness/tests/fixtures/):
+
+  kernels/histogram.txt   -> hist_f64.json      (format: kernel_parity.rs:17-25)
+  kernels/split.txt       -> split_scan.json    (format: kernel_parity.rs:285-360)
+  kernels/subtract.txt    -> subtract.json
+  kernels/partition.txt   -> partition.json     (format: kernel_parity.rs:1162-1220)
+  learner/spine_real.txt, learner/mfb_pos_real.txt -> learner_real.json
+      (real lib_lightgbm 4.6 model text; the corpora are the ones the reference
+       test drives, oracle-harness/tests/learner_parity.rs:1214-1330)
+
+plus the hand-computed discretizer cases of
+crates/lgbm-treelearner/src/gradient_discretizer.rs:269-333 -> discretizer_cases.json.
+"""
+import json
+import os
+import struct
+import sys
+
+REF = "/root/reference/crates/oracle-harness/tests/fixtures"
+OUT = os.path.dirname(os.path.abspath(__file__))
+
+
+def field(tokens, key):
+    for t in tokens:
+        if t.startswith(key + "="):
+            return t[len(key) + 1:]
+    return None
+
+
+def ints(s):
+    return [int(x) for x in s.split(";")] if s else []
+
+
+def read(path):
+    with open(os.path.join(REF, path)) as f:
+        return [ln.rstrip("\n") for ln in f]
+
+
+def hist_cases():
+    lines = [l for l in read("kernels/histogram.txt") if l and not l.startswith("#")]
+    out, i = [], 0
+    while i < len(lines):
+        t = lines[i].split()
+        if t[0] != "HCASE":
+            i += 1
+            continue
+        name = field(t, "name")
+        num_bin = int(field(t, "num_bin"))
+        bins = ints(lines[i + 1].split()[1] if len(lines[i + 1].split()) > 1 else "")
+        grad = ints(lines[i + 2].split()[1] if len(lines[i + 2].split()) > 1 else "")
+        hess = ints(lines[i + 3].split()[1] if len(lines[i + 3].split()) > 1 else "")
+        hist = ints(lines[i + 4].split()[1])
+        assert lines[i + 1].startswith("BINS") and lines[i + 4].startswith("HIST")
+        nz = [[k, v] for k, v in enumerate(hist) if v != 0]
+        out.append(dict(name=name, num_bin=num_bin, bins=bins, grad_bits=grad, hess_bits=hess,
+                        hist_len=len(hist), hist_nonzero_bits=nz))
+        i += 5
+    return out
+
+
+def split_cases():
+    lines = [l for l in read("kernels/split.txt") if l and not l.startswith("#")]
+    out, i = [], 0
+    keys_i = ["num_bin", "offset", "default_bin", "skip_default_bin", "na_as_missing", "use_l1",
+              "min_data_in_leaf", "num_data"]
+    keys_f = ["min_sum_hessian_in_leaf", "lambda_l1", "lambda_l2", "min_gain_to_split",
+              "sum_gradient", "sum_hessian"]
+    while i < len(lines):
+        t = lines[i].split()
+        if t[0] != "SCASE":
+            i += 1
+            continue
+        c = dict(name=field(t, "name"))
+        for k in keys_i:
+            c[k] = int(field(t, k))
+        for k in keys_f:
+            c[k + "_bits"] = int(field(t, k))
+        c["hist_bits"] = ints(lines[i + 1].split()[1])
+        c["cand_rev_bits"] = ints(lines[i + 2].split()[1]) if len(lines[i + 2].split()) > 1 else []
+        c["cand_fwd_bits"] = ints(lines[i + 3].split()[1]) if len(lines[i + 3].split()) > 1 else []
+        w = lines[i + 4].split()
+        assert w[0] == "SWIN"
+        win = {}
+        for k in ["is_splittable", "threshold", "left_count", "right_count", "default_left"]:
+            win[k] = int(field(w, k))
+        for k in ["gain", "min_gain_shift", "left_sum_gradient", "left_sum_hessian",
+                  "right_sum_gradient", "right_sum_hessian", "left_output", "right_output"]:
+            win[k + "_bits"] = int(field(w, k))
+        c["win"] = win
+        out.append(c)
+        i += 5
+    return out
+
+
+def subtract_cases():
+    lines = [l for l in read("kernels/subtract.txt") if l and not l.startswith("#")]
+    out, i = [], 0
+    while i < len(lines):
+        t = lines[i].split()
+        if t[0] != "SUBCASE":
+            i += 1
+            continue
+        out.append(dict(name=field(t, "name"), parent_bits=ints(lines[i + 1].split()[1]),
+                        child_bits=ints(lines[i + 2].split()[1]),
+                        derived_bits=ints(lines[i + 3].split()[1])))
+        i += 4
+    return out
+
+
+def partition_cases():
+    lines = [l for l in read("kernels/partition.txt") if l and not l.startswith("#")]
+    out, i = [], 0
+    while i < len(lines):
+        t = lines[i].split()
+        if t[0] != "PCASE":
+            i += 1
+            continue
+        c = dict(name=field(t, "name"))
+        for k in ["num_bin", "min_bin", "max_bin", "threshold", "most_freq_bin", "missing_type",
+                  "default_bin", "default_left"]:
+            c[k] = int(field(t, k))
+        c["bins"] = ints(lines[i + 1].split()[1])
+        c["order"] = ints(lines[i + 2].split()[1])
+        c["split_point"] = int(lines[i + 3].split()[1])
+        out.append(c)
+        i += 4
+    return out
+
+
+def parse_model_tree(path):
+    """Tree=0 block of a LightGBM v4 model text -> dict of string lists."""
+    tree, inside = {}, False
+    for ln in read(path):
+        if ln.startswith("Tree=0"):
+            inside = True
+            continue
+        if inside:
+            if not ln.strip():
+                break
+            k, _, v = ln.partition("=")
+            tree[k] = v.split()
+    return tree
+
+
+def f64bits(x):
+    return struct.unpack("<Q", struct.pack("<d", x))[0]
+
+
+def real_upper_bounds(num_bin, zero_sentinel_bin0=False):
+    # learner_parity.rs:1070-1085 / 1112-1118: midpoint (b + 0.5) + 1 ULP; the mfb>0
+    # corpus carries kZeroThreshold = 1e-35f widened at bin 0.
+    out = []
+    for b in range(num_bin):
+        out.append(struct.unpack("<d", struct.pack("<Q", f64bits(b + 0.5) + 1))[0])
+    if zero_sentinel_bin0:
+        out[0] = struct.unpack("<f", struct.pack("<f", 1e-35))[0]
+    return out
+
+
+def learner_real():
+    cases = []
+    # learner_parity.rs:1214-1230 (spine_real)
+    cases.append(dict(
+        name="spine_real", golden_file="learner/spine_real.txt",
+        bins=[0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 5, 5],
+        grad=[-6.0, -6.0, -5.0, -5.0, -1.0, -1.0, 1.0, 1.0, 5.0, 5.0, 6.0, 6.0],
+        num_bin=6, most_freq_bin=0, upper=real_upper_bounds(6),
+        tree=parse_model_tree("learner/spine_real.txt")))
+    # learner_parity.rs:1297-1330 (mfb_pos_real)
+    cases.append(dict(
+        name="mfb_pos_real", golden_file="learner/mfb_pos_real.txt",
+        bins=[0, 1, 2, 2, 2, 2, 2, 2, 3, 3, 1, 0],
+        grad=[-6.0, -3.0, -1.0, -1.0, -1.0, 1.0, 1.0, 1.0, 4.0, 5.0, -3.0, -6.0],
+        num_bin=4, most_freq_bin=0, upper=real_upper_bounds(4, zero_sentinel_bin0=True),
+        tree=parse_model_tree("learner/mfb_pos_real.txt")))
+    for c in cases:
+        c["upper_bits"] = [f64bits(x) for x in c.pop("upper")]
+        # single_feature_corpus (learner_parity.rs:1039-1062)
+        c.update(hess=[1.0] * len(c["grad"]), min_data_in_leaf=1, min_sum_hessian_in_leaf=1e-3,
+                 num_leaves=4, max_depth=-1, shrinkage=0.1)
+    return cases
+
+
+def discretizer_cases():
+    # Hand-computed unit cases, gradient_discretizer.rs:269-333 (inputs -> expected ints).
+    return [
+        dict(name="deterministic_quantize_constant_hessian_bins4", bins=4, const_hess=1,
+             grad=[1.0, -1.0, 0.5, -0.5, 0.3, -0.3], hess=[1.0] * 6,
+             grad_scale=0.5, q_grad=[2, -2, 1, -1, 1, -1], q_hess=[1] * 6),
+        dict(name="half_rounds_away_from_zero", bins=4, const_hess=1,
+             grad=[0.75, -0.75, 1.0], hess=[1.0] * 3, q_grad_sel={"0": 2, "1": -2}),
+        dict(name="nonconstant_hessian_uses_full_bins", bins=4, const_hess=0,
+             grad=[0.5, -0.5], hess=[0.25, 0.125], hess_scale=0.0625, q_hess=[4, 2]),
+        dict(name="int_histogram_sums_per_bin", bins=4, const_hess=1,
+             grad=[1.0, -1.0, 0.5, -0.5], hess=[1.0] * 4, binned=[0, 0, 1, 1], num_bin=2,
+             int_hist=[0, 2, 0, 2]),
+    ]
+
+
+def main():
+    if not os.path.isdir(REF):
+        sys.exit("reference fixtures not found at " + REF)
+    outs = {
+        "hist_f64.json": hist_cases(),
+        "split_scan.json": split_cases(),
+        "subtract.json": subtract_cases(),
+        "partition.json": partition_cases(),
+        "learner_real.json": learner_real(),
+        "discretizer_cases.json": discretizer_cases(),
+    }
+    for name, data in outs.items():
+        with open(os.path.join(OUT, name), "w") as f:
+            json.dump(data, f, separators=(",", ":"))
+        print(name, len(data), os.path.getsize(os.path.join(OUT, name)), "bytes")
+
+
+if __name__ == "__main__":
+    main()
