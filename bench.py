@@ -1,0 +1,138 @@
+"""Benchmark: histogram GB/s + seconds per 100 trees, 10.5M x 28 quantized-grad, 1 MI355X.
+
+One step = one boosting iteration of BASELINE.json configs[1] (binary logloss,
+num_leaves 255, max_bin 63, int8 gradients with 4 quantization bins and stochastic
+rounding) with every input resident in HBM: objective -> quantize -> grow the tree
+(histogram, split scan, partition for all 254 splits) -> score update.  Binning and
+the one-time upload are outside the timed region.
+
+Prints ONE JSON line.  `value` is seconds per 100 trees (lower is better); the
+histogram bandwidth of the dominant kernel is reported in `roofline`, timed with HIP
+events on the library's own stream.  `cpu_baseline` times the CPU restatement of the
+reference learner (oracle/) on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--rows", type=int, default=10_500_000)
+    ap.add_argument("--num-leaves", type=int, default=255)
+    ap.add_argument("--cpu-iters", type=int, default=2,
+                    help="boosting iterations of the CPU baseline sample (0 disables)")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU (--gpus {args.gpus} requested): this build "
+              "has no multi-GPU path; see DESIGN.md for how the path would shard.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from lightgbm_rs_amd import GainConfig, HipBackend
+    from lightgbm_rs_amd.synth import config1_like
+
+    n, nl = args.rows, args.num_leaves
+    t0 = time.perf_counter()
+    dev = torch.device("cuda:0") if torch.cuda.is_available() else None
+    bins, meta, ub, y = config1_like(n, device=dev)
+    log(f"data: {n} x 28, num_bin {max(m.num_bin for m in meta)}, gen {time.perf_counter()-t0:.1f}s")
+    pos = float(y.mean())
+    eps = float(np.float32(1e-15))
+    pavg = min(max(pos, eps), 1.0 - eps)
+    init = float(np.log(pavg / (1.0 - pavg)))  # BinaryLogloss::boost_from_score
+    cfg = GainConfig.make(min_data_in_leaf=20, min_sum_hessian_in_leaf=1e-3)
+    lr = 0.1
+
+    be = HipBackend(0)
+    t1 = time.perf_counter()
+    be.upload_resident_bins(bins, meta, ub)
+    be.set_labels(y, init)
+    log(f"upload {time.perf_counter()-t1:.2f}s")
+    for i in range(args.warmup):
+        be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=False)
+    be.set_timing(True)
+    torch.cuda.synchronize() if dev is not None else None
+    leaves = []
+    t2 = time.perf_counter()
+    for i in range(args.warmup, args.warmup + args.steps):
+        t = be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=True)
+        leaves.append(t["num_leaves"])
+    torch.cuda.synchronize() if dev is not None else None
+    elapsed = time.perf_counter() - t2
+    tm = be.timing()
+    be.close()
+    ms_per_step = elapsed / args.steps * 1e3
+    s_per_100 = elapsed / args.steps * 100.0
+    hist_gbs = tm["hist_bytes"] / (tm["hist_ms"] * 1e-3) / 1e9 if tm["hist_ms"] > 0 else 0.0
+    per_launch_bytes = tm["hist_bytes"] / max(tm["hist_launches"], 1)
+    log(f"gpu: {ms_per_step:.2f} ms/step, leaves {min(leaves)}..{max(leaves)}, timing {tm}")
+
+    cpu = None
+    if args.cpu_iters > 0:
+        from oracle import oracle
+        threads = args.cpu_threads or (os.cpu_count() or 1)
+        threads = oracle.set_threads(threads)
+        tc = time.perf_counter()
+        oracle.train_binary(bins, meta, ub, y, cfg, nl, -1, args.cpu_iters, lr,
+                            boost_from_average=True, quantized=True, quant_bins=4,
+                            stochastic=True, want_trees=False)
+        cs = time.perf_counter() - tc
+        cpu = {"value": cs / args.cpu_iters * 100.0, "unit": "s/100 trees", "cores": threads,
+               "kind": "port",
+               "sample": f"{args.cpu_iters} boosting iterations of the same {n}x28 workload "
+                         f"(C++ restatement of the reference CpuBackend learner, OpenMP), "
+                         f"extrapolated to 100 trees; {cs:.1f}s measured"}
+        log(f"cpu: {cs:.1f}s for {args.cpu_iters} iters on {threads} threads")
+
+    out = {
+        "metric": "histogram GB/s + sec per 100 trees, 10.5M x 28 quantized-grad, 1 MI355X",
+        "value": round(s_per_100, 4),
+        "unit": "s/100 trees",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 grad/hess, int32 histogram, f64 split math",
+        "data": "synthetic (BASELINE.json configs[1] recipe, quantile-binned)",
+        "config": {"workload": "configs[1]: binary, 10.5M rows x 28 features, max_bin 63, "
+                               "num_leaves 255, quantized int8 grads (4 bins, stochastic)",
+                   "rows": n, "features": 28, "num_leaves": nl, "learning_rate": lr},
+        "hist_GBps": round(hist_gbs, 2),
+        "roofline": {"bound": "hbm", "achieved": round(hist_gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(hist_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "k_hist (ConstructHistogram)",
+                     "bytes_per_launch": round(per_launch_bytes, 1),
+                     "launches": tm["hist_launches"],
+                     "avg_launch_us": round(tm["hist_ms"] * 1e3 / max(tm["hist_launches"], 1), 3)},
+        "phase_ms_per_step": {k: round(tm[k] / args.steps, 4) for k in
+                              ("hist_ms", "partition_ms", "scan_ms", "quant_ms", "objective_ms")},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

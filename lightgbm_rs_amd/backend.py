@@ -1,0 +1,241 @@
+"""HipBackend — Python mirror of the reference's `Backend` seam over the C-ABI.
+
+Method names follow `trait Backend` (crates/lgbm-compute/src/lib.rs:1092-2782) and
+`GradientDiscretizer` (crates/lgbm-treelearner/src/gradient_discretizer.rs); every
+call goes to lightgbm_rs_amd/liblgbm_hip.so.  There is no CPU fallback: if the
+library or a HIP device is missing, construction raises.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+from ._abi import (STATUS, BatchedFeature, FeatureMeta, GainConfig, LayoutBuffers, SplitInfo,
+                   TreeBuffers, ptr)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liblgbm_hip.so")
+
+_lib = None
+
+
+class HipError(RuntimeError):
+    """A non-zero status from the C-ABI (mirrors `ComputeError`, error.rs)."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"{STATUS.get(code, code)}: {msg}")
+        self.code = code
+
+
+def load_library():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"HIP library not built: {LIB_PATH} (run __graft_entry__.build())")
+        _lib = C.CDLL(LIB_PATH)
+    return _lib
+
+
+def _feature_meta_array(meta):
+    arr = (FeatureMeta * len(meta))()
+    for i, m in enumerate(meta):
+        arr[i] = m
+    return arr
+
+
+class HipBackend:
+    """One device context (`GpuBackend` with its resident caches, lib.rs:3848-3934)."""
+
+    def __init__(self, device=0):
+        self.lib = load_library()
+        self.ctx = C.c_void_p()
+        rc = self.lib.lgbm_hip_ctx_create(C.c_int(device), C.byref(self.ctx))
+        if rc != 0:
+            raise HipError(rc, self._err(None))
+        self.num_data = 0
+        self.num_features = 0
+        self.slot_len = 0
+
+    def _err(self, ctx):
+        buf = C.create_string_buffer(1024)
+        self.lib.lgbm_hip_last_error(ctx, buf, C.c_size_t(1024))
+        return buf.value.decode()
+
+    def _check(self, rc):
+        if rc != 0:
+            raise HipError(rc, self._err(self.ctx))
+
+    def close(self):
+        if self.ctx:
+            self.lib.lgbm_hip_ctx_destroy(self.ctx)
+            self.ctx = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- resident data -------------------------------------------------------
+    def upload_resident_bins(self, bins_feature_major, meta, bin_upper_bound=None):
+        """`Backend::upload_resident_bins` (lib.rs:1564): bins [F, N] u8."""
+        b = np.ascontiguousarray(bins_feature_major, dtype=np.uint8)
+        F, N = b.shape
+        marr = _feature_meta_array(meta)
+        ub = None if bin_upper_bound is None else np.ascontiguousarray(bin_upper_bound, np.float64)
+        self._check(self.lib.lgbm_hip_upload_bins(self.ctx, ptr(b, C.c_uint8), C.c_int32(F),
+                                                  C.c_int64(N), marr, ptr(ub, C.c_double)))
+        self.num_data, self.num_features = N, F
+        self.slot_len = 2 * sum(m.num_bin for m in meta)
+
+    def upload_resident_grad_hess(self, grad, hess):
+        """`Backend::upload_resident_grad_hess` (lib.rs:1607)."""
+        g = np.ascontiguousarray(grad, dtype=np.float32)
+        h = np.ascontiguousarray(hess, dtype=np.float32)
+        self._check(self.lib.lgbm_hip_set_gradients(self.ctx, ptr(g, C.c_float), ptr(h, C.c_float),
+                                                    C.c_int64(len(g))))
+
+    def discretize_dequantize_in_place(self, num_grad_quant_bins=4, stochastic=True, seed=0,
+                                       want_values=False):
+        """`GradientDiscretizer::discretize_dequantize_in_place` on the resident g/h.
+
+        Returns (scales, dequantized grad, dequantized hess) — the last two only
+        when want_values."""
+        n = self.num_data
+        dg = np.zeros(n, np.float32) if want_values else None
+        dh = np.zeros(n, np.float32) if want_values else None
+        scales = np.zeros(2, np.float64)
+        self._check(self.lib.lgbm_hip_quantize(self.ctx, C.c_int32(num_grad_quant_bins),
+                                               C.c_int32(int(stochastic)), C.c_uint64(seed),
+                                               ptr(dg, C.c_float), ptr(dh, C.c_float),
+                                               ptr(scales, C.c_double)))
+        return scales, dg, dh
+
+    def discretized(self):
+        """The `discretize` buffer: out[2i] = hess, out[2i+1] = grad (i8)."""
+        out = np.zeros(2 * self.num_data, np.int8)
+        self._check(self.lib.lgbm_hip_get_discretized(self.ctx, ptr(out, C.c_int8),
+                                                      C.c_int64(self.num_data)))
+        return out
+
+    # ---- per-op seam ---------------------------------------------------------
+    def construct_int_histogram(self, leaf_rows=None):
+        """Exact integer histogram of the quantized gradients (all features)."""
+        rows = None if leaf_rows is None else np.ascontiguousarray(leaf_rows, np.uint32)
+        out = np.zeros(self.slot_len, np.int64)
+        self._check(self.lib.lgbm_hip_build_int_histogram(
+            self.ctx, ptr(rows, C.c_uint32), C.c_int64(0 if rows is None else len(rows)),
+            ptr(out, C.c_int64)))
+        return out
+
+    def build_resident_leaf(self, leaf_rows, sum_gradient, sum_hessian):
+        """`Backend::build_resident_leaf` (lib.rs:1953-1972): build + fix + compact."""
+        rows = None if leaf_rows is None else np.ascontiguousarray(leaf_rows, np.uint32)
+        out = np.zeros(self.slot_len, np.float64)
+        self._check(self.lib.lgbm_hip_build_leaf_histogram(
+            self.ctx, ptr(rows, C.c_uint32), C.c_int64(0 if rows is None else len(rows)),
+            C.c_double(sum_gradient), C.c_double(sum_hessian), ptr(out, C.c_double)))
+        return out
+
+    def find_best_splits_batched(self, hist, feats, cfg, sum_gradient, sum_hessian, num_data):
+        """`Backend::find_best_splits_batched` (lib.rs:1500-1548)."""
+        h = np.ascontiguousarray(hist, np.float64)
+        farr = (BatchedFeature * len(feats))(*feats)
+        out = (SplitInfo * len(feats))()
+        self._check(self.lib.lgbm_hip_find_best_splits(
+            self.ctx, ptr(h, C.c_double), C.c_int64(len(h)), farr, C.c_int32(len(feats)),
+            C.byref(cfg), C.c_double(sum_gradient), C.c_double(sum_hessian), C.c_int32(num_data),
+            out))
+        return list(out)
+
+    def subtract_histograms(self, parent, child):
+        """`Backend::subtract_histograms` (lib.rs:1314)."""
+        p = np.ascontiguousarray(parent, np.float64)
+        c = np.ascontiguousarray(child, np.float64)
+        out = np.zeros_like(p)
+        self._check(self.lib.lgbm_hip_subtract_histograms(self.ctx, ptr(p, C.c_double),
+                                                          ptr(c, C.c_double), C.c_int64(len(p)),
+                                                          ptr(out, C.c_double)))
+        return out
+
+    def data_partition(self, bins, num_bin, min_bin, max_bin, threshold, most_freq_bin,
+                       na_as_missing=False, default_left=False):
+        """`Backend::data_partition` (lib.rs:1206) -> (order, split_point)."""
+        b = np.ascontiguousarray(bins, np.uint32)
+        order = np.zeros(len(b), np.uint32)
+        lc = C.c_int64(0)
+        self._check(self.lib.lgbm_hip_data_partition(
+            self.ctx, ptr(b, C.c_uint32), C.c_int64(len(b)), C.c_uint32(num_bin),
+            C.c_uint32(min_bin), C.c_uint32(max_bin), C.c_uint32(threshold),
+            C.c_uint32(most_freq_bin), C.c_int32(int(na_as_missing)),
+            C.c_int32(int(default_left)), ptr(order, C.c_uint32), C.byref(lc)))
+        return order, lc.value
+
+    # ---- coarse seam -----------------------------------------------------------
+    def grow_tree_on_device_with_cfg(self, cfg, num_leaves, max_depth=-1, want_layout=True):
+        """`Backend::grow_tree_on_device_with_cfg` (lib.rs:2771) -> (tree, layout)."""
+        tb = TreeBuffers(num_leaves)
+        lb = LayoutBuffers(self.num_data, num_leaves) if want_layout else None
+        self._check(self.lib.lgbm_hip_grow_tree(self.ctx, C.byref(cfg), C.c_int32(num_leaves),
+                                                C.c_int32(max_depth), C.byref(tb.out),
+                                                C.byref(lb.out) if lb else None))
+        t = tb.to_dict()
+        layout = None
+        if lb is not None:
+            nl = t["num_leaves"]
+            layout = {"indices": lb.indices, "leaf_begin": lb.leaf_begin[:nl].copy(),
+                      "leaf_count": lb.leaf_count[:nl].copy()}
+        return t, layout
+
+    # ---- boosting on device ------------------------------------------------------
+    def set_labels(self, labels, init_score=0.0):
+        lab = np.ascontiguousarray(labels, np.float32)
+        self._check(self.lib.lgbm_hip_set_labels(self.ctx, ptr(lab, C.c_float), C.c_int64(len(lab)),
+                                                 C.c_double(init_score)))
+
+    def train_iter_binary(self, it, cfg, num_leaves, max_depth, learning_rate,
+                          num_grad_quant_bins=4, stochastic=True, want_tree=True):
+        tb = TreeBuffers(num_leaves) if want_tree else None
+        self._check(self.lib.lgbm_hip_train_iter_binary(
+            self.ctx, C.c_int32(it), C.byref(cfg), C.c_int32(num_leaves), C.c_int32(max_depth),
+            C.c_double(learning_rate), C.c_int32(num_grad_quant_bins), C.c_int32(int(stochastic)),
+            C.byref(tb.out) if tb else None))
+        return tb.to_dict() if tb else None
+
+    def scores(self):
+        out = np.zeros(self.num_data, np.float64)
+        self._check(self.lib.lgbm_hip_get_scores(self.ctx, ptr(out, C.c_double),
+                                                 C.c_int64(self.num_data)))
+        return out
+
+    def set_timing(self, enable=True):
+        self._check(self.lib.lgbm_hip_set_timing(self.ctx, C.c_int32(int(enable))))
+
+    def timing(self):
+        ms = np.zeros(5, np.float64)
+        nbytes = C.c_double(0)
+        launches = C.c_int64(0)
+        self._check(self.lib.lgbm_hip_get_timing(self.ctx, ptr(ms, C.c_double), C.byref(nbytes),
+                                                 C.byref(launches)))
+        return {"hist_ms": ms[0], "partition_ms": ms[1], "scan_ms": ms[2], "quant_ms": ms[3],
+                "objective_ms": ms[4], "hist_bytes": nbytes.value,
+                "hist_launches": launches.value}
+
+
+def feature_meta(num_bin, most_freq_bin=0, missing_type=0, default_bin=None, real_index=0,
+                 min_bin=0, max_bin=None):
+    """FeatureColumn descriptors with the offset rule of offset_for_most_freq_bin
+    (lgbm-treelearner/src/lib.rs:89-95)."""
+    m = FeatureMeta()
+    m.num_bin = num_bin
+    m.offset = 1 if most_freq_bin == 0 else 0
+    m.min_bin = min_bin
+    m.max_bin = num_bin - 1 if max_bin is None else max_bin
+    m.default_bin = num_bin if default_bin is None else default_bin
+    m.most_freq_bin = most_freq_bin
+    m.missing_type = missing_type
+    m.real_feature_index = real_index
+    return m
+
+
+__all__ = ["HipBackend", "HipError", "GainConfig", "feature_meta", "load_library"]

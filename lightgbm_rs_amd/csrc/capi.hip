@@ -1,0 +1,963 @@
+// capi.hip — the C-ABI (include/lgbm_hip.h) over the gfx950 kernels.
+//
+// A context owns every device allocation.  Each call is synchronous at the API
+// boundary (the reference backend's calls are blocking, lib.rs:3840-3846); inside a
+// call everything is queued on the context's own HIP stream.
+#include <algorithm>
+#include <array>
+#include <cstddef>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+
+using namespace lgbm;
+
+namespace {
+
+thread_local std::string g_create_err;
+
+struct EventPair {
+  hipEvent_t a, b;
+  int family;
+};
+
+}  // namespace
+
+struct lgbm_hip_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  // shape
+  int64_t N = 0;
+  int32_t F = 0, W = 0, total_cells = 0;
+  uint64_t slot_len = 0;
+  std::vector<DevFeature> feats;
+  bool have_bins = false, have_grad = false, quant_ready = false, have_labels = false;
+  int32_t quant_bins = 0;
+  // device memory
+  Ctl* ctl = nullptr;
+  DevFeature* d_feats = nullptr;
+  double* d_ub = nullptr;
+  uint4* rec[NBUF] = {};
+  uint16_t* gh[NBUF] = {};
+  int64_t buf_rows[NBUF] = {};
+  float *g = nullptr, *h = nullptr, *label = nullptr;
+  double* score = nullptr;
+  int32_t* hist_int = nullptr;
+  uint64_t* tile_state = nullptr;
+  int64_t tile_cap = 0;
+  uint64_t *wave_mats = nullptr, *lane_mats = nullptr;
+  double* stats = nullptr;
+  // tree-sized
+  int32_t lcap = 0;
+  double* slots = nullptr;
+  lgbm_split_info *feat_split = nullptr, *best = nullptr;
+  int32_t* best_feat = nullptr;
+  uint8_t* splittable = nullptr;
+  DevLeaves leaves{};
+  DevTree tree{};
+  // scratch
+  void* scratch = nullptr;
+  size_t scratch_cap = 0;
+  double* slot_tmp = nullptr;
+  uint32_t* d_indices = nullptr;
+  int64_t indices_cap = 0;
+  // timing
+  bool timing = false;
+  std::vector<EventPair> ev_pool;
+  size_t ev_used = 0;
+  double ms[5] = {0, 0, 0, 0, 0};
+};
+
+namespace {
+
+int set_err(lgbm_hip_ctx* c, int code, const std::string& m) {
+  if (c)
+    c->err = m;
+  else
+    g_create_err = m;
+  return code;
+}
+
+#define HIPCHK(c, expr)                                                                   \
+  do {                                                                                    \
+    hipError_t _e = (expr);                                                               \
+    if (_e != hipSuccess)                                                                 \
+      return set_err(c, LGBM_HIP_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(_e)); \
+  } while (0)
+
+template <typename T>
+int dalloc(lgbm_hip_ctx* c, T** p, size_t count) {
+  if (*p) {
+    (void)hipFree(*p);
+    *p = nullptr;
+  }
+  if (count == 0) count = 1;
+  HIPCHK(c, hipMalloc((void**)p, count * sizeof(T)));
+  return LGBM_HIP_OK;
+}
+
+// ---- xorshift64 jump matrices (GF(2)); column i = image of basis vector e_i ----
+using Mat = std::array<uint64_t, 64>;
+uint64_t xs_step(uint64_t x) {
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  return x;
+}
+uint64_t mat_apply(const Mat& m, uint64_t v) {
+  uint64_t y = 0;
+  for (int i = 0; i < 64; ++i)
+    if ((v >> i) & 1ull) y ^= m[i];
+  return y;
+}
+Mat mat_mul(const Mat& a, const Mat& b) {
+  Mat c;
+  for (int i = 0; i < 64; ++i) c[i] = mat_apply(a, b[i]);
+  return c;
+}
+
+int init_jump_tables(lgbm_hip_ctx* c) {
+  Mat m;
+  for (int i = 0; i < 64; ++i) m[i] = xs_step(1ull << i);
+  // T = M^(2*C): two draws per row, C rows per lane
+  Mat t = m;
+  static_assert(QUANT_ROWS_PER_LANE == 32, "2*C must be 64 = 2^6");
+  for (int i = 0; i < 6; ++i) t = mat_mul(t, t);
+  std::vector<uint64_t> lane(QUANT_LANE_MATS * 64), wave(QUANT_WAVE_MATS * 64);
+  Mat r = t;
+  for (int k = 0; k < QUANT_LANE_MATS; ++k) {
+    std::copy(r.begin(), r.end(), lane.begin() + k * 64);
+    if (k + 1 < QUANT_LANE_MATS) r = mat_mul(r, r);
+  }
+  Mat p = mat_mul(r, r);  // T^64 = M^(2*C*64)
+  for (int k = 0; k < QUANT_WAVE_MATS; ++k) {
+    std::copy(p.begin(), p.end(), wave.begin() + k * 64);
+    p = mat_mul(p, p);
+  }
+  int rc = dalloc(c, &c->lane_mats, lane.size());
+  if (rc) return rc;
+  rc = dalloc(c, &c->wave_mats, wave.size());
+  if (rc) return rc;
+  HIPCHK(c, hipMemcpy(c->lane_mats, lane.data(), lane.size() * 8, hipMemcpyHostToDevice));
+  HIPCHK(c, hipMemcpy(c->wave_mats, wave.data(), wave.size() * 8, hipMemcpyHostToDevice));
+  return LGBM_HIP_OK;
+}
+
+DevLearner make_learner(lgbm_hip_ctx* c) {
+  DevLearner L{};
+  L.ctl = c->ctl;
+  L.feats = c->d_feats;
+  L.ub = c->d_ub;
+  L.F = c->F;
+  L.W = c->W;
+  L.total_cells = c->total_cells;
+  L.N = c->N;
+  L.slot_len = c->slot_len;
+  L.hist_int = c->hist_int;
+  L.slots = c->slots;
+  L.feat_split = c->feat_split;
+  L.best = c->best;
+  L.best_feat = c->best_feat;
+  L.splittable = c->splittable;
+  L.tile_state = c->tile_state;
+  L.stats = c->stats;
+  L.leaves = c->leaves;
+  L.tree = c->tree;
+  for (int i = 0; i < NBUF; ++i) {
+    L.bufs.rec[i] = c->rec[i];
+    L.bufs.gh[i] = c->gh[i];
+  }
+  return L;
+}
+
+template <typename T>
+int ctl_write(lgbm_hip_ctx* c, size_t off, const T& v) {
+  HIPCHK(c, hipMemcpyAsync((char*)c->ctl + off, &v, sizeof(T), hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return LGBM_HIP_OK;
+}
+template <typename T>
+int ctl_read(lgbm_hip_ctx* c, size_t off, T* v) {
+  HIPCHK(c, hipMemcpyAsync(v, (char*)c->ctl + off, sizeof(T), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return LGBM_HIP_OK;
+}
+#define CTL_OFF(field) offsetof(Ctl, field)
+
+int ensure_scratch_rows(lgbm_hip_ctx* c, int64_t n) {
+  for (int b : {BUF_S0, BUF_S1}) {
+    if (c->buf_rows[b] >= n && c->rec[b]) continue;
+    int rc = dalloc(c, &c->rec[b], (size_t)std::max<int64_t>(n, 1) * std::max(c->W, 1));
+    if (rc) return rc;
+    rc = dalloc(c, &c->gh[b], (size_t)std::max<int64_t>(n, 1));
+    if (rc) return rc;
+    c->buf_rows[b] = n;
+  }
+  return LGBM_HIP_OK;
+}
+
+int ensure_scratch_bytes(lgbm_hip_ctx* c, size_t bytes) {
+  if (c->scratch_cap >= bytes && c->scratch) return LGBM_HIP_OK;
+  if (c->scratch) (void)hipFree(c->scratch);
+  c->scratch = nullptr;
+  HIPCHK(c, hipMalloc(&c->scratch, std::max<size_t>(bytes, 256)));
+  c->scratch_cap = std::max<size_t>(bytes, 256);
+  return LGBM_HIP_OK;
+}
+
+int ensure_tile_state(lgbm_hip_ctx* c, int64_t rows) {
+  const int64_t tiles = (rows + PART_TILE - 1) / PART_TILE + 1;
+  if (c->tile_cap >= tiles) return LGBM_HIP_OK;
+  int rc = dalloc(c, &c->tile_state, (size_t)tiles);
+  if (rc) return rc;
+  HIPCHK(c, hipMemset(c->tile_state, 0, (size_t)tiles * 8));
+  c->tile_cap = tiles;
+  return LGBM_HIP_OK;
+}
+
+int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
+  if (c->lcap >= L) return LGBM_HIP_OK;
+  int rc = 0;
+  const size_t F = (size_t)c->F;
+  if ((rc = dalloc(c, &c->slots, (size_t)L * c->slot_len))) return rc;
+  if ((rc = dalloc(c, &c->feat_split, (size_t)L * F))) return rc;
+  if ((rc = dalloc(c, &c->best, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &c->best_feat, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &c->splittable, (size_t)L * F))) return rc;
+  if ((rc = dalloc(c, &c->leaves.begin, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &c->leaves.count, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &c->leaves.buf, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &c->leaves.rev, (size_t)L))) return rc;
+  DevTree& T = c->tree;
+  if ((rc = dalloc(c, &T.split_feature, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.threshold_in_bin, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.threshold, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.split_gain, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.decision_type, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.left_child, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.right_child, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.internal_value, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.internal_count, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.leaf_value, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.leaf_weight, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.leaf_count, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.leaf_depth, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.leaf_parent, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &T.nodes, (size_t)L))) return rc;
+  c->lcap = L;
+  return LGBM_HIP_OK;
+}
+
+// ---- timing ---------------------------------------------------------------
+hipEvent_t ev_begin(lgbm_hip_ctx* c, int family) {
+  if (!c->timing) return nullptr;
+  if (c->ev_used == c->ev_pool.size()) {
+    EventPair p{};
+    (void)hipEventCreate(&p.a);
+    (void)hipEventCreate(&p.b);
+    c->ev_pool.push_back(p);
+  }
+  EventPair& p = c->ev_pool[c->ev_used];
+  p.family = family;
+  (void)hipEventRecord(p.a, c->stream);
+  return p.a;
+}
+void ev_end(lgbm_hip_ctx* c) {
+  if (!c->timing) return;
+  (void)hipEventRecord(c->ev_pool[c->ev_used].b, c->stream);
+  c->ev_used++;
+}
+void ev_collect(lgbm_hip_ctx* c) {
+  if (!c->timing) return;
+  for (size_t i = 0; i < c->ev_used; ++i) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, c->ev_pool[i].a, c->ev_pool[i].b) == hipSuccess)
+      c->ms[c->ev_pool[i].family] += ms;
+  }
+  c->ev_used = 0;
+}
+enum { FAM_HIST = 0, FAM_PART = 1, FAM_SCAN = 2, FAM_QUANT = 3, FAM_OBJ = 4 };
+
+int check_ctx(lgbm_hip_ctx* c) {
+  if (!c) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  HIPCHK(c, hipSetDevice(c->device));
+  return LGBM_HIP_OK;
+}
+
+int do_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_t seed, float* dg,
+                float* dh) {
+  ev_begin(c, FAM_QUANT);
+  launch_absmax(c->g, c->h, c->N, c->ctl, c->stream);
+  launch_quant_scales(c->ctl, bins, -1, c->stream);
+  launch_quantize(c->g, c->h, c->N, c->ctl, c->wave_mats, c->lane_mats,
+                  seed ^ 0x9E3779B97F4A7C15ull, stochastic, c->gh[BUF_ORIG], dg, dh, c->stream);
+  ev_end(c);
+  HIPCHK(c, hipGetLastError());
+  c->quant_ready = true;
+  c->quant_bins = bins;
+  return LGBM_HIP_OK;
+}
+
+int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_leaves,
+                    int32_t max_depth) {
+  int rc = ensure_leaves(c, num_leaves);
+  if (rc) return rc;
+  HIPCHK(c, hipMemcpyAsync((char*)c->ctl + CTL_OFF(cfg), cfg, sizeof(*cfg), hipMemcpyHostToDevice,
+                           c->stream));
+  DevLearner L = make_learner(c);
+  launch_tree_init(L, num_leaves, max_depth, c->stream);
+  ev_begin(c, FAM_HIST);
+  launch_hist(L, 2, c->N, c->stream);
+  ev_end(c);
+  ev_begin(c, FAM_SCAN);
+  launch_fixscan(L, 1, nullptr, c->stream);
+  ev_end(c);
+  for (int32_t s = 1; s < num_leaves; ++s) {
+    ev_begin(c, FAM_SCAN);
+    launch_split(L, c->stream);
+    ev_end(c);
+    ev_begin(c, FAM_PART);
+    launch_partition(L, c->W, s == 1 ? c->N : 0, c->stream);
+    ev_end(c);
+    if (s + 1 < num_leaves) {
+      ev_begin(c, FAM_HIST);
+      launch_hist(L, 1, 0, c->stream);
+      ev_end(c);
+      ev_begin(c, FAM_SCAN);
+      launch_fixscan(L, 0, nullptr, c->stream);
+      ev_end(c);
+    }
+  }
+  HIPCHK(c, hipGetLastError());
+  return LGBM_HIP_OK;
+}
+
+int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, double shrink) {
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  ev_collect(c);
+  int32_t nl = 0, err = 0;
+  int rc = ctl_read(c, CTL_OFF(num_leaves), &nl);
+  if (rc) return rc;
+  rc = ctl_read(c, CTL_OFF(error), &err);
+  if (rc) return rc;
+  if (err & ERR_ROOT_HESSIAN)
+    return set_err(c, LGBM_HIP_ERR_INVALID_LEAF_HESSIAN, "root sum_hessian <= 0");
+  if (err & ERR_SPIN) return set_err(c, LGBM_HIP_ERR_RUNTIME, "partition look-back spin limit");
+  if (err) return set_err(c, LGBM_HIP_ERR_RUNTIME, "device learner error");
+  if (out) {
+    out->num_leaves = nl;
+    const DevTree& T = c->tree;
+    const size_t ni = (size_t)std::max(nl - 1, 0), nl_ = (size_t)nl;
+    auto cp = [&](void* dst, const void* src, size_t bytes) -> int {
+      if (dst && bytes) HIPCHK(c, hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+      return LGBM_HIP_OK;
+    };
+    if ((rc = cp(out->split_feature, T.split_feature, ni * 4))) return rc;
+    if ((rc = cp(out->threshold_in_bin, T.threshold_in_bin, ni * 4))) return rc;
+    if ((rc = cp(out->threshold, T.threshold, ni * 8))) return rc;
+    if ((rc = cp(out->split_gain, T.split_gain, ni * 4))) return rc;
+    if ((rc = cp(out->decision_type, T.decision_type, ni))) return rc;
+    if ((rc = cp(out->left_child, T.left_child, ni * 4))) return rc;
+    if ((rc = cp(out->right_child, T.right_child, ni * 4))) return rc;
+    if ((rc = cp(out->internal_value, T.internal_value, ni * 8))) return rc;
+    if ((rc = cp(out->internal_count, T.internal_count, ni * 4))) return rc;
+    if ((rc = cp(out->leaf_value, T.leaf_value, nl_ * 8))) return rc;
+    if ((rc = cp(out->leaf_weight, T.leaf_weight, nl_ * 8))) return rc;
+    if ((rc = cp(out->leaf_count, T.leaf_count, nl_ * 4))) return rc;
+    if ((rc = cp(out->leaf_depth, T.leaf_depth, nl_ * 4))) return rc;
+    if ((rc = cp(out->leaf_parent, T.leaf_parent, nl_ * 4))) return rc;
+    if (shrink != 1.0) {
+      // Tree::shrinkage (tree.rs:1074): MaybeRoundToZero(v * rate)
+      const double z = (double)1e-35f;
+      auto mrz = [z](double v) { return (v >= -z && v <= z) ? 0.0 : v; };
+      if (out->leaf_value)
+        for (size_t i = 0; i < nl_; ++i) out->leaf_value[i] = mrz(out->leaf_value[i] * shrink);
+      if (out->internal_value)
+        for (size_t i = 0; i < ni; ++i) out->internal_value[i] = mrz(out->internal_value[i] * shrink);
+    }
+  }
+  if (layout) {
+    if (layout->indices) {
+      if (c->indices_cap < c->N) {
+        if ((rc = dalloc(c, &c->d_indices, (size_t)c->N))) return rc;
+        c->indices_cap = c->N;
+      }
+      DevLearner L = make_learner(c);
+      launch_export_layout(L, nl, c->d_indices, c->stream);
+      HIPCHK(c, hipStreamSynchronize(c->stream));
+      HIPCHK(c, hipMemcpy(layout->indices, c->d_indices, (size_t)c->N * 4, hipMemcpyDeviceToHost));
+    }
+    if (layout->leaf_begin)
+      HIPCHK(c, hipMemcpy(layout->leaf_begin, c->leaves.begin, (size_t)nl * 4,
+                          hipMemcpyDeviceToHost));
+    if (layout->leaf_count)
+      HIPCHK(c, hipMemcpy(layout->leaf_count, c->leaves.count, (size_t)nl * 4,
+                          hipMemcpyDeviceToHost));
+  }
+  return LGBM_HIP_OK;
+}
+
+DevFeature feature_from_batched(const lgbm_batched_feature& b) {
+  DevFeature f{};
+  f.num_bin = b.num_bin;
+  f.offset = b.offset;
+  f.default_bin = b.default_bin;
+  f.mfb = b.most_freq_bin;
+  f.slot_off = (uint32_t)b.slot_off;
+  f.cell_base = (uint32_t)(b.slot_off / 2);
+  f.skip_default_bin = b.skip_default_bin;
+  f.na_as_missing = b.na_as_missing;
+  f.run_forward = b.run_forward;
+  f.real_index = -1;
+  return f;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
+  if (!out) return set_err(nullptr, LGBM_HIP_ERR_INVALID_ARGUMENT, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0)
+    return set_err(nullptr, LGBM_HIP_ERR_CAPABILITY, "no HIP device available");
+  if (device < 0 || device >= n)
+    return set_err(nullptr, LGBM_HIP_ERR_INVALID_ARGUMENT, "device index out of range");
+  lgbm_hip_ctx* c = new lgbm_hip_ctx();
+  c->device = device;
+  auto fail = [&](int rc) {
+    g_create_err = c->err;
+    lgbm_hip_ctx_destroy(c);
+    return rc;
+  };
+  if (hipSetDevice(device) != hipSuccess) return fail(set_err(c, LGBM_HIP_ERR_HIP, "hipSetDevice"));
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
+    return fail(set_err(c, LGBM_HIP_ERR_HIP, "hipStreamCreate"));
+  int rc = dalloc(c, &c->ctl, 1);
+  if (rc) return fail(rc);
+  Ctl init;
+  std::memset(&init, 0, sizeof(init));
+  init.epoch = 1u;
+  init.hmin_key = 0xffffffffu;
+  if (hipMemcpy(c->ctl, &init, sizeof(init), hipMemcpyHostToDevice) != hipSuccess)
+    return fail(set_err(c, LGBM_HIP_ERR_HIP, "ctl init"));
+  if ((rc = dalloc(c, &c->stats, 4))) return fail(rc);
+  if (hipMemset(c->stats, 0, 32) != hipSuccess) return fail(set_err(c, LGBM_HIP_ERR_HIP, "stats"));
+  if ((rc = init_jump_tables(c))) return fail(rc);
+  *out = c;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
+  if (!c) return LGBM_HIP_OK;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  auto F = [](void* p) {
+    if (p) (void)hipFree(p);
+  };
+  F(c->ctl);
+  F(c->d_feats);
+  F(c->d_ub);
+  for (int i = 0; i < NBUF; ++i) {
+    F(c->rec[i]);
+    F(c->gh[i]);
+  }
+  F(c->g);
+  F(c->h);
+  F(c->label);
+  F(c->score);
+  F(c->hist_int);
+  F(c->tile_state);
+  F(c->wave_mats);
+  F(c->lane_mats);
+  F(c->stats);
+  F(c->slots);
+  F(c->feat_split);
+  F(c->best);
+  F(c->best_feat);
+  F(c->splittable);
+  F(c->leaves.begin);
+  F(c->leaves.count);
+  F(c->leaves.buf);
+  F(c->leaves.rev);
+  DevTree& T = c->tree;
+  F(T.split_feature);
+  F(T.threshold_in_bin);
+  F(T.threshold);
+  F(T.split_gain);
+  F(T.decision_type);
+  F(T.left_child);
+  F(T.right_child);
+  F(T.internal_value);
+  F(T.internal_count);
+  F(T.leaf_value);
+  F(T.leaf_weight);
+  F(T.leaf_count);
+  F(T.leaf_depth);
+  F(T.leaf_parent);
+  F(T.nodes);
+  F(c->scratch);
+  F(c->slot_tmp);
+  F(c->d_indices);
+  for (auto& p : c->ev_pool) {
+    (void)hipEventDestroy(p.a);
+    (void)hipEventDestroy(p.b);
+  }
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_last_error(const lgbm_hip_ctx* c, char* buf, size_t size) {
+  if (!buf || size == 0) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  const std::string& s = c ? c->err : g_create_err;
+  std::snprintf(buf, size, "%s", s.c_str());
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_features,
+                         int64_t num_data, const lgbm_feature_meta* meta,
+                         const double* bin_upper_bound) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!bins || !meta || num_features <= 0 || num_data <= 0)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null bins/meta or empty shape");
+  if (num_features > 16 * LGBM_MAX_W - 4)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "more features than the record layout holds");
+  if (num_data >= (1ll << 31) - 1)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_data must fit data_size_t (i32)");
+  const int32_t F = num_features;
+  std::vector<DevFeature> feats(F);
+  uint32_t acc = 0, uacc = 0;
+  for (int f = 0; f < F; ++f) {
+    const lgbm_feature_meta& m = meta[f];
+    if (m.num_bin == 0 || m.num_bin > 256)
+      return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be in 1..=256 (u8 bin storage)");
+    DevFeature& d = feats[f];
+    d.num_bin = m.num_bin;
+    d.offset = m.offset;
+    d.min_bin = m.min_bin;
+    d.max_bin = m.max_bin;
+    d.default_bin = m.default_bin;
+    d.mfb = m.most_freq_bin;
+    d.missing_type = m.missing_type;
+    d.real_index = m.real_feature_index;
+    d.slot_off = 2 * acc;
+    d.cell_base = acc;
+    d.ub_off = uacc;
+    d.skip_default_bin = (m.num_bin > 2 && m.missing_type == LGBM_MISSING_ZERO) ? 1 : 0;
+    d.na_as_missing = (m.num_bin > 2 && m.missing_type == LGBM_MISSING_NAN) ? 1 : 0;
+    d.run_forward = (m.num_bin > 2 && m.missing_type != LGBM_MISSING_NONE) ? 1 : 0;
+    acc += m.num_bin;
+    uacc += m.num_bin;
+  }
+  if (acc > 8192)  // 8 B per LDS cell, 64 KiB of dynamic LDS per block
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "histogram exceeds the LDS budget");
+  // bin-range gate (learner.rs:1161-1187): first offending bin, feature order
+  for (int f = 0; f < F; ++f) {
+    const uint8_t* col = bins + (size_t)f * (size_t)num_data;
+    const uint32_t nb = feats[f].num_bin;
+    if (nb >= 256) continue;
+    for (int64_t r = 0; r < num_data; ++r)
+      if (col[r] >= nb)
+        return set_err(c, LGBM_HIP_ERR_BIN_OUT_OF_RANGE,
+                       "bin " + std::to_string(col[r]) + " >= num_bin " + std::to_string(nb) +
+                           " (feature " + std::to_string(f) + ", row " + std::to_string(r) + ")");
+  }
+  c->F = F;
+  c->N = num_data;
+  c->W = (F + 4 + 15) / 16;
+  c->total_cells = (int32_t)acc;
+  c->slot_len = 2ull * acc;
+  c->feats = feats;
+  c->lcap = 0;  // slots depend on slot_len
+  if ((rc = dalloc(c, &c->d_feats, (size_t)F))) return rc;
+  HIPCHK(c, hipMemcpy(c->d_feats, feats.data(), F * sizeof(DevFeature), hipMemcpyHostToDevice));
+  if (bin_upper_bound) {
+    if ((rc = dalloc(c, &c->d_ub, (size_t)uacc))) return rc;
+    HIPCHK(c, hipMemcpy(c->d_ub, bin_upper_bound, uacc * 8, hipMemcpyHostToDevice));
+  } else if (c->d_ub) {
+    (void)hipFree(c->d_ub);
+    c->d_ub = nullptr;
+  }
+  const size_t words = (size_t)num_data * c->W;
+  for (int b : {BUF_ORIG, BUF_A, BUF_B}) {
+    if ((rc = dalloc(c, &c->rec[b], words))) return rc;
+    if ((rc = dalloc(c, &c->gh[b], (size_t)num_data))) return rc;
+    c->buf_rows[b] = num_data;
+  }
+  c->buf_rows[BUF_S0] = c->buf_rows[BUF_S1] = 0;
+  if ((rc = dalloc(c, &c->g, (size_t)num_data))) return rc;
+  if ((rc = dalloc(c, &c->h, (size_t)num_data))) return rc;
+  if ((rc = dalloc(c, &c->hist_int, (size_t)acc * 3))) return rc;
+  HIPCHK(c, hipMemset(c->hist_int, 0, (size_t)acc * 3 * 4));
+  if ((rc = ensure_tile_state(c, num_data))) return rc;
+  // transpose the feature-major upload into records
+  uint8_t* tmp = nullptr;
+  HIPCHK(c, hipMalloc((void**)&tmp, (size_t)F * num_data));
+  hipError_t e = hipMemcpy(tmp, bins, (size_t)F * num_data, hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    launch_pack_records(tmp, num_data, F, c->W, c->rec[BUF_ORIG], c->stream);
+    e = hipStreamSynchronize(c->stream);
+  }
+  (void)hipFree(tmp);
+  if (e != hipSuccess) return set_err(c, LGBM_HIP_ERR_HIP, hipGetErrorString(e));
+  c->have_bins = true;
+  c->have_grad = c->quant_ready = c->have_labels = false;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_set_gradients(lgbm_hip_ctx* c, const float* grad, const float* hess, int64_t n) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
+  if (!grad || !hess) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null gradients");
+  if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "gradient length != num_data");
+  HIPCHK(c, hipMemcpy(c->g, grad, (size_t)n * 4, hipMemcpyHostToDevice));
+  HIPCHK(c, hipMemcpy(c->h, hess, (size_t)n * 4, hipMemcpyHostToDevice));
+  c->have_grad = true;
+  c->quant_ready = false;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_t seed,
+                      float* dg_out, float* dh_out, double* scales_out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set gradients first");
+  if (bins < 1 || bins > 254)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_grad_quant_bins must be in 1..=254");
+  float *dg = nullptr, *dh = nullptr;
+  if (dg_out || dh_out) {
+    if ((rc = ensure_scratch_bytes(c, (size_t)c->N * 8))) return rc;
+    dg = (float*)c->scratch;
+    dh = dg + c->N;
+  }
+  if ((rc = do_quantize(c, bins, stochastic, seed, dg, dh))) return rc;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  ev_collect(c);
+  if (dg_out) HIPCHK(c, hipMemcpy(dg_out, dg, (size_t)c->N * 4, hipMemcpyDeviceToHost));
+  if (dh_out) HIPCHK(c, hipMemcpy(dh_out, dh, (size_t)c->N * 4, hipMemcpyDeviceToHost));
+  if (scales_out) {
+    double s[2];
+    if ((rc = ctl_read(c, CTL_OFF(gs), &s[0]))) return rc;
+    if ((rc = ctl_read(c, CTL_OFF(hs), &s[1]))) return rc;
+    scales_out[0] = s[0];
+    scales_out[1] = s[1];
+  }
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_get_discretized(lgbm_hip_ctx* c, int8_t* out, int64_t n) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->quant_ready) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize first");
+  if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_data");
+  std::vector<uint16_t> q((size_t)n);
+  HIPCHK(c, hipMemcpy(q.data(), c->gh[BUF_ORIG], (size_t)n * 2, hipMemcpyDeviceToHost));
+  for (int64_t i = 0; i < n; ++i) {
+    out[2 * i] = (int8_t)(uint8_t)(q[i] >> 8);        // hess
+    out[2 * i + 1] = (int8_t)(uint8_t)(q[i] & 0xff);  // grad
+  }
+  return LGBM_HIP_OK;
+}
+
+static int set_hist_job(lgbm_hip_ctx* c, const uint32_t* rows, int64_t n_rows) {
+  int rc;
+  int32_t buf = BUF_ORIG;
+  int64_t count = c->N;
+  if (rows) {
+    for (int64_t i = 0; i < n_rows; ++i)
+      if (rows[i] >= (uint64_t)c->N)
+        return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "leaf row index out of range");
+    if ((rc = ensure_scratch_rows(c, n_rows))) return rc;
+    if ((rc = ensure_scratch_bytes(c, (size_t)std::max<int64_t>(n_rows, 1) * 4))) return rc;
+    HIPCHK(c, hipMemcpy(c->scratch, rows, (size_t)n_rows * 4, hipMemcpyHostToDevice));
+    launch_gather_rows(c->W, (const uint32_t*)c->scratch, n_rows, c->rec[BUF_ORIG],
+                       c->gh[BUF_ORIG], c->rec[BUF_S0], c->gh[BUF_S0], c->stream);
+    buf = BUF_S0;
+    count = n_rows;
+  }
+  if ((rc = ctl_write(c, CTL_OFF(h_buf), buf))) return rc;
+  const int64_t zero = 0;
+  if ((rc = ctl_write(c, CTL_OFF(h_begin), zero))) return rc;
+  if ((rc = ctl_write(c, CTL_OFF(h_count), count))) return rc;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_build_int_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int64_t n_rows,
+                                 int64_t* out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->quant_ready) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize first");
+  if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  if ((rc = set_hist_job(c, leaf_rows, n_rows))) return rc;
+  DevLearner L = make_learner(c);
+  launch_hist(L, 0, leaf_rows ? n_rows : c->N, c->stream);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  std::vector<int32_t> cells((size_t)c->total_cells * 3);
+  HIPCHK(c, hipMemcpy(cells.data(), c->hist_int, cells.size() * 4, hipMemcpyDeviceToHost));
+  HIPCHK(c, hipMemset(c->hist_int, 0, cells.size() * 4));
+  for (int32_t i = 0; i < c->total_cells; ++i) {
+    out[2 * i] = cells[3 * (size_t)i];
+    out[2 * i + 1] = cells[3 * (size_t)i + 1];
+  }
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int64_t n_rows,
+                                  double sum_gradient, double sum_hessian, double* out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->quant_ready) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize first");
+  if (c->quant_bins != 2 && c->quant_bins != 4)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "exact f64 histogram requires num_grad_quant_bins in {2, 4}");
+  if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  if ((rc = set_hist_job(c, leaf_rows, n_rows))) return rc;
+  LeafSums s{sum_gradient, sum_hessian, 0.0, (int32_t)(leaf_rows ? n_rows : c->N), 0};
+  if ((rc = ctl_write(c, CTL_OFF(sm), s))) return rc;
+  if ((rc = dalloc(c, &c->slot_tmp, (size_t)c->slot_len))) return rc;
+  DevLearner L = make_learner(c);
+  launch_hist(L, 0, leaf_rows ? n_rows : c->N, c->stream);
+  launch_fixscan(L, 2, c->slot_tmp, c->stream);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipMemcpy(out, c->slot_tmp, (size_t)c->slot_len * 8, hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_find_best_splits(lgbm_hip_ctx* c, const double* hist, int64_t hist_len,
+                              const lgbm_batched_feature* feats, int32_t n_feats,
+                              const lgbm_gain_config* cfg, double sum_gradient,
+                              double sum_hessian, int32_t num_data, lgbm_split_info* out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!hist || !feats || !cfg || !out || n_feats < 0)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  if (n_feats == 0) return LGBM_HIP_OK;
+  std::vector<DevFeature> df(n_feats);
+  for (int i = 0; i < n_feats; ++i) {
+    if (feats[i].num_bin == 0) return set_err(c, LGBM_HIP_ERR_RUNTIME, "num_bin must be > 0");
+    if (feats[i].num_bin > 256)
+      return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be <= 256");
+    if (feats[i].slot_off + 2ull * feats[i].num_bin > (uint64_t)hist_len)
+      return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "feature region beyond the histogram");
+    df[i] = feature_from_batched(feats[i]);
+  }
+  if (!(sum_hessian > 0.0))
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "find_best_split: sum_hessian must be > 0");
+  const size_t bytes = (size_t)hist_len * 8 + (size_t)n_feats * (sizeof(DevFeature) + sizeof(lgbm_split_info)) + 64;
+  if ((rc = ensure_scratch_bytes(c, bytes))) return rc;
+  char* base = (char*)c->scratch;
+  double* d_hist = (double*)base;
+  DevFeature* d_f = (DevFeature*)(base + ((size_t)hist_len * 8 + 15) / 16 * 16);
+  lgbm_split_info* d_out = (lgbm_split_info*)((char*)d_f + (size_t)n_feats * sizeof(DevFeature));
+  HIPCHK(c, hipMemcpy(d_hist, hist, (size_t)hist_len * 8, hipMemcpyHostToDevice));
+  HIPCHK(c, hipMemcpy(d_f, df.data(), df.size() * sizeof(DevFeature), hipMemcpyHostToDevice));
+  launch_scan_explicit(d_hist, d_f, n_feats, *cfg, sum_gradient, sum_hessian, num_data, d_out,
+                       c->stream);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipMemcpy(out, d_out, (size_t)n_feats * sizeof(lgbm_split_info), hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_subtract_histograms(lgbm_hip_ctx* c, const double* parent, const double* child,
+                                 int64_t len, double* out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!parent || !child || !out || len < 0)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  if (len == 0) return LGBM_HIP_OK;
+  if ((rc = ensure_scratch_bytes(c, (size_t)len * 24))) return rc;
+  double* a = (double*)c->scratch;
+  double* b = a + len;
+  double* o = b + len;
+  HIPCHK(c, hipMemcpy(a, parent, (size_t)len * 8, hipMemcpyHostToDevice));
+  HIPCHK(c, hipMemcpy(b, child, (size_t)len * 8, hipMemcpyHostToDevice));
+  launch_subtract(a, b, len, o, c->stream);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipMemcpy(out, o, (size_t)len * 8, hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, uint32_t num_bin,
+                            uint32_t min_bin, uint32_t max_bin, uint32_t threshold,
+                            uint32_t most_freq_bin, int32_t na_as_missing, int32_t default_left,
+                            uint32_t* order_out, int64_t* left_count_out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if ((!bins && n > 0) || (!order_out && n > 0) || !left_count_out || n < 0)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  if (num_bin == 0) return set_err(c, LGBM_HIP_ERR_RUNTIME, "data_partition: num_bin must be > 0");
+  if (threshold >= num_bin)
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "data_partition: threshold >= num_bin");
+  for (int64_t i = 0; i < n; ++i)
+    if (bins[i] >= num_bin)
+      return set_err(c, LGBM_HIP_ERR_BIN_OUT_OF_RANGE,
+                     "bin " + std::to_string(bins[i]) + " >= num_bin at row " + std::to_string(i));
+  if (num_bin > 256) return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be <= 256");
+  if (n == 0) {
+    *left_count_out = 0;
+    return LGBM_HIP_OK;
+  }
+  const int savedW = c->W;
+  c->W = 1;
+  rc = ensure_scratch_rows(c, n);
+  c->W = savedW;
+  if (rc) return rc;
+  if ((rc = ensure_tile_state(c, n))) return rc;
+  if ((rc = ensure_scratch_bytes(c, (size_t)n * 4))) return rc;
+  HIPCHK(c, hipMemcpy(c->scratch, bins, (size_t)n * 4, hipMemcpyHostToDevice));
+  launch_pack_partition((const uint32_t*)c->scratch, n, c->rec[BUF_S0], c->stream);
+  HIPCHK(c, hipMemsetAsync(c->gh[BUF_S0], 0, (size_t)n * 2, c->stream));
+  PartJob J{};
+  J.src_buf = BUF_S0;
+  J.dst_buf = BUF_S1;
+  J.begin = 0;
+  J.count = n;
+  J.rev = 0;
+  J.fbyte = 0;
+  J.pmin = (int32_t)min_bin;
+  J.max_bin = (int32_t)max_bin;
+  J.th = (int32_t)threshold + (int32_t)min_bin - (most_freq_bin == 0 ? 1 : 0);
+  J.na_bin = (int32_t)num_bin - 1;
+  J.flags = ((int32_t)most_freq_bin > (int32_t)threshold ? 1 : 0) | (na_as_missing ? 2 : 0) |
+            (default_left ? 4 : 0);
+  J.driver = 0;
+  if ((rc = ctl_write(c, CTL_OFF(part), J))) return rc;
+  DevLearner L = make_learner(c);
+  L.W = 1;
+  launch_partition(L, 1, n, c->stream);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  int32_t lc = 0;
+  if ((rc = ctl_read(c, CTL_OFF(part_left_count), &lc))) return rc;
+  std::vector<uint4> recs((size_t)n);
+  HIPCHK(c, hipMemcpy(recs.data(), c->rec[BUF_S1], (size_t)n * 16, hipMemcpyDeviceToHost));
+  for (int64_t i = 0; i < lc; ++i) order_out[i] = recs[i].w;
+  for (int64_t i = lc; i < n; ++i) order_out[i] = recs[n - 1 - (i - lc)].w;  // stored reversed
+  *left_count_out = lc;
+  // the scratch rows were sized for W=1 here; force a re-size for the next gather
+  c->buf_rows[BUF_S0] = c->buf_rows[BUF_S1] = 0;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_leaves,
+                       int32_t max_depth, lgbm_tree_out* tree, lgbm_layout_out* layout) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
+  if (num_leaves < 1) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_leaves must be >= 1");
+  if (num_leaves > 256) return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_leaves must be <= 256");
+  if (!c->quant_ready) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize gradients first");
+  if (c->quant_bins != 2 && c->quant_bins != 4)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "device learner requires num_grad_quant_bins in {2, 4}");
+  if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth))) return rc;
+  return finish_tree(c, tree, layout, 1.0);
+}
+
+int lgbm_hip_set_labels(lgbm_hip_ctx* c, const float* labels, int64_t n, double init_score) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
+  if (!labels) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null labels");
+  if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "labels length != num_data");
+  if ((rc = dalloc(c, &c->label, (size_t)n))) return rc;
+  if ((rc = dalloc(c, &c->score, (size_t)n))) return rc;
+  HIPCHK(c, hipMemcpy(c->label, labels, (size_t)n * 4, hipMemcpyHostToDevice));
+  std::vector<double> s((size_t)n, init_score);
+  HIPCHK(c, hipMemcpy(c->score, s.data(), (size_t)n * 8, hipMemcpyHostToDevice));
+  c->have_labels = true;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_config* cfg,
+                               int32_t num_leaves, int32_t max_depth, double learning_rate,
+                               int32_t num_grad_quant_bins, int32_t stochastic,
+                               lgbm_tree_out* tree) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_labels) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set labels first");
+  if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
+  if (num_leaves < 1 || num_leaves > 256)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_leaves must be in 1..=256");
+  if (num_grad_quant_bins != 2 && num_grad_quant_bins != 4)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "device learner requires num_grad_quant_bins in {2, 4}");
+  ev_begin(c, FAM_OBJ);
+  launch_grad_binary(c->score, c->label, c->g, c->h, c->N, c->ctl, c->stream);
+  ev_end(c);
+  c->have_grad = true;
+  const uint64_t seed = ((uint64_t)(uint32_t)iter << 20) ^ 0ull ^ 0x51702010ull;  // gbdt.rs:950
+  ev_begin(c, FAM_QUANT);
+  launch_quant_scales(c->ctl, num_grad_quant_bins, -1, c->stream);
+  launch_quantize(c->g, c->h, c->N, c->ctl, c->wave_mats, c->lane_mats,
+                  seed ^ 0x9E3779B97F4A7C15ull, stochastic, c->gh[BUF_ORIG], nullptr, nullptr,
+                  c->stream);
+  ev_end(c);
+  c->quant_ready = true;
+  c->quant_bins = num_grad_quant_bins;
+  if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth))) return rc;
+  ev_begin(c, FAM_OBJ);
+  DevLearner L = make_learner(c);
+  launch_score_update(L, learning_rate, c->score, c->stream);
+  ev_end(c);
+  HIPCHK(c, hipGetLastError());
+  return finish_tree(c, tree, nullptr, learning_rate);
+}
+
+int lgbm_hip_get_scores(lgbm_hip_ctx* c, double* out, int64_t n) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_labels) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set labels first");
+  if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_data");
+  HIPCHK(c, hipMemcpy(out, c->score, (size_t)n * 8, hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_set_timing(lgbm_hip_ctx* c, int32_t enable) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  ev_collect(c);
+  c->timing = enable != 0;
+  for (double& m : c->ms) m = 0.0;
+  HIPCHK(c, hipMemset(c->stats, 0, 32));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_get_timing(lgbm_hip_ctx* c, double* ms_out5, double* hist_bytes_out,
+                        int64_t* hist_launches_out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  ev_collect(c);
+  if (ms_out5)
+    for (int i = 0; i < 5; ++i) ms_out5[i] = c->ms[i];
+  double st[4] = {0, 0, 0, 0};
+  HIPCHK(c, hipMemcpy(st, c->stats, 32, hipMemcpyDeviceToHost));
+  const double roots = c->N > 0 ? st[2] / (double)c->N : 0.0;
+  // algorithmic bytes: rows x (F bins + 2 B packed g/h [+ 4 B row index off the root])
+  // + the histogram write (cells x 2 x 4 B) per launch
+  const double cell_bytes = (double)c->total_cells * 2.0 * 4.0;
+  const double bytes = st[2] * (double)(c->F + 2) + st[0] * (double)(c->F + 2 + 4) +
+                       (roots + st[1]) * cell_bytes;
+  if (hist_bytes_out) *hist_bytes_out = bytes;
+  if (hist_launches_out) *hist_launches_out = (int64_t)(roots + st[1] + 0.5);
+  return LGBM_HIP_OK;
+}
+
+}  // extern "C"

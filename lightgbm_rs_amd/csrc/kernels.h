@@ -1,0 +1,103 @@
+// lgbm_kernels.h — gfx950 kernels of the tree-learner hot path.
+//
+// Row store.  Every row is one record of W x 16 bytes: bytes [0, F) hold the
+// row's u8 bins (feature-major upload transposed once, lib.rs:4368-4433 is the
+// reference's upload), bytes [16W-4, 16W) the original row index.  A second
+// array holds the row's packed quantized (grad, hess) int8 pair.  Records are
+// *physically* repartitioned at every split into ping-pong buffers, so a leaf's
+// rows are always one contiguous range: ConstructHistogram streams them, and
+// the partition is a single pass.  The right child of a split is stored in
+// reverse order (its logical order is the reference's ascending order; see
+// k_partition), which lets the partition place both children without knowing
+// the left count in advance.
+//
+// Histograms are exact integers: per (feature, bin) cell the kernel counts
+// sum(q_g), sum(q_h) and #(q_h == 3).  With num_grad_quant_bins = 4 every
+// dequantized f32 value the reference folds is v(q) = f32(q * scale); v(+-1),
+// v(+-2), v(4) are exact multiples of v(1) and v(3) is the only other value, so
+// the reference's sequential f64 fold of those values equals
+//   grad = sum(q_g) * v_g(1),  hess = (sum(q_h) - 3 n3) * v_h(1) + n3 * v_h(3)
+// exactly (all partial sums are integer multiples of one ulp unit below 2^53).
+#pragma once
+
+#include "lgbm_device.h"
+
+struct RowBufs {
+  uint4* rec[NBUF];
+  uint16_t* gh[NBUF];
+};
+
+struct DevLeaves {
+  int32_t* begin;
+  int32_t* count;
+  int32_t* buf;
+  int32_t* rev;
+};
+
+struct DevTree {
+  int32_t* split_feature;
+  uint32_t* threshold_in_bin;
+  double* threshold;
+  float* split_gain;
+  int8_t* decision_type;
+  int32_t* left_child;
+  int32_t* right_child;
+  double* internal_value;
+  int32_t* internal_count;
+  double* leaf_value;
+  double* leaf_weight;
+  int32_t* leaf_count;
+  int32_t* leaf_depth;
+  int32_t* leaf_parent;
+  NodeRoute* nodes;
+};
+
+struct DevLearner {
+  Ctl* ctl;
+  const DevFeature* feats;
+  const double* ub;
+  int32_t F;
+  int32_t W;
+  int32_t total_cells;
+  int32_t _pad;
+  int64_t N;
+  uint64_t slot_len;
+  int32_t* hist_int;          // [total_cells][3]
+  double* slots;              // [max_leaves][slot_len]
+  lgbm_split_info* feat_split;  // [max_leaves][F]
+  lgbm_split_info* best;        // [max_leaves]
+  int32_t* best_feat;           // [max_leaves]
+  uint8_t* splittable;          // [max_leaves][F]
+  uint64_t* tile_state;
+  double* stats;                // [0] hist rows (non-root), [1] hist launches, [2] root rows
+  DevLeaves leaves;
+  DevTree tree;
+  RowBufs bufs;
+};
+
+namespace lgbm {
+void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t W, uint4* rec,
+                         hipStream_t s);
+void launch_absmax(const float* g, const float* h, int64_t n, Ctl* ctl, hipStream_t s);
+void launch_grad_binary(const double* score, const float* label, float* g, float* h, int64_t n,
+                        Ctl* ctl, hipStream_t s);
+void launch_quant_scales(Ctl* ctl, int32_t bins, int32_t force_const, hipStream_t s);
+void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,
+                     const uint64_t* wave_mats, const uint64_t* lane_mats, uint64_t s0,
+                     int32_t stochastic, uint16_t* gh, float* dg, float* dh, hipStream_t s);
+void launch_hist(const DevLearner& L, int32_t driver, int64_t count_hint, hipStream_t s);
+void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s);
+void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
+                          const lgbm_gain_config& cfg, double sg, double sh, int32_t n,
+                          lgbm_split_info* out, hipStream_t s);
+void launch_split(const DevLearner& L, hipStream_t s);
+void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s);
+void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, hipStream_t s);
+void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s);
+void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
+                          hipStream_t s);
+void launch_gather_rows(int W, const uint32_t* rows, int64_t n, const uint4* rec,
+                        const uint16_t* gh, uint4* rec_out, uint16_t* gh_out, hipStream_t s);
+void launch_subtract(const double* a, const double* b, int64_t n, double* out, hipStream_t s);
+void launch_pack_partition(const uint32_t* bins, int64_t n, uint4* rec, hipStream_t s);
+}  // namespace lgbm

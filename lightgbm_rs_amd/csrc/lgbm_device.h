@@ -1,0 +1,243 @@
+// lgbm_device.h — device-side structures and arithmetic shared by the gfx950 kernels.
+//
+// The f64 arithmetic here restates the reference's CPU path operation for operation
+// (no contraction: the library is compiled with -ffp-contract=off; the only fused
+// multiply-add is the explicit one of GetLeafGainGivenOutput, gain.rs:204-220).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lgbm_hip.h"
+
+#define LGBM_WAVE 64
+#define LGBM_MAX_W 8                    // record words (16 B): features <= 16*W - 4
+#define HIST_THREADS 1024               // ConstructHistogram block
+#define HIST_MAX_BLOCKS 256             // one block per CU
+#define HIST_MIN_ROWS_PER_BLOCK 4096
+#define HIST_MAX_ROWS_PER_BLOCK ((1 << 19) - 1)  // packed 64-bit LDS cell field limits
+#define PART_THREADS 256
+#define PART_ROWS_PER_THREAD 8
+#define PART_TILE (PART_THREADS * PART_ROWS_PER_THREAD)
+#define PART_MAX_BLOCKS 1024
+#define SCAN_THREADS 128                // two waves: smaller leaf, larger leaf
+#define QUANT_ROWS_PER_LANE 32
+#define QUANT_LANE_MATS 6               // log2(64)
+#define QUANT_WAVE_MATS 26              // wave index bits (N <= 2^26 * 2048)
+
+// Buffer ids of the row stores.
+#define BUF_ORIG 0
+#define BUF_A 1
+#define BUF_B 2
+#define BUF_S0 3   // scratch (per-op entry points)
+#define BUF_S1 4
+#define NBUF 5
+
+// ctl->error bits
+#define ERR_SPIN 1
+#define ERR_ROOT_HESSIAN 2
+#define ERR_FEATURE 4
+
+struct DevFeature {
+  uint32_t num_bin;
+  int32_t offset;
+  uint32_t min_bin;
+  uint32_t max_bin;
+  uint32_t default_bin;
+  uint32_t mfb;
+  int32_t missing_type;
+  int32_t real_index;
+  uint32_t slot_off;   // first f64 cell of the feature in a leaf slot
+  uint32_t cell_base;  // first bin cell in the integer histogram (= slot_off / 2)
+  uint32_t ub_off;     // first bin_upper_bound entry
+  int32_t skip_default_bin;
+  int32_t na_as_missing;
+  int32_t run_forward;
+  int32_t _pad[2];
+};
+
+struct LeafSums {
+  double sg, sh, weight;
+  int32_t n;
+  int32_t _pad;
+};
+
+// Node routing parameters recorded at split time (the SplitInner router inputs,
+// data_partition.rs:387-417), used by the score-update traversal.
+struct NodeRoute {
+  int32_t f;          // feature position (record byte)
+  int32_t pmin;       // min_bin + offset
+  int32_t max_bin;
+  int32_t th;         // threshold + pmin (- 1 if mfb == 0)
+  int32_t na_bin;     // num_bin - 1
+  int32_t flags;      // 1: default_to_right, 2: na_as_missing, 4: default_left
+  int32_t left, right;
+};
+
+struct PartJob {
+  int32_t src_buf, dst_buf;
+  int64_t begin, count;
+  int32_t rev;        // source stored reversed
+  int32_t fbyte;      // feature byte in the record
+  int32_t pmin, max_bin, th, na_bin, flags;  // router
+  int32_t driver;     // 1: write tree / leaf bookkeeping
+};
+
+struct Ctl {
+  // ---- quantizer (per iteration) ----
+  double gs, hs, igs, ihs;
+  float vg1, vh1, vh3, _f0;
+  uint32_t max_g_bits, max_h_bits;  // |g|, |h| maxima as f32 bit patterns
+  uint32_t hmin_key, hmax_key;       // order-preserving keys of min/max hessian
+  int32_t quant_bins;
+  int32_t const_hess;
+  // ---- tree state ----
+  int32_t done, error, skip, pending_reduce;
+  int32_t num_leaves, max_leaves, max_depth, _i0;
+  int32_t left_leaf, right_leaf, smaller, larger;
+  int32_t split_leaf, split_f, new_right, node;
+  lgbm_split_info split;
+  LeafSums sm, lg;
+  // ---- histogram job ----
+  int32_t h_buf, _i1;
+  int64_t h_begin, h_count;
+  // ---- partition job + look-back bookkeeping ----
+  PartJob part;
+  uint32_t epoch;
+  int32_t part_ticket, part_exit;
+  int32_t part_left_count;
+  // ---- gain config ----
+  lgbm_gain_config cfg;
+};
+
+// ---------------------------------------------------------------------------
+// arithmetic helpers (restating crates/lgbm-compute/src/gain.rs)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double k_eps() { return (double)1e-15f; }
+
+__device__ __forceinline__ int32_t sat_i32(double x) {
+  if (x != x) return 0;
+  if (x >= 2147483647.0) return 2147483647;
+  if (x <= -2147483648.0) return (int32_t)(-2147483647 - 1);
+  return (int32_t)x;
+}
+__device__ __forceinline__ int8_t sat_i8(double x) {
+  if (x != x) return 0;
+  if (x >= 127.0) return 127;
+  if (x <= -128.0) return -128;
+  return (int8_t)(int32_t)x;
+}
+__device__ __forceinline__ int32_t round_int(double x) { return sat_i32(x + (double)0.5f); }
+
+__device__ __forceinline__ double threshold_l1(double s, double l1) {
+  double reg = fmax(0.0, fabs(s) - l1);
+  double pos = s > 0.0 ? 1.0 : 0.0;
+  double neg = s < 0.0 ? 1.0 : 0.0;
+  return (pos - neg) * reg;
+}
+__device__ __forceinline__ double leaf_gain(bool use_l1, double g, double h, double l1, double l2) {
+  if (use_l1) {
+    double s = threshold_l1(g, l1);
+    return (s * s) / (h + l2);
+  }
+  return (g * g) / (h + l2);
+}
+__device__ __forceinline__ double leaf_output(bool use_l1, double g, double h, double l1, double l2) {
+  if (use_l1) return -threshold_l1(g, l1) / (h + l2);
+  return -g / (h + l2);
+}
+__device__ __forceinline__ double leaf_output_full(bool use_l1, double g, double h, double l1,
+                                                   double l2, double mds, bool sm, double ps,
+                                                   int32_t n, double po) {
+  double base = leaf_output(use_l1, g, h, l1, l2);
+  bool clamp = mds > 0.0 && fabs(base) > mds;
+  double pos = base > 0.0 ? 1.0 : 0.0;
+  double neg = base < 0.0 ? 1.0 : 0.0;
+  double c = clamp ? (pos - neg) * mds : base;
+  if (sm) {
+    double nps = (double)n / ps;
+    return c * nps / (nps + 1.0) + po / (nps + 1.0);
+  }
+  return c;
+}
+__device__ __forceinline__ double leaf_gain_full(bool use_l1, double g, double h, double l1,
+                                                 double l2, double mds, bool sm, double ps,
+                                                 int32_t n, double po) {
+  if (mds > 0.0 || sm) {
+    double out = leaf_output_full(use_l1, g, h, l1, l2, mds, sm, ps, n, po);
+    double gg = use_l1 ? threshold_l1(g, l1) : g;
+    return -__builtin_fma(2.0 * gg, out, (h + l2) * out * out);
+  }
+  return leaf_gain(use_l1, g, h, l1, l2);
+}
+
+struct ScanCfg {
+  bool use_l1, use_smoothing, use_full;
+  double l1, l2, mds, ps, min_h, min_gain;
+  int32_t min_d;
+};
+
+__device__ __forceinline__ ScanCfg make_scan_cfg(const lgbm_gain_config& c) {
+  ScanCfg s;
+  s.use_l1 = c.lambda_l1 > 0.0;
+  s.use_smoothing = c.path_smooth > k_eps();
+  s.use_full = s.use_smoothing || c.max_delta_step > 0.0;
+  s.l1 = c.lambda_l1;
+  s.l2 = c.lambda_l2;
+  s.mds = c.max_delta_step;
+  s.ps = c.path_smooth;
+  s.min_h = c.min_sum_hessian_in_leaf;
+  s.min_gain = c.min_gain_to_split;
+  s.min_d = c.min_data_in_leaf;
+  return s;
+}
+
+__device__ __forceinline__ double split_gain_of(const ScanCfg& c, double lg, double lh, double rg,
+                                                double rh, int32_t lc, int32_t rc, double po) {
+  if (c.use_full)
+    return leaf_gain_full(c.use_l1, lg, lh, c.l1, c.l2, c.mds, c.use_smoothing, c.ps, lc, po) +
+           leaf_gain_full(c.use_l1, rg, rh, c.l1, c.l2, c.mds, c.use_smoothing, c.ps, rc, po);
+  return leaf_gain(c.use_l1, lg, lh, c.l1, c.l2) + leaf_gain(c.use_l1, rg, rh, c.l1, c.l2);
+}
+
+__device__ __forceinline__ void split_set_none(lgbm_split_info* s) {
+  s->threshold = 0;
+  s->left_count = 0;
+  s->right_count = 0;
+  s->default_left = 1;
+  s->gain = -__builtin_inf();
+  s->left_sum_gradient = 0.0;
+  s->left_sum_hessian = 0.0;
+  s->right_sum_gradient = 0.0;
+  s->right_sum_hessian = 0.0;
+  s->left_output = 0.0;
+  s->right_output = 0.0;
+}
+
+// split_gt (crates/lgbm-treelearner/src/split_info.rs:28-35)
+__device__ __forceinline__ bool split_gt(double ag, int32_t af, double bg, int32_t bf) {
+  if (ag != bg) return ag > bg;
+  int32_t x = af == -1 ? 0x7fffffff : af;
+  int32_t y = bf == -1 ? 0x7fffffff : bf;
+  return x < y;
+}
+
+__device__ __forceinline__ double maybe_round_to_zero(double v) {
+  const double z = (double)1e-35f;
+  return (v >= -z && v <= z) ? 0.0 : v;
+}
+
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & (LGBM_WAVE - 1); }
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  uint32_t l = lane_id();
+  return l == 0 ? 0ull : ((1ull << l) - 1ull);
+}
+
+// SplitInner router (data_partition.rs:387-417).
+__device__ __forceinline__ bool route_right(int32_t bin, int32_t pmin, int32_t max_bin, int32_t th,
+                                            int32_t na_bin, int32_t flags) {
+  if ((flags & 2) && bin == na_bin) return !(flags & 4);
+  if (bin < pmin || bin > max_bin) return (flags & 1) != 0;
+  return bin > th;
+}

@@ -1,0 +1,88 @@
+"""Synthetic inputs of BASELINE.json's configurations (no datasets offline).
+
+config1_like(): configs[1] — N rows x 28 float32 features (21 ~N(0,1), 7 derived as
+products / abs of pairs), logistic label logit = w.x + 0.5*x0*x1 + N(0, 0.1) with
+w ~ N(0,1), binned to <= max_bin quantile bins per feature (u8).  Binning sits
+outside the timed hot path; quantile cut points stand in for
+BinMapper::find_bin_from_column.  With `device` set to a torch CUDA device the
+generation and binning run there (same recipe, torch's generator).
+"""
+import numpy as np
+
+from ._abi import FeatureMeta
+
+DERIVED = [("mul", 0, 1), ("mul", 2, 3), ("abs", 4, None), ("mul", 5, 6), ("absmul", 7, 8),
+           ("mul", 9, 10), ("abs", 11, None)]
+
+
+def _meta_for(num_bins):
+    meta = []
+    for f, nb in enumerate(num_bins):
+        m = FeatureMeta()
+        m.num_bin = nb
+        m.offset = 1
+        m.min_bin = 0
+        m.max_bin = nb - 1
+        m.default_bin = nb
+        m.most_freq_bin = 0
+        m.missing_type = 0
+        m.real_feature_index = f
+        meta.append(m)
+    return meta
+
+
+def _derive(X, lib):
+    out = []
+    for kind, a, b in DERIVED:
+        if kind == "mul":
+            out.append(X[a] * X[b])
+        elif kind == "abs":
+            out.append(lib.abs(X[a]))
+        else:
+            out.append(lib.abs(X[a] * X[b]))
+    return out
+
+
+def config1_like(n, seed=0x5EED0001, max_bin=63, device=None):
+    if device is not None:
+        return _config1_torch(n, seed, max_bin, device)
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((21, n), dtype=np.float32)
+    X = np.concatenate([X, np.stack(_derive(X, np))], axis=0)
+    w = rng.standard_normal(28).astype(np.float32)
+    logit = w @ X + 0.5 * X[0] * X[1] + rng.normal(0, 0.1, n).astype(np.float32)
+    y = (rng.random(n, dtype=np.float32) < 1.0 / (1.0 + np.exp(-logit))).astype(np.float32)
+    bins = np.zeros((28, n), dtype=np.uint8)
+    upper, nbs = [], []
+    sample = X[:, :: max(1, n // 200000)]
+    for f in range(28):
+        qs = np.unique(np.quantile(sample[f], np.linspace(0, 1, max_bin + 1)[1:-1]).astype(np.float32))
+        bins[f] = np.searchsorted(qs, X[f], side="left").astype(np.uint8)
+        nbs.append(len(qs) + 1)
+        upper.extend([float(q) for q in qs] + [np.inf])
+    return bins, _meta_for(nbs), np.array(upper, dtype=np.float64), y
+
+
+def _config1_torch(n, seed, max_bin, device):
+    import torch
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    X = torch.randn((21, n), generator=gen, device=device, dtype=torch.float32)
+    X = torch.cat([X, torch.stack(_derive(X, torch))], dim=0)
+    w = torch.randn(28, generator=gen, device=device, dtype=torch.float32)
+    noise = torch.randn(n, generator=gen, device=device, dtype=torch.float32) * 0.1
+    logit = w @ X + 0.5 * X[0] * X[1] + noise
+    u = torch.rand(n, generator=gen, device=device, dtype=torch.float32)
+    y = (u < torch.sigmoid(logit)).to(torch.float32)
+    step = max(1, n // 200000)
+    qgrid = torch.linspace(0, 1, max_bin + 1, device=device, dtype=torch.float32)[1:-1]
+    bins = torch.empty((28, n), dtype=torch.uint8, device=device)
+    upper, nbs = [], []
+    for f in range(28):
+        qs = torch.unique(torch.quantile(X[f, ::step].contiguous(), qgrid))
+        bins[f] = torch.bucketize(X[f], qs, right=False).to(torch.uint8)
+        nbs.append(int(qs.numel()) + 1)
+        upper.extend([float(q) for q in qs.cpu()] + [float("inf")])
+    return (bins.cpu().numpy(), _meta_for(nbs), np.array(upper, dtype=np.float64),
+            y.cpu().numpy())

@@ -1,0 +1,329 @@
+"""HIP path vs the CPU oracle (and the reference's golden vectors), on a real MI355X.
+
+Bar: bit-exact for every integer / index result and for every f64 produced in the
+quantized (integer-exact) mode; the oracle is tests' checker only.
+"""
+import json
+import os
+import struct
+import sys
+
+import numpy as np
+import pytest
+
+from lightgbm_rs_amd import GainConfig, HipBackend
+from lightgbm_rs_amd._abi import BatchedFeature
+from oracle import oracle
+from tests.datagen import binary_gh, config1_like, make_binned
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def be():
+    b = HipBackend(0)
+    yield b
+    b.close()
+
+
+def bits(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint64 if a.dtype == np.float64 else np.uint32)
+
+
+def b64(x):
+    return struct.unpack("<Q", struct.pack("<d", float(x)))[0]
+
+
+def f64(bitlist):
+    return np.array(bitlist, dtype=np.uint64).view(np.float64)
+
+
+def slot_layout(meta):
+    offs, acc = [], 0
+    for m in meta:
+        offs.append(acc)
+        acc += 2 * m.num_bin
+    return offs, acc
+
+
+# ---------------------------------------------------------------------------
+# quantizer
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n,stochastic,seed", [(1000, False, 0), (1000, True, 3),
+                                               (300_001, True, 0x51702010),
+                                               (2_500_000, True, (7 << 20) ^ 0x51702010)])
+def test_quantize_matches_oracle(be, n, stochastic, seed):
+    say(f"quantize n={n} stochastic={stochastic} seed={seed}")
+    bins, meta, ub = make_binned(n, 3, seed=1)
+    g, h, _ = binary_gh(n, seed=2)
+    be.upload_resident_bins(bins, meta, ub)
+    be.upload_resident_grad_hess(g, h)
+    scales, dg, dh = be.discretize_dequantize_in_place(4, stochastic, seed, want_values=True)
+    og, oh, disc, oscales = oracle.quantize(g, h, bins=4, stochastic=stochastic, seed=seed)
+    assert np.array_equal(bits(scales), bits(oscales))
+    assert np.array_equal(be.discretized(), disc)
+    assert np.array_equal(bits(dg), bits(og))
+    assert np.array_equal(bits(dh), bits(oh))
+
+
+def test_quantize_constant_hessian(be):
+    n = 5000
+    bins, meta, ub = make_binned(n, 2, seed=4)
+    g = np.random.default_rng(5).normal(size=n).astype(np.float32)
+    h = np.ones(n, np.float32)
+    be.upload_resident_bins(bins, meta, ub)
+    be.upload_resident_grad_hess(g, h)
+    scales, dg, dh = be.discretize_dequantize_in_place(4, True, 11, want_values=True)
+    og, oh, disc, osc = oracle.quantize(g, h, bins=4, stochastic=True, seed=11)
+    assert np.array_equal(be.discretized(), disc)
+    assert np.array_equal(bits(scales), bits(osc))
+
+
+# ---------------------------------------------------------------------------
+# ConstructHistogram
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n,F,subset", [(20_000, 7, False), (20_000, 7, True),
+                                        (1_000_003, 28, False), (1_000_003, 28, True)])
+def test_int_histogram_matches_oracle(be, n, F, subset):
+    say(f"int histogram n={n} F={F} subset={subset}")
+    bins, meta, ub = make_binned(n, F, seed=n + F)
+    g, h, _ = binary_gh(n, seed=3)
+    be.upload_resident_bins(bins, meta, ub)
+    be.upload_resident_grad_hess(g, h)
+    be.discretize_dequantize_in_place(4, True, 99)
+    disc = be.discretized()
+    rows = None
+    if subset:
+        rows = np.sort(np.random.default_rng(7).choice(n, size=n // 3, replace=False)).astype(np.uint32)
+    got = be.construct_int_histogram(rows)
+    offs, total = slot_layout(meta)
+    r = np.arange(n, dtype=np.uint32) if rows is None else rows
+    for f, m in enumerate(meta):
+        exp = oracle.int_histogram(bins[f].astype(np.uint32), disc, r, m.num_bin)
+        assert np.array_equal(got[offs[f]:offs[f] + 2 * m.num_bin], exp), f"feature {f}"
+
+
+@pytest.mark.parametrize("n,F", [(30_000, 9), (400_000, 28)])
+def test_leaf_histogram_bit_exact_vs_f64_fold(be, n, F):
+    """Integer build + exact f64 conversion + FixHistogram + compaction equals the
+    reference's ascending-row f64 fold of the dequantized values (build_leaf_histogram_into)."""
+    say(f"leaf histogram n={n} F={F}")
+    bins, meta, ub = make_binned(n, F, seed=F)
+    g, h, _ = binary_gh(n, seed=5)
+    be.upload_resident_bins(bins, meta, ub)
+    be.upload_resident_grad_hess(g, h)
+    _, dg, dh = be.discretize_dequantize_in_place(4, True, 1234, want_values=True)
+    rows = np.sort(np.random.default_rng(1).choice(n, size=n // 2, replace=False)).astype(np.uint32)
+    # leaf sums with kEpsilon-style provenance (not exactly the fold) to exercise the fix
+    sg = float(np.sum(dg[rows].astype(np.float64))) + 1e-15
+    sh = float(np.sum(dh[rows].astype(np.float64))) + 2e-15
+    got = be.build_resident_leaf(rows, sg, sh)
+    offs, total = slot_layout(meta)
+    for f, m in enumerate(meta):
+        hist = oracle.construct_histogram(bins[f][rows], dg[rows], dh[rows], m.num_bin)
+        hist = oracle.fix_histogram(hist, m.num_bin, m.most_freq_bin, sg, sh)
+        hist = oracle.compact_histogram(hist, m.num_bin, m.offset)
+        assert np.array_equal(bits(got[offs[f]:offs[f] + 2 * m.num_bin]), bits(hist)), f"feature {f}"
+
+
+# ---------------------------------------------------------------------------
+# FindBestThreshold
+# ---------------------------------------------------------------------------
+def _golden_cfg(c):
+    return GainConfig.make(min_data_in_leaf=c["min_data_in_leaf"],
+                           min_sum_hessian_in_leaf=f64([c["min_sum_hessian_in_leaf_bits"]])[0],
+                           lambda_l1=f64([c["lambda_l1_bits"]])[0],
+                           lambda_l2=f64([c["lambda_l2_bits"]])[0],
+                           min_gain_to_split=f64([c["min_gain_to_split_bits"]])[0])
+
+
+def test_find_best_splits_golden(be):
+    """kernels/split.txt winners (kernel_parity.rs:512), bit-exact on the device scan."""
+    cases = json.load(open(os.path.join(GOLD, "split_scan.json")))
+    for c in cases:
+        bf = BatchedFeature(0, c["num_bin"], c["offset"], c["default_bin"], 0,
+                            c["skip_default_bin"], c["na_as_missing"], 1, 0)
+        [si] = be.find_best_splits_batched(f64(c["hist_bits"]), [bf], _golden_cfg(c),
+                                           f64([c["sum_gradient_bits"]])[0],
+                                           f64([c["sum_hessian_bits"]])[0], c["num_data"])
+        w = c["win"]
+        assert (si.gain == -np.inf) == (not w["is_splittable"]), c["name"]
+        if w["is_splittable"]:
+            for k in ["gain", "left_sum_gradient", "left_sum_hessian", "right_sum_gradient",
+                      "right_sum_hessian", "left_output", "right_output"]:
+                assert b64(getattr(si, k)) == w[k + "_bits"], (c["name"], k)
+            assert (si.threshold, si.left_count, si.right_count, si.default_left) == (
+                w["threshold"], w["left_count"], w["right_count"], w["default_left"]), c["name"]
+
+
+def _random_scan_case(rng, nb):
+    g = rng.normal(0, 1, nb) * (rng.random(nb) < 0.9)
+    h = rng.random(nb) * 3 * (rng.random(nb) < 0.9)
+    hist = np.empty(2 * nb)
+    hist[0::2], hist[1::2] = g, h
+    return hist
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_find_best_splits_random_vs_oracle(be, seed):
+    rng = np.random.default_rng(seed)
+    feats, hists = [], []
+    off = 0
+    for j in range(24):
+        nb = int(rng.choice([2, 3, 5, 17, 63, 64, 65, 130, 256]))
+        mt = int(rng.integers(0, 3)) if nb > 2 else 0
+        offset = int(rng.integers(0, 2))
+        defb = int(rng.integers(0, nb + 1))
+        hist = _random_scan_case(rng, nb)
+        feats.append(BatchedFeature(off, nb, offset, defb, 0, int(nb > 2 and mt == 1),
+                                    int(nb > 2 and mt == 2), int(nb > 2 and mt != 0), 0))
+        hists.append(hist)
+        off += 2 * nb
+    allh = np.concatenate(hists)
+    cfgs = [GainConfig.make(min_data_in_leaf=int(rng.integers(0, 30)),
+                            min_sum_hessian_in_leaf=float(rng.choice([0.0, 1e-3, 0.5]))),
+            GainConfig.make(min_data_in_leaf=3, lambda_l1=0.3, lambda_l2=1.5, min_gain_to_split=0.1),
+            GainConfig.make(min_data_in_leaf=2, max_delta_step=0.7),
+            GainConfig.make(min_data_in_leaf=2, path_smooth=2.0, lambda_l2=0.5)]
+    for cfg in cfgs:
+        cfg.parent_output = float(rng.normal())
+        sg = float(rng.normal() * 5)
+        sh = float(rng.random() * 40 + 1)
+        n = int(rng.integers(50, 5000))
+        got = be.find_best_splits_batched(allh, feats, cfg, sg, sh, n)
+        for j, bf in enumerate(feats):
+            exp = oracle.find_best_split(hists[j], cfg, bf.num_bin, bf.offset, bf.default_bin,
+                                         bf.skip_default_bin, bf.na_as_missing, bf.run_forward,
+                                         sg, sh, n)
+            gd, ed = got[j].as_dict(), exp.as_dict()
+            for k in ed:
+                if isinstance(ed[k], float):
+                    assert b64(gd[k]) == b64(ed[k]), (seed, j, k, gd[k], ed[k])
+                else:
+                    assert gd[k] == ed[k], (seed, j, k)
+
+
+# ---------------------------------------------------------------------------
+# subtract / partition
+# ---------------------------------------------------------------------------
+def test_subtract_golden(be):
+    for c in json.load(open(os.path.join(GOLD, "subtract.json"))):
+        got = be.subtract_histograms(f64(c["parent_bits"]), f64(c["child_bits"]))
+        assert np.array_equal(bits(got), np.array(c["derived_bits"], dtype=np.uint64))
+
+
+def test_partition_golden(be):
+    for c in json.load(open(os.path.join(GOLD, "partition.json"))):
+        if c["missing_type"] != 0:
+            continue
+        order, split = be.data_partition(c["bins"], c["num_bin"], c["min_bin"], c["max_bin"],
+                                         c["threshold"], c["most_freq_bin"])
+        assert order.tolist() == c["order"], c["name"]
+        assert split == c["split_point"], c["name"]
+
+
+@pytest.mark.parametrize("n", [1, 2047, 2048, 2049, 100_000, 1_234_567])
+def test_partition_random_vs_oracle(be, n):
+    say(f"partition n={n}")
+    rng = np.random.default_rng(n)
+    nb = 64
+    bins = rng.integers(0, nb, n).astype(np.uint32)
+    for (mn, mx, thr, mfb, na, dl) in [(0, 63, 20, 0, 0, 0), (1, 62, 40, 5, 1, 1),
+                                       (0, 63, 62, 63, 1, 0), (3, 10, 5, 0, 0, 0)]:
+        got, gl = be.data_partition(bins, nb, mn, mx, thr, mfb, na, dl)
+        exp, el = oracle.data_partition(bins, nb, mn, mx, thr, mfb, na, dl)
+        assert gl == el
+        assert np.array_equal(got, exp)
+
+
+def test_partition_errors(be):
+    from lightgbm_rs_amd import HipError
+    with pytest.raises(HipError) as e:
+        be.data_partition([0, 9], 8, 0, 7, 3, 0)
+    assert e.value.code == -2
+    with pytest.raises(HipError) as e:
+        be.data_partition([0, 1], 8, 0, 7, 8, 0)
+    assert e.value.code == -4
+
+
+# ---------------------------------------------------------------------------
+# whole tree (coarse seam) vs the oracle learner
+# ---------------------------------------------------------------------------
+def _compare_trees(t, o, tag):
+    assert t["num_leaves"] == o["num_leaves"], tag
+    for k in o:
+        if k == "num_leaves":
+            continue
+        a, b = np.asarray(t[k]), np.asarray(o[k])
+        if a.dtype.kind == "f":
+            assert np.array_equal(bits(a), bits(b)), (tag, k)
+        else:
+            assert np.array_equal(a, b), (tag, k)
+
+
+@pytest.mark.parametrize("n,F,nl,md,seed", [
+    (500, 3, 8, -1, 1),
+    (20_000, 9, 31, -1, 2),
+    (20_000, 9, 63, 4, 3),
+    (200_000, 28, 255, -1, 4),
+])
+def test_grow_tree_matches_oracle(be, n, F, nl, md, seed):
+    say(f"grow_tree n={n} F={F} num_leaves={nl} max_depth={md}")
+    bins, meta, ub = make_binned(n, F, seed=seed)
+    g, h, _ = binary_gh(n, seed=seed)
+    be.upload_resident_bins(bins, meta, ub)
+    be.upload_resident_grad_hess(g, h)
+    _, dg, dh = be.discretize_dequantize_in_place(4, True, seed * 77, want_values=True)
+    og, oh, _, _ = oracle.quantize(g, h, bins=4, stochastic=True, seed=seed * 77)
+    assert np.array_equal(bits(dg), bits(og))
+    cfg = GainConfig.make(min_data_in_leaf=20)
+    t, lay = be.grow_tree_on_device_with_cfg(cfg, nl, md)
+    o, olay = oracle.train_tree(bins, meta, ub, og, oh, cfg, nl, md)
+    _compare_trees(t, o, (n, F, nl))
+    assert np.array_equal(lay["leaf_begin"], olay["leaf_begin"])
+    assert np.array_equal(lay["leaf_count"], olay["leaf_count"])
+    assert np.array_equal(lay["indices"], olay["indices"])
+
+
+def test_grow_tree_config1_shape(be):
+    """Config-1 shaped (quantile-binned, 28 features, max_bin 63, 255 leaves) at 1M rows."""
+    n = 1_000_000
+    say(f"grow_tree config1-like n={n}")
+    bins, meta, ub, y = config1_like(n)
+    g, h, _ = binary_gh(n, seed=9)
+    be.upload_resident_bins(bins, meta, ub)
+    be.upload_resident_grad_hess(g, h)
+    _, dg, dh = be.discretize_dequantize_in_place(4, True, 0x51702010, want_values=True)
+    og, oh, _, _ = oracle.quantize(g, h, bins=4, stochastic=True, seed=0x51702010)
+    cfg = GainConfig.make(min_data_in_leaf=20)
+    t, lay = be.grow_tree_on_device_with_cfg(cfg, 255, -1)
+    o, olay = oracle.train_tree(bins, meta, ub, og, oh, cfg, 255, -1)
+    _compare_trees(t, o, "config1")
+    assert np.array_equal(lay["indices"], olay["indices"])
+
+
+def test_train_binary_matches_oracle(be):
+    """Five resident boosting iterations (objective -> quantize -> grow -> score)."""
+    n, iters, nl = 50_000, 5, 31
+    bins, meta, ub, y = config1_like(n, seed=3)
+    init = oracle.boost_from_score(y)
+    be.upload_resident_bins(bins, meta, ub)
+    be.set_labels(y, init)
+    cfg = GainConfig.make(min_data_in_leaf=20)
+    trees = [be.train_iter_binary(i, cfg, nl, -1, 0.1) for i in range(iters)]
+    scores = be.scores()
+    oscores, otrees = oracle.train_binary(bins, meta, ub, y, cfg, nl, -1, iters, 0.1)
+    # the first tree carries add_bias(init) in the oracle model; compare structure
+    same = sum(int(np.array_equal(t["split_feature"], o["split_feature"]) and
+                   np.array_equal(t["threshold_in_bin"], o["threshold_in_bin"]) and
+                   np.array_equal(t["leaf_count"], o["leaf_count"]))
+               for t, o in zip(trees, otrees))
+    assert same == iters
+    np.testing.assert_allclose(scores, oscores, rtol=0, atol=1e-9)
