@@ -275,6 +275,14 @@ int lgbm_hip_set_timing(lgbm_hip_ctx* ctx, int32_t enable);
 int lgbm_hip_get_timing(lgbm_hip_ctx* ctx, double* ms_out5, double* hist_bytes_out,
                         int64_t* hist_launches_out);
 
+/* Counters since the last lgbm_hip_set_timing (no reference counterpart; the
+ * reference's equivalent is its env-gated phase profiler, lgbm-treelearner/src/
+ * phase_prof.rs:1-60).  out[0..4]: ms per kernel family as above; [5] root
+ * ConstructHistogram rows; [6] root ConstructHistogram launches; [7] rows moved by
+ * partition passes (which also build the left child's histogram); [8] partition
+ * launches; [9] bytes per row record; [10] features; [11] histogram cells. */
+int lgbm_hip_get_stats(lgbm_hip_ctx* ctx, double* out12);
+
 #ifdef __cplusplus
 }
 #endif

@@ -212,14 +212,13 @@ class HipBackend:
         self._check(self.lib.lgbm_hip_set_timing(self.ctx, C.c_int32(int(enable))))
 
     def timing(self):
-        ms = np.zeros(5, np.float64)
-        nbytes = C.c_double(0)
-        launches = C.c_int64(0)
-        self._check(self.lib.lgbm_hip_get_timing(self.ctx, ptr(ms, C.c_double), C.byref(nbytes),
-                                                 C.byref(launches)))
-        return {"hist_ms": ms[0], "partition_ms": ms[1], "scan_ms": ms[2], "quant_ms": ms[3],
-                "objective_ms": ms[4], "hist_bytes": nbytes.value,
-                "hist_launches": launches.value}
+        """Per-family device ms (HIP events) and row counters since set_timing."""
+        st = np.zeros(12, np.float64)
+        self._check(self.lib.lgbm_hip_get_stats(self.ctx, ptr(st, C.c_double)))
+        keys = ["hist_ms", "partition_ms", "scan_ms", "quant_ms", "objective_ms", "root_rows",
+                "hist_launches", "partition_rows", "partition_launches", "record_bytes",
+                "features", "cells"]
+        return {k: float(v) for k, v in zip(keys, st)}
 
 
 def feature_meta(num_bin, most_freq_bin=0, missing_type=0, default_bin=None, real_index=0,

@@ -7,6 +7,7 @@
 #include <array>
 #include <cstddef>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -51,20 +52,32 @@ struct lgbm_hip_ctx {
   int64_t tile_cap = 0;
   uint64_t *wave_mats = nullptr, *lane_mats = nullptr;
   double* stats = nullptr;
+  uint4* partials = nullptr;  // per-block g/h statistics
   // tree-sized
   int32_t lcap = 0;
   double* slots = nullptr;
   lgbm_split_info *feat_split = nullptr, *best = nullptr;
   int32_t* best_feat = nullptr;
+  int32_t* best_fpos = nullptr;
+  int32_t* int_slots = nullptr;
   uint8_t* splittable = nullptr;
   DevLeaves leaves{};
   DevTree tree{};
+  void* tree_blob = nullptr;   // device tree arrays, one allocation
+  void* tree_host = nullptr;   // pinned staging for the one-copy readback
+  size_t tree_blob_bytes = 0;
+  size_t tree_off[16] = {};
   // scratch
   void* scratch = nullptr;
   size_t scratch_cap = 0;
   double* slot_tmp = nullptr;
   uint32_t* d_indices = nullptr;
   int64_t indices_cap = 0;
+  // captured per-tree launch sequence (all parameters live in device memory)
+  hipGraphExec_t graph_exec = nullptr;
+  int32_t graph_nl = -1, graph_md = 0;
+  uint64_t graph_gen = 0, buf_gen = 1;
+  bool use_graphs = true;
   // timing
   bool timing = false;
   std::vector<EventPair> ev_pool;
@@ -125,8 +138,8 @@ int init_jump_tables(lgbm_hip_ctx* c) {
   for (int i = 0; i < 64; ++i) m[i] = xs_step(1ull << i);
   // T = M^(2*C): two draws per row, C rows per lane
   Mat t = m;
-  static_assert(QUANT_ROWS_PER_LANE == 32, "2*C must be 64 = 2^6");
-  for (int i = 0; i < 6; ++i) t = mat_mul(t, t);
+  static_assert(QUANT_ROWS_PER_LANE == 16, "2*C must be 32 = 2^5");
+  for (int i = 0; i < 5; ++i) t = mat_mul(t, t);
   std::vector<uint64_t> lane(QUANT_LANE_MATS * 64), wave(QUANT_WAVE_MATS * 64);
   Mat r = t;
   for (int k = 0; k < QUANT_LANE_MATS; ++k) {
@@ -162,6 +175,8 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.feat_split = c->feat_split;
   L.best = c->best;
   L.best_feat = c->best_feat;
+  L.best_fpos = c->best_fpos;
+  L.int_slots = c->int_slots;
   L.splittable = c->splittable;
   L.tile_state = c->tile_state;
   L.stats = c->stats;
@@ -196,6 +211,7 @@ int ensure_scratch_rows(lgbm_hip_ctx* c, int64_t n) {
     rc = dalloc(c, &c->gh[b], (size_t)std::max<int64_t>(n, 1));
     if (rc) return rc;
     c->buf_rows[b] = n;
+    c->buf_gen++;
   }
   return LGBM_HIP_OK;
 }
@@ -212,6 +228,7 @@ int ensure_scratch_bytes(lgbm_hip_ctx* c, size_t bytes) {
 int ensure_tile_state(lgbm_hip_ctx* c, int64_t rows) {
   const int64_t tiles = (rows + PART_TILE - 1) / PART_TILE + 1;
   if (c->tile_cap >= tiles) return LGBM_HIP_OK;
+  c->buf_gen++;
   int rc = dalloc(c, &c->tile_state, (size_t)tiles);
   if (rc) return rc;
   HIPCHK(c, hipMemset(c->tile_state, 0, (size_t)tiles * 8));
@@ -232,23 +249,42 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   if ((rc = dalloc(c, &c->leaves.count, (size_t)L))) return rc;
   if ((rc = dalloc(c, &c->leaves.buf, (size_t)L))) return rc;
   if ((rc = dalloc(c, &c->leaves.rev, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &c->best_fpos, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &c->int_slots, (size_t)L * c->total_cells * 3))) return rc;
+  if ((rc = dalloc(c, &c->tree.nodes, (size_t)L))) return rc;
+  // tree arrays: one device blob (one readback per tree) + pinned host staging
+  const size_t sizes[15] = {64, 4, 4, 8, 4, 1, 4, 4, 8, 4, 8, 8, 4, 4, 4};
+  size_t off = 0;
+  for (int i = 0; i < 15; ++i) {
+    c->tree_off[i] = off;
+    off += ((i == 0 ? 64 : sizes[i] * (size_t)L) + 15) / 16 * 16;
+  }
+  c->tree_blob_bytes = off;
+  if (c->tree_blob) (void)hipFree(c->tree_blob);
+  if (c->tree_host) (void)hipHostFree(c->tree_host);
+  c->tree_blob = nullptr;
+  c->tree_host = nullptr;
+  HIPCHK(c, hipMalloc(&c->tree_blob, off));
+  HIPCHK(c, hipHostMalloc(&c->tree_host, off, hipHostMallocDefault));
+  char* base = (char*)c->tree_blob;
   DevTree& T = c->tree;
-  if ((rc = dalloc(c, &T.split_feature, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.threshold_in_bin, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.threshold, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.split_gain, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.decision_type, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.left_child, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.right_child, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.internal_value, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.internal_count, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.leaf_value, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.leaf_weight, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.leaf_count, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.leaf_depth, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.leaf_parent, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &T.nodes, (size_t)L))) return rc;
+  T.header = (int32_t*)(base + c->tree_off[0]);
+  T.split_feature = (int32_t*)(base + c->tree_off[1]);
+  T.threshold_in_bin = (uint32_t*)(base + c->tree_off[2]);
+  T.threshold = (double*)(base + c->tree_off[3]);
+  T.split_gain = (float*)(base + c->tree_off[4]);
+  T.decision_type = (int8_t*)(base + c->tree_off[5]);
+  T.left_child = (int32_t*)(base + c->tree_off[6]);
+  T.right_child = (int32_t*)(base + c->tree_off[7]);
+  T.internal_value = (double*)(base + c->tree_off[8]);
+  T.internal_count = (int32_t*)(base + c->tree_off[9]);
+  T.leaf_value = (double*)(base + c->tree_off[10]);
+  T.leaf_weight = (double*)(base + c->tree_off[11]);
+  T.leaf_count = (int32_t*)(base + c->tree_off[12]);
+  T.leaf_depth = (int32_t*)(base + c->tree_off[13]);
+  T.leaf_parent = (int32_t*)(base + c->tree_off[14]);
   c->lcap = L;
+  c->buf_gen++;
   return LGBM_HIP_OK;
 }
 
@@ -291,8 +327,8 @@ int check_ctx(lgbm_hip_ctx* c) {
 int do_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_t seed, float* dg,
                 float* dh) {
   ev_begin(c, FAM_QUANT);
-  launch_absmax(c->g, c->h, c->N, c->ctl, c->stream);
-  launch_quant_scales(c->ctl, bins, -1, c->stream);
+  launch_absmax(c->g, c->h, c->N, c->partials, c->stream);
+  launch_quant_scales(c->ctl, c->partials, c->N, bins, -1, c->stream);
   launch_quantize(c->g, c->h, c->N, c->ctl, c->wave_mats, c->lane_mats,
                   seed ^ 0x9E3779B97F4A7C15ull, stochastic, c->gh[BUF_ORIG], dg, dh, c->stream);
   ev_end(c);
@@ -302,12 +338,10 @@ int do_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_t seed
   return LGBM_HIP_OK;
 }
 
-int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_leaves,
-                    int32_t max_depth) {
-  int rc = ensure_leaves(c, num_leaves);
-  if (rc) return rc;
-  HIPCHK(c, hipMemcpyAsync((char*)c->ctl + CTL_OFF(cfg), cfg, sizeof(*cfg), hipMemcpyHostToDevice,
-                           c->stream));
+// The per-tree kernel sequence: root histogram + scan (whose last block picks split
+// 1), then per split s a partition pass (which also builds the left child's
+// histogram) and, unless it is the last split, the scan that picks split s + 1.
+void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth) {
   DevLearner L = make_learner(c);
   launch_tree_init(L, num_leaves, max_depth, c->stream);
   ev_begin(c, FAM_HIST);
@@ -317,59 +351,86 @@ int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_le
   launch_fixscan(L, 1, nullptr, c->stream);
   ev_end(c);
   for (int32_t s = 1; s < num_leaves; ++s) {
-    ev_begin(c, FAM_SCAN);
-    launch_split(L, c->stream);
-    ev_end(c);
     ev_begin(c, FAM_PART);
     launch_partition(L, c->W, s == 1 ? c->N : 0, c->stream);
     ev_end(c);
     if (s + 1 < num_leaves) {
-      ev_begin(c, FAM_HIST);
-      launch_hist(L, 1, 0, c->stream);
-      ev_end(c);
       ev_begin(c, FAM_SCAN);
       launch_fixscan(L, 0, nullptr, c->stream);
       ev_end(c);
     }
   }
-  HIPCHK(c, hipGetLastError());
+}
+
+int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_leaves,
+                    int32_t max_depth) {
+  int rc = ensure_leaves(c, num_leaves);
+  if (rc) return rc;
+  HIPCHK(c, hipMemcpyAsync((char*)c->ctl + CTL_OFF(cfg), cfg, sizeof(*cfg), hipMemcpyHostToDevice,
+                           c->stream));
+  if (c->timing || !c->use_graphs) {
+    enqueue_tree(c, num_leaves, max_depth);
+    HIPCHK(c, hipGetLastError());
+    return LGBM_HIP_OK;
+  }
+  if (!(c->graph_exec && c->graph_nl == num_leaves && c->graph_md == max_depth &&
+        c->graph_gen == c->buf_gen)) {
+    if (c->graph_exec) {
+      (void)hipGraphExecDestroy(c->graph_exec);
+      c->graph_exec = nullptr;
+    }
+    hipGraph_t g = nullptr;
+    HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    enqueue_tree(c, num_leaves, max_depth);
+    HIPCHK(c, hipStreamEndCapture(c->stream, &g));
+    hipError_t e = hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+      c->graph_exec = nullptr;
+      return set_err(c, LGBM_HIP_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    }
+    c->graph_nl = num_leaves;
+    c->graph_md = max_depth;
+    c->graph_gen = c->buf_gen;
+  }
+  HIPCHK(c, hipGraphLaunch(c->graph_exec, c->stream));
   return LGBM_HIP_OK;
 }
 
 int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, double shrink) {
+  DevLearner L0 = make_learner(c);
+  launch_tree_finalize(L0, c->stream);
+  HIPCHK(c, hipMemcpyAsync(c->tree_host, c->tree_blob, out ? c->tree_blob_bytes : 64,
+                           hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
   ev_collect(c);
-  int32_t nl = 0, err = 0;
-  int rc = ctl_read(c, CTL_OFF(num_leaves), &nl);
-  if (rc) return rc;
-  rc = ctl_read(c, CTL_OFF(error), &err);
-  if (rc) return rc;
+  const char* hb = (const char*)c->tree_host;
+  const int32_t nl = ((const int32_t*)hb)[0], err = ((const int32_t*)hb)[1];
+  int rc = 0;
   if (err & ERR_ROOT_HESSIAN)
     return set_err(c, LGBM_HIP_ERR_INVALID_LEAF_HESSIAN, "root sum_hessian <= 0");
   if (err & ERR_SPIN) return set_err(c, LGBM_HIP_ERR_RUNTIME, "partition look-back spin limit");
   if (err) return set_err(c, LGBM_HIP_ERR_RUNTIME, "device learner error");
   if (out) {
     out->num_leaves = nl;
-    const DevTree& T = c->tree;
     const size_t ni = (size_t)std::max(nl - 1, 0), nl_ = (size_t)nl;
-    auto cp = [&](void* dst, const void* src, size_t bytes) -> int {
-      if (dst && bytes) HIPCHK(c, hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
-      return LGBM_HIP_OK;
+    auto cp = [&](void* dst, int idx, size_t bytes) {
+      if (dst && bytes) std::memcpy(dst, hb + c->tree_off[idx], bytes);
     };
-    if ((rc = cp(out->split_feature, T.split_feature, ni * 4))) return rc;
-    if ((rc = cp(out->threshold_in_bin, T.threshold_in_bin, ni * 4))) return rc;
-    if ((rc = cp(out->threshold, T.threshold, ni * 8))) return rc;
-    if ((rc = cp(out->split_gain, T.split_gain, ni * 4))) return rc;
-    if ((rc = cp(out->decision_type, T.decision_type, ni))) return rc;
-    if ((rc = cp(out->left_child, T.left_child, ni * 4))) return rc;
-    if ((rc = cp(out->right_child, T.right_child, ni * 4))) return rc;
-    if ((rc = cp(out->internal_value, T.internal_value, ni * 8))) return rc;
-    if ((rc = cp(out->internal_count, T.internal_count, ni * 4))) return rc;
-    if ((rc = cp(out->leaf_value, T.leaf_value, nl_ * 8))) return rc;
-    if ((rc = cp(out->leaf_weight, T.leaf_weight, nl_ * 8))) return rc;
-    if ((rc = cp(out->leaf_count, T.leaf_count, nl_ * 4))) return rc;
-    if ((rc = cp(out->leaf_depth, T.leaf_depth, nl_ * 4))) return rc;
-    if ((rc = cp(out->leaf_parent, T.leaf_parent, nl_ * 4))) return rc;
+    cp(out->split_feature, 1, ni * 4);
+    cp(out->threshold_in_bin, 2, ni * 4);
+    cp(out->threshold, 3, ni * 8);
+    cp(out->split_gain, 4, ni * 4);
+    cp(out->decision_type, 5, ni);
+    cp(out->left_child, 6, ni * 4);
+    cp(out->right_child, 7, ni * 4);
+    cp(out->internal_value, 8, ni * 8);
+    cp(out->internal_count, 9, ni * 4);
+    cp(out->leaf_value, 10, nl_ * 8);
+    cp(out->leaf_weight, 11, nl_ * 8);
+    cp(out->leaf_count, 12, nl_ * 4);
+    cp(out->leaf_depth, 13, nl_ * 4);
+    cp(out->leaf_parent, 14, nl_ * 4);
     if (shrink != 1.0) {
       // Tree::shrinkage (tree.rs:1074): MaybeRoundToZero(v * rate)
       const double z = (double)1e-35f;
@@ -444,12 +505,13 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   Ctl init;
   std::memset(&init, 0, sizeof(init));
   init.epoch = 1u;
-  init.hmin_key = 0xffffffffu;
   if (hipMemcpy(c->ctl, &init, sizeof(init), hipMemcpyHostToDevice) != hipSuccess)
     return fail(set_err(c, LGBM_HIP_ERR_HIP, "ctl init"));
   if ((rc = dalloc(c, &c->stats, 4))) return fail(rc);
   if (hipMemset(c->stats, 0, 32) != hipSuccess) return fail(set_err(c, LGBM_HIP_ERR_HIP, "stats"));
   if ((rc = init_jump_tables(c))) return fail(rc);
+  if ((rc = dalloc(c, &c->partials, STAT_BLOCKS))) return fail(rc);
+  if (const char* e = std::getenv("LGBM_HIP_GRAPHS")) c->use_graphs = std::strcmp(e, "0") != 0;
   *out = c;
   return LGBM_HIP_OK;
 }
@@ -458,6 +520,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   if (!c) return LGBM_HIP_OK;
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
+  if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
   auto F = [](void* p) {
     if (p) (void)hipFree(p);
   };
@@ -477,6 +540,11 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->wave_mats);
   F(c->lane_mats);
   F(c->stats);
+  F(c->partials);
+  F(c->best_fpos);
+  F(c->int_slots);
+  F(c->tree_blob);
+  if (c->tree_host) (void)hipHostFree(c->tree_host);
   F(c->slots);
   F(c->feat_split);
   F(c->best);
@@ -487,20 +555,6 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->leaves.buf);
   F(c->leaves.rev);
   DevTree& T = c->tree;
-  F(T.split_feature);
-  F(T.threshold_in_bin);
-  F(T.threshold);
-  F(T.split_gain);
-  F(T.decision_type);
-  F(T.left_child);
-  F(T.right_child);
-  F(T.internal_value);
-  F(T.internal_count);
-  F(T.leaf_value);
-  F(T.leaf_weight);
-  F(T.leaf_count);
-  F(T.leaf_depth);
-  F(T.leaf_parent);
   F(T.nodes);
   F(c->scratch);
   F(c->slot_tmp);
@@ -610,6 +664,7 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   if (e != hipSuccess) return set_err(c, LGBM_HIP_ERR_HIP, hipGetErrorString(e));
   c->have_bins = true;
   c->have_grad = c->quant_ready = c->have_labels = false;
+  c->buf_gen++;
   return LGBM_HIP_OK;
 }
 
@@ -897,12 +952,12 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "device learner requires num_grad_quant_bins in {2, 4}");
   ev_begin(c, FAM_OBJ);
-  launch_grad_binary(c->score, c->label, c->g, c->h, c->N, c->ctl, c->stream);
+  launch_grad_binary(c->score, c->label, c->g, c->h, c->N, c->partials, c->stream);
   ev_end(c);
   c->have_grad = true;
   const uint64_t seed = ((uint64_t)(uint32_t)iter << 20) ^ 0ull ^ 0x51702010ull;  // gbdt.rs:950
   ev_begin(c, FAM_QUANT);
-  launch_quant_scales(c->ctl, num_grad_quant_bins, -1, c->stream);
+  launch_quant_scales(c->ctl, c->partials, c->N, num_grad_quant_bins, -1, c->stream);
   launch_quantize(c->g, c->h, c->N, c->ctl, c->wave_mats, c->lane_mats,
                   seed ^ 0x9E3779B97F4A7C15ull, stochastic, c->gh[BUF_ORIG], nullptr, nullptr,
                   c->stream);
@@ -941,22 +996,34 @@ int lgbm_hip_set_timing(lgbm_hip_ctx* c, int32_t enable) {
 
 int lgbm_hip_get_timing(lgbm_hip_ctx* c, double* ms_out5, double* hist_bytes_out,
                         int64_t* hist_launches_out) {
+  double st[12];
+  int rc = lgbm_hip_get_stats(c, st);
+  if (rc) return rc;
+  if (ms_out5)
+    for (int i = 0; i < 5; ++i) ms_out5[i] = st[i];
+  // root ConstructHistogram algorithmic bytes: rows x (F bins + 2 B packed g/h)
+  // + the histogram write (cells x 2 x 4 B) per launch
+  if (hist_bytes_out) *hist_bytes_out = st[5] * (st[10] + 2.0) + st[6] * st[11] * 8.0;
+  if (hist_launches_out) *hist_launches_out = (int64_t)(st[6] + 0.5);
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_get_stats(lgbm_hip_ctx* c, double* out) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
   HIPCHK(c, hipStreamSynchronize(c->stream));
   ev_collect(c);
-  if (ms_out5)
-    for (int i = 0; i < 5; ++i) ms_out5[i] = c->ms[i];
   double st[4] = {0, 0, 0, 0};
   HIPCHK(c, hipMemcpy(st, c->stats, 32, hipMemcpyDeviceToHost));
-  const double roots = c->N > 0 ? st[2] / (double)c->N : 0.0;
-  // algorithmic bytes: rows x (F bins + 2 B packed g/h [+ 4 B row index off the root])
-  // + the histogram write (cells x 2 x 4 B) per launch
-  const double cell_bytes = (double)c->total_cells * 2.0 * 4.0;
-  const double bytes = st[2] * (double)(c->F + 2) + st[0] * (double)(c->F + 2 + 4) +
-                       (roots + st[1]) * cell_bytes;
-  if (hist_bytes_out) *hist_bytes_out = bytes;
-  if (hist_launches_out) *hist_launches_out = (int64_t)(roots + st[1] + 0.5);
+  for (int i = 0; i < 5; ++i) out[i] = c->ms[i];
+  out[5] = st[2];
+  out[6] = st[3];
+  out[7] = st[0];
+  out[8] = st[1];
+  out[9] = 16.0 * c->W;
+  out[10] = c->F;
+  out[11] = c->total_cells;
   return LGBM_HIP_OK;
 }
 

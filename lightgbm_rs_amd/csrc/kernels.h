@@ -35,6 +35,7 @@ struct DevLeaves {
 };
 
 struct DevTree {
+  int32_t* header;            // [0] num_leaves, [1] error (written by k_tree_finalize)
   int32_t* split_feature;
   uint32_t* threshold_in_bin;
   double* threshold;
@@ -62,11 +63,13 @@ struct DevLearner {
   int32_t _pad;
   int64_t N;
   uint64_t slot_len;
-  int32_t* hist_int;          // [total_cells][3]
+  int32_t* hist_int;          // [total_cells][3] accumulator (flush target)
+  int32_t* int_slots;         // [max_leaves][total_cells][3] per-leaf integer histograms
   double* slots;              // [max_leaves][slot_len]
   lgbm_split_info* feat_split;  // [max_leaves][F]
   lgbm_split_info* best;        // [max_leaves]
-  int32_t* best_feat;           // [max_leaves]
+  int32_t* best_feat;           // [max_leaves] real feature index
+  int32_t* best_fpos;           // [max_leaves] feature position
   uint8_t* splittable;          // [max_leaves][F]
   uint64_t* tile_state;
   double* stats;                // [0] hist rows (non-root), [1] hist launches, [2] root rows
@@ -78,10 +81,11 @@ struct DevLearner {
 namespace lgbm {
 void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t W, uint4* rec,
                          hipStream_t s);
-void launch_absmax(const float* g, const float* h, int64_t n, Ctl* ctl, hipStream_t s);
+void launch_absmax(const float* g, const float* h, int64_t n, uint4* partials, hipStream_t s);
 void launch_grad_binary(const double* score, const float* label, float* g, float* h, int64_t n,
-                        Ctl* ctl, hipStream_t s);
-void launch_quant_scales(Ctl* ctl, int32_t bins, int32_t force_const, hipStream_t s);
+                        uint4* partials, hipStream_t s);
+void launch_quant_scales(Ctl* ctl, const uint4* partials, int64_t n, int32_t bins,
+                         int32_t force_const, hipStream_t s);
 void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,
                      const uint64_t* wave_mats, const uint64_t* lane_mats, uint64_t s0,
                      int32_t stochastic, uint16_t* gh, float* dg, float* dh, hipStream_t s);
@@ -90,10 +94,10 @@ void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hip
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,
                           lgbm_split_info* out, hipStream_t s);
-void launch_split(const DevLearner& L, hipStream_t s);
 void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s);
 void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, hipStream_t s);
 void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s);
+void launch_tree_finalize(const DevLearner& L, hipStream_t s);
 void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
                           hipStream_t s);
 void launch_gather_rows(int W, const uint32_t* rows, int64_t n, const uint4* rec,

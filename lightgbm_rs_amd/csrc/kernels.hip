@@ -9,7 +9,7 @@
 //   k_fixscan        f64 cells + FixHistogram + compaction + subtraction trick +
 //                    FindBestThreshold (fix_histogram.rs:50-80, learner.rs:4460-4492,
 //                    histogram_pool.rs:249, kernels/split.rs:8970-9329)
-//   k_split          per-leaf argmax (scan_leaf_histogram, learner.rs:3290-3330),
+//   split_step       (last block of k_fixscan) per-leaf argmax (learner.rs:3290-3330),
 //                    cross-leaf ArgMax (learner.rs:4537), Tree::split (tree.rs:614-700)
 //   k_partition      DataPartition::split (data_partition.rs:192-288,360-463)
 //   k_score_update   score update through the grown tree (score_updater.rs:133;
@@ -47,79 +47,108 @@ __device__ __forceinline__ float f32_from_key(uint32_t k) {
   return __uint_as_float(b);
 }
 
-__device__ __forceinline__ void reduce_gh_stats(float gv, float hv, bool valid, Ctl* ctl) {
-  // max |g|, max |h| (f64::max ignores NaN: a NaN contributes nothing), min/max of h
-  // for the all-equal test of quantize_grad_hess_in_place (gbdt.rs:54).
-  uint32_t ag = 0u, ah = 0u, hmin = 0xffffffffu, hmax = 0u;
-  if (valid) {
-    if (gv == gv) ag = __float_as_uint(fabsf(gv));
-    if (hv == hv) {
-      ah = __float_as_uint(fabsf(hv));
-      hmin = hmax = f32_order_key(hv);
-    }
+// Per-block partial statistics of (g, h): max |g|, max |h| (f64::max ignores NaN, so a
+// NaN contributes nothing) and min/max of h for the all-equal test of
+// quantize_grad_hess_in_place (gbdt.rs:54).  No atomics: each block writes one
+// partial and k_quant_scales reduces them.
+struct GhStat {
+  uint32_t ag, ah, hmin, hmax;
+};
+__device__ __forceinline__ void stat_add(GhStat& s, float gv, float hv) {
+  if (gv == gv) s.ag = max(s.ag, __float_as_uint(fabsf(gv)));
+  if (hv == hv) {
+    s.ah = max(s.ah, __float_as_uint(fabsf(hv)));
+    const uint32_t k = f32_order_key(hv);
+    s.hmin = min(s.hmin, k);
+    s.hmax = max(s.hmax, k);
   }
+}
+__device__ __forceinline__ void stat_merge(GhStat& a, const GhStat& b) {
+  a.ag = max(a.ag, b.ag);
+  a.ah = max(a.ah, b.ah);
+  a.hmin = min(a.hmin, b.hmin);
+  a.hmax = max(a.hmax, b.hmax);
+}
+__device__ void block_stat_write(GhStat s, uint4* __restrict__ partials) {
+  __shared__ GhStat sh[16];
   for (int off = 32; off >= 1; off >>= 1) {
-    ag = max(ag, (uint32_t)__shfl_xor((int)ag, off));
-    ah = max(ah, (uint32_t)__shfl_xor((int)ah, off));
-    hmin = min(hmin, (uint32_t)__shfl_xor((int)hmin, off));
-    hmax = max(hmax, (uint32_t)__shfl_xor((int)hmax, off));
+    GhStat o;
+    o.ag = (uint32_t)__shfl_xor((int)s.ag, off);
+    o.ah = (uint32_t)__shfl_xor((int)s.ah, off);
+    o.hmin = (uint32_t)__shfl_xor((int)s.hmin, off);
+    o.hmax = (uint32_t)__shfl_xor((int)s.hmax, off);
+    stat_merge(s, o);
   }
-  if (lane_id() == 0) {
-    if (ag) atomicMax(&ctl->max_g_bits, ag);
-    if (ah) atomicMax(&ctl->max_h_bits, ah);
-    if (hmin != 0xffffffffu) atomicMin(&ctl->hmin_key, hmin);
-    if (hmax) atomicMax(&ctl->hmax_key, hmax);
+  if (lane_id() == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    GhStat r = sh[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) stat_merge(r, sh[w]);
+    partials[blockIdx.x] = make_uint4(r.ag, r.ah, r.hmin, r.hmax);
   }
 }
 
-__global__ void k_absmax(const float* __restrict__ g, const float* __restrict__ h, int64_t n,
-                         Ctl* ctl) {
+__global__ __launch_bounds__(256) void k_absmax(const float* __restrict__ g,
+                                                const float* __restrict__ h, int64_t n,
+                                                uint4* __restrict__ partials) {
+  GhStat s{0u, 0u, 0xffffffffu, 0u};
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  // wave-uniform trip count so the shuffles in reduce_gh_stats see the whole wave
-  const int64_t base0 = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~63);
-  for (int64_t b = base0; b < n; b += stride, r += stride) {
-    bool v = r < n;
-    reduce_gh_stats(v ? g[r] : 0.f, v ? h[r] : 0.f, v, ctl);
-  }
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride)
+    stat_add(s, g[r], h[r]);
+  block_stat_write(s, partials);
 }
 
 // BinaryLogloss::get_gradients (binary.rs:134-172), sigmoid = 1, balanced weights.
-__global__ void k_grad_binary(const double* __restrict__ score, const float* __restrict__ label,
-                              float* __restrict__ g, float* __restrict__ h, int64_t n, Ctl* ctl) {
+__global__ __launch_bounds__(256) void k_grad_binary(const double* __restrict__ score,
+                                                     const float* __restrict__ label,
+                                                     float* __restrict__ g, float* __restrict__ h,
+                                                     int64_t n, uint4* __restrict__ partials) {
+  GhStat s{0u, 0u, 0xffffffffu, 0u};
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t base0 = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~63);
   const double sigmoid = 1.0;
-  for (int64_t b = base0; b < n; b += stride, r += stride) {
-    const bool v = r < n;
-    float gv = 0.f, hv = 0.f;
-    if (v) {
-      const bool pos = label[r] > 0.0f;
-      const double lv = pos ? 1.0 : -1.0;
-      const double resp = -lv * sigmoid / (1.0 + exp(lv * sigmoid * score[r]));
-      const double ar = fabs(resp);
-      gv = (float)(resp * 1.0);
-      hv = (float)(ar * (sigmoid - ar) * 1.0);
-      g[r] = gv;
-      h[r] = hv;
-    }
-    reduce_gh_stats(gv, hv, v, ctl);
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
+    const bool pos = label[r] > 0.0f;
+    const double lv = pos ? 1.0 : -1.0;
+    const double resp = -lv * sigmoid / (1.0 + exp(lv * sigmoid * score[r]));
+    const double ar = fabs(resp);
+    const float gv = (float)(resp * 1.0);
+    const float hv = (float)(ar * (sigmoid - ar) * 1.0);
+    g[r] = gv;
+    h[r] = hv;
+    stat_add(s, gv, hv);
   }
+  block_stat_write(s, partials);
 }
 
-// compute_scales (gradient_discretizer.rs:145-165) from the reduced maxima; resets
-// the accumulators for the next iteration.
-__global__ void k_quant_scales(Ctl* ctl, int32_t bins, int32_t force_const) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  const double mg = (double)__uint_as_float(ctl->max_g_bits);
-  const double mh = (double)__uint_as_float(ctl->max_h_bits);
+// compute_scales (gradient_discretizer.rs:145-165) from the reduced statistics.
+__global__ __launch_bounds__(256) void k_quant_scales(Ctl* ctl, const uint4* __restrict__ partials,
+                                                      int32_t nparts, int32_t bins,
+                                                      int32_t force_const) {
+  GhStat s{0u, 0u, 0xffffffffu, 0u};
+  for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+    const uint4 p = partials[i];
+    stat_merge(s, GhStat{p.x, p.y, p.z, p.w});
+  }
+  __shared__ GhStat sh[4];
+  for (int off = 32; off >= 1; off >>= 1) {
+    GhStat o;
+    o.ag = (uint32_t)__shfl_xor((int)s.ag, off);
+    o.ah = (uint32_t)__shfl_xor((int)s.ah, off);
+    o.hmin = (uint32_t)__shfl_xor((int)s.hmin, off);
+    o.hmax = (uint32_t)__shfl_xor((int)s.hmax, off);
+    stat_merge(s, o);
+  }
+  if (lane_id() == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) stat_merge(s, sh[w]);
+  const double mg = (double)__uint_as_float(s.ag);
+  const double mh = (double)__uint_as_float(s.ah);
   bool ch;
   if (force_const >= 0) {
     ch = force_const != 0;
   } else {
-    const float lo = f32_from_key(ctl->hmin_key), hi = f32_from_key(ctl->hmax_key);
-    ch = lo == hi;
+    ch = f32_from_key(s.hmin) == f32_from_key(s.hmax);
   }
   const double half = (double)(bins / 2);
   ctl->gs = mg / half;
@@ -131,10 +160,6 @@ __global__ void k_quant_scales(Ctl* ctl, int32_t bins, int32_t force_const) {
   ctl->vh3 = (float)(3.0 * ctl->hs);
   ctl->const_hess = ch ? 1 : 0;
   ctl->quant_bins = bins;
-  ctl->max_g_bits = 0u;
-  ctl->max_h_bits = 0u;
-  ctl->hmin_key = 0xffffffffu;
-  ctl->hmax_key = 0u;
 }
 
 // ===========================================================================
@@ -155,6 +180,12 @@ __device__ __forceinline__ double next_u01(uint64_t& s) {
   return (double)(x >> 11) / (double)(1ull << 53);
 }
 
+// Rows per block: 4 waves x 64 lanes x QUANT_ROWS_PER_LANE.  g/h are staged through
+// LDS so global loads and stores are coalesced while each lane walks its own run of
+// consecutive rows (padded index: one spare slot per 16 rows avoids bank conflicts).
+#define QUANT_BLOCK_ROWS (4 * LGBM_WAVE * QUANT_ROWS_PER_LANE)
+__device__ __forceinline__ int qidx(int r) { return r + (r >> 4); }
+
 __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ g,
                                                   const float* __restrict__ h, int64_t n,
                                                   const Ctl* __restrict__ ctl,
@@ -163,10 +194,20 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ g,
                                                   uint64_t s0, int32_t stochastic,
                                                   uint16_t* __restrict__ gh,
                                                   float* __restrict__ dg, float* __restrict__ dh) {
-  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  __shared__ float sg_[QUANT_BLOCK_ROWS + QUANT_BLOCK_ROWS / 16];
+  __shared__ float sh_[QUANT_BLOCK_ROWS + QUANT_BLOCK_ROWS / 16];
+  __shared__ uint16_t sq_[QUANT_BLOCK_ROWS + QUANT_BLOCK_ROWS / 16];
+  const int64_t brow0 = (int64_t)blockIdx.x * QUANT_BLOCK_ROWS;
+  if (brow0 >= n) return;
+  const int tid = threadIdx.x;
+  const int64_t nblk = min((int64_t)QUANT_BLOCK_ROWS, n - brow0);
+  for (int r = tid; r < QUANT_BLOCK_ROWS; r += 256) {
+    const bool v = r < nblk;
+    sg_[qidx(r)] = v ? g[brow0 + r] : 0.f;
+    sh_[qidx(r)] = v ? h[brow0 + r] : 0.f;
+  }
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + tid) >> 6;
   const int lane = (int)lane_id();
-  const int64_t row0 = wave * (int64_t)(LGBM_WAVE * QUANT_ROWS_PER_LANE);
-  if (row0 >= n) return;  // wave-uniform
   const double igs = ctl->igs, ihs = ctl->ihs, gs = ctl->gs, hs = ctl->hs;
   const bool ch = ctl->const_hess != 0;
   uint64_t st = 0;
@@ -190,11 +231,12 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ g,
     }
     st = sl;
   }
-  const int64_t lrow = row0 + (int64_t)lane * QUANT_ROWS_PER_LANE;
+  __syncthreads();
+  const int lrow = (tid >> 6) * (LGBM_WAVE * QUANT_ROWS_PER_LANE) + lane * QUANT_ROWS_PER_LANE;
   for (int j = 0; j < QUANT_ROWS_PER_LANE; ++j) {
-    const int64_t r = lrow + j;
-    if (r >= n) break;
-    const float gv = g[r], hv = h[r];
+    const int r = lrow + j;
+    if (r >= nblk) break;
+    const float gv = sg_[qidx(r)], hv = sh_[qidx(r)];
     double bg = 0.5, bh = 0.5;
     if (stochastic) {
       bg = next_u01(st);
@@ -203,12 +245,14 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ g,
     const double x = (double)gv * igs;
     const int8_t qg = sat_i8(gv >= 0.0f ? x + bg : x - bg);
     const int8_t qh = ch ? (int8_t)1 : sat_i8((double)hv * ihs + bh);
-    gh[r] = (uint16_t)((uint16_t)(uint8_t)qg | ((uint16_t)(uint8_t)qh << 8));
+    sq_[qidx(r)] = (uint16_t)((uint16_t)(uint8_t)qg | ((uint16_t)(uint8_t)qh << 8));
     if (dg) {
-      dg[r] = (float)((double)qg * gs);
-      dh[r] = (float)((double)qh * hs);
+      dg[brow0 + r] = (float)((double)qg * gs);
+      dh[brow0 + r] = (float)((double)qh * hs);
     }
   }
+  __syncthreads();
+  for (int r = tid; r < nblk; r += 256) gh[brow0 + r] = sq_[qidx(r)];
 }
 
 // ===========================================================================
@@ -347,23 +391,25 @@ __device__ void wave_scan(const double* hist, const DevFeature& ft, const ScanCf
     const int32_t t_start = nb - 1 - offset - na;
     for (int32_t base = 0; base < rev_count; base += LGBM_WAVE) {
       const int32_t cnt = min(LGBM_WAVE, rev_count - base);
-      double sg = cg, sh = ch;
-      int32_t rc = cc;
-      for (int32_t i = 0; i < cnt; ++i) {
-        const int32_t t = t_start - (base + i);
-        const bool act = (t >= 1 - offset) && !(skip_def && t + offset == defb);
-        if (act) {
-          const double hg = hist[2 * t], hh = hist[2 * t + 1];
-          if (i <= lane) {
-            sg += hg;
-            sh += hh;
-            rc += round_int(hh * cf);
-          }
-        }
-      }
       const bool valid = lane < cnt;
       const int32_t t = t_start - (base + lane);
       const bool act = valid && (t >= 1 - offset) && !(skip_def && t + offset == defb);
+      const double mg = act ? hist[2 * t] : 0.0, mh = act ? hist[2 * t + 1] : 0.0;
+      const int32_t mc = act ? round_int(mh * cf) : 0;
+      double sg = cg, sh = ch;
+      int32_t rc = cc;
+      for (int32_t i = 0; i < cnt; ++i) {
+        const int32_t ti = t_start - (base + i);
+        if ((ti >= 1 - offset) && !(skip_def && ti + offset == defb)) {  // wave-uniform
+          const double xg = readlane_f64(mg, i), xh = readlane_f64(mh, i);
+          const int32_t xc = readlane_i32(mc, i);
+          if (i <= lane) {
+            sg += xg;
+            sh += xh;
+            rc += xc;
+          }
+        }
+      }
       const int32_t lc = num_data - rc;
       const double slh = shb - sh, slg = sum_gradient - sg;
       const bool cont = rc < c.min_d || sh < c.min_h;
@@ -406,32 +452,42 @@ __device__ void wave_scan(const double* hist, const DevFeature& ft, const ScanCf
       cg = sum_gradient;
       ch = shb - eps;
       cc = num_data;
-      for (int32_t i = 0; i < nb - offset; ++i) {
-        cg -= hist[2 * i];
-        ch -= hist[2 * i + 1];
-        cc -= round_int(hist[2 * i + 1] * cf);
+      const int32_t m = nb - offset;
+      for (int32_t c0 = 0; c0 < m; c0 += LGBM_WAVE) {
+        const int32_t bb = c0 + lane;
+        const double vg = bb < m ? hist[2 * bb] : 0.0, vh = bb < m ? hist[2 * bb + 1] : 0.0;
+        const int32_t vc = bb < m ? round_int(vh * cf) : 0;
+        const int32_t lim = min(LGBM_WAVE, m - c0);
+        for (int32_t i = 0; i < lim; ++i) {
+          cg -= readlane_f64(vg, i);
+          ch -= readlane_f64(vh, i);
+          cc -= readlane_i32(vc, i);
+        }
       }
       fwd_start = -1;
     }
     for (int32_t base = 0; base < fwd_count; base += LGBM_WAVE) {
       const int32_t cnt = min(LGBM_WAVE, fwd_count - base);
-      double sg = cg, sh = ch;
-      int32_t lcn = cc;
-      for (int32_t i = 0; i < cnt; ++i) {
-        const int32_t t = fwd_start + base + i;
-        const bool act = !(skip_def && t + offset == defb);
-        if (act && t >= 0) {
-          const double hg = hist[2 * t], hh = hist[2 * t + 1];
-          if (i <= lane) {
-            sg += hg;
-            sh += hh;
-            lcn += round_int(hh * cf);
-          }
-        }
-      }
       const bool valid = lane < cnt;
       const int32_t t = fwd_start + base + lane;
       const bool act = valid && !(skip_def && t + offset == defb);
+      const bool addl = act && t >= 0;
+      const double mg = addl ? hist[2 * t] : 0.0, mh = addl ? hist[2 * t + 1] : 0.0;
+      const int32_t mc = addl ? round_int(mh * cf) : 0;
+      double sg = cg, sh = ch;
+      int32_t lcn = cc;
+      for (int32_t i = 0; i < cnt; ++i) {
+        const int32_t ti = fwd_start + base + i;
+        if (!(skip_def && ti + offset == defb) && ti >= 0) {  // wave-uniform
+          const double xg = readlane_f64(mg, i), xh = readlane_f64(mh, i);
+          const int32_t xc = readlane_i32(mc, i);
+          if (i <= lane) {
+            sg += xg;
+            sh += xh;
+            lcn += xc;
+          }
+        }
+      }
       const int32_t rc = num_data - lcn;
       const double srh = shb - sh, srg = sum_gradient - sg;
       const bool cont = lcn < c.min_d || sh < c.min_h;
@@ -494,221 +550,11 @@ __device__ void wave_scan(const double* hist, const DevFeature& ft, const ScanCf
 }
 
 // ===========================================================================
-// k_fixscan: one block (two waves) per feature.
-//   mode 0 (pair):  smaller child cells from the integer histogram -> FixHistogram on
-//                   the smaller's RAW sums -> compaction -> slot[smaller];
-//                   slot[larger] = slot[parent] - slot[smaller]; scan both leaves.
-//   mode 1 (root):  leaf 0 from all rows; root LeafSplits sums from the histogram.
-//   mode 2 (build): per-op build into `explicit_out` (no scan).
-// The integer cells are cleared after reading so the next build starts from zero.
-// ===========================================================================
-__global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t mode,
-                                                          double* __restrict__ explicit_out) {
-  __shared__ double cs[2 * 256];
-  __shared__ double cp[2 * 256];
-  __shared__ long long tot[3][SCAN_THREADS / LGBM_WAVE];
-  Ctl* ctl = L.ctl;
-  const int f = blockIdx.x;
-  if (mode == 0 && ctl->done) return;
-  const bool skip = mode == 0 ? (ctl->skip != 0) : (mode == 1 ? (ctl->skip != 0) : false);
-  if (mode == 0 && skip) return;
-  const DevFeature ft = L.feats[f];
-  const int nb = (int)ft.num_bin;
-  const int tid = threadIdx.x;
-  const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
-  const int F = L.F;
-
-  long long tg = 0, th = 0, t3 = 0;
-  for (int b = tid; b < nb; b += SCAN_THREADS) {
-    int32_t* cell = L.hist_int + (size_t)(ft.cell_base + b) * 3;
-    const int32_t G = cell[0], H = cell[1], T = cell[2];
-    cell[0] = 0;
-    cell[1] = 0;
-    cell[2] = 0;
-    cs[2 * b] = (double)G * vg1;
-    cs[2 * b + 1] = (double)((long long)H - 3ll * T) * vh1 + (double)T * vh3;
-    tg += G;
-    th += H;
-    t3 += T;
-  }
-  // leaf sums
-  double sg, sh, weight;
-  int32_t nrows;
-  if (mode == 1) {
-    for (int off = 32; off >= 1; off >>= 1) {
-      tg += __shfl_xor(tg, off);
-      th += __shfl_xor(th, off);
-      t3 += __shfl_xor(t3, off);
-    }
-    if (lane_id() == 0) {
-      tot[0][tid >> 6] = tg;
-      tot[1][tid >> 6] = th;
-      tot[2][tid >> 6] = t3;
-    }
-    __syncthreads();
-    long long G = 0, H = 0, T = 0;
-    for (int w = 0; w < SCAN_THREADS / LGBM_WAVE; ++w) {
-      G += tot[0][w];
-      H += tot[1][w];
-      T += tot[2][w];
-    }
-    // LeafSplits::init (leaf_splits.rs:75-89): the ordered f64 fold of the
-    // dequantized values equals these exact integer-weighted sums.
-    sg = (double)G * vg1;
-    sh = (double)(H - 3ll * T) * vh1 + (double)T * vh3;
-    nrows = (int32_t)L.N;
-    const lgbm_gain_config& cfg = ctl->cfg;
-    weight = leaf_output_full(cfg.lambda_l1 > 0.0, sg, sh, cfg.lambda_l1, cfg.lambda_l2,
-                              cfg.max_delta_step, false, cfg.path_smooth, 0, 0.0);
-    if (f == 0 && tid == 0) {
-      ctl->sm.sg = sg;
-      ctl->sm.sh = sh;
-      ctl->sm.weight = weight;
-      ctl->sm.n = nrows;
-      L.tree.leaf_value[0] = weight;
-      if (!(sh > 0.0)) {
-        ctl->error |= ERR_ROOT_HESSIAN;
-        ctl->done = 1;
-      }
-    }
-  } else {
-    sg = ctl->sm.sg;
-    sh = ctl->sm.sh;
-    weight = ctl->sm.weight;
-    nrows = ctl->sm.n;
-  }
-  __syncthreads();
-
-  const int32_t left_leaf = ctl->left_leaf;
-  const int32_t smaller = mode == 1 ? 0 : ctl->smaller;
-  const int32_t larger = mode == 0 ? ctl->larger : -1;
-  const bool pgate = mode == 0 && L.splittable[(size_t)left_leaf * F + f] == 0;
-  const bool buildable = sh > 0.0 && nrows > 0;
-
-  if (!buildable || pgate) {
-    for (int i = tid; i < 2 * nb; i += SCAN_THREADS) cs[i] = 0.0;
-  } else {
-    __syncthreads();
-    // FixHistogram (fix_histogram.rs:50-80): sequential, ascending bins.
-    const uint32_t mfb = ft.mfb;
-    if (tid == 0 && mfb > 0 && mfb < ft.num_bin) {
-      double g = sg, h = sh;
-      for (int i = 0; i < nb; ++i) {
-        if (i != (int)mfb) {
-          g -= cs[2 * i];
-          h -= cs[2 * i + 1];
-        }
-      }
-      cs[2 * mfb] = g;
-      cs[2 * mfb + 1] = h;
-    }
-    __syncthreads();
-    // compact_histogram (learner.rs:4460-4492)
-    if (ft.offset > 0) {
-      const int off = ft.offset;
-      double a[4], b2[4];
-      int k = 0;
-      for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
-        const int src = c + off;
-        a[k] = src < nb ? cs[2 * src] : 0.0;
-        b2[k] = src < nb ? cs[2 * src + 1] : 0.0;
-      }
-      __syncthreads();
-      k = 0;
-      for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
-        cs[2 * c] = a[k];
-        cs[2 * c + 1] = b2[k];
-      }
-    }
-  }
-  __syncthreads();
-
-  if (mode == 2) {
-    for (int i = tid; i < 2 * nb; i += SCAN_THREADS) explicit_out[ft.slot_off + i] = cs[i];
-    return;
-  }
-  const size_t sl = L.slot_len;
-  double* s_small = L.slots + (size_t)smaller * sl + ft.slot_off;
-  if (larger >= 0) {
-    // parent region lives in the slot of left_leaf (the split leaf keeps its id)
-    const double* s_par = L.slots + (size_t)left_leaf * sl + ft.slot_off;
-    for (int i = tid; i < 2 * nb; i += SCAN_THREADS) cp[i] = s_par[i];
-    __syncthreads();
-    double* s_large = L.slots + (size_t)larger * sl + ft.slot_off;
-    for (int i = tid; i < 2 * nb; i += SCAN_THREADS) {
-      const double d = cp[i] - cs[i];
-      cp[i] = d;
-      s_small[i] = cs[i];
-      s_large[i] = d;
-    }
-  } else {
-    for (int i = tid; i < 2 * nb; i += SCAN_THREADS) s_small[i] = cs[i];
-  }
-  __syncthreads();
-  if (skip) return;  // root gated: sums and leaf value recorded, no scan
-
-  // ---- scans: wave 0 -> smaller (or root), wave 1 -> larger ----
-  const int wave = tid >> 6;
-  int32_t leaf;
-  const double* hist;
-  double lsg, lsh, lpo;
-  int32_t ln;
-  if (wave == 0) {
-    leaf = smaller;
-    hist = cs;
-    lsg = sg;
-    lsh = sh;
-    lpo = weight;
-    ln = nrows;
-  } else {
-    if (larger < 0) return;
-    leaf = larger;
-    hist = cp;
-    lsg = ctl->lg.sg;
-    lsh = ctl->lg.sh;
-    lpo = ctl->lg.weight;
-    ln = ctl->lg.n;
-  }
-  lgbm_split_info* out = L.feat_split + (size_t)leaf * F + f;
-  const bool scannable = lsh > 0.0 && ln > 0;
-  if (!scannable) {
-    if (lane_id() == 0) split_set_none(out);
-    return;
-  }
-  if (pgate) {
-    if (lane_id() == 0) {
-      split_set_none(out);
-      L.splittable[(size_t)leaf * F + f] = 0;
-    }
-    return;
-  }
-  lgbm_gain_config cfg = ctl->cfg;
-  const ScanCfg sc = make_scan_cfg(cfg);
-  wave_scan(hist, ft, sc, lsg, lsh, ln, lpo, out);
-  if (lane_id() == 0) L.splittable[(size_t)leaf * F + f] = out->gain > -__builtin_inf() ? 1 : 0;
-}
-
-// Per-op FindBestThreshold over explicit features (find_best_splits_batched,
-// lib.rs:1500-1548): one wave per feature, host-provided histogram.
-__global__ __launch_bounds__(LGBM_WAVE) void k_scan_explicit(const double* __restrict__ hist,
-                                                             const DevFeature* __restrict__ feats,
-                                                             int32_t n_feats,
-                                                             lgbm_gain_config cfg, double sg,
-                                                             double sh, int32_t n,
-                                                             lgbm_split_info* out) {
-  __shared__ double cs[2 * 256];
-  const int f = blockIdx.x;
-  if (f >= n_feats) return;
-  const DevFeature ft = feats[f];
-  for (int i = threadIdx.x; i < 2 * (int)ft.num_bin; i += LGBM_WAVE) cs[i] = hist[ft.slot_off + i];
-  __syncthreads();
-  const ScanCfg sc = make_scan_cfg(cfg);
-  wave_scan(cs, ft, sc, sg, sh, n, cfg.parent_output, out + f);
-}
-
-// ===========================================================================
-// k_split: per-leaf feature argmax for the leaves scanned last, cross-leaf ArgMax,
-// stop test, and the Tree::split bookkeeping of the chosen split.
+// Split step: per-leaf feature argmax for the leaves scanned last (the argmax of
+// scan_leaf_histogram, learner.rs:3290-3330), the cross-leaf ArgMax
+// (learner.rs:4537), the stop test (learner.rs:1503) and the Tree::split bookkeeping
+// of the chosen split (tree.rs:614-700), plus the router and partition job of the
+// split (split_inner, learner.rs:3895-4011).  Run by one whole block.
 // ===========================================================================
 struct BestKey {
   double gain;
@@ -740,10 +586,9 @@ __device__ BestKey block_best(BestKey k, BestKey* sh) {
   return r;
 }
 
-__global__ __launch_bounds__(256) void k_split(DevLearner L) {
-  __shared__ BestKey sh[4];
+__device__ void split_step(DevLearner& L) {
+  __shared__ BestKey sh[16];
   Ctl* ctl = L.ctl;
-  if (ctl->done) return;
   const int F = L.F;
   const int tid = threadIdx.x;
   const double ninf = -__builtin_inf();
@@ -754,23 +599,26 @@ __global__ __launch_bounds__(256) void k_split(DevLearner L) {
       if (leaf < 0) continue;
       BestKey k{ninf, -1, 0x7fffffff};
       for (int f = tid; f < F; f += blockDim.x) {
-        const lgbm_split_info& s = L.feat_split[(size_t)leaf * F + f];
-        BestKey c{s.gain, L.feats[f].real_index, f};
-        if (s.gain > ninf && key_better(c, k)) k = c;
+        const double g = L.feat_split[(size_t)leaf * F + f].gain;
+        BestKey c{g, L.feats[f].real_index, f};
+        if (g > ninf && key_better(c, k)) k = c;
       }
       const BestKey r = block_best(k, sh);
       if (tid == 0) {
         if (r.idx != 0x7fffffff && r.gain > ninf) {
           L.best[leaf] = L.feat_split[(size_t)leaf * F + r.idx];
           L.best_feat[leaf] = r.feat;
+          L.best_fpos[leaf] = r.idx;
         } else {
           split_set_none(&L.best[leaf]);
           L.best_feat[leaf] = -1;
+          L.best_fpos[leaf] = -1;
         }
       }
       __syncthreads();
     }
     if (tid == 0) ctl->pending_reduce = 0;
+    __threadfence_block();
   }
   const int32_t nl = ctl->num_leaves;
   BestKey k{ninf, -1, 0x7fffffff};
@@ -781,39 +629,45 @@ __global__ __launch_bounds__(256) void k_split(DevLearner L) {
   const BestKey r = block_best(k, sh);
   if (tid != 0) return;
   const int32_t bl = r.idx == 0x7fffffff ? 0 : r.idx;
+  // independent loads first
   const lgbm_split_info b = L.best[bl];
+  const int32_t fr = L.best_feat[bl];
+  const int32_t f = L.best_fpos[bl];
+  DevTree& T = L.tree;
+  const int32_t parent = T.leaf_parent[bl];
+  const double lv_old = T.leaf_value[bl];
+  const int32_t depth = T.leaf_depth[bl];
+  const int32_t src_buf = L.leaves.buf[bl];
+  const int32_t lbegin = L.leaves.begin[bl];
+  const int32_t lcount = L.leaves.count[bl];
+  const int32_t lrev = L.leaves.rev[bl];
   if (!(b.gain > 0.0)) {  // learner.rs:1503: stop when gain <= 0
     ctl->done = 1;
     return;
   }
-  const int32_t fr = L.best_feat[bl];
-  int32_t f = -1;
-  for (int j = 0; j < F; ++j)
-    if (L.feats[j].real_index == fr) {
-      f = j;
-      break;
-    }
-  if (f < 0) {
+  if (f < 0 || f >= F) {
     ctl->error |= ERR_FEATURE;
     ctl->done = 1;
     return;
   }
-  const DevFeature& ft = L.feats[f];
+  const DevFeature ft = L.feats[f];
   const int32_t node = nl - 1, nr = nl;
-  DevTree& T = L.tree;
+  const double thr_real = L.ub ? L.ub[ft.ub_off + b.threshold] : (double)b.threshold;
   // Tree::split (tree.rs:614-700); counts are written by k_partition.
-  const int32_t parent = T.leaf_parent[bl];
   if (parent >= 0) {
-    if (T.right_child[parent] == ~bl)
+    if (T.right_child[parent] == ~bl) {
       T.right_child[parent] = node;
-    else
+      T.nodes[parent].right = node;
+    } else {
       T.left_child[parent] = node;
+      T.nodes[parent].left = node;
+    }
   }
   T.split_feature[node] = fr;
   T.split_gain[node] = (float)(b.gain + ctl->cfg.min_gain_to_split);
   T.threshold_in_bin[node] = b.threshold;
-  T.threshold[node] = L.ub ? L.ub[ft.ub_off + b.threshold] : (double)b.threshold;
-  T.internal_value[node] = T.leaf_value[bl];
+  T.threshold[node] = thr_real;
+  T.internal_value[node] = lv_old;
   T.left_child[node] = ~bl;
   T.right_child[node] = ~nr;
   int8_t dt = 0;
@@ -824,8 +678,8 @@ __global__ __launch_bounds__(256) void k_split(DevLearner L) {
   T.leaf_weight[bl] = b.left_sum_hessian;
   T.leaf_value[nr] = b.right_output;
   T.leaf_weight[nr] = b.right_sum_hessian;
-  T.leaf_depth[nr] = T.leaf_depth[bl] + 1;
-  T.leaf_depth[bl] += 1;
+  T.leaf_depth[nr] = depth + 1;
+  T.leaf_depth[bl] = depth + 1;
   T.leaf_parent[bl] = node;
   T.leaf_parent[nr] = node;
   // router (split_inner, learner.rs:3957; data_partition.rs:387-417)
@@ -836,7 +690,7 @@ __global__ __launch_bounds__(256) void k_split(DevLearner L) {
   if ((int32_t)ft.mfb > (int32_t)b.threshold) flags |= 1;
   if (ft.na_as_missing) flags |= 2;
   if (b.default_left) flags |= 4;
-  NodeRoute& nrt = T.nodes[node];
+  NodeRoute nrt;
   nrt.f = f;
   nrt.pmin = pmin;
   nrt.max_bin = (int32_t)ft.max_bin;
@@ -845,19 +699,13 @@ __global__ __launch_bounds__(256) void k_split(DevLearner L) {
   nrt.flags = flags;
   nrt.left = ~bl;
   nrt.right = ~nr;
-  if (parent >= 0) {
-    NodeRoute& pn = T.nodes[parent];
-    if (pn.right == ~bl)
-      pn.right = node;
-    else
-      pn.left = node;
-  }
-  PartJob& J = ctl->part;
-  J.src_buf = L.leaves.buf[bl];
-  J.dst_buf = J.src_buf == BUF_A ? BUF_B : BUF_A;
-  J.begin = L.leaves.begin[bl];
-  J.count = L.leaves.count[bl];
-  J.rev = L.leaves.rev[bl];
+  T.nodes[node] = nrt;
+  PartJob J;
+  J.src_buf = src_buf;
+  J.dst_buf = src_buf == BUF_A ? BUF_B : BUF_A;
+  J.begin = lbegin;
+  J.count = lcount;
+  J.rev = lrev;
   J.fbyte = f;
   J.pmin = pmin;
   J.max_bin = (int32_t)ft.max_bin;
@@ -865,6 +713,7 @@ __global__ __launch_bounds__(256) void k_split(DevLearner L) {
   J.na_bin = (int32_t)ft.num_bin - 1;
   J.flags = flags;
   J.driver = 1;
+  ctl->part = J;
   ctl->split = b;
   ctl->split_leaf = bl;
   ctl->split_f = f;
@@ -872,11 +721,272 @@ __global__ __launch_bounds__(256) void k_split(DevLearner L) {
   ctl->node = node;
   split_set_none(&L.best[bl]);
   L.best_feat[bl] = -1;
+  L.best_fpos[bl] = -1;
   split_set_none(&L.best[nr]);
   L.best_feat[nr] = -1;
+  L.best_fpos[nr] = -1;
   ctl->num_leaves = nl + 1;
   ctl->left_leaf = bl;
   ctl->right_leaf = nr;
+}
+
+// ===========================================================================
+// k_fixscan: one block (two waves) per feature, then the split step in the block
+// that finishes last.
+//   mode 0 (pair):  smaller child cells from the integer histogram -> FixHistogram on
+//                   the smaller's RAW sums -> compaction -> slot[smaller];
+//                   slot[larger] = slot[parent] - slot[smaller]; scan both leaves.
+//   mode 1 (root):  leaf 0 from all rows; root LeafSplits sums from the histogram.
+//   mode 2 (build): per-op build into `explicit_out` (no scan, no split step).
+// The integer cells are cleared after reading so the next build starts from zero.
+// With ctl->skip set (a gated pair), only the split step runs.
+// ===========================================================================
+__global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t mode,
+                                                          double* __restrict__ explicit_out) {
+  __shared__ double cs[2 * 256];
+  __shared__ double cp[2 * 256];
+  __shared__ long long tot[3][SCAN_THREADS / LGBM_WAVE];
+  __shared__ int32_t s_last;
+  Ctl* ctl = L.ctl;
+  const int f = blockIdx.x;
+  if (mode == 0 && ctl->done) return;
+  const bool skip = mode == 2 ? false : (ctl->skip != 0);
+  const int tid = threadIdx.x;
+  const int F = L.F;
+
+  const DevFeature ft = L.feats[f];
+  const int nb = (int)ft.num_bin;
+  const int cells = L.total_cells;
+  long long tg = 0, th = 0, t3 = 0;
+  {
+    // Integer cells.  mode 0: the accumulator holds the LEFT child's histogram (built in
+    // the partition pass); right = parent - left; the per-leaf integer slots keep both
+    // for later splits.  mode 1: the root.  mode 2: a per-op build.
+    const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
+    const int32_t bl = ctl->left_leaf, nr = ctl->right_leaf, sml = ctl->smaller;
+    for (int b = tid; b < nb; b += SCAN_THREADS) {
+      const size_t ci = (size_t)(ft.cell_base + b);
+      int32_t* acc = L.hist_int + ci * 3;
+      int32_t G = acc[0], H = acc[1], T = acc[2];
+      acc[0] = 0;
+      acc[1] = 0;
+      acc[2] = 0;
+      if (mode == 0) {
+        int32_t* ps = L.int_slots + ((size_t)bl * cells + ci) * 3;
+        int32_t* rs = L.int_slots + ((size_t)nr * cells + ci) * 3;
+        const int32_t RG = ps[0] - G, RH = ps[1] - H, RT = ps[2] - T;
+        ps[0] = G;
+        ps[1] = H;
+        ps[2] = T;
+        rs[0] = RG;
+        rs[1] = RH;
+        rs[2] = RT;
+        if (sml == nr) {
+          G = RG;
+          H = RH;
+          T = RT;
+        }
+      } else if (mode == 1) {
+        int32_t* ps = L.int_slots + ci * 3;
+        ps[0] = G;
+        ps[1] = H;
+        ps[2] = T;
+      }
+      cs[2 * b] = (double)G * vg1;
+      cs[2 * b + 1] = (double)((long long)H - 3ll * T) * vh1 + (double)T * vh3;
+      tg += G;
+      th += H;
+      t3 += T;
+    }
+  }
+
+  if (!(mode == 0 && skip)) {
+    const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
+    double sg, sh, weight;
+    int32_t nrows;
+    if (mode == 1) {
+      for (int off = 32; off >= 1; off >>= 1) {
+        tg += __shfl_xor(tg, off);
+        th += __shfl_xor(th, off);
+        t3 += __shfl_xor(t3, off);
+      }
+      if (lane_id() == 0) {
+        tot[0][tid >> 6] = tg;
+        tot[1][tid >> 6] = th;
+        tot[2][tid >> 6] = t3;
+      }
+      __syncthreads();
+      long long G = 0, H = 0, T = 0;
+      for (int w = 0; w < SCAN_THREADS / LGBM_WAVE; ++w) {
+        G += tot[0][w];
+        H += tot[1][w];
+        T += tot[2][w];
+      }
+      // LeafSplits::init (leaf_splits.rs:75-89): the ordered f64 fold of the
+      // dequantized values equals these exact integer-weighted sums.
+      sg = (double)G * vg1;
+      sh = (double)(H - 3ll * T) * vh1 + (double)T * vh3;
+      nrows = (int32_t)L.N;
+      const lgbm_gain_config& cfg = ctl->cfg;
+      weight = leaf_output_full(cfg.lambda_l1 > 0.0, sg, sh, cfg.lambda_l1, cfg.lambda_l2,
+                                cfg.max_delta_step, false, cfg.path_smooth, 0, 0.0);
+      if (f == 0 && tid == 0) {
+        ctl->sm.sg = sg;
+        ctl->sm.sh = sh;
+        ctl->sm.weight = weight;
+        ctl->sm.n = nrows;
+        L.tree.leaf_value[0] = weight;
+        if (!(sh > 0.0)) {
+          ctl->error |= ERR_ROOT_HESSIAN;
+          ctl->done = 1;
+        }
+      }
+    } else {
+      sg = ctl->sm.sg;
+      sh = ctl->sm.sh;
+      weight = ctl->sm.weight;
+      nrows = ctl->sm.n;
+    }
+    __syncthreads();
+
+    const int32_t left_leaf = ctl->left_leaf;
+    const int32_t smaller = mode == 1 ? 0 : ctl->smaller;
+    const int32_t larger = mode == 0 ? ctl->larger : -1;
+    const bool pgate = mode == 0 && L.splittable[(size_t)left_leaf * F + f] == 0;
+    const bool buildable = sh > 0.0 && nrows > 0;
+
+    if (!buildable || pgate) {
+      for (int i = tid; i < 2 * nb; i += SCAN_THREADS) cs[i] = 0.0;
+    } else {
+      // FixHistogram (fix_histogram.rs:50-80): sequential f64 subtraction in ascending
+      // bin order, each wave-0 lane holding one bin and broadcasting it in turn.
+      const int mfb = (int)ft.mfb;
+      __syncthreads();
+      if (tid < LGBM_WAVE && mfb > 0 && mfb < nb) {
+        double g = sg, h = sh;
+        for (int c0 = 0; c0 < nb; c0 += LGBM_WAVE) {
+          const int bb = c0 + tid;
+          const double vg = bb < nb ? cs[2 * bb] : 0.0;
+          const double vh = bb < nb ? cs[2 * bb + 1] : 0.0;
+          const int lim = min(LGBM_WAVE, nb - c0);
+          for (int i = 0; i < lim; ++i) {
+            if (c0 + i != mfb) {
+              g -= readlane_f64(vg, i);
+              h -= readlane_f64(vh, i);
+            }
+          }
+        }
+        if (tid == 0) {
+          cs[2 * mfb] = g;
+          cs[2 * mfb + 1] = h;
+        }
+      }
+      __syncthreads();
+      // compact_histogram (learner.rs:4460-4492)
+      if (ft.offset > 0) {
+        const int off = ft.offset;
+        double a[4], b2[4];
+        int k = 0;
+        for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
+          const int src = c + off;
+          a[k] = src < nb ? cs[2 * src] : 0.0;
+          b2[k] = src < nb ? cs[2 * src + 1] : 0.0;
+        }
+        __syncthreads();
+        k = 0;
+        for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
+          cs[2 * c] = a[k];
+          cs[2 * c + 1] = b2[k];
+        }
+      }
+    }
+    __syncthreads();
+
+    if (mode == 2) {
+      for (int i = tid; i < 2 * nb; i += SCAN_THREADS) explicit_out[ft.slot_off + i] = cs[i];
+      return;
+    }
+    const size_t sl = L.slot_len;
+    double* s_small = L.slots + (size_t)smaller * sl + ft.slot_off;
+    if (larger >= 0) {
+      // parent region lives in the slot of left_leaf (the split leaf keeps its id)
+      const double* s_par = L.slots + (size_t)left_leaf * sl + ft.slot_off;
+      for (int i = tid; i < 2 * nb; i += SCAN_THREADS) cp[i] = s_par[i];
+      __syncthreads();
+      double* s_large = L.slots + (size_t)larger * sl + ft.slot_off;
+      for (int i = tid; i < 2 * nb; i += SCAN_THREADS) {
+        const double d = cp[i] - cs[i];
+        cp[i] = d;
+        s_small[i] = cs[i];
+        s_large[i] = d;
+      }
+    } else {
+      for (int i = tid; i < 2 * nb; i += SCAN_THREADS) s_small[i] = cs[i];
+    }
+    __syncthreads();
+
+    // ---- scans: wave 0 -> smaller (or root), wave 1 -> larger ----
+    if (!skip) {
+      const int wave = tid >> 6;
+      const bool have = wave == 0 || larger >= 0;
+      if (have) {
+        const int32_t leaf = wave == 0 ? smaller : larger;
+        const double* hist = wave == 0 ? cs : cp;
+        const double lsg = wave == 0 ? sg : ctl->lg.sg;
+        const double lsh = wave == 0 ? sh : ctl->lg.sh;
+        const double lpo = wave == 0 ? weight : ctl->lg.weight;
+        const int32_t ln = wave == 0 ? nrows : ctl->lg.n;
+        lgbm_split_info* out = L.feat_split + (size_t)leaf * F + f;
+        const bool scannable = lsh > 0.0 && ln > 0;
+        if (!scannable) {
+          if (lane_id() == 0) split_set_none(out);
+        } else if (pgate) {
+          if (lane_id() == 0) {
+            split_set_none(out);
+            L.splittable[(size_t)leaf * F + f] = 0;
+          }
+        } else {
+          const lgbm_gain_config cfg = ctl->cfg;
+          const ScanCfg sc = make_scan_cfg(cfg);
+          wave_scan(hist, ft, sc, lsg, lsh, ln, lpo, out);
+          if (lane_id() == 0)
+            L.splittable[(size_t)leaf * F + f] = out->gain > -__builtin_inf() ? 1 : 0;
+        }
+      }
+    }
+  }
+  // ---- the last block to finish runs the split step ----
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const int32_t prev =
+        __hip_atomic_fetch_add(&ctl->fs_count, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (int32_t)gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  if (tid == 0) __hip_atomic_store(&ctl->fs_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (ctl->done) return;
+  split_step(L);
+}
+
+// Per-op FindBestThreshold over explicit features (find_best_splits_batched,
+// lib.rs:1500-1548): one wave per feature, host-provided histogram.
+__global__ __launch_bounds__(LGBM_WAVE) void k_scan_explicit(const double* __restrict__ hist,
+                                                             const DevFeature* __restrict__ feats,
+                                                             int32_t n_feats,
+                                                             lgbm_gain_config cfg, double sg,
+                                                             double sh, int32_t n,
+                                                             lgbm_split_info* out) {
+  __shared__ double cs[2 * 256];
+  const int f = blockIdx.x;
+  if (f >= n_feats) return;
+  const DevFeature ft = feats[f];
+  for (int i = threadIdx.x; i < 2 * (int)ft.num_bin; i += LGBM_WAVE) cs[i] = hist[ft.slot_off + i];
+  __syncthreads();
+  const ScanCfg sc = make_scan_cfg(cfg);
+  wave_scan(cs, ft, sc, sg, sh, n, cfg.parent_output, out + f);
 }
 
 // ===========================================================================
@@ -892,11 +1002,58 @@ __global__ __launch_bounds__(256) void k_split(DevLearner L) {
 #define TS_INC 2ull
 #define SPIN_LIMIT (1 << 20)
 
+// Accumulate one row (packed quantized pair q) into the LDS histogram of all features.
+template <int W>
+__device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int32_t* cb, int F,
+                                             const uint4 (&w)[W], uint32_t q) {
+  const int32_t qg = (int32_t)(int8_t)(q & 0xffu);
+  const int32_t qh = (int32_t)(int8_t)(q >> 8);
+  const unsigned long long v = (unsigned long long)(long long)qg +
+                               ((unsigned long long)(uint32_t)qh << 22) +
+                               ((unsigned long long)(qh == 3 ? 1u : 0u) << 43);
+#pragma unroll
+  for (int wi = 0; wi < W; ++wi) {
+    const uint32_t ww[4] = {w[wi].x, w[wi].y, w[wi].z, w[wi].w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int f = wi * 16 + j;
+      if (f < F) {
+        const uint32_t bin = (ww[j >> 2] >> (8 * (j & 3))) & 0xffu;
+        __hip_atomic_fetch_add(&lds[cb[f] + bin], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+  }
+}
+
+// Flush a block's packed LDS histogram into the global [cells][3] integer cells.
+__device__ __forceinline__ void lds_hist_flush(const unsigned long long* lds, int cells,
+                                               int32_t* __restrict__ out) {
+  for (int c = threadIdx.x; c < cells; c += blockDim.x) {
+    const unsigned long long p = lds[c];
+    if (p == 0ull) continue;
+    const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
+    const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
+    const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
+    const int32_t hsum = (int32_t)(rest & ((1ull << 21) - 1));
+    const int32_t n3 = (int32_t)(rest >> 21);
+    int32_t* dst = out + (size_t)c * 3;
+    if (gsum) __hip_atomic_fetch_add(dst, (int32_t)gsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (hsum) __hip_atomic_fetch_add(dst + 1, hsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (n3) __hip_atomic_fetch_add(dst + 2, n3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// In the tree driver, the partition pass also builds the LEFT child's integer
+// histogram (ConstructHistogram over the rows routed left, accumulated while they are
+// in registers); the right child's is parent - left in integers (k_fixscan).  The
+// last split of a tree has no scan after it and skips the accumulation.
 template <int W>
 __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
+  extern __shared__ unsigned long long lds_hist[];
+  __shared__ int32_t cb[16 * LGBM_MAX_W];
   __shared__ int32_t s_tile;
-  __shared__ int32_t s_cnt[PART_ROWS_PER_THREAD][PART_THREADS / LGBM_WAVE];
-  __shared__ int32_t s_pref[PART_ROWS_PER_THREAD][PART_THREADS / LGBM_WAVE];
+  __shared__ int32_t s_cnt[PART_ROWS_PER_THREAD][PART_WAVES];
+  __shared__ int32_t s_pref[PART_ROWS_PER_THREAD][PART_WAVES];
   __shared__ int32_t s_total;
   __shared__ int32_t s_excl;
   Ctl* ctl = L.ctl;
@@ -906,8 +1063,14 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   const int64_t num_tiles = (count + PART_TILE - 1) / PART_TILE;
   const int64_t nblk = min((int64_t)gridDim.x, num_tiles);
   if ((int64_t)blockIdx.x >= nblk) return;
+  const bool accum = J.driver && ctl->num_leaves < ctl->max_leaves;
   const uint32_t epoch = ctl->epoch & 0x3fffffffu;
   const int tid = threadIdx.x, wave = tid >> 6;
+  const int F = L.F, cells = L.total_cells;
+  if (accum) {
+    for (int c = tid; c < cells; c += PART_THREADS) lds_hist[c] = 0ull;
+    for (int f = tid; f < F; f += PART_THREADS) cb[f] = (int32_t)L.feats[f].cell_base;
+  }
   const uint4* __restrict__ src = L.bufs.rec[J.src_buf];
   const uint16_t* __restrict__ sgh = L.bufs.gh[J.src_buf];
   uint4* __restrict__ dst = L.bufs.rec[J.dst_buf];
@@ -948,7 +1111,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     if (tid == 0) {
       int32_t acc = 0;
       for (int k = 0; k < PART_ROWS_PER_THREAD; ++k)
-        for (int wv = 0; wv < PART_THREADS / LGBM_WAVE; ++wv) {
+        for (int wv = 0; wv < PART_WAVES; ++wv) {
           s_pref[k][wv] = acc;
           acc += s_cnt[k][wv];
         }
@@ -966,9 +1129,9 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
         int64_t p = t - 1;
         int spins = 0;
         while (p >= 0) {
-          const uint64_t s = __hip_atomic_load(&ts[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const bool fresh = (s >> 34) == (uint64_t)epoch;
-          const uint64_t flag = (s >> 32) & 3ull;
+          const uint64_t st = __hip_atomic_load(&ts[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const bool fresh = (st >> 34) == (uint64_t)epoch;
+          const uint64_t flag = (st >> 32) & 3ull;
           if (!fresh || flag == 0ull) {
             ++spins;
             const bool give_up =
@@ -983,7 +1146,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
             __builtin_amdgcn_s_sleep(1);
             continue;
           }
-          excl += (int64_t)(uint32_t)s;
+          excl += (int64_t)(uint32_t)st;
           if (flag == TS_INC) break;
           --p;
         }
@@ -1010,6 +1173,11 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
 #pragma unroll
       for (int i = 0; i < W; ++i) dst[d * W + i] = w[k][i];
       dgh[d] = q[k];
+    }
+    if (accum) {
+#pragma unroll
+      for (int k = 0; k < PART_ROWS_PER_THREAD; ++k)
+        if (isleft[k]) lds_hist_add<W>(lds_hist, cb, F, w[k], q[k]);
     }
     if (t == num_tiles - 1 && tid == 0) {
       const int32_t lc = (int32_t)(excl + s_total);
@@ -1051,18 +1219,16 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
         if (ctl->num_leaves >= ctl->max_leaves) did = false;  // last split: no scan follows
         ctl->skip = did ? 0 : 1;
         ctl->pending_reduce = did ? 1 : 0;
-        const int32_t s = ctl->smaller;
-        ctl->h_buf = J.dst_buf;
-        ctl->h_begin = L.leaves.begin[s];
-        ctl->h_count = L.leaves.count[s];
-        if (did) {
-          L.stats[0] += (double)L.leaves.count[s];
-          L.stats[1] += 1.0;
-        }
+        L.stats[0] += (double)count;
+        L.stats[1] += 1.0;
       } else {
         ctl->part_left_count = lc;
       }
     }
+  }
+  if (accum) {
+    __syncthreads();
+    lds_hist_flush(lds_hist, cells, L.hist_int);
   }
   if (tid == 0) {
     const int32_t prev =
@@ -1088,8 +1254,10 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth)
   for (int i = tid; i < max_leaves; i += nthr) {
     split_set_none(&L.best[i]);
     L.best_feat[i] = -1;
+    L.best_fpos[i] = -1;
   }
   for (int i = tid; i < max_leaves * F; i += nthr) L.splittable[i] = 1;
+  for (int i = tid; i < L.total_cells * 3; i += nthr) L.hist_int[i] = 0;
   if (tid == 0) {
     const int32_t N = (int32_t)L.N;
     ctl->done = 0;
@@ -1118,6 +1286,7 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth)
     L.tree.leaf_weight[0] = 0.0;
     L.tree.leaf_value[0] = 0.0;
     L.stats[2] += (double)N;
+    L.stats[3] += 1.0;
   }
 }
 
@@ -1150,6 +1319,13 @@ __global__ __launch_bounds__(256) void k_score_update(DevLearner L, double lr,
       node = route_right(bin, n.pmin, n.max_bin, n.th, n.na_bin, n.flags) ? n.right : n.left;
     }
     if (node < 0 && ~node < nl) score[r] += vals[~node];
+  }
+}
+
+__global__ void k_tree_finalize(DevLearner L) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    L.tree.header[0] = L.ctl->num_leaves;
+    L.tree.header[1] = L.ctl->error;
   }
 }
 
@@ -1214,26 +1390,25 @@ void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t W, u
   const int64_t blocks = (n + 255) / 256;
   k_pack_records<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(bins, n, F, W, rec);
 }
-void launch_absmax(const float* g, const float* h, int64_t n, Ctl* ctl, hipStream_t s) {
-  int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
-  if (blocks < 1) blocks = 1;
-  k_absmax<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(g, h, n, ctl);
+int32_t stat_blocks(int64_t n) {
+  return (int32_t)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, STAT_BLOCKS));
+}
+void launch_absmax(const float* g, const float* h, int64_t n, uint4* partials, hipStream_t s) {
+  k_absmax<<<dim3((unsigned)stat_blocks(n)), dim3(256), 0, s>>>(g, h, n, partials);
 }
 void launch_grad_binary(const double* score, const float* label, float* g, float* h, int64_t n,
-                        Ctl* ctl, hipStream_t s) {
-  int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
-  if (blocks < 1) blocks = 1;
-  k_grad_binary<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(score, label, g, h, n, ctl);
+                        uint4* partials, hipStream_t s) {
+  k_grad_binary<<<dim3((unsigned)stat_blocks(n)), dim3(256), 0, s>>>(score, label, g, h, n,
+                                                                     partials);
 }
-void launch_quant_scales(Ctl* ctl, int32_t bins, int32_t force_const, hipStream_t s) {
-  k_quant_scales<<<1, 1, 0, s>>>(ctl, bins, force_const);
+void launch_quant_scales(Ctl* ctl, const uint4* partials, int64_t n, int32_t bins,
+                         int32_t force_const, hipStream_t s) {
+  k_quant_scales<<<1, 256, 0, s>>>(ctl, partials, stat_blocks(n), bins, force_const);
 }
 void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,
                      const uint64_t* wave_mats, const uint64_t* lane_mats, uint64_t s0,
                      int32_t stochastic, uint16_t* gh, float* dg, float* dh, hipStream_t s) {
-  const int64_t rows_per_wave = (int64_t)LGBM_WAVE * QUANT_ROWS_PER_LANE;
-  const int64_t waves = (n + rows_per_wave - 1) / rows_per_wave;
-  const int64_t blocks = (waves + 3) / 4;
+  const int64_t blocks = (n + QUANT_BLOCK_ROWS - 1) / QUANT_BLOCK_ROWS;
   k_quantize<<<dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0, s>>>(
       g, h, n, ctl, wave_mats, lane_mats, s0, stochastic, gh, dg, dh);
 }
@@ -1255,12 +1430,12 @@ void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n
   k_scan_explicit<<<dim3((unsigned)n_feats), dim3(LGBM_WAVE), 0, s>>>(hist, feats, n_feats, cfg, sg,
                                                                        sh, n, out);
 }
-void launch_split(const DevLearner& L, hipStream_t s) { k_split<<<1, 256, 0, s>>>(L); }
 void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s) {
   int64_t blocks = PART_MAX_BLOCKS;
   if (count_hint > 0) blocks = std::min<int64_t>(blocks, (count_hint + PART_TILE - 1) / PART_TILE);
   if (blocks < 1) blocks = 1;
-  DISPATCH_W(W, (k_partition<kW><<<dim3((unsigned)blocks), dim3(PART_THREADS), 0, s>>>(L)));
+  const size_t lds = (size_t)std::max(L.total_cells, 1) * sizeof(unsigned long long);
+  DISPATCH_W(W, (k_partition<kW><<<dim3((unsigned)blocks), dim3(PART_THREADS), lds, s>>>(L)));
 }
 void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, hipStream_t s) {
   k_tree_init<<<dim3(16), dim3(256), 0, s>>>(L, max_leaves, max_depth);
@@ -1270,6 +1445,7 @@ void launch_score_update(const DevLearner& L, double lr, double* score, hipStrea
   if (blocks < 1) blocks = 1;
   DISPATCH_W(L.W, (k_score_update<kW><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(L, lr, score)));
 }
+void launch_tree_finalize(const DevLearner& L, hipStream_t s) { k_tree_finalize<<<1, 64, 0, s>>>(L); }
 void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
                           hipStream_t s) {
   DISPATCH_W(L.W, (k_export_layout<kW><<<dim3(64, (unsigned)num_leaves), dim3(256), 0, s>>>(

@@ -16,14 +16,16 @@
 #define HIST_MAX_BLOCKS 256             // one block per CU
 #define HIST_MIN_ROWS_PER_BLOCK 4096
 #define HIST_MAX_ROWS_PER_BLOCK ((1 << 19) - 1)  // packed 64-bit LDS cell field limits
-#define PART_THREADS 256
-#define PART_ROWS_PER_THREAD 8
+#define PART_THREADS 1024
+#define PART_WAVES (PART_THREADS / LGBM_WAVE)
+#define PART_ROWS_PER_THREAD 4
 #define PART_TILE (PART_THREADS * PART_ROWS_PER_THREAD)
-#define PART_MAX_BLOCKS 1024
+#define PART_MAX_BLOCKS 256
 #define SCAN_THREADS 128                // two waves: smaller leaf, larger leaf
-#define QUANT_ROWS_PER_LANE 32
+#define QUANT_ROWS_PER_LANE 16
 #define QUANT_LANE_MATS 6               // log2(64)
-#define QUANT_WAVE_MATS 26              // wave index bits (N <= 2^26 * 2048)
+#define QUANT_WAVE_MATS 27              // wave index bits (N <= 2^27 * 1024)
+#define STAT_BLOCKS 1024                // partial-statistics blocks of the g/h reduction
 
 // Buffer ids of the row stores.
 #define BUF_ORIG 0
@@ -87,8 +89,6 @@ struct Ctl {
   // ---- quantizer (per iteration) ----
   double gs, hs, igs, ihs;
   float vg1, vh1, vh3, _f0;
-  uint32_t max_g_bits, max_h_bits;  // |g|, |h| maxima as f32 bit patterns
-  uint32_t hmin_key, hmax_key;       // order-preserving keys of min/max hessian
   int32_t quant_bins;
   int32_t const_hess;
   // ---- tree state ----
@@ -106,6 +106,8 @@ struct Ctl {
   uint32_t epoch;
   int32_t part_ticket, part_exit;
   int32_t part_left_count;
+  int32_t fs_count;                  // blocks of k_fixscan finished (self-resetting)
+  int32_t _i2;
   // ---- gain config ----
   lgbm_gain_config cfg;
 };
@@ -228,6 +230,17 @@ __device__ __forceinline__ double maybe_round_to_zero(double v) {
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & (LGBM_WAVE - 1); }
+
+// Broadcast lane `lane` (wave-uniform) of a register to the whole wave.
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ int32_t readlane_i32(int32_t v, int lane) {
+  return __builtin_amdgcn_readlane(v, lane);
+}
 
 __device__ __forceinline__ uint64_t lanemask_lt() {
   uint32_t l = lane_id();

@@ -327,3 +327,32 @@ def test_train_binary_matches_oracle(be):
                for t, o in zip(trees, otrees))
     assert same == iters
     np.testing.assert_allclose(scores, oscores, rtol=0, atol=1e-9)
+
+
+def test_graph_replays_match_eager():
+    """The captured per-tree graph, replayed with fresh gradients between eager work and
+    synchronizations, grows exactly the trees the per-launch path grows."""
+    n = 100_000
+    bins, meta, ub = make_binned(n, 11, seed=21)
+    os.environ["LGBM_HIP_GRAPHS"] = "0"
+    try:
+        eager = HipBackend(0)
+    finally:
+        del os.environ["LGBM_HIP_GRAPHS"]
+    graph = HipBackend(0)
+    try:
+        for be_ in (eager, graph):
+            be_.upload_resident_bins(bins, meta, ub)
+        cfg = GainConfig.make(min_data_in_leaf=20)
+        for rep in range(4):
+            g, h, _ = binary_gh(n, seed=100 + rep)
+            outs = []
+            for be_ in (eager, graph):
+                be_.upload_resident_grad_hess(g, h)
+                be_.discretize_dequantize_in_place(4, True, rep)
+                outs.append(be_.grow_tree_on_device_with_cfg(cfg, 63, -1))
+            _compare_trees(outs[1][0], outs[0][0], ("replay", rep))
+            assert np.array_equal(outs[1][1]["indices"], outs[0][1]["indices"])
+    finally:
+        eager.close()
+        graph.close()
