@@ -27,6 +27,26 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def traffic_for(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary.
+
+    profiles/traffic_config1_10.5Mx28.md holds, per kernel, the FETCH_SIZE and
+    WRITE_SIZE readings of two counter runs of this script, each already scaled
+    by what the same counter reads for a device copy of known size (the
+    --copy-probe-mib kernel), as lines `traffic <kernel> <bytes per launch>`.
+    Returns None when no such measurement exists."""
+    path = os.path.join(ROOT, "profiles", "traffic_config1_10.5Mx28.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.strip().strip("`").split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel:
+                    return float(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -39,6 +59,10 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--prof-steps", type=int, default=3,
                     help="extra iterations timed per kernel with HIP events")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="after the run, copy a buffer of this many MiB device-to-device "
+                         "(3 times): the known-size kernel that scales rocprofv3 "
+                         "FETCH_SIZE/WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (--gpus {args.gpus} requested): this build "
@@ -88,6 +112,15 @@ def main():
         be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=False)
     tm = be.timing()
     be.close()
+    if args.copy_probe_mib > 0 and dev is not None:
+        nb = args.copy_probe_mib << 20
+        src = torch.ones(nb // 4, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: {nb} bytes read + {nb} bytes written per launch")
+        del src, dst
     tsteps = max(args.prof_steps, 1)
     ms_per_step = elapsed / args.steps * 1e3
     s_per_100 = elapsed / args.steps * 100.0
@@ -144,7 +177,7 @@ def main():
         "partition_hist_GBps": round(part_gbs, 2),
         "roofline": {"bound": "hbm", "achieved": round(dom[1], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dom[1] / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": traffic_for(dom[0].split()[0]),
                      "kernel": dom[0],
                      "bytes_per_launch": round(dom[2] / max(dom[3], 1), 1),
                      "launches": int(dom[3]),

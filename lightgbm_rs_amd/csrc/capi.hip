@@ -82,6 +82,12 @@ struct lgbm_hip_ctx {
   bool timing = false;
   std::vector<EventPair> ev_pool;
   size_t ev_used = 0;
+  // Per-tree chain: chain[0] is a marker recorded before the tree's first kernel,
+  // chain[i] (i > 0) is stamped by kernel i at its end; kernel i's time is
+  // chain[i] - chain[i-1] (its own duration plus the dispatch gap before it).
+  std::vector<hipEvent_t> chain;
+  std::vector<int> chain_family;
+  size_t chain_used = 0;
   double ms[5] = {0, 0, 0, 0, 0};
 };
 
@@ -293,14 +299,38 @@ hipEvent_t ev_begin(lgbm_hip_ctx* c, int family) {
   if (!c->timing) return nullptr;
   if (c->ev_used == c->ev_pool.size()) {
     EventPair p{};
-    (void)hipEventCreate(&p.a);
-    (void)hipEventCreate(&p.b);
+    (void)hipEventCreateWithFlags(&p.a, hipEventDisableSystemFence);
+    (void)hipEventCreateWithFlags(&p.b, hipEventDisableSystemFence);
     c->ev_pool.push_back(p);
   }
   EventPair& p = c->ev_pool[c->ev_used];
   p.family = family;
   (void)hipEventRecord(p.a, c->stream);
   return p.a;
+}
+hipEvent_t chain_next(lgbm_hip_ctx* c, int family) {
+  if (c->chain_used == c->chain.size()) {
+    hipEvent_t e = nullptr;
+    (void)hipEventCreateWithFlags(&e, hipEventDisableSystemFence);
+    c->chain.push_back(e);
+    c->chain_family.push_back(-1);
+  }
+  c->chain_family[c->chain_used] = family;
+  return c->chain[c->chain_used++];
+}
+// Opens a chain: a plain marker ahead of the first chained kernel.
+void chain_start(lgbm_hip_ctx* c) {
+  if (!c->timing) return;
+  (void)hipEventRecord(chain_next(c, -1), c->stream);
+}
+// The stop event for one kernel launch of the chain (family -1: not counted).  The
+// launch binds it to the kernel's own end (hipExtLaunchKernel), so no marker packet
+// sits between consecutive kernels.
+const KernelEvents* ev_kernel(lgbm_hip_ctx* c, int family, KernelEvents* slot) {
+  if (!c->timing) return nullptr;
+  slot->start = nullptr;
+  slot->stop = chain_next(c, family);
+  return slot;
 }
 void ev_end(lgbm_hip_ctx* c) {
   if (!c->timing) return;
@@ -315,6 +345,13 @@ void ev_collect(lgbm_hip_ctx* c) {
       c->ms[c->ev_pool[i].family] += ms;
   }
   c->ev_used = 0;
+  for (size_t i = 1; i < c->chain_used; ++i) {
+    float ms = 0.f;
+    if (c->chain_family[i] >= 0 &&
+        hipEventElapsedTime(&ms, c->chain[i - 1], c->chain[i]) == hipSuccess)
+      c->ms[c->chain_family[i]] += ms;
+  }
+  c->chain_used = 0;
 }
 enum { FAM_HIST = 0, FAM_PART = 1, FAM_SCAN = 2, FAM_QUANT = 3, FAM_OBJ = 4 };
 
@@ -343,22 +380,14 @@ int do_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_t seed
 // histogram) and, unless it is the last split, the scan that picks split s + 1.
 void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth) {
   DevLearner L = make_learner(c);
-  launch_tree_init(L, num_leaves, max_depth, c->stream);
-  ev_begin(c, FAM_HIST);
-  launch_hist(L, 2, c->N, c->stream);
-  ev_end(c);
-  ev_begin(c, FAM_SCAN);
-  launch_fixscan(L, 1, nullptr, c->stream);
-  ev_end(c);
+  KernelEvents ke;
+  chain_start(c);
+  launch_tree_init(L, num_leaves, max_depth, c->stream, ev_kernel(c, -1, &ke));
+  launch_hist(L, 2, c->N, c->stream, ev_kernel(c, FAM_HIST, &ke));
+  launch_fixscan(L, 1, nullptr, c->stream, ev_kernel(c, FAM_SCAN, &ke));
   for (int32_t s = 1; s < num_leaves; ++s) {
-    ev_begin(c, FAM_PART);
-    launch_partition(L, c->W, s == 1 ? c->N : 0, c->stream);
-    ev_end(c);
-    if (s + 1 < num_leaves) {
-      ev_begin(c, FAM_SCAN);
-      launch_fixscan(L, 0, nullptr, c->stream);
-      ev_end(c);
-    }
+    launch_partition(L, c->W, s == 1 ? c->N : 0, c->stream, ev_kernel(c, FAM_PART, &ke));
+    if (s + 1 < num_leaves) launch_fixscan(L, 0, nullptr, c->stream, ev_kernel(c, FAM_SCAN, &ke));
   }
 }
 
@@ -563,6 +592,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
     (void)hipEventDestroy(p.a);
     (void)hipEventDestroy(p.b);
   }
+  for (hipEvent_t e : c->chain) (void)hipEventDestroy(e);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
   return LGBM_HIP_OK;
@@ -965,10 +995,9 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
   c->quant_ready = true;
   c->quant_bins = num_grad_quant_bins;
   if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth))) return rc;
-  ev_begin(c, FAM_OBJ);
   DevLearner L = make_learner(c);
-  launch_score_update(L, learning_rate, c->score, c->stream);
-  ev_end(c);
+  KernelEvents ke;
+  launch_score_update(L, learning_rate, c->score, c->stream, ev_kernel(c, FAM_OBJ, &ke));
   HIPCHK(c, hipGetLastError());
   return finish_tree(c, tree, nullptr, learning_rate);
 }

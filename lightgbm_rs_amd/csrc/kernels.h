@@ -79,6 +79,13 @@ struct DevLearner {
 };
 
 namespace lgbm {
+// Per-launch timing: when either event is set, the launch goes through
+// hipExtLaunchKernel, which binds `start` / `stop` to that kernel's begin / end.
+struct KernelEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+
 void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t W, uint4* rec,
                          hipStream_t s);
 void launch_absmax(const float* g, const float* h, int64_t n, uint4* partials, hipStream_t s);
@@ -89,14 +96,19 @@ void launch_quant_scales(Ctl* ctl, const uint4* partials, int64_t n, int32_t bin
 void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,
                      const uint64_t* wave_mats, const uint64_t* lane_mats, uint64_t s0,
                      int32_t stochastic, uint16_t* gh, float* dg, float* dh, hipStream_t s);
-void launch_hist(const DevLearner& L, int32_t driver, int64_t count_hint, hipStream_t s);
-void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s);
+void launch_hist(const DevLearner& L, int32_t driver, int64_t count_hint, hipStream_t s,
+                 const KernelEvents* ev = nullptr);
+void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s,
+                    const KernelEvents* ev = nullptr);
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,
                           lgbm_split_info* out, hipStream_t s);
-void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s);
-void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, hipStream_t s);
-void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s);
+void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s,
+                      const KernelEvents* ev = nullptr);
+void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, hipStream_t s,
+                      const KernelEvents* ev = nullptr);
+void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s,
+                         const KernelEvents* ev = nullptr);
 void launch_tree_finalize(const DevLearner& L, hipStream_t s);
 void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
                           hipStream_t s);

@@ -16,6 +16,8 @@
 //                    learner.rs:4380-4395)
 #include "kernels.h"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 
 namespace lgbm {
@@ -1385,6 +1387,16 @@ __global__ void k_pack_partition(const uint32_t* __restrict__ bins, int64_t n,
     default: break;                                                         \
   }
 
+// Launch `kern` plainly, or with the kernel-stamped events of `ev` when timing.
+#define KLAUNCH(ev, kern, grid, block, lds, s, ...)                                        \
+  do {                                                                                   \
+    if ((ev) && ((ev)->start || (ev)->stop))                                             \
+      hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)(lds), s, (ev)->start, (ev)->stop, \
+                            0u, __VA_ARGS__);                                            \
+    else                                                                                 \
+      kern<<<grid, block, lds, s>>>(__VA_ARGS__);                                        \
+  } while (0)
+
 void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t W, uint4* rec,
                          hipStream_t s) {
   const int64_t blocks = (n + 255) / 256;
@@ -1412,17 +1424,20 @@ void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,
   k_quantize<<<dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0, s>>>(
       g, h, n, ctl, wave_mats, lane_mats, s0, stochastic, gh, dg, dh);
 }
-void launch_hist(const DevLearner& L, int32_t driver, int64_t count_hint, hipStream_t s) {
+void launch_hist(const DevLearner& L, int32_t driver, int64_t count_hint, hipStream_t s,
+                 const KernelEvents* ev) {
   int64_t blocks = HIST_MAX_BLOCKS;
   if (count_hint > 0)
     blocks = std::min<int64_t>(HIST_MAX_BLOCKS,
                                (count_hint + HIST_MIN_ROWS_PER_BLOCK - 1) / HIST_MIN_ROWS_PER_BLOCK);
   if (blocks < 1) blocks = 1;
   const size_t lds = (size_t)L.total_cells * sizeof(unsigned long long);
-  DISPATCH_W(L.W, (k_hist<kW><<<dim3((unsigned)blocks), dim3(HIST_THREADS), lds, s>>>(L, driver)));
+  DISPATCH_W(L.W, KLAUNCH(ev, k_hist<kW>, dim3((unsigned)blocks), dim3(HIST_THREADS), lds, s, L,
+                          driver));
 }
-void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s) {
-  k_fixscan<<<dim3((unsigned)L.F), dim3(SCAN_THREADS), 0, s>>>(L, mode, explicit_out);
+void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s,
+                    const KernelEvents* ev) {
+  KLAUNCH(ev, k_fixscan, dim3((unsigned)L.F), dim3(SCAN_THREADS), 0, s, L, mode, explicit_out);
 }
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,
@@ -1430,20 +1445,24 @@ void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n
   k_scan_explicit<<<dim3((unsigned)n_feats), dim3(LGBM_WAVE), 0, s>>>(hist, feats, n_feats, cfg, sg,
                                                                        sh, n, out);
 }
-void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s) {
+void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s,
+                      const KernelEvents* ev) {
   int64_t blocks = PART_MAX_BLOCKS;
   if (count_hint > 0) blocks = std::min<int64_t>(blocks, (count_hint + PART_TILE - 1) / PART_TILE);
   if (blocks < 1) blocks = 1;
   const size_t lds = (size_t)std::max(L.total_cells, 1) * sizeof(unsigned long long);
-  DISPATCH_W(W, (k_partition<kW><<<dim3((unsigned)blocks), dim3(PART_THREADS), lds, s>>>(L)));
+  DISPATCH_W(W, KLAUNCH(ev, k_partition<kW>, dim3((unsigned)blocks), dim3(PART_THREADS), lds, s, L));
 }
-void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, hipStream_t s) {
-  k_tree_init<<<dim3(16), dim3(256), 0, s>>>(L, max_leaves, max_depth);
+void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, hipStream_t s,
+                      const KernelEvents* ev) {
+  KLAUNCH(ev, k_tree_init, dim3(16), dim3(256), 0, s, L, max_leaves, max_depth);
 }
-void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s) {
+void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s,
+                         const KernelEvents* ev) {
   int64_t blocks = std::min<int64_t>((L.N + 255) / 256, 4096);
   if (blocks < 1) blocks = 1;
-  DISPATCH_W(L.W, (k_score_update<kW><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(L, lr, score)));
+  DISPATCH_W(L.W, KLAUNCH(ev, k_score_update<kW>, dim3((unsigned)blocks), dim3(256), 0, s, L, lr,
+                          score));
 }
 void launch_tree_finalize(const DevLearner& L, hipStream_t s) { k_tree_finalize<<<1, 64, 0, s>>>(L); }
 void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
