@@ -126,10 +126,11 @@ def main():
     s_per_100 = elapsed / args.steps * 100.0
     F, cells, rec = tm["features"], tm["cells"], tm["record_bytes"]
     # Algorithmic bytes.  Root ConstructHistogram: rows x (F bin bytes + 2 B packed
-    # g/h) + cells x 2 x 4 B written.  Partition pass (also builds the left child's
-    # histogram): rows x (record + 2 B g/h) read and written + cells x 2 x 4 B.
+    # g/h) + cells x 2 x 4 B written.  Partition round (also builds one child's
+    # histogram per split): rows x (record + 2 B g/h) read and written + cells x 2 x
+    # 4 B per split.
     root_bytes = tm["root_rows"] * (F + 2) + tm["hist_launches"] * cells * 8
-    part_bytes = tm["partition_rows"] * 2 * (rec + 2) + tm["partition_launches"] * cells * 8
+    part_bytes = tm["partition_rows"] * 2 * (rec + 2) + tm["partition_jobs"] * cells * 8
     root_gbs = root_bytes / (tm["hist_ms"] * 1e-3) / 1e9 if tm["hist_ms"] > 0 else 0.0
     part_gbs = part_bytes / (tm["partition_ms"] * 1e-3) / 1e9 if tm["partition_ms"] > 0 else 0.0
     if tm["partition_ms"] >= tm["hist_ms"]:

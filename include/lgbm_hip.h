@@ -279,9 +279,12 @@ int lgbm_hip_get_timing(lgbm_hip_ctx* ctx, double* ms_out5, double* hist_bytes_o
  * reference's equivalent is its env-gated phase profiler, lgbm-treelearner/src/
  * phase_prof.rs:1-60).  out[0..4]: ms per kernel family as above; [5] root
  * ConstructHistogram rows; [6] root ConstructHistogram launches; [7] rows moved by
- * partition passes (which also build the left child's histogram); [8] partition
- * launches; [9] bytes per row record; [10] features; [11] histogram cells. */
-int lgbm_hip_get_stats(lgbm_hip_ctx* ctx, double* out12);
+ * partition passes (which also build one child's histogram per split); [8]
+ * partition launches; [9] bytes per row record; [10] features; [11] histogram
+ * cells; [12] leaf splits partitioned (including splits made ahead of their turn
+ * that the tree never used); [13] partition rounds over all trees; [14] trees;
+ * [15] rounds launched after the captured per-tree sequence. */
+int lgbm_hip_get_stats(lgbm_hip_ctx* ctx, double* out16);
 
 #ifdef __cplusplus
 }

@@ -48,19 +48,22 @@ struct lgbm_hip_ctx {
   float *g = nullptr, *h = nullptr, *label = nullptr;
   double* score = nullptr;
   int32_t* hist_int = nullptr;
+  int32_t* hist_acc = nullptr;
   uint64_t* tile_state = nullptr;
   int64_t tile_cap = 0;
   uint64_t *wave_mats = nullptr, *lane_mats = nullptr;
   double* stats = nullptr;
   uint4* partials = nullptr;  // per-block g/h statistics
-  // tree-sized
+  // tree-sized: node slots (SLOT_CAP(lcap)) and per-leaf arrays
   int32_t lcap = 0;
   double* slots = nullptr;
   lgbm_split_info *feat_split = nullptr, *best = nullptr;
-  int32_t* best_feat = nullptr;
   int32_t* best_fpos = nullptr;
   int32_t* int_slots = nullptr;
   uint8_t* splittable = nullptr;
+  int32_t* leaf_slot = nullptr;
+  int32_t* leaf_side = nullptr;
+  DevNodes nodes{};
   DevLeaves leaves{};
   DevTree tree{};
   void* tree_blob = nullptr;   // device tree arrays, one allocation
@@ -75,7 +78,11 @@ struct lgbm_hip_ctx {
   int64_t indices_cap = 0;
   // captured per-tree launch sequence (all parameters live in device memory)
   hipGraphExec_t graph_exec = nullptr;
-  int32_t graph_nl = -1, graph_md = 0;
+  int32_t graph_nl = -1, graph_md = 0, graph_rounds = 0, graph_spec = 0;
+  int32_t round_cap = 24;     // partition rounds in the captured sequence
+  int32_t spec_max = SPEC_DEFAULT;
+  int32_t* done_host = nullptr;  // pinned: ctl->done after the captured rounds
+  double tree_rounds = 0.0, trees = 0.0, extra_rounds = 0.0;
   uint64_t graph_gen = 0, buf_gen = 1;
   bool use_graphs = true;
   // timing
@@ -177,13 +184,16 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.N = c->N;
   L.slot_len = c->slot_len;
   L.hist_int = c->hist_int;
+  L.hist_acc = c->hist_acc;
   L.slots = c->slots;
   L.feat_split = c->feat_split;
   L.best = c->best;
-  L.best_feat = c->best_feat;
   L.best_fpos = c->best_fpos;
   L.int_slots = c->int_slots;
   L.splittable = c->splittable;
+  L.leaf_slot = c->leaf_slot;
+  L.leaf_side = c->leaf_side;
+  L.nodes = c->nodes;
   L.tile_state = c->tile_state;
   L.stats = c->stats;
   L.leaves = c->leaves;
@@ -231,8 +241,11 @@ int ensure_scratch_bytes(lgbm_hip_ctx* c, size_t bytes) {
   return LGBM_HIP_OK;
 }
 
+// A round's tiles: every job rounds its own rows up to whole tiles, so the jobs of
+// one round (disjoint leaves, at most SPEC_MAX) use at most rows / PART_TILE +
+// SPEC_MAX tiles.
 int ensure_tile_state(lgbm_hip_ctx* c, int64_t rows) {
-  const int64_t tiles = (rows + PART_TILE - 1) / PART_TILE + 1;
+  const int64_t tiles = (rows + PART_TILE - 1) / PART_TILE + SPEC_MAX + 1;
   if (c->tile_cap >= tiles) return LGBM_HIP_OK;
   c->buf_gen++;
   int rc = dalloc(c, &c->tile_state, (size_t)tiles);
@@ -246,17 +259,29 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   if (c->lcap >= L) return LGBM_HIP_OK;
   int rc = 0;
   const size_t F = (size_t)c->F;
-  if ((rc = dalloc(c, &c->slots, (size_t)L * c->slot_len))) return rc;
-  if ((rc = dalloc(c, &c->feat_split, (size_t)L * F))) return rc;
-  if ((rc = dalloc(c, &c->best, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &c->best_feat, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &c->splittable, (size_t)L * F))) return rc;
+  const size_t P = (size_t)SLOT_CAP(L);  // node slots
+  if ((rc = dalloc(c, &c->slots, P * c->slot_len))) return rc;
+  if ((rc = dalloc(c, &c->feat_split, P * F))) return rc;
+  if ((rc = dalloc(c, &c->best, P))) return rc;
+  if ((rc = dalloc(c, &c->splittable, P * F))) return rc;
+  if ((rc = dalloc(c, &c->best_fpos, P))) return rc;
+  if ((rc = dalloc(c, &c->int_slots, P * c->total_cells * 3))) return rc;
+  DevNodes& nd = c->nodes;
+  if ((rc = dalloc(c, &nd.begin, P))) return rc;
+  if ((rc = dalloc(c, &nd.count, P))) return rc;
+  if ((rc = dalloc(c, &nd.buf, P))) return rc;
+  if ((rc = dalloc(c, &nd.rev, P))) return rc;
+  if ((rc = dalloc(c, &nd.depth, P))) return rc;
+  if ((rc = dalloc(c, &nd.child, 2 * P))) return rc;
+  if ((rc = dalloc(c, &nd.sums, P))) return rc;
+  if ((rc = dalloc(c, &nd.key_gain, P))) return rc;
+  if ((rc = dalloc(c, &nd.key_feat, P))) return rc;
+  if ((rc = dalloc(c, &c->leaf_slot, (size_t)MAX_LEAVES))) return rc;
+  if ((rc = dalloc(c, &c->leaf_side, (size_t)MAX_LEAVES))) return rc;
   if ((rc = dalloc(c, &c->leaves.begin, (size_t)L))) return rc;
   if ((rc = dalloc(c, &c->leaves.count, (size_t)L))) return rc;
   if ((rc = dalloc(c, &c->leaves.buf, (size_t)L))) return rc;
   if ((rc = dalloc(c, &c->leaves.rev, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &c->best_fpos, (size_t)L))) return rc;
-  if ((rc = dalloc(c, &c->int_slots, (size_t)L * c->total_cells * 3))) return rc;
   if ((rc = dalloc(c, &c->tree.nodes, (size_t)L))) return rc;
   // tree arrays: one device blob (one readback per tree) + pinned host staging
   const size_t sizes[15] = {64, 4, 4, 8, 4, 1, 4, 4, 8, 4, 8, 8, 4, 4, 4};
@@ -375,20 +400,63 @@ int do_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_t seed
   return LGBM_HIP_OK;
 }
 
-// The per-tree kernel sequence: root histogram + scan (whose last block picks split
-// 1), then per split s a partition pass (which also builds the left child's
-// histogram) and, unless it is the last split, the scan that picks split s + 1.
-void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth) {
+// One partition round: plan (commit finished splits, pick the next leaves), the
+// partition pass of every picked leaf, and the children's scans.  Rounds after the
+// tree is complete return at once.
+void enqueue_rounds(lgbm_hip_ctx* c, int32_t rounds) {
+  DevLearner L = make_learner(c);
+  KernelEvents ke;
+  for (int32_t r = 0; r < rounds; ++r) {
+    launch_plan(L, c->stream, ev_kernel(c, FAM_SCAN, &ke));
+    launch_partition(L, c->W, 0, c->stream, ev_kernel(c, FAM_PART, &ke));
+    launch_pair_scan(L, c->stream, ev_kernel(c, FAM_SCAN, &ke));
+  }
+}
+
+// The per-tree kernel sequence: reset, root histogram + root scan, then rounds.
+void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth, int32_t rounds) {
   DevLearner L = make_learner(c);
   KernelEvents ke;
   chain_start(c);
-  launch_tree_init(L, num_leaves, max_depth, c->stream, ev_kernel(c, -1, &ke));
+  launch_tree_init(L, num_leaves, max_depth, SLOT_CAP(num_leaves), c->spec_max, c->stream,
+                   ev_kernel(c, -1, &ke));
   launch_hist(L, 2, c->N, c->stream, ev_kernel(c, FAM_HIST, &ke));
   launch_fixscan(L, 1, nullptr, c->stream, ev_kernel(c, FAM_SCAN, &ke));
-  for (int32_t s = 1; s < num_leaves; ++s) {
-    launch_partition(L, c->W, s == 1 ? c->N : 0, c->stream, ev_kernel(c, FAM_PART, &ke));
-    if (s + 1 < num_leaves) launch_fixscan(L, 0, nullptr, c->stream, ev_kernel(c, FAM_SCAN, &ke));
+  enqueue_rounds(c, rounds);
+}
+
+// After the enqueued rounds: rounds commit at least one split each once the first
+// leaf is picked, so a tree needs at most num_leaves + 1 plans.  Runs further rounds
+// (checked after every chunk) until the plan reports the tree complete, then the
+// finalize kernel.
+int finish_rounds(lgbm_hip_ctx* c, int32_t num_leaves, int32_t rounds) {
+  static_assert(offsetof(Ctl, rounds) - offsetof(Ctl, done) < 64, "ctl readback window");
+  const size_t r_off = (offsetof(Ctl, rounds) - offsetof(Ctl, done)) / 4;
+  int32_t done_rounds = rounds;
+  while (true) {
+    HIPCHK(c, hipMemcpyAsync(c->done_host, (char*)c->ctl + CTL_OFF(done), r_off * 4 + 4,
+                             hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (c->done_host[0]) {
+      // Plans this tree ran; a longer captured sequence serves the next trees (later
+      // boosting iterations tend to need more rounds).
+      const int32_t used = c->done_host[r_off];
+      if (used > c->round_cap) c->round_cap = std::min(num_leaves + 1, used + 2);
+      break;
+    }
+    if (done_rounds > num_leaves + 2)
+      return set_err(c, LGBM_HIP_ERR_RUNTIME, "tree driver did not complete");
+    const int32_t chunk = 4;
+    enqueue_rounds(c, chunk);
+    HIPCHK(c, hipGetLastError());
+    done_rounds += chunk;
+    c->extra_rounds += chunk;
   }
+  DevLearner L = make_learner(c);
+  KernelEvents ke;
+  launch_tree_finalize(L, c->stream, ev_kernel(c, -1, &ke));
+  HIPCHK(c, hipGetLastError());
+  return LGBM_HIP_OK;
 }
 
 int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_leaves,
@@ -397,20 +465,21 @@ int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_le
   if (rc) return rc;
   HIPCHK(c, hipMemcpyAsync((char*)c->ctl + CTL_OFF(cfg), cfg, sizeof(*cfg), hipMemcpyHostToDevice,
                            c->stream));
+  const int32_t rounds = std::max(1, std::min(c->round_cap, num_leaves + 1));
   if (c->timing || !c->use_graphs) {
-    enqueue_tree(c, num_leaves, max_depth);
+    enqueue_tree(c, num_leaves, max_depth, rounds);
     HIPCHK(c, hipGetLastError());
-    return LGBM_HIP_OK;
+    return finish_rounds(c, num_leaves, rounds);
   }
   if (!(c->graph_exec && c->graph_nl == num_leaves && c->graph_md == max_depth &&
-        c->graph_gen == c->buf_gen)) {
+        c->graph_gen == c->buf_gen && c->graph_rounds == rounds && c->graph_spec == c->spec_max)) {
     if (c->graph_exec) {
       (void)hipGraphExecDestroy(c->graph_exec);
       c->graph_exec = nullptr;
     }
     hipGraph_t g = nullptr;
     HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    enqueue_tree(c, num_leaves, max_depth);
+    enqueue_tree(c, num_leaves, max_depth, rounds);
     HIPCHK(c, hipStreamEndCapture(c->stream, &g));
     hipError_t e = hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
@@ -421,24 +490,27 @@ int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_le
     c->graph_nl = num_leaves;
     c->graph_md = max_depth;
     c->graph_gen = c->buf_gen;
+    c->graph_rounds = rounds;
+    c->graph_spec = c->spec_max;
   }
   HIPCHK(c, hipGraphLaunch(c->graph_exec, c->stream));
-  return LGBM_HIP_OK;
+  return finish_rounds(c, num_leaves, rounds);
 }
 
 int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, double shrink) {
-  DevLearner L0 = make_learner(c);
-  launch_tree_finalize(L0, c->stream);
   HIPCHK(c, hipMemcpyAsync(c->tree_host, c->tree_blob, out ? c->tree_blob_bytes : 64,
                            hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
   ev_collect(c);
   const char* hb = (const char*)c->tree_host;
   const int32_t nl = ((const int32_t*)hb)[0], err = ((const int32_t*)hb)[1];
+  c->tree_rounds += ((const int32_t*)hb)[2];
+  c->trees += 1.0;
   int rc = 0;
   if (err & ERR_ROOT_HESSIAN)
     return set_err(c, LGBM_HIP_ERR_INVALID_LEAF_HESSIAN, "root sum_hessian <= 0");
   if (err & ERR_SPIN) return set_err(c, LGBM_HIP_ERR_RUNTIME, "partition look-back spin limit");
+  if (err & ERR_SLOTS) return set_err(c, LGBM_HIP_ERR_RUNTIME, "node slot budget exhausted");
   if (err) return set_err(c, LGBM_HIP_ERR_RUNTIME, "device learner error");
   if (out) {
     out->num_leaves = nl;
@@ -536,11 +608,16 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   init.epoch = 1u;
   if (hipMemcpy(c->ctl, &init, sizeof(init), hipMemcpyHostToDevice) != hipSuccess)
     return fail(set_err(c, LGBM_HIP_ERR_HIP, "ctl init"));
-  if ((rc = dalloc(c, &c->stats, 4))) return fail(rc);
-  if (hipMemset(c->stats, 0, 32) != hipSuccess) return fail(set_err(c, LGBM_HIP_ERR_HIP, "stats"));
+  if ((rc = dalloc(c, &c->stats, 8))) return fail(rc);
+  if (hipMemset(c->stats, 0, 64) != hipSuccess) return fail(set_err(c, LGBM_HIP_ERR_HIP, "stats"));
+  if (hipHostMalloc((void**)&c->done_host, 64, hipHostMallocDefault) != hipSuccess)
+    return fail(set_err(c, LGBM_HIP_ERR_HIP, "hipHostMalloc"));
   if ((rc = init_jump_tables(c))) return fail(rc);
   if ((rc = dalloc(c, &c->partials, STAT_BLOCKS))) return fail(rc);
   if (const char* e = std::getenv("LGBM_HIP_GRAPHS")) c->use_graphs = std::strcmp(e, "0") != 0;
+  if (const char* e = std::getenv("LGBM_HIP_ROUNDS")) c->round_cap = std::max(1, std::atoi(e));
+  if (const char* e = std::getenv("LGBM_HIP_SPEC"))
+    c->spec_max = std::max(1, std::min(SPEC_MAX, std::atoi(e)));
   *out = c;
   return LGBM_HIP_OK;
 }
@@ -565,6 +642,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->label);
   F(c->score);
   F(c->hist_int);
+  F(c->hist_acc);
   F(c->tile_state);
   F(c->wave_mats);
   F(c->lane_mats);
@@ -577,8 +655,19 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->slots);
   F(c->feat_split);
   F(c->best);
-  F(c->best_feat);
   F(c->splittable);
+  F(c->leaf_slot);
+  F(c->leaf_side);
+  F(c->nodes.begin);
+  F(c->nodes.count);
+  F(c->nodes.buf);
+  F(c->nodes.rev);
+  F(c->nodes.depth);
+  F(c->nodes.child);
+  F(c->nodes.sums);
+  F(c->nodes.key_gain);
+  F(c->nodes.key_feat);
+  if (c->done_host) (void)hipHostFree(c->done_host);
   F(c->leaves.begin);
   F(c->leaves.count);
   F(c->leaves.buf);
@@ -681,6 +770,8 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   if ((rc = dalloc(c, &c->h, (size_t)num_data))) return rc;
   if ((rc = dalloc(c, &c->hist_int, (size_t)acc * 3))) return rc;
   HIPCHK(c, hipMemset(c->hist_int, 0, (size_t)acc * 3 * 4));
+  if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * acc * 3))) return rc;
+  HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * acc * 3 * 4));
   if ((rc = ensure_tile_state(c, num_data))) return rc;
   // transpose the feature-major upload into records
   uint8_t* tmp = nullptr;
@@ -907,6 +998,12 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   launch_pack_partition((const uint32_t*)c->scratch, n, c->rec[BUF_S0], c->stream);
   HIPCHK(c, hipMemsetAsync(c->gh[BUF_S0], 0, (size_t)n * 2, c->stream));
   PartJob J{};
+  J.parent = -1;
+  J.cl = -1;
+  J.cr = -1;
+  J.acc_right = -1;
+  J.ntiles = (int32_t)((n + PART_TILE - 1) / PART_TILE);
+  J.tile0 = 0;
   J.src_buf = BUF_S0;
   J.dst_buf = BUF_S1;
   J.begin = 0;
@@ -919,8 +1016,11 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   J.na_bin = (int32_t)num_bin - 1;
   J.flags = ((int32_t)most_freq_bin > (int32_t)threshold ? 1 : 0) | (na_as_missing ? 2 : 0) |
             (default_left ? 4 : 0);
-  J.driver = 0;
-  if ((rc = ctl_write(c, CTL_OFF(part), J))) return rc;
+  if ((rc = ctl_write(c, CTL_OFF(jobs), J))) return rc;
+  const int32_t one = 1;
+  if ((rc = ctl_write(c, CTL_OFF(n_jobs), one))) return rc;
+  const int64_t tiles = J.ntiles;
+  if ((rc = ctl_write(c, CTL_OFF(tile_total), tiles))) return rc;
   DevLearner L = make_learner(c);
   L.W = 1;
   launch_partition(L, 1, n, c->stream);
@@ -1019,13 +1119,14 @@ int lgbm_hip_set_timing(lgbm_hip_ctx* c, int32_t enable) {
   ev_collect(c);
   c->timing = enable != 0;
   for (double& m : c->ms) m = 0.0;
-  HIPCHK(c, hipMemset(c->stats, 0, 32));
+  HIPCHK(c, hipMemset(c->stats, 0, 64));
+  c->tree_rounds = c->trees = c->extra_rounds = 0.0;
   return LGBM_HIP_OK;
 }
 
 int lgbm_hip_get_timing(lgbm_hip_ctx* c, double* ms_out5, double* hist_bytes_out,
                         int64_t* hist_launches_out) {
-  double st[12];
+  double st[16];
   int rc = lgbm_hip_get_stats(c, st);
   if (rc) return rc;
   if (ms_out5)
@@ -1043,8 +1144,8 @@ int lgbm_hip_get_stats(lgbm_hip_ctx* c, double* out) {
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
   HIPCHK(c, hipStreamSynchronize(c->stream));
   ev_collect(c);
-  double st[4] = {0, 0, 0, 0};
-  HIPCHK(c, hipMemcpy(st, c->stats, 32, hipMemcpyDeviceToHost));
+  double st[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  HIPCHK(c, hipMemcpy(st, c->stats, 64, hipMemcpyDeviceToHost));
   for (int i = 0; i < 5; ++i) out[i] = c->ms[i];
   out[5] = st[2];
   out[6] = st[3];
@@ -1053,6 +1154,10 @@ int lgbm_hip_get_stats(lgbm_hip_ctx* c, double* out) {
   out[9] = 16.0 * c->W;
   out[10] = c->F;
   out[11] = c->total_cells;
+  out[12] = st[4];
+  out[13] = c->tree_rounds;
+  out[14] = c->trees;
+  out[15] = c->extra_rounds;
   return LGBM_HIP_OK;
 }
 

@@ -1,0 +1,781 @@
+// grow.hip — the leaf-wise tree driver on device, in rounds of partition jobs.
+//
+// The reference grows a tree best-first (SerialTreeLearner::train_inner,
+// crates/lgbm-treelearner/src/learner.rs:980-1562): split the leaf of highest gain
+// (ArgMax, learner.rs:4537), build the smaller child's histogram, derive the larger
+// one by subtraction, scan both, repeat.  Everything a split computes for its two
+// children depends only on the split leaf itself (its rows, histogram, sums, depth
+// and feature mask), never on the rest of the tree.  So each round here splits up to
+// SPEC_MAX leaves at once — the best-ranked leaves that are not split yet — and the
+// plan kernel then commits finished splits to the tree strictly in the reference's
+// ArgMax order, assigning leaf ids and node numbers exactly as Tree::split does.
+// A leaf split ahead of its turn that the reference never splits costs only the
+// wasted pass; the tree is the reference's tree either way.
+//
+//   k_tree_init    per-tree reset (DataPartition::new, root LeafSplits; learner.rs:
+//                  1242-1376)
+//   k_plan         per-leaf feature ArgMax of the children scanned last round
+//                  (learner.rs:3290-3330), commit loop (ArgMax + stop test,
+//                  learner.rs:1503, 4537; Tree::split bookkeeping, tree.rs:614-700),
+//                  selection of the next round's leaves and their partition jobs
+//                  (split_inner router, learner.rs:3895-4011)
+//   k_partition    DataPartition::split of every job of the round
+//                  (data_partition.rs:192-288,360-463) + the ConstructHistogram of
+//                  one child per job, accumulated while its rows are in registers
+//   k_pair_scan    per (feature, job): integer other-child = parent - built child,
+//                  exact f64 cells of the smaller child, FixHistogram, compaction,
+//                  larger = parent - smaller (histogram_pool.rs:249), and
+//                  FindBestThreshold of both children (kernels/split.rs:8970-9329)
+//   k_tree_finalize  leaf arrays of the Tree and the LeafPartitionLayout ranges
+#include "scan.h"
+
+#include <hip/hip_ext.h>
+
+#include <algorithm>
+
+namespace lgbm {
+
+#define TS_AGG 1ull
+#define TS_INC 2ull
+#define SPIN_LIMIT (1 << 20)
+#define PLAN_WAVES (PLAN_THREADS / LGBM_WAVE)
+#define INT_MAX32 0x7fffffff
+
+// Wave-level ordering point for LDS state written by one lane and read by all.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// SplitInner router inputs (split_inner, learner.rs:3957; data_partition.rs:387-417).
+__device__ __forceinline__ void router_of(const DevFeature& ft, const lgbm_split_info& b,
+                                          int32_t* pmin, int32_t* th, int32_t* flags) {
+  const int32_t pm = (int32_t)ft.min_bin + max(ft.offset, 0);
+  int32_t thr = (int32_t)b.threshold + pm;
+  if (ft.mfb == 0) thr -= 1;
+  int32_t fl = 0;
+  if ((int32_t)ft.mfb > (int32_t)b.threshold) fl |= 1;
+  if (ft.na_as_missing) fl |= 2;
+  if (b.default_left) fl |= 4;
+  *pmin = pm;
+  *th = thr;
+  *flags = fl;
+}
+
+// ===========================================================================
+// per-tree reset
+// ===========================================================================
+__global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth, int32_t slot_cap,
+                            int32_t spec_max) {
+  Ctl* ctl = L.ctl;
+  const int tid = blockIdx.x * blockDim.x + threadIdx.x;
+  const int nthr = gridDim.x * blockDim.x;
+  for (int i = tid; i < L.F; i += nthr) L.splittable[i] = 1;  // node slot 0
+  for (int i = tid; i < L.total_cells * 3; i += nthr) L.hist_int[i] = 0;
+  for (int i = tid; i < SPEC_MAX * L.total_cells * 3; i += nthr) L.hist_acc[i] = 0;
+  if (tid == 0) {
+    const int32_t N = (int32_t)L.N;
+    ctl->done = 0;
+    ctl->error = 0;
+    ctl->num_leaves = 1;
+    ctl->max_leaves = max_leaves;
+    ctl->max_depth = max_depth;
+    ctl->n_slots = 1;
+    ctl->slot_cap = slot_cap;
+    ctl->spec_max = spec_max;
+    ctl->n_jobs = 0;
+    ctl->rounds = 0;
+    ctl->tile_total = 0;
+    // root gate (before_find_best_split, learner.rs:1830-1836): a single leaf with
+    // fewer than 2 * min_data_in_leaf rows is never scanned
+    const bool did = N >= ctl->cfg.min_data_in_leaf * 2;
+    ctl->root_skip = did ? 0 : 1;
+    ctl->n_reduce = did ? 1 : 0;
+    ctl->reduce_list[0] = 0;
+    ctl->h_buf = BUF_ORIG;
+    ctl->h_begin = 0;
+    ctl->h_count = N;
+    DevNodes& nd = L.nodes;
+    nd.begin[0] = 0;
+    nd.count[0] = N;
+    nd.buf[0] = BUF_ORIG;
+    nd.rev[0] = 0;
+    nd.depth[0] = 0;
+    nd.child[0] = -1;
+    nd.child[1] = -1;
+    nd.sums[0] = LeafSums{0.0, 0.0, 0.0, N, 0};
+    nd.key_gain[0] = -__builtin_inf();
+    nd.key_feat[0] = -1;
+    split_set_none(&L.best[0]);
+    L.best_fpos[0] = -1;
+    L.leaf_slot[0] = 0;
+    L.leaf_side[0] = 0;
+    L.tree.leaf_parent[0] = -1;
+    L.stats[2] += (double)N;
+    L.stats[3] += 1.0;
+  }
+}
+
+// ===========================================================================
+// k_plan: one block.
+//   1. per-leaf feature ArgMax for the node slots scanned since the last plan
+//      (the argmax of scan_leaf_histogram, learner.rs:3290-3330);
+//   2. commit loop (wave 0): repeat the reference's ArgMax over the committed leaves
+//      (learner.rs:4537, split_gt order, first leaf id wins) and its stop test
+//      (gain <= 0, learner.rs:1503; num_leaves splits at most); while the chosen leaf
+//      has already been split, commit that split: node = num_leaves - 1, the left
+//      child keeps the leaf id, the right child gets id num_leaves (tree.rs:614-700);
+//   3. selection (wave 0): the chosen leaf, then the next best-ranked unsplit leaves
+//      with gain > 0, up to spec_max, while two node slots per split the tree may
+//      still need stay in reserve;
+//   4. (all threads) the Tree::split fields of the committed splits, and the
+//      partition jobs + child node slots of the selected leaves.
+// ===========================================================================
+__global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L) {
+  __shared__ double s_gain[SLOT_CAP(MAX_LEAVES)];
+  __shared__ int32_t s_feat[SLOT_CAP(MAX_LEAVES)];
+  __shared__ int32_t s_child[2 * SLOT_CAP(MAX_LEAVES)];
+  __shared__ int32_t s_leaf_slot[MAX_LEAVES];
+  __shared__ int32_t s_leaf_parent[MAX_LEAVES];
+  __shared__ int32_t s_leaf_side[MAX_LEAVES];
+  __shared__ int32_t s_left[MAX_LEAVES];
+  __shared__ int32_t s_right[MAX_LEAVES];
+  __shared__ int4 s_commit[MAX_LEAVES];  // (leaf, node slot, node, new right leaf)
+  __shared__ int4 s_pick[SPEC_MAX];      // (leaf, node slot, left slot, right slot)
+  __shared__ int32_t s_ntiles[SPEC_MAX];
+  __shared__ int32_t s_nc, s_nj, s_nl, s_done, s_nslots;
+  Ctl* ctl = L.ctl;
+  if (ctl->done) return;
+  const int tid = threadIdx.x;
+  const int lane = (int)lane_id();
+  const int wave = tid >> 6;
+  const int F = L.F;
+  const double ninf = -__builtin_inf();
+  const int32_t nl0 = ctl->num_leaves, ns0 = ctl->n_slots, maxl = ctl->max_leaves;
+  const DevNodes& nd = L.nodes;
+  DevTree& T = L.tree;
+  for (int s = tid; s < ns0; s += PLAN_THREADS) {
+    s_gain[s] = nd.key_gain[s];
+    s_feat[s] = nd.key_feat[s];
+    s_child[2 * s] = nd.child[2 * s];
+    s_child[2 * s + 1] = nd.child[2 * s + 1];
+  }
+  for (int l = tid; l < nl0; l += PLAN_THREADS) {
+    s_leaf_slot[l] = L.leaf_slot[l];
+    s_leaf_parent[l] = T.leaf_parent[l];
+    s_leaf_side[l] = L.leaf_side[l];
+  }
+  for (int n = tid; n < nl0 - 1; n += PLAN_THREADS) {
+    s_left[n] = T.left_child[n];
+    s_right[n] = T.right_child[n];
+  }
+  __syncthreads();
+
+  // ---- 1. per-slot feature ArgMax -------------------------------------------
+  const int nred = ctl->n_reduce;
+  for (int i = wave; i < nred; i += PLAN_WAVES) {
+    const int32_t s = ctl->reduce_list[i];
+    BestKey k{ninf, -1, INT_MAX32};
+    for (int f = lane; f < F; f += LGBM_WAVE) {
+      const double g = L.feat_split[(size_t)s * F + f].gain;
+      const BestKey c{g, L.feats[f].real_index, f};
+      if (g > ninf && key_better(c, k)) k = c;
+    }
+    k = wave_best(k);
+    const bool have = k.idx != INT_MAX32 && k.gain > ninf;
+    if (lane == 0) {
+      if (have) {
+        L.best[s] = L.feat_split[(size_t)s * F + k.idx];
+      } else {
+        split_set_none(&L.best[s]);
+      }
+      L.best_fpos[s] = have ? k.idx : -1;
+      nd.key_gain[s] = have ? k.gain : ninf;
+      nd.key_feat[s] = have ? k.feat : -1;
+      s_gain[s] = have ? k.gain : ninf;
+      s_feat[s] = have ? k.feat : -1;
+    }
+  }
+  __syncthreads();
+
+  // ---- 2./3. commit loop and selection (wave 0) -------------------------------
+  if (wave == 0) {
+    int32_t nl = nl0, nc = 0, ns = ns0, nj = 0;
+    int32_t done = ctl->error ? 1 : 0;
+    double kg[MAX_LEAVES / LGBM_WAVE];
+    int32_t kf[MAX_LEAVES / LGBM_WAVE];
+#pragma unroll
+    for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i) {
+      const int l = lane + LGBM_WAVE * i;
+      kg[i] = ninf;
+      kf[i] = -1;
+      if (l < nl) {
+        const int32_t s = s_leaf_slot[l];
+        kg[i] = s_gain[s];
+        kf[i] = s_feat[s];
+      }
+    }
+    while (!done) {
+      BestKey k{ninf, -1, INT_MAX32};
+#pragma unroll
+      for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i) {
+        const int l = lane + LGBM_WAVE * i;
+        const BestKey c{kg[i], kf[i], l};
+        if (l < nl && key_better(c, k)) k = c;
+      }
+      k = wave_best(k);
+      if (!(k.gain > 0.0) || nl >= maxl) {
+        done = 1;
+        break;
+      }
+      const int32_t bl = k.idx;
+      const int32_t p = s_leaf_slot[bl];
+      const int32_t cl = s_child[2 * p], cr = s_child[2 * p + 1];
+      if (cl < 0) break;  // not split yet: it leads the next round
+      const int32_t node = nl - 1, nr = nl;
+      if (lane == 0) {
+        const int32_t pn = s_leaf_parent[bl];
+        if (pn >= 0) {
+          if (s_leaf_side[bl])
+            s_right[pn] = node;
+          else
+            s_left[pn] = node;
+        }
+        s_left[node] = ~bl;
+        s_right[node] = ~nr;
+        s_leaf_parent[bl] = node;
+        s_leaf_side[bl] = 0;
+        s_leaf_parent[nr] = node;
+        s_leaf_side[nr] = 1;
+        s_leaf_slot[bl] = cl;
+        s_leaf_slot[nr] = cr;
+        s_commit[nc] = make_int4(bl, p, node, nr);
+      }
+      const double gl = s_gain[cl], gr = s_gain[cr];
+      const int32_t fl = s_feat[cl], fr = s_feat[cr];
+#pragma unroll
+      for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i) {
+        const int l = lane + LGBM_WAVE * i;
+        if (l == bl) {
+          kg[i] = gl;
+          kf[i] = fl;
+        }
+        if (l == nr) {
+          kg[i] = gr;
+          kf[i] = fr;
+        }
+      }
+      ++nc;
+      ++nl;
+      wave_sync();
+    }
+    if (!done) {
+      // The first pick is the ArgMax leaf the commit loop stopped at.  Further picks
+      // keep two node slots in reserve for every split the tree may still need, so
+      // the ArgMax leaf of every later round can always be split.
+      bool cand[MAX_LEAVES / LGBM_WAVE];
+#pragma unroll
+      for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i) {
+        const int l = lane + LGBM_WAVE * i;
+        cand[i] = l < nl && s_child[2 * s_leaf_slot[l]] < 0 && kg[i] > 0.0;
+      }
+      const int32_t take = ctl->spec_max;
+      const int32_t cap = ctl->slot_cap;
+      while (nj < take) {
+        BestKey k{ninf, -1, INT_MAX32};
+#pragma unroll
+        for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i) {
+          const BestKey c{kg[i], kf[i], lane + LGBM_WAVE * i};
+          if (cand[i] && key_better(c, k)) k = c;
+        }
+        k = wave_best(k);
+        if (!(k.gain > 0.0)) break;
+        if (nj == 0 ? ns + 2 > cap : ns + 2 + 2 * (maxl - nl) > cap) break;
+#pragma unroll
+        for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i)
+          if (lane + LGBM_WAVE * i == k.idx) cand[i] = false;
+        if (lane == 0) s_pick[nj] = make_int4(k.idx, s_leaf_slot[k.idx], ns, ns + 1);
+        ns += 2;
+        ++nj;
+      }
+      if (nj == 0) {  // the slot reserve makes this unreachable
+        done = 1;
+        if (lane == 0) atomicOr(&ctl->error, ERR_SLOTS);
+      }
+    }
+    if (lane == 0) {
+      s_nc = nc;
+      s_nj = nj;
+      s_nl = nl;
+      s_done = done;
+      s_nslots = ns;
+    }
+  }
+  __syncthreads();
+
+  // ---- 4. tree fields of the committed splits; jobs of the selected leaves ------
+  const int32_t nc = s_nc, nj = s_nj, nl = s_nl;
+  for (int c = tid; c < nc; c += PLAN_THREADS) {
+    const int4 cm = s_commit[c];
+    const int32_t p = cm.y, node = cm.z;
+    const lgbm_split_info b = L.best[p];
+    const DevFeature ft = L.feats[L.best_fpos[p]];
+    T.split_feature[node] = ft.real_index;
+    T.split_gain[node] = (float)(b.gain + ctl->cfg.min_gain_to_split);  // learner.rs:3985
+    T.threshold_in_bin[node] = b.threshold;
+    T.threshold[node] = L.ub ? L.ub[ft.ub_off + b.threshold] : (double)b.threshold;
+    int8_t dt = 0;
+    if (b.default_left) dt |= 2;
+    dt |= (int8_t)((ft.missing_type & 3) << 2);
+    T.decision_type[node] = dt;
+    T.internal_value[node] = nd.sums[p].weight;  // the split leaf's output
+    T.internal_count[node] = nd.count[p];        // partition counts (learner.rs:3994-4011)
+    NodeRoute r;
+    r.f = L.best_fpos[p];
+    router_of(ft, b, &r.pmin, &r.th, &r.flags);
+    r.max_bin = (int32_t)ft.max_bin;
+    r.na_bin = (int32_t)ft.num_bin - 1;
+    r.left = ~cm.x;
+    r.right = ~cm.w;
+    T.nodes[node] = r;
+  }
+  for (int n = tid; n < nl - 1; n += PLAN_THREADS) {
+    T.left_child[n] = s_left[n];
+    T.right_child[n] = s_right[n];
+  }
+  for (int l = tid; l < nl; l += PLAN_THREADS) {
+    L.leaf_slot[l] = s_leaf_slot[l];
+    T.leaf_parent[l] = s_leaf_parent[l];
+    L.leaf_side[l] = s_leaf_side[l];
+  }
+  for (int j = tid; j < nj; j += PLAN_THREADS) {
+    const int4 pk = s_pick[j];
+    const int32_t p = pk.y, cl = pk.z, cr = pk.w;
+    const lgbm_split_info b = L.best[p];
+    const int32_t fpos = L.best_fpos[p];
+    const DevFeature ft = L.feats[fpos];
+    PartJob J;
+    J.parent = p;
+    J.cl = cl;
+    J.cr = cr;
+    J.src_buf = nd.buf[p];
+    J.dst_buf = J.src_buf == BUF_A ? BUF_B : BUF_A;
+    J.rev = nd.rev[p];
+    J.begin = nd.begin[p];
+    J.count = nd.count[p];
+    J.fbyte = fpos;
+    router_of(ft, b, &J.pmin, &J.th, &J.flags);
+    J.max_bin = (int32_t)ft.max_bin;
+    J.na_bin = (int32_t)ft.num_bin - 1;
+    // build the histogram of the side the scan expects to be smaller
+    J.acc_right = b.right_count < b.left_count ? 1 : 0;
+    J.ntiles = (int32_t)((J.count + PART_TILE - 1) / PART_TILE);
+    J.tile0 = 0;
+    ctl->jobs[j] = J;
+    s_ntiles[j] = J.ntiles;
+    const int32_t d = nd.depth[p] + 1;
+    nd.child[2 * p] = cl;
+    nd.child[2 * p + 1] = cr;
+    nd.child[2 * cl] = -1;
+    nd.child[2 * cl + 1] = -1;
+    nd.child[2 * cr] = -1;
+    nd.child[2 * cr + 1] = -1;
+    nd.depth[cl] = d;
+    nd.depth[cr] = d;
+    // LeafSplits::init_from_split (leaf_splits.rs:162-173): sums and outputs of the
+    // SplitInfo; counts come from the partition.
+    nd.sums[cl] = LeafSums{b.left_sum_gradient, b.left_sum_hessian, b.left_output, 0, 0};
+    nd.sums[cr] = LeafSums{b.right_sum_gradient, b.right_sum_hessian, b.right_output, 0, 0};
+    nd.key_gain[cl] = ninf;
+    nd.key_gain[cr] = ninf;
+    nd.key_feat[cl] = -1;
+    nd.key_feat[cr] = -1;
+    L.best_fpos[cl] = -1;
+    L.best_fpos[cr] = -1;
+    ctl->reduce_list[2 * j] = cl;
+    ctl->reduce_list[2 * j + 1] = cr;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int64_t acc = 0;
+    for (int j = 0; j < nj; ++j) {
+      ctl->jobs[j].tile0 = acc;
+      acc += s_ntiles[j];
+    }
+    ctl->tile_total = acc;
+    ctl->n_jobs = nj;
+    ctl->n_reduce = 2 * nj;
+    ctl->num_leaves = nl;
+    ctl->n_slots = s_nslots;
+    ctl->rounds += 1;
+    if (s_done) ctl->done = 1;
+  }
+}
+
+// ===========================================================================
+// k_partition: stable single-pass split of every job of the round.  The tiles of all
+// jobs form one ticket space (job j owns [tile0, tile0 + ntiles)); each tile ranks
+// its rows with wave ballots, publishes its left count and derives its exclusive left
+// prefix by decoupled look-back over the earlier tiles of the same job.  Left rows go
+// to [begin, begin + L) ascending; right rows to [begin + L, begin + count) in
+// descending position (logical order = ascending, stored reversed), so no total is
+// needed in advance.  Look-back words: epoch(30) | flag(2) | value(32).
+// In the tree driver the pass also builds one child's integer histogram per job (the
+// side the scan predicts to be smaller) from the rows while they are in registers;
+// the other child's is parent - built in integers (k_pair_scan).
+// ===========================================================================
+template <int W>
+__global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
+  extern __shared__ unsigned long long lds_hist[];
+  __shared__ int32_t cb[16 * LGBM_MAX_W];
+  __shared__ PartJob s_jobs[SPEC_MAX];
+  __shared__ int64_t s_tile;
+  __shared__ int32_t s_cnt[PART_ROWS_PER_THREAD][PART_WAVES];
+  __shared__ int32_t s_pref[PART_ROWS_PER_THREAD][PART_WAVES];
+  __shared__ int32_t s_total;
+  __shared__ int32_t s_excl;
+  Ctl* ctl = L.ctl;
+  const int32_t nj = ctl->n_jobs;
+  const int64_t total = ctl->tile_total;
+  if (nj <= 0 || total <= 0) return;
+  const int64_t nblk = min((int64_t)gridDim.x, total);
+  if ((int64_t)blockIdx.x >= nblk) return;
+  const uint32_t epoch = ctl->epoch & 0x3fffffffu;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int F = L.F, cells = L.total_cells;
+  if (tid < nj) s_jobs[tid] = ctl->jobs[tid];
+  for (int c = tid; c < cells; c += PART_THREADS) lds_hist[c] = 0ull;
+  for (int f = tid; f < F; f += PART_THREADS) cb[f] = (int32_t)L.feats[f].cell_base;
+  int32_t cur = -1;  // job whose rows the LDS histogram holds
+  while (true) {
+    __syncthreads();
+    if (tid == 0)
+      s_tile = (int64_t)__hip_atomic_fetch_add(&ctl->part_ticket, 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int64_t t = s_tile;
+    if (t >= total) break;
+    int32_t j = 0;
+    while (j + 1 < nj && s_jobs[j + 1].tile0 <= t) ++j;
+    if (j != cur) {
+      if (cur >= 0 && s_jobs[cur].acc_right >= 0) {
+        lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3);
+        __syncthreads();
+      }
+      cur = j;
+    }
+    const PartJob& J = s_jobs[j];
+    const int64_t count = J.count, begin = J.begin;
+    const int64_t lt = t - J.tile0;
+    const int64_t base = lt * PART_TILE;
+    const uint4* __restrict__ src = L.bufs.rec[J.src_buf];
+    const uint16_t* __restrict__ sgh = L.bufs.gh[J.src_buf];
+    uint4* __restrict__ dst = L.bufs.rec[J.dst_buf];
+    uint16_t* __restrict__ dgh = L.bufs.gh[J.dst_buf];
+    uint4 w[PART_ROWS_PER_THREAD][W];
+    uint16_t q[PART_ROWS_PER_THREAD];
+    bool isleft[PART_ROWS_PER_THREAD], valid[PART_ROWS_PER_THREAD];
+    int32_t rank[PART_ROWS_PER_THREAD];
+#pragma unroll
+    for (int k = 0; k < PART_ROWS_PER_THREAD; ++k) {
+      const int64_t p = base + (int64_t)k * PART_THREADS + tid;
+      valid[k] = p < count;
+      bool right = false;
+      if (valid[k]) {
+        const int64_t phys = J.rev ? begin + count - 1 - p : begin + p;
+#pragma unroll
+        for (int i = 0; i < W; ++i) w[k][i] = src[phys * W + i];
+        q[k] = sgh[phys];
+        const int32_t bin = (int32_t)rec_byte(w[k], J.fbyte);
+        right = route_right(bin, J.pmin, J.max_bin, J.th, J.na_bin, J.flags);
+      }
+      isleft[k] = valid[k] && !right;
+      const unsigned long long m = __ballot(isleft[k]);
+      rank[k] = (int32_t)__popcll(m & lanemask_lt());
+      if (lane_id() == 0) s_cnt[k][wave] = (int32_t)__popcll(m);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int32_t acc = 0;
+      for (int k = 0; k < PART_ROWS_PER_THREAD; ++k)
+        for (int wv = 0; wv < PART_WAVES; ++wv) {
+          s_pref[k][wv] = acc;
+          acc += s_cnt[k][wv];
+        }
+      s_total = acc;
+      // publish + look-back within the job
+      uint64_t* ts = L.tile_state;
+      const uint64_t ep = (uint64_t)epoch << 34;
+      int64_t excl = 0;
+      if (lt == 0) {
+        __hip_atomic_store(&ts[t], ep | (TS_INC << 32) | (uint32_t)acc, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        __hip_atomic_store(&ts[t], ep | (TS_AGG << 32) | (uint32_t)acc, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        int64_t p = t - 1;
+        int spins = 0;
+        while (p >= J.tile0) {
+          const uint64_t st = __hip_atomic_load(&ts[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const bool fresh = (st >> 34) == (uint64_t)epoch;
+          const uint64_t flag = (st >> 32) & 3ull;
+          if (!fresh || flag == 0ull) {
+            ++spins;
+            const bool give_up =
+                spins > SPIN_LIMIT ||
+                ((spins & 1023) == 0 &&
+                 (__hip_atomic_load(&ctl->error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
+                  ERR_SPIN));
+            if (give_up) {
+              atomicOr(&ctl->error, ERR_SPIN);
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            continue;
+          }
+          excl += (int64_t)(uint32_t)st;
+          if (flag == TS_INC) break;
+          --p;
+        }
+        __hip_atomic_store(&ts[t], ep | (TS_INC << 32) | (uint32_t)(excl + acc), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+      s_excl = (int32_t)excl;
+    }
+    __syncthreads();
+    const int64_t excl = s_excl;
+    const int64_t rbase = base - excl;  // right rows before this tile
+#pragma unroll
+    for (int k = 0; k < PART_ROWS_PER_THREAD; ++k) {
+      if (!valid[k]) continue;
+      const int64_t pos = (int64_t)k * PART_THREADS + tid;
+      const int64_t lrank = s_pref[k][wave] + rank[k];
+      int64_t d;
+      if (isleft[k]) {
+        d = begin + excl + lrank;
+      } else {
+        const int64_t r = rbase + (pos - lrank);
+        d = begin + count - 1 - r;
+      }
+#pragma unroll
+      for (int i = 0; i < W; ++i) dst[d * W + i] = w[k][i];
+      dgh[d] = q[k];
+    }
+    if (J.acc_right >= 0) {
+      const bool want_left = J.acc_right == 0;
+#pragma unroll
+      for (int k = 0; k < PART_ROWS_PER_THREAD; ++k)
+        if (valid[k] && isleft[k] == want_left) lds_hist_add<W>(lds_hist, cb, F, w[k], q[k]);
+    }
+    if (lt == J.ntiles - 1 && tid == 0) {
+      const int32_t lc = (int32_t)(excl + s_total);
+      const int32_t rc = (int32_t)(count - lc);
+      if (J.parent >= 0) {
+        DevNodes& nd = L.nodes;
+        nd.begin[J.cl] = (int32_t)begin;
+        nd.count[J.cl] = lc;
+        nd.buf[J.cl] = J.dst_buf;
+        nd.rev[J.cl] = 0;
+        nd.begin[J.cr] = (int32_t)(begin + lc);
+        nd.count[J.cr] = rc;
+        nd.buf[J.cr] = J.dst_buf;
+        nd.rev[J.cr] = 1;
+        nd.sums[J.cl].n = lc;
+        nd.sums[J.cr].n = rc;
+        atomicAdd(&L.stats[0], (double)count);
+        atomicAdd(&L.stats[4], 1.0);
+      } else {
+        ctl->part_left_count = lc;
+      }
+    }
+  }
+  if (cur >= 0 && s_jobs[cur].acc_right >= 0)
+    lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3);
+  if (tid == 0) {
+    const int32_t prev =
+        __hip_atomic_fetch_add(&ctl->part_exit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == (int32_t)nblk - 1) {
+      __hip_atomic_store(&ctl->part_ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ctl->part_exit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ctl->epoch = (ctl->epoch + 1u) & 0x3fffffffu;
+      if (ctl->epoch == 0u) ctl->epoch = 1u;
+      L.stats[1] += 1.0;
+    }
+  }
+}
+
+// ===========================================================================
+// k_pair_scan: block (feature f, job j), two waves.  The children of job j:
+//   integer cells: the built side from the job's accumulator, the other side =
+//   parent - built (exact); both stored in the children's integer slots;
+//   smaller child (partition counts, a tie makes the right child the smaller one:
+//   learner.rs:4061-4089): exact f64 cells -> FixHistogram on its RAW sums ->
+//   compaction; larger = parent - smaller in f64 (histogram_pool.rs:249, not re-fixed);
+//   wave 0 scans the smaller, wave 1 the larger.  Children of a gated pair
+//   (before_find_best_split, learner.rs:1808-1839: max_depth reached, or both below
+//   2 * min_data_in_leaf rows) are not built or scanned.
+// ===========================================================================
+__global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L) {
+  __shared__ double cs[2 * 256];
+  __shared__ double cp[2 * 256];
+  Ctl* ctl = L.ctl;
+  const int f = blockIdx.x, j = blockIdx.y;
+  if (j >= ctl->n_jobs) return;
+  const PartJob& J = ctl->jobs[j];
+  const int32_t p = J.parent, cl = J.cl, cr = J.cr, acc_right = J.acc_right;
+  const int tid = threadIdx.x, F = L.F, cells = L.total_cells;
+  const DevFeature ft = L.feats[f];
+  const int nb = (int)ft.num_bin;
+  const DevNodes& nd = L.nodes;
+  const int32_t lcnt = nd.count[cl], rcnt = nd.count[cr];
+  const int32_t md = ctl->max_depth, min2 = ctl->cfg.min_data_in_leaf * 2;
+  const bool gated = (md > 0 && nd.depth[cl] >= md) || (lcnt < min2 && rcnt < min2);
+  const bool right_small = !(lcnt < rcnt);
+  const int32_t sm = right_small ? cr : cl, lg = right_small ? cl : cr;
+  const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
+  int32_t* acc = L.hist_acc + (size_t)j * cells * 3;
+  for (int b = tid; b < nb; b += SCAN_THREADS) {
+    const size_t ci = (size_t)(ft.cell_base + b);
+    int32_t* a = acc + ci * 3;
+    const int32_t AG = a[0], AH = a[1], AT = a[2];
+    a[0] = 0;
+    a[1] = 0;
+    a[2] = 0;
+    if (gated) continue;
+    const int32_t* ps = L.int_slots + ((size_t)p * cells + ci) * 3;
+    const int32_t OG = ps[0] - AG, OH = ps[1] - AH, OT = ps[2] - AT;
+    int32_t* ls = L.int_slots + ((size_t)cl * cells + ci) * 3;
+    int32_t* rs = L.int_slots + ((size_t)cr * cells + ci) * 3;
+    const int32_t LG_ = acc_right ? OG : AG, LH = acc_right ? OH : AH, LT = acc_right ? OT : AT;
+    const int32_t RG = acc_right ? AG : OG, RH = acc_right ? AH : OH, RT = acc_right ? AT : OT;
+    ls[0] = LG_;
+    ls[1] = LH;
+    ls[2] = LT;
+    rs[0] = RG;
+    rs[1] = RH;
+    rs[2] = RT;
+    if (right_small)
+      int_cell_to_f64(RG, RH, RT, vg1, vh1, vh3, &cs[2 * b], &cs[2 * b + 1]);
+    else
+      int_cell_to_f64(LG_, LH, LT, vg1, vh1, vh3, &cs[2 * b], &cs[2 * b + 1]);
+  }
+  if (gated) {
+    if (tid == 0) {
+      split_set_none(&L.feat_split[(size_t)cl * F + f]);
+      split_set_none(&L.feat_split[(size_t)cr * F + f]);
+    }
+    return;
+  }
+  const LeafSums ss = nd.sums[sm], gs = nd.sums[lg];
+  const bool pgate = L.splittable[(size_t)p * F + f] == 0;
+  fix_compact_block(ft, cs, ss.sg, ss.sh, pgate || !(ss.sh > 0.0 && ss.n > 0));
+  const size_t sl = L.slot_len;
+  const double* s_par = L.slots + (size_t)p * sl + ft.slot_off;
+  double* s_sm = L.slots + (size_t)sm * sl + ft.slot_off;
+  double* s_lg = L.slots + (size_t)lg * sl + ft.slot_off;
+  for (int i = tid; i < 2 * nb; i += SCAN_THREADS) {
+    const double v = cs[i];
+    const double d = s_par[i] - v;
+    cp[i] = d;
+    s_sm[i] = v;
+    s_lg[i] = d;
+  }
+  __syncthreads();
+  const int wv = tid >> 6;
+  const int32_t leaf = wv == 0 ? sm : lg;
+  const LeafSums ls = wv == 0 ? ss : gs;
+  lgbm_split_info* out = L.feat_split + (size_t)leaf * F + f;
+  if (!(ls.sh > 0.0 && ls.n > 0)) {
+    if (lane_id() == 0) split_set_none(out);
+  } else if (pgate) {
+    if (lane_id() == 0) {
+      split_set_none(out);
+      L.splittable[(size_t)leaf * F + f] = 0;
+    }
+  } else {
+    const ScanCfg sc = make_scan_cfg(ctl->cfg);
+    wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
+    if (lane_id() == 0) L.splittable[(size_t)leaf * F + f] = out->gain > -__builtin_inf() ? 1 : 0;
+  }
+}
+
+// ===========================================================================
+// k_tree_finalize: the Tree's leaf arrays from the committed leaves' node slots
+// (leaf_value = the leaf's output, leaf_weight = its sum_hessian, 0 for an unsplit
+// root: Tree::root, learner.rs:5398-5424), the score-update routes, and the per-leaf
+// ranges of the LeafPartitionLayout.
+// ===========================================================================
+__global__ void k_tree_finalize(DevLearner L) {
+  const Ctl* ctl = L.ctl;
+  const int32_t nl = ctl->num_leaves;
+  DevTree& T = L.tree;
+  const DevNodes& nd = L.nodes;
+  for (int l = threadIdx.x; l < nl; l += blockDim.x) {
+    const int32_t s = L.leaf_slot[l];
+    T.leaf_value[l] = nd.sums[s].weight;
+    T.leaf_weight[l] = s == 0 ? 0.0 : nd.sums[s].sh;
+    T.leaf_count[l] = nd.count[s];
+    T.leaf_depth[l] = nd.depth[s];
+    L.leaves.begin[l] = nd.begin[s];
+    L.leaves.count[l] = nd.count[s];
+    L.leaves.buf[l] = nd.buf[s];
+    L.leaves.rev[l] = nd.rev[s];
+  }
+  for (int n = threadIdx.x; n < nl - 1; n += blockDim.x) {
+    T.nodes[n].left = T.left_child[n];
+    T.nodes[n].right = T.right_child[n];
+  }
+  if (threadIdx.x == 0) {
+    T.header[0] = nl;
+    T.header[1] = ctl->error;
+    T.header[2] = ctl->rounds;
+    T.header[3] = ctl->done;
+  }
+}
+
+// Exports the partition layout: indices[leaf_begin[l] + p] = row of logical position p.
+template <int W>
+__global__ void k_export_layout(DevLearner L, uint32_t* __restrict__ indices) {
+  const int32_t l = blockIdx.y;
+  if (l >= L.ctl->num_leaves) return;
+  const int64_t b = L.leaves.begin[l], c = L.leaves.count[l];
+  const int32_t rev = L.leaves.rev[l];
+  const uint4* __restrict__ rec = L.bufs.rec[L.leaves.buf[l]];
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < c;
+       p += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t phys = rev ? b + c - 1 - p : b + p;
+    indices[b + p] = rec[phys * W + (W - 1)].w;
+  }
+}
+
+// ===========================================================================
+// launchers
+// ===========================================================================
+void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, int32_t slot_cap,
+                      int32_t spec_max, hipStream_t s, const KernelEvents* ev) {
+  KLAUNCH(ev, k_tree_init, dim3(16), dim3(256), 0, s, L, max_leaves, max_depth, slot_cap, spec_max);
+}
+void launch_plan(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
+  KLAUNCH(ev, k_plan, dim3(1), dim3(PLAN_THREADS), 0, s, L);
+}
+void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s,
+                      const KernelEvents* ev) {
+  int64_t blocks = PART_MAX_BLOCKS;
+  if (count_hint > 0) blocks = std::min<int64_t>(blocks, (count_hint + PART_TILE - 1) / PART_TILE);
+  if (blocks < 1) blocks = 1;
+  const size_t lds = (size_t)std::max(L.total_cells, 1) * sizeof(unsigned long long);
+  DISPATCH_W(W, KLAUNCH(ev, k_partition<kW>, dim3((unsigned)blocks), dim3(PART_THREADS), lds, s, L));
+}
+void launch_pair_scan(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
+  KLAUNCH(ev, k_pair_scan, dim3((unsigned)L.F, SPEC_MAX), dim3(SCAN_THREADS), 0, s, L);
+}
+void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
+  KLAUNCH(ev, k_tree_finalize, dim3(1), dim3(256), 0, s, L);
+}
+void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
+                          hipStream_t s) {
+  DISPATCH_W(L.W, (k_export_layout<kW><<<dim3(64, (unsigned)num_leaves), dim3(256), 0, s>>>(
+                      L, indices)));
+}
+
+}  // namespace lgbm

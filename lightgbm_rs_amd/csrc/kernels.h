@@ -27,11 +27,30 @@ struct RowBufs {
   uint16_t* gh[NBUF];
 };
 
+// Per-leaf-id partition ranges, filled by k_tree_finalize for the layout export.
 struct DevLeaves {
   int32_t* begin;
   int32_t* count;
   int32_t* buf;
   int32_t* rev;
+};
+
+// Node slots.  Every node the driver creates (the root, and both children of every
+// split it performs, including speculative ones) owns one slot; a committed leaf id
+// maps onto the slot of its current node (leaf_slot).  Slot state: the node's row
+// range in a row buffer, depth, LeafSums, its speculated children (child[2s],
+// child[2s+1], -1 if not split yet), and its best split (key_gain / key_feat, best,
+// best_fpos) with the per-feature results and histograms it came from.
+struct DevNodes {
+  int32_t* begin;
+  int32_t* count;
+  int32_t* buf;
+  int32_t* rev;
+  int32_t* depth;
+  int32_t* child;       // [2 * slot_cap]
+  LeafSums* sums;
+  double* key_gain;     // best split gain (-inf: none)
+  int32_t* key_feat;    // real feature index of the best split (-1: none)
 };
 
 struct DevTree {
@@ -63,16 +82,20 @@ struct DevLearner {
   int32_t _pad;
   int64_t N;
   uint64_t slot_len;
-  int32_t* hist_int;          // [total_cells][3] accumulator (flush target)
-  int32_t* int_slots;         // [max_leaves][total_cells][3] per-leaf integer histograms
-  double* slots;              // [max_leaves][slot_len]
-  lgbm_split_info* feat_split;  // [max_leaves][F]
-  lgbm_split_info* best;        // [max_leaves]
-  int32_t* best_feat;           // [max_leaves] real feature index
-  int32_t* best_fpos;           // [max_leaves] feature position
-  uint8_t* splittable;          // [max_leaves][F]
+  int32_t* hist_int;          // [total_cells][3] root / per-op accumulator
+  int32_t* hist_acc;          // [SPEC_MAX][total_cells][3] per-job accumulators
+  int32_t* int_slots;         // [slot_cap][total_cells][3] per-node integer histograms
+  double* slots;              // [slot_cap][slot_len] per-node f64 histograms
+  lgbm_split_info* feat_split;  // [slot_cap][F]
+  lgbm_split_info* best;        // [slot_cap]
+  int32_t* best_fpos;           // [slot_cap] feature position of best
+  uint8_t* splittable;          // [slot_cap][F]
+  int32_t* leaf_slot;           // [MAX_LEAVES] leaf id -> node slot
+  int32_t* leaf_side;           // [MAX_LEAVES] 1: right child of leaf_parent
   uint64_t* tile_state;
-  double* stats;                // [0] hist rows (non-root), [1] hist launches, [2] root rows
+  double* stats;                // [0] rows partitioned, [1] partition launches, [2] root
+                                // rows, [3] root launches, [4] partition jobs
+  DevNodes nodes;
   DevLeaves leaves;
   DevTree tree;
   RowBufs bufs;
@@ -100,16 +123,19 @@ void launch_hist(const DevLearner& L, int32_t driver, int64_t count_hint, hipStr
                  const KernelEvents* ev = nullptr);
 void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s,
                     const KernelEvents* ev = nullptr);
+void launch_plan(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
+void launch_pair_scan(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,
                           lgbm_split_info* out, hipStream_t s);
 void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s,
                       const KernelEvents* ev = nullptr);
-void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, hipStream_t s,
+void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth,
+                      int32_t slot_cap, int32_t spec_max, hipStream_t s,
                       const KernelEvents* ev = nullptr);
 void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s,
                          const KernelEvents* ev = nullptr);
-void launch_tree_finalize(const DevLearner& L, hipStream_t s);
+void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
 void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
                           hipStream_t s);
 void launch_gather_rows(int W, const uint32_t* rows, int64_t n, const uint4* rec,

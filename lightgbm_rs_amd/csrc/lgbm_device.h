@@ -22,6 +22,9 @@
 #define PART_TILE (PART_THREADS * PART_ROWS_PER_THREAD)
 #define PART_MAX_BLOCKS 256
 #define SCAN_THREADS 128                // two waves: smaller leaf, larger leaf
+#define PLAN_THREADS 1024
+#define MAX_LEAVES 256                  // tree leaves per context (u8 leaf ids in the plan)
+#define SLOT_CAP(leaves) (6 * (leaves) + 4)  // node slots: root + two per (speculated) split
 #define QUANT_ROWS_PER_LANE 16
 #define QUANT_LANE_MATS 6               // log2(64)
 #define QUANT_WAVE_MATS 27              // wave index bits (N <= 2^27 * 1024)
@@ -39,6 +42,7 @@
 #define ERR_SPIN 1
 #define ERR_ROOT_HESSIAN 2
 #define ERR_FEATURE 4
+#define ERR_SLOTS 8
 
 struct DevFeature {
   uint32_t num_bin;
@@ -76,14 +80,22 @@ struct NodeRoute {
   int32_t left, right;
 };
 
+// One leaf split of a partition round.  The tree driver splits up to SPEC_MAX
+// leaves per round (the best-ranked leaves not yet split; each is committed to
+// the tree later in the reference's own ArgMax order), the per-op entry point
+// exactly one.  parent/cl/cr are node slots (-1 in per-op mode).
 struct PartJob {
-  int32_t src_buf, dst_buf;
+  int32_t parent, cl, cr;
+  int32_t src_buf, dst_buf, rev;  // rev: source range stored reversed
   int64_t begin, count;
-  int32_t rev;        // source stored reversed
-  int32_t fbyte;      // feature byte in the record
-  int32_t pmin, max_bin, th, na_bin, flags;  // router
-  int32_t driver;     // 1: write tree / leaf bookkeeping
+  int32_t fbyte, pmin, max_bin, th, na_bin, flags;  // router
+  int32_t acc_right;  // histogram side built in the pass: 0 left, 1 right, -1 none
+  int32_t ntiles;
+  int64_t tile0;      // first tile of the job in the round's tile space
 };
+
+#define SPEC_MAX 32        // partition jobs per round
+#define SPEC_DEFAULT 8
 
 struct Ctl {
   // ---- quantizer (per iteration) ----
@@ -92,22 +104,20 @@ struct Ctl {
   int32_t quant_bins;
   int32_t const_hess;
   // ---- tree state ----
-  int32_t done, error, skip, pending_reduce;
-  int32_t num_leaves, max_leaves, max_depth, _i0;
-  int32_t left_leaf, right_leaf, smaller, larger;
-  int32_t split_leaf, split_f, new_right, node;
-  lgbm_split_info split;
-  LeafSums sm, lg;
-  // ---- histogram job ----
+  int32_t done, error, num_leaves, max_leaves;
+  int32_t max_depth, n_slots, slot_cap, spec_max;
+  int32_t n_jobs, n_reduce, rounds, root_skip;
+  int64_t tile_total;
+  // ---- root / per-op histogram job ----
   int32_t h_buf, _i1;
   int64_t h_begin, h_count;
-  // ---- partition job + look-back bookkeeping ----
-  PartJob part;
+  LeafSums sm;                       // per-op build: the leaf's raw sums
+  // ---- partition round + look-back bookkeeping ----
   uint32_t epoch;
   int32_t part_ticket, part_exit;
   int32_t part_left_count;
-  int32_t fs_count;                  // blocks of k_fixscan finished (self-resetting)
-  int32_t _i2;
+  PartJob jobs[SPEC_MAX];
+  int32_t reduce_list[2 * SPEC_MAX + 2];
   // ---- gain config ----
   lgbm_gain_config cfg;
 };

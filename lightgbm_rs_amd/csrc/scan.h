@@ -1,0 +1,405 @@
+// scan.h — device code shared by the tree-growth kernels: record byte access, the
+// packed LDS histogram of quantized pairs, FindBestThreshold for one (leaf, feature)
+// by one wave, and the split ordering.
+#pragma once
+
+#include "kernels.h"
+
+#include <hip/hip_ext.h>
+
+namespace lgbm {
+
+#define DISPATCH_W(W, ...)                                                 \
+  switch (W) {                                                              \
+    case 1: { constexpr int kW = 1; __VA_ARGS__; } break;                  \
+    case 2: { constexpr int kW = 2; __VA_ARGS__; } break;                  \
+    case 3: { constexpr int kW = 3; __VA_ARGS__; } break;                  \
+    case 4: { constexpr int kW = 4; __VA_ARGS__; } break;                  \
+    case 5: { constexpr int kW = 5; __VA_ARGS__; } break;                  \
+    case 6: { constexpr int kW = 6; __VA_ARGS__; } break;                  \
+    case 7: { constexpr int kW = 7; __VA_ARGS__; } break;                  \
+    case 8: { constexpr int kW = 8; __VA_ARGS__; } break;                  \
+    default: break;                                                         \
+  }
+
+// Launch `kern` plainly, or with the kernel-stamped events of `ev` when timing.
+#define KLAUNCH(ev, kern, grid, block, lds, s, ...)                                        \
+  do {                                                                                   \
+    if ((ev) && ((ev)->start || (ev)->stop))                                             \
+      hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)(lds), s, (ev)->start, (ev)->stop, \
+                            0u, __VA_ARGS__);                                            \
+    else                                                                                 \
+      kern<<<grid, block, lds, s>>>(__VA_ARGS__);                                        \
+  } while (0)
+
+// Byte f of a record held in registers.  Selects with compile-time indices only, so
+// the record never leaves the register file.
+template <int W>
+__device__ __forceinline__ uint32_t rec_byte(const uint4 (&w)[W], int f) {
+  const int wi = f >> 4;
+  const int j = (f >> 2) & 3;
+  uint32_t word = 0u;
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    const uint4 q = w[i];
+    const uint32_t x = j == 0 ? q.x : (j == 1 ? q.y : (j == 2 ? q.z : q.w));
+    word = i == wi ? x : word;
+  }
+  return (word >> (8 * (f & 3))) & 0xffu;
+}
+
+// Accumulate one row (packed quantized pair q) into the LDS histogram of all features.
+template <int W>
+__device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int32_t* cb, int F,
+                                             const uint4 (&w)[W], uint32_t q) {
+  const int32_t qg = (int32_t)(int8_t)(q & 0xffu);
+  const int32_t qh = (int32_t)(int8_t)(q >> 8);
+  const unsigned long long v = (unsigned long long)(long long)qg +
+                               ((unsigned long long)(uint32_t)qh << 22) +
+                               ((unsigned long long)(qh == 3 ? 1u : 0u) << 43);
+#pragma unroll
+  for (int wi = 0; wi < W; ++wi) {
+    const uint32_t ww[4] = {w[wi].x, w[wi].y, w[wi].z, w[wi].w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int f = wi * 16 + j;
+      if (f < F) {
+        const uint32_t bin = (ww[j >> 2] >> (8 * (j & 3))) & 0xffu;
+        __hip_atomic_fetch_add(&lds[cb[f] + bin], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+  }
+}
+
+// Flush a block's packed LDS histogram into the global [cells][3] integer cells.
+__device__ __forceinline__ void lds_hist_flush(const unsigned long long* lds, int cells,
+                                               int32_t* __restrict__ out) {
+  for (int c = threadIdx.x; c < cells; c += blockDim.x) {
+    const unsigned long long p = lds[c];
+    if (p == 0ull) continue;
+    const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
+    const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
+    const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
+    const int32_t hsum = (int32_t)(rest & ((1ull << 21) - 1));
+    const int32_t n3 = (int32_t)(rest >> 21);
+    int32_t* dst = out + (size_t)c * 3;
+    if (gsum) __hip_atomic_fetch_add(dst, (int32_t)gsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (hsum) __hip_atomic_fetch_add(dst + 1, hsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (n3) __hip_atomic_fetch_add(dst + 2, n3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Flush a block's packed LDS histogram into `out` and clear it for the next job.
+// The caller has synchronised the block after the last accumulation.
+__device__ __forceinline__ void lds_hist_flush_clear(unsigned long long* lds, int cells,
+                                                     int32_t* __restrict__ out) {
+  for (int c = threadIdx.x; c < cells; c += blockDim.x) {
+    const unsigned long long p = lds[c];
+    if (p == 0ull) continue;
+    lds[c] = 0ull;
+    const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
+    const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
+    const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
+    const int32_t hsum = (int32_t)(rest & ((1ull << 21) - 1));
+    const int32_t n3 = (int32_t)(rest >> 21);
+    int32_t* dst = out + (size_t)c * 3;
+    if (gsum) __hip_atomic_fetch_add(dst, (int32_t)gsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (hsum) __hip_atomic_fetch_add(dst + 1, hsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (n3) __hip_atomic_fetch_add(dst + 2, n3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ===========================================================================
+// FindBestThreshold for one (leaf, feature) by one wave: find_best_split_cpu_native
+// (kernels/split.rs:8970-9329).  The reference accumulates the candidate sums in a
+// fixed sequential f64 order starting at kEpsilon; here lane k of a 64-candidate
+// chunk recomputes the prefix over candidates 0..k in that same order (uniform LDS
+// broadcast reads), so every lane holds bit-identical sums.  The sticky `done`
+// break becomes "first candidate with active && !cont && brk" (ballot), and the
+// sequential strict-> best becomes a max-gain, lowest-index wave reduction.
+// ===========================================================================
+static __device__ void wave_scan(const double* hist, const DevFeature& ft, const ScanCfg& c,
+                          double sum_gradient, double sum_hessian, int32_t num_data, double po,
+                          lgbm_split_info* out) {
+  const int lane = (int)lane_id();
+  const double eps = k_eps();
+  const double ninf = -__builtin_inf();
+  const double shb = sum_hessian + 2.0 * eps;
+  const double gain_shift =
+      c.use_full ? leaf_gain_full(c.use_l1, sum_gradient, shb, c.l1, c.l2, c.mds, c.use_smoothing,
+                                  c.ps, num_data, po)
+                 : leaf_gain(c.use_l1, sum_gradient, shb, c.l1, c.l2);
+  const double mgs = gain_shift + c.min_gain;
+  const int32_t nb = (int32_t)ft.num_bin;
+  const int32_t offset = ft.offset;
+  const bool skip_def = ft.skip_default_bin != 0;
+  const bool na_m = ft.na_as_missing != 0;
+  const int32_t na = na_m ? 1 : 0;
+  const int32_t defb = (int32_t)ft.default_bin;
+  const int32_t rev_count = max(nb - 1 - na, 0);
+  const bool na_pre = na_m && offset == 1;
+  int32_t fwd_count = 0;
+  if (ft.run_forward) {
+    const int32_t base = max(nb - 1 - offset, 0);
+    fwd_count = na_pre ? base + 1 : base;
+  }
+  const double cf = (double)num_data / shb;
+
+  bool any_split = false;
+  double best_gain = ninf, best_lg = 0.0, best_lh = 0.0;
+  int32_t best_lc = 0, best_thr = 0;
+  bool best_dl = true;
+
+  {  // REVERSE (split.rs:9078-9176)
+    double cg = 0.0, ch = eps;
+    int32_t cc = 0;
+    const int32_t t_start = nb - 1 - offset - na;
+    for (int32_t base = 0; base < rev_count; base += LGBM_WAVE) {
+      const int32_t cnt = min(LGBM_WAVE, rev_count - base);
+      const bool valid = lane < cnt;
+      const int32_t t = t_start - (base + lane);
+      const bool act = valid && (t >= 1 - offset) && !(skip_def && t + offset == defb);
+      const double mg = act ? hist[2 * t] : 0.0, mh = act ? hist[2 * t + 1] : 0.0;
+      const int32_t mc = act ? round_int(mh * cf) : 0;
+      double sg = cg, sh = ch;
+      int32_t rc = cc;
+      for (int32_t i = 0; i < cnt; ++i) {
+        const int32_t ti = t_start - (base + i);
+        if ((ti >= 1 - offset) && !(skip_def && ti + offset == defb)) {  // wave-uniform
+          const double xg = readlane_f64(mg, i), xh = readlane_f64(mh, i);
+          const int32_t xc = readlane_i32(mc, i);
+          if (i <= lane) {
+            sg += xg;
+            sh += xh;
+            rc += xc;
+          }
+        }
+      }
+      const int32_t lc = num_data - rc;
+      const double slh = shb - sh, slg = sum_gradient - sg;
+      const bool cont = rc < c.min_d || sh < c.min_h;
+      const bool brk = lc < c.min_d || slh < c.min_h;
+      const unsigned long long bm = __ballot(act && !cont && brk);
+      const int first_brk = bm ? (__ffsll((unsigned long long)bm) - 1) : LGBM_WAVE;
+      const bool consider = act && !cont && lane < first_brk;
+      double gain = ninf;
+      if (consider) gain = split_gain_of(c, slg, slh, sg, sh, lc, rc, po);
+      const bool cand = consider && gain > mgs;
+      if (__ballot(cand)) any_split = true;
+      double rg = cand ? gain : ninf;
+      int32_t rl = cand ? lane : LGBM_WAVE;
+      for (int off = 32; off >= 1; off >>= 1) {
+        const double og = __shfl_xor(rg, off);
+        const int32_t ol = __shfl_xor(rl, off);
+        if (og > rg || (og == rg && ol < rl)) {
+          rg = og;
+          rl = ol;
+        }
+      }
+      if (rl < LGBM_WAVE && rg > best_gain) {
+        best_gain = rg;
+        best_lc = __shfl(lc, rl);
+        best_lg = __shfl(slg, rl);
+        best_lh = __shfl(slh, rl);
+        best_thr = __shfl(t, rl) - 1 + offset;
+        best_dl = true;
+      }
+      if (bm) break;
+      cg = __shfl(sg, cnt - 1);
+      ch = __shfl(sh, cnt - 1);
+      cc = __shfl(rc, cnt - 1);
+    }
+  }
+  {  // FORWARD (split.rs:9178-9277)
+    double cg = 0.0, ch = eps;
+    int32_t cc = 0, fwd_start = 0;
+    if (na_pre) {
+      cg = sum_gradient;
+      ch = shb - eps;
+      cc = num_data;
+      const int32_t m = nb - offset;
+      for (int32_t c0 = 0; c0 < m; c0 += LGBM_WAVE) {
+        const int32_t bb = c0 + lane;
+        const double vg = bb < m ? hist[2 * bb] : 0.0, vh = bb < m ? hist[2 * bb + 1] : 0.0;
+        const int32_t vc = bb < m ? round_int(vh * cf) : 0;
+        const int32_t lim = min(LGBM_WAVE, m - c0);
+        for (int32_t i = 0; i < lim; ++i) {
+          cg -= readlane_f64(vg, i);
+          ch -= readlane_f64(vh, i);
+          cc -= readlane_i32(vc, i);
+        }
+      }
+      fwd_start = -1;
+    }
+    for (int32_t base = 0; base < fwd_count; base += LGBM_WAVE) {
+      const int32_t cnt = min(LGBM_WAVE, fwd_count - base);
+      const bool valid = lane < cnt;
+      const int32_t t = fwd_start + base + lane;
+      const bool act = valid && !(skip_def && t + offset == defb);
+      const bool addl = act && t >= 0;
+      const double mg = addl ? hist[2 * t] : 0.0, mh = addl ? hist[2 * t + 1] : 0.0;
+      const int32_t mc = addl ? round_int(mh * cf) : 0;
+      double sg = cg, sh = ch;
+      int32_t lcn = cc;
+      for (int32_t i = 0; i < cnt; ++i) {
+        const int32_t ti = fwd_start + base + i;
+        if (!(skip_def && ti + offset == defb) && ti >= 0) {  // wave-uniform
+          const double xg = readlane_f64(mg, i), xh = readlane_f64(mh, i);
+          const int32_t xc = readlane_i32(mc, i);
+          if (i <= lane) {
+            sg += xg;
+            sh += xh;
+            lcn += xc;
+          }
+        }
+      }
+      const int32_t rc = num_data - lcn;
+      const double srh = shb - sh, srg = sum_gradient - sg;
+      const bool cont = lcn < c.min_d || sh < c.min_h;
+      const bool brk = rc < c.min_d || srh < c.min_h;
+      const unsigned long long bm = __ballot(act && !cont && brk);
+      const int first_brk = bm ? (__ffsll((unsigned long long)bm) - 1) : LGBM_WAVE;
+      const bool consider = act && !cont && lane < first_brk;
+      double gain = ninf;
+      if (consider) gain = split_gain_of(c, sg, sh, srg, srh, lcn, rc, po);
+      const bool cand = consider && gain > mgs;
+      if (__ballot(cand)) any_split = true;
+      double rg = cand ? gain : ninf;
+      int32_t rl = cand ? lane : LGBM_WAVE;
+      for (int off = 32; off >= 1; off >>= 1) {
+        const double og = __shfl_xor(rg, off);
+        const int32_t ol = __shfl_xor(rl, off);
+        if (og > rg || (og == rg && ol < rl)) {
+          rg = og;
+          rl = ol;
+        }
+      }
+      if (rl < LGBM_WAVE && rg > best_gain) {
+        best_gain = rg;
+        best_lc = __shfl(lcn, rl);
+        best_lg = __shfl(sg, rl);
+        best_lh = __shfl(sh, rl);
+        best_thr = __shfl(t, rl) + offset;
+        best_dl = false;
+      }
+      if (bm) break;
+      cg = __shfl(sg, cnt - 1);
+      ch = __shfl(sh, cnt - 1);
+      cc = __shfl(lcn, cnt - 1);
+    }
+  }
+  if (lane == 0) {
+    if (any_split && best_gain > ninf) {
+      const int32_t best_rc = num_data - best_lc;
+      const double lo = leaf_output_full(c.use_l1, best_lg, best_lh, c.l1, c.l2, c.mds,
+                                         c.use_smoothing, c.ps, best_lc, po);
+      const double rsg = sum_gradient - best_lg;
+      const double rsh = shb - best_lh;
+      const double ro = leaf_output_full(c.use_l1, rsg, rsh, c.l1, c.l2, c.mds, c.use_smoothing,
+                                         c.ps, best_rc, po);
+      out->threshold = (uint32_t)best_thr;
+      out->gain = best_gain - mgs;
+      out->left_count = best_lc;
+      out->right_count = num_data - best_lc;
+      out->left_sum_gradient = best_lg;
+      out->left_sum_hessian = best_lh - eps;
+      out->right_sum_gradient = rsg;
+      out->right_sum_hessian = rsh - eps;
+      out->left_output = lo;
+      out->right_output = ro;
+      out->default_left = best_dl ? 1 : 0;
+    } else {
+      split_set_none(out);
+    }
+  }
+}
+
+struct BestKey {
+  double gain;
+  int32_t feat;  // real feature index (-1 none)
+  int32_t idx;   // feature position / leaf id
+};
+
+// split_gt order (split_info.rs:28-35), ties to the lower position / leaf id (the
+// reference's sequential strict-> scans).
+__device__ __forceinline__ bool key_better(const BestKey& a, const BestKey& b) {
+  if (split_gt(a.gain, a.feat, b.gain, b.feat)) return true;
+  if (split_gt(b.gain, b.feat, a.gain, a.feat)) return false;
+  return a.idx < b.idx;
+}
+
+__device__ __forceinline__ BestKey wave_best(BestKey k) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    BestKey o;
+    o.gain = __shfl_xor(k.gain, off);
+    o.feat = __shfl_xor(k.feat, off);
+    o.idx = __shfl_xor(k.idx, off);
+    if (key_better(o, k)) k = o;
+  }
+  return k;
+}
+
+// FixHistogram (fix_histogram.rs:50-80) on the RAW leaf sums, then compaction
+// (compact_histogram, learner.rs:4460-4492), on one feature's cells in LDS.  The fix
+// is the reference's sequential f64 subtraction in ascending bin order: each lane of
+// wave 0 holds one bin and broadcasts it in turn.  `zero` (a leaf with no rows or no
+// hessian, or a feature masked out by the parent) clears the cells instead.  Called by
+// every thread of a SCAN_THREADS block.
+__device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* cs, double sg,
+                                                  double sh, bool zero) {
+  const int tid = threadIdx.x;
+  const int nb = (int)ft.num_bin;
+  __syncthreads();
+  if (zero) {
+    for (int i = tid; i < 2 * nb; i += SCAN_THREADS) cs[i] = 0.0;
+    __syncthreads();
+    return;
+  }
+  const int mfb = (int)ft.mfb;
+  if (tid < LGBM_WAVE && mfb > 0 && mfb < nb) {
+    double g = sg, h = sh;
+    for (int c0 = 0; c0 < nb; c0 += LGBM_WAVE) {
+      const int bb = c0 + tid;
+      const double vg = bb < nb ? cs[2 * bb] : 0.0;
+      const double vh = bb < nb ? cs[2 * bb + 1] : 0.0;
+      const int lim = min(LGBM_WAVE, nb - c0);
+      for (int i = 0; i < lim; ++i) {
+        if (c0 + i != mfb) {
+          g -= readlane_f64(vg, i);
+          h -= readlane_f64(vh, i);
+        }
+      }
+    }
+    if (tid == 0) {
+      cs[2 * mfb] = g;
+      cs[2 * mfb + 1] = h;
+    }
+  }
+  __syncthreads();
+  if (ft.offset > 0) {
+    const int off = ft.offset;
+    double a[256 / SCAN_THREADS], b2[256 / SCAN_THREADS];
+    int k = 0;
+    for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
+      const int src = c + off;
+      a[k] = src < nb ? cs[2 * src] : 0.0;
+      b2[k] = src < nb ? cs[2 * src + 1] : 0.0;
+    }
+    __syncthreads();
+    k = 0;
+    for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
+      cs[2 * c] = a[k];
+      cs[2 * c + 1] = b2[k];
+    }
+  }
+  __syncthreads();
+}
+
+// Exact f64 histogram cells from the integer counters (sum q_g, sum q_h, #q_h==3).
+__device__ __forceinline__ void int_cell_to_f64(int32_t G, int32_t H, int32_t T, double vg1,
+                                                double vh1, double vh3, double* g, double* h) {
+  *g = (double)G * vg1;
+  *h = (double)((long long)H - 3ll * T) * vh1 + (double)T * vh3;
+}
+
+}  // namespace lgbm

@@ -356,3 +356,39 @@ def test_graph_replays_match_eager():
     finally:
         eager.close()
         graph.close()
+
+
+@pytest.mark.parametrize("spec,rounds", [(1, 300), (3, 2), (16, 1), (16, 64)])
+def test_speculative_rounds_match_oracle(spec, rounds):
+    """Leaves split ahead of their turn (up to `spec` per round) and any number of
+    captured rounds (too few ones are completed by eager rounds) grow the oracle's
+    tree: commits follow the reference's ArgMax order regardless."""
+    n, F, nl = 150_000, 13, 127
+    say(f"speculative rounds spec={spec} rounds={rounds}")
+    bins, meta, ub = make_binned(n, F, seed=31)
+    g, h, _ = binary_gh(n, seed=31)
+    os.environ["LGBM_HIP_SPEC"] = str(spec)
+    os.environ["LGBM_HIP_ROUNDS"] = str(rounds)
+    try:
+        b = HipBackend(0)
+    finally:
+        del os.environ["LGBM_HIP_SPEC"]
+        del os.environ["LGBM_HIP_ROUNDS"]
+    try:
+        b.upload_resident_bins(bins, meta, ub)
+        b.upload_resident_grad_hess(g, h)
+        _, dg, dh = b.discretize_dequantize_in_place(4, True, 5, want_values=True)
+        og, oh, _, _ = oracle.quantize(g, h, bins=4, stochastic=True, seed=5)
+        cfg = GainConfig.make(min_data_in_leaf=20)
+        b.set_timing(True)
+        t, lay = b.grow_tree_on_device_with_cfg(cfg, nl, -1)
+        tm = b.timing()
+        say(f"  rounds {tm['rounds']:.0f}, jobs {tm['partition_jobs']:.0f}, leaves {t['num_leaves']}")
+        o, olay = oracle.train_tree(bins, meta, ub, og, oh, cfg, nl, -1)
+        _compare_trees(t, o, ("spec", spec, rounds))
+        assert np.array_equal(lay["indices"], olay["indices"])
+        assert tm["partition_jobs"] >= t["num_leaves"] - 1
+        if spec == 1:
+            assert tm["partition_jobs"] == t["num_leaves"] - 1
+    finally:
+        b.close()
