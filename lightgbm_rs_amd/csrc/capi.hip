@@ -47,8 +47,8 @@ struct lgbm_hip_ctx {
   int64_t buf_rows[NBUF] = {};
   float *g = nullptr, *h = nullptr, *label = nullptr;
   double* score = nullptr;
-  int32_t* hist_int = nullptr;
-  int32_t* hist_acc = nullptr;
+  int32_t* hist_part = nullptr;  // [HIST_SLOTS][cells][3]
+  int32_t* hist_acc = nullptr;   // [SPEC_MAX][cells][3]
   uint64_t* tile_state = nullptr;
   int64_t tile_cap = 0;
   uint64_t *wave_mats = nullptr, *lane_mats = nullptr;
@@ -61,8 +61,7 @@ struct lgbm_hip_ctx {
   int32_t* best_fpos = nullptr;
   int32_t* int_slots = nullptr;
   uint8_t* splittable = nullptr;
-  int32_t* leaf_slot = nullptr;
-  int32_t* leaf_side = nullptr;
+  int32_t* plan_state = nullptr;  // [5][MAX_LEAVES]
   DevNodes nodes{};
   DevLeaves leaves{};
   DevTree tree{};
@@ -81,6 +80,7 @@ struct lgbm_hip_ctx {
   int32_t graph_nl = -1, graph_md = 0, graph_rounds = 0, graph_spec = 0;
   int32_t round_cap = 24;     // partition rounds in the captured sequence
   int32_t spec_max = SPEC_DEFAULT;
+  int32_t part_shape = 0, part_blocks = PART_MAX_BLOCKS;  // partition launch shape / grid
   int32_t* done_host = nullptr;  // pinned: ctl->done after the captured rounds
   double tree_rounds = 0.0, trees = 0.0, extra_rounds = 0.0;
   uint64_t graph_gen = 0, buf_gen = 1;
@@ -183,7 +183,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.total_cells = c->total_cells;
   L.N = c->N;
   L.slot_len = c->slot_len;
-  L.hist_int = c->hist_int;
+  L.hist_part = c->hist_part;
   L.hist_acc = c->hist_acc;
   L.slots = c->slots;
   L.feat_split = c->feat_split;
@@ -191,8 +191,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.best_fpos = c->best_fpos;
   L.int_slots = c->int_slots;
   L.splittable = c->splittable;
-  L.leaf_slot = c->leaf_slot;
-  L.leaf_side = c->leaf_side;
+  L.plan_state = c->plan_state;
   L.nodes = c->nodes;
   L.tile_state = c->tile_state;
   L.stats = c->stats;
@@ -242,10 +241,10 @@ int ensure_scratch_bytes(lgbm_hip_ctx* c, size_t bytes) {
 }
 
 // A round's tiles: every job rounds its own rows up to whole tiles, so the jobs of
-// one round (disjoint leaves, at most SPEC_MAX) use at most rows / PART_TILE +
-// SPEC_MAX tiles.
+// one round (disjoint leaves, at most SPEC_MAX) use at most rows / tile + SPEC_MAX
+// tiles; sized for the smallest tile of any launch shape.
 int ensure_tile_state(lgbm_hip_ctx* c, int64_t rows) {
-  const int64_t tiles = (rows + PART_TILE - 1) / PART_TILE + SPEC_MAX + 1;
+  const int64_t tiles = (rows + PART_MIN_TILE - 1) / PART_MIN_TILE + SPEC_MAX + 1;
   if (c->tile_cap >= tiles) return LGBM_HIP_OK;
   c->buf_gen++;
   int rc = dalloc(c, &c->tile_state, (size_t)tiles);
@@ -276,8 +275,7 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   if ((rc = dalloc(c, &nd.sums, P))) return rc;
   if ((rc = dalloc(c, &nd.key_gain, P))) return rc;
   if ((rc = dalloc(c, &nd.key_feat, P))) return rc;
-  if ((rc = dalloc(c, &c->leaf_slot, (size_t)MAX_LEAVES))) return rc;
-  if ((rc = dalloc(c, &c->leaf_side, (size_t)MAX_LEAVES))) return rc;
+  if ((rc = dalloc(c, &c->plan_state, (size_t)5 * MAX_LEAVES))) return rc;
   if ((rc = dalloc(c, &c->leaves.begin, (size_t)L))) return rc;
   if ((rc = dalloc(c, &c->leaves.count, (size_t)L))) return rc;
   if ((rc = dalloc(c, &c->leaves.buf, (size_t)L))) return rc;
@@ -401,15 +399,16 @@ int do_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_t seed
 }
 
 // One partition round: plan (commit finished splits, pick the next leaves), the
-// partition pass of every picked leaf, and the children's scans.  Rounds after the
-// tree is complete return at once.
+// partition pass of every picked leaf (which also builds one child's histogram), and
+// the children's scans.  Rounds after the tree is complete return at once.
 void enqueue_rounds(lgbm_hip_ctx* c, int32_t rounds) {
   DevLearner L = make_learner(c);
   KernelEvents ke;
   for (int32_t r = 0; r < rounds; ++r) {
-    launch_plan(L, c->stream, ev_kernel(c, FAM_SCAN, &ke));
-    launch_partition(L, c->W, 0, c->stream, ev_kernel(c, FAM_PART, &ke));
-    launch_pair_scan(L, c->stream, ev_kernel(c, FAM_SCAN, &ke));
+    launch_plan(L, SLOT_CAP(c->lcap), part_tile_of(c->part_shape), c->stream,
+                ev_kernel(c, FAM_SCAN, &ke));
+    launch_partition(L, c->W, c->part_shape, c->part_blocks, c->stream, ev_kernel(c, FAM_PART, &ke));
+    launch_pair_scan(L, c->spec_max, c->stream, ev_kernel(c, FAM_SCAN, &ke));
   }
 }
 
@@ -420,7 +419,7 @@ void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth, int32_
   chain_start(c);
   launch_tree_init(L, num_leaves, max_depth, SLOT_CAP(num_leaves), c->spec_max, c->stream,
                    ev_kernel(c, -1, &ke));
-  launch_hist(L, 2, c->N, c->stream, ev_kernel(c, FAM_HIST, &ke));
+  launch_hist(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
   launch_fixscan(L, 1, nullptr, c->stream, ev_kernel(c, FAM_SCAN, &ke));
   enqueue_rounds(c, rounds);
 }
@@ -616,6 +615,13 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   if ((rc = dalloc(c, &c->partials, STAT_BLOCKS))) return fail(rc);
   if (const char* e = std::getenv("LGBM_HIP_GRAPHS")) c->use_graphs = std::strcmp(e, "0") != 0;
   if (const char* e = std::getenv("LGBM_HIP_ROUNDS")) c->round_cap = std::max(1, std::atoi(e));
+  if (const char* e = std::getenv("LGBM_HIP_PART")) {
+    int sh = 0, bl = PART_MAX_BLOCKS;
+    if (std::sscanf(e, "%d,%d", &sh, &bl) >= 1) {
+      c->part_shape = std::max(0, std::min(4, sh));
+      c->part_blocks = std::max(1, std::min(4096, bl));
+    }
+  }
   if (const char* e = std::getenv("LGBM_HIP_SPEC"))
     c->spec_max = std::max(1, std::min(SPEC_MAX, std::atoi(e)));
   *out = c;
@@ -641,7 +647,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->h);
   F(c->label);
   F(c->score);
-  F(c->hist_int);
+  F(c->hist_part);
   F(c->hist_acc);
   F(c->tile_state);
   F(c->wave_mats);
@@ -656,8 +662,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->feat_split);
   F(c->best);
   F(c->splittable);
-  F(c->leaf_slot);
-  F(c->leaf_side);
+  F(c->plan_state);
   F(c->nodes.begin);
   F(c->nodes.count);
   F(c->nodes.buf);
@@ -732,6 +737,9 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   }
   if (acc > 8192)  // 8 B per LDS cell, 64 KiB of dynamic LDS per block
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "histogram exceeds the LDS budget");
+  if (acc > HIST_WAVE_CELLS && num_data > (int64_t)HIST_GRID * HIST_BLOCK_MAX_ROWS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "rows per histogram block exceed the packed LDS cell fields");
   // bin-range gate (learner.rs:1161-1187): first offending bin, feature order
   for (int f = 0; f < F; ++f) {
     const uint8_t* col = bins + (size_t)f * (size_t)num_data;
@@ -768,8 +776,7 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   c->buf_rows[BUF_S0] = c->buf_rows[BUF_S1] = 0;
   if ((rc = dalloc(c, &c->g, (size_t)num_data))) return rc;
   if ((rc = dalloc(c, &c->h, (size_t)num_data))) return rc;
-  if ((rc = dalloc(c, &c->hist_int, (size_t)acc * 3))) return rc;
-  HIPCHK(c, hipMemset(c->hist_int, 0, (size_t)acc * 3 * 4));
+  if ((rc = dalloc(c, &c->hist_part, (size_t)HIST_SLOTS * acc * 3))) return rc;
   if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * acc * 3))) return rc;
   HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * acc * 3 * 4));
   if ((rc = ensure_tile_state(c, num_data))) return rc;
@@ -861,10 +868,10 @@ static int set_hist_job(lgbm_hip_ctx* c, const uint32_t* rows, int64_t n_rows) {
     buf = BUF_S0;
     count = n_rows;
   }
-  if ((rc = ctl_write(c, CTL_OFF(h_buf), buf))) return rc;
-  const int64_t zero = 0;
-  if ((rc = ctl_write(c, CTL_OFF(h_begin), zero))) return rc;
-  if ((rc = ctl_write(c, CTL_OFF(h_count), count))) return rc;
+  const HistJob hj{buf, 0, 0, count, 0, 0};
+  if ((rc = ctl_write(c, CTL_OFF(hjobs), hj))) return rc;
+  const int32_t one = 1;
+  if ((rc = ctl_write(c, CTL_OFF(n_hjobs), one))) return rc;
   return LGBM_HIP_OK;
 }
 
@@ -876,15 +883,24 @@ int lgbm_hip_build_int_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
   if ((rc = set_hist_job(c, leaf_rows, n_rows))) return rc;
   DevLearner L = make_learner(c);
-  launch_hist(L, 0, leaf_rows ? n_rows : c->N, c->stream);
+  launch_hist(L, c->stream);
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  std::vector<int32_t> cells((size_t)c->total_cells * 3);
-  HIPCHK(c, hipMemcpy(cells.data(), c->hist_int, cells.size() * 4, hipMemcpyDeviceToHost));
-  HIPCHK(c, hipMemset(c->hist_int, 0, cells.size() * 4));
+  HistJob hj{};
+  if ((rc = ctl_read(c, CTL_OFF(hjobs), &hj))) return rc;
+  const size_t stride = (size_t)c->total_cells * 3;
+  std::vector<int32_t> part((size_t)std::max(hj.nblk, 1) * stride, 0);
+  if (hj.nblk > 0)
+    HIPCHK(c, hipMemcpy(part.data(), c->hist_part + (size_t)hj.a0 * stride,
+                        (size_t)hj.nblk * stride * 4, hipMemcpyDeviceToHost));
   for (int32_t i = 0; i < c->total_cells; ++i) {
-    out[2 * i] = cells[3 * (size_t)i];
-    out[2 * i + 1] = cells[3 * (size_t)i + 1];
+    int64_t g = 0, h = 0;
+    for (int32_t k = 0; k < hj.nblk; ++k) {
+      g += part[k * stride + 3 * (size_t)i];
+      h += part[k * stride + 3 * (size_t)i + 1];
+    }
+    out[2 * i] = g;
+    out[2 * i + 1] = h;
   }
   return LGBM_HIP_OK;
 }
@@ -903,7 +919,7 @@ int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, in
   if ((rc = ctl_write(c, CTL_OFF(sm), s))) return rc;
   if ((rc = dalloc(c, &c->slot_tmp, (size_t)c->slot_len))) return rc;
   DevLearner L = make_learner(c);
-  launch_hist(L, 0, leaf_rows ? n_rows : c->N, c->stream);
+  launch_hist(L, c->stream);
   launch_fixscan(L, 2, c->slot_tmp, c->stream);
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -998,11 +1014,12 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   launch_pack_partition((const uint32_t*)c->scratch, n, c->rec[BUF_S0], c->stream);
   HIPCHK(c, hipMemsetAsync(c->gh[BUF_S0], 0, (size_t)n * 2, c->stream));
   PartJob J{};
+  J.acc_right = -1;
   J.parent = -1;
   J.cl = -1;
   J.cr = -1;
-  J.acc_right = -1;
-  J.ntiles = (int32_t)((n + PART_TILE - 1) / PART_TILE);
+  const int32_t tile = part_tile_of(c->part_shape);
+  J.ntiles = (int32_t)((n + tile - 1) / tile);
   J.tile0 = 0;
   J.src_buf = BUF_S0;
   J.dst_buf = BUF_S1;
@@ -1017,13 +1034,20 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   J.flags = ((int32_t)most_freq_bin > (int32_t)threshold ? 1 : 0) | (na_as_missing ? 2 : 0) |
             (default_left ? 4 : 0);
   if ((rc = ctl_write(c, CTL_OFF(jobs), J))) return rc;
+  uint32_t ep = 0;
+  if ((rc = ctl_read(c, CTL_OFF(epoch), &ep))) return rc;
+  ep = (ep + 1u) & 0x3fffffffu;
+  if (ep == 0u) ep = 1u;
+  if ((rc = ctl_write(c, CTL_OFF(epoch), ep))) return rc;
+  const int32_t zero32 = 0;
+  if ((rc = ctl_write(c, CTL_OFF(part_ticket), zero32))) return rc;
   const int32_t one = 1;
   if ((rc = ctl_write(c, CTL_OFF(n_jobs), one))) return rc;
   const int64_t tiles = J.ntiles;
   if ((rc = ctl_write(c, CTL_OFF(tile_total), tiles))) return rc;
   DevLearner L = make_learner(c);
   L.W = 1;
-  launch_partition(L, 1, n, c->stream);
+  launch_partition(L, 1, c->part_shape, std::min<int64_t>(c->part_blocks, J.ntiles), c->stream);
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));
   int32_t lc = 0;

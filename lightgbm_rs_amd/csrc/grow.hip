@@ -40,12 +40,14 @@ namespace lgbm {
 #define SPIN_LIMIT (1 << 20)
 #define PLAN_WAVES (PLAN_THREADS / LGBM_WAVE)
 #define INT_MAX32 0x7fffffff
+// plan_state rows (MAX_LEAVES entries each): the tree's leaf -> node-slot map and
+// linkage, owned by k_plan and copied into the Tree by k_tree_finalize.
+#define PS_LEAF_SLOT 0    // committed leaf id -> node slot
+#define PS_LEAF_SIDE 1    // 1: the leaf is its parent node's right child
+#define PS_LEAF_PARENT 2  // Tree::leaf_parent
+#define PS_NODE_LEFT 3    // Tree::left_child
+#define PS_NODE_RIGHT 4   // Tree::right_child
 
-// Wave-level ordering point for LDS state written by one lane and read by all.
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-}
 
 // SplitInner router inputs (split_inner, learner.rs:3957; data_partition.rs:387-417).
 __device__ __forceinline__ void router_of(const DevFeature& ft, const lgbm_split_info& b,
@@ -71,7 +73,6 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
   const int tid = blockIdx.x * blockDim.x + threadIdx.x;
   const int nthr = gridDim.x * blockDim.x;
   for (int i = tid; i < L.F; i += nthr) L.splittable[i] = 1;  // node slot 0
-  for (int i = tid; i < L.total_cells * 3; i += nthr) L.hist_int[i] = 0;
   for (int i = tid; i < SPEC_MAX * L.total_cells * 3; i += nthr) L.hist_acc[i] = 0;
   if (tid == 0) {
     const int32_t N = (int32_t)L.N;
@@ -92,9 +93,9 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
     ctl->root_skip = did ? 0 : 1;
     ctl->n_reduce = did ? 1 : 0;
     ctl->reduce_list[0] = 0;
-    ctl->h_buf = BUF_ORIG;
-    ctl->h_begin = 0;
-    ctl->h_count = N;
+    // the root ConstructHistogram: all rows
+    ctl->n_hjobs = 1;
+    ctl->hjobs[0] = HistJob{BUF_ORIG, 0, 0, N, 0, 0};
     DevNodes& nd = L.nodes;
     nd.begin[0] = 0;
     nd.count[0] = N;
@@ -108,9 +109,9 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
     nd.key_feat[0] = -1;
     split_set_none(&L.best[0]);
     L.best_fpos[0] = -1;
-    L.leaf_slot[0] = 0;
-    L.leaf_side[0] = 0;
-    L.tree.leaf_parent[0] = -1;
+    L.plan_state[PS_LEAF_SLOT * MAX_LEAVES] = 0;
+    L.plan_state[PS_LEAF_SIDE * MAX_LEAVES] = 0;
+    L.plan_state[PS_LEAF_PARENT * MAX_LEAVES] = -1;
     L.stats[2] += (double)N;
     L.stats[3] += 1.0;
   }
@@ -118,183 +119,223 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
 
 // ===========================================================================
 // k_plan: one block.
+//   0. one prefetch of everything it reads (control block, features, node-slot keys,
+//      leaf / node linkage) into LDS;
 //   1. per-leaf feature ArgMax for the node slots scanned since the last plan
-//      (the argmax of scan_leaf_histogram, learner.rs:3290-3330);
+//      (the argmax of scan_leaf_histogram, learner.rs:3290-3330), one wave per slot;
 //   2. commit loop (wave 0): repeat the reference's ArgMax over the committed leaves
 //      (learner.rs:4537, split_gt order, first leaf id wins) and its stop test
-//      (gain <= 0, learner.rs:1503; num_leaves splits at most); while the chosen leaf
-//      has already been split, commit that split: node = num_leaves - 1, the left
-//      child keeps the leaf id, the right child gets id num_leaves (tree.rs:614-700);
+//      (gain <= 0, learner.rs:1503; num_leaves - 1 splits at most); while the chosen
+//      leaf has already been split, commit that split: node = num_leaves - 1, the
+//      left child keeps the leaf id, the right child gets id num_leaves
+//      (tree.rs:614-700);
 //   3. selection (wave 0): the chosen leaf, then the next best-ranked unsplit leaves
 //      with gain > 0, up to spec_max, while two node slots per split the tree may
 //      still need stay in reserve;
-//   4. (all threads) the Tree::split fields of the committed splits, and the
-//      partition jobs + child node slots of the selected leaves.
+//   4. (all threads) the Tree::split fields of the committed splits, the partition
+//      jobs and child node slots of the selected leaves, and the next round's
+//      partition ticket / look-back epoch.
+// A slot's best split is feat_split[slot * F + best_fpos[slot]].
 // ===========================================================================
-__global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L) {
+// ArgMax over the leaves held by a wave (lane l: leaves l + 64 i, i < PL) in the
+// reference's order: the highest gain, then the lower real feature index (-1 last),
+// then the lower leaf id (split_gt, split_info.rs:28-35; ArgMax's first-max-wins
+// scan, learner.rs:4537).  Only positive gains qualify (smaller ones stop the tree);
+// `cand` (optional) masks leaves out.  Returns the leaf id, or -1.  The bit pattern
+// of a positive double orders like the double, so the maximum gain is one u64
+// reduction; equal gains (the only case where the other keys matter) take the full
+// comparison.  Wave-uniform; requires all 64 lanes active.
+template <int PL>
+__device__ __forceinline__ int32_t plan_argmax(const double (&kg)[PL], const int32_t (&kf)[PL],
+                                               const bool* cand, int32_t nl) {
+  const int lane = (int)lane_id();
+  uint64_t k[PL];
+  uint64_t lm = 0ull;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const bool ok = (lane + LGBM_WAVE * i < nl) && kg[i] > 0.0 && (cand == nullptr || cand[i]);
+    k[i] = ok ? (uint64_t)__double_as_longlong(kg[i]) : 0ull;
+    lm = k[i] > lm ? k[i] : lm;
+  }
+  const uint64_t m = wave_max_u64(lm);
+  if (m == 0ull) return -1;
+  int cnt = 0, mi = 0;
+#pragma unroll
+  for (int i = PL - 1; i >= 0; --i)
+    if (k[i] == m) {
+      ++cnt;
+      mi = i;
+    }
+  const unsigned long long any = __ballot(cnt > 0);
+  const unsigned long long multi = __ballot(cnt > 1);
+  if (multi == 0ull && __popcll(any) == 1) {
+    const int w = __ffsll(any) - 1;
+    return w + LGBM_WAVE * readlane_i32(mi, w);
+  }
+  // a gain tie: full order among the tied leaves
+  BestKey lb{-__builtin_inf(), -1, 0x7fffffff};
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const BestKey c{kg[i], kf[i], lane + LGBM_WAVE * i};
+    if (k[i] == m && key_better(c, lb)) lb = c;
+  }
+  return wave_best(lb).idx;
+}
+
+__global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slot_cap,
+                                                       int32_t part_tile) {
   __shared__ double s_gain[SLOT_CAP(MAX_LEAVES)];
   __shared__ int32_t s_feat[SLOT_CAP(MAX_LEAVES)];
-  __shared__ int32_t s_child[2 * SLOT_CAP(MAX_LEAVES)];
-  __shared__ int32_t s_leaf_slot[MAX_LEAVES];
-  __shared__ int32_t s_leaf_parent[MAX_LEAVES];
-  __shared__ int32_t s_leaf_side[MAX_LEAVES];
-  __shared__ int32_t s_left[MAX_LEAVES];
-  __shared__ int32_t s_right[MAX_LEAVES];
-  __shared__ int4 s_commit[MAX_LEAVES];  // (leaf, node slot, node, new right leaf)
-  __shared__ int4 s_pick[SPEC_MAX];      // (leaf, node slot, left slot, right slot)
+  __shared__ int32_t s_fpos[SLOT_CAP(MAX_LEAVES)];
+  __shared__ int2 s_child[SLOT_CAP(MAX_LEAVES)];
+  __shared__ int32_t s_ps[5][MAX_LEAVES];  // PS_* linkage
+  __shared__ DevFeature s_ft[16 * LGBM_MAX_W];
+  __shared__ int4 s_commit[MAX_LEAVES];    // (leaf, node slot, node, new right leaf)
+  __shared__ int2 s_lc[MAX_LEAVES];        // per leaf: speculated children slots
+  __shared__ double2 s_lcg[MAX_LEAVES];    //   and their keys
+  __shared__ int2 s_lcf[MAX_LEAVES];
+  __shared__ int4 s_pick[SPEC_MAX];        // (leaf, node slot, left slot, right slot)
+  __shared__ int32_t s_red[2 * SPEC_MAX + 2];
   __shared__ int32_t s_ntiles[SPEC_MAX];
   __shared__ int32_t s_nc, s_nj, s_nl, s_done, s_nslots;
   Ctl* ctl = L.ctl;
-  if (ctl->done) return;
   const int tid = threadIdx.x;
   const int lane = (int)lane_id();
   const int wave = tid >> 6;
   const int F = L.F;
   const double ninf = -__builtin_inf();
-  const int32_t nl0 = ctl->num_leaves, ns0 = ctl->n_slots, maxl = ctl->max_leaves;
   const DevNodes& nd = L.nodes;
   DevTree& T = L.tree;
-  for (int s = tid; s < ns0; s += PLAN_THREADS) {
+  // ---- 0. prefetch --------------------------------------------------------------
+  const int32_t cdone = ctl->done;
+  const int32_t nl0 = ctl->num_leaves, ns0 = ctl->n_slots, maxl = ctl->max_leaves;
+  const int32_t nred = ctl->n_reduce, spec = ctl->spec_max, cerr = ctl->error;
+  if (tid < 2 * SPEC_MAX + 2) s_red[tid] = ctl->reduce_list[tid];
+  for (int f = tid; f < F; f += PLAN_THREADS) s_ft[f] = L.feats[f];
+  for (int s = tid; s < slot_cap; s += PLAN_THREADS) {
     s_gain[s] = nd.key_gain[s];
     s_feat[s] = nd.key_feat[s];
-    s_child[2 * s] = nd.child[2 * s];
-    s_child[2 * s + 1] = nd.child[2 * s + 1];
+    s_fpos[s] = L.best_fpos[s];
+    s_child[s] = make_int2(nd.child[2 * s], nd.child[2 * s + 1]);
   }
-  for (int l = tid; l < nl0; l += PLAN_THREADS) {
-    s_leaf_slot[l] = L.leaf_slot[l];
-    s_leaf_parent[l] = T.leaf_parent[l];
-    s_leaf_side[l] = L.leaf_side[l];
-  }
-  for (int n = tid; n < nl0 - 1; n += PLAN_THREADS) {
-    s_left[n] = T.left_child[n];
-    s_right[n] = T.right_child[n];
-  }
+  for (int i = tid; i < 5 * MAX_LEAVES; i += PLAN_THREADS) (&s_ps[0][0])[i] = L.plan_state[i];
+  if (cdone) return;
   __syncthreads();
 
   // ---- 1. per-slot feature ArgMax -------------------------------------------
-  const int nred = ctl->n_reduce;
   for (int i = wave; i < nred; i += PLAN_WAVES) {
-    const int32_t s = ctl->reduce_list[i];
+    const int32_t s = s_red[i];
     BestKey k{ninf, -1, INT_MAX32};
     for (int f = lane; f < F; f += LGBM_WAVE) {
       const double g = L.feat_split[(size_t)s * F + f].gain;
-      const BestKey c{g, L.feats[f].real_index, f};
+      const BestKey c{g, s_ft[f].real_index, f};
       if (g > ninf && key_better(c, k)) k = c;
     }
     k = wave_best(k);
     const bool have = k.idx != INT_MAX32 && k.gain > ninf;
     if (lane == 0) {
-      if (have) {
-        L.best[s] = L.feat_split[(size_t)s * F + k.idx];
-      } else {
-        split_set_none(&L.best[s]);
-      }
-      L.best_fpos[s] = have ? k.idx : -1;
-      nd.key_gain[s] = have ? k.gain : ninf;
-      nd.key_feat[s] = have ? k.feat : -1;
-      s_gain[s] = have ? k.gain : ninf;
-      s_feat[s] = have ? k.feat : -1;
+      const double kg = have ? k.gain : ninf;
+      const int32_t kf = have ? k.feat : -1, kp = have ? k.idx : -1;
+      nd.key_gain[s] = kg;
+      nd.key_feat[s] = kf;
+      L.best_fpos[s] = kp;
+      s_gain[s] = kg;
+      s_feat[s] = kf;
+      s_fpos[s] = kp;
     }
   }
   __syncthreads();
 
   // ---- 2./3. commit loop and selection (wave 0) -------------------------------
+  // Lane l holds the keys of leaves l, l + 64, l + 128, l + 192 in registers; the
+  // rest of a leaf's state (node slot, speculated children and their keys, parent
+  // node and side) is in LDS by leaf id, so a commit reads it in one LDS round trip.
+  for (int l = tid; l < nl0; l += PLAN_THREADS) {
+    const int2 ch = s_child[s_ps[PS_LEAF_SLOT][l]];
+    s_lc[l] = ch;
+    if (ch.x >= 0) {
+      s_lcg[l] = make_double2(s_gain[ch.x], s_gain[ch.y]);
+      s_lcf[l] = make_int2(s_feat[ch.x], s_feat[ch.y]);
+    }
+  }
+  __syncthreads();
   if (wave == 0) {
+    constexpr int PL = MAX_LEAVES / LGBM_WAVE;
     int32_t nl = nl0, nc = 0, ns = ns0, nj = 0;
-    int32_t done = ctl->error ? 1 : 0;
-    double kg[MAX_LEAVES / LGBM_WAVE];
-    int32_t kf[MAX_LEAVES / LGBM_WAVE];
+    int32_t done = cerr ? 1 : 0;
+    double kg[PL];
+    int32_t kf[PL];
 #pragma unroll
-    for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i) {
+    for (int i = 0; i < PL; ++i) {
       const int l = lane + LGBM_WAVE * i;
       kg[i] = ninf;
       kf[i] = -1;
       if (l < nl) {
-        const int32_t s = s_leaf_slot[l];
+        const int32_t s = s_ps[PS_LEAF_SLOT][l];
         kg[i] = s_gain[s];
         kf[i] = s_feat[s];
       }
     }
     while (!done) {
-      BestKey k{ninf, -1, INT_MAX32};
-#pragma unroll
-      for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i) {
-        const int l = lane + LGBM_WAVE * i;
-        const BestKey c{kg[i], kf[i], l};
-        if (l < nl && key_better(c, k)) k = c;
-      }
-      k = wave_best(k);
-      if (!(k.gain > 0.0) || nl >= maxl) {
+      const int32_t bl = plan_argmax<PL>(kg, kf, nullptr, nl);
+      if (bl < 0 || nl >= maxl) {  // no positive gain left, or all leaves used
         done = 1;
         break;
       }
-      const int32_t bl = k.idx;
-      const int32_t p = s_leaf_slot[bl];
-      const int32_t cl = s_child[2 * p], cr = s_child[2 * p + 1];
-      if (cl < 0) break;  // not split yet: it leads the next round
+      const int2 ch = s_lc[bl];
+      if (ch.x < 0) break;  // not split yet: it leads the next round
+      const double2 cg = s_lcg[bl];
+      const int2 cf = s_lcf[bl];
+      const int32_t p = s_ps[PS_LEAF_SLOT][bl];
+      const int32_t pn = s_ps[PS_LEAF_PARENT][bl], side = s_ps[PS_LEAF_SIDE][bl];
       const int32_t node = nl - 1, nr = nl;
       if (lane == 0) {
-        const int32_t pn = s_leaf_parent[bl];
-        if (pn >= 0) {
-          if (s_leaf_side[bl])
-            s_right[pn] = node;
-          else
-            s_left[pn] = node;
-        }
-        s_left[node] = ~bl;
-        s_right[node] = ~nr;
-        s_leaf_parent[bl] = node;
-        s_leaf_side[bl] = 0;
-        s_leaf_parent[nr] = node;
-        s_leaf_side[nr] = 1;
-        s_leaf_slot[bl] = cl;
-        s_leaf_slot[nr] = cr;
+        if (pn >= 0) s_ps[side ? PS_NODE_RIGHT : PS_NODE_LEFT][pn] = node;
+        s_ps[PS_NODE_LEFT][node] = ~bl;
+        s_ps[PS_NODE_RIGHT][node] = ~nr;
+        s_ps[PS_LEAF_SLOT][bl] = ch.x;
+        s_ps[PS_LEAF_SLOT][nr] = ch.y;
+        s_ps[PS_LEAF_PARENT][bl] = node;
+        s_ps[PS_LEAF_PARENT][nr] = node;
+        s_ps[PS_LEAF_SIDE][bl] = 0;
+        s_ps[PS_LEAF_SIDE][nr] = 1;
+        s_lc[bl] = make_int2(-1, -1);  // fresh leaves: not split yet
+        s_lc[nr] = make_int2(-1, -1);
         s_commit[nc] = make_int4(bl, p, node, nr);
       }
-      const double gl = s_gain[cl], gr = s_gain[cr];
-      const int32_t fl = s_feat[cl], fr = s_feat[cr];
 #pragma unroll
-      for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i) {
+      for (int i = 0; i < PL; ++i) {
         const int l = lane + LGBM_WAVE * i;
         if (l == bl) {
-          kg[i] = gl;
-          kf[i] = fl;
+          kg[i] = cg.x;
+          kf[i] = cf.x;
         }
         if (l == nr) {
-          kg[i] = gr;
-          kf[i] = fr;
+          kg[i] = cg.y;
+          kf[i] = cf.y;
         }
       }
       ++nc;
       ++nl;
-      wave_sync();
     }
     if (!done) {
       // The first pick is the ArgMax leaf the commit loop stopped at.  Further picks
       // keep two node slots in reserve for every split the tree may still need, so
       // the ArgMax leaf of every later round can always be split.
-      bool cand[MAX_LEAVES / LGBM_WAVE];
+      bool cand[PL];
 #pragma unroll
-      for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i) {
+      for (int i = 0; i < PL; ++i) {
         const int l = lane + LGBM_WAVE * i;
-        cand[i] = l < nl && s_child[2 * s_leaf_slot[l]] < 0 && kg[i] > 0.0;
+        cand[i] = l < nl && kg[i] > 0.0 && s_lc[l].x < 0;
       }
-      const int32_t take = ctl->spec_max;
-      const int32_t cap = ctl->slot_cap;
-      while (nj < take) {
-        BestKey k{ninf, -1, INT_MAX32};
+      while (nj < spec) {
+        const int32_t l = plan_argmax<PL>(kg, kf, cand, nl);
+        if (l < 0) break;
+        if (nj == 0 ? ns + 2 > slot_cap : ns + 2 + 2 * (maxl - nl) > slot_cap) break;
 #pragma unroll
-        for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i) {
-          const BestKey c{kg[i], kf[i], lane + LGBM_WAVE * i};
-          if (cand[i] && key_better(c, k)) k = c;
-        }
-        k = wave_best(k);
-        if (!(k.gain > 0.0)) break;
-        if (nj == 0 ? ns + 2 > cap : ns + 2 + 2 * (maxl - nl) > cap) break;
-#pragma unroll
-        for (int i = 0; i < MAX_LEAVES / LGBM_WAVE; ++i)
-          if (lane + LGBM_WAVE * i == k.idx) cand[i] = false;
-        if (lane == 0) s_pick[nj] = make_int4(k.idx, s_leaf_slot[k.idx], ns, ns + 1);
+        for (int i = 0; i < PL; ++i)
+          if (lane + LGBM_WAVE * i == l) cand[i] = false;
+        if (lane == 0) s_pick[nj] = make_int4(l, s_ps[PS_LEAF_SLOT][l], ns, ns + 1);
         ns += 2;
         ++nj;
       }
@@ -317,63 +358,69 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L) {
   const int32_t nc = s_nc, nj = s_nj, nl = s_nl;
   for (int c = tid; c < nc; c += PLAN_THREADS) {
     const int4 cm = s_commit[c];
-    const int32_t p = cm.y, node = cm.z;
-    const lgbm_split_info b = L.best[p];
-    const DevFeature ft = L.feats[L.best_fpos[p]];
+    const int32_t p = cm.y, node = cm.z, fpos = s_fpos[p];
+    const lgbm_split_info& b = L.feat_split[(size_t)p * F + fpos];
+    const uint32_t thr = b.threshold;
+    const double gain = b.gain;
+    const int32_t dl = b.default_left;
+    const double iv = nd.sums[p].weight;
+    const int32_t ic = nd.count[p];
+    const DevFeature& ft = s_ft[fpos];
     T.split_feature[node] = ft.real_index;
-    T.split_gain[node] = (float)(b.gain + ctl->cfg.min_gain_to_split);  // learner.rs:3985
-    T.threshold_in_bin[node] = b.threshold;
-    T.threshold[node] = L.ub ? L.ub[ft.ub_off + b.threshold] : (double)b.threshold;
+    T.split_gain[node] = (float)(gain + ctl->cfg.min_gain_to_split);  // learner.rs:3985
+    T.threshold_in_bin[node] = thr;
     int8_t dt = 0;
-    if (b.default_left) dt |= 2;
+    if (dl) dt |= 2;
     dt |= (int8_t)((ft.missing_type & 3) << 2);
     T.decision_type[node] = dt;
-    T.internal_value[node] = nd.sums[p].weight;  // the split leaf's output
-    T.internal_count[node] = nd.count[p];        // partition counts (learner.rs:3994-4011)
+    T.internal_value[node] = iv;  // the split leaf's output
+    T.internal_count[node] = ic;  // partition counts (learner.rs:3994-4011)
+    lgbm_split_info bb;
+    bb.threshold = thr;
+    bb.default_left = dl;
     NodeRoute r;
-    r.f = L.best_fpos[p];
-    router_of(ft, b, &r.pmin, &r.th, &r.flags);
+    r.f = fpos;
+    router_of(ft, bb, &r.pmin, &r.th, &r.flags);
     r.max_bin = (int32_t)ft.max_bin;
     r.na_bin = (int32_t)ft.num_bin - 1;
     r.left = ~cm.x;
     r.right = ~cm.w;
     T.nodes[node] = r;
   }
-  for (int n = tid; n < nl - 1; n += PLAN_THREADS) {
-    T.left_child[n] = s_left[n];
-    T.right_child[n] = s_right[n];
-  }
   for (int l = tid; l < nl; l += PLAN_THREADS) {
-    L.leaf_slot[l] = s_leaf_slot[l];
-    T.leaf_parent[l] = s_leaf_parent[l];
-    L.leaf_side[l] = s_leaf_side[l];
+    L.plan_state[PS_LEAF_SLOT * MAX_LEAVES + l] = s_ps[PS_LEAF_SLOT][l];
+    L.plan_state[PS_LEAF_SIDE * MAX_LEAVES + l] = s_ps[PS_LEAF_SIDE][l];
+    L.plan_state[PS_LEAF_PARENT * MAX_LEAVES + l] = s_ps[PS_LEAF_PARENT][l];
+  }
+  for (int n = tid; n < nl - 1; n += PLAN_THREADS) {
+    L.plan_state[PS_NODE_LEFT * MAX_LEAVES + n] = s_ps[PS_NODE_LEFT][n];
+    L.plan_state[PS_NODE_RIGHT * MAX_LEAVES + n] = s_ps[PS_NODE_RIGHT][n];
   }
   for (int j = tid; j < nj; j += PLAN_THREADS) {
     const int4 pk = s_pick[j];
-    const int32_t p = pk.y, cl = pk.z, cr = pk.w;
-    const lgbm_split_info b = L.best[p];
-    const int32_t fpos = L.best_fpos[p];
-    const DevFeature ft = L.feats[fpos];
+    const int32_t p = pk.y, cl = pk.z, cr = pk.w, fpos = s_fpos[p];
+    const lgbm_split_info b = L.feat_split[(size_t)p * F + fpos];
+    const DevFeature& ft = s_ft[fpos];
     PartJob J;
     J.parent = p;
     J.cl = cl;
     J.cr = cr;
     J.src_buf = nd.buf[p];
-    J.dst_buf = J.src_buf == BUF_A ? BUF_B : BUF_A;
     J.rev = nd.rev[p];
     J.begin = nd.begin[p];
     J.count = nd.count[p];
+    const int32_t d = nd.depth[p] + 1;
+    J.dst_buf = J.src_buf == BUF_A ? BUF_B : BUF_A;
     J.fbyte = fpos;
     router_of(ft, b, &J.pmin, &J.th, &J.flags);
     J.max_bin = (int32_t)ft.max_bin;
     J.na_bin = (int32_t)ft.num_bin - 1;
     // build the histogram of the side the scan expects to be smaller
     J.acc_right = b.right_count < b.left_count ? 1 : 0;
-    J.ntiles = (int32_t)((J.count + PART_TILE - 1) / PART_TILE);
+    J.ntiles = (int32_t)((J.count + part_tile - 1) / part_tile);
     J.tile0 = 0;
     ctl->jobs[j] = J;
     s_ntiles[j] = J.ntiles;
-    const int32_t d = nd.depth[p] + 1;
     nd.child[2 * p] = cl;
     nd.child[2 * p + 1] = cr;
     nd.child[2 * cl] = -1;
@@ -408,6 +455,13 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L) {
     ctl->num_leaves = nl;
     ctl->n_slots = s_nslots;
     ctl->rounds += 1;
+    if (nj > 0) {
+      // the round's partition: fresh tickets and a new look-back epoch
+      ctl->part_ticket = 0;
+      uint32_t ep = (ctl->epoch + 1u) & 0x3fffffffu;
+      ctl->epoch = ep == 0u ? 1u : ep;
+      L.stats[1] += 1.0;
+    }
     if (s_done) ctl->done = 1;
   }
 }
@@ -419,33 +473,40 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L) {
 // prefix by decoupled look-back over the earlier tiles of the same job.  Left rows go
 // to [begin, begin + L) ascending; right rows to [begin + L, begin + count) in
 // descending position (logical order = ascending, stored reversed), so no total is
-// needed in advance.  Look-back words: epoch(30) | flag(2) | value(32).
+// needed in advance.  Look-back words: epoch(30) | flag(2) | value(32).  The launcher
+// of a round (k_plan, or the host for the per-op entry point) resets the ticket
+// counter and moves to a fresh epoch, so stale words of earlier rounds never match.
 // In the tree driver the pass also builds one child's integer histogram per job (the
 // side the scan predicts to be smaller) from the rows while they are in registers;
 // the other child's is parent - built in integers (k_pair_scan).
 // ===========================================================================
-template <int W>
-__global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
+template <int W, int PT, int PR>
+__global__ __launch_bounds__(PT) void k_partition(DevLearner L) {
+  constexpr int kWaves = PT / LGBM_WAVE;
+  constexpr int kTile = PT * PR;
   extern __shared__ unsigned long long lds_hist[];
   __shared__ int32_t cb[16 * LGBM_MAX_W];
   __shared__ PartJob s_jobs[SPEC_MAX];
   __shared__ int64_t s_tile;
-  __shared__ int32_t s_cnt[PART_ROWS_PER_THREAD][PART_WAVES];
-  __shared__ int32_t s_pref[PART_ROWS_PER_THREAD][PART_WAVES];
+  __shared__ int32_t s_cnt[PR][kWaves];
+  __shared__ int32_t s_pref[PR][kWaves];
   __shared__ int32_t s_total;
   __shared__ int32_t s_excl;
   Ctl* ctl = L.ctl;
+  const int tid = threadIdx.x, wave = tid >> 6;
   const int32_t nj = ctl->n_jobs;
   const int64_t total = ctl->tile_total;
-  if (nj <= 0 || total <= 0) return;
-  const int64_t nblk = min((int64_t)gridDim.x, total);
-  if ((int64_t)blockIdx.x >= nblk) return;
   const uint32_t epoch = ctl->epoch & 0x3fffffffu;
-  const int tid = threadIdx.x, wave = tid >> 6;
-  const int F = L.F, cells = L.total_cells;
-  if (tid < nj) s_jobs[tid] = ctl->jobs[tid];
-  for (int c = tid; c < cells; c += PART_THREADS) lds_hist[c] = 0ull;
-  for (int f = tid; f < F; f += PART_THREADS) cb[f] = (int32_t)L.feats[f].cell_base;
+  if (tid < SPEC_MAX) s_jobs[tid] = ctl->jobs[tid];
+  if (nj <= 0 || total <= 0 || (int64_t)blockIdx.x >= total) return;
+  const int F = L.F, cells = L.total_cells, nw = (F + 3) / 4;
+  for (int c = tid; c < cells + 4; c += PT) lds_hist[c] = 0ull;
+  for (int f = tid; f < 16 * W; f += PT) cb[f] = f < F ? (int32_t)L.feats[f].cell_base : cells;
+  __syncthreads();
+  // feature cell bases in scalar registers (bytes beyond F map to the trash cell)
+  int32_t cbr[16 * W];
+#pragma unroll
+  for (int f = 0; f < 16 * W; ++f) cbr[f] = __builtin_amdgcn_readfirstlane(cb[f]);
   int32_t cur = -1;  // job whose rows the LDS histogram holds
   while (true) {
     __syncthreads();
@@ -459,7 +520,8 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     while (j + 1 < nj && s_jobs[j + 1].tile0 <= t) ++j;
     if (j != cur) {
       if (cur >= 0 && s_jobs[cur].acc_right >= 0) {
-        lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3);
+        lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3,
+                             s_jobs[cur].ntiles == 1);
         __syncthreads();
       }
       cur = j;
@@ -467,18 +529,18 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     const PartJob& J = s_jobs[j];
     const int64_t count = J.count, begin = J.begin;
     const int64_t lt = t - J.tile0;
-    const int64_t base = lt * PART_TILE;
+    const int64_t base = lt * kTile;
     const uint4* __restrict__ src = L.bufs.rec[J.src_buf];
     const uint16_t* __restrict__ sgh = L.bufs.gh[J.src_buf];
     uint4* __restrict__ dst = L.bufs.rec[J.dst_buf];
     uint16_t* __restrict__ dgh = L.bufs.gh[J.dst_buf];
-    uint4 w[PART_ROWS_PER_THREAD][W];
-    uint16_t q[PART_ROWS_PER_THREAD];
-    bool isleft[PART_ROWS_PER_THREAD], valid[PART_ROWS_PER_THREAD];
-    int32_t rank[PART_ROWS_PER_THREAD];
+    uint4 w[PR][W];
+    uint16_t q[PR];
+    bool isleft[PR], valid[PR];
+    int32_t rank[PR];
 #pragma unroll
-    for (int k = 0; k < PART_ROWS_PER_THREAD; ++k) {
-      const int64_t p = base + (int64_t)k * PART_THREADS + tid;
+    for (int k = 0; k < PR; ++k) {
+      const int64_t p = base + (int64_t)k * PT + tid;
       valid[k] = p < count;
       bool right = false;
       if (valid[k]) {
@@ -497,8 +559,8 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     __syncthreads();
     if (tid == 0) {
       int32_t acc = 0;
-      for (int k = 0; k < PART_ROWS_PER_THREAD; ++k)
-        for (int wv = 0; wv < PART_WAVES; ++wv) {
+      for (int k = 0; k < PR; ++k)
+        for (int wv = 0; wv < kWaves; ++wv) {
           s_pref[k][wv] = acc;
           acc += s_cnt[k][wv];
         }
@@ -546,9 +608,9 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     const int64_t excl = s_excl;
     const int64_t rbase = base - excl;  // right rows before this tile
 #pragma unroll
-    for (int k = 0; k < PART_ROWS_PER_THREAD; ++k) {
+    for (int k = 0; k < PR; ++k) {
       if (!valid[k]) continue;
-      const int64_t pos = (int64_t)k * PART_THREADS + tid;
+      const int64_t pos = (int64_t)k * PT + tid;
       const int64_t lrank = s_pref[k][wave] + rank[k];
       int64_t d;
       if (isleft[k]) {
@@ -564,8 +626,8 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     if (J.acc_right >= 0) {
       const bool want_left = J.acc_right == 0;
 #pragma unroll
-      for (int k = 0; k < PART_ROWS_PER_THREAD; ++k)
-        if (valid[k] && isleft[k] == want_left) lds_hist_add<W>(lds_hist, cb, F, w[k], q[k]);
+      for (int k = 0; k < PR; ++k)
+        if (valid[k] && isleft[k] == want_left) lds_hist_add<W>(lds_hist, cbr, nw, w[k], q[k]);
     }
     if (lt == J.ntiles - 1 && tid == 0) {
       const int32_t lc = (int32_t)(excl + s_total);
@@ -590,24 +652,15 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     }
   }
   if (cur >= 0 && s_jobs[cur].acc_right >= 0)
-    lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3);
-  if (tid == 0) {
-    const int32_t prev =
-        __hip_atomic_fetch_add(&ctl->part_exit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == (int32_t)nblk - 1) {
-      __hip_atomic_store(&ctl->part_ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&ctl->part_exit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ctl->epoch = (ctl->epoch + 1u) & 0x3fffffffu;
-      if (ctl->epoch == 0u) ctl->epoch = 1u;
-      L.stats[1] += 1.0;
-    }
-  }
+    lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3,
+                         s_jobs[cur].ntiles == 1);
 }
 
 // ===========================================================================
 // k_pair_scan: block (feature f, job j), two waves.  The children of job j:
-//   integer cells: the built side from the job's accumulator, the other side =
-//   parent - built (exact); both stored in the children's integer slots;
+//   integer cells: the side built in the partition pass from the job's accumulator
+//   (cleared after reading), the other side = parent - built (exact); both stored in
+//   the children's integer slots;
 //   smaller child (partition counts, a tie makes the right child the smaller one:
 //   learner.rs:4061-4089): exact f64 cells -> FixHistogram on its RAW sums ->
 //   compaction; larger = parent - smaller in f64 (histogram_pool.rs:249, not re-fixed);
@@ -637,13 +690,13 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L) {
   for (int b = tid; b < nb; b += SCAN_THREADS) {
     const size_t ci = (size_t)(ft.cell_base + b);
     int32_t* a = acc + ci * 3;
-    const int32_t AG = a[0], AH = a[1], AT = a[2];
+    const int32_t AG = a[0], AH = a[1], AT = a[2];  // the side built in the partition pass
     a[0] = 0;
     a[1] = 0;
     a[2] = 0;
     if (gated) continue;
     const int32_t* ps = L.int_slots + ((size_t)p * cells + ci) * 3;
-    const int32_t OG = ps[0] - AG, OH = ps[1] - AH, OT = ps[2] - AT;
+    const int32_t OG = ps[0] - AG, OH = ps[1] - AH, OT = ps[2] - AT;  // exact
     int32_t* ls = L.int_slots + ((size_t)cl * cells + ci) * 3;
     int32_t* rs = L.int_slots + ((size_t)cr * cells + ci) * 3;
     const int32_t LG_ = acc_right ? OG : AG, LH = acc_right ? OH : AH, LT = acc_right ? OT : AT;
@@ -702,16 +755,18 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L) {
 // ===========================================================================
 // k_tree_finalize: the Tree's leaf arrays from the committed leaves' node slots
 // (leaf_value = the leaf's output, leaf_weight = its sum_hessian, 0 for an unsplit
-// root: Tree::root, learner.rs:5398-5424), the score-update routes, and the per-leaf
-// ranges of the LeafPartitionLayout.
+// root: Tree::root, learner.rs:5398-5424), its linkage and real thresholds, the
+// score-update routes, and the per-leaf ranges of the LeafPartitionLayout.
 // ===========================================================================
 __global__ void k_tree_finalize(DevLearner L) {
   const Ctl* ctl = L.ctl;
   const int32_t nl = ctl->num_leaves;
   DevTree& T = L.tree;
   const DevNodes& nd = L.nodes;
+  const int32_t* ps = L.plan_state;
   for (int l = threadIdx.x; l < nl; l += blockDim.x) {
-    const int32_t s = L.leaf_slot[l];
+    const int32_t s = ps[PS_LEAF_SLOT * MAX_LEAVES + l];
+    T.leaf_parent[l] = ps[PS_LEAF_PARENT * MAX_LEAVES + l];
     T.leaf_value[l] = nd.sums[s].weight;
     T.leaf_weight[l] = s == 0 ? 0.0 : nd.sums[s].sh;
     T.leaf_count[l] = nd.count[s];
@@ -722,8 +777,14 @@ __global__ void k_tree_finalize(DevLearner L) {
     L.leaves.rev[l] = nd.rev[s];
   }
   for (int n = threadIdx.x; n < nl - 1; n += blockDim.x) {
-    T.nodes[n].left = T.left_child[n];
-    T.nodes[n].right = T.right_child[n];
+    const int32_t lc = ps[PS_NODE_LEFT * MAX_LEAVES + n], rc = ps[PS_NODE_RIGHT * MAX_LEAVES + n];
+    T.left_child[n] = lc;
+    T.right_child[n] = rc;
+    T.nodes[n].left = lc;
+    T.nodes[n].right = rc;
+    // real_threshold (learner.rs:198-203): the bin's upper bound
+    const uint32_t tb = T.threshold_in_bin[n];
+    T.threshold[n] = L.ub ? L.ub[L.feats[T.nodes[n].f].ub_off + tb] : (double)tb;
   }
   if (threadIdx.x == 0) {
     T.header[0] = nl;
@@ -755,19 +816,40 @@ void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth
                       int32_t spec_max, hipStream_t s, const KernelEvents* ev) {
   KLAUNCH(ev, k_tree_init, dim3(16), dim3(256), 0, s, L, max_leaves, max_depth, slot_cap, spec_max);
 }
-void launch_plan(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
-  KLAUNCH(ev, k_plan, dim3(1), dim3(PLAN_THREADS), 0, s, L);
+void launch_plan(const DevLearner& L, int32_t slot_cap, int32_t part_tile, hipStream_t s,
+                 const KernelEvents* ev) {
+  KLAUNCH(ev, k_plan, dim3(1), dim3(PLAN_THREADS), 0, s, L, slot_cap, part_tile);
 }
-void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s,
+// Partition launch shapes: (threads, rows per thread); the tile is their product.
+int part_tile_of(int shape) {
+  static const int t[5][2] = {{1024, 4}, {512, 4}, {512, 2}, {256, 4}, {256, 8}};
+  return t[shape][0] * t[shape][1];
+}
+void launch_partition(const DevLearner& L, int W, int shape, int64_t blocks, hipStream_t s,
                       const KernelEvents* ev) {
-  int64_t blocks = PART_MAX_BLOCKS;
-  if (count_hint > 0) blocks = std::min<int64_t>(blocks, (count_hint + PART_TILE - 1) / PART_TILE);
   if (blocks < 1) blocks = 1;
-  const size_t lds = (size_t)std::max(L.total_cells, 1) * sizeof(unsigned long long);
-  DISPATCH_W(W, KLAUNCH(ev, k_partition<kW>, dim3((unsigned)blocks), dim3(PART_THREADS), lds, s, L));
+  const size_t lds = (size_t)(std::max(L.total_cells, 1) + 4) * sizeof(unsigned long long);
+  const dim3 g((unsigned)blocks);
+#define PART_SHAPES(kW)                                                                    \
+  switch (shape) {                                                                         \
+    case 1: KLAUNCH(ev, (k_partition<kW, 512, 4>), g, dim3(512), lds, s, L); break;        \
+    case 2: KLAUNCH(ev, (k_partition<kW, 512, 2>), g, dim3(512), lds, s, L); break;        \
+    case 3: KLAUNCH(ev, (k_partition<kW, 256, 4>), g, dim3(256), lds, s, L); break;        \
+    case 4: KLAUNCH(ev, (k_partition<kW, 256, 8>), g, dim3(256), lds, s, L); break;        \
+    default: KLAUNCH(ev, (k_partition<kW, 1024, 4>), g, dim3(1024), lds, s, L); break;     \
+  }
+  switch (W) {
+    case 1: { PART_SHAPES(1) } break;
+    case 2: { PART_SHAPES(2) } break;
+    default:
+      DISPATCH_W(W, KLAUNCH(ev, (k_partition<kW, 1024, 4>), g, dim3(1024), lds, s, L));
+      break;
+  }
+#undef PART_SHAPES
 }
-void launch_pair_scan(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
-  KLAUNCH(ev, k_pair_scan, dim3((unsigned)L.F, SPEC_MAX), dim3(SCAN_THREADS), 0, s, L);
+void launch_pair_scan(const DevLearner& L, int32_t spec_max, hipStream_t s,
+                      const KernelEvents* ev) {
+  KLAUNCH(ev, k_pair_scan, dim3((unsigned)L.F, (unsigned)spec_max), dim3(SCAN_THREADS), 0, s, L);
 }
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
   KLAUNCH(ev, k_tree_finalize, dim3(1), dim3(256), 0, s, L);

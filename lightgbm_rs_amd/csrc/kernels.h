@@ -82,7 +82,7 @@ struct DevLearner {
   int32_t _pad;
   int64_t N;
   uint64_t slot_len;
-  int32_t* hist_int;          // [total_cells][3] root / per-op accumulator
+  int32_t* hist_part;         // [HIST_SLOTS][total_cells][3] root / per-op partials
   int32_t* hist_acc;          // [SPEC_MAX][total_cells][3] per-job accumulators
   int32_t* int_slots;         // [slot_cap][total_cells][3] per-node integer histograms
   double* slots;              // [slot_cap][slot_len] per-node f64 histograms
@@ -90,8 +90,7 @@ struct DevLearner {
   lgbm_split_info* best;        // [slot_cap]
   int32_t* best_fpos;           // [slot_cap] feature position of best
   uint8_t* splittable;          // [slot_cap][F]
-  int32_t* leaf_slot;           // [MAX_LEAVES] leaf id -> node slot
-  int32_t* leaf_side;           // [MAX_LEAVES] 1: right child of leaf_parent
+  int32_t* plan_state;          // [5][MAX_LEAVES] leaf / node linkage owned by k_plan
   uint64_t* tile_state;
   double* stats;                // [0] rows partitioned, [1] partition launches, [2] root
                                 // rows, [3] root launches, [4] partition jobs
@@ -119,16 +118,18 @@ void launch_quant_scales(Ctl* ctl, const uint4* partials, int64_t n, int32_t bin
 void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,
                      const uint64_t* wave_mats, const uint64_t* lane_mats, uint64_t s0,
                      int32_t stochastic, uint16_t* gh, float* dg, float* dh, hipStream_t s);
-void launch_hist(const DevLearner& L, int32_t driver, int64_t count_hint, hipStream_t s,
-                 const KernelEvents* ev = nullptr);
+void launch_hist(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
 void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s,
                     const KernelEvents* ev = nullptr);
-void launch_plan(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
-void launch_pair_scan(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
+void launch_plan(const DevLearner& L, int32_t slot_cap, int32_t part_tile, hipStream_t s,
+                 const KernelEvents* ev = nullptr);
+void launch_pair_scan(const DevLearner& L, int32_t spec_max, hipStream_t s,
+                      const KernelEvents* ev = nullptr);
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,
                           lgbm_split_info* out, hipStream_t s);
-void launch_partition(const DevLearner& L, int W, int64_t count_hint, hipStream_t s,
+int part_tile_of(int shape);
+void launch_partition(const DevLearner& L, int W, int shape, int64_t blocks, hipStream_t s,
                       const KernelEvents* ev = nullptr);
 void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth,
                       int32_t slot_cap, int32_t spec_max, hipStream_t s,

@@ -258,74 +258,191 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ g,
 }
 
 // ===========================================================================
-// ConstructHistogram (integer).  A block owns a contiguous run of the leaf's rows
-// and a private LDS histogram of packed 64-bit cells
-//   cell += q_g + (q_h << 22) + ([q_h == 3] << 43)
-// (fields: 22-bit signed, 21-bit, 21-bit; exact for < 2^19 rows per block), then
-// flushes the three fields with integer atomics into the global [cells][3] array.
-// Integer addition is associative, so the result is independent of scheduling.
+// ConstructHistogram (integer), batched over the histogram jobs of a round (the
+// smaller child of every split; the root; a per-op build).  A job is a physical row
+// range of one row buffer; row order is irrelevant because integer addition is
+// associative.  The rows of all jobs are cut into chunks of R rows (at least
+// HIST_MIN_ROWS, at most HIST_GRID chunks over all jobs); chunk a is one block, which
+// stores its histogram with plain stores into partial slot a.  Consumers add the
+// partial slots [a0, a0 + nblk) of a job (recorded in its HistJob by block 0).
+//
+// Two accumulation schemes:
+//  - wave-private (cells <= HIST_WAVE_CELLS): each wave owns a u32 LDS histogram of
+//    packed cells  q_g + (q_h << 11) + ([q_h == 3] << 22)  (fields 11-bit signed,
+//    11-bit, 10-bit: exact for <= 511 rows), folds it into per-lane register sums
+//    at least every HIST_FOLD_STEPS x 64 rows (lane l owns cells l, l + 64, ...), and
+//    the waves are combined at the end.  One 32-bit LDS atomic per (row, feature).
+//  - block-shared: one u64 LDS histogram per block, cells
+//    q_g + (q_h << 22) + ([q_h == 3] << 43) (exact for < 2^19 rows per block).
 // ===========================================================================
-template <int W>
-__global__ __launch_bounds__(HIST_THREADS) void k_hist(DevLearner L, int32_t driver) {
-  extern __shared__ unsigned long long lds_hist[];
+__device__ __forceinline__ void hist_assign(const Ctl* ctl, int32_t nj, int32_t* s_a0,
+                                            int32_t* s_nb, int64_t* s_R) {
+  int64_t S = 0;
+  for (int j = 0; j < nj; ++j) S += max(ctl->hjobs[j].count, (int64_t)0);
+  int64_t R = (S + HIST_GRID - 1) / HIST_GRID;
+  if (R < HIST_MIN_ROWS) R = HIST_MIN_ROWS;
+  int32_t acc = 0;
+  for (int j = 0; j < nj; ++j) {
+    const int64_t c = ctl->hjobs[j].count;
+    const int32_t nb = c > 0 ? (int32_t)((c + R - 1) / R) : 0;
+    s_a0[j] = acc;
+    s_nb[j] = nb;
+    acc += nb;
+  }
+  *s_R = R;
+}
+
+template <int W, bool WAVE_PRIVATE>
+__global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
+  extern __shared__ uint32_t lds_u32[];
   __shared__ int32_t cb[16 * LGBM_MAX_W];
-  const Ctl* ctl = L.ctl;
-  // driver 2: the root build of the tree driver, which the reference performs
-  // unconditionally (LeafSplits::init, learner.rs:1323-1328); 0: per-op build.
-  if (driver == 2 && ctl->done) return;
-  const int32_t buf = ctl->h_buf;
-  const int64_t begin = ctl->h_begin, count = ctl->h_count;
-  if (count <= 0) return;
-  int64_t nblk = (count + HIST_MIN_ROWS_PER_BLOCK - 1) / HIST_MIN_ROWS_PER_BLOCK;
-  if (nblk > gridDim.x) nblk = gridDim.x;
-  if ((int64_t)blockIdx.x >= nblk) return;
-  const int64_t per = (count + nblk - 1) / nblk;
-  const int64_t lo = (int64_t)blockIdx.x * per;
-  const int64_t hi = min(count, lo + per);
-  if (lo >= hi) return;
+  __shared__ int32_t s_a0[SPEC_MAX], s_nb[SPEC_MAX];
+  __shared__ int64_t s_R;
+  Ctl* ctl = L.ctl;
+  const int32_t nj = ctl->n_hjobs;
+  if (nj <= 0) return;
+  const int tid = threadIdx.x, lane = (int)lane_id(), wave = tid >> 6;
   const int F = L.F, cells = L.total_cells;
-  for (int c = threadIdx.x; c < cells; c += HIST_THREADS) lds_hist[c] = 0ull;
-  for (int f = threadIdx.x; f < F; f += HIST_THREADS) cb[f] = (int32_t)L.feats[f].cell_base;
+  // Record words 0 .. nw-1 hold the bins (four features each); bytes of the last word
+  // beyond F are zero and land in a trash cell at index `cells`.
+  const int nw = (F + 3) / 4;
+  if (tid == 0) {
+    hist_assign(ctl, nj, s_a0, s_nb, &s_R);
+    if (blockIdx.x == 0)
+      for (int j = 0; j < nj; ++j) {
+        ctl->hjobs[j].a0 = s_a0[j];
+        ctl->hjobs[j].nblk = s_nb[j];
+      }
+  }
+  for (int f = tid; f < 16 * W; f += HIST_THREADS)
+    cb[f] = f < F ? (int32_t)L.feats[f].cell_base : cells;
   __syncthreads();
-  const uint4* __restrict__ rec = L.bufs.rec[buf] + begin * W;
-  const uint16_t* __restrict__ gh = L.bufs.gh[buf] + begin;
-  for (int64_t r = lo + threadIdx.x; r < hi; r += HIST_THREADS) {
-    uint4 w[W];
+  const int32_t a = (int32_t)blockIdx.x;
+  int32_t j = -1;
+  for (int k = 0; k < nj; ++k)
+    if (a >= s_a0[k] && a < s_a0[k] + s_nb[k]) j = k;
+  if (j < 0) return;
+  const HistJob& J = ctl->hjobs[j];
+  const int64_t R = s_R;
+  const int64_t lo = (int64_t)(a - s_a0[j]) * R;
+  const int64_t hi = min(J.count, lo + R);
+  const uint4* __restrict__ rec = L.bufs.rec[J.buf] + J.begin * W;
+  const uint16_t* __restrict__ gh = L.bufs.gh[J.buf] + J.begin;
+  int32_t* __restrict__ out = L.hist_part + (size_t)a * cells * 3;
+  // feature cell bases in scalar registers (wave-uniform)
+  int32_t cbr[16 * W];
 #pragma unroll
-    for (int i = 0; i < W; ++i) w[i] = rec[r * W + i];
-    const uint32_t q = gh[r];
-    const int32_t qg = (int32_t)(int8_t)(q & 0xffu);
-    const int32_t qh = (int32_t)(int8_t)(q >> 8);
-    const unsigned long long v = (unsigned long long)(long long)qg +
-                                 ((unsigned long long)(uint32_t)qh << 22) +
-                                 ((unsigned long long)(qh == 3 ? 1u : 0u) << 43);
+  for (int f = 0; f < 16 * W; ++f) cbr[f] = __builtin_amdgcn_readfirstlane(cb[f]);
+
+  if constexpr (WAVE_PRIVATE) {
+    constexpr int NPL = HIST_WAVE_CELLS / LGBM_WAVE;  // cells per lane
+    const int stride = cells + 4;                     // + trash cell
+    uint32_t* my = lds_u32 + (size_t)wave * stride;
+    for (int c = lane; c < stride; c += LGBM_WAVE) my[c] = 0u;
+    int32_t sg[NPL], sh[NPL], s3[NPL];
 #pragma unroll
-    for (int wi = 0; wi < W; ++wi) {
-      const uint32_t ww[4] = {w[wi].x, w[wi].y, w[wi].z, w[wi].w};
+    for (int i = 0; i < NPL; ++i) {
+      sg[i] = 0;
+      sh[i] = 0;
+      s3[i] = 0;
+    }
+    // the wave's contiguous share of the block's rows, HIST_ROWS_PER_LANE per lane
+    // per step (loads first, then the atomics)
+    const int64_t n = hi - lo;
+    const int64_t wper = (n + HIST_WAVES - 1) / HIST_WAVES;
+    const int64_t wlo = lo + min(n, (int64_t)wave * wper);
+    const int64_t whi = lo + min(n, (int64_t)(wave + 1) * wper);
+    int step = 0;
+    auto fold = [&]() {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int f = wi * 16 + j;
-        if (f < F) {
-          const uint32_t bin = (ww[j >> 2] >> (8 * (j & 3))) & 0xffu;
-          __hip_atomic_fetch_add(&lds_hist[cb[f] + bin], v, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+      for (int i = 0; i < NPL; ++i) {
+        const int c = i * LGBM_WAVE + lane;
+        if (c < cells) {
+          const uint32_t p = my[c];
+          my[c] = 0u;
+          const int32_t g = ((int32_t)(p << 21)) >> 21;
+          const uint32_t rest = (p - (uint32_t)g) >> 11;
+          sg[i] += g;
+          sh[i] += (int32_t)(rest & 0x7ffu);
+          s3[i] += (int32_t)(rest >> 11);
         }
       }
+    };
+    constexpr int U = HIST_ROWS_PER_LANE;
+    for (int64_t r0 = wlo; r0 < whi; r0 += LGBM_WAVE * U) {
+      uint4 w[U][W];
+      uint32_t q[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t r = r0 + u * LGBM_WAVE + lane;
+        q[u] = 0u;
+        if (r < whi) {
+#pragma unroll
+          for (int i = 0; i < W; ++i) w[u][i] = rec[r * W + i];
+          q[u] = (uint32_t)gh[r] | 0x10000u;  // bit 16: a real row
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (q[u] == 0u) continue;
+        const int32_t qg = (int32_t)(int8_t)(q[u] & 0xffu);
+        const int32_t qh = (int32_t)(int8_t)((q[u] >> 8) & 0xffu);
+        const uint32_t v = (uint32_t)qg + ((uint32_t)qh << 11) + ((qh == 3 ? 1u : 0u) << 22);
+#pragma unroll
+        for (int k = 0; k < 4 * W - 1; ++k) {
+          if (k < nw) {
+            const uint4 wd = w[u][k >> 2];
+            const uint32_t word = (k & 3) == 0 ? wd.x : ((k & 3) == 1 ? wd.y : ((k & 3) == 2 ? wd.z : wd.w));
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb)
+              __hip_atomic_fetch_add(&my[cbr[4 * k + bb] + ((word >> (8 * bb)) & 0xffu)], v,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+          }
+        }
+      }
+      step += U;
+      if (step + U > HIST_FOLD_STEPS) {
+        step = 0;
+        fold();
+      }
     }
-  }
-  __syncthreads();
-  for (int c = threadIdx.x; c < cells; c += HIST_THREADS) {
-    const unsigned long long p = lds_hist[c];
-    if (p == 0ull) continue;
-    const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
-    const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
-    const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
-    const int32_t hsum = (int32_t)(rest & ((1ull << 21) - 1));
-    const int32_t n3 = (int32_t)(rest >> 21);
-    int32_t* dst = L.hist_int + (size_t)c * 3;
-    if (gsum) __hip_atomic_fetch_add(dst, (int32_t)gsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (hsum) __hip_atomic_fetch_add(dst + 1, hsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (n3) __hip_atomic_fetch_add(dst + 2, n3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    fold();
+    // combine the waves: int32 [cells][3] in the (now free) LDS
+    __syncthreads();
+    int32_t* acc = (int32_t*)lds_u32;
+    for (int c = tid; c < cells * 3; c += HIST_THREADS) acc[c] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int c = i * LGBM_WAVE + lane;
+      if (c < cells) {
+        if (sg[i]) atomicAdd(&acc[c * 3], sg[i]);
+        if (sh[i]) atomicAdd(&acc[c * 3 + 1], sh[i]);
+        if (s3[i]) atomicAdd(&acc[c * 3 + 2], s3[i]);
+      }
+    }
+    __syncthreads();
+    for (int c = tid; c < cells * 3; c += HIST_THREADS) out[c] = acc[c];
+  } else {
+    unsigned long long* h64 = (unsigned long long*)lds_u32;
+    for (int c = tid; c < cells + 4; c += HIST_THREADS) h64[c] = 0ull;
+    __syncthreads();
+    for (int64_t r = lo + tid; r < hi; r += HIST_THREADS) {
+      uint4 w[W];
+#pragma unroll
+      for (int i = 0; i < W; ++i) w[i] = rec[r * W + i];
+      lds_hist_add<W>(h64, cbr, nw, w, gh[r]);
+    }
+    __syncthreads();
+    for (int c = tid; c < cells; c += HIST_THREADS) {
+      const unsigned long long p = h64[c];
+      const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
+      const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
+      const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
+      out[c * 3] = (int32_t)gsum;
+      out[c * 3 + 1] = (int32_t)(rest & ((1ull << 21) - 1));
+      out[c * 3 + 2] = (int32_t)(rest >> 21);
+    }
   }
 }
 
@@ -335,7 +452,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist(DevLearner L, int32_t dri
 //                   (exact, from the integer totals), FixHistogram, compaction, and
 //                   the root's FindBestThreshold (wave 0).
 //   mode 2 (build): per-op build into `explicit_out` (no scan).
-// The integer accumulator cells are cleared after reading.
+// The integer cells are the sum of histogram job 0's partial slots.
 // ===========================================================================
 __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t mode,
                                                           double* __restrict__ explicit_out) {
@@ -349,13 +466,11 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
   const int nb = (int)ft.num_bin;
   const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
   long long tg = 0, th = 0, t3 = 0;
+  const int32_t a0 = ctl->hjobs[0].a0, na = ctl->hjobs[0].nblk;
   for (int b = tid; b < nb; b += SCAN_THREADS) {
     const size_t ci = (size_t)(ft.cell_base + b);
-    int32_t* acc = L.hist_int + ci * 3;
-    const int32_t G = acc[0], H = acc[1], T = acc[2];
-    acc[0] = 0;
-    acc[1] = 0;
-    acc[2] = 0;
+    int32_t G = 0, H = 0, T = 0;
+    hist_part_sum(L, a0, na, ci, &G, &H, &T);
     if (mode == 1) {
       int32_t* ps = L.int_slots + ci * 3;  // node slot 0
       ps[0] = G;
@@ -534,16 +649,15 @@ void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,
   k_quantize<<<dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0, s>>>(
       g, h, n, ctl, wave_mats, lane_mats, s0, stochastic, gh, dg, dh);
 }
-void launch_hist(const DevLearner& L, int32_t driver, int64_t count_hint, hipStream_t s,
-                 const KernelEvents* ev) {
-  int64_t blocks = HIST_MAX_BLOCKS;
-  if (count_hint > 0)
-    blocks = std::min<int64_t>(HIST_MAX_BLOCKS,
-                               (count_hint + HIST_MIN_ROWS_PER_BLOCK - 1) / HIST_MIN_ROWS_PER_BLOCK);
-  if (blocks < 1) blocks = 1;
-  const size_t lds = (size_t)L.total_cells * sizeof(unsigned long long);
-  DISPATCH_W(L.W, KLAUNCH(ev, k_hist<kW>, dim3((unsigned)blocks), dim3(HIST_THREADS), lds, s, L,
-                          driver));
+void launch_hist(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
+  const dim3 g(HIST_SLOTS), blk(HIST_THREADS);
+  if (L.total_cells <= HIST_WAVE_CELLS) {
+    const size_t lds = (size_t)HIST_WAVES * (L.total_cells + 4) * sizeof(uint32_t);
+    DISPATCH_W(L.W, KLAUNCH(ev, (k_hist_jobs<kW, true>), g, blk, lds, s, L));
+  } else {
+    const size_t lds = (size_t)(L.total_cells + 4) * sizeof(unsigned long long);
+    DISPATCH_W(L.W, KLAUNCH(ev, (k_hist_jobs<kW, false>), g, blk, lds, s, L));
+  }
 }
 void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s,
                     const KernelEvents* ev) {

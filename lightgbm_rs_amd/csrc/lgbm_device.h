@@ -12,15 +12,21 @@
 
 #define LGBM_WAVE 64
 #define LGBM_MAX_W 8                    // record words (16 B): features <= 16*W - 4
-#define HIST_THREADS 1024               // ConstructHistogram block
-#define HIST_MAX_BLOCKS 256             // one block per CU
-#define HIST_MIN_ROWS_PER_BLOCK 4096
-#define HIST_MAX_ROWS_PER_BLOCK ((1 << 19) - 1)  // packed 64-bit LDS cell field limits
+#define HIST_THREADS 512                // ConstructHistogram block
+#define HIST_WAVES (HIST_THREADS / LGBM_WAVE)
+#define HIST_GRID 256                   // chunks over all jobs of a launch (at most)
+#define HIST_SLOTS (HIST_GRID + SPEC_MAX)  // partial slots = blocks launched
+#define HIST_MIN_ROWS 4096              // rows per chunk (at least)
+#define HIST_WAVE_CELLS 1792            // wave-private scheme: 28 cells per lane
+#define HIST_FOLD_STEPS 7               // 7 x 64 rows <= 511 per 11-bit field
+#define HIST_ROWS_PER_LANE 2            // rows per lane in flight per step
+#define HIST_BLOCK_MAX_ROWS ((1 << 19) - 1)  // block-shared scheme field limit
 #define PART_THREADS 1024
 #define PART_WAVES (PART_THREADS / LGBM_WAVE)
 #define PART_ROWS_PER_THREAD 4
 #define PART_TILE (PART_THREADS * PART_ROWS_PER_THREAD)
 #define PART_MAX_BLOCKS 256
+#define PART_MIN_TILE 1024                // smallest tile of any partition launch shape
 #define SCAN_THREADS 128                // two waves: smaller leaf, larger leaf
 #define PLAN_THREADS 1024
 #define MAX_LEAVES 256                  // tree leaves per context (u8 leaf ids in the plan)
@@ -97,6 +103,14 @@ struct PartJob {
 #define SPEC_MAX 32        // partition jobs per round
 #define SPEC_DEFAULT 8
 
+// A histogram job: a physical row range of one row buffer.  nblk partial slots from
+// a0 hold its histogram after k_hist_jobs.
+struct HistJob {
+  int32_t buf, _pad;
+  int64_t begin, count;
+  int32_t a0, nblk;
+};
+
 struct Ctl {
   // ---- quantizer (per iteration) ----
   double gs, hs, igs, ihs;
@@ -108,9 +122,9 @@ struct Ctl {
   int32_t max_depth, n_slots, slot_cap, spec_max;
   int32_t n_jobs, n_reduce, rounds, root_skip;
   int64_t tile_total;
-  // ---- root / per-op histogram job ----
-  int32_t h_buf, _i1;
-  int64_t h_begin, h_count;
+  // ---- histogram jobs of the current launch ----
+  int32_t n_hjobs, _i1;
+  HistJob hjobs[SPEC_MAX];
   LeafSums sm;                       // per-op build: the leaf's raw sums
   // ---- partition round + look-back bookkeeping ----
   uint32_t epoch;

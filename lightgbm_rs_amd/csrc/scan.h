@@ -48,9 +48,11 @@ __device__ __forceinline__ uint32_t rec_byte(const uint4 (&w)[W], int f) {
   return (word >> (8 * (f & 3))) & 0xffu;
 }
 
-// Accumulate one row (packed quantized pair q) into the LDS histogram of all features.
+// Accumulate one row (packed quantized pair q) into the LDS histogram of all features:
+// every byte of record words 0 .. nw-1 (wave-uniform); cbr[f] is feature f's first
+// cell, with bytes beyond the last feature mapped to a trash cell.
 template <int W>
-__device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int32_t* cb, int F,
+__device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int32_t* cbr, int nw,
                                              const uint4 (&w)[W], uint32_t q) {
   const int32_t qg = (int32_t)(int8_t)(q & 0xffu);
   const int32_t qh = (int32_t)(int8_t)(q >> 8);
@@ -58,56 +60,18 @@ __device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int3
                                ((unsigned long long)(uint32_t)qh << 22) +
                                ((unsigned long long)(qh == 3 ? 1u : 0u) << 43);
 #pragma unroll
-  for (int wi = 0; wi < W; ++wi) {
-    const uint32_t ww[4] = {w[wi].x, w[wi].y, w[wi].z, w[wi].w};
+  for (int k = 0; k < 4 * W - 1; ++k) {
+    if (k < nw) {
+      const uint4 wd = w[k >> 2];
+      const uint32_t word = (k & 3) == 0 ? wd.x : ((k & 3) == 1 ? wd.y : ((k & 3) == 2 ? wd.z : wd.w));
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int f = wi * 16 + j;
-      if (f < F) {
-        const uint32_t bin = (ww[j >> 2] >> (8 * (j & 3))) & 0xffu;
-        __hip_atomic_fetch_add(&lds[cb[f] + bin], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
+      for (int bb = 0; bb < 4; ++bb)
+        __hip_atomic_fetch_add(&lds[cbr[4 * k + bb] + ((word >> (8 * bb)) & 0xffu)], v,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
 }
 
-// Flush a block's packed LDS histogram into the global [cells][3] integer cells.
-__device__ __forceinline__ void lds_hist_flush(const unsigned long long* lds, int cells,
-                                               int32_t* __restrict__ out) {
-  for (int c = threadIdx.x; c < cells; c += blockDim.x) {
-    const unsigned long long p = lds[c];
-    if (p == 0ull) continue;
-    const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
-    const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
-    const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
-    const int32_t hsum = (int32_t)(rest & ((1ull << 21) - 1));
-    const int32_t n3 = (int32_t)(rest >> 21);
-    int32_t* dst = out + (size_t)c * 3;
-    if (gsum) __hip_atomic_fetch_add(dst, (int32_t)gsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (hsum) __hip_atomic_fetch_add(dst + 1, hsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (n3) __hip_atomic_fetch_add(dst + 2, n3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
-// Flush a block's packed LDS histogram into `out` and clear it for the next job.
-// The caller has synchronised the block after the last accumulation.
-__device__ __forceinline__ void lds_hist_flush_clear(unsigned long long* lds, int cells,
-                                                     int32_t* __restrict__ out) {
-  for (int c = threadIdx.x; c < cells; c += blockDim.x) {
-    const unsigned long long p = lds[c];
-    if (p == 0ull) continue;
-    lds[c] = 0ull;
-    const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
-    const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
-    const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
-    const int32_t hsum = (int32_t)(rest & ((1ull << 21) - 1));
-    const int32_t n3 = (int32_t)(rest >> 21);
-    int32_t* dst = out + (size_t)c * 3;
-    if (gsum) __hip_atomic_fetch_add(dst, (int32_t)gsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (hsum) __hip_atomic_fetch_add(dst + 1, hsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (n3) __hip_atomic_fetch_add(dst + 2, n3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
 
 // ===========================================================================
 // FindBestThreshold for one (leaf, feature) by one wave: find_best_split_cpu_native
@@ -393,6 +357,118 @@ __device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* 
     }
   }
   __syncthreads();
+}
+
+// One DPP row-rotate of a 64-bit value (all 64 lanes active).
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo =
+      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Wave-wide maximum of an unsigned 64-bit value, uniform result.  Row rotations by
+// 1, 2, 4, 8 leave every lane of a 16-lane row holding the row maximum; the four
+// row maxima are then combined from lanes 0, 16, 32, 48.  Requires all 64 lanes
+// active.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  uint64_t t;
+  t = dpp_u64<0x121>(v);  // row_ror:1
+  v = t > v ? t : v;
+  t = dpp_u64<0x122>(v);  // row_ror:2
+  v = t > v ? t : v;
+  t = dpp_u64<0x124>(v);  // row_ror:4
+  v = t > v ? t : v;
+  t = dpp_u64<0x128>(v);  // row_ror:8
+  v = t > v ? t : v;
+  uint64_t m = readlane_u64(v, 0);
+  uint64_t a = readlane_u64(v, 16);
+  m = a > m ? a : m;
+  a = readlane_u64(v, 32);
+  m = a > m ? a : m;
+  a = readlane_u64(v, 48);
+  m = a > m ? a : m;
+  return m;
+}
+
+
+// Flush a block's packed LDS histogram into `out` and clear it for the next job.
+// `sole`: this block is the only one accumulating into `out`, which it then writes
+// with plain stores (every cell, zeros included) instead of atomics.  The caller has
+// synchronised the block after the last accumulation.
+__device__ __forceinline__ void lds_hist_flush_clear(unsigned long long* lds, int cells,
+                                                     int32_t* __restrict__ out, bool sole) {
+  for (int c = threadIdx.x; c < cells + 4; c += blockDim.x) {
+    const unsigned long long p = lds[c];
+    if (c >= cells) {  // trash cells
+      lds[c] = 0ull;
+      continue;
+    }
+    int32_t* dst = out + (size_t)c * 3;
+    if (p == 0ull) {
+      if (sole) {
+        dst[0] = 0;
+        dst[1] = 0;
+        dst[2] = 0;
+      }
+      continue;
+    }
+    lds[c] = 0ull;
+    const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
+    const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
+    const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
+    const int32_t hsum = (int32_t)(rest & ((1ull << 21) - 1));
+    const int32_t n3 = (int32_t)(rest >> 21);
+    if (sole) {
+      dst[0] = (int32_t)gsum;
+      dst[1] = hsum;
+      dst[2] = n3;
+      continue;
+    }
+    if (gsum) __hip_atomic_fetch_add(dst, (int32_t)gsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (hsum) __hip_atomic_fetch_add(dst + 1, hsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (n3) __hip_atomic_fetch_add(dst + 2, n3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Integer cells (sum q_g, sum q_h, #q_h==3) of cell ci of a histogram job: the sum
+// of its partial slots [a0, a0 + na), four slots per step with independent loads.
+__device__ __forceinline__ void hist_part_sum(const DevLearner& L, int32_t a0, int32_t na, size_t ci,
+                                              int32_t* G, int32_t* H, int32_t* T) {
+  const size_t stride = (size_t)L.total_cells * 3;
+  const int32_t* p = L.hist_part + (size_t)a0 * stride + ci * 3;
+  int32_t g = 0, h = 0, t = 0;
+  int32_t k = 0;
+  for (; k + 4 <= na; k += 4, p += 4 * stride) {
+    int32_t x[12];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      x[3 * u] = p[u * stride];
+      x[3 * u + 1] = p[u * stride + 1];
+      x[3 * u + 2] = p[u * stride + 2];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      g += x[3 * u];
+      h += x[3 * u + 1];
+      t += x[3 * u + 2];
+    }
+  }
+  for (; k < na; ++k, p += stride) {
+    g += p[0];
+    h += p[1];
+    t += p[2];
+  }
+  *G = g;
+  *H = h;
+  *T = t;
 }
 
 // Exact f64 histogram cells from the integer counters (sum q_g, sum q_h, #q_h==3).

@@ -392,3 +392,51 @@ def test_speculative_rounds_match_oracle(spec, rounds):
             assert tm["partition_jobs"] == t["num_leaves"] - 1
     finally:
         b.close()
+
+
+def test_tied_leaf_gains_break_by_leaf_id(be):
+    """Mirrored groups: rows of group B repeat the bins of group A except for a marker
+    feature and carry negated gradients (deterministic rounding keeps q(-g) = -q(g));
+    group C (marker bin 2) is unrelated, so every feature has a real gain at the root.
+    Once the marker splits off A, B and C, gains depend on G^2, so every leaf of A's
+    subtree has a twin in B's with a bit-identical gain and feature: the cross-leaf
+    ArgMax must break those ties by the lower leaf id, as the reference's sequential
+    strict-> scan does."""
+    na, nc_, F = 30_000, 20_000, 8
+    b0, meta0, ub0 = make_binned(na + nc_, F - 1, seed=41, missing_mix=False, mfb_mix=False)
+    n = 2 * na + nc_
+    bins = np.zeros((F, n), dtype=np.uint8)
+    bins[0, na:2 * na] = 1
+    bins[0, 2 * na:] = 2
+    bins[1:, :na] = b0[:, :na]
+    bins[1:, na:2 * na] = b0[:, :na]
+    bins[1:, 2 * na:] = b0[:, na:]
+    from lightgbm_rs_amd import feature_meta
+    meta = [feature_meta(3, real_index=0)]
+    for i, m in enumerate(meta0):
+        m.real_feature_index = i + 1
+        meta.append(m)
+    ub = np.concatenate([np.array([0.5, 1.5, 2.5]), ub0])
+    ga, ha, _ = binary_gh(na, seed=41)
+    # one sign per mirrored group (the marker splits first), and a signal on features
+    # 1 and 4 so that the twin subtrees keep splitting
+    ga = (np.abs(ga) * 0.3 + 0.01 + 0.6 * (b0[0, :na] > np.median(b0[0, :na]))
+          + 0.3 * (b0[3, :na] % 2)).astype(np.float32)
+    gc, hc, _ = binary_gh(nc_, seed=42)
+    g = np.concatenate([ga, -ga, gc]).astype(np.float32)
+    h = np.concatenate([ha, ha, hc]).astype(np.float32)
+    be.upload_resident_bins(bins, meta, ub)
+    be.upload_resident_grad_hess(g, h)
+    _, dg, dh = be.discretize_dequantize_in_place(4, False, 0, want_values=True)
+    og, oh, _, _ = oracle.quantize(g, h, bins=4, stochastic=False, seed=0)
+    assert np.array_equal(bits(dg), bits(og))
+    assert np.array_equal(dg[na:2 * na], -dg[:na])  # values: q = 0 dequantizes to +0.0
+    cfg = GainConfig.make(min_data_in_leaf=20)
+    t, lay = be.grow_tree_on_device_with_cfg(cfg, 63, -1)
+    o, olay = oracle.train_tree(bins, meta, ub, og, oh, cfg, 63, -1)
+    _compare_trees(t, o, "tied")
+    assert np.array_equal(lay["indices"], olay["indices"])
+    gains = t["split_gain"][: t["num_leaves"] - 1]
+    say(f"  leaves {t['num_leaves']}, splits {len(gains)}, distinct gains {len(np.unique(gains))}")
+    assert t["split_feature"][0] == 0
+    assert len(gains) - len(np.unique(gains)) >= 10, "expected twin splits with equal gains"
