@@ -44,11 +44,17 @@ struct lgbm_hip_ctx {
   double* d_ub = nullptr;
   uint4* rec[NBUF] = {};
   uint16_t* gh[NBUF] = {};
+  float2* g32[NBUF] = {};  // f32 (g, h) pairs, allocated on first f32-gradient use
+  int64_t g32_rows[NBUF] = {};
   int64_t buf_rows[NBUF] = {};
   float *g = nullptr, *h = nullptr, *label = nullptr;
   double* score = nullptr;
   int32_t* hist_part = nullptr;  // [HIST_SLOTS][cells][3]
   int32_t* hist_acc = nullptr;   // [SPEC_MAX][cells][3]
+  int64_t* hist_part64 = nullptr;  // [HIST_SLOTS][cells][2]
+  int64_t* int_slots64 = nullptr;  // [SLOT_CAP][cells][2]
+  int32_t n_fgroups = 0;
+  int32_t fgroup_first[MAX_FGROUPS + 1] = {};
   uint64_t* tile_state = nullptr;
   int64_t tile_cap = 0;
   uint64_t *wave_mats = nullptr, *lane_mats = nullptr;
@@ -77,10 +83,10 @@ struct lgbm_hip_ctx {
   int64_t indices_cap = 0;
   // captured per-tree launch sequence (all parameters live in device memory)
   hipGraphExec_t graph_exec = nullptr;
-  int32_t graph_nl = -1, graph_md = 0, graph_rounds = 0, graph_spec = 0;
+  int32_t graph_nl = -1, graph_md = 0, graph_rounds = 0, graph_spec = 0, graph_fp = -1;
   int32_t round_cap = 24;     // partition rounds in the captured sequence
   int32_t spec_max = SPEC_DEFAULT;
-  int32_t part_shape = 0, part_blocks = PART_MAX_BLOCKS;  // partition launch shape / grid
+  int32_t part_blocks = PART_MAX_BLOCKS;  // partition grid
   int32_t* done_host = nullptr;  // pinned: ctl->done after the captured rounds
   double tree_rounds = 0.0, trees = 0.0, extra_rounds = 0.0;
   uint64_t graph_gen = 0, buf_gen = 1;
@@ -185,6 +191,10 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.slot_len = c->slot_len;
   L.hist_part = c->hist_part;
   L.hist_acc = c->hist_acc;
+  L.hist_part64 = c->hist_part64;
+  L.int_slots64 = c->int_slots64;
+  L.n_fgroups = c->n_fgroups;
+  for (int i = 0; i <= MAX_FGROUPS; ++i) L.fgroup_first[i] = c->fgroup_first[i];
   L.slots = c->slots;
   L.feat_split = c->feat_split;
   L.best = c->best;
@@ -200,6 +210,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   for (int i = 0; i < NBUF; ++i) {
     L.bufs.rec[i] = c->rec[i];
     L.bufs.gh[i] = c->gh[i];
+    L.bufs.g32[i] = c->g32[i];
   }
   return L;
 }
@@ -225,6 +236,9 @@ int ensure_scratch_rows(lgbm_hip_ctx* c, int64_t n) {
     if (rc) return rc;
     rc = dalloc(c, &c->gh[b], (size_t)std::max<int64_t>(n, 1));
     if (rc) return rc;
+    rc = dalloc(c, &c->g32[b], (size_t)std::max<int64_t>(n, 1));
+    if (rc) return rc;
+    c->g32_rows[b] = n;
     c->buf_rows[b] = n;
     c->buf_gen++;
   }
@@ -265,6 +279,7 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   if ((rc = dalloc(c, &c->splittable, P * F))) return rc;
   if ((rc = dalloc(c, &c->best_fpos, P))) return rc;
   if ((rc = dalloc(c, &c->int_slots, P * c->total_cells * 3))) return rc;
+  if ((rc = dalloc(c, &c->int_slots64, P * c->total_cells * 2))) return rc;
   DevNodes& nd = c->nodes;
   if ((rc = dalloc(c, &nd.begin, P))) return rc;
   if ((rc = dalloc(c, &nd.count, P))) return rc;
@@ -314,6 +329,18 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   T.leaf_parent = (int32_t*)(base + c->tree_off[14]);
   c->lcap = L;
   c->buf_gen++;
+  return LGBM_HIP_OK;
+}
+
+// f32-gradient training: the (g, h) pair buffers that move with the rows.
+int ensure_fp(lgbm_hip_ctx* c) {
+  for (int b : {BUF_ORIG, BUF_A, BUF_B}) {
+    if (c->g32[b] && c->g32_rows[b] >= c->N) continue;
+    int rc = dalloc(c, &c->g32[b], (size_t)c->N);
+    if (rc) return rc;
+    c->g32_rows[b] = c->N;
+    c->buf_gen++;
+  }
   return LGBM_HIP_OK;
 }
 
@@ -401,34 +428,38 @@ int do_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_t seed
 // One partition round: plan (commit finished splits, pick the next leaves), the
 // partition pass of every picked leaf (which also builds one child's histogram), and
 // the children's scans.  Rounds after the tree is complete return at once.
-void enqueue_rounds(lgbm_hip_ctx* c, int32_t rounds) {
+void enqueue_rounds(lgbm_hip_ctx* c, int32_t rounds, int32_t fp) {
   DevLearner L = make_learner(c);
   KernelEvents ke;
   for (int32_t r = 0; r < rounds; ++r) {
-    launch_plan(L, SLOT_CAP(c->lcap), part_tile_of(c->part_shape), c->stream,
-                ev_kernel(c, FAM_SCAN, &ke));
-    launch_partition(L, c->W, c->part_shape, c->part_blocks, c->stream, ev_kernel(c, FAM_PART, &ke));
+    launch_plan(L, SLOT_CAP(c->lcap), c->stream, ev_kernel(c, FAM_SCAN, &ke));
+    launch_partition(L, c->W, fp, c->part_blocks, c->stream, ev_kernel(c, FAM_PART, &ke));
+    if (fp) launch_hist_f32(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
     launch_pair_scan(L, c->spec_max, c->stream, ev_kernel(c, FAM_SCAN, &ke));
   }
 }
 
 // The per-tree kernel sequence: reset, root histogram + root scan, then rounds.
-void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth, int32_t rounds) {
+void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth, int32_t rounds,
+                  int32_t fp) {
   DevLearner L = make_learner(c);
   KernelEvents ke;
   chain_start(c);
-  launch_tree_init(L, num_leaves, max_depth, SLOT_CAP(num_leaves), c->spec_max, c->stream,
+  launch_tree_init(L, num_leaves, max_depth, SLOT_CAP(num_leaves), c->spec_max, fp, c->stream,
                    ev_kernel(c, -1, &ke));
-  launch_hist(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
+  if (fp)
+    launch_hist_f32(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
+  else
+    launch_hist(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
   launch_fixscan(L, 1, nullptr, c->stream, ev_kernel(c, FAM_SCAN, &ke));
-  enqueue_rounds(c, rounds);
+  enqueue_rounds(c, rounds, fp);
 }
 
 // After the enqueued rounds: rounds commit at least one split each once the first
 // leaf is picked, so a tree needs at most num_leaves + 1 plans.  Runs further rounds
 // (checked after every chunk) until the plan reports the tree complete, then the
 // finalize kernel.
-int finish_rounds(lgbm_hip_ctx* c, int32_t num_leaves, int32_t rounds) {
+int finish_rounds(lgbm_hip_ctx* c, int32_t num_leaves, int32_t rounds, int32_t fp) {
   static_assert(offsetof(Ctl, rounds) - offsetof(Ctl, done) < 64, "ctl readback window");
   const size_t r_off = (offsetof(Ctl, rounds) - offsetof(Ctl, done)) / 4;
   int32_t done_rounds = rounds;
@@ -446,7 +477,7 @@ int finish_rounds(lgbm_hip_ctx* c, int32_t num_leaves, int32_t rounds) {
     if (done_rounds > num_leaves + 2)
       return set_err(c, LGBM_HIP_ERR_RUNTIME, "tree driver did not complete");
     const int32_t chunk = 4;
-    enqueue_rounds(c, chunk);
+    enqueue_rounds(c, chunk, fp);
     HIPCHK(c, hipGetLastError());
     done_rounds += chunk;
     c->extra_rounds += chunk;
@@ -458,27 +489,30 @@ int finish_rounds(lgbm_hip_ctx* c, int32_t num_leaves, int32_t rounds) {
   return LGBM_HIP_OK;
 }
 
+// One tree from the current gradients: fp = 0 quantized (lgbm_hip_quantize ran), 1 f32
+// (the packed pairs and fixed-point scales were prepared by launch_fp_prep).
 int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_leaves,
-                    int32_t max_depth) {
+                    int32_t max_depth, int32_t fp) {
   int rc = ensure_leaves(c, num_leaves);
   if (rc) return rc;
   HIPCHK(c, hipMemcpyAsync((char*)c->ctl + CTL_OFF(cfg), cfg, sizeof(*cfg), hipMemcpyHostToDevice,
                            c->stream));
   const int32_t rounds = std::max(1, std::min(c->round_cap, num_leaves + 1));
   if (c->timing || !c->use_graphs) {
-    enqueue_tree(c, num_leaves, max_depth, rounds);
+    enqueue_tree(c, num_leaves, max_depth, rounds, fp);
     HIPCHK(c, hipGetLastError());
-    return finish_rounds(c, num_leaves, rounds);
+    return finish_rounds(c, num_leaves, rounds, fp);
   }
   if (!(c->graph_exec && c->graph_nl == num_leaves && c->graph_md == max_depth &&
-        c->graph_gen == c->buf_gen && c->graph_rounds == rounds && c->graph_spec == c->spec_max)) {
+        c->graph_gen == c->buf_gen && c->graph_rounds == rounds && c->graph_spec == c->spec_max &&
+        c->graph_fp == fp)) {
     if (c->graph_exec) {
       (void)hipGraphExecDestroy(c->graph_exec);
       c->graph_exec = nullptr;
     }
     hipGraph_t g = nullptr;
     HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    enqueue_tree(c, num_leaves, max_depth, rounds);
+    enqueue_tree(c, num_leaves, max_depth, rounds, fp);
     HIPCHK(c, hipStreamEndCapture(c->stream, &g));
     hipError_t e = hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
@@ -491,9 +525,10 @@ int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_le
     c->graph_gen = c->buf_gen;
     c->graph_rounds = rounds;
     c->graph_spec = c->spec_max;
+    c->graph_fp = fp;
   }
   HIPCHK(c, hipGraphLaunch(c->graph_exec, c->stream));
-  return finish_rounds(c, num_leaves, rounds);
+  return finish_rounds(c, num_leaves, rounds, fp);
 }
 
 int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, double shrink) {
@@ -615,13 +650,6 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   if ((rc = dalloc(c, &c->partials, STAT_BLOCKS))) return fail(rc);
   if (const char* e = std::getenv("LGBM_HIP_GRAPHS")) c->use_graphs = std::strcmp(e, "0") != 0;
   if (const char* e = std::getenv("LGBM_HIP_ROUNDS")) c->round_cap = std::max(1, std::atoi(e));
-  if (const char* e = std::getenv("LGBM_HIP_PART")) {
-    int sh = 0, bl = PART_MAX_BLOCKS;
-    if (std::sscanf(e, "%d,%d", &sh, &bl) >= 1) {
-      c->part_shape = std::max(0, std::min(4, sh));
-      c->part_blocks = std::max(1, std::min(4096, bl));
-    }
-  }
   if (const char* e = std::getenv("LGBM_HIP_SPEC"))
     c->spec_max = std::max(1, std::min(SPEC_MAX, std::atoi(e)));
   *out = c;
@@ -642,6 +670,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   for (int i = 0; i < NBUF; ++i) {
     F(c->rec[i]);
     F(c->gh[i]);
+    F(c->g32[i]);
   }
   F(c->g);
   F(c->h);
@@ -649,6 +678,8 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->score);
   F(c->hist_part);
   F(c->hist_acc);
+  F(c->hist_part64);
+  F(c->int_slots64);
   F(c->tile_state);
   F(c->wave_mats);
   F(c->lane_mats);
@@ -737,6 +768,8 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   }
   if (acc > 8192)  // 8 B per LDS cell, 64 KiB of dynamic LDS per block
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "histogram exceeds the LDS budget");
+  if (acc > (uint32_t)(MAX_FGROUPS - 1) * (HIST_FP_CELLS - 256))
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "too many histogram cells for the f32 feature groups");
   if (acc > HIST_WAVE_CELLS && num_data > (int64_t)HIST_GRID * HIST_BLOCK_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "rows per histogram block exceed the packed LDS cell fields");
@@ -777,6 +810,23 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   if ((rc = dalloc(c, &c->g, (size_t)num_data))) return rc;
   if ((rc = dalloc(c, &c->h, (size_t)num_data))) return rc;
   if ((rc = dalloc(c, &c->hist_part, (size_t)HIST_SLOTS * acc * 3))) return rc;
+  if ((rc = dalloc(c, &c->hist_part64, (size_t)HIST_SLOTS * acc * 2))) return rc;
+  // feature groups of the f32 histogram kernel: consecutive features whose cells fit
+  // one block's LDS
+  {
+    int32_t ng = 0;
+    uint32_t gcells = 0;
+    c->fgroup_first[0] = 0;
+    for (int f = 0; f < F; ++f) {
+      if (f > 0 && gcells + feats[f].num_bin > HIST_FP_CELLS) {
+        c->fgroup_first[++ng] = f;
+        gcells = 0;
+      }
+      gcells += feats[f].num_bin;
+    }
+    c->fgroup_first[++ng] = F;
+    c->n_fgroups = ng;
+  }
   if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * acc * 3))) return rc;
   HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * acc * 3 * 4));
   if ((rc = ensure_tile_state(c, num_data))) return rc;
@@ -864,7 +914,8 @@ static int set_hist_job(lgbm_hip_ctx* c, const uint32_t* rows, int64_t n_rows) {
     if ((rc = ensure_scratch_bytes(c, (size_t)std::max<int64_t>(n_rows, 1) * 4))) return rc;
     HIPCHK(c, hipMemcpy(c->scratch, rows, (size_t)n_rows * 4, hipMemcpyHostToDevice));
     launch_gather_rows(c->W, (const uint32_t*)c->scratch, n_rows, c->rec[BUF_ORIG],
-                       c->gh[BUF_ORIG], c->rec[BUF_S0], c->gh[BUF_S0], c->stream);
+                       c->gh[BUF_ORIG], c->g32[BUF_ORIG], c->rec[BUF_S0], c->gh[BUF_S0],
+                       c->g32[BUF_S0], c->stream);
     buf = BUF_S0;
     count = n_rows;
   }
@@ -909,17 +960,29 @@ int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, in
                                   double sum_gradient, double sum_hessian, double* out) {
   int rc = check_ctx(c);
   if (rc) return rc;
-  if (!c->quant_ready) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize first");
-  if (c->quant_bins != 2 && c->quant_bins != 4)
+  // quantized gradients (after lgbm_hip_quantize) or the f32 gradients as uploaded
+  const int32_t fp = c->quant_ready ? 0 : 1;
+  if (fp && !c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set gradients first");
+  if (!fp && c->quant_bins != 2 && c->quant_bins != 4)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "exact f64 histogram requires num_grad_quant_bins in {2, 4}");
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  DevLearner L0 = make_learner(c);
+  if (fp) {
+    if ((rc = ensure_fp(c))) return rc;
+    L0 = make_learner(c);
+    launch_fp_prep(L0, c->g, c->h, c->N, c->partials, c->stream);
+  }
   if ((rc = set_hist_job(c, leaf_rows, n_rows))) return rc;
   LeafSums s{sum_gradient, sum_hessian, 0.0, (int32_t)(leaf_rows ? n_rows : c->N), 0};
   if ((rc = ctl_write(c, CTL_OFF(sm), s))) return rc;
+  if ((rc = ctl_write(c, CTL_OFF(fp_mode), fp))) return rc;
   if ((rc = dalloc(c, &c->slot_tmp, (size_t)c->slot_len))) return rc;
   DevLearner L = make_learner(c);
-  launch_hist(L, c->stream);
+  if (fp)
+    launch_hist_f32(L, c->stream);
+  else
+    launch_hist(L, c->stream);
   launch_fixscan(L, 2, c->slot_tmp, c->stream);
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -1018,8 +1081,7 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   J.parent = -1;
   J.cl = -1;
   J.cr = -1;
-  const int32_t tile = part_tile_of(c->part_shape);
-  J.ntiles = (int32_t)((n + tile - 1) / tile);
+  J.ntiles = (int32_t)((n + PART_TILE - 1) / PART_TILE);
   J.tile0 = 0;
   J.src_buf = BUF_S0;
   J.dst_buf = BUF_S1;
@@ -1047,7 +1109,7 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   if ((rc = ctl_write(c, CTL_OFF(tile_total), tiles))) return rc;
   DevLearner L = make_learner(c);
   L.W = 1;
-  launch_partition(L, 1, c->part_shape, std::min<int64_t>(c->part_blocks, J.ntiles), c->stream);
+  launch_partition(L, 1, 0, std::min<int64_t>(c->part_blocks, J.ntiles), c->stream);
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));
   int32_t lc = 0;
@@ -1069,11 +1131,19 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num
   if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
   if (num_leaves < 1) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_leaves must be >= 1");
   if (num_leaves > 256) return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_leaves must be <= 256");
-  if (!c->quant_ready) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize gradients first");
-  if (c->quant_bins != 2 && c->quant_bins != 4)
+  // quantized gradients (after lgbm_hip_quantize) or the f32 gradients as uploaded
+  const int32_t fp = c->quant_ready ? 0 : 1;
+  if (fp && !c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set gradients first");
+  if (!fp && c->quant_bins != 2 && c->quant_bins != 4)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "device learner requires num_grad_quant_bins in {2, 4}");
-  if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth))) return rc;
+  if (fp) {
+    if ((rc = ensure_fp(c))) return rc;
+    if ((rc = ensure_leaves(c, num_leaves))) return rc;
+    DevLearner L = make_learner(c);
+    launch_fp_prep(L, c->g, c->h, c->N, c->partials, c->stream);
+  }
+  if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
   return finish_tree(c, tree, layout, 1.0);
 }
 
@@ -1102,23 +1172,37 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
   if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
   if (num_leaves < 1 || num_leaves > 256)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_leaves must be in 1..=256");
-  if (num_grad_quant_bins != 2 && num_grad_quant_bins != 4)
+  // num_grad_quant_bins = 0: use_quantized_grad = false (f32 gradients)
+  const int32_t fp = num_grad_quant_bins == 0 ? 1 : 0;
+  if (!fp && num_grad_quant_bins != 2 && num_grad_quant_bins != 4)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
-                   "device learner requires num_grad_quant_bins in {2, 4}");
+                   "device learner requires num_grad_quant_bins in {0, 2, 4}");
+  if (fp) {
+    if ((rc = ensure_fp(c))) return rc;
+    if ((rc = ensure_leaves(c, num_leaves))) return rc;
+  }
   ev_begin(c, FAM_OBJ);
   launch_grad_binary(c->score, c->label, c->g, c->h, c->N, c->partials, c->stream);
   ev_end(c);
   c->have_grad = true;
-  const uint64_t seed = ((uint64_t)(uint32_t)iter << 20) ^ 0ull ^ 0x51702010ull;  // gbdt.rs:950
-  ev_begin(c, FAM_QUANT);
-  launch_quant_scales(c->ctl, c->partials, c->N, num_grad_quant_bins, -1, c->stream);
-  launch_quantize(c->g, c->h, c->N, c->ctl, c->wave_mats, c->lane_mats,
-                  seed ^ 0x9E3779B97F4A7C15ull, stochastic, c->gh[BUF_ORIG], nullptr, nullptr,
-                  c->stream);
-  ev_end(c);
-  c->quant_ready = true;
-  c->quant_bins = num_grad_quant_bins;
-  if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth))) return rc;
+  if (fp) {
+    ev_begin(c, FAM_QUANT);
+    DevLearner L0 = make_learner(c);
+    launch_fp_prep(L0, c->g, c->h, c->N, c->partials, c->stream);
+    ev_end(c);
+    c->quant_ready = false;
+  } else {
+    const uint64_t seed = ((uint64_t)(uint32_t)iter << 20) ^ 0ull ^ 0x51702010ull;  // gbdt.rs:950
+    ev_begin(c, FAM_QUANT);
+    launch_quant_scales(c->ctl, c->partials, c->N, num_grad_quant_bins, -1, c->stream);
+    launch_quantize(c->g, c->h, c->N, c->ctl, c->wave_mats, c->lane_mats,
+                    seed ^ 0x9E3779B97F4A7C15ull, stochastic, c->gh[BUF_ORIG], nullptr, nullptr,
+                    c->stream);
+    ev_end(c);
+    c->quant_ready = true;
+    c->quant_bins = num_grad_quant_bins;
+  }
+  if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
   DevLearner L = make_learner(c);
   KernelEvents ke;
   launch_score_update(L, learning_rate, c->score, c->stream, ev_kernel(c, FAM_OBJ, &ke));

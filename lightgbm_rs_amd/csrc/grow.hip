@@ -68,7 +68,7 @@ __device__ __forceinline__ void router_of(const DevFeature& ft, const lgbm_split
 // per-tree reset
 // ===========================================================================
 __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth, int32_t slot_cap,
-                            int32_t spec_max) {
+                            int32_t spec_max, int32_t fp_mode) {
   Ctl* ctl = L.ctl;
   const int tid = blockIdx.x * blockDim.x + threadIdx.x;
   const int nthr = gridDim.x * blockDim.x;
@@ -84,6 +84,7 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
     ctl->n_slots = 1;
     ctl->slot_cap = slot_cap;
     ctl->spec_max = spec_max;
+    ctl->fp_mode = fp_mode;
     ctl->n_jobs = 0;
     ctl->rounds = 0;
     ctl->tile_total = 0;
@@ -182,8 +183,7 @@ __device__ __forceinline__ int32_t plan_argmax(const double (&kg)[PL], const int
   return wave_best(lb).idx;
 }
 
-__global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slot_cap,
-                                                       int32_t part_tile) {
+__global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slot_cap) {
   __shared__ double s_gain[SLOT_CAP(MAX_LEAVES)];
   __shared__ int32_t s_feat[SLOT_CAP(MAX_LEAVES)];
   __shared__ int32_t s_fpos[SLOT_CAP(MAX_LEAVES)];
@@ -210,6 +210,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   const int32_t cdone = ctl->done;
   const int32_t nl0 = ctl->num_leaves, ns0 = ctl->n_slots, maxl = ctl->max_leaves;
   const int32_t nred = ctl->n_reduce, spec = ctl->spec_max, cerr = ctl->error;
+  const bool fp = ctl->fp_mode != 0;
   if (tid < 2 * SPEC_MAX + 2) s_red[tid] = ctl->reduce_list[tid];
   for (int f = tid; f < F; f += PLAN_THREADS) s_ft[f] = L.feats[f];
   for (int s = tid; s < slot_cap; s += PLAN_THREADS) {
@@ -415,9 +416,10 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     router_of(ft, b, &J.pmin, &J.th, &J.flags);
     J.max_bin = (int32_t)ft.max_bin;
     J.na_bin = (int32_t)ft.num_bin - 1;
-    // build the histogram of the side the scan expects to be smaller
-    J.acc_right = b.right_count < b.left_count ? 1 : 0;
-    J.ntiles = (int32_t)((J.count + part_tile - 1) / part_tile);
+    // quantized gradients: build the histogram of the side the scan expects to be
+    // smaller inside the partition pass (f32: k_hist_f32 builds the smaller child)
+    J.acc_right = fp ? -1 : (b.right_count < b.left_count ? 1 : 0);
+    J.ntiles = (int32_t)((J.count + PART_TILE - 1) / PART_TILE);
     J.tile0 = 0;
     ctl->jobs[j] = J;
     s_ntiles[j] = J.ntiles;
@@ -451,6 +453,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     }
     ctl->tile_total = acc;
     ctl->n_jobs = nj;
+    if (fp) ctl->n_hjobs = nj;  // k_partition fills in each job's smaller child
     ctl->n_reduce = 2 * nj;
     ctl->num_leaves = nl;
     ctl->n_slots = s_nslots;
@@ -476,14 +479,18 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
 // needed in advance.  Look-back words: epoch(30) | flag(2) | value(32).  The launcher
 // of a round (k_plan, or the host for the per-op entry point) resets the ticket
 // counter and moves to a fresh epoch, so stale words of earlier rounds never match.
-// In the tree driver the pass also builds one child's integer histogram per job (the
-// side the scan predicts to be smaller) from the rows while they are in registers;
-// the other child's is parent - built in integers (k_pair_scan).
+// Quantized gradients (FP = 0): in the tree driver the pass also builds one child's
+// integer histogram per job (the side the scan predicts to be smaller) from the rows
+// while they are in registers; the other child's is parent - built in integers
+// (k_pair_scan).  f32 gradients (FP = 1) move as (g, h) pairs; the smaller child's
+// histogram is built afterwards by k_hist_f32.
 // ===========================================================================
-template <int W, int PT, int PR>
-__global__ __launch_bounds__(PT) void k_partition(DevLearner L) {
+template <int W, int FP>
+__global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
+  constexpr int PT = PART_THREADS, PR = PART_ROWS_PER_THREAD;
   constexpr int kWaves = PT / LGBM_WAVE;
   constexpr int kTile = PT * PR;
+  using GhT = typename std::conditional<FP != 0, float2, uint16_t>::type;
   extern __shared__ unsigned long long lds_hist[];
   __shared__ int32_t cb[16 * LGBM_MAX_W];
   __shared__ PartJob s_jobs[SPEC_MAX];
@@ -500,7 +507,8 @@ __global__ __launch_bounds__(PT) void k_partition(DevLearner L) {
   if (tid < SPEC_MAX) s_jobs[tid] = ctl->jobs[tid];
   if (nj <= 0 || total <= 0 || (int64_t)blockIdx.x >= total) return;
   const int F = L.F, cells = L.total_cells, nw = (F + 3) / 4;
-  for (int c = tid; c < cells + 4; c += PT) lds_hist[c] = 0ull;
+  if constexpr (FP == 0)
+    for (int c = tid; c < cells + 4; c += PT) lds_hist[c] = 0ull;
   for (int f = tid; f < 16 * W; f += PT) cb[f] = f < F ? (int32_t)L.feats[f].cell_base : cells;
   __syncthreads();
   // feature cell bases in scalar registers (bytes beyond F map to the trash cell)
@@ -518,7 +526,7 @@ __global__ __launch_bounds__(PT) void k_partition(DevLearner L) {
     if (t >= total) break;
     int32_t j = 0;
     while (j + 1 < nj && s_jobs[j + 1].tile0 <= t) ++j;
-    if (j != cur) {
+    if (FP == 0 && j != cur) {
       if (cur >= 0 && s_jobs[cur].acc_right >= 0) {
         lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3,
                              s_jobs[cur].ntiles == 1);
@@ -531,11 +539,11 @@ __global__ __launch_bounds__(PT) void k_partition(DevLearner L) {
     const int64_t lt = t - J.tile0;
     const int64_t base = lt * kTile;
     const uint4* __restrict__ src = L.bufs.rec[J.src_buf];
-    const uint16_t* __restrict__ sgh = L.bufs.gh[J.src_buf];
+    const GhT* __restrict__ sgh = gh_buf<GhT>(L.bufs, J.src_buf);
     uint4* __restrict__ dst = L.bufs.rec[J.dst_buf];
-    uint16_t* __restrict__ dgh = L.bufs.gh[J.dst_buf];
+    GhT* __restrict__ dgh = gh_buf<GhT>(L.bufs, J.dst_buf);
     uint4 w[PR][W];
-    uint16_t q[PR];
+    GhT q[PR];
     bool isleft[PR], valid[PR];
     int32_t rank[PR];
 #pragma unroll
@@ -623,11 +631,12 @@ __global__ __launch_bounds__(PT) void k_partition(DevLearner L) {
       for (int i = 0; i < W; ++i) dst[d * W + i] = w[k][i];
       dgh[d] = q[k];
     }
-    if (J.acc_right >= 0) {
+    if (FP == 0 && J.acc_right >= 0) {
       const bool want_left = J.acc_right == 0;
 #pragma unroll
       for (int k = 0; k < PR; ++k)
-        if (valid[k] && isleft[k] == want_left) lds_hist_add<W>(lds_hist, cbr, nw, w[k], q[k]);
+        if (valid[k] && isleft[k] == want_left)
+          lds_hist_add<W>(lds_hist, cbr, nw, w[k], gh_bits(q[k]));
     }
     if (lt == J.ntiles - 1 && tid == 0) {
       const int32_t lc = (int32_t)(excl + s_total);
@@ -644,6 +653,22 @@ __global__ __launch_bounds__(PT) void k_partition(DevLearner L) {
         nd.rev[J.cr] = 1;
         nd.sums[J.cl].n = lc;
         nd.sums[J.cr].n = rc;
+        if (FP) {
+          // the round's ConstructHistogram job (k_hist_f32 runs next): the smaller
+          // child (partition counts; a tie makes the right child the smaller one,
+          // learner.rs:4061-4089), none for a gated pair (before_find_best_split,
+          // learner.rs:1808-1839)
+          const int32_t md = ctl->max_depth, min2 = ctl->cfg.min_data_in_leaf * 2;
+          const bool gated = (md > 0 && nd.depth[J.cl] >= md) || (lc < min2 && rc < min2);
+          HistJob hj;
+          hj.buf = J.dst_buf;
+          hj._pad = 0;
+          hj.begin = lc < rc ? begin : begin + lc;
+          hj.count = gated ? 0 : (lc < rc ? lc : rc);
+          hj.a0 = 0;
+          hj.nblk = 0;
+          ctl->hjobs[j] = hj;
+        }
         atomicAdd(&L.stats[0], (double)count);
         atomicAdd(&L.stats[4], 1.0);
       } else {
@@ -651,7 +676,7 @@ __global__ __launch_bounds__(PT) void k_partition(DevLearner L) {
       }
     }
   }
-  if (cur >= 0 && s_jobs[cur].acc_right >= 0)
+  if (FP == 0 && cur >= 0 && s_jobs[cur].acc_right >= 0)
     lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3,
                          s_jobs[cur].ntiles == 1);
 }
@@ -686,8 +711,31 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L) {
   const bool right_small = !(lcnt < rcnt);
   const int32_t sm = right_small ? cr : cl, lg = right_small ? cl : cr;
   const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
+  if (ctl->fp_mode) {
+    // f32 gradients: the smaller child from its k_hist_f32 partial slots; the larger =
+    // parent - smaller, exact in 64-bit fixed point
+    const int32_t a0 = ctl->hjobs[j].a0, na = ctl->hjobs[j].nblk;
+    const double gu = ldexp(1.0, -ctl->g_shift), hu = ldexp(1.0, -ctl->h_shift);
+    if (!gated) {
+      for (int b = tid; b < nb; b += SCAN_THREADS) {
+        const size_t ci = (size_t)(ft.cell_base + b);
+        long long SG, SH;
+        hist_part_sum64(L, a0, na, ci, &SG, &SH);
+        const int64_t* ps = L.int_slots64 + ((size_t)p * cells + ci) * 2;
+        int64_t* ss = L.int_slots64 + ((size_t)sm * cells + ci) * 2;
+        int64_t* gs_ = L.int_slots64 + ((size_t)lg * cells + ci) * 2;
+        ss[0] = SG;
+        ss[1] = SH;
+        gs_[0] = ps[0] - SG;
+        gs_[1] = ps[1] - SH;
+        cs[2 * b] = (double)SG * gu;
+        cs[2 * b + 1] = (double)SH * hu;
+      }
+    }
+  }
   int32_t* acc = L.hist_acc + (size_t)j * cells * 3;
-  for (int b = tid; b < nb; b += SCAN_THREADS) {
+  const int nbq = ctl->fp_mode ? 0 : nb;  // quantized gradients only
+  for (int b = tid; b < nbq; b += SCAN_THREADS) {
     const size_t ci = (size_t)(ft.cell_base + b);
     int32_t* a = acc + ci * 3;
     const int32_t AG = a[0], AH = a[1], AT = a[2];  // the side built in the partition pass
@@ -813,39 +861,23 @@ __global__ void k_export_layout(DevLearner L, uint32_t* __restrict__ indices) {
 // launchers
 // ===========================================================================
 void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, int32_t slot_cap,
-                      int32_t spec_max, hipStream_t s, const KernelEvents* ev) {
-  KLAUNCH(ev, k_tree_init, dim3(16), dim3(256), 0, s, L, max_leaves, max_depth, slot_cap, spec_max);
+                      int32_t spec_max, int32_t fp_mode, hipStream_t s, const KernelEvents* ev) {
+  KLAUNCH(ev, k_tree_init, dim3(16), dim3(256), 0, s, L, max_leaves, max_depth, slot_cap, spec_max,
+          fp_mode);
 }
-void launch_plan(const DevLearner& L, int32_t slot_cap, int32_t part_tile, hipStream_t s,
-                 const KernelEvents* ev) {
-  KLAUNCH(ev, k_plan, dim3(1), dim3(PLAN_THREADS), 0, s, L, slot_cap, part_tile);
+void launch_plan(const DevLearner& L, int32_t slot_cap, hipStream_t s, const KernelEvents* ev) {
+  KLAUNCH(ev, k_plan, dim3(1), dim3(PLAN_THREADS), 0, s, L, slot_cap);
 }
-// Partition launch shapes: (threads, rows per thread); the tile is their product.
-int part_tile_of(int shape) {
-  static const int t[5][2] = {{1024, 4}, {512, 4}, {512, 2}, {256, 4}, {256, 8}};
-  return t[shape][0] * t[shape][1];
-}
-void launch_partition(const DevLearner& L, int W, int shape, int64_t blocks, hipStream_t s,
+void launch_partition(const DevLearner& L, int W, int fp, int64_t blocks, hipStream_t s,
                       const KernelEvents* ev) {
   if (blocks < 1) blocks = 1;
-  const size_t lds = (size_t)(std::max(L.total_cells, 1) + 4) * sizeof(unsigned long long);
-  const dim3 g((unsigned)blocks);
-#define PART_SHAPES(kW)                                                                    \
-  switch (shape) {                                                                         \
-    case 1: KLAUNCH(ev, (k_partition<kW, 512, 4>), g, dim3(512), lds, s, L); break;        \
-    case 2: KLAUNCH(ev, (k_partition<kW, 512, 2>), g, dim3(512), lds, s, L); break;        \
-    case 3: KLAUNCH(ev, (k_partition<kW, 256, 4>), g, dim3(256), lds, s, L); break;        \
-    case 4: KLAUNCH(ev, (k_partition<kW, 256, 8>), g, dim3(256), lds, s, L); break;        \
-    default: KLAUNCH(ev, (k_partition<kW, 1024, 4>), g, dim3(1024), lds, s, L); break;     \
+  const dim3 g((unsigned)blocks), b(PART_THREADS);
+  if (fp) {
+    DISPATCH_W(W, KLAUNCH(ev, (k_partition<kW, 1>), g, b, 0, s, L));
+  } else {
+    const size_t lds = (size_t)(std::max(L.total_cells, 1) + 4) * sizeof(unsigned long long);
+    DISPATCH_W(W, KLAUNCH(ev, (k_partition<kW, 0>), g, b, lds, s, L));
   }
-  switch (W) {
-    case 1: { PART_SHAPES(1) } break;
-    case 2: { PART_SHAPES(2) } break;
-    default:
-      DISPATCH_W(W, KLAUNCH(ev, (k_partition<kW, 1024, 4>), g, dim3(1024), lds, s, L));
-      break;
-  }
-#undef PART_SHAPES
 }
 void launch_pair_scan(const DevLearner& L, int32_t spec_max, hipStream_t s,
                       const KernelEvents* ev) {

@@ -24,8 +24,18 @@
 
 struct RowBufs {
   uint4* rec[NBUF];
-  uint16_t* gh[NBUF];
+  uint16_t* gh[NBUF];   // packed quantized (q_g, q_h) per row
+  float2* g32[NBUF];    // f32 (g, h) per row (non-quantized training)
 };
+
+template <typename T>
+__device__ __forceinline__ T* gh_buf(const RowBufs& b, int i);
+template <>
+__device__ __forceinline__ uint16_t* gh_buf<uint16_t>(const RowBufs& b, int i) { return b.gh[i]; }
+template <>
+__device__ __forceinline__ float2* gh_buf<float2>(const RowBufs& b, int i) { return b.g32[i]; }
+__device__ __forceinline__ uint32_t gh_bits(uint16_t q) { return q; }
+__device__ __forceinline__ uint32_t gh_bits(float2) { return 0u; }
 
 // Per-leaf-id partition ranges, filled by k_tree_finalize for the layout export.
 struct DevLeaves {
@@ -84,6 +94,11 @@ struct DevLearner {
   uint64_t slot_len;
   int32_t* hist_part;         // [HIST_SLOTS][total_cells][3] root / per-op partials
   int32_t* hist_acc;          // [SPEC_MAX][total_cells][3] per-job accumulators
+  // f32-gradient training: 64-bit fixed-point (g, h) cells
+  int64_t* hist_part64;       // [HIST_SLOTS][total_cells][2]
+  int64_t* int_slots64;       // [slot_cap][total_cells][2]
+  int32_t n_fgroups;          // feature groups of k_hist_f32 (cells of a group fit LDS)
+  int32_t fgroup_first[MAX_FGROUPS + 1];
   int32_t* int_slots;         // [slot_cap][total_cells][3] per-node integer histograms
   double* slots;              // [slot_cap][slot_len] per-node f64 histograms
   lgbm_split_info* feat_split;  // [slot_cap][F]
@@ -121,18 +136,20 @@ void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,
 void launch_hist(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
 void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s,
                     const KernelEvents* ev = nullptr);
-void launch_plan(const DevLearner& L, int32_t slot_cap, int32_t part_tile, hipStream_t s,
+void launch_plan(const DevLearner& L, int32_t slot_cap, hipStream_t s,
                  const KernelEvents* ev = nullptr);
 void launch_pair_scan(const DevLearner& L, int32_t spec_max, hipStream_t s,
                       const KernelEvents* ev = nullptr);
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,
                           lgbm_split_info* out, hipStream_t s);
-int part_tile_of(int shape);
-void launch_partition(const DevLearner& L, int W, int shape, int64_t blocks, hipStream_t s,
+void launch_partition(const DevLearner& L, int W, int fp, int64_t blocks, hipStream_t s,
                       const KernelEvents* ev = nullptr);
+void launch_hist_f32(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
+void launch_fp_prep(const DevLearner& L, const float* g, const float* h, int64_t n,
+                    const uint4* partials, hipStream_t s);
 void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth,
-                      int32_t slot_cap, int32_t spec_max, hipStream_t s,
+                      int32_t slot_cap, int32_t spec_max, int32_t fp_mode, hipStream_t s,
                       const KernelEvents* ev = nullptr);
 void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s,
                          const KernelEvents* ev = nullptr);
@@ -140,7 +157,8 @@ void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents
 void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
                           hipStream_t s);
 void launch_gather_rows(int W, const uint32_t* rows, int64_t n, const uint4* rec,
-                        const uint16_t* gh, uint4* rec_out, uint16_t* gh_out, hipStream_t s);
+                        const uint16_t* gh, const float2* g32, uint4* rec_out, uint16_t* gh_out,
+                        float2* g32_out, hipStream_t s);
 void launch_subtract(const double* a, const double* b, int64_t n, double* out, hipStream_t s);
 void launch_pack_partition(const uint32_t* bins, int64_t n, uint4* rec, hipStream_t s);
 }  // namespace lgbm

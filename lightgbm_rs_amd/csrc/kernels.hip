@@ -165,6 +165,53 @@ __global__ __launch_bounds__(256) void k_quant_scales(Ctl* ctl, const uint4* __r
 }
 
 // ===========================================================================
+// f32 gradients (use_quantized_grad = false): 64-bit fixed-point histogram scales.
+// A row's g becomes the integer round(g * 2^g_shift) (h likewise).  With |g| <= 2^e
+// and fewer than 2^b rows, g_shift = 62 - b - e keeps every partial sum below 2^62,
+// so cells, leaf totals and parent - child differences are exact integers, and the
+// f64 cell (double)sum * 2^-g_shift is within one rounding of the exact sum of the
+// f32 values — far inside the 1e-5 relative parity bound of the f64 fold.
+// ===========================================================================
+__device__ __forceinline__ int32_t fp_shift(float amax, int64_t n) {
+  int b = 1;
+  while ((1ll << b) <= n) ++b;
+  if (!(amax > 0.0f) || !(amax < __builtin_inff())) return 62 - b;
+  int e = 0;
+  (void)frexpf(amax, &e);  // amax < 2^e
+  return 62 - b - e;
+}
+
+__global__ __launch_bounds__(256) void k_fp_scales(Ctl* ctl, const uint4* __restrict__ partials,
+                                                   int32_t nparts, int64_t n) {
+  GhStat s{0u, 0u, 0xffffffffu, 0u};
+  for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+    const uint4 p = partials[i];
+    stat_merge(s, GhStat{p.x, p.y, p.z, p.w});
+  }
+  __shared__ GhStat sh[4];
+  for (int off = 32; off >= 1; off >>= 1) {
+    GhStat o;
+    o.ag = (uint32_t)__shfl_xor((int)s.ag, off);
+    o.ah = (uint32_t)__shfl_xor((int)s.ah, off);
+    o.hmin = (uint32_t)__shfl_xor((int)s.hmin, off);
+    o.hmax = (uint32_t)__shfl_xor((int)s.hmax, off);
+    stat_merge(s, o);
+  }
+  if (lane_id() == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) stat_merge(s, sh[w]);
+  ctl->g_shift = fp_shift(__uint_as_float(s.ag), n);
+  ctl->h_shift = fp_shift(__uint_as_float(s.ah), n);
+}
+
+__global__ void k_pack_g32(const float* __restrict__ g, const float* __restrict__ h, int64_t n,
+                           float2* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = make_float2(g[i], h[i]);
+}
+
+// ===========================================================================
 // quantize: discretize_dequantize_in_place (gradient_discretizer.rs:126-139,
 // quantize_pair :173-188, next_u01 :255-263).  Row r consumes xorshift draws
 // 2r+1 (grad) and 2r+2 (hess) of the sequential stream; a lane starts at row
@@ -446,6 +493,67 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
   }
 }
 
+// f32 gradients: ConstructHistogram of the histogram jobs into 64-bit fixed-point
+// (g, h) cells with 64-bit LDS atomics (exact, order-independent).  Block (chunk a,
+// feature group y): the rows of chunk a (hist_assign) and the features of group y,
+// whose cells fit LDS; partial slot a receives the group's cells.
+template <int W>
+__global__ __launch_bounds__(HIST_THREADS) void k_hist_f32(DevLearner L) {
+  extern __shared__ unsigned long long lds64[];
+  __shared__ int32_t cb[16 * LGBM_MAX_W];
+  __shared__ int32_t s_a0[SPEC_MAX], s_nb[SPEC_MAX];
+  __shared__ int64_t s_R;
+  Ctl* ctl = L.ctl;
+  const int32_t nj = ctl->n_hjobs;
+  const int grp = blockIdx.y;
+  if (nj <= 0 || grp >= L.n_fgroups) return;
+  const int tid = threadIdx.x;
+  const int cells = L.total_cells;
+  const int f0 = L.fgroup_first[grp], f1 = L.fgroup_first[grp + 1];
+  if (tid == 0) {
+    hist_assign(ctl, nj, s_a0, s_nb, &s_R);
+    if (blockIdx.x == 0 && grp == 0)
+      for (int j = 0; j < nj; ++j) {
+        ctl->hjobs[j].a0 = s_a0[j];
+        ctl->hjobs[j].nblk = s_nb[j];
+      }
+  }
+  for (int f = f0 + tid; f < f1; f += HIST_THREADS) cb[f] = (int32_t)L.feats[f].cell_base;
+  __syncthreads();
+  const int32_t a = (int32_t)blockIdx.x;
+  int32_t j = -1;
+  for (int k = 0; k < nj; ++k)
+    if (a >= s_a0[k] && a < s_a0[k] + s_nb[k]) j = k;
+  if (j < 0) return;
+  const int cbase = cb[f0];
+  const int gcells = (f1 < L.F ? (int)L.feats[f1].cell_base : cells) - cbase;
+  for (int c = tid; c < 2 * gcells; c += HIST_THREADS) lds64[c] = 0ull;
+  __syncthreads();
+  const HistJob& J = ctl->hjobs[j];
+  const int64_t R = s_R;
+  const int64_t lo = (int64_t)(a - s_a0[j]) * R;
+  const int64_t hi = min(J.count, lo + R);
+  const uint4* __restrict__ rec = L.bufs.rec[J.buf] + J.begin * W;
+  const float2* __restrict__ gh = L.bufs.g32[J.buf] + J.begin;
+  const double gm = ldexp(1.0, ctl->g_shift), hm = ldexp(1.0, ctl->h_shift);
+  for (int64_t r = lo + tid; r < hi; r += HIST_THREADS) {
+    uint4 w[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[i] = rec[r * W + i];
+    const float2 v = gh[r];
+    const unsigned long long gi = (unsigned long long)(long long)rint((double)v.x * gm);
+    const unsigned long long hi_ = (unsigned long long)(long long)rint((double)v.y * hm);
+    for (int f = f0; f < f1; ++f) {
+      const int c = cb[f] - cbase + (int)rec_byte(w, f);
+      __hip_atomic_fetch_add(&lds64[2 * c], gi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_fetch_add(&lds64[2 * c + 1], hi_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+  __syncthreads();
+  int64_t* out = L.hist_part64 + ((size_t)a * cells + cbase) * 2;
+  for (int c = tid; c < 2 * gcells; c += HIST_THREADS) out[c] = (int64_t)lds64[c];
+}
+
 // ===========================================================================
 // k_fixscan: one block (two waves) per feature.
 //   mode 1 (root):  node slot 0 from the histogram of all rows: root LeafSplits sums
@@ -467,8 +575,24 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
   const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
   long long tg = 0, th = 0, t3 = 0;
   const int32_t a0 = ctl->hjobs[0].a0, na = ctl->hjobs[0].nblk;
+  const bool fp = ctl->fp_mode != 0;
+  const double gu = ldexp(1.0, -ctl->g_shift), hu = ldexp(1.0, -ctl->h_shift);
   for (int b = tid; b < nb; b += SCAN_THREADS) {
     const size_t ci = (size_t)(ft.cell_base + b);
+    if (fp) {
+      long long G = 0, H = 0;
+      hist_part_sum64(L, a0, na, ci, &G, &H);
+      if (mode == 1) {
+        int64_t* ps = L.int_slots64 + ci * 2;  // node slot 0
+        ps[0] = G;
+        ps[1] = H;
+      }
+      cs[2 * b] = (double)G * gu;
+      cs[2 * b + 1] = (double)H * hu;
+      tg += G;
+      th += H;
+      continue;
+    }
     int32_t G = 0, H = 0, T = 0;
     hist_part_sum(L, a0, na, ci, &G, &H, &T);
     if (mode == 1) {
@@ -505,8 +629,13 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
       H += tot[1][w];
       T += tot[2][w];
     }
-    sg = (double)G * vg1;
-    sh = (double)(H - 3ll * T) * vh1 + (double)T * vh3;
+    if (fp) {
+      sg = (double)G * gu;
+      sh = (double)H * hu;
+    } else {
+      sg = (double)G * vg1;
+      sh = (double)(H - 3ll * T) * vh1 + (double)T * vh3;
+    }
     nrows = (int32_t)L.N;
     const lgbm_gain_config& cfg = ctl->cfg;
     weight = leaf_output_full(cfg.lambda_l1 > 0.0, sg, sh, cfg.lambda_l1, cfg.lambda_l2,
@@ -596,14 +725,16 @@ __global__ __launch_bounds__(256) void k_score_update(DevLearner L, double lr,
 
 template <int W>
 __global__ void k_gather_rows(const uint32_t* __restrict__ rows, int64_t n, const uint4* __restrict__ rec,
-                              const uint16_t* __restrict__ gh, uint4* __restrict__ rec_out,
-                              uint16_t* __restrict__ gh_out) {
+                              const uint16_t* __restrict__ gh, const float2* __restrict__ g32,
+                              uint4* __restrict__ rec_out, uint16_t* __restrict__ gh_out,
+                              float2* __restrict__ g32_out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int64_t r = rows[i];
 #pragma unroll
   for (int k = 0; k < W; ++k) rec_out[i * W + k] = rec[r * W + k];
-  gh_out[i] = gh[r];
+  if (gh) gh_out[i] = gh[r];
+  if (g32) g32_out[i] = g32[r];
 }
 
 __global__ void k_subtract(const double* __restrict__ a, const double* __restrict__ b, int64_t n,
@@ -659,6 +790,17 @@ void launch_hist(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
     DISPATCH_W(L.W, KLAUNCH(ev, (k_hist_jobs<kW, false>), g, blk, lds, s, L));
   }
 }
+void launch_hist_f32(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
+  const dim3 g(HIST_SLOTS, (unsigned)std::max(L.n_fgroups, 1)), blk(HIST_THREADS);
+  const size_t lds = (size_t)2 * HIST_FP_CELLS * sizeof(unsigned long long);
+  DISPATCH_W(L.W, KLAUNCH(ev, (k_hist_f32<kW>), g, blk, lds, s, L));
+}
+void launch_fp_prep(const DevLearner& L, const float* g, const float* h, int64_t n,
+                    const uint4* partials, hipStream_t s) {
+  k_absmax<<<dim3((unsigned)stat_blocks(n)), dim3(256), 0, s>>>(g, h, n, (uint4*)partials);
+  k_fp_scales<<<1, 256, 0, s>>>(L.ctl, partials, stat_blocks(n), n);
+  k_pack_g32<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(g, h, n, L.bufs.g32[BUF_ORIG]);
+}
 void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s,
                     const KernelEvents* ev) {
   KLAUNCH(ev, k_fixscan, dim3((unsigned)L.F), dim3(SCAN_THREADS), 0, s, L, mode, explicit_out);
@@ -677,11 +819,12 @@ void launch_score_update(const DevLearner& L, double lr, double* score, hipStrea
                           score));
 }
 void launch_gather_rows(int W, const uint32_t* rows, int64_t n, const uint4* rec, const uint16_t* gh,
-                        uint4* rec_out, uint16_t* gh_out, hipStream_t s) {
+                        const float2* g32, uint4* rec_out, uint16_t* gh_out, float2* g32_out,
+                        hipStream_t s) {
   const int64_t blocks = (n + 255) / 256;
   if (blocks < 1) return;
-  DISPATCH_W(W, (k_gather_rows<kW><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(rows, n, rec, gh,
-                                                                                 rec_out, gh_out)));
+  DISPATCH_W(W, (k_gather_rows<kW><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+                    rows, n, rec, gh, g32, rec_out, gh_out, g32_out)));
 }
 void launch_subtract(const double* a, const double* b, int64_t n, double* out, hipStream_t s) {
   const int64_t blocks = (n + 255) / 256;

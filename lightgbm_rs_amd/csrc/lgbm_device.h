@@ -21,6 +21,8 @@
 #define HIST_FOLD_STEPS 7               // 7 x 64 rows <= 511 per 11-bit field
 #define HIST_ROWS_PER_LANE 2            // rows per lane in flight per step
 #define HIST_BLOCK_MAX_ROWS ((1 << 19) - 1)  // block-shared scheme field limit
+#define HIST_FP_CELLS 3584              // f32 gradients: cells per feature group (16 B each)
+#define MAX_FGROUPS 32
 #define PART_THREADS 1024
 #define PART_WAVES (PART_THREADS / LGBM_WAVE)
 #define PART_ROWS_PER_THREAD 4
@@ -121,6 +123,9 @@ struct Ctl {
   int32_t done, error, num_leaves, max_leaves;
   int32_t max_depth, n_slots, slot_cap, spec_max;
   int32_t n_jobs, n_reduce, rounds, root_skip;
+  int32_t fp_mode;                   // 1: f32 gradients (64-bit fixed-point histograms)
+  int32_t g_shift, h_shift;          // fixed-point exponents: cell = sum * 2^-shift
+  int32_t _i4;
   int64_t tile_total;
   // ---- histogram jobs of the current launch ----
   int32_t n_hjobs, _i1;

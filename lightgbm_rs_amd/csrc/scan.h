@@ -471,6 +471,20 @@ __device__ __forceinline__ void hist_part_sum(const DevLearner& L, int32_t a0, i
   *T = t;
 }
 
+// The 64-bit fixed-point (g, h) cells of a histogram job (f32 gradients).
+__device__ __forceinline__ void hist_part_sum64(const DevLearner& L, int32_t a0, int32_t na,
+                                                size_t ci, long long* G, long long* H) {
+  const size_t stride = (size_t)L.total_cells * 2;
+  const int64_t* p = L.hist_part64 + (size_t)a0 * stride + ci * 2;
+  long long g = 0, h = 0;
+  for (int32_t k = 0; k < na; ++k, p += stride) {
+    g += p[0];
+    h += p[1];
+  }
+  *G = g;
+  *H = h;
+}
+
 // Exact f64 histogram cells from the integer counters (sum q_g, sum q_h, #q_h==3).
 __device__ __forceinline__ void int_cell_to_f64(int32_t G, int32_t H, int32_t T, double vg1,
                                                 double vh1, double vh3, double* g, double* h) {

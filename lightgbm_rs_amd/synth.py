@@ -1,5 +1,8 @@
 """Synthetic inputs of BASELINE.json's configurations (no datasets offline).
 
+config0_like(): configs[0] — N rows x 28 float32 features ~N(0,1), the same logistic
+label, binned to <= 255 quantile bins (the f32-gradient CPU-reference case).
+
 config1_like(): configs[1] — N rows x 28 float32 features (21 ~N(0,1), 7 derived as
 products / abs of pairs), logistic label logit = w.x + 0.5*x0*x1 + N(0, 0.1) with
 w ~ N(0,1), binned to <= max_bin quantile bins per feature (u8).  Binning sits
@@ -43,12 +46,19 @@ def _derive(X, lib):
     return out
 
 
-def config1_like(n, seed=0x5EED0001, max_bin=63, device=None):
+def config0_like(n, seed=0x5EED0000, max_bin=255):
+    return config1_like(n, seed=seed, max_bin=max_bin, derived=False)
+
+
+def config1_like(n, seed=0x5EED0001, max_bin=63, device=None, derived=True):
     if device is not None:
         return _config1_torch(n, seed, max_bin, device)
     rng = np.random.default_rng(seed)
-    X = rng.standard_normal((21, n), dtype=np.float32)
-    X = np.concatenate([X, np.stack(_derive(X, np))], axis=0)
+    if derived:
+        X = rng.standard_normal((21, n), dtype=np.float32)
+        X = np.concatenate([X, np.stack(_derive(X, np))], axis=0)
+    else:
+        X = rng.standard_normal((28, n), dtype=np.float32)
     w = rng.standard_normal(28).astype(np.float32)
     logit = w @ X + 0.5 * X[0] * X[1] + rng.normal(0, 0.1, n).astype(np.float32)
     y = (rng.random(n, dtype=np.float32) < 1.0 / (1.0 + np.exp(-logit))).astype(np.float32)

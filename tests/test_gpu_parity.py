@@ -440,3 +440,94 @@ def test_tied_leaf_gains_break_by_leaf_id(be):
     say(f"  leaves {t['num_leaves']}, splits {len(gains)}, distinct gains {len(np.unique(gains))}")
     assert t["split_feature"][0] == 0
     assert len(gains) - len(np.unique(gains)) >= 10, "expected twin splits with equal gains"
+
+
+# ---------------------------------------------------------------------------
+# f32 gradients (use_quantized_grad = false).  Parity bar: histograms and leaf values
+# within 1e-5 relative of the reference's f64 fold (the 64-bit fixed-point build is
+# within ~1e-10); tree structure and partitions identical on these inputs.
+# ---------------------------------------------------------------------------
+def _auc(y, s):
+    """ROC AUC by the rank-sum (Mann-Whitney) formula, average ranks for ties."""
+    order = np.argsort(s, kind="mergesort")
+    ranks = np.empty(len(s), np.float64)
+    ss = s[order]
+    i = 0
+    while i < len(ss):
+        j = i
+        while j + 1 < len(ss) and ss[j + 1] == ss[i]:
+            j += 1
+        ranks[order[i:j + 1]] = 0.5 * (i + j) + 1.0
+        i = j + 1
+    pos = y > 0
+    npos, nneg = pos.sum(), (~pos).sum()
+    return (ranks[pos].sum() - npos * (npos + 1) / 2.0) / (npos * nneg)
+
+
+@pytest.mark.parametrize("n,F,max_bin", [(40_000, 28, 255), (300_000, 13, 64)])
+def test_fp32_leaf_histogram_vs_f64_fold(be, n, F, max_bin):
+    say(f"fp32 leaf histogram n={n} F={F} max_bin={max_bin}")
+    bins, meta, ub = make_binned(n, F, seed=F + 100, max_bin=max_bin)
+    g, h, _ = binary_gh(n, seed=6)
+    be.upload_resident_bins(bins, meta, ub)
+    be.upload_resident_grad_hess(g, h)  # not quantized: f32 gradients
+    rows = np.sort(np.random.default_rng(2).choice(n, size=n // 3, replace=False)).astype(np.uint32)
+    sg = float(np.sum(g[rows].astype(np.float64)))
+    sh = float(np.sum(h[rows].astype(np.float64)))
+    got = be.build_resident_leaf(rows, sg, sh)
+    offs, _ = slot_layout(meta)
+    gabs = float(np.abs(g[rows].astype(np.float64)).sum())
+    for f, m in enumerate(meta):
+        hist = oracle.construct_histogram(bins[f][rows], g[rows], h[rows], m.num_bin)
+        hist = oracle.fix_histogram(hist, m.num_bin, m.most_freq_bin, sg, sh)
+        hist = oracle.compact_histogram(hist, m.num_bin, m.offset)
+        np.testing.assert_allclose(got[offs[f]:offs[f] + 2 * m.num_bin], hist, rtol=1e-5,
+                                   atol=1e-9 * gabs, err_msg=f"feature {f}")
+
+
+@pytest.mark.parametrize("n,F,nl,max_bin,seed", [(100_000, 28, 31, 255, 7), (60_000, 9, 63, 64, 8)])
+def test_fp32_grow_tree_vs_oracle(be, n, F, nl, max_bin, seed):
+    say(f"fp32 grow_tree n={n} F={F} num_leaves={nl} max_bin={max_bin}")
+    bins, meta, ub = make_binned(n, F, seed=seed, max_bin=max_bin)
+    g, h, _ = binary_gh(n, seed=seed)
+    be.upload_resident_bins(bins, meta, ub)
+    be.upload_resident_grad_hess(g, h)
+    cfg = GainConfig.make(min_data_in_leaf=20)
+    t, lay = be.grow_tree_on_device_with_cfg(cfg, nl, -1)
+    o, olay = oracle.train_tree(bins, meta, ub, g, h, cfg, nl, -1)
+    assert t["num_leaves"] == o["num_leaves"]
+    for k in ("split_feature", "threshold_in_bin", "left_child", "right_child", "leaf_count",
+              "internal_count", "decision_type", "leaf_depth", "leaf_parent"):
+        assert np.array_equal(t[k], o[k]), k
+    for k in ("leaf_value", "internal_value", "leaf_weight", "threshold"):
+        np.testing.assert_allclose(t[k], o[k], rtol=1e-5, atol=1e-12, err_msg=k)
+    np.testing.assert_allclose(t["split_gain"], o["split_gain"], rtol=1e-5, err_msg="split_gain")
+    assert np.array_equal(lay["indices"], olay["indices"])
+
+
+def test_fp32_train_binary_config0_auc():
+    """BASELINE configs[0] shape (100k x 28 ~N(0,1), max_bin 255, f32 gradients,
+    num_leaves 31): 10 resident boosting iterations; training scores within 1e-6 and
+    AUC within 1e-6 of the oracle's."""
+    from lightgbm_rs_amd.synth import config0_like
+    n, iters, nl = 100_000, 10, 31
+    bins, meta, ub, y = config0_like(n)
+    init = oracle.boost_from_score(y)
+    b = HipBackend(0)
+    try:
+        b.upload_resident_bins(bins, meta, ub)
+        b.set_labels(y, init)
+        cfg = GainConfig.make(min_data_in_leaf=20)
+        trees = [b.train_iter_binary(i, cfg, nl, -1, 0.1, 0, False) for i in range(iters)]
+        scores = b.scores()
+    finally:
+        b.close()
+    oscores, otrees = oracle.train_binary(bins, meta, ub, y, cfg, nl, -1, iters, 0.1,
+                                          quantized=False)
+    for i, (t, o) in enumerate(zip(trees, otrees)):
+        assert np.array_equal(t["split_feature"], o["split_feature"]), i
+        assert np.array_equal(t["threshold_in_bin"], o["threshold_in_bin"]), i
+    np.testing.assert_allclose(scores, oscores, rtol=0, atol=1e-6)
+    a, oa = _auc(y, scores), _auc(y, oscores)
+    say(f"  AUC {a:.9f} oracle {oa:.9f}")
+    assert abs(a - oa) <= 1e-6
