@@ -134,10 +134,10 @@ def main():
     root_gbs = root_bytes / (tm["hist_ms"] * 1e-3) / 1e9 if tm["hist_ms"] > 0 else 0.0
     part_gbs = part_bytes / (tm["partition_ms"] * 1e-3) / 1e9 if tm["partition_ms"] > 0 else 0.0
     if tm["partition_ms"] >= tm["hist_ms"]:
-        dom = ("k_partition (DataPartition + left-child ConstructHistogram, fused)", part_gbs,
+        dom = ("k_partition (DataPartition + smaller-child ConstructHistogram, fused)", part_gbs,
                part_bytes, tm["partition_launches"], tm["partition_ms"])
     else:
-        dom = ("k_hist (ConstructHistogram, root)", root_gbs, root_bytes, tm["hist_launches"],
+        dom = ("k_hist_jobs (ConstructHistogram, root)", root_gbs, root_bytes, tm["hist_launches"],
                tm["hist_ms"])
     log(f"gpu: {ms_per_step:.2f} ms/step, leaves {min(leaves)}..{max(leaves)}, timing {tm}")
 

@@ -205,11 +205,13 @@ int lgbm_hip_get_discretized(lgbm_hip_ctx* ctx, int8_t* out, int64_t n);
 int lgbm_hip_build_int_histogram(lgbm_hip_ctx* ctx, const uint32_t* leaf_rows, int64_t n_rows,
                                  int64_t* out);
 
-/* Build one leaf's f64 histogram from the quantized gradients, then FixHistogram
- * on the RAW leaf sums and compaction: the device analog of
- * `build_leaf_histogram_into` (learner.rs:2464-2566) =
- * `Backend::build_resident_leaf` (lib.rs:1953-1972).  out has slot_len doubles.
- * Requires a prior lgbm_hip_quantize. */
+/* Build one leaf's f64 histogram, then FixHistogram on the RAW leaf sums and
+ * compaction: the device analog of `build_leaf_histogram_into`
+ * (learner.rs:2464-2566) = `Backend::build_resident_leaf` (lib.rs:1953-1972).  out
+ * has slot_len doubles.  Uses the quantized gradients after lgbm_hip_quantize
+ * (bit-exact with the f64 fold of the dequantized values), otherwise the f32
+ * gradients of lgbm_hip_set_gradients (64-bit fixed-point build, within ~1e-10
+ * relative of the f64 fold). */
 int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* ctx, const uint32_t* leaf_rows, int64_t n_rows,
                                   double sum_gradient, double sum_hessian, double* out);
 
@@ -239,11 +241,13 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* ctx, const uint32_t* bins, int64_t n, 
 
 /* ---- coarse seam: one whole tree per call ----------------------------------- */
 
-/* Grow one tree on device from the resident bins and the CURRENT quantized
- * gradients: `Backend::grow_tree_on_device_with_cfg` (lib.rs:2688,2771;
+/* Grow one tree on device from the resident bins and the CURRENT gradients:
+ * `Backend::grow_tree_on_device_with_cfg` (lib.rs:2688,2771;
  * kernels/grow_driver.rs:1219), following the CPU learner `train_inner`
- * (learner.rs:980-1562) decision for decision.  Quantized (integer-exact) path
- * only: call lgbm_hip_quantize first.  `tree` arrays need num_leaves capacity;
+ * (learner.rs:980-1562) decision for decision.  After lgbm_hip_quantize the
+ * quantized gradients are used (use_quantized_grad: trees bit-exact with the CPU
+ * learner); otherwise the f32 gradients of lgbm_hip_set_gradients
+ * (use_quantized_grad = false).  `tree` arrays need num_leaves capacity (<= 256);
  * `layout` may be NULL (else indices has num_data entries). */
 int lgbm_hip_grow_tree(lgbm_hip_ctx* ctx, const lgbm_gain_config* cfg, int32_t num_leaves,
                        int32_t max_depth, lgbm_tree_out* tree, lgbm_layout_out* layout);
@@ -254,10 +258,12 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* ctx, const lgbm_gain_config* cfg, int32_t n
  * (`ScoreUpdater::new` + `add_constant`, lgbm-boosting/src/score_updater.rs:63-99). */
 int lgbm_hip_set_labels(lgbm_hip_ctx* ctx, const float* labels, int64_t n, double init_score);
 
-/* One binary-logloss boosting iteration with quantized gradients, all resident:
+/* One binary-logloss boosting iteration, all resident:
  * `BinaryLogloss::get_gradients` (lgbm-objective/src/binary.rs:134-172) ->
  * quantize (gbdt.rs:945-960, seed ((iter<<20) ^ 0x51702010)) -> grow tree ->
  * `Tree::shrinkage` (tree.rs:1074) -> score update (score_updater.rs:133).
+ * num_grad_quant_bins 2 or 4: use_quantized_grad; 0: f32 gradients
+ * (use_quantized_grad = false, no quantization step).
  * `tree` (may be NULL) receives the shrunk tree. */
 int lgbm_hip_train_iter_binary(lgbm_hip_ctx* ctx, int32_t iter, const lgbm_gain_config* cfg,
                                int32_t num_leaves, int32_t max_depth, double learning_rate,
@@ -280,7 +286,8 @@ int lgbm_hip_get_timing(lgbm_hip_ctx* ctx, double* ms_out5, double* hist_bytes_o
  * phase_prof.rs:1-60).  out[0..4]: ms per kernel family as above; [5] root
  * ConstructHistogram rows; [6] root ConstructHistogram launches; [7] rows moved by
  * partition passes (which also build one child's histogram per split); [8]
- * partition launches; [9] bytes per row record; [10] features; [11] histogram
+ * partition kernels launched while timing (rounds after a tree is complete
+ * included); [9] bytes per row record; [10] features; [11] histogram
  * cells; [12] leaf splits partitioned (including splits made ahead of their turn
  * that the tree never used); [13] partition rounds over all trees; [14] trees;
  * [15] rounds launched after the captured per-tree sequence. */

@@ -89,15 +89,16 @@ struct lgbm_hip_ctx {
   int32_t part_blocks = PART_MAX_BLOCKS;  // partition grid
   int32_t* done_host = nullptr;  // pinned: ctl->done after the captured rounds
   double tree_rounds = 0.0, trees = 0.0, extra_rounds = 0.0;
+  double part_launches = 0.0;  // partition kernels enqueued while timing (empty rounds too)
   uint64_t graph_gen = 0, buf_gen = 1;
   bool use_graphs = true;
   // timing
   bool timing = false;
   std::vector<EventPair> ev_pool;
   size_t ev_used = 0;
-  // Per-tree chain: chain[0] is a marker recorded before the tree's first kernel,
-  // chain[i] (i > 0) is stamped by kernel i at its end; kernel i's time is
-  // chain[i] - chain[i-1] (its own duration plus the dispatch gap before it).
+  // Per-tree event list: every timed kernel gets a (start, stop) pair bound to its own
+  // begin / end by the launch, so chain[i] - chain[i-1] for a stop event i is that
+  // kernel's duration alone (dispatch gaps excluded).
   std::vector<hipEvent_t> chain;
   std::vector<int> chain_family;
   size_t chain_used = 0;
@@ -368,17 +369,12 @@ hipEvent_t chain_next(lgbm_hip_ctx* c, int family) {
   c->chain_family[c->chain_used] = family;
   return c->chain[c->chain_used++];
 }
-// Opens a chain: a plain marker ahead of the first chained kernel.
-void chain_start(lgbm_hip_ctx* c) {
-  if (!c->timing) return;
-  (void)hipEventRecord(chain_next(c, -1), c->stream);
-}
-// The stop event for one kernel launch of the chain (family -1: not counted).  The
-// launch binds it to the kernel's own end (hipExtLaunchKernel), so no marker packet
-// sits between consecutive kernels.
+// The (start, stop) events of one kernel launch (family -1: not counted).  The launch
+// binds them to the kernel's own begin and end (hipExtLaunchKernel), so no marker
+// packet sits between consecutive kernels.
 const KernelEvents* ev_kernel(lgbm_hip_ctx* c, int family, KernelEvents* slot) {
   if (!c->timing) return nullptr;
-  slot->start = nullptr;
+  slot->start = chain_next(c, -1);
   slot->stop = chain_next(c, family);
   return slot;
 }
@@ -431,6 +427,7 @@ int do_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_t seed
 void enqueue_rounds(lgbm_hip_ctx* c, int32_t rounds, int32_t fp) {
   DevLearner L = make_learner(c);
   KernelEvents ke;
+  if (c->timing) c->part_launches += rounds;
   for (int32_t r = 0; r < rounds; ++r) {
     launch_plan(L, SLOT_CAP(c->lcap), c->stream, ev_kernel(c, FAM_SCAN, &ke));
     launch_partition(L, c->W, fp, c->part_blocks, c->stream, ev_kernel(c, FAM_PART, &ke));
@@ -444,7 +441,6 @@ void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth, int32_
                   int32_t fp) {
   DevLearner L = make_learner(c);
   KernelEvents ke;
-  chain_start(c);
   launch_tree_init(L, num_leaves, max_depth, SLOT_CAP(num_leaves), c->spec_max, fp, c->stream,
                    ev_kernel(c, -1, &ke));
   if (fp)
@@ -1228,7 +1224,7 @@ int lgbm_hip_set_timing(lgbm_hip_ctx* c, int32_t enable) {
   c->timing = enable != 0;
   for (double& m : c->ms) m = 0.0;
   HIPCHK(c, hipMemset(c->stats, 0, 64));
-  c->tree_rounds = c->trees = c->extra_rounds = 0.0;
+  c->tree_rounds = c->trees = c->extra_rounds = c->part_launches = 0.0;
   return LGBM_HIP_OK;
 }
 
@@ -1258,7 +1254,7 @@ int lgbm_hip_get_stats(lgbm_hip_ctx* c, double* out) {
   out[5] = st[2];
   out[6] = st[3];
   out[7] = st[0];
-  out[8] = st[1];
+  out[8] = c->part_launches;
   out[9] = 16.0 * c->W;
   out[10] = c->F;
   out[11] = c->total_cells;
