@@ -86,7 +86,7 @@ struct lgbm_hip_ctx {
   int32_t graph_nl = -1, graph_md = 0, graph_rounds = 0, graph_spec = 0, graph_fp = -1;
   int32_t round_cap = 24;     // partition rounds in the captured sequence
   int32_t spec_max = SPEC_DEFAULT;
-  int32_t part_blocks = PART_MAX_BLOCKS;  // partition grid
+  int32_t part_blocks = 256 * PART_BLOCKS_PER_CU;  // partition grid (set from the CU count)
   int32_t* done_host = nullptr;  // pinned: ctl->done after the captured rounds
   double tree_rounds = 0.0, trees = 0.0, extra_rounds = 0.0;
   double part_launches = 0.0;  // partition kernels enqueued while timing (empty rounds too)
@@ -255,9 +255,8 @@ int ensure_scratch_bytes(lgbm_hip_ctx* c, size_t bytes) {
   return LGBM_HIP_OK;
 }
 
-// A round's tiles: every job rounds its own rows up to whole tiles, so the jobs of
-// one round (disjoint leaves, at most SPEC_MAX) use at most rows / tile + SPEC_MAX
-// tiles; sized for the smallest tile of any launch shape.
+// Per-tile left-row prefix of the stable per-op partition (one job: at most
+// rows / tile + 1 tiles); sized for the smallest tile of any launch shape.
 int ensure_tile_state(lgbm_hip_ctx* c, int64_t rows) {
   const int64_t tiles = (rows + PART_MIN_TILE - 1) / PART_MIN_TILE + SPEC_MAX + 1;
   if (c->tile_cap >= tiles) return LGBM_HIP_OK;
@@ -539,7 +538,9 @@ int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, do
   int rc = 0;
   if (err & ERR_ROOT_HESSIAN)
     return set_err(c, LGBM_HIP_ERR_INVALID_LEAF_HESSIAN, "root sum_hessian <= 0");
-  if (err & ERR_SPIN) return set_err(c, LGBM_HIP_ERR_RUNTIME, "partition look-back spin limit");
+  if (err & ERR_NEG_HESSIAN)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT,
+                   "quantized gradients need non-negative hessians");
   if (err & ERR_SLOTS) return set_err(c, LGBM_HIP_ERR_RUNTIME, "node slot budget exhausted");
   if (err) return set_err(c, LGBM_HIP_ERR_RUNTIME, "device learner error");
   if (out) {
@@ -578,8 +579,10 @@ int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, do
         if ((rc = dalloc(c, &c->d_indices, (size_t)c->N))) return rc;
         c->indices_cap = c->N;
       }
+      if ((rc = ensure_scratch_bytes(c, export_layout_scratch_bytes(c->N, nl)))) return rc;
       DevLearner L = make_learner(c);
-      launch_export_layout(L, nl, c->d_indices, c->stream);
+      launch_export_layout(L, nl, c->d_indices, c->scratch, c->stream);
+      HIPCHK(c, hipGetLastError());
       HIPCHK(c, hipStreamSynchronize(c->stream));
       HIPCHK(c, hipMemcpy(layout->indices, c->d_indices, (size_t)c->N * 4, hipMemcpyDeviceToHost));
     }
@@ -635,7 +638,6 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   if (rc) return fail(rc);
   Ctl init;
   std::memset(&init, 0, sizeof(init));
-  init.epoch = 1u;
   if (hipMemcpy(c->ctl, &init, sizeof(init), hipMemcpyHostToDevice) != hipSuccess)
     return fail(set_err(c, LGBM_HIP_ERR_HIP, "ctl init"));
   if ((rc = dalloc(c, &c->stats, 8))) return fail(rc);
@@ -644,6 +646,12 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
     return fail(set_err(c, LGBM_HIP_ERR_HIP, "hipHostMalloc"));
   if ((rc = init_jump_tables(c))) return fail(rc);
   if ((rc = dalloc(c, &c->partials, STAT_BLOCKS))) return fail(rc);
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
+      cus > 0)
+    c->part_blocks = cus * PART_BLOCKS_PER_CU;
+  if (const char* e = std::getenv("LGBM_HIP_PART_BLOCKS"))
+    c->part_blocks = std::max(1, std::min(65535, std::atoi(e)));
   if (const char* e = std::getenv("LGBM_HIP_GRAPHS")) c->use_graphs = std::strcmp(e, "0") != 0;
   if (const char* e = std::getenv("LGBM_HIP_ROUNDS")) c->round_cap = std::max(1, std::atoi(e));
   if (const char* e = std::getenv("LGBM_HIP_SPEC"))
@@ -1092,20 +1100,13 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   J.flags = ((int32_t)most_freq_bin > (int32_t)threshold ? 1 : 0) | (na_as_missing ? 2 : 0) |
             (default_left ? 4 : 0);
   if ((rc = ctl_write(c, CTL_OFF(jobs), J))) return rc;
-  uint32_t ep = 0;
-  if ((rc = ctl_read(c, CTL_OFF(epoch), &ep))) return rc;
-  ep = (ep + 1u) & 0x3fffffffu;
-  if (ep == 0u) ep = 1u;
-  if ((rc = ctl_write(c, CTL_OFF(epoch), ep))) return rc;
-  const int32_t zero32 = 0;
-  if ((rc = ctl_write(c, CTL_OFF(part_ticket), zero32))) return rc;
   const int32_t one = 1;
   if ((rc = ctl_write(c, CTL_OFF(n_jobs), one))) return rc;
   const int64_t tiles = J.ntiles;
   if ((rc = ctl_write(c, CTL_OFF(tile_total), tiles))) return rc;
   DevLearner L = make_learner(c);
   L.W = 1;
-  launch_partition(L, 1, 0, std::min<int64_t>(c->part_blocks, J.ntiles), c->stream);
+  launch_partition_stable(L, tiles, std::min<int64_t>(c->part_blocks, tiles), c->stream);
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));
   int32_t lc = 0;

@@ -35,9 +35,6 @@
 
 namespace lgbm {
 
-#define TS_AGG 1ull
-#define TS_INC 2ull
-#define SPIN_LIMIT (1 << 20)
 #define PLAN_WAVES (PLAN_THREADS / LGBM_WAVE)
 #define INT_MAX32 0x7fffffff
 // plan_state rows (MAX_LEAVES entries each): the tree's leaf -> node-slot map and
@@ -134,8 +131,7 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
 //      with gain > 0, up to spec_max, while two node slots per split the tree may
 //      still need stay in reserve;
 //   4. (all threads) the Tree::split fields of the committed splits, the partition
-//      jobs and child node slots of the selected leaves, and the next round's
-//      partition ticket / look-back epoch.
+//      jobs (with zeroed output cursors) and child node slots of the selected leaves.
 // A slot's best split is feat_split[slot * F + best_fpos[slot]].
 // ===========================================================================
 // ArgMax over the leaves held by a wave (lane l: leaves l + 64 i, i < PL) in the
@@ -422,6 +418,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     J.ntiles = (int32_t)((J.count + PART_TILE - 1) / PART_TILE);
     J.tile0 = 0;
     ctl->jobs[j] = J;
+    ctl->part_cur[j] = 0ull;
     s_ntiles[j] = J.ntiles;
     nd.child[2 * p] = cl;
     nd.child[2 * p + 1] = cr;
@@ -458,54 +455,62 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     ctl->num_leaves = nl;
     ctl->n_slots = s_nslots;
     ctl->rounds += 1;
-    if (nj > 0) {
-      // the round's partition: fresh tickets and a new look-back epoch
-      ctl->part_ticket = 0;
-      uint32_t ep = (ctl->epoch + 1u) & 0x3fffffffu;
-      ctl->epoch = ep == 0u ? 1u : ep;
-      L.stats[1] += 1.0;
-    }
+    if (nj > 0) L.stats[1] += 1.0;
     if (s_done) ctl->done = 1;
   }
 }
 
 // ===========================================================================
-// k_partition: stable single-pass split of every job of the round.  The tiles of all
-// jobs form one ticket space (job j owns [tile0, tile0 + ntiles)); each tile ranks
-// its rows with wave ballots, publishes its left count and derives its exclusive left
-// prefix by decoupled look-back over the earlier tiles of the same job.  Left rows go
-// to [begin, begin + L) ascending; right rows to [begin + L, begin + count) in
-// descending position (logical order = ascending, stored reversed), so no total is
-// needed in advance.  Look-back words: epoch(30) | flag(2) | value(32).  The launcher
-// of a round (k_plan, or the host for the per-op entry point) resets the ticket
-// counter and moves to a fresh epoch, so stale words of earlier rounds never match.
+// k_partition: DataPartition::split of every job of the round in one pass.  The
+// tiles of all jobs (job j owns tiles [tile0, tile0 + ntiles), PART_TILE rows each,
+// in the parent's logical row order) are dealt to the blocks in contiguous runs, so a
+// block meets few job boundaries.  A tile ranks its rows with wave ballots, then
+// takes its output ranges:
+//   tree driver (STABLE = false): one 64-bit atomic add on the job's cursor reserves
+//     (left rows, right rows) at once, so no tile waits for another; the order of
+//     rows inside a child is then unspecified (every consumer is order-free: integer
+//     histogram cells, per-row score update; the layout export sorts each leaf);
+//   per-op entry point (STABLE = true): the exclusive left prefix of the tile within
+//     its job, precomputed by k_tile_count + k_tile_scan, keeps DataPartition::split's
+//     stable order.
+// Left rows go to [begin, begin + L) ascending, right rows to [begin + L, begin +
+// count) filled from the end (stored reversed: logical order = reverse storage
+// order).  The block that completes a job (last cursor reservation, or the job's last
+// tile when stable) records the children's ranges and counts.
 // Quantized gradients (FP = 0): in the tree driver the pass also builds one child's
 // integer histogram per job (the side the scan predicts to be smaller) from the rows
-// while they are in registers; the other child's is parent - built in integers
-// (k_pair_scan).  f32 gradients (FP = 1) move as (g, h) pairs; the smaller child's
-// histogram is built afterwards by k_hist_f32.
+// while they are in registers, flushed per (block, job) into the job's accumulator;
+// the other child's is parent - built in integers (k_pair_scan).  f32 gradients
+// (FP = 1) move as (g, h) pairs; the smaller child's histogram is built afterwards by
+// k_hist_f32.
 // ===========================================================================
-template <int W, int FP>
+template <int W, int FP, bool STABLE>
 __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   constexpr int PT = PART_THREADS, PR = PART_ROWS_PER_THREAD;
   constexpr int kWaves = PT / LGBM_WAVE;
   constexpr int kTile = PT * PR;
+  constexpr int kSlots = PR * kWaves;  // (row k, wave) left counts, k-major = row order
+  static_assert(kSlots <= LGBM_WAVE, "wave 0 scans the per-(row, wave) left counts");
+  // An LDS cell holds sums of q_h <= 4 below 2^21 (and |q_g| <= 2 below 2^21): a
+  // block flushes its histogram after this many tiles of one job.
+  constexpr int kFlushTiles = ((1 << 19) - 1) / kTile;
+  static_assert(kFlushTiles >= 1, "tile larger than an LDS cell's row capacity");
   using GhT = typename std::conditional<FP != 0, float2, uint16_t>::type;
   extern __shared__ unsigned long long lds_hist[];
   __shared__ int32_t cb[16 * LGBM_MAX_W];
   __shared__ PartJob s_jobs[SPEC_MAX];
-  __shared__ int64_t s_tile;
-  __shared__ int32_t s_cnt[PR][kWaves];
-  __shared__ int32_t s_pref[PR][kWaves];
-  __shared__ int32_t s_total;
-  __shared__ int32_t s_excl;
+  __shared__ int32_t s_cnt[kSlots];
+  __shared__ int32_t s_pref[kSlots];
+  __shared__ int32_t s_lbase, s_rbase, s_total, s_last;
   Ctl* ctl = L.ctl;
-  const int tid = threadIdx.x, wave = tid >> 6;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = (int)lane_id();
   const int32_t nj = ctl->n_jobs;
   const int64_t total = ctl->tile_total;
-  const uint32_t epoch = ctl->epoch & 0x3fffffffu;
+  const int64_t G = gridDim.x;
+  const int64_t t_lo = (int64_t)blockIdx.x * total / G;
+  const int64_t t_hi = ((int64_t)blockIdx.x + 1) * total / G;
   if (tid < SPEC_MAX) s_jobs[tid] = ctl->jobs[tid];
-  if (nj <= 0 || total <= 0 || (int64_t)blockIdx.x >= total) return;
+  if (nj <= 0 || t_lo >= t_hi) return;
   const int F = L.F, cells = L.total_cells, nw = (F + 3) / 4;
   if constexpr (FP == 0)
     for (int c = tid; c < cells + 4; c += PT) lds_hist[c] = 0ull;
@@ -515,24 +520,34 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   int32_t cbr[16 * W];
 #pragma unroll
   for (int f = 0; f < 16 * W; ++f) cbr[f] = __builtin_amdgcn_readfirstlane(cb[f]);
-  int32_t cur = -1;  // job whose rows the LDS histogram holds
-  while (true) {
-    __syncthreads();
-    if (tid == 0)
-      s_tile = (int64_t)__hip_atomic_fetch_add(&ctl->part_ticket, 1, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    const int64_t t = s_tile;
-    if (t >= total) break;
-    int32_t j = 0;
+  int32_t j = 0;
+  int32_t cur = -1;       // job whose rows the LDS histogram holds
+  int32_t held = 0;       // tiles of that job in the LDS histogram
+  bool flushed = false;   // part of that job already flushed by this block
+  // The accumulator of job `cur` gets this block's cells: plain stores when the block
+  // covers the whole job in one flush, else atomic adds (k_pair_scan clears it).
+  auto flush = [&](bool final_flush) {
+    const PartJob& C = s_jobs[cur];
+    const bool sole = final_flush && !flushed && C.tile0 >= t_lo && C.tile0 + C.ntiles <= t_hi;
+    lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3, sole);
+  };
+  // Shared-state hand-off per tile: s_cnt is written after the loads and read by
+  // wave 0 before barrier B; s_pref / s_lbase / s_rbase / s_total / s_last are
+  // written by wave 0 between barriers A and B and read after B; the next tile's
+  // writes of each come after a barrier every reader has passed.  Histogram adds end
+  // before B, so a flush at the top of the next tile sees them all.
+  for (int64_t t = t_lo; t < t_hi; ++t) {
     while (j + 1 < nj && s_jobs[j + 1].tile0 <= t) ++j;
-    if (FP == 0 && j != cur) {
-      if (cur >= 0 && s_jobs[cur].acc_right >= 0) {
-        lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3,
-                             s_jobs[cur].ntiles == 1);
+    if (FP == 0 && (j != cur || held == kFlushTiles)) {
+      if (cur >= 0 && s_jobs[cur].acc_right >= 0 && held > 0) {
+        flush(j != cur);
+        flushed = j == cur;
         __syncthreads();
+      } else {
+        flushed = false;
       }
       cur = j;
+      held = 0;
     }
     const PartJob& J = s_jobs[j];
     const int64_t count = J.count, begin = J.begin;
@@ -544,102 +559,92 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     GhT* __restrict__ dgh = gh_buf<GhT>(L.bufs, J.dst_buf);
     uint4 w[PR][W];
     GhT q[PR];
-    bool isleft[PR], valid[PR];
-    int32_t rank[PR];
+    bool valid[PR];
+    // every load of the tile in flight at once (positions past the job's end re-read
+    // its last row; a job that owns a tile has count >= 1)
 #pragma unroll
     for (int k = 0; k < PR; ++k) {
       const int64_t p = base + (int64_t)k * PT + tid;
       valid[k] = p < count;
-      bool right = false;
-      if (valid[k]) {
-        const int64_t phys = J.rev ? begin + count - 1 - p : begin + p;
+      const int64_t pc = valid[k] ? p : count - 1;
+      const int64_t phys = J.rev ? begin + count - 1 - pc : begin + pc;
 #pragma unroll
-        for (int i = 0; i < W; ++i) w[k][i] = src[phys * W + i];
-        q[k] = sgh[phys];
-        const int32_t bin = (int32_t)rec_byte(w[k], J.fbyte);
-        right = route_right(bin, J.pmin, J.max_bin, J.th, J.na_bin, J.flags);
-      }
-      isleft[k] = valid[k] && !right;
-      const unsigned long long m = __ballot(isleft[k]);
-      rank[k] = (int32_t)__popcll(m & lanemask_lt());
-      if (lane_id() == 0) s_cnt[k][wave] = (int32_t)__popcll(m);
+      for (int i = 0; i < W; ++i) w[k][i] = src[phys * W + i];
+      q[k] = sgh[phys];
     }
-    __syncthreads();
-    if (tid == 0) {
-      int32_t acc = 0;
-      for (int k = 0; k < PR; ++k)
-        for (int wv = 0; wv < kWaves; ++wv) {
-          s_pref[k][wv] = acc;
-          acc += s_cnt[k][wv];
-        }
-      s_total = acc;
-      // publish + look-back within the job
-      uint64_t* ts = L.tile_state;
-      const uint64_t ep = (uint64_t)epoch << 34;
-      int64_t excl = 0;
-      if (lt == 0) {
-        __hip_atomic_store(&ts[t], ep | (TS_INC << 32) | (uint32_t)acc, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      } else {
-        __hip_atomic_store(&ts[t], ep | (TS_AGG << 32) | (uint32_t)acc, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        int64_t p = t - 1;
-        int spins = 0;
-        while (p >= J.tile0) {
-          const uint64_t st = __hip_atomic_load(&ts[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const bool fresh = (st >> 34) == (uint64_t)epoch;
-          const uint64_t flag = (st >> 32) & 3ull;
-          if (!fresh || flag == 0ull) {
-            ++spins;
-            const bool give_up =
-                spins > SPIN_LIMIT ||
-                ((spins & 1023) == 0 &&
-                 (__hip_atomic_load(&ctl->error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
-                  ERR_SPIN));
-            if (give_up) {
-              atomicOr(&ctl->error, ERR_SPIN);
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-            continue;
-          }
-          excl += (int64_t)(uint32_t)st;
-          if (flag == TS_INC) break;
-          --p;
-        }
-        __hip_atomic_store(&ts[t], ep | (TS_INC << 32) | (uint32_t)(excl + acc), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-      s_excl = (int32_t)excl;
-    }
-    __syncthreads();
-    const int64_t excl = s_excl;
-    const int64_t rbase = base - excl;  // right rows before this tile
+    bool isleft[PR];
+    int32_t rank[PR];
 #pragma unroll
     for (int k = 0; k < PR; ++k) {
-      if (!valid[k]) continue;
-      const int64_t pos = (int64_t)k * PT + tid;
-      const int64_t lrank = s_pref[k][wave] + rank[k];
-      int64_t d;
-      if (isleft[k]) {
-        d = begin + excl + lrank;
-      } else {
-        const int64_t r = rbase + (pos - lrank);
-        d = begin + count - 1 - r;
-      }
-#pragma unroll
-      for (int i = 0; i < W; ++i) dst[d * W + i] = w[k][i];
-      dgh[d] = q[k];
+      const int32_t bin = (int32_t)rec_byte(w[k], J.fbyte);
+      isleft[k] = valid[k] && !route_right(bin, J.pmin, J.max_bin, J.th, J.na_bin, J.flags);
+      const unsigned long long m = __ballot(isleft[k]);
+      rank[k] = (int32_t)__popcll(m & lanemask_lt());
+      if (lane == 0) s_cnt[k * kWaves + wave] = (int32_t)__popcll(m);
     }
+    __syncthreads();  // A
+    if (wave == 0) {
+      // exclusive prefix of the (row, wave) counts
+      const int32_t c = lane < kSlots ? s_cnt[lane] : 0;
+      int32_t incl = c;
+#pragma unroll
+      for (int off = 1; off < kSlots; off <<= 1) {
+        const int32_t v = __shfl_up(incl, off);
+        if (lane >= off) incl += v;
+      }
+      if (lane < kSlots) s_pref[lane] = incl - c;
+      const int32_t acc = __shfl(incl, kSlots - 1);
+      if (lane == 0) {
+        const int32_t trows = (int32_t)min((int64_t)kTile, count - base);
+        int64_t lb, rb;
+        bool last;
+        if constexpr (STABLE) {
+          lb = (int64_t)L.tile_state[t];
+          rb = base - lb;
+          last = lt == J.ntiles - 1;
+        } else {
+          const unsigned long long old = atomicAdd(
+              &ctl->part_cur[j],
+              (unsigned long long)(uint32_t)acc | ((unsigned long long)(uint32_t)(trows - acc) << 32));
+          lb = (int64_t)(uint32_t)old;
+          rb = (int64_t)(old >> 32);
+          last = lb + rb + trows == count;
+        }
+        s_lbase = (int32_t)lb;
+        s_rbase = (int32_t)rb;
+        s_total = acc;
+        s_last = last ? 1 : 0;
+      }
+    }
+    // histogram adds (wave 0 after its reservation, the other waves meanwhile)
     if (FP == 0 && J.acc_right >= 0) {
       const bool want_left = J.acc_right == 0;
 #pragma unroll
       for (int k = 0; k < PR; ++k)
         if (valid[k] && isleft[k] == want_left)
           lds_hist_add<W>(lds_hist, cbr, nw, w[k], gh_bits(q[k]));
+      ++held;
     }
-    if (lt == J.ntiles - 1 && tid == 0) {
-      const int32_t lc = (int32_t)(excl + s_total);
+    __syncthreads();  // B
+    const int64_t lbase = s_lbase, rbase = s_rbase;
+#pragma unroll
+    for (int k = 0; k < PR; ++k) {
+      if (!valid[k]) continue;
+      const int64_t pos = (int64_t)k * PT + tid;
+      const int64_t lrank = s_pref[k * kWaves + wave] + rank[k];
+      int64_t d;
+      if (isleft[k]) {
+        d = begin + lbase + lrank;
+      } else {
+        const int64_t r = rbase + (pos - lrank);  // right rows before this one
+        d = begin + count - 1 - r;
+      }
+#pragma unroll
+      for (int i = 0; i < W; ++i) dst[d * W + i] = w[k][i];
+      dgh[d] = q[k];
+    }
+    if (tid == 0 && s_last) {
+      const int32_t lc = (int32_t)(lbase + s_total);
       const int32_t rc = (int32_t)(count - lc);
       if (J.parent >= 0) {
         DevNodes& nd = L.nodes;
@@ -676,9 +681,64 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
       }
     }
   }
-  if (FP == 0 && cur >= 0 && s_jobs[cur].acc_right >= 0)
-    lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3,
-                         s_jobs[cur].ntiles == 1);
+  if (FP == 0 && cur >= 0 && s_jobs[cur].acc_right >= 0 && held > 0) flush(true);
+}
+
+// Stable per-op partition, step 1: the left-row count of every tile of job 0.
+template <int W>
+__global__ __launch_bounds__(PART_THREADS) void k_tile_count(DevLearner L) {
+  constexpr int PT = PART_THREADS, PR = PART_ROWS_PER_THREAD, kTile = PT * PR;
+  __shared__ int32_t s_w[PT / LGBM_WAVE];
+  const PartJob J = L.ctl->jobs[0];
+  const int64_t t = blockIdx.x;
+  if (t >= J.ntiles) return;
+  const uint4* __restrict__ src = L.bufs.rec[J.src_buf];
+  int32_t n = 0;
+  for (int k = 0; k < PR; ++k) {
+    const int64_t p = t * kTile + (int64_t)k * PT + threadIdx.x;
+    if (p >= J.count) continue;
+    const int64_t phys = J.rev ? J.begin + J.count - 1 - p : J.begin + p;
+    uint4 w[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[i] = src[phys * W + i];
+    const int32_t bin = (int32_t)rec_byte(w, J.fbyte);
+    n += route_right(bin, J.pmin, J.max_bin, J.th, J.na_bin, J.flags) ? 0 : 1;
+  }
+  for (int off = 32; off >= 1; off >>= 1) n += __shfl_xor(n, off);
+  if (lane_id() == 0) s_w[threadIdx.x >> 6] = n;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t s = 0;
+    for (int i = 0; i < PT / LGBM_WAVE; ++i) s += s_w[i];
+    L.tile_state[t] = (uint64_t)s;
+  }
+}
+
+// Stable per-op partition, step 2: tile counts -> exclusive prefix (one block).
+__global__ __launch_bounds__(1024) void k_tile_scan(DevLearner L) {
+  __shared__ int64_t s_part[1024 / LGBM_WAVE];
+  __shared__ int64_t s_carry;
+  const int64_t n = L.ctl->jobs[0].ntiles;
+  const int tid = threadIdx.x, lane = (int)lane_id(), wave = tid >> 6;
+  if (tid == 0) s_carry = 0;
+  __syncthreads();
+  for (int64_t b0 = 0; b0 < n; b0 += 1024) {
+    const int64_t i = b0 + tid;
+    const int64_t v = i < n ? (int64_t)L.tile_state[i] : 0;
+    int64_t incl = v;
+    for (int off = 1; off < LGBM_WAVE; off <<= 1) {
+      const int64_t u = __shfl_up(incl, off);
+      if (lane >= off) incl += u;
+    }
+    if (lane == LGBM_WAVE - 1) s_part[wave] = incl;
+    __syncthreads();
+    int64_t before = s_carry;
+    for (int k = 0; k < wave; ++k) before += s_part[k];
+    if (i < n) L.tile_state[i] = (uint64_t)(before + incl - v);
+    __syncthreads();
+    if (tid == 1023) s_carry = before + incl;
+    __syncthreads();
+  }
 }
 
 // ===========================================================================
@@ -842,18 +902,102 @@ __global__ void k_tree_finalize(DevLearner L) {
   }
 }
 
-// Exports the partition layout: indices[leaf_begin[l] + p] = row of logical position p.
+// Exports the partition layout the way DataPartition::split leaves it: each leaf's
+// rows in ascending row order at the leaf's begin offset (leaf_of, then a stable rank
+// of every row within its leaf), whatever the storage order inside the leaf.
 template <int W>
-__global__ void k_export_layout(DevLearner L, uint32_t* __restrict__ indices) {
+__global__ void k_leaf_of(DevLearner L, uint8_t* __restrict__ leaf_of) {
   const int32_t l = blockIdx.y;
   if (l >= L.ctl->num_leaves) return;
   const int64_t b = L.leaves.begin[l], c = L.leaves.count[l];
-  const int32_t rev = L.leaves.rev[l];
   const uint4* __restrict__ rec = L.bufs.rec[L.leaves.buf[l]];
   for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < c;
-       p += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t phys = rev ? b + c - 1 - p : b + p;
-    indices[b + p] = rec[phys * W + (W - 1)].w;
+       p += (int64_t)gridDim.x * blockDim.x)
+    leaf_of[rec[(b + p) * W + (W - 1)].w] = (uint8_t)l;
+}
+
+// Stable rank of every row among the rows of its leaf, RANK_ROWS rows per block in
+// row order: wave peers by eight key-bit ballots, waves in order through LDS, and a
+// running per-leaf count.  COUNT pass: per (leaf, block) row counts.  Scatter pass:
+// indices[offset of (leaf, block) + rank in block] = row.
+#define RANK_THREADS 256
+#define RANK_ROWS 1024
+template <bool SCATTER>
+__global__ __launch_bounds__(RANK_THREADS) void k_leaf_rank(const uint8_t* __restrict__ leaf_of,
+                                                          int64_t n, int32_t nl, int64_t nblk,
+                                                          uint32_t* __restrict__ tab,
+                                                          uint32_t* __restrict__ indices) {
+  constexpr int kWaves = RANK_THREADS / LGBM_WAVE;
+  __shared__ uint32_t run[256];
+  __shared__ uint32_t wc[kWaves][256];
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int64_t blk = blockIdx.x;
+  for (int i = tid; i < 256; i += RANK_THREADS) {
+    run[i] = 0u;
+    for (int w = 0; w < kWaves; ++w) wc[w][i] = 0u;
+  }
+  __syncthreads();
+  for (int k = 0; k < RANK_ROWS / RANK_THREADS; ++k) {
+    const int64_t r = blk * RANK_ROWS + (int64_t)k * RANK_THREADS + tid;
+    const bool valid = r < n;
+    const uint32_t key = valid ? (uint32_t)leaf_of[r] : 0u;
+    unsigned long long peers = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const bool set = (key >> bit) & 1u;
+      const unsigned long long bb = __ballot(set);
+      peers &= set ? bb : ~bb;
+    }
+    const unsigned long long before = peers & lanemask_lt();
+    if (valid && before == 0ull) wc[wave][key] = (uint32_t)__popcll(peers);
+    __syncthreads();
+    if (SCATTER && valid) {
+      uint32_t off = run[key] + (uint32_t)__popcll(before);
+      for (int w = 0; w < wave; ++w) off += wc[w][key];
+      indices[tab[(size_t)key * nblk + blk] + off] = (uint32_t)r;
+    }
+    __syncthreads();
+    for (int i = tid; i < 256; i += RANK_THREADS) {
+      uint32_t add = 0u;
+      for (int w = 0; w < kWaves; ++w) {
+        add += wc[w][i];
+        wc[w][i] = 0u;
+      }
+      run[i] += add;
+    }
+    __syncthreads();
+  }
+  if (!SCATTER)
+    for (int i = tid; i < nl; i += RANK_THREADS) tab[(size_t)i * nblk + blk] = run[i];
+}
+
+// Per leaf (one block each): (leaf, block) counts -> output offsets, starting at the
+// leaf's begin.
+__global__ __launch_bounds__(1024) void k_leaf_rank_offsets(DevLearner L, int64_t nblk,
+                                                            uint32_t* __restrict__ tab) {
+  __shared__ int64_t s_part[1024 / LGBM_WAVE];
+  __shared__ int64_t s_carry;
+  const int32_t l = blockIdx.x;
+  const int tid = threadIdx.x, lane = (int)lane_id(), wave = tid >> 6;
+  uint32_t* row = tab + (size_t)l * nblk;
+  if (tid == 0) s_carry = L.leaves.begin[l];
+  __syncthreads();
+  for (int64_t b0 = 0; b0 < nblk; b0 += 1024) {
+    const int64_t i = b0 + tid;
+    const int64_t v = i < nblk ? (int64_t)row[i] : 0;
+    int64_t incl = v;
+    for (int off = 1; off < LGBM_WAVE; off <<= 1) {
+      const int64_t u = __shfl_up(incl, off);
+      if (lane >= off) incl += u;
+    }
+    if (lane == LGBM_WAVE - 1) s_part[wave] = incl;
+    __syncthreads();
+    int64_t before = s_carry;
+    for (int k = 0; k < wave; ++k) before += s_part[k];
+    if (i < nblk) row[i] = (uint32_t)(before + incl - v);
+    __syncthreads();
+    if (tid == 1023) s_carry = before + incl;
+    __syncthreads();
   }
 }
 
@@ -873,11 +1017,18 @@ void launch_partition(const DevLearner& L, int W, int fp, int64_t blocks, hipStr
   if (blocks < 1) blocks = 1;
   const dim3 g((unsigned)blocks), b(PART_THREADS);
   if (fp) {
-    DISPATCH_W(W, KLAUNCH(ev, (k_partition<kW, 1>), g, b, 0, s, L));
+    DISPATCH_W(W, KLAUNCH(ev, (k_partition<kW, 1, false>), g, b, 0, s, L));
   } else {
     const size_t lds = (size_t)(std::max(L.total_cells, 1) + 4) * sizeof(unsigned long long);
-    DISPATCH_W(W, KLAUNCH(ev, (k_partition<kW, 0>), g, b, lds, s, L));
+    DISPATCH_W(W, KLAUNCH(ev, (k_partition<kW, 0, false>), g, b, lds, s, L));
   }
+}
+void launch_partition_stable(const DevLearner& L, int64_t ntiles, int64_t blocks, hipStream_t s) {
+  if (blocks < 1) blocks = 1;
+  k_tile_count<1><<<dim3((unsigned)ntiles), dim3(PART_THREADS), 0, s>>>(L);
+  k_tile_scan<<<dim3(1), dim3(1024), 0, s>>>(L);
+  const size_t lds = (size_t)(std::max(L.total_cells, 1) + 4) * sizeof(unsigned long long);
+  k_partition<1, 0, true><<<dim3((unsigned)blocks), dim3(PART_THREADS), lds, s>>>(L);
 }
 void launch_pair_scan(const DevLearner& L, int32_t spec_max, hipStream_t s,
                       const KernelEvents* ev) {
@@ -886,10 +1037,21 @@ void launch_pair_scan(const DevLearner& L, int32_t spec_max, hipStream_t s,
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
   KLAUNCH(ev, k_tree_finalize, dim3(1), dim3(256), 0, s, L);
 }
+size_t export_layout_scratch_bytes(int64_t n, int32_t num_leaves) {
+  const int64_t nblk = (n + RANK_ROWS - 1) / RANK_ROWS;
+  return (((size_t)n + 255) & ~(size_t)255) + (size_t)num_leaves * (size_t)nblk * 4;
+}
 void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
-                          hipStream_t s) {
-  DISPATCH_W(L.W, (k_export_layout<kW><<<dim3(64, (unsigned)num_leaves), dim3(256), 0, s>>>(
-                      L, indices)));
+                          void* scratch, hipStream_t s) {
+  const int64_t n = L.N, nblk = (n + RANK_ROWS - 1) / RANK_ROWS;
+  uint8_t* leaf_of = (uint8_t*)scratch;
+  uint32_t* tab = (uint32_t*)((char*)scratch + (((size_t)n + 255) & ~(size_t)255));
+  DISPATCH_W(L.W, (k_leaf_of<kW><<<dim3(64, (unsigned)num_leaves), dim3(256), 0, s>>>(L, leaf_of)));
+  k_leaf_rank<false><<<dim3((unsigned)nblk), dim3(RANK_THREADS), 0, s>>>(leaf_of, n, num_leaves,
+                                                                        nblk, tab, nullptr);
+  k_leaf_rank_offsets<<<dim3((unsigned)num_leaves), dim3(1024), 0, s>>>(L, nblk, tab);
+  k_leaf_rank<true><<<dim3((unsigned)nblk), dim3(RANK_THREADS), 0, s>>>(leaf_of, n, num_leaves,
+                                                                       nblk, tab, indices);
 }
 
 }  // namespace lgbm

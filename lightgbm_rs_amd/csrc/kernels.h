@@ -106,7 +106,7 @@ struct DevLearner {
   int32_t* best_fpos;           // [slot_cap] feature position of best
   uint8_t* splittable;          // [slot_cap][F]
   int32_t* plan_state;          // [5][MAX_LEAVES] leaf / node linkage owned by k_plan
-  uint64_t* tile_state;
+  uint64_t* tile_state;         // stable per-op partition: left-row prefix per tile
   double* stats;                // [0] rows partitioned, [1] partition launches, [2] root
                                 // rows, [3] root launches, [4] partition jobs
   DevNodes nodes;
@@ -145,6 +145,9 @@ void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n
                           lgbm_split_info* out, hipStream_t s);
 void launch_partition(const DevLearner& L, int W, int fp, int64_t blocks, hipStream_t s,
                       const KernelEvents* ev = nullptr);
+// Stable variant for the per-op entry point (job 0, W = 1): tile counts, their
+// prefix, then the partition in DataPartition::split order.
+void launch_partition_stable(const DevLearner& L, int64_t ntiles, int64_t blocks, hipStream_t s);
 void launch_hist_f32(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
 void launch_fp_prep(const DevLearner& L, const float* g, const float* h, int64_t n,
                     const uint4* partials, hipStream_t s);
@@ -154,8 +157,9 @@ void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth
 void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s,
                          const KernelEvents* ev = nullptr);
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
+size_t export_layout_scratch_bytes(int64_t n, int32_t num_leaves);
 void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
-                          hipStream_t s);
+                          void* scratch, hipStream_t s);
 void launch_gather_rows(int W, const uint32_t* rows, int64_t n, const uint4* rec,
                         const uint16_t* gh, const float2* g32, uint4* rec_out, uint16_t* gh_out,
                         float2* g32_out, hipStream_t s);

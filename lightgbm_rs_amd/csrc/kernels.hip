@@ -162,6 +162,7 @@ __global__ __launch_bounds__(256) void k_quant_scales(Ctl* ctl, const uint4* __r
   ctl->vh3 = (float)(3.0 * ctl->hs);
   ctl->const_hess = ch ? 1 : 0;
   ctl->quant_bins = bins;
+  ctl->hmin = s.hmin == 0xffffffffu ? 0.f : f32_from_key(s.hmin);
 }
 
 // ===========================================================================
@@ -644,6 +645,11 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
       L.nodes.sums[0] = LeafSums{sg, sh, weight, nrows, 0};
       if (!(sh > 0.0)) {
         ctl->error |= ERR_ROOT_HESSIAN;
+        ctl->done = 1;
+      }
+      // the packed integer cells hold q_h in [0, bins]
+      if (!fp && ctl->hmin < 0.f) {
+        ctl->error |= ERR_NEG_HESSIAN;
         ctl->done = 1;
       }
     }

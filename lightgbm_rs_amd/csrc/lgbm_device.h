@@ -23,11 +23,17 @@
 #define HIST_BLOCK_MAX_ROWS ((1 << 19) - 1)  // block-shared scheme field limit
 #define HIST_FP_CELLS 3584              // f32 gradients: cells per feature group (16 B each)
 #define MAX_FGROUPS 32
-#define PART_THREADS 1024
-#define PART_WAVES (PART_THREADS / LGBM_WAVE)
+#ifndef PART_THREADS
+#define PART_THREADS 1024               // partition block (one per CU)
+#endif
+#ifndef PART_ROWS_PER_THREAD
 #define PART_ROWS_PER_THREAD 4
+#endif
+#ifndef PART_BLOCKS_PER_CU
+#define PART_BLOCKS_PER_CU 1
+#endif
+#define PART_WAVES (PART_THREADS / LGBM_WAVE)
 #define PART_TILE (PART_THREADS * PART_ROWS_PER_THREAD)
-#define PART_MAX_BLOCKS 256
 #define PART_MIN_TILE 1024                // smallest tile of any partition launch shape
 #define SCAN_THREADS 128                // two waves: smaller leaf, larger leaf
 #define PLAN_THREADS 1024
@@ -47,10 +53,10 @@
 #define NBUF 5
 
 // ctl->error bits
-#define ERR_SPIN 1
 #define ERR_ROOT_HESSIAN 2
 #define ERR_FEATURE 4
 #define ERR_SLOTS 8
+#define ERR_NEG_HESSIAN 16  // quantized histograms: a hessian below zero
 
 struct DevFeature {
   uint32_t num_bin;
@@ -116,7 +122,8 @@ struct HistJob {
 struct Ctl {
   // ---- quantizer (per iteration) ----
   double gs, hs, igs, ihs;
-  float vg1, vh1, vh3, _f0;
+  float vg1, vh1, vh3;
+  float hmin;                        // smallest hessian of the iteration
   int32_t quant_bins;
   int32_t const_hess;
   // ---- tree state ----
@@ -131,10 +138,9 @@ struct Ctl {
   int32_t n_hjobs, _i1;
   HistJob hjobs[SPEC_MAX];
   LeafSums sm;                       // per-op build: the leaf's raw sums
-  // ---- partition round + look-back bookkeeping ----
-  uint32_t epoch;
-  int32_t part_ticket, part_exit;
-  int32_t part_left_count;
+  // ---- partition round ----
+  int32_t part_left_count, _i6;
+  unsigned long long part_cur[SPEC_MAX];  // per job: (left rows, right rows) reserved
   PartJob jobs[SPEC_MAX];
   int32_t reduce_list[2 * SPEC_MAX + 2];
   // ---- gain config ----
