@@ -51,6 +51,7 @@ struct lgbm_hip_ctx {
   double* score = nullptr;
   int32_t* hist_part = nullptr;  // [HIST_SLOTS][cells][3]
   int32_t* hist_acc = nullptr;   // [SPEC_MAX][cells][3]
+  int32_t* part_slots = nullptr; // [part_blocks + SPEC_MAX][cells][3]
   int64_t* hist_part64 = nullptr;  // [HIST_SLOTS][cells][2]
   int64_t* int_slots64 = nullptr;  // [SLOT_CAP][cells][2]
   int32_t n_fgroups = 0;
@@ -192,6 +193,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.slot_len = c->slot_len;
   L.hist_part = c->hist_part;
   L.hist_acc = c->hist_acc;
+  L.part_slots = c->part_slots;
   L.hist_part64 = c->hist_part64;
   L.int_slots64 = c->int_slots64;
   L.n_fgroups = c->n_fgroups;
@@ -431,7 +433,7 @@ void enqueue_rounds(lgbm_hip_ctx* c, int32_t rounds, int32_t fp) {
     launch_plan(L, SLOT_CAP(c->lcap), c->stream, ev_kernel(c, FAM_SCAN, &ke));
     launch_partition(L, c->W, fp, c->part_blocks, c->stream, ev_kernel(c, FAM_PART, &ke));
     if (fp) launch_hist_f32(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
-    launch_pair_scan(L, c->spec_max, c->stream, ev_kernel(c, FAM_SCAN, &ke));
+    launch_pair_scan(L, c->spec_max, c->part_blocks, c->stream, ev_kernel(c, FAM_SCAN, &ke));
   }
 }
 
@@ -682,6 +684,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->score);
   F(c->hist_part);
   F(c->hist_acc);
+  F(c->part_slots);
   F(c->hist_part64);
   F(c->int_slots64);
   F(c->tile_state);
@@ -833,6 +836,7 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   }
   if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * acc * 3))) return rc;
   HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * acc * 3 * 4));
+  if ((rc = dalloc(c, &c->part_slots, ((size_t)c->part_blocks + SPEC_MAX) * acc * 3))) return rc;
   if ((rc = ensure_tile_state(c, num_data))) return rc;
   // transpose the feature-major upload into records
   uint8_t* tmp = nullptr;
@@ -1085,7 +1089,7 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   J.parent = -1;
   J.cl = -1;
   J.cr = -1;
-  J.ntiles = (int32_t)((n + PART_TILE - 1) / PART_TILE);
+  J.ntiles = (int32_t)((n + part_tile(1) - 1) / part_tile(1));
   J.tile0 = 0;
   J.src_buf = BUF_S0;
   J.dst_buf = BUF_S1;

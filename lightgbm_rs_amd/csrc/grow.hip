@@ -415,7 +415,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     // quantized gradients: build the histogram of the side the scan expects to be
     // smaller inside the partition pass (f32: k_hist_f32 builds the smaller child)
     J.acc_right = fp ? -1 : (b.right_count < b.left_count ? 1 : 0);
-    J.ntiles = (int32_t)((J.count + PART_TILE - 1) / PART_TILE);
+    J.ntiles = (int32_t)((J.count + part_tile(L.W) - 1) / part_tile(L.W));
     J.tile0 = 0;
     ctl->jobs[j] = J;
     ctl->part_cur[j] = 0ull;
@@ -462,7 +462,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
 
 // ===========================================================================
 // k_partition: DataPartition::split of every job of the round in one pass.  The
-// tiles of all jobs (job j owns tiles [tile0, tile0 + ntiles), PART_TILE rows each,
+// tiles of all jobs (job j owns tiles [tile0, tile0 + ntiles), part_tile(W) rows each,
 // in the parent's logical row order) are dealt to the blocks in contiguous runs, so a
 // block meets few job boundaries.  A tile ranks its rows with wave ballots, then
 // takes its output ranges:
@@ -486,7 +486,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
 // ===========================================================================
 template <int W, int FP, bool STABLE>
 __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
-  constexpr int PT = PART_THREADS, PR = PART_ROWS_PER_THREAD;
+  constexpr int PT = PART_THREADS, PR = part_rows(W);
   constexpr int kWaves = PT / LGBM_WAVE;
   constexpr int kTile = PT * PR;
   constexpr int kSlots = PR * kWaves;  // (row k, wave) left counts, k-major = row order
@@ -520,27 +520,60 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   int32_t cbr[16 * W];
 #pragma unroll
   for (int f = 0; f < 16 * W; ++f) cbr[f] = __builtin_amdgcn_readfirstlane(cb[f]);
-  int32_t j = 0;
+  int32_t jl = 0;         // job of the last tile loaded
   int32_t cur = -1;       // job whose rows the LDS histogram holds
   int32_t held = 0;       // tiles of that job in the LDS histogram
-  bool flushed = false;   // part of that job already flushed by this block
-  // The accumulator of job `cur` gets this block's cells: plain stores when the block
-  // covers the whole job in one flush, else atomic adds (k_pair_scan clears it).
-  auto flush = [&](bool final_flush) {
+  bool flushed = false;   // this block already flushed part of that job
+  // Where this block's cells of job `cur` go: a job spread over at most PART_SLOT_MAX
+  // blocks gets one slot per block (slot block + job: unique, since blocks and jobs
+  // both advance along the tile order), which k_pair_scan sums; a wider job gets
+  // atomic adds into its accumulator (cleared by k_pair_scan).
+  auto flush = [&]() {
     const PartJob& C = s_jobs[cur];
-    const bool sole = final_flush && !flushed && C.tile0 >= t_lo && C.tile0 + C.ntiles <= t_hi;
-    lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3, sole);
+    const int64_t nblk = part_owner(C.tile0 + C.ntiles - 1, total, G) -
+                         part_owner(C.tile0, total, G) + 1;
+    if (nblk <= PART_SLOT_MAX)
+      lds_hist_flush_clear(lds_hist, cells,
+                           L.part_slots + ((size_t)blockIdx.x + cur) * cells * 3,
+                           flushed ? FLUSH_ADD : FLUSH_STORE);
+    else
+      lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3, FLUSH_ATOMIC);
+  };
+  struct TileBuf {
+    uint4 w[PR][W];
+    GhT q[PR];
+    bool valid[PR];
+  };
+  // Issues every load of tile t at once (positions past the job's end re-read its
+  // last row; a job that owns a tile has count >= 1).  Returns the tile's job.
+  auto load = [&](int64_t t, TileBuf& B) -> int32_t {
+    while (jl + 1 < nj && s_jobs[jl + 1].tile0 <= t) ++jl;
+    const PartJob& J = s_jobs[jl];
+    const int64_t count = J.count, begin = J.begin;
+    const int64_t base = (t - J.tile0) * kTile;
+    const uint4* __restrict__ src = L.bufs.rec[J.src_buf];
+    const GhT* __restrict__ sgh = gh_buf<GhT>(L.bufs, J.src_buf);
+#pragma unroll
+    for (int k = 0; k < PR; ++k) {
+      const int64_t p = base + (int64_t)k * PT + tid;
+      B.valid[k] = p < count;
+      const int64_t pc = B.valid[k] ? p : count - 1;
+      const int64_t phys = J.rev ? begin + count - 1 - pc : begin + pc;
+#pragma unroll
+      for (int i = 0; i < W; ++i) B.w[k][i] = src[phys * W + i];
+      B.q[k] = sgh[phys];
+    }
+    return jl;
   };
   // Shared-state hand-off per tile: s_cnt is written after the loads and read by
   // wave 0 before barrier B; s_pref / s_lbase / s_rbase / s_total / s_last are
   // written by wave 0 between barriers A and B and read after B; the next tile's
   // writes of each come after a barrier every reader has passed.  Histogram adds end
   // before B, so a flush at the top of the next tile sees them all.
-  for (int64_t t = t_lo; t < t_hi; ++t) {
-    while (j + 1 < nj && s_jobs[j + 1].tile0 <= t) ++j;
+  auto process = [&](int64_t t, int32_t j, TileBuf& B) {
     if (FP == 0 && (j != cur || held == kFlushTiles)) {
       if (cur >= 0 && s_jobs[cur].acc_right >= 0 && held > 0) {
-        flush(j != cur);
+        flush();
         flushed = j == cur;
         __syncthreads();
       } else {
@@ -553,25 +586,11 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     const int64_t count = J.count, begin = J.begin;
     const int64_t lt = t - J.tile0;
     const int64_t base = lt * kTile;
-    const uint4* __restrict__ src = L.bufs.rec[J.src_buf];
-    const GhT* __restrict__ sgh = gh_buf<GhT>(L.bufs, J.src_buf);
     uint4* __restrict__ dst = L.bufs.rec[J.dst_buf];
     GhT* __restrict__ dgh = gh_buf<GhT>(L.bufs, J.dst_buf);
-    uint4 w[PR][W];
-    GhT q[PR];
-    bool valid[PR];
-    // every load of the tile in flight at once (positions past the job's end re-read
-    // its last row; a job that owns a tile has count >= 1)
-#pragma unroll
-    for (int k = 0; k < PR; ++k) {
-      const int64_t p = base + (int64_t)k * PT + tid;
-      valid[k] = p < count;
-      const int64_t pc = valid[k] ? p : count - 1;
-      const int64_t phys = J.rev ? begin + count - 1 - pc : begin + pc;
-#pragma unroll
-      for (int i = 0; i < W; ++i) w[k][i] = src[phys * W + i];
-      q[k] = sgh[phys];
-    }
+    auto& w = B.w;
+    auto& q = B.q;
+    auto& valid = B.valid;
     bool isleft[PR];
     int32_t rank[PR];
 #pragma unroll
@@ -680,14 +699,31 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
         ctl->part_left_count = lc;
       }
     }
+  };
+  // Two register buffers: the next tile's loads are in flight while this tile is
+  // ranked, histogrammed and scattered (its stores queue behind those loads).
+  TileBuf b0, b1;
+  int64_t t = t_lo;
+  int32_t j0 = load(t, b0), j1 = 0;
+  while (true) {
+    const bool more1 = t + 1 < t_hi;
+    if (more1) j1 = load(t + 1, b1);
+    process(t, j0, b0);
+    if (!more1) break;
+    ++t;
+    const bool more0 = t + 1 < t_hi;
+    if (more0) j0 = load(t + 1, b0);
+    process(t, j1, b1);
+    if (!more0) break;
+    ++t;
   }
-  if (FP == 0 && cur >= 0 && s_jobs[cur].acc_right >= 0 && held > 0) flush(true);
+  if (FP == 0 && cur >= 0 && s_jobs[cur].acc_right >= 0 && held > 0) flush();
 }
 
 // Stable per-op partition, step 1: the left-row count of every tile of job 0.
 template <int W>
 __global__ __launch_bounds__(PART_THREADS) void k_tile_count(DevLearner L) {
-  constexpr int PT = PART_THREADS, PR = PART_ROWS_PER_THREAD, kTile = PT * PR;
+  constexpr int PT = PART_THREADS, PR = part_rows(W), kTile = PT * PR;
   __shared__ int32_t s_w[PT / LGBM_WAVE];
   const PartJob J = L.ctl->jobs[0];
   const int64_t t = blockIdx.x;
@@ -753,7 +789,7 @@ __global__ __launch_bounds__(1024) void k_tile_scan(DevLearner L) {
 //   (before_find_best_split, learner.rs:1808-1839: max_depth reached, or both below
 //   2 * min_data_in_leaf rows) are not built or scanned.
 // ===========================================================================
-__global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L) {
+__global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_t part_grid) {
   __shared__ double cs[2 * 256];
   __shared__ double cp[2 * 256];
   Ctl* ctl = L.ctl;
@@ -793,15 +829,35 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L) {
       }
     }
   }
+  // the side built in the partition pass: the job's per-block slots (the blocks of
+  // the partition launch from the one holding its first tile to the one holding its
+  // last, slot = block + j; blocks without tiles wrote nothing), or its accumulator
   int32_t* acc = L.hist_acc + (size_t)j * cells * 3;
+  const int64_t T = ctl->tile_total;
+  const int64_t s0 = J.ntiles > 0 ? part_owner(J.tile0, T, part_grid) : 0;
+  const int64_t s1 = J.ntiles > 0 ? part_owner(J.tile0 + J.ntiles - 1, T, part_grid) : -1;
+  const bool use_slots = s1 - s0 + 1 <= PART_SLOT_MAX;
   const int nbq = ctl->fp_mode ? 0 : nb;  // quantized gradients only
   for (int b = tid; b < nbq; b += SCAN_THREADS) {
     const size_t ci = (size_t)(ft.cell_base + b);
-    int32_t* a = acc + ci * 3;
-    const int32_t AG = a[0], AH = a[1], AT = a[2];  // the side built in the partition pass
-    a[0] = 0;
-    a[1] = 0;
-    a[2] = 0;
+    int32_t AG = 0, AH = 0, AT = 0;
+    if (use_slots) {
+      for (int64_t k = s0; k <= s1; ++k) {
+        if (k * T / part_grid >= (k + 1) * T / part_grid) continue;  // a block with no tiles
+        const int32_t* a = L.part_slots + ((size_t)(k + j) * cells + ci) * 3;
+        AG += a[0];
+        AH += a[1];
+        AT += a[2];
+      }
+    } else {
+      int32_t* a = acc + ci * 3;
+      AG = a[0];
+      AH = a[1];
+      AT = a[2];
+      a[0] = 0;
+      a[1] = 0;
+      a[2] = 0;
+    }
     if (gated) continue;
     const int32_t* ps = L.int_slots + ((size_t)p * cells + ci) * 3;
     const int32_t OG = ps[0] - AG, OH = ps[1] - AH, OT = ps[2] - AT;  // exact
@@ -1030,9 +1086,10 @@ void launch_partition_stable(const DevLearner& L, int64_t ntiles, int64_t blocks
   const size_t lds = (size_t)(std::max(L.total_cells, 1) + 4) * sizeof(unsigned long long);
   k_partition<1, 0, true><<<dim3((unsigned)blocks), dim3(PART_THREADS), lds, s>>>(L);
 }
-void launch_pair_scan(const DevLearner& L, int32_t spec_max, hipStream_t s,
+void launch_pair_scan(const DevLearner& L, int32_t spec_max, int32_t part_grid, hipStream_t s,
                       const KernelEvents* ev) {
-  KLAUNCH(ev, k_pair_scan, dim3((unsigned)L.F, (unsigned)spec_max), dim3(SCAN_THREADS), 0, s, L);
+  KLAUNCH(ev, k_pair_scan, dim3((unsigned)L.F, (unsigned)spec_max), dim3(SCAN_THREADS), 0, s, L,
+          part_grid);
 }
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
   KLAUNCH(ev, k_tree_finalize, dim3(1), dim3(256), 0, s, L);

@@ -94,6 +94,7 @@ struct DevLearner {
   uint64_t slot_len;
   int32_t* hist_part;         // [HIST_SLOTS][total_cells][3] root / per-op partials
   int32_t* hist_acc;          // [SPEC_MAX][total_cells][3] per-job accumulators
+  int32_t* part_slots;        // [part blocks + SPEC_MAX][total_cells][3] (block, job) cells
   // f32-gradient training: 64-bit fixed-point (g, h) cells
   int64_t* hist_part64;       // [HIST_SLOTS][total_cells][2]
   int64_t* int_slots64;       // [slot_cap][total_cells][2]
@@ -138,7 +139,7 @@ void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hip
                     const KernelEvents* ev = nullptr);
 void launch_plan(const DevLearner& L, int32_t slot_cap, hipStream_t s,
                  const KernelEvents* ev = nullptr);
-void launch_pair_scan(const DevLearner& L, int32_t spec_max, hipStream_t s,
+void launch_pair_scan(const DevLearner& L, int32_t spec_max, int32_t part_grid, hipStream_t s,
                       const KernelEvents* ev = nullptr);
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,

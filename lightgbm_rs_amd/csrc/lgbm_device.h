@@ -24,16 +24,16 @@
 #define HIST_FP_CELLS 3584              // f32 gradients: cells per feature group (16 B each)
 #define MAX_FGROUPS 32
 #ifndef PART_THREADS
-#define PART_THREADS 1024               // partition block (one per CU)
+#define PART_THREADS 512                // partition block (two per CU)
 #endif
 #ifndef PART_ROWS_PER_THREAD
-#define PART_ROWS_PER_THREAD 4
+#define PART_ROWS_PER_THREAD 4          // records of <= 32 B; fewer for wider records
 #endif
 #ifndef PART_BLOCKS_PER_CU
-#define PART_BLOCKS_PER_CU 1
+#define PART_BLOCKS_PER_CU 2
 #endif
 #define PART_WAVES (PART_THREADS / LGBM_WAVE)
-#define PART_TILE (PART_THREADS * PART_ROWS_PER_THREAD)
+#define PART_SLOT_MAX 8                 // blocks per job whose cells go to per-block slots
 #define PART_MIN_TILE 1024                // smallest tile of any partition launch shape
 #define SCAN_THREADS 128                // two waves: smaller leaf, larger leaf
 #define PLAN_THREADS 1024
@@ -57,6 +57,20 @@
 #define ERR_FEATURE 4
 #define ERR_SLOTS 8
 #define ERR_NEG_HESSIAN 16  // quantized histograms: a hessian below zero
+
+// Partition rows per thread for a W-word record: two tiles of records stay in
+// registers (the next tile's loads overlap this tile's work) within 128 VGPRs.
+__host__ __device__ constexpr int part_rows(int W) {
+  return W <= 2 ? PART_ROWS_PER_THREAD : (W <= 4 ? 2 : 1);
+}
+__host__ __device__ constexpr int64_t part_tile(int W) {
+  return (int64_t)PART_THREADS * part_rows(W);
+}
+// Block b of a G-block partition launch over T tiles takes tiles [b*T/G, (b+1)*T/G);
+// the block that takes tile t:
+__host__ __device__ inline int64_t part_owner(int64_t t, int64_t T, int64_t G) {
+  return ((t + 1) * G - 1) / T;
+}
 
 struct DevFeature {
   uint32_t num_bin;

@@ -394,6 +394,35 @@ def test_speculative_rounds_match_oracle(spec, rounds):
         b.close()
 
 
+@pytest.mark.parametrize("blocks", [1, 37, 1000])
+def test_partition_grid_shapes_match_oracle(blocks):
+    """Partition launches of any width grow the oracle's tree: one block (all tiles of
+    the root job in one block, so its histogram is flushed mid-job into the same
+    slot), an odd width (slots of narrow jobs, accumulators of wide ones), and more
+    blocks than tiles (blocks without tiles inside a job's block span)."""
+    n, nl = 600_000, 63
+    say(f"partition grid blocks={blocks}")
+    bins, meta, ub, _ = config1_like(n, seed=41)
+    g, h, _ = binary_gh(n, seed=41)
+    os.environ["LGBM_HIP_PART_BLOCKS"] = str(blocks)
+    try:
+        b = HipBackend(0)
+    finally:
+        del os.environ["LGBM_HIP_PART_BLOCKS"]
+    try:
+        b.upload_resident_bins(bins, meta, ub)
+        b.upload_resident_grad_hess(g, h)
+        _, dg, dh = b.discretize_dequantize_in_place(4, True, 7, want_values=True)
+        og, oh, _, _ = oracle.quantize(g, h, bins=4, stochastic=True, seed=7)
+        cfg = GainConfig.make(min_data_in_leaf=20)
+        t, lay = b.grow_tree_on_device_with_cfg(cfg, nl, -1)
+        o, olay = oracle.train_tree(bins, meta, ub, og, oh, cfg, nl, -1)
+        _compare_trees(t, o, ("grid", blocks))
+        assert np.array_equal(lay["indices"], olay["indices"])
+    finally:
+        b.close()
+
+
 def test_tied_leaf_gains_break_by_leaf_id(be):
     """Mirrored groups: rows of group B repeat the bins of group A except for a marker
     feature and carry negated gradients (deterministic rounding keeps q(-g) = -q(g));
