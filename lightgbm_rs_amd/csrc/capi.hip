@@ -974,6 +974,8 @@ int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, in
   if (!fp && c->quant_bins != 2 && c->quant_bins != 4)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "exact f64 histogram requires num_grad_quant_bins in {2, 4}");
+  if (!fp && c->N >= QUANT_MAX_ROWS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
   DevLearner L0 = make_learner(c);
   if (fp) {
@@ -1138,6 +1140,8 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num
   if (!fp && c->quant_bins != 2 && c->quant_bins != 4)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "device learner requires num_grad_quant_bins in {2, 4}");
+  if (!fp && c->N >= QUANT_MAX_ROWS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
   if (fp) {
     if ((rc = ensure_fp(c))) return rc;
     if ((rc = ensure_leaves(c, num_leaves))) return rc;
@@ -1178,6 +1182,8 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
   if (!fp && num_grad_quant_bins != 2 && num_grad_quant_bins != 4)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "device learner requires num_grad_quant_bins in {0, 2, 4}");
+  if (!fp && c->N >= QUANT_MAX_ROWS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
   if (fp) {
     if ((rc = ensure_fp(c))) return rc;
     if ((rc = ensure_leaves(c, num_leaves))) return rc;

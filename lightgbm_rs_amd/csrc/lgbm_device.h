@@ -34,6 +34,7 @@
 #endif
 #define PART_WAVES (PART_THREADS / LGBM_WAVE)
 #define PART_SLOT_MAX 8                 // blocks per job whose cells go to per-block slots
+#define QUANT_MAX_ROWS (1ll << 29)      // int32 cells: sum of q_h <= 4 N < 2^31
 #define PART_MIN_TILE 1024                // smallest tile of any partition launch shape
 #define SCAN_THREADS 128                // two waves: smaller leaf, larger leaf
 #define PLAN_THREADS 1024
