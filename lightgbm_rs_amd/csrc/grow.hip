@@ -115,70 +115,56 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
   }
 }
 
+// Leaf keys in the reference's ArgMax order (split_gt, split_info.rs:28-35: higher
+// gain, then lower real feature index with -1 last; then the lower leaf id, the
+// first-max-wins scan of learner.rs:4537) packed into 128 bits that compare as
+// unsigned integers.  Only positive gains qualify (smaller ones stop the tree): any
+// other leaf gets 0, below every qualifying key.  The bit pattern of a positive
+// double orders like the double.
+struct LKey {
+  uint64_t hi, lo;
+};
+__device__ __forceinline__ LKey lkey(double gain, int32_t feat, int32_t leaf) {
+  if (!(gain > 0.0)) return LKey{0ull, 0ull};
+  const uint32_t f = feat == -1 ? 0x7fffffffu : (uint32_t)feat;
+  return LKey{(uint64_t)__double_as_longlong(gain),
+              ((uint64_t)(0x7fffffffu - f) << 32) | (uint64_t)(0xffffffffu - (uint32_t)leaf)};
+}
+__device__ __forceinline__ bool lk_gt(const LKey& a, const LKey& b) {
+  return a.hi > b.hi || (a.hi == b.hi && a.lo > b.lo);
+}
+__device__ __forceinline__ LKey lk_max(const LKey& a, const LKey& b) { return lk_gt(a, b) ? a : b; }
+__device__ __forceinline__ LKey lk_shfl_up(const LKey& k, int off) {
+  return LKey{(uint64_t)__shfl_up((unsigned long long)k.hi, off),
+              (uint64_t)__shfl_up((unsigned long long)k.lo, off)};
+}
+__device__ __forceinline__ LKey lk_readlane(const LKey& k, int lane) {
+  auto rl = [&](uint64_t v) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane) << 32) |
+           (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  };
+  return LKey{rl(k.hi), rl(k.lo)};
+}
+
 // ===========================================================================
 // k_plan: one block.
 //   0. one prefetch of everything it reads (control block, features, node-slot keys,
 //      leaf / node linkage) into LDS;
 //   1. per-leaf feature ArgMax for the node slots scanned since the last plan
 //      (the argmax of scan_leaf_histogram, learner.rs:3290-3330), one wave per slot;
-//   2. commit loop (wave 0): repeat the reference's ArgMax over the committed leaves
+//   2. commits: the reference's repeated ArgMax over the committed leaves
 //      (learner.rs:4537, split_gt order, first leaf id wins) and its stop test
 //      (gain <= 0, learner.rs:1503; num_leaves - 1 splits at most); while the chosen
 //      leaf has already been split, commit that split: node = num_leaves - 1, the
 //      left child keeps the leaf id, the right child gets id num_leaves
-//      (tree.rs:614-700);
-//   3. selection (wave 0): the chosen leaf, then the next best-ranked unsplit leaves
-//      with gain > 0, up to spec_max, while two node slots per split the tree may
-//      still need stay in reserve;
+//      (tree.rs:614-700).  Computed as a rank of the split leaves and one pass;
+//   3. selection: the chosen leaf, then the next best-ranked unsplit leaves with
+//      gain > 0, up to spec_max, while two node slots per split the tree may still
+//      need stay in reserve (ranks counted in parallel);
 //   4. (all threads) the Tree::split fields of the committed splits, the partition
 //      jobs (with zeroed output cursors) and child node slots of the selected leaves.
 // A slot's best split is feat_split[slot * F + best_fpos[slot]].
 // ===========================================================================
-// ArgMax over the leaves held by a wave (lane l: leaves l + 64 i, i < PL) in the
-// reference's order: the highest gain, then the lower real feature index (-1 last),
-// then the lower leaf id (split_gt, split_info.rs:28-35; ArgMax's first-max-wins
-// scan, learner.rs:4537).  Only positive gains qualify (smaller ones stop the tree);
-// `cand` (optional) masks leaves out.  Returns the leaf id, or -1.  The bit pattern
-// of a positive double orders like the double, so the maximum gain is one u64
-// reduction; equal gains (the only case where the other keys matter) take the full
-// comparison.  Wave-uniform; requires all 64 lanes active.
-template <int PL>
-__device__ __forceinline__ int32_t plan_argmax(const double (&kg)[PL], const int32_t (&kf)[PL],
-                                               const bool* cand, int32_t nl) {
-  const int lane = (int)lane_id();
-  uint64_t k[PL];
-  uint64_t lm = 0ull;
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const bool ok = (lane + LGBM_WAVE * i < nl) && kg[i] > 0.0 && (cand == nullptr || cand[i]);
-    k[i] = ok ? (uint64_t)__double_as_longlong(kg[i]) : 0ull;
-    lm = k[i] > lm ? k[i] : lm;
-  }
-  const uint64_t m = wave_max_u64(lm);
-  if (m == 0ull) return -1;
-  int cnt = 0, mi = 0;
-#pragma unroll
-  for (int i = PL - 1; i >= 0; --i)
-    if (k[i] == m) {
-      ++cnt;
-      mi = i;
-    }
-  const unsigned long long any = __ballot(cnt > 0);
-  const unsigned long long multi = __ballot(cnt > 1);
-  if (multi == 0ull && __popcll(any) == 1) {
-    const int w = __ffsll(any) - 1;
-    return w + LGBM_WAVE * readlane_i32(mi, w);
-  }
-  // a gain tie: full order among the tied leaves
-  BestKey lb{-__builtin_inf(), -1, 0x7fffffff};
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const BestKey c{kg[i], kf[i], lane + LGBM_WAVE * i};
-    if (k[i] == m && key_better(c, lb)) lb = c;
-  }
-  return wave_best(lb).idx;
-}
-
 __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slot_cap) {
   __shared__ double s_gain[SLOT_CAP(MAX_LEAVES)];
   __shared__ int32_t s_feat[SLOT_CAP(MAX_LEAVES)];
@@ -193,7 +179,13 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   __shared__ int4 s_pick[SPEC_MAX];        // (leaf, node slot, left slot, right slot)
   __shared__ int32_t s_red[2 * SPEC_MAX + 2];
   __shared__ int32_t s_ntiles[SPEC_MAX];
-  __shared__ int32_t s_nc, s_nj, s_nl, s_done, s_nslots;
+  __shared__ int32_t s_nc, s_nj, s_nl, s_done, s_nslots, s_nS, s_ncand;
+  __shared__ unsigned long long s_uhi, s_ulo;  // best unsplit leaf key at the start
+  __shared__ LKey s_key[MAX_LEAVES];       // per leaf: its ArgMax key
+  __shared__ LKey s_ck[MAX_LEAVES];        //   the same for selection candidates, else 0
+  __shared__ int32_t s_S[MAX_LEAVES];      // split, uncommitted leaves
+  __shared__ LKey s_SK[MAX_LEAVES];        //   and their keys
+  __shared__ int32_t s_sorted[MAX_LEAVES]; //   in key order
   Ctl* ctl = L.ctl;
   const int tid = threadIdx.x;
   const int lane = (int)lane_id();
@@ -208,6 +200,12 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   const int32_t nred = ctl->n_reduce, spec = ctl->spec_max, cerr = ctl->error;
   const bool fp = ctl->fp_mode != 0;
   if (tid < 2 * SPEC_MAX + 2) s_red[tid] = ctl->reduce_list[tid];
+  if (tid == 0) {
+    s_nS = 0;
+    s_ncand = 0;
+    s_uhi = 0ull;
+    s_ulo = 0ull;
+  }
   for (int f = tid; f < F; f += PLAN_THREADS) s_ft[f] = L.feats[f];
   for (int s = tid; s < slot_cap; s += PLAN_THREADS) {
     s_gain[s] = nd.key_gain[s];
@@ -243,111 +241,156 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   }
   __syncthreads();
 
-  // ---- 2./3. commit loop and selection (wave 0) -------------------------------
-  // Lane l holds the keys of leaves l, l + 64, l + 128, l + 192 in registers; the
-  // rest of a leaf's state (node slot, speculated children and their keys, parent
-  // node and side) is in LDS by leaf id, so a commit reads it in one LDS round trip.
+  // ---- 2. commits ------------------------------------------------------------
+  // Leaves split in earlier rounds but not committed yet (S) keep their keys, and a
+  // commit only adds its two fresh, unsplit children.  So the reference's repeated
+  // ArgMax commits S in key order for as long as the next S key beats the best
+  // unsplit key so far (the best unsplit leaf at the start, raised by the children
+  // of each commit); the right child of the i-th commit gets leaf id nl0 + i.  With S
+  // ranked, that is one exclusive prefix maximum over the ranks and a ballot.
   for (int l = tid; l < nl0; l += PLAN_THREADS) {
-    const int2 ch = s_child[s_ps[PS_LEAF_SLOT][l]];
+    const int32_t s = s_ps[PS_LEAF_SLOT][l];
+    const int2 ch = s_child[s];
+    const LKey k = lkey(s_gain[s], s_feat[s], l);
     s_lc[l] = ch;
+    s_key[l] = k;
     if (ch.x >= 0) {
       s_lcg[l] = make_double2(s_gain[ch.x], s_gain[ch.y]);
       s_lcf[l] = make_int2(s_feat[ch.x], s_feat[ch.y]);
+      if (k.hi != 0ull) {
+        const int32_t pos = atomicAdd(&s_nS, 1);
+        s_S[pos] = l;
+        s_SK[pos] = k;
+      }
+    } else if (k.hi != 0ull) {
+      atomicMax(&s_uhi, (unsigned long long)k.hi);
     }
   }
   __syncthreads();
+  for (int l = tid; l < nl0; l += PLAN_THREADS) {
+    const LKey k = s_key[l];
+    if (s_lc[l].x < 0 && k.hi != 0ull && k.hi == s_uhi) atomicMax(&s_ulo, (unsigned long long)k.lo);
+  }
+  const int32_t nS = s_nS;
+  for (int i = tid; i < nS; i += PLAN_THREADS) {  // rank of each S leaf within S
+    const LKey c = s_SK[i];
+    int32_t r = 0;
+#pragma unroll 4
+    for (int k = 0; k < nS; ++k) r += lk_gt(s_SK[k], c) ? 1 : 0;
+    s_sorted[r] = s_S[i];
+  }
+  __syncthreads();
   if (wave == 0) {
-    constexpr int PL = MAX_LEAVES / LGBM_WAVE;
-    int32_t nl = nl0, nc = 0, ns = ns0, nj = 0;
-    int32_t done = cerr ? 1 : 0;
-    double kg[PL];
-    int32_t kf[PL];
+    LKey P{s_uhi, s_ulo};  // best unsplit key so far (0: none)
+    int32_t nc = 0;
+    bool stop = cerr != 0;
+    for (int base = 0; base < nS && !stop; base += LGBM_WAVE) {
+      const int i = base + lane;
+      const bool in = i < nS;
+      LKey e{0ull, 0ull}, M{0ull, 0ull};
+      if (in) {
+        const int32_t l = s_sorted[i];
+        const double2 cg = s_lcg[l];
+        const int2 cf = s_lcf[l];
+        e = s_key[l];
+        M = lk_max(lkey(cg.x, cf.x, l), lkey(cg.y, cf.y, nl0 + i));  // Tree::split ids
+      }
+      LKey inc = M;  // inclusive prefix maximum of the children keys
 #pragma unroll
-    for (int i = 0; i < PL; ++i) {
-      const int l = lane + LGBM_WAVE * i;
-      kg[i] = ninf;
-      kf[i] = -1;
-      if (l < nl) {
-        const int32_t s = s_ps[PS_LEAF_SLOT][l];
-        kg[i] = s_gain[s];
-        kf[i] = s_feat[s];
+      for (int off = 1; off < LGBM_WAVE; off <<= 1) {
+        const LKey o = lk_shfl_up(inc, off);
+        if (lane >= off) inc = lk_max(inc, o);
       }
-    }
-    while (!done) {
-      const int32_t bl = plan_argmax<PL>(kg, kf, nullptr, nl);
-      if (bl < 0 || nl >= maxl) {  // no positive gain left, or all leaves used
-        done = 1;
-        break;
-      }
-      const int2 ch = s_lc[bl];
-      if (ch.x < 0) break;  // not split yet: it leads the next round
-      const double2 cg = s_lcg[bl];
-      const int2 cf = s_lcf[bl];
-      const int32_t p = s_ps[PS_LEAF_SLOT][bl];
-      const int32_t pn = s_ps[PS_LEAF_PARENT][bl], side = s_ps[PS_LEAF_SIDE][bl];
-      const int32_t node = nl - 1, nr = nl;
-      if (lane == 0) {
-        if (pn >= 0) s_ps[side ? PS_NODE_RIGHT : PS_NODE_LEFT][pn] = node;
-        s_ps[PS_NODE_LEFT][node] = ~bl;
-        s_ps[PS_NODE_RIGHT][node] = ~nr;
-        s_ps[PS_LEAF_SLOT][bl] = ch.x;
-        s_ps[PS_LEAF_SLOT][nr] = ch.y;
-        s_ps[PS_LEAF_PARENT][bl] = node;
-        s_ps[PS_LEAF_PARENT][nr] = node;
-        s_ps[PS_LEAF_SIDE][bl] = 0;
-        s_ps[PS_LEAF_SIDE][nr] = 1;
-        s_lc[bl] = make_int2(-1, -1);  // fresh leaves: not split yet
-        s_lc[nr] = make_int2(-1, -1);
-        s_commit[nc] = make_int4(bl, p, node, nr);
-      }
-#pragma unroll
-      for (int i = 0; i < PL; ++i) {
-        const int l = lane + LGBM_WAVE * i;
-        if (l == bl) {
-          kg[i] = cg.x;
-          kf[i] = cf.x;
-        }
-        if (l == nr) {
-          kg[i] = cg.y;
-          kf[i] = cf.y;
-        }
-      }
-      ++nc;
-      ++nl;
-    }
-    if (!done) {
-      // The first pick is the ArgMax leaf the commit loop stopped at.  Further picks
-      // keep two node slots in reserve for every split the tree may still need, so
-      // the ArgMax leaf of every later round can always be split.
-      bool cand[PL];
-#pragma unroll
-      for (int i = 0; i < PL; ++i) {
-        const int l = lane + LGBM_WAVE * i;
-        cand[i] = l < nl && kg[i] > 0.0 && s_lc[l].x < 0;
-      }
-      while (nj < spec) {
-        const int32_t l = plan_argmax<PL>(kg, kf, cand, nl);
-        if (l < 0) break;
-        if (nj == 0 ? ns + 2 > slot_cap : ns + 2 + 2 * (maxl - nl) > slot_cap) break;
-#pragma unroll
-        for (int i = 0; i < PL; ++i)
-          if (lane + LGBM_WAVE * i == l) cand[i] = false;
-        if (lane == 0) s_pick[nj] = make_int4(l, s_ps[PS_LEAF_SLOT][l], ns, ns + 1);
-        ns += 2;
-        ++nj;
-      }
-      if (nj == 0) {  // the slot reserve makes this unreachable
-        done = 1;
-        if (lane == 0) atomicOr(&ctl->error, ERR_SLOTS);
-      }
+      LKey ex = lk_shfl_up(inc, 1);
+      if (lane == 0) ex = LKey{0ull, 0ull};
+      ex = lk_max(ex, P);
+      const bool ok = in && i < maxl - nl0 && lk_gt(e, ex);
+      const unsigned long long okm = __ballot(ok);
+      const int run = okm == ~0ull ? LGBM_WAVE : (int)__builtin_ctzll(~okm);
+      if (run > 0) P = lk_max(P, lk_readlane(inc, run - 1));
+      nc = base + run;
+      stop = run < LGBM_WAVE;
     }
     if (lane == 0) {
+      const int32_t nl = nl0 + nc;
+      // the stop test of the next ArgMax: no positive gain left, or all leaves used
+      const bool done = cerr != 0 || nl >= maxl || (nc == nS && P.hi == 0ull);
       s_nc = nc;
-      s_nj = nj;
       s_nl = nl;
-      s_done = done;
-      s_nslots = ns;
+      s_done = done ? 1 : 0;
     }
+  }
+  __syncthreads();
+  const int32_t nc_ = s_nc, nl_ = s_nl;
+  for (int c = tid; c < nc_; c += PLAN_THREADS) {
+    // commit c: node nl0 - 1 + c, left child keeps the leaf id, right child nl0 + c.
+    // Committed leaves are distinct leaves of earlier rounds, so these writes are
+    // disjoint.
+    const int32_t bl = s_sorted[c], node = nl0 - 1 + c, nr = nl0 + c;
+    const int2 ch = s_lc[bl];
+    const double2 cg = s_lcg[bl];
+    const int2 cf = s_lcf[bl];
+    const int32_t p = s_ps[PS_LEAF_SLOT][bl];
+    const int32_t pn = s_ps[PS_LEAF_PARENT][bl], side = s_ps[PS_LEAF_SIDE][bl];
+    if (pn >= 0) s_ps[side ? PS_NODE_RIGHT : PS_NODE_LEFT][pn] = node;
+    s_ps[PS_NODE_LEFT][node] = ~bl;
+    s_ps[PS_NODE_RIGHT][node] = ~nr;
+    s_ps[PS_LEAF_SLOT][bl] = ch.x;
+    s_ps[PS_LEAF_SLOT][nr] = ch.y;
+    s_ps[PS_LEAF_PARENT][bl] = node;
+    s_ps[PS_LEAF_PARENT][nr] = node;
+    s_ps[PS_LEAF_SIDE][bl] = 0;
+    s_ps[PS_LEAF_SIDE][nr] = 1;
+    s_lc[bl] = make_int2(-1, -1);  // fresh leaves: not split yet
+    s_lc[nr] = make_int2(-1, -1);
+    s_key[bl] = lkey(cg.x, cf.x, bl);
+    s_key[nr] = lkey(cg.y, cf.y, nr);
+    s_commit[c] = make_int4(bl, p, node, nr);
+  }
+  __syncthreads();
+
+  // ---- 3. selection ------------------------------------------------------------
+  // The ArgMax leaf, then the next best-ranked unsplit leaves with gain > 0, up to
+  // spec_max; beyond the first, two node slots stay in reserve for every split the
+  // tree may still need, so the ArgMax leaf of every later round can be split.  Each
+  // candidate's rank (number of better candidates) is counted by 4 threads.
+  if (!s_done) {
+    const int32_t nl = nl_;
+    for (int l = tid; l < nl; l += PLAN_THREADS) {
+      const LKey k = s_key[l];
+      const bool cand = s_lc[l].x < 0 && k.hi != 0ull;
+      s_ck[l] = cand ? k : LKey{0ull, 0ull};
+      if (cand) atomicAdd(&s_ncand, 1);
+    }
+    __syncthreads();
+    int32_t allowed = 0;
+    if (ns0 + 2 <= slot_cap) {
+      const int32_t extra = (slot_cap - ns0 - 2 - 2 * (maxl - nl)) / 2;
+      allowed = min(spec, 1 + max(extra, 0));
+    }
+    const int32_t l = tid >> 2, q = tid & 3;
+    const LKey c = l < nl ? s_ck[l] : LKey{0ull, 0ull};
+    int32_t r = 0;
+    if (c.hi != 0ull) {
+#pragma unroll 4
+      for (int m = q; m < nl; m += 4) r += lk_gt(s_ck[m], c) ? 1 : 0;
+    }
+    r += __shfl_xor(r, 1);
+    r += __shfl_xor(r, 2);
+    if (q == 0 && c.hi != 0ull && r < allowed)
+      s_pick[r] = make_int4(l, s_ps[PS_LEAF_SLOT][l], ns0 + 2 * r, ns0 + 2 * r + 1);
+    if (tid == 0) {
+      const int32_t nj = min(s_ncand, allowed);
+      s_nj = nj;
+      s_nslots = ns0 + 2 * nj;
+      if (nj == 0) {  // the slot reserve makes this unreachable
+        s_done = 1;
+        atomicOr(&ctl->error, ERR_SLOTS);
+      }
+    }
+  } else if (tid == 0) {
+    s_nj = 0;
+    s_nslots = ns0;
   }
   __syncthreads();
 

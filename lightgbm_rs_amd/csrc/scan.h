@@ -359,46 +359,6 @@ __device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* 
   __syncthreads();
 }
 
-// One DPP row-rotate of a 64-bit value (all 64 lanes active).
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-  const uint32_t lo =
-      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
-  const uint32_t hi =
-      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
-  return ((uint64_t)hi << 32) | lo;
-}
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// Wave-wide maximum of an unsigned 64-bit value, uniform result.  Row rotations by
-// 1, 2, 4, 8 leave every lane of a 16-lane row holding the row maximum; the four
-// row maxima are then combined from lanes 0, 16, 32, 48.  Requires all 64 lanes
-// active.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  uint64_t t;
-  t = dpp_u64<0x121>(v);  // row_ror:1
-  v = t > v ? t : v;
-  t = dpp_u64<0x122>(v);  // row_ror:2
-  v = t > v ? t : v;
-  t = dpp_u64<0x124>(v);  // row_ror:4
-  v = t > v ? t : v;
-  t = dpp_u64<0x128>(v);  // row_ror:8
-  v = t > v ? t : v;
-  uint64_t m = readlane_u64(v, 0);
-  uint64_t a = readlane_u64(v, 16);
-  m = a > m ? a : m;
-  a = readlane_u64(v, 32);
-  m = a > m ? a : m;
-  a = readlane_u64(v, 48);
-  m = a > m ? a : m;
-  return m;
-}
-
-
 // Moves a block's packed LDS histogram (fields: q_g sum signed 22 bits, q_h sum 21
 // bits, count of q_h == 3 21 bits) into integer cells out[c] = (G, H, T) and clears
 // it (the trash cells too).  mode FLUSH_ATOMIC: atomic adds into a shared
