@@ -159,15 +159,19 @@ int init_jump_tables(lgbm_hip_ctx* c) {
   for (int i = 0; i < 64; ++i) m[i] = xs_step(1ull << i);
   // T = M^(2*C): two draws per row, C rows per lane
   Mat t = m;
-  static_assert(QUANT_ROWS_PER_LANE == 16, "2*C must be 32 = 2^5");
-  for (int i = 0; i < 5; ++i) t = mat_mul(t, t);
-  std::vector<uint64_t> lane(QUANT_LANE_MATS * 64), wave(QUANT_WAVE_MATS * 64);
-  Mat r = t;
-  for (int k = 0; k < QUANT_LANE_MATS; ++k) {
-    std::copy(r.begin(), r.end(), lane.begin() + k * 64);
-    if (k + 1 < QUANT_LANE_MATS) r = mat_mul(r, r);
+  static_assert((QUANT_ROWS_PER_LANE & (QUANT_ROWS_PER_LANE - 1)) == 0, "C must be a power of 2");
+  for (int k = 1; k < 2 * QUANT_ROWS_PER_LANE; k *= 2) t = mat_mul(t, t);
+  // lane table: T^l for l = 0..63, stored column-major across lanes
+  // (entry [i][l] = column i of T^l) so a wave reads one column of every lane's
+  // matrix in one coalesced load
+  std::vector<uint64_t> lane(64 * 64), wave(QUANT_WAVE_MATS * 64);
+  Mat r;
+  for (int i = 0; i < 64; ++i) r[i] = 1ull << i;  // T^0
+  for (int l = 0; l < 64; ++l) {
+    for (int i = 0; i < 64; ++i) lane[(size_t)i * 64 + l] = r[i];
+    r = mat_mul(r, t);
   }
-  Mat p = mat_mul(r, r);  // T^64 = M^(2*C*64)
+  Mat p = r;  // T^64 = M^(2*C*64): one wave's rows
   for (int k = 0; k < QUANT_WAVE_MATS; ++k) {
     std::copy(p.begin(), p.end(), wave.begin() + k * 64);
     p = mat_mul(p, p);
@@ -298,6 +302,8 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   if ((rc = dalloc(c, &c->leaves.buf, (size_t)L))) return rc;
   if ((rc = dalloc(c, &c->leaves.rev, (size_t)L))) return rc;
   if ((rc = dalloc(c, &c->tree.nodes, (size_t)L))) return rc;
+  if ((rc = dalloc(c, &c->tree.route_mask, (size_t)L * 8))) return rc;
+  if ((rc = dalloc(c, &c->tree.route_node, (size_t)L))) return rc;
   // tree arrays: one device blob (one readback per tree) + pinned host staging
   const size_t sizes[15] = {64, 4, 4, 8, 4, 1, 4, 4, 8, 4, 8, 8, 4, 4, 4};
   size_t off = 0;
@@ -717,6 +723,8 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->leaves.rev);
   DevTree& T = c->tree;
   F(T.nodes);
+  F(T.route_mask);
+  F(T.route_node);
   F(c->scratch);
   F(c->slot_tmp);
   F(c->d_indices);

@@ -992,6 +992,14 @@ __global__ void k_tree_finalize(DevLearner L) {
     // real_threshold (learner.rs:198-203): the bin's upper bound
     const uint32_t tb = T.threshold_in_bin[n];
     T.threshold[n] = L.ub ? L.ub[L.feats[T.nodes[n].f].ub_off + tb] : (double)tb;
+    // the score update's routes: the bins going right as a 256-bit set, and the
+    // record byte and children packed in one word (children fit 12 signed bits)
+    const NodeRoute r = T.nodes[n];
+#pragma unroll
+    for (int w = 0; w < 8; ++w)
+      T.route_mask[n * 8 + w] = route_right_word(w, r.pmin, r.max_bin, r.th, r.na_bin, r.flags);
+    T.route_node[n] = ((uint32_t)r.f & 0xffu) | (((uint32_t)lc & 0xfffu) << 8) |
+                      (((uint32_t)rc & 0xfffu) << 20);
   }
   if (threadIdx.x == 0) {
     T.header[0] = nl;

@@ -80,6 +80,8 @@ struct DevTree {
   int32_t* leaf_depth;
   int32_t* leaf_parent;
   NodeRoute* nodes;
+  uint32_t* route_mask;       // [MAX_LEAVES - 1][8]: bins a node routes right (bit set)
+  uint32_t* route_node;       // [MAX_LEAVES - 1]: record byte | left << 8 | right << 20
 };
 
 struct DevLearner {

@@ -217,10 +217,36 @@ __global__ void k_pack_g32(const float* __restrict__ g, const float* __restrict_
 // quantize_pair :173-188, next_u01 :255-263).  Row r consumes xorshift draws
 // 2r+1 (grad) and 2r+2 (hess) of the sequential stream; a lane starts at row
 // wave_row0 + lane*C with state M^(2*(row)) s0, M being the GF(2) matrix of one
-// xorshift step: the wave applies the precomputed powers P_k = M^(2*64*C*2^k)
-// cooperatively (lane i owns column i, xor-reduce), then each lane applies
-// R_k = M^(2*C*2^k) for the bits of its lane id.
+// xorshift step: the wave applies the precomputed powers P_k = M^(2*64*C*2^k) for the
+// bits of its wave index cooperatively (lane i owns column i, xor-reduce), then
+// lane l applies T^l, T = M^(2*C), from a table of all 64 lane offsets.
 // ===========================================================================
+// One DPP row rotation of a 64-bit value (all 64 lanes active).
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_ror_u64(uint64_t v) {
+  const uint32_t lo =
+      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+// XOR of a 64-bit value over the wave, uniform result: row rotations by 1, 2, 4, 8
+// leave every lane of a 16-lane row with the row's XOR; rows combine from lanes
+// 0, 16, 32, 48.  Requires all 64 lanes active.
+__device__ __forceinline__ uint64_t wave_xor_u64(uint64_t v) {
+  v ^= dpp_ror_u64<0x121>(v);
+  v ^= dpp_ror_u64<0x122>(v);
+  v ^= dpp_ror_u64<0x124>(v);
+  v ^= dpp_ror_u64<0x128>(v);
+  uint64_t r = 0ull;
+#pragma unroll
+  for (int row = 0; row < 4; ++row) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * row);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 16 * row);
+    r ^= ((uint64_t)hi << 32) | lo;
+  }
+  return r;
+}
 __device__ __forceinline__ double next_u01(uint64_t& s) {
   uint64_t x = s;
   x ^= x << 13;
@@ -232,9 +258,11 @@ __device__ __forceinline__ double next_u01(uint64_t& s) {
 
 // Rows per block: 4 waves x 64 lanes x QUANT_ROWS_PER_LANE.  g/h are staged through
 // LDS so global loads and stores are coalesced while each lane walks its own run of
-// consecutive rows (padded index: one spare slot per 16 rows avoids bank conflicts).
+// consecutive rows (padded index: one spare slot per run makes the lane stride odd,
+// so the lanes of a wave hit different banks).
 #define QUANT_BLOCK_ROWS (4 * LGBM_WAVE * QUANT_ROWS_PER_LANE)
-__device__ __forceinline__ int qidx(int r) { return r + (r >> 4); }
+#define QUANT_LDS_ROWS (QUANT_BLOCK_ROWS + QUANT_BLOCK_ROWS / QUANT_ROWS_PER_LANE)
+__device__ __forceinline__ int qidx(int r) { return r + r / QUANT_ROWS_PER_LANE; }
 
 __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ g,
                                                   const float* __restrict__ h, int64_t n,
@@ -244,9 +272,9 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ g,
                                                   uint64_t s0, int32_t stochastic,
                                                   uint16_t* __restrict__ gh,
                                                   float* __restrict__ dg, float* __restrict__ dh) {
-  __shared__ float sg_[QUANT_BLOCK_ROWS + QUANT_BLOCK_ROWS / 16];
-  __shared__ float sh_[QUANT_BLOCK_ROWS + QUANT_BLOCK_ROWS / 16];
-  __shared__ uint16_t sq_[QUANT_BLOCK_ROWS + QUANT_BLOCK_ROWS / 16];
+  __shared__ float sg_[QUANT_LDS_ROWS];
+  __shared__ float sh_[QUANT_LDS_ROWS];
+  __shared__ uint16_t sq_[QUANT_LDS_ROWS];
   const int64_t brow0 = (int64_t)blockIdx.x * QUANT_BLOCK_ROWS;
   if (brow0 >= n) return;
   const int tid = threadIdx.x;
@@ -265,21 +293,15 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ g,
     uint64_t sw = s0;
     for (int k = 0; k < QUANT_WAVE_MATS; ++k) {
       if ((wave >> k) & 1) {
-        uint64_t term = ((sw >> lane) & 1ull) ? wave_mats[k * 64 + lane] : 0ull;
-        for (int off = 32; off >= 1; off >>= 1) term ^= __shfl_xor(term, off);
-        sw = term;
+        const uint64_t term = ((sw >> lane) & 1ull) ? wave_mats[k * 64 + lane] : 0ull;
+        sw = wave_xor_u64(term);
       }
     }
-    uint64_t sl = sw;
-    for (int k = 0; k < QUANT_LANE_MATS; ++k) {
-      uint64_t y = 0ull;
-      for (int i = 0; i < 64; ++i) {
-        const uint64_t col = lane_mats[k * 64 + i];
-        y ^= ((sl >> i) & 1ull) ? col : 0ull;
-      }
-      if ((lane >> k) & 1) sl = y;
-    }
-    st = sl;
+    // lane l: T^l applied to the wave's state (sw is wave-uniform)
+    uint64_t y = 0ull;
+    for (int i = 0; i < 64; ++i)
+      if ((sw >> i) & 1ull) y ^= lane_mats[i * 64 + lane];
+    st = y;
   }
   __syncthreads();
   const int lrow = (tid >> 6) * (LGBM_WAVE * QUANT_ROWS_PER_LANE) + lane * QUANT_ROWS_PER_LANE;
@@ -700,30 +722,46 @@ __global__ __launch_bounds__(LGBM_WAVE) void k_scan_explicit(const double* __res
 // ===========================================================================
 // score update: traverse the tree per row with the split routers
 // (equivalent to AddPredictionToScore over the partition, learner.rs:4380-4395),
-// adding the shrunk leaf value (Tree::shrinkage, tree.rs:1074).
+// adding the shrunk leaf value (Tree::shrinkage, tree.rs:1074).  A thread stages its
+// record in LDS and walks the tree with one byte read and one route-mask word per
+// level (k_tree_finalize precomputes, per node, the set of bins routed right).
 // ===========================================================================
 template <int W>
 __global__ __launch_bounds__(256) void k_score_update(DevLearner L, double lr,
                                                       double* __restrict__ score) {
-  __shared__ NodeRoute nodes[256];
-  __shared__ double vals[256];
+  constexpr int kStride = 4 * W + 1;  // words per staged record: odd, so byte reads of
+                                      // different lanes hit different banks
+  __shared__ uint32_t s_mask[(MAX_LEAVES - 1) * 8];
+  __shared__ uint32_t s_node[MAX_LEAVES - 1];
+  __shared__ double vals[MAX_LEAVES];
+  __shared__ uint32_t s_rec[256 * kStride];
   const int32_t nl = L.ctl->num_leaves;
   if (nl <= 1) return;
-  for (int i = threadIdx.x; i < nl - 1; i += blockDim.x) nodes[i] = L.tree.nodes[i];
-  for (int i = threadIdx.x; i < nl; i += blockDim.x)
+  const int tid = threadIdx.x;
+  for (int i = tid; i < (nl - 1) * 8; i += blockDim.x) s_mask[i] = L.tree.route_mask[i];
+  for (int i = tid; i < nl - 1; i += blockDim.x) s_node[i] = L.tree.route_node[i];
+  for (int i = tid; i < nl; i += blockDim.x)
     vals[i] = maybe_round_to_zero(L.tree.leaf_value[i] * lr);
   __syncthreads();
   const uint4* __restrict__ rec = L.bufs.rec[BUF_ORIG];
+  uint32_t* mine = s_rec + tid * kStride;
+  const uint8_t* bytes = (const uint8_t*)mine;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < L.N; r += stride) {
-    uint4 w[W];
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + tid; r < L.N; r += stride) {
 #pragma unroll
-    for (int i = 0; i < W; ++i) w[i] = rec[r * W + i];
+    for (int i = 0; i < W; ++i) {
+      const uint4 w = rec[r * W + i];
+      mine[4 * i] = w.x;
+      mine[4 * i + 1] = w.y;
+      mine[4 * i + 2] = w.z;
+      mine[4 * i + 3] = w.w;
+    }
     int32_t node = 0;
     for (int depth = 0; depth < nl && node >= 0; ++depth) {  // a path has < nl nodes
-      const NodeRoute& n = nodes[node];
-      const int32_t bin = (int32_t)rec_byte(w, n.f);
-      node = route_right(bin, n.pmin, n.max_bin, n.th, n.na_bin, n.flags) ? n.right : n.left;
+      const uint32_t u = s_node[node];
+      const uint32_t bin = bytes[u & 0xffu];
+      const uint32_t right = (s_mask[node * 8 + (bin >> 5)] >> (bin & 31u)) & 1u;
+      node = right ? ((int32_t)u >> 20) : ((int32_t)(u << 12) >> 20);
     }
     if (node < 0 && ~node < nl) score[r] += vals[~node];
   }
@@ -819,7 +857,7 @@ void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n
 }
 void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s,
                          const KernelEvents* ev) {
-  int64_t blocks = std::min<int64_t>((L.N + 255) / 256, 4096);
+  int64_t blocks = std::min<int64_t>((L.N + 255) / 256, 2048);
   if (blocks < 1) blocks = 1;
   DISPATCH_W(L.W, KLAUNCH(ev, k_score_update<kW>, dim3((unsigned)blocks), dim3(256), 0, s, L, lr,
                           score));

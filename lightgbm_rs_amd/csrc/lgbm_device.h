@@ -40,9 +40,8 @@
 #define PLAN_THREADS 1024
 #define MAX_LEAVES 256                  // tree leaves per context (u8 leaf ids in the plan)
 #define SLOT_CAP(leaves) (6 * (leaves) + 4)  // node slots: root + two per (speculated) split
-#define QUANT_ROWS_PER_LANE 16
-#define QUANT_LANE_MATS 6               // log2(64)
-#define QUANT_WAVE_MATS 27              // wave index bits (N <= 2^27 * 1024)
+#define QUANT_ROWS_PER_LANE 8          // consecutive rows per lane (power of 2)
+#define QUANT_WAVE_MATS 27              // wave index bits (N <= 2^27 * 64 * C)
 #define STAT_BLOCKS 1024                // partial-statistics blocks of the g/h reduction
 
 // Buffer ids of the row stores.
@@ -298,9 +297,33 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 }
 
 // SplitInner router (data_partition.rs:387-417).
-__device__ __forceinline__ bool route_right(int32_t bin, int32_t pmin, int32_t max_bin, int32_t th,
-                                            int32_t na_bin, int32_t flags) {
+__host__ __device__ __forceinline__ bool route_right(int32_t bin, int32_t pmin, int32_t max_bin,
+                                                     int32_t th, int32_t na_bin, int32_t flags) {
   if ((flags & 2) && bin == na_bin) return !(flags & 4);
   if (bin < pmin || bin > max_bin) return (flags & 1) != 0;
   return bin > th;
+}
+
+// Bits of the bins in [a, b] that fall in word w (bins 32w .. 32w + 31).
+__host__ __device__ __forceinline__ uint32_t bin_range_bits(int32_t w, int32_t a, int32_t b) {
+  const int32_t lo = 32 * w, hi = lo + 31;
+  if (a < lo) a = lo;
+  if (b > hi) b = hi;
+  if (a > b) return 0u;
+  const uint32_t upto_b = (b - lo) == 31 ? 0xffffffffu : ((1u << (b - lo + 1)) - 1u);
+  return upto_b & ~((1u << (a - lo)) - 1u);
+}
+// route_right over all 256 u8 bins as a bit set: word w, bit b <=> bin 32w + b goes
+// right.
+__host__ __device__ __forceinline__ uint32_t route_right_word(int32_t w, int32_t pmin,
+                                                            int32_t max_bin, int32_t th,
+                                                            int32_t na_bin, int32_t flags) {
+  const int32_t first_right = th + 1 > pmin ? th + 1 : pmin;
+  uint32_t m = bin_range_bits(w, first_right, max_bin);
+  if (flags & 1) m |= ~bin_range_bits(w, pmin, max_bin);  // out of range: default right
+  if ((flags & 2) && na_bin >= 32 * w && na_bin < 32 * w + 32) {
+    const uint32_t bit = 1u << (na_bin - 32 * w);
+    m = (flags & 4) ? (m & ~bit) : (m | bit);
+  }
+  return m;
 }
