@@ -51,7 +51,7 @@ struct lgbm_hip_ctx {
   double* score = nullptr;
   int32_t* hist_part = nullptr;  // [HIST_SLOTS][cells][3]
   int32_t* hist_acc = nullptr;   // [SPEC_MAX][cells][3]
-  int32_t* part_slots = nullptr; // [part_blocks + SPEC_MAX][cells][3]
+  int32_t* part_slots = nullptr; // [part_blocks + SPEC_MAX][cells] int4
   int64_t* hist_part64 = nullptr;  // [HIST_SLOTS][cells][2]
   int64_t* int_slots64 = nullptr;  // [SLOT_CAP][cells][2]
   int32_t n_fgroups = 0;
@@ -844,7 +844,7 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   }
   if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * acc * 3))) return rc;
   HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * acc * 3 * 4));
-  if ((rc = dalloc(c, &c->part_slots, ((size_t)c->part_blocks + SPEC_MAX) * acc * 3))) return rc;
+  if ((rc = dalloc(c, &c->part_slots, ((size_t)c->part_blocks + SPEC_MAX) * acc * 4))) return rc;
   if ((rc = ensure_tile_state(c, num_data))) return rc;
   // transpose the feature-major upload into records
   uint8_t* tmp = nullptr;

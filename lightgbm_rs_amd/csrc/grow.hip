@@ -573,11 +573,9 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   // atomic adds into its accumulator (cleared by k_pair_scan).
   auto flush = [&]() {
     const PartJob& C = s_jobs[cur];
-    const int64_t nblk = part_owner(C.tile0 + C.ntiles - 1, total, G) -
-                         part_owner(C.tile0, total, G) + 1;
-    if (nblk <= PART_SLOT_MAX)
+    if (part_span_blocks(C.tile0, C.ntiles, total, G) <= PART_SLOT_MAX)
       lds_hist_flush_clear(lds_hist, cells,
-                           L.part_slots + ((size_t)blockIdx.x + cur) * cells * 3,
+                           L.part_slots + ((size_t)blockIdx.x + cur) * cells * 4,
                            flushed ? FLUSH_ADD : FLUSH_STORE);
     else
       lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3, FLUSH_ATOMIC);
@@ -594,7 +592,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     const PartJob& J = s_jobs[jl];
     const int64_t count = J.count, begin = J.begin;
     const int64_t base = (t - J.tile0) * kTile;
-    const uint4* __restrict__ src = L.bufs.rec[J.src_buf];
+    const uint4* __restrict__ src = rec_buf(L.bufs, J.src_buf);
     const GhT* __restrict__ sgh = gh_buf<GhT>(L.bufs, J.src_buf);
 #pragma unroll
     for (int k = 0; k < PR; ++k) {
@@ -629,7 +627,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     const int64_t count = J.count, begin = J.begin;
     const int64_t lt = t - J.tile0;
     const int64_t base = lt * kTile;
-    uint4* __restrict__ dst = L.bufs.rec[J.dst_buf];
+    uint4* __restrict__ dst = rec_buf(L.bufs, J.dst_buf);
     GhT* __restrict__ dgh = gh_buf<GhT>(L.bufs, J.dst_buf);
     auto& w = B.w;
     auto& q = B.q;
@@ -744,21 +742,19 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     }
   };
   // Two register buffers: the next tile's loads are in flight while this tile is
-  // ranked, histogrammed and scattered (its stores queue behind those loads).
-  TileBuf b0, b1;
-  int64_t t = t_lo;
-  int32_t j0 = load(t, b0), j1 = 0;
-  while (true) {
-    const bool more1 = t + 1 < t_hi;
-    if (more1) j1 = load(t + 1, b1);
-    process(t, j0, b0);
-    if (!more1) break;
-    ++t;
-    const bool more0 = t + 1 < t_hi;
-    if (more0) j0 = load(t + 1, b0);
-    process(t, j1, b1);
-    if (!more0) break;
-    ++t;
+  // ranked, histogrammed and scattered (its stores queue behind those loads).  One
+  // copy of the per-tile code (the buffers swap by register moves) keeps the kernel
+  // small enough to stay in the instruction cache next to the round's other kernels.
+  TileBuf cur_b, next_b;
+  int32_t jc = load(t_lo, cur_b), jn = 0;
+  for (int64_t t = t_lo; t < t_hi; ++t) {
+    const bool more = t + 1 < t_hi;
+    if (more) jn = load(t + 1, next_b);
+    process(t, jc, cur_b);
+    if (more) {
+      cur_b = next_b;
+      jc = jn;
+    }
   }
   if (FP == 0 && cur >= 0 && s_jobs[cur].acc_right >= 0 && held > 0) flush();
 }
@@ -771,7 +767,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_tile_count(DevLearner L) {
   const PartJob J = L.ctl->jobs[0];
   const int64_t t = blockIdx.x;
   if (t >= J.ntiles) return;
-  const uint4* __restrict__ src = L.bufs.rec[J.src_buf];
+  const uint4* __restrict__ src = rec_buf(L.bufs, J.src_buf);
   int32_t n = 0;
   for (int k = 0; k < PR; ++k) {
     const int64_t p = t * kTile + (int64_t)k * PT + threadIdx.x;
@@ -879,7 +875,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
   const int64_t T = ctl->tile_total;
   const int64_t s0 = J.ntiles > 0 ? part_owner(J.tile0, T, part_grid) : 0;
   const int64_t s1 = J.ntiles > 0 ? part_owner(J.tile0 + J.ntiles - 1, T, part_grid) : -1;
-  const bool use_slots = s1 - s0 + 1 <= PART_SLOT_MAX;
+  const bool use_slots =
+      J.ntiles > 0 ? part_span_blocks(J.tile0, J.ntiles, T, part_grid) <= PART_SLOT_MAX : true;
   const int nbq = ctl->fp_mode ? 0 : nb;  // quantized gradients only
   for (int b = tid; b < nbq; b += SCAN_THREADS) {
     const size_t ci = (size_t)(ft.cell_base + b);
@@ -887,10 +884,10 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
     if (use_slots) {
       for (int64_t k = s0; k <= s1; ++k) {
         if (k * T / part_grid >= (k + 1) * T / part_grid) continue;  // a block with no tiles
-        const int32_t* a = L.part_slots + ((size_t)(k + j) * cells + ci) * 3;
-        AG += a[0];
-        AH += a[1];
-        AT += a[2];
+        const int4 a = ((const int4*)L.part_slots)[(size_t)(k + j) * cells + ci];
+        AG += a.x;
+        AH += a.y;
+        AT += a.z;
       }
     } else {
       int32_t* a = acc + ci * 3;
@@ -1017,7 +1014,7 @@ __global__ void k_leaf_of(DevLearner L, uint8_t* __restrict__ leaf_of) {
   const int32_t l = blockIdx.y;
   if (l >= L.ctl->num_leaves) return;
   const int64_t b = L.leaves.begin[l], c = L.leaves.count[l];
-  const uint4* __restrict__ rec = L.bufs.rec[L.leaves.buf[l]];
+  const uint4* __restrict__ rec = rec_buf(L.bufs, L.leaves.buf[l]);
   for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < c;
        p += (int64_t)gridDim.x * blockDim.x)
     leaf_of[rec[(b + p) * W + (W - 1)].w] = (uint8_t)l;

@@ -28,12 +28,26 @@ struct RowBufs {
   float2* g32[NBUF];    // f32 (g, h) per row (non-quantized training)
 };
 
+// Buffer i of a row store, selected without indexing the kernel-argument array (the
+// pointers stay in scalar registers; i is wave-uniform).
+template <typename T>
+__device__ __forceinline__ T* buf_sel(T* const (&a)[NBUF], int i) {
+  T* p = a[0];
+#pragma unroll
+  for (int k = 1; k < NBUF; ++k) p = i == k ? a[k] : p;
+  return p;
+}
+__device__ __forceinline__ uint4* rec_buf(const RowBufs& b, int i) { return buf_sel(b.rec, i); }
 template <typename T>
 __device__ __forceinline__ T* gh_buf(const RowBufs& b, int i);
 template <>
-__device__ __forceinline__ uint16_t* gh_buf<uint16_t>(const RowBufs& b, int i) { return b.gh[i]; }
+__device__ __forceinline__ uint16_t* gh_buf<uint16_t>(const RowBufs& b, int i) {
+  return buf_sel(b.gh, i);
+}
 template <>
-__device__ __forceinline__ float2* gh_buf<float2>(const RowBufs& b, int i) { return b.g32[i]; }
+__device__ __forceinline__ float2* gh_buf<float2>(const RowBufs& b, int i) {
+  return buf_sel(b.g32, i);
+}
 __device__ __forceinline__ uint32_t gh_bits(uint16_t q) { return q; }
 __device__ __forceinline__ uint32_t gh_bits(float2) { return 0u; }
 
@@ -96,7 +110,7 @@ struct DevLearner {
   uint64_t slot_len;
   int32_t* hist_part;         // [HIST_SLOTS][total_cells][3] root / per-op partials
   int32_t* hist_acc;          // [SPEC_MAX][total_cells][3] per-job accumulators
-  int32_t* part_slots;        // [part blocks + SPEC_MAX][total_cells][3] (block, job) cells
+  int32_t* part_slots;        // [part blocks + SPEC_MAX][total_cells] int4 (block, job) cells
   // f32-gradient training: 64-bit fixed-point (g, h) cells
   int64_t* hist_part64;       // [HIST_SLOTS][total_cells][2]
   int64_t* int_slots64;       // [slot_cap][total_cells][2]

@@ -396,7 +396,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
   const int64_t R = s_R;
   const int64_t lo = (int64_t)(a - s_a0[j]) * R;
   const int64_t hi = min(J.count, lo + R);
-  const uint4* __restrict__ rec = L.bufs.rec[J.buf] + J.begin * W;
+  const uint4* __restrict__ rec = rec_buf(L.bufs, J.buf) + J.begin * W;
   const uint16_t* __restrict__ gh = L.bufs.gh[J.buf] + J.begin;
   int32_t* __restrict__ out = L.hist_part + (size_t)a * cells * 3;
   // feature cell bases in scalar registers (wave-uniform)
@@ -556,7 +556,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_f32(DevLearner L) {
   const int64_t R = s_R;
   const int64_t lo = (int64_t)(a - s_a0[j]) * R;
   const int64_t hi = min(J.count, lo + R);
-  const uint4* __restrict__ rec = L.bufs.rec[J.buf] + J.begin * W;
+  const uint4* __restrict__ rec = rec_buf(L.bufs, J.buf) + J.begin * W;
   const float2* __restrict__ gh = L.bufs.g32[J.buf] + J.begin;
   const double gm = ldexp(1.0, ctl->g_shift), hm = ldexp(1.0, ctl->h_shift);
   for (int64_t r = lo + tid; r < hi; r += HIST_THREADS) {

@@ -71,6 +71,12 @@ __host__ __device__ constexpr int64_t part_tile(int W) {
 __host__ __device__ inline int64_t part_owner(int64_t t, int64_t T, int64_t G) {
   return ((t + 1) * G - 1) / T;
 }
+// Blocks holding at least one of the tiles [t0, t0 + n) (n >= 1): one per tile when
+// there are fewer tiles than blocks, else every block from the first owner to the
+// last.
+__host__ __device__ inline int64_t part_span_blocks(int64_t t0, int64_t n, int64_t T, int64_t G) {
+  return T < G ? n : part_owner(t0 + n - 1, T, G) - part_owner(t0, T, G) + 1;
+}
 
 struct DevFeature {
   uint32_t num_bin;

@@ -360,11 +360,12 @@ __device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* 
 }
 
 // Moves a block's packed LDS histogram (fields: q_g sum signed 22 bits, q_h sum 21
-// bits, count of q_h == 3 21 bits) into integer cells out[c] = (G, H, T) and clears
-// it (the trash cells too).  mode FLUSH_ATOMIC: atomic adds into a shared
-// accumulator (zero cells skipped); FLUSH_STORE: the block's own slot, every cell
-// written; FLUSH_ADD: add into the block's own slot (written by an earlier store).
-// The caller has synchronised the block after the last accumulation.
+// bits, count of q_h == 3 21 bits) into integer cells (G, H, T) and clears it (the
+// trash cells too).  mode FLUSH_ATOMIC: atomic adds into a shared int32 [cells][3]
+// accumulator (zero cells skipped); FLUSH_STORE: the block's own int4 [cells] slot,
+// every cell written with one 16-byte store; FLUSH_ADD: add into the block's own
+// slot (written by an earlier store).  The caller has synchronised the block after
+// the last accumulation.
 #define FLUSH_ATOMIC 0
 #define FLUSH_STORE 1
 #define FLUSH_ADD 2
@@ -374,21 +375,18 @@ __device__ __forceinline__ void lds_hist_flush_clear(unsigned long long* lds, in
     const unsigned long long p = lds[c];
     lds[c] = 0ull;
     if (c >= cells) continue;  // trash cells
-    int32_t* dst = out + (size_t)c * 3;
     const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
     const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
     const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
     const int32_t hsum = (int32_t)(rest & ((1ull << 21) - 1));
     const int32_t n3 = (int32_t)(rest >> 21);
     if (mode == FLUSH_STORE) {
-      dst[0] = (int32_t)gsum;
-      dst[1] = hsum;
-      dst[2] = n3;
+      ((int4*)out)[c] = make_int4((int32_t)gsum, hsum, n3, 0);
     } else if (mode == FLUSH_ADD) {
-      dst[0] += (int32_t)gsum;
-      dst[1] += hsum;
-      dst[2] += n3;
+      const int4 o = ((const int4*)out)[c];
+      ((int4*)out)[c] = make_int4(o.x + (int32_t)gsum, o.y + hsum, o.z + n3, 0);
     } else if (p != 0ull) {
+      int32_t* dst = out + (size_t)c * 3;
       if (gsum) __hip_atomic_fetch_add(dst, (int32_t)gsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (hsum) __hip_atomic_fetch_add(dst + 1, hsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (n3) __hip_atomic_fetch_add(dst + 2, n3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
