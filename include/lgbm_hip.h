@@ -293,6 +293,46 @@ int lgbm_hip_get_timing(lgbm_hip_ctx* ctx, double* ms_out5, double* hist_bytes_o
  * [15] rounds launched after the captured per-tree sequence. */
 int lgbm_hip_get_stats(lgbm_hip_ctx* ctx, double* out16);
 
+/* ---- models and batch prediction ------------------------------------------ */
+
+/* A LightGBM v4 model text, parsed on the host (no device needed): replaces
+ * `lgbm_model::model_text::load` (crates/lgbm-model/src/model_text.rs:48-160) with
+ * `Tree::parse` (tree.rs:846-1060) and the objective line (objective.rs:125-225).
+ * Numerical and categorical splits; linear trees and objectives outside
+ * objective.rs's list are rejected (LGBM_HIP_ERR_INVALID_ARGUMENT, like the
+ * reference's MalformedModel).  The text is borrowed for the call only. */
+typedef struct lgbm_hip_model lgbm_hip_model;
+int lgbm_hip_model_load(const char* text, int64_t len, lgbm_hip_model** out);
+int lgbm_hip_model_free(lgbm_hip_model* model);
+/* Message of the last failed lgbm_hip_model_load (process-wide). */
+int lgbm_hip_model_last_error(char* buf, size_t size);
+/* out[0] trees, [1] num_class, [2] num_tree_per_iteration, [3] max_feature_idx,
+ * [4] iterations (trees / num_tree_per_iteration), [5] objective (PredObjective:
+ * 0 regression, 1 regression sqrt, 2 binary, 3 multiclass, 4 multiclassova,
+ * 5 poisson/gamma/tweedie, 6 cross_entropy, 7 cross_entropy_lambda). */
+int lgbm_hip_model_info(const lgbm_hip_model* model, int64_t* out6);
+
+#define LGBM_HIP_PREDICT_RAW 0
+#define LGBM_HIP_PREDICT_TRANSFORMED 1
+#define LGBM_HIP_PREDICT_LEAF 2
+/* Batch prediction of a dense row-major f32 matrix [num_rows][num_cols]
+ * (num_cols >= max_feature_idx + 1), over iterations [start_iteration,
+ * start_iteration + num_iteration) clamped as GbdtModel::init_predict
+ * (ensemble.rs:75-84; num_iteration <= 0: all).  Replaces predict_raw_mat_range,
+ * predict_mat and predict_leaf_index_mat (crates/lgbm-model/src/predict.rs:75-131,
+ * 378-485).  kind RAW / TRANSFORMED: out is double[num_rows * num_tree_per_iteration]
+ * (the f64 scores the reference casts to f32 at its own boundary); LEAF: out is
+ * int32[num_rows * trees in range], row-major, trees in model order.  data and out
+ * are host pointers (copied through the context's device buffers). */
+int lgbm_hip_predict(lgbm_hip_ctx* ctx, const lgbm_hip_model* model, const float* data,
+                     int64_t num_rows, int32_t num_cols, int32_t start_iteration,
+                     int32_t num_iteration, int32_t kind, void* out);
+/* The same with data and out in device memory of the context's device (no copies;
+ * the call returns when the results are written). */
+int lgbm_hip_predict_device(lgbm_hip_ctx* ctx, const lgbm_hip_model* model, const float* d_data,
+                            int64_t num_rows, int32_t num_cols, int32_t start_iteration,
+                            int32_t num_iteration, int32_t kind, void* d_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -221,6 +221,82 @@ class HipBackend:
         return {k: float(v) for k, v in zip(keys, st)}
 
 
+PREDICT_KINDS = {"raw": 0, "transformed": 1, "leaf": 2}
+
+
+class Model:
+    """A LightGBM v4 model text parsed by the library (`model_text::load`,
+    crates/lgbm-model/src/model_text.rs:48-160); host only, no device needed."""
+
+    def __init__(self, text):
+        self.lib = load_library()
+        data = text.encode() if isinstance(text, str) else bytes(text)
+        self.handle = C.c_void_p()
+        rc = self.lib.lgbm_hip_model_load(C.c_char_p(data), C.c_int64(len(data)),
+                                          C.byref(self.handle))
+        if rc != 0:
+            buf = C.create_string_buffer(1024)
+            self.lib.lgbm_hip_model_last_error(buf, C.c_size_t(1024))
+            raise HipError(rc, buf.value.decode())
+        info = np.zeros(6, np.int64)
+        self.lib.lgbm_hip_model_info(self.handle, ptr(info, C.c_int64))
+        (self.num_trees, self.num_class, self.num_tree_per_iteration, self.max_feature_idx,
+         self.num_iterations, self.objective) = (int(x) for x in info)
+
+    @classmethod
+    def from_file(cls, path):
+        with open(path, "rb") as f:
+            return cls(f.read())
+
+    def close(self):
+        if self.handle:
+            self.lib.lgbm_hip_model_free(self.handle)
+            self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _predict_shape(model, kind, rows, start_iteration, num_iteration):
+    total = model.num_iterations
+    start = min(max(start_iteration, 0), total)
+    num = min(num_iteration, total - start) if num_iteration > 0 else total - start
+    width = num * model.num_tree_per_iteration if kind == "leaf" else model.num_tree_per_iteration
+    return (rows, width)
+
+
+def _predict(self, model, X, kind="raw", start_iteration=0, num_iteration=-1):
+    """predict_raw_mat_range / predict_mat / predict_leaf_index_mat
+    (crates/lgbm-model/src/predict.rs:75-131, 378-485) on the device: X is a dense
+    [rows, cols] float32 matrix; returns float64 [rows, outputs] or int32 [rows, trees]."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    rows, cols = X.shape
+    shape = _predict_shape(model, kind, rows, start_iteration, num_iteration)
+    out = np.zeros(shape, np.int32 if kind == "leaf" else np.float64)
+    self._check(self.lib.lgbm_hip_predict(
+        self.ctx, model.handle, ptr(X, C.c_float), C.c_int64(rows), C.c_int32(cols),
+        C.c_int32(start_iteration), C.c_int32(num_iteration), C.c_int32(PREDICT_KINDS[kind]),
+        out.ctypes.data_as(C.c_void_p)))
+    return out
+
+
+def _predict_device(self, model, x_ptr, rows, cols, out_ptr, kind="raw", start_iteration=0,
+                    num_iteration=-1):
+    """The same over device-resident buffers (raw device pointers, e.g. torch tensors'
+    data_ptr())."""
+    self._check(self.lib.lgbm_hip_predict_device(
+        self.ctx, model.handle, C.c_void_p(x_ptr), C.c_int64(rows), C.c_int32(cols),
+        C.c_int32(start_iteration), C.c_int32(num_iteration), C.c_int32(PREDICT_KINDS[kind]),
+        C.c_void_p(out_ptr)))
+
+
+HipBackend.predict = _predict
+HipBackend.predict_device = _predict_device
+
+
 def feature_meta(num_bin, most_freq_bin=0, missing_type=0, default_bin=None, real_index=0,
                  min_bin=0, max_bin=None):
     """FeatureColumn descriptors with the offset rule of offset_for_most_freq_bin
@@ -237,4 +313,4 @@ def feature_meta(num_bin, most_freq_bin=0, missing_type=0, default_bin=None, rea
     return m
 
 
-__all__ = ["HipBackend", "HipError", "GainConfig", "feature_meta", "load_library"]
+__all__ = ["HipBackend", "HipError", "GainConfig", "Model", "feature_meta", "load_library"]

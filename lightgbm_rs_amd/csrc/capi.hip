@@ -13,12 +13,22 @@
 #include <vector>
 
 #include "kernels.h"
+#include "model.h"
 
 using namespace lgbm;
+
+namespace lgbm {
+void launch_predict(const PredNode* nodes, const PredTree* trees, const double* leaves,
+                    const int32_t* cat_bounds, const uint32_t* cat_words, const float* X,
+                    int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
+                    int32_t objective, double sigmoid, double* out, int32_t* leaf_out,
+                    hipStream_t s);
+}
 
 namespace {
 
 thread_local std::string g_create_err;
+std::string g_model_err;  // last failed lgbm_hip_model_load
 
 struct EventPair {
   hipEvent_t a, b;
@@ -28,6 +38,17 @@ struct EventPair {
 }  // namespace
 
 struct lgbm_hip_ctx {
+  // device copy of the last model predicted with (keyed by the model's uid)
+  uint64_t pm_uid = 0;
+  PredNode* pm_nodes = nullptr;
+  PredTree* pm_trees = nullptr;
+  double* pm_leaves = nullptr;
+  int32_t* pm_catb = nullptr;
+  uint32_t* pm_catw = nullptr;
+  float* pm_x = nullptr;  // host-input staging
+  size_t pm_x_cap = 0;
+  void* pm_out = nullptr;
+  size_t pm_out_cap = 0;
   int device = 0;
   hipStream_t stream = nullptr;
   std::string err;
@@ -721,6 +742,13 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->leaves.count);
   F(c->leaves.buf);
   F(c->leaves.rev);
+  F(c->pm_nodes);
+  F(c->pm_trees);
+  F(c->pm_leaves);
+  F(c->pm_catb);
+  F(c->pm_catw);
+  F(c->pm_x);
+  F(c->pm_out);
   DevTree& T = c->tree;
   F(T.nodes);
   F(T.route_mask);
@@ -1282,6 +1310,149 @@ int lgbm_hip_get_stats(lgbm_hip_ctx* c, double* out) {
   out[14] = c->trees;
   out[15] = c->extra_rounds;
   return LGBM_HIP_OK;
+}
+
+// ---- models and batch prediction ---------------------------------------------
+
+int lgbm_hip_model_load(const char* text, int64_t len, lgbm_hip_model** out) {
+  if (!text || !out || len < 0) {
+    g_model_err = "null text/out or negative length";
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  *out = nullptr;
+  lgbm_hip_model* m = new lgbm_hip_model();
+  std::string err;
+  if (!parse_model_text(text, (size_t)len, m, &err)) {
+    delete m;
+    g_model_err = err;
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  *out = m;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_model_free(lgbm_hip_model* model) {
+  delete model;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_model_last_error(char* buf, size_t size) {
+  if (buf && size > 0) {
+    std::snprintf(buf, size, "%s", g_model_err.c_str());
+  }
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_model_info(const lgbm_hip_model* m, int64_t* out) {
+  if (!m || !out) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  out[0] = (int64_t)m->trees.size();
+  out[1] = m->num_class;
+  out[2] = m->num_tree_per_iteration;
+  out[3] = m->max_feature_idx;
+  out[4] = (int64_t)m->trees.size() / m->num_tree_per_iteration;
+  out[5] = m->objective;
+  return LGBM_HIP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+template <typename T>
+int upload_vec(lgbm_hip_ctx* c, T** dst, const std::vector<T>& v) {
+  int rc = dalloc(c, dst, v.size());
+  if (rc) return rc;
+  if (!v.empty()) HIPCHK(c, hipMemcpy(*dst, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice));
+  return LGBM_HIP_OK;
+}
+
+// Validates the call, uploads the model when it is not the cached one, and returns
+// the clamped iteration range and output width.
+int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int32_t cols,
+                    int32_t start_iteration, int32_t num_iteration, int32_t kind, int32_t* it0,
+                    int32_t* it1, int64_t* width) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!m) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null model");
+  if (rows < 0 || cols < 0) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "negative shape");
+  if (cols < m->max_feature_idx + 1)
+    return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH,
+                   "input has " + std::to_string(cols) + " columns, model needs max_feature_idx+1 = " +
+                       std::to_string(m->max_feature_idx + 1));
+  if (kind < LGBM_HIP_PREDICT_RAW || kind > LGBM_HIP_PREDICT_LEAF)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "unknown prediction kind");
+  // GbdtModel::init_predict (ensemble.rs:75-84)
+  const int32_t total = (int32_t)(m->trees.size() / m->num_tree_per_iteration);
+  const int32_t start = std::min(std::max(start_iteration, 0), total);
+  const int32_t num = num_iteration > 0 ? std::min(num_iteration, total - start) : total - start;
+  *it0 = start;
+  *it1 = start + num;
+  *width = kind == LGBM_HIP_PREDICT_LEAF ? (int64_t)num * m->num_tree_per_iteration
+                                         : (int64_t)m->num_tree_per_iteration;
+  if (c->pm_uid != m->uid) {
+    if ((rc = upload_vec(c, &c->pm_nodes, m->nodes))) return rc;
+    if ((rc = upload_vec(c, &c->pm_trees, m->tree_index))) return rc;
+    if ((rc = upload_vec(c, &c->pm_leaves, m->leaf_values))) return rc;
+    if ((rc = upload_vec(c, &c->pm_catb, m->cat_bounds))) return rc;
+    if ((rc = upload_vec(c, &c->pm_catw, m->cat_words))) return rc;
+    c->pm_uid = m->uid;
+  }
+  return LGBM_HIP_OK;
+}
+
+int predict_run(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* d_x, int64_t rows,
+                int32_t cols, int32_t it0, int32_t it1, int32_t kind, void* d_out) {
+  launch_predict(c->pm_nodes, c->pm_trees, c->pm_leaves, c->pm_catb, c->pm_catw, d_x, rows, cols,
+                 it0, it1, m->num_tree_per_iteration, kind, m->objective, m->sigmoid,
+                 kind == LGBM_HIP_PREDICT_LEAF ? nullptr : (double*)d_out,
+                 kind == LGBM_HIP_PREDICT_LEAF ? (int32_t*)d_out : nullptr, c->stream);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return LGBM_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lgbm_hip_predict(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* data, int64_t rows,
+                     int32_t cols, int32_t start_iteration, int32_t num_iteration, int32_t kind,
+                     void* out) {
+  int32_t it0 = 0, it1 = 0;
+  int64_t width = 0;
+  int rc = predict_prepare(c, m, rows, cols, start_iteration, num_iteration, kind, &it0, &it1, &width);
+  if (rc) return rc;
+  if (rows == 0 || width == 0) return LGBM_HIP_OK;
+  if (!data || !out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null data/out");
+  const size_t xb = (size_t)rows * (size_t)cols * 4;
+  const size_t ob = (size_t)rows * (size_t)width * (kind == LGBM_HIP_PREDICT_LEAF ? 4 : 8);
+  if (c->pm_x_cap < xb) {
+    if ((rc = dalloc(c, &c->pm_x, (size_t)rows * (size_t)cols))) return rc;
+    c->pm_x_cap = xb;
+  }
+  if (c->pm_out_cap < ob) {
+    char* p = nullptr;
+    if ((rc = dalloc(c, &p, ob))) return rc;
+    if (c->pm_out) (void)hipFree(c->pm_out);
+    c->pm_out = p;
+    c->pm_out_cap = ob;
+  }
+  HIPCHK(c, hipMemcpy(c->pm_x, data, xb, hipMemcpyHostToDevice));
+  if ((rc = predict_run(c, m, c->pm_x, rows, cols, it0, it1, kind, c->pm_out))) return rc;
+  HIPCHK(c, hipMemcpy(out, c->pm_out, ob, hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_predict_device(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* d_data,
+                            int64_t rows, int32_t cols, int32_t start_iteration,
+                            int32_t num_iteration, int32_t kind, void* d_out) {
+  int32_t it0 = 0, it1 = 0;
+  int64_t width = 0;
+  int rc = predict_prepare(c, m, rows, cols, start_iteration, num_iteration, kind, &it0, &it1, &width);
+  if (rc) return rc;
+  if (rows == 0 || width == 0) return LGBM_HIP_OK;
+  if (!d_data || !d_out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null data/out");
+  return predict_run(c, m, d_data, rows, cols, it0, it1, kind, d_out);
 }
 
 }  // extern "C"

@@ -1,0 +1,56 @@
+// model.h — LightGBM v4 model text on the host and its flattened device form.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+// Objective ConvertOutput kinds (crates/lgbm-model/src/objective.rs:48-88).
+enum PredObjective : int32_t {
+  OBJ_REGRESSION = 0,       // identity
+  OBJ_REGRESSION_SQRT = 1,  // sign(x) * x * x
+  OBJ_BINARY = 2,           // 1 / (1 + exp(-sigmoid * x))
+  OBJ_MULTICLASS = 3,       // softmax with max subtraction
+  OBJ_MULTICLASS_OVA = 4,   // per-class sigmoid
+  OBJ_EXP = 5,              // poisson / gamma / tweedie: exp(x)
+  OBJ_XENTROPY = 6,         // 1 / (1 + exp(-x))
+  OBJ_XENTLAMBDA = 7,       // log1p(exp(x))
+};
+
+// One internal node as the device reads it (24 bytes).  For a categorical split,
+// `threshold` is the index of its bitset (Tree::cat_boundaries), as in the model text.
+struct PredNode {
+  double threshold;
+  int32_t feature;
+  int32_t left, right;  // >= 0: internal node of the same tree; < 0: ~leaf
+  int32_t dtype;        // decision_type bits (1 categorical, 2 default left, missing << 2)
+};
+
+// Per tree: where its nodes, leaf values and categorical bitset bounds start.
+struct PredTree {
+  int32_t node0, leaf0, cat0, num_leaves;
+};
+
+struct HostTree {
+  int32_t num_leaves = 0, num_cat = 0;
+  std::vector<int32_t> split_feature, left_child, right_child, decision_type, cat_boundaries;
+  std::vector<double> threshold, leaf_value;
+  std::vector<uint32_t> cat_threshold;
+};
+
+struct lgbm_hip_model {
+  int32_t num_class = 1, num_tree_per_iteration = 1, max_feature_idx = -1;
+  int32_t objective = OBJ_REGRESSION;
+  double sigmoid = 1.0;
+  std::vector<HostTree> trees;
+  uint64_t uid = 0;  // distinguishes models in the per-context device cache
+  // flattened form
+  std::vector<PredNode> nodes;
+  std::vector<PredTree> tree_index;
+  std::vector<double> leaf_values;
+  std::vector<int32_t> cat_bounds;  // absolute offsets into cat_words
+  std::vector<uint32_t> cat_words;
+};
+
+// Parses `text`; on failure returns false with `err` set (nothing is allocated).
+bool parse_model_text(const char* text, size_t len, lgbm_hip_model* m, std::string* err);

@@ -1,0 +1,136 @@
+// predict.hip — batch prediction of a LightGBM model over dense f32 rows.
+//
+// One thread per row walks every tree of the requested iteration range on the raw
+// feature values (no binning), as the reference predictor does:
+//   Tree::get_leaf / numerical_decision / categorical_decision (tree.rs:160-340),
+//   GbdtModel::predict_raw (ensemble.rs:75-102): per class an f64 sum over the
+//   iterations in order, starting from 0.0 — here class by class, which adds each
+//   class's trees in the same order,
+//   ConvertOutput (objective.rs:241-340) for the transformed kind.
+#include <hip/hip_runtime.h>
+
+#include "model.h"
+
+namespace lgbm {
+
+struct PredModelDev {
+  const PredNode* nodes;
+  const PredTree* trees;
+  const double* leaves;
+  const int32_t* cat_bounds;
+  const uint32_t* cat_words;
+};
+
+__device__ __forceinline__ int32_t pred_next(const PredNode& n, double fval, const PredModelDev& M,
+                                             int32_t cat0) {
+  if (n.dtype & 1) {  // CategoricalDecision (tree.rs:212-237)
+    if (isnan(fval)) return n.right;
+    const int32_t iv = fval >= 2147483647.0 ? 2147483647
+                       : fval <= -2147483648.0 ? (int32_t)(-2147483647 - 1)
+                                               : (int32_t)fval;  // saturating `as i32`
+    if (iv < 0) return n.right;
+    const int32_t ci = (int32_t)n.threshold;  // checked at load: 0 <= ci < num_cat
+    const int32_t lo = M.cat_bounds[cat0 + ci], hi = M.cat_bounds[cat0 + ci + 1];
+    const int32_t w = iv >> 5;
+    if (w >= hi - lo) return n.right;
+    return ((M.cat_words[lo + w] >> (iv & 31)) & 1u) ? n.left : n.right;
+  }
+  // NumericalDecision (tree.rs:193-210)
+  const int32_t mt = (n.dtype >> 2) & 3;
+  if (isnan(fval) && mt != 2) fval = 0.0;
+  if ((mt == 1 && fval >= -1e-35 && fval <= 1e-35) || (mt == 2 && isnan(fval)))
+    return (n.dtype & 2) ? n.left : n.right;
+  return fval <= n.threshold ? n.left : n.right;
+}
+
+// Leaf of tree t for the row at x (a path visits fewer than num_leaves nodes: the
+// structure was checked at load).
+__device__ __forceinline__ int32_t pred_leaf(const PredModelDev& M, int32_t t, const float* x) {
+  const PredTree T = M.trees[t];
+  if (T.num_leaves <= 1) return 0;
+  int32_t node = 0;
+  for (int32_t d = 0; d < T.num_leaves && node >= 0; ++d) {
+    const PredNode n = M.nodes[T.node0 + node];
+    node = pred_next(n, (double)x[n.feature], M, T.cat0);
+  }
+  return node < 0 ? ~node : 0;
+}
+
+__device__ __forceinline__ double pred_sigmoid(double x, double s) { return 1.0 / (1.0 + exp(-s * x)); }
+
+__global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __restrict__ X,
+                                                 int64_t rows, int32_t cols, int32_t it0,
+                                                 int32_t it1, int32_t ntpi, int32_t kind,
+                                                 int32_t objective, double sigmoid,
+                                                 double* __restrict__ out,
+                                                 int32_t* __restrict__ leaf_out) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float* x = X + r * cols;
+  if (kind == 2) {
+    const int64_t nt = (int64_t)(it1 - it0) * ntpi;
+    for (int32_t i = it0; i < it1; ++i)
+      for (int32_t k = 0; k < ntpi; ++k)
+        leaf_out[r * nt + (int64_t)(i - it0) * ntpi + k] = pred_leaf(M, i * ntpi + k, x);
+    return;
+  }
+  double* o = out + r * ntpi;
+  for (int32_t k = 0; k < ntpi; ++k) {
+    double acc = 0.0;
+    for (int32_t i = it0; i < it1; ++i) {
+      const int32_t t = i * ntpi + k;
+      acc += M.leaves[M.trees[t].leaf0 + pred_leaf(M, t, x)];
+    }
+    o[k] = acc;
+  }
+  if (kind != 1) return;
+  switch (objective) {
+    case OBJ_REGRESSION_SQRT: {
+      const double v = o[0];
+      o[0] = (v > 0.0 ? 1.0 : (v < 0.0 ? -1.0 : 0.0)) * v * v;
+      break;
+    }
+    case OBJ_BINARY:
+      o[0] = pred_sigmoid(o[0], sigmoid);
+      break;
+    case OBJ_XENTROPY:
+      o[0] = pred_sigmoid(o[0], 1.0);
+      break;
+    case OBJ_XENTLAMBDA:
+      o[0] = log1p(exp(o[0]));
+      break;
+    case OBJ_EXP:
+      o[0] = exp(o[0]);
+      break;
+    case OBJ_MULTICLASS: {  // Common::Softmax: max subtraction, sum in class order
+      double wmax = o[0];
+      for (int32_t k = 1; k < ntpi; ++k) wmax = o[k] > wmax ? o[k] : wmax;
+      double wsum = 0.0;
+      for (int32_t k = 0; k < ntpi; ++k) {
+        o[k] = exp(o[k] - wmax);
+        wsum += o[k];
+      }
+      for (int32_t k = 0; k < ntpi; ++k) o[k] /= wsum;
+      break;
+    }
+    case OBJ_MULTICLASS_OVA:
+      for (int32_t k = 0; k < ntpi; ++k) o[k] = pred_sigmoid(o[k], sigmoid);
+      break;
+    default:
+      break;
+  }
+}
+
+void launch_predict(const PredNode* nodes, const PredTree* trees, const double* leaves,
+                    const int32_t* cat_bounds, const uint32_t* cat_words, const float* X,
+                    int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
+                    int32_t objective, double sigmoid, double* out, int32_t* leaf_out,
+                    hipStream_t s) {
+  if (rows <= 0) return;
+  const PredModelDev M{nodes, trees, leaves, cat_bounds, cat_words};
+  const int64_t blocks = (rows + 255) / 256;
+  k_predict<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(M, X, rows, cols, it0, it1, ntpi, kind,
+                                                         objective, sigmoid, out, leaf_out);
+}
+
+}  // namespace lgbm

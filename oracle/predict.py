@@ -1,0 +1,193 @@
+"""CPU restatement of the reference's model-text loader and batch predictor.
+
+Test infrastructure only (the parity checker of the device predictor).  Follows
+crates/lgbm-model/src/:
+  model_text.rs:48-160  header keys (num_class, num_tree_per_iteration,
+                        max_feature_idx, objective) and the Tree= blocks
+  tree.rs:846-1000      Tree::parse (per-tree key=value fields)
+  tree.rs:160-340       NumericalDecision / CategoricalDecision / GetLeaf
+  ensemble.rs:75-102    init_predict + predict_raw (f64 accumulation per class,
+                        iteration order)
+  objective.rs:125-340  objective= parsing and ConvertOutput
+  predict.rs:75-131     dense f32 rows widened to f64
+Pinned by the reference's prediction goldens (tests/golden/predict/).
+"""
+import math
+
+import numpy as np
+
+K_ZERO_THRESHOLD = 1e-35
+MISSING_NONE, MISSING_ZERO, MISSING_NAN = 0, 1, 2
+CATEGORICAL_MASK, DEFAULT_LEFT_MASK = 1, 2
+
+
+def _f64_list(v):
+    return np.array([float(t) for t in v.split()], dtype=np.float64)
+
+
+def _i_list(v, dtype=np.int64):
+    return np.array([int(t) for t in v.split()], dtype=dtype)
+
+
+def parse_tree(lines):
+    kv = {}
+    for line in lines:
+        if not line:
+            break
+        k, _, v = line.partition("=")
+        kv[k] = v
+    t = {"num_leaves": int(kv["num_leaves"]), "num_cat": int(kv["num_cat"]),
+         "leaf_value": _f64_list(kv["leaf_value"])}
+    if t["num_leaves"] > 1:
+        t["split_feature"] = _i_list(kv["split_feature"])
+        t["threshold"] = _f64_list(kv["threshold"])
+        t["decision_type"] = _i_list(kv["decision_type"])
+        t["left_child"] = _i_list(kv["left_child"])
+        t["right_child"] = _i_list(kv["right_child"])
+        if t["num_cat"] > 0:
+            t["cat_boundaries"] = _i_list(kv["cat_boundaries"])
+            t["cat_threshold"] = _i_list(kv["cat_threshold"], np.uint64)
+    if int(kv.get("is_linear", "0")) != 0:
+        raise ValueError("linear trees are not supported")
+    return t
+
+
+def parse_model(text):
+    lines = text.replace("\r", "").split("\n")
+    head, i = {}, 0
+    while i < len(lines) and not lines[i].startswith("Tree="):
+        k, sep, v = lines[i].partition("=")
+        if sep:
+            head[k] = v
+        i += 1
+    trees = []
+    while i < len(lines):
+        if lines[i].startswith("Tree="):
+            j = i + 1
+            block = []
+            while j < len(lines) and lines[j]:
+                block.append(lines[j])
+                j += 1
+            trees.append(parse_tree(block))
+            i = j
+        elif lines[i].startswith("end of trees"):
+            break
+        else:
+            i += 1
+    num_class = int(head["num_class"])
+    obj = head.get("objective", "regression").split()
+    params = dict(t.split(":", 1) for t in obj[1:] if ":" in t)
+    return {"num_class": num_class,
+            "num_tree_per_iteration": int(head.get("num_tree_per_iteration", num_class)),
+            "max_feature_idx": int(head["max_feature_idx"]),
+            "objective": obj[0], "sqrt": "sqrt" in obj[1:],
+            "sigmoid": float(params.get("sigmoid", "1")), "trees": trees}
+
+
+def _decide(t, node, fval):
+    """Next node for the rows at internal `node` (arrays), tree.rs:193-245."""
+    dt = t["decision_type"][node]
+    thr = t["threshold"][node]
+    left, right = t["left_child"][node], t["right_child"][node]
+    out = np.empty_like(node)
+    cat = (dt & CATEGORICAL_MASK) > 0
+    # numerical
+    mt = (dt >> 2) & 3
+    nan = np.isnan(fval)
+    fv = np.where(nan & (mt != MISSING_NAN), 0.0, fval)
+    is_zero = (fv >= -K_ZERO_THRESHOLD) & (fv <= K_ZERO_THRESHOLD)
+    missing = ((mt == MISSING_ZERO) & is_zero) | ((mt == MISSING_NAN) & np.isnan(fv))
+    dleft = (dt & DEFAULT_LEFT_MASK) > 0
+    num_next = np.where(missing, np.where(dleft, left, right), np.where(fv <= thr, left, right))
+    out[:] = num_next
+    if cat.any():
+        idx = np.nonzero(cat)[0]
+        for r in idx:  # categorical rows: small cases only
+            v = fval[r]
+            if math.isnan(v):
+                out[r] = right[r]
+                continue
+            iv = int(v) if abs(v) < 2 ** 31 else (2 ** 31 - 1 if v > 0 else -2 ** 31)
+            if iv < 0:
+                out[r] = right[r]
+                continue
+            ci = int(thr[r])
+            lo, hi = t["cat_boundaries"][ci], t["cat_boundaries"][ci + 1]
+            w = iv // 32
+            hit = w < hi - lo and (int(t["cat_threshold"][lo + w]) >> (iv % 32)) & 1
+            out[r] = left[r] if hit else right[r]
+    return out
+
+
+def leaf_of(t, X64):
+    n = X64.shape[0]
+    if t["num_leaves"] <= 1:
+        return np.zeros(n, dtype=np.int64)
+    node = np.zeros(n, dtype=np.int64)
+    rows = np.arange(n)
+    active = node >= 0
+    while active.any():
+        r = rows[active]
+        nd = node[r]
+        fval = X64[r, t["split_feature"][nd]]
+        node[r] = _decide(t, nd, fval)
+        active = node >= 0
+    return ~node
+
+
+def _range(model, start_iteration, num_iteration):
+    ntpi = model["num_tree_per_iteration"]
+    total = len(model["trees"]) // ntpi
+    start = min(max(start_iteration, 0), total)
+    num = min(num_iteration, total - start) if num_iteration > 0 else total - start
+    return start, num
+
+
+def predict(model, X, start_iteration=0, num_iteration=-1, kind="raw"):
+    """kind: 'raw' (f64 [rows, ntpi]), 'transformed', or 'leaf' (int [rows, trees])."""
+    X64 = np.asarray(X, dtype=np.float32).astype(np.float64)
+    ntpi = model["num_tree_per_iteration"]
+    start, num = _range(model, start_iteration, num_iteration)
+    trees = model["trees"]
+    if kind == "leaf":
+        cols = [leaf_of(trees[i * ntpi + k], X64) for i in range(start, start + num)
+                for k in range(ntpi)]
+        return np.stack(cols, axis=1) if cols else np.zeros((X64.shape[0], 0), np.int64)
+    raw = np.zeros((X64.shape[0], ntpi), dtype=np.float64)
+    for i in range(start, start + num):
+        for k in range(ntpi):
+            t = trees[i * ntpi + k]
+            raw[:, k] = raw[:, k] + t["leaf_value"][leaf_of(t, X64)]
+    if kind == "raw":
+        return raw
+    return convert(model, raw)
+
+
+def convert(model, raw):
+    obj, out = model["objective"], np.empty_like(raw)
+    sig = model["sigmoid"]
+    for r in range(raw.shape[0]):
+        v = raw[r]
+        if obj in ("binary",):
+            out[r, 0] = 1.0 / (1.0 + math.exp(-sig * v[0]))
+        elif obj in ("cross_entropy", "xentropy"):
+            out[r, 0] = 1.0 / (1.0 + math.exp(-v[0]))
+        elif obj in ("cross_entropy_lambda", "xentlambda"):
+            out[r, 0] = math.log1p(math.exp(v[0]))
+        elif obj in ("poisson", "gamma", "tweedie"):
+            out[r, 0] = math.exp(v[0])
+        elif obj in ("multiclass", "softmax"):
+            wmax = v[0]
+            for x in v[1:]:
+                wmax = max(x, wmax)
+            e = [math.exp(x - wmax) for x in v]
+            s = 0.0
+            for x in e:
+                s += x
+            out[r] = [x / s for x in e]
+        elif obj in ("multiclassova", "multiclass_ova", "ova", "ovr"):
+            out[r] = [1.0 / (1.0 + math.exp(-sig * x)) for x in v]
+        else:  # regression family
+            x = v[0]
+            out[r, 0] = (math.copysign(1.0, x) if x != 0 else 0.0) * x * x if model["sqrt"] else x
+    return out
