@@ -130,6 +130,8 @@ typedef struct lgbm_tree_out {
   int32_t* leaf_count;
   int32_t* leaf_depth;
   int32_t* leaf_parent;
+  double* internal_weight;     /* left + right sum_hessian of the split (the C++
+                                  Tree::Split rule; tree.rs:655 stores 0) */
 } lgbm_tree_out;
 
 /* `LeafPartitionLayout` (crates/lgbm-dataset/src/dataset.rs:88-97): the data
@@ -304,13 +306,38 @@ int lgbm_hip_get_stats(lgbm_hip_ctx* ctx, double* out16);
 typedef struct lgbm_hip_model lgbm_hip_model;
 int lgbm_hip_model_load(const char* text, int64_t len, lgbm_hip_model** out);
 int lgbm_hip_model_free(lgbm_hip_model* model);
-/* Message of the last failed lgbm_hip_model_load (process-wide). */
+/* Message of the last failed lgbm_hip_model_load / _create / _add_tree (process-wide). */
 int lgbm_hip_model_last_error(char* buf, size_t size);
 /* out[0] trees, [1] num_class, [2] num_tree_per_iteration, [3] max_feature_idx,
  * [4] iterations (trees / num_tree_per_iteration), [5] objective (PredObjective:
  * 0 regression, 1 regression sqrt, 2 binary, 3 multiclass, 4 multiclassova,
  * 5 poisson/gamma/tweedie, 6 cross_entropy, 7 cross_entropy_lambda). */
 int lgbm_hip_model_info(const lgbm_hip_model* model, int64_t* out6);
+
+/* A model built in memory, for trees grown by this library: the `GbdtModel` the
+ * reference's boosting loop fills (crates/lgbm-boosting/src/gbdt.rs:1094-1140).
+ * objective: the model text's objective= value (e.g. "binary sigmoid:1"), or NULL
+ * for none; feature_names / feature_infos: the space-separated lines, or NULL for
+ * `Column_<i>` / `none` per feature. */
+int lgbm_hip_model_create(int32_t num_class, int32_t num_tree_per_iteration,
+                          int32_t max_feature_idx, const char* objective,
+                          const char* feature_names, const char* feature_infos,
+                          lgbm_hip_model** out);
+/* Appends a grown tree (lgbm_tree_out as lgbm_hip_train_iter_binary or
+ * lgbm_hip_grow_tree_on_device fill it; leaf and internal values already shrunk)
+ * recording `shrinkage` as Tree::shrinkage does (tree.rs:1074-1096), then adds
+ * `bias` to every leaf and internal value (Tree::add_bias, tree.rs:1161-1168: the
+ * boost-from-average init score folded into the first iteration's trees,
+ * gbdt.rs:1130-1140; 0 for none).  internal_weight is written as 0 like Tree::split
+ * (tree.rs:655).  The tree is checked like a loaded one. */
+int lgbm_hip_model_add_tree(lgbm_hip_model* model, const lgbm_tree_out* tree, double shrinkage,
+                            double bias);
+/* The model text (`model_text::save`, crates/lgbm-model/src/model_text.rs:216-320:
+ * envelope, Tree::to_string blocks (tree.rs:800-836), tree_sizes, split-count
+ * feature_importances, the verbatim `parameters:` tail of a loaded model).  Writes
+ * at most size bytes including a terminating NUL and sets *needed to the full size
+ * with the NUL; LGBM_HIP_ERR_LENGTH_MISMATCH when buf was too small (truncated). */
+int lgbm_hip_model_to_text(const lgbm_hip_model* model, char* buf, size_t size, size_t* needed);
 
 #define LGBM_HIP_PREDICT_RAW 0
 #define LGBM_HIP_PREDICT_TRANSFORMED 1

@@ -133,6 +133,7 @@ class TreeOut(C.Structure):
         ("leaf_count", C.POINTER(C.c_int32)),
         ("leaf_depth", C.POINTER(C.c_int32)),
         ("leaf_parent", C.POINTER(C.c_int32)),
+        ("internal_weight", C.POINTER(C.c_double)),
     ]
 
 
@@ -167,6 +168,7 @@ _TREE_FIELDS = [
     ("leaf_count", np.int32, C.c_int32, "leaf"),
     ("leaf_depth", np.int32, C.c_int32, "leaf"),
     ("leaf_parent", np.int32, C.c_int32, "leaf"),
+    ("internal_weight", np.float64, C.c_double, "node"),
 ]
 
 
@@ -182,6 +184,18 @@ class TreeBuffers:
             a = np.zeros(n, dtype=dt)
             self.arrays[name] = a
             setattr(self.out, name, ptr(a, ct))
+
+    @classmethod
+    def from_dict(cls, d):
+        """A TreeOut over copies of a tree dict's arrays (as to_dict returns it)."""
+        lens = [len(d[n]) + (1 if k == "node" else 0) for n, _, _, k in _TREE_FIELDS if n in d]
+        tb = cls(max([int(d["num_leaves"]), 1] + lens))
+        tb.out.num_leaves = int(d["num_leaves"])
+        for name, dt, _, _ in _TREE_FIELDS:
+            if name in d:
+                v = np.asarray(d[name], dtype=dt)
+                tb.arrays[name][:len(v)] = v
+        return tb
 
     def to_dict(self):
         nl = self.out.num_leaves

@@ -232,12 +232,51 @@ class Model:
         self.lib = load_library()
         data = text.encode() if isinstance(text, str) else bytes(text)
         self.handle = C.c_void_p()
-        rc = self.lib.lgbm_hip_model_load(C.c_char_p(data), C.c_int64(len(data)),
-                                          C.byref(self.handle))
+        self._check(self.lib.lgbm_hip_model_load(C.c_char_p(data), C.c_int64(len(data)),
+                                                 C.byref(self.handle)))
+        self._info()
+
+    def _check(self, rc):
         if rc != 0:
             buf = C.create_string_buffer(1024)
             self.lib.lgbm_hip_model_last_error(buf, C.c_size_t(1024))
             raise HipError(rc, buf.value.decode())
+
+    @classmethod
+    def create(cls, num_class=1, num_tree_per_iteration=None, max_feature_idx=0,
+               objective=None, feature_names=None, feature_infos=None):
+        """An empty model to append grown trees to (the boosting loop's GbdtModel,
+        crates/lgbm-boosting/src/gbdt.rs:1094-1140)."""
+        self = cls.__new__(cls)
+        self.lib = load_library()
+        self.handle = C.c_void_p()
+        enc = lambda v: None if v is None else C.c_char_p(v.encode())
+        ntpi = num_class if num_tree_per_iteration is None else num_tree_per_iteration
+        self._check(self.lib.lgbm_hip_model_create(
+            C.c_int32(num_class), C.c_int32(ntpi), C.c_int32(max_feature_idx), enc(objective),
+            enc(feature_names), enc(feature_infos), C.byref(self.handle)))
+        self._info()
+        return self
+
+    def add_tree(self, tree, shrinkage=1.0, bias=0.0):
+        """Append a grown tree dict (HipBackend.train_iter_binary / grow_tree_*):
+        values already shrunk, `shrinkage` recorded, `bias` added to every value
+        (Tree::add_bias, crates/lgbm-model/src/tree.rs:1161)."""
+        tb = TreeBuffers.from_dict(tree)
+        self._check(self.lib.lgbm_hip_model_add_tree(self.handle, C.byref(tb.out),
+                                                     C.c_double(shrinkage), C.c_double(bias)))
+        self._info()
+
+    def to_text(self):
+        """The model text (model_text::save, crates/lgbm-model/src/model_text.rs:216-320)."""
+        need = C.c_size_t(0)
+        self._check(self.lib.lgbm_hip_model_to_text(self.handle, None, C.c_size_t(0),
+                                                    C.byref(need)))
+        buf = C.create_string_buffer(need.value)
+        self._check(self.lib.lgbm_hip_model_to_text(self.handle, buf, need, C.byref(need)))
+        return buf.raw[:need.value - 1].decode()
+
+    def _info(self):
         info = np.zeros(6, np.int64)
         self.lib.lgbm_hip_model_info(self.handle, ptr(info, C.c_int64))
         (self.num_trees, self.num_class, self.num_tree_per_iteration, self.max_feature_idx,

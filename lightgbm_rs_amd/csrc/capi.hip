@@ -10,6 +10,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "kernels.h"
@@ -21,8 +22,8 @@ namespace lgbm {
 void launch_predict(const PredNode* nodes, const PredTree* trees, const double* leaves,
                     const int32_t* cat_bounds, const uint32_t* cat_words, const float* X,
                     int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
-                    int32_t objective, double sigmoid, double* out, int32_t* leaf_out,
-                    hipStream_t s);
+                    int32_t objective, double sigmoid, int32_t average_output, double* out,
+                    int32_t* leaf_out, hipStream_t s);
 }
 
 namespace {
@@ -326,9 +327,9 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   if ((rc = dalloc(c, &c->tree.route_mask, (size_t)L * 8))) return rc;
   if ((rc = dalloc(c, &c->tree.route_node, (size_t)L))) return rc;
   // tree arrays: one device blob (one readback per tree) + pinned host staging
-  const size_t sizes[15] = {64, 4, 4, 8, 4, 1, 4, 4, 8, 4, 8, 8, 4, 4, 4};
+  const size_t sizes[16] = {64, 4, 4, 8, 4, 1, 4, 4, 8, 4, 8, 8, 4, 4, 4, 8};
   size_t off = 0;
-  for (int i = 0; i < 15; ++i) {
+  for (int i = 0; i < 16; ++i) {
     c->tree_off[i] = off;
     off += ((i == 0 ? 64 : sizes[i] * (size_t)L) + 15) / 16 * 16;
   }
@@ -356,6 +357,7 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   T.leaf_count = (int32_t*)(base + c->tree_off[12]);
   T.leaf_depth = (int32_t*)(base + c->tree_off[13]);
   T.leaf_parent = (int32_t*)(base + c->tree_off[14]);
+  T.internal_weight = (double*)(base + c->tree_off[15]);
   c->lcap = L;
   c->buf_gen++;
   return LGBM_HIP_OK;
@@ -592,6 +594,7 @@ int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, do
     cp(out->leaf_count, 12, nl_ * 4);
     cp(out->leaf_depth, 13, nl_ * 4);
     cp(out->leaf_parent, 14, nl_ * 4);
+    cp(out->internal_weight, 15, ni * 8);
     if (shrink != 1.0) {
       // Tree::shrinkage (tree.rs:1074): MaybeRoundToZero(v * rate)
       const double z = (double)1e-35f;
@@ -1343,6 +1346,103 @@ int lgbm_hip_model_last_error(char* buf, size_t size) {
   return LGBM_HIP_OK;
 }
 
+int lgbm_hip_model_create(int32_t num_class, int32_t num_tree_per_iteration,
+                          int32_t max_feature_idx, const char* objective,
+                          const char* feature_names, const char* feature_infos,
+                          lgbm_hip_model** out) {
+  if (!out || num_class < 1 || num_tree_per_iteration < 1 || max_feature_idx < 0) {
+    g_model_err = "null out, or num_class / num_tree_per_iteration < 1, or max_feature_idx < 0";
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  *out = nullptr;
+  lgbm_hip_model* m = new lgbm_hip_model();
+  m->num_class = num_class;
+  m->num_tree_per_iteration = num_tree_per_iteration;
+  m->max_feature_idx = max_feature_idx;
+  std::string err;
+  if (objective && !model_set_objective(m, objective, &err)) {
+    delete m;
+    g_model_err = err;
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  // Dataset defaults (`Column_<i>` names, `none` infos) for the columns not named.
+  auto fill = [&](const char* given, std::string* dst, bool names) {
+    if (given) {
+      *dst = given;
+      return;
+    }
+    for (int32_t f = 0; f <= max_feature_idx; ++f) {
+      if (f) *dst += ' ';
+      *dst += names ? "Column_" + std::to_string(f) : std::string("none");
+    }
+  };
+  fill(feature_names, &m->feature_names, true);
+  fill(feature_infos, &m->feature_infos, false);
+  *out = m;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_model_add_tree(lgbm_hip_model* m, const lgbm_tree_out* t, double shrinkage,
+                            double bias) {
+  if (!m || !t || t->num_leaves < 1) {
+    g_model_err = "null model/tree or num_leaves < 1";
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  const int32_t nl = t->num_leaves, ni = nl - 1;
+  if (!t->leaf_value || (ni > 0 && (!t->split_feature || !t->threshold || !t->decision_type ||
+                                    !t->left_child || !t->right_child))) {
+    g_model_err = "tree without leaf_value or a structural array";
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  HostTree h;
+  h.num_leaves = nl;
+  h.num_cat = 0;
+  h.shrinkage = shrinkage;
+  auto take = [](auto* dst, const auto* src, int32_t n) {
+    using T = typename std::remove_reference<decltype(*dst)>::type::value_type;
+    dst->resize((size_t)n);
+    for (int32_t i = 0; i < n; ++i) (*dst)[(size_t)i] = src ? (T)src[i] : T(0);
+  };
+  take(&h.split_feature, t->split_feature, ni);
+  take(&h.threshold, t->threshold, ni);
+  take(&h.decision_type, t->decision_type, ni);
+  take(&h.left_child, t->left_child, ni);
+  take(&h.right_child, t->right_child, ni);
+  take(&h.split_gain, t->split_gain, ni);
+  take(&h.internal_value, t->internal_value, ni);
+  take(&h.internal_count, t->internal_count, ni);
+  take(&h.internal_weight, t->internal_weight, ni);  // NULL: 0, as tree.rs:655 stores
+  take(&h.leaf_value, t->leaf_value, nl);
+  if (nl > 1) take(&h.leaf_weight, t->leaf_weight, nl);  // constant tree: empty, as C++ writes it
+  take(&h.leaf_count, t->leaf_count, nl);
+  if (bias != 0.0) {
+    // Tree::add_bias (tree.rs:1161): MaybeRoundToZero(v + bias)
+    const double z = (double)1e-35f;
+    auto mrz = [z](double v) { return (v >= -z && v <= z) ? 0.0 : v; };
+    for (double& v : h.leaf_value) v = mrz(v + bias);
+    for (double& v : h.internal_value) v = mrz(v + bias);
+    h.shrinkage = 1.0;  // AddBias forces shrinkage_ to 1 (the model texts' first trees)
+  }
+  std::string err;
+  if (!model_add_tree(m, std::move(h), &err)) {
+    g_model_err = err;
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_model_to_text(const lgbm_hip_model* m, char* buf, size_t size, size_t* needed) {
+  if (!m) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  const std::string s = model_to_text(*m);
+  if (needed) *needed = s.size() + 1;
+  if (buf && size > 0) {
+    const size_t n = std::min(size - 1, s.size());
+    std::memcpy(buf, s.data(), n);
+    buf[n] = '\0';
+  }
+  return buf && size < s.size() + 1 ? LGBM_HIP_ERR_LENGTH_MISMATCH : LGBM_HIP_OK;
+}
+
 int lgbm_hip_model_info(const lgbm_hip_model* m, int64_t* out) {
   if (!m || !out) return LGBM_HIP_ERR_INVALID_ARGUMENT;
   out[0] = (int64_t)m->trees.size();
@@ -1381,6 +1481,16 @@ int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int3
                        std::to_string(m->max_feature_idx + 1));
   if (kind < LGBM_HIP_PREDICT_RAW || kind > LGBM_HIP_PREDICT_LEAF)
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "unknown prediction kind");
+  if (kind == LGBM_HIP_PREDICT_TRANSFORMED) {
+    // resolve_objective (predict.rs:305-322)
+    if (!m->have_objective)
+      return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT,
+                     "model has no objective= line; cannot apply ConvertOutput");
+    if (m->objective_outputs != m->num_tree_per_iteration)
+      return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT,
+                     "objective output width " + std::to_string(m->objective_outputs) +
+                         " != num_tree_per_iteration " + std::to_string(m->num_tree_per_iteration));
+  }
   // GbdtModel::init_predict (ensemble.rs:75-84)
   const int32_t total = (int32_t)(m->trees.size() / m->num_tree_per_iteration);
   const int32_t start = std::min(std::max(start_iteration, 0), total);
@@ -1404,7 +1514,7 @@ int predict_run(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* d_x, int6
                 int32_t cols, int32_t it0, int32_t it1, int32_t kind, void* d_out) {
   launch_predict(c->pm_nodes, c->pm_trees, c->pm_leaves, c->pm_catb, c->pm_catw, d_x, rows, cols,
                  it0, it1, m->num_tree_per_iteration, kind, m->objective, m->sigmoid,
-                 kind == LGBM_HIP_PREDICT_LEAF ? nullptr : (double*)d_out,
+                 m->average_output ? 1 : 0, kind == LGBM_HIP_PREDICT_LEAF ? nullptr : (double*)d_out,
                  kind == LGBM_HIP_PREDICT_LEAF ? (int32_t*)d_out : nullptr, c->stream);
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));

@@ -415,6 +415,9 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     T.decision_type[node] = dt;
     T.internal_value[node] = iv;  // the split leaf's output
     T.internal_count[node] = ic;  // partition counts (learner.rs:3994-4011)
+    // Tree::Split: internal_weight = left_weight + right_weight (the children's
+    // sum_hessians, which become their leaf_weight)
+    T.internal_weight[node] = nd.sums[s_ps[PS_LEAF_SLOT][cm.x]].sh + nd.sums[s_ps[PS_LEAF_SLOT][cm.w]].sh;
     lgbm_split_info bb;
     bb.threshold = thr;
     bb.default_left = dl;

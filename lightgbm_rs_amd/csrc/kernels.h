@@ -93,6 +93,7 @@ struct DevTree {
   int32_t* leaf_count;
   int32_t* leaf_depth;
   int32_t* leaf_parent;
+  double* internal_weight;  // left + right sum_hessian at the split (Tree::split)
   NodeRoute* nodes;
   uint32_t* route_mask;       // [MAX_LEAVES - 1][8]: bins a node routes right (bit set)
   uint32_t* route_node;       // [MAX_LEAVES - 1]: record byte | left << 8 | right << 20

@@ -16,8 +16,12 @@
 #include <cerrno>
 #include <cmath>
 #include <cstdlib>
+#include <algorithm>
+#include <cstdio>
 #include <cstring>
 #include <map>
+
+bool check_tree(const HostTree& t, int32_t max_feature_idx, std::string* err);
 
 namespace {
 
@@ -81,6 +85,7 @@ bool parse_objective(const std::string& line, lgbm_hip_model* m, std::string* er
     i = j;
   }
   if (tok.empty()) return fail(err, "empty objective= line");
+  m->objective_outputs = 1;
   bool sqrt_ = false, have_nc = false;
   int32_t nc = 0;
   for (size_t k = 1; k < tok.size(); ++k) {
@@ -111,10 +116,12 @@ bool parse_objective(const std::string& line, lgbm_hip_model* m, std::string* er
   } else if (n == "multiclass" || n == "softmax") {
     if (!have_nc || nc < 1) return fail(err, "multiclass objective must contain num_class >= 1");
     m->objective = OBJ_MULTICLASS;
+    m->objective_outputs = nc;
   } else if (n == "multiclassova" || n == "multiclass_ova" || n == "ova" || n == "ovr") {
     if (!have_nc || nc < 1) return fail(err, "multiclassova objective must contain num_class >= 1");
     if (!(m->sigmoid > 0.0)) return fail(err, "multiclassova sigmoid must be > 0");
     m->objective = OBJ_MULTICLASS_OVA;
+    m->objective_outputs = nc;
   } else if (n == "poisson" || n == "gamma" || n == "tweedie") {
     m->objective = OBJ_EXP;
   } else if (n == "cross_entropy" || n == "xentropy") {
@@ -148,8 +155,49 @@ bool parse_tree(const std::map<std::string, std::string>& kv, int32_t max_featur
   if (!(s = get("leaf_value"))) return fail(err, "tree model should contain leaf_value field");
   if (!parse_f64s(*s, &t->leaf_value, "leaf_value", err)) return false;
   if ((int64_t)t->leaf_value.size() != t->num_leaves) return fail(err, "leaf_value length");
-  if (t->num_leaves == 1) return true;
   const int32_t ni = t->num_leaves - 1;
+  // metadata (optional; the reference's defaults)
+  auto meta_f64 = [&](const char* k, std::vector<double>* v, int32_t n) -> bool {
+    if ((s = get(k))) {
+      if (!parse_f64s(*s, v, k, err)) return false;
+      if ((int32_t)v->size() != n) return fail(err, std::string(k) + " length");
+    } else {
+      v->assign(n, 0.0);
+    }
+    return true;
+  };
+  auto meta_i32 = [&](const char* k, std::vector<int32_t>* v, int32_t n) -> bool {
+    if ((s = get(k))) {
+      if (!parse_ints(*s, v, k, err)) return false;
+      if ((int32_t)v->size() != n) return fail(err, std::string(k) + " length");
+    } else {
+      v->assign(n, 0);
+    }
+    return true;
+  };
+  // A constant tree's leaf_weight line is empty in the C++ writer's output; kept so.
+  const std::string* lw = get("leaf_weight");
+  if (t->num_leaves == 1 && lw && lw->find_first_not_of(' ') == std::string::npos) {
+    t->leaf_weight.clear();
+  } else if (!meta_f64("leaf_weight", &t->leaf_weight, t->num_leaves)) {
+    return false;
+  }
+  if (!meta_i32("leaf_count", &t->leaf_count, t->num_leaves)) return false;
+  if ((s = get("shrinkage"))) {
+    std::vector<double> v;
+    if (!parse_f64s(*s, &v, "shrinkage", err)) return false;
+    if (v.size() != 1) return fail(err, "bad scalar shrinkage");
+    t->shrinkage = v[0];
+  }
+  if (t->num_leaves == 1) return true;
+  if (!meta_f64("internal_value", &t->internal_value, ni)) return false;
+  if (!meta_f64("internal_weight", &t->internal_weight, ni)) return false;
+  if (!meta_i32("internal_count", &t->internal_count, ni)) return false;
+  {
+    std::vector<double> g;
+    if (!meta_f64("split_gain", &g, ni)) return false;
+    t->split_gain.assign(g.begin(), g.end());
+  }
   if (!(s = get("split_feature"))) return fail(err, "tree without split_feature");
   if (!parse_ints(*s, &t->split_feature, "split_feature", err)) return false;
   if (!(s = get("threshold"))) return fail(err, "tree model should contain threshold field");
@@ -179,6 +227,117 @@ bool parse_tree(const std::map<std::string, std::string>& kv, int32_t max_featur
       if (t->cat_boundaries[i] < 0 || t->cat_boundaries[i] > t->cat_boundaries[i + 1])
         return fail(err, "cat_boundaries not ascending");
   }
+  return check_tree(*t, max_feature_idx, err);
+}
+
+void flatten_tree(lgbm_hip_model* m, const HostTree& t) {
+  PredTree pt;
+  pt.node0 = (int32_t)m->nodes.size();
+  pt.leaf0 = (int32_t)m->leaf_values.size();
+  pt.cat0 = (int32_t)m->cat_bounds.size();
+  pt.num_leaves = t.num_leaves;
+  m->tree_index.push_back(pt);
+  const int32_t word0 = (int32_t)m->cat_words.size();
+  for (int32_t i = 0; i + 1 < t.num_leaves; ++i) {
+    PredNode n;
+    n.threshold = t.threshold[i];
+    n.feature = t.split_feature[i];
+    n.left = t.left_child[i];
+    n.right = t.right_child[i];
+    n.dtype = t.decision_type[i];
+    m->nodes.push_back(n);
+  }
+  for (double v : t.leaf_value) m->leaf_values.push_back(v);
+  for (int32_t b : t.cat_boundaries) m->cat_bounds.push_back(word0 + b);
+  for (uint32_t w : t.cat_threshold) m->cat_words.push_back(w);
+}
+
+// ---- model text writer ---------------------------------------------------------
+// `%.17g` for threshold / leaf_value / leaf_weight, `%g` for split_gain /
+// internal_value / internal_weight / shrinkage (the C printf forms the reference
+// reproduces, format.rs:1-60).
+void put_g(std::string* s, double v, int prec) {
+  char buf[64];
+  std::snprintf(buf, sizeof buf, "%.*g", prec, v);
+  *s += buf;
+}
+template <typename T, typename F>
+void put_list(std::string* s, const char* key, const std::vector<T>& v, F put) {
+  *s += key;
+  *s += '=';
+  for (size_t i = 0; i < v.size(); ++i) {
+    if (i) *s += ' ';
+    put(v[i]);
+  }
+  *s += '\n';
+}
+
+// Tree::to_string (tree.rs:800-836).
+std::string tree_to_text(const HostTree& t) {
+  std::string s;
+  auto ints = [&](const char* k, const std::vector<int32_t>& v) {
+    put_list(&s, k, v, [&](int32_t x) { s += std::to_string(x); });
+  };
+  auto g17 = [&](const char* k, const std::vector<double>& v) {
+    put_list(&s, k, v, [&](double x) { put_g(&s, x, 17); });
+  };
+  auto g6 = [&](const char* k, const std::vector<double>& v) {
+    put_list(&s, k, v, [&](double x) { put_g(&s, x, 6); });
+  };
+  s += "num_leaves=" + std::to_string(t.num_leaves) + "\n";
+  s += "num_cat=" + std::to_string(t.num_cat) + "\n";
+  ints("split_feature", t.split_feature);
+  put_list(&s, "split_gain", t.split_gain, [&](float x) { put_g(&s, (double)x, 6); });
+  g17("threshold", t.threshold);
+  ints("decision_type", t.decision_type);
+  ints("left_child", t.left_child);
+  ints("right_child", t.right_child);
+  g17("leaf_value", t.leaf_value);
+  g17("leaf_weight", t.leaf_weight);
+  ints("leaf_count", t.leaf_count);
+  g6("internal_value", t.internal_value);
+  g6("internal_weight", t.internal_weight);
+  ints("internal_count", t.internal_count);
+  if (t.num_cat > 0) {
+    ints("cat_boundaries", t.cat_boundaries);
+    put_list(&s, "cat_threshold", t.cat_threshold, [&](uint32_t x) { s += std::to_string(x); });
+  }
+  s += "is_linear=0\n";
+  s += "shrinkage=";
+  put_g(&s, t.shrinkage, 6);
+  s += "\n\n";
+  return s;
+}
+
+}  // namespace
+
+bool check_tree(const HostTree& t_, int32_t max_feature_idx, std::string* err) {
+  const HostTree* t = &t_;
+  const int32_t ni = t->num_leaves - 1;
+  if (t->num_leaves < 1) return fail(err, "num_leaves must be >= 1");
+  if ((int32_t)t->leaf_value.size() != t->num_leaves) return fail(err, "leaf_value length");
+  if (t->num_cat < 0) return fail(err, "num_cat must be >= 0");
+  const bool lw_ok = (int32_t)t->leaf_weight.size() == t->num_leaves ||
+                     (t->num_leaves == 1 && t->leaf_weight.empty());
+  if (!lw_ok || (int32_t)t->leaf_count.size() != t->num_leaves)
+    return fail(err, "leaf_weight / leaf_count length");
+  if (t->num_cat > 0) {
+    if ((int32_t)t->cat_boundaries.size() != t->num_cat + 1) return fail(err, "cat_boundaries length");
+    for (int32_t i = 0; i < t->num_cat; ++i)
+      if (t->cat_boundaries[i] < 0 || t->cat_boundaries[i] > t->cat_boundaries[i + 1])
+        return fail(err, "cat_boundaries not ascending");
+    if ((int64_t)t->cat_threshold.size() != (int64_t)t->cat_boundaries.back())
+      return fail(err, "cat_threshold length");
+  } else if (!t->cat_boundaries.empty() || !t->cat_threshold.empty()) {
+    return fail(err, "categorical bitsets in a tree with num_cat=0");
+  }
+  if (ni == 0) return true;
+  if ((int32_t)t->split_feature.size() != ni || (int32_t)t->threshold.size() != ni ||
+      (int32_t)t->left_child.size() != ni || (int32_t)t->right_child.size() != ni ||
+      (int32_t)t->decision_type.size() != ni || (int32_t)t->split_gain.size() != ni ||
+      (int32_t)t->internal_value.size() != ni || (int32_t)t->internal_weight.size() != ni ||
+      (int32_t)t->internal_count.size() != ni)
+    return fail(err, "internal node array length != num_leaves - 1");
   // every index the traversal follows
   std::vector<int32_t> seen_node(ni, 0), seen_leaf(t->num_leaves, 0);
   for (int32_t i = 0; i < ni; ++i) {
@@ -218,31 +377,78 @@ bool parse_tree(const std::map<std::string, std::string>& kv, int32_t max_featur
   return true;
 }
 
-void flatten(lgbm_hip_model* m) {
-  for (const HostTree& t : m->trees) {
-    PredTree pt;
-    pt.node0 = (int32_t)m->nodes.size();
-    pt.leaf0 = (int32_t)m->leaf_values.size();
-    pt.cat0 = (int32_t)m->cat_bounds.size();
-    pt.num_leaves = t.num_leaves;
-    m->tree_index.push_back(pt);
-    const int32_t word0 = (int32_t)m->cat_words.size();
-    for (int32_t i = 0; i + 1 < t.num_leaves; ++i) {
-      PredNode n;
-      n.threshold = t.threshold[i];
-      n.feature = t.split_feature[i];
-      n.left = t.left_child[i];
-      n.right = t.right_child[i];
-      n.dtype = t.decision_type[i];
-      m->nodes.push_back(n);
-    }
-    for (double v : t.leaf_value) m->leaf_values.push_back(v);
-    for (int32_t b : t.cat_boundaries) m->cat_bounds.push_back(word0 + b);
-    for (uint32_t w : t.cat_threshold) m->cat_words.push_back(w);
-  }
+bool model_set_objective(lgbm_hip_model* m, const std::string& line, std::string* err) {
+  if (!parse_objective(line, m, err)) return false;
+  m->objective_line = line;
+  m->have_objective = true;
+  return true;
 }
 
-}  // namespace
+bool model_add_tree(lgbm_hip_model* m, HostTree&& t, std::string* err) {
+  if (!check_tree(t, m->max_feature_idx, err)) return false;
+  flatten_tree(m, t);
+  m->trees.push_back(std::move(t));
+  m->uid = g_model_uid.fetch_add(1);  // a changed model is a new device copy
+  return true;
+}
+
+// GBDT::SaveModelToString (model_text.rs:231-320).
+std::string model_to_text(const lgbm_hip_model& m) {
+  std::string s = "tree\nversion=v4\n";
+  s += "num_class=" + std::to_string(m.num_class) + "\n";
+  s += "num_tree_per_iteration=" + std::to_string(m.num_tree_per_iteration) + "\n";
+  s += "label_index=" + std::to_string(m.label_index) + "\n";
+  s += "max_feature_idx=" + std::to_string(m.max_feature_idx) + "\n";
+  if (m.have_objective) s += "objective=" + m.objective_line + "\n";
+  if (m.average_output) s += "average_output\n";
+  s += "feature_names=" + m.feature_names + "\n";
+  if (m.have_monotone) s += "monotone_constraints=" + m.monotone_constraints + "\n";
+  s += "feature_infos=" + m.feature_infos + "\n";
+  std::vector<std::string> blocks;
+  for (size_t i = 0; i < m.trees.size(); ++i)
+    blocks.push_back("Tree=" + std::to_string(i) + "\n" + tree_to_text(m.trees[i]) + "\n");
+  s += "tree_sizes=";
+  for (size_t i = 0; i < blocks.size(); ++i) {
+    if (i) s += ' ';
+    s += std::to_string(blocks[i].size());
+  }
+  s += "\n\n";
+  for (const std::string& b : blocks) s += b;
+  s += "end of trees\n";
+  // split-count importances of splits with gain > 0, by count descending (stable)
+  const int32_t nf = m.max_feature_idx + 1;
+  std::vector<uint64_t> cnt((size_t)std::max(nf, 0), 0);
+  for (const HostTree& t : m.trees)
+    for (size_t i = 0; i < t.split_feature.size(); ++i)
+      if (i < t.split_gain.size() && t.split_gain[i] > 0.0f && t.split_feature[i] < nf)
+        ++cnt[(size_t)t.split_feature[i]];
+  std::vector<std::string> names;
+  {
+    size_t p = 0;
+    while (true) {
+      const size_t e = m.feature_names.find(' ', p);
+      names.push_back(m.feature_names.substr(p, e == std::string::npos ? std::string::npos : e - p));
+      if (e == std::string::npos) break;
+      p = e + 1;
+    }
+  }
+  std::vector<std::pair<uint64_t, size_t>> pairs;
+  for (size_t f = 0; f < cnt.size(); ++f)
+    if (cnt[f] > 0) pairs.push_back({cnt[f], f});
+  std::stable_sort(pairs.begin(), pairs.end(),
+                   [](const std::pair<uint64_t, size_t>& a, const std::pair<uint64_t, size_t>& b) {
+                     return a.first > b.first;
+                   });
+  s += "\nfeature_importances:\n";
+  for (const auto& pr : pairs)
+    s += (pr.second < names.size() ? names[pr.second] : std::string()) + "=" +
+         std::to_string(pr.first) + "\n";
+  if (m.have_trailer) {
+    s += "\n";
+    s += m.trailer;
+  }
+  return s;
+}
 
 bool parse_model_text(const char* text, size_t len, lgbm_hip_model* m, std::string* err) {
   std::string all(text, len);
@@ -257,9 +463,10 @@ bool parse_model_text(const char* text, size_t len, lgbm_hip_model* m, std::stri
     p = e + 1;
   }
   size_t i = 0;
-  bool have_nc = false, have_ntpi = false, have_mfi = false, have_obj = false;
+  bool have_nc = false, have_ntpi = false, have_mfi = false;
   for (; i < lines.size() && lines[i].compare(0, 5, "Tree=") != 0; ++i) {
     const std::string& l = lines[i];
+    if (l == "average_output") m->average_output = true;
     const size_t eq = l.find('=');
     if (eq == std::string::npos) continue;
     const std::string k = l.substr(0, eq), v = l.substr(eq + 1);
@@ -273,14 +480,21 @@ bool parse_model_text(const char* text, size_t len, lgbm_hip_model* m, std::stri
       if (!parse_int(v, &m->max_feature_idx, "max_feature_idx", err)) return false;
       have_mfi = true;
     } else if (k == "objective") {
-      if (!parse_objective(v, m, err)) return false;
-      have_obj = true;
+      if (!model_set_objective(m, v, err)) return false;
+    } else if (k == "label_index") {
+      if (!parse_int(v, &m->label_index, "label_index", err)) return false;
+    } else if (k == "feature_names") {
+      m->feature_names = v;
+    } else if (k == "feature_infos") {
+      m->feature_infos = v;
+    } else if (k == "monotone_constraints") {
+      m->monotone_constraints = v;
+      m->have_monotone = true;
     }
   }
   if (!have_nc) return fail(err, "model without num_class");
   if (!have_mfi) return fail(err, "model without max_feature_idx");
   if (!have_ntpi) m->num_tree_per_iteration = m->num_class;
-  if (!have_obj) m->objective = OBJ_REGRESSION;
   if (m->num_class < 1 || m->num_tree_per_iteration < 1 || m->max_feature_idx < 0)
     return fail(err, "bad num_class / num_tree_per_iteration / max_feature_idx");
   while (i < lines.size()) {
@@ -302,9 +516,26 @@ bool parse_model_text(const char* text, size_t len, lgbm_hip_model* m, std::stri
       ++i;
     }
   }
+  // the `parameters:`..EOF tail, kept verbatim (model_text.rs:190-206)
+  const size_t eot = all.find("end of trees");
+  if (eot != std::string::npos) {
+    size_t q = eot;
+    while ((q = all.find("parameters:", q)) != std::string::npos) {
+      const bool line_start = q == 0 || all[q - 1] == '\n';
+      const size_t after = q + 11;
+      const bool line_end = after == all.size() || all[after] == '\n' ||
+                            (all[after] == '\r' && after + 1 < all.size() && all[after + 1] == '\n');
+      if (line_start && line_end) {
+        m->trailer = all.substr(q);
+        m->have_trailer = true;
+        break;
+      }
+      q = after;
+    }
+  }
   if (m->trees.size() % (size_t)m->num_tree_per_iteration != 0)
     return fail(err, "tree count is not a multiple of num_tree_per_iteration");
-  flatten(m);
+  for (const HostTree& t : m->trees) flatten_tree(m, t);
   m->uid = g_model_uid.fetch_add(1);
   return true;
 }

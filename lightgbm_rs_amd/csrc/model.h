@@ -36,12 +36,23 @@ struct HostTree {
   std::vector<int32_t> split_feature, left_child, right_child, decision_type, cat_boundaries;
   std::vector<double> threshold, leaf_value;
   std::vector<uint32_t> cat_threshold;
+  // metadata kept for the model text (Tree::to_string, tree.rs:800-836)
+  std::vector<float> split_gain;
+  std::vector<double> leaf_weight, internal_value, internal_weight;
+  std::vector<int32_t> leaf_count, internal_count;
+  double shrinkage = 1.0;
 };
 
 struct lgbm_hip_model {
   int32_t num_class = 1, num_tree_per_iteration = 1, max_feature_idx = -1;
   int32_t objective = OBJ_REGRESSION;
   double sigmoid = 1.0;
+  int32_t objective_outputs = 1;  // ObjectiveKind::num_output: num_class for the multiclass kinds
+  // envelope kept verbatim for the model text (model_text.rs:216-320)
+  int32_t label_index = 0;
+  bool average_output = false;
+  bool have_objective = false, have_monotone = false, have_trailer = false;
+  std::string objective_line, feature_names, feature_infos, monotone_constraints, trailer;
   std::vector<HostTree> trees;
   uint64_t uid = 0;  // distinguishes models in the per-context device cache
   // flattened form
@@ -54,3 +65,9 @@ struct lgbm_hip_model {
 
 // Parses `text`; on failure returns false with `err` set (nothing is allocated).
 bool parse_model_text(const char* text, size_t len, lgbm_hip_model* m, std::string* err);
+// The model text of `m` (GBDT::SaveModelToString with split-count importances).
+std::string model_to_text(const lgbm_hip_model& m);
+// Checks a tree built in memory and appends it (flattened form included).
+bool model_add_tree(lgbm_hip_model* m, HostTree&& t, std::string* err);
+// Parses the objective line into m->objective / m->sigmoid.
+bool model_set_objective(lgbm_hip_model* m, const std::string& line, std::string* err);

@@ -62,6 +62,7 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
                                                  int64_t rows, int32_t cols, int32_t it0,
                                                  int32_t it1, int32_t ntpi, int32_t kind,
                                                  int32_t objective, double sigmoid,
+                                                 int32_t average_output,
                                                  double* __restrict__ out,
                                                  int32_t* __restrict__ leaf_out) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -84,6 +85,8 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
     o[k] = acc;
   }
   if (kind != 1) return;
+  if (average_output && it1 > it0)  // RF: raw sum / iterations before ConvertOutput
+    for (int32_t k = 0; k < ntpi; ++k) o[k] /= (double)(it1 - it0);
   switch (objective) {
     case OBJ_REGRESSION_SQRT: {
       const double v = o[0];
@@ -124,13 +127,14 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
 void launch_predict(const PredNode* nodes, const PredTree* trees, const double* leaves,
                     const int32_t* cat_bounds, const uint32_t* cat_words, const float* X,
                     int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
-                    int32_t objective, double sigmoid, double* out, int32_t* leaf_out,
-                    hipStream_t s) {
+                    int32_t objective, double sigmoid, int32_t average_output, double* out,
+                    int32_t* leaf_out, hipStream_t s) {
   if (rows <= 0) return;
   const PredModelDev M{nodes, trees, leaves, cat_bounds, cat_words};
   const int64_t blocks = (rows + 255) / 256;
   k_predict<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(M, X, rows, cols, it0, it1, ntpi, kind,
-                                                         objective, sigmoid, out, leaf_out);
+                                                         objective, sigmoid, average_output, out,
+                                                         leaf_out);
 }
 
 }  // namespace lgbm

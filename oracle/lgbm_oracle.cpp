@@ -539,7 +539,7 @@ struct Tree {
   std::vector<int32_t> split_feature, left_child, right_child, internal_count, leaf_count,
       leaf_depth, leaf_parent;
   std::vector<uint32_t> threshold_in_bin;
-  std::vector<double> threshold, internal_value, leaf_value, leaf_weight;
+  std::vector<double> threshold, internal_value, internal_weight, leaf_value, leaf_weight;
   std::vector<float> split_gain;
   std::vector<int8_t> decision_type;
 
@@ -572,6 +572,7 @@ struct Tree {
     threshold.push_back(thr);
     internal_value.push_back(leaf_value[leaf]);
     internal_count.push_back(lc + rc);
+    internal_weight.push_back(lw + rw);  // C++ Tree::Split (tree.rs:655 keeps 0)
     left_child.push_back(~leaf);
     right_child.push_back(~new_leaf);
     int8_t dt = 0;
@@ -610,6 +611,7 @@ struct Tree {
       if (o->right_child) o->right_child[i] = right_child[i];
       if (o->internal_value) o->internal_value[i] = internal_value[i];
       if (o->internal_count) o->internal_count[i] = internal_count[i];
+      if (o->internal_weight) o->internal_weight[i] = internal_weight[i];
     }
     for (int i = 0; i < num_leaves; ++i) {
       if (o->leaf_value) o->leaf_value[i] = leaf_value[i];

@@ -54,8 +54,9 @@ def parse_tree(lines):
 
 def parse_model(text):
     lines = text.replace("\r", "").split("\n")
-    head, i = {}, 0
+    head, head_lines, i = {}, set(), 0
     while i < len(lines) and not lines[i].startswith("Tree="):
+        head_lines.add(lines[i])
         k, sep, v = lines[i].partition("=")
         if sep:
             head[k] = v
@@ -75,13 +76,14 @@ def parse_model(text):
         else:
             i += 1
     num_class = int(head["num_class"])
-    obj = head.get("objective", "regression").split()
+    obj = head.get("objective", "").split() or [None]
     params = dict(t.split(":", 1) for t in obj[1:] if ":" in t)
     return {"num_class": num_class,
             "num_tree_per_iteration": int(head.get("num_tree_per_iteration", num_class)),
             "max_feature_idx": int(head["max_feature_idx"]),
             "objective": obj[0], "sqrt": "sqrt" in obj[1:],
-            "sigmoid": float(params.get("sigmoid", "1")), "trees": trees}
+            "sigmoid": float(params.get("sigmoid", "1")), "trees": trees,
+            "average_output": "average_output" in head_lines}
 
 
 def _decide(t, node, fval):
@@ -160,6 +162,11 @@ def predict(model, X, start_iteration=0, num_iteration=-1, kind="raw"):
             raw[:, k] = raw[:, k] + t["leaf_value"][leaf_of(t, X64)]
     if kind == "raw":
         return raw
+    if model["objective"] is None:
+        raise ValueError("model has no objective= line; cannot apply ConvertOutput")
+    if model["average_output"] and num > 0:
+        # predict.rs:338-349: RF divides the raw sum by the iteration count first
+        raw = raw / float(num)
     return convert(model, raw)
 
 

@@ -1,0 +1,48 @@
+"""Copy a selection of the reference's committed LightGBM v4 model texts.
+
+Run in the build container (where /root/reference exists):
+
+    python tests/golden/make_model_text_golden.py
+
+The files are data of the reference's own tests (model texts written by the real
+LightGBM 4.6 binary, crates/oracle-harness/tests/fixtures/**); they are copied
+unchanged to tests/golden/model_text/<name>.txt.  Chosen to cover every envelope
+and tree-block form the writer emits: monotone constraints, categorical bitsets
+(num_cat > 0), a constant first tree (empty leaf_weight), average_output (random
+forest), no objective line, multiclass / multiclassova, the exp-family and
+cross-entropy objectives, DART shrinkage values, and the boosting spine models.
+"""
+import os
+import shutil
+
+FIX = "/root/reference/crates/oracle-harness/tests/fixtures"
+OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "model_text")
+FILES = {
+    "mono_mixed": "constraints/mono_mixed.txt",
+    "cat_manyvsmany": "categorical/cat_manyvsmany.txt",
+    "cat_onehot": "categorical/cat_onehot.txt",
+    "l1_constant_tree": "boosting/regression_l1_bag1_es0_bfa0_model.txt",
+    "rf_multi_bag": "rf/rf_multi_bag_model.txt",
+    "rf_single_bag": "rf/rf_single_bag_model.txt",
+    "custom_no_objective": "boosting/custom_spine_model.txt",
+    "multiclassova_spine": "boosting/multiclassova_spine_model.txt",
+    "multiclass_spine": "boosting/multiclass_spine_model.txt",
+    "poisson_spine": "boosting/poisson_spine_model.txt",
+    "xentlambda_spine": "boosting/cross_entropy_lambda_spine_model.txt",
+    "dart_u1_x1_bag1": "dart/dart_u1_x1_bag1_model.txt",
+    "na_missing": "na_missing/model_real.txt",
+    "binary_spine": "boosting/binary_spine_model.txt",
+    "regression_spine": "boosting/regression_spine_model.txt",
+    "forced_nested": "constraints/forced_nested.txt",
+}
+
+
+def main():
+    os.makedirs(OUT, exist_ok=True)
+    for name, rel in FILES.items():
+        shutil.copyfile(os.path.join(FIX, rel), os.path.join(OUT, name + ".txt"))
+        print(name, "<-", rel)
+
+
+if __name__ == "__main__":
+    main()

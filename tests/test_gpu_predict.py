@@ -117,3 +117,70 @@ def test_predict_errors(be):
         be.predict(m, d["X"][:, :20], "raw")
     assert e.value.code == -1  # LENGTH_MISMATCH: fewer columns than max_feature_idx + 1
     assert be.predict(m, d["X"][:0], "raw").shape == (0, 1)
+
+
+@pytest.mark.parametrize("name", ["rf_multi_bag", "rf_single_bag"])
+def test_predict_average_output_vs_oracle(be, name):
+    """Random-forest models (average_output): transformed divides the raw sum by the
+    iteration count before ConvertOutput (predict.rs:338-349)."""
+    text = open(os.path.join(os.path.dirname(GOLD), "model_text", name + ".txt")).read()
+    m, om = Model(text), P.parse_model(text)
+    X = np.random.default_rng(5).normal(size=(4096, m.max_feature_idx + 1)).astype(np.float32)
+    assert np.array_equal(bits(be.predict(m, X, "raw")), bits(P.predict(om, X, kind="raw")))
+    np.testing.assert_allclose(be.predict(m, X, "transformed"),
+                               P.predict(om, X, kind="transformed"), rtol=1e-14, atol=0)
+
+
+def test_transformed_needs_objective(be):
+    text = open(os.path.join(os.path.dirname(GOLD), "model_text", "custom_no_objective.txt")).read()
+    m = Model(text)
+    X = np.zeros((3, m.max_feature_idx + 1), np.float32)
+    be.predict(m, X, "raw")
+    with pytest.raises(HipError) as e:
+        be.predict(m, X, "transformed")
+    assert "objective" in str(e.value)
+
+
+def _binned_table(n, seed, max_bin=63):
+    """float32 features with their quantile bins (bin b <=> ub[b-1] < x <= ub[b])."""
+    from lightgbm_rs_amd.synth import _meta_for
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((n, 12)).astype(np.float32)
+    X[:, 3] = np.round(X[:, 3] * 2)  # a few-valued column
+    w = rng.standard_normal(12).astype(np.float32)
+    y = (rng.random(n) < 1 / (1 + np.exp(-(X @ w)))).astype(np.float32)
+    bins = np.zeros((12, n), np.uint8)
+    ub, nbs = [], []
+    for f in range(12):
+        qs = np.unique(np.quantile(X[:, f], np.linspace(0, 1, max_bin + 1)[1:-1]).astype(np.float32))
+        bins[f] = np.searchsorted(qs, X[:, f], side="left")
+        nbs.append(len(qs) + 1)
+        ub.extend([float(q) for q in qs] + [np.inf])
+    return X, bins, _meta_for(nbs), np.array(ub), y
+
+
+@pytest.mark.parametrize("quant", [4, 0])
+def test_trained_model_text_predicts_training_scores(be, quant):
+    """Trees grown by the resident boosting loop, assembled into a model (the first
+    tree carrying the init score), written as model text and read back: the device
+    predictor reproduces the training scores bit for bit."""
+    from lightgbm_rs_amd import GainConfig
+    from oracle import oracle
+    print(f"trained model predict quant={quant}", flush=True)
+    X, bins, meta, ub, y = _binned_table(30_000, seed=41)
+    init = oracle.boost_from_score(y)
+    be.upload_resident_bins(bins, meta, ub)
+    be.set_labels(y, init)
+    cfg = GainConfig.make(min_data_in_leaf=20)
+    m = Model.create(num_class=1, max_feature_idx=11, objective="binary sigmoid:1")
+    for i in range(6):
+        t = be.train_iter_binary(i, cfg, 31, -1, 0.1, quant, quant > 0)
+        assert np.all(t["internal_weight"] > 0)
+        m.add_tree(t, shrinkage=0.1, bias=init if i == 0 else 0.0)
+    scores = be.scores()
+    text = m.to_text()
+    back = Model(text)
+    assert back.to_text() == text
+    got = be.predict(back, X, "raw")[:, 0]
+    assert np.array_equal(bits(got), bits(scores))
+    assert np.array_equal(bits(P.predict(P.parse_model(text), X, kind="raw")[:, 0]), bits(scores))
