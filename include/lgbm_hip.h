@@ -295,6 +295,90 @@ int lgbm_hip_get_timing(lgbm_hip_ctx* ctx, double* ms_out5, double* hist_bytes_o
  * [15] rounds launched after the captured per-tree sequence. */
 int lgbm_hip_get_stats(lgbm_hip_ctx* ctx, double* out16);
 
+/* ---- binning ------------------------------------------------------------------ */
+
+/* BinMapper construction parameters (crates/lgbm/src/builder.rs config fields;
+ * LightGBM defaults in brackets). */
+typedef struct lgbm_bin_params {
+  int32_t max_bin;                  /* [255] */
+  int32_t min_data_in_bin;          /* [3] */
+  int32_t min_data_in_leaf;         /* [20] scaled into the pre-filter threshold */
+  int32_t pre_filter;               /* [0] feature_pre_filter (the facade passes false) */
+  int32_t use_missing;              /* [1] */
+  int32_t zero_as_missing;          /* [0] */
+  int32_t bin_construct_sample_cnt; /* [200000] */
+  int32_t data_random_seed;         /* [1] */
+} lgbm_bin_params;
+
+#define LGBM_BIN_NUMERICAL 0
+#define LGBM_BIN_CATEGORICAL 1
+typedef struct lgbm_bin_mapper_info {
+  int32_t num_bin;
+  int32_t missing_type; /* LGBM_MISSING_* */
+  int32_t bin_type;     /* LGBM_BIN_* */
+  int32_t is_trivial;
+  uint32_t default_bin; /* ValueToBin(0) */
+  uint32_t most_freq_bin;
+  double sparse_rate;
+  double min_val;
+  double max_val;
+} lgbm_bin_mapper_info;
+
+/* One feature's value -> bin mapper, built on the host. */
+typedef struct lgbm_hip_bin_mapper lgbm_hip_bin_mapper;
+/* BinMapper::find_bin_from_column (crates/lgbm-dataset/src/bin_mapper.rs:613-651):
+ * Random(data_random_seed).Sample(num_rows, min(num_rows, bin_construct_sample_cnt))
+ * rows of the column, the pre-filter threshold min_data_in_leaf * sampled / num_rows,
+ * then the numeric FindBin (bin_mapper.rs:191-365) with optional forced bounds. */
+int lgbm_hip_bin_mapper_from_column(const double* column, int64_t num_rows,
+                                    const lgbm_bin_params* params,
+                                    const double* forced_upper_bounds, int32_t num_forced,
+                                    lgbm_hip_bin_mapper** out);
+/* FindBin on given sample values: find_bin_numeric (bin_mapper.rs:191-365) or, with
+ * categorical set, find_bin_categorical (bin_mapper.rs:409-560; the booster bins
+ * categorical columns whole, booster.rs:466-476).  total_sample_cnt - num_values
+ * zeros are implied; min_split_data is the pre-filter threshold as is. */
+int lgbm_hip_bin_mapper_from_sample(const double* values, int64_t num_values,
+                                    int64_t total_sample_cnt, int32_t categorical,
+                                    const lgbm_bin_params* params, int32_t min_split_data,
+                                    const double* forced_upper_bounds, int32_t num_forced,
+                                    lgbm_hip_bin_mapper** out);
+int lgbm_hip_bin_mapper_free(lgbm_hip_bin_mapper* mapper);
+/* Message of the last failed lgbm_hip_bin_mapper_from_* (process-wide). */
+int lgbm_hip_bin_last_error(char* buf, size_t size);
+int lgbm_hip_bin_mapper_info(const lgbm_hip_bin_mapper* mapper, lgbm_bin_mapper_info* out);
+/* num_bin entries each (either may be NULL): numerical upper bounds
+ * (bin_upper_bound_, NaN for the NaN bin), categorical bin -> category
+ * (bin_2_categorical_, -1 for bin 0). */
+int lgbm_hip_bin_mapper_bounds(const lgbm_hip_bin_mapper* mapper, double* upper,
+                               int32_t* categories);
+/* ValueToBin (bin_mapper.rs:148-189) on the host. */
+int lgbm_hip_bin_mapper_value_to_bin(const lgbm_hip_bin_mapper* mapper, const double* values,
+                                     int64_t n, uint32_t* out);
+/* Random::sample (crates/lgbm-core/src/random.rs) of min(num_rows, sample_cnt) rows:
+ * out (capacity min(num_rows, sample_cnt), may be NULL) gets the ascending indices. */
+int lgbm_hip_sample_indices(int32_t num_rows, int32_t sample_cnt, int32_t seed, int32_t* out,
+                            int32_t* out_len);
+
+#define LGBM_HIP_DTYPE_F32 0
+#define LGBM_HIP_DTYPE_F64 1
+/* Bins a dense raw matrix on the device into the resident bin layout: the feature
+ * columns of the booster's ingestion (crates/lgbm/src/booster.rs:449-520: value_to_bin
+ * per row, one single-feature group per mapper, offset_for_most_freq_bin), replacing
+ * lgbm_hip_upload_bins' host-binned input.  values: num_rows x num_cols of
+ * LGBM_HIP_DTYPE_*, column-major ([col][row]) when col_major is set, else row-major;
+ * mappers[num_cols] numerical (categorical: LGBM_HIP_ERR_CAPABILITY).  _device takes
+ * device memory of the context's device; the other copies a host matrix over. */
+int lgbm_hip_upload_raw_device(lgbm_hip_ctx* ctx, const void* d_values, int32_t dtype,
+                               int32_t col_major, int64_t num_rows, int32_t num_cols,
+                               const lgbm_hip_bin_mapper* const* mappers);
+int lgbm_hip_upload_raw(lgbm_hip_ctx* ctx, const void* values, int32_t dtype, int32_t col_major,
+                        int64_t num_rows, int32_t num_cols,
+                        const lgbm_hip_bin_mapper* const* mappers);
+/* The resident bins, feature-major [num_features][num_data] (no reference
+ * counterpart: the reference's FeatureColumn.bins are host data). */
+int lgbm_hip_get_bins(lgbm_hip_ctx* ctx, uint8_t* out, int64_t num_data);
+
 /* ---- models and batch prediction ------------------------------------------ */
 
 /* A LightGBM v4 model text, parsed on the host (no device needed): replaces

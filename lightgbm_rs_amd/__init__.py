@@ -5,3 +5,4 @@ this package is the Python host mirror of the reference's `Backend` seam.
 """
 from ._abi import FeatureMeta, GainConfig, SplitInfo, BatchedFeature  # noqa: F401
 from .backend import HipBackend, HipError, Model, feature_meta, load_library  # noqa: F401
+from .binning import BinMapper, feature_mappers, sample_indices  # noqa: F401

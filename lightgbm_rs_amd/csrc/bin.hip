@@ -1,0 +1,118 @@
+// bin.hip — raw feature values -> resident bin records on the device.
+//
+// ValueToBin (crates/lgbm-dataset/src/bin_mapper.rs:148-189) for every value of a
+// dense matrix, fused with the record packing of k_pack_records: one thread per
+// row, the row's bins packed into its 16W-byte record with the row index in the
+// last word.  Numerical features search their upper bounds (staged in LDS) with
+// the reference's `m = (r + l - 1) / 2`, `v <= ub[m]` bisection; categorical
+// features look their integer category up in a sorted (category, bin) table.
+// HBM-bound: 4 or 8 bytes read and one byte written per value, plus the 4-byte row
+// index per record.
+#include "kernels.h"
+
+namespace lgbm {
+
+namespace {
+
+constexpr int32_t BIN_LDS_BOUNDS = 7168;  // 56 KiB of staged upper bounds
+
+__device__ __forceinline__ int32_t sat_i32(double x) {
+  if (!(x == x)) return 0;
+  if (x >= 2147483647.0) return 2147483647;
+  if (x <= -2147483648.0) return (-2147483647 - 1);
+  return (int32_t)x;
+}
+
+__device__ __forceinline__ uint32_t bin_of(const DevBinFeature& f, const double* ub,
+                                           const int2* __restrict__ cats, double v) {
+  if (v != v) {
+    if (f.categorical) return 0u;
+    if (f.nan_bin >= 0) return (uint32_t)f.nan_bin;
+    v = 0.0;
+  }
+  if (!f.categorical) {
+    const double* u = ub + f.off;
+    int32_t l = 0, r = f.last;
+    while (l < r) {
+      const int32_t m = (r + l - 1) / 2;
+      if (v <= u[m])
+        r = m;
+      else
+        l = m + 1;
+    }
+    return (uint32_t)l;
+  }
+  const int32_t key = sat_i32(v);
+  if (key < 0) return 0u;
+  const int2* c = cats + f.off;
+  int32_t lo = 0, hi = f.ncat;
+  while (lo < hi) {
+    const int32_t m = (lo + hi) >> 1;
+    if (c[m].x < key)
+      lo = m + 1;
+    else
+      hi = m;
+  }
+  return (lo < f.ncat && c[lo].x == key) ? (uint32_t)c[lo].y : 0u;
+}
+
+template <typename T, bool COL_MAJOR>
+__global__ __launch_bounds__(256) void k_bin_records(const T* __restrict__ x, int64_t n, int32_t F,
+                                                     int32_t W, const DevBinFeature* __restrict__ feats,
+                                                     const double* __restrict__ ub, int32_t ub_count,
+                                                     const int2* __restrict__ cats,
+                                                     uint4* __restrict__ rec) {
+  extern __shared__ double s_ub[];
+  __shared__ DevBinFeature s_f[16 * LGBM_MAX_W];
+  // bounds beyond the LDS budget are read through the caches instead
+  const bool staged = ub_count <= BIN_LDS_BOUNDS;
+  if (staged)
+    for (int i = threadIdx.x; i < ub_count; i += blockDim.x) s_ub[i] = ub[i];
+  const double* bounds = staged ? s_ub : ub;
+  for (int i = threadIdx.x; i < F; i += blockDim.x) s_f[i] = feats[i];
+  __syncthreads();
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
+    uint32_t words[4 * LGBM_MAX_W];
+#pragma unroll
+    for (int i = 0; i < 4 * LGBM_MAX_W; ++i) words[i] = 0u;
+    for (int f = 0; f < F; ++f) {
+      const double v = (double)(COL_MAJOR ? x[(int64_t)f * n + r] : x[r * F + f]);
+      words[f >> 2] |= bin_of(s_f[f], bounds, cats, v) << (8 * (f & 3));
+    }
+    words[4 * W - 1] = (uint32_t)r;
+    for (int w = 0; w < W; ++w)
+      rec[r * W + w] = make_uint4(words[4 * w], words[4 * w + 1], words[4 * w + 2], words[4 * w + 3]);
+  }
+}
+
+template <typename T, bool CM>
+void launch_typed(const void* x, int64_t n, int32_t F, int32_t W, const DevBinFeature* feats,
+                  const double* ub, int32_t ub_count, const int2* cats, uint4* rec, hipStream_t s) {
+  const int64_t want = (n + 255) / 256;
+  const unsigned blocks = (unsigned)std::min<int64_t>(std::max<int64_t>(want, 1), 4096);
+  const size_t lds = ub_count <= BIN_LDS_BOUNDS ? (size_t)ub_count * sizeof(double) : 0;
+  k_bin_records<T, CM><<<dim3(blocks), dim3(256), lds, s>>>(
+      (const T*)x, n, F, W, feats, ub, ub_count, cats, rec);
+}
+
+}  // namespace
+
+void launch_bin_records(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
+                        int32_t W, const DevBinFeature* feats, const double* ub, int32_t ub_count,
+                        const int2* cats, uint4* rec, hipStream_t s) {
+  if (n <= 0) return;
+  if (f64) {
+    if (col_major)
+      launch_typed<double, true>(x, n, F, W, feats, ub, ub_count, cats, rec, s);
+    else
+      launch_typed<double, false>(x, n, F, W, feats, ub, ub_count, cats, rec, s);
+  } else {
+    if (col_major)
+      launch_typed<float, true>(x, n, F, W, feats, ub, ub_count, cats, rec, s);
+    else
+      launch_typed<float, false>(x, n, F, W, feats, ub, ub_count, cats, rec, s);
+  }
+}
+
+}  // namespace lgbm

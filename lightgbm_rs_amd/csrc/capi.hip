@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "kernels.h"
+#include "binning.h"
 #include "model.h"
 
 using namespace lgbm;
@@ -29,6 +30,7 @@ void launch_predict(const PredNode* nodes, const PredTree* trees, const double* 
 namespace {
 
 thread_local std::string g_create_err;
+std::string g_bin_err;    // last failed lgbm_hip_bin_mapper_*
 std::string g_model_err;  // last failed lgbm_hip_model_load
 
 struct EventPair {
@@ -645,6 +647,115 @@ DevFeature feature_from_batched(const lgbm_batched_feature& b) {
 
 }  // namespace
 
+// Shared by the bin uploads: feature table, record and histogram buffers for a
+// resident matrix of F features x N rows (the records themselves are written by the
+// caller).
+int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_feature_meta* meta,
+                   const double* bin_upper_bound) {
+  int rc = 0;
+  const int32_t F = F_in;
+  if (F > 16 * LGBM_MAX_W - 4)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "more features than the record layout holds");
+  if (num_data >= (1ll << 31) - 1)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_data must fit data_size_t (i32)");
+  std::vector<DevFeature> feats(F);
+  uint32_t acc = 0, uacc = 0;
+  for (int f = 0; f < F; ++f) {
+    const lgbm_feature_meta& m = meta[f];
+    if (m.num_bin == 0 || m.num_bin > 256)
+      return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be in 1..=256 (u8 bin storage)");
+    DevFeature& d = feats[f];
+    d.num_bin = m.num_bin;
+    d.offset = m.offset;
+    d.min_bin = m.min_bin;
+    d.max_bin = m.max_bin;
+    d.default_bin = m.default_bin;
+    d.mfb = m.most_freq_bin;
+    d.missing_type = m.missing_type;
+    d.real_index = m.real_feature_index;
+    d.slot_off = 2 * acc;
+    d.cell_base = acc;
+    d.ub_off = uacc;
+    d.skip_default_bin = (m.num_bin > 2 && m.missing_type == LGBM_MISSING_ZERO) ? 1 : 0;
+    d.na_as_missing = (m.num_bin > 2 && m.missing_type == LGBM_MISSING_NAN) ? 1 : 0;
+    d.run_forward = (m.num_bin > 2 && m.missing_type != LGBM_MISSING_NONE) ? 1 : 0;
+    acc += m.num_bin;
+    uacc += m.num_bin;
+  }
+  if (acc > 8192)  // 8 B per LDS cell, 64 KiB of dynamic LDS per block
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "histogram exceeds the LDS budget");
+  if (acc > (uint32_t)(MAX_FGROUPS - 1) * (HIST_FP_CELLS - 256))
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "too many histogram cells for the f32 feature groups");
+  if (acc > HIST_WAVE_CELLS && num_data > (int64_t)HIST_GRID * HIST_BLOCK_MAX_ROWS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "rows per histogram block exceed the packed LDS cell fields");
+  c->F = F;
+  c->N = num_data;
+  c->W = (F + 4 + 15) / 16;
+  c->total_cells = (int32_t)acc;
+  c->slot_len = 2ull * acc;
+  c->feats = feats;
+  c->lcap = 0;  // slots depend on slot_len
+  if ((rc = dalloc(c, &c->d_feats, (size_t)F))) return rc;
+  HIPCHK(c, hipMemcpy(c->d_feats, feats.data(), F * sizeof(DevFeature), hipMemcpyHostToDevice));
+  if (bin_upper_bound) {
+    if ((rc = dalloc(c, &c->d_ub, (size_t)uacc))) return rc;
+    HIPCHK(c, hipMemcpy(c->d_ub, bin_upper_bound, uacc * 8, hipMemcpyHostToDevice));
+  } else if (c->d_ub) {
+    (void)hipFree(c->d_ub);
+    c->d_ub = nullptr;
+  }
+  const size_t words = (size_t)num_data * c->W;
+  for (int b : {BUF_ORIG, BUF_A, BUF_B}) {
+    if ((rc = dalloc(c, &c->rec[b], words))) return rc;
+    if ((rc = dalloc(c, &c->gh[b], (size_t)num_data))) return rc;
+    c->buf_rows[b] = num_data;
+  }
+  c->buf_rows[BUF_S0] = c->buf_rows[BUF_S1] = 0;
+  if ((rc = dalloc(c, &c->g, (size_t)num_data))) return rc;
+  if ((rc = dalloc(c, &c->h, (size_t)num_data))) return rc;
+  if ((rc = dalloc(c, &c->hist_part, (size_t)HIST_SLOTS * acc * 3))) return rc;
+  if ((rc = dalloc(c, &c->hist_part64, (size_t)HIST_SLOTS * acc * 2))) return rc;
+  // feature groups of the f32 histogram kernel: consecutive features whose cells fit
+  // one block's LDS
+  {
+    int32_t ng = 0;
+    uint32_t gcells = 0;
+    c->fgroup_first[0] = 0;
+    for (int f = 0; f < F; ++f) {
+      if (f > 0 && gcells + feats[f].num_bin > HIST_FP_CELLS) {
+        c->fgroup_first[++ng] = f;
+        gcells = 0;
+      }
+      gcells += feats[f].num_bin;
+    }
+    c->fgroup_first[++ng] = F;
+    c->n_fgroups = ng;
+  }
+  if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * acc * 3))) return rc;
+  HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * acc * 3 * 4));
+  if ((rc = dalloc(c, &c->part_slots, ((size_t)c->part_blocks + SPEC_MAX) * acc * 4))) return rc;
+  if ((rc = ensure_tile_state(c, num_data))) return rc;
+  return LGBM_HIP_OK;
+}
+
+BinParams bin_params_of(const lgbm_bin_params& p) {
+  BinParams b;
+  b.max_bin = p.max_bin;
+  b.min_data_in_bin = p.min_data_in_bin;
+  b.pre_filter = p.pre_filter != 0;
+  b.use_missing = p.use_missing != 0;
+  b.zero_as_missing = p.zero_as_missing != 0;
+  return b;
+}
+
+int resident_done(lgbm_hip_ctx* c) {
+  c->have_bins = true;
+  c->have_grad = c->quant_ready = c->have_labels = false;
+  c->buf_gen++;
+  return LGBM_HIP_OK;
+}
+
 extern "C" {
 
 int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
@@ -783,46 +894,14 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   if (rc) return rc;
   if (!bins || !meta || num_features <= 0 || num_data <= 0)
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null bins/meta or empty shape");
-  if (num_features > 16 * LGBM_MAX_W - 4)
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "more features than the record layout holds");
-  if (num_data >= (1ll << 31) - 1)
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_data must fit data_size_t (i32)");
   const int32_t F = num_features;
-  std::vector<DevFeature> feats(F);
-  uint32_t acc = 0, uacc = 0;
-  for (int f = 0; f < F; ++f) {
-    const lgbm_feature_meta& m = meta[f];
-    if (m.num_bin == 0 || m.num_bin > 256)
+  for (int f = 0; f < F; ++f)
+    if (meta[f].num_bin == 0 || meta[f].num_bin > 256)
       return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be in 1..=256 (u8 bin storage)");
-    DevFeature& d = feats[f];
-    d.num_bin = m.num_bin;
-    d.offset = m.offset;
-    d.min_bin = m.min_bin;
-    d.max_bin = m.max_bin;
-    d.default_bin = m.default_bin;
-    d.mfb = m.most_freq_bin;
-    d.missing_type = m.missing_type;
-    d.real_index = m.real_feature_index;
-    d.slot_off = 2 * acc;
-    d.cell_base = acc;
-    d.ub_off = uacc;
-    d.skip_default_bin = (m.num_bin > 2 && m.missing_type == LGBM_MISSING_ZERO) ? 1 : 0;
-    d.na_as_missing = (m.num_bin > 2 && m.missing_type == LGBM_MISSING_NAN) ? 1 : 0;
-    d.run_forward = (m.num_bin > 2 && m.missing_type != LGBM_MISSING_NONE) ? 1 : 0;
-    acc += m.num_bin;
-    uacc += m.num_bin;
-  }
-  if (acc > 8192)  // 8 B per LDS cell, 64 KiB of dynamic LDS per block
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "histogram exceeds the LDS budget");
-  if (acc > (uint32_t)(MAX_FGROUPS - 1) * (HIST_FP_CELLS - 256))
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "too many histogram cells for the f32 feature groups");
-  if (acc > HIST_WAVE_CELLS && num_data > (int64_t)HIST_GRID * HIST_BLOCK_MAX_ROWS)
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
-                   "rows per histogram block exceed the packed LDS cell fields");
   // bin-range gate (learner.rs:1161-1187): first offending bin, feature order
   for (int f = 0; f < F; ++f) {
     const uint8_t* col = bins + (size_t)f * (size_t)num_data;
-    const uint32_t nb = feats[f].num_bin;
+    const uint32_t nb = meta[f].num_bin;
     if (nb >= 256) continue;
     for (int64_t r = 0; r < num_data; ++r)
       if (col[r] >= nb)
@@ -830,53 +909,7 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
                        "bin " + std::to_string(col[r]) + " >= num_bin " + std::to_string(nb) +
                            " (feature " + std::to_string(f) + ", row " + std::to_string(r) + ")");
   }
-  c->F = F;
-  c->N = num_data;
-  c->W = (F + 4 + 15) / 16;
-  c->total_cells = (int32_t)acc;
-  c->slot_len = 2ull * acc;
-  c->feats = feats;
-  c->lcap = 0;  // slots depend on slot_len
-  if ((rc = dalloc(c, &c->d_feats, (size_t)F))) return rc;
-  HIPCHK(c, hipMemcpy(c->d_feats, feats.data(), F * sizeof(DevFeature), hipMemcpyHostToDevice));
-  if (bin_upper_bound) {
-    if ((rc = dalloc(c, &c->d_ub, (size_t)uacc))) return rc;
-    HIPCHK(c, hipMemcpy(c->d_ub, bin_upper_bound, uacc * 8, hipMemcpyHostToDevice));
-  } else if (c->d_ub) {
-    (void)hipFree(c->d_ub);
-    c->d_ub = nullptr;
-  }
-  const size_t words = (size_t)num_data * c->W;
-  for (int b : {BUF_ORIG, BUF_A, BUF_B}) {
-    if ((rc = dalloc(c, &c->rec[b], words))) return rc;
-    if ((rc = dalloc(c, &c->gh[b], (size_t)num_data))) return rc;
-    c->buf_rows[b] = num_data;
-  }
-  c->buf_rows[BUF_S0] = c->buf_rows[BUF_S1] = 0;
-  if ((rc = dalloc(c, &c->g, (size_t)num_data))) return rc;
-  if ((rc = dalloc(c, &c->h, (size_t)num_data))) return rc;
-  if ((rc = dalloc(c, &c->hist_part, (size_t)HIST_SLOTS * acc * 3))) return rc;
-  if ((rc = dalloc(c, &c->hist_part64, (size_t)HIST_SLOTS * acc * 2))) return rc;
-  // feature groups of the f32 histogram kernel: consecutive features whose cells fit
-  // one block's LDS
-  {
-    int32_t ng = 0;
-    uint32_t gcells = 0;
-    c->fgroup_first[0] = 0;
-    for (int f = 0; f < F; ++f) {
-      if (f > 0 && gcells + feats[f].num_bin > HIST_FP_CELLS) {
-        c->fgroup_first[++ng] = f;
-        gcells = 0;
-      }
-      gcells += feats[f].num_bin;
-    }
-    c->fgroup_first[++ng] = F;
-    c->n_fgroups = ng;
-  }
-  if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * acc * 3))) return rc;
-  HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * acc * 3 * 4));
-  if ((rc = dalloc(c, &c->part_slots, ((size_t)c->part_blocks + SPEC_MAX) * acc * 4))) return rc;
-  if ((rc = ensure_tile_state(c, num_data))) return rc;
+  if ((rc = resident_setup(c, F, num_data, meta, bin_upper_bound))) return rc;
   // transpose the feature-major upload into records
   uint8_t* tmp = nullptr;
   HIPCHK(c, hipMalloc((void**)&tmp, (size_t)F * num_data));
@@ -887,9 +920,213 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   }
   (void)hipFree(tmp);
   if (e != hipSuccess) return set_err(c, LGBM_HIP_ERR_HIP, hipGetErrorString(e));
-  c->have_bins = true;
-  c->have_grad = c->quant_ready = c->have_labels = false;
-  c->buf_gen++;
+  return resident_done(c);
+}
+
+// ---- binning ------------------------------------------------------------------
+
+int lgbm_hip_bin_mapper_from_column(const double* column, int64_t num_rows,
+                                    const lgbm_bin_params* p, const double* forced_upper_bounds,
+                                    int32_t num_forced, lgbm_hip_bin_mapper** out) {
+  if (!out || !p || (num_rows > 0 && !column) || num_rows < 0 || num_rows >= (1ll << 31) ||
+      num_forced < 0 || (num_forced > 0 && !forced_upper_bounds)) {
+    g_bin_err = "null argument, negative size or more than 2^31-1 rows";
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  if (p->max_bin < 2 || p->bin_construct_sample_cnt < 1) {
+    g_bin_err = "max_bin must be >= 2 and bin_construct_sample_cnt >= 1";
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  // BinMapper::find_bin_from_column (bin_mapper.rs:613-651): sample, scale the
+  // pre-filter threshold, then the numeric FindBin
+  const int32_t n = (int32_t)num_rows;
+  const std::vector<int32_t> idx = bin_sample_indices(n, p->bin_construct_sample_cnt,
+                                                      p->data_random_seed);
+  std::vector<double> sample(idx.size());
+  for (size_t i = 0; i < idx.size(); ++i) sample[i] = column[idx[i]];
+  BinParams bp = bin_params_of(*p);
+  bp.min_split_data = bin_scaled_filter_cnt(p->min_data_in_leaf, (int32_t)sample.size(), n);
+  const int64_t total = (int64_t)sample.size();
+  *out = new lgbm_hip_bin_mapper(find_bin_numeric(
+      std::move(sample), bp, total,
+      std::vector<double>(forced_upper_bounds, forced_upper_bounds + num_forced)));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_bin_mapper_from_sample(const double* values, int64_t num_values,
+                                    int64_t total_sample_cnt, int32_t categorical,
+                                    const lgbm_bin_params* p, int32_t min_split_data,
+                                    const double* forced_upper_bounds, int32_t num_forced,
+                                    lgbm_hip_bin_mapper** out) {
+  if (!out || !p || (num_values > 0 && !values) || num_values < 0 ||
+      total_sample_cnt < num_values || total_sample_cnt >= (1ll << 31) || num_forced < 0 ||
+      (num_forced > 0 && !forced_upper_bounds)) {
+    g_bin_err = "null argument, or total_sample_cnt outside [num_values, 2^31)";
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  if (p->max_bin < 2) {
+    g_bin_err = "max_bin must be >= 2";
+    return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  }
+  BinParams bp = bin_params_of(*p);
+  bp.min_split_data = min_split_data;
+  std::vector<double> v(values, values + num_values);
+  if (categorical)
+    *out = new lgbm_hip_bin_mapper(find_bin_categorical(std::move(v), bp, total_sample_cnt));
+  else
+    *out = new lgbm_hip_bin_mapper(find_bin_numeric(
+        std::move(v), bp, total_sample_cnt,
+        std::vector<double>(forced_upper_bounds, forced_upper_bounds + num_forced)));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_bin_mapper_free(lgbm_hip_bin_mapper* m) {
+  delete m;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_bin_last_error(char* buf, size_t size) {
+  if (buf && size > 0) std::snprintf(buf, size, "%s", g_bin_err.c_str());
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_bin_mapper_info(const lgbm_hip_bin_mapper* m, lgbm_bin_mapper_info* out) {
+  if (!m || !out) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  out->num_bin = m->num_bin;
+  out->missing_type = m->missing_type;
+  out->bin_type = m->bin_type;
+  out->is_trivial = m->is_trivial ? 1 : 0;
+  out->default_bin = m->default_bin;
+  out->most_freq_bin = m->most_freq_bin;
+  out->sparse_rate = m->sparse_rate;
+  out->min_val = m->min_val;
+  out->max_val = m->max_val;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_bin_mapper_bounds(const lgbm_hip_bin_mapper* m, double* upper, int32_t* categories) {
+  if (!m) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  for (int32_t b = 0; b < m->num_bin; ++b) {
+    if (upper) upper[b] = m->bin_type == LGBM_BIN_NUMERICAL ? m->upper[(size_t)b] : 0.0;
+    if (categories)
+      categories[b] = m->bin_type == LGBM_BIN_CATEGORICAL && (size_t)b < m->bin_to_cat.size()
+                          ? m->bin_to_cat[(size_t)b]
+                          : 0;
+  }
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_bin_mapper_value_to_bin(const lgbm_hip_bin_mapper* m, const double* values,
+                                     int64_t n, uint32_t* out) {
+  if (!m || n < 0 || (n > 0 && (!values || !out))) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  for (int64_t i = 0; i < n; ++i) out[i] = m->value_to_bin(values[i]);
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_sample_indices(int32_t num_rows, int32_t sample_cnt, int32_t seed, int32_t* out,
+                            int32_t* out_len) {
+  if (!out_len || num_rows < 0) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  const std::vector<int32_t> idx = bin_sample_indices(num_rows, sample_cnt, seed);
+  *out_len = (int32_t)idx.size();
+  if (out && !idx.empty()) std::memcpy(out, idx.data(), idx.size() * 4);
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dtype,
+                               int32_t col_major, int64_t num_rows, int32_t num_cols,
+                               const lgbm_hip_bin_mapper* const* mappers) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!d_values || !mappers || num_rows <= 0 || num_cols <= 0)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null values/mappers or empty shape");
+  if (dtype != LGBM_HIP_DTYPE_F32 && dtype != LGBM_HIP_DTYPE_F64)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "dtype must be F32 or F64");
+  const int32_t F = num_cols;
+  // feature columns (booster.rs:449-520): one single-feature group per mapper
+  std::vector<lgbm_feature_meta> meta((size_t)F);
+  std::vector<DevBinFeature> bf((size_t)F);
+  std::vector<double> ub;
+  std::vector<int2> cats;
+  for (int32_t f = 0; f < F; ++f) {
+    const lgbm_hip_bin_mapper* m = mappers[f];
+    if (!m) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null mapper");
+    if (m->num_bin < 1 || m->num_bin > 256)
+      return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be in 1..=256 (u8 bin storage)");
+    if (m->bin_type == LGBM_BIN_CATEGORICAL)
+      return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                     "categorical features need the categorical split scan, which this build lacks");
+    lgbm_feature_meta& d = meta[(size_t)f];
+    d.num_bin = (uint32_t)m->num_bin;
+    d.offset = m->most_freq_bin == 0 ? 1 : 0;  // offset_for_most_freq_bin (lib.rs:89-95)
+    d.min_bin = 0;
+    d.max_bin = (uint32_t)m->num_bin - 1;
+    d.default_bin = m->default_bin;
+    d.most_freq_bin = m->most_freq_bin;
+    d.missing_type = m->missing_type;
+    d.real_feature_index = f;
+    DevBinFeature& b = bf[(size_t)f];
+    b = DevBinFeature{};
+    b.categorical = 0;
+    b.nan_bin = m->missing_type == BIN_MISSING_NAN ? m->num_bin - 1 : -1;
+    b.last = m->num_bin - 1 - (b.nan_bin >= 0 ? 1 : 0);
+    b.off = (int32_t)ub.size();
+    ub.insert(ub.end(), m->upper.begin(), m->upper.end());
+  }
+  cats.push_back(make_int2(0, 0));  // never read: keeps the table non-empty
+  if ((rc = resident_setup(c, F, num_rows, meta.data(), ub.data()))) return rc;
+  DevBinFeature* d_bf = nullptr;
+  int2* d_cats = nullptr;
+  hipError_t e = hipMalloc((void**)&d_bf, bf.size() * sizeof(DevBinFeature));
+  if (e == hipSuccess) e = hipMalloc((void**)&d_cats, cats.size() * sizeof(int2));
+  if (e == hipSuccess)
+    e = hipMemcpy(d_bf, bf.data(), bf.size() * sizeof(DevBinFeature), hipMemcpyHostToDevice);
+  if (e == hipSuccess)
+    e = hipMemcpy(d_cats, cats.data(), cats.size() * sizeof(int2), hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    // c->d_ub holds the same bounds, concatenated in feature order
+    launch_bin_records(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->W, d_bf,
+                       c->d_ub, (int32_t)ub.size(), d_cats, c->rec[BUF_ORIG], c->stream);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  }
+  (void)hipFree(d_bf);
+  (void)hipFree(d_cats);
+  if (e != hipSuccess) return set_err(c, LGBM_HIP_ERR_HIP, hipGetErrorString(e));
+  return resident_done(c);
+}
+
+int lgbm_hip_upload_raw(lgbm_hip_ctx* c, const void* values, int32_t dtype, int32_t col_major,
+                        int64_t num_rows, int32_t num_cols,
+                        const lgbm_hip_bin_mapper* const* mappers) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!values || num_rows <= 0 || num_cols <= 0)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null values or empty shape");
+  const size_t bytes = (size_t)num_rows * (size_t)num_cols * (dtype == LGBM_HIP_DTYPE_F64 ? 8 : 4);
+  void* tmp = nullptr;
+  HIPCHK(c, hipMalloc(&tmp, bytes));
+  hipError_t e = hipMemcpy(tmp, values, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(tmp);
+    return set_err(c, LGBM_HIP_ERR_HIP, hipGetErrorString(e));
+  }
+  rc = lgbm_hip_upload_raw_device(c, tmp, dtype, col_major, num_rows, num_cols, mappers);
+  (void)hipFree(tmp);
+  return rc;
+}
+
+int lgbm_hip_get_bins(lgbm_hip_ctx* c, uint8_t* out, int64_t n) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "no resident bins");
+  if (!out || n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_data");
+  // the original (unpartitioned) records, feature-major
+  std::vector<uint32_t> rec((size_t)c->N * 4 * c->W);
+  HIPCHK(c, hipMemcpy(rec.data(), c->rec[BUF_ORIG], rec.size() * 4, hipMemcpyDeviceToHost));
+  for (int64_t r = 0; r < c->N; ++r)
+    for (int32_t f = 0; f < c->F; ++f)
+      out[(size_t)f * c->N + r] =
+          (uint8_t)(rec[(size_t)r * 4 * c->W + (f >> 2)] >> (8 * (f & 3)));
   return LGBM_HIP_OK;
 }
 

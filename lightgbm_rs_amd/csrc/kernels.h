@@ -143,6 +143,22 @@ struct KernelEvents {
 
 void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t W, uint4* rec,
                          hipStream_t s);
+
+// One feature's mapper as the binning kernel reads it (ValueToBin,
+// lgbm-dataset/src/bin_mapper.rs:148-189).
+struct DevBinFeature {
+  int32_t categorical;  // 0 numerical (search ub), 1 categorical (search cats)
+  int32_t last;         // numerical: last searchable bin (num_bin-1, -1 more with a NaN bin)
+  int32_t nan_bin;      // numerical: the NaN bin (num_bin-1) when missing_type is NaN, else -1
+  int32_t off;          // offset into ub (numerical) or cats (categorical)
+  int32_t ncat;         // categorical: number of (category, bin) pairs, sorted by category
+  int32_t _pad[3];
+};
+// Bins a dense raw matrix (f32 or f64; row-major [n][F] or column-major [F][n]) into
+// the resident records; `ub_count` upper bounds are staged in LDS.
+void launch_bin_records(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
+                        int32_t W, const DevBinFeature* feats, const double* ub, int32_t ub_count,
+                        const int2* cats, uint4* rec, hipStream_t s);
 void launch_absmax(const float* g, const float* h, int64_t n, uint4* partials, hipStream_t s);
 void launch_grad_binary(const double* score, const float* label, float* g, float* h, int64_t n,
                         uint4* partials, hipStream_t s);
