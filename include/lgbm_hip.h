@@ -272,6 +272,16 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* ctx, int32_t iter, const lgbm_gain_
                                int32_t num_grad_quant_bins, int32_t stochastic,
                                lgbm_tree_out* tree);
 
+/* BinaryLogloss::boost_from_score (crates/lgbm-objective/src/binary.rs:178-192):
+ * log(pavg / (1 - pavg)) / sigmoid for the positive fraction pavg (label > 0)
+ * clamped to [kEpsilon, 1 - kEpsilon]; 0 for n == 0.  Host only. */
+int lgbm_hip_binary_boost_from_score(const float* label, int64_t n, double sigmoid, double* out);
+
+/* The f32 gradients / hessians of the last objective evaluation on the device
+ * (BinaryLogloss::get_gradients, binary.rs:134-172; either pointer may be NULL).
+ * No reference counterpart at the boundary: the reference's are host arrays. */
+int lgbm_hip_get_gradients(lgbm_hip_ctx* ctx, float* grad, float* hess, int64_t n);
+
 /* Copy the resident f64 training score back to the host. */
 int lgbm_hip_get_scores(lgbm_hip_ctx* ctx, double* out, int64_t n);
 

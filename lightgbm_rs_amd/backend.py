@@ -202,6 +202,14 @@ class HipBackend:
             C.byref(tb.out) if tb else None))
         return tb.to_dict() if tb else None
 
+    def gradients(self):
+        """The device's f32 (grad, hess) of the last objective evaluation."""
+        g = np.zeros(self.num_data, np.float32)
+        h = np.zeros(self.num_data, np.float32)
+        self._check(self.lib.lgbm_hip_get_gradients(self.ctx, ptr(g, C.c_float), ptr(h, C.c_float),
+                                                    C.c_int64(self.num_data)))
+        return g, h
+
     def scores(self):
         out = np.zeros(self.num_data, np.float64)
         self._check(self.lib.lgbm_hip_get_scores(self.ctx, ptr(out, C.c_double),
@@ -219,6 +227,18 @@ class HipBackend:
                 "hist_launches", "partition_rows", "partition_launches", "record_bytes",
                 "features", "cells", "partition_jobs", "rounds", "trees", "extra_rounds"]
         return {k: float(v) for k, v in zip(keys, st)}
+
+
+def binary_boost_from_score(labels, sigmoid=1.0):
+    """BinaryLogloss::boost_from_score (lgbm-objective/src/binary.rs:178-192)."""
+    lib = load_library()
+    lab = np.ascontiguousarray(labels, np.float32)
+    out = C.c_double(0.0)
+    rc = lib.lgbm_hip_binary_boost_from_score(ptr(lab, C.c_float), C.c_int64(len(lab)),
+                                              C.c_double(sigmoid), C.byref(out))
+    if rc != 0:
+        raise HipError(rc, "boost_from_score: bad arguments")
+    return out.value
 
 
 PREDICT_KINDS = {"raw": 0, "transformed": 1, "leaf": 2}
@@ -352,4 +372,5 @@ def feature_meta(num_bin, most_freq_bin=0, missing_type=0, default_bin=None, rea
     return m
 
 
-__all__ = ["HipBackend", "HipError", "GainConfig", "Model", "feature_meta", "load_library"]
+__all__ = ["HipBackend", "HipError", "GainConfig", "Model", "binary_boost_from_score",
+           "feature_meta", "load_library"]

@@ -4,6 +4,7 @@
 // boundary (the reference backend's calls are blocking, lib.rs:3840-3846); inside a
 // call everything is queued on the context's own HIP stream.
 #include <algorithm>
+#include <cmath>
 #include <array>
 #include <cstddef>
 #include <cstdio>
@@ -1491,6 +1492,33 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
   launch_score_update(L, learning_rate, c->score, c->stream, ev_kernel(c, FAM_OBJ, &ke));
   HIPCHK(c, hipGetLastError());
   return finish_tree(c, tree, nullptr, learning_rate);
+}
+
+int lgbm_hip_binary_boost_from_score(const float* label, int64_t n, double sigmoid, double* out) {
+  if (!out || n < 0 || (n > 0 && !label) || !(sigmoid > 0.0)) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  // BinaryLogloss::boost_from_score (binary.rs:178-192): log-odds of the positive
+  // fraction, clamped to [kEpsilon, 1 - kEpsilon]
+  if (n == 0) {
+    *out = 0.0;
+    return LGBM_HIP_OK;
+  }
+  double pos = 0.0;
+  for (int64_t i = 0; i < n; ++i) pos += label[i] > 0.0f ? 1.0 : 0.0;
+  const double eps = (double)1e-15f;
+  const double pavg = std::max(std::min(pos / (double)n, 1.0 - eps), eps);
+  *out = std::log(pavg / (1.0 - pavg)) / sigmoid;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_get_gradients(lgbm_hip_ctx* c, float* grad, float* hess, int64_t n) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "no gradients yet");
+  if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_data");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (grad) HIPCHK(c, hipMemcpy(grad, c->g, (size_t)n * 4, hipMemcpyDeviceToHost));
+  if (hess) HIPCHK(c, hipMemcpy(hess, c->h, (size_t)n * 4, hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
 }
 
 int lgbm_hip_get_scores(lgbm_hip_ctx* c, double* out, int64_t n) {

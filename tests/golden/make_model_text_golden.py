@@ -37,11 +37,21 @@ FILES = {
 }
 
 
+# The binary spine's per-iteration goldens (boosting_parity.rs:787-810): raw scores
+# after every iteration (f64 bits), iteration-1 and iteration-5 gradients (f32 bits)
+# and the transformed predictions (f64 bits) of the real binary on the 12-row corpus.
+SPINE = ["binary_scores.txt", "binary_gh_iter1.txt", "binary_gh_iterN.txt",
+         "binary_spine_pred.txt"]
+
+
 def main():
     os.makedirs(OUT, exist_ok=True)
     for name, rel in FILES.items():
         shutil.copyfile(os.path.join(FIX, rel), os.path.join(OUT, name + ".txt"))
         print(name, "<-", rel)
+    os.makedirs(os.path.join(OUT, "spine"), exist_ok=True)
+    for name in SPINE:
+        shutil.copyfile(os.path.join(FIX, "boosting", name), os.path.join(OUT, "spine", name))
 
 
 if __name__ == "__main__":

@@ -84,3 +84,20 @@ def test_create_without_device_returns_status():
     buf = C.create_string_buffer(256)
     assert lib.lgbm_hip_last_error(None, buf, 256) == 0
     assert len(buf.value) > 0
+
+
+def test_binary_boost_from_score_matches_oracle_and_capture():
+    """The library's BinaryLogloss::boost_from_score against the oracle and the real
+    binary's captured init score (-0.33647223662121273 = log(5/7) for the binary
+    spine corpus, boosting/binary_gh_iterN.txt)."""
+    import numpy as np
+
+    from lightgbm_rs_amd import binary_boost_from_score
+    from oracle import oracle
+    y = np.array([0, 0, 0, 0, 0, 1, 0, 1, 1, 0, 1, 1], np.float32)
+    assert binary_boost_from_score(y) == -0.33647223662121273
+    rng = np.random.default_rng(4)
+    for lab in [(rng.random(10001) < 0.3).astype(np.float32), np.ones(4, np.float32),
+                np.zeros(4, np.float32), np.array([], np.float32)]:
+        assert binary_boost_from_score(lab) == oracle.boost_from_score(lab)
+    assert binary_boost_from_score(y, sigmoid=2.0) == -0.33647223662121273 / 2.0

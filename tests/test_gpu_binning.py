@@ -7,7 +7,8 @@ import numpy as np
 import pytest
 
 from tests import binning_fixtures as BF
-from lightgbm_rs_amd import BinMapper, GainConfig, HipBackend, HipError, Model, feature_mappers
+from lightgbm_rs_amd import (BinMapper, GainConfig, HipBackend, HipError, Model,
+                             binary_boost_from_score, feature_mappers)
 from oracle import binning as OB
 
 pytestmark = pytest.mark.gpu
@@ -96,7 +97,6 @@ def test_raw_to_model_predicts_training_scores(be):
     """Raw features -> device bins -> resident boosting -> model text -> device
     prediction on the same raw features reproduces the training scores bit for bit
     (the bin upper bounds are the split thresholds)."""
-    from oracle import oracle
     n = 40_000
     X = _table(n, 10, seed=17).astype(np.float32).astype(np.float64)  # the predictor reads f32
     rng = np.random.default_rng(3)
@@ -104,7 +104,7 @@ def test_raw_to_model_predicts_training_scores(be):
     y = (rng.random(n) < 1 / (1 + np.exp(-logit))).astype(np.float32)
     ms = feature_mappers(X, max_bin=63)
     be.upload_raw(X, ms)
-    init = oracle.boost_from_score(y)
+    init = binary_boost_from_score(y)
     be.set_labels(y, init)
     cfg = GainConfig.make(min_data_in_leaf=20)
     infos = " ".join(f"[{np.nanmin(X[:, f]):g}:{np.nanmax(X[:, f]):g}]" for f in range(10))

@@ -164,11 +164,10 @@ def test_trained_model_text_predicts_training_scores(be, quant):
     """Trees grown by the resident boosting loop, assembled into a model (the first
     tree carrying the init score), written as model text and read back: the device
     predictor reproduces the training scores bit for bit."""
-    from lightgbm_rs_amd import GainConfig
-    from oracle import oracle
+    from lightgbm_rs_amd import GainConfig, binary_boost_from_score
     print(f"trained model predict quant={quant}", flush=True)
     X, bins, meta, ub, y = _binned_table(30_000, seed=41)
-    init = oracle.boost_from_score(y)
+    init = binary_boost_from_score(y)
     be.upload_resident_bins(bins, meta, ub)
     be.set_labels(y, init)
     cfg = GainConfig.make(min_data_in_leaf=20)
