@@ -3,8 +3,10 @@
 One step = one boosting iteration of BASELINE.json configs[1] (binary logloss,
 num_leaves 255, max_bin 63, int8 gradients with 4 quantization bins and stochastic
 rounding) with every input resident in HBM: objective -> quantize -> grow the tree
-(histogram, split scan, partition for all 254 splits) -> score update.  Binning and
-the one-time upload are outside the timed region.
+(histogram, split scan, partition for all 254 splits) -> score update.  The raw
+table is binned by the library (BinMapper on a 200k-row sample on the host, then
+ValueToBin on the device) before the timed region; the binning kernel and a batch
+prediction with the trained trees are reported as secondary lines (`next_rows`).
 
 Prints ONE JSON line.  `value` is seconds per 100 trees (lower is better); the
 histogram bandwidth of the dominant kernel is reported in `roofline`, timed with HIP
@@ -47,6 +49,21 @@ def traffic_for(kernel):
     return None
 
 
+def _line(kernel, ms, launches, bytes_per_launch, workload, walks=None):
+    """A secondary kernel's per-launch time and algorithmic bandwidth (HIP events on
+    the library's stream)."""
+    if launches <= 0 or ms <= 0:
+        return None
+    us = ms * 1e3 / launches
+    gbs = bytes_per_launch / (us * 1e-6) / 1e9
+    out = {"kernel": kernel, "workload": workload, "avg_launch_us": round(us, 2),
+           "bytes_per_launch": int(bytes_per_launch), "achieved_GBps": round(gbs, 1),
+           "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    if walks is not None:
+        out["row_trees_per_s"] = float(f"{walks / (ms * 1e-3):.4g}")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -73,45 +90,76 @@ def main():
     import numpy as np
     import torch
 
-    from lightgbm_rs_amd import GainConfig, HipBackend
-    from lightgbm_rs_amd.synth import config1_like
+    from lightgbm_rs_amd import (BinMapper, GainConfig, HipBackend, Model,
+                                 binary_boost_from_score, sample_indices)
+    from lightgbm_rs_amd.synth import config1_raw
 
     n, nl = args.rows, args.num_leaves
     t0 = time.perf_counter()
     dev = torch.device("cuda:0") if torch.cuda.is_available() else None
-    bins, meta, ub, y = config1_like(n, device=dev)
-    log(f"data: {n} x 28, num_bin {max(m.num_bin for m in meta)}, gen {time.perf_counter()-t0:.1f}s")
-    pos = float(y.mean())
-    eps = float(np.float32(1e-15))
-    pavg = min(max(pos, eps), 1.0 - eps)
-    init = float(np.log(pavg / (1.0 - pavg)))  # BinaryLogloss::boost_from_score
+    if dev is None:
+        sys.exit("bench.py needs a HIP device")
+    # raw table generated on the device by torch, then handed to the library as host
+    # memory (torch and the library each bring their own HIP runtime)
+    Xd, y = config1_raw(n, device=dev)
+    idx = torch.from_numpy(sample_indices(n, 200000, 1).astype(np.int64)).to(dev)
+    sampled = Xd[:, idx].double().cpu().numpy()
+    X = Xd.cpu().numpy()  # [28, n] float32, one feature per row
+    del Xd, idx
+    torch.cuda.empty_cache()
+    mappers = [BinMapper.from_sampled_column(sampled[f], n, max_bin=63) for f in range(28)]
+    log(f"data: {n} x 28, num_bin {max(m.num_bin for m in mappers)}, "
+        f"gen + mappers {time.perf_counter()-t0:.1f}s")
+    init = binary_boost_from_score(y)
     cfg = GainConfig.make(min_data_in_leaf=20, min_sum_hessian_in_leaf=1e-3)
     lr = 0.1
 
     be = HipBackend(0)
     t1 = time.perf_counter()
-    be.upload_resident_bins(bins, meta, ub)
+    be.set_timing(True)
+    be.upload_raw(X, mappers, col_major=True)
+    bin_tm = be.timing()
+    be.set_timing(False)
     be.set_labels(y, init)
-    log(f"upload {time.perf_counter()-t1:.2f}s")
+    bins = be.get_bins() if args.cpu_iters > 0 else None  # the CPU baseline's input
+    log(f"upload + device binning {time.perf_counter()-t1:.2f}s "
+        f"(kernel {bin_tm['bin_ms']:.3f} ms)")
+    # the host reads each tree while the device already computes the next
+    # iteration's gradients and quantization (results unchanged)
+    be.set_lookahead(True)
     for i in range(args.warmup):
         be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=False)
     torch.cuda.synchronize() if dev is not None else None
-    leaves = []
+    leaves, trees = [], []
     t2 = time.perf_counter()
     for i in range(args.warmup, args.warmup + args.steps):
         t = be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=True)
         leaves.append(t["num_leaves"])
+        trees.append(t)
     torch.cuda.synchronize() if dev is not None else None
     elapsed = time.perf_counter() - t2
     # Per-kernel device time: HIP events around every launch on the library's stream.
     # The per-tree sequence then runs as individual launches (no graph), so this pass
     # measures kernel durations, not the timed loop's wall clock.
+    be.set_lookahead(False)
     be.set_timing(True)
     it0 = args.warmup + args.steps
     for i in range(it0, it0 + args.prof_steps):
         be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=False)
     tm = be.timing()
+    # secondary: batch prediction of the timed iterations' trees on the first
+    # `pred_rows` rows (row-major f32, as the predictor reads them)
+    model = Model.create(num_class=1, max_feature_idx=27, objective="binary sigmoid:1")
+    for t in trees:
+        model.add_tree(t, shrinkage=lr)
+    pred_rows = min(n, 2_000_000)
+    Xp = np.ascontiguousarray(X[:, :pred_rows].T)
+    be.set_timing(True)
+    for _ in range(3):
+        be.predict(model, Xp, "raw")
+    pred_tm = be.timing()
     be.close()
+    del Xp
     if args.copy_probe_mib > 0 and dev is not None:
         nb = args.copy_probe_mib << 20
         src = torch.ones(nb // 4, dtype=torch.int32, device=dev)
@@ -144,6 +192,10 @@ def main():
     cpu = None
     if args.cpu_iters > 0:
         from oracle import oracle
+        from lightgbm_rs_amd import feature_meta
+        meta = [feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f)
+                for f, m in enumerate(mappers)]
+        ub = np.concatenate([m.upper_bounds for m in mappers])
         threads = args.cpu_threads or (os.cpu_count() or 1)
         threads = oracle.set_threads(threads)
         tc = time.perf_counter()
@@ -170,7 +222,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 grad/hess, int32 histogram, f64 split math",
-        "data": "synthetic (BASELINE.json configs[1] recipe, quantile-binned)",
+        "data": "synthetic (BASELINE.json configs[1] recipe), binned by the library's "
+                "BinMapper (200k-row sample, max_bin 63)",
         "config": {"workload": "configs[1]: binary, 10.5M rows x 28 features, max_bin 63, "
                                "num_leaves 255, quantized int8 grads (4 bins, stochastic)",
                    "rows": n, "features": 28, "num_leaves": nl, "learning_rate": lr},
@@ -186,6 +239,15 @@ def main():
         "phase_ms_per_step": {k: round(tm[k] / tsteps, 4) for k in
                               ("hist_ms", "partition_ms", "scan_ms", "quant_ms", "objective_ms")},
         "cpu_baseline": cpu,
+        "next_rows": {
+            "binning": _line("k_bin_records (ValueToBin + record packing, f32 column-major "
+                             "input)", bin_tm["bin_ms"], bin_tm["bin_launches"],
+                             n * (28 * 4 + int(rec)), f"{n} rows x 28 features"),
+            "predict": _line("k_predict (raw scores)", pred_tm["predict_ms"],
+                             pred_tm["predict_launches"], pred_rows * (28 * 4 + 8),
+                             f"{pred_rows} rows x {len(trees)} trees of {nl} leaves",
+                             walks=pred_tm["predict_walks"]),
+        },
     }
     print(json.dumps(out), flush=True)
 

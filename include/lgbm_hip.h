@@ -282,6 +282,16 @@ int lgbm_hip_binary_boost_from_score(const float* label, int64_t n, double sigmo
  * No reference counterpart at the boundary: the reference's are host arrays. */
 int lgbm_hip_get_gradients(lgbm_hip_ctx* ctx, float* grad, float* hess, int64_t n);
 
+/* Lookahead for lgbm_hip_train_iter_binary (off by default; no reference
+ * counterpart): after enqueueing iteration i's tree copy, the call also enqueues
+ * iteration i + 1's gradients and quantization (same num_grad_quant_bins and
+ * stochastic) and returns once the copy is done, so the device works while the host
+ * handles the tree.  The next call with iter == i + 1 and the same settings uses
+ * them; any other call that changes the device inputs drops them.  Results are
+ * identical either way.  While it is on, lgbm_hip_get_gradients and the quantized
+ * values describe the iteration enqueued ahead.  Ignored while timing is enabled. */
+int lgbm_hip_set_lookahead(lgbm_hip_ctx* ctx, int32_t enable);
+
 /* Copy the resident f64 training score back to the host. */
 int lgbm_hip_get_scores(lgbm_hip_ctx* ctx, double* out, int64_t n);
 
@@ -302,8 +312,10 @@ int lgbm_hip_get_timing(lgbm_hip_ctx* ctx, double* ms_out5, double* hist_bytes_o
  * included); [9] bytes per row record; [10] features; [11] histogram
  * cells; [12] leaf splits partitioned (including splits made ahead of their turn
  * that the tree never used); [13] partition rounds over all trees; [14] trees;
- * [15] rounds launched after the captured per-tree sequence. */
-int lgbm_hip_get_stats(lgbm_hip_ctx* ctx, double* out16);
+ * [15] rounds launched after the captured per-tree sequence; [16] ms in the binning
+ * kernel (lgbm_hip_upload_raw*), [17] its launches, [18] values binned; [19] ms in
+ * the prediction kernel, [20] its launches, [21] rows x trees walked. */
+int lgbm_hip_get_stats(lgbm_hip_ctx* ctx, double* out22);
 
 /* ---- binning ------------------------------------------------------------------ */
 

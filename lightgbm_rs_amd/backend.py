@@ -56,6 +56,13 @@ class HipBackend:
         self.num_features = 0
         self.slot_len = 0
 
+    def _tree_buffers(self, num_leaves):
+        """Host arrays for one grown tree, reused across calls (to_dict copies)."""
+        cache = self.__dict__.setdefault("_tb_cache", {})
+        if num_leaves not in cache:
+            cache[num_leaves] = TreeBuffers(num_leaves)
+        return cache[num_leaves]
+
     def _err(self, ctx):
         buf = C.create_string_buffer(1024)
         self.lib.lgbm_hip_last_error(ctx, buf, C.c_size_t(1024))
@@ -174,7 +181,7 @@ class HipBackend:
     # ---- coarse seam -----------------------------------------------------------
     def grow_tree_on_device_with_cfg(self, cfg, num_leaves, max_depth=-1, want_layout=True):
         """`Backend::grow_tree_on_device_with_cfg` (lib.rs:2771) -> (tree, layout)."""
-        tb = TreeBuffers(num_leaves)
+        tb = self._tree_buffers(num_leaves)
         lb = LayoutBuffers(self.num_data, num_leaves) if want_layout else None
         self._check(self.lib.lgbm_hip_grow_tree(self.ctx, C.byref(cfg), C.c_int32(num_leaves),
                                                 C.c_int32(max_depth), C.byref(tb.out),
@@ -195,7 +202,7 @@ class HipBackend:
 
     def train_iter_binary(self, it, cfg, num_leaves, max_depth, learning_rate,
                           num_grad_quant_bins=4, stochastic=True, want_tree=True):
-        tb = TreeBuffers(num_leaves) if want_tree else None
+        tb = self._tree_buffers(num_leaves) if want_tree else None
         self._check(self.lib.lgbm_hip_train_iter_binary(
             self.ctx, C.c_int32(it), C.byref(cfg), C.c_int32(num_leaves), C.c_int32(max_depth),
             C.c_double(learning_rate), C.c_int32(num_grad_quant_bins), C.c_int32(int(stochastic)),
@@ -210,6 +217,11 @@ class HipBackend:
                                                     C.c_int64(self.num_data)))
         return g, h
 
+    def set_lookahead(self, enable=True):
+        """Enqueue the next iteration's gradients + quantization inside
+        train_iter_binary (lgbm_hip_set_lookahead); results are unchanged."""
+        self._check(self.lib.lgbm_hip_set_lookahead(self.ctx, C.c_int32(int(enable))))
+
     def scores(self):
         out = np.zeros(self.num_data, np.float64)
         self._check(self.lib.lgbm_hip_get_scores(self.ctx, ptr(out, C.c_double),
@@ -221,11 +233,13 @@ class HipBackend:
 
     def timing(self):
         """Per-family device ms (HIP events) and row counters since set_timing."""
-        st = np.zeros(16, np.float64)
+        st = np.zeros(22, np.float64)
         self._check(self.lib.lgbm_hip_get_stats(self.ctx, ptr(st, C.c_double)))
         keys = ["hist_ms", "partition_ms", "scan_ms", "quant_ms", "objective_ms", "root_rows",
                 "hist_launches", "partition_rows", "partition_launches", "record_bytes",
-                "features", "cells", "partition_jobs", "rounds", "trees", "extra_rounds"]
+                "features", "cells", "partition_jobs", "rounds", "trees", "extra_rounds",
+                "bin_ms", "bin_launches", "bin_values", "predict_ms", "predict_launches",
+                "predict_walks"]
         return {k: float(v) for k, v in zip(keys, st)}
 
 

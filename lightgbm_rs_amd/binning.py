@@ -97,6 +97,20 @@ class BinMapper:
                          C.c_int32(int(categorical)), C.byref(p), C.c_int32(min_split_data),
                          forced.ctypes.data_as(C.c_void_p), C.c_int32(len(forced)))
 
+    @classmethod
+    def from_sampled_column(cls, sampled, num_rows, **params):
+        """find_bin_from_column when the caller has already gathered the column's
+        values at sample_indices(num_rows, bin_construct_sample_cnt, data_random_seed)
+        (e.g. on the device): the same mapper without the full column on the host."""
+        v = _f64(sampled)
+        p = dict(DEFAULTS, **params)
+        if len(v) != min(num_rows, p["bin_construct_sample_cnt"]):
+            raise ValueError("sampled values do not match the sample size")
+        filt = (p["min_data_in_leaf"] * len(v)) // num_rows if num_rows else p["min_data_in_leaf"]
+        kw = {k: p[k] for k in ("max_bin", "min_data_in_bin", "pre_filter", "use_missing",
+                                "zero_as_missing")}
+        return cls.from_sample(v, len(v), min_split_data=filt, **kw)
+
     def value_to_bin(self, values):
         """ValueToBin (bin_mapper.rs:148-189) on the host."""
         v = _f64(values).ravel()

@@ -3,8 +3,8 @@
 // ValueToBin (crates/lgbm-dataset/src/bin_mapper.rs:148-189) for every value of a
 // dense matrix, fused with the record packing of k_pack_records: one thread per
 // row, the row's bins packed into its 16W-byte record with the row index in the
-// last word.  Numerical features search their upper bounds (staged in LDS) with
-// the reference's `m = (r + l - 1) / 2`, `v <= ub[m]` bisection; categorical
+// last word.  Numerical features search their upper bounds (staged in LDS) for the
+// reference's bisection result (the first bin whose bound is >= v); categorical
 // features look their integer category up in a sorted (category, bin) table.
 // HBM-bound: 4 or 8 bytes read and one byte written per value, plus the 4-byte row
 // index per record.
@@ -31,16 +31,17 @@ __device__ __forceinline__ uint32_t bin_of(const DevBinFeature& f, const double*
     v = 0.0;
   }
   if (!f.categorical) {
+    // The reference's bisection returns the first b in [0, last] with v <= ub[b]
+    // (or last); over non-decreasing bounds that is the number of ub[0..last-1]
+    // below v.  Counted here by binary lifting with eight fixed steps: every lane
+    // of every feature runs the same trip count, the first probe is one broadcast
+    // LDS address, and the unrolled searches of neighbouring features overlap.
     const double* u = ub + f.off;
-    int32_t l = 0, r = f.last;
-    while (l < r) {
-      const int32_t m = (r + l - 1) / 2;
-      if (v <= u[m])
-        r = m;
-      else
-        l = m + 1;
-    }
-    return (uint32_t)l;
+    int32_t pos = 0;
+#pragma unroll
+    for (int32_t step = 128; step > 0; step >>= 1)
+      if (pos + step <= f.last && u[pos + step - 1] < v) pos += step;
+    return (uint32_t)pos;
   }
   const int32_t key = sat_i32(v);
   if (key < 0) return 0u;
@@ -73,16 +74,26 @@ __global__ __launch_bounds__(256) void k_bin_records(const T* __restrict__ x, in
   __syncthreads();
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
-    uint32_t words[4 * LGBM_MAX_W];
+    // one 16-byte record word at a time, its four u32 built in registers (fixed
+    // indices after unrolling); the row index fills the record's last u32
+    for (int w = 0; w < W; ++w) {
+      uint32_t q[4];
 #pragma unroll
-    for (int i = 0; i < 4 * LGBM_MAX_W; ++i) words[i] = 0u;
-    for (int f = 0; f < F; ++f) {
-      const double v = (double)(COL_MAJOR ? x[(int64_t)f * n + r] : x[r * F + f]);
-      words[f >> 2] |= bin_of(s_f[f], bounds, cats, v) << (8 * (f & 3));
+      for (int k = 0; k < 4; ++k) {
+        uint32_t word = 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int f = 16 * w + 4 * k + j;
+          if (f < F) {
+            const double v = (double)(COL_MAJOR ? x[(int64_t)f * n + r] : x[r * F + f]);
+            word |= bin_of(s_f[f], bounds, cats, v) << (8 * j);
+          }
+        }
+        q[k] = word;
+      }
+      if (w == W - 1) q[3] = (uint32_t)r;
+      rec[r * W + w] = make_uint4(q[0], q[1], q[2], q[3]);
     }
-    words[4 * W - 1] = (uint32_t)r;
-    for (int w = 0; w < W; ++w)
-      rec[r * W + w] = make_uint4(words[4 * w], words[4 * w + 1], words[4 * w + 2], words[4 * w + 3]);
   }
 }
 

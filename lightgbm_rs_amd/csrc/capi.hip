@@ -63,6 +63,11 @@ struct lgbm_hip_ctx {
   std::vector<DevFeature> feats;
   bool have_bins = false, have_grad = false, quant_ready = false, have_labels = false;
   int32_t quant_bins = 0;
+  // lookahead (lgbm_hip_set_lookahead): the next iteration's objective + quantizer
+  // enqueued by train_iter_binary before it waits for its tree copy
+  bool lookahead = false, ahead = false;
+  int32_t ahead_iter = 0, ahead_qbins = 0, ahead_stoch = 0;
+  hipEvent_t tree_ev = nullptr;
   // device memory
   Ctl* ctl = nullptr;
   DevFeature* d_feats = nullptr;
@@ -116,6 +121,8 @@ struct lgbm_hip_ctx {
   int32_t* done_host = nullptr;  // pinned: ctl->done after the captured rounds
   double tree_rounds = 0.0, trees = 0.0, extra_rounds = 0.0;
   double part_launches = 0.0;  // partition kernels enqueued while timing (empty rounds too)
+  // binning and prediction launches while timing: launches, values binned, row-trees walked
+  double bin_launches = 0.0, bin_values = 0.0, pred_launches = 0.0, pred_walks = 0.0;
   uint64_t graph_gen = 0, buf_gen = 1;
   bool use_graphs = true;
   // timing
@@ -128,7 +135,7 @@ struct lgbm_hip_ctx {
   std::vector<hipEvent_t> chain;
   std::vector<int> chain_family;
   size_t chain_used = 0;
-  double ms[5] = {0, 0, 0, 0, 0};
+  double ms[7] = {0, 0, 0, 0, 0, 0, 0};
 };
 
 namespace {
@@ -432,7 +439,8 @@ void ev_collect(lgbm_hip_ctx* c) {
   }
   c->chain_used = 0;
 }
-enum { FAM_HIST = 0, FAM_PART = 1, FAM_SCAN = 2, FAM_QUANT = 3, FAM_OBJ = 4 };
+enum { FAM_HIST = 0, FAM_PART = 1, FAM_SCAN = 2, FAM_QUANT = 3, FAM_OBJ = 4, FAM_BIN = 5,
+       FAM_PRED = 6 };
 
 int check_ctx(lgbm_hip_ctx* c) {
   if (!c) return LGBM_HIP_ERR_INVALID_ARGUMENT;
@@ -560,11 +568,16 @@ int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_le
   return finish_rounds(c, num_leaves, rounds, fp);
 }
 
-int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, double shrink) {
-  HIPCHK(c, hipMemcpyAsync(c->tree_host, c->tree_blob, out ? c->tree_blob_bytes : 64,
-                           hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(c, hipStreamSynchronize(c->stream));
-  ev_collect(c);
+// `copied`: the caller has enqueued the blob copy and waited for it (the stream may
+// still be busy with later work).
+int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, double shrink,
+                bool copied = false) {
+  if (!copied) {
+    HIPCHK(c, hipMemcpyAsync(c->tree_host, c->tree_blob, out ? c->tree_blob_bytes : 64,
+                             hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    ev_collect(c);
+  }
   const char* hb = (const char*)c->tree_host;
   const int32_t nl = ((const int32_t*)hb)[0], err = ((const int32_t*)hb)[1];
   c->tree_rounds += ((const int32_t*)hb)[2];
@@ -740,6 +753,32 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   return LGBM_HIP_OK;
 }
 
+// BinaryLogloss::get_gradients on the resident score, then the f32 pair prep or the
+// quantizer with iteration `iter`'s seed (gbdt.rs:945-960).
+void enqueue_objective(lgbm_hip_ctx* c, int32_t iter, int32_t qbins, int32_t stochastic) {
+  ev_begin(c, FAM_OBJ);
+  launch_grad_binary(c->score, c->label, c->g, c->h, c->N, c->partials, c->stream);
+  ev_end(c);
+  c->have_grad = true;
+  if (qbins == 0) {
+    ev_begin(c, FAM_QUANT);
+    DevLearner L0 = make_learner(c);
+    launch_fp_prep(L0, c->g, c->h, c->N, c->partials, c->stream);
+    ev_end(c);
+    c->quant_ready = false;
+  } else {
+    const uint64_t seed = ((uint64_t)(uint32_t)iter << 20) ^ 0ull ^ 0x51702010ull;  // gbdt.rs:950
+    ev_begin(c, FAM_QUANT);
+    launch_quant_scales(c->ctl, c->partials, c->N, qbins, -1, c->stream);
+    launch_quantize(c->g, c->h, c->N, c->ctl, c->wave_mats, c->lane_mats,
+                    seed ^ 0x9E3779B97F4A7C15ull, stochastic, c->gh[BUF_ORIG], nullptr, nullptr,
+                    c->stream);
+    ev_end(c);
+    c->quant_ready = true;
+    c->quant_bins = qbins;
+  }
+}
+
 BinParams bin_params_of(const lgbm_bin_params& p) {
   BinParams b;
   b.max_bin = p.max_bin;
@@ -778,6 +817,8 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   if (hipSetDevice(device) != hipSuccess) return fail(set_err(c, LGBM_HIP_ERR_HIP, "hipSetDevice"));
   if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess)
     return fail(set_err(c, LGBM_HIP_ERR_HIP, "hipStreamCreate"));
+  if (hipEventCreateWithFlags(&c->tree_ev, hipEventDisableTiming) != hipSuccess)
+    return fail(set_err(c, LGBM_HIP_ERR_HIP, "hipEventCreate"));
   int rc = dalloc(c, &c->ctl, 1);
   if (rc) return fail(rc);
   Ctl init;
@@ -876,6 +917,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
     (void)hipEventDestroy(p.b);
   }
   for (hipEvent_t e : c->chain) (void)hipEventDestroy(e);
+  if (c->tree_ev) (void)hipEventDestroy(c->tree_ev);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
   return LGBM_HIP_OK;
@@ -893,6 +935,7 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
                          const double* bin_upper_bound) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!bins || !meta || num_features <= 0 || num_data <= 0)
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null bins/meta or empty shape");
   const int32_t F = num_features;
@@ -1038,6 +1081,7 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
                                const lgbm_hip_bin_mapper* const* mappers) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!d_values || !mappers || num_rows <= 0 || num_cols <= 0)
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null values/mappers or empty shape");
   if (dtype != LGBM_HIP_DTYPE_F32 && dtype != LGBM_HIP_DTYPE_F64)
@@ -1085,8 +1129,14 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
     e = hipMemcpy(d_cats, cats.data(), cats.size() * sizeof(int2), hipMemcpyHostToDevice);
   if (e == hipSuccess) {
     // c->d_ub holds the same bounds, concatenated in feature order
+    ev_begin(c, FAM_BIN);
     launch_bin_records(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->W, d_bf,
                        c->d_ub, (int32_t)ub.size(), d_cats, c->rec[BUF_ORIG], c->stream);
+    ev_end(c);
+    if (c->timing) {
+      c->bin_launches += 1.0;
+      c->bin_values += (double)num_rows * F;
+    }
     e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   }
@@ -1134,6 +1184,7 @@ int lgbm_hip_get_bins(lgbm_hip_ctx* c, uint8_t* out, int64_t n) {
 int lgbm_hip_set_gradients(lgbm_hip_ctx* c, const float* grad, const float* hess, int64_t n) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
   if (!grad || !hess) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null gradients");
   if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "gradient length != num_data");
@@ -1148,6 +1199,7 @@ int lgbm_hip_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_
                       float* dg_out, float* dh_out, double* scales_out) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set gradients first");
   if (bins < 1 || bins > 254)
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_grad_quant_bins must be in 1..=254");
@@ -1215,6 +1267,7 @@ int lgbm_hip_build_int_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int
                                  int64_t* out) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!c->quant_ready) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize first");
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
   if ((rc = set_hist_job(c, leaf_rows, n_rows))) return rc;
@@ -1245,6 +1298,7 @@ int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, in
                                   double sum_gradient, double sum_hessian, double* out) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   // quantized gradients (after lgbm_hip_quantize) or the f32 gradients as uploaded
   const int32_t fp = c->quant_ready ? 0 : 1;
   if (fp && !c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set gradients first");
@@ -1283,6 +1337,7 @@ int lgbm_hip_find_best_splits(lgbm_hip_ctx* c, const double* hist, int64_t hist_
                               double sum_hessian, int32_t num_data, lgbm_split_info* out) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!hist || !feats || !cfg || !out || n_feats < 0)
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null argument");
   if (n_feats == 0) return LGBM_HIP_OK;
@@ -1317,6 +1372,7 @@ int lgbm_hip_subtract_histograms(lgbm_hip_ctx* c, const double* parent, const do
                                  int64_t len, double* out) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!parent || !child || !out || len < 0)
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null argument");
   if (len == 0) return LGBM_HIP_OK;
@@ -1339,6 +1395,7 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
                             uint32_t* order_out, int64_t* left_count_out) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   if ((!bins && n > 0) || (!order_out && n > 0) || !left_count_out || n < 0)
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null argument");
   if (num_bin == 0) return set_err(c, LGBM_HIP_ERR_RUNTIME, "data_partition: num_bin must be > 0");
@@ -1408,6 +1465,7 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num
                        int32_t max_depth, lgbm_tree_out* tree, lgbm_layout_out* layout) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
   if (num_leaves < 1) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_leaves must be >= 1");
   if (num_leaves > 256) return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_leaves must be <= 256");
@@ -1432,6 +1490,7 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num
 int lgbm_hip_set_labels(lgbm_hip_ctx* c, const float* labels, int64_t n, double init_score) {
   int rc = check_ctx(c);
   if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
   if (!labels) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null labels");
   if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "labels length != num_data");
@@ -1465,33 +1524,41 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
     if ((rc = ensure_fp(c))) return rc;
     if ((rc = ensure_leaves(c, num_leaves))) return rc;
   }
-  ev_begin(c, FAM_OBJ);
-  launch_grad_binary(c->score, c->label, c->g, c->h, c->N, c->partials, c->stream);
-  ev_end(c);
-  c->have_grad = true;
-  if (fp) {
-    ev_begin(c, FAM_QUANT);
-    DevLearner L0 = make_learner(c);
-    launch_fp_prep(L0, c->g, c->h, c->N, c->partials, c->stream);
-    ev_end(c);
-    c->quant_ready = false;
-  } else {
-    const uint64_t seed = ((uint64_t)(uint32_t)iter << 20) ^ 0ull ^ 0x51702010ull;  // gbdt.rs:950
-    ev_begin(c, FAM_QUANT);
-    launch_quant_scales(c->ctl, c->partials, c->N, num_grad_quant_bins, -1, c->stream);
-    launch_quantize(c->g, c->h, c->N, c->ctl, c->wave_mats, c->lane_mats,
-                    seed ^ 0x9E3779B97F4A7C15ull, stochastic, c->gh[BUF_ORIG], nullptr, nullptr,
-                    c->stream);
-    ev_end(c);
-    c->quant_ready = true;
-    c->quant_bins = num_grad_quant_bins;
-  }
+  const bool pro = c->ahead && c->ahead_iter == iter && c->ahead_qbins == num_grad_quant_bins &&
+                   c->ahead_stoch == stochastic;
+  c->ahead = false;
+  if (!pro) enqueue_objective(c, iter, num_grad_quant_bins, stochastic);
   if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
   DevLearner L = make_learner(c);
   KernelEvents ke;
   launch_score_update(L, learning_rate, c->score, c->stream, ev_kernel(c, FAM_OBJ, &ke));
   HIPCHK(c, hipGetLastError());
+  if (c->lookahead && !c->timing) {
+    // the tree copy is enqueued first, then iteration iter + 1's gradients and
+    // quantization (they read the score this tree just updated): the host waits for
+    // the copy alone while the device goes on
+    HIPCHK(c, hipMemcpyAsync(c->tree_host, c->tree_blob, tree ? c->tree_blob_bytes : 64,
+                             hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipEventRecord(c->tree_ev, c->stream));
+    enqueue_objective(c, iter + 1, num_grad_quant_bins, stochastic);
+    HIPCHK(c, hipGetLastError());
+    c->ahead = true;
+    c->ahead_iter = iter + 1;
+    c->ahead_qbins = num_grad_quant_bins;
+    c->ahead_stoch = stochastic;
+    HIPCHK(c, hipEventSynchronize(c->tree_ev));
+    return finish_tree(c, tree, nullptr, learning_rate, true);
+  }
   return finish_tree(c, tree, nullptr, learning_rate);
+}
+
+int lgbm_hip_set_lookahead(lgbm_hip_ctx* c, int32_t enable) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  c->lookahead = enable != 0;
+  c->ahead = false;
+  return LGBM_HIP_OK;
 }
 
 int lgbm_hip_binary_boost_from_score(const float* label, int64_t n, double sigmoid, double* out) {
@@ -1540,12 +1607,13 @@ int lgbm_hip_set_timing(lgbm_hip_ctx* c, int32_t enable) {
   for (double& m : c->ms) m = 0.0;
   HIPCHK(c, hipMemset(c->stats, 0, 64));
   c->tree_rounds = c->trees = c->extra_rounds = c->part_launches = 0.0;
+  c->bin_launches = c->bin_values = c->pred_launches = c->pred_walks = 0.0;
   return LGBM_HIP_OK;
 }
 
 int lgbm_hip_get_timing(lgbm_hip_ctx* c, double* ms_out5, double* hist_bytes_out,
                         int64_t* hist_launches_out) {
-  double st[16];
+  double st[22];
   int rc = lgbm_hip_get_stats(c, st);
   if (rc) return rc;
   if (ms_out5)
@@ -1577,6 +1645,12 @@ int lgbm_hip_get_stats(lgbm_hip_ctx* c, double* out) {
   out[13] = c->tree_rounds;
   out[14] = c->trees;
   out[15] = c->extra_rounds;
+  out[16] = c->ms[FAM_BIN];
+  out[17] = c->bin_launches;
+  out[18] = c->bin_values;
+  out[19] = c->ms[FAM_PRED];
+  out[20] = c->pred_launches;
+  out[21] = c->pred_walks;
   return LGBM_HIP_OK;
 }
 
@@ -1777,10 +1851,16 @@ int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int3
 
 int predict_run(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* d_x, int64_t rows,
                 int32_t cols, int32_t it0, int32_t it1, int32_t kind, void* d_out) {
+  ev_begin(c, FAM_PRED);
   launch_predict(c->pm_nodes, c->pm_trees, c->pm_leaves, c->pm_catb, c->pm_catw, d_x, rows, cols,
                  it0, it1, m->num_tree_per_iteration, kind, m->objective, m->sigmoid,
                  m->average_output ? 1 : 0, kind == LGBM_HIP_PREDICT_LEAF ? nullptr : (double*)d_out,
                  kind == LGBM_HIP_PREDICT_LEAF ? (int32_t*)d_out : nullptr, c->stream);
+  ev_end(c);
+  if (c->timing) {
+    c->pred_launches += 1.0;
+    c->pred_walks += (double)rows * (double)(it1 - it0) * m->num_tree_per_iteration;
+  }
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));
   return LGBM_HIP_OK;

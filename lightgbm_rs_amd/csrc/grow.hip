@@ -646,6 +646,8 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
       if (lane == 0) s_cnt[k * kWaves + wave] = (int32_t)__popcll(m);
     }
     __syncthreads();  // A
+    int32_t acc = 0, trows = 0;
+    unsigned long long old = 0ull;
     if (wave == 0) {
       // exclusive prefix of the (row, wave) counts
       const int32_t c = lane < kSlots ? s_cnt[lane] : 0;
@@ -656,30 +658,16 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
         if (lane >= off) incl += v;
       }
       if (lane < kSlots) s_pref[lane] = incl - c;
-      const int32_t acc = __shfl(incl, kSlots - 1);
-      if (lane == 0) {
-        const int32_t trows = (int32_t)min((int64_t)kTile, count - base);
-        int64_t lb, rb;
-        bool last;
-        if constexpr (STABLE) {
-          lb = (int64_t)L.tile_state[t];
-          rb = base - lb;
-          last = lt == J.ntiles - 1;
-        } else {
-          const unsigned long long old = atomicAdd(
-              &ctl->part_cur[j],
-              (unsigned long long)(uint32_t)acc | ((unsigned long long)(uint32_t)(trows - acc) << 32));
-          lb = (int64_t)(uint32_t)old;
-          rb = (int64_t)(old >> 32);
-          last = lb + rb + trows == count;
-        }
-        s_lbase = (int32_t)lb;
-        s_rbase = (int32_t)rb;
-        s_total = acc;
-        s_last = last ? 1 : 0;
-      }
+      acc = __shfl(incl, kSlots - 1);
+      trows = (int32_t)min((int64_t)kTile, count - base);
+      // the reservation is issued here and its result used after this wave's
+      // histogram adds, so the atomic's round trip overlaps them
+      if constexpr (!STABLE)
+        if (lane == 0)
+          old = atomicAdd(&ctl->part_cur[j], (unsigned long long)(uint32_t)acc |
+                                                 ((unsigned long long)(uint32_t)(trows - acc) << 32));
     }
-    // histogram adds (wave 0 after its reservation, the other waves meanwhile)
+    // histogram adds (every wave, wave 0 while its reservation is in flight)
     if (FP == 0 && J.acc_right >= 0) {
       const bool want_left = J.acc_right == 0;
 #pragma unroll
@@ -687,6 +675,23 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
         if (valid[k] && isleft[k] == want_left)
           lds_hist_add<W>(lds_hist, cbr, nw, w[k], gh_bits(q[k]));
       ++held;
+    }
+    if (wave == 0 && lane == 0) {
+      int64_t lb, rb;
+      bool last;
+      if constexpr (STABLE) {
+        lb = (int64_t)L.tile_state[t];
+        rb = base - lb;
+        last = lt == J.ntiles - 1;
+      } else {
+        lb = (int64_t)(uint32_t)old;
+        rb = (int64_t)(old >> 32);
+        last = lb + rb + trows == count;
+      }
+      s_lbase = (int32_t)lb;
+      s_rbase = (int32_t)rb;
+      s_total = acc;
+      s_last = last ? 1 : 0;
     }
     __syncthreads();  // B
     const int64_t lbase = s_lbase, rbase = s_rbase;
@@ -832,24 +837,43 @@ __global__ __launch_bounds__(1024) void k_tile_scan(DevLearner L) {
 //   2 * min_data_in_leaf rows) are not built or scanned.
 // ===========================================================================
 __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_t part_grid) {
+  static_assert(SCAN_THREADS == 128, "two bins and four f64 cells per thread cover 256 bins");
   __shared__ double cs[2 * 256];
   __shared__ double cp[2 * 256];
   Ctl* ctl = L.ctl;
   const int f = blockIdx.x, j = blockIdx.y;
-  if (j >= ctl->n_jobs) return;
-  const PartJob& J = ctl->jobs[j];
-  const int32_t p = J.parent, cl = J.cl, cr = J.cr, acc_right = J.acc_right;
   const int tid = threadIdx.x, F = L.F, cells = L.total_cells;
+  // The loads are grouped so the block waits for three memory round trips — the job
+  // record (with the feature and the round's uniforms), then everything the job
+  // names, then the parent's cells — instead of one per dependent step.
+  const int32_t n_jobs = ctl->n_jobs;
+  const PartJob& J = ctl->jobs[j];  // slot j always exists; its fields are used below
+  const int32_t p = J.parent, cl = J.cl, cr = J.cr, acc_right = J.acc_right;
+  const int32_t jnt = J.ntiles;
+  const int64_t jt0 = J.tile0;
   const DevFeature ft = L.feats[f];
-  const int nb = (int)ft.num_bin;
-  const DevNodes& nd = L.nodes;
-  const int32_t lcnt = nd.count[cl], rcnt = nd.count[cr];
+  const int64_t T = ctl->tile_total;
   const int32_t md = ctl->max_depth, min2 = ctl->cfg.min_data_in_leaf * 2;
-  const bool gated = (md > 0 && nd.depth[cl] >= md) || (lcnt < min2 && rcnt < min2);
+  const int32_t fp_mode = ctl->fp_mode;
+  if (j >= n_jobs) return;  // only after the job's fields are known to be live
+  const DevNodes& nd = L.nodes;
+  const int32_t lcnt = nd.count[cl], rcnt = nd.count[cr], dcl = nd.depth[cl];
+  const LeafSums scl = nd.sums[cl], scr = nd.sums[cr];
+  const bool pgate = L.splittable[(size_t)p * F + f] == 0;
+  const int nb = (int)ft.num_bin;
+  const size_t sl = L.slot_len;
+  const double* s_par = L.slots + (size_t)p * sl + ft.slot_off;
+  double pv[4];  // the parent's f64 cells i = tid + 128 k
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int i = tid + SCAN_THREADS * k;
+    pv[k] = i < 2 * nb ? s_par[i] : 0.0;
+  }
+  const bool gated = (md > 0 && dcl >= md) || (lcnt < min2 && rcnt < min2);
   const bool right_small = !(lcnt < rcnt);
   const int32_t sm = right_small ? cr : cl, lg = right_small ? cl : cr;
   const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
-  if (ctl->fp_mode) {
+  if (fp_mode) {
     // f32 gradients: the smaller child from its k_hist_f32 partial slots; the larger =
     // parent - smaller, exact in 64-bit fixed point
     const int32_t a0 = ctl->hjobs[j].a0, na = ctl->hjobs[j].nblk;
@@ -870,54 +894,68 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
         cs[2 * b + 1] = (double)SH * hu;
       }
     }
-  }
-  // the side built in the partition pass: the job's per-block slots (the blocks of
-  // the partition launch from the one holding its first tile to the one holding its
-  // last, slot = block + j; blocks without tiles wrote nothing), or its accumulator
-  int32_t* acc = L.hist_acc + (size_t)j * cells * 3;
-  const int64_t T = ctl->tile_total;
-  const int64_t s0 = J.ntiles > 0 ? part_owner(J.tile0, T, part_grid) : 0;
-  const int64_t s1 = J.ntiles > 0 ? part_owner(J.tile0 + J.ntiles - 1, T, part_grid) : -1;
-  const bool use_slots =
-      J.ntiles > 0 ? part_span_blocks(J.tile0, J.ntiles, T, part_grid) <= PART_SLOT_MAX : true;
-  const int nbq = ctl->fp_mode ? 0 : nb;  // quantized gradients only
-  for (int b = tid; b < nbq; b += SCAN_THREADS) {
-    const size_t ci = (size_t)(ft.cell_base + b);
-    int32_t AG = 0, AH = 0, AT = 0;
-    if (use_slots) {
-      for (int64_t k = s0; k <= s1; ++k) {
-        if (k * T / part_grid >= (k + 1) * T / part_grid) continue;  // a block with no tiles
-        const int4 a = ((const int4*)L.part_slots)[(size_t)(k + j) * cells + ci];
-        AG += a.x;
-        AH += a.y;
-        AT += a.z;
+  } else {
+    // the side built in the partition pass: the job's per-block slots (the blocks of
+    // the partition launch from the one holding its first tile to the one holding
+    // its last, slot = block + j; blocks without tiles wrote nothing), or its
+    // accumulator (read and cleared even when the children are gated)
+    const int64_t s0 = jnt > 0 ? part_owner(jt0, T, part_grid) : 0;
+    const int64_t s1 = jnt > 0 ? part_owner(jt0 + jnt - 1, T, part_grid) : -1;
+    const bool use_slots = jnt > 0 ? part_span_blocks(jt0, jnt, T, part_grid) <= PART_SLOT_MAX : true;
+    int32_t* acc = L.hist_acc + (size_t)j * cells * 3;
+    const int4* slots = (const int4*)L.part_slots;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int b = tid + SCAN_THREADS * q;
+      if (b >= nb) continue;
+      const size_t ci = (size_t)(ft.cell_base + b);
+      int32_t AG = 0, AH = 0, AT = 0;
+      if (use_slots) {
+        // at most PART_SLOT_MAX blocks, enumerated without a dependent chain so all
+        // their loads are issued before the sums: with fewer tiles than blocks each
+        // tile has a block of its own, otherwise every block from s0 to s1 has tiles
+#pragma unroll
+        for (int u = 0; u < PART_SLOT_MAX; ++u) {
+          int64_t k;
+          if (T < part_grid) {
+            if (u >= jnt) continue;
+            k = part_owner(jt0 + u, T, part_grid);
+          } else {
+            k = s0 + u;
+            if (k > s1) continue;
+          }
+          const int4 a = slots[(size_t)(k + j) * cells + ci];
+          AG += a.x;
+          AH += a.y;
+          AT += a.z;
+        }
+      } else {
+        int32_t* a = acc + ci * 3;
+        AG = a[0];
+        AH = a[1];
+        AT = a[2];
+        a[0] = 0;
+        a[1] = 0;
+        a[2] = 0;
       }
-    } else {
-      int32_t* a = acc + ci * 3;
-      AG = a[0];
-      AH = a[1];
-      AT = a[2];
-      a[0] = 0;
-      a[1] = 0;
-      a[2] = 0;
+      if (gated) continue;
+      const int32_t* ps = L.int_slots + ((size_t)p * cells + ci) * 3;
+      const int32_t OG = ps[0] - AG, OH = ps[1] - AH, OT = ps[2] - AT;  // exact
+      int32_t* ls = L.int_slots + ((size_t)cl * cells + ci) * 3;
+      int32_t* rs = L.int_slots + ((size_t)cr * cells + ci) * 3;
+      const int32_t LG_ = acc_right ? OG : AG, LH = acc_right ? OH : AH, LT = acc_right ? OT : AT;
+      const int32_t RG = acc_right ? AG : OG, RH = acc_right ? AH : OH, RT = acc_right ? AT : OT;
+      ls[0] = LG_;
+      ls[1] = LH;
+      ls[2] = LT;
+      rs[0] = RG;
+      rs[1] = RH;
+      rs[2] = RT;
+      if (right_small)
+        int_cell_to_f64(RG, RH, RT, vg1, vh1, vh3, &cs[2 * b], &cs[2 * b + 1]);
+      else
+        int_cell_to_f64(LG_, LH, LT, vg1, vh1, vh3, &cs[2 * b], &cs[2 * b + 1]);
     }
-    if (gated) continue;
-    const int32_t* ps = L.int_slots + ((size_t)p * cells + ci) * 3;
-    const int32_t OG = ps[0] - AG, OH = ps[1] - AH, OT = ps[2] - AT;  // exact
-    int32_t* ls = L.int_slots + ((size_t)cl * cells + ci) * 3;
-    int32_t* rs = L.int_slots + ((size_t)cr * cells + ci) * 3;
-    const int32_t LG_ = acc_right ? OG : AG, LH = acc_right ? OH : AH, LT = acc_right ? OT : AT;
-    const int32_t RG = acc_right ? AG : OG, RH = acc_right ? AH : OH, RT = acc_right ? AT : OT;
-    ls[0] = LG_;
-    ls[1] = LH;
-    ls[2] = LT;
-    rs[0] = RG;
-    rs[1] = RH;
-    rs[2] = RT;
-    if (right_small)
-      int_cell_to_f64(RG, RH, RT, vg1, vh1, vh3, &cs[2 * b], &cs[2 * b + 1]);
-    else
-      int_cell_to_f64(LG_, LH, LT, vg1, vh1, vh3, &cs[2 * b], &cs[2 * b + 1]);
   }
   if (gated) {
     if (tid == 0) {
@@ -926,16 +964,16 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
     }
     return;
   }
-  const LeafSums ss = nd.sums[sm], gs = nd.sums[lg];
-  const bool pgate = L.splittable[(size_t)p * F + f] == 0;
+  const LeafSums ss = right_small ? scr : scl, gs = right_small ? scl : scr;
   fix_compact_block(ft, cs, ss.sg, ss.sh, pgate || !(ss.sh > 0.0 && ss.n > 0));
-  const size_t sl = L.slot_len;
-  const double* s_par = L.slots + (size_t)p * sl + ft.slot_off;
   double* s_sm = L.slots + (size_t)sm * sl + ft.slot_off;
   double* s_lg = L.slots + (size_t)lg * sl + ft.slot_off;
-  for (int i = tid; i < 2 * nb; i += SCAN_THREADS) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int i = tid + SCAN_THREADS * k;
+    if (i >= 2 * nb) continue;
     const double v = cs[i];
-    const double d = s_par[i] - v;
+    const double d = pv[k] - v;
     cp[i] = d;
     s_sm[i] = v;
     s_lg[i] = d;

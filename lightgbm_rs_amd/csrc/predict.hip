@@ -21,26 +21,34 @@ struct PredModelDev {
   const uint32_t* cat_words;
 };
 
-__device__ __forceinline__ int32_t pred_next(const PredNode& n, double fval, const PredModelDev& M,
+// The node's fields arrive as values: selecting between members of a struct held by
+// reference makes the compiler keep the struct in scratch memory.
+__device__ __forceinline__ int32_t pred_next(double thr, int32_t dtype, int32_t left,
+                                             int32_t right, double fval, const PredModelDev& M,
                                              int32_t cat0) {
-  if (n.dtype & 1) {  // CategoricalDecision (tree.rs:212-237)
-    if (isnan(fval)) return n.right;
-    const int32_t iv = fval >= 2147483647.0 ? 2147483647
-                       : fval <= -2147483648.0 ? (int32_t)(-2147483647 - 1)
-                                               : (int32_t)fval;  // saturating `as i32`
-    if (iv < 0) return n.right;
-    const int32_t ci = (int32_t)n.threshold;  // checked at load: 0 <= ci < num_cat
-    const int32_t lo = M.cat_bounds[cat0 + ci], hi = M.cat_bounds[cat0 + ci + 1];
-    const int32_t w = iv >> 5;
-    if (w >= hi - lo) return n.right;
-    return ((M.cat_words[lo + w] >> (iv & 31)) & 1u) ? n.left : n.right;
+  bool go_left;
+  if (dtype & 1) {  // CategoricalDecision (tree.rs:212-237)
+    go_left = false;
+    if (!isnan(fval)) {
+      const int32_t iv = fval >= 2147483647.0 ? 2147483647
+                         : fval <= -2147483648.0 ? (int32_t)(-2147483647 - 1)
+                                                 : (int32_t)fval;  // saturating `as i32`
+      if (iv >= 0) {
+        const int32_t ci = (int32_t)thr;  // checked at load: 0 <= ci < num_cat
+        const int32_t lo = M.cat_bounds[cat0 + ci], hi = M.cat_bounds[cat0 + ci + 1];
+        const int32_t w = iv >> 5;
+        go_left = w < hi - lo && ((M.cat_words[lo + w] >> (iv & 31)) & 1u) != 0u;
+      }
+    }
+  } else {  // NumericalDecision (tree.rs:193-210)
+    const int32_t mt = (dtype >> 2) & 3;
+    if (isnan(fval) && mt != 2) fval = 0.0;
+    if ((mt == 1 && fval >= -1e-35 && fval <= 1e-35) || (mt == 2 && isnan(fval)))
+      go_left = (dtype & 2) != 0;
+    else
+      go_left = fval <= thr;
   }
-  // NumericalDecision (tree.rs:193-210)
-  const int32_t mt = (n.dtype >> 2) & 3;
-  if (isnan(fval) && mt != 2) fval = 0.0;
-  if ((mt == 1 && fval >= -1e-35 && fval <= 1e-35) || (mt == 2 && isnan(fval)))
-    return (n.dtype & 2) ? n.left : n.right;
-  return fval <= n.threshold ? n.left : n.right;
+  return go_left ? left : right;
 }
 
 // Leaf of tree t for the row at x (a path visits fewer than num_leaves nodes: the
@@ -50,14 +58,22 @@ __device__ __forceinline__ int32_t pred_leaf(const PredModelDev& M, int32_t t, c
   if (T.num_leaves <= 1) return 0;
   int32_t node = 0;
   for (int32_t d = 0; d < T.num_leaves && node >= 0; ++d) {
-    const PredNode n = M.nodes[T.node0 + node];
-    node = pred_next(n, (double)x[n.feature], M, T.cat0);
+    const PredNode* nd = M.nodes + T.node0 + node;
+    const double thr = nd->threshold;
+    const int32_t feat = nd->feature, left = nd->left, right = nd->right, dtype = nd->dtype;
+    node = pred_next(thr, dtype, left, right, (double)x[feat], M, T.cat0);
   }
   return node < 0 ? ~node : 0;
 }
 
 __device__ __forceinline__ double pred_sigmoid(double x, double s) { return 1.0 / (1.0 + exp(-s * x)); }
 
+// Rows of up to this many columns are staged in LDS (256 rows x an odd stride of at
+// most 63 floats = 63 KiB): one coalesced load of the block's rows, then every tree
+// walk reads its feature values from LDS instead of one cache line per node visit.
+constexpr int32_t PRED_STAGE_COLS = 63;
+
+template <bool STAGE>
 __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __restrict__ X,
                                                  int64_t rows, int32_t cols, int32_t it0,
                                                  int32_t it1, int32_t ntpi, int32_t kind,
@@ -65,9 +81,25 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
                                                  int32_t average_output,
                                                  double* __restrict__ out,
                                                  int32_t* __restrict__ leaf_out) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
-  const float* x = X + r * cols;
+  extern __shared__ float s_x[];
+  const int64_t r0 = (int64_t)blockIdx.x * blockDim.x;
+  const int64_t r = r0 + threadIdx.x;
+  const float* x;
+  if (STAGE) {
+    const int32_t stride = cols | 1;  // odd: lanes' rows fall in different banks
+    const int32_t total = (int32_t)(min((int64_t)blockDim.x, rows - r0) * cols);
+    const float* src = X + r0 * cols;
+    for (int32_t i = threadIdx.x; i < total; i += blockDim.x) {
+      const int32_t rr = i / cols;
+      s_x[rr * stride + (i - rr * cols)] = src[i];
+    }
+    __syncthreads();
+    if (r >= rows) return;
+    x = s_x + threadIdx.x * stride;
+  } else {
+    if (r >= rows) return;
+    x = X + r * cols;
+  }
   if (kind == 2) {
     const int64_t nt = (int64_t)(it1 - it0) * ntpi;
     for (int32_t i = it0; i < it1; ++i)
@@ -132,9 +164,13 @@ void launch_predict(const PredNode* nodes, const PredTree* trees, const double* 
   if (rows <= 0) return;
   const PredModelDev M{nodes, trees, leaves, cat_bounds, cat_words};
   const int64_t blocks = (rows + 255) / 256;
-  k_predict<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(M, X, rows, cols, it0, it1, ntpi, kind,
-                                                         objective, sigmoid, average_output, out,
-                                                         leaf_out);
+  if (cols <= PRED_STAGE_COLS)
+    k_predict<true><<<dim3((unsigned)blocks), dim3(256), (size_t)256 * (cols | 1) * sizeof(float),
+                      s>>>(M, X, rows, cols, it0, it1, ntpi, kind, objective, sigmoid,
+                           average_output, out, leaf_out);
+  else
+    k_predict<false><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+        M, X, rows, cols, it0, it1, ntpi, kind, objective, sigmoid, average_output, out, leaf_out);
 }
 
 }  // namespace lgbm

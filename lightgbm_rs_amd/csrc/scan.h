@@ -82,6 +82,38 @@ __device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int3
 // break becomes "first candidate with active && !cont && brk" (ballot), and the
 // sequential strict-> best becomes a max-gain, lowest-index wave reduction.
 // ===========================================================================
+// Per lane k < cnt: (sg, sh, sc) += the lanes' (g, h, c) of lanes 0..k, added one at a
+// time in lane order — the reference's sequential f64 accumulation, so every prefix
+// rounds exactly as its loop does.  Lanes that hold no bin pass (+0.0, +0.0, 0):
+// adding +0.0 to an accumulation that started at a value other than -0.0 never
+// changes it.  The values go through a per-wave LDS row so the chain reads them as
+// uniform (broadcast) loads; the loop has no branch and no cross-lane move.
+__device__ __forceinline__ void prefix_in_order(double g, double h, int32_t c, int32_t cnt,
+                                                int lane, double* sg, double* sh, int32_t* sc) {
+  __shared__ double pf_g[SCAN_THREADS / LGBM_WAVE][LGBM_WAVE];
+  __shared__ double pf_h[SCAN_THREADS / LGBM_WAVE][LGBM_WAVE];
+  __shared__ int32_t pf_c[SCAN_THREADS / LGBM_WAVE][LGBM_WAVE];
+  const int w = (int)(threadIdx.x / LGBM_WAVE);
+  pf_g[w][lane] = g;
+  pf_h[w][lane] = h;
+  pf_c[w][lane] = c;
+  __builtin_amdgcn_wave_barrier();
+  double ag = *sg, ah = *sh;
+  int32_t ac = *sc;
+  for (int32_t i = 0; i < cnt; ++i) {
+    // lanes before i add +0.0 (all-zero bits): a mask, not a select, so the loads
+    // stay unconditional and the loop branch-free
+    const unsigned long long m = i <= lane ? ~0ull : 0ull;
+    ag += __longlong_as_double((long long)((unsigned long long)__double_as_longlong(pf_g[w][i]) & m));
+    ah += __longlong_as_double((long long)((unsigned long long)__double_as_longlong(pf_h[w][i]) & m));
+    ac += pf_c[w][i] & (int32_t)(uint32_t)m;
+  }
+  __builtin_amdgcn_wave_barrier();  // the row is rewritten by the next call
+  *sg = ag;
+  *sh = ah;
+  *sc = ac;
+}
+
 static __device__ void wave_scan(const double* hist, const DevFeature& ft, const ScanCfg& c,
                           double sum_gradient, double sum_hessian, int32_t num_data, double po,
                           lgbm_split_info* out) {
@@ -127,18 +159,7 @@ static __device__ void wave_scan(const double* hist, const DevFeature& ft, const
       const int32_t mc = act ? round_int(mh * cf) : 0;
       double sg = cg, sh = ch;
       int32_t rc = cc;
-      for (int32_t i = 0; i < cnt; ++i) {
-        const int32_t ti = t_start - (base + i);
-        if ((ti >= 1 - offset) && !(skip_def && ti + offset == defb)) {  // wave-uniform
-          const double xg = readlane_f64(mg, i), xh = readlane_f64(mh, i);
-          const int32_t xc = readlane_i32(mc, i);
-          if (i <= lane) {
-            sg += xg;
-            sh += xh;
-            rc += xc;
-          }
-        }
-      }
+      prefix_in_order(mg, mh, mc, cnt, lane, &sg, &sh, &rc);
       const int32_t lc = num_data - rc;
       const double slh = shb - sh, slg = sum_gradient - sg;
       const bool cont = rc < c.min_d || sh < c.min_h;
@@ -205,18 +226,7 @@ static __device__ void wave_scan(const double* hist, const DevFeature& ft, const
       const int32_t mc = addl ? round_int(mh * cf) : 0;
       double sg = cg, sh = ch;
       int32_t lcn = cc;
-      for (int32_t i = 0; i < cnt; ++i) {
-        const int32_t ti = fwd_start + base + i;
-        if (!(skip_def && ti + offset == defb) && ti >= 0) {  // wave-uniform
-          const double xg = readlane_f64(mg, i), xh = readlane_f64(mh, i);
-          const int32_t xc = readlane_i32(mc, i);
-          if (i <= lane) {
-            sg += xg;
-            sh += xh;
-            lcn += xc;
-          }
-        }
-      }
+      prefix_in_order(mg, mh, mc, cnt, lane, &sg, &sh, &lcn);
       const int32_t rc = num_data - lcn;
       const double srh = shb - sh, srg = sum_gradient - sg;
       const bool cont = lcn < c.min_d || sh < c.min_h;

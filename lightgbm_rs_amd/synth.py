@@ -73,6 +73,24 @@ def config1_like(n, seed=0x5EED0001, max_bin=63, device=None, derived=True):
     return bins, _meta_for(nbs), np.array(upper, dtype=np.float64), y
 
 
+def config1_raw(n, seed=0x5EED0001, device=None):
+    """configs[1]'s raw table before binning: X as a torch float32 tensor [28, n] on
+    `device` (column-major: one feature per row) and the labels as numpy float32.
+    The same recipe and generator draws as config1_like(device=...)."""
+    import torch
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    X = torch.randn((21, n), generator=gen, device=device, dtype=torch.float32)
+    X = torch.cat([X, torch.stack(_derive(X, torch))], dim=0)
+    w = torch.randn(28, generator=gen, device=device, dtype=torch.float32)
+    noise = torch.randn(n, generator=gen, device=device, dtype=torch.float32) * 0.1
+    logit = w @ X + 0.5 * X[0] * X[1] + noise
+    u = torch.rand(n, generator=gen, device=device, dtype=torch.float32)
+    y = (u < torch.sigmoid(logit)).to(torch.float32)
+    return X.contiguous(), y.cpu().numpy()
+
+
 def _config1_torch(n, seed, max_bin, device):
     import torch
 

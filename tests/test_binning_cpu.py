@@ -145,3 +145,20 @@ def test_from_column_rejects_bad_params():
         BinMapper.from_column(np.zeros(10), max_bin=1)
     with pytest.raises(TypeError):
         BinMapper.from_column(np.zeros(10), maxbin=10)
+
+
+def test_from_sampled_column_equals_from_column():
+    """Gathering the sample rows outside the library gives the same mapper."""
+    rng = np.random.default_rng(21)
+    col = rng.normal(size=30000)
+    col[rng.random(30000) < 0.1] = 0.0
+    col[rng.random(30000) < 0.02] = np.nan
+    for kw in [dict(bin_construct_sample_cnt=5000, data_random_seed=9, max_bin=63),
+               dict(bin_construct_sample_cnt=50000, max_bin=255),
+               dict(bin_construct_sample_cnt=1000, pre_filter=True, min_data_in_leaf=500)]:
+        a = BinMapper.from_column(col, **kw)
+        idx = sample_indices(len(col), kw["bin_construct_sample_cnt"], kw.get("data_random_seed", 1))
+        b = BinMapper.from_sampled_column(col[idx], len(col), **kw)
+        assert np.array_equal(a.upper_bounds.view(np.uint64), b.upper_bounds.view(np.uint64))
+        for k in ("num_bin", "missing_type", "default_bin", "most_freq_bin", "is_trivial"):
+            assert getattr(a, k) == getattr(b, k), k

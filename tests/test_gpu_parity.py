@@ -560,3 +560,32 @@ def test_fp32_train_binary_config0_auc():
     a, oa = _auc(y, scores), _auc(y, oscores)
     say(f"  AUC {a:.9f} oracle {oa:.9f}")
     assert abs(a - oa) <= 1e-6
+
+
+@pytest.mark.parametrize("qbins", [4, 0])
+def test_lookahead_matches_plain_iterations(qbins):
+    """lgbm_hip_set_lookahead: the next iteration's gradients and quantization run
+    while the host reads the tree; trees and scores are bit-identical to the plain
+    loop, also across an invalidating call (set_labels) and a skipped iteration."""
+    from lightgbm_rs_amd import binary_boost_from_score
+    n = 60_000
+    bins, meta, ub, y = config1_like(n, seed=13)
+    init = binary_boost_from_score(y)
+    cfg = GainConfig.make(min_data_in_leaf=20)
+    runs = []
+    for look in (False, True):
+        b = HipBackend(0)
+        try:
+            b.upload_resident_bins(bins, meta, ub)
+            b.set_labels(y, init)
+            b.set_lookahead(look)
+            trees = [b.train_iter_binary(i, cfg, 63, -1, 0.1, qbins, True) for i in range(3)]
+            b.set_labels(y, init)  # drops a pending lookahead
+            trees += [b.train_iter_binary(i, cfg, 63, -1, 0.1, qbins, True) for i in (0, 1, 5, 6)]
+            runs.append((trees, b.scores()))
+        finally:
+            b.close()
+    (ta, sa), (tb, sb) = runs
+    for i, (x, z) in enumerate(zip(ta, tb)):
+        _compare_trees(x, z, f"iteration {i}")
+    assert np.array_equal(bits(sa), bits(sb))
