@@ -99,30 +99,31 @@ __global__ __launch_bounds__(256) void k_bin_records(const T* __restrict__ x, in
 
 template <typename T, bool CM>
 void launch_typed(const void* x, int64_t n, int32_t F, int32_t W, const DevBinFeature* feats,
-                  const double* ub, int32_t ub_count, const int2* cats, uint4* rec, hipStream_t s) {
+                  const double* ub, int32_t ub_count, const int2* cats, uint4* rec, hipStream_t s,
+                  const KernelEvents* ev) {
   const int64_t want = (n + 255) / 256;
   const unsigned blocks = (unsigned)std::min<int64_t>(std::max<int64_t>(want, 1), 4096);
   const size_t lds = ub_count <= BIN_LDS_BOUNDS ? (size_t)ub_count * sizeof(double) : 0;
-  k_bin_records<T, CM><<<dim3(blocks), dim3(256), lds, s>>>(
-      (const T*)x, n, F, W, feats, ub, ub_count, cats, rec);
+  KLAUNCH(ev, (k_bin_records<T, CM>), dim3(blocks), dim3(256), lds, s, (const T*)x, n, F, W,
+          feats, ub, ub_count, cats, rec);
 }
 
 }  // namespace
 
 void launch_bin_records(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
                         int32_t W, const DevBinFeature* feats, const double* ub, int32_t ub_count,
-                        const int2* cats, uint4* rec, hipStream_t s) {
+                        const int2* cats, uint4* rec, hipStream_t s, const KernelEvents* ev) {
   if (n <= 0) return;
   if (f64) {
     if (col_major)
-      launch_typed<double, true>(x, n, F, W, feats, ub, ub_count, cats, rec, s);
+      launch_typed<double, true>(x, n, F, W, feats, ub, ub_count, cats, rec, s, ev);
     else
-      launch_typed<double, false>(x, n, F, W, feats, ub, ub_count, cats, rec, s);
+      launch_typed<double, false>(x, n, F, W, feats, ub, ub_count, cats, rec, s, ev);
   } else {
     if (col_major)
-      launch_typed<float, true>(x, n, F, W, feats, ub, ub_count, cats, rec, s);
+      launch_typed<float, true>(x, n, F, W, feats, ub, ub_count, cats, rec, s, ev);
     else
-      launch_typed<float, false>(x, n, F, W, feats, ub, ub_count, cats, rec, s);
+      launch_typed<float, false>(x, n, F, W, feats, ub, ub_count, cats, rec, s, ev);
   }
 }
 

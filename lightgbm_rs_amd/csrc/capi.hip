@@ -25,7 +25,7 @@ void launch_predict(const PredNode* nodes, const PredTree* trees, const double* 
                     const int32_t* cat_bounds, const uint32_t* cat_words, const float* X,
                     int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
                     int32_t objective, double sigmoid, int32_t average_output, double* out,
-                    int32_t* leaf_out, hipStream_t s);
+                    int32_t* leaf_out, hipStream_t s, const KernelEvents* ev);
 }
 
 namespace {
@@ -1129,10 +1129,10 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
     e = hipMemcpy(d_cats, cats.data(), cats.size() * sizeof(int2), hipMemcpyHostToDevice);
   if (e == hipSuccess) {
     // c->d_ub holds the same bounds, concatenated in feature order
-    ev_begin(c, FAM_BIN);
+    KernelEvents ke;
     launch_bin_records(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->W, d_bf,
-                       c->d_ub, (int32_t)ub.size(), d_cats, c->rec[BUF_ORIG], c->stream);
-    ev_end(c);
+                       c->d_ub, (int32_t)ub.size(), d_cats, c->rec[BUF_ORIG], c->stream,
+                       ev_kernel(c, FAM_BIN, &ke));
     if (c->timing) {
       c->bin_launches += 1.0;
       c->bin_values += (double)num_rows * F;
@@ -1851,12 +1851,12 @@ int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int3
 
 int predict_run(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* d_x, int64_t rows,
                 int32_t cols, int32_t it0, int32_t it1, int32_t kind, void* d_out) {
-  ev_begin(c, FAM_PRED);
+  KernelEvents ke;
   launch_predict(c->pm_nodes, c->pm_trees, c->pm_leaves, c->pm_catb, c->pm_catw, d_x, rows, cols,
                  it0, it1, m->num_tree_per_iteration, kind, m->objective, m->sigmoid,
                  m->average_output ? 1 : 0, kind == LGBM_HIP_PREDICT_LEAF ? nullptr : (double*)d_out,
-                 kind == LGBM_HIP_PREDICT_LEAF ? (int32_t*)d_out : nullptr, c->stream);
-  ev_end(c);
+                 kind == LGBM_HIP_PREDICT_LEAF ? (int32_t*)d_out : nullptr, c->stream,
+                 ev_kernel(c, FAM_PRED, &ke));
   if (c->timing) {
     c->pred_launches += 1.0;
     c->pred_walks += (double)rows * (double)(it1 - it0) * m->num_tree_per_iteration;

@@ -22,6 +22,8 @@
 
 #include "lgbm_device.h"
 
+#include <hip/hip_ext.h>
+
 struct RowBufs {
   uint4* rec[NBUF];
   uint16_t* gh[NBUF];   // packed quantized (q_g, q_h) per row
@@ -141,6 +143,16 @@ struct KernelEvents {
   hipEvent_t stop = nullptr;
 };
 
+// Launch `kern` plainly, or with the kernel-stamped events of `ev` when timing.
+#define KLAUNCH(ev, kern, grid, block, lds, s, ...)                                        \
+  do {                                                                                   \
+    if ((ev) && ((ev)->start || (ev)->stop))                                             \
+      hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)(lds), s, (ev)->start, (ev)->stop, \
+                            0u, __VA_ARGS__);                                            \
+    else                                                                                 \
+      kern<<<grid, block, lds, s>>>(__VA_ARGS__);                                        \
+  } while (0)
+
 void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t W, uint4* rec,
                          hipStream_t s);
 
@@ -158,7 +170,7 @@ struct DevBinFeature {
 // the resident records; `ub_count` upper bounds are staged in LDS.
 void launch_bin_records(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
                         int32_t W, const DevBinFeature* feats, const double* ub, int32_t ub_count,
-                        const int2* cats, uint4* rec, hipStream_t s);
+                        const int2* cats, uint4* rec, hipStream_t s, const KernelEvents* ev);
 void launch_absmax(const float* g, const float* h, int64_t n, uint4* partials, hipStream_t s);
 void launch_grad_binary(const double* score, const float* label, float* g, float* h, int64_t n,
                         uint4* partials, hipStream_t s);

@@ -9,6 +9,7 @@
 //   ConvertOutput (objective.rs:241-340) for the transformed kind.
 #include <hip/hip_runtime.h>
 
+#include "kernels.h"
 #include "model.h"
 
 namespace lgbm {
@@ -160,17 +161,17 @@ void launch_predict(const PredNode* nodes, const PredTree* trees, const double* 
                     const int32_t* cat_bounds, const uint32_t* cat_words, const float* X,
                     int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
                     int32_t objective, double sigmoid, int32_t average_output, double* out,
-                    int32_t* leaf_out, hipStream_t s) {
+                    int32_t* leaf_out, hipStream_t s, const KernelEvents* ev) {
   if (rows <= 0) return;
   const PredModelDev M{nodes, trees, leaves, cat_bounds, cat_words};
   const int64_t blocks = (rows + 255) / 256;
   if (cols <= PRED_STAGE_COLS)
-    k_predict<true><<<dim3((unsigned)blocks), dim3(256), (size_t)256 * (cols | 1) * sizeof(float),
-                      s>>>(M, X, rows, cols, it0, it1, ntpi, kind, objective, sigmoid,
-                           average_output, out, leaf_out);
+    KLAUNCH(ev, k_predict<true>, dim3((unsigned)blocks), dim3(256),
+            (size_t)256 * (cols | 1) * sizeof(float), s, M, X, rows, cols, it0, it1, ntpi, kind,
+            objective, sigmoid, average_output, out, leaf_out);
   else
-    k_predict<false><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
-        M, X, rows, cols, it0, it1, ntpi, kind, objective, sigmoid, average_output, out, leaf_out);
+    KLAUNCH(ev, k_predict<false>, dim3((unsigned)blocks), dim3(256), 0, s, M, X, rows, cols, it0,
+            it1, ntpi, kind, objective, sigmoid, average_output, out, leaf_out);
 }
 
 }  // namespace lgbm

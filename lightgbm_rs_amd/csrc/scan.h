@@ -22,15 +22,6 @@ namespace lgbm {
     default: break;                                                         \
   }
 
-// Launch `kern` plainly, or with the kernel-stamped events of `ev` when timing.
-#define KLAUNCH(ev, kern, grid, block, lds, s, ...)                                        \
-  do {                                                                                   \
-    if ((ev) && ((ev)->start || (ev)->stop))                                             \
-      hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)(lds), s, (ev)->start, (ev)->stop, \
-                            0u, __VA_ARGS__);                                            \
-    else                                                                                 \
-      kern<<<grid, block, lds, s>>>(__VA_ARGS__);                                        \
-  } while (0)
 
 // Byte f of a record held in registers.  Selects with compile-time indices only, so
 // the record never leaves the register file.
