@@ -466,6 +466,18 @@ int lgbm_hip_predict_device(lgbm_hip_ctx* ctx, const lgbm_hip_model* model, cons
                             int64_t num_rows, int32_t num_cols, int32_t start_iteration,
                             int32_t num_iteration, int32_t kind, void* d_out);
 
+/* Prediction early stopping: predict_raw_early_stop_mat (crates/lgbm-model/src/
+ * predict.rs:557-605) over GbdtModel::predict_raw_early_stop (ensemble.rs:120-151).
+ * Every `freq` iterations a row whose margin exceeds `margin` (binary: 2|score|;
+ * multiclass: top score minus the second) stops; objectives that need accurate
+ * prediction (all but binary / multiclass / multiclassova) evaluate the whole range.
+ * out: double[num_rows * num_tree_per_iteration] raw scores; iterations (may be
+ * NULL): int32[num_rows] iterations evaluated per row.  Host buffers. */
+int lgbm_hip_predict_early_stop(lgbm_hip_ctx* ctx, const lgbm_hip_model* model, const float* data,
+                                int64_t num_rows, int32_t num_cols, int32_t start_iteration,
+                                int32_t num_iteration, int32_t freq, double margin, double* out,
+                                int32_t* iterations);
+
 #ifdef __cplusplus
 }
 #endif

@@ -366,7 +366,22 @@ def _predict_device(self, model, x_ptr, rows, cols, out_ptr, kind="raw", start_i
         C.c_void_p(out_ptr)))
 
 
+def _predict_early_stop(self, model, X, freq, margin, start_iteration=0, num_iteration=-1):
+    """predict_raw_early_stop_mat (crates/lgbm-model/src/predict.rs:557-605) on the
+    device: (raw float64 [rows, num_tree_per_iteration], iterations int32 [rows])."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    rows, cols = X.shape
+    out = np.zeros((rows, model.num_tree_per_iteration), np.float64)
+    iters = np.zeros(rows, np.int32)
+    self._check(self.lib.lgbm_hip_predict_early_stop(
+        self.ctx, model.handle, ptr(X, C.c_float), C.c_int64(rows), C.c_int32(cols),
+        C.c_int32(start_iteration), C.c_int32(num_iteration), C.c_int32(freq),
+        C.c_double(margin), ptr(out, C.c_double), ptr(iters, C.c_int32)))
+    return out, iters
+
+
 HipBackend.predict = _predict
+HipBackend.predict_early_stop = _predict_early_stop
 HipBackend.predict_device = _predict_device
 
 

@@ -24,8 +24,9 @@ namespace lgbm {
 void launch_predict(const PredNode* nodes, const PredTree* trees, const double* leaves,
                     const int32_t* cat_bounds, const uint32_t* cat_words, const float* X,
                     int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
-                    int32_t objective, double sigmoid, int32_t average_output, double* out,
-                    int32_t* leaf_out, hipStream_t s, const KernelEvents* ev);
+                    int32_t objective, double sigmoid, int32_t average_output, int32_t es_freq,
+                    double es_margin, int32_t* es_iters, double* out, int32_t* leaf_out,
+                    hipStream_t s, const KernelEvents* ev);
 }
 
 namespace {
@@ -1850,11 +1851,13 @@ int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int3
 }
 
 int predict_run(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* d_x, int64_t rows,
-                int32_t cols, int32_t it0, int32_t it1, int32_t kind, void* d_out) {
+                int32_t cols, int32_t it0, int32_t it1, int32_t kind, void* d_out,
+                int32_t es_freq = 0, double es_margin = 0.0, int32_t* d_iters = nullptr) {
   KernelEvents ke;
   launch_predict(c->pm_nodes, c->pm_trees, c->pm_leaves, c->pm_catb, c->pm_catw, d_x, rows, cols,
                  it0, it1, m->num_tree_per_iteration, kind, m->objective, m->sigmoid,
-                 m->average_output ? 1 : 0, kind == LGBM_HIP_PREDICT_LEAF ? nullptr : (double*)d_out,
+                 m->average_output ? 1 : 0, es_freq, es_margin, d_iters,
+                 kind == LGBM_HIP_PREDICT_LEAF ? nullptr : (double*)d_out,
                  kind == LGBM_HIP_PREDICT_LEAF ? (int32_t*)d_out : nullptr, c->stream,
                  ev_kernel(c, FAM_PRED, &ke));
   if (c->timing) {
@@ -1908,6 +1911,57 @@ int lgbm_hip_predict_device(lgbm_hip_ctx* c, const lgbm_hip_model* m, const floa
   if (rows == 0 || width == 0) return LGBM_HIP_OK;
   if (!d_data || !d_out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null data/out");
   return predict_run(c, m, d_data, rows, cols, it0, it1, kind, d_out);
+}
+
+int lgbm_hip_predict_early_stop(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* data,
+                                int64_t rows, int32_t cols, int32_t start_iteration,
+                                int32_t num_iteration, int32_t freq, double margin, double* out,
+                                int32_t* iterations) {
+  int32_t it0 = 0, it1 = 0;
+  int64_t width = 0;
+  int rc = predict_prepare(c, m, rows, cols, start_iteration, num_iteration, LGBM_HIP_PREDICT_RAW,
+                           &it0, &it1, &width);
+  if (rc) return rc;
+  if (rows == 0) return LGBM_HIP_OK;
+  if (!data || !out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null data/out");
+  // resolve_objective + the C++ Predictor gate (predict.rs:557-605): objectives that
+  // need accurate prediction evaluate the whole range
+  if (!m->have_objective)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT,
+                   "model has no objective= line; cannot apply ConvertOutput");
+  const bool accurate = !(m->objective == OBJ_BINARY || m->objective == OBJ_MULTICLASS ||
+                          m->objective == OBJ_MULTICLASS_OVA);
+  const int32_t f = accurate ? 0 : freq;
+  const size_t xb = (size_t)rows * (size_t)cols * 4, ob = (size_t)rows * (size_t)width * 8;
+  if (c->pm_x_cap < xb) {
+    if ((rc = dalloc(c, &c->pm_x, (size_t)rows * (size_t)cols))) return rc;
+    c->pm_x_cap = xb;
+  }
+  const size_t need = ob + (size_t)rows * 4;
+  if (c->pm_out_cap < need) {
+    char* p = nullptr;
+    if ((rc = dalloc(c, &p, need))) return rc;
+    if (c->pm_out) (void)hipFree(c->pm_out);
+    c->pm_out = p;
+    c->pm_out_cap = need;
+  }
+  int32_t* d_iters = (int32_t*)((char*)c->pm_out + ob);
+  HIPCHK(c, hipMemcpy(c->pm_x, data, xb, hipMemcpyHostToDevice));
+  if (f <= 0) {
+    // the whole range: raw scores, every row evaluating every iteration
+    if ((rc = predict_run(c, m, c->pm_x, rows, cols, it0, it1, LGBM_HIP_PREDICT_RAW, c->pm_out)))
+      return rc;
+    HIPCHK(c, hipMemcpy(out, c->pm_out, ob, hipMemcpyDeviceToHost));
+    if (iterations)
+      for (int64_t r = 0; r < rows; ++r) iterations[r] = it1 - it0;
+    return LGBM_HIP_OK;
+  }
+  if ((rc = predict_run(c, m, c->pm_x, rows, cols, it0, it1, LGBM_HIP_PREDICT_RAW, c->pm_out, f,
+                        margin, d_iters)))
+    return rc;
+  HIPCHK(c, hipMemcpy(out, c->pm_out, ob, hipMemcpyDeviceToHost));
+  if (iterations) HIPCHK(c, hipMemcpy(iterations, d_iters, (size_t)rows * 4, hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
 }
 
 }  // extern "C"

@@ -79,7 +79,8 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
                                                  int64_t rows, int32_t cols, int32_t it0,
                                                  int32_t it1, int32_t ntpi, int32_t kind,
                                                  int32_t objective, double sigmoid,
-                                                 int32_t average_output,
+                                                 int32_t average_output, int32_t es_freq,
+                                                 double es_margin, int32_t* __restrict__ es_iters,
                                                  double* __restrict__ out,
                                                  int32_t* __restrict__ leaf_out) {
   extern __shared__ float s_x[];
@@ -109,6 +110,42 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
     return;
   }
   double* o = out + r * ntpi;
+  if (es_freq > 0) {
+    // GbdtModel::predict_raw_early_stop (ensemble.rs:120-151): iterations in order,
+    // each adding its trees class by class; every es_freq iterations the margin
+    // test of pred_early_stop_should_stop (ensemble.rs:337-356) may end the row
+    for (int32_t k = 0; k < ntpi; ++k) o[k] = 0.0;
+    int32_t counter = 0, evaluated = 0;
+    for (int32_t i = it0; i < it1; ++i) {
+      for (int32_t k = 0; k < ntpi; ++k) {
+        const int32_t t = i * ntpi + k;
+        o[k] += M.leaves[M.trees[t].leaf0 + pred_leaf(M, t, x)];
+      }
+      ++evaluated;
+      if (++counter == es_freq) {
+        bool stop;
+        if (ntpi == 1) {
+          stop = 2.0 * fabs(o[0]) > es_margin;
+        } else {
+          double top1 = -__builtin_inf(), top2 = -__builtin_inf();
+          for (int32_t k = 0; k < ntpi; ++k) {
+            const double v = o[k];
+            if (v > top1) {
+              top2 = top1;
+              top1 = v;
+            } else if (v > top2) {
+              top2 = v;
+            }
+          }
+          stop = (top1 - top2) > es_margin;
+        }
+        if (stop) break;
+        counter = 0;
+      }
+    }
+    es_iters[r] = evaluated;
+    return;
+  }
   for (int32_t k = 0; k < ntpi; ++k) {
     double acc = 0.0;
     for (int32_t i = it0; i < it1; ++i) {
@@ -160,18 +197,20 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
 void launch_predict(const PredNode* nodes, const PredTree* trees, const double* leaves,
                     const int32_t* cat_bounds, const uint32_t* cat_words, const float* X,
                     int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
-                    int32_t objective, double sigmoid, int32_t average_output, double* out,
-                    int32_t* leaf_out, hipStream_t s, const KernelEvents* ev) {
+                    int32_t objective, double sigmoid, int32_t average_output, int32_t es_freq,
+                    double es_margin, int32_t* es_iters, double* out, int32_t* leaf_out,
+                    hipStream_t s, const KernelEvents* ev) {
   if (rows <= 0) return;
   const PredModelDev M{nodes, trees, leaves, cat_bounds, cat_words};
   const int64_t blocks = (rows + 255) / 256;
   if (cols <= PRED_STAGE_COLS)
     KLAUNCH(ev, k_predict<true>, dim3((unsigned)blocks), dim3(256),
             (size_t)256 * (cols | 1) * sizeof(float), s, M, X, rows, cols, it0, it1, ntpi, kind,
-            objective, sigmoid, average_output, out, leaf_out);
+            objective, sigmoid, average_output, es_freq, es_margin, es_iters, out, leaf_out);
   else
     KLAUNCH(ev, k_predict<false>, dim3((unsigned)blocks), dim3(256), 0, s, M, X, rows, cols, it0,
-            it1, ntpi, kind, objective, sigmoid, average_output, out, leaf_out);
+            it1, ntpi, kind, objective, sigmoid, average_output, es_freq, es_margin, es_iters, out,
+            leaf_out);
 }
 
 }  // namespace lgbm

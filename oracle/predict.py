@@ -198,3 +198,50 @@ def convert(model, raw):
             x = v[0]
             out[r, 0] = (math.copysign(1.0, x) if x != 0 else 0.0) * x * x if model["sqrt"] else x
     return out
+
+
+def _es_stop(out, margin):
+    """pred_early_stop_should_stop (crates/lgbm-model/src/ensemble.rs:337-356)."""
+    if len(out) == 1:
+        return 2.0 * abs(out[0]) > margin
+    top1 = top2 = -math.inf
+    for v in out:
+        if v > top1:
+            top2, top1 = top1, v
+        elif v > top2:
+            top2 = v
+    return (top1 - top2) > margin
+
+
+def predict_early_stop(model, X, freq, margin, start_iteration=0, num_iteration=-1):
+    """GbdtModel::predict_raw_early_stop per row (ensemble.rs:120-151) behind the
+    accurate-prediction gate of predict_raw_early_stop_mat (predict.rs:557-605):
+    returns (raw [rows, ntpi] float64, iterations evaluated [rows])."""
+    if model["objective"] not in ("binary", "multiclass", "softmax", "multiclassova",
+                                  "multiclass_ova", "ova", "ovr"):
+        freq = 0
+    X64 = np.asarray(X, dtype=np.float32).astype(np.float64)
+    ntpi = model["num_tree_per_iteration"]
+    start, num = _range(model, start_iteration, num_iteration)
+    trees = model["trees"]
+    leaves = [[leaf_of(trees[i * ntpi + k], X64) for k in range(ntpi)]
+              for i in range(start, start + num)]
+    raw = np.zeros((len(X64), ntpi))
+    iters = np.zeros(len(X64), np.int32)
+    for r in range(len(X64)):
+        out = [0.0] * ntpi
+        counter = 0
+        n = 0
+        for ii in range(num):
+            for k in range(ntpi):
+                t = trees[(start + ii) * ntpi + k]
+                out[k] += t["leaf_value"][leaves[ii][k][r]]
+            n += 1
+            counter += 1
+            if freq > 0 and counter == freq:
+                if _es_stop(out, margin):
+                    break
+                counter = 0
+        raw[r] = out
+        iters[r] = n
+    return raw, iters

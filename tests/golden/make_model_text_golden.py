@@ -42,6 +42,10 @@ FILES = {
 # and the transformed predictions (f64 bits) of the real binary on the 12-row corpus.
 SPINE = ["binary_scores.txt", "binary_gh_iter1.txt", "binary_gh_iterN.txt",
          "binary_spine_pred.txt"]
+# Prediction early stopping (predict_parity.rs:160-226): model, input rows (f64 bits)
+# and the real binary's frozen raw scores per (freq, margin) cell.
+PREDICT_MODES = {"numeric": ["model.txt", "X.txt", "early_stop.txt"],
+                 "multiclass": ["model.txt", "X.txt", "early_stop.txt"]}
 
 
 def main():
@@ -52,6 +56,11 @@ def main():
     os.makedirs(os.path.join(OUT, "spine"), exist_ok=True)
     for name in SPINE:
         shutil.copyfile(os.path.join(FIX, "boosting", name), os.path.join(OUT, "spine", name))
+    for corpus, names in PREDICT_MODES.items():
+        dst = os.path.join(os.path.dirname(OUT), "predict_modes", corpus)
+        os.makedirs(dst, exist_ok=True)
+        for name in names:
+            shutil.copyfile(os.path.join(FIX, "predict_modes", corpus, name), os.path.join(dst, name))
 
 
 if __name__ == "__main__":

@@ -183,3 +183,28 @@ def test_trained_model_text_predicts_training_scores(be, quant):
     got = be.predict(back, X, "raw")[:, 0]
     assert np.array_equal(bits(got), bits(scores))
     assert np.array_equal(bits(P.predict(P.parse_model(text), X, kind="raw")[:, 0]), bits(scores))
+
+
+@pytest.mark.parametrize("name", ["numeric", "multiclass"])
+def test_device_early_stop_matches_reference_captures(be, name):
+    from tests import predict_modes as PM
+    text, X, cells = PM.corpus(name)
+    m, om = Model(text), P.parse_model(text)
+    for freq, margin, exp in cells:
+        raw, iters = be.predict_early_stop(m, X, freq, margin)
+        assert np.array_equal(bits(raw), bits(exp)), (freq, margin)
+        _, oiters = P.predict_early_stop(om, X, freq, margin)
+        assert np.array_equal(iters, oiters), (freq, margin)
+
+
+def test_device_early_stop_vs_oracle_large(be):
+    """More rows, several margins and an iteration slice, against the oracle."""
+    text, d = corpus("multiclass")
+    m, om = Model(text), P.parse_model(text)
+    rng = np.random.default_rng(8)
+    X = (d["X"][rng.integers(0, len(d["X"]), 3000)] + rng.normal(0, 0.1, (3000, 28))).astype(np.float32)
+    for freq, margin, s, n in [(1, 0.5, 0, -1), (3, 2.0, 0, -1), (2, 1.0, 2, 6), (5, 0.0, 0, -1)]:
+        raw, iters = be.predict_early_stop(m, X, freq, margin, s, n)
+        oraw, oiters = P.predict_early_stop(om, X, freq, margin, s, n)
+        assert np.array_equal(bits(raw), bits(oraw)), (freq, margin, s, n)
+        assert np.array_equal(iters, oiters), (freq, margin, s, n)

@@ -121,3 +121,22 @@ def test_library_rejects_malformed_models(edit, needle):
     with pytest.raises(HipError) as e:
         Model(text)
     assert needle in str(e.value)
+
+
+@pytest.mark.parametrize("name", ["numeric", "multiclass"])
+def test_oracle_early_stop_matches_reference_captures(name):
+    """Prediction early stopping (predict_parity.rs:160-226): every (freq, margin)
+    cell's frozen raw scores; the regression model ignores the request (accurate
+    prediction) and the multiclass model stops at its margin."""
+    from tests import predict_modes as PM
+    text, X, cells = PM.corpus(name)
+    m = P.parse_model(text)
+    full = P.predict(m, X, kind="raw")
+    stopped = False
+    for freq, margin, exp in cells:
+        raw, iters = P.predict_early_stop(m, X, freq, margin)
+        assert np.array_equal(bits(raw), bits(exp)), (freq, margin)
+        stopped |= bool(np.any(iters < len(m["trees"]) // m["num_tree_per_iteration"]))
+    assert stopped == (name == "multiclass")
+    if name == "numeric":
+        assert np.array_equal(bits(cells[0][2]), bits(full))
