@@ -22,8 +22,9 @@ using namespace lgbm;
 
 namespace lgbm {
 void launch_predict(const PredNode* nodes, const PredTree* trees, const double* leaves,
-                    const int32_t* cat_bounds, const uint32_t* cat_words, const float* X,
-                    int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
+                    const int32_t* cat_bounds, const uint32_t* cat_words,
+                    const PredLinLeaf* lin_leaves, const int32_t* lin_features,
+                    const double* lin_coeffs, const float* X, int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
                     int32_t objective, double sigmoid, int32_t average_output, int32_t es_freq,
                     double es_margin, int32_t* es_iters, double* out, int32_t* leaf_out,
                     hipStream_t s, const KernelEvents* ev);
@@ -50,6 +51,9 @@ struct lgbm_hip_ctx {
   double* pm_leaves = nullptr;
   int32_t* pm_catb = nullptr;
   uint32_t* pm_catw = nullptr;
+  PredLinLeaf* pm_linl = nullptr;
+  int32_t* pm_linf = nullptr;
+  double* pm_linc = nullptr;
   float* pm_x = nullptr;  // host-input staging
   size_t pm_x_cap = 0;
   void* pm_out = nullptr;
@@ -904,6 +908,9 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->pm_leaves);
   F(c->pm_catb);
   F(c->pm_catw);
+  F(c->pm_linl);
+  F(c->pm_linf);
+  F(c->pm_linc);
   F(c->pm_x);
   F(c->pm_out);
   DevTree& T = c->tree;
@@ -1845,6 +1852,9 @@ int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int3
     if ((rc = upload_vec(c, &c->pm_leaves, m->leaf_values))) return rc;
     if ((rc = upload_vec(c, &c->pm_catb, m->cat_bounds))) return rc;
     if ((rc = upload_vec(c, &c->pm_catw, m->cat_words))) return rc;
+    if ((rc = upload_vec(c, &c->pm_linl, m->lin_leaves))) return rc;
+    if ((rc = upload_vec(c, &c->pm_linf, m->lin_features))) return rc;
+    if ((rc = upload_vec(c, &c->pm_linc, m->lin_coeffs))) return rc;
     c->pm_uid = m->uid;
   }
   return LGBM_HIP_OK;
@@ -1854,7 +1864,8 @@ int predict_run(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* d_x, int6
                 int32_t cols, int32_t it0, int32_t it1, int32_t kind, void* d_out,
                 int32_t es_freq = 0, double es_margin = 0.0, int32_t* d_iters = nullptr) {
   KernelEvents ke;
-  launch_predict(c->pm_nodes, c->pm_trees, c->pm_leaves, c->pm_catb, c->pm_catw, d_x, rows, cols,
+  launch_predict(c->pm_nodes, c->pm_trees, c->pm_leaves, c->pm_catb, c->pm_catw, c->pm_linl,
+                 c->pm_linf, c->pm_linc, d_x, rows, cols,
                  it0, it1, m->num_tree_per_iteration, kind, m->objective, m->sigmoid,
                  m->average_output ? 1 : 0, es_freq, es_margin, d_iters,
                  kind == LGBM_HIP_PREDICT_LEAF ? nullptr : (double*)d_out,

@@ -150,7 +150,16 @@ bool parse_tree(const std::map<std::string, std::string>& kv, int32_t max_featur
   if ((s = get("is_linear"))) {
     int32_t lin = 0;
     if (!parse_int(*s, &lin, "is_linear", err)) return false;
-    if (lin) return fail(err, "linear trees are not supported");
+    t->is_linear = lin != 0;
+  }
+  if (t->is_linear) {  // parse_linear_model (tree.rs:1341-1412), also for one-leaf trees
+    if (!(s = get("leaf_const"))) return fail(err, "linear tree model should contain leaf_const field");
+    if (!parse_f64s(*s, &t->leaf_const, "leaf_const", err)) return false;
+    if (!(s = get("num_features"))) return fail(err, "linear tree model should contain num_features field");
+    if (!parse_ints(*s, &t->leaf_nfeat, "num_features", err)) return false;
+    if ((s = get("leaf_features")) && !parse_ints(*s, &t->leaf_features, "leaf_features", err))
+      return false;
+    if ((s = get("leaf_coeff")) && !parse_f64s(*s, &t->leaf_coeff, "leaf_coeff", err)) return false;
   }
   if (!(s = get("leaf_value"))) return fail(err, "tree model should contain leaf_value field");
   if (!parse_f64s(*s, &t->leaf_value, "leaf_value", err)) return false;
@@ -236,6 +245,17 @@ void flatten_tree(lgbm_hip_model* m, const HostTree& t) {
   pt.leaf0 = (int32_t)m->leaf_values.size();
   pt.cat0 = (int32_t)m->cat_bounds.size();
   pt.num_leaves = t.num_leaves;
+  pt.lin0 = -1;
+  if (t.is_linear) {
+    pt.lin0 = (int32_t)m->lin_leaves.size();
+    int32_t off = (int32_t)m->lin_features.size();
+    for (int32_t l = 0; l < t.num_leaves; ++l) {
+      m->lin_leaves.push_back(PredLinLeaf{t.leaf_const[l], off, t.leaf_nfeat[l]});
+      off += t.leaf_nfeat[l];
+    }
+    m->lin_features.insert(m->lin_features.end(), t.leaf_features.begin(), t.leaf_features.end());
+    m->lin_coeffs.insert(m->lin_coeffs.end(), t.leaf_coeff.begin(), t.leaf_coeff.end());
+  }
   m->tree_index.push_back(pt);
   const int32_t word0 = (int32_t)m->cat_words.size();
   for (int32_t i = 0; i + 1 < t.num_leaves; ++i) {
@@ -302,7 +322,24 @@ std::string tree_to_text(const HostTree& t) {
     ints("cat_boundaries", t.cat_boundaries);
     put_list(&s, "cat_threshold", t.cat_threshold, [&](uint32_t x) { s += std::to_string(x); });
   }
-  s += "is_linear=0\n";
+  s += t.is_linear ? "is_linear=1\n" : "is_linear=0\n";
+  if (t.is_linear) {
+    // one "<value> " per term and one more space after each leaf's group (tree.rs:820-834)
+    g17("leaf_const", t.leaf_const);
+    ints("num_features", t.leaf_nfeat);
+    std::string lf = "leaf_features=", lc = "leaf_coeff=";
+    size_t k = 0;
+    for (const int32_t c : t.leaf_nfeat) {
+      for (int32_t j = 0; j < c; ++j, ++k) {
+        lf += std::to_string(t.leaf_features[k]) + ' ';
+        put_g(&lc, t.leaf_coeff[k], 17);
+        lc += ' ';
+      }
+      lf += ' ';
+      lc += ' ';
+    }
+    s += lf + "\n" + lc + "\n";
+  }
   s += "shrinkage=";
   put_g(&s, t.shrinkage, 6);
   s += "\n\n";
@@ -330,6 +367,22 @@ bool check_tree(const HostTree& t_, int32_t max_feature_idx, std::string* err) {
       return fail(err, "cat_threshold length");
   } else if (!t->cat_boundaries.empty() || !t->cat_threshold.empty()) {
     return fail(err, "categorical bitsets in a tree with num_cat=0");
+  }
+  if (t->is_linear) {
+    if ((int32_t)t->leaf_const.size() != t->num_leaves) return fail(err, "leaf_const length");
+    if ((int32_t)t->leaf_nfeat.size() != t->num_leaves) return fail(err, "num_features length");
+    int64_t total = 0;
+    for (const int32_t c : t->leaf_nfeat) {
+      if (c < 0) return fail(err, "num_features entry is negative");
+      total += c;
+    }
+    if ((int64_t)t->leaf_features.size() != total) return fail(err, "leaf_features length");
+    if ((int64_t)t->leaf_coeff.size() != total) return fail(err, "leaf_coeff length");
+    for (const int32_t f : t->leaf_features)
+      if (f < 0 || f > max_feature_idx) return fail(err, "leaf_features entry out of range");
+  } else if (!t->leaf_const.empty() || !t->leaf_nfeat.empty() || !t->leaf_features.empty() ||
+             !t->leaf_coeff.empty()) {
+    return fail(err, "linear leaves in a tree with is_linear=0");
   }
   if (ni == 0) return true;
   if ((int32_t)t->split_feature.size() != ni || (int32_t)t->threshold.size() != ni ||

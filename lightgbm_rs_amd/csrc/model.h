@@ -29,6 +29,14 @@ struct PredNode {
 // Per tree: where its nodes, leaf values and categorical bitset bounds start.
 struct PredTree {
   int32_t node0, leaf0, cat0, num_leaves;
+  int32_t lin0;  // first PredLinLeaf of a linear tree; -1 for constant leaves
+};
+
+// A linear tree's leaf (Tree::linear_leaf_output, tree.rs:301-316): the output is
+// `c + sum_j coeff[start + j] * x[feature[start + j]]` over `count` terms.
+struct PredLinLeaf {
+  double c;
+  int32_t start, count;
 };
 
 struct HostTree {
@@ -41,6 +49,10 @@ struct HostTree {
   std::vector<double> leaf_weight, internal_value, internal_weight;
   std::vector<int32_t> leaf_count, internal_count;
   double shrinkage = 1.0;
+  // linear leaves (tree.rs:69-90): leaf_const, num_features, flat leaf_features / leaf_coeff
+  bool is_linear = false;
+  std::vector<double> leaf_const, leaf_coeff;
+  std::vector<int32_t> leaf_nfeat, leaf_features;
 };
 
 struct lgbm_hip_model {
@@ -61,6 +73,9 @@ struct lgbm_hip_model {
   std::vector<double> leaf_values;
   std::vector<int32_t> cat_bounds;  // absolute offsets into cat_words
   std::vector<uint32_t> cat_words;
+  std::vector<PredLinLeaf> lin_leaves;
+  std::vector<int32_t> lin_features;
+  std::vector<double> lin_coeffs;
 };
 
 // Parses `text`; on failure returns false with `err` set (nothing is allocated).

@@ -20,6 +20,9 @@ struct PredModelDev {
   const double* leaves;
   const int32_t* cat_bounds;
   const uint32_t* cat_words;
+  const PredLinLeaf* lin_leaves;
+  const int32_t* lin_features;
+  const double* lin_coeffs;
 };
 
 // The node's fields arrive as values: selecting between members of a struct held by
@@ -65,6 +68,24 @@ __device__ __forceinline__ int32_t pred_leaf(const PredModelDev& M, int32_t t, c
     node = pred_next(thr, dtype, left, right, (double)x[feat], M, T.cat0);
   }
   return node < 0 ? ~node : 0;
+}
+
+// Tree::predict (tree.rs:279-316): the leaf's value, or for a linear tree the leaf's
+// `leaf_const + sum coeff * x[feature]` in term order (f64, no fused multiply-add),
+// falling back to the leaf's value when any of its features is NaN.
+__device__ __forceinline__ double pred_tree(const PredModelDev& M, int32_t t, const float* x) {
+  const int32_t leaf = pred_leaf(M, t, x);
+  const PredTree T = M.trees[t];
+  const double lv = M.leaves[T.leaf0 + leaf];
+  if (T.lin0 < 0) return lv;
+  const PredLinLeaf L = M.lin_leaves[T.lin0 + leaf];
+  double v = L.c;
+  for (int32_t j = 0; j < L.count; ++j) {
+    const double xv = (double)x[M.lin_features[L.start + j]];
+    if (isnan(xv)) return lv;
+    v += M.lin_coeffs[L.start + j] * xv;
+  }
+  return v;
 }
 
 __device__ __forceinline__ double pred_sigmoid(double x, double s) { return 1.0 / (1.0 + exp(-s * x)); }
@@ -119,7 +140,7 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
     for (int32_t i = it0; i < it1; ++i) {
       for (int32_t k = 0; k < ntpi; ++k) {
         const int32_t t = i * ntpi + k;
-        o[k] += M.leaves[M.trees[t].leaf0 + pred_leaf(M, t, x)];
+        o[k] += pred_tree(M, t, x);
       }
       ++evaluated;
       if (++counter == es_freq) {
@@ -150,7 +171,7 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
     double acc = 0.0;
     for (int32_t i = it0; i < it1; ++i) {
       const int32_t t = i * ntpi + k;
-      acc += M.leaves[M.trees[t].leaf0 + pred_leaf(M, t, x)];
+      acc += pred_tree(M, t, x);
     }
     o[k] = acc;
   }
@@ -195,13 +216,15 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
 }
 
 void launch_predict(const PredNode* nodes, const PredTree* trees, const double* leaves,
-                    const int32_t* cat_bounds, const uint32_t* cat_words, const float* X,
-                    int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
+                    const int32_t* cat_bounds, const uint32_t* cat_words,
+                    const PredLinLeaf* lin_leaves, const int32_t* lin_features,
+                    const double* lin_coeffs, const float* X, int64_t rows, int32_t cols, int32_t it0, int32_t it1, int32_t ntpi, int32_t kind,
                     int32_t objective, double sigmoid, int32_t average_output, int32_t es_freq,
                     double es_margin, int32_t* es_iters, double* out, int32_t* leaf_out,
                     hipStream_t s, const KernelEvents* ev) {
   if (rows <= 0) return;
-  const PredModelDev M{nodes, trees, leaves, cat_bounds, cat_words};
+  const PredModelDev M{nodes,      trees,        leaves,    cat_bounds,
+                       cat_words,  lin_leaves,   lin_features, lin_coeffs};
   const int64_t blocks = (rows + 255) / 256;
   if (cols <= PRED_STAGE_COLS)
     KLAUNCH(ev, k_predict<true>, dim3((unsigned)blocks), dim3(256),

@@ -6,6 +6,7 @@ crates/lgbm-model/src/:
                         max_feature_idx, objective) and the Tree= blocks
   tree.rs:846-1000      Tree::parse (per-tree key=value fields)
   tree.rs:160-340       NumericalDecision / CategoricalDecision / GetLeaf
+  tree.rs:279-316       linear leaves (leaf_const + sum coeff * x, NaN -> leaf_value)
   ensemble.rs:75-102    init_predict + predict_raw (f64 accumulation per class,
                         iteration order)
   objective.rs:125-340  objective= parsing and ConvertOutput
@@ -48,8 +49,39 @@ def parse_tree(lines):
             t["cat_boundaries"] = _i_list(kv["cat_boundaries"])
             t["cat_threshold"] = _i_list(kv["cat_threshold"], np.uint64)
     if int(kv.get("is_linear", "0")) != 0:
-        raise ValueError("linear trees are not supported")
+        # parse_linear_model (tree.rs:1341-1412): per-leaf groups of the flat streams
+        const, counts = _f64_list(kv["leaf_const"]), _i_list(kv["num_features"])
+        feats = _i_list(kv.get("leaf_features", ""))
+        coeff = _f64_list(kv.get("leaf_coeff", ""))
+        if len(const) != t["num_leaves"] or len(counts) != t["num_leaves"]:
+            raise ValueError("linear leaf arrays != num_leaves")
+        if (counts < 0).any() or len(feats) != counts.sum() or len(coeff) != counts.sum():
+            raise ValueError("leaf_features / leaf_coeff length != sum(num_features)")
+        off = np.concatenate([[0], np.cumsum(counts)])
+        t["linear"] = [(const[l], feats[off[l]:off[l + 1]], coeff[off[l]:off[l + 1]])
+                       for l in range(t["num_leaves"])]
     return t
+
+
+def tree_output(t, X64):
+    """Tree::predict (tree.rs:279-316): the leaf's value; for a linear tree the leaf's
+    `leaf_const + sum coeff * x[feature]` added term by term, or the leaf's value when
+    any of those features is NaN."""
+    leaf = leaf_of(t, X64)
+    out = t["leaf_value"][leaf]
+    if "linear" not in t:
+        return out
+    out = out.copy()
+    for l, (c, feats, coeff) in enumerate(t["linear"]):
+        rows = np.nonzero(leaf == l)[0]
+        v = np.full(len(rows), c)
+        nan = np.zeros(len(rows), dtype=bool)
+        for f, w in zip(feats, coeff):
+            xv = X64[rows, f]
+            nan |= np.isnan(xv)
+            v = v + w * xv
+        out[rows] = np.where(nan, t["leaf_value"][l], v)
+    return out
 
 
 def parse_model(text):
@@ -159,7 +191,7 @@ def predict(model, X, start_iteration=0, num_iteration=-1, kind="raw"):
     for i in range(start, start + num):
         for k in range(ntpi):
             t = trees[i * ntpi + k]
-            raw[:, k] = raw[:, k] + t["leaf_value"][leaf_of(t, X64)]
+            raw[:, k] = raw[:, k] + tree_output(t, X64)
     if kind == "raw":
         return raw
     if model["objective"] is None:
@@ -224,8 +256,8 @@ def predict_early_stop(model, X, freq, margin, start_iteration=0, num_iteration=
     ntpi = model["num_tree_per_iteration"]
     start, num = _range(model, start_iteration, num_iteration)
     trees = model["trees"]
-    leaves = [[leaf_of(trees[i * ntpi + k], X64) for k in range(ntpi)]
-              for i in range(start, start + num)]
+    vals = [[tree_output(trees[i * ntpi + k], X64) for k in range(ntpi)]
+            for i in range(start, start + num)]
     raw = np.zeros((len(X64), ntpi))
     iters = np.zeros(len(X64), np.int32)
     for r in range(len(X64)):
@@ -234,8 +266,7 @@ def predict_early_stop(model, X, freq, margin, start_iteration=0, num_iteration=
         n = 0
         for ii in range(num):
             for k in range(ntpi):
-                t = trees[(start + ii) * ntpi + k]
-                out[k] += t["leaf_value"][leaves[ii][k][r]]
+                out[k] += vals[ii][k][r]
             n += 1
             counter += 1
             if freq > 0 and counter == freq:
