@@ -448,6 +448,7 @@ int lgbm_hip_model_to_text(const lgbm_hip_model* model, char* buf, size_t size, 
 #define LGBM_HIP_PREDICT_RAW 0
 #define LGBM_HIP_PREDICT_TRANSFORMED 1
 #define LGBM_HIP_PREDICT_LEAF 2
+#define LGBM_HIP_PREDICT_CONTRIB 3
 /* Batch prediction of a dense row-major f32 matrix [num_rows][num_cols]
  * (num_cols >= max_feature_idx + 1), over iterations [start_iteration,
  * start_iteration + num_iteration) clamped as GbdtModel::init_predict
@@ -455,8 +456,12 @@ int lgbm_hip_model_to_text(const lgbm_hip_model* model, char* buf, size_t size, 
  * predict_mat and predict_leaf_index_mat (crates/lgbm-model/src/predict.rs:75-131,
  * 378-485).  kind RAW / TRANSFORMED: out is double[num_rows * num_tree_per_iteration]
  * (the f64 scores the reference casts to f32 at its own boundary); LEAF: out is
- * int32[num_rows * trees in range], row-major, trees in model order.  data and out
- * are host pointers (copied through the context's device buffers). */
+ * int32[num_rows * trees in range], row-major, trees in model order; CONTRIB
+ * (predict_contrib_mat, predict.rs:607-697, TreeSHAP of tree.rs:336-583): out is
+ * double[num_rows * num_tree_per_iteration * (max_feature_idx + 2)], per row and
+ * class the feature contributions then the expected-value base (refused for
+ * linear-tree models, as predict.rs:626-635).  data and out are host pointers
+ * (copied through the context's device buffers). */
 int lgbm_hip_predict(lgbm_hip_ctx* ctx, const lgbm_hip_model* model, const float* data,
                      int64_t num_rows, int32_t num_cols, int32_t start_iteration,
                      int32_t num_iteration, int32_t kind, void* out);

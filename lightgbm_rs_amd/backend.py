@@ -255,7 +255,7 @@ def binary_boost_from_score(labels, sigmoid=1.0):
     return out.value
 
 
-PREDICT_KINDS = {"raw": 0, "transformed": 1, "leaf": 2}
+PREDICT_KINDS = {"raw": 0, "transformed": 1, "leaf": 2, "contrib": 3}
 
 
 class Model:
@@ -337,14 +337,21 @@ def _predict_shape(model, kind, rows, start_iteration, num_iteration):
     total = model.num_iterations
     start = min(max(start_iteration, 0), total)
     num = min(num_iteration, total - start) if num_iteration > 0 else total - start
-    width = num * model.num_tree_per_iteration if kind == "leaf" else model.num_tree_per_iteration
+    if kind == "leaf":
+        width = num * model.num_tree_per_iteration
+    elif kind == "contrib":
+        width = model.num_tree_per_iteration * (model.max_feature_idx + 2)
+    else:
+        width = model.num_tree_per_iteration
     return (rows, width)
 
 
 def _predict(self, model, X, kind="raw", start_iteration=0, num_iteration=-1):
-    """predict_raw_mat_range / predict_mat / predict_leaf_index_mat
-    (crates/lgbm-model/src/predict.rs:75-131, 378-485) on the device: X is a dense
-    [rows, cols] float32 matrix; returns float64 [rows, outputs] or int32 [rows, trees]."""
+    """predict_raw_mat_range / predict_mat / predict_leaf_index_mat / predict_contrib_mat
+    (crates/lgbm-model/src/predict.rs:75-131, 378-485, 675-697) on the device: X is a
+    dense [rows, cols] float32 matrix; returns float64 [rows, outputs], int32
+    [rows, trees] ("leaf") or float64 [rows, classes * (max_feature_idx + 2)]
+    ("contrib": per class the feature contributions then the expected value)."""
     X = np.ascontiguousarray(X, dtype=np.float32)
     rows, cols = X.shape
     shape = _predict_shape(model, kind, rows, start_iteration, num_iteration)

@@ -28,6 +28,13 @@ void launch_predict(const PredNode* nodes, const PredTree* trees, const double* 
                     int32_t objective, double sigmoid, int32_t average_output, int32_t es_freq,
                     double es_margin, int32_t* es_iters, double* out, int32_t* leaf_out,
                     hipStream_t s, const KernelEvents* ev);
+int64_t shap_bytes_per_row(int32_t depth);
+void launch_contrib(const PredNode* nodes, const PredTree* trees, const double* leaves,
+                    const int32_t* cat_bounds, const uint32_t* cat_words, const double* node_cover,
+                    const double* leaf_cover, const double* expected, const float* X, int64_t r0,
+                    int64_t n, int64_t rows, int32_t cols, int32_t nf, int32_t it0, int32_t it1,
+                    int32_t ntpi, int32_t depth, void* ws, double* out, hipStream_t s,
+                    const KernelEvents* ev);
 }
 
 namespace {
@@ -54,6 +61,11 @@ struct lgbm_hip_ctx {
   PredLinLeaf* pm_linl = nullptr;
   int32_t* pm_linf = nullptr;
   double* pm_linc = nullptr;
+  double* pm_ncov = nullptr;  // TreeSHAP covers and expected values
+  double* pm_lcov = nullptr;
+  double* pm_expv = nullptr;
+  char* pm_shap = nullptr;  // TreeSHAP path workspace
+  size_t pm_shap_cap = 0;
   float* pm_x = nullptr;  // host-input staging
   size_t pm_x_cap = 0;
   void* pm_out = nullptr;
@@ -911,6 +923,10 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->pm_linl);
   F(c->pm_linf);
   F(c->pm_linc);
+  F(c->pm_ncov);
+  F(c->pm_lcov);
+  F(c->pm_expv);
+  F(c->pm_shap);
   F(c->pm_x);
   F(c->pm_out);
   DevTree& T = c->tree;
@@ -1826,8 +1842,11 @@ int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int3
     return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH,
                    "input has " + std::to_string(cols) + " columns, model needs max_feature_idx+1 = " +
                        std::to_string(m->max_feature_idx + 1));
-  if (kind < LGBM_HIP_PREDICT_RAW || kind > LGBM_HIP_PREDICT_LEAF)
+  if (kind < LGBM_HIP_PREDICT_RAW || kind > LGBM_HIP_PREDICT_CONTRIB)
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "unknown prediction kind");
+  if (kind == LGBM_HIP_PREDICT_CONTRIB && m->any_linear)  // check_no_linear_trees (predict.rs:626-635)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT,
+                   "feature contributions are not supported for linear_tree models");
   if (kind == LGBM_HIP_PREDICT_TRANSFORMED) {
     // resolve_objective (predict.rs:305-322)
     if (!m->have_objective)
@@ -1845,7 +1864,9 @@ int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int3
   *it0 = start;
   *it1 = start + num;
   *width = kind == LGBM_HIP_PREDICT_LEAF ? (int64_t)num * m->num_tree_per_iteration
-                                         : (int64_t)m->num_tree_per_iteration;
+           : kind == LGBM_HIP_PREDICT_CONTRIB
+               ? (int64_t)m->num_tree_per_iteration * (m->max_feature_idx + 2)
+               : (int64_t)m->num_tree_per_iteration;
   if (c->pm_uid != m->uid) {
     if ((rc = upload_vec(c, &c->pm_nodes, m->nodes))) return rc;
     if ((rc = upload_vec(c, &c->pm_trees, m->tree_index))) return rc;
@@ -1855,6 +1876,9 @@ int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int3
     if ((rc = upload_vec(c, &c->pm_linl, m->lin_leaves))) return rc;
     if ((rc = upload_vec(c, &c->pm_linf, m->lin_features))) return rc;
     if ((rc = upload_vec(c, &c->pm_linc, m->lin_coeffs))) return rc;
+    if ((rc = upload_vec(c, &c->pm_ncov, m->node_cover))) return rc;
+    if ((rc = upload_vec(c, &c->pm_lcov, m->leaf_cover))) return rc;
+    if ((rc = upload_vec(c, &c->pm_expv, m->tree_expected))) return rc;
     c->pm_uid = m->uid;
   }
   return LGBM_HIP_OK;
@@ -1863,6 +1887,31 @@ int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int3
 int predict_run(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* d_x, int64_t rows,
                 int32_t cols, int32_t it0, int32_t it1, int32_t kind, void* d_out,
                 int32_t es_freq = 0, double es_margin = 0.0, int32_t* d_iters = nullptr) {
+  if (kind == LGBM_HIP_PREDICT_CONTRIB) {
+    // the deepest tree of the range sizes each row's path buffer; rows go in chunks
+    // whose workspace stays within 256 MiB
+    int32_t depth = 0;
+    for (int64_t t = (int64_t)it0 * m->num_tree_per_iteration;
+         t < (int64_t)it1 * m->num_tree_per_iteration; ++t)
+      depth = std::max(depth, m->tree_depth[t]);
+    const int64_t per_row = shap_bytes_per_row(depth);
+    int64_t chunk = std::max<int64_t>(256, ((int64_t)256 << 20) / per_row / 256 * 256);
+    chunk = std::min(chunk, rows);
+    const size_t need = (size_t)(per_row * chunk);
+    if (c->pm_shap_cap < need) {
+      int rc = dalloc(c, &c->pm_shap, need);
+      if (rc) return rc;
+      c->pm_shap_cap = need;
+    }
+    for (int64_t r0 = 0; r0 < rows; r0 += chunk)
+      launch_contrib(c->pm_nodes, c->pm_trees, c->pm_leaves, c->pm_catb, c->pm_catw, c->pm_ncov,
+                     c->pm_lcov, c->pm_expv, d_x, r0, std::min(chunk, rows - r0), rows, cols,
+                     m->max_feature_idx + 1, it0, it1, m->num_tree_per_iteration, depth,
+                     c->pm_shap, (double*)d_out, c->stream, nullptr);
+    HIPCHK(c, hipGetLastError());
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return LGBM_HIP_OK;
+  }
   KernelEvents ke;
   launch_predict(c->pm_nodes, c->pm_trees, c->pm_leaves, c->pm_catb, c->pm_catw, c->pm_linl,
                  c->pm_linf, c->pm_linc, d_x, rows, cols,

@@ -12,11 +12,11 @@
 // within the tree's bitsets; linear trees are rejected.
 #include "model.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cerrno>
 #include <cmath>
 #include <cstdlib>
-#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -257,6 +257,31 @@ void flatten_tree(lgbm_hip_model* m, const HostTree& t) {
     m->lin_coeffs.insert(m->lin_coeffs.end(), t.leaf_coeff.begin(), t.leaf_coeff.end());
   }
   m->tree_index.push_back(pt);
+  m->any_linear = m->any_linear || t.is_linear;
+  // Tree::expected_value (tree.rs:351-361) and the depth of Tree::max_depth (tree.rs:367-386)
+  double ev = t.leaf_value[0];
+  int32_t depth = 0;
+  if (t.num_leaves > 1) {
+    const double total = (double)t.internal_count[0];
+    ev = 0.0;
+    for (int32_t i = 0; i < t.num_leaves; ++i)
+      ev += ((double)t.leaf_count[i] / total) * t.leaf_value[i];
+    std::vector<std::pair<int32_t, int32_t>> stack{{0, 0}};
+    while (!stack.empty()) {
+      const auto [n, d] = stack.back();
+      stack.pop_back();
+      if (n < 0) {
+        depth = std::max(depth, d);
+      } else {
+        stack.push_back({t.left_child[n], d + 1});
+        stack.push_back({t.right_child[n], d + 1});
+      }
+    }
+    for (int32_t i = 0; i + 1 < t.num_leaves; ++i) m->node_cover.push_back((double)t.internal_count[i]);
+  }
+  for (int32_t i = 0; i < t.num_leaves; ++i) m->leaf_cover.push_back((double)t.leaf_count[i]);
+  m->tree_expected.push_back(ev);
+  m->tree_depth.push_back(depth);
   const int32_t word0 = (int32_t)m->cat_words.size();
   for (int32_t i = 0; i + 1 < t.num_leaves; ++i) {
     PredNode n;

@@ -73,6 +73,11 @@ struct lgbm_hip_model {
   std::vector<double> leaf_values;
   std::vector<int32_t> cat_bounds;  // absolute offsets into cat_words
   std::vector<uint32_t> cat_words;
+  // TreeSHAP inputs (tree.rs:336-400): covers per node and leaf (data counts as f64),
+  // each tree's cover-weighted leaf average and maximum leaf depth
+  std::vector<double> node_cover, leaf_cover, tree_expected;
+  std::vector<int32_t> tree_depth;
+  bool any_linear = false;
   std::vector<PredLinLeaf> lin_leaves;
   std::vector<int32_t> lin_features;
   std::vector<double> lin_coeffs;

@@ -215,6 +215,228 @@ __global__ __launch_bounds__(256) void k_predict(PredModelDev M, const float* __
   }
 }
 
+// ---- feature contributions (TreeSHAP) ------------------------------------------------
+// Lundberg et al., arXiv:1706.06060, Algorithm 2, as the reference computes it
+// (Tree::predict_contrib / extend_path / unwind_path / unwound_path_sum / tree_shap,
+// tree.rs:400-583): one thread per row, the recursion turned into a loop over the hot
+// child with a stack of pending cold calls (popped in the recursion's order, so every
+// f64 update happens in the same sequence), and every product and quotient in the
+// reference's association (this file is built without fused multiply-add).
+//
+// Each thread's unique paths live in one flat buffer of (D+1)(D+2)/2 elements for the
+// deepest tree D, as in the reference: a call's frame starts `d` elements after its
+// parent's and copies the parent's first `d` elements; the cold call reads its parent's
+// frame after the hot subtree returns, which wrote only past it.  The buffers are
+// workspace memory laid out element-major (element k of thread i at k * stride + i), so
+// a wave's accesses to one element are contiguous.
+struct ShapWork {
+  int32_t* feat;
+  double* zero;
+  double* one;
+  double* pw;
+  int32_t* s_node;  // pending cold calls: node, parent frame base, depth, split feature
+  int32_t* s_base;
+  int32_t* s_depth;
+  int32_t* s_feat;
+  double* s_zero;
+  int64_t stride;  // threads of the launch
+};
+
+struct ShapModelDev {
+  const double* node_cover;
+  const double* leaf_cover;
+  const double* expected;
+};
+
+__device__ __forceinline__ void shap_extend(const ShapWork& W, int64_t i0, int32_t b, int32_t d,
+                                            double zf, double of, int32_t feat) {
+  const int64_t e = (int64_t)(b + d) * W.stride + i0;
+  W.feat[e] = feat;
+  W.zero[e] = zf;
+  W.one[e] = of;
+  W.pw[e] = d == 0 ? 1.0 : 0.0;
+  const double dd = (double)d;
+  for (int32_t i = d - 1; i >= 0; --i) {
+    const int64_t ei = (int64_t)(b + i) * W.stride + i0;
+    const double prev = W.pw[ei];
+    W.pw[ei + W.stride] += of * prev * ((double)i + 1.0) / (dd + 1.0);
+    W.pw[ei] = zf * prev * (dd - (double)i) / (dd + 1.0);
+  }
+}
+
+__device__ __forceinline__ void shap_unwind(const ShapWork& W, int64_t i0, int32_t b, int32_t d,
+                                            int32_t k) {
+  const int64_t ek = (int64_t)(b + k) * W.stride + i0;
+  const double of = W.one[ek], zf = W.zero[ek];
+  double next = W.pw[(int64_t)(b + d) * W.stride + i0];
+  const double dd = (double)d;
+  for (int32_t i = d - 1; i >= 0; --i) {
+    const int64_t ei = (int64_t)(b + i) * W.stride + i0;
+    if (of != 0.0) {
+      const double tmp = W.pw[ei];
+      W.pw[ei] = next * (dd + 1.0) / (((double)i + 1.0) * of);
+      next = tmp - W.pw[ei] * zf * (dd - (double)i) / (dd + 1.0);
+    } else {
+      W.pw[ei] = (W.pw[ei] * (dd + 1.0)) / (zf * (dd - (double)i));
+    }
+  }
+  for (int32_t i = k; i < d; ++i) {
+    const int64_t ei = (int64_t)(b + i) * W.stride + i0;
+    W.feat[ei] = W.feat[ei + W.stride];
+    W.zero[ei] = W.zero[ei + W.stride];
+    W.one[ei] = W.one[ei + W.stride];
+  }
+}
+
+__device__ __forceinline__ double shap_unwound_sum(const ShapWork& W, int64_t i0, int32_t b,
+                                                   int32_t d, int32_t k) {
+  const int64_t ek = (int64_t)(b + k) * W.stride + i0;
+  const double of = W.one[ek], zf = W.zero[ek];
+  double next = W.pw[(int64_t)(b + d) * W.stride + i0];
+  double total = 0.0;
+  const double dd = (double)d;
+  for (int32_t i = d - 1; i >= 0; --i) {
+    const double pwi = W.pw[(int64_t)(b + i) * W.stride + i0];
+    if (of != 0.0) {
+      const double tmp = next * (dd + 1.0) / (((double)i + 1.0) * of);
+      total += tmp;
+      next = pwi - tmp * zf * ((dd - (double)i) / (dd + 1.0));
+    } else {
+      total += (pwi / zf) / ((dd - (double)i) / (dd + 1.0));
+    }
+  }
+  return total;
+}
+
+__global__ __launch_bounds__(256) void k_contrib(PredModelDev M, ShapModelDev S, ShapWork W,
+                                                 const float* __restrict__ X, int64_t r0,
+                                                 int64_t rows, int32_t cols, int32_t nf,
+                                                 int32_t it0, int32_t it1, int32_t ntpi,
+                                                 double* __restrict__ out) {
+  const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t r = r0 + i0;
+  if (i0 >= W.stride || r >= rows) return;
+  const float* x = X + r * cols;
+  const int32_t block = nf + 1;
+  double* o = out + r * (int64_t)ntpi * block;
+  for (int32_t j = 0; j < ntpi * block; ++j) o[j] = 0.0;
+  for (int32_t it = it0; it < it1; ++it) {
+    for (int32_t k = 0; k < ntpi; ++k) {
+      const int32_t t = it * ntpi + k;
+      double* phi = o + k * block;
+      phi[nf] += S.expected[t];
+      const PredTree T = M.trees[t];
+      if (T.num_leaves <= 1) continue;
+      int32_t node = 0, pb = 0, d = 0, pf = -1, sp = 0;
+      double pz = 1.0, po = 1.0;
+      for (;;) {
+        const int32_t b = pb + d;
+        for (int32_t i = 0; i < d; ++i) {
+          const int64_t src = (int64_t)(pb + i) * W.stride + i0, dst = (int64_t)(b + i) * W.stride + i0;
+          W.feat[dst] = W.feat[src];
+          W.zero[dst] = W.zero[src];
+          W.one[dst] = W.one[src];
+          W.pw[dst] = W.pw[src];
+        }
+        shap_extend(W, i0, b, d, pz, po, pf);
+        if (node < 0) {
+          const double lv = M.leaves[T.leaf0 + ~node];
+          for (int32_t i = 1; i <= d; ++i) {
+            const double w = shap_unwound_sum(W, i0, b, d, i);
+            const int64_t ei = (int64_t)(b + i) * W.stride + i0;
+            phi[W.feat[ei]] += w * (W.one[ei] - W.zero[ei]) * lv;
+          }
+          if (sp == 0) break;
+          --sp;
+          const int64_t es = (int64_t)sp * W.stride + i0;
+          node = W.s_node[es];
+          pb = W.s_base[es];
+          d = W.s_depth[es];
+          pf = W.s_feat[es];
+          pz = W.s_zero[es];
+          po = 0.0;
+          continue;
+        }
+        const PredNode* nd = M.nodes + T.node0 + node;
+        const double thr = nd->threshold;
+        const int32_t f = nd->feature, left = nd->left, right = nd->right, dtype = nd->dtype;
+        const int32_t hot = pred_next(thr, dtype, left, right, (double)x[f], M, T.cat0);
+        const int32_t cold = hot == left ? right : left;
+        const double w = S.node_cover[T.node0 + node];
+        const double hc = hot >= 0 ? S.node_cover[T.node0 + hot] : S.leaf_cover[T.leaf0 + ~hot];
+        const double cc = cold >= 0 ? S.node_cover[T.node0 + cold] : S.leaf_cover[T.leaf0 + ~cold];
+        const double hz = hc / w, cz = cc / w;
+        double iz = 1.0, io = 1.0;
+        int32_t pi = 0;
+        while (pi <= d && W.feat[(int64_t)(b + pi) * W.stride + i0] != f) ++pi;
+        int32_t nd1 = d;
+        if (pi != d + 1) {
+          const int64_t ep = (int64_t)(b + pi) * W.stride + i0;
+          iz = W.zero[ep];
+          io = W.one[ep];
+          shap_unwind(W, i0, b, d, pi);
+          nd1 -= 1;
+        }
+        const int64_t es = (int64_t)sp * W.stride + i0;
+        W.s_node[es] = cold;
+        W.s_base[es] = b;
+        W.s_depth[es] = nd1 + 1;
+        W.s_feat[es] = f;
+        W.s_zero[es] = cz * iz;
+        ++sp;
+        node = hot;
+        pb = b;
+        d = nd1 + 1;
+        pz = hz * iz;
+        po = io;
+        pf = f;
+      }
+    }
+  }
+}
+
+// Path elements and stack entries one thread needs for trees of depth at most `depth`.
+int64_t shap_path_elems(int32_t depth) { return (int64_t)(depth + 1) * (depth + 2) / 2; }
+int64_t shap_bytes_per_row(int32_t depth) {
+  return shap_path_elems(depth) * (4 + 8 + 8 + 8) + (int64_t)(depth + 1) * (4 * 4 + 8);
+}
+
+// Runs TreeSHAP for rows [r0, r0 + n) with `ws` holding shap_bytes_per_row(depth) * n
+// bytes (n a multiple of 256 or the tail of the rows).
+void launch_contrib(const PredNode* nodes, const PredTree* trees, const double* leaves,
+                    const int32_t* cat_bounds, const uint32_t* cat_words, const double* node_cover,
+                    const double* leaf_cover, const double* expected, const float* X, int64_t r0,
+                    int64_t n, int64_t rows, int32_t cols, int32_t nf, int32_t it0, int32_t it1,
+                    int32_t ntpi, int32_t depth, void* ws, double* out, hipStream_t s,
+                    const KernelEvents* ev) {
+  if (n <= 0) return;
+  const PredModelDev M{nodes, trees, leaves, cat_bounds, cat_words, nullptr, nullptr, nullptr};
+  const ShapModelDev S{node_cover, leaf_cover, expected};
+  const int64_t pe = shap_path_elems(depth), se = depth + 1;
+  char* p = (char*)ws;
+  ShapWork W;
+  W.stride = n;
+  W.pw = (double*)p;
+  p += pe * n * 8;
+  W.zero = (double*)p;
+  p += pe * n * 8;
+  W.one = (double*)p;
+  p += pe * n * 8;
+  W.s_zero = (double*)p;
+  p += se * n * 8;
+  W.feat = (int32_t*)p;
+  p += pe * n * 4;
+  W.s_node = (int32_t*)p;
+  p += se * n * 4;
+  W.s_base = (int32_t*)p;
+  p += se * n * 4;
+  W.s_depth = (int32_t*)p;
+  p += se * n * 4;
+  W.s_feat = (int32_t*)p;
+  KLAUNCH(ev, k_contrib, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, S, W, X, r0, rows,
+          cols, nf, it0, it1, ntpi, out);
+}
+
 void launch_predict(const PredNode* nodes, const PredTree* trees, const double* leaves,
                     const int32_t* cat_bounds, const uint32_t* cat_words,
                     const PredLinLeaf* lin_leaves, const int32_t* lin_features,

@@ -7,6 +7,8 @@ crates/lgbm-model/src/:
   tree.rs:846-1000      Tree::parse (per-tree key=value fields)
   tree.rs:160-340       NumericalDecision / CategoricalDecision / GetLeaf
   tree.rs:279-316       linear leaves (leaf_const + sum coeff * x, NaN -> leaf_value)
+  tree.rs:336-583       ExpectedValue and TreeSHAP (feature contributions),
+                        predict.rs:607-697 their per-class layout
   ensemble.rs:75-102    init_predict + predict_raw (f64 accumulation per class,
                         iteration order)
   objective.rs:125-340  objective= parsing and ConvertOutput
@@ -48,6 +50,11 @@ def parse_tree(lines):
         if t["num_cat"] > 0:
             t["cat_boundaries"] = _i_list(kv["cat_boundaries"])
             t["cat_threshold"] = _i_list(kv["cat_threshold"], np.uint64)
+    # data counts (TreeSHAP covers); the reference's parser defaults them to 0
+    t["leaf_count"] = _i_list(kv.get("leaf_count", " ".join(["0"] * t["num_leaves"])))
+    if t["num_leaves"] > 1:
+        t["internal_count"] = _i_list(kv.get("internal_count",
+                                             " ".join(["0"] * (t["num_leaves"] - 1))))
     if int(kv.get("is_linear", "0")) != 0:
         # parse_linear_model (tree.rs:1341-1412): per-leaf groups of the flat streams
         const, counts = _f64_list(kv["leaf_const"]), _i_list(kv["num_features"])
@@ -276,3 +283,132 @@ def predict_early_stop(model, X, freq, margin, start_iteration=0, num_iteration=
         raw[r] = out
         iters[r] = n
     return raw, iters
+
+
+# ---- TreeSHAP (feature contributions) ---------------------------------------------
+# Lundberg et al., "Consistent Individualized Feature Attribution for Tree Ensembles"
+# (arXiv:1706.06060), Algorithm 2, in the form the reference uses (tree.rs:336-583):
+# covers are the data counts, each recursion frame copies its parent's unique path
+# forward in one flat buffer, and every product / quotient keeps the association the
+# reference writes, so the f64 results agree bit for bit.
+
+def _count(t, node):
+    return float(t["internal_count"][node]) if node >= 0 else float(t["leaf_count"][~node])
+
+
+def expected_value(t):
+    """Tree::expected_value (tree.rs:351-361): the cover-weighted leaf average."""
+    if t["num_leaves"] == 1:
+        return float(t["leaf_value"][0])
+    total = float(t["internal_count"][0])
+    e = 0.0
+    for i in range(t["num_leaves"]):
+        e += (float(t["leaf_count"][i]) / total) * float(t["leaf_value"][i])
+    return e
+
+
+def _extend(path, b, d, zf, of, feat):
+    """ExtendPath (tree.rs:413-433) on the frame starting at path[b]."""
+    path[b + d] = [feat, zf, of, 1.0 if d == 0 else 0.0]
+    for i in range(d - 1, -1, -1):
+        prev = path[b + i][3]
+        path[b + i + 1][3] += of * prev * (i + 1.0) / (d + 1.0)
+        path[b + i][3] = zf * prev * (d - i) / (d + 1.0)
+
+
+def _unwind(path, b, d, k):
+    """UnwindPath (tree.rs:435-460)."""
+    of, zf = path[b + k][2], path[b + k][1]
+    nxt = path[b + d][3]
+    for i in range(d - 1, -1, -1):
+        if of != 0.0:
+            tmp = path[b + i][3]
+            path[b + i][3] = nxt * (d + 1.0) / ((i + 1.0) * of)
+            nxt = tmp - path[b + i][3] * zf * (d - i) / (d + 1.0)
+        else:
+            path[b + i][3] = (path[b + i][3] * (d + 1.0)) / (zf * (d - i))
+    for i in range(k, d):
+        path[b + i][0:3] = path[b + i + 1][0:3]
+
+
+def _unwound_sum(path, b, d, k):
+    """UnwoundPathSum (tree.rs:462-485)."""
+    of, zf = path[b + k][2], path[b + k][1]
+    nxt = path[b + d][3]
+    total = 0.0
+    for i in range(d - 1, -1, -1):
+        if of != 0.0:
+            tmp = nxt * (d + 1.0) / ((i + 1.0) * of)
+            total += tmp
+            nxt = path[b + i][3] - tmp * zf * ((d - i) / (d + 1.0))
+        else:
+            total += (path[b + i][3] / zf) / ((d - i) / (d + 1.0))
+    return total
+
+
+def _shap(t, x, phi, node, d, path, b, pz, po, pf):
+    """TreeSHAP (tree.rs:487-583); the frame of this call starts at path[b + d]."""
+    for i in range(d):
+        path[b + d + i] = list(path[b + i])
+    b += d
+    _extend(path, b, d, pz, po, pf)
+    if node < 0:
+        lv = float(t["leaf_value"][~node])
+        for i in range(1, d + 1):
+            w = _unwound_sum(path, b, d, i)
+            el = path[b + i]
+            phi[el[0]] += w * (el[2] - el[1]) * lv
+        return
+    f = int(t["split_feature"][node])
+    hot = int(_decide(t, np.array([node]), np.array([x[f]], dtype=np.float64))[0])
+    cold = int(t["right_child"][node]) if hot == t["left_child"][node] else int(t["left_child"][node])
+    w = _count(t, node)
+    hz, cz = _count(t, hot) / w, _count(t, cold) / w
+    iz, io = 1.0, 1.0
+    k = 0
+    while k <= d and path[b + k][0] != f:
+        k += 1
+    nd = d
+    if k != d + 1:
+        iz, io = path[b + k][1], path[b + k][2]
+        _unwind(path, b, d, k)
+        nd -= 1
+    _shap(t, x, phi, hot, nd + 1, path, b, hz * iz, io, f)
+    _shap(t, x, phi, cold, nd + 1, path, b, cz * iz, 0.0, f)
+
+
+def _max_depth(t):
+    if t["num_leaves"] <= 1:
+        return 0
+    best, stack = 0, [(0, 0)]
+    while stack:
+        n, dep = stack.pop()
+        if n < 0:
+            best = max(best, dep)
+        else:
+            stack += [(int(t["left_child"][n]), dep + 1), (int(t["right_child"][n]), dep + 1)]
+    return best
+
+
+def predict_contrib(model, X, start_iteration=0, num_iteration=-1):
+    """predict_contrib_mat (predict.rs:607-697): per row and class a block of
+    max_feature_idx + 1 feature contributions and the expected-value base, summed over
+    the iterations in order (f32 rows widened to f64).  Pure Python: small inputs."""
+    if any("linear" in t for t in model["trees"]):
+        raise ValueError("feature contributions are not defined for linear trees")
+    X64 = np.asarray(X, dtype=np.float32).astype(np.float64)
+    ntpi, nf = model["num_tree_per_iteration"], model["max_feature_idx"] + 1
+    start, num = _range(model, start_iteration, num_iteration)
+    out = np.zeros((X64.shape[0], ntpi * (nf + 1)))
+    for r in range(X64.shape[0]):
+        row = out[r]
+        for i in range(start, start + num):
+            for k in range(ntpi):
+                t = model["trees"][i * ntpi + k]
+                phi = row[k * (nf + 1):(k + 1) * (nf + 1)]
+                phi[nf] += expected_value(t)
+                if t["num_leaves"] > 1:
+                    L = _max_depth(t) + 1
+                    path = [[0, 0.0, 0.0, 0.0] for _ in range(L * (L + 1) // 2)]
+                    _shap(t, X64[r], phi, 0, 0, path, 0, 1.0, 1.0, -1)
+    return out

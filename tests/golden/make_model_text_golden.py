@@ -44,8 +44,9 @@ SPINE = ["binary_scores.txt", "binary_gh_iter1.txt", "binary_gh_iterN.txt",
          "binary_spine_pred.txt"]
 # Prediction early stopping (predict_parity.rs:160-226): model, input rows (f64 bits)
 # and the real binary's frozen raw scores per (freq, margin) cell.
-PREDICT_MODES = {"numeric": ["model.txt", "X.txt", "early_stop.txt"],
-                 "multiclass": ["model.txt", "X.txt", "early_stop.txt"]}
+PREDICT_MODES = {"numeric": ["model.txt", "X.txt", "early_stop.txt", "contrib.txt"],
+                 "multiclass": ["model.txt", "X.txt", "early_stop.txt", "contrib.txt"],
+                 "categorical": ["model.txt", "X.txt", "contrib.txt"]}
 
 
 def main():

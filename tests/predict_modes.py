@@ -29,3 +29,16 @@ def corpus(name):
         else:
             cur[2].append(_bits(toks))
     return text, X, [(f, m, np.stack(r)) for f, m, r in cells]
+
+
+def contrib(name):
+    """(model text, X float32 [rows, cols], contributions f64 [rows, width]) of the real
+    binary's `predict(pred_contrib=True)` capture."""
+    d = os.path.join(DIR, name)
+    text = open(os.path.join(d, "model.txt")).read()
+    rows = [line.split() for line in open(os.path.join(d, "X.txt"))
+            if line.strip() and not line.startswith("#")]
+    X = np.stack([_bits(r) for r in rows]).astype(np.float32)
+    out = [_bits(line.split()) for line in open(os.path.join(d, "contrib.txt"))
+           if line.strip() and not line.startswith("#")]
+    return text, X, np.stack(out)
