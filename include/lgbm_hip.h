@@ -471,6 +471,19 @@ int lgbm_hip_predict_device(lgbm_hip_ctx* ctx, const lgbm_hip_model* model, cons
                             int64_t num_rows, int32_t num_cols, int32_t start_iteration,
                             int32_t num_iteration, int32_t kind, void* d_out);
 
+/* The same kinds over a CSR matrix (predict_raw_csr_range / predict_csr /
+ * predict_leaf_index_csr / predict_contrib_csr, crates/lgbm-model/src/predict.rs:132-160,
+ * 405-500, 699-722): indptr int64[num_rows + 1], indices int32[nnz], values
+ * float[nnz], host pointers.  Each row is all 0.0 but its entries (a repeated column
+ * keeps its last value; columns past max_feature_idx are ignored), as scatter_csr_row
+ * (predict.rs:841-870).  LGBM_HIP_ERR_INVALID_ARGUMENT for an indptr pair outside
+ * [0, nnz] or decreasing, LGBM_HIP_ERR_LENGTH_MISMATCH for a column outside
+ * [0, num_cols). */
+int lgbm_hip_predict_csr(lgbm_hip_ctx* ctx, const lgbm_hip_model* model, const int64_t* indptr,
+                         const int32_t* indices, const float* values, int64_t nnz,
+                         int64_t num_rows, int32_t num_cols, int32_t start_iteration,
+                         int32_t num_iteration, int32_t kind, void* out);
+
 /* Prediction early stopping: predict_raw_early_stop_mat (crates/lgbm-model/src/
  * predict.rs:557-605) over GbdtModel::predict_raw_early_stop (ensemble.rs:120-151).
  * Every `freq` iterations a row whose margin exceeds `margin` (binary: 2|score|;

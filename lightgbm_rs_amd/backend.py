@@ -387,7 +387,30 @@ def _predict_early_stop(self, model, X, freq, margin, start_iteration=0, num_ite
     return out, iters
 
 
+def _predict_csr(self, model, indptr, indices, values, num_cols, kind="raw", start_iteration=0,
+                 num_iteration=-1):
+    """predict_raw_csr_range / predict_csr / predict_leaf_index_csr / predict_contrib_csr
+    (crates/lgbm-model/src/predict.rs:132-160, 405-500, 699-722) on the device: a CSR
+    matrix (indptr int64 [rows + 1], indices int32, values float32) of num_cols columns;
+    returns what `predict` returns for the same rows made dense."""
+    indptr = np.ascontiguousarray(indptr, dtype=np.int64)
+    indices = np.ascontiguousarray(indices, dtype=np.int32)
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    if indices.shape != values.shape:
+        raise ValueError("indices and values differ in length")
+    rows = len(indptr) - 1
+    shape = _predict_shape(model, kind, rows, start_iteration, num_iteration)
+    out = np.zeros(shape, np.int32 if kind == "leaf" else np.float64)
+    self._check(self.lib.lgbm_hip_predict_csr(
+        self.ctx, model.handle, ptr(indptr, C.c_int64), ptr(indices, C.c_int32),
+        ptr(values, C.c_float), C.c_int64(len(values)), C.c_int64(rows), C.c_int32(num_cols),
+        C.c_int32(start_iteration), C.c_int32(num_iteration), C.c_int32(PREDICT_KINDS[kind]),
+        out.ctypes.data_as(C.c_void_p)))
+    return out
+
+
 HipBackend.predict = _predict
+HipBackend.predict_csr = _predict_csr
 HipBackend.predict_early_stop = _predict_early_stop
 HipBackend.predict_device = _predict_device
 

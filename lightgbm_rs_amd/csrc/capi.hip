@@ -29,6 +29,9 @@ void launch_predict(const PredNode* nodes, const PredTree* trees, const double* 
                     double es_margin, int32_t* es_iters, double* out, int32_t* leaf_out,
                     hipStream_t s, const KernelEvents* ev);
 int64_t shap_bytes_per_row(int32_t depth);
+void launch_csr_dense(const int64_t* indptr, const int32_t* indices, const float* values,
+                      int64_t nnz, int64_t rows, int32_t cols, int32_t width, float* dense,
+                      uint32_t* err, hipStream_t s);
 void launch_contrib(const PredNode* nodes, const PredTree* trees, const double* leaves,
                     const int32_t* cat_bounds, const uint32_t* cat_words, const double* node_cover,
                     const double* leaf_cover, const double* expected, const float* X, int64_t r0,
@@ -64,6 +67,8 @@ struct lgbm_hip_ctx {
   double* pm_ncov = nullptr;  // TreeSHAP covers and expected values
   double* pm_lcov = nullptr;
   double* pm_expv = nullptr;
+  char* pm_csr = nullptr;  // sparse-input staging: error word, indptr, indices, values
+  size_t pm_csr_cap = 0;
   char* pm_shap = nullptr;  // TreeSHAP path workspace
   size_t pm_shap_cap = 0;
   float* pm_x = nullptr;  // host-input staging
@@ -927,6 +932,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->pm_lcov);
   F(c->pm_expv);
   F(c->pm_shap);
+  F(c->pm_csr);
   F(c->pm_x);
   F(c->pm_out);
   DevTree& T = c->tree;
@@ -1971,6 +1977,63 @@ int lgbm_hip_predict_device(lgbm_hip_ctx* c, const lgbm_hip_model* m, const floa
   if (rows == 0 || width == 0) return LGBM_HIP_OK;
   if (!d_data || !d_out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null data/out");
   return predict_run(c, m, d_data, rows, cols, it0, it1, kind, d_out);
+}
+
+int lgbm_hip_predict_csr(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t* indptr,
+                         const int32_t* indices, const float* values, int64_t nnz,
+                         int64_t num_rows, int32_t num_cols, int32_t start_iteration,
+                         int32_t num_iteration, int32_t kind, void* out) {
+  int32_t it0 = 0, it1 = 0;
+  int64_t width = 0;
+  int rc = predict_prepare(c, m, num_rows, num_cols, start_iteration, num_iteration, kind, &it0,
+                           &it1, &width);
+  if (rc) return rc;
+  if (nnz < 0) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "negative nnz");
+  if (!indptr || (nnz > 0 && (!indices || !values)))
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null indptr/indices/values");
+  if (num_rows == 0 || width == 0) return LGBM_HIP_OK;
+  if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  const int32_t fw = m->max_feature_idx + 1;  // the dense rows the model reads
+  const size_t pb = (size_t)(num_rows + 1) * 8, ib = (size_t)nnz * 4;
+  const size_t need = 256 + pb + 2 * ib;
+  if (c->pm_csr_cap < need) {
+    if ((rc = dalloc(c, &c->pm_csr, need))) return rc;
+    c->pm_csr_cap = need;
+  }
+  uint32_t* d_err = (uint32_t*)c->pm_csr;
+  int64_t* d_ptr = (int64_t*)(c->pm_csr + 256);
+  int32_t* d_idx = (int32_t*)(c->pm_csr + 256 + pb);
+  float* d_val = (float*)(c->pm_csr + 256 + pb + ib);
+  const size_t xb = (size_t)num_rows * (size_t)std::max(fw, 1) * 4;
+  const size_t ob = (size_t)num_rows * (size_t)width * (kind == LGBM_HIP_PREDICT_LEAF ? 4 : 8);
+  if (c->pm_x_cap < xb) {
+    if ((rc = dalloc(c, &c->pm_x, xb / 4))) return rc;
+    c->pm_x_cap = xb;
+  }
+  if (c->pm_out_cap < ob) {
+    char* p = nullptr;
+    if ((rc = dalloc(c, &p, ob))) return rc;
+    if (c->pm_out) (void)hipFree(c->pm_out);
+    c->pm_out = p;
+    c->pm_out_cap = ob;
+  }
+  const uint32_t zero = 0;
+  HIPCHK(c, hipMemcpy(d_err, &zero, 4, hipMemcpyHostToDevice));
+  HIPCHK(c, hipMemcpy(d_ptr, indptr, pb, hipMemcpyHostToDevice));
+  if (nnz > 0) {
+    HIPCHK(c, hipMemcpy(d_idx, indices, ib, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(d_val, values, ib, hipMemcpyHostToDevice));
+  }
+  launch_csr_dense(d_ptr, d_idx, d_val, nnz, num_rows, num_cols, fw, c->pm_x, d_err, c->stream);
+  HIPCHK(c, hipGetLastError());
+  uint32_t bad = 0;
+  HIPCHK(c, hipMemcpyAsync(&bad, d_err, 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (bad & 1u) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "malformed indptr");
+  if (bad & 2u) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "csr column index out of range");
+  if ((rc = predict_run(c, m, c->pm_x, num_rows, fw, it0, it1, kind, c->pm_out))) return rc;
+  HIPCHK(c, hipMemcpy(out, c->pm_out, ob, hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
 }
 
 int lgbm_hip_predict_early_stop(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* data,

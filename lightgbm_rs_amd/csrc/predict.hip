@@ -437,6 +437,45 @@ void launch_contrib(const PredNode* nodes, const PredTree* trees, const double* 
           cols, nf, it0, it1, ntpi, out);
 }
 
+// ---- sparse rows ------------------------------------------------------------------
+// scatter_csr_row + validate_indptr_pair (predict.rs:772-870): one thread per row
+// zeroes its dense row of `width` (= max_feature_idx + 1) floats and writes its
+// entries in order (a repeated column keeps the last value; columns in [width, cols)
+// are dropped).  A row whose indptr pair leaves [0, nnz] or runs backwards sets bit 0
+// of *err, a column outside [0, cols) bit 1; the host refuses the call on either.
+__global__ __launch_bounds__(256) void k_csr_dense(const int64_t* __restrict__ indptr,
+                                                   const int32_t* __restrict__ indices,
+                                                   const float* __restrict__ values, int64_t nnz,
+                                                   int64_t rows, int32_t cols, int32_t width,
+                                                   float* __restrict__ dense,
+                                                   uint32_t* __restrict__ err) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  float* row = dense + r * width;
+  for (int32_t c = 0; c < width; ++c) row[c] = 0.0f;
+  const int64_t lo = indptr[r], hi = indptr[r + 1];
+  if (lo < 0 || hi < lo || hi > nnz) {
+    atomicOr(err, 1u);
+    return;
+  }
+  for (int64_t k = lo; k < hi; ++k) {
+    const int32_t c = indices[k];
+    if (c < 0 || c >= cols) {
+      atomicOr(err, 2u);
+      return;
+    }
+    if (c < width) row[c] = values[k];
+  }
+}
+
+void launch_csr_dense(const int64_t* indptr, const int32_t* indices, const float* values,
+                      int64_t nnz, int64_t rows, int32_t cols, int32_t width, float* dense,
+                      uint32_t* err, hipStream_t s) {
+  if (rows <= 0) return;
+  k_csr_dense<<<dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s>>>(
+      indptr, indices, values, nnz, rows, cols, width, dense, err);
+}
+
 void launch_predict(const PredNode* nodes, const PredTree* trees, const double* leaves,
                     const int32_t* cat_bounds, const uint32_t* cat_words,
                     const PredLinLeaf* lin_leaves, const int32_t* lin_features,
