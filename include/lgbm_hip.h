@@ -484,6 +484,16 @@ int lgbm_hip_predict_csr(lgbm_hip_ctx* ctx, const lgbm_hip_model* model, const i
                          int64_t num_rows, int32_t num_cols, int32_t start_iteration,
                          int32_t num_iteration, int32_t kind, void* out);
 
+/* The same over a CSC matrix (predict_raw_csc_range / predict_csc /
+ * predict_leaf_index_csc / predict_contrib_csc): indptr int64[num_cols + 1], indices
+ * (row numbers) int32[nnz], values float[nnz]; scatter_csc_dense (predict.rs:868-894):
+ * a repeated row of a column keeps its last value.  LGBM_HIP_ERR_LENGTH_MISMATCH for a
+ * row outside [0, num_rows). */
+int lgbm_hip_predict_csc(lgbm_hip_ctx* ctx, const lgbm_hip_model* model, const int64_t* indptr,
+                         const int32_t* indices, const float* values, int64_t nnz,
+                         int64_t num_rows, int32_t num_cols, int32_t start_iteration,
+                         int32_t num_iteration, int32_t kind, void* out);
+
 /* Prediction early stopping: predict_raw_early_stop_mat (crates/lgbm-model/src/
  * predict.rs:557-605) over GbdtModel::predict_raw_early_stop (ensemble.rs:120-151).
  * Every `freq` iterations a row whose margin exceeds `margin` (binary: 2|score|;

@@ -409,7 +409,28 @@ def _predict_csr(self, model, indptr, indices, values, num_cols, kind="raw", sta
     return out
 
 
+def _predict_csc(self, model, indptr, indices, values, num_rows, kind="raw", start_iteration=0,
+                 num_iteration=-1):
+    """predict_raw_csc_range / predict_csc / predict_leaf_index_csc / predict_contrib_csc
+    (crates/lgbm-model/src/predict.rs:209-240) on the device: a CSC matrix (indptr int64
+    [cols + 1], row indices int32, values float32) of num_rows rows."""
+    indptr = np.ascontiguousarray(indptr, dtype=np.int64)
+    indices = np.ascontiguousarray(indices, dtype=np.int32)
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    if indices.shape != values.shape:
+        raise ValueError("indices and values differ in length")
+    shape = _predict_shape(model, kind, num_rows, start_iteration, num_iteration)
+    out = np.zeros(shape, np.int32 if kind == "leaf" else np.float64)
+    self._check(self.lib.lgbm_hip_predict_csc(
+        self.ctx, model.handle, ptr(indptr, C.c_int64), ptr(indices, C.c_int32),
+        ptr(values, C.c_float), C.c_int64(len(values)), C.c_int64(num_rows),
+        C.c_int32(len(indptr) - 1), C.c_int32(start_iteration), C.c_int32(num_iteration),
+        C.c_int32(PREDICT_KINDS[kind]), out.ctypes.data_as(C.c_void_p)))
+    return out
+
+
 HipBackend.predict = _predict
+HipBackend.predict_csc = _predict_csc
 HipBackend.predict_csr = _predict_csr
 HipBackend.predict_early_stop = _predict_early_stop
 HipBackend.predict_device = _predict_device

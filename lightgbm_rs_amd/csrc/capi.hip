@@ -32,6 +32,9 @@ int64_t shap_bytes_per_row(int32_t depth);
 void launch_csr_dense(const int64_t* indptr, const int32_t* indices, const float* values,
                       int64_t nnz, int64_t rows, int32_t cols, int32_t width, float* dense,
                       uint32_t* err, hipStream_t s);
+void launch_csc_dense(const int64_t* indptr, const int32_t* indices, const float* values,
+                      int64_t nnz, int64_t rows, int32_t cols, int32_t width, float* dense,
+                      uint32_t* err, hipStream_t s);
 void launch_contrib(const PredNode* nodes, const PredTree* trees, const double* leaves,
                     const int32_t* cat_bounds, const uint32_t* cat_words, const double* node_cover,
                     const double* leaf_cover, const double* expected, const float* X, int64_t r0,
@@ -1979,10 +1982,14 @@ int lgbm_hip_predict_device(lgbm_hip_ctx* c, const lgbm_hip_model* m, const floa
   return predict_run(c, m, d_data, rows, cols, it0, it1, kind, d_out);
 }
 
-int lgbm_hip_predict_csr(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t* indptr,
-                         const int32_t* indices, const float* values, int64_t nnz,
-                         int64_t num_rows, int32_t num_cols, int32_t start_iteration,
-                         int32_t num_iteration, int32_t kind, void* out) {
+}  // extern "C"
+
+namespace {
+// CSR (csc = false) or CSC rows made dense on the device, then predicted.
+int predict_sparse(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t* indptr,
+                   const int32_t* indices, const float* values, int64_t nnz, int64_t num_rows,
+                   int32_t num_cols, int32_t start_iteration, int32_t num_iteration, int32_t kind,
+                   void* out, bool csc) {
   int32_t it0 = 0, it1 = 0;
   int64_t width = 0;
   int rc = predict_prepare(c, m, num_rows, num_cols, start_iteration, num_iteration, kind, &it0,
@@ -1994,7 +2001,7 @@ int lgbm_hip_predict_csr(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t
   if (num_rows == 0 || width == 0) return LGBM_HIP_OK;
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
   const int32_t fw = m->max_feature_idx + 1;  // the dense rows the model reads
-  const size_t pb = (size_t)(num_rows + 1) * 8, ib = (size_t)nnz * 4;
+  const size_t pb = (size_t)((csc ? (int64_t)num_cols : num_rows) + 1) * 8, ib = (size_t)nnz * 4;
   const size_t need = 256 + pb + 2 * ib;
   if (c->pm_csr_cap < need) {
     if ((rc = dalloc(c, &c->pm_csr, need))) return rc;
@@ -2024,16 +2031,42 @@ int lgbm_hip_predict_csr(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t
     HIPCHK(c, hipMemcpy(d_idx, indices, ib, hipMemcpyHostToDevice));
     HIPCHK(c, hipMemcpy(d_val, values, ib, hipMemcpyHostToDevice));
   }
-  launch_csr_dense(d_ptr, d_idx, d_val, nnz, num_rows, num_cols, fw, c->pm_x, d_err, c->stream);
+  if (csc) {
+    HIPCHK(c, hipMemsetAsync(c->pm_x, 0, (size_t)num_rows * (size_t)fw * 4, c->stream));
+    launch_csc_dense(d_ptr, d_idx, d_val, nnz, num_rows, num_cols, fw, c->pm_x, d_err, c->stream);
+  } else {
+    launch_csr_dense(d_ptr, d_idx, d_val, nnz, num_rows, num_cols, fw, c->pm_x, d_err, c->stream);
+  }
   HIPCHK(c, hipGetLastError());
   uint32_t bad = 0;
   HIPCHK(c, hipMemcpyAsync(&bad, d_err, 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
   if (bad & 1u) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "malformed indptr");
-  if (bad & 2u) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "csr column index out of range");
+  if (bad & 2u)
+    return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH,
+                   csc ? "csc row index out of range" : "csr column index out of range");
   if ((rc = predict_run(c, m, c->pm_x, num_rows, fw, it0, it1, kind, c->pm_out))) return rc;
   HIPCHK(c, hipMemcpy(out, c->pm_out, ob, hipMemcpyDeviceToHost));
   return LGBM_HIP_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int lgbm_hip_predict_csr(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t* indptr,
+                         const int32_t* indices, const float* values, int64_t nnz,
+                         int64_t num_rows, int32_t num_cols, int32_t start_iteration,
+                         int32_t num_iteration, int32_t kind, void* out) {
+  return predict_sparse(c, m, indptr, indices, values, nnz, num_rows, num_cols, start_iteration,
+                        num_iteration, kind, out, false);
+}
+
+int lgbm_hip_predict_csc(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t* indptr,
+                         const int32_t* indices, const float* values, int64_t nnz,
+                         int64_t num_rows, int32_t num_cols, int32_t start_iteration,
+                         int32_t num_iteration, int32_t kind, void* out) {
+  return predict_sparse(c, m, indptr, indices, values, nnz, num_rows, num_cols, start_iteration,
+                        num_iteration, kind, out, true);
 }
 
 int lgbm_hip_predict_early_stop(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* data,

@@ -468,6 +468,41 @@ __global__ __launch_bounds__(256) void k_csr_dense(const int64_t* __restrict__ i
   }
 }
 
+// scatter_csc_dense (predict.rs:868-894): one thread per column writes its entries
+// into the zeroed dense rows (a repeated row keeps the last value; columns past
+// `width` are only checked).  Bit 0 of *err: a bad indptr pair; bit 1: a row index
+// outside [0, rows).
+__global__ __launch_bounds__(256) void k_csc_dense(const int64_t* __restrict__ indptr,
+                                                   const int32_t* __restrict__ indices,
+                                                   const float* __restrict__ values, int64_t nnz,
+                                                   int64_t rows, int32_t cols, int32_t width,
+                                                   float* __restrict__ dense,
+                                                   uint32_t* __restrict__ err) {
+  const int32_t c = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (c >= cols) return;
+  const int64_t lo = indptr[c], hi = indptr[c + 1];
+  if (lo < 0 || hi < lo || hi > nnz) {
+    atomicOr(err, 1u);
+    return;
+  }
+  for (int64_t k = lo; k < hi; ++k) {
+    const int32_t r = indices[k];
+    if (r < 0 || (int64_t)r >= rows) {
+      atomicOr(err, 2u);
+      return;
+    }
+    if (c < width) dense[(int64_t)r * width + c] = values[k];
+  }
+}
+
+void launch_csc_dense(const int64_t* indptr, const int32_t* indices, const float* values,
+                      int64_t nnz, int64_t rows, int32_t cols, int32_t width, float* dense,
+                      uint32_t* err, hipStream_t s) {
+  if (cols <= 0) return;
+  k_csc_dense<<<dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s>>>(
+      indptr, indices, values, nnz, rows, cols, width, dense, err);
+}
+
 void launch_csr_dense(const int64_t* indptr, const int32_t* indices, const float* values,
                       int64_t nnz, int64_t rows, int32_t cols, int32_t width, float* dense,
                       uint32_t* err, hipStream_t s) {

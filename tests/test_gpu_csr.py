@@ -83,3 +83,43 @@ def test_csr_errors(be):
     # a valid call after the refusals
     got = be.predict_csr(m, np.array([0, 1, 2, 3], np.int64), ind, val, 2)
     assert np.array_equal(got, be.predict(m, densify([0, 1, 2, 3], ind, val, 2), "raw"))
+
+
+def to_csc(indptr, indices, values, num_cols):
+    """The same entries column by column, each column's entries in row order (so a
+    repeated (row, column) keeps the value the CSR rule keeps: the last)."""
+    rows = np.repeat(np.arange(len(indptr) - 1), np.diff(indptr))
+    order = np.lexsort((np.arange(len(indices)), rows, indices))
+    cptr = np.concatenate([[0], np.cumsum(np.bincount(indices, minlength=num_cols))])
+    return cptr.astype(np.int64), rows[order].astype(np.int32), values[order]
+
+
+@pytest.mark.parametrize("name", ["binary_spine", "multiclass_spine", "cat_manyvsmany"])
+def test_csc_predict_equals_dense(be, name):
+    print("csc", name, flush=True)
+    text = open(os.path.join(MT, name + ".txt")).read()
+    m = Model(text)
+    width = P.parse_model(text)["max_feature_idx"] + 1
+    rng = np.random.default_rng(22)
+    num_cols = width + 2
+    indptr, indices, values = random_csr(rng, 4001, num_cols, 2 * width)
+    X = densify(indptr, indices, values, width)
+    cptr, rows, vals = to_csc(indptr, indices, values, num_cols)
+    for kind in ("raw", "leaf", "contrib"):
+        got = be.predict_csc(m, cptr, rows, vals, len(indptr) - 1, kind)
+        ref = be.predict(m, X, kind)
+        assert np.array_equal(got.view(np.uint8), ref.view(np.uint8)), kind
+
+
+def test_csc_errors(be):
+    print("csc errors", flush=True)
+    m = Model(open(os.path.join(MT, "binary_spine.txt")).read())
+    rows = np.array([0, 1, 2], np.int32)
+    val = np.ones(3, np.float32)
+    with pytest.raises(HipError, match="malformed indptr"):
+        be.predict_csc(m, np.array([0, 2, 1], np.int64), rows, val, 3)
+    with pytest.raises(HipError, match="row index out of range"):
+        be.predict_csc(m, np.array([0, 2, 3], np.int64), rows, val, 2)
+    got = be.predict_csc(m, np.array([0, 2, 3], np.int64), rows, val, 3)
+    X = np.array([[1, 0], [1, 0], [0, 1]], np.float32)
+    assert np.array_equal(got, be.predict(m, X, "raw"))
