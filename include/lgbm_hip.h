@@ -199,6 +199,29 @@ int lgbm_hip_quantize(lgbm_hip_ctx* ctx, int32_t num_grad_quant_bins, int32_t st
  * out[2*i] = hessian, out[2*i+1] = gradient (gradient_discretizer.rs:25-26,104-118). */
 int lgbm_hip_get_discretized(lgbm_hip_ctx* ctx, int8_t* out, int64_t n);
 
+/* Quantized gradients from their dequantized values, for the drop-in wiring at the
+ * quantizer call site (quantize_grad_hess_in_place, gbdt.rs:43-62,945-960): the
+ * reference replaces g/h in place by f32(q * scale) and the learner then uploads
+ * those arrays.  Quantizing them again is not idempotent (the recomputed scales
+ * round differently, stochastic draws differ), so this entry recovers q instead:
+ * q = round(v / scale) per row, exact for every v = f32(q * scale), verified by
+ * f32(q * scale) == v.  grad_scale / hess_scale are the discretizer's scales
+ * (GradientDiscretizer grad_scale / hess_scale, gradient_discretizer.rs:145-165);
+ * both <= 0 take those of this context's last lgbm_hip_quantize.  A row that is not
+ * f32(q * scale) with |q_grad| <= num_grad_quant_bins / 2 and 0 <= q_hess <=
+ * num_grad_quant_bins returns LGBM_HIP_ERR_INVALID_ARGUMENT naming the row, and the
+ * context then holds no quantized gradients. */
+int lgbm_hip_set_dequantized_gradients(lgbm_hip_ctx* ctx, const float* grad, const float* hess,
+                                       int64_t n, int32_t num_grad_quant_bins,
+                                       double grad_scale, double hess_scale);
+
+/* config.feature_contri: per-feature split-gain multipliers indexed by REAL feature
+ * index (n entries; features whose real index is >= n keep 1), applied to each
+ * feature's scan result after its splittability is recorded and before the
+ * cross-feature ArgMax (learner.rs:3235-3252, 3701-3709).  Affects the trees grown
+ * after the call; a bins upload resets every multiplier to 1, as does n == 0. */
+int lgbm_hip_set_feature_contri(lgbm_hip_ctx* ctx, const double* contri, int32_t n);
+
 /* ---- per-op seam (parity tests / fine-grained driver) ----------------------- */
 
 /* Exact integer histogram of the quantized gradients over `leaf_rows` (or all rows

@@ -118,6 +118,23 @@ class HipBackend:
                                                ptr(scales, C.c_double)))
         return scales, dg, dh
 
+    def set_dequantized_grad_hess(self, grad, hess, num_grad_quant_bins=4, grad_scale=0.0,
+                                  hess_scale=0.0):
+        """The quantized pairs recovered exactly from dequantized values f32(q * scale)
+        (the arrays quantize_grad_hess_in_place leaves, gbdt.rs:43-62); scales <= 0
+        take the last discretize_dequantize_in_place's."""
+        g = np.ascontiguousarray(grad, dtype=np.float32)
+        h = np.ascontiguousarray(hess, dtype=np.float32)
+        self._check(self.lib.lgbm_hip_set_dequantized_gradients(
+            self.ctx, ptr(g, C.c_float), ptr(h, C.c_float), C.c_int64(len(g)),
+            C.c_int32(num_grad_quant_bins), C.c_double(grad_scale), C.c_double(hess_scale)))
+
+    def set_feature_contri(self, contri=None):
+        """config.feature_contri gain multipliers by real feature index (None: reset)."""
+        c = None if contri is None else np.ascontiguousarray(contri, dtype=np.float64)
+        self._check(self.lib.lgbm_hip_set_feature_contri(self.ctx, ptr(c, C.c_double),
+                                                         C.c_int32(0 if c is None else len(c))))
+
     def discretized(self):
         """The `discretize` buffer: out[2i] = hess, out[2i+1] = grad (i8)."""
         out = np.zeros(2 * self.num_data, np.int8)

@@ -116,6 +116,7 @@ struct lgbm_hip_ctx {
   uint64_t *wave_mats = nullptr, *lane_mats = nullptr;
   double* stats = nullptr;
   uint4* partials = nullptr;  // per-block g/h statistics
+  unsigned long long* d_flags = nullptr;  // [2]: check kernels' (count, first row)
   // tree-sized: node slots (SLOT_CAP(lcap)) and per-leaf arrays
   int32_t lcap = 0;
   double* slots = nullptr;
@@ -680,6 +681,7 @@ DevFeature feature_from_batched(const lgbm_batched_feature& b) {
   f.skip_default_bin = b.skip_default_bin;
   f.na_as_missing = b.na_as_missing;
   f.run_forward = b.run_forward;
+  f.penalty = 1.0;
   f.real_index = -1;
   return f;
 }
@@ -693,6 +695,16 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
                    const double* bin_upper_bound) {
   int rc = 0;
   const int32_t F = F_in;
+  // Until the new layout is complete the context holds no usable resident state: a
+  // failed allocation or copy below must not leave flags (or a captured graph)
+  // pointing at buffers this call frees.
+  c->have_bins = c->have_grad = c->quant_ready = c->have_labels = false;
+  c->ahead = false;
+  c->buf_gen++;
+  if (c->graph_exec) {
+    (void)hipGraphExecDestroy(c->graph_exec);
+    c->graph_exec = nullptr;
+  }
   if (F > 16 * LGBM_MAX_W - 4)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "more features than the record layout holds");
   if (num_data >= (1ll << 31) - 1)
@@ -718,6 +730,7 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
     d.skip_default_bin = (m.num_bin > 2 && m.missing_type == LGBM_MISSING_ZERO) ? 1 : 0;
     d.na_as_missing = (m.num_bin > 2 && m.missing_type == LGBM_MISSING_NAN) ? 1 : 0;
     d.run_forward = (m.num_bin > 2 && m.missing_type != LGBM_MISSING_NONE) ? 1 : 0;
+    d.penalty = 1.0;
     acc += m.num_bin;
     uacc += m.num_bin;
   }
@@ -856,6 +869,7 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
     return fail(set_err(c, LGBM_HIP_ERR_HIP, "hipHostMalloc"));
   if ((rc = init_jump_tables(c))) return fail(rc);
   if ((rc = dalloc(c, &c->partials, STAT_BLOCKS))) return fail(rc);
+  if ((rc = dalloc(c, &c->d_flags, 2))) return fail(rc);
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
       cus > 0)
@@ -900,6 +914,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->lane_mats);
   F(c->stats);
   F(c->partials);
+  F(c->d_flags);
   F(c->best_fpos);
   F(c->int_slots);
   F(c->tree_blob);
@@ -1269,6 +1284,72 @@ int lgbm_hip_get_discretized(lgbm_hip_ctx* c, int8_t* out, int64_t n) {
     out[2 * i] = (int8_t)(uint8_t)(q[i] >> 8);        // hess
     out[2 * i + 1] = (int8_t)(uint8_t)(q[i] & 0xff);  // grad
   }
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_set_dequantized_gradients(lgbm_hip_ctx* c, const float* grad, const float* hess,
+                                       int64_t n, int32_t bins, double grad_scale,
+                                       double hess_scale) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
+  if (!grad || !hess) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null gradients");
+  if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "gradient length != num_data");
+  if (bins < 1 || bins > 254)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_grad_quant_bins must be in 1..=254");
+  const bool given = grad_scale > 0.0 && hess_scale > 0.0;
+  if (!given) {
+    if (!c->quant_ready || c->quant_bins != bins)
+      return set_err(c, LGBM_HIP_ERR_RUNTIME,
+                     "no scales given and no lgbm_hip_quantize with these bins to take them from");
+  }
+  c->quant_ready = false;
+  HIPCHK(c, hipMemcpy(c->g, grad, (size_t)n * 4, hipMemcpyHostToDevice));
+  HIPCHK(c, hipMemcpy(c->h, hess, (size_t)n * 4, hipMemcpyHostToDevice));
+  c->have_grad = true;
+  if (given) {
+    // the quantizer header of the control block, as compute_scales leaves it
+    // (gradient_discretizer.rs:145-165); the packed cells need q_h >= 0 (hmin 0)
+    const double v[4] = {grad_scale, hess_scale, 1.0 / grad_scale, 1.0 / hess_scale};
+    const float f[4] = {(float)(1.0 * grad_scale), (float)(1.0 * hess_scale),
+                        (float)(3.0 * hess_scale), 0.0f};
+    HIPCHK(c, hipMemcpy((char*)c->ctl + CTL_OFF(gs), v, sizeof(v), hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy((char*)c->ctl + CTL_OFF(vg1), f, sizeof(f), hipMemcpyHostToDevice));
+    const int32_t qb[2] = {bins, 0};
+    HIPCHK(c, hipMemcpy((char*)c->ctl + CTL_OFF(quant_bins), qb, sizeof(qb), hipMemcpyHostToDevice));
+  }
+  const unsigned long long init[2] = {0ull, ~0ull};
+  HIPCHK(c, hipMemcpyAsync(c->d_flags, init, sizeof(init), hipMemcpyHostToDevice, c->stream));
+  launch_requant(c->g, c->h, n, c->ctl, bins, c->gh[BUF_ORIG], c->d_flags, c->stream);
+  HIPCHK(c, hipGetLastError());
+  unsigned long long bad[2] = {0ull, 0ull};
+  HIPCHK(c, hipMemcpyAsync(bad, c->d_flags, sizeof(bad), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (bad[0]) {
+    c->have_grad = false;  // nothing consistent to grow from
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT,
+                   std::to_string(bad[0]) + " rows are not f32(q * scale) for an in-range q "
+                   "(first row " + std::to_string(bad[1]) + ")");
+  }
+  c->quant_ready = true;
+  c->quant_bins = bins;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_set_feature_contri(lgbm_hip_ctx* c, const double* contri, int32_t n) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
+  if (n < 0 || (n > 0 && !contri))
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null contri or negative length");
+  for (DevFeature& d : c->feats) {
+    const int32_t ri = d.real_index;
+    d.penalty = (ri >= 0 && ri < n) ? contri[ri] : 1.0;
+  }
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipMemcpy(c->d_feats, c->feats.data(), c->feats.size() * sizeof(DevFeature),
+                      hipMemcpyHostToDevice));
   return LGBM_HIP_OK;
 }
 
@@ -1877,6 +1958,7 @@ int predict_prepare(lgbm_hip_ctx* c, const lgbm_hip_model* m, int64_t rows, int3
                ? (int64_t)m->num_tree_per_iteration * (m->max_feature_idx + 2)
                : (int64_t)m->num_tree_per_iteration;
   if (c->pm_uid != m->uid) {
+    c->pm_uid = 0;  // a partial upload must not pass for the cached model
     if ((rc = upload_vec(c, &c->pm_nodes, m->nodes))) return rc;
     if ((rc = upload_vec(c, &c->pm_trees, m->tree_index))) return rc;
     if ((rc = upload_vec(c, &c->pm_leaves, m->leaf_values))) return rc;
@@ -1908,6 +1990,7 @@ int predict_run(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* d_x, int6
     chunk = std::min(chunk, rows);
     const size_t need = (size_t)(per_row * chunk);
     if (c->pm_shap_cap < need) {
+      c->pm_shap_cap = 0;  // dalloc frees the old workspace first
       int rc = dalloc(c, &c->pm_shap, need);
       if (rc) return rc;
       c->pm_shap_cap = need;
@@ -1954,6 +2037,7 @@ int lgbm_hip_predict(lgbm_hip_ctx* c, const lgbm_hip_model* m, const float* data
   const size_t xb = (size_t)rows * (size_t)cols * 4;
   const size_t ob = (size_t)rows * (size_t)width * (kind == LGBM_HIP_PREDICT_LEAF ? 4 : 8);
   if (c->pm_x_cap < xb) {
+    c->pm_x_cap = 0;  // dalloc frees the old staging first
     if ((rc = dalloc(c, &c->pm_x, (size_t)rows * (size_t)cols))) return rc;
     c->pm_x_cap = xb;
   }
@@ -2004,6 +2088,7 @@ int predict_sparse(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t* indp
   const size_t pb = (size_t)((csc ? (int64_t)num_cols : num_rows) + 1) * 8, ib = (size_t)nnz * 4;
   const size_t need = 256 + pb + 2 * ib;
   if (c->pm_csr_cap < need) {
+    c->pm_csr_cap = 0;  // dalloc frees the old staging first
     if ((rc = dalloc(c, &c->pm_csr, need))) return rc;
     c->pm_csr_cap = need;
   }
@@ -2014,6 +2099,7 @@ int predict_sparse(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t* indp
   const size_t xb = (size_t)num_rows * (size_t)std::max(fw, 1) * 4;
   const size_t ob = (size_t)num_rows * (size_t)width * (kind == LGBM_HIP_PREDICT_LEAF ? 4 : 8);
   if (c->pm_x_cap < xb) {
+    c->pm_x_cap = 0;  // dalloc frees the old staging first
     if ((rc = dalloc(c, &c->pm_x, xb / 4))) return rc;
     c->pm_x_cap = xb;
   }
@@ -2090,6 +2176,7 @@ int lgbm_hip_predict_early_stop(lgbm_hip_ctx* c, const lgbm_hip_model* m, const 
   const int32_t f = accurate ? 0 : freq;
   const size_t xb = (size_t)rows * (size_t)cols * 4, ob = (size_t)rows * (size_t)width * 8;
   if (c->pm_x_cap < xb) {
+    c->pm_x_cap = 0;  // dalloc frees the old staging first
     if ((rc = dalloc(c, &c->pm_x, (size_t)rows * (size_t)cols))) return rc;
     c->pm_x_cap = xb;
   }

@@ -993,7 +993,12 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
   } else {
     const ScanCfg sc = make_scan_cfg(ctl->cfg);
     wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
-    if (lane_id() == 0) L.splittable[(size_t)leaf * F + f] = out->gain > -__builtin_inf() ? 1 : 0;
+    if (lane_id() == 0) {
+      // splittability from the raw scan, then feature_contri scales the gain the
+      // ArgMax compares (learner.rs:3235-3252)
+      L.splittable[(size_t)leaf * F + f] = out->gain > -__builtin_inf() ? 1 : 0;
+      out->gain *= ft.penalty;
+    }
   }
 }
 

@@ -179,6 +179,8 @@ void launch_quant_scales(Ctl* ctl, const uint4* partials, int64_t n, int32_t bin
 void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,
                      const uint64_t* wave_mats, const uint64_t* lane_mats, uint64_t s0,
                      int32_t stochastic, uint16_t* gh, float* dg, float* dh, hipStream_t s);
+void launch_requant(const float* g, const float* h, int64_t n, const Ctl* ctl, int32_t bins,
+                    uint16_t* gh, unsigned long long* bad, hipStream_t s);
 void launch_hist(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
 void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s,
                     const KernelEvents* ev = nullptr);

@@ -327,6 +327,31 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ g,
   for (int r = tid; r < nblk; r += 256) gh[brow0 + r] = sq_[qidx(r)];
 }
 
+// Recovery of the quantized pairs from dequantized values f32(q * scale)
+// (lgbm_hip_set_dequantized_gradients): q = round(v / scale), checked by the product.
+// bad[0] counts rows that fail, bad[1] is the first such row.
+__global__ __launch_bounds__(256) void k_requant(const float* __restrict__ g,
+                                                 const float* __restrict__ h, int64_t n,
+                                                 const Ctl* __restrict__ ctl, int32_t bins,
+                                                 uint16_t* __restrict__ gh,
+                                                 unsigned long long* __restrict__ bad) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const double gs = ctl->gs, hs = ctl->hs;
+  const float gv = g[r], hv = h[r];
+  const double qgd = rint((double)gv / gs), qhd = rint((double)hv / hs);
+  const double gmax = (double)(bins / 2);
+  bool ok = qgd >= -gmax && qgd <= gmax && qhd >= 0.0 && qhd <= (double)bins;
+  const int32_t qg = ok ? (int32_t)qgd : 0, qh = ok ? (int32_t)qhd : 0;
+  ok = ok && (float)((double)qg * gs) == gv && (float)((double)qh * hs) == hv;
+  if (!ok) {
+    atomicAdd(&bad[0], 1ull);
+    atomicMin(&bad[1], (unsigned long long)r);
+    return;
+  }
+  gh[r] = (uint16_t)((uint16_t)(uint8_t)(int8_t)qg | ((uint16_t)(uint8_t)qh << 8));
+}
+
 // ===========================================================================
 // ConstructHistogram (integer), batched over the histogram jobs of a round (the
 // smaller child of every split; the root; a per-op build).  A job is a physical row
@@ -698,7 +723,10 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
   }
   const ScanCfg sc = make_scan_cfg(ctl->cfg);
   wave_scan(cs, ft, sc, sg, sh, nrows, weight, out);
-  if (lane_id() == 0) L.splittable[f] = out->gain > -__builtin_inf() ? 1 : 0;
+  if (lane_id() == 0) {
+    L.splittable[f] = out->gain > -__builtin_inf() ? 1 : 0;
+    out->gain *= ft.penalty;  // feature_contri (learner.rs:3235-3252)
+  }
 }
 
 // Per-op FindBestThreshold over explicit features (find_best_splits_batched,
@@ -823,6 +851,12 @@ void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,
   const int64_t blocks = (n + QUANT_BLOCK_ROWS - 1) / QUANT_BLOCK_ROWS;
   k_quantize<<<dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0, s>>>(
       g, h, n, ctl, wave_mats, lane_mats, s0, stochastic, gh, dg, dh);
+}
+void launch_requant(const float* g, const float* h, int64_t n, const Ctl* ctl, int32_t bins,
+                    uint16_t* gh, unsigned long long* bad, hipStream_t s) {
+  const int64_t blocks = (n + 255) / 256;
+  if (blocks < 1) return;
+  k_requant<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(g, h, n, ctl, bins, gh, bad);
 }
 void launch_hist(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
   const dim3 g(HIST_SLOTS), blk(HIST_THREADS);

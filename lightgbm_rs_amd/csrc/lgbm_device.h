@@ -93,7 +93,7 @@ struct DevFeature {
   int32_t skip_default_bin;
   int32_t na_as_missing;
   int32_t run_forward;
-  int32_t _pad[2];
+  double penalty;      // config.feature_contri of the feature's real index (1: none)
 };
 
 struct LeafSums {

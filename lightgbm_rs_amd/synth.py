@@ -5,10 +5,12 @@ label, binned to <= 255 quantile bins (the f32-gradient CPU-reference case).
 
 config1_like(): configs[1] — N rows x 28 float32 features (21 ~N(0,1), 7 derived as
 products / abs of pairs), logistic label logit = w.x + 0.5*x0*x1 + N(0, 0.1) with
-w ~ N(0,1), binned to <= max_bin quantile bins per feature (u8).  Binning sits
-outside the timed hot path; quantile cut points stand in for
-BinMapper::find_bin_from_column.  With `device` set to a torch CUDA device the
-generation and binning run there (same recipe, torch's generator).
+w ~ N(0,1), binned to <= max_bin bins per feature (u8) by this library's BinMapper
+(BinMapper::find_bin_from_column on a bin_construct_sample_cnt = 200000 row sample,
+then ValueToBin), so the feature descriptors are the reference's: most_freq_bin,
+default_bin, missing type and the offset rule come from the mappers.  With `device`
+set to a torch CUDA device the generation and a quantile binning run there (same
+recipe, torch's generator).
 """
 import numpy as np
 
@@ -50,9 +52,9 @@ def config0_like(n, seed=0x5EED0000, max_bin=255):
     return config1_like(n, seed=seed, max_bin=max_bin, derived=False)
 
 
-def config1_like(n, seed=0x5EED0001, max_bin=63, device=None, derived=True):
-    if device is not None:
-        return _config1_torch(n, seed, max_bin, device)
+def config1_raw_host(n, seed=0x5EED0001, derived=True):
+    """configs[1]'s raw table on the host: X float32 [28, n] (one feature per row) and
+    the labels, drawn with numpy's generator."""
     rng = np.random.default_rng(seed)
     if derived:
         X = rng.standard_normal((21, n), dtype=np.float32)
@@ -62,15 +64,35 @@ def config1_like(n, seed=0x5EED0001, max_bin=63, device=None, derived=True):
     w = rng.standard_normal(28).astype(np.float32)
     logit = w @ X + 0.5 * X[0] * X[1] + rng.normal(0, 0.1, n).astype(np.float32)
     y = (rng.random(n, dtype=np.float32) < 1.0 / (1.0 + np.exp(-logit))).astype(np.float32)
-    bins = np.zeros((28, n), dtype=np.uint8)
-    upper, nbs = [], []
-    sample = X[:, :: max(1, n // 200000)]
-    for f in range(28):
-        qs = np.unique(np.quantile(sample[f], np.linspace(0, 1, max_bin + 1)[1:-1]).astype(np.float32))
-        bins[f] = np.searchsorted(qs, X[f], side="left").astype(np.uint8)
-        nbs.append(len(qs) + 1)
-        upper.extend([float(q) for q in qs] + [np.inf])
-    return bins, _meta_for(nbs), np.array(upper, dtype=np.float64), y
+    return X, y
+
+
+def config1_like(n, seed=0x5EED0001, max_bin=63, device=None, derived=True):
+    if device is not None:
+        return _config1_torch(n, seed, max_bin, device)
+    X, y = config1_raw_host(n, seed, derived)
+    bins, meta, upper = bin_with_mappers(X, max_bin)
+    return bins, meta, upper, y
+
+
+def bin_with_mappers(X, max_bin, min_data_in_leaf=20):
+    """X [F, n] -> (bins u8 [F, n], feature meta, concatenated upper bounds) with this
+    library's BinMapper: find_bin_from_column's 200000-row sample (data_random_seed 1),
+    ValueToBin on the host, the descriptors of the booster's feature columns
+    (booster.rs:449-520)."""
+    from .backend import feature_meta
+    from .binning import BinMapper, sample_indices
+    F, n = X.shape
+    idx = sample_indices(n, 200000, 1)
+    bins = np.zeros((F, n), dtype=np.uint8)
+    meta, upper = [], []
+    for f in range(F):
+        m = BinMapper.from_sampled_column(X[f, idx].astype(np.float64), n, max_bin=max_bin,
+                                          min_data_in_leaf=min_data_in_leaf)
+        bins[f] = m.value_to_bin(X[f]).astype(np.uint8)
+        meta.append(feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f))
+        upper.extend(m.upper_bounds.tolist())
+    return bins, meta, np.array(upper, dtype=np.float64)
 
 
 def config1_raw(n, seed=0x5EED0001, device=None):

@@ -166,11 +166,22 @@ lgbm_split_info split_none() {
 // ---------------------------------------------------------------------------
 // find_best_split_cpu_native (kernels/split.rs:8970-9329)
 // ---------------------------------------------------------------------------
+// Candidate record (optional): every REVERSE / FORWARD candidate the scan visits, in
+// scan order, as the gain it compares against min_gain_shift, or NaN where the
+// candidate is gated out (default-bin skip, continue gate, the break candidate, or a
+// gain not above min_gain_shift).  The scan stops after a break candidate.  This is
+// the encoding of the reference's SCAND_REV / SCAND_FWD goldens (kernel_parity.rs:
+// 369-466).
+struct ScanCandidates {
+  std::vector<double> rev, fwd;
+};
+
 int find_best_split(const double* hist, size_t hist_len, const lgbm_gain_config& cfg,
                     uint32_t num_bin, int32_t offset, uint32_t default_bin,
                     bool skip_default_bin, bool na_as_missing, bool run_forward,
                     double sum_gradient, double sum_hessian, int32_t num_data,
-                    lgbm_split_info* out) {
+                    lgbm_split_info* out, ScanCandidates* cand = nullptr) {
+  const double kNaN = std::numeric_limits<double>::quiet_NaN();
   if (num_bin == 0) return fail(LGBM_HIP_ERR_RUNTIME, "find_best_split: num_bin must be > 0");
   if (hist_len != 2ull * num_bin) return fail(LGBM_HIP_ERR_LENGTH_MISMATCH, "hist length");
   if (!(sum_hessian > 0.0))
@@ -233,9 +244,11 @@ int find_best_split(const double* hist, size_t hist_len, const lgbm_gain_config&
       const bool cont = rc < min_d || srh < min_h;
       const bool brk = lc < min_d || slh < min_h;
       done = done || (active && !cont && brk);
+      double rec = kNaN;
       if (active && !cont && !done) {
         double g = gain_of(slg, slh, srg, srh, lc, rc);
         if (g > min_gain_shift) {
+          rec = g;
           is_splittable = true;
           if (g > best_gain) {
             best_lc = lc;
@@ -247,6 +260,7 @@ int find_best_split(const double* hist, size_t hist_len, const lgbm_gain_config&
           }
         }
       }
+      if (cand) cand->rev.push_back(rec);
     }
   }
   {  // FORWARD
@@ -282,9 +296,11 @@ int find_best_split(const double* hist, size_t hist_len, const lgbm_gain_config&
       const bool cont = lc < min_d || slh < min_h;
       const bool brk = rc < min_d || srh < min_h;
       done = done || (active && !cont && brk);
+      double rec = kNaN;
       if (active && !cont && !done) {
         double g = gain_of(slg, slh, srg, srh, lc, rc);
         if (g > min_gain_shift) {
+          rec = g;
           is_splittable = true;
           if (g > best_gain) {
             best_lc = lc;
@@ -296,6 +312,7 @@ int find_best_split(const double* hist, size_t hist_len, const lgbm_gain_config&
           }
         }
       }
+      if (cand) cand->fwd.push_back(rec);
     }
   }
   const int32_t best_rc = num_data - best_lc;
@@ -752,6 +769,9 @@ struct Learner {
   size_t slot_len = 0;
   lgbm_gain_config cfg;
   int32_t num_leaves, max_depth;
+  // config.feature_contri: per-feature split-gain multiplier by REAL feature index
+  // (learner.rs:456-459, 3701-3709); empty = no multiply.
+  std::vector<double> contri;
 
   bool skip_default_bin(int f) const {
     return meta[f].num_bin > 2 && meta[f].missing_type == LGBM_MISSING_ZERO;
@@ -789,8 +809,12 @@ struct Learner {
     int32_t lbf = -1;
     for (int f = 0; f < F; ++f) {
       if (!scanned[f]) continue;
-      const lgbm_split_info& s = res[f];
+      lgbm_split_info& s = res[f];
+      // splittability is recorded from the raw scan result, then feature_contri
+      // multiplies the gain before the cross-feature ArgMax (learner.rs:3235-3252)
       this_split[f] = s.gain > kMinScore;
+      const int32_t ri = meta[f].real_feature_index;
+      if (ri >= 0 && (size_t)ri < contri.size()) s.gain *= contri[(size_t)ri];
       if (s.gain > kMinScore && split_gt(s, meta[f].real_feature_index, lb, lbf)) {
         lb = s;
         lbf = meta[f].real_feature_index;
@@ -1100,6 +1124,18 @@ int oracle_xorshift_u01(uint64_t state, int64_t n, double* out) {
   return LGBM_HIP_OK;
 }
 
+// Raw xorshift64 states (the transition next_u01 applies, gradient_discretizer.rs:
+// 255-263): out[i] = the state after i + 1 steps.
+int oracle_xorshift_states(uint64_t state, int64_t n, uint64_t* out) {
+  Discretizer d;
+  d.rng = state;
+  for (int64_t i = 0; i < n; ++i) {
+    (void)d.next_u01();
+    out[i] = d.rng;
+  }
+  return LGBM_HIP_OK;
+}
+
 int oracle_fix_histogram(double* hist, uint32_t num_bin, uint32_t mfb, double sg, double sh) {
   fix_histogram(hist, num_bin, mfb, sg, sh);
   return LGBM_HIP_OK;
@@ -1123,6 +1159,29 @@ int oracle_find_best_split(const double* hist, int64_t hist_len, const lgbm_gain
                          sum_gradient, sum_hessian, num_data, out);
 }
 
+// The per-candidate record of one FindBestThreshold scan (ScanCandidates): rev / fwd
+// receive up to cap values each; *n_rev / *n_fwd the number the scan produced.
+int oracle_split_candidates(const double* hist, int64_t hist_len, const lgbm_gain_config* cfg,
+                            uint32_t num_bin, int32_t offset, uint32_t default_bin,
+                            int32_t skip_default_bin, int32_t na_as_missing, int32_t run_forward,
+                            double sum_gradient, double sum_hessian, int32_t num_data,
+                            double* rev, int32_t* n_rev, double* fwd, int32_t* n_fwd,
+                            int32_t cap) {
+  lgbm_split_info out;
+  ScanCandidates c;
+  int rc = find_best_split(hist, (size_t)hist_len, *cfg, num_bin, offset, default_bin,
+                           skip_default_bin != 0, na_as_missing != 0, run_forward != 0,
+                           sum_gradient, sum_hessian, num_data, &out, &c);
+  if (rc) return rc;
+  if ((int64_t)c.rev.size() > cap || (int64_t)c.fwd.size() > cap)
+    return fail(LGBM_HIP_ERR_LENGTH_MISMATCH, "candidate capacity");
+  std::copy(c.rev.begin(), c.rev.end(), rev);
+  std::copy(c.fwd.begin(), c.fwd.end(), fwd);
+  *n_rev = (int32_t)c.rev.size();
+  *n_fwd = (int32_t)c.fwd.size();
+  return LGBM_HIP_OK;
+}
+
 // The learner router over a row set: stable [left | right] order of local positions.
 int oracle_data_partition(const uint32_t* bins, int64_t n, uint32_t num_bin, uint32_t min_bin,
                           uint32_t max_bin, uint32_t threshold, uint32_t mfb,
@@ -1143,13 +1202,16 @@ int oracle_data_partition(const uint32_t* bins, int64_t n, uint32_t num_bin, uin
 }
 
 // One tree of the SerialTreeLearner spine over feature-major bins of `width` bytes.
+// feature_contri (n_contri entries by real feature index) may be NULL.
 int oracle_train_tree(const void* bins, int32_t width, int32_t F, int64_t N,
                       const lgbm_feature_meta* meta, const double* ub, const float* g,
                       const float* h, const lgbm_gain_config* cfg, int32_t num_leaves,
-                      int32_t max_depth, lgbm_tree_out* tree_out, lgbm_layout_out* layout) {
+                      int32_t max_depth, const double* feature_contri, int32_t n_contri,
+                      lgbm_tree_out* tree_out, lgbm_layout_out* layout) {
   Learner L;
   int rc = make_learner(L, bins, width, F, N, meta, ub, cfg, num_leaves, max_depth);
   if (rc) return rc;
+  if (feature_contri && n_contri > 0) L.contri.assign(feature_contri, feature_contri + n_contri);
   Tree t;
   DataPartition dp(N, num_leaves);
   rc = L.train(g, h, t, dp);

@@ -86,6 +86,13 @@ def xorshift_u01(state, n):
     return out
 
 
+def xorshift_states(state, n):
+    """The raw xorshift64 states after 1..n steps of the discretizer's stream."""
+    out = np.zeros(n, dtype=np.uint64)
+    _check(lib().oracle_xorshift_states(C.c_uint64(state), C.c_int64(n), ptr(out, C.c_uint64)))
+    return out
+
+
 def fix_histogram(hist, num_bin, mfb, sum_g, sum_h):
     h = np.array(hist, dtype=np.float64, copy=True)
     _check(lib().oracle_fix_histogram(ptr(h, C.c_double), C.c_uint32(num_bin), C.c_uint32(mfb),
@@ -121,6 +128,23 @@ def find_best_split(hist, cfg, num_bin, offset, default_bin, skip_default_bin, n
     return out
 
 
+def split_candidates(hist, cfg, num_bin, offset, default_bin, skip_default_bin, na_as_missing,
+                     run_forward, sum_gradient, sum_hessian, num_data):
+    """Every REVERSE / FORWARD candidate of one scan: its gain, or NaN where gated."""
+    h = np.ascontiguousarray(hist, dtype=np.float64)
+    cap = 2 * int(num_bin) + 2
+    rev = np.zeros(cap, dtype=np.float64)
+    fwd = np.zeros(cap, dtype=np.float64)
+    nr, nf = C.c_int32(0), C.c_int32(0)
+    _check(lib().oracle_split_candidates(
+        ptr(h, C.c_double), C.c_int64(len(h)), C.byref(cfg), C.c_uint32(num_bin),
+        C.c_int32(offset), C.c_uint32(default_bin), C.c_int32(int(skip_default_bin)),
+        C.c_int32(int(na_as_missing)), C.c_int32(int(run_forward)), C.c_double(sum_gradient),
+        C.c_double(sum_hessian), C.c_int32(num_data), ptr(rev, C.c_double), C.byref(nr),
+        ptr(fwd, C.c_double), C.byref(nf), C.c_int32(cap)))
+    return rev[:nr.value].copy(), fwd[:nf.value].copy()
+
+
 def data_partition(bins, num_bin, min_bin, max_bin, threshold, mfb, na_as_missing=False,
                    default_left=False):
     b = np.ascontiguousarray(bins, dtype=np.uint32)
@@ -148,9 +172,12 @@ def _meta_arr(meta):
     return arr
 
 
-def train_tree(bins_fm, meta, upper, grad, hess, cfg, num_leaves, max_depth=-1):
-    """bins_fm: [F, N] u8/u16/u32 feature-major.  Returns (tree dict, layout)."""
+def train_tree(bins_fm, meta, upper, grad, hess, cfg, num_leaves, max_depth=-1,
+               feature_contri=None):
+    """bins_fm: [F, N] u8/u16/u32 feature-major.  Returns (tree dict, layout).
+    feature_contri: per-feature gain multipliers by real feature index (or None)."""
     b, width = _bins_arg(bins_fm)
+    fc = None if feature_contri is None else np.ascontiguousarray(feature_contri, np.float64)
     F, N = b.shape
     marr = _meta_arr(meta)
     ub = None if upper is None else np.ascontiguousarray(upper, dtype=np.float64)
@@ -161,7 +188,9 @@ def train_tree(bins_fm, meta, upper, grad, hess, cfg, num_leaves, max_depth=-1):
     _check(lib().oracle_train_tree(b.ctypes.data_as(C.c_void_p), C.c_int32(width), C.c_int32(F),
                                    C.c_int64(N), marr, ptr(ub, C.c_double), ptr(g, C.c_float),
                                    ptr(h, C.c_float), C.byref(cfg), C.c_int32(num_leaves),
-                                   C.c_int32(max_depth), C.byref(tb.out), C.byref(lb.out)))
+                                   C.c_int32(max_depth), ptr(fc, C.c_double),
+                                   C.c_int32(0 if fc is None else len(fc)), C.byref(tb.out),
+                                   C.byref(lb.out)))
     t = tb.to_dict()
     nl = t["num_leaves"]
     layout = {"indices": lb.indices, "leaf_begin": lb.leaf_begin[:nl].copy(),

@@ -12,9 +12,13 @@ patterns); this script only re-encodes them.  Sources (under
   kernels/split.txt       -> split_scan.json    (format: kernel_parity.rs:285-360)
   kernels/subtract.txt    -> subtract.json
   kernels/partition.txt   -> partition.json     (format: kernel_parity.rs:1162-1220)
-  learner/spine_real.txt, learner/mfb_pos_real.txt -> learner_real.json
+  learner/spine_real.txt, learner/mfb_pos_real.txt, na_missing/model_real.txt,
+  gain_params/{penalty,max_delta_step,path_smooth}/model_real.txt -> learner_real.json
       (real lib_lightgbm 4.6 model text; the corpora are the ones the reference
-       test drives, oracle-harness/tests/learner_parity.rs:1214-1330)
+       tests drive: learner_parity.rs:1214-1330, na_missing_parity.rs:108-141,
+       gain_params_parity.rs:93-226)
+  path_smooth/path_smooth_golden.json -> path_smooth.npz
+      (real lightgbm 4.6 boosting runs; path_smooth_parity.rs:226-345)
 
 plus the hand-computed discretizer cases of
 crates/lgbm-treelearner/src/gradient_discretizer.rs:269-333 -> discretizer_cases.json.
@@ -182,11 +186,65 @@ def learner_real():
         num_bin=4, most_freq_bin=0, upper=real_upper_bounds(4, zero_sentinel_bin0=True),
         tree=parse_model_tree("learner/mfb_pos_real.txt")))
     for c in cases:
-        c["upper_bits"] = [f64bits(x) for x in c.pop("upper")]
         # single_feature_corpus (learner_parity.rs:1039-1062)
         c.update(hess=[1.0] * len(c["grad"]), min_data_in_leaf=1, min_sum_hessian_in_leaf=1e-3,
                  num_leaves=4, max_depth=-1, shrinkage=0.1)
+    # na_missing_parity.rs:108-141: NaN rows carry the top bin (num_bin - 1), missing
+    # type NaN, offset 1, default_bin out of range; num_leaves 2
+    cases.append(dict(
+        name="na_missing_real", golden_file="na_missing/model_real.txt",
+        bins=[0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 5, 5],
+        grad=[-6.0, -6.0, -5.0, -5.0, -1.0, -1.0, 1.0, 1.0, 5.0, 5.0, 6.0, 6.0],
+        num_bin=6, most_freq_bin=0, missing_type=2, default_bin=6,
+        upper=real_upper_bounds(6), tree=parse_model_tree("na_missing/model_real.txt"),
+        hess=[1.0] * 12, min_data_in_leaf=1, min_sum_hessian_in_leaf=1e-3, num_leaves=2,
+        max_depth=-1, shrinkage=0.1))
+    # gain_params_parity.rs:93-226: one corpus, three gain options (feature_contri 0.5,
+    # max_delta_step 0.7, path_smooth 2.0); split_gain compared too
+    for which, extra in (("penalty", dict(feature_contri=[0.5])),
+                         ("max_delta_step", dict(max_delta_step=0.7)),
+                         ("path_smooth", dict(path_smooth=2.0))):
+        c = dict(name="gain_params_" + which, golden_file=f"gain_params/{which}/model_real.txt",
+                 bins=[0, 0, 1, 1, 2, 2, 3, 3, 4, 4],
+                 grad=[-6.0, -6.0, -5.0, -5.0, -1.0, -1.0, 1.0, 1.0, 6.0, 6.0],
+                 num_bin=5, most_freq_bin=0, missing_type=0, default_bin=5,
+                 upper=real_upper_bounds(5),
+                 tree=parse_model_tree(f"gain_params/{which}/model_real.txt"),
+                 hess=[1.0] * 10, min_data_in_leaf=1, min_sum_hessian_in_leaf=1e-3,
+                 num_leaves=2, max_depth=-1, shrinkage=0.1, check_split_gain=True)
+        c.update(extra)
+        cases.append(c)
+    for c in cases:
+        c["upper_bits"] = [f64bits(x) for x in c.pop("upper")]
     return cases
+
+
+def path_smooth_golden():
+    """path_smooth/path_smooth_golden.json (the real lightgbm 4.6 binary, capture.py:
+    800 x 10 N(0,1) features, binary labels, 8 iterations, max_bin 63,
+    min_data_in_leaf 5, 13 (path_smooth, max_delta_step, lambda_l1, num_leaves) cells)
+    -> path_smooth.npz: X [800, 10] f64, y, cells [13, 4], per-cell raw predictions
+    and leaf values (flattened, with per-tree counts)."""
+    import numpy as np
+    with open(os.path.join(REF, "path_smooth/path_smooth_golden.json")) as f:
+        d = json.load(f)
+    n, m = d["num_rows"], d["num_cols"]
+    X = np.array([int(h, 16) for h in d["features_bits"]], dtype=np.uint64).view(np.float64)
+    y = np.array([int(h, 16) for h in d["labels_bits"]], dtype=np.uint64).view(np.float64)
+    cells, preds, flat, counts = [], [], [], []
+    for key in sorted(d["cells"]):
+        c = d["cells"][key]
+        cells.append([c["path_smooth"], c["max_delta_step"], c["lambda_l1"], c["num_leaves"]])
+        preds.append(np.array([int(h, 16) for h in c["pred_bits"]], dtype=np.uint64))
+        counts.append([len(t) for t in c["leaf_values"]])
+        for t in c["leaf_values"]:
+            flat.extend(t)
+    out = os.path.join(OUT, "path_smooth.npz")
+    np.savez_compressed(out, X=X.reshape(n, m), y=y, cells=np.array(cells, dtype=np.float64),
+                        pred_bits=np.stack(preds), leaf_flat=np.array(flat, dtype=np.float64),
+                        leaf_counts=np.array(counts, dtype=np.int32),
+                        num_iterations=np.int32(d["num_iterations"]))
+    return len(cells), out
 
 
 def discretizer_cases():
@@ -220,6 +278,8 @@ def main():
         with open(os.path.join(OUT, name), "w") as f:
             json.dump(data, f, separators=(",", ":"))
         print(name, len(data), os.path.getsize(os.path.join(OUT, name)), "bytes")
+    k, path = path_smooth_golden()
+    print(os.path.basename(path), k, os.path.getsize(path), "bytes")
 
 
 if __name__ == "__main__":

@@ -309,8 +309,28 @@ def test_grow_tree_config1_shape(be):
     assert np.array_equal(lay["indices"], olay["indices"])
 
 
+def _mrz(v):
+    z = float(np.float32(1e-35))
+    return np.where((v >= -z) & (v <= z), 0.0, v)
+
+
+def compare_boosted(trees, scores, otrees, oscores, init, tag):
+    """Device iterations vs the oracle's boosting loop, every field bit-exact.  The
+    oracle's first tree carries Tree::add_bias(init) (tree.rs:1161); the device
+    returns the shrunk tree and keeps the bias in the scores."""
+    assert len(trees) == len(otrees), tag
+    for i, (t, o) in enumerate(zip(trees, otrees)):
+        t = dict(t)
+        if i == 0 and init != 0.0:
+            t["leaf_value"] = _mrz(t["leaf_value"] + init)
+            t["internal_value"] = _mrz(t["internal_value"] + init)
+        _compare_trees(t, o, (tag, i))
+    assert np.array_equal(bits(scores), bits(oscores)), tag
+
+
 def test_train_binary_matches_oracle(be):
-    """Five resident boosting iterations (objective -> quantize -> grow -> score)."""
+    """Five resident boosting iterations (objective -> quantize -> grow -> score):
+    trees and training scores bit-exact."""
     n, iters, nl = 50_000, 5, 31
     bins, meta, ub, y = config1_like(n, seed=3)
     init = oracle.boost_from_score(y)
@@ -320,13 +340,46 @@ def test_train_binary_matches_oracle(be):
     trees = [be.train_iter_binary(i, cfg, nl, -1, 0.1) for i in range(iters)]
     scores = be.scores()
     oscores, otrees = oracle.train_binary(bins, meta, ub, y, cfg, nl, -1, iters, 0.1)
-    # the first tree carries add_bias(init) in the oracle model; compare structure
-    same = sum(int(np.array_equal(t["split_feature"], o["split_feature"]) and
-                   np.array_equal(t["threshold_in_bin"], o["threshold_in_bin"]) and
-                   np.array_equal(t["leaf_count"], o["leaf_count"]))
-               for t, o in zip(trees, otrees))
-    assert same == iters
-    np.testing.assert_allclose(scores, oscores, rtol=0, atol=1e-9)
+    compare_boosted(trees, scores, otrees, oscores, init, "train_binary")
+
+
+def test_config1_full_size_chain_matches_oracle():
+    """BASELINE configs[1] at its full size through the chain bench.py times: the raw
+    10.5M x 28 table -> BinMapper on the 200000-row sample -> device binning
+    (lgbm_hip_upload_raw) -> resident quantized boosting (4 bins, stochastic, 255
+    leaves).  Two iterations against the oracle's boosting loop on the device's own
+    bins: every tree field and every training score bit-exact
+    (gbdt.rs:691-1160)."""
+    from lightgbm_rs_amd import BinMapper, binary_boost_from_score, feature_meta, sample_indices
+    from lightgbm_rs_amd.synth import config1_raw_host
+    n, iters, nl = 10_500_000, 2, 255
+    say(f"config1 full-size chain n={n} iterations={iters}")
+    X, y = config1_raw_host(n)
+    idx = sample_indices(n, 200000, 1)
+    ms = [BinMapper.from_sampled_column(X[f, idx].astype(np.float64), n, max_bin=63)
+          for f in range(28)]
+    meta = [feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f)
+            for f, m in enumerate(ms)]
+    assert any(m.most_freq_bin > 0 for m in meta) and any(m.most_freq_bin == 0 for m in meta)
+    ub = np.concatenate([m.upper_bounds for m in ms])
+    init = binary_boost_from_score(y)
+    cfg = GainConfig.make(min_data_in_leaf=20, min_sum_hessian_in_leaf=1e-3)
+    b = HipBackend(0)
+    try:
+        b.upload_raw(X, ms, col_major=True)
+        b.set_labels(y, init)
+        trees = [b.train_iter_binary(i, cfg, nl, -1, 0.1, 4, True) for i in range(iters)]
+        scores = b.scores()
+        bins = b.get_bins()
+    finally:
+        b.close()
+    del X
+    say("  device done, oracle ...")
+    oscores, otrees = oracle.train_binary(bins, meta, ub, y, cfg, nl, -1, iters, 0.1,
+                                          boost_from_average=True, quantized=True, quant_bins=4,
+                                          stochastic=True)
+    assert trees[0]["num_leaves"] == nl
+    compare_boosted(trees, scores, otrees, oscores, init, "config1 full size")
 
 
 def test_graph_replays_match_eager():
