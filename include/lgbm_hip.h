@@ -249,6 +249,24 @@ int lgbm_hip_find_best_splits(lgbm_hip_ctx* ctx, const double* hist, int64_t his
                               const lgbm_gain_config* cfg, double sum_gradient,
                               double sum_hessian, int32_t num_data, lgbm_split_info* out);
 
+/* The same scans over device-resident inputs with no allocation at all: hist
+ * (hist_len doubles), feats (n_feats lgbm_batched_feature) and out (n_feats
+ * lgbm_split_info) are device memory of the context's device; cfg is a host struct.
+ * No counterpart in the reference: this is for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  Its working memory is one fixed library-owned device array per GPU
+ * (LGBM_HIP_NOALLOC_MAX_FEATURES feature descriptors), held until the process ends
+ * and shared by every context on that GPU: calls that overlap on one GPU race.
+ * n_feats above the maximum returns LGBM_HIP_ERR_CAPABILITY before any work; a
+ * feature the host entry would refuse returns the same status (first such feature
+ * in order) after the scans, with out undefined for it. */
+#define LGBM_HIP_NOALLOC_MAX_FEATURES 8192
+int lgbm_hip_find_best_splits_noalloc(lgbm_hip_ctx* ctx, const double* d_hist, int64_t hist_len,
+                                      const lgbm_batched_feature* d_feats, int32_t n_feats,
+                                      const lgbm_gain_config* cfg, double sum_gradient,
+                                      double sum_hessian, int32_t num_data,
+                                      lgbm_split_info* d_out);
+
 /* Elementwise larger = parent - smaller (`Backend::subtract_histograms`,
  * lib.rs:1314; kernels/subtract.rs:204-215). */
 int lgbm_hip_subtract_histograms(lgbm_hip_ctx* ctx, const double* parent, const double* child,

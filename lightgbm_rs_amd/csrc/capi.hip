@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <type_traits>
 #include <vector>
@@ -42,6 +43,14 @@ void launch_contrib(const PredNode* nodes, const PredTree* trees, const double* 
                     int32_t ntpi, int32_t depth, void* ws, double* out, hipStream_t s,
                     const KernelEvents* ev);
 }
+
+// Working memory of lgbm_hip_find_best_splits_noalloc: a 256-byte header (word 0:
+// the first invalid feature's error code) and the converted feature table.  Host
+// code never uses this name for memory: each device's address comes from
+// hipGetSymbolAddress at context creation (noalloc_scratch_ptr).
+#define NOALLOC_HEADER 256
+static __device__ __align__(256) unsigned char
+    scratch[NOALLOC_HEADER + (size_t)LGBM_HIP_NOALLOC_MAX_FEATURES * sizeof(DevFeature)];
 
 namespace {
 
@@ -81,6 +90,7 @@ struct lgbm_hip_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   std::string err;
+  unsigned char* noalloc = nullptr;  // this device's `scratch` (hipGetSymbolAddress)
   // shape
   int64_t N = 0;
   int32_t F = 0, W = 0, total_cells = 0;
@@ -165,6 +175,23 @@ struct lgbm_hip_ctx {
 };
 
 namespace {
+
+// Per-device address of `scratch`, resolved once per device with that device current.
+std::mutex g_noalloc_mu;
+std::vector<unsigned char*> g_noalloc_ptr;
+
+int noalloc_scratch_ptr(int device, unsigned char** out) {
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if ((int)g_noalloc_ptr.size() <= device) g_noalloc_ptr.resize((size_t)device + 1, nullptr);
+  if (!g_noalloc_ptr[(size_t)device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return (int)e ? (int)e : -1;
+    g_noalloc_ptr[(size_t)device] = (unsigned char*)p;
+  }
+  *out = g_noalloc_ptr[(size_t)device];
+  return 0;
+}
 
 int set_err(lgbm_hip_ctx* c, int code, const std::string& m) {
   if (c)
@@ -868,6 +895,8 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   if (hipHostMalloc((void**)&c->done_host, 64, hipHostMallocDefault) != hipSuccess)
     return fail(set_err(c, LGBM_HIP_ERR_HIP, "hipHostMalloc"));
   if ((rc = init_jump_tables(c))) return fail(rc);
+  if (noalloc_scratch_ptr(device, &c->noalloc) != 0)
+    return fail(set_err(c, LGBM_HIP_ERR_HIP, "hipGetSymbolAddress(scratch) failed"));
   if ((rc = dalloc(c, &c->partials, STAT_BLOCKS))) return fail(rc);
   if ((rc = dalloc(c, &c->d_flags, 2))) return fail(rc);
   int cus = 0;
@@ -1479,6 +1508,80 @@ int lgbm_hip_find_best_splits(lgbm_hip_ctx* c, const double* hist, int64_t hist_
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));
   HIPCHK(c, hipMemcpy(out, d_out, (size_t)n_feats * sizeof(lgbm_split_info), hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
+}
+
+}  // extern "C"
+
+// lgbm_hip_find_best_splits_noalloc's feature table: the host entry's checks and
+// feature_from_batched on the device.  One block; word 0 of the header receives the
+// smallest (feature * 4 + check) that fails (0 num_bin == 0, 1 num_bin > 256,
+// 2 region past hist_len), ~0 for none.  A failing feature gets num_bin 0, which the
+// scan reads as an empty feature.
+__global__ __launch_bounds__(256) void k_noalloc_feats(const lgbm_batched_feature* __restrict__ in,
+                                                       int32_t n, int64_t hist_len,
+                                                       unsigned char* __restrict__ ws) {
+  uint32_t* err = (uint32_t*)ws;
+  DevFeature* out = (DevFeature*)(ws + NOALLOC_HEADER);
+  if (threadIdx.x == 0) *err = ~0u;
+  __syncthreads();
+  for (int32_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const lgbm_batched_feature b = in[i];
+    int32_t bad = -1;
+    if (b.num_bin == 0) bad = 0;
+    else if (b.num_bin > 256) bad = 1;
+    else if (b.slot_off + 2ull * b.num_bin > (uint64_t)hist_len) bad = 2;
+    DevFeature f{};
+    f.num_bin = bad < 0 ? b.num_bin : 0u;
+    f.offset = b.offset;
+    f.default_bin = b.default_bin;
+    f.mfb = b.most_freq_bin;
+    f.slot_off = bad < 0 ? (uint32_t)b.slot_off : 0u;
+    f.cell_base = f.slot_off / 2;
+    f.skip_default_bin = b.skip_default_bin;
+    f.na_as_missing = b.na_as_missing;
+    f.run_forward = b.run_forward;
+    f.real_index = -1;
+    f.penalty = 1.0;
+    out[i] = f;
+    if (bad >= 0) atomicMin(err, (uint32_t)i * 4u + (uint32_t)bad);
+  }
+}
+
+extern "C" {
+
+int lgbm_hip_find_best_splits_noalloc(lgbm_hip_ctx* c, const double* d_hist, int64_t hist_len,
+                                      const lgbm_batched_feature* d_feats, int32_t n_feats,
+                                      const lgbm_gain_config* cfg, double sum_gradient,
+                                      double sum_hessian, int32_t num_data,
+                                      lgbm_split_info* d_out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
+  if (!d_hist || !d_feats || !cfg || !d_out || n_feats < 0 || hist_len < 0)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null argument or negative size");
+  if (n_feats > LGBM_HIP_NOALLOC_MAX_FEATURES)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "n_feats " + std::to_string(n_feats) + " exceeds the no-allocation maximum " +
+                       std::to_string(LGBM_HIP_NOALLOC_MAX_FEATURES));
+  if (n_feats == 0) return LGBM_HIP_OK;
+  if (!c->noalloc) return set_err(c, LGBM_HIP_ERR_HIP, "no-allocation working memory unresolved");
+  if (!(sum_hessian > 0.0))
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "find_best_split: sum_hessian must be > 0");
+  k_noalloc_feats<<<dim3(1), dim3(256), 0, c->stream>>>(d_feats, n_feats, hist_len, c->noalloc);
+  launch_scan_explicit(d_hist, (const DevFeature*)(c->noalloc + NOALLOC_HEADER), n_feats, *cfg,
+                       sum_gradient, sum_hessian, num_data, d_out, c->stream);
+  HIPCHK(c, hipGetLastError());
+  uint32_t err = 0;
+  HIPCHK(c, hipMemcpyAsync(&err, c->noalloc, sizeof(err), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (err != ~0u) {
+    const uint32_t f = err / 4u, k = err % 4u;
+    if (k == 0) return set_err(c, LGBM_HIP_ERR_RUNTIME, "num_bin must be > 0 (feature " + std::to_string(f) + ")");
+    if (k == 1) return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be <= 256 (feature " + std::to_string(f) + ")");
+    return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH,
+                   "feature region beyond the histogram (feature " + std::to_string(f) + ")");
+  }
   return LGBM_HIP_OK;
 }
 
