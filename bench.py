@@ -8,10 +8,15 @@ table is binned by the library (BinMapper on a 200k-row sample on the host, then
 ValueToBin on the device) before the timed region; the binning kernel and a batch
 prediction with the trained trees are reported as secondary lines (`next_rows`).
 
-Prints ONE JSON line.  `value` is seconds per 100 trees (lower is better); the
-histogram bandwidth of the dominant kernel is reported in `roofline`, timed with HIP
-events on the library's own stream.  `cpu_baseline` times the CPU restatement of the
-reference learner (oracle/) on a bounded sample of the same workload.
+Prints ONE JSON line.  `value` is seconds per 100 trees (lower is better) over the
+timed iterations 0 .. K-1 (default K = 100: the metric's first 100 trees), the first
+of `--repeats` timed runs (their median is reported beside it).  `roofline` is the
+dominant kernel at the survey's algorithmic bytes, timed with HIP events on the
+library's own stream; `hist_GBps` is every ConstructHistogram of the iterations at
+those bytes over the kernels that perform them.  `cpu_baseline` times the CPU
+restatement of the reference learner (oracle/) on a bounded sample of the same
+workload and bins (all cores and one thread), and `parity` compares the device's
+first iterations with that run's trees and scores, bit for bit.
 """
 import argparse
 import json
@@ -64,16 +69,78 @@ def _line(kernel, ms, launches, bytes_per_launch, workload, walks=None):
     return out
 
 
+def cpu_info():
+    """(CPU model name, physical cores) of this host from /proc/cpuinfo."""
+    model, cores = None, set()
+    try:
+        phys = core = None
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model is None:
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+            elif not k and phys is not None:
+                cores.add((phys, core))
+                phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    return model, (len(cores) or None)
+
+
+def compare_iterations(trees, scores, otrees, oscores, init):
+    """The device's first iterations vs the CPU baseline's: every tree field and every
+    training score bit-exact (the oracle's first tree carries Tree::add_bias(init))."""
+    import numpy as np
+    z = float(np.float32(1e-35))
+
+    def mrz(v):
+        return np.where((v >= -z) & (v <= z), 0.0, v)
+
+    bad = []
+    for i, (t, o) in enumerate(zip(trees, otrees)):
+        t = dict(t)
+        if i == 0 and init != 0.0:
+            t["leaf_value"] = mrz(t["leaf_value"] + init)
+            t["internal_value"] = mrz(t["internal_value"] + init)
+        if t["num_leaves"] != o["num_leaves"]:
+            bad.append(f"tree {i} num_leaves")
+            continue
+        for k in o:
+            if k == "num_leaves":
+                continue
+            a, b = np.ascontiguousarray(t[k]), np.ascontiguousarray(o[k])
+            if a.shape != b.shape or a.tobytes() != b.tobytes():
+                bad.append(f"tree {i} {k}")
+    same_scores = bool(np.ascontiguousarray(scores).tobytes() ==
+                       np.ascontiguousarray(oscores).tobytes())
+    return {"iterations": len(trees), "trees_bit_exact": not bad, "mismatches": bad[:8],
+            "scores_bit_exact": same_scores,
+            "leaves": [int(t["num_leaves"]) for t in trees]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--rows", type=int, default=10_500_000)
     ap.add_argument("--num-leaves", type=int, default=255)
-    ap.add_argument("--cpu-iters", type=int, default=2,
-                    help="boosting iterations of the CPU baseline sample (0 disables)")
-    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--cpu-iters", type=int, default=5,
+                    help="boosting iterations of the all-core CPU baseline sample, also "
+                         "replayed on the device for the parity check (0 disables both)")
+    ap.add_argument("--cpu-iters-1t", type=int, default=3,
+                    help="boosting iterations of the 1-thread CPU baseline sample")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="all-core thread count (default: OMP_NUM_THREADS, else usable CPUs)")
+    ap.add_argument("--repeats", type=int, default=3,
+                    help="timed loops of --steps iterations; value is the first, the median "
+                         "of all is reported beside it")
     ap.add_argument("--prof-steps", type=int, default=3,
                     help="extra iterations timed per kernel with HIP events")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -131,23 +198,41 @@ def main():
     for i in range(args.warmup):
         be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=False)
     torch.cuda.synchronize() if dev is not None else None
+    # Timed: iterations 0 .. K-1 of the boosting run (the score is reset to the init
+    # score before each repeat, so every repeat does the same work as a fresh run of
+    # the first K iterations; the warmup only captured the per-tree graph).
     leaves, trees = [], []
-    t2 = time.perf_counter()
-    for i in range(args.warmup, args.warmup + args.steps):
-        t = be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=True)
-        leaves.append(t["num_leaves"])
-        trees.append(t)
-    torch.cuda.synchronize() if dev is not None else None
-    elapsed = time.perf_counter() - t2
+    runs = []
+    for rep in range(max(args.repeats, 1)):
+        be.set_labels(y, init)
+        torch.cuda.synchronize() if dev is not None else None
+        t2 = time.perf_counter()
+        for i in range(args.steps):
+            t = be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=True)
+            if rep == 0:
+                leaves.append(t["num_leaves"])
+                trees.append(t)
+        torch.cuda.synchronize() if dev is not None else None
+        runs.append(time.perf_counter() - t2)
+    elapsed = runs[0]
+    it = args.steps
     # Per-kernel device time: HIP events around every launch on the library's stream.
     # The per-tree sequence then runs as individual launches (no graph), so this pass
     # measures kernel durations, not the timed loop's wall clock.
     be.set_lookahead(False)
     be.set_timing(True)
-    it0 = args.warmup + args.steps
+    it0 = it
     for i in range(it0, it0 + args.prof_steps):
         be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=False)
     tm = be.timing()
+    # parity leg (outside the timed region): the first cpu_iters iterations again from
+    # the initial score, for the bit-exact comparison with the CPU baseline's trees
+    gpu_iters = None
+    if args.cpu_iters > 0:
+        be.set_labels(y, init)
+        gpu_iters = [be.train_iter_binary(i, cfg, nl, -1, lr, 4, True, want_tree=True)
+                     for i in range(args.cpu_iters)]
+        gpu_scores = be.scores()
     # secondary: batch prediction of the timed iterations' trees on the first
     # `pred_rows` rows (row-major f32, as the predictor reads them)
     model = Model.create(num_class=1, max_feature_idx=27, objective="binary sigmoid:1")
@@ -175,42 +260,78 @@ def main():
     ms_per_step = elapsed / args.steps * 1e3
     s_per_100 = elapsed / args.steps * 100.0
     F, cells, rec = tm["features"], tm["cells"], tm["record_bytes"]
-    # Algorithmic bytes.  Root ConstructHistogram: rows x (F bin bytes + 2 B packed
-    # g/h) + cells x 2 x 4 B written.  Partition round (also builds one child's
-    # histogram per split): rows x (record + 2 B g/h) read and written + cells x 2 x
-    # 4 B per split.
-    root_bytes = tm["root_rows"] * (F + 2) + tm["hist_launches"] * cells * 8
-    part_bytes = tm["partition_rows"] * 2 * (rec + 2) + tm["partition_jobs"] * cells * 8
+    # Algorithmic bytes (the survey's per-unit figures; u8 bins, packed int8 g/h, u32
+    # row index, int32 histogram cells):
+    #   root ConstructHistogram: rows x (F + 2) + cells x 2 x 4 per launch;
+    #   a split's DataPartition: parent rows x (4 + 1 + 4) (index in, bin, index out);
+    #   its smaller child's ConstructHistogram: rows x (F + 2 + 4) + cells x 2 x 4.
+    # k_partition does both for every split of a round.  The bytes it actually moves
+    # (records of `rec` bytes + 2 B g/h, read and written) are reported as `design`.
+    hist_w = cells * 8
+    root_bytes = tm["root_rows"] * (F + 2) + tm["hist_launches"] * hist_w
+    part_bytes = (tm["partition_rows"] * 9 + tm["hist_child_rows"] * (F + 6)
+                  + tm["partition_jobs"] * hist_w)
+    design_bytes = tm["partition_rows"] * 2 * (rec + 2) + tm["partition_jobs"] * hist_w
     root_gbs = root_bytes / (tm["hist_ms"] * 1e-3) / 1e9 if tm["hist_ms"] > 0 else 0.0
     part_gbs = part_bytes / (tm["partition_ms"] * 1e-3) / 1e9 if tm["partition_ms"] > 0 else 0.0
+    design_gbs = design_bytes / (tm["partition_ms"] * 1e-3) / 1e9 if tm["partition_ms"] > 0 else 0.0
+    # every ConstructHistogram of the iterations (root + each split's child) over the
+    # time of the kernels that perform them (the child builds are fused into k_partition)
+    build_bytes = root_bytes + tm["hist_child_rows"] * (F + 6) + tm["partition_jobs"] * hist_w
+    build_ms = tm["hist_ms"] + tm["partition_ms"]
+    hist_gbs = build_bytes / (build_ms * 1e-3) / 1e9 if build_ms > 0 else 0.0
+    launches = tm["partition_launches"]
     if tm["partition_ms"] >= tm["hist_ms"]:
         dom = ("k_partition (DataPartition + smaller-child ConstructHistogram, fused)", part_gbs,
-               part_bytes, tm["partition_launches"], tm["partition_ms"])
+               part_bytes, launches, tm["partition_ms"])
     else:
         dom = ("k_hist_jobs (ConstructHistogram, root)", root_gbs, root_bytes, tm["hist_launches"],
                tm["hist_ms"])
-    log(f"gpu: {ms_per_step:.2f} ms/step, leaves {min(leaves)}..{max(leaves)}, timing {tm}")
+    log(f"gpu: {ms_per_step:.2f} ms/step (repeats {[round(r / args.steps * 1e3, 3) for r in runs]}),"
+        f" leaves {min(leaves)}..{max(leaves)}, timing {tm}")
 
-    cpu = None
+    cpu, parity = None, None
     if args.cpu_iters > 0:
         from oracle import oracle
         from lightgbm_rs_amd import feature_meta
         meta = [feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f)
                 for f, m in enumerate(mappers)]
         ub = np.concatenate([m.upper_bounds for m in mappers])
-        threads = args.cpu_threads or (os.cpu_count() or 1)
-        threads = oracle.set_threads(threads)
+        env_threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+        want = args.cpu_threads or env_threads or len(os.sched_getaffinity(0))
+        threads = oracle.set_threads(want)
         tc = time.perf_counter()
-        oracle.train_binary(bins, meta, ub, y, cfg, nl, -1, args.cpu_iters, lr,
-                            boost_from_average=True, quantized=True, quant_bins=4,
-                            stochastic=True, want_trees=False)
+        oscores, otrees = oracle.train_binary(bins, meta, ub, y, cfg, nl, -1, args.cpu_iters, lr,
+                                              boost_from_average=True, quantized=True,
+                                              quant_bins=4, stochastic=True, want_trees=True)
         cs = time.perf_counter() - tc
-        cpu = {"value": cs / args.cpu_iters * 100.0, "unit": "s/100 trees", "cores": threads,
-               "kind": "port",
-               "sample": f"{args.cpu_iters} boosting iterations of the same {n}x28 workload "
-                         f"(C++ restatement of the reference CpuBackend learner, OpenMP), "
-                         f"extrapolated to 100 trees; {cs:.1f}s measured"}
         log(f"cpu: {cs:.1f}s for {args.cpu_iters} iters on {threads} threads")
+        one = None
+        if args.cpu_iters_1t > 0:
+            oracle.set_threads(1)
+            t1c = time.perf_counter()
+            oracle.train_binary(bins, meta, ub, y, cfg, nl, -1, args.cpu_iters_1t, lr,
+                                boost_from_average=True, quantized=True, quant_bins=4,
+                                stochastic=True, want_trees=False)
+            one = time.perf_counter() - t1c
+            oracle.set_threads(threads)
+            log(f"cpu: {one:.1f}s for {args.cpu_iters_1t} iters on 1 thread")
+        model_name, phys = cpu_info()
+        cpu = {"value": round(cs / args.cpu_iters * 100.0, 3), "unit": "s/100 trees",
+               "cores": threads, "kind": "port",
+               "sample": f"the first {args.cpu_iters} boosting iterations of the same "
+                         f"{n}x28 workload and bins (C++ restatement of the reference "
+                         f"CpuBackend learner, OpenMP, {threads} threads: {cs:.1f}s), scaled "
+                         f"to 100 trees",
+               "one_thread": None if one is None else {
+                   "value": round(one / args.cpu_iters_1t * 100.0, 3), "unit": "s/100 trees",
+                   "sample": f"the first {args.cpu_iters_1t} iterations on 1 thread: "
+                             f"{one:.1f}s"},
+               "cpu_model": model_name, "physical_cores": phys,
+               "usable_cpus": len(os.sched_getaffinity(0)),
+               "gpu_speedup": round((cs / args.cpu_iters) / (elapsed / args.steps), 1)}
+        parity = compare_iterations(gpu_iters, gpu_scores, otrees, oscores, init)
+        log(f"parity: {parity}")
 
     out = {
         "metric": "histogram GB/s + sec per 100 trees, 10.5M x 28 quantized-grad, 1 MI355X",
@@ -229,15 +350,20 @@ def main():
         "config": {"workload": "configs[1]: binary, 10.5M rows x 28 features, max_bin 63, "
                                "num_leaves 255, quantized int8 grads (4 bins, stochastic)",
                    "rows": n, "features": 28, "num_leaves": nl, "learning_rate": lr},
+        "ms_per_step_median": round(sorted(runs)[len(runs) // 2] / args.steps * 1e3, 4),
+        "ms_per_step_runs": [round(r / args.steps * 1e3, 4) for r in runs],
+        "hist_GBps": round(hist_gbs, 2),
         "hist_GBps_root": round(root_gbs, 2),
-        "partition_hist_GBps": round(part_gbs, 2),
         "roofline": {"bound": "hbm", "achieved": round(dom[1], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dom[1] / HBM_PEAK_GBS, 4),
                      "traffic": traffic_for(dom[0].split()[0]),
                      "kernel": dom[0],
                      "bytes_per_launch": round(dom[2] / max(dom[3], 1), 1),
                      "launches": int(dom[3]),
-                     "avg_launch_us": round(dom[4] * 1e3 / max(dom[3], 1), 3)},
+                     "avg_launch_us": round(dom[4] * 1e3 / max(dom[3], 1), 3),
+                     "design_bytes_per_launch": round(design_bytes / max(launches, 1), 1),
+                     "design_GBps": round(design_gbs, 2)},
+        "parity": parity,
         "phase_ms_per_step": {k: round(tm[k] / tsteps, 4) for k in
                               ("hist_ms", "partition_ms", "scan_ms", "quant_ms", "objective_ms")},
         "cpu_baseline": cpu,

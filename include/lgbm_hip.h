@@ -355,8 +355,9 @@ int lgbm_hip_get_timing(lgbm_hip_ctx* ctx, double* ms_out5, double* hist_bytes_o
  * that the tree never used); [13] partition rounds over all trees; [14] trees;
  * [15] rounds launched after the captured per-tree sequence; [16] ms in the binning
  * kernel (lgbm_hip_upload_raw*), [17] its launches, [18] values binned; [19] ms in
- * the prediction kernel, [20] its launches, [21] rows x trees walked. */
-int lgbm_hip_get_stats(lgbm_hip_ctx* ctx, double* out22);
+ * the prediction kernel, [20] its launches, [21] rows x trees walked; [22] rows
+ * whose histogram the partition passes built (the child each split builds). */
+int lgbm_hip_get_stats(lgbm_hip_ctx* ctx, double* out23);
 
 /* ---- binning ------------------------------------------------------------------ */
 

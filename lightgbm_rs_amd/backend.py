@@ -250,13 +250,13 @@ class HipBackend:
 
     def timing(self):
         """Per-family device ms (HIP events) and row counters since set_timing."""
-        st = np.zeros(22, np.float64)
+        st = np.zeros(23, np.float64)
         self._check(self.lib.lgbm_hip_get_stats(self.ctx, ptr(st, C.c_double)))
         keys = ["hist_ms", "partition_ms", "scan_ms", "quant_ms", "objective_ms", "root_rows",
                 "hist_launches", "partition_rows", "partition_launches", "record_bytes",
                 "features", "cells", "partition_jobs", "rounds", "trees", "extra_rounds",
                 "bin_ms", "bin_launches", "bin_values", "predict_ms", "predict_launches",
-                "predict_walks"]
+                "predict_walks", "hist_child_rows"]
         return {k: float(v) for k, v in zip(keys, st)}
 
 

@@ -1830,7 +1830,7 @@ int lgbm_hip_set_timing(lgbm_hip_ctx* c, int32_t enable) {
 
 int lgbm_hip_get_timing(lgbm_hip_ctx* c, double* ms_out5, double* hist_bytes_out,
                         int64_t* hist_launches_out) {
-  double st[22];
+  double st[23];
   int rc = lgbm_hip_get_stats(c, st);
   if (rc) return rc;
   if (ms_out5)
@@ -1868,6 +1868,7 @@ int lgbm_hip_get_stats(lgbm_hip_ctx* c, double* out) {
   out[19] = c->ms[FAM_PRED];
   out[20] = c->pred_launches;
   out[21] = c->pred_walks;
+  out[22] = st[5];
   return LGBM_HIP_OK;
 }
 

@@ -744,6 +744,8 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
         }
         atomicAdd(&L.stats[0], (double)count);
         atomicAdd(&L.stats[4], 1.0);
+        // rows whose histogram this pass built (the side predicted smaller)
+        if (!FP && J.acc_right >= 0) atomicAdd(&L.stats[5], (double)(J.acc_right ? rc : lc));
       } else {
         ctl->part_left_count = lc;
       }

@@ -128,7 +128,8 @@ struct DevLearner {
   int32_t* plan_state;          // [5][MAX_LEAVES] leaf / node linkage owned by k_plan
   uint64_t* tile_state;         // stable per-op partition: left-row prefix per tile
   double* stats;                // [0] rows partitioned, [1] partition launches, [2] root
-                                // rows, [3] root launches, [4] partition jobs
+                                // rows, [3] root launches, [4] partition jobs, [5] rows
+                                // histogrammed by partition passes
   DevNodes nodes;
   DevLeaves leaves;
   DevTree tree;
