@@ -115,8 +115,9 @@ struct lgbm_hip_ctx {
   float *g = nullptr, *h = nullptr, *label = nullptr;
   double* score = nullptr;
   int32_t* hist_part = nullptr;  // [HIST_SLOTS][cells][3]
+  int32_t* hist_sum = nullptr;   // [cells][3]
   int32_t* hist_acc = nullptr;   // [SPEC_MAX][cells][3]
-  int32_t* part_slots = nullptr; // [part_blocks + SPEC_MAX][cells] int4
+  unsigned long long* part_slots = nullptr;  // [part_blocks + SPEC_MAX][cells] packed
   int64_t* hist_part64 = nullptr;  // [HIST_SLOTS][cells][2]
   int64_t* int_slots64 = nullptr;  // [SLOT_CAP][cells][2]
   int32_t n_fgroups = 0;
@@ -281,6 +282,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.N = c->N;
   L.slot_len = c->slot_len;
   L.hist_part = c->hist_part;
+  L.hist_sum = c->hist_sum;
   L.hist_acc = c->hist_acc;
   L.part_slots = c->part_slots;
   L.hist_part64 = c->hist_part64;
@@ -765,7 +767,7 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "histogram exceeds the LDS budget");
   if (acc > (uint32_t)(MAX_FGROUPS - 1) * (HIST_FP_CELLS - 256))
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "too many histogram cells for the f32 feature groups");
-  if (acc > HIST_WAVE_CELLS && num_data > (int64_t)HIST_GRID * HIST_BLOCK_MAX_ROWS)
+  if (acc > HIST_WAVE_CELLS && num_data > (int64_t)HIST_GRID_Q * HIST_BLOCK_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "rows per histogram block exceed the packed LDS cell fields");
   c->F = F;
@@ -794,6 +796,7 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   if ((rc = dalloc(c, &c->g, (size_t)num_data))) return rc;
   if ((rc = dalloc(c, &c->h, (size_t)num_data))) return rc;
   if ((rc = dalloc(c, &c->hist_part, (size_t)HIST_SLOTS * acc * 3))) return rc;
+  if ((rc = dalloc(c, &c->hist_sum, (size_t)acc * 3))) return rc;
   if ((rc = dalloc(c, &c->hist_part64, (size_t)HIST_SLOTS * acc * 2))) return rc;
   // feature groups of the f32 histogram kernel: consecutive features whose cells fit
   // one block's LDS
@@ -813,7 +816,7 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   }
   if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * acc * 3))) return rc;
   HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * acc * 3 * 4));
-  if ((rc = dalloc(c, &c->part_slots, ((size_t)c->part_blocks + SPEC_MAX) * acc * 4))) return rc;
+  if ((rc = dalloc(c, &c->part_slots, ((size_t)c->part_blocks + SPEC_MAX) * acc))) return rc;
   if ((rc = ensure_tile_state(c, num_data))) return rc;
   return LGBM_HIP_OK;
 }
@@ -934,6 +937,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->label);
   F(c->score);
   F(c->hist_part);
+  F(c->hist_sum);
   F(c->hist_acc);
   F(c->part_slots);
   F(c->hist_part64);

@@ -465,6 +465,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     J.tile0 = 0;
     ctl->jobs[j] = J;
     ctl->part_cur[j] = 0ull;
+    ctl->acc_used[j] = 0;
     s_ntiles[j] = J.ntiles;
     nd.child[2 * p] = cl;
     nd.child[2 * p + 1] = cr;
@@ -571,17 +572,19 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   int32_t held = 0;       // tiles of that job in the LDS histogram
   bool flushed = false;   // this block already flushed part of that job
   // Where this block's cells of job `cur` go: a job spread over at most PART_SLOT_MAX
-  // blocks gets one slot per block (slot block + job: unique, since blocks and jobs
-  // both advance along the tile order), which k_pair_scan sums; a wider job gets
-  // atomic adds into its accumulator (cleared by k_pair_scan).
+  // blocks gets one packed slot per block (slot block + job: unique, since blocks and
+  // jobs both advance along the tile order), which k_pair_scan sums; a wider job, and
+  // a block's second and later flush of one job, atomic adds into the job's
+  // accumulator and marks it used (k_pair_scan then reads and clears it).
   auto flush = [&]() {
     const PartJob& C = s_jobs[cur];
-    if (part_span_blocks(C.tile0, C.ntiles, total, G) <= PART_SLOT_MAX)
-      lds_hist_flush_clear(lds_hist, cells,
-                           L.part_slots + ((size_t)blockIdx.x + cur) * cells * 4,
-                           flushed ? FLUSH_ADD : FLUSH_STORE);
-    else
+    if (!flushed && part_span_blocks(C.tile0, C.ntiles, total, G) <= PART_SLOT_MAX) {
+      lds_hist_flush_clear(lds_hist, cells, L.part_slots + ((size_t)blockIdx.x + cur) * cells,
+                           FLUSH_STORE);
+    } else {
+      if (tid == 0) ctl->acc_used[cur] = 1;
       lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3, FLUSH_ATOMIC);
+    }
   };
   struct TileBuf {
     uint4 w[PR][W];
@@ -672,7 +675,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
       const bool want_left = J.acc_right == 0;
 #pragma unroll
       for (int k = 0; k < PR; ++k)
-        if (valid[k] && isleft[k] == want_left)
+        if (valid[k] && isleft[k] == want_left && gh_bits(q[k]) != 0u)
           lds_hist_add<W>(lds_hist, cbr, nw, w[k], gh_bits(q[k]));
       ++held;
     }
@@ -851,6 +854,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
   const int32_t n_jobs = ctl->n_jobs;
   const PartJob& J = ctl->jobs[j];  // slot j always exists; its fields are used below
   const int32_t p = J.parent, cl = J.cl, cr = J.cr, acc_right = J.acc_right;
+  const int32_t acc_used = ctl->acc_used[j];
   const int32_t jnt = J.ntiles;
   const int64_t jt0 = J.tile0;
   const DevFeature ft = L.feats[f];
@@ -897,21 +901,32 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
       }
     }
   } else {
-    // the side built in the partition pass: the job's per-block slots (the blocks of
-    // the partition launch from the one holding its first tile to the one holding
-    // its last, slot = block + j; blocks without tiles wrote nothing), or its
-    // accumulator (read and cleared even when the children are gated)
+    // the side built in the partition pass: for a job spread over few blocks its
+    // per-block slots (the blocks of the partition launch from the one holding its
+    // first tile to the one holding its last, slot = block + j; blocks without tiles
+    // wrote nothing), plus the job's accumulator when a flush used it (read and
+    // cleared even when the children are gated)
     const int64_t s0 = jnt > 0 ? part_owner(jt0, T, part_grid) : 0;
     const int64_t s1 = jnt > 0 ? part_owner(jt0 + jnt - 1, T, part_grid) : -1;
     const bool use_slots = jnt > 0 ? part_span_blocks(jt0, jnt, T, part_grid) <= PART_SLOT_MAX : true;
+    const bool read_acc = !use_slots || acc_used != 0;
     int32_t* acc = L.hist_acc + (size_t)j * cells * 3;
-    const int4* slots = (const int4*)L.part_slots;
+    const unsigned long long* slots = L.part_slots;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int b = tid + SCAN_THREADS * q;
       if (b >= nb) continue;
       const size_t ci = (size_t)(ft.cell_base + b);
       int32_t AG = 0, AH = 0, AT = 0;
+      if (read_acc) {
+        int32_t* a = acc + ci * 3;
+        AG = a[0];
+        AH = a[1];
+        AT = a[2];
+        a[0] = 0;
+        a[1] = 0;
+        a[2] = 0;
+      }
       if (use_slots) {
         // at most PART_SLOT_MAX blocks, enumerated without a dependent chain so all
         // their loads are issued before the sums: with fewer tiles than blocks each
@@ -926,19 +941,12 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
             k = s0 + u;
             if (k > s1) continue;
           }
-          const int4 a = slots[(size_t)(k + j) * cells + ci];
-          AG += a.x;
-          AH += a.y;
-          AT += a.z;
+          int32_t sg_, sh_, st_;
+          unpack_cell(slots[(size_t)(k + j) * cells + ci], &sg_, &sh_, &st_);
+          AG += sg_;
+          AH += sh_;
+          AT += st_;
         }
-      } else {
-        int32_t* a = acc + ci * 3;
-        AG = a[0];
-        AH = a[1];
-        AT = a[2];
-        a[0] = 0;
-        a[1] = 0;
-        a[2] = 0;
       }
       if (gated) continue;
       const int32_t* ps = L.int_slots + ((size_t)p * cells + ci) * 3;

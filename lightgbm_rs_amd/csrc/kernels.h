@@ -112,8 +112,9 @@ struct DevLearner {
   int64_t N;
   uint64_t slot_len;
   int32_t* hist_part;         // [HIST_SLOTS][total_cells][3] root / per-op partials
+  int32_t* hist_sum;          // [total_cells][3] job 0's partials summed (k_hist_reduce)
   int32_t* hist_acc;          // [SPEC_MAX][total_cells][3] per-job accumulators
-  int32_t* part_slots;        // [part blocks + SPEC_MAX][total_cells] int4 (block, job) cells
+  unsigned long long* part_slots;  // [part blocks + SPEC_MAX][total_cells] packed (block, job) cells
   // f32-gradient training: 64-bit fixed-point (g, h) cells
   int64_t* hist_part64;       // [HIST_SLOTS][total_cells][2]
   int64_t* int_slots64;       // [slot_cap][total_cells][2]

@@ -364,17 +364,20 @@ __global__ __launch_bounds__(256) void k_requant(const float* __restrict__ g,
 // Two accumulation schemes:
 //  - wave-private (cells <= HIST_WAVE_CELLS): each wave owns a u32 LDS histogram of
 //    packed cells  q_g + (q_h << 11) + ([q_h == 3] << 22)  (fields 11-bit signed,
-//    11-bit, 10-bit: exact for <= 511 rows), folds it into per-lane register sums
-//    at least every HIST_FOLD_STEPS x 64 rows (lane l owns cells l, l + 64, ...), and
-//    the waves are combined at the end.  One 32-bit LDS atomic per (row, feature).
+//    11-bit, 10-bit: exact for <= 511 rows), folds it at least every
+//    HIST_FOLD_STEPS x 64 rows into one 64-bit register per lane cell (lane l owns
+//    cells l, l + 64, ...) packed the same way with 22 / 21 / 21-bit fields (exact
+//    for < 2^19 rows per wave: N < 2^29 over 512 blocks of 8 waves), and the waves
+//    are combined at the end.  One 32-bit LDS atomic per (row, feature); rows whose
+//    quantized pair is (0, 0) add nothing and are skipped.
 //  - block-shared: one u64 LDS histogram per block, cells
 //    q_g + (q_h << 22) + ([q_h == 3] << 43) (exact for < 2^19 rows per block).
 // ===========================================================================
 __device__ __forceinline__ void hist_assign(const Ctl* ctl, int32_t nj, int32_t* s_a0,
-                                            int32_t* s_nb, int64_t* s_R) {
+                                            int32_t* s_nb, int64_t* s_R, int64_t grid) {
   int64_t S = 0;
   for (int j = 0; j < nj; ++j) S += max(ctl->hjobs[j].count, (int64_t)0);
-  int64_t R = (S + HIST_GRID - 1) / HIST_GRID;
+  int64_t R = (S + grid - 1) / grid;
   if (R < HIST_MIN_ROWS) R = HIST_MIN_ROWS;
   int32_t acc = 0;
   for (int j = 0; j < nj; ++j) {
@@ -388,7 +391,7 @@ __device__ __forceinline__ void hist_assign(const Ctl* ctl, int32_t nj, int32_t*
 }
 
 template <int W, bool WAVE_PRIVATE>
-__global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
+__global__ __launch_bounds__(HIST_THREADS, 2) void k_hist_jobs(DevLearner L) {
   extern __shared__ uint32_t lds_u32[];
   __shared__ int32_t cb[16 * LGBM_MAX_W];
   __shared__ int32_t s_a0[SPEC_MAX], s_nb[SPEC_MAX];
@@ -402,7 +405,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
   // beyond F are zero and land in a trash cell at index `cells`.
   const int nw = (F + 3) / 4;
   if (tid == 0) {
-    hist_assign(ctl, nj, s_a0, s_nb, &s_R);
+    hist_assign(ctl, nj, s_a0, s_nb, &s_R, HIST_GRID_Q);
     if (blockIdx.x == 0)
       for (int j = 0; j < nj; ++j) {
         ctl->hjobs[j].a0 = s_a0[j];
@@ -434,13 +437,9 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
     const int stride = cells + 4;                     // + trash cell
     uint32_t* my = lds_u32 + (size_t)wave * stride;
     for (int c = lane; c < stride; c += LGBM_WAVE) my[c] = 0u;
-    int32_t sg[NPL], sh[NPL], s3[NPL];
+    unsigned long long acc64[NPL];
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-      sg[i] = 0;
-      sh[i] = 0;
-      s3[i] = 0;
-    }
+    for (int i = 0; i < NPL; ++i) acc64[i] = 0ull;
     // the wave's contiguous share of the block's rows, HIST_ROWS_PER_LANE per lane
     // per step (loads first, then the atomics)
     const int64_t n = hi - lo;
@@ -457,9 +456,9 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
           my[c] = 0u;
           const int32_t g = ((int32_t)(p << 21)) >> 21;
           const uint32_t rest = (p - (uint32_t)g) >> 11;
-          sg[i] += g;
-          sh[i] += (int32_t)(rest & 0x7ffu);
-          s3[i] += (int32_t)(rest >> 11);
+          acc64[i] += (unsigned long long)(long long)g +
+                      ((unsigned long long)(rest & 0x7ffu) << 22) +
+                      ((unsigned long long)(rest >> 11) << 43);
         }
       }
     };
@@ -474,7 +473,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
         if (r < whi) {
 #pragma unroll
           for (int i = 0; i < W; ++i) w[u][i] = rec[r * W + i];
-          q[u] = (uint32_t)gh[r] | 0x10000u;  // bit 16: a real row
+          q[u] = (uint32_t)gh[r];  // 0: no row, or a (0, 0) pair
         }
       }
 #pragma unroll
@@ -510,10 +509,15 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
       const int c = i * LGBM_WAVE + lane;
-      if (c < cells) {
-        if (sg[i]) atomicAdd(&acc[c * 3], sg[i]);
-        if (sh[i]) atomicAdd(&acc[c * 3 + 1], sh[i]);
-        if (s3[i]) atomicAdd(&acc[c * 3 + 2], s3[i]);
+      if (c < cells && acc64[i] != 0ull) {
+        const unsigned long long p = acc64[i];
+        const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
+        const int64_t g = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
+        const unsigned long long rest = (p - (unsigned long long)g) >> 22;
+        const int32_t h = (int32_t)(rest & ((1ull << 21) - 1)), t = (int32_t)(rest >> 21);
+        if (g) atomicAdd(&acc[c * 3], (int32_t)g);
+        if (h) atomicAdd(&acc[c * 3 + 1], h);
+        if (t) atomicAdd(&acc[c * 3 + 2], t);
       }
     }
     __syncthreads();
@@ -526,7 +530,8 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
       uint4 w[W];
 #pragma unroll
       for (int i = 0; i < W; ++i) w[i] = rec[r * W + i];
-      lds_hist_add<W>(h64, cbr, nw, w, gh[r]);
+      const uint16_t q = gh[r];
+      if (q) lds_hist_add<W>(h64, cbr, nw, w, q);  // a (0, 0) pair adds nothing
     }
     __syncthreads();
     for (int c = tid; c < cells; c += HIST_THREADS) {
@@ -538,6 +543,38 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_jobs(DevLearner L) {
       out[c * 3 + 1] = (int32_t)(rest & ((1ull << 21) - 1));
       out[c * 3 + 2] = (int32_t)(rest >> 21);
     }
+  }
+}
+
+// Sum of histogram job 0's partial slots into L.hist_sum ([cells][3] int32): one
+// thread per (column, slot group), 16 columns x 16 groups per block, the groups
+// combined through LDS.  Consumers then read one slot instead of one per block.
+__global__ __launch_bounds__(256) void k_hist_reduce(DevLearner L) {
+  __shared__ int32_t part[16][17];
+  const Ctl* ctl = L.ctl;
+  const int32_t a0 = ctl->hjobs[0].a0, na = ctl->n_hjobs > 0 ? ctl->hjobs[0].nblk : 0;
+  const int64_t ncol = (int64_t)L.total_cells * 3;
+  const int cl = threadIdx.x & 15, g = threadIdx.x >> 4;
+  const int64_t col = (int64_t)blockIdx.x * 16 + cl;
+  int32_t s = 0;
+  if (col < ncol) {
+    const int32_t* p = L.hist_part + (size_t)a0 * ncol + col;
+    int32_t x[4] = {0, 0, 0, 0};
+    int k = g;
+    for (; k + 48 < na; k += 64) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) x[u] += p[(size_t)(k + 16 * u) * ncol];
+    }
+    for (; k < na; k += 16) x[0] += p[(size_t)k * ncol];
+    s = (x[0] + x[1]) + (x[2] + x[3]);
+  }
+  part[g][cl] = s;
+  __syncthreads();
+  if (g == 0 && col < ncol) {
+    int32_t t = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t += part[k][cl];
+    L.hist_sum[col] = t;
   }
 }
 
@@ -559,7 +596,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_f32(DevLearner L) {
   const int cells = L.total_cells;
   const int f0 = L.fgroup_first[grp], f1 = L.fgroup_first[grp + 1];
   if (tid == 0) {
-    hist_assign(ctl, nj, s_a0, s_nb, &s_R);
+    hist_assign(ctl, nj, s_a0, s_nb, &s_R, HIST_GRID);
     if (blockIdx.x == 0 && grp == 0)
       for (int j = 0; j < nj; ++j) {
         ctl->hjobs[j].a0 = s_a0[j];
@@ -641,8 +678,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
       th += H;
       continue;
     }
-    int32_t G = 0, H = 0, T = 0;
-    hist_part_sum(L, a0, na, ci, &G, &H, &T);
+    const int32_t G = L.hist_sum[ci * 3], H = L.hist_sum[ci * 3 + 1], T = L.hist_sum[ci * 3 + 2];
     if (mode == 1) {
       int32_t* ps = L.int_slots + ci * 3;  // node slot 0
       ps[0] = G;
@@ -859,7 +895,7 @@ void launch_requant(const float* g, const float* h, int64_t n, const Ctl* ctl, i
   k_requant<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(g, h, n, ctl, bins, gh, bad);
 }
 void launch_hist(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
-  const dim3 g(HIST_SLOTS), blk(HIST_THREADS);
+  const dim3 g(HIST_GRID_Q + SPEC_MAX), blk(HIST_THREADS);
   if (L.total_cells <= HIST_WAVE_CELLS) {
     const size_t lds = (size_t)HIST_WAVES * (L.total_cells + 4) * sizeof(uint32_t);
     DISPATCH_W(L.W, KLAUNCH(ev, (k_hist_jobs<kW, true>), g, blk, lds, s, L));
@@ -869,7 +905,7 @@ void launch_hist(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
   }
 }
 void launch_hist_f32(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
-  const dim3 g(HIST_SLOTS, (unsigned)std::max(L.n_fgroups, 1)), blk(HIST_THREADS);
+  const dim3 g(HIST_GRID + SPEC_MAX, (unsigned)std::max(L.n_fgroups, 1)), blk(HIST_THREADS);
   const size_t lds = (size_t)2 * HIST_FP_CELLS * sizeof(unsigned long long);
   DISPATCH_W(L.W, KLAUNCH(ev, (k_hist_f32<kW>), g, blk, lds, s, L));
 }
@@ -881,6 +917,10 @@ void launch_fp_prep(const DevLearner& L, const float* g, const float* h, int64_t
 }
 void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s,
                     const KernelEvents* ev) {
+  // quantized: the partial slots summed into hist_sum first (f32 cells are summed by
+  // k_fixscan itself); f32 mode never reads hist_sum, so the launch is harmless
+  const int64_t cols = (int64_t)L.total_cells * 3;
+  k_hist_reduce<<<dim3((unsigned)((cols + 15) / 16)), dim3(256), 0, s>>>(L);
   KLAUNCH(ev, k_fixscan, dim3((unsigned)L.F), dim3(SCAN_THREADS), 0, s, L, mode, explicit_out);
 }
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,

@@ -14,8 +14,9 @@
 #define LGBM_MAX_W 8                    // record words (16 B): features <= 16*W - 4
 #define HIST_THREADS 512                // ConstructHistogram block
 #define HIST_WAVES (HIST_THREADS / LGBM_WAVE)
-#define HIST_GRID 256                   // chunks over all jobs of a launch (at most)
-#define HIST_SLOTS (HIST_GRID + SPEC_MAX)  // partial slots = blocks launched
+#define HIST_GRID 256                   // f32 builds: chunks over all jobs of a launch (at most)
+#define HIST_GRID_Q 512                 // quantized builds: two 512-thread blocks per CU
+#define HIST_SLOTS (HIST_GRID_Q + SPEC_MAX)  // partial slots >= blocks launched
 #define HIST_MIN_ROWS 4096              // rows per chunk (at least)
 #define HIST_WAVE_CELLS 1792            // wave-private scheme: 28 cells per lane
 #define HIST_FOLD_STEPS 7               // 7 x 64 rows <= 511 per 11-bit field
@@ -161,6 +162,7 @@ struct Ctl {
   // ---- partition round ----
   int32_t part_left_count, _i6;
   unsigned long long part_cur[SPEC_MAX];  // per job: (left rows, right rows) reserved
+  int32_t acc_used[SPEC_MAX];        // per job: a partition flush used its accumulator
   PartJob jobs[SPEC_MAX];
   int32_t reduce_list[2 * SPEC_MAX + 2];
   // ---- gain config ----

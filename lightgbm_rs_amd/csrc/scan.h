@@ -41,7 +41,8 @@ __device__ __forceinline__ uint32_t rec_byte(const uint4 (&w)[W], int f) {
 
 // Accumulate one row (packed quantized pair q) into the LDS histogram of all features:
 // every byte of record words 0 .. nw-1 (wave-uniform); cbr[f] is feature f's first
-// cell, with bytes beyond the last feature mapped to a trash cell.
+// cell, with bytes beyond the last feature mapped to a trash cell.  Callers skip a
+// (0, 0) pair: it adds nothing.
 template <int W>
 __device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int32_t* cbr, int nw,
                                              const uint4 (&w)[W], uint32_t q) {
@@ -360,34 +361,40 @@ __device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* 
   __syncthreads();
 }
 
-// Moves a block's packed LDS histogram (fields: q_g sum signed 22 bits, q_h sum 21
-// bits, count of q_h == 3 21 bits) into integer cells (G, H, T) and clears it (the
+// Packed cell (fields: q_g sum signed 22 bits, q_h sum 21 bits, count of q_h == 3
+// 21 bits) -> its integer counters.
+__device__ __forceinline__ void unpack_cell(unsigned long long p, int32_t* g, int32_t* h,
+                                            int32_t* t) {
+  const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
+  const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
+  const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
+  *g = (int32_t)gsum;
+  *h = (int32_t)(rest & ((1ull << 21) - 1));
+  *t = (int32_t)(rest >> 21);
+}
+
+// Moves a block's packed LDS histogram into integer cells (G, H, T) and clears it (the
 // trash cells too).  mode FLUSH_ATOMIC: atomic adds into a shared int32 [cells][3]
-// accumulator (zero cells skipped); FLUSH_STORE: the block's own int4 [cells] slot,
-// every cell written with one 16-byte store; FLUSH_ADD: add into the block's own
-// slot (written by an earlier store).  The caller has synchronised the block after
-// the last accumulation.
+// accumulator (zero cells skipped); FLUSH_STORE: the packed cells as they are into
+// the block's own u64 [cells] slot (one flush per slot: a slot holds fewer than 2^19
+// rows per cell, as the LDS histogram does).  The caller has synchronised the block
+// after the last accumulation.
 #define FLUSH_ATOMIC 0
 #define FLUSH_STORE 1
-#define FLUSH_ADD 2
 __device__ __forceinline__ void lds_hist_flush_clear(unsigned long long* lds, int cells,
-                                                     int32_t* __restrict__ out, int mode) {
+                                                     void* __restrict__ out, int mode) {
   for (int c = threadIdx.x; c < cells + 4; c += blockDim.x) {
     const unsigned long long p = lds[c];
     lds[c] = 0ull;
     if (c >= cells) continue;  // trash cells
-    const int64_t lo22 = (int64_t)(p & ((1ull << 22) - 1));
-    const int64_t gsum = lo22 >= (1ll << 21) ? lo22 - (1ll << 22) : lo22;
-    const unsigned long long rest = (p - (unsigned long long)gsum) >> 22;
-    const int32_t hsum = (int32_t)(rest & ((1ull << 21) - 1));
-    const int32_t n3 = (int32_t)(rest >> 21);
     if (mode == FLUSH_STORE) {
-      ((int4*)out)[c] = make_int4((int32_t)gsum, hsum, n3, 0);
-    } else if (mode == FLUSH_ADD) {
-      const int4 o = ((const int4*)out)[c];
-      ((int4*)out)[c] = make_int4(o.x + (int32_t)gsum, o.y + hsum, o.z + n3, 0);
-    } else if (p != 0ull) {
-      int32_t* dst = out + (size_t)c * 3;
+      ((unsigned long long*)out)[c] = p;
+      continue;
+    }
+    int32_t gsum, hsum, n3;
+    unpack_cell(p, &gsum, &hsum, &n3);
+    if (p != 0ull) {
+      int32_t* dst = (int32_t*)out + (size_t)c * 3;
       if (gsum) __hip_atomic_fetch_add(dst, (int32_t)gsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (hsum) __hip_atomic_fetch_add(dst + 1, hsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (n3) __hip_atomic_fetch_add(dst + 2, n3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
