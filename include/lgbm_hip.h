@@ -96,9 +96,14 @@ typedef struct lgbm_batched_feature {
   int32_t _pad;
 } lgbm_batched_feature;
 
-/* The numeric `FeatureColumn` descriptors (crates/lgbm-treelearner/src/
- * learner.rs:87-204) minus the bins themselves; `bin_upper_bound` values are
- * passed as one concatenated array (feature f at sum_{f'<f} num_bin[f']). */
+#define LGBM_BIN_NUMERICAL 0
+#define LGBM_BIN_CATEGORICAL 1
+
+/* The `FeatureColumn` descriptors (crates/lgbm-treelearner/src/learner.rs:87-204)
+ * minus the bins themselves; `bin_upper_bound` values are passed as one
+ * concatenated array (feature f at sum_{f'<f} num_bin[f']): a numerical feature's
+ * upper bounds, a categorical feature's `bin_to_category` (bin -> category value,
+ * -1 for bin 0, the NaN / unseen-category bin). */
 typedef struct lgbm_feature_meta {
   uint32_t num_bin;
   int32_t offset; /* offset_for_most_freq_bin(most_freq_bin) (lgbm-treelearner/src/lib.rs:89-95) */
@@ -108,6 +113,7 @@ typedef struct lgbm_feature_meta {
   uint32_t most_freq_bin;
   int32_t missing_type; /* LGBM_MISSING_* */
   int32_t real_feature_index;
+  int32_t bin_type; /* LGBM_BIN_*: categorical features split by category sets */
 } lgbm_feature_meta;
 
 /* A grown tree (crates/lgbm-model/src/tree.rs: Tree fields written by
@@ -132,6 +138,14 @@ typedef struct lgbm_tree_out {
   int32_t* leaf_parent;
   double* internal_weight;     /* left + right sum_hessian of the split (the C++
                                   Tree::Split rule; tree.rs:655 stores 0) */
+  /* Categorical splits (Tree::split_categorical, tree.rs:710-790): such a node's
+   * threshold / threshold_in_bin hold its index among the categorical nodes and
+   * decision_type has bit 0 set; its category set (left: in the set) is the bitset
+   * cat_threshold[cat_boundaries[i] .. cat_boundaries[i + 1]) over category values. */
+  int32_t num_cat;             /* out */
+  int32_t cat_threshold_cap;   /* in: capacity of cat_threshold in 32-bit words */
+  int32_t* cat_boundaries;     /* num_leaves_cap entries (num_cat + 1 used; NULL: none) */
+  uint32_t* cat_threshold;
 } lgbm_tree_out;
 
 /* `LeafPartitionLayout` (crates/lgbm-dataset/src/dataset.rs:88-97): the data
@@ -374,8 +388,6 @@ typedef struct lgbm_bin_params {
   int32_t data_random_seed;         /* [1] */
 } lgbm_bin_params;
 
-#define LGBM_BIN_NUMERICAL 0
-#define LGBM_BIN_CATEGORICAL 1
 typedef struct lgbm_bin_mapper_info {
   int32_t num_bin;
   int32_t missing_type; /* LGBM_MISSING_* */

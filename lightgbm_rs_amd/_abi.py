@@ -112,6 +112,7 @@ class FeatureMeta(C.Structure):
         ("most_freq_bin", C.c_uint32),
         ("missing_type", C.c_int32),
         ("real_feature_index", C.c_int32),
+        ("bin_type", C.c_int32),
     ]
 
 
@@ -134,6 +135,10 @@ class TreeOut(C.Structure):
         ("leaf_depth", C.POINTER(C.c_int32)),
         ("leaf_parent", C.POINTER(C.c_int32)),
         ("internal_weight", C.POINTER(C.c_double)),
+        ("num_cat", C.c_int32),
+        ("cat_threshold_cap", C.c_int32),
+        ("cat_boundaries", C.POINTER(C.c_int32)),
+        ("cat_threshold", C.POINTER(C.c_uint32)),
     ]
 
 
@@ -172,6 +177,9 @@ _TREE_FIELDS = [
 ]
 
 
+CAT_WORDS_PER_NODE = 64  # category bitset capacity per categorical node (2048 categories)
+
+
 class TreeBuffers:
     """Host arrays backing one TreeOut (capacity num_leaves)."""
 
@@ -184,6 +192,11 @@ class TreeBuffers:
             a = np.zeros(n, dtype=dt)
             self.arrays[name] = a
             setattr(self.out, name, ptr(a, ct))
+        self.cat_boundaries = np.zeros(max(num_leaves, 2), dtype=np.int32)
+        self.cat_threshold = np.zeros(max(num_leaves - 1, 1) * CAT_WORDS_PER_NODE, dtype=np.uint32)
+        self.out.cat_boundaries = ptr(self.cat_boundaries, C.c_int32)
+        self.out.cat_threshold = ptr(self.cat_threshold, C.c_uint32)
+        self.out.cat_threshold_cap = len(self.cat_threshold)
 
     @classmethod
     def from_dict(cls, d):
@@ -195,6 +208,17 @@ class TreeBuffers:
             if name in d:
                 v = np.asarray(d[name], dtype=dt)
                 tb.arrays[name][:len(v)] = v
+        nc = int(d.get("num_cat", 0))
+        tb.out.num_cat = nc
+        if nc:
+            cb = np.asarray(d["cat_boundaries"], np.int32)
+            ct = np.asarray(d["cat_threshold"], np.uint32)
+            if len(ct) > len(tb.cat_threshold):
+                tb.cat_threshold = np.zeros(len(ct), np.uint32)
+                tb.out.cat_threshold = ptr(tb.cat_threshold, C.c_uint32)
+                tb.out.cat_threshold_cap = len(ct)
+            tb.cat_boundaries[:len(cb)] = cb
+            tb.cat_threshold[:len(ct)] = ct
         return tb
 
     def to_dict(self):
@@ -203,6 +227,11 @@ class TreeBuffers:
         for name, _, _, kind in _TREE_FIELDS:
             n = nl - 1 if kind == "node" else nl
             d[name] = self.arrays[name][:n].copy()
+        nc = int(self.out.num_cat)
+        d["num_cat"] = nc
+        d["cat_boundaries"] = self.cat_boundaries[:nc + 1].copy() if nc else np.zeros(0, np.int32)
+        d["cat_threshold"] = (self.cat_threshold[:self.cat_boundaries[nc]].copy() if nc
+                              else np.zeros(0, np.uint32))
         return d
 
 

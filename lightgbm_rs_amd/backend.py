@@ -454,9 +454,9 @@ HipBackend.predict_device = _predict_device
 
 
 def feature_meta(num_bin, most_freq_bin=0, missing_type=0, default_bin=None, real_index=0,
-                 min_bin=0, max_bin=None):
+                 min_bin=0, max_bin=None, bin_type=0):
     """FeatureColumn descriptors with the offset rule of offset_for_most_freq_bin
-    (lgbm-treelearner/src/lib.rs:89-95)."""
+    (lgbm-treelearner/src/lib.rs:89-95); bin_type 1: categorical."""
     m = FeatureMeta()
     m.num_bin = num_bin
     m.offset = 1 if most_freq_bin == 0 else 0
@@ -466,6 +466,7 @@ def feature_meta(num_bin, most_freq_bin=0, missing_type=0, default_bin=None, rea
     m.most_freq_bin = most_freq_bin
     m.missing_type = missing_type
     m.real_feature_index = real_index
+    m.bin_type = bin_type
     return m
 
 

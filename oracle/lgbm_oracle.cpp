@@ -378,6 +378,153 @@ void compact_histogram(double* hist, uint32_t num_bin, int32_t offset) {
 }
 
 // ---------------------------------------------------------------------------
+// Categorical split finding: find_best_threshold_categorical
+// (lgbm-treelearner/src/feature_histogram_categorical.rs:96-495), the one-hot scan
+// for num_bin <= max_cat_to_onehot, else many-vs-many over the bins sorted by
+// grad / (hess + cat_smooth).  sum_hessian arrives bumped by 2 kEpsilon (the caller,
+// learner.rs:3104-3118).  out->threshold is 0, default_left false; cat_bins
+// receives the winning REAL bins (cat_threshold of the reference).
+// ---------------------------------------------------------------------------
+void find_best_threshold_categorical(const double* hist, const lgbm_gain_config& cfg,
+                                     int32_t num_bin, int32_t offset, double sum_gradient,
+                                     double sum_hessian, int32_t num_data, lgbm_split_info* out,
+                                     std::vector<uint32_t>* cat_bins) {
+  const bool use_l1 = cfg_use_l1(cfg);
+  const double l1 = cfg.lambda_l1, eps = kEps;
+  const double mds = cfg.max_delta_step, ps = cfg.path_smooth, parent = cfg.parent_output;
+  const bool smoothing = cfg_use_smoothing(cfg);
+  auto G = [&](int32_t t) { return hist[(size_t)t * 2]; };
+  auto Hs = [&](int32_t t) { return hist[(size_t)t * 2 + 1]; };
+  bool is_splittable = false;
+  double best_gain = kMinScore, best_lg = 0.0, best_lh = 0.0;
+  int32_t best_lc = 0;
+  // gain_shift with the ORIGINAL l2 (the deliberate asymmetry, :123-157)
+  const double gain_shift =
+      smoothing ? get_leaf_gain_given_output(use_l1, sum_gradient, sum_hessian, l1, cfg.lambda_l2,
+                                             parent)
+                : get_leaf_gain_full(use_l1, sum_gradient, sum_hessian, l1, cfg.lambda_l2, mds,
+                                     false, 0.0, num_data, 0.0);
+  const double min_gain_shift = gain_shift + cfg.min_gain_to_split;
+  const int32_t bin_start = 1 - offset, bin_end = num_bin - offset;
+  const double cnt_factor = (double)num_data / sum_hessian;
+  const bool use_onehot = num_bin <= cfg.max_cat_to_onehot;
+  std::vector<int32_t> sorted_idx;
+  int32_t used_bin = -1, best_threshold = -1, best_dir = 1;
+  double l2 = cfg.lambda_l2;
+  if (use_onehot) {
+    for (int32_t t = bin_start; t < bin_end; ++t) {
+      const double grad = G(t), hess = Hs(t);
+      const int32_t cnt = round_int(hess * cnt_factor);
+      if (cnt < cfg.min_data_in_leaf || hess < cfg.min_sum_hessian_in_leaf) continue;
+      const int32_t other_count = num_data - cnt;
+      if (other_count < cfg.min_data_in_leaf) continue;
+      const double sum_other_hessian = sum_hessian - hess - eps;
+      if (sum_other_hessian < cfg.min_sum_hessian_in_leaf) continue;
+      const double sum_other_gradient = sum_gradient - grad;
+      const double g = get_split_gains_full(use_l1, sum_other_gradient, sum_other_hessian, grad,
+                                            hess + eps, l1, l2, mds, smoothing, ps, other_count,
+                                            cnt, parent);
+      if (g <= min_gain_shift) continue;
+      is_splittable = true;
+      if (g > best_gain) {
+        best_threshold = t;
+        best_lg = grad;
+        best_lh = hess + eps;
+        best_lc = cnt;
+        best_gain = g;
+      }
+    }
+  } else {
+    for (int32_t i = bin_start; i < bin_end; ++i)
+      if ((double)round_int(Hs(i) * cnt_factor) >= cfg.cat_smooth) sorted_idx.push_back(i);
+    used_bin = (int32_t)sorted_idx.size();
+    l2 += cfg.cat_l2;
+    const double cat_smooth = cfg.cat_smooth;
+    auto ctr = [&](int32_t t) { return G(t) / (Hs(t) + cat_smooth); };
+    std::stable_sort(sorted_idx.begin(), sorted_idx.end(),
+                     [&](int32_t a, int32_t b) { return ctr(a) < ctr(b); });
+    const int32_t dirs[2] = {1, -1}, starts[2] = {0, used_bin - 1};
+    const int32_t max_num_cat = std::min(cfg.max_cat_threshold, (used_bin + 1) / 2);
+    is_splittable = false;
+    for (int o = 0; o < 2; ++o) {
+      const int32_t dir = dirs[o];
+      int32_t start_pos = starts[o], cnt_cur_group = 0, left_count = 0;
+      double slg = 0.0, slh = eps;
+      for (int32_t i = 0; i < used_bin && i < max_num_cat; ++i) {
+        const int32_t t = sorted_idx[(size_t)start_pos];
+        start_pos += dir;
+        const double grad = G(t), hess = Hs(t);
+        const int32_t cnt = round_int(hess * cnt_factor);
+        slg += grad;
+        slh += hess;
+        left_count += cnt;
+        cnt_cur_group += cnt;
+        if (left_count < cfg.min_data_in_leaf || slh < cfg.min_sum_hessian_in_leaf) continue;
+        const int32_t right_count = num_data - left_count;
+        if (right_count < cfg.min_data_in_leaf || right_count < cfg.min_data_per_group) break;
+        const double srh = sum_hessian - slh;
+        if (srh < cfg.min_sum_hessian_in_leaf) break;
+        if (cnt_cur_group < cfg.min_data_per_group) continue;
+        cnt_cur_group = 0;
+        const double srg = sum_gradient - slg;
+        const double g = get_split_gains_full(use_l1, slg, slh, srg, srh, l1, l2, mds, smoothing, ps,
+                                              left_count, right_count, parent);
+        if (g <= min_gain_shift) continue;
+        is_splittable = true;
+        if (g > best_gain) {
+          best_lc = left_count;
+          best_lg = slg;
+          best_lh = slh;
+          best_threshold = i;
+          best_gain = g;
+          best_dir = dir;
+        }
+      }
+    }
+  }
+  cat_bins->clear();
+  if (!is_splittable) {
+    *out = split_none();
+    out->default_left = 0;
+    return;
+  }
+  // finalize (:395-495): outputs with this scan's l2, counts, sums, net gain, bins
+  const int32_t rc_out = num_data - best_lc;
+  out->left_output = calc_leaf_output_full(use_l1, best_lg, best_lh, l1, l2, mds, smoothing, ps,
+                                           best_lc, parent);
+  out->left_count = best_lc;
+  out->left_sum_gradient = best_lg;
+  out->left_sum_hessian = best_lh - eps;
+  out->right_output = calc_leaf_output_full(use_l1, sum_gradient - best_lg, sum_hessian - best_lh,
+                                            l1, l2, mds, smoothing, ps, rc_out, parent);
+  out->right_count = rc_out;
+  out->right_sum_gradient = sum_gradient - best_lg;
+  out->right_sum_hessian = sum_hessian - best_lh - eps;
+  out->gain = best_gain - min_gain_shift;
+  out->default_left = 0;
+  out->threshold = 0;
+  if (use_onehot) {
+    cat_bins->push_back((uint32_t)(best_threshold + offset));
+  } else {
+    for (int32_t i = 0; i < best_threshold + 1; ++i) {
+      const int32_t t = best_dir == 1 ? sorted_idx[(size_t)i] : sorted_idx[(size_t)(used_bin - 1 - i)];
+      cat_bins->push_back((uint32_t)(t + offset));
+    }
+  }
+}
+
+// Common::ConstructBitset (feature_histogram_categorical.rs:499-510): 32-bit blocks,
+// max(vals) / 32 + 1 of them.
+std::vector<uint32_t> construct_bitset(const std::vector<uint32_t>& vals) {
+  std::vector<uint32_t> bits;
+  if (vals.empty()) return bits;
+  const uint32_t mx = *std::max_element(vals.begin(), vals.end());
+  bits.assign(mx / 32 + 1, 0u);
+  for (uint32_t v : vals) bits[v / 32] |= 1u << (v % 32);
+  return bits;
+}
+
+// ---------------------------------------------------------------------------
 // GradientDiscretizer (gradient_discretizer.rs)
 // ---------------------------------------------------------------------------
 struct Discretizer {
@@ -559,6 +706,9 @@ struct Tree {
   std::vector<double> threshold, internal_value, internal_weight, leaf_value, leaf_weight;
   std::vector<float> split_gain;
   std::vector<int8_t> decision_type;
+  int32_t num_cat = 0;
+  std::vector<int32_t> cat_boundaries;  // {0, ...} once a categorical node exists
+  std::vector<uint32_t> cat_threshold;   // real-category bitsets, concatenated
 
   // root_tree (learner.rs:5398-5424)
   static Tree root(double out, int32_t n) {
@@ -608,6 +758,46 @@ struct Tree {
     leaf_parent.push_back(node);
     num_leaves += 1;
   }
+  // Tree::split_categorical (tree.rs:710-790): threshold / threshold_in_bin hold the
+  // node's categorical index, decision_type the categorical bit and the missing type;
+  // the category bitset (over category VALUES) is appended to cat_threshold.
+  void split_categorical(int32_t leaf, int32_t real_feature, const std::vector<uint32_t>& bits,
+                         double lv, double rv, int32_t lc, int32_t rc, double lw, double rw,
+                         float gain, int8_t missing_type) {
+    const int32_t node = num_leaves - 1, new_leaf = num_leaves;
+    const int32_t parent = leaf_parent[leaf];
+    if (parent >= 0) {
+      if (right_child[parent] == ~leaf)
+        right_child[parent] = node;
+      else
+        left_child[parent] = node;
+    }
+    split_feature.push_back(real_feature);
+    split_gain.push_back(gain);
+    threshold_in_bin.push_back((uint32_t)num_cat);
+    threshold.push_back((double)num_cat);
+    internal_value.push_back(leaf_value[leaf]);
+    internal_count.push_back(lc + rc);
+    internal_weight.push_back(lw + rw);  // C++ Tree::SplitCategorical
+    left_child.push_back(~leaf);
+    right_child.push_back(~new_leaf);
+    decision_type.push_back((int8_t)(1 | ((missing_type & 3) << 2)));  // kCategoricalMask
+    if (cat_boundaries.empty()) cat_boundaries.push_back(0);
+    cat_boundaries.push_back(cat_boundaries.back() + (int32_t)bits.size());
+    cat_threshold.insert(cat_threshold.end(), bits.begin(), bits.end());
+    num_cat += 1;
+    leaf_value[leaf] = lv;
+    leaf_weight[leaf] = lw;
+    leaf_count[leaf] = lc;
+    leaf_value.push_back(rv);
+    leaf_weight.push_back(rw);
+    leaf_count.push_back(rc);
+    leaf_depth.push_back(leaf_depth[leaf] + 1);
+    leaf_depth[leaf] += 1;
+    leaf_parent[leaf] = node;
+    leaf_parent.push_back(node);
+    num_leaves += 1;
+  }
   void shrinkage(double rate) {  // tree.rs:1074
     for (auto& v : leaf_value) v = maybe_round_to_zero(v * rate);
     for (auto& v : internal_value) v = maybe_round_to_zero(v * rate);
@@ -636,6 +826,13 @@ struct Tree {
       if (o->leaf_count) o->leaf_count[i] = leaf_count[i];
       if (o->leaf_depth) o->leaf_depth[i] = leaf_depth[i];
       if (o->leaf_parent) o->leaf_parent[i] = leaf_parent[i];
+    }
+    o->num_cat = num_cat;
+    if (num_cat > 0) {
+      if (o->cat_boundaries)
+        for (size_t i = 0; i < cat_boundaries.size(); ++i) o->cat_boundaries[i] = cat_boundaries[i];
+      if (o->cat_threshold && (int64_t)cat_threshold.size() <= (int64_t)o->cat_threshold_cap)
+        for (size_t i = 0; i < cat_threshold.size(); ++i) o->cat_threshold[i] = cat_threshold[i];
     }
   }
 };
@@ -666,6 +863,29 @@ struct Router {  // split_fused_host_impl router (data_partition.rs:387-417)
 };
 
 struct DataPartition {
+  // split_categorical (data_partition.rs:636-686): rows whose bin is in `left_bins`
+  // go left, the others (bin 0, the NaN / unseen category, included) right; stable.
+  int split_categorical(int32_t leaf, int32_t right_leaf, const Bins& bins, int f,
+                        const std::vector<char>& left_bin) {
+    const int64_t begin = leaf_begin[leaf], count = leaf_count[leaf];
+    uint32_t* idx = indices.data() + begin;
+    int64_t lc = 0, rc = 0;
+    for (int64_t i = 0; i < count; ++i) {
+      const uint32_t row = idx[i];
+      const uint32_t b = bins.at(f, row);
+      const bool left = b < left_bin.size() && left_bin[b];
+      part_left[lc] = row;
+      part_right[rc] = row;
+      lc += left ? 1 : 0;
+      rc += left ? 0 : 1;
+    }
+    std::memcpy(idx, part_left.data(), (size_t)lc * 4);
+    std::memcpy(idx + lc, part_right.data(), (size_t)rc * 4);
+    leaf_count[leaf] = (int32_t)lc;
+    leaf_begin[right_leaf] = (int32_t)(begin + lc);
+    leaf_count[right_leaf] = (int32_t)rc;
+    return LGBM_HIP_OK;
+  }
   int64_t n;
   std::vector<uint32_t> indices, part_left, part_right;
   std::vector<int32_t> leaf_begin, leaf_count;
@@ -773,6 +993,10 @@ struct Learner {
   // (learner.rs:456-459, 3701-3709); empty = no multiply.
   std::vector<double> contri;
 
+  // winning categorical bins per leaf (empty: the winner is numerical)
+  std::vector<std::vector<uint32_t>> best_cat;
+
+  bool is_cat(int f) const { return meta[f].bin_type == LGBM_BIN_CATEGORICAL; }
   bool skip_default_bin(int f) const {
     return meta[f].num_bin > 2 && meta[f].missing_type == LGBM_MISSING_ZERO;
   }
@@ -787,6 +1011,7 @@ struct Learner {
   void scan_leaf(int32_t leaf, const LeafSplits& ls, const double* buf,
                  const std::vector<char>* parent_split, std::vector<lgbm_split_info>& best,
                  std::vector<int32_t>& best_feat, std::vector<std::vector<char>>& splittable) {
+    best_cat[leaf].clear();
     if (!(ls.sh > 0.0) || ls.n <= 0) {
       best[leaf] = split_none();
       best_feat[leaf] = -1;
@@ -795,13 +1020,18 @@ struct Learner {
     lgbm_gain_config lc = cfg;
     lc.parent_output = ls.weight;
     std::vector<lgbm_split_info> res(F);
+    std::vector<std::vector<uint32_t>> cats(F);
     std::vector<char> scanned(F, 0);
 #pragma omp parallel for schedule(dynamic, 1) if (F >= 16)
     for (int f = 0; f < F; ++f) {
       if (parent_split && !(*parent_split)[f]) continue;
-      find_best_split(buf + slot_off[f], 2ull * num_bin[f], lc, num_bin[f], meta[f].offset,
-                      meta[f].default_bin, skip_default_bin(f), na_as_missing(f), run_forward(f),
-                      ls.sg, ls.sh, ls.n, &res[f]);
+      if (is_cat(f))  // bin_type dispatch (learner.rs:3103-3118): the bumped sum_hessian
+        find_best_threshold_categorical(buf + slot_off[f], lc, (int32_t)num_bin[f], meta[f].offset,
+                                        ls.sg, ls.sh + 2.0 * kEps, ls.n, &res[f], &cats[f]);
+      else
+        find_best_split(buf + slot_off[f], 2ull * num_bin[f], lc, num_bin[f], meta[f].offset,
+                        meta[f].default_bin, skip_default_bin(f), na_as_missing(f),
+                        run_forward(f), ls.sg, ls.sh, ls.n, &res[f]);
       scanned[f] = 1;
     }
     std::vector<char> this_split(F, 0);
@@ -818,6 +1048,7 @@ struct Learner {
       if (s.gain > kMinScore && split_gt(s, meta[f].real_feature_index, lb, lbf)) {
         lb = s;
         lbf = meta[f].real_feature_index;
+        best_cat[leaf] = cats[f];
       }
     }
     best[leaf] = lb;
@@ -876,6 +1107,7 @@ struct Learner {
     std::vector<lgbm_split_info> best(num_leaves, split_none());
     std::vector<int32_t> best_feat(num_leaves, -1);
     std::vector<std::vector<char>> splittable(num_leaves, std::vector<char>(F, 1));
+    best_cat.assign(num_leaves, {});
     int32_t left_leaf = 0, right_leaf = -1;
     for (int32_t it = 0; it < num_leaves - 1; ++it) {
       // before_find_best_split (learner.rs:1808-1839)
@@ -954,18 +1186,43 @@ struct Learner {
         }
       const int32_t new_left = bl, new_right = tree.num_leaves;
       const lgbm_feature_meta& m = meta[f];
+      const float gain_field = (float)(b.gain + cfg.min_gain_to_split);
+      int32_t pl = 0, pr = 0;
+      if (is_cat(f)) {
+        // split_inner_categorical (learner.rs:4104-4186): partition by the winning
+        // bins, record the bitset over their category values (bin_to_category)
+        std::vector<char> left_bin(m.num_bin, 0);
+        std::vector<uint32_t> vals;
+        for (uint32_t bb : best_cat[bl]) {
+          if (bb < m.num_bin) left_bin[bb] = 1;
+          const double cv = ub ? ub[ub_off[f] + bb] : (double)bb;
+          vals.push_back((uint32_t)(int32_t)cv);
+        }
+        int rc = dp.split_categorical(bl, new_right, bins, f, left_bin);
+        if (rc != LGBM_HIP_OK) return rc;
+        pl = dp.leaf_count[new_left];
+        pr = dp.leaf_count[new_right];
+        tree.split_categorical(bl, fr, construct_bitset(vals), b.left_output, b.right_output, pl,
+                               pr, b.left_sum_hessian, b.right_sum_hessian, gain_field,
+                               (int8_t)m.missing_type);
+      } else {
       const uint32_t pmin = m.min_bin + (uint32_t)std::max(m.offset, 0);
       int rc = dp.split(bl, new_right, bins, f, m.num_bin, pmin, m.max_bin, b.threshold,
                         m.most_freq_bin, na_as_missing(f), b.default_left != 0);
       if (rc != LGBM_HIP_OK) return rc;
       const double thr_real =
           ub ? ub[ub_off[f] + b.threshold] : (double)b.threshold;  // real_threshold (learner.rs:198-203)
-      const float gain_field = (float)(b.gain + cfg.min_gain_to_split);
-      const int32_t pl = dp.leaf_count[new_left], pr = dp.leaf_count[new_right];
+      pl = dp.leaf_count[new_left];
+      pr = dp.leaf_count[new_right];
       tree.split(bl, fr, b.threshold, thr_real, b.left_output, b.right_output, pl, pr,
                  b.left_sum_hessian, b.right_sum_hessian, gain_field, (int8_t)m.missing_type,
                  b.default_left != 0);
-      if (pl < pr) {
+      }
+      // Child seeding: the numerical path orders the children by partition counts
+      // (learner.rs:4061), the categorical one by the SplitInfo counts
+      // (seed_child_leaf_splits, learner.rs:4202); the histogram of the next pass goes
+      // to the partition-smaller leaf either way.
+      if (is_cat(f) ? b.left_count < b.right_count : pl < pr) {
         smaller = {pl, b.left_sum_gradient, b.left_sum_hessian, b.left_output};
         larger = {pr, b.right_sum_gradient, b.right_sum_hessian, b.right_output};
       } else {
@@ -974,6 +1231,7 @@ struct Learner {
       }
       best[bl] = split_none();
       best_feat[bl] = -1;
+      best_cat[bl].clear();
       best[new_left] = split_none();
       best_feat[new_left] = -1;
       best[new_right] = split_none();
@@ -1038,6 +1296,60 @@ double binary_boost_from_score(const float* label, int64_t n, double sigmoid) {
   pavg = std::fmax(pavg, kEps);
   return std::log(pavg / (1.0 - pavg)) / sigmoid;
 }
+
+// MulticlassSoftmax (lgbm-objective/src/multiclass.rs:48-200).  Labels truncate to
+// int class ids in [0, K) (:76-101); factor = K / (K - 1) (:84).
+struct Multiclass {
+  int32_t K = 0;
+  double factor = 0.0;
+  std::vector<int32_t> label;
+  std::vector<double> init_probs;  // class_init_probs (:81-101)
+  int init(const float* labels, int64_t n, int32_t k) {
+    if (k < 2) return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "multiclass needs num_class >= 2");
+    K = k;
+    factor = (double)k / ((double)k - 1.0);
+    label.resize(n);
+    init_probs.assign(k, 0.0);
+    for (int64_t i = 0; i < n; ++i) {
+      const int32_t li = (int32_t)labels[i];  // truncation toward zero
+      if (!(labels[i] == labels[i]) || li < 0 || li >= k)
+        return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "multiclass label out of [0, num_class)");
+      init_probs[li] += 1.0;
+      label[i] = li;
+    }
+    if (n > 0)
+      for (double& p : init_probs) p /= (double)n;
+    return LGBM_HIP_OK;
+  }
+  // get_gradients (:138-180) with Common::Softmax (lgbm-model/src/objective.rs:307-322):
+  // max by fold from rec[0], exp(v - max), sum in class order, divide.
+  void gradients(const double* score, int64_t n, float* g, float* h) const {
+#pragma omp parallel for schedule(static) if (n > 65536)
+    for (int64_t i = 0; i < n; ++i) {
+      double rec[256];
+      double wmax = score[i];
+      for (int32_t k = 1; k < K; ++k) wmax = std::fmax(score[(size_t)k * n + i], wmax);
+      double wsum = 0.0;
+      for (int32_t k = 0; k < K; ++k) {
+        rec[k] = std::exp(score[(size_t)k * n + i] - wmax);
+        wsum += rec[k];
+      }
+      for (int32_t k = 0; k < K; ++k) {
+        const double p = rec[k] / wsum;
+        const size_t idx = (size_t)k * n + i;
+        g[idx] = label[i] == k ? (float)(p - 1.0) : (float)p;
+        h[idx] = (float)(factor * p * (1.0 - p));
+      }
+    }
+  }
+  // boost_from_score (:184-187): log(max(p, kEpsilon))
+  double boost_from_score(int32_t k) const { return std::log(std::fmax(init_probs[k], kEps)); }
+  // class_need_train (:193-197)
+  bool need_train(int32_t k) const {
+    const double p = std::fabs(init_probs[k]);
+    return !(p <= kEps || p >= 1.0 - kEps);
+  }
+};
 
 }  // namespace
 
@@ -1234,6 +1546,93 @@ int oracle_binary_gradients(const double* score, const float* label, float* g, f
 }
 double oracle_binary_boost_from_score(const float* label, int64_t n) {
   return binary_boost_from_score(label, n, 1.0);
+}
+
+int oracle_multiclass_gradients(const double* score, const float* label, int64_t n,
+                                int32_t num_class, float* g, float* h) {
+  if (num_class > 256) return fail(LGBM_HIP_ERR_CAPABILITY, "num_class must be <= 256");
+  Multiclass M;
+  int rc = M.init(label, n, num_class);
+  if (rc) return rc;
+  M.gradients(score, n, g, h);
+  return LGBM_HIP_OK;
+}
+
+// The multiclass (softmax) boosting loop (gbdt.rs:691-1373, no bagging): per
+// iteration the class-major gradients of all K classes from the current scores,
+// optional quantization per class (seed (iter << 20) ^ class ^ 0x51702010,
+// gbdt.rs:946-958), then per class: class_need_train gate (a constant tree),
+// grow, shrinkage, score update of that class, add_bias(init) on the first
+// iteration; a class that does not split gets a constant tree (init on the first
+// iteration, else 0).  A round in which no class splits ends training (after the
+// first iteration its trees are dropped: gbdt.rs:1330-1349).  `scores` (K * n,
+// class-major) receives the final scores; trees_out (optional) holds iters * K trees.
+int oracle_train_multiclass(const void* bins, int32_t width, int32_t F, int64_t N,
+                            const lgbm_feature_meta* meta, const double* ub, const float* label,
+                            int32_t num_class, const lgbm_gain_config* cfg, int32_t num_leaves,
+                            int32_t max_depth, int32_t iters, double lr,
+                            int32_t boost_from_average, int32_t quantized, int32_t quant_bins,
+                            int32_t stochastic, double* scores, lgbm_tree_out* trees_out,
+                            int32_t* n_trees) {
+  if (num_class > 256) return fail(LGBM_HIP_ERR_CAPABILITY, "num_class must be <= 256");
+  Learner L;
+  int rc = make_learner(L, bins, width, F, N, meta, ub, cfg, num_leaves, max_depth);
+  if (rc) return rc;
+  Multiclass M;
+  if ((rc = M.init(label, N, num_class))) return rc;
+  const int32_t K = num_class;
+  std::vector<double> score((size_t)K * N, 0.0), init(K, 0.0);
+  if (boost_from_average)
+    for (int32_t k = 0; k < K; ++k) {
+      init[k] = M.boost_from_score(k);
+      if (std::fabs(init[k]) > kEps)
+        for (int64_t i = 0; i < N; ++i) score[(size_t)k * N + i] += init[k];
+    }
+  std::vector<float> g((size_t)K * N), h((size_t)K * N);
+  int32_t nt = 0;
+  for (int32_t it = 0; it < iters; ++it) {
+    M.gradients(score.data(), N, g.data(), h.data());
+    if (quantized)
+      for (int32_t k = 0; k < K; ++k) {
+        const uint64_t seed = ((uint64_t)it << 20) ^ (uint64_t)k ^ 0x51702010ull;
+        quantize_in_place(g.data() + (size_t)k * N, h.data() + (size_t)k * N, N, quant_bins,
+                          stochastic != 0, seed, nullptr, nullptr);
+      }
+    const int32_t before = nt;
+    bool any_split = false;
+    for (int32_t k = 0; k < K; ++k) {
+      Tree t;
+      bool trained = false;
+      if (M.need_train(k)) {
+        DataPartition dp(N, num_leaves);
+        rc = L.train(g.data() + (size_t)k * N, h.data() + (size_t)k * N, t, dp);
+        if (rc) return rc;
+        if (t.num_leaves > 1) {
+          trained = true;
+          any_split = true;
+          t.shrinkage(lr);
+          double* sk = score.data() + (size_t)k * N;
+          for (int32_t leaf = 0; leaf < t.num_leaves; ++leaf) {
+            const double v = t.leaf_value[leaf];
+            const uint32_t* rows = dp.indices.data() + dp.leaf_begin[leaf];
+            const int32_t c = dp.leaf_count[leaf];
+            for (int32_t r = 0; r < c; ++r) sk[rows[r]] += v;
+          }
+          if (it == 0 && std::fabs(init[k]) > kEps) t.add_bias(init[k]);
+        }
+      }
+      if (!trained) t = Tree::root(it == 0 ? init[k] : 0.0, (int32_t)N);
+      if (trees_out) t.to_out(&trees_out[nt]);
+      nt++;
+    }
+    if (!any_split) {
+      if (it > 0) nt = before;
+      break;
+    }
+  }
+  if (scores) std::memcpy(scores, score.data(), (size_t)K * N * 8);
+  if (n_trees) *n_trees = nt;
+  return LGBM_HIP_OK;
 }
 
 // The binary boosting loop (gbdt.rs:691-1300 for K = 1, no bagging): gradients ->

@@ -238,3 +238,46 @@ def train_binary(bins_fm, meta, upper, label, cfg, num_leaves, max_depth, iters,
             trees[i].out = tarr[i]
             out_trees.append(trees[i].to_dict())
     return scores, out_trees
+
+
+def multiclass_gradients(score, label, num_class):
+    """MulticlassSoftmax::get_gradients over class-major scores (K * n) -> (g, h)."""
+    s = np.ascontiguousarray(score, dtype=np.float64)
+    l = np.ascontiguousarray(label, dtype=np.float32)
+    n = len(l)
+    assert len(s) == n * num_class
+    g = np.zeros(n * num_class, dtype=np.float32)
+    h = np.zeros(n * num_class, dtype=np.float32)
+    _check(lib().oracle_multiclass_gradients(ptr(s, C.c_double), ptr(l, C.c_float), C.c_int64(n),
+                                             C.c_int32(num_class), ptr(g, C.c_float),
+                                             ptr(h, C.c_float)))
+    return g, h
+
+
+def train_multiclass(bins_fm, meta, upper, label, num_class, cfg, num_leaves, max_depth, iters,
+                     lr, boost_from_average=True, quantized=False, quant_bins=4, stochastic=True,
+                     want_trees=True):
+    """Softmax boosting: (class-major final scores [K * n], trees in iteration-major,
+    class-minor order)."""
+    b, width = _bins_arg(bins_fm)
+    F, N = b.shape
+    marr = _meta_arr(meta)
+    ub = None if upper is None else np.ascontiguousarray(upper, dtype=np.float64)
+    lab = np.ascontiguousarray(label, dtype=np.float32)
+    scores = np.zeros(N * num_class, dtype=np.float64)
+    cap = iters * num_class
+    trees = [TreeBuffers(num_leaves) for _ in range(cap)] if want_trees else []
+    tarr = (type(trees[0].out) * cap)(*[t.out for t in trees]) if want_trees else None
+    nt = C.c_int32(0)
+    _check(lib().oracle_train_multiclass(
+        b.ctypes.data_as(C.c_void_p), C.c_int32(width), C.c_int32(F), C.c_int64(N), marr,
+        ptr(ub, C.c_double), ptr(lab, C.c_float), C.c_int32(num_class), C.byref(cfg),
+        C.c_int32(num_leaves), C.c_int32(max_depth), C.c_int32(iters), C.c_double(lr),
+        C.c_int32(int(boost_from_average)), C.c_int32(int(quantized)), C.c_int32(quant_bins),
+        C.c_int32(int(stochastic)), ptr(scores, C.c_double), tarr, C.byref(nt)))
+    out_trees = []
+    if want_trees:
+        for i in range(nt.value):
+            trees[i].out = tarr[i]
+            out_trees.append(trees[i].to_dict())
+    return scores, out_trees

@@ -13,10 +13,13 @@ patterns); this script only re-encodes them.  Sources (under
   kernels/subtract.txt    -> subtract.json
   kernels/partition.txt   -> partition.json     (format: kernel_parity.rs:1162-1220)
   learner/spine_real.txt, learner/mfb_pos_real.txt, na_missing/model_real.txt,
-  gain_params/{penalty,max_delta_step,path_smooth}/model_real.txt -> learner_real.json
+  gain_params/{penalty,max_delta_step,path_smooth}/model_real.txt,
+  categorical/{cat_onehot,cat_manyvsmany}.{txt,bins.json} -> learner_real.json
       (real lib_lightgbm 4.6 model text; the corpora are the ones the reference
-       tests drive: learner_parity.rs:1214-1330, na_missing_parity.rs:108-141,
-       gain_params_parity.rs:93-226)
+       tests drive: learner_parity.rs:1214-1330 and 1455-1483,
+       na_missing_parity.rs:108-141, gain_params_parity.rs:93-226)
+  boosting/multiclass_{scores,gh_iter1,gh_iterN}.txt, multiclass_spine_model.txt
+      -> multiclass_spine.json (boosting_parity.rs:110-170, 1259-1300)
   path_smooth/path_smooth_golden.json -> path_smooth.npz
       (real lightgbm 4.6 boosting runs; path_smooth_parity.rs:226-345)
 
@@ -154,6 +157,52 @@ def parse_model_tree(path):
     return tree
 
 
+def parse_model_trees(path):
+    """Every Tree=i block of a LightGBM v4 model text -> list of dicts of string lists."""
+    trees, cur = [], None
+    for ln in read(path):
+        if ln.startswith("Tree="):
+            cur = {}
+            trees.append(cur)
+            continue
+        if cur is not None:
+            if not ln.strip():
+                cur = None
+                continue
+            k, _, v = ln.partition("=")
+            cur[k] = v.split()
+    return trees
+
+
+def multiclass_spine():
+    """boosting/multiclass_* (the real lightgbm 4.6 binary; boosting_parity.rs:110-170,
+    1259-1300): the 12-row, 2-feature, 3-class corpus, 5 iterations, lr 0.1,
+    num_leaves 4, min_data_in_leaf 1, boost_from_average; the per-iteration
+    class-major raw scores (f64 bits), the iteration-1 and iteration-4 gradients
+    (f32 bits) and the 15 trees of the model text."""
+    f0 = [0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 5, 5]
+    f1 = [0, 1, 2, 0, 1, 2, 0, 1, 2, 0, 1, 2]
+    labels = [0.0, 0.0, 0.0, 1.0, 1.0, 1.0, 2.0, 2.0, 2.0, 0.0, 1.0, 2.0]
+    scores = [[int(t) for t in ln.split()] for ln in read("boosting/multiclass_scores.txt")
+              if ln.strip() and not ln.startswith("#")]
+
+    def gh(name):
+        out = {}
+        for ln in read(name):
+            if ln.startswith("GRAD") or ln.startswith("HESS"):
+                k, *v = ln.split()
+                out[k] = [int(t) for t in v]
+        return out
+    trees = parse_model_trees("boosting/multiclass_spine_model.txt")
+    keep = ("num_leaves", "split_feature", "threshold", "decision_type", "left_child",
+            "right_child", "leaf_value", "leaf_count", "internal_count")
+    return dict(X=[[a, b] for a, b in zip(f0, f1)], labels=labels, num_class=3,
+                num_iterations=5, learning_rate=0.1, num_leaves=4, min_data_in_leaf=1,
+                score_bits=scores, gh_iter1=gh("boosting/multiclass_gh_iter1.txt"),
+                gh_iter4=gh("boosting/multiclass_gh_iterN.txt"),
+                trees=[{k: t[k] for k in keep if k in t} for t in trees])
+
+
 def f64bits(x):
     return struct.unpack("<Q", struct.pack("<d", x))[0]
 
@@ -214,6 +263,25 @@ def learner_real():
                  num_leaves=2, max_depth=-1, shrinkage=0.1, check_split_gain=True)
         c.update(extra)
         cases.append(c)
+    # learner_parity.rs:1455-1483 (cat_corpus): one categorical feature, hess 1,
+    # missing type None, default_bin = num_bin; the feature's per-bin values are its
+    # bin -> category map (bin 0 is the NaN dummy, category -1)
+    for name in ("cat_onehot", "cat_manyvsmany"):
+        with open(os.path.join(REF, f"categorical/{name}.bins.json")) as f:
+            s = json.load(f)
+        n = len(s["grad"])
+        cases.append(dict(
+            name=name + "_real", golden_file=f"categorical/{name}.txt",
+            bins=s["bins"], grad=s["grad"], num_bin=s["num_bin"],
+            most_freq_bin=s["most_freq_bin"], missing_type=0, default_bin=s["num_bin"],
+            bin_type=1, upper=[float(v) for v in s["bin_2_categorical"]],
+            tree=parse_model_tree(f"categorical/{name}.txt"), hess=[1.0] * n,
+            min_data_in_leaf=1, min_sum_hessian_in_leaf=1e-3, num_leaves=s["num_leaves"],
+            max_depth=-1, shrinkage=s["shrinkage"], check_split_gain=True,
+            cat=dict(cat_l2=s["cat_l2"], cat_smooth=s["cat_smooth"],
+                     min_data_per_group=s["min_data_per_group"],
+                     max_cat_threshold=s["max_cat_threshold"],
+                     max_cat_to_onehot=s["max_cat_to_onehot"])))
     for c in cases:
         c["upper_bits"] = [f64bits(x) for x in c.pop("upper")]
     return cases
@@ -273,6 +341,7 @@ def main():
         "partition.json": partition_cases(),
         "learner_real.json": learner_real(),
         "discretizer_cases.json": discretizer_cases(),
+        "multiclass_spine.json": multiclass_spine(),
     }
     for name, data in outs.items():
         with open(os.path.join(OUT, name), "w") as f:

@@ -104,12 +104,14 @@ def learner_case_inputs(case):
     nb = case["num_bin"]
     meta = [FeatureMeta(nb, 1 if case["most_freq_bin"] == 0 else 0, 0, nb - 1,
                         case.get("default_bin", nb), case["most_freq_bin"],
-                        case.get("missing_type", 0), 0)]
+                        case.get("missing_type", 0), 0, case.get("bin_type", 0))]
     bins = np.array([case["bins"]], dtype=np.uint32)
     cfg = GainConfig.make(min_data_in_leaf=case["min_data_in_leaf"],
                           min_sum_hessian_in_leaf=case["min_sum_hessian_in_leaf"],
                           max_delta_step=case.get("max_delta_step", 0.0),
                           path_smooth=case.get("path_smooth", 0.0))
+    for k, v in case.get("cat", {}).items():
+        setattr(cfg, k, v)
     return bins, meta, f64(case["upper_bits"]), cfg, case.get("feature_contri")
 
 
@@ -126,10 +128,15 @@ def assert_real_tree(t, case):
     assert [b64(x) for x in t["threshold"]] == [b64(float(x)) for x in g["threshold"]]
     shrunk = [_maybe_round_to_zero(v * case["shrinkage"]) for v in t["leaf_value"]]
     assert [b64(x) for x in shrunk] == [b64(float(x)) for x in g["leaf_value"]]
+    # categorical splits: the real-category bitsets (Tree::split_categorical)
+    assert t["num_cat"] == int(g.get("num_cat", ["0"])[0])
+    if t["num_cat"]:
+        assert t["cat_boundaries"].tolist() == [int(x) for x in g["cat_boundaries"]]
+        assert t["cat_threshold"].tolist() == [int(x) for x in g["cat_threshold"]]
     if case.get("check_split_gain"):
         # split_gain is f32 in the model and %g in the text (gain_params_parity.rs:151-158)
-        assert [np.float32(x) for x in t["split_gain"]] == [np.float32(float(x))
-                                                           for x in g["split_gain"]]
+        assert ["%g" % np.float32(x) for x in t["split_gain"]] == [
+            "%g" % float(x) for x in g["split_gain"]]
 
 
 @pytest.mark.parametrize("case", load("learner_real.json"), ids=lambda c: c["name"])
@@ -227,6 +234,31 @@ def test_learner_real_cases_have_teeth():
     g = cases["na_missing_real"]["tree"]
     assert (t["decision_type"].tolist() != [int(x) for x in g["decision_type"]] or
             t["leaf_count"].tolist() != [int(x) for x in g["leaf_count"]])
+
+
+def _real_tree_fails(case):
+    bins, meta, upper, cfg, contri = learner_case_inputs(case)
+    t, _ = oracle.train_tree(bins, meta, upper, case["grad"], case["hess"], cfg,
+                             case["num_leaves"], case["max_depth"], feature_contri=contri)
+    try:
+        assert_real_tree(t, case)
+    except AssertionError:
+        return True
+    return False
+
+
+def test_categorical_cases_have_teeth():
+    """The categorical goldens tell apart the scan's options: one-hot in place of
+    many-vs-many, a dropped cat_l2, a different cat_smooth, and the feature taken as numerical
+    each fail a case."""
+    cases = {c["name"]: c for c in load("learner_real.json")}
+    mvm, onehot = cases["cat_manyvsmany_real"], cases["cat_onehot_real"]
+    assert not _real_tree_fails(mvm) and not _real_tree_fails(onehot)
+    assert _real_tree_fails(dict(mvm, cat=dict(mvm["cat"], max_cat_to_onehot=64)))
+    assert _real_tree_fails(dict(onehot, cat=dict(onehot["cat"], cat_l2=0.0)))
+    # cat_smooth both smooths the sort key and drops categories with fewer rows
+    assert _real_tree_fails(dict(mvm, cat=dict(mvm["cat"], cat_smooth=11.0)))
+    assert _real_tree_fails(dict(mvm, bin_type=0))
 
 
 # --- kernel_parity.rs:240-320, 369-466 (per-candidate REVERSE / FORWARD gains) ----
