@@ -347,8 +347,38 @@ int lgbm_hip_get_gradients(lgbm_hip_ctx* ctx, float* grad, float* hess, int64_t 
  * values describe the iteration enqueued ahead.  Ignored while timing is enabled. */
 int lgbm_hip_set_lookahead(lgbm_hip_ctx* ctx, int32_t enable);
 
-/* Copy the resident f64 training score back to the host. */
+/* Copy the resident f64 training score back to the host: n = num_data, or
+ * num_class * num_data (class-major) after lgbm_hip_set_labels_multiclass. */
 int lgbm_hip_get_scores(lgbm_hip_ctx* ctx, double* out, int64_t n);
+
+/* ---- boosting loop on device (multiclass softmax) --------------------------- */
+
+/* Upload f32 class labels (truncated toward zero to class ids in [0, num_class),
+ * MulticlassSoftmax::new, lgbm-objective/src/multiclass.rs:76-101) and reset the
+ * resident class-major f64 score [num_class][num_data] to init_scores[k] per class
+ * (NULL: 0; the reference's BoostFromAverage adds log(max(kEpsilon, prior_k)),
+ * gbdt.rs:614-640, multiclass.rs:184-187).  num_class in 2..=256. */
+int lgbm_hip_set_labels_multiclass(lgbm_hip_ctx* ctx, const float* labels, int64_t n,
+                                   int32_t num_class, const double* init_scores);
+
+/* One softmax boosting iteration, all resident (gbdt.rs:691-1373, no bagging):
+ * `MulticlassSoftmax::get_gradients` (multiclass.rs:138-180) for every class from
+ * the current scores, then per class k: quantize (seed (iter << 20) ^ k ^
+ * 0x51702010, gbdt.rs:946-958; num_grad_quant_bins 0: f32 gradients) -> grow tree
+ * -> `Tree::shrinkage` -> score update of class k.  class_need_train (may be NULL:
+ * all) skips a class (gbdt.rs:1003-1018): its tree gets num_leaves = 0.  `trees`
+ * (may be NULL) is an array of num_class trees receiving the shrunk trees; the
+ * caller pushes the reference's constant tree for a tree with num_leaves <= 1 and
+ * adds the first iteration's init score (Tree::add_bias). */
+int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* ctx, int32_t iter, const lgbm_gain_config* cfg,
+                                   int32_t num_leaves, int32_t max_depth, double learning_rate,
+                                   int32_t num_grad_quant_bins, int32_t stochastic,
+                                   const int32_t* class_need_train, lgbm_tree_out* trees);
+
+/* The class-major f32 gradients / hessians of the last softmax evaluation
+ * (n = num_class * num_data; either pointer may be NULL).  No reference counterpart
+ * at the boundary: the reference's are host arrays. */
+int lgbm_hip_get_multiclass_gradients(lgbm_hip_ctx* ctx, float* grad, float* hess, int64_t n);
 
 /* Per-kernel device time (ms, HIP events on the context stream) accumulated since
  * the last reset, by kernel family: [0] histogram, [1] partition, [2] split scan,

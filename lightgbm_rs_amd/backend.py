@@ -56,8 +56,11 @@ class HipBackend:
         self.num_features = 0
         self.slot_len = 0
 
-    def _tree_buffers(self, num_leaves):
-        """Host arrays for one grown tree, reused across calls (to_dict copies)."""
+    def _tree_buffers(self, num_leaves, fresh=False):
+        """Host arrays for one grown tree, reused across calls (to_dict copies);
+        fresh=True: new arrays (several trees filled by one call)."""
+        if fresh:
+            return TreeBuffers(num_leaves)
         cache = self.__dict__.setdefault("_tb_cache", {})
         if num_leaves not in cache:
             cache[num_leaves] = TreeBuffers(num_leaves)
@@ -216,6 +219,7 @@ class HipBackend:
         lab = np.ascontiguousarray(labels, np.float32)
         self._check(self.lib.lgbm_hip_set_labels(self.ctx, ptr(lab, C.c_float), C.c_int64(len(lab)),
                                                  C.c_double(init_score)))
+        self.num_class = 1
 
     def train_iter_binary(self, it, cfg, num_leaves, max_depth, learning_rate,
                           num_grad_quant_bins=4, stochastic=True, want_tree=True):
@@ -225,6 +229,48 @@ class HipBackend:
             C.c_double(learning_rate), C.c_int32(num_grad_quant_bins), C.c_int32(int(stochastic)),
             C.byref(tb.out) if tb else None))
         return tb.to_dict() if tb else None
+
+    def set_labels_multiclass(self, labels, num_class, init_scores=None):
+        """Class labels + the class-major score reset to init_scores[k] per class
+        (lgbm_hip_set_labels_multiclass)."""
+        lab = np.ascontiguousarray(labels, np.float32)
+        init = None if init_scores is None else np.ascontiguousarray(init_scores, np.float64)
+        self._check(self.lib.lgbm_hip_set_labels_multiclass(
+            self.ctx, ptr(lab, C.c_float), C.c_int64(len(lab)), C.c_int32(num_class),
+            ptr(init, C.c_double)))
+        self.num_class = int(num_class)
+
+    def train_iter_multiclass(self, it, cfg, num_leaves, max_depth, learning_rate,
+                              num_grad_quant_bins=0, stochastic=True, class_need_train=None,
+                              want_trees=True):
+        """One softmax iteration (lgbm_hip_train_iter_multiclass): the num_class shrunk
+        trees (num_leaves 0 for a class skipped by class_need_train)."""
+        K = self.num_class
+        tbs = [self._tree_buffers(num_leaves, fresh=True) for _ in range(K)] if want_trees else None
+        arr = None
+        if tbs:
+            arr = (type(tbs[0].out) * K)(*[t.out for t in tbs])
+        need = None if class_need_train is None else np.ascontiguousarray(class_need_train, np.int32)
+        self._check(self.lib.lgbm_hip_train_iter_multiclass(
+            self.ctx, C.c_int32(it), C.byref(cfg), C.c_int32(num_leaves), C.c_int32(max_depth),
+            C.c_double(learning_rate), C.c_int32(num_grad_quant_bins), C.c_int32(int(stochastic)),
+            ptr(need, C.c_int32), arr))
+        if not tbs:
+            return None
+        out = []
+        for k, tb in enumerate(tbs):
+            tb.out = arr[k]
+            out.append(tb.to_dict())
+        return out
+
+    def multiclass_gradients(self):
+        """The device's class-major f32 (grad, hess) of the last softmax evaluation."""
+        n = self.num_class * self.num_data
+        g = np.zeros(n, np.float32)
+        h = np.zeros(n, np.float32)
+        self._check(self.lib.lgbm_hip_get_multiclass_gradients(
+            self.ctx, ptr(g, C.c_float), ptr(h, C.c_float), C.c_int64(n)))
+        return g, h
 
     def gradients(self):
         """The device's f32 (grad, hess) of the last objective evaluation."""
@@ -240,9 +286,10 @@ class HipBackend:
         self._check(self.lib.lgbm_hip_set_lookahead(self.ctx, C.c_int32(int(enable))))
 
     def scores(self):
-        out = np.zeros(self.num_data, np.float64)
+        """The resident training score (class-major [num_class * num_data] for multiclass)."""
+        out = np.zeros(getattr(self, "num_class", 1) * self.num_data, np.float64)
         self._check(self.lib.lgbm_hip_get_scores(self.ctx, ptr(out, C.c_double),
-                                                 C.c_int64(self.num_data)))
+                                                 C.c_int64(len(out))))
         return out
 
     def set_timing(self, enable=True):

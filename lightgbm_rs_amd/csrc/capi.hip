@@ -96,6 +96,7 @@ struct lgbm_hip_ctx {
   int32_t F = 0, W = 0, total_cells = 0;
   uint64_t slot_len = 0;
   std::vector<DevFeature> feats;
+  std::vector<double> ub_host;  // per-bin values (numerical: upper bounds, categorical: categories)
   bool have_bins = false, have_grad = false, quant_ready = false, have_labels = false;
   int32_t quant_bins = 0;
   // lookahead (lgbm_hip_set_lookahead): the next iteration's objective + quantizer
@@ -113,7 +114,9 @@ struct lgbm_hip_ctx {
   int64_t g32_rows[NBUF] = {};
   int64_t buf_rows[NBUF] = {};
   float *g = nullptr, *h = nullptr, *label = nullptr;
-  double* score = nullptr;
+  double* score = nullptr;     // [num_class][N] class-major
+  int32_t num_class = 1;       // classes of the resident score (lgbm_hip_set_labels*)
+  float *gk = nullptr, *hk = nullptr;  // multiclass: [num_class][N] gradients
   int32_t* hist_part = nullptr;  // [HIST_SLOTS][cells][3]
   int32_t* hist_sum = nullptr;   // [cells][3]
   int32_t* hist_acc = nullptr;   // [SPEC_MAX][cells][3]
@@ -135,6 +138,7 @@ struct lgbm_hip_ctx {
   int32_t* best_fpos = nullptr;
   int32_t* int_slots = nullptr;
   uint8_t* splittable = nullptr;
+  uint32_t* cat_bits = nullptr;   // [SLOT_CAP][F][8]
   int32_t* plan_state = nullptr;  // [5][MAX_LEAVES]
   DevNodes nodes{};
   DevLeaves leaves{};
@@ -142,7 +146,7 @@ struct lgbm_hip_ctx {
   void* tree_blob = nullptr;   // device tree arrays, one allocation
   void* tree_host = nullptr;   // pinned staging for the one-copy readback
   size_t tree_blob_bytes = 0;
-  size_t tree_off[16] = {};
+  size_t tree_off[17] = {};
   // scratch
   void* scratch = nullptr;
   size_t scratch_cap = 0;
@@ -295,6 +299,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.best_fpos = c->best_fpos;
   L.int_slots = c->int_slots;
   L.splittable = c->splittable;
+  L.cat_bits = c->cat_bits;
   L.plan_state = c->plan_state;
   L.nodes = c->nodes;
   L.tile_state = c->tile_state;
@@ -370,6 +375,7 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   if ((rc = dalloc(c, &c->feat_split, P * F))) return rc;
   if ((rc = dalloc(c, &c->best, P))) return rc;
   if ((rc = dalloc(c, &c->splittable, P * F))) return rc;
+  if ((rc = dalloc(c, &c->cat_bits, P * F * 8))) return rc;
   if ((rc = dalloc(c, &c->best_fpos, P))) return rc;
   if ((rc = dalloc(c, &c->int_slots, P * c->total_cells * 3))) return rc;
   if ((rc = dalloc(c, &c->int_slots64, P * c->total_cells * 2))) return rc;
@@ -392,9 +398,9 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   if ((rc = dalloc(c, &c->tree.route_mask, (size_t)L * 8))) return rc;
   if ((rc = dalloc(c, &c->tree.route_node, (size_t)L))) return rc;
   // tree arrays: one device blob (one readback per tree) + pinned host staging
-  const size_t sizes[16] = {64, 4, 4, 8, 4, 1, 4, 4, 8, 4, 8, 8, 4, 4, 4, 8};
+  const size_t sizes[17] = {64, 4, 4, 8, 4, 1, 4, 4, 8, 4, 8, 8, 4, 4, 4, 8, 32};
   size_t off = 0;
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 17; ++i) {
     c->tree_off[i] = off;
     off += ((i == 0 ? 64 : sizes[i] * (size_t)L) + 15) / 16 * 16;
   }
@@ -423,6 +429,7 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   T.leaf_depth = (int32_t*)(base + c->tree_off[13]);
   T.leaf_parent = (int32_t*)(base + c->tree_off[14]);
   T.internal_weight = (double*)(base + c->tree_off[15]);
+  T.cat_left = (uint32_t*)(base + c->tree_off[16]);
   c->lcap = L;
   c->buf_gen++;
   return LGBM_HIP_OK;
@@ -666,6 +673,49 @@ int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, do
     cp(out->leaf_depth, 13, nl_ * 4);
     cp(out->leaf_parent, 14, nl_ * 4);
     cp(out->internal_weight, 15, ni * 8);
+    // Categorical nodes (Tree::split_categorical, learner.rs:4104-4186): in node order
+    // the k-th gets bitset index k as its threshold; its bitset is ConstructBitset over
+    // the category values of the bins that went left.
+    std::vector<int32_t> bounds{0};
+    std::vector<uint32_t> words;
+    const int8_t* dt = (const int8_t*)(hb + c->tree_off[5]);
+    const int32_t* sf = (const int32_t*)(hb + c->tree_off[1]);
+    const uint32_t* cl = (const uint32_t*)(hb + c->tree_off[16]);
+    for (size_t n = 0; n < ni; ++n) {
+      if (!(dt[n] & 1)) continue;
+      const int32_t k = (int32_t)bounds.size() - 1;
+      if (out->threshold_in_bin) out->threshold_in_bin[n] = (uint32_t)k;
+      if (out->threshold) out->threshold[n] = (double)k;
+      int32_t fpos = -1;
+      for (int32_t f = 0; f < c->F; ++f)
+        if (c->feats[(size_t)f].real_index == sf[n]) {
+          fpos = f;
+          break;
+        }
+      std::vector<uint32_t> bits;
+      for (int32_t b = 0; b < 256; ++b) {
+        if (!((cl[n * 8 + (size_t)(b >> 5)] >> (b & 31)) & 1u)) continue;
+        const DevFeature& ft = c->feats[(size_t)std::max(fpos, 0)];
+        const double v = fpos >= 0 && ft.ub_off + (size_t)b < c->ub_host.size()
+                             ? c->ub_host[ft.ub_off + (size_t)b]
+                             : (double)b;
+        const uint32_t cat = (uint32_t)(int32_t)v;
+        if (bits.size() <= cat / 32) bits.resize(cat / 32 + 1, 0u);
+        bits[cat / 32] |= 1u << (cat % 32);
+      }
+      words.insert(words.end(), bits.begin(), bits.end());
+      bounds.push_back((int32_t)words.size());
+    }
+    out->num_cat = (int32_t)bounds.size() - 1;
+    if (out->num_cat > 0) {
+      if (!out->cat_boundaries || !out->cat_threshold ||
+          (int64_t)words.size() > (int64_t)out->cat_threshold_cap)
+        return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH,
+                       "categorical tree: cat_threshold needs " + std::to_string(words.size()) +
+                           " words (cat_threshold_cap " + std::to_string(out->cat_threshold_cap) + ")");
+      std::memcpy(out->cat_boundaries, bounds.data(), bounds.size() * 4);
+      std::memcpy(out->cat_threshold, words.data(), words.size() * 4);
+    }
     if (shrink != 1.0) {
       // Tree::shrinkage (tree.rs:1074): MaybeRoundToZero(v * rate)
       const double z = (double)1e-35f;
@@ -760,11 +810,13 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
     d.na_as_missing = (m.num_bin > 2 && m.missing_type == LGBM_MISSING_NAN) ? 1 : 0;
     d.run_forward = (m.num_bin > 2 && m.missing_type != LGBM_MISSING_NONE) ? 1 : 0;
     d.penalty = 1.0;
+    d.categorical = m.bin_type == LGBM_BIN_CATEGORICAL ? 1 : 0;
+    if (d.categorical && !bin_upper_bound)
+      return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT,
+                     "categorical features need their bin -> category values in bin_upper_bound");
     acc += m.num_bin;
     uacc += m.num_bin;
   }
-  if (acc > 8192)  // 8 B per LDS cell, 64 KiB of dynamic LDS per block
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "histogram exceeds the LDS budget");
   if (acc > (uint32_t)(MAX_FGROUPS - 1) * (HIST_FP_CELLS - 256))
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "too many histogram cells for the f32 feature groups");
   if (acc > HIST_WAVE_CELLS && num_data > (int64_t)HIST_GRID_Q * HIST_BLOCK_MAX_ROWS)
@@ -779,6 +831,8 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   c->lcap = 0;  // slots depend on slot_len
   if ((rc = dalloc(c, &c->d_feats, (size_t)F))) return rc;
   HIPCHK(c, hipMemcpy(c->d_feats, feats.data(), F * sizeof(DevFeature), hipMemcpyHostToDevice));
+  c->ub_host.assign(bin_upper_bound ? bin_upper_bound : nullptr,
+                    bin_upper_bound ? bin_upper_bound + uacc : nullptr);
   if (bin_upper_bound) {
     if ((rc = dalloc(c, &c->d_ub, (size_t)uacc))) return rc;
     HIPCHK(c, hipMemcpy(c->d_ub, bin_upper_bound, uacc * 8, hipMemcpyHostToDevice));
@@ -936,6 +990,8 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->h);
   F(c->label);
   F(c->score);
+  F(c->gk);
+  F(c->hk);
   F(c->hist_part);
   F(c->hist_sum);
   F(c->hist_acc);
@@ -1178,9 +1234,7 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
     if (!m) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null mapper");
     if (m->num_bin < 1 || m->num_bin > 256)
       return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be in 1..=256 (u8 bin storage)");
-    if (m->bin_type == LGBM_BIN_CATEGORICAL)
-      return set_err(c, LGBM_HIP_ERR_CAPABILITY,
-                     "categorical features need the categorical split scan, which this build lacks");
+    const bool cat = m->bin_type == LGBM_BIN_CATEGORICAL;
     lgbm_feature_meta& d = meta[(size_t)f];
     d.num_bin = (uint32_t)m->num_bin;
     d.offset = m->most_freq_bin == 0 ? 1 : 0;  // offset_for_most_freq_bin (lib.rs:89-95)
@@ -1190,15 +1244,29 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
     d.most_freq_bin = m->most_freq_bin;
     d.missing_type = m->missing_type;
     d.real_feature_index = f;
+    d.bin_type = cat ? LGBM_BIN_CATEGORICAL : LGBM_BIN_NUMERICAL;
     DevBinFeature& b = bf[(size_t)f];
     b = DevBinFeature{};
+    if (cat) {
+      // ValueToBin of a categorical mapper: the (category, bin) pairs sorted by
+      // category; the feature's per-bin values are its categories (bin 0: -1)
+      b.categorical = 1;
+      b.off = (int32_t)cats.size();
+      std::vector<std::pair<int32_t, uint32_t>> pairs(m->cat_to_bin.begin(), m->cat_to_bin.end());
+      std::sort(pairs.begin(), pairs.end());
+      for (const auto& pr : pairs) cats.push_back(make_int2(pr.first, (int32_t)pr.second));
+      b.ncat = (int32_t)pairs.size();
+      for (int32_t k = 0; k < m->num_bin; ++k)
+        ub.push_back((size_t)k < m->bin_to_cat.size() ? (double)m->bin_to_cat[(size_t)k] : -1.0);
+      continue;
+    }
     b.categorical = 0;
     b.nan_bin = m->missing_type == BIN_MISSING_NAN ? m->num_bin - 1 : -1;
     b.last = m->num_bin - 1 - (b.nan_bin >= 0 ? 1 : 0);
     b.off = (int32_t)ub.size();
     ub.insert(ub.end(), m->upper.begin(), m->upper.end());
   }
-  cats.push_back(make_int2(0, 0));  // never read: keeps the table non-empty
+  cats.push_back(make_int2(0, 0));  // keeps the table non-empty
   if ((rc = resident_setup(c, F, num_rows, meta.data(), ub.data()))) return rc;
   DevBinFeature* d_bf = nullptr;
   int2* d_cats = nullptr;
@@ -1417,6 +1485,9 @@ int lgbm_hip_build_int_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int
   c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!c->quant_ready) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize first");
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  if (c->total_cells > QUANT_LDS_CELLS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
   if ((rc = set_hist_job(c, leaf_rows, n_rows))) return rc;
   DevLearner L = make_learner(c);
   launch_hist(L, c->stream);
@@ -1454,6 +1525,9 @@ int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, in
                    "exact f64 histogram requires num_grad_quant_bins in {2, 4}");
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
+  if (!fp && c->total_cells > QUANT_LDS_CELLS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
   DevLearner L0 = make_learner(c);
   if (fp) {
@@ -1698,6 +1772,9 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num
                    "device learner requires num_grad_quant_bins in {2, 4}");
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
+  if (!fp && c->total_cells > QUANT_LDS_CELLS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
   if (fp) {
     if ((rc = ensure_fp(c))) return rc;
     if ((rc = ensure_leaves(c, num_leaves))) return rc;
@@ -1720,6 +1797,7 @@ int lgbm_hip_set_labels(lgbm_hip_ctx* c, const float* labels, int64_t n, double 
   HIPCHK(c, hipMemcpy(c->label, labels, (size_t)n * 4, hipMemcpyHostToDevice));
   std::vector<double> s((size_t)n, init_score);
   HIPCHK(c, hipMemcpy(c->score, s.data(), (size_t)n * 8, hipMemcpyHostToDevice));
+  c->num_class = 1;
   c->have_labels = true;
   return LGBM_HIP_OK;
 }
@@ -1731,6 +1809,8 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
   int rc = check_ctx(c);
   if (rc) return rc;
   if (!c->have_labels) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set labels first");
+  if (c->num_class != 1)
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "the resident labels are multiclass");
   if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
   if (num_leaves < 1 || num_leaves > 256)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_leaves must be in 1..=256");
@@ -1741,6 +1821,9 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
                    "device learner requires num_grad_quant_bins in {0, 2, 4}");
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
+  if (!fp && c->total_cells > QUANT_LDS_CELLS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
   if (fp) {
     if ((rc = ensure_fp(c))) return rc;
     if ((rc = ensure_leaves(c, num_leaves))) return rc;
@@ -1771,6 +1854,126 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
     return finish_tree(c, tree, nullptr, learning_rate, true);
   }
   return finish_tree(c, tree, nullptr, learning_rate);
+}
+
+int lgbm_hip_set_labels_multiclass(lgbm_hip_ctx* c, const float* labels, int64_t n,
+                                   int32_t num_class, const double* init_scores) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
+  if (!labels) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null labels");
+  if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "labels length != num_data");
+  if (num_class < 2 || num_class > 256)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_class must be in 2..=256");
+  // MulticlassSoftmax::new (multiclass.rs:76-101): labels truncate toward zero (a
+  // NaN to 0, the saturating cast) to class ids in [0, num_class)
+  for (int64_t i = 0; i < n; ++i) {
+    const double l = labels[i];
+    if (l == l && (l <= -1.0 || l >= (double)num_class))
+      return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT,
+                     "label " + std::to_string(l) + " at row " + std::to_string(i) +
+                         " is not a class in [0, num_class)");
+  }
+  c->have_labels = false;
+  const size_t kn = (size_t)num_class * (size_t)n;
+  if ((rc = dalloc(c, &c->label, (size_t)n))) return rc;
+  if ((rc = dalloc(c, &c->score, kn))) return rc;
+  if ((rc = dalloc(c, &c->gk, kn))) return rc;
+  if ((rc = dalloc(c, &c->hk, kn))) return rc;
+  HIPCHK(c, hipMemcpy(c->label, labels, (size_t)n * 4, hipMemcpyHostToDevice));
+  std::vector<double> s(kn, 0.0);
+  if (init_scores)
+    for (int32_t k = 0; k < num_class; ++k)
+      std::fill(s.begin() + (size_t)k * n, s.begin() + (size_t)(k + 1) * n, init_scores[k]);
+  HIPCHK(c, hipMemcpy(c->score, s.data(), kn * 8, hipMemcpyHostToDevice));
+  c->num_class = num_class;
+  c->have_labels = true;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_config* cfg,
+                                   int32_t num_leaves, int32_t max_depth, double learning_rate,
+                                   int32_t num_grad_quant_bins, int32_t stochastic,
+                                   const int32_t* class_need_train, lgbm_tree_out* trees) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;
+  if (!c->have_labels || c->num_class < 2)
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "set multiclass labels first");
+  if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
+  if (num_leaves < 1 || num_leaves > 256)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_leaves must be in 1..=256");
+  const int32_t fp = num_grad_quant_bins == 0 ? 1 : 0;
+  if (!fp && num_grad_quant_bins != 2 && num_grad_quant_bins != 4)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "device learner requires num_grad_quant_bins in {0, 2, 4}");
+  if (!fp && c->N >= QUANT_MAX_ROWS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
+  if (!fp && c->total_cells > QUANT_LDS_CELLS)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
+  if ((rc = ensure_leaves(c, num_leaves))) return rc;
+  if (fp && (rc = ensure_fp(c))) return rc;
+  const int32_t K = c->num_class;
+  const int64_t N = c->N;
+  // factor = K / (K - 1) (multiclass.rs:84)
+  const double factor = (double)K / ((double)K - 1.0);
+  ev_begin(c, FAM_OBJ);
+  launch_grad_softmax(c->score, c->label, c->gk, c->hk, N, K, factor, c->stream);
+  ev_end(c);
+  HIPCHK(c, hipGetLastError());
+  for (int32_t k = 0; k < K; ++k) {
+    lgbm_tree_out* out = trees ? &trees[k] : nullptr;
+    if (class_need_train && !class_need_train[k]) {
+      // class_need_train gate (gbdt.rs:1003-1018): no tree for this class
+      if (out) out->num_leaves = 0;
+      continue;
+    }
+    const float* gk = c->gk + (size_t)k * N;
+    const float* hk = c->hk + (size_t)k * N;
+    DevLearner L0 = make_learner(c);
+    if (fp) {
+      ev_begin(c, FAM_QUANT);
+      launch_fp_prep(L0, gk, hk, N, c->partials, c->stream);
+      ev_end(c);
+      c->quant_ready = false;
+    } else {
+      // per-(iteration, class) seed (gbdt.rs:946-958)
+      const uint64_t seed = ((uint64_t)(uint32_t)iter << 20) ^ (uint64_t)(uint32_t)k ^ 0x51702010ull;
+      ev_begin(c, FAM_QUANT);
+      launch_absmax(gk, hk, N, c->partials, c->stream);
+      launch_quant_scales(c->ctl, c->partials, N, num_grad_quant_bins, -1, c->stream);
+      launch_quantize(gk, hk, N, c->ctl, c->wave_mats, c->lane_mats, seed ^ 0x9E3779B97F4A7C15ull,
+                      stochastic, c->gh[BUF_ORIG], nullptr, nullptr, c->stream);
+      ev_end(c);
+      c->quant_ready = true;
+      c->quant_bins = num_grad_quant_bins;
+    }
+    HIPCHK(c, hipGetLastError());
+    c->have_grad = false;  // c->g / c->h do not hold this class's gradients
+    if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
+    DevLearner L = make_learner(c);
+    KernelEvents ke;
+    launch_score_update(L, learning_rate, c->score + (size_t)k * N, c->stream,
+                        ev_kernel(c, FAM_OBJ, &ke));
+    HIPCHK(c, hipGetLastError());
+    if ((rc = finish_tree(c, out, nullptr, learning_rate))) return rc;
+  }
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_get_multiclass_gradients(lgbm_hip_ctx* c, float* grad, float* hess, int64_t n) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_labels || c->num_class < 2 || !c->gk)
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "no multiclass gradients yet");
+  if (n != (int64_t)c->num_class * c->N)
+    return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_class * num_data");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (grad) HIPCHK(c, hipMemcpy(grad, c->gk, (size_t)n * 4, hipMemcpyDeviceToHost));
+  if (hess) HIPCHK(c, hipMemcpy(hess, c->hk, (size_t)n * 4, hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
 }
 
 int lgbm_hip_set_lookahead(lgbm_hip_ctx* c, int32_t enable) {
@@ -1814,7 +2017,9 @@ int lgbm_hip_get_scores(lgbm_hip_ctx* c, double* out, int64_t n) {
   if (rc) return rc;
   if (!c->have_labels) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set labels first");
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
-  if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_data");
+  if (n != (int64_t)c->num_class * c->N)
+    return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_class * num_data");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
   HIPCHK(c, hipMemcpy(out, c->score, (size_t)n * 8, hipMemcpyDeviceToHost));
   return LGBM_HIP_OK;
 }

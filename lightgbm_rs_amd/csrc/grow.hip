@@ -410,7 +410,10 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     T.split_gain[node] = (float)(gain + ctl->cfg.min_gain_to_split);  // learner.rs:3985
     T.threshold_in_bin[node] = thr;
     int8_t dt = 0;
-    if (dl) dt |= 2;
+    if (ft.categorical)
+      dt |= 1;  // Tree::split_categorical: no default-left bit
+    else if (dl)
+      dt |= 2;
     dt |= (int8_t)((ft.missing_type & 3) << 2);
     T.decision_type[node] = dt;
     T.internal_value[node] = iv;  // the split leaf's output
@@ -428,6 +431,12 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     r.na_bin = (int32_t)ft.num_bin - 1;
     r.left = ~cm.x;
     r.right = ~cm.w;
+    if (ft.categorical) {
+      r.flags = ROUTE_CAT;
+      const uint32_t* cb = L.cat_bits + ((size_t)p * F + fpos) * 8;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) T.cat_left[node * 8 + w] = cb[w];
+    }
     T.nodes[node] = r;
   }
   for (int l = tid; l < nl; l += PLAN_THREADS) {
@@ -458,6 +467,13 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     router_of(ft, b, &J.pmin, &J.th, &J.flags);
     J.max_bin = (int32_t)ft.max_bin;
     J.na_bin = (int32_t)ft.num_bin - 1;
+    if (ft.categorical) {
+      // bit 8: the SplitInfo counts make the left child the smaller one
+      J.flags = ROUTE_CAT | (b.left_count < b.right_count ? 1 << 8 : 0);
+      const uint32_t* cb = L.cat_bits + ((size_t)p * F + fpos) * 8;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) J.cat[w] = cb[w];
+    }
     // quantized gradients: build the histogram of the side the scan expects to be
     // smaller inside the partition pass (f32: k_hist_f32 builds the smaller child)
     J.acc_right = fp ? -1 : (b.right_count < b.left_count ? 1 : 0);
@@ -643,7 +659,10 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
 #pragma unroll
     for (int k = 0; k < PR; ++k) {
       const int32_t bin = (int32_t)rec_byte(w[k], J.fbyte);
-      isleft[k] = valid[k] && !route_right(bin, J.pmin, J.max_bin, J.th, J.na_bin, J.flags);
+      const bool left = (J.flags & ROUTE_CAT)
+                            ? ((J.cat[bin >> 5] >> (bin & 31)) & 1u) != 0u
+                            : !route_right(bin, J.pmin, J.max_bin, J.th, J.na_bin, J.flags);
+      isleft[k] = valid[k] && left;
       const unsigned long long m = __ballot(isleft[k]);
       rank[k] = (int32_t)__popcll(m & lanemask_lt());
       if (lane == 0) s_cnt[k * kWaves + wave] = (int32_t)__popcll(m);
@@ -729,6 +748,11 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
         nd.rev[J.cr] = 1;
         nd.sums[J.cl].n = lc;
         nd.sums[J.cr].n = rc;
+        // categorical: the children's scan seeds follow the SplitInfo counts (pending
+        // order in the job flags), the histogram the partition counts
+        const int32_t sw = (J.flags & ROUTE_CAT) && (((J.flags >> 8) & 1) != (lc < rc ? 1 : 0));
+        nd.sums[J.cl]._pad = sw;
+        nd.sums[J.cr]._pad = sw;
         if (FP) {
           // the round's ConstructHistogram job (k_hist_f32 runs next): the smaller
           // child (partition counts; a tie makes the right child the smaller one,
@@ -864,7 +888,15 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
   if (j >= n_jobs) return;  // only after the job's fields are known to be live
   const DevNodes& nd = L.nodes;
   const int32_t lcnt = nd.count[cl], rcnt = nd.count[cr], dcl = nd.depth[cl];
-  const LeafSums scl = nd.sums[cl], scr = nd.sums[cr];
+  LeafSums scl = nd.sums[cl], scr = nd.sums[cr];
+  if (scl._pad) {
+    // a categorical split whose SplitInfo counts order the children unlike the
+    // partition: the reference seeds each child's scan with the other's sums and count
+    // (seed_child_leaf_splits, learner.rs:4191-4229)
+    const LeafSums t = scl;
+    scl = scr;
+    scr = t;
+  }
   const bool pgate = L.splittable[(size_t)p * F + f] == 0;
   const int nb = (int)ft.num_bin;
   const size_t sl = L.slot_len;
@@ -1002,7 +1034,11 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
     }
   } else {
     const ScanCfg sc = make_scan_cfg(ctl->cfg);
-    wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
+    if (ft.categorical)  // bin_type dispatch (learner.rs:3103-3118)
+      wave_scan_cat(wv == 0 ? cs : cp, ft, sc, ctl->cfg, ls.sg, ls.sh, ls.n, ls.weight, out,
+                    L.cat_bits + ((size_t)leaf * F + f) * 8);
+    else
+      wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
     if (lane_id() == 0) {
       // splittability from the raw scan, then feature_contri scales the gain the
       // ArgMax compares (learner.rs:3235-3252)
@@ -1050,7 +1086,9 @@ __global__ void k_tree_finalize(DevLearner L) {
     const NodeRoute r = T.nodes[n];
 #pragma unroll
     for (int w = 0; w < 8; ++w)
-      T.route_mask[n * 8 + w] = route_right_word(w, r.pmin, r.max_bin, r.th, r.na_bin, r.flags);
+      T.route_mask[n * 8 + w] = (r.flags & ROUTE_CAT)
+                                    ? ~T.cat_left[n * 8 + w]
+                                    : route_right_word(w, r.pmin, r.max_bin, r.th, r.na_bin, r.flags);
     T.route_node[n] = ((uint32_t)r.f & 0xffu) | (((uint32_t)lc & 0xfffu) << 8) |
                       (((uint32_t)rc & 0xfffu) << 20);
   }

@@ -99,6 +99,7 @@ struct DevTree {
   NodeRoute* nodes;
   uint32_t* route_mask;       // [MAX_LEAVES - 1][8]: bins a node routes right (bit set)
   uint32_t* route_node;       // [MAX_LEAVES - 1]: record byte | left << 8 | right << 20
+  uint32_t* cat_left;         // [MAX_LEAVES - 1][8]: categorical node: bins going left
 };
 
 struct DevLearner {
@@ -126,6 +127,7 @@ struct DevLearner {
   lgbm_split_info* best;        // [slot_cap]
   int32_t* best_fpos;           // [slot_cap] feature position of best
   uint8_t* splittable;          // [slot_cap][F]
+  uint32_t* cat_bits;           // [slot_cap][F][8] categorical features: best split's left bins
   int32_t* plan_state;          // [5][MAX_LEAVES] leaf / node linkage owned by k_plan
   uint64_t* tile_state;         // stable per-op partition: left-row prefix per tile
   double* stats;                // [0] rows partitioned, [1] partition launches, [2] root
@@ -176,6 +178,8 @@ void launch_bin_records(const void* x, int32_t f64, int32_t col_major, int64_t n
 void launch_absmax(const float* g, const float* h, int64_t n, uint4* partials, hipStream_t s);
 void launch_grad_binary(const double* score, const float* label, float* g, float* h, int64_t n,
                         uint4* partials, hipStream_t s);
+void launch_grad_softmax(const double* score, const float* label, float* g, float* h, int64_t n,
+                         int32_t K, double factor, hipStream_t s);
 void launch_quant_scales(Ctl* ctl, const uint4* partials, int64_t n, int32_t bins,
                          int32_t force_const, hipStream_t s);
 void launch_quantize(const float* g, const float* h, int64_t n, const Ctl* ctl,

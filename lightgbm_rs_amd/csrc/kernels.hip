@@ -2,6 +2,7 @@
 //
 //   k_pack_records   resident bin layout (upload_resident_bins, lib.rs:4368-4433)
 //   k_grad_binary    BinaryLogloss::get_gradients (lgbm-objective/src/binary.rs:134-172)
+//   k_grad_softmax   MulticlassSoftmax::get_gradients (lgbm-objective/src/multiclass.rs:138-180)
 //   k_absmax         compute_scales max-abs pass (gradient_discretizer.rs:145-165)
 //   k_quant_scales   compute_scales scale math
 //   k_quantize       discretize (+ dequantized write-back), xorshift64 with jump-ahead
@@ -120,6 +121,54 @@ __global__ __launch_bounds__(256) void k_grad_binary(const double* __restrict__ 
     stat_add(s, gv, hv);
   }
   block_stat_write(s, partials);
+}
+
+// MulticlassSoftmax::get_gradients (lgbm-objective/src/multiclass.rs:138-180) with
+// Common::Softmax (lgbm-model/src/objective.rs:307-322), per row over the class-major
+// scores: the max by a fold from class 0, e_k = exp(s_k - max), their sum in class
+// order, p_k = e_k / sum; grad = p - 1 for the row's class, else p; hess =
+// factor p (1 - p); f32 on store.  KR > 0: the K exponentials stay in registers; KR =
+// 0 (any K): they are recomputed (the same operations, so the same values).
+template <int KR>
+__global__ __launch_bounds__(256) void k_grad_softmax(const double* __restrict__ score,
+                                                      const float* __restrict__ label,
+                                                      float* __restrict__ g, float* __restrict__ h,
+                                                      int64_t n, int32_t K, double factor) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
+    const float lf = label[r];
+    const int32_t li = lf == lf ? (int32_t)lf : 0;  // labels were checked to lie in (-1, K)
+    if constexpr (KR > 0) {
+      double e[KR];
+#pragma unroll
+      for (int k = 0; k < KR; ++k) e[k] = score[(size_t)k * n + r];
+      double wmax = e[0];
+#pragma unroll
+      for (int k = 1; k < KR; ++k) wmax = fmax(e[k], wmax);
+      double wsum = 0.0;
+#pragma unroll
+      for (int k = 0; k < KR; ++k) {
+        e[k] = exp(e[k] - wmax);
+        wsum += e[k];
+      }
+#pragma unroll
+      for (int k = 0; k < KR; ++k) {
+        const double p = e[k] / wsum;
+        g[(size_t)k * n + r] = li == k ? (float)(p - 1.0) : (float)p;
+        h[(size_t)k * n + r] = (float)(factor * p * (1.0 - p));
+      }
+    } else {
+      double wmax = score[r];
+      for (int32_t k = 1; k < K; ++k) wmax = fmax(score[(size_t)k * n + r], wmax);
+      double wsum = 0.0;
+      for (int32_t k = 0; k < K; ++k) wsum += exp(score[(size_t)k * n + r] - wmax);
+      for (int32_t k = 0; k < K; ++k) {
+        const double p = exp(score[(size_t)k * n + r] - wmax) / wsum;
+        g[(size_t)k * n + r] = li == k ? (float)(p - 1.0) : (float)p;
+        h[(size_t)k * n + r] = (float)(factor * p * (1.0 - p));
+      }
+    }
+  }
 }
 
 // compute_scales (gradient_discretizer.rs:145-165) from the reduced statistics.
@@ -758,7 +807,10 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
     return;
   }
   const ScanCfg sc = make_scan_cfg(ctl->cfg);
-  wave_scan(cs, ft, sc, sg, sh, nrows, weight, out);
+  if (ft.categorical)  // bin_type dispatch (learner.rs:3103-3118)
+    wave_scan_cat(cs, ft, sc, ctl->cfg, sg, sh, nrows, weight, out, L.cat_bits + (size_t)f * 8);
+  else
+    wave_scan(cs, ft, sc, sg, sh, nrows, weight, out);
   if (lane_id() == 0) {
     L.splittable[f] = out->gain > -__builtin_inf() ? 1 : 0;
     out->gain *= ft.penalty;  // feature_contri (learner.rs:3235-3252)
@@ -876,6 +928,23 @@ void launch_grad_binary(const double* score, const float* label, float* g, float
                         uint4* partials, hipStream_t s) {
   k_grad_binary<<<dim3((unsigned)stat_blocks(n)), dim3(256), 0, s>>>(score, label, g, h, n,
                                                                      partials);
+}
+void launch_grad_softmax(const double* score, const float* label, float* g, float* h, int64_t n,
+                         int32_t K, double factor, hipStream_t s) {
+  const int64_t blocks = std::min<int64_t>(std::max<int64_t>((n + 255) / 256, 1), 4096);
+  const dim3 gr((unsigned)blocks), b(256);
+  switch (K) {
+#define SOFTMAX_K(k) \
+  case k:            \
+    k_grad_softmax<k><<<gr, b, 0, s>>>(score, label, g, h, n, K, factor); \
+    break;
+    SOFTMAX_K(2) SOFTMAX_K(3) SOFTMAX_K(4) SOFTMAX_K(5) SOFTMAX_K(6) SOFTMAX_K(7) SOFTMAX_K(8)
+    SOFTMAX_K(9) SOFTMAX_K(10) SOFTMAX_K(11) SOFTMAX_K(12) SOFTMAX_K(13) SOFTMAX_K(14)
+    SOFTMAX_K(15) SOFTMAX_K(16)
+#undef SOFTMAX_K
+    default:
+      k_grad_softmax<0><<<gr, b, 0, s>>>(score, label, g, h, n, K, factor);
+  }
 }
 void launch_quant_scales(Ctl* ctl, const uint4* partials, int64_t n, int32_t bins,
                          int32_t force_const, hipStream_t s) {

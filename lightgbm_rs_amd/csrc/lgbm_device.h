@@ -36,6 +36,7 @@
 #define PART_WAVES (PART_THREADS / LGBM_WAVE)
 #define PART_SLOT_MAX 8                 // blocks per job whose cells go to per-block slots
 #define QUANT_MAX_ROWS (1ll << 29)      // int32 cells: sum of q_h <= 4 N < 2^31
+#define QUANT_LDS_CELLS 8192            // quantized builds: every cell in LDS (8 B, 64 KiB)
 #define PART_MIN_TILE 1024                // smallest tile of any partition launch shape
 #define SCAN_THREADS 128                // two waves: smaller leaf, larger leaf
 #define PLAN_THREADS 1024
@@ -95,6 +96,8 @@ struct DevFeature {
   int32_t na_as_missing;
   int32_t run_forward;
   double penalty;      // config.feature_contri of the feature's real index (1: none)
+  int32_t categorical; // 1: split by category sets (FindBestThresholdCategorical)
+  int32_t _pad2;
 };
 
 struct LeafSums {
@@ -111,9 +114,11 @@ struct NodeRoute {
   int32_t max_bin;
   int32_t th;         // threshold + pmin (- 1 if mfb == 0)
   int32_t na_bin;     // num_bin - 1
-  int32_t flags;      // 1: default_to_right, 2: na_as_missing, 4: default_left
+  int32_t flags;      // 1: default_to_right, 2: na_as_missing, 4: default_left,
+                      // ROUTE_CAT: categorical (the bins going left are a bit set)
   int32_t left, right;
 };
+#define ROUTE_CAT 8
 
 // One leaf split of a partition round.  The tree driver splits up to SPEC_MAX
 // leaves per round (the best-ranked leaves not yet split; each is committed to
@@ -127,6 +132,7 @@ struct PartJob {
   int32_t acc_right;  // histogram side built in the pass: 0 left, 1 right, -1 none
   int32_t ntiles;
   int64_t tile0;      // first tile of the job in the round's tile space
+  uint32_t cat[8];    // flags & ROUTE_CAT: bins going left (bit b of word w: bin 32w + b)
 };
 
 #define SPEC_MAX 32        // partition jobs per round

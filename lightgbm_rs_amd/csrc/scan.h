@@ -280,6 +280,217 @@ static __device__ void wave_scan(const double* hist, const DevFeature& ft, const
   }
 }
 
+// ===========================================================================
+// FindBestThresholdCategorical for one (leaf, feature) by one wave
+// (feature_histogram_categorical.rs:96-495) over the compacted histogram (index t =
+// bin - offset, categories t in [1 - offset, num_bin - offset)).
+//   one-hot (num_bin <= max_cat_to_onehot): lane t tries "category t left, the rest
+//   right"; the strict-> best keeps the lowest t on ties;
+//   many-vs-many: the categories whose round_int(hess * cnt_factor) >= cat_smooth,
+//   ranked by grad / (hess + cat_smooth) with ties in bin order (the stable sort),
+//   then lane 0 walks the ranked list from its low end and lane 1 from its high end
+//   with the reference's sequential sums, gates and group counter; the low-end walk
+//   wins ties (it runs first in the reference).
+// sum_hessian is the leaf's raw sum; the scan bumps it by 2 kEpsilon as the
+// categorical dispatch does (learner.rs:3103-3118).  `bits` (8 words) receives the
+// bins that go left.  A NaN sort key (cat_smooth <= 0 and an empty category) ranks
+// as 0.0: the reference's order for it depends on its sort algorithm.
+// ===========================================================================
+__device__ __forceinline__ double leaf_gain_given_output(bool use_l1, double g, double h,
+                                                         double l1, double l2, double out) {
+  const double gg = use_l1 ? threshold_l1(g, l1) : g;
+  return -__builtin_fma(2.0 * gg, out, (h + l2) * out * out);
+}
+
+static __device__ void wave_scan_cat(const double* hist, const DevFeature& ft, const ScanCfg& c,
+                                     const lgbm_gain_config& cfg, double sum_gradient,
+                                     double sum_hessian, int32_t num_data, double po,
+                                     lgbm_split_info* out, uint32_t* bits) {
+  __shared__ double s_key[SCAN_THREADS / LGBM_WAVE][256];
+  __shared__ int32_t s_sorted[SCAN_THREADS / LGBM_WAVE][256];
+  __shared__ uint32_t s_bits[SCAN_THREADS / LGBM_WAVE][8];
+  const int w = (int)(threadIdx.x / LGBM_WAVE);
+  const int lane = (int)lane_id();
+  const double eps = k_eps();
+  const double ninf = -__builtin_inf();
+  const double sh = sum_hessian + 2.0 * eps;
+  const double gain_shift =
+      c.use_smoothing
+          ? leaf_gain_given_output(c.use_l1, sum_gradient, sh, c.l1, c.l2, po)
+          : leaf_gain_full(c.use_l1, sum_gradient, sh, c.l1, c.l2, c.mds, false, 0.0, num_data, 0.0);
+  const double mgs = gain_shift + c.min_gain;
+  const int32_t nb = (int32_t)ft.num_bin, offset = ft.offset;
+  const int32_t t0 = 1 - offset, t1 = nb - offset;  // categories t in [t0, t1)
+  const double cf = (double)num_data / sh;
+  const bool onehot = nb <= cfg.max_cat_to_onehot;
+  ScanCfg cc = c;  // many-vs-many: l2 + cat_l2 for the gains and outputs
+  if (!onehot) cc.l2 = c.l2 + cfg.cat_l2;
+  bool any = false;
+  double best_gain = ninf, best_lg = 0.0, best_lh = 0.0;
+  int32_t best_lc = 0, best_t = -1, best_dir = 1, used = 0;
+  if (lane < 8) s_bits[w][lane] = 0u;
+  if (onehot) {
+    for (int32_t base = t0; base < t1; base += LGBM_WAVE) {
+      const int32_t t = base + lane;
+      double gain = ninf, grad = 0.0, hess = 0.0;
+      int32_t cnt = 0;
+      bool cand = false;
+      if (t < t1) {
+        grad = hist[2 * t];
+        hess = hist[2 * t + 1];
+        cnt = round_int(hess * cf);
+        const int32_t other = num_data - cnt;
+        const double soh = sh - hess - eps;
+        if (!(cnt < c.min_d || hess < c.min_h) && !(other < c.min_d) && !(soh < c.min_h)) {
+          gain = split_gain_of(c, sum_gradient - grad, soh, grad, hess + eps, other, cnt, po);
+          cand = gain > mgs;
+        }
+      }
+      if (__ballot(cand)) any = true;
+      double rg = cand ? gain : ninf;
+      int32_t rl = cand ? lane : LGBM_WAVE;
+      for (int off = 32; off >= 1; off >>= 1) {
+        const double og = __shfl_xor(rg, off);
+        const int32_t ol = __shfl_xor(rl, off);
+        if (og > rg || (og == rg && ol < rl)) {
+          rg = og;
+          rl = ol;
+        }
+      }
+      if (rl < LGBM_WAVE && rg > best_gain) {
+        best_gain = rg;
+        best_t = __shfl(t, rl);
+        best_lg = __shfl(grad, rl);
+        best_lh = __shfl(hess, rl) + eps;
+        best_lc = __shfl(cnt, rl);
+      }
+    }
+  } else {
+    // ranks of the kept categories by (key, bin); n kept in total
+    const int32_t m = t1 - t0;
+    unsigned long long keep[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int32_t i = lane + LGBM_WAVE * k;
+      const int32_t t = t0 + i;
+      bool kp = false;
+      double key = 0.0;
+      if (i < m) {
+        const double hess = hist[2 * t + 1];
+        kp = (double)round_int(hess * cf) >= cfg.cat_smooth;
+        key = hist[2 * t] / (hess + cfg.cat_smooth);
+        if (key != key) key = 0.0;
+      }
+      keep[k] = __ballot(kp);
+      s_key[w][i] = key;
+    }
+    used = __popcll(keep[0]) + __popcll(keep[1]) + __popcll(keep[2]) + __popcll(keep[3]);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int32_t i = lane + LGBM_WAVE * k;
+      if (!((keep[k] >> lane) & 1ull)) continue;
+      const double key = s_key[w][i];
+      int32_t r = 0;
+      for (int32_t j = 0; j < m; ++j) {
+        if (!((keep[j >> 6] >> (j & 63)) & 1ull)) continue;
+        const double o = s_key[w][j];
+        r += (o < key || (!(key < o) && j < i)) ? 1 : 0;
+      }
+      s_sorted[w][r] = t0 + i;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int32_t max_num_cat = min(cfg.max_cat_threshold, (used + 1) / 2);
+    bool split = false;
+    double g_best = ninf, g_lg = 0.0, g_lh = 0.0;
+    int32_t g_lc = 0, g_i = -1;
+    if (lane < 2) {
+      const int32_t dir = lane == 0 ? 1 : -1;
+      int32_t pos = lane == 0 ? 0 : used - 1;
+      int32_t group = 0, lcnt = 0;
+      double slg = 0.0, slh = eps;
+      for (int32_t i = 0; i < used && i < max_num_cat; ++i) {
+        const int32_t t = s_sorted[w][pos];
+        pos += dir;
+        const double grad = hist[2 * t], hess = hist[2 * t + 1];
+        const int32_t cnt = round_int(hess * cf);
+        slg += grad;
+        slh += hess;
+        lcnt += cnt;
+        group += cnt;
+        if (lcnt < c.min_d || slh < c.min_h) continue;
+        const int32_t rcnt = num_data - lcnt;
+        if (rcnt < c.min_d || rcnt < cfg.min_data_per_group) break;
+        const double srh = sh - slh;
+        if (srh < c.min_h) break;
+        if (group < cfg.min_data_per_group) continue;
+        group = 0;
+        const double gain = split_gain_of(cc, slg, slh, sum_gradient - slg, srh, lcnt, rcnt, po);
+        if (gain <= mgs) continue;
+        split = true;
+        if (gain > g_best) {
+          g_best = gain;
+          g_lc = lcnt;
+          g_lg = slg;
+          g_lh = slh;
+          g_i = i;
+        }
+      }
+    }
+    // lane 0: the low-end walk; lane 1 replaces it only with a strictly larger gain
+    const bool s1 = __shfl(split, 1) != 0;
+    const double gb1 = __shfl(g_best, 1);
+    any = (__shfl(split, 0) != 0) || s1;
+    const int src = gb1 > __shfl(g_best, 0) ? 1 : 0;
+    best_gain = __shfl(g_best, src);
+    best_lg = __shfl(g_lg, src);
+    best_lh = __shfl(g_lh, src);
+    best_lc = __shfl(g_lc, src);
+    best_t = __shfl(g_i, src);
+    best_dir = src == 0 ? 1 : -1;
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (any) {
+    if (onehot) {
+      if (lane == 0) {
+        const int32_t b = best_t + offset;
+        s_bits[w][b >> 5] |= 1u << (b & 31);
+      }
+    } else {
+      for (int32_t p = lane; p < used; p += LGBM_WAVE) {
+        const bool sel = best_dir == 1 ? p <= best_t : p >= used - 1 - best_t;
+        if (!sel) continue;
+        const int32_t b = s_sorted[w][p] + offset;
+        atomicOr(&s_bits[w][b >> 5], 1u << (b & 31));
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (lane < 8) bits[lane] = s_bits[w][lane];
+  if (lane == 0) {
+    if (!any) {
+      split_set_none(out);
+      out->default_left = 0;
+    } else {
+      // the finalization (:395-495): outputs with the scan's l2, sums without kEpsilon
+      const int32_t rc = num_data - best_lc;
+      out->left_output = leaf_output_full(cc.use_l1, best_lg, best_lh, cc.l1, cc.l2, cc.mds,
+                                          cc.use_smoothing, cc.ps, best_lc, po);
+      out->left_count = best_lc;
+      out->left_sum_gradient = best_lg;
+      out->left_sum_hessian = best_lh - eps;
+      out->right_output = leaf_output_full(cc.use_l1, sum_gradient - best_lg, sh - best_lh, cc.l1,
+                                           cc.l2, cc.mds, cc.use_smoothing, cc.ps, rc, po);
+      out->right_count = rc;
+      out->right_sum_gradient = sum_gradient - best_lg;
+      out->right_sum_hessian = sh - best_lh - eps;
+      out->gain = best_gain - mgs;
+      out->default_left = 0;
+      out->threshold = 0;
+    }
+  }
+}
+
 struct BestKey {
   double gain;
   int32_t feat;  // real feature index (-1 none)

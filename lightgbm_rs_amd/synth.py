@@ -3,6 +3,13 @@
 config0_like(): configs[0] — N rows x 28 float32 features ~N(0,1), the same logistic
 label, binned to <= 255 quantile bins (the f32-gradient CPU-reference case).
 
+config3_raw_host() / config3_binned(): configs[3] — N rows x 100 float32 features (80
+~N(0,1), 20 integer-coded categoricals with 32 levels), class = argmax of 10 random
+linear projections of the features (the categoricals one-hot encoded) + Gumbel noise;
+numerical features binned like
+configs[1] (max_bin 255), categorical ones by find_bin_categorical over the whole
+column (booster.rs:449-520).
+
 config1_like(): configs[1] — N rows x 28 float32 features (21 ~N(0,1), 7 derived as
 products / abs of pairs), logistic label logit = w.x + 0.5*x0*x1 + N(0, 0.1) with
 w ~ N(0,1), binned to <= max_bin bins per feature (u8) by this library's BinMapper
@@ -136,3 +143,51 @@ def _config1_torch(n, seed, max_bin, device):
         upper.extend([float(q) for q in qs.cpu()] + [float("inf")])
     return (bins.cpu().numpy(), _meta_for(nbs), np.array(upper, dtype=np.float64),
             y.cpu().numpy())
+
+
+def config3_raw_host(n, seed=0x5EED0003, num_class=10, n_num=80, n_cat=20, levels=32):
+    """configs[3]'s raw table on the host: X float32 [n_num + n_cat, n] (one feature per
+    row; the last n_cat rows hold category codes 0..levels-1), the class labels as
+    float32, and the categorical feature positions."""
+    rng = np.random.default_rng(seed)
+    F = n_num + n_cat
+    X = np.empty((F, n), dtype=np.float32)
+    X[:n_num] = rng.standard_normal((n_num, n), dtype=np.float32)
+    X[n_num:] = rng.integers(0, levels, (n_cat, n)).astype(np.float32)
+    # the projections read the numerical features directly and each categorical one
+    # through its one-hot encoding (a random weight per (class, level))
+    W = rng.standard_normal((num_class, n_num)).astype(np.float32) / np.float32(np.sqrt(n_num))
+    E = rng.standard_normal((n_cat, levels, num_class)).astype(np.float32) * np.float32(0.5)
+    logits = W @ X[:n_num]
+    for j in range(n_cat):
+        logits += E[j][X[n_num + j].astype(np.int64)].T
+    u = rng.random((num_class, n), dtype=np.float32)
+    gumbel = -np.log(-np.log(np.clip(u, 1e-12, 1.0 - 1e-7)))
+    y = np.argmax(logits + gumbel, axis=0).astype(np.float32)
+    return X, y, list(range(n_num, F))
+
+
+def config3_binned(n, seed=0x5EED0003, max_bin=255, min_data_in_leaf=20, **kw):
+    """configs[3] binned: (bins u8 [F, n], feature meta, per-bin values (numerical upper
+    bounds, categorical category codes), labels, categorical positions, raw X)."""
+    from .backend import feature_meta
+    from .binning import BinMapper, sample_indices
+    X, y, cat = config3_raw_host(n, seed, **kw)
+    F = X.shape[0]
+    idx = sample_indices(n, 200000, 1)
+    bins = np.zeros((F, n), dtype=np.uint8)
+    meta, vals, mappers = [], [], []
+    for f in range(F):
+        if f in cat:
+            m = BinMapper.from_sample(X[f].astype(np.float64), n, categorical=True,
+                                      min_split_data=min_data_in_leaf, max_bin=max_bin)
+            vals.extend(float(c) for c in m.categories)
+        else:
+            m = BinMapper.from_sampled_column(X[f, idx].astype(np.float64), n, max_bin=max_bin,
+                                              min_data_in_leaf=min_data_in_leaf)
+            vals.extend(m.upper_bounds.tolist())
+        bins[f] = m.value_to_bin(X[f]).astype(np.uint8)
+        meta.append(feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f,
+                                 bin_type=m.bin_type))
+        mappers.append(m)
+    return bins, meta, np.array(vals, dtype=np.float64), y, cat, X, mappers

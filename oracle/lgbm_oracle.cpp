@@ -1311,9 +1311,11 @@ struct Multiclass {
     label.resize(n);
     init_probs.assign(k, 0.0);
     for (int64_t i = 0; i < n; ++i) {
-      const int32_t li = (int32_t)labels[i];  // truncation toward zero
-      if (!(labels[i] == labels[i]) || li < 0 || li >= k)
+      // `l as i32`: truncation toward zero, NaN to 0 (saturating cast)
+      const double l = labels[i];
+      if (l == l && (l <= -1.0 || l >= (double)k))
         return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "multiclass label out of [0, num_class)");
+      const int32_t li = l == l ? (int32_t)l : 0;
       init_probs[li] += 1.0;
       label[i] = li;
     }

@@ -85,12 +85,27 @@ def test_device_bins_from_device_memory(be):
         hip.hipFree(d)
 
 
-def test_categorical_mapper_is_refused(be):
-    X = np.random.default_rng(1).integers(0, 5, (1000, 2)).astype(np.float64)
-    ms = feature_mappers(X, categorical_features=[1])
-    with pytest.raises(HipError) as e:
-        be.upload_raw(X, ms)
-    assert "categorical" in str(e.value)
+def test_categorical_columns_bin_like_the_mapper(be):
+    """Categorical columns on the device: ValueToBin of the categorical mapper (the
+    sorted (category, bin) table), NaN / negative / unseen categories to bin 0."""
+    rng = np.random.default_rng(1)
+    n = 50_000
+    X = np.empty((n, 3), np.float64)
+    X[:, 0] = rng.standard_normal(n)
+    X[:, 1] = rng.integers(0, 40, n)
+    X[:, 2] = rng.integers(0, 7, n)
+    ms = feature_mappers(X[:40_000], categorical_features=[1, 2], max_bin=255)
+    X[::97, 1] = np.nan
+    X[::89, 1] = -3.0
+    X[::83, 2] = 1000.0  # unseen by the mapper
+    X[::79, 2] = 2.7     # truncates to category 2
+    be.upload_raw(X, ms)
+    got = be.get_bins()
+    for f, m in enumerate(ms):
+        assert np.array_equal(got[f], m.value_to_bin(X[:, f]).astype(np.uint8)), f
+    unseen = np.arange(0, n, 83)
+    unseen = unseen[unseen % 79 != 0]  # rows not overwritten with 2.7
+    assert (got[1][::97] == 0).all() and (got[2][unseen] == 0).all()
 
 
 def test_raw_to_model_predicts_training_scores(be):

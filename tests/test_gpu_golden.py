@@ -142,13 +142,11 @@ def test_failed_reupload_leaves_no_usable_state():
         b.upload_resident_grad_hess(g, h)
         b.discretize_dequantize_in_place(4, True, 1)
         b.grow_tree_on_device_with_cfg(cfg, 31, -1)  # captures the tree graph
-        # 40 features x 256 bins: more histogram cells than the layout holds
-        wide, wmeta, wub = make_binned(1000, 40, seed=82, max_bin=256, missing_mix=False,
+        # 130 features: more than a row record holds
+        wide, wmeta, wub = make_binned(1000, 130, seed=82, max_bin=16, missing_mix=False,
                                        mfb_mix=False)
-        for m in wmeta:
-            m.num_bin, m.max_bin, m.default_bin = 256, 255, 256
         with pytest.raises(HipError):
-            b.upload_resident_bins(wide, wmeta, None)
+            b.upload_resident_bins(wide, wmeta, wub)
         with pytest.raises(HipError):
             b.grow_tree_on_device_with_cfg(cfg, 31, -1)
         with pytest.raises(HipError):
