@@ -248,23 +248,40 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   // unsplit key so far (the best unsplit leaf at the start, raised by the children
   // of each commit); the right child of the i-th commit gets leaf id nl0 + i.  With S
   // ranked, that is one exclusive prefix maximum over the ranks and a ballot.
-  for (int l = tid; l < nl0; l += PLAN_THREADS) {
-    const int32_t s = s_ps[PS_LEAF_SLOT][l];
-    const int2 ch = s_child[s];
-    const LKey k = lkey(s_gain[s], s_feat[s], l);
-    s_lc[l] = ch;
-    s_key[l] = k;
-    if (ch.x >= 0) {
+  static_assert(MAX_LEAVES <= PLAN_THREADS, "one thread per leaf");
+  if (tid < MAX_LEAVES) {  // whole waves: the wave reductions below see every lane
+    const int l = tid;
+    const bool live = l < nl0;
+    const int32_t s = live ? s_ps[PS_LEAF_SLOT][l] : 0;
+    const int2 ch = live ? s_child[s] : make_int2(-1, -1);
+    const LKey k = live ? lkey(s_gain[s], s_feat[s], l) : LKey{0ull, 0ull};
+    if (live) {
+      s_lc[l] = ch;
+      s_key[l] = k;
+    }
+    if (live && ch.x >= 0) {
       s_lcg[l] = make_double2(s_gain[ch.x], s_gain[ch.y]);
       s_lcf[l] = make_int2(s_feat[ch.x], s_feat[ch.y]);
-      if (k.hi != 0ull) {
-        const int32_t pos = atomicAdd(&s_nS, 1);
-        s_S[pos] = l;
-        s_SK[pos] = k;
-      }
-    } else if (k.hi != 0ull) {
-      atomicMax(&s_uhi, (unsigned long long)k.hi);
     }
+    // S: one LDS atomic per wave reserves the wave's entries
+    const bool in_s = live && ch.x >= 0 && k.hi != 0ull;
+    const unsigned long long sm = __ballot(in_s);
+    int32_t base = 0;
+    if (lane == 0 && sm) base = atomicAdd(&s_nS, (int32_t)__popcll(sm));
+    base = __shfl(base, 0);
+    if (in_s) {
+      const int32_t pos = base + (int32_t)__popcll(sm & lanemask_lt());
+      s_S[pos] = l;
+      s_SK[pos] = k;
+    }
+    // the best unsplit key's high word: a wave maximum, one LDS atomic per wave
+    unsigned long long u = (live && ch.x < 0) ? k.hi : 0ull;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const unsigned long long o = __shfl_xor(u, off);
+      u = o > u ? o : u;
+    }
+    if (lane == 0 && u != 0ull) atomicMax(&s_uhi, u);
   }
   __syncthreads();
   for (int l = tid; l < nl0; l += PLAN_THREADS) {
@@ -356,11 +373,16 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   // candidate's rank (number of better candidates) is counted by 4 threads.
   if (!s_done) {
     const int32_t nl = nl_;
-    for (int l = tid; l < nl; l += PLAN_THREADS) {
-      const LKey k = s_key[l];
-      const bool cand = s_lc[l].x < 0 && k.hi != 0ull;
-      s_ck[l] = cand ? k : LKey{0ull, 0ull};
-      if (cand) atomicAdd(&s_ncand, 1);
+    if (tid < MAX_LEAVES) {  // whole waves, one LDS atomic per wave
+      const int l = tid;
+      bool cand = false;
+      if (l < nl) {
+        const LKey k = s_key[l];
+        cand = s_lc[l].x < 0 && k.hi != 0ull;
+        s_ck[l] = cand ? k : LKey{0ull, 0ull};
+      }
+      const unsigned long long cm = __ballot(cand);
+      if (lane == 0 && cm) atomicAdd(&s_ncand, (int32_t)__popcll(cm));
     }
     __syncthreads();
     int32_t allowed = 0;

@@ -79,26 +79,40 @@ __device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int3
 // rounds exactly as its loop does.  Lanes that hold no bin pass (+0.0, +0.0, 0):
 // adding +0.0 to an accumulation that started at a value other than -0.0 never
 // changes it.  The values go through a per-wave LDS row so the chain reads them as
-// uniform (broadcast) loads; the loop has no branch and no cross-lane move.
+// uniform (broadcast) loads, eight candidates per batch so a batch's loads are all in
+// flight before its adds (lanes at or past cnt store zeros, so a batch may run past
+// cnt); the loop has no branch and no cross-lane move.
 __device__ __forceinline__ void prefix_in_order(double g, double h, int32_t c, int32_t cnt,
                                                 int lane, double* sg, double* sh, int32_t* sc) {
   __shared__ double pf_g[SCAN_THREADS / LGBM_WAVE][LGBM_WAVE];
   __shared__ double pf_h[SCAN_THREADS / LGBM_WAVE][LGBM_WAVE];
   __shared__ int32_t pf_c[SCAN_THREADS / LGBM_WAVE][LGBM_WAVE];
   const int w = (int)(threadIdx.x / LGBM_WAVE);
-  pf_g[w][lane] = g;
-  pf_h[w][lane] = h;
-  pf_c[w][lane] = c;
+  const bool in = lane < cnt;
+  pf_g[w][lane] = in ? g : 0.0;
+  pf_h[w][lane] = in ? h : 0.0;
+  pf_c[w][lane] = in ? c : 0;
   __builtin_amdgcn_wave_barrier();
   double ag = *sg, ah = *sh;
   int32_t ac = *sc;
-  for (int32_t i = 0; i < cnt; ++i) {
-    // lanes before i add +0.0 (all-zero bits): a mask, not a select, so the loads
-    // stay unconditional and the loop branch-free
-    const unsigned long long m = i <= lane ? ~0ull : 0ull;
-    ag += __longlong_as_double((long long)((unsigned long long)__double_as_longlong(pf_g[w][i]) & m));
-    ah += __longlong_as_double((long long)((unsigned long long)__double_as_longlong(pf_h[w][i]) & m));
-    ac += pf_c[w][i] & (int32_t)(uint32_t)m;
+  const int32_t n8 = (cnt + 7) & ~7;
+  for (int32_t i0 = 0; i0 < n8; i0 += 8) {
+    double vg[8], vh[8];
+    int32_t vc[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      vg[u] = pf_g[w][i0 + u];
+      vh[u] = pf_h[w][i0 + u];
+      vc[u] = pf_c[w][i0 + u];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      // lanes before i add +0.0 (all-zero bits): a mask, not a select
+      const unsigned long long m = i0 + u <= lane ? ~0ull : 0ull;
+      ag += __longlong_as_double((long long)((unsigned long long)__double_as_longlong(vg[u]) & m));
+      ah += __longlong_as_double((long long)((unsigned long long)__double_as_longlong(vh[u]) & m));
+      ac += vc[u] & (int32_t)(uint32_t)m;
+    }
   }
   __builtin_amdgcn_wave_barrier();  // the row is rewritten by the next call
   *sg = ag;
@@ -534,17 +548,25 @@ __device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* 
   }
   const int mfb = (int)ft.mfb;
   if (tid < LGBM_WAVE && mfb > 0 && mfb < nb) {
+    // leaf sum minus the other bins in ascending order (the sequential f64 chain),
+    // every lane of wave 0 the same chain over broadcast LDS reads, eight bins per
+    // batch; the skipped bin and bins past num_bin subtract +0.0 (an exact no-op)
     double g = sg, h = sh;
-    for (int c0 = 0; c0 < nb; c0 += LGBM_WAVE) {
-      const int bb = c0 + tid;
-      const double vg = bb < nb ? cs[2 * bb] : 0.0;
-      const double vh = bb < nb ? cs[2 * bb + 1] : 0.0;
-      const int lim = min(LGBM_WAVE, nb - c0);
-      for (int i = 0; i < lim; ++i) {
-        if (c0 + i != mfb) {
-          g -= readlane_f64(vg, i);
-          h -= readlane_f64(vh, i);
-        }
+    const int n8 = (nb + 7) & ~7;
+    for (int i0 = 0; i0 < n8; i0 += 8) {
+      double vg[8], vh[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + u;
+        const bool use = i < nb && i != mfb;
+        const double a = cs[2 * i], b = cs[2 * i + 1];
+        vg[u] = use ? a : 0.0;
+        vh[u] = use ? b : 0.0;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        g -= vg[u];
+        h -= vh[u];
       }
     }
     if (tid == 0) {
