@@ -271,7 +271,8 @@ def main():
     root_bytes = tm["root_rows"] * (F + 2) + tm["hist_launches"] * hist_w
     part_bytes = (tm["partition_rows"] * 9 + tm["hist_child_rows"] * (F + 6)
                   + tm["partition_jobs"] * hist_w)
-    design_bytes = tm["partition_rows"] * 2 * (rec + 2) + tm["partition_jobs"] * hist_w
+    # record_bytes: what a partition pass reads per row (record + separately stored pair)
+    design_bytes = tm["partition_rows"] * 2 * rec + tm["partition_jobs"] * hist_w
     root_gbs = root_bytes / (tm["hist_ms"] * 1e-3) / 1e9 if tm["hist_ms"] > 0 else 0.0
     part_gbs = part_bytes / (tm["partition_ms"] * 1e-3) / 1e9 if tm["partition_ms"] > 0 else 0.0
     design_gbs = design_bytes / (tm["partition_ms"] * 1e-3) / 1e9 if tm["partition_ms"] > 0 else 0.0

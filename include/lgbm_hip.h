@@ -394,7 +394,9 @@ int lgbm_hip_get_timing(lgbm_hip_ctx* ctx, double* ms_out5, double* hist_bytes_o
  * ConstructHistogram rows; [6] root ConstructHistogram launches; [7] rows moved by
  * partition passes (which also build one child's histogram per split); [8]
  * partition kernels launched while timing (rounds after a tree is complete
- * included); [9] bytes per row record; [10] features; [11] histogram
+ * included); [9] bytes a partition pass reads per quantized row: the row record
+ * plus its separately stored quantized pair (none when the record holds it);
+ * [10] features; [11] histogram
  * cells; [12] leaf splits partitioned (including splits made ahead of their turn
  * that the tree never used); [13] partition rounds over all trees; [14] trees;
  * [15] rounds launched after the captured per-tree sequence; [16] ms in the binning

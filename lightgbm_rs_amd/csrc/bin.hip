@@ -59,7 +59,7 @@ __device__ __forceinline__ uint32_t bin_of(const DevBinFeature& f, const double*
 
 template <typename T, bool COL_MAJOR>
 __global__ __launch_bounds__(256) void k_bin_records(const T* __restrict__ x, int64_t n, int32_t F,
-                                                     int32_t W, const DevBinFeature* __restrict__ feats,
+                                                     int32_t fmt, const DevBinFeature* __restrict__ feats,
                                                      const double* __restrict__ ub, int32_t ub_count,
                                                      const int2* __restrict__ cats,
                                                      uint4* __restrict__ rec) {
@@ -73,57 +73,62 @@ __global__ __launch_bounds__(256) void k_bin_records(const T* __restrict__ x, in
   for (int i = threadIdx.x; i < F; i += blockDim.x) s_f[i] = feats[i];
   __syncthreads();
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  // record format (lgbm_device.h): bins per u32 and their width; the legacy format's
+  // last u32 holds the row index, the packed one's stays clear (its quantized pair
+  // is written by the partition)
+  const int U = rec_words(fmt), bpw = rec_bpw(fmt), bb = rec_bits(fmt);
+  const bool packed = rec_packed(fmt);
+  uint2* out = (uint2*)rec;
   for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
-    // one 16-byte record word at a time, its four u32 built in registers (fixed
-    // indices after unrolling); the row index fills the record's last u32
-    for (int w = 0; w < W; ++w) {
-      uint32_t q[4];
+    // two record words at a time, built in registers
+    for (int w2 = 0; w2 < U / 2; ++w2) {
+      uint32_t q[2];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < 2; ++k) {
+        const int wi = 2 * w2 + k;
         uint32_t word = 0u;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int f = 16 * w + 4 * k + j;
+        for (int j = 0; j < bpw; ++j) {
+          const int f = bpw * wi + j;
           if (f < F) {
             const double v = (double)(COL_MAJOR ? x[(int64_t)f * n + r] : x[r * F + f]);
-            word |= bin_of(s_f[f], bounds, cats, v) << (8 * j);
+            word |= bin_of(s_f[f], bounds, cats, v) << (bb * j);
           }
         }
         q[k] = word;
       }
-      if (w == W - 1) q[3] = (uint32_t)r;
-      rec[r * W + w] = make_uint4(q[0], q[1], q[2], q[3]);
+      if (!packed && w2 == U / 2 - 1) q[1] = (uint32_t)r;
+      out[r * (U / 2) + w2] = make_uint2(q[0], q[1]);
     }
   }
 }
 
 template <typename T, bool CM>
-void launch_typed(const void* x, int64_t n, int32_t F, int32_t W, const DevBinFeature* feats,
+void launch_typed(const void* x, int64_t n, int32_t F, int32_t fmt, const DevBinFeature* feats,
                   const double* ub, int32_t ub_count, const int2* cats, uint4* rec, hipStream_t s,
                   const KernelEvents* ev) {
   const int64_t want = (n + 255) / 256;
   const unsigned blocks = (unsigned)std::min<int64_t>(std::max<int64_t>(want, 1), 4096);
   const size_t lds = ub_count <= BIN_LDS_BOUNDS ? (size_t)ub_count * sizeof(double) : 0;
-  KLAUNCH(ev, (k_bin_records<T, CM>), dim3(blocks), dim3(256), lds, s, (const T*)x, n, F, W,
+  KLAUNCH(ev, (k_bin_records<T, CM>), dim3(blocks), dim3(256), lds, s, (const T*)x, n, F, fmt,
           feats, ub, ub_count, cats, rec);
 }
 
 }  // namespace
 
 void launch_bin_records(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
-                        int32_t W, const DevBinFeature* feats, const double* ub, int32_t ub_count,
+                        int32_t fmt, const DevBinFeature* feats, const double* ub, int32_t ub_count,
                         const int2* cats, uint4* rec, hipStream_t s, const KernelEvents* ev) {
   if (n <= 0) return;
   if (f64) {
     if (col_major)
-      launch_typed<double, true>(x, n, F, W, feats, ub, ub_count, cats, rec, s, ev);
+      launch_typed<double, true>(x, n, F, fmt, feats, ub, ub_count, cats, rec, s, ev);
     else
-      launch_typed<double, false>(x, n, F, W, feats, ub, ub_count, cats, rec, s, ev);
+      launch_typed<double, false>(x, n, F, fmt, feats, ub, ub_count, cats, rec, s, ev);
   } else {
     if (col_major)
-      launch_typed<float, true>(x, n, F, W, feats, ub, ub_count, cats, rec, s, ev);
+      launch_typed<float, true>(x, n, F, fmt, feats, ub, ub_count, cats, rec, s, ev);
     else
-      launch_typed<float, false>(x, n, F, W, feats, ub, ub_count, cats, rec, s, ev);
+      launch_typed<float, false>(x, n, F, fmt, feats, ub, ub_count, cats, rec, s, ev);
   }
 }
 

@@ -93,7 +93,8 @@ struct lgbm_hip_ctx {
   unsigned char* noalloc = nullptr;  // this device's `scratch` (hipGetSymbolAddress)
   // shape
   int64_t N = 0;
-  int32_t F = 0, W = 0, total_cells = 0;
+  int32_t F = 0, fmt = 1, total_cells = 0;  // fmt: row record format (lgbm_device.h)
+  bool legacy_records = false;              // LGBM_HIP_RECORDS=legacy: 8-bit records only
   uint64_t slot_len = 0;
   std::vector<DevFeature> feats;
   std::vector<double> ub_host;  // per-bin values (numerical: upper bounds, categorical: categories)
@@ -281,7 +282,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.feats = c->d_feats;
   L.ub = c->d_ub;
   L.F = c->F;
-  L.W = c->W;
+  L.fmt = c->fmt;
   L.total_cells = c->total_cells;
   L.N = c->N;
   L.slot_len = c->slot_len;
@@ -328,10 +329,15 @@ int ctl_read(lgbm_hip_ctx* c, size_t off, T* v) {
 }
 #define CTL_OFF(field) offsetof(Ctl, field)
 
+// Records of n rows in a given format, in 16-byte units.
+size_t rec_units(int fmt, int64_t n) {
+  return ((size_t)std::max<int64_t>(n, 1) * (size_t)rec_bytes(fmt) + 15) / 16;
+}
+
 int ensure_scratch_rows(lgbm_hip_ctx* c, int64_t n) {
   for (int b : {BUF_S0, BUF_S1}) {
     if (c->buf_rows[b] >= n && c->rec[b]) continue;
-    int rc = dalloc(c, &c->rec[b], (size_t)std::max<int64_t>(n, 1) * std::max(c->W, 1));
+    int rc = dalloc(c, &c->rec[b], rec_units(c->fmt, n));
     if (rc) return rc;
     rc = dalloc(c, &c->gh[b], (size_t)std::max<int64_t>(n, 1));
     if (rc) return rc;
@@ -533,7 +539,7 @@ void enqueue_rounds(lgbm_hip_ctx* c, int32_t rounds, int32_t fp) {
   if (c->timing) c->part_launches += rounds;
   for (int32_t r = 0; r < rounds; ++r) {
     launch_plan(L, SLOT_CAP(c->lcap), c->stream, ev_kernel(c, FAM_SCAN, &ke));
-    launch_partition(L, c->W, fp, c->part_blocks, c->stream, ev_kernel(c, FAM_PART, &ke));
+    launch_partition(L, fp, c->part_blocks, c->stream, ev_kernel(c, FAM_PART, &ke));
     if (fp) launch_hist_f32(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
     launch_pair_scan(L, c->spec_max, c->part_blocks, c->stream, ev_kernel(c, FAM_SCAN, &ke));
   }
@@ -824,7 +830,16 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
                    "rows per histogram block exceed the packed LDS cell fields");
   c->F = F;
   c->N = num_data;
-  c->W = (F + 4 + 15) / 16;
+  // record format: 6-bit bins with the quantized pair inside when every feature has at
+  // most 64 bins and fits (F <= 39), else 8-bit bins and the row index
+  uint32_t max_nb = 0;
+  for (int f = 0; f < F; ++f) max_nb = std::max(max_nb, meta[f].num_bin);
+  c->fmt = (F + 4 + 15) / 16;
+  if (!c->legacy_records && max_nb <= 64 && F <= 39) {
+    int U = (F + 5) / 5;
+    U = std::max(U + (U & 1), 2);
+    c->fmt = REC_FMT_PACKED + U;
+  }
   c->total_cells = (int32_t)acc;
   c->slot_len = 2ull * acc;
   c->feats = feats;
@@ -840,7 +855,7 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
     (void)hipFree(c->d_ub);
     c->d_ub = nullptr;
   }
-  const size_t words = (size_t)num_data * c->W;
+  const size_t words = rec_units(c->fmt, num_data);
   for (int b : {BUF_ORIG, BUF_A, BUF_B}) {
     if ((rc = dalloc(c, &c->rec[b], words))) return rc;
     if ((rc = dalloc(c, &c->gh[b], (size_t)num_data))) return rc;
@@ -963,6 +978,7 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   if (const char* e = std::getenv("LGBM_HIP_PART_BLOCKS"))
     c->part_blocks = std::max(1, std::min(65535, std::atoi(e)));
   if (const char* e = std::getenv("LGBM_HIP_GRAPHS")) c->use_graphs = std::strcmp(e, "0") != 0;
+  if (const char* e = std::getenv("LGBM_HIP_RECORDS")) c->legacy_records = std::strcmp(e, "legacy") == 0;
   if (const char* e = std::getenv("LGBM_HIP_ROUNDS")) c->round_cap = std::max(1, std::atoi(e));
   if (const char* e = std::getenv("LGBM_HIP_SPEC"))
     c->spec_max = std::max(1, std::min(SPEC_MAX, std::atoi(e)));
@@ -1096,7 +1112,7 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   HIPCHK(c, hipMalloc((void**)&tmp, (size_t)F * num_data));
   hipError_t e = hipMemcpy(tmp, bins, (size_t)F * num_data, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
-    launch_pack_records(tmp, num_data, F, c->W, c->rec[BUF_ORIG], c->stream);
+    launch_pack_records(tmp, num_data, F, c->fmt, c->rec[BUF_ORIG], c->stream);
     e = hipStreamSynchronize(c->stream);
   }
   (void)hipFree(tmp);
@@ -1279,7 +1295,7 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
   if (e == hipSuccess) {
     // c->d_ub holds the same bounds, concatenated in feature order
     KernelEvents ke;
-    launch_bin_records(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->W, d_bf,
+    launch_bin_records(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->fmt, d_bf,
                        c->d_ub, (int32_t)ub.size(), d_cats, c->rec[BUF_ORIG], c->stream,
                        ev_kernel(c, FAM_BIN, &ke));
     if (c->timing) {
@@ -1321,12 +1337,16 @@ int lgbm_hip_get_bins(lgbm_hip_ctx* c, uint8_t* out, int64_t n) {
   if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "no resident bins");
   if (!out || n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_data");
   // the original (unpartitioned) records, feature-major
-  std::vector<uint32_t> rec((size_t)c->N * 4 * c->W);
+  const int U = rec_words(c->fmt);
+  const uint32_t mask = (1u << rec_bits(c->fmt)) - 1u;
+  std::vector<uint32_t> rec((size_t)c->N * U);
   HIPCHK(c, hipMemcpy(rec.data(), c->rec[BUF_ORIG], rec.size() * 4, hipMemcpyDeviceToHost));
-  for (int64_t r = 0; r < c->N; ++r)
-    for (int32_t f = 0; f < c->F; ++f)
-      out[(size_t)f * c->N + r] =
-          (uint8_t)(rec[(size_t)r * 4 * c->W + (f >> 2)] >> (8 * (f & 3)));
+  for (int32_t f = 0; f < c->F; ++f) {
+    int wi, sh;
+    rec_field_pos(c->fmt, f, &wi, &sh);
+    for (int64_t r = 0; r < c->N; ++r)
+      out[(size_t)f * c->N + r] = (uint8_t)((rec[(size_t)r * U + wi] >> sh) & mask);
+  }
   return LGBM_HIP_OK;
 }
 
@@ -1465,7 +1485,7 @@ static int set_hist_job(lgbm_hip_ctx* c, const uint32_t* rows, int64_t n_rows) {
     if ((rc = ensure_scratch_rows(c, n_rows))) return rc;
     if ((rc = ensure_scratch_bytes(c, (size_t)std::max<int64_t>(n_rows, 1) * 4))) return rc;
     HIPCHK(c, hipMemcpy(c->scratch, rows, (size_t)n_rows * 4, hipMemcpyHostToDevice));
-    launch_gather_rows(c->W, (const uint32_t*)c->scratch, n_rows, c->rec[BUF_ORIG],
+    launch_gather_rows(c->fmt, (const uint32_t*)c->scratch, n_rows, c->rec[BUF_ORIG],
                        c->gh[BUF_ORIG], c->g32[BUF_ORIG], c->rec[BUF_S0], c->gh[BUF_S0],
                        c->g32[BUF_S0], c->stream);
     buf = BUF_S0;
@@ -1705,10 +1725,10 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
     *left_count_out = 0;
     return LGBM_HIP_OK;
   }
-  const int savedW = c->W;
-  c->W = 1;
+  const int saved_fmt = c->fmt;
+  c->fmt = 1;  // the per-op partition's own one-word records (k_pack_partition)
   rc = ensure_scratch_rows(c, n);
-  c->W = savedW;
+  c->fmt = saved_fmt;
   if (rc) return rc;
   if ((rc = ensure_tile_state(c, n))) return rc;
   if ((rc = ensure_scratch_bytes(c, (size_t)n * 4))) return rc;
@@ -1740,7 +1760,7 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   const int64_t tiles = J.ntiles;
   if ((rc = ctl_write(c, CTL_OFF(tile_total), tiles))) return rc;
   DevLearner L = make_learner(c);
-  L.W = 1;
+  L.fmt = 1;
   launch_partition_stable(L, tiles, std::min<int64_t>(c->part_blocks, tiles), c->stream);
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -2064,7 +2084,7 @@ int lgbm_hip_get_stats(lgbm_hip_ctx* c, double* out) {
   out[6] = st[3];
   out[7] = st[0];
   out[8] = c->part_launches;
-  out[9] = 16.0 * c->W;
+  out[9] = (double)(rec_bytes(c->fmt) + (rec_packed(c->fmt) ? 0 : 2));
   out[10] = c->F;
   out[11] = c->total_cells;
   out[12] = st[4];

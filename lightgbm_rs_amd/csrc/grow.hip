@@ -499,7 +499,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     // quantized gradients: build the histogram of the side the scan expects to be
     // smaller inside the partition pass (f32: k_hist_f32 builds the smaller child)
     J.acc_right = fp ? -1 : (b.right_count < b.left_count ? 1 : 0);
-    J.ntiles = (int32_t)((J.count + part_tile(L.W) - 1) / part_tile(L.W));
+    J.ntiles = (int32_t)((J.count + part_tile(L.fmt) - 1) / part_tile(L.fmt));
     J.tile0 = 0;
     ctl->jobs[j] = J;
     ctl->part_cur[j] = 0ull;
@@ -547,7 +547,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
 
 // ===========================================================================
 // k_partition: DataPartition::split of every job of the round in one pass.  The
-// tiles of all jobs (job j owns tiles [tile0, tile0 + ntiles), part_tile(W) rows each,
+// tiles of all jobs (job j owns tiles [tile0, tile0 + ntiles), part_tile(fmt) rows each,
 // in the parent's logical row order) are dealt to the blocks in contiguous runs, so a
 // block meets few job boundaries.  A tile ranks its rows with wave ballots, then
 // takes its output ranges:
@@ -569,9 +569,13 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
 // (FP = 1) move as (g, h) pairs; the smaller child's histogram is built afterwards by
 // k_hist_f32.
 // ===========================================================================
-template <int W, int FP, bool STABLE>
+template <int FMT, int FP, bool STABLE>
 __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
-  constexpr int PT = PART_THREADS, PR = part_rows(W);
+  constexpr int PT = PART_THREADS, PR = part_rows(FMT);
+  constexpr int U = rec_words(FMT), NS = rec_slots(FMT), BPW = rec_bpw(FMT);
+  // packed records carry the quantized pair in their last word (the original order's
+  // pairs come from the quantizer's array)
+  constexpr bool EMBED = rec_packed(FMT) && FP == 0;
   constexpr int kWaves = PT / LGBM_WAVE;
   constexpr int kTile = PT * PR;
   constexpr int kSlots = PR * kWaves;  // (row k, wave) left counts, k-major = row order
@@ -582,7 +586,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   static_assert(kFlushTiles >= 1, "tile larger than an LDS cell's row capacity");
   using GhT = typename std::conditional<FP != 0, float2, uint16_t>::type;
   extern __shared__ unsigned long long lds_hist[];
-  __shared__ int32_t cb[16 * LGBM_MAX_W];
+  __shared__ int32_t cb[NS];
   __shared__ PartJob s_jobs[SPEC_MAX];
   __shared__ int32_t s_cnt[kSlots];
   __shared__ int32_t s_pref[kSlots];
@@ -596,15 +600,15 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   const int64_t t_hi = ((int64_t)blockIdx.x + 1) * total / G;
   if (tid < SPEC_MAX) s_jobs[tid] = ctl->jobs[tid];
   if (nj <= 0 || t_lo >= t_hi) return;
-  const int F = L.F, cells = L.total_cells, nw = (F + 3) / 4;
+  const int F = L.F, cells = L.total_cells, nw = (F + BPW - 1) / BPW;
   if constexpr (FP == 0)
-    for (int c = tid; c < cells + 4; c += PT) lds_hist[c] = 0ull;
-  for (int f = tid; f < 16 * W; f += PT) cb[f] = f < F ? (int32_t)L.feats[f].cell_base : cells;
+    for (int c = tid; c < cells + LDS_TRASH_CELLS; c += PT) lds_hist[c] = 0ull;
+  for (int f = tid; f < NS; f += PT) cb[f] = f < F ? (int32_t)L.feats[f].cell_base : cells;
   __syncthreads();
-  // feature cell bases in scalar registers (bytes beyond F map to the trash cell)
-  int32_t cbr[16 * W];
+  // bin-slot cell bases in scalar registers (slots beyond F map to the trash cell)
+  int32_t cbr[NS];
 #pragma unroll
-  for (int f = 0; f < 16 * W; ++f) cbr[f] = __builtin_amdgcn_readfirstlane(cb[f]);
+  for (int f = 0; f < NS; ++f) cbr[f] = __builtin_amdgcn_readfirstlane(cb[f]);
   int32_t jl = 0;         // job of the last tile loaded
   int32_t cur = -1;       // job whose rows the LDS histogram holds
   int32_t held = 0;       // tiles of that job in the LDS histogram
@@ -625,7 +629,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     }
   };
   struct TileBuf {
-    uint4 w[PR][W];
+    uint32_t w[PR][U];
     GhT q[PR];
     bool valid[PR];
   };
@@ -638,15 +642,25 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     const int64_t base = (t - J.tile0) * kTile;
     const uint4* __restrict__ src = rec_buf(L.bufs, J.src_buf);
     const GhT* __restrict__ sgh = gh_buf<GhT>(L.bufs, J.src_buf);
+    const bool from_rec = EMBED && J.src_buf != BUF_ORIG;
 #pragma unroll
     for (int k = 0; k < PR; ++k) {
       const int64_t p = base + (int64_t)k * PT + tid;
       B.valid[k] = p < count;
       const int64_t pc = B.valid[k] ? p : count - 1;
       const int64_t phys = J.rev ? begin + count - 1 - pc : begin + pc;
+      rec_load<FMT>(src, phys, B.w[k]);
+      if constexpr (EMBED) {
+        if (!from_rec) B.q[k] = sgh[phys];
+      } else {
+        B.q[k] = sgh[phys];
+      }
+    }
+    if constexpr (EMBED) {
+      if (from_rec) {
 #pragma unroll
-      for (int i = 0; i < W; ++i) B.w[k][i] = src[phys * W + i];
-      B.q[k] = sgh[phys];
+        for (int k = 0; k < PR; ++k) B.q[k] = (GhT)rec_gh<FMT>(B.w[k]);
+      }
     }
     return jl;
   };
@@ -678,9 +692,11 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     auto& valid = B.valid;
     bool isleft[PR];
     int32_t rank[PR];
+    int fwi, fsh;
+    rec_field_pos(FMT, J.fbyte, &fwi, &fsh);
 #pragma unroll
     for (int k = 0; k < PR; ++k) {
-      const int32_t bin = (int32_t)rec_byte(w[k], J.fbyte);
+      const int32_t bin = (int32_t)rec_field<FMT>(w[k], fwi, fsh);
       const bool left = (J.flags & ROUTE_CAT)
                             ? ((J.cat[bin >> 5] >> (bin & 31)) & 1u) != 0u
                             : !route_right(bin, J.pmin, J.max_bin, J.th, J.na_bin, J.flags);
@@ -717,7 +733,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
 #pragma unroll
       for (int k = 0; k < PR; ++k)
         if (valid[k] && isleft[k] == want_left && gh_bits(q[k]) != 0u)
-          lds_hist_add<W>(lds_hist, cbr, nw, w[k], gh_bits(q[k]));
+          lds_hist_add<FMT>(lds_hist, cbr, nw, F, cells + 4 + lane, w[k], gh_bits(q[k]));
       ++held;
     }
     if (wave == 0 && lane == 0) {
@@ -751,9 +767,13 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
         const int64_t r = rbase + (pos - lrank);  // right rows before this one
         d = begin + count - 1 - r;
       }
-#pragma unroll
-      for (int i = 0; i < W; ++i) dst[d * W + i] = w[k][i];
-      dgh[d] = q[k];
+      if constexpr (EMBED) {
+        rec_set_gh<FMT>(w[k], gh_bits(q[k]));
+        rec_store<FMT>(dst, d, w[k]);
+      } else {
+        rec_store<FMT>(dst, d, w[k]);
+        dgh[d] = q[k];
+      }
     }
     if (tid == 0 && s_last) {
       const int32_t lc = (int32_t)(lbase + s_total);
@@ -819,9 +839,10 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
 }
 
 // Stable per-op partition, step 1: the left-row count of every tile of job 0.
-template <int W>
+template <int FMT>
 __global__ __launch_bounds__(PART_THREADS) void k_tile_count(DevLearner L) {
-  constexpr int PT = PART_THREADS, PR = part_rows(W), kTile = PT * PR;
+  constexpr int PT = PART_THREADS, PR = part_rows(FMT), kTile = PT * PR;
+  constexpr int U = rec_words(FMT);
   __shared__ int32_t s_w[PT / LGBM_WAVE];
   const PartJob J = L.ctl->jobs[0];
   const int64_t t = blockIdx.x;
@@ -832,10 +853,11 @@ __global__ __launch_bounds__(PART_THREADS) void k_tile_count(DevLearner L) {
     const int64_t p = t * kTile + (int64_t)k * PT + threadIdx.x;
     if (p >= J.count) continue;
     const int64_t phys = J.rev ? J.begin + J.count - 1 - p : J.begin + p;
-    uint4 w[W];
-#pragma unroll
-    for (int i = 0; i < W; ++i) w[i] = src[phys * W + i];
-    const int32_t bin = (int32_t)rec_byte(w, J.fbyte);
+    uint32_t w[U];
+    rec_load<FMT>(src, phys, w);
+    int fwi, fsh;
+    rec_field_pos(FMT, J.fbyte, &fwi, &fsh);
+    const int32_t bin = (int32_t)rec_field<FMT>(w, fwi, fsh);
     n += route_right(bin, J.pmin, J.max_bin, J.th, J.na_bin, J.flags) ? 0 : 1;
   }
   for (int off = 32; off >= 1; off >>= 1) n += __shfl_xor(n, off);
@@ -1123,18 +1145,9 @@ __global__ void k_tree_finalize(DevLearner L) {
 }
 
 // Exports the partition layout the way DataPartition::split leaves it: each leaf's
-// rows in ascending row order at the leaf's begin offset (leaf_of, then a stable rank
-// of every row within its leaf), whatever the storage order inside the leaf.
-template <int W>
-__global__ void k_leaf_of(DevLearner L, uint8_t* __restrict__ leaf_of) {
-  const int32_t l = blockIdx.y;
-  if (l >= L.ctl->num_leaves) return;
-  const int64_t b = L.leaves.begin[l], c = L.leaves.count[l];
-  const uint4* __restrict__ rec = rec_buf(L.bufs, L.leaves.buf[l]);
-  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < c;
-       p += (int64_t)gridDim.x * blockDim.x)
-    leaf_of[rec[(b + p) * W + (W - 1)].w] = (uint8_t)l;
-}
+// rows in ascending row order at the leaf's begin offset (the leaf of every row by a
+// walk of the tree over its original record, k_walk; then a stable rank of every row
+// within its leaf), whatever the storage order inside the leaf.
 
 // Stable rank of every row among the rows of its leaf, RANK_ROWS rows per block in
 // row order: wave peers by eight key-bit ballots, waves in order through LDS, and a
@@ -1232,22 +1245,22 @@ void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth
 void launch_plan(const DevLearner& L, int32_t slot_cap, hipStream_t s, const KernelEvents* ev) {
   KLAUNCH(ev, k_plan, dim3(1), dim3(PLAN_THREADS), 0, s, L, slot_cap);
 }
-void launch_partition(const DevLearner& L, int W, int fp, int64_t blocks, hipStream_t s,
+void launch_partition(const DevLearner& L, int fp, int64_t blocks, hipStream_t s,
                       const KernelEvents* ev) {
   if (blocks < 1) blocks = 1;
   const dim3 g((unsigned)blocks), b(PART_THREADS);
   if (fp) {
-    DISPATCH_W(W, KLAUNCH(ev, (k_partition<kW, 1, false>), g, b, 0, s, L));
+    DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_partition<kF, 1, false>), g, b, 0, s, L));
   } else {
-    const size_t lds = (size_t)(std::max(L.total_cells, 1) + 4) * sizeof(unsigned long long);
-    DISPATCH_W(W, KLAUNCH(ev, (k_partition<kW, 0, false>), g, b, lds, s, L));
+    const size_t lds = (size_t)(std::max(L.total_cells, 1) + LDS_TRASH_CELLS) * sizeof(unsigned long long);
+    DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_partition<kF, 0, false>), g, b, lds, s, L));
   }
 }
 void launch_partition_stable(const DevLearner& L, int64_t ntiles, int64_t blocks, hipStream_t s) {
   if (blocks < 1) blocks = 1;
   k_tile_count<1><<<dim3((unsigned)ntiles), dim3(PART_THREADS), 0, s>>>(L);
   k_tile_scan<<<dim3(1), dim3(1024), 0, s>>>(L);
-  const size_t lds = (size_t)(std::max(L.total_cells, 1) + 4) * sizeof(unsigned long long);
+  const size_t lds = (size_t)(std::max(L.total_cells, 1) + LDS_TRASH_CELLS) * sizeof(unsigned long long);
   k_partition<1, 0, true><<<dim3((unsigned)blocks), dim3(PART_THREADS), lds, s>>>(L);
 }
 void launch_pair_scan(const DevLearner& L, int32_t spec_max, int32_t part_grid, hipStream_t s,
@@ -1267,7 +1280,7 @@ void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* ind
   const int64_t n = L.N, nblk = (n + RANK_ROWS - 1) / RANK_ROWS;
   uint8_t* leaf_of = (uint8_t*)scratch;
   uint32_t* tab = (uint32_t*)((char*)scratch + (((size_t)n + 255) & ~(size_t)255));
-  DISPATCH_W(L.W, (k_leaf_of<kW><<<dim3(64, (unsigned)num_leaves), dim3(256), 0, s>>>(L, leaf_of)));
+  launch_leaf_of(L, leaf_of, s);
   k_leaf_rank<false><<<dim3((unsigned)nblk), dim3(RANK_THREADS), 0, s>>>(leaf_of, n, num_leaves,
                                                                         nblk, tab, nullptr);
   k_leaf_rank_offsets<<<dim3((unsigned)num_leaves), dim3(1024), 0, s>>>(L, nblk, tab);

@@ -1,15 +1,15 @@
 // lgbm_kernels.h — gfx950 kernels of the tree-learner hot path.
 //
-// Row store.  Every row is one record of W x 16 bytes: bytes [0, F) hold the
-// row's u8 bins (feature-major upload transposed once, lib.rs:4368-4433 is the
-// reference's upload), bytes [16W-4, 16W) the original row index.  A second
-// array holds the row's packed quantized (grad, hess) int8 pair.  Records are
-// *physically* repartitioned at every split into ping-pong buffers, so a leaf's
-// rows are always one contiguous range: ConstructHistogram streams them, and
-// the partition is a single pass.  The right child of a split is stored in
+// Row store.  Every row is one record (formats in lgbm_device.h): its bins, and either
+// the original row index (8-bit bins, W x 16 bytes) or, with every num_bin <= 64, 6-bit
+// bins and the row's quantized pair (4U bytes: 24 at 28 features).  A separate array
+// holds the packed quantized (grad, hess) pairs in the original order (the quantizer's
+// output).  Records are *physically* repartitioned at every split into ping-pong
+// buffers, so a leaf's rows are always one contiguous range: ConstructHistogram streams
+// them, and the partition is a single pass.  The right child of a split is stored in
 // reverse order (its logical order is the reference's ascending order; see
-// k_partition), which lets the partition place both children without knowing
-// the left count in advance.
+// k_partition), which lets the partition place both children without knowing the left
+// count in advance.
 //
 // Histograms are exact integers: per (feature, bin) cell the kernel counts
 // sum(q_g), sum(q_h) and #(q_h == 3).  With num_grad_quant_bins = 4 every
@@ -107,9 +107,8 @@ struct DevLearner {
   const DevFeature* feats;
   const double* ub;
   int32_t F;
-  int32_t W;
   int32_t total_cells;
-  int32_t _pad;
+  int32_t fmt;                // row record format (rec_words / rec_packed)
   int64_t N;
   uint64_t slot_len;
   int32_t* hist_part;         // [HIST_SLOTS][total_cells][3] root / per-op partials
@@ -157,7 +156,7 @@ struct KernelEvents {
       kern<<<grid, block, lds, s>>>(__VA_ARGS__);                                        \
   } while (0)
 
-void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t W, uint4* rec,
+void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t fmt, uint4* rec,
                          hipStream_t s);
 
 // One feature's mapper as the binning kernel reads it (ValueToBin,
@@ -173,7 +172,7 @@ struct DevBinFeature {
 // Bins a dense raw matrix (f32 or f64; row-major [n][F] or column-major [F][n]) into
 // the resident records; `ub_count` upper bounds are staged in LDS.
 void launch_bin_records(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
-                        int32_t W, const DevBinFeature* feats, const double* ub, int32_t ub_count,
+                        int32_t fmt, const DevBinFeature* feats, const double* ub, int32_t ub_count,
                         const int2* cats, uint4* rec, hipStream_t s, const KernelEvents* ev);
 void launch_absmax(const float* g, const float* h, int64_t n, uint4* partials, hipStream_t s);
 void launch_grad_binary(const double* score, const float* label, float* g, float* h, int64_t n,
@@ -197,7 +196,7 @@ void launch_pair_scan(const DevLearner& L, int32_t spec_max, int32_t part_grid, 
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,
                           lgbm_split_info* out, hipStream_t s);
-void launch_partition(const DevLearner& L, int W, int fp, int64_t blocks, hipStream_t s,
+void launch_partition(const DevLearner& L, int fp, int64_t blocks, hipStream_t s,
                       const KernelEvents* ev = nullptr);
 // Stable variant for the per-op entry point (job 0, W = 1): tile counts, their
 // prefix, then the partition in DataPartition::split order.
@@ -210,11 +209,13 @@ void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth
                       const KernelEvents* ev = nullptr);
 void launch_score_update(const DevLearner& L, double lr, double* score, hipStream_t s,
                          const KernelEvents* ev = nullptr);
+// leaf id (num_leaves <= 256) of every row by walking the tree from its original record
+void launch_leaf_of(const DevLearner& L, uint8_t* leaf_of, hipStream_t s);
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
 size_t export_layout_scratch_bytes(int64_t n, int32_t num_leaves);
 void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
                           void* scratch, hipStream_t s);
-void launch_gather_rows(int W, const uint32_t* rows, int64_t n, const uint4* rec,
+void launch_gather_rows(int fmt, const uint32_t* rows, int64_t n, const uint4* rec,
                         const uint16_t* gh, const float2* g32, uint4* rec_out, uint16_t* gh_out,
                         float2* g32_out, hipStream_t s);
 void launch_subtract(const double* a, const double* b, int64_t n, double* out, hipStream_t s);

@@ -13,7 +13,7 @@
 //   split_step       (last block of k_fixscan) per-leaf argmax (learner.rs:3290-3330),
 //                    cross-leaf ArgMax (learner.rs:4537), Tree::split (tree.rs:614-700)
 //   k_partition      DataPartition::split (data_partition.rs:192-288,360-463)
-//   k_score_update   score update through the grown tree (score_updater.rs:133;
+//   k_walk           score update through the grown tree (and the layout's leaf ids) (score_updater.rs:133;
 //                    learner.rs:4380-4395)
 #include "scan.h"
 
@@ -26,16 +26,21 @@ namespace lgbm {
 // ===========================================================================
 // upload: feature-major u8 -> records
 // ===========================================================================
-__global__ void k_pack_records(const uint8_t* __restrict__ bins, int64_t n, int32_t F, int32_t W,
+__global__ void k_pack_records(const uint8_t* __restrict__ bins, int64_t n, int32_t F, int32_t fmt,
                                uint4* __restrict__ rec) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= n) return;
+  const int U = rec_words(fmt);
   uint32_t words[4 * LGBM_MAX_W];
-  for (int i = 0; i < 4 * W; ++i) words[i] = 0u;
-  for (int f = 0; f < F; ++f) words[f >> 2] |= (uint32_t)bins[(size_t)f * n + r] << (8 * (f & 3));
-  words[4 * W - 1] = (uint32_t)r;
-  for (int w = 0; w < W; ++w)
-    rec[r * W + w] = make_uint4(words[4 * w], words[4 * w + 1], words[4 * w + 2], words[4 * w + 3]);
+  for (int i = 0; i < U; ++i) words[i] = 0u;
+  for (int f = 0; f < F; ++f) {
+    int wi, sh;
+    rec_field_pos(fmt, f, &wi, &sh);
+    words[wi] |= (uint32_t)bins[(size_t)f * n + r] << sh;
+  }
+  if (!rec_packed(fmt)) words[U - 1] = (uint32_t)r;
+  uint2* out = (uint2*)rec;
+  for (int i = 0; i < U / 2; ++i) out[r * (U / 2) + i] = make_uint2(words[2 * i], words[2 * i + 1]);
 }
 
 // ===========================================================================
@@ -439,10 +444,12 @@ __device__ __forceinline__ void hist_assign(const Ctl* ctl, int32_t nj, int32_t*
   *s_R = R;
 }
 
-template <int W, bool WAVE_PRIVATE>
+template <int FMT, bool WAVE_PRIVATE>
 __global__ __launch_bounds__(HIST_THREADS, 2) void k_hist_jobs(DevLearner L) {
+  constexpr int U = rec_words(FMT), BPW = rec_bpw(FMT), BB = rec_bits(FMT), NS = rec_slots(FMT);
+  constexpr uint32_t BM = (1u << BB) - 1u;
   extern __shared__ uint32_t lds_u32[];
-  __shared__ int32_t cb[16 * LGBM_MAX_W];
+  __shared__ int32_t cb[NS];
   __shared__ int32_t s_a0[SPEC_MAX], s_nb[SPEC_MAX];
   __shared__ int64_t s_R;
   Ctl* ctl = L.ctl;
@@ -450,9 +457,9 @@ __global__ __launch_bounds__(HIST_THREADS, 2) void k_hist_jobs(DevLearner L) {
   if (nj <= 0) return;
   const int tid = threadIdx.x, lane = (int)lane_id(), wave = tid >> 6;
   const int F = L.F, cells = L.total_cells;
-  // Record words 0 .. nw-1 hold the bins (four features each); bytes of the last word
-  // beyond F are zero and land in a trash cell at index `cells`.
-  const int nw = (F + 3) / 4;
+  // Record words 0 .. nw-1 hold the bins; slots of the last word beyond F are zero
+  // and land in a trash cell at index `cells`.
+  const int nw = (F + BPW - 1) / BPW;
   if (tid == 0) {
     hist_assign(ctl, nj, s_a0, s_nb, &s_R, HIST_GRID_Q);
     if (blockIdx.x == 0)
@@ -461,7 +468,7 @@ __global__ __launch_bounds__(HIST_THREADS, 2) void k_hist_jobs(DevLearner L) {
         ctl->hjobs[j].nblk = s_nb[j];
       }
   }
-  for (int f = tid; f < 16 * W; f += HIST_THREADS)
+  for (int f = tid; f < NS; f += HIST_THREADS)
     cb[f] = f < F ? (int32_t)L.feats[f].cell_base : cells;
   __syncthreads();
   const int32_t a = (int32_t)blockIdx.x;
@@ -473,17 +480,20 @@ __global__ __launch_bounds__(HIST_THREADS, 2) void k_hist_jobs(DevLearner L) {
   const int64_t R = s_R;
   const int64_t lo = (int64_t)(a - s_a0[j]) * R;
   const int64_t hi = min(J.count, lo + R);
-  const uint4* __restrict__ rec = rec_buf(L.bufs, J.buf) + J.begin * W;
+  // the jobs read the original order (root) or a gathered scratch buffer: pairs from
+  // the gh array
+  const uint4* __restrict__ rec = rec_buf(L.bufs, J.buf);  // rows J.begin + r
   const uint16_t* __restrict__ gh = L.bufs.gh[J.buf] + J.begin;
+  const int64_t rb = J.begin;
   int32_t* __restrict__ out = L.hist_part + (size_t)a * cells * 3;
-  // feature cell bases in scalar registers (wave-uniform)
-  int32_t cbr[16 * W];
+  // bin-slot cell bases in scalar registers (wave-uniform)
+  int32_t cbr[NS];
 #pragma unroll
-  for (int f = 0; f < 16 * W; ++f) cbr[f] = __builtin_amdgcn_readfirstlane(cb[f]);
+  for (int f = 0; f < NS; ++f) cbr[f] = __builtin_amdgcn_readfirstlane(cb[f]);
 
   if constexpr (WAVE_PRIVATE) {
     constexpr int NPL = HIST_WAVE_CELLS / LGBM_WAVE;  // cells per lane
-    const int stride = cells + 4;                     // + trash cell
+    const int stride = cells + LDS_TRASH_CELLS;       // + trash cells
     uint32_t* my = lds_u32 + (size_t)wave * stride;
     for (int c = lane; c < stride; c += LGBM_WAVE) my[c] = 0u;
     unsigned long long acc64[NPL];
@@ -511,40 +521,42 @@ __global__ __launch_bounds__(HIST_THREADS, 2) void k_hist_jobs(DevLearner L) {
         }
       }
     };
-    constexpr int U = HIST_ROWS_PER_LANE;
-    for (int64_t r0 = wlo; r0 < whi; r0 += LGBM_WAVE * U) {
-      uint4 w[U][W];
-      uint32_t q[U];
+    constexpr int RU = HIST_ROWS_PER_LANE;
+    for (int64_t r0 = wlo; r0 < whi; r0 += LGBM_WAVE * RU) {
+      uint32_t w[RU][U];
+      uint32_t q[RU];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
+      for (int u = 0; u < RU; ++u) {
         const int64_t r = r0 + u * LGBM_WAVE + lane;
         q[u] = 0u;
         if (r < whi) {
-#pragma unroll
-          for (int i = 0; i < W; ++i) w[u][i] = rec[r * W + i];
+          rec_load<FMT>(rec, rb + r, w[u]);
           q[u] = (uint32_t)gh[r];  // 0: no row, or a (0, 0) pair
         }
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
+      for (int u = 0; u < RU; ++u) {
         if (q[u] == 0u) continue;
         const int32_t qg = (int32_t)(int8_t)(q[u] & 0xffu);
         const int32_t qh = (int32_t)(int8_t)((q[u] >> 8) & 0xffu);
         const uint32_t v = (uint32_t)qg + ((uint32_t)qh << 11) + ((qh == 3 ? 1u : 0u) << 22);
+        // slots past F go to the lane's own trash cell (no conflicts, no branch)
 #pragma unroll
-        for (int k = 0; k < 4 * W - 1; ++k) {
+        for (int k = 0; k < (NS + BPW - 1) / BPW; ++k) {
           if (k < nw) {
-            const uint4 wd = w[u][k >> 2];
-            const uint32_t word = (k & 3) == 0 ? wd.x : ((k & 3) == 1 ? wd.y : ((k & 3) == 2 ? wd.z : wd.w));
+            const uint32_t word = w[u][k];
 #pragma unroll
-            for (int bb = 0; bb < 4; ++bb)
-              __hip_atomic_fetch_add(&my[cbr[4 * k + bb] + ((word >> (8 * bb)) & 0xffu)], v,
-                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+            for (int bb = 0; bb < BPW; ++bb)
+              if (BPW * k + bb < NS) {
+                const int ad = BPW * k + bb < F ? cbr[BPW * k + bb] + (int)((word >> (BB * bb)) & BM)
+                                                : cells + 4 + lane;
+                __hip_atomic_fetch_add(&my[ad], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+              }
           }
         }
       }
-      step += U;
-      if (step + U > HIST_FOLD_STEPS) {
+      step += RU;
+      if (step + RU > HIST_FOLD_STEPS) {
         step = 0;
         fold();
       }
@@ -573,14 +585,13 @@ __global__ __launch_bounds__(HIST_THREADS, 2) void k_hist_jobs(DevLearner L) {
     for (int c = tid; c < cells * 3; c += HIST_THREADS) out[c] = acc[c];
   } else {
     unsigned long long* h64 = (unsigned long long*)lds_u32;
-    for (int c = tid; c < cells + 4; c += HIST_THREADS) h64[c] = 0ull;
+    for (int c = tid; c < cells + LDS_TRASH_CELLS; c += HIST_THREADS) h64[c] = 0ull;
     __syncthreads();
     for (int64_t r = lo + tid; r < hi; r += HIST_THREADS) {
-      uint4 w[W];
-#pragma unroll
-      for (int i = 0; i < W; ++i) w[i] = rec[r * W + i];
+      uint32_t w[U];
+      rec_load<FMT>(rec, rb + r, w);
       const uint16_t q = gh[r];
-      if (q) lds_hist_add<W>(h64, cbr, nw, w, q);  // a (0, 0) pair adds nothing
+      if (q) lds_hist_add<FMT>(h64, cbr, nw, F, cells + 4 + lane, w, q);  // (0, 0) adds nothing
     }
     __syncthreads();
     for (int c = tid; c < cells; c += HIST_THREADS) {
@@ -631,10 +642,12 @@ __global__ __launch_bounds__(256) void k_hist_reduce(DevLearner L) {
 // (g, h) cells with 64-bit LDS atomics (exact, order-independent).  Block (chunk a,
 // feature group y): the rows of chunk a (hist_assign) and the features of group y,
 // whose cells fit LDS; partial slot a receives the group's cells.
-template <int W>
+template <int FMT>
 __global__ __launch_bounds__(HIST_THREADS) void k_hist_f32(DevLearner L) {
+  constexpr int U = rec_words(FMT);
   extern __shared__ unsigned long long lds64[];
   __shared__ int32_t cb[16 * LGBM_MAX_W];
+  __shared__ int32_t s_pos[16 * LGBM_MAX_W];  // feature f's field: word << 8 | shift
   __shared__ int32_t s_a0[SPEC_MAX], s_nb[SPEC_MAX];
   __shared__ int64_t s_R;
   Ctl* ctl = L.ctl;
@@ -652,7 +665,12 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_f32(DevLearner L) {
         ctl->hjobs[j].nblk = s_nb[j];
       }
   }
-  for (int f = f0 + tid; f < f1; f += HIST_THREADS) cb[f] = (int32_t)L.feats[f].cell_base;
+  for (int f = f0 + tid; f < f1; f += HIST_THREADS) {
+    cb[f] = (int32_t)L.feats[f].cell_base;
+    int wi, sh;
+    rec_field_pos(FMT, f, &wi, &sh);
+    s_pos[f] = (wi << 8) | sh;
+  }
   __syncthreads();
   const int32_t a = (int32_t)blockIdx.x;
   int32_t j = -1;
@@ -667,18 +685,19 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_f32(DevLearner L) {
   const int64_t R = s_R;
   const int64_t lo = (int64_t)(a - s_a0[j]) * R;
   const int64_t hi = min(J.count, lo + R);
-  const uint4* __restrict__ rec = rec_buf(L.bufs, J.buf) + J.begin * W;
+  const uint4* __restrict__ rec = rec_buf(L.bufs, J.buf);  // rows J.begin + r
   const float2* __restrict__ gh = L.bufs.g32[J.buf] + J.begin;
+  const int64_t rb = J.begin;
   const double gm = ldexp(1.0, ctl->g_shift), hm = ldexp(1.0, ctl->h_shift);
   for (int64_t r = lo + tid; r < hi; r += HIST_THREADS) {
-    uint4 w[W];
-#pragma unroll
-    for (int i = 0; i < W; ++i) w[i] = rec[r * W + i];
+    uint32_t w[U];
+    rec_load<FMT>(rec, rb + r, w);
     const float2 v = gh[r];
     const unsigned long long gi = (unsigned long long)(long long)rint((double)v.x * gm);
     const unsigned long long hi_ = (unsigned long long)(long long)rint((double)v.y * hm);
     for (int f = f0; f < f1; ++f) {
-      const int c = cb[f] - cbase + (int)rec_byte(w, f);
+      const int pos = s_pos[f];
+      const int c = cb[f] - cbase + (int)rec_field<FMT>(w, pos >> 8, pos & 0xff);
       __hip_atomic_fetch_add(&lds64[2 * c], gi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       __hip_atomic_fetch_add(&lds64[2 * c + 1], hi_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
@@ -842,57 +861,61 @@ __global__ __launch_bounds__(LGBM_WAVE) void k_scan_explicit(const double* __res
 // record in LDS and walks the tree with one byte read and one route-mask word per
 // level (k_tree_finalize precomputes, per node, the set of bins routed right).
 // ===========================================================================
-template <int W>
-__global__ __launch_bounds__(256) void k_score_update(DevLearner L, double lr,
-                                                      double* __restrict__ score) {
-  constexpr int kStride = 4 * W + 1;  // words per staged record: odd, so byte reads of
-                                      // different lanes hit different banks
+template <int FMT, bool LEAF_OF>
+__global__ __launch_bounds__(256) void k_walk(DevLearner L, double lr, double* __restrict__ score,
+                                              uint8_t* __restrict__ leaf_of) {
+  constexpr int U = rec_words(FMT), BPW = rec_bpw(FMT), BB = rec_bits(FMT);
+  constexpr uint32_t BM = (1u << BB) - 1u;
+  constexpr int kStride = U + 1;  // words per staged record: odd (U is even), so word
+                                  // reads of different lanes hit different banks
   __shared__ uint32_t s_mask[(MAX_LEAVES - 1) * 8];
   __shared__ uint32_t s_node[MAX_LEAVES - 1];
   __shared__ double vals[MAX_LEAVES];
   __shared__ uint32_t s_rec[256 * kStride];
   const int32_t nl = L.ctl->num_leaves;
-  if (nl <= 1) return;
+  if (!LEAF_OF && nl <= 1) return;
   const int tid = threadIdx.x;
   for (int i = tid; i < (nl - 1) * 8; i += blockDim.x) s_mask[i] = L.tree.route_mask[i];
   for (int i = tid; i < nl - 1; i += blockDim.x) s_node[i] = L.tree.route_node[i];
-  for (int i = tid; i < nl; i += blockDim.x)
-    vals[i] = maybe_round_to_zero(L.tree.leaf_value[i] * lr);
+  if (!LEAF_OF)
+    for (int i = tid; i < nl; i += blockDim.x)
+      vals[i] = maybe_round_to_zero(L.tree.leaf_value[i] * lr);
   __syncthreads();
   const uint4* __restrict__ rec = L.bufs.rec[BUF_ORIG];
   uint32_t* mine = s_rec + tid * kStride;
-  const uint8_t* bytes = (const uint8_t*)mine;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t r = (int64_t)blockIdx.x * blockDim.x + tid; r < L.N; r += stride) {
+    uint32_t w[U];
+    rec_load<FMT>(rec, r, w);
 #pragma unroll
-    for (int i = 0; i < W; ++i) {
-      const uint4 w = rec[r * W + i];
-      mine[4 * i] = w.x;
-      mine[4 * i + 1] = w.y;
-      mine[4 * i + 2] = w.z;
-      mine[4 * i + 3] = w.w;
-    }
+    for (int i = 0; i < U; ++i) mine[i] = w[i];
     int32_t node = 0;
     for (int depth = 0; depth < nl && node >= 0; ++depth) {  // a path has < nl nodes
       const uint32_t u = s_node[node];
-      const uint32_t bin = bytes[u & 0xffu];
+      const uint32_t f = u & 0xffu;
+      const uint32_t wi = f / BPW;
+      const uint32_t bin = (mine[wi] >> (BB * (f - wi * BPW))) & BM;
       const uint32_t right = (s_mask[node * 8 + (bin >> 5)] >> (bin & 31u)) & 1u;
       node = right ? ((int32_t)u >> 20) : ((int32_t)(u << 12) >> 20);
     }
-    if (node < 0 && ~node < nl) score[r] += vals[~node];
+    if (LEAF_OF) {
+      leaf_of[r] = (uint8_t)(nl <= 1 ? 0 : ~node);
+    } else if (node < 0 && ~node < nl) {
+      score[r] += vals[~node];
+    }
   }
 }
 
-template <int W>
-__global__ void k_gather_rows(const uint32_t* __restrict__ rows, int64_t n, const uint4* __restrict__ rec,
-                              const uint16_t* __restrict__ gh, const float2* __restrict__ g32,
-                              uint4* __restrict__ rec_out, uint16_t* __restrict__ gh_out,
-                              float2* __restrict__ g32_out) {
+__global__ void k_gather_rows(const uint32_t* __restrict__ rows, int64_t n, int32_t U,
+                              const uint4* __restrict__ rec, const uint16_t* __restrict__ gh,
+                              const float2* __restrict__ g32, uint4* __restrict__ rec_out,
+                              uint16_t* __restrict__ gh_out, float2* __restrict__ g32_out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int64_t r = rows[i];
-#pragma unroll
-  for (int k = 0; k < W; ++k) rec_out[i * W + k] = rec[r * W + k];
+  const uint2* src = (const uint2*)rec;
+  uint2* dst = (uint2*)rec_out;
+  for (int k = 0; k < U / 2; ++k) dst[i * (U / 2) + k] = src[r * (U / 2) + k];
   if (gh) gh_out[i] = gh[r];
   if (g32) g32_out[i] = g32[r];
 }
@@ -913,10 +936,10 @@ __global__ void k_pack_partition(const uint32_t* __restrict__ bins, int64_t n,
 // ===========================================================================
 // launchers
 // ===========================================================================
-void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t W, uint4* rec,
+void launch_pack_records(const uint8_t* bins, int64_t n, int32_t F, int32_t fmt, uint4* rec,
                          hipStream_t s) {
   const int64_t blocks = (n + 255) / 256;
-  k_pack_records<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(bins, n, F, W, rec);
+  k_pack_records<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(bins, n, F, fmt, rec);
 }
 int32_t stat_blocks(int64_t n) {
   return (int32_t)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, STAT_BLOCKS));
@@ -966,17 +989,17 @@ void launch_requant(const float* g, const float* h, int64_t n, const Ctl* ctl, i
 void launch_hist(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
   const dim3 g(HIST_GRID_Q + SPEC_MAX), blk(HIST_THREADS);
   if (L.total_cells <= HIST_WAVE_CELLS) {
-    const size_t lds = (size_t)HIST_WAVES * (L.total_cells + 4) * sizeof(uint32_t);
-    DISPATCH_W(L.W, KLAUNCH(ev, (k_hist_jobs<kW, true>), g, blk, lds, s, L));
+    const size_t lds = (size_t)HIST_WAVES * (L.total_cells + LDS_TRASH_CELLS) * sizeof(uint32_t);
+    DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_hist_jobs<kF, true>), g, blk, lds, s, L));
   } else {
-    const size_t lds = (size_t)(L.total_cells + 4) * sizeof(unsigned long long);
-    DISPATCH_W(L.W, KLAUNCH(ev, (k_hist_jobs<kW, false>), g, blk, lds, s, L));
+    const size_t lds = (size_t)(L.total_cells + LDS_TRASH_CELLS) * sizeof(unsigned long long);
+    DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_hist_jobs<kF, false>), g, blk, lds, s, L));
   }
 }
 void launch_hist_f32(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
   const dim3 g(HIST_GRID + SPEC_MAX, (unsigned)std::max(L.n_fgroups, 1)), blk(HIST_THREADS);
   const size_t lds = (size_t)2 * HIST_FP_CELLS * sizeof(unsigned long long);
-  DISPATCH_W(L.W, KLAUNCH(ev, (k_hist_f32<kW>), g, blk, lds, s, L));
+  DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_hist_f32<kF>), g, blk, lds, s, L));
 }
 void launch_fp_prep(const DevLearner& L, const float* g, const float* h, int64_t n,
                     const uint4* partials, hipStream_t s) {
@@ -1002,16 +1025,22 @@ void launch_score_update(const DevLearner& L, double lr, double* score, hipStrea
                          const KernelEvents* ev) {
   int64_t blocks = std::min<int64_t>((L.N + 255) / 256, 2048);
   if (blocks < 1) blocks = 1;
-  DISPATCH_W(L.W, KLAUNCH(ev, k_score_update<kW>, dim3((unsigned)blocks), dim3(256), 0, s, L, lr,
-                          score));
+  DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_walk<kF, false>), dim3((unsigned)blocks), dim3(256), 0, s, L,
+                              lr, score, (uint8_t*)nullptr));
 }
-void launch_gather_rows(int W, const uint32_t* rows, int64_t n, const uint4* rec, const uint16_t* gh,
+void launch_leaf_of(const DevLearner& L, uint8_t* leaf_of, hipStream_t s) {
+  int64_t blocks = std::min<int64_t>((L.N + 255) / 256, 2048);
+  if (blocks < 1) blocks = 1;
+  DISPATCH_FMT(L.fmt, (k_walk<kF, true><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+                          L, 0.0, (double*)nullptr, leaf_of)));
+}
+void launch_gather_rows(int fmt, const uint32_t* rows, int64_t n, const uint4* rec, const uint16_t* gh,
                         const float2* g32, uint4* rec_out, uint16_t* gh_out, float2* g32_out,
                         hipStream_t s) {
   const int64_t blocks = (n + 255) / 256;
   if (blocks < 1) return;
-  DISPATCH_W(W, (k_gather_rows<kW><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
-                    rows, n, rec, gh, g32, rec_out, gh_out, g32_out)));
+  k_gather_rows<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(rows, n, rec_words(fmt), rec, gh, g32,
+                                                              rec_out, gh_out, g32_out);
 }
 void launch_subtract(const double* a, const double* b, int64_t n, double* out, hipStream_t s) {
   const int64_t blocks = (n + 255) / 256;

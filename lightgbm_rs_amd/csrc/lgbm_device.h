@@ -60,13 +60,51 @@
 #define ERR_SLOTS 8
 #define ERR_NEG_HESSIAN 16  // quantized histograms: a hessian below zero
 
-// Partition rows per thread for a W-word record: two tiles of records stay in
-// registers (the next tile's loads overlap this tile's work) within 128 VGPRs.
-__host__ __device__ constexpr int part_rows(int W) {
-  return W <= 2 ? PART_ROWS_PER_THREAD : (W <= 4 ? 2 : 1);
+// Row record formats, one code per resident layout (`fmt`):
+//   1..8   (W): W 16-byte words = 4W u32; four 8-bit bins per u32 (features 0..F-1 in
+//          order), the row's original index in the last u32;
+//   16 + U (U even, 2..8): U u32 = 4U bytes; five 6-bit bins per u32 (bits 0-29;
+//          every num_bin <= 64), the quantized pair in bits 24-29 of the last u32
+//          (which holds at most four bins: F <= 5U - 1); no row index.
+#define REC_FMT_PACKED 16
+__host__ __device__ constexpr bool rec_packed(int fmt) { return fmt > REC_FMT_PACKED; }
+__host__ __device__ constexpr int rec_words(int fmt) {  // u32 per record
+  return rec_packed(fmt) ? fmt - REC_FMT_PACKED : 4 * fmt;
 }
-__host__ __device__ constexpr int64_t part_tile(int W) {
-  return (int64_t)PART_THREADS * part_rows(W);
+__host__ __device__ constexpr int rec_bytes(int fmt) { return 4 * rec_words(fmt); }
+__host__ __device__ constexpr int rec_bpw(int fmt) { return rec_packed(fmt) ? 5 : 4; }
+__host__ __device__ constexpr int rec_bits(int fmt) { return rec_packed(fmt) ? 6 : 8; }
+// bin slots of a record (the histogram's cell-base table covers them all; slots past
+// the last feature read zero bins into a trash cell): legacy 4 per u32 but none in
+// the row-index u32; packed 5 per u32 but 4 in the last (its top bits hold the pair)
+__host__ __device__ constexpr int rec_slots(int fmt) {
+  return rec_packed(fmt) ? 5 * rec_words(fmt) - 1 : 4 * (rec_words(fmt) - 1);
+}
+// word and bit offset of feature f's bin in a record
+__host__ __device__ inline void rec_field_pos(int fmt, int f, int* wi, int* sh) {
+  const int bpw = rec_bpw(fmt);
+  *wi = f / bpw;
+  *sh = (f - *wi * bpw) * rec_bits(fmt);
+}
+// packed quantized pair <-> the u16 form (q_g as u8) | (q_h as u8) << 8 used elsewhere:
+// 6 bits (q_g + 2) | q_h << 3 for q_g in [-2, 2], q_h in [0, 4]
+__host__ __device__ inline uint32_t gh_pack6(uint32_t q16) {
+  const int32_t qg = (int32_t)(int8_t)(q16 & 0xffu);
+  const uint32_t qh = (q16 >> 8) & 0xffu;
+  return (uint32_t)(qg + 2) | (qh << 3);
+}
+__host__ __device__ inline uint32_t gh_unpack6(uint32_t e) {
+  const int32_t qg = (int32_t)(e & 7u) - 2;
+  return (uint32_t)(uint8_t)(int8_t)qg | ((e >> 3) << 8);
+}
+
+// Partition rows per thread: two tiles of records stay in registers (the next tile's
+// loads overlap this tile's work) within 128 VGPRs.
+__host__ __device__ constexpr int part_rows(int fmt) {
+  return rec_bytes(fmt) <= 32 ? PART_ROWS_PER_THREAD : (rec_bytes(fmt) <= 64 ? 2 : 1);
+}
+__host__ __device__ constexpr int64_t part_tile(int fmt) {
+  return (int64_t)PART_THREADS * part_rows(fmt);
 }
 // Block b of a G-block partition launch over T tiles takes tiles [b*T/G, (b+1)*T/G);
 // the block that takes tile t:

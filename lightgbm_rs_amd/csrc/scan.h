@@ -9,61 +9,121 @@
 
 namespace lgbm {
 
-#define DISPATCH_W(W, ...)                                                 \
-  switch (W) {                                                              \
-    case 1: { constexpr int kW = 1; __VA_ARGS__; } break;                  \
-    case 2: { constexpr int kW = 2; __VA_ARGS__; } break;                  \
-    case 3: { constexpr int kW = 3; __VA_ARGS__; } break;                  \
-    case 4: { constexpr int kW = 4; __VA_ARGS__; } break;                  \
-    case 5: { constexpr int kW = 5; __VA_ARGS__; } break;                  \
-    case 6: { constexpr int kW = 6; __VA_ARGS__; } break;                  \
-    case 7: { constexpr int kW = 7; __VA_ARGS__; } break;                  \
-    case 8: { constexpr int kW = 8; __VA_ARGS__; } break;                  \
+// One case per record format (lgbm_device.h): kF is the format as a constant.
+#define DISPATCH_FMT(FMT, ...)                                              \
+  switch (FMT) {                                                            \
+    case 1: { constexpr int kF = 1; __VA_ARGS__; } break;                   \
+    case 2: { constexpr int kF = 2; __VA_ARGS__; } break;                   \
+    case 3: { constexpr int kF = 3; __VA_ARGS__; } break;                   \
+    case 4: { constexpr int kF = 4; __VA_ARGS__; } break;                   \
+    case 5: { constexpr int kF = 5; __VA_ARGS__; } break;                   \
+    case 6: { constexpr int kF = 6; __VA_ARGS__; } break;                   \
+    case 7: { constexpr int kF = 7; __VA_ARGS__; } break;                   \
+    case 8: { constexpr int kF = 8; __VA_ARGS__; } break;                   \
+    case REC_FMT_PACKED + 2: { constexpr int kF = REC_FMT_PACKED + 2; __VA_ARGS__; } break; \
+    case REC_FMT_PACKED + 4: { constexpr int kF = REC_FMT_PACKED + 4; __VA_ARGS__; } break; \
+    case REC_FMT_PACKED + 6: { constexpr int kF = REC_FMT_PACKED + 6; __VA_ARGS__; } break; \
+    case REC_FMT_PACKED + 8: { constexpr int kF = REC_FMT_PACKED + 8; __VA_ARGS__; } break; \
     default: break;                                                         \
   }
 
-
-// Byte f of a record held in registers.  Selects with compile-time indices only, so
-// the record never leaves the register file.
-template <int W>
-__device__ __forceinline__ uint32_t rec_byte(const uint4 (&w)[W], int f) {
-  const int wi = f >> 4;
-  const int j = (f >> 2) & 3;
-  uint32_t word = 0u;
+// Record r of a buffer into registers / out of registers: u32 words, moved as 16-byte
+// words when the record size allows, else 8-byte words.
+template <int FMT>
+__device__ __forceinline__ void rec_load(const uint4* __restrict__ base, int64_t r,
+                                         uint32_t (&w)[rec_words(FMT)]) {
+  constexpr int U = rec_words(FMT);
+  if constexpr (U % 4 == 0) {
 #pragma unroll
-  for (int i = 0; i < W; ++i) {
-    const uint4 q = w[i];
-    const uint32_t x = j == 0 ? q.x : (j == 1 ? q.y : (j == 2 ? q.z : q.w));
-    word = i == wi ? x : word;
+    for (int i = 0; i < U / 4; ++i) {
+      const uint4 q = base[r * (U / 4) + i];
+      w[4 * i] = q.x;
+      w[4 * i + 1] = q.y;
+      w[4 * i + 2] = q.z;
+      w[4 * i + 3] = q.w;
+    }
+  } else {
+    const uint2* b2 = (const uint2*)base;
+#pragma unroll
+    for (int i = 0; i < U / 2; ++i) {
+      const uint2 q = b2[r * (U / 2) + i];
+      w[2 * i] = q.x;
+      w[2 * i + 1] = q.y;
+    }
   }
-  return (word >> (8 * (f & 3))) & 0xffu;
+}
+template <int FMT>
+__device__ __forceinline__ void rec_store(uint4* __restrict__ base, int64_t r,
+                                          const uint32_t (&w)[rec_words(FMT)]) {
+  constexpr int U = rec_words(FMT);
+  if constexpr (U % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < U / 4; ++i)
+      base[r * (U / 4) + i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+  } else {
+    uint2* b2 = (uint2*)base;
+#pragma unroll
+    for (int i = 0; i < U / 2; ++i) b2[r * (U / 2) + i] = make_uint2(w[2 * i], w[2 * i + 1]);
+  }
 }
 
-// Accumulate one row (packed quantized pair q) into the LDS histogram of all features:
-// every byte of record words 0 .. nw-1 (wave-uniform); cbr[f] is feature f's first
-// cell, with bytes beyond the last feature mapped to a trash cell.  Callers skip a
-// (0, 0) pair: it adds nothing.
-template <int W>
+// Word wi of a record held in registers: an OR of masked words with compile-time
+// indices (a select chain would be turned into an indexed load, which moves the record
+// to scratch memory); wi is wave-uniform where it is used.
+template <int FMT>
+__device__ __forceinline__ uint32_t rec_word(const uint32_t (&w)[rec_words(FMT)], int wi) {
+  uint32_t x = 0u;
+#pragma unroll
+  for (int i = 0; i < rec_words(FMT); ++i)
+    x |= w[i] & (uint32_t)__builtin_amdgcn_readfirstlane(-(int32_t)(i == wi));
+  return x;
+}
+// The bin of a feature whose field is word wi, bit sh (rec_field_pos).
+template <int FMT>
+__device__ __forceinline__ uint32_t rec_field(const uint32_t (&w)[rec_words(FMT)], int wi, int sh) {
+  return (rec_word<FMT>(w, wi) >> sh) & ((1u << rec_bits(FMT)) - 1u);
+}
+// The quantized pair of a packed record, in the u16 form.
+template <int FMT>
+__device__ __forceinline__ uint32_t rec_gh(const uint32_t (&w)[rec_words(FMT)]) {
+  return gh_unpack6((w[rec_words(FMT) - 1] >> 24) & 63u);
+}
+template <int FMT>
+__device__ __forceinline__ void rec_set_gh(uint32_t (&w)[rec_words(FMT)], uint32_t q16) {
+  constexpr int U = rec_words(FMT);
+  w[U - 1] = (w[U - 1] & 0x00ffffffu) | (gh_pack6(q16) << 24);
+}
+
+// Accumulate one row (quantized pair q in the u16 form) into the packed u64 LDS
+// histogram of all features: every bin slot of the record words 0 .. nw-1; cbr[s] is
+// slot s's first cell.  Slots at or past F (wave-uniform) hold no feature: they go to
+// the lane's own trash cell tl (cells + 4 + lane), so they cost no address conflicts
+// and no branch.  Callers skip a (0, 0) pair: it adds nothing.
+#define LDS_TRASH_CELLS (4 + LGBM_WAVE)
+template <int FMT>
 __device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int32_t* cbr, int nw,
-                                             const uint4 (&w)[W], uint32_t q) {
+                                             int F, int tl, const uint32_t (&w)[rec_words(FMT)],
+                                             uint32_t q) {
+  constexpr int BPW = rec_bpw(FMT), BB = rec_bits(FMT), NS = rec_slots(FMT);
+  constexpr uint32_t M = (1u << BB) - 1u;
   const int32_t qg = (int32_t)(int8_t)(q & 0xffu);
   const int32_t qh = (int32_t)(int8_t)(q >> 8);
   const unsigned long long v = (unsigned long long)(long long)qg +
                                ((unsigned long long)(uint32_t)qh << 22) +
                                ((unsigned long long)(qh == 3 ? 1u : 0u) << 43);
 #pragma unroll
-  for (int k = 0; k < 4 * W - 1; ++k) {
+  for (int k = 0; k < (NS + BPW - 1) / BPW; ++k) {
     if (k < nw) {
-      const uint4 wd = w[k >> 2];
-      const uint32_t word = (k & 3) == 0 ? wd.x : ((k & 3) == 1 ? wd.y : ((k & 3) == 2 ? wd.z : wd.w));
+      const uint32_t word = w[k];
 #pragma unroll
-      for (int bb = 0; bb < 4; ++bb)
-        __hip_atomic_fetch_add(&lds[cbr[4 * k + bb] + ((word >> (8 * bb)) & 0xffu)], v,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      for (int bb = 0; bb < BPW; ++bb)
+        if (BPW * k + bb < NS) {
+          const int a = BPW * k + bb < F ? cbr[BPW * k + bb] + (int)((word >> (BB * bb)) & M) : tl;
+          __hip_atomic_fetch_add(&lds[a], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
     }
   }
 }
-
 
 // ===========================================================================
 // FindBestThreshold for one (leaf, feature) by one wave: find_best_split_cpu_native
