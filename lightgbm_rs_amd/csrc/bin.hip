@@ -102,6 +102,71 @@ __global__ __launch_bounds__(256) void k_bin_records(const T* __restrict__ x, in
   }
 }
 
+// The wide layout: block (row chunk, 16-feature word); the word's bounds staged in
+// LDS (16 features x at most 256 bins), one thread per row writes the word's 16 bytes
+// of the row's binmat row (padding features 0).  Feature group 0 also writes the
+// identity row-index records.
+constexpr int32_t BIN_WIDE_F = 16;
+template <typename T, bool COL_MAJOR>
+__global__ __launch_bounds__(256) void k_bin_wide(const T* __restrict__ x, int64_t n, int32_t F,
+                                                  int64_t stride,
+                                                  const DevBinFeature* __restrict__ feats,
+                                                  const double* __restrict__ ub,
+                                                  const int2* __restrict__ cats,
+                                                  uint8_t* __restrict__ binmat,
+                                                  uint32_t* __restrict__ rec) {
+  __shared__ double s_ub[BIN_WIDE_F * 256];
+  __shared__ DevBinFeature s_f[BIN_WIDE_F];
+  __shared__ int32_t s_lo, s_hi;
+  const int f0 = (int)blockIdx.y * BIN_WIDE_F;
+  const int nf = min(BIN_WIDE_F, F - f0);
+  if (threadIdx.x < (unsigned)nf) s_f[threadIdx.x] = feats[f0 + threadIdx.x];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // the word's entries of the bounds array: from its first feature's to the next
+    // word's first feature's (every feature holds num_bin entries)
+    int32_t lo = nf > 0 ? s_f[0].ub_pos : 0, hi = lo;
+    for (int k = 0; k < nf; ++k) {
+      const DevBinFeature& f = s_f[k];
+      const int32_t end = f.categorical ? f.ub_pos : f.off + f.last + 1;
+      hi = max(hi, end);
+    }
+    s_lo = lo;
+    s_hi = hi;
+  }
+  __syncthreads();
+  const int32_t lo = s_lo, cnt = s_hi - s_lo;
+  for (int i = threadIdx.x; i < cnt; i += blockDim.x) s_ub[i] = ub[lo + i];
+  if (threadIdx.x < (unsigned)nf && !s_f[threadIdx.x].categorical) s_f[threadIdx.x].off -= lo;
+  __syncthreads();
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += step) {
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < BIN_WIDE_F; ++k) {
+      if (k < nf) {
+        const int f = f0 + k;
+        const double val = (double)(COL_MAJOR ? x[(int64_t)f * n + r] : x[r * F + f]);
+        v[k >> 2] |= bin_of(s_f[k], s_ub, cats, val) << (8 * (k & 3));
+      }
+    }
+    *(uint4*)(binmat + r * stride + f0) = make_uint4(v[0], v[1], v[2], v[3]);
+    if (blockIdx.y == 0) rec[r] = (uint32_t)r;
+  }
+}
+
+template <typename T, bool CM>
+void launch_wide_typed(const void* x, int64_t n, int32_t F, int64_t stride, const DevBinFeature* feats,
+                       const double* ub, const int2* cats, uint8_t* binmat, uint4* rec, hipStream_t s,
+                       const KernelEvents* ev) {
+  const int64_t want = (n + 255) / 256;
+  const unsigned blocks = (unsigned)std::min<int64_t>(std::max<int64_t>(want, 1), 1024);
+  // every 16-byte word of a row, the padding words too (zeros)
+  const unsigned words = (unsigned)(stride / BIN_WIDE_F);
+  KLAUNCH(ev, (k_bin_wide<T, CM>), dim3(blocks, words), dim3(256), 0, s, (const T*)x, n, F, stride,
+          feats, ub, cats, binmat, (uint32_t*)rec);
+}
+
 template <typename T, bool CM>
 void launch_typed(const void* x, int64_t n, int32_t F, int32_t fmt, const DevBinFeature* feats,
                   const double* ub, int32_t ub_count, const int2* cats, uint4* rec, hipStream_t s,
@@ -114,6 +179,24 @@ void launch_typed(const void* x, int64_t n, int32_t F, int32_t fmt, const DevBin
 }
 
 }  // namespace
+
+void launch_bin_wide(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
+                     int64_t stride, const DevBinFeature* feats, const double* ub,
+                     const int2* cats, uint8_t* binmat, uint4* rec, hipStream_t s,
+                     const KernelEvents* ev) {
+  if (n <= 0) return;
+  if (f64) {
+    if (col_major)
+      launch_wide_typed<double, true>(x, n, F, stride, feats, ub, cats, binmat, rec, s, ev);
+    else
+      launch_wide_typed<double, false>(x, n, F, stride, feats, ub, cats, binmat, rec, s, ev);
+  } else {
+    if (col_major)
+      launch_wide_typed<float, true>(x, n, F, stride, feats, ub, cats, binmat, rec, s, ev);
+    else
+      launch_wide_typed<float, false>(x, n, F, stride, feats, ub, cats, binmat, rec, s, ev);
+  }
+}
 
 void launch_bin_records(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
                         int32_t fmt, const DevBinFeature* feats, const double* ub, int32_t ub_count,

@@ -94,7 +94,9 @@ struct lgbm_hip_ctx {
   // shape
   int64_t N = 0;
   int32_t F = 0, fmt = 1, total_cells = 0;  // fmt: row record format (lgbm_device.h)
-  bool legacy_records = false;              // LGBM_HIP_RECORDS=legacy: 8-bit records only
+  int32_t records_env = 0;  // LGBM_HIP_RECORDS: 0 automatic, 1 legacy (8-bit records), 2 wide
+  uint8_t* binmat = nullptr;  // wide layout: row-major bins [N][row_stride]
+  int64_t row_stride = 0;
   uint64_t slot_len = 0;
   std::vector<DevFeature> feats;
   std::vector<double> ub_host;  // per-bin values (numerical: upper bounds, categorical: categories)
@@ -120,7 +122,9 @@ struct lgbm_hip_ctx {
   float *gk = nullptr, *hk = nullptr;  // multiclass: [num_class][N] gradients
   int32_t* hist_part = nullptr;  // [HIST_SLOTS][cells][3]
   int32_t* hist_sum = nullptr;   // [cells][3]
-  int32_t* hist_acc = nullptr;   // [SPEC_MAX][cells][3]
+  int32_t* hist_acc = nullptr;   // [SPEC_MAX][acc_cells][3]
+  int64_t* hist_acc64 = nullptr;  // wide layout: [SPEC_MAX][acc_cells][2]
+  int32_t acc_cells = 0;          // total_cells (+ 1 totals cell in the wide layout)
   unsigned long long* part_slots = nullptr;  // [part_blocks + SPEC_MAX][cells] packed
   int64_t* hist_part64 = nullptr;  // [HIST_SLOTS][cells][2]
   int64_t* int_slots64 = nullptr;  // [SLOT_CAP][cells][2]
@@ -289,6 +293,10 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.hist_part = c->hist_part;
   L.hist_sum = c->hist_sum;
   L.hist_acc = c->hist_acc;
+  L.hist_acc64 = c->hist_acc64;
+  L.acc_cells = c->acc_cells;
+  L.binmat = c->binmat;
+  L.row_stride = c->row_stride;
   L.part_slots = c->part_slots;
   L.hist_part64 = c->hist_part64;
   L.int_slots64 = c->int_slots64;
@@ -540,7 +548,10 @@ void enqueue_rounds(lgbm_hip_ctx* c, int32_t rounds, int32_t fp) {
   for (int32_t r = 0; r < rounds; ++r) {
     launch_plan(L, SLOT_CAP(c->lcap), c->stream, ev_kernel(c, FAM_SCAN, &ke));
     launch_partition(L, fp, c->part_blocks, c->stream, ev_kernel(c, FAM_PART, &ke));
-    if (fp) launch_hist_f32(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
+    if (rec_wide(c->fmt))
+      launch_hist_wide(L, fp, c->stream, ev_kernel(c, FAM_HIST, &ke));
+    else if (fp)
+      launch_hist_f32(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
     launch_pair_scan(L, c->spec_max, c->part_blocks, c->stream, ev_kernel(c, FAM_SCAN, &ke));
   }
 }
@@ -552,7 +563,9 @@ void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth, int32_
   KernelEvents ke;
   launch_tree_init(L, num_leaves, max_depth, SLOT_CAP(num_leaves), c->spec_max, fp, c->stream,
                    ev_kernel(c, -1, &ke));
-  if (fp)
+  if (rec_wide(c->fmt))
+    launch_hist_wide(L, fp, c->stream, ev_kernel(c, FAM_HIST, &ke));
+  else if (fp)
     launch_hist_f32(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
   else
     launch_hist(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
@@ -790,8 +803,9 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
     (void)hipGraphExecDestroy(c->graph_exec);
     c->graph_exec = nullptr;
   }
-  if (F > 16 * LGBM_MAX_W - 4)
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "more features than the record layout holds");
+  if (F > WIDE_MAX_F)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "more than " + std::to_string(WIDE_MAX_F) + " features");
   if (num_data >= (1ll << 31) - 1)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_data must fit data_size_t (i32)");
   std::vector<DevFeature> feats(F);
@@ -823,24 +837,30 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
     acc += m.num_bin;
     uacc += m.num_bin;
   }
-  if (acc > (uint32_t)(MAX_FGROUPS - 1) * (HIST_FP_CELLS - 256))
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "too many histogram cells for the f32 feature groups");
-  if (acc > HIST_WAVE_CELLS && num_data > (int64_t)HIST_GRID_Q * HIST_BLOCK_MAX_ROWS)
+  // row layout: the wide one (row indices moved, bins in a fixed row-major matrix)
+  // when the records cannot hold the features or the quantized builds' LDS cannot
+  // hold the cells; else 6-bit bins with the quantized pair inside when every feature
+  // has at most 64 bins and fits (F <= 39), else 8-bit bins and the row index
+  const bool wide = c->records_env == 2 || F > 16 * LGBM_MAX_W - 4 || acc > QUANT_LDS_CELLS;
+  if (!wide && acc > HIST_WAVE_CELLS && num_data > (int64_t)HIST_GRID_Q * HIST_BLOCK_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "rows per histogram block exceed the packed LDS cell fields");
+  if (wide && wide_prepare())
+    return set_err(c, LGBM_HIP_ERR_HIP, "the wide histogram kernels' LDS size was refused");
   c->F = F;
   c->N = num_data;
-  // record format: 6-bit bins with the quantized pair inside when every feature has at
-  // most 64 bins and fits (F <= 39), else 8-bit bins and the row index
   uint32_t max_nb = 0;
   for (int f = 0; f < F; ++f) max_nb = std::max(max_nb, meta[f].num_bin);
   c->fmt = (F + 4 + 15) / 16;
-  if (!c->legacy_records && max_nb <= 64 && F <= 39) {
+  if (wide) {
+    c->fmt = REC_FMT_WIDE;
+  } else if (c->records_env != 1 && max_nb <= 64 && F <= 39) {
     int U = (F + 5) / 5;
     U = std::max(U + (U & 1), 2);
     c->fmt = REC_FMT_PACKED + U;
   }
   c->total_cells = (int32_t)acc;
+  c->acc_cells = (int32_t)acc + (wide ? 1 : 0);
   c->slot_len = 2ull * acc;
   c->feats = feats;
   c->lcap = 0;  // slots depend on slot_len
@@ -864,17 +884,36 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   c->buf_rows[BUF_S0] = c->buf_rows[BUF_S1] = 0;
   if ((rc = dalloc(c, &c->g, (size_t)num_data))) return rc;
   if ((rc = dalloc(c, &c->h, (size_t)num_data))) return rc;
-  if ((rc = dalloc(c, &c->hist_part, (size_t)HIST_SLOTS * acc * 3))) return rc;
+  // the record layouts' partial slots (the wide layout builds into the accumulators)
+  const size_t pc = wide ? 1 : acc;
+  if ((rc = dalloc(c, &c->hist_part, (size_t)HIST_SLOTS * pc * 3))) return rc;
   if ((rc = dalloc(c, &c->hist_sum, (size_t)acc * 3))) return rc;
-  if ((rc = dalloc(c, &c->hist_part64, (size_t)HIST_SLOTS * acc * 2))) return rc;
-  // feature groups of the f32 histogram kernel: consecutive features whose cells fit
-  // one block's LDS
-  {
+  if ((rc = dalloc(c, &c->hist_part64, (size_t)HIST_SLOTS * pc * 2))) return rc;
+  if (wide) {
+    c->row_stride = ((int64_t)F + WIDE_GF_Q - 1) / WIDE_GF_Q * WIDE_GF_Q;
+    if ((rc = dalloc(c, &c->binmat, (size_t)num_data * (size_t)c->row_stride))) return rc;
+    if ((rc = dalloc(c, &c->hist_acc64, (size_t)SPEC_MAX * c->acc_cells * 2))) return rc;
+    HIPCHK(c, hipMemset(c->hist_acc64, 0, (size_t)SPEC_MAX * c->acc_cells * 2 * 8));
+  } else {
+    c->row_stride = 0;
+    if (c->binmat) (void)hipFree(c->binmat);
+    if (c->hist_acc64) (void)hipFree(c->hist_acc64);
+    c->binmat = nullptr;
+    c->hist_acc64 = nullptr;
+    if (acc > (uint32_t)(MAX_FGROUPS - 1) * (HIST_FP_CELLS - 256))
+      return set_err(c, LGBM_HIP_ERR_CAPABILITY, "too many histogram cells for the f32 feature groups");
+  }
+  // feature groups of the record layouts' f32 histogram kernel: consecutive features
+  // whose cells fit one block's LDS (at most MAX_FGROUPS: the cell check above)
+  c->n_fgroups = 0;
+  if (!wide) {
     int32_t ng = 0;
     uint32_t gcells = 0;
     c->fgroup_first[0] = 0;
     for (int f = 0; f < F; ++f) {
       if (f > 0 && gcells + feats[f].num_bin > HIST_FP_CELLS) {
+        if (ng + 1 >= MAX_FGROUPS)
+          return set_err(c, LGBM_HIP_ERR_CAPABILITY, "too many f32 feature groups");
         c->fgroup_first[++ng] = f;
         gcells = 0;
       }
@@ -883,9 +922,9 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
     c->fgroup_first[++ng] = F;
     c->n_fgroups = ng;
   }
-  if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * acc * 3))) return rc;
-  HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * acc * 3 * 4));
-  if ((rc = dalloc(c, &c->part_slots, ((size_t)c->part_blocks + SPEC_MAX) * acc))) return rc;
+  if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * c->acc_cells * 3))) return rc;
+  HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * c->acc_cells * 3 * 4));
+  if ((rc = dalloc(c, &c->part_slots, ((size_t)c->part_blocks + SPEC_MAX) * pc))) return rc;
   if ((rc = ensure_tile_state(c, num_data))) return rc;
   return LGBM_HIP_OK;
 }
@@ -978,7 +1017,8 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   if (const char* e = std::getenv("LGBM_HIP_PART_BLOCKS"))
     c->part_blocks = std::max(1, std::min(65535, std::atoi(e)));
   if (const char* e = std::getenv("LGBM_HIP_GRAPHS")) c->use_graphs = std::strcmp(e, "0") != 0;
-  if (const char* e = std::getenv("LGBM_HIP_RECORDS")) c->legacy_records = std::strcmp(e, "legacy") == 0;
+  if (const char* e = std::getenv("LGBM_HIP_RECORDS"))
+    c->records_env = std::strcmp(e, "legacy") == 0 ? 1 : std::strcmp(e, "wide") == 0 ? 2 : 0;
   if (const char* e = std::getenv("LGBM_HIP_ROUNDS")) c->round_cap = std::max(1, std::atoi(e));
   if (const char* e = std::getenv("LGBM_HIP_SPEC"))
     c->spec_max = std::max(1, std::min(SPEC_MAX, std::atoi(e)));
@@ -1011,6 +1051,9 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->hist_part);
   F(c->hist_sum);
   F(c->hist_acc);
+  F(c->hist_acc64);
+  F(c->binmat);
+  F(c->cat_bits);
   F(c->part_slots);
   F(c->hist_part64);
   F(c->int_slots64);
@@ -1112,7 +1155,10 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   HIPCHK(c, hipMalloc((void**)&tmp, (size_t)F * num_data));
   hipError_t e = hipMemcpy(tmp, bins, (size_t)F * num_data, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
-    launch_pack_records(tmp, num_data, F, c->fmt, c->rec[BUF_ORIG], c->stream);
+    if (rec_wide(c->fmt))
+      launch_pack_wide(tmp, num_data, F, c->row_stride, c->binmat, c->rec[BUF_ORIG], c->stream);
+    else
+      launch_pack_records(tmp, num_data, F, c->fmt, c->rec[BUF_ORIG], c->stream);
     e = hipStreamSynchronize(c->stream);
   }
   (void)hipFree(tmp);
@@ -1263,6 +1309,7 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
     d.bin_type = cat ? LGBM_BIN_CATEGORICAL : LGBM_BIN_NUMERICAL;
     DevBinFeature& b = bf[(size_t)f];
     b = DevBinFeature{};
+    b.ub_pos = (int32_t)ub.size();
     if (cat) {
       // ValueToBin of a categorical mapper: the (category, bin) pairs sorted by
       // category; the feature's per-bin values are its categories (bin 0: -1)
@@ -1295,9 +1342,14 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
   if (e == hipSuccess) {
     // c->d_ub holds the same bounds, concatenated in feature order
     KernelEvents ke;
-    launch_bin_records(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->fmt, d_bf,
-                       c->d_ub, (int32_t)ub.size(), d_cats, c->rec[BUF_ORIG], c->stream,
-                       ev_kernel(c, FAM_BIN, &ke));
+    if (rec_wide(c->fmt))
+      launch_bin_wide(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->row_stride,
+                      d_bf, c->d_ub, d_cats, c->binmat, c->rec[BUF_ORIG], c->stream,
+                      ev_kernel(c, FAM_BIN, &ke));
+    else
+      launch_bin_records(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->fmt,
+                         d_bf, c->d_ub, (int32_t)ub.size(), d_cats, c->rec[BUF_ORIG], c->stream,
+                         ev_kernel(c, FAM_BIN, &ke));
     if (c->timing) {
       c->bin_launches += 1.0;
       c->bin_values += (double)num_rows * F;
@@ -1336,6 +1388,14 @@ int lgbm_hip_get_bins(lgbm_hip_ctx* c, uint8_t* out, int64_t n) {
   if (rc) return rc;
   if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "no resident bins");
   if (!out || n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_data");
+  if (rec_wide(c->fmt)) {
+    const size_t st = (size_t)c->row_stride;
+    std::vector<uint8_t> m((size_t)c->N * st);
+    HIPCHK(c, hipMemcpy(m.data(), c->binmat, m.size(), hipMemcpyDeviceToHost));
+    for (int32_t f = 0; f < c->F; ++f)
+      for (int64_t r = 0; r < c->N; ++r) out[(size_t)f * c->N + r] = m[(size_t)r * st + f];
+    return LGBM_HIP_OK;
+  }
   // the original (unpartitioned) records, feature-major
   const int U = rec_words(c->fmt);
   const uint32_t mask = (1u << rec_bits(c->fmt)) - 1u;
@@ -1505,6 +1565,9 @@ int lgbm_hip_build_int_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int
   c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!c->quant_ready) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize first");
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  if (rec_wide(c->fmt))
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "per-op histogram builds need the record layouts (F <= 124, cells <= 8192)");
   if (c->total_cells > QUANT_LDS_CELLS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
@@ -1537,6 +1600,9 @@ int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, in
   int rc = check_ctx(c);
   if (rc) return rc;
   c->ahead = false;  // device inputs change: a pending lookahead is stale
+  if (rec_wide(c->fmt))
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "per-op histogram builds need the record layouts (F <= 124, cells <= 8192)");
   // quantized gradients (after lgbm_hip_quantize) or the f32 gradients as uploaded
   const int32_t fp = c->quant_ready ? 0 : 1;
   if (fp && !c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set gradients first");
@@ -1545,7 +1611,7 @@ int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, in
                    "exact f64 histogram requires num_grad_quant_bins in {2, 4}");
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
-  if (!fp && c->total_cells > QUANT_LDS_CELLS)
+  if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
@@ -1761,6 +1827,7 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   if ((rc = ctl_write(c, CTL_OFF(tile_total), tiles))) return rc;
   DevLearner L = make_learner(c);
   L.fmt = 1;
+  L.total_cells = 0;  // partition only: no histogram cells in LDS
   launch_partition_stable(L, tiles, std::min<int64_t>(c->part_blocks, tiles), c->stream);
   HIPCHK(c, hipGetLastError());
   HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -1792,7 +1859,7 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num
                    "device learner requires num_grad_quant_bins in {2, 4}");
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
-  if (!fp && c->total_cells > QUANT_LDS_CELLS)
+  if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
   if (fp) {
@@ -1841,7 +1908,7 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
                    "device learner requires num_grad_quant_bins in {0, 2, 4}");
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
-  if (!fp && c->total_cells > QUANT_LDS_CELLS)
+  if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
   if (fp) {
@@ -1930,7 +1997,7 @@ int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gai
                    "device learner requires num_grad_quant_bins in {0, 2, 4}");
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
-  if (!fp && c->total_cells > QUANT_LDS_CELLS)
+  if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
   if ((rc = ensure_leaves(c, num_leaves))) return rc;

@@ -70,7 +70,23 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
   const int tid = blockIdx.x * blockDim.x + threadIdx.x;
   const int nthr = gridDim.x * blockDim.x;
   for (int i = tid; i < L.F; i += nthr) L.splittable[i] = 1;  // node slot 0
-  for (int i = tid; i < SPEC_MAX * L.total_cells * 3; i += nthr) L.hist_acc[i] = 0;
+  if (rec_wide(L.fmt)) {
+    // the readers clear every cell they read; the totals cells only the root build
+    // writes (job 0), read by every root scan block
+    for (int j = tid; j < SPEC_MAX; j += nthr) {
+      const size_t t = (size_t)j * L.acc_cells + L.total_cells;
+      if (fp_mode) {
+        L.hist_acc64[2 * t] = 0;
+        L.hist_acc64[2 * t + 1] = 0;
+      } else {
+        L.hist_acc[3 * t] = 0;
+        L.hist_acc[3 * t + 1] = 0;
+        L.hist_acc[3 * t + 2] = 0;
+      }
+    }
+  } else {
+    for (int i = tid; i < SPEC_MAX * L.acc_cells * 3; i += nthr) L.hist_acc[i] = 0;
+  }
   if (tid == 0) {
     const int32_t N = (int32_t)L.N;
     ctl->done = 0;
@@ -93,7 +109,7 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
     ctl->reduce_list[0] = 0;
     // the root ConstructHistogram: all rows
     ctl->n_hjobs = 1;
-    ctl->hjobs[0] = HistJob{BUF_ORIG, 0, 0, N, 0, 0};
+    ctl->hjobs[0] = HistJob{BUF_ORIG, 1, 0, N, 0, 0};  // _pad bit 0: the root build
     DevNodes& nd = L.nodes;
     nd.begin[0] = 0;
     nd.count[0] = N;
@@ -171,7 +187,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   __shared__ int32_t s_fpos[SLOT_CAP(MAX_LEAVES)];
   __shared__ int2 s_child[SLOT_CAP(MAX_LEAVES)];
   __shared__ int32_t s_ps[5][MAX_LEAVES];  // PS_* linkage
-  __shared__ DevFeature s_ft[16 * LGBM_MAX_W];
+  __shared__ DevFeature s_ft[16 * LGBM_MAX_W];  // the record layouts' features (wide: global)
   __shared__ int4 s_commit[MAX_LEAVES];    // (leaf, node slot, node, new right leaf)
   __shared__ int2 s_lc[MAX_LEAVES];        // per leaf: speculated children slots
   __shared__ double2 s_lcg[MAX_LEAVES];    //   and their keys
@@ -206,7 +222,10 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     s_uhi = 0ull;
     s_ulo = 0ull;
   }
-  for (int f = tid; f < F; f += PLAN_THREADS) s_ft[f] = L.feats[f];
+  const bool ft_lds = F <= 16 * LGBM_MAX_W;
+  const DevFeature* __restrict__ fts = ft_lds ? s_ft : L.feats;
+  if (ft_lds)
+    for (int f = tid; f < F; f += PLAN_THREADS) s_ft[f] = L.feats[f];
   for (int s = tid; s < slot_cap; s += PLAN_THREADS) {
     s_gain[s] = nd.key_gain[s];
     s_feat[s] = nd.key_feat[s];
@@ -223,7 +242,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     BestKey k{ninf, -1, INT_MAX32};
     for (int f = lane; f < F; f += LGBM_WAVE) {
       const double g = L.feat_split[(size_t)s * F + f].gain;
-      const BestKey c{g, s_ft[f].real_index, f};
+      const BestKey c{g, fts[f].real_index, f};
       if (g > ninf && key_better(c, k)) k = c;
     }
     k = wave_best(k);
@@ -427,7 +446,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     const int32_t dl = b.default_left;
     const double iv = nd.sums[p].weight;
     const int32_t ic = nd.count[p];
-    const DevFeature& ft = s_ft[fpos];
+    const DevFeature ft = fts[fpos];
     T.split_feature[node] = ft.real_index;
     T.split_gain[node] = (float)(gain + ctl->cfg.min_gain_to_split);  // learner.rs:3985
     T.threshold_in_bin[node] = thr;
@@ -474,7 +493,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     const int4 pk = s_pick[j];
     const int32_t p = pk.y, cl = pk.z, cr = pk.w, fpos = s_fpos[p];
     const lgbm_split_info b = L.feat_split[(size_t)p * F + fpos];
-    const DevFeature& ft = s_ft[fpos];
+    const DevFeature ft = fts[fpos];
     PartJob J;
     J.parent = p;
     J.cl = cl;
@@ -535,7 +554,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     }
     ctl->tile_total = acc;
     ctl->n_jobs = nj;
-    if (fp) ctl->n_hjobs = nj;  // k_partition fills in each job's smaller child
+    if (fp || rec_wide(L.fmt)) ctl->n_hjobs = nj;  // k_partition fills in each job's side
     ctl->n_reduce = 2 * nj;
     ctl->num_leaves = nl;
     ctl->n_slots = s_nslots;
@@ -572,7 +591,12 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
 template <int FMT, int FP, bool STABLE>
 __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   constexpr int PT = PART_THREADS, PR = part_rows(FMT);
-  constexpr int U = rec_words(FMT), NS = rec_slots(FMT), BPW = rec_bpw(FMT);
+  constexpr int U = rec_words(FMT), BPW = rec_bpw(FMT);
+  constexpr int NS = rec_slots(FMT) > 0 ? rec_slots(FMT) : 1;
+  // wide records are row indices: the pass routes by one byte of the row's binmat row
+  // and builds no histogram (k_hist_wide builds the job's histogram side afterwards)
+  constexpr bool WIDE = rec_wide(FMT);
+  constexpr bool HIST = FP == 0 && !WIDE;
   // packed records carry the quantized pair in their last word (the original order's
   // pairs come from the quantizer's array)
   constexpr bool EMBED = rec_packed(FMT) && FP == 0;
@@ -601,7 +625,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   if (tid < SPEC_MAX) s_jobs[tid] = ctl->jobs[tid];
   if (nj <= 0 || t_lo >= t_hi) return;
   const int F = L.F, cells = L.total_cells, nw = (F + BPW - 1) / BPW;
-  if constexpr (FP == 0)
+  if constexpr (HIST)
     for (int c = tid; c < cells + LDS_TRASH_CELLS; c += PT) lds_hist[c] = 0ull;
   for (int f = tid; f < NS; f += PT) cb[f] = f < F ? (int32_t)L.feats[f].cell_base : cells;
   __syncthreads();
@@ -625,7 +649,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
                            FLUSH_STORE);
     } else {
       if (tid == 0) ctl->acc_used[cur] = 1;
-      lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * cells * 3, FLUSH_ATOMIC);
+      lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * L.acc_cells * 3, FLUSH_ATOMIC);
     }
   };
   struct TileBuf {
@@ -670,7 +694,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   // writes of each come after a barrier every reader has passed.  Histogram adds end
   // before B, so a flush at the top of the next tile sees them all.
   auto process = [&](int64_t t, int32_t j, TileBuf& B) {
-    if (FP == 0 && (j != cur || held == kFlushTiles)) {
+    if (HIST && (j != cur || held == kFlushTiles)) {
       if (cur >= 0 && s_jobs[cur].acc_right >= 0 && held > 0) {
         flush();
         flushed = j == cur;
@@ -694,9 +718,16 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     int32_t rank[PR];
     int fwi, fsh;
     rec_field_pos(FMT, J.fbyte, &fwi, &fsh);
+    int32_t wbin[PR];
+    if constexpr (WIDE) {
+      const uint8_t* __restrict__ col = L.binmat + J.fbyte;
+      const int64_t stride = L.row_stride;
+#pragma unroll
+      for (int k = 0; k < PR; ++k) wbin[k] = col[(int64_t)w[k][0] * stride];
+    }
 #pragma unroll
     for (int k = 0; k < PR; ++k) {
-      const int32_t bin = (int32_t)rec_field<FMT>(w[k], fwi, fsh);
+      const int32_t bin = WIDE ? wbin[k] : (int32_t)rec_field<FMT>(w[k], fwi, fsh);
       const bool left = (J.flags & ROUTE_CAT)
                             ? ((J.cat[bin >> 5] >> (bin & 31)) & 1u) != 0u
                             : !route_right(bin, J.pmin, J.max_bin, J.th, J.na_bin, J.flags);
@@ -728,13 +759,15 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
                                                  ((unsigned long long)(uint32_t)(trows - acc) << 32));
     }
     // histogram adds (every wave, wave 0 while its reservation is in flight)
-    if (FP == 0 && J.acc_right >= 0) {
-      const bool want_left = J.acc_right == 0;
+    if constexpr (HIST) {
+      if (J.acc_right >= 0) {
+        const bool want_left = J.acc_right == 0;
 #pragma unroll
-      for (int k = 0; k < PR; ++k)
-        if (valid[k] && isleft[k] == want_left && gh_bits(q[k]) != 0u)
-          lds_hist_add<FMT>(lds_hist, cbr, nw, F, cells + 4 + lane, w[k], gh_bits(q[k]));
-      ++held;
+        for (int k = 0; k < PR; ++k)
+          if (valid[k] && isleft[k] == want_left && gh_bits(q[k]) != 0u)
+            lds_hist_add<FMT>(lds_hist, cbr, nw, F, cells + 4 + lane, w[k], gh_bits(q[k]));
+        ++held;
+      }
     }
     if (wave == 0 && lane == 0) {
       int64_t lb, rb;
@@ -795,18 +828,20 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
         const int32_t sw = (J.flags & ROUTE_CAT) && (((J.flags >> 8) & 1) != (lc < rc ? 1 : 0));
         nd.sums[J.cl]._pad = sw;
         nd.sums[J.cr]._pad = sw;
-        if (FP) {
-          // the round's ConstructHistogram job (k_hist_f32 runs next): the smaller
-          // child (partition counts; a tie makes the right child the smaller one,
-          // learner.rs:4061-4089), none for a gated pair (before_find_best_split,
-          // learner.rs:1808-1839)
+        if (FP || WIDE) {
+          // the round's ConstructHistogram job (k_hist_f32 / k_hist_wide run next):
+          // f32, the smaller child (partition counts; a tie makes the right child the
+          // smaller one, learner.rs:4061-4089); quantized, the side the scan predicted
+          // smaller (the other is parent - built in integers); none for a gated pair
+          // (before_find_best_split, learner.rs:1808-1839)
           const int32_t md = ctl->max_depth, min2 = ctl->cfg.min_data_in_leaf * 2;
           const bool gated = (md > 0 && nd.depth[J.cl] >= md) || (lc < min2 && rc < min2);
+          const bool right = FP ? !(lc < rc) : J.acc_right == 1;
           HistJob hj;
           hj.buf = J.dst_buf;
           hj._pad = 0;
-          hj.begin = lc < rc ? begin : begin + lc;
-          hj.count = gated ? 0 : (lc < rc ? lc : rc);
+          hj.begin = right ? begin + lc : begin;
+          hj.count = gated ? 0 : (right ? rc : lc);
           hj.a0 = 0;
           hj.nblk = 0;
           ctl->hjobs[j] = hj;
@@ -814,7 +849,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
         atomicAdd(&L.stats[0], (double)count);
         atomicAdd(&L.stats[4], 1.0);
         // rows whose histogram this pass built (the side predicted smaller)
-        if (!FP && J.acc_right >= 0) atomicAdd(&L.stats[5], (double)(J.acc_right ? rc : lc));
+        if (HIST && J.acc_right >= 0) atomicAdd(&L.stats[5], (double)(J.acc_right ? rc : lc));
       } else {
         ctl->part_left_count = lc;
       }
@@ -835,7 +870,7 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
       jc = jn;
     }
   }
-  if (FP == 0 && cur >= 0 && s_jobs[cur].acc_right >= 0 && held > 0) flush();
+  if (HIST && cur >= 0 && s_jobs[cur].acc_right >= 0 && held > 0) flush();
 }
 
 // Stable per-op partition, step 1: the left-row count of every tile of job 0.
@@ -955,16 +990,26 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
   const bool right_small = !(lcnt < rcnt);
   const int32_t sm = right_small ? cr : cl, lg = right_small ? cl : cr;
   const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
+  const bool wide = rec_wide(L.fmt);
   if (fp_mode) {
-    // f32 gradients: the smaller child from its k_hist_f32 partial slots; the larger =
-    // parent - smaller, exact in 64-bit fixed point
+    // f32 gradients: the smaller child from its k_hist_f32 partial slots (wide: its
+    // accumulator, read and cleared); the larger = parent - smaller, exact in 64-bit
+    // fixed point
     const int32_t a0 = ctl->hjobs[j].a0, na = ctl->hjobs[j].nblk;
     const double gu = ldexp(1.0, -ctl->g_shift), hu = ldexp(1.0, -ctl->h_shift);
+    int64_t* acc64 = L.hist_acc64 + (size_t)j * L.acc_cells * 2;
     if (!gated) {
       for (int b = tid; b < nb; b += SCAN_THREADS) {
         const size_t ci = (size_t)(ft.cell_base + b);
         long long SG, SH;
-        hist_part_sum64(L, a0, na, ci, &SG, &SH);
+        if (wide) {
+          SG = acc64[2 * ci];
+          SH = acc64[2 * ci + 1];
+          acc64[2 * ci] = 0;
+          acc64[2 * ci + 1] = 0;
+        } else {
+          hist_part_sum64(L, a0, na, ci, &SG, &SH);
+        }
         const int64_t* ps = L.int_slots64 + ((size_t)p * cells + ci) * 2;
         int64_t* ss = L.int_slots64 + ((size_t)sm * cells + ci) * 2;
         int64_t* gs_ = L.int_slots64 + ((size_t)lg * cells + ci) * 2;
@@ -982,11 +1027,13 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
     // first tile to the one holding its last, slot = block + j; blocks without tiles
     // wrote nothing), plus the job's accumulator when a flush used it (read and
     // cleared even when the children are gated)
+    // (wide: k_hist_wide's accumulator)
     const int64_t s0 = jnt > 0 ? part_owner(jt0, T, part_grid) : 0;
     const int64_t s1 = jnt > 0 ? part_owner(jt0 + jnt - 1, T, part_grid) : -1;
-    const bool use_slots = jnt > 0 ? part_span_blocks(jt0, jnt, T, part_grid) <= PART_SLOT_MAX : true;
+    const bool use_slots =
+        !wide && (jnt > 0 ? part_span_blocks(jt0, jnt, T, part_grid) <= PART_SLOT_MAX : true);
     const bool read_acc = !use_slots || acc_used != 0;
-    int32_t* acc = L.hist_acc + (size_t)j * cells * 3;
+    int32_t* acc = L.hist_acc + (size_t)j * L.acc_cells * 3;
     const unsigned long long* slots = L.part_slots;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -1249,7 +1296,12 @@ void launch_partition(const DevLearner& L, int fp, int64_t blocks, hipStream_t s
                       const KernelEvents* ev) {
   if (blocks < 1) blocks = 1;
   const dim3 g((unsigned)blocks), b(PART_THREADS);
-  if (fp) {
+  if (rec_wide(L.fmt)) {
+    if (fp)
+      KLAUNCH(ev, (k_partition<REC_FMT_WIDE, 1, false>), g, b, 0, s, L);
+    else
+      KLAUNCH(ev, (k_partition<REC_FMT_WIDE, 0, false>), g, b, 0, s, L);
+  } else if (fp) {
     DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_partition<kF, 1, false>), g, b, 0, s, L));
   } else {
     const size_t lds = (size_t)(std::max(L.total_cells, 1) + LDS_TRASH_CELLS) * sizeof(unsigned long long);

@@ -113,7 +113,11 @@ struct DevLearner {
   uint64_t slot_len;
   int32_t* hist_part;         // [HIST_SLOTS][total_cells][3] root / per-op partials
   int32_t* hist_sum;          // [total_cells][3] job 0's partials summed (k_hist_reduce)
-  int32_t* hist_acc;          // [SPEC_MAX][total_cells][3] per-job accumulators
+  int32_t* hist_acc;          // [SPEC_MAX][acc_cells][3] per-job accumulators
+  int64_t* hist_acc64;        // wide layout, f32 gradients: [SPEC_MAX][acc_cells][2]
+  int32_t acc_cells;          // cells per accumulator: total_cells, + 1 (row totals) when wide
+  const uint8_t* binmat;      // wide layout: row-major bins [N][row_stride]
+  int64_t row_stride;
   unsigned long long* part_slots;  // [part blocks + SPEC_MAX][total_cells] packed (block, job) cells
   // f32-gradient training: 64-bit fixed-point (g, h) cells
   int64_t* hist_part64;       // [HIST_SLOTS][total_cells][2]
@@ -167,7 +171,8 @@ struct DevBinFeature {
   int32_t nan_bin;      // numerical: the NaN bin (num_bin-1) when missing_type is NaN, else -1
   int32_t off;          // offset into ub (numerical) or cats (categorical)
   int32_t ncat;         // categorical: number of (category, bin) pairs, sorted by category
-  int32_t _pad[3];
+  int32_t ub_pos;       // first of the feature's entries in the bounds array (any type)
+  int32_t _pad[2];
 };
 // Bins a dense raw matrix (f32 or f64; row-major [n][F] or column-major [F][n]) into
 // the resident records; `ub_count` upper bounds are staged in LDS.
@@ -219,5 +224,18 @@ void launch_gather_rows(int fmt, const uint32_t* rows, int64_t n, const uint4* r
                         const uint16_t* gh, const float2* g32, uint4* rec_out, uint16_t* gh_out,
                         float2* g32_out, hipStream_t s);
 void launch_subtract(const double* a, const double* b, int64_t n, double* out, hipStream_t s);
+// wide layout (REC_FMT_WIDE): feature-major u8 bins [F][n] -> the row-major matrix
+// [n][stride] (padding bytes zero) and the identity row-index records
+void launch_pack_wide(const uint8_t* bins, int64_t n, int32_t F, int64_t stride, uint8_t* binmat,
+                      uint4* rec, hipStream_t s);
+// Opts the wide histogram kernels into their LDS size (outside graph capture); 0 = ok.
+int wide_prepare();
+// ConstructHistogram of the launch's histogram jobs into the per-job accumulators
+void launch_hist_wide(const DevLearner& L, int fp, hipStream_t s, const KernelEvents* ev = nullptr);
+// raw values -> the row-major matrix (ValueToBin per feature group, bounds in LDS)
+void launch_bin_wide(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
+                     int64_t stride, const DevBinFeature* feats, const double* ub,
+                     const int2* cats, uint8_t* binmat, uint4* rec, hipStream_t s,
+                     const KernelEvents* ev);
 void launch_pack_partition(const uint32_t* bins, int64_t n, uint4* rec, hipStream_t s);
 }  // namespace lgbm

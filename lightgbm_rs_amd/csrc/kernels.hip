@@ -713,7 +713,9 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_f32(DevLearner L) {
 //                   (exact, from the integer totals), FixHistogram, compaction, and
 //                   the root's FindBestThreshold (wave 0).
 //   mode 2 (build): per-op build into `explicit_out` (no scan).
-// The integer cells are the sum of histogram job 0's partial slots.
+// The integer cells are the sum of histogram job 0's partial slots; in the wide layout
+// job 0's accumulator (read and cleared), whose totals cell holds the root sums (its
+// most-frequent-bin cells are not accumulated).
 // ===========================================================================
 __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t mode,
                                                           double* __restrict__ explicit_out) {
@@ -729,12 +731,20 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
   long long tg = 0, th = 0, t3 = 0;
   const int32_t a0 = ctl->hjobs[0].a0, na = ctl->hjobs[0].nblk;
   const bool fp = ctl->fp_mode != 0;
+  const bool wide = rec_wide(L.fmt);
   const double gu = ldexp(1.0, -ctl->g_shift), hu = ldexp(1.0, -ctl->h_shift);
   for (int b = tid; b < nb; b += SCAN_THREADS) {
     const size_t ci = (size_t)(ft.cell_base + b);
     if (fp) {
       long long G = 0, H = 0;
-      hist_part_sum64(L, a0, na, ci, &G, &H);
+      if (wide) {
+        G = L.hist_acc64[2 * ci];
+        H = L.hist_acc64[2 * ci + 1];
+        L.hist_acc64[2 * ci] = 0;
+        L.hist_acc64[2 * ci + 1] = 0;
+      } else {
+        hist_part_sum64(L, a0, na, ci, &G, &H);
+      }
       if (mode == 1) {
         int64_t* ps = L.int_slots64 + ci * 2;  // node slot 0
         ps[0] = G;
@@ -746,7 +756,13 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
       th += H;
       continue;
     }
-    const int32_t G = L.hist_sum[ci * 3], H = L.hist_sum[ci * 3 + 1], T = L.hist_sum[ci * 3 + 2];
+    int32_t* hs = (wide ? L.hist_acc : L.hist_sum) + ci * 3;
+    const int32_t G = hs[0], H = hs[1], T = hs[2];
+    if (wide) {
+      hs[0] = 0;
+      hs[1] = 0;
+      hs[2] = 0;
+    }
     if (mode == 1) {
       int32_t* ps = L.int_slots + ci * 3;  // node slot 0
       ps[0] = G;
@@ -780,6 +796,17 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
       G += tot[0][w];
       H += tot[1][w];
       T += tot[2][w];
+    }
+    if (wide) {  // the totals cell (job 0, cell total_cells)
+      const size_t t = (size_t)L.total_cells;
+      if (fp) {
+        G = L.hist_acc64[2 * t];
+        H = L.hist_acc64[2 * t + 1];
+      } else {
+        G = L.hist_acc[3 * t];
+        H = L.hist_acc[3 * t + 1];
+        T = L.hist_acc[3 * t + 2];
+      }
     }
     if (fp) {
       sg = (double)G * gu;
@@ -859,7 +886,8 @@ __global__ __launch_bounds__(LGBM_WAVE) void k_scan_explicit(const double* __res
 // (equivalent to AddPredictionToScore over the partition, learner.rs:4380-4395),
 // adding the shrunk leaf value (Tree::shrinkage, tree.rs:1074).  A thread stages its
 // record in LDS and walks the tree with one byte read and one route-mask word per
-// level (k_tree_finalize precomputes, per node, the set of bins routed right).
+// level (k_tree_finalize precomputes, per node, the set of bins routed right).  The
+// wide layout reads each level's byte from the row's binmat row instead.
 // ===========================================================================
 template <int FMT, bool LEAF_OF>
 __global__ __launch_bounds__(256) void k_walk(DevLearner L, double lr, double* __restrict__ score,
@@ -868,8 +896,10 @@ __global__ __launch_bounds__(256) void k_walk(DevLearner L, double lr, double* _
   constexpr uint32_t BM = (1u << BB) - 1u;
   constexpr int kStride = U + 1;  // words per staged record: odd (U is even), so word
                                   // reads of different lanes hit different banks
+  constexpr bool WIDE = rec_wide(FMT);
   __shared__ uint32_t s_mask[(MAX_LEAVES - 1) * 8];
   __shared__ uint32_t s_node[MAX_LEAVES - 1];
+  __shared__ int32_t s_wf[WIDE ? MAX_LEAVES - 1 : 1];  // wide: node -> feature position
   __shared__ double vals[MAX_LEAVES];
   __shared__ uint32_t s_rec[256 * kStride];
   const int32_t nl = L.ctl->num_leaves;
@@ -877,6 +907,8 @@ __global__ __launch_bounds__(256) void k_walk(DevLearner L, double lr, double* _
   const int tid = threadIdx.x;
   for (int i = tid; i < (nl - 1) * 8; i += blockDim.x) s_mask[i] = L.tree.route_mask[i];
   for (int i = tid; i < nl - 1; i += blockDim.x) s_node[i] = L.tree.route_node[i];
+  if constexpr (WIDE)
+    for (int i = tid; i < nl - 1; i += blockDim.x) s_wf[i] = L.tree.nodes[i].f;
   if (!LEAF_OF)
     for (int i = tid; i < nl; i += blockDim.x)
       vals[i] = maybe_round_to_zero(L.tree.leaf_value[i] * lr);
@@ -884,17 +916,26 @@ __global__ __launch_bounds__(256) void k_walk(DevLearner L, double lr, double* _
   const uint4* __restrict__ rec = L.bufs.rec[BUF_ORIG];
   uint32_t* mine = s_rec + tid * kStride;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const uint8_t* __restrict__ bm = L.binmat;
+  const int64_t rstride = L.row_stride;
   for (int64_t r = (int64_t)blockIdx.x * blockDim.x + tid; r < L.N; r += stride) {
-    uint32_t w[U];
-    rec_load<FMT>(rec, r, w);
+    if constexpr (!WIDE) {
+      uint32_t w[U];
+      rec_load<FMT>(rec, r, w);
 #pragma unroll
-    for (int i = 0; i < U; ++i) mine[i] = w[i];
+      for (int i = 0; i < U; ++i) mine[i] = w[i];
+    }
     int32_t node = 0;
     for (int depth = 0; depth < nl && node >= 0; ++depth) {  // a path has < nl nodes
       const uint32_t u = s_node[node];
-      const uint32_t f = u & 0xffu;
-      const uint32_t wi = f / BPW;
-      const uint32_t bin = (mine[wi] >> (BB * (f - wi * BPW))) & BM;
+      uint32_t bin;
+      if constexpr (WIDE) {
+        bin = bm[r * rstride + s_wf[node]];
+      } else {
+        const uint32_t f = u & 0xffu;
+        const uint32_t wi = f / BPW;
+        bin = (mine[wi] >> (BB * (f - wi * BPW))) & BM;
+      }
       const uint32_t right = (s_mask[node * 8 + (bin >> 5)] >> (bin & 31u)) & 1u;
       node = right ? ((int32_t)u >> 20) : ((int32_t)(u << 12) >> 20);
     }
@@ -1012,7 +1053,8 @@ void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hip
   // quantized: the partial slots summed into hist_sum first (f32 cells are summed by
   // k_fixscan itself); f32 mode never reads hist_sum, so the launch is harmless
   const int64_t cols = (int64_t)L.total_cells * 3;
-  k_hist_reduce<<<dim3((unsigned)((cols + 15) / 16)), dim3(256), 0, s>>>(L);
+  if (!rec_wide(L.fmt))
+    k_hist_reduce<<<dim3((unsigned)((cols + 15) / 16)), dim3(256), 0, s>>>(L);
   KLAUNCH(ev, k_fixscan, dim3((unsigned)L.F), dim3(SCAN_THREADS), 0, s, L, mode, explicit_out);
 }
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
@@ -1025,14 +1067,22 @@ void launch_score_update(const DevLearner& L, double lr, double* score, hipStrea
                          const KernelEvents* ev) {
   int64_t blocks = std::min<int64_t>((L.N + 255) / 256, 2048);
   if (blocks < 1) blocks = 1;
-  DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_walk<kF, false>), dim3((unsigned)blocks), dim3(256), 0, s, L,
-                              lr, score, (uint8_t*)nullptr));
+  if (rec_wide(L.fmt))
+    KLAUNCH(ev, (k_walk<REC_FMT_WIDE, false>), dim3((unsigned)blocks), dim3(256), 0, s, L, lr,
+            score, (uint8_t*)nullptr);
+  else
+    DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_walk<kF, false>), dim3((unsigned)blocks), dim3(256), 0, s, L,
+                                lr, score, (uint8_t*)nullptr));
 }
 void launch_leaf_of(const DevLearner& L, uint8_t* leaf_of, hipStream_t s) {
   int64_t blocks = std::min<int64_t>((L.N + 255) / 256, 2048);
   if (blocks < 1) blocks = 1;
-  DISPATCH_FMT(L.fmt, (k_walk<kF, true><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
-                          L, 0.0, (double*)nullptr, leaf_of)));
+  if (rec_wide(L.fmt))
+    k_walk<REC_FMT_WIDE, true><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(L, 0.0, (double*)nullptr,
+                                                                           leaf_of);
+  else
+    DISPATCH_FMT(L.fmt, (k_walk<kF, true><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+                            L, 0.0, (double*)nullptr, leaf_of)));
 }
 void launch_gather_rows(int fmt, const uint32_t* rows, int64_t n, const uint4* rec, const uint16_t* gh,
                         const float2* g32, uint4* rec_out, uint16_t* gh_out, float2* g32_out,

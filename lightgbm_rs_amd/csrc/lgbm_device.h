@@ -24,6 +24,16 @@
 #define HIST_BLOCK_MAX_ROWS ((1 << 19) - 1)  // block-shared scheme field limit
 #define HIST_FP_CELLS 3584              // f32 gradients: cells per feature group (16 B each)
 #define MAX_FGROUPS 32
+// wide layout (REC_FMT_WIDE): ConstructHistogram per (row chunk, feature group); a
+// group is WIDE_GF_Q (quantized, 8-byte LDS cells) or WIDE_GF_F (f32, two 8-byte
+// cells) consecutive features, at most 256 bins each: 128 KiB of LDS either way
+#define WIDE_GF_Q 64
+#define WIDE_GF_F 32
+#define WIDE_THREADS 1024
+#define WIDE_GRID 1024                  // row-chunk blocks over all groups (at least)
+#define WIDE_MIN_ROWS 16384             // rows per chunk (at least): a flush costs a group
+#define WIDE_MAX_ROWS ((1 << 19) - 1)   // packed LDS cell field limit (quantized)
+#define WIDE_MAX_F 4096
 #ifndef PART_THREADS
 #define PART_THREADS 512                // partition block (two per CU)
 #endif
@@ -66,10 +76,18 @@
 //   16 + U (U even, 2..8): U u32 = 4U bytes; five 6-bit bins per u32 (bits 0-29;
 //          every num_bin <= 64), the quantized pair in bits 24-29 of the last u32
 //          (which holds at most four bins: F <= 5U - 1); no row index.
+//   32     (wide): the record is the row's original index (one u32); the bins stay
+//          in a row-major matrix binmat[N][Fp] (u8, Fp = F rounded up to WIDE_GF_Q)
+//          that is never moved.  For many features, where moving every bin at every
+//          split would cost 2 F bytes per row.
 #define REC_FMT_PACKED 16
-__host__ __device__ constexpr bool rec_packed(int fmt) { return fmt > REC_FMT_PACKED; }
+#define REC_FMT_WIDE 32
+__host__ __device__ constexpr bool rec_wide(int fmt) { return fmt == REC_FMT_WIDE; }
+__host__ __device__ constexpr bool rec_packed(int fmt) {
+  return fmt > REC_FMT_PACKED && fmt < REC_FMT_WIDE;
+}
 __host__ __device__ constexpr int rec_words(int fmt) {  // u32 per record
-  return rec_packed(fmt) ? fmt - REC_FMT_PACKED : 4 * fmt;
+  return rec_wide(fmt) ? 1 : rec_packed(fmt) ? fmt - REC_FMT_PACKED : 4 * fmt;
 }
 __host__ __device__ constexpr int rec_bytes(int fmt) { return 4 * rec_words(fmt); }
 __host__ __device__ constexpr int rec_bpw(int fmt) { return rec_packed(fmt) ? 5 : 4; }
@@ -78,7 +96,7 @@ __host__ __device__ constexpr int rec_bits(int fmt) { return rec_packed(fmt) ? 6
 // the last feature read zero bins into a trash cell): legacy 4 per u32 but none in
 // the row-index u32; packed 5 per u32 but 4 in the last (its top bits hold the pair)
 __host__ __device__ constexpr int rec_slots(int fmt) {
-  return rec_packed(fmt) ? 5 * rec_words(fmt) - 1 : 4 * (rec_words(fmt) - 1);
+  return rec_wide(fmt) ? 0 : rec_packed(fmt) ? 5 * rec_words(fmt) - 1 : 4 * (rec_words(fmt) - 1);
 }
 // word and bit offset of feature f's bin in a record
 __host__ __device__ inline void rec_field_pos(int fmt, int f, int* wi, int* sh) {

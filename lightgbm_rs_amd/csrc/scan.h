@@ -33,7 +33,9 @@ template <int FMT>
 __device__ __forceinline__ void rec_load(const uint4* __restrict__ base, int64_t r,
                                          uint32_t (&w)[rec_words(FMT)]) {
   constexpr int U = rec_words(FMT);
-  if constexpr (U % 4 == 0) {
+  if constexpr (U == 1) {
+    w[0] = ((const uint32_t*)base)[r];
+  } else if constexpr (U % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < U / 4; ++i) {
       const uint4 q = base[r * (U / 4) + i];
@@ -56,7 +58,9 @@ template <int FMT>
 __device__ __forceinline__ void rec_store(uint4* __restrict__ base, int64_t r,
                                           const uint32_t (&w)[rec_words(FMT)]) {
   constexpr int U = rec_words(FMT);
-  if constexpr (U % 4 == 0) {
+  if constexpr (U == 1) {
+    ((uint32_t*)base)[r] = w[0];
+  } else if constexpr (U % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < U / 4; ++i)
       base[r * (U / 4) + i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);

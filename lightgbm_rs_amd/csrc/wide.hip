@@ -1,0 +1,287 @@
+// wide.hip — the wide row layout (REC_FMT_WIDE) for hundreds to thousands of features.
+//
+// The record layouts move every row's bins at every split, 2 F bytes per row and
+// level; at F = 700 or 2000 that traffic dwarfs the histogram reads.  Here the bins
+// stay in one row-major matrix binmat[N][Fp] (u8, Fp = F rounded up to WIDE_GF_Q,
+// padding bytes 0) that is never moved; the partition moves the 4-byte row index and
+// the row's gradient pair, and routes by one byte gathered from binmat.
+//
+// ConstructHistogram (build_histograms_into, crates/lgbm-compute/src/lib.rs:262-390:
+// per feature, the leaf's rows folded into their bins) cannot hold a leaf's cells in
+// LDS at this width (F x num_bin, up to 512k cells), so a block owns one group of
+// consecutive features (WIDE_GF_Q = 64 with quantized pairs in packed 8-byte cells,
+// WIDE_GF_F = 32 with 64-bit fixed-point (g, h) cells: 128 KiB of LDS either way)
+// and a contiguous chunk of one job's rows.  Each thread takes a row at a time: its
+// index, its pair, and the group's bytes of its binmat row in 16-byte loads; then one
+// LDS atomic per (row, feature).  The block's cells go to the job's accumulator with
+// global atomic adds (zero cells skipped); the reader (k_fixscan for the root,
+// k_pair_scan for the children) clears them.
+//
+// The most frequent bin of a feature is never accumulated.  The scans never read
+// that cell's own sum: FixHistogram (fix_histogram.rs:50-80) overwrites it with the
+// leaf sum minus the other bins when most_freq_bin > 0, and compaction drops bin 0
+// when most_freq_bin == 0 (offset 1, lgbm-treelearner/src/lib.rs:89-95).  Every
+// node's integer cell at that bin is then 0 (0 - 0 in the subtraction), and the f64
+// cells the scans see are the reference's.  Sparse columns (most rows in one bin)
+// thus cost one byte read per row but almost no atomics.  The root's sums, which
+// the record layouts take from any feature's cells, come from a totals cell (index
+// total_cells of the accumulator) that feature group 0's blocks fill for the root job.
+#include "scan.h"
+
+namespace lgbm {
+
+namespace {
+
+// Rows per chunk R and the first chunk of every job: jobs get ceil(count / R) chunks,
+// R = the launch's rows / `chunks` (at least WIDE_MIN_ROWS); the host sizes `chunks`
+// so that R <= WIDE_MAX_ROWS, and launches chunks + SPEC_MAX blocks per group.
+__device__ __forceinline__ void wide_assign(const Ctl* ctl, int32_t nj, int32_t* s_a0,
+                                            int32_t* s_nb, int64_t* s_R, int64_t chunks) {
+  int64_t S = 0;
+  for (int j = 0; j < nj; ++j) S += max(ctl->hjobs[j].count, (int64_t)0);
+  int64_t R = (S + chunks - 1) / chunks;
+  if (R < WIDE_MIN_ROWS) R = WIDE_MIN_ROWS;
+  int32_t acc = 0;
+  for (int j = 0; j < nj; ++j) {
+    const int64_t c = ctl->hjobs[j].count;
+    const int32_t nb = c > 0 ? (int32_t)((c + R - 1) / R) : 0;
+    s_a0[j] = acc;
+    s_nb[j] = nb;
+    acc += nb;
+  }
+  *s_R = R;
+}
+
+template <int FP>
+__global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
+  constexpr int GF = FP ? WIDE_GF_F : WIDE_GF_Q;
+  constexpr int NV = GF / 16;      // 16-byte words of a row's group bytes
+  constexpr int RU = FP ? 4 : 2;   // rows per thread in flight
+  constexpr int NW = WIDE_THREADS / LGBM_WAVE;
+  extern __shared__ unsigned long long lds[];
+  __shared__ uint32_t s_fd[GF];    // per feature: (first cell - group base) << 8 | mfb
+  __shared__ int32_t s_a0[SPEC_MAX], s_nb[SPEC_MAX];
+  __shared__ int64_t s_R;
+  __shared__ long long s_tot[3][NW];
+  Ctl* ctl = L.ctl;
+  const int32_t nj = ctl->n_hjobs;
+  if (nj <= 0) return;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int F = L.F, cells = L.total_cells;
+  const int f0 = (int)blockIdx.y * GF;
+  if (f0 >= F) return;
+  if (tid == 0) wide_assign(ctl, nj, s_a0, s_nb, &s_R, (int64_t)gridDim.x - SPEC_MAX);
+  __syncthreads();
+  const int32_t a = (int32_t)blockIdx.x;
+  int32_t j = -1;
+  for (int k = 0; k < nj; ++k)
+    if (a >= s_a0[k] && a < s_a0[k] + s_nb[k]) j = k;
+  if (j < 0) return;
+  const int f1 = min(f0 + GF, F);
+  const int gbase = (int)L.feats[f0].cell_base;
+  const int gcells = (f1 < F ? (int)L.feats[f1].cell_base : cells) - gbase;
+  for (int k = tid; k < GF; k += WIDE_THREADS) {
+    uint32_t d = 0u;  // padding bytes: bin 0 == "mfb" 0, never added
+    if (f0 + k < F) {
+      const DevFeature& ft = L.feats[f0 + k];
+      d = ((ft.cell_base - (uint32_t)gbase) << 8) | (ft.mfb & 0xffu);
+    }
+    s_fd[k] = d;
+  }
+  for (int c = tid; c < gcells * (FP ? 2 : 1); c += WIDE_THREADS) lds[c] = 0ull;
+  __syncthreads();
+
+  const HistJob& J = ctl->hjobs[j];
+  const int64_t R = s_R;
+  const int64_t lo = (int64_t)(a - s_a0[j]) * R;
+  const int64_t hi = min(J.count, lo + R);
+  const int64_t jb = J.begin;
+  const bool orig = J.buf == BUF_ORIG;
+  const uint32_t* __restrict__ rows = (const uint32_t*)rec_buf(L.bufs, J.buf) + jb;
+  const uint8_t* __restrict__ bm = L.binmat + f0;
+  const int64_t stride = L.row_stride;
+  const bool totals = (J._pad & 1) != 0 && blockIdx.y == 0;
+  const uint16_t* __restrict__ ghq = L.bufs.gh[0];
+  const float2* __restrict__ gh32 = L.bufs.g32[0];
+  if constexpr (FP)
+    gh32 = buf_sel(L.bufs.g32, J.buf) + jb;
+  else
+    ghq = buf_sel(L.bufs.gh, J.buf) + jb;
+  const double gm = FP ? ldexp(1.0, ctl->g_shift) : 0.0, hm = FP ? ldexp(1.0, ctl->h_shift) : 0.0;
+  long long tg = 0, th = 0, t3 = 0;
+  for (int64_t b0 = lo; b0 < hi; b0 += (int64_t)WIDE_THREADS * RU) {
+    int64_t row[RU];
+    bool ok[RU];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const int64_t r = b0 + (int64_t)u * WIDE_THREADS + tid;
+      ok[u] = r < hi;
+      const int64_t rr = ok[u] ? r : lo;  // in-range stand-in, adds nothing
+      row[u] = rr;
+    }
+    uint4 w[RU][NV];
+    unsigned long long va[RU], vb[RU];  // quantized: packed cell add; f32: g, h fixed point
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const int64_t src_row = orig ? jb + row[u] : (int64_t)rows[row[u]];
+      const uint4* src = (const uint4*)(bm + src_row * stride);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) w[u][i] = src[i];
+      if constexpr (FP) {
+        const float2 v = gh32[row[u]];
+        const long long gi = (long long)rint((double)v.x * gm);
+        const long long hi_ = (long long)rint((double)v.y * hm);
+        va[u] = ok[u] ? (unsigned long long)gi : 0ull;
+        vb[u] = ok[u] ? (unsigned long long)hi_ : 0ull;
+        tg += (long long)va[u];
+        th += (long long)vb[u];
+      } else {
+        const uint32_t q = ok[u] ? (uint32_t)ghq[row[u]] : 0u;
+        const int32_t qg = (int32_t)(int8_t)(q & 0xffu);
+        const int32_t qh = (int32_t)(int8_t)(q >> 8);
+        va[u] = q == 0u ? 0ull
+                        : (unsigned long long)(long long)qg + ((unsigned long long)(uint32_t)qh << 22) +
+                              ((unsigned long long)(qh == 3 ? 1u : 0u) << 43);
+        tg += qg;
+        th += qh;
+        t3 += qh == 3 ? 1 : 0;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      uint32_t fd[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) fd[k] = __builtin_amdgcn_readfirstlane(s_fd[16 * i + k]);
+#pragma unroll
+      for (int u = 0; u < RU; ++u) {
+        const bool live = FP ? ok[u] : va[u] != 0ull;
+        if (!live) continue;
+        const uint32_t word[4] = {w[u][i].x, w[u][i].y, w[u][i].z, w[u][i].w};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const uint32_t bin = (word[k >> 2] >> (8 * (k & 3))) & 0xffu;
+          if (bin != (fd[k] & 0xffu)) {
+            const int c = (int)(fd[k] >> 8) + (int)bin;
+            if constexpr (FP) {
+              __hip_atomic_fetch_add(&lds[2 * c], va[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+              __hip_atomic_fetch_add(&lds[2 * c + 1], vb[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            } else {
+              __hip_atomic_fetch_add(&lds[c], va[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const size_t ac = (size_t)L.acc_cells;
+  if constexpr (FP) {
+    unsigned long long* acc = (unsigned long long*)L.hist_acc64 + ((size_t)j * ac + gbase) * 2;
+    for (int c = tid; c < gcells; c += WIDE_THREADS) {
+      const unsigned long long G = lds[2 * c], H = lds[2 * c + 1];
+      if (G) atomicAdd(&acc[2 * c], G);
+      if (H) atomicAdd(&acc[2 * c + 1], H);
+    }
+  } else {
+    int32_t* acc = L.hist_acc + ((size_t)j * ac + gbase) * 3;
+    for (int c = tid; c < gcells; c += WIDE_THREADS) {
+      const unsigned long long p = lds[c];
+      if (p == 0ull) continue;
+      int32_t g, h, t;
+      unpack_cell(p, &g, &h, &t);
+      if (g) atomicAdd(&acc[3 * c], g);
+      if (h) atomicAdd(&acc[3 * c + 1], h);
+      if (t) atomicAdd(&acc[3 * c + 2], t);
+    }
+  }
+  if (totals) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      tg += __shfl_xor(tg, off);
+      th += __shfl_xor(th, off);
+      t3 += __shfl_xor(t3, off);
+    }
+    if (lane_id() == 0) {
+      s_tot[0][wave] = tg;
+      s_tot[1][wave] = th;
+      s_tot[2][wave] = t3;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      long long G = 0, H = 0, T = 0;
+      for (int w = 0; w < NW; ++w) {
+        G += s_tot[0][w];
+        H += s_tot[1][w];
+        T += s_tot[2][w];
+      }
+      if constexpr (FP) {
+        unsigned long long* tc = (unsigned long long*)L.hist_acc64 + ((size_t)j * ac + cells) * 2;
+        atomicAdd(&tc[0], (unsigned long long)G);
+        atomicAdd(&tc[1], (unsigned long long)H);
+      } else {
+        int32_t* tc = L.hist_acc + ((size_t)j * ac + cells) * 3;
+        atomicAdd(&tc[0], (int32_t)G);
+        atomicAdd(&tc[1], (int32_t)H);
+        atomicAdd(&tc[2], (int32_t)T);
+      }
+    }
+  }
+}
+
+// Feature-major bins -> row-major matrix: thread = (16-feature word, row), rows
+// fastest (the byte reads of a wave are contiguous).
+__global__ void k_pack_wide(const uint8_t* __restrict__ bins, int64_t n, int32_t F, int64_t stride,
+                            uint8_t* __restrict__ binmat, uint32_t* __restrict__ rec) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t words = stride / 16;
+  if (i >= n * words) return;
+  const int64_t wd = i / n, r = i - wd * n;
+  uint32_t v[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t f = wd * 16 + k;
+    if (f < F) v[k >> 2] |= (uint32_t)bins[f * n + r] << (8 * (k & 3));
+  }
+  ((uint4*)(binmat + r * stride))[wd] = make_uint4(v[0], v[1], v[2], v[3]);
+  if (wd == 0) rec[r] = (uint32_t)r;
+}
+
+}  // namespace
+
+size_t wide_lds_bytes(int fp) {
+  return (size_t)(fp ? WIDE_GF_F * 256 * 16 : WIDE_GF_Q * 256 * 8);
+}
+
+// Opt the histogram kernels into their LDS size (outside any graph capture).
+int wide_prepare() {
+  if (hipFuncSetAttribute((const void*)k_hist_wide<0>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)wide_lds_bytes(0)) != hipSuccess)
+    return 1;
+  if (hipFuncSetAttribute((const void*)k_hist_wide<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)wide_lds_bytes(1)) != hipSuccess)
+    return 1;
+  return 0;
+}
+
+void launch_hist_wide(const DevLearner& L, int fp, hipStream_t s, const KernelEvents* ev) {
+  const int GF = fp ? WIDE_GF_F : WIDE_GF_Q;
+  const int ng = (L.F + GF - 1) / GF;
+  int64_t chunks = std::max<int64_t>(WIDE_GRID / ng, (L.N + WIDE_MAX_ROWS - 1) / WIDE_MAX_ROWS);
+  chunks = std::max<int64_t>(chunks, 1);
+  const dim3 g((unsigned)(chunks + SPEC_MAX), (unsigned)ng), blk(WIDE_THREADS);
+  if (fp)
+    KLAUNCH(ev, k_hist_wide<1>, g, blk, wide_lds_bytes(1), s, L);
+  else
+    KLAUNCH(ev, k_hist_wide<0>, g, blk, wide_lds_bytes(0), s, L);
+}
+
+void launch_pack_wide(const uint8_t* bins, int64_t n, int32_t F, int64_t stride, uint8_t* binmat,
+                      uint4* rec, hipStream_t s) {
+  const int64_t total = n * (stride / 16);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks < 1) return;
+  k_pack_wide<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(bins, n, F, stride, binmat,
+                                                          (uint32_t*)rec);
+}
+
+}  // namespace lgbm

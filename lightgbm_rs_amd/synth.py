@@ -191,3 +191,71 @@ def config3_binned(n, seed=0x5EED0003, max_bin=255, min_data_in_leaf=20, **kw):
                                  bin_type=m.bin_type))
         mappers.append(m)
     return bins, meta, np.array(vals, dtype=np.float64), y, cat, X, mappers
+
+
+def _bin_columns(X, max_bin, min_data_in_leaf=20):
+    """X [F, n] -> (bins u8 [F, n], feature meta, concatenated upper bounds, mappers)
+    with this library's BinMapper (find_bin_from_column's 200000-row sample)."""
+    from .backend import feature_meta
+    from .binning import BinMapper, sample_indices
+    F, n = X.shape
+    idx = sample_indices(n, 200000, 1)
+    bins = np.zeros((F, n), dtype=np.uint8)
+    meta, upper, mappers = [], [], []
+    for f in range(F):
+        m = BinMapper.from_sampled_column(X[f, idx].astype(np.float64), n, max_bin=max_bin,
+                                          min_data_in_leaf=min_data_in_leaf)
+        bins[f] = m.value_to_bin(X[f]).astype(np.uint8)
+        meta.append(feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f))
+        upper.extend(m.upper_bounds.tolist())
+        mappers.append(m)
+    return bins, meta, np.array(upper, dtype=np.float64), mappers
+
+
+def config2_raw_host(n, seed=0x5EED0002, F=2000, informative=50):
+    """configs[2]'s raw table: X float32 [F, n] with 90% exact zeros per feature and
+    LogNormal(0, 1) nonzeros; the L2 target = sum over `informative` random features of
+    x * U(-1, 1) + N(0, 0.5)."""
+    rng = np.random.default_rng(seed)
+    X = np.zeros((F, n), dtype=np.float32)
+    for f in range(F):
+        nz = rng.random(n) < 0.1
+        X[f, nz] = np.exp(rng.standard_normal(int(nz.sum()))).astype(np.float32)
+    feats = rng.choice(F, size=informative, replace=False)
+    w = rng.uniform(-1.0, 1.0, informative)
+    y = (X[feats].astype(np.float64).T @ w + rng.normal(0.0, 0.5, n)).astype(np.float32)
+    return X, y
+
+
+def config2_binned(n, seed=0x5EED0002, F=2000, max_bin=255):
+    X, y = config2_raw_host(n, seed, F)
+    bins, meta, upper, _ = _bin_columns(X, max_bin)
+    return bins, meta, upper, y
+
+
+def config4_raw_host(n, seed=0x5EED0004, F=700, mean_group=120):
+    """configs[4]'s raw table: X float32 [F, n] ~U(0, 1) with 30% zeros, query groups of
+    Poisson(mean_group) sizes (at least 1; the last one cut at n), graded relevance 0-4
+    from the quintiles of a random linear score plus noise.  Returns (X, relevance
+    float32, group sizes int32)."""
+    rng = np.random.default_rng(seed)
+    X = rng.random((F, n), dtype=np.float32)
+    X[rng.random((F, n)) < 0.3] = 0.0
+    w = rng.standard_normal(F)
+    s = X.astype(np.float64).T @ w
+    s += rng.normal(0.0, float(np.std(s)) * 0.5 + 1e-12, n)
+    y = np.searchsorted(np.quantile(s, [0.2, 0.4, 0.6, 0.8]), s, side="right").astype(np.float32)
+    sizes = []
+    left = n
+    while left > 0:
+        k = max(1, int(rng.poisson(mean_group)))
+        k = min(k, left)
+        sizes.append(k)
+        left -= k
+    return X, y, np.array(sizes, dtype=np.int32)
+
+
+def config4_binned(n, seed=0x5EED0004, F=700, max_bin=255):
+    X, y, groups = config4_raw_host(n, seed, F)
+    bins, meta, upper, _ = _bin_columns(X, max_bin)
+    return bins, meta, upper, y, groups

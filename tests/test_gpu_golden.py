@@ -142,8 +142,8 @@ def test_failed_reupload_leaves_no_usable_state():
         b.upload_resident_grad_hess(g, h)
         b.discretize_dequantize_in_place(4, True, 1)
         b.grow_tree_on_device_with_cfg(cfg, 31, -1)  # captures the tree graph
-        # 130 features: more than a row record holds
-        wide, wmeta, wub = make_binned(1000, 130, seed=82, max_bin=16, missing_mix=False,
+        # 4097 features: more than any row layout holds (WIDE_MAX_F)
+        wide, wmeta, wub = make_binned(64, 4097, seed=82, max_bin=4, missing_mix=False,
                                        mfb_mix=False)
         with pytest.raises(HipError):
             b.upload_resident_bins(wide, wmeta, wub)
