@@ -22,7 +22,14 @@
 //   learner loop        lgbm-treelearner/src/learner.rs:980-2453,2708-3355,3895-4092
 //   Tree::split         lgbm-model/src/tree.rs:614-700, shrinkage :1074, add_bias :1161
 //   binary objective    lgbm-objective/src/binary.rs:134-220
-//   boosting loop       lgbm-boosting/src/gbdt.rs:612-640,691-1300 (binary spine)
+//   L2 regression       lgbm-objective/src/regression.rs:398-431,563-575
+//   lambdarank          lgbm-objective/src/rank.rs:100-390,
+//                       lgbm-metric/src/dcg_calculator.rs:40-170
+//   softmax multiclass  lgbm-objective/src/multiclass.rs:48-200
+//   Random / ColSampler lgbm-core/src/random.rs:37-123,
+//                       lgbm-treelearner/src/col_sampler.rs:68-203, learner.rs:1190-1240
+//   boosting loop       lgbm-boosting/src/gbdt.rs:612-640,691-1300,
+//                       lgbm-boosting/src/objective.rs:100-140 (ranking: no init score)
 //
 // Numeric conventions follow the Rust source: no FP contraction anywhere (build
 // with -ffp-contract=off) except the explicit fma in GetLeafGainGivenOutput
@@ -995,6 +1002,9 @@ struct Learner {
 
   // winning categorical bins per leaf (empty: the winner is numerical)
   std::vector<std::vector<uint32_t>> best_cat;
+  // the tree's ColSampler selection by feature position (is_feature_used_bytree,
+  // learner.rs:1932-1990): unselected features are never scanned; empty = all
+  std::vector<char> tree_used;
 
   bool is_cat(int f) const { return meta[f].bin_type == LGBM_BIN_CATEGORICAL; }
   bool skip_default_bin(int f) const {
@@ -1024,6 +1034,7 @@ struct Learner {
     std::vector<char> scanned(F, 0);
 #pragma omp parallel for schedule(dynamic, 1) if (F >= 16)
     for (int f = 0; f < F; ++f) {
+      if (!tree_used.empty() && !tree_used[f]) continue;
       if (parent_split && !(*parent_split)[f]) continue;
       if (is_cat(f))  // bin_type dispatch (learner.rs:3103-3118): the bumped sum_hessian
         find_best_threshold_categorical(buf + slot_off[f], lc, (int32_t)num_bin[f], meta[f].offset,
@@ -1353,6 +1364,251 @@ struct Multiclass {
   }
 };
 
+// ---------------------------------------------------------------------------
+// Random (lgbm-core/src/random.rs:37-123): LightGBM's LCG, x = 214013 x + 2531011.
+// ---------------------------------------------------------------------------
+struct LcgRandom {
+  uint32_t x;
+  explicit LcgRandom(int32_t seed) : x((uint32_t)seed) {}
+  int32_t rand_int16() {
+    x = x * 214013u + 2531011u;
+    return (int32_t)((x >> 16) & 0x7FFFu);
+  }
+  int32_t rand_int32() {
+    x = x * 214013u + 2531011u;
+    return (int32_t)(x & 0x7FFFFFFFu);
+  }
+  int32_t next_int(int32_t lo, int32_t hi) { return rand_int32() % (hi - lo) + lo; }
+  float next_float() { return (float)rand_int16() / 32768.0f; }
+  // Sample(N, K) (:87-123): K ordered values of 0..N-1; the streaming branch when
+  // K > N / log2(K) (f64), else the ordered-set branch.
+  std::vector<int32_t> sample(int32_t n, int32_t k) {
+    std::vector<int32_t> ret;
+    if (k > n || k <= 0) return ret;
+    if (k == n) {
+      for (int32_t i = 0; i < n; ++i) ret.push_back(i);
+    } else if (k > 1 && (double)k > ((double)n / std::log2((double)k))) {
+      for (int32_t i = 0; i < n; ++i) {
+        const double prob = (double)(k - (int32_t)ret.size()) / (double)(n - i);
+        if ((double)next_float() < prob) ret.push_back(i);
+      }
+    } else {
+      std::vector<char> in(n, 0);
+      for (int32_t r = n - k; r < n; ++r) {
+        const int32_t v = next_int(0, r + 1);
+        if (in[v])
+          in[r] = 1;
+        else
+          in[v] = 1;
+      }
+      for (int32_t i = 0; i < n; ++i)
+        if (in[i]) ret.push_back(i);
+    }
+    return ret;
+  }
+};
+
+// ColSampler (lgbm-treelearner/src/col_sampler.rs:68-203), no interaction
+// constraints: the Init draw at construction, then reset_by_tree once per tree
+// (learner.rs:1190-1225: tree t uses draw t + 2), get_by_node per node.
+struct ColSampler {
+  double frac_tree = 1.0, frac_node = 1.0;
+  LcgRandom rnd{0};
+  bool need_reset = false;
+  int32_t used_cnt = 0;
+  std::vector<int32_t> valid, used_idx;
+  std::vector<char> is_used;  // by real feature index
+  static int32_t get_cnt(size_t total, double fraction) {  // GetCnt (:80-84)
+    const int32_t mn = std::min<int32_t>(1, (int32_t)total);
+    const int32_t c = (int32_t)((double)total * fraction + (double)0.5f);
+    return std::max(c, mn);
+  }
+  void init(double ff, double ffn, int32_t seed, std::vector<int32_t> v, size_t nf) {
+    frac_tree = ff;
+    frac_node = ffn;
+    rnd = LcgRandom(seed);
+    need_reset = !(ff >= 1.0);
+    valid = std::move(v);
+    used_cnt = need_reset ? get_cnt(valid.size(), ff) : (int32_t)valid.size();
+    is_used.assign(nf, 1);
+    reset_by_tree();
+  }
+  void reset_by_tree() {  // (:119-135)
+    if (!need_reset) return;
+    std::fill(is_used.begin(), is_used.end(), 0);
+    used_idx = rnd.sample((int32_t)valid.size(), used_cnt);
+    for (int32_t pos : used_idx) is_used[(size_t)valid[(size_t)pos]] = 1;
+  }
+  std::vector<char> get_by_node() {  // (:150-185)
+    const size_t nf = is_used.size();
+    if (frac_node >= 1.0) return std::vector<char>(nf, 1);
+    std::vector<char> ret(nf, 0);
+    if (need_reset) {
+      const int32_t cnt = get_cnt(used_idx.size(), frac_node);
+      for (int32_t i : rnd.sample((int32_t)used_idx.size(), cnt))
+        ret[(size_t)valid[(size_t)used_idx[(size_t)i]]] = 1;
+    } else {
+      const int32_t cnt = get_cnt(valid.size(), frac_node);
+      for (int32_t i : rnd.sample((int32_t)valid.size(), cnt)) ret[(size_t)valid[(size_t)i]] = 1;
+    }
+    return ret;
+  }
+};
+
+// Objective::Regression (L2) get_gradients (lgbm-objective/src/regression.rs:427-431):
+// grad = f32(score - f64(label)), hess = 1.
+void l2_gradients(const double* score, const float* label, float* g, float* h, int64_t n) {
+#pragma omp parallel for schedule(static) if (n > 65536)
+  for (int64_t i = 0; i < n; ++i) {
+    g[i] = (float)(score[i] - (double)label[i]);
+    h[i] = 1.0f;
+  }
+}
+// boost_from_score (regression.rs:563-575): the ordered f64 label mean.
+double l2_boost_from_score(const float* label, int64_t n) {
+  if (n == 0) return 0.0;
+  double suml = 0.0;
+  for (int64_t i = 0; i < n; ++i) suml += (double)label[i];
+  return suml / (double)n;
+}
+
+// LambdaRank with NDCG (lgbm-objective/src/rank.rs:100-390) and its DCG tables
+// (lgbm-metric/src/dcg_calculator.rs:40-170): default label gain 2^i - 1 (31
+// entries), discount 1 / log2(2 + i) for i < 10000, per-query inverse max DCG at
+// the truncation level, the 2^20-bin sigmoid table.
+struct Lambdarank {
+  static constexpr int32_t kMaxPosition = 10000;
+  static constexpr int32_t kSigmoidBins = 1024 * 1024;
+  double sigmoid = 1.0;
+  bool norm = true;
+  int32_t trunc = 30;
+  std::vector<int32_t> qb;
+  std::vector<float> label;
+  std::vector<double> gain, discount, inv_max_dcg, table;
+  double min_in = 0, max_in = 0, idx_factor = 0;
+  int init(const float* labels, int64_t n, const int32_t* bounds, int32_t nq, double sig,
+           bool nrm, int32_t truncation) {
+    if (!(sig > 0.0)) return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "lambdarank sigmoid must be > 0");
+    if (!bounds || nq < 1 || bounds[0] != 0 || bounds[nq] != n)
+      return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "query boundaries must run from 0 to num_data");
+    for (int32_t q = 0; q < nq; ++q) {
+      if (bounds[q + 1] < bounds[q])
+        return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "query boundaries must be non-decreasing");
+      if (bounds[q + 1] - bounds[q] > kMaxPosition)
+        return fail(LGBM_HIP_ERR_CAPABILITY, "a query holds more than 10000 rows");
+    }
+    sigmoid = sig;
+    norm = nrm;
+    trunc = truncation;
+    qb.assign(bounds, bounds + nq + 1);
+    label.assign(labels, labels + n);
+    gain.assign(1, 0.0);
+    for (int i = 1; i < 31; ++i) gain.push_back((double)((1ll << i) - 1));
+    for (int64_t i = 0; i < n; ++i) {  // DCGCalculator::check_labels order
+      const float l = labels[i];
+      if (std::fabs(l - (float)(int32_t)l) > (float)1e-15f)
+        return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "ranking labels must be integers");
+      if (l < 0.0f || (size_t)l >= gain.size())
+        return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "ranking label out of the label gain table");
+    }
+    discount.resize(kMaxPosition);
+    for (int32_t i = 0; i < kMaxPosition; ++i) discount[i] = 1.0 / std::log2(2.0 + (double)i);
+    inv_max_dcg.resize(nq);
+    for (int32_t q = 0; q < nq; ++q) {
+      double m = cal_max_dcg_at_k(trunc, labels + bounds[q], bounds[q + 1] - bounds[q]);
+      if (m > 0.0) m = 1.0 / m;
+      inv_max_dcg[q] = m;
+    }
+    min_in = -50.0;
+    min_in = min_in / sigmoid / 2.0;
+    max_in = -min_in;
+    idx_factor = (double)kSigmoidBins / (max_in - min_in);
+    table.resize(kSigmoidBins);
+    for (int32_t i = 0; i < kSigmoidBins; ++i) {
+      const double sc = (double)i / idx_factor + min_in;
+      table[i] = 1.0 / (1.0 + std::exp(sc * sigmoid));
+    }
+    return LGBM_HIP_OK;
+  }
+  double cal_max_dcg_at_k(int32_t k, const float* labels, int32_t cnt) const {
+    std::vector<int64_t> lc(gain.size(), 0);
+    for (int32_t i = 0; i < cnt; ++i) lc[(size_t)labels[i]] += 1;
+    int64_t top = (int64_t)gain.size() - 1;
+    double ret = 0.0;
+    const int32_t kk = std::min(k, cnt);
+    for (int32_t j = 0; j < kk; ++j) {
+      while (top > 0 && lc[(size_t)top] <= 0) top -= 1;
+      if (top < 0) break;
+      ret += discount[j] * gain[(size_t)top];
+      lc[(size_t)top] -= 1;
+    }
+    return ret;
+  }
+  double get_sigmoid(double s) const {
+    if (s <= min_in) return table[0];
+    if (s >= max_in) return table[kSigmoidBins - 1];
+    return table[(size_t)((s - min_in) * idx_factor)];
+  }
+  // get_gradients -> gradients_for_one_query (rank.rs:260-365)
+  void gradients(const double* score, float* g, float* h) const {
+    const int32_t nq = (int32_t)qb.size() - 1;
+    const double kMin = -std::numeric_limits<double>::infinity();
+#pragma omp parallel for schedule(dynamic, 64) if (nq > 256)
+    for (int32_t q = 0; q < nq; ++q) {
+      const int32_t st = qb[q], cnt = qb[q + 1] - qb[q];
+      const double* s = score + st;
+      const float* ql = label.data() + st;
+      float* lam = g + st;
+      float* hes = h + st;
+      for (int32_t i = 0; i < cnt; ++i) {
+        lam[i] = 0.0f;
+        hes[i] = 0.0f;
+      }
+      if (cnt == 0) continue;
+      std::vector<int32_t> si(cnt);
+      for (int32_t i = 0; i < cnt; ++i) si[i] = i;
+      std::stable_sort(si.begin(), si.end(), [&](int32_t a, int32_t b) { return s[a] > s[b]; });
+      const double best = s[si[0]];
+      int32_t wi = cnt - 1;
+      if (wi > 0 && s[si[wi]] == kMin) wi -= 1;
+      const double worst = s[si[wi]];
+      const double imd = inv_max_dcg[q];
+      double sum_lambdas = 0.0;
+      for (int32_t i = 0; i + 1 < cnt && i < trunc; ++i) {
+        if (s[si[i]] == kMin) continue;
+        for (int32_t j = i + 1; j < cnt; ++j) {
+          if (s[si[j]] == kMin) continue;
+          if (ql[si[i]] == ql[si[j]]) continue;
+          const bool ihigh = ql[si[i]] > ql[si[j]];
+          const int32_t hr = ihigh ? i : j, lr = ihigh ? j : i;
+          const int32_t hi = si[hr], lo = si[lr];
+          const double delta_score = s[hi] - s[lo];
+          const double dcg_gap = gain[(size_t)ql[hi]] - gain[(size_t)ql[lo]];
+          const double paired = std::fabs(discount[hr] - discount[lr]);
+          double dpn = dcg_gap * paired * imd;
+          if (norm && best != worst) dpn /= (double)0.01f + std::fabs(delta_score);
+          double pl = get_sigmoid(delta_score);
+          double ph = pl * (1.0 - pl);
+          pl *= -sigmoid * dpn;
+          ph *= sigmoid * sigmoid * dpn;
+          lam[lo] -= (float)pl;
+          hes[lo] += (float)ph;
+          lam[hi] += (float)pl;
+          hes[hi] += (float)ph;
+          sum_lambdas -= 2.0 * pl;
+        }
+      }
+      if (norm && sum_lambdas > 0.0) {
+        const double nf = std::log2(1.0 + sum_lambdas) / sum_lambdas;
+        for (int32_t i = 0; i < cnt; ++i) {
+          lam[i] = (float)((double)lam[i] * nf);
+          hes[i] = (float)((double)hes[i] * nf);
+        }
+      }
+    }
+  }
+};
+
 }  // namespace
 
 // ===========================================================================
@@ -1642,32 +1898,77 @@ int oracle_train_multiclass(const void* bins, int32_t width, int32_t F, int64_t 
 // through the partition (learner.rs:4380-4395) -> add_bias on the first tree.
 // `scores` (n) receives the final training scores; trees_out (optional) is an array of
 // `iters` tree descriptors.  Returns the number of trees in *n_trees.
-int oracle_train_binary(const void* bins, int32_t width, int32_t F, int64_t N,
-                        const lgbm_feature_meta* meta, const double* ub, const float* label,
-                        const lgbm_gain_config* cfg, int32_t num_leaves, int32_t max_depth,
-                        int32_t iters, double lr, int32_t boost_from_average, int32_t quantized,
-                        int32_t quant_bins, int32_t stochastic, double* scores,
-                        lgbm_tree_out* trees_out, int32_t* n_trees) {
+// The boosting loop (gbdt.rs:612-640,691-1300) for one tree per iteration: the
+// objective's BoostFromAverage init (added when |init| > kEpsilon; the first tree
+// carries it as add_bias), gradients, the optional quantizer, the column sampler's
+// per-tree draw, the tree, score updates, and the stop when a tree cannot split.
+typedef struct {
+  int32_t objective;  // 0 binary logloss, 1 L2 regression, 2 lambdarank
+  int32_t num_leaves, max_depth, iters;
+  double learning_rate;
+  int32_t boost_from_average, quantized, quant_bins, stochastic;
+  double feature_fraction;  // < 1: ColSampler by tree (feature_fraction_bynode = 1)
+  int32_t feature_fraction_seed, lambdarank_norm;
+  double sigmoid;
+  int32_t truncation_level, num_queries;
+  const int32_t* query_boundaries;  // num_queries + 1 (lambdarank)
+} oracle_train_params;
+
+int oracle_train(const void* bins, int32_t width, int32_t F, int64_t N,
+                 const lgbm_feature_meta* meta, const double* ub, const float* label,
+                 const lgbm_gain_config* cfg, const oracle_train_params* p, double* scores,
+                 lgbm_tree_out* trees_out, int32_t* n_trees) {
+  if (!p || !label) return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "null params or labels");
   Learner L;
-  int rc = make_learner(L, bins, width, F, N, meta, ub, cfg, num_leaves, max_depth);
+  int rc = make_learner(L, bins, width, F, N, meta, ub, cfg, p->num_leaves, p->max_depth);
   if (rc) return rc;
+  Lambdarank rank;
+  if (p->objective == 2) {
+    rc = rank.init(label, N, p->query_boundaries, p->num_queries, p->sigmoid,
+                   p->lambdarank_norm != 0, p->truncation_level);
+    if (rc) return rc;
+  } else if (p->objective != 0 && p->objective != 1) {
+    return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "objective must be 0, 1 or 2");
+  }
+  ColSampler cs;
+  const bool sampling = p->feature_fraction < 1.0;
+  if (sampling) {
+    std::vector<int32_t> valid(F);
+    int32_t max_real = -1;
+    for (int f = 0; f < F; ++f) {
+      valid[f] = meta[f].real_feature_index;
+      max_real = std::max(max_real, valid[f]);
+    }
+    cs.init(p->feature_fraction, 1.0, p->feature_fraction_seed, valid,
+            (size_t)std::max<int32_t>(max_real + 1, F));
+  }
   std::vector<double> score(N, 0.0);
   double init = 0.0;
-  if (boost_from_average) {
-    init = binary_boost_from_score(label, N, 1.0);
+  if (p->boost_from_average) {
+    // ranking objectives have no init score (boosting/src/objective.rs:112-116)
+    if (p->objective == 0) init = binary_boost_from_score(label, N, 1.0);
+    if (p->objective == 1) init = l2_boost_from_score(label, N);
     if (std::fabs(init) > kEps)
       for (int64_t i = 0; i < N; ++i) score[i] += init;
   }
   std::vector<float> g(N), h(N);
   int32_t nt = 0;
-  for (int32_t it = 0; it < iters; ++it) {
-    binary_gradients(score.data(), label, g.data(), h.data(), N, 1.0);
-    if (quantized) {
+  for (int32_t it = 0; it < p->iters; ++it) {
+    if (p->objective == 0) binary_gradients(score.data(), label, g.data(), h.data(), N, 1.0);
+    if (p->objective == 1) l2_gradients(score.data(), label, g.data(), h.data(), N);
+    if (p->objective == 2) rank.gradients(score.data(), g.data(), h.data());
+    if (p->quantized) {
       uint64_t seed = ((uint64_t)it << 20) ^ 0ull ^ 0x51702010ull;
-      quantize_in_place(g.data(), h.data(), N, quant_bins, stochastic != 0, seed, nullptr, nullptr);
+      quantize_in_place(g.data(), h.data(), N, p->quant_bins, p->stochastic != 0, seed, nullptr,
+                        nullptr);
+    }
+    if (sampling) {
+      cs.reset_by_tree();
+      L.tree_used.assign(F, 0);
+      for (int f = 0; f < F; ++f) L.tree_used[f] = cs.is_used[(size_t)meta[f].real_feature_index];
     }
     Tree t;
-    DataPartition dp(N, num_leaves);
+    DataPartition dp(N, p->num_leaves);
     rc = L.train(g.data(), h.data(), t, dp);
     if (rc) return rc;
     if (t.num_leaves <= 1) {
@@ -1682,7 +1983,7 @@ int oracle_train_binary(const void* bins, int32_t width, int32_t F, int64_t N,
       break;
     }
     {
-      t.shrinkage(lr);
+      t.shrinkage(p->learning_rate);
       for (int32_t leaf = 0; leaf < t.num_leaves; ++leaf) {
         const double v = t.leaf_value[leaf];
         const uint32_t* rows = dp.indices.data() + dp.leaf_begin[leaf];
@@ -1696,6 +1997,74 @@ int oracle_train_binary(const void* bins, int32_t width, int32_t F, int64_t N,
   }
   if (scores) std::memcpy(scores, score.data(), (size_t)N * 8);
   if (n_trees) *n_trees = nt;
+  return LGBM_HIP_OK;
+}
+
+int oracle_train_binary(const void* bins, int32_t width, int32_t F, int64_t N,
+                        const lgbm_feature_meta* meta, const double* ub, const float* label,
+                        const lgbm_gain_config* cfg, int32_t num_leaves, int32_t max_depth,
+                        int32_t iters, double lr, int32_t boost_from_average, int32_t quantized,
+                        int32_t quant_bins, int32_t stochastic, double* scores,
+                        lgbm_tree_out* trees_out, int32_t* n_trees) {
+  oracle_train_params p{};
+  p.objective = 0;
+  p.num_leaves = num_leaves;
+  p.max_depth = max_depth;
+  p.iters = iters;
+  p.learning_rate = lr;
+  p.boost_from_average = boost_from_average;
+  p.quantized = quantized;
+  p.quant_bins = quant_bins;
+  p.stochastic = stochastic;
+  p.feature_fraction = 1.0;
+  return oracle_train(bins, width, F, N, meta, ub, label, cfg, &p, scores, trees_out, n_trees);
+}
+
+int oracle_regression_gradients(const double* score, const float* label, int64_t n, float* g,
+                                float* h) {
+  l2_gradients(score, label, g, h, n);
+  return LGBM_HIP_OK;
+}
+double oracle_regression_boost_from_score(const float* label, int64_t n) {
+  return l2_boost_from_score(label, n);
+}
+
+int oracle_lambdarank_gradients(const double* score, const float* label, int64_t n,
+                                const int32_t* query_boundaries, int32_t num_queries,
+                                double sigmoid, int32_t norm, int32_t truncation_level, float* g,
+                                float* h) {
+  Lambdarank r;
+  int rc = r.init(label, n, query_boundaries, num_queries, sigmoid, norm != 0, truncation_level);
+  if (rc) return rc;
+  r.gradients(score, g, h);
+  return LGBM_HIP_OK;
+}
+
+// The column sampler's draws as the learner makes them: construction (the Init
+// draw), one reset_by_tree, then n_nodes get_by_node calls.  Writes the tree's
+// selection (nf flags) and each node's (n_nodes x nf flags).
+int oracle_col_sampler_trace(double feature_fraction, double feature_fraction_bynode, int32_t seed,
+                             int32_t nf, int32_t n_nodes, int8_t* bytree, int8_t* nodes) {
+  if (nf <= 0 || !bytree || (n_nodes > 0 && !nodes))
+    return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "bad trace arguments");
+  ColSampler cs;
+  std::vector<int32_t> valid(nf);
+  for (int32_t f = 0; f < nf; ++f) valid[f] = f;
+  cs.init(feature_fraction, feature_fraction_bynode, seed, valid, (size_t)nf);
+  cs.reset_by_tree();
+  for (int32_t f = 0; f < nf; ++f) bytree[f] = cs.is_used[(size_t)f];
+  for (int32_t k = 0; k < n_nodes; ++k) {
+    const std::vector<char> m = cs.get_by_node();
+    for (int32_t f = 0; f < nf; ++f) nodes[(size_t)k * nf + f] = m[(size_t)f];
+  }
+  return LGBM_HIP_OK;
+}
+
+int oracle_random_sample(int32_t seed, int32_t n, int32_t k, int32_t* out, int32_t* out_len) {
+  LcgRandom r(seed);
+  const std::vector<int32_t> v = r.sample(n, k);
+  for (size_t i = 0; i < v.size(); ++i) out[i] = v[i];
+  *out_len = (int32_t)v.size();
   return LGBM_HIP_OK;
 }
 

@@ -30,6 +30,7 @@ def lib():
             build()
         L = C.CDLL(LIB_PATH)
         L.oracle_binary_boost_from_score.restype = C.c_double
+        L.oracle_regression_boost_from_score.restype = C.c_double
         _lib = L
     return _lib
 
@@ -281,3 +282,105 @@ def train_multiclass(bins_fm, meta, upper, label, num_class, cfg, num_leaves, ma
             trees[i].out = tarr[i]
             out_trees.append(trees[i].to_dict())
     return scores, out_trees
+
+
+OBJECTIVE_BINARY, OBJECTIVE_REGRESSION, OBJECTIVE_LAMBDARANK = 0, 1, 2
+
+
+class TrainParams(C.Structure):
+    """oracle_train_params (lgbm_oracle.cpp)."""
+    _fields_ = [("objective", C.c_int32), ("num_leaves", C.c_int32), ("max_depth", C.c_int32),
+                ("iters", C.c_int32), ("learning_rate", C.c_double),
+                ("boost_from_average", C.c_int32), ("quantized", C.c_int32),
+                ("quant_bins", C.c_int32), ("stochastic", C.c_int32),
+                ("feature_fraction", C.c_double), ("feature_fraction_seed", C.c_int32),
+                ("lambdarank_norm", C.c_int32), ("sigmoid", C.c_double),
+                ("truncation_level", C.c_int32), ("num_queries", C.c_int32),
+                ("query_boundaries", C.POINTER(C.c_int32))]
+
+
+def train(bins_fm, meta, upper, label, cfg, objective, num_leaves, max_depth, iters, lr,
+          boost_from_average=True, quantized=False, quant_bins=4, stochastic=True,
+          feature_fraction=1.0, feature_fraction_seed=2, query_boundaries=None, sigmoid=1.0,
+          lambdarank_norm=True, truncation_level=30, want_trees=True):
+    """The one-tree-per-iteration boosting loop for binary logloss (0), L2 regression
+    (1) or lambdarank (2, over `query_boundaries`), with the optional quantizer and
+    per-tree column sampling.  Returns (final scores, trees)."""
+    b, width = _bins_arg(bins_fm)
+    F, N = b.shape
+    marr = _meta_arr(meta)
+    ub = None if upper is None else np.ascontiguousarray(upper, dtype=np.float64)
+    lab = np.ascontiguousarray(label, dtype=np.float32)
+    qb = None if query_boundaries is None else np.ascontiguousarray(query_boundaries, np.int32)
+    p = TrainParams()
+    p.objective = objective
+    p.num_leaves, p.max_depth, p.iters, p.learning_rate = num_leaves, max_depth, iters, lr
+    p.boost_from_average, p.quantized = int(boost_from_average), int(quantized)
+    p.quant_bins, p.stochastic = quant_bins, int(stochastic)
+    p.feature_fraction, p.feature_fraction_seed = feature_fraction, feature_fraction_seed
+    p.lambdarank_norm, p.sigmoid, p.truncation_level = int(lambdarank_norm), sigmoid, truncation_level
+    p.num_queries = 0 if qb is None else len(qb) - 1
+    p.query_boundaries = ptr(qb, C.c_int32) if qb is not None else None
+    scores = np.zeros(N, dtype=np.float64)
+    trees = [TreeBuffers(num_leaves) for _ in range(iters)] if want_trees else []
+    tarr = (type(trees[0].out) * iters)(*[t.out for t in trees]) if want_trees else None
+    nt = C.c_int32(0)
+    _check(lib().oracle_train(b.ctypes.data_as(C.c_void_p), C.c_int32(width), C.c_int32(F),
+                              C.c_int64(N), marr, ptr(ub, C.c_double), ptr(lab, C.c_float),
+                              C.byref(cfg), C.byref(p), ptr(scores, C.c_double), tarr,
+                              C.byref(nt)))
+    out_trees = []
+    if want_trees:
+        for i in range(nt.value):
+            trees[i].out = tarr[i]
+            out_trees.append(trees[i].to_dict())
+    return scores, out_trees
+
+
+def regression_gradients(score, label):
+    s = np.ascontiguousarray(score, dtype=np.float64)
+    l = np.ascontiguousarray(label, dtype=np.float32)
+    g = np.zeros(len(s), dtype=np.float32)
+    h = np.zeros(len(s), dtype=np.float32)
+    _check(lib().oracle_regression_gradients(ptr(s, C.c_double), ptr(l, C.c_float),
+                                             C.c_int64(len(s)), ptr(g, C.c_float),
+                                             ptr(h, C.c_float)))
+    return g, h
+
+
+def regression_boost_from_score(label):
+    l = np.ascontiguousarray(label, dtype=np.float32)
+    return lib().oracle_regression_boost_from_score(ptr(l, C.c_float), C.c_int64(len(l)))
+
+
+def lambdarank_gradients(score, label, query_boundaries, sigmoid=1.0, norm=True,
+                         truncation_level=30):
+    s = np.ascontiguousarray(score, dtype=np.float64)
+    l = np.ascontiguousarray(label, dtype=np.float32)
+    qb = np.ascontiguousarray(query_boundaries, dtype=np.int32)
+    g = np.zeros(len(s), dtype=np.float32)
+    h = np.zeros(len(s), dtype=np.float32)
+    _check(lib().oracle_lambdarank_gradients(
+        ptr(s, C.c_double), ptr(l, C.c_float), C.c_int64(len(s)), ptr(qb, C.c_int32),
+        C.c_int32(len(qb) - 1), C.c_double(sigmoid), C.c_int32(int(norm)),
+        C.c_int32(truncation_level), ptr(g, C.c_float), ptr(h, C.c_float)))
+    return g, h
+
+
+def col_sampler_trace(feature_fraction, feature_fraction_bynode, seed, num_features, n_nodes):
+    """(tree selection [nf] int8, node selections [n_nodes, nf] int8) of a fresh sampler."""
+    bt = np.zeros(num_features, dtype=np.int8)
+    nodes = np.zeros((max(n_nodes, 1), num_features), dtype=np.int8)
+    _check(lib().oracle_col_sampler_trace(C.c_double(feature_fraction),
+                                          C.c_double(feature_fraction_bynode), C.c_int32(seed),
+                                          C.c_int32(num_features), C.c_int32(n_nodes),
+                                          ptr(bt, C.c_int8), ptr(nodes, C.c_int8)))
+    return bt, nodes[:n_nodes]
+
+
+def random_sample(seed, n, k):
+    out = np.zeros(max(k, 1), dtype=np.int32)
+    ln = C.c_int32(0)
+    _check(lib().oracle_random_sample(C.c_int32(seed), C.c_int32(n), C.c_int32(k),
+                                      ptr(out, C.c_int32), C.byref(ln)))
+    return out[:ln.value]

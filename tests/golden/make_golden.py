@@ -315,6 +315,88 @@ def path_smooth_golden():
     return len(cells), out
 
 
+def col_sampler_golden():
+    """learner/col_sampler.txt (the genuine Random::Sample transcription driven as the
+    learner drives it): one sampler, its per-tree selection, then five per-node
+    draws in order."""
+    out = {"nodes": []}
+    for ln in read("learner/col_sampler.txt"):
+        if ln.startswith("CS_CONFIG"):
+            kv = dict(t.split("=") for t in ln.split()[1:])
+            out["feature_fraction"] = struct.unpack("<d", struct.pack("<Q", int(kv["feature_fraction_bits"])))[0]
+            out["feature_fraction_bynode"] = struct.unpack(
+                "<d", struct.pack("<Q", int(kv["feature_fraction_bynode_bits"])))[0]
+            out["seed"] = int(kv["seed"])
+            out["num_features"] = int(kv["num_features"])
+        elif ln.startswith("CS_BYTREE"):
+            out["bytree"] = [int(t) for t in ln.split()[1].split(";")]
+        elif ln.startswith("CS_NODE"):
+            out["nodes"].append([int(t) for t in ln.split()[2].split(";")])
+    return out
+
+
+def feature_fraction_golden():
+    """feature_fraction/feature_fraction_golden.json (the real lightgbm 4.6 binary,
+    capture.py: 600 x 20 N(0,1), binary labels, 8 iterations, num_leaves 8,
+    min_data_in_leaf 5, max_bin 63, feature_fraction_seed 2) -> feature_fraction.npz:
+    the per-tree column sampling cells (feature_fraction_bynode = 1): raw predictions
+    (f64 bits) and each tree's set of split features."""
+    import numpy as np
+    with open(os.path.join(REF, "feature_fraction/feature_fraction_golden.json")) as f:
+        d = json.load(f)
+    n, m = d["num_rows"], d["num_cols"]
+    X = np.array([int(h, 16) for h in d["features_bits"]], dtype=np.uint64).view(np.float64)
+    y = np.array([int(h, 16) for h in d["labels_bits"]], dtype=np.uint64).view(np.float64)
+    fracs, preds, flat, counts = [], [], [], []
+    for key in sorted(d["cells"]):
+        c = d["cells"][key]
+        if c["feature_fraction_bynode"] != 1.0:
+            continue
+        fracs.append(c["feature_fraction"])
+        preds.append(np.array([int(h, 16) for h in c["pred_bits"]], dtype=np.uint64))
+        counts.append([len(t) for t in c["per_tree_split_features"]])
+        for t in c["per_tree_split_features"]:
+            flat.extend(t)
+    out = os.path.join(OUT, "feature_fraction.npz")
+    np.savez_compressed(out, X=X.reshape(n, m), y=y, fractions=np.array(fracs, dtype=np.float64),
+                        pred_bits=np.stack(preds), split_flat=np.array(flat, dtype=np.int32),
+                        split_counts=np.array(counts, dtype=np.int32),
+                        num_iterations=np.int32(d["num_iterations"]))
+    return len(fracs), out
+
+
+def lambdarank_golden():
+    """rank/ (the real lightgbm 4.6 binary, xtask/py/rank_oracle_capture.py): the
+    30-row, 6-query corpus (X: RandomState(20240607).randint(0, 8, (30, 3)), the
+    recipe's first draw; labels from the scores golden), the iteration-1 gradients
+    at zero scores (f32 bits; sigmoid 1, lambdarank_norm, truncation level 5), the
+    final raw scores of the 10-iteration model (f64 bits) and its trees (num_leaves
+    7, learning_rate 0.1, min_data_in_leaf 1, max_bin 255, min_data_in_bin 1)."""
+    import numpy as np
+    sc = {}
+    for ln in read("rank/lambdarank_scores.txt"):
+        if "=" in ln and not ln.startswith("#"):
+            k, _, v = ln.partition("=")
+            sc[k] = [int(t) for t in v.split(",")]
+    gh = {}
+    for ln in read("rank/lambdarank_gh_iter1.txt"):
+        if ln.startswith("GRAD") or ln.startswith("HESS"):
+            k, *v = ln.split()
+            gh[k] = [int(t) for t in v]
+    rng = np.random.RandomState(20240607)
+    X = rng.randint(0, 8, size=(30, 3)).astype(np.float64)
+    labels = rng.randint(0, 4, size=30).astype(np.float32)
+    lab_bits = np.array(sc["labels"], dtype=np.uint32).view(np.float32)
+    assert np.array_equal(labels, lab_bits), "the corpus recipe reproduces the golden labels"
+    trees = parse_model_trees("rank/rank_lambdarank_byq0_es0_model.txt")
+    keep = ("num_leaves", "split_feature", "threshold", "decision_type", "left_child",
+            "right_child", "leaf_value", "leaf_count", "internal_count", "leaf_weight")
+    return dict(X=X.tolist(), label_bits=sc["labels"], query_boundaries=sc["query_boundaries"],
+                score_bits=sc["scores"], gh_iter1=gh, num_iterations=10, num_leaves=7,
+                learning_rate=0.1, min_data_in_leaf=1, sigmoid=1.0, lambdarank_norm=True,
+                truncation_level=5, trees=[{k: t[k] for k in keep if k in t} for t in trees])
+
+
 def discretizer_cases():
     # Hand-computed unit cases, gradient_discretizer.rs:269-333 (inputs -> expected ints).
     return [
@@ -342,13 +424,16 @@ def main():
         "learner_real.json": learner_real(),
         "discretizer_cases.json": discretizer_cases(),
         "multiclass_spine.json": multiclass_spine(),
+        "col_sampler.json": col_sampler_golden(),
+        "lambdarank.json": lambdarank_golden(),
     }
     for name, data in outs.items():
         with open(os.path.join(OUT, name), "w") as f:
             json.dump(data, f, separators=(",", ":"))
         print(name, len(data), os.path.getsize(os.path.join(OUT, name)), "bytes")
-    k, path = path_smooth_golden()
-    print(os.path.basename(path), k, os.path.getsize(path), "bytes")
+    for fn in (path_smooth_golden, feature_fraction_golden):
+        k, path = fn()
+        print(os.path.basename(path), k, os.path.getsize(path), "bytes")
 
 
 if __name__ == "__main__":
