@@ -332,6 +332,47 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* ctx, int32_t iter, const lgbm_gain_
  * clamped to [kEpsilon, 1 - kEpsilon]; 0 for n == 0.  Host only. */
 int lgbm_hip_binary_boost_from_score(const float* label, int64_t n, double sigmoid, double* out);
 
+/* ---- other one-tree-per-iteration objectives, column sampling ---------------- */
+
+/* Objectives of lgbm_hip_train_iter. */
+#define LGBM_HIP_OBJECTIVE_BINARY 0     /* BinaryLogloss (binary.rs:134-172) */
+#define LGBM_HIP_OBJECTIVE_REGRESSION 1 /* L2: Objective::Regression (regression.rs:427-431) */
+#define LGBM_HIP_OBJECTIVE_LAMBDARANK 2 /* Lambdarank (rank.rs:100-365) */
+
+/* The objective lgbm_hip_train_iter evaluates (binary by default); a reference
+ * `Objective` / `BoostObjective` value (lgbm-boosting/src/objective.rs). */
+int lgbm_hip_set_objective(lgbm_hip_ctx* ctx, int32_t objective);
+
+/* LambdaRank over the resident labels (set with lgbm_hip_set_labels, init score 0:
+ * ranking has no BoostFromAverage, lgbm-boosting/src/objective.rs:112-116):
+ * `Lambdarank::new` (rank.rs:131-198) with the query boundaries (num_queries + 1
+ * prefix sums from 0 to num_data), sigmoid > 0, lambdarank_norm and the truncation
+ * level; the default label gains 2^i - 1 (labels must be integers in 0..=30).  Also
+ * selects the objective.  Queries of more than 2048 rows are refused. */
+int lgbm_hip_set_lambdarank(lgbm_hip_ctx* ctx, const int32_t* query_boundaries,
+                            int32_t num_queries, double sigmoid, int32_t norm,
+                            int32_t truncation_level);
+
+/* One boosting iteration of the objective set by lgbm_hip_set_objective /
+ * lgbm_hip_set_lambdarank, as lgbm_hip_train_iter_binary does for the binary one
+ * (gbdt.rs:691-1300 with `objective.get_gradients`). */
+int lgbm_hip_train_iter(lgbm_hip_ctx* ctx, int32_t iter, const lgbm_gain_config* cfg,
+                        int32_t num_leaves, int32_t max_depth, double learning_rate,
+                        int32_t num_grad_quant_bins, int32_t stochastic, lgbm_tree_out* tree);
+
+/* Per-tree column sampling: `ColSampler` with feature_fraction and
+ * feature_fraction_seed (lgbm-treelearner/src/col_sampler.rs:68-140; the draw at
+ * creation, then one before every tree grown on this context, learner.rs:1190-1240;
+ * features outside a tree's sample are never scanned).  feature_fraction >= 1 turns
+ * it off; feature_fraction_bynode must be 1 (per-node sampling is not built).  A
+ * new bins upload turns it off. */
+int lgbm_hip_set_col_sampler(lgbm_hip_ctx* ctx, double feature_fraction,
+                             double feature_fraction_bynode, int32_t seed);
+
+/* The objective's BoostFromScore on host labels: binary log-odds (sigmoid 1), the
+ * L2 label mean (regression.rs:563-575), 0 for lambdarank.  Host only. */
+int lgbm_hip_boost_from_score(int32_t objective, const float* label, int64_t n, double* out);
+
 /* The f32 gradients / hessians of the last objective evaluation on the device
  * (BinaryLogloss::get_gradients, binary.rs:134-172; either pointer may be NULL).
  * No reference counterpart at the boundary: the reference's are host arrays. */

@@ -230,6 +230,35 @@ class HipBackend:
             C.byref(tb.out) if tb else None))
         return tb.to_dict() if tb else None
 
+    # objectives other than binary (lgbm_hip_set_objective / lgbm_hip_train_iter)
+    OBJECTIVES = {"binary": 0, "regression": 1, "lambdarank": 2}
+
+    def set_objective(self, objective):
+        self._check(self.lib.lgbm_hip_set_objective(self.ctx, C.c_int32(self.OBJECTIVES[objective])))
+
+    def set_lambdarank(self, query_boundaries, sigmoid=1.0, norm=True, truncation_level=30):
+        """LambdaRank over the resident labels (lgbm_hip_set_lambdarank)."""
+        qb = np.ascontiguousarray(query_boundaries, np.int32)
+        self._check(self.lib.lgbm_hip_set_lambdarank(
+            self.ctx, ptr(qb, C.c_int32), C.c_int32(len(qb) - 1), C.c_double(sigmoid),
+            C.c_int32(int(norm)), C.c_int32(truncation_level)))
+
+    def set_col_sampler(self, feature_fraction, feature_fraction_bynode=1.0, seed=2):
+        """Per-tree column sampling (lgbm_hip_set_col_sampler)."""
+        self._check(self.lib.lgbm_hip_set_col_sampler(self.ctx, C.c_double(feature_fraction),
+                                                      C.c_double(feature_fraction_bynode),
+                                                      C.c_int32(seed)))
+
+    def train_iter(self, it, cfg, num_leaves, max_depth, learning_rate, num_grad_quant_bins=4,
+                   stochastic=True, want_tree=True):
+        """One iteration of the context's objective (lgbm_hip_train_iter)."""
+        tb = self._tree_buffers(num_leaves) if want_tree else None
+        self._check(self.lib.lgbm_hip_train_iter(
+            self.ctx, C.c_int32(it), C.byref(cfg), C.c_int32(num_leaves), C.c_int32(max_depth),
+            C.c_double(learning_rate), C.c_int32(num_grad_quant_bins), C.c_int32(int(stochastic)),
+            C.byref(tb.out) if tb else None))
+        return tb.to_dict() if tb else None
+
     def set_labels_multiclass(self, labels, num_class, init_scores=None):
         """Class labels + the class-major score reset to init_scores[k] per class
         (lgbm_hip_set_labels_multiclass)."""
@@ -314,6 +343,19 @@ def binary_boost_from_score(labels, sigmoid=1.0):
     out = C.c_double(0.0)
     rc = lib.lgbm_hip_binary_boost_from_score(ptr(lab, C.c_float), C.c_int64(len(lab)),
                                               C.c_double(sigmoid), C.byref(out))
+    if rc != 0:
+        raise HipError(rc, "boost_from_score: bad arguments")
+    return out.value
+
+
+def boost_from_score(objective, labels):
+    """The objective's BoostFromScore (lgbm_hip_boost_from_score): binary log-odds,
+    the L2 label mean, 0 for lambdarank."""
+    lib = load_library()
+    lab = np.ascontiguousarray(labels, np.float32)
+    out = C.c_double(0.0)
+    rc = lib.lgbm_hip_boost_from_score(C.c_int32(HipBackend.OBJECTIVES[objective]),
+                                       ptr(lab, C.c_float), C.c_int64(len(lab)), C.byref(out))
     if rc != 0:
         raise HipError(rc, "boost_from_score: bad arguments")
     return out.value

@@ -63,6 +63,65 @@ struct EventPair {
   int family;
 };
 
+// LightGBM's LCG (lgbm-core/src/random.rs:37-123: x = 214013 x + 2531011) and its
+// Sample(n, k).
+struct Lcg32 {
+  uint32_t state = 0;
+  int32_t step16() {
+    state = state * 214013u + 2531011u;
+    return (int32_t)((state >> 16) & 0x7fffu);
+  }
+  int32_t step31() {
+    state = state * 214013u + 2531011u;
+    return (int32_t)(state & 0x7fffffffu);
+  }
+  // k sorted distinct values of [0, n): all of them when k == n; a streaming pass
+  // when k > n / log2(k); else k draws into a set, a repeated draw v taking r instead
+  std::vector<int32_t> sample(int32_t n, int32_t k) {
+    std::vector<int32_t> out;
+    if (k > n || k <= 0) return out;
+    if (k == n) {
+      for (int32_t i = 0; i < n; ++i) out.push_back(i);
+      return out;
+    }
+    if (k > 1 && (double)k > (double)n / std::log2((double)k)) {
+      for (int32_t i = 0; i < n; ++i) {
+        const float u = (float)step16() / 32768.0f;
+        if ((double)u < (double)(k - (int32_t)out.size()) / (double)(n - i)) out.push_back(i);
+      }
+      return out;
+    }
+    std::vector<uint8_t> taken((size_t)n, 0);
+    for (int32_t r = n - k; r < n; ++r) {
+      const int32_t v = step31() % (r + 1);
+      taken[(size_t)(taken[(size_t)v] ? r : v)] = 1;
+    }
+    for (int32_t i = 0; i < n; ++i)
+      if (taken[(size_t)i]) out.push_back(i);
+    return out;
+  }
+};
+
+// The per-tree column sample of feature_fraction (ColSampler, lgbm-treelearner/src/
+// col_sampler.rs:68-140): the sampler draws once when it is created and once before
+// every tree (learner.rs:1190-1240), round(F * fraction) (at least one) features.
+struct FeatureSampler {
+  Lcg32 rng;
+  int32_t count = 0, F = 0;
+  std::vector<uint8_t> used;  // by feature position
+  void start(double fraction, int32_t seed, int32_t num_features) {
+    rng.state = (uint32_t)seed;
+    F = num_features;
+    const int32_t c = (int32_t)((double)F * fraction + (double)0.5f);
+    count = std::max(c, std::min(1, F));
+    next_tree();
+  }
+  void next_tree() {
+    used.assign((size_t)F, 0);
+    for (int32_t pos : rng.sample(F, count)) used[(size_t)pos] = 1;
+  }
+};
+
 }  // namespace
 
 struct lgbm_hip_ctx {
@@ -105,7 +164,19 @@ struct lgbm_hip_ctx {
   // lookahead (lgbm_hip_set_lookahead): the next iteration's objective + quantizer
   // enqueued by train_iter_binary before it waits for its tree copy
   bool lookahead = false, ahead = false;
-  int32_t ahead_iter = 0, ahead_qbins = 0, ahead_stoch = 0;
+  int32_t ahead_iter = 0, ahead_qbins = 0, ahead_stoch = 0, ahead_obj = 0;
+  // objective of lgbm_hip_train_iter (LGBM_HIP_OBJECTIVE_*)
+  int32_t objective = LGBM_HIP_OBJECTIVE_BINARY;
+  // lambdarank tables (lgbm_hip_set_lambdarank)
+  int32_t* rk_qb = nullptr;
+  double *rk_imd = nullptr, *rk_table = nullptr, *rk_disc = nullptr, *rk_gain = nullptr;
+  RankTables rank{};
+  bool have_rank = false;
+  // feature_fraction (lgbm_hip_set_col_sampler): a new column sample before every tree
+  FeatureSampler colsamp;
+  bool colsamp_on = false;
+  uint8_t* d_feat_used = nullptr;
+  uint8_t* feat_used_host = nullptr;  // pinned
   hipEvent_t tree_ev = nullptr;
   // device memory
   Ctl* ctl = nullptr;
@@ -297,6 +368,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.acc_cells = c->acc_cells;
   L.binmat = c->binmat;
   L.row_stride = c->row_stride;
+  L.feat_used = c->colsamp_on ? c->d_feat_used : nullptr;
   L.part_slots = c->part_slots;
   L.hist_part64 = c->hist_part64;
   L.int_slots64 = c->int_slots64;
@@ -613,6 +685,14 @@ int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_le
                     int32_t max_depth, int32_t fp) {
   int rc = ensure_leaves(c, num_leaves);
   if (rc) return rc;
+  if (c->colsamp_on) {
+    // this tree's column sample (BeforeTrain's ResetByTree); the pinned copy is not
+    // rewritten before this tree completes (every tree ends with a stream wait)
+    c->colsamp.next_tree();
+    std::memcpy(c->feat_used_host, c->colsamp.used.data(), (size_t)c->F);
+    HIPCHK(c, hipMemcpyAsync(c->d_feat_used, c->feat_used_host, (size_t)c->F,
+                             hipMemcpyHostToDevice, c->stream));
+  }
   HIPCHK(c, hipMemcpyAsync((char*)c->ctl + CTL_OFF(cfg), cfg, sizeof(*cfg), hipMemcpyHostToDevice,
                            c->stream));
   const int32_t rounds = std::max(1, std::min(c->round_cap, num_leaves + 1));
@@ -798,6 +878,8 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   // pointing at buffers this call frees.
   c->have_bins = c->have_grad = c->quant_ready = c->have_labels = false;
   c->ahead = false;
+  c->colsamp_on = false;
+  c->have_rank = false;
   c->buf_gen++;
   if (c->graph_exec) {
     (void)hipGraphExecDestroy(c->graph_exec);
@@ -931,9 +1013,18 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
 
 // BinaryLogloss::get_gradients on the resident score, then the f32 pair prep or the
 // quantizer with iteration `iter`'s seed (gbdt.rs:945-960).
-void enqueue_objective(lgbm_hip_ctx* c, int32_t iter, int32_t qbins, int32_t stochastic) {
+void enqueue_objective(lgbm_hip_ctx* c, int32_t objective, int32_t iter, int32_t qbins,
+                       int32_t stochastic) {
   ev_begin(c, FAM_OBJ);
-  launch_grad_binary(c->score, c->label, c->g, c->h, c->N, c->partials, c->stream);
+  if (objective == LGBM_HIP_OBJECTIVE_BINARY) {
+    launch_grad_binary(c->score, c->label, c->g, c->h, c->N, c->partials, c->stream);
+  } else {
+    if (objective == LGBM_HIP_OBJECTIVE_REGRESSION)
+      launch_grad_l2(c->score, c->label, c->g, c->h, c->N, c->stream);
+    else
+      launch_grad_lambdarank(c->score, c->label, c->rank, c->g, c->h, c->stream);
+    if (qbins) launch_absmax(c->g, c->h, c->N, c->partials, c->stream);  // quantizer statistics
+  }
   ev_end(c);
   c->have_grad = true;
   if (qbins == 0) {
@@ -1053,6 +1144,13 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->hist_acc);
   F(c->hist_acc64);
   F(c->binmat);
+  F(c->rk_qb);
+  F(c->rk_imd);
+  F(c->rk_table);
+  F(c->rk_disc);
+  F(c->rk_gain);
+  F(c->d_feat_used);
+  if (c->feat_used_host) (void)hipHostFree(c->feat_used_host);
   F(c->cat_bits);
   F(c->part_slots);
   F(c->hist_part64);
@@ -1886,16 +1984,22 @@ int lgbm_hip_set_labels(lgbm_hip_ctx* c, const float* labels, int64_t n, double 
   HIPCHK(c, hipMemcpy(c->score, s.data(), (size_t)n * 8, hipMemcpyHostToDevice));
   c->num_class = 1;
   c->have_labels = true;
+  c->have_rank = false;  // the lambdarank tables were built from the old labels
   return LGBM_HIP_OK;
 }
 
-int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_config* cfg,
-                               int32_t num_leaves, int32_t max_depth, double learning_rate,
-                               int32_t num_grad_quant_bins, int32_t stochastic,
-                               lgbm_tree_out* tree) {
+}  // extern "C"
+
+namespace {
+// One resident boosting iteration of a one-tree-per-iteration objective.
+int train_iter_single(lgbm_hip_ctx* c, int32_t objective, int32_t iter, const lgbm_gain_config* cfg,
+                      int32_t num_leaves, int32_t max_depth, double learning_rate,
+                      int32_t num_grad_quant_bins, int32_t stochastic, lgbm_tree_out* tree) {
   int rc = check_ctx(c);
   if (rc) return rc;
   if (!c->have_labels) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set labels first");
+  if (objective == LGBM_HIP_OBJECTIVE_LAMBDARANK && !c->have_rank)
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "lambdarank needs lgbm_hip_set_lambdarank");
   if (c->num_class != 1)
     return set_err(c, LGBM_HIP_ERR_RUNTIME, "the resident labels are multiclass");
   if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
@@ -1916,9 +2020,9 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
     if ((rc = ensure_leaves(c, num_leaves))) return rc;
   }
   const bool pro = c->ahead && c->ahead_iter == iter && c->ahead_qbins == num_grad_quant_bins &&
-                   c->ahead_stoch == stochastic;
+                   c->ahead_stoch == stochastic && c->ahead_obj == objective;
   c->ahead = false;
-  if (!pro) enqueue_objective(c, iter, num_grad_quant_bins, stochastic);
+  if (!pro) enqueue_objective(c, objective, iter, num_grad_quant_bins, stochastic);
   if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
   DevLearner L = make_learner(c);
   KernelEvents ke;
@@ -1931,16 +2035,187 @@ int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_co
     HIPCHK(c, hipMemcpyAsync(c->tree_host, c->tree_blob, tree ? c->tree_blob_bytes : 64,
                              hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipEventRecord(c->tree_ev, c->stream));
-    enqueue_objective(c, iter + 1, num_grad_quant_bins, stochastic);
+    enqueue_objective(c, objective, iter + 1, num_grad_quant_bins, stochastic);
     HIPCHK(c, hipGetLastError());
     c->ahead = true;
     c->ahead_iter = iter + 1;
     c->ahead_qbins = num_grad_quant_bins;
     c->ahead_stoch = stochastic;
+    c->ahead_obj = objective;
     HIPCHK(c, hipEventSynchronize(c->tree_ev));
     return finish_tree(c, tree, nullptr, learning_rate, true);
   }
   return finish_tree(c, tree, nullptr, learning_rate);
+}
+
+// DCGCalculator::cal_max_dcg_at_k (lgbm-metric/src/dcg_calculator.rs:142-165)
+double max_dcg_at_k(const std::vector<double>& gain, const std::vector<double>& disc, int32_t k,
+                    const float* labels, int32_t cnt) {
+  std::vector<int64_t> n_of((size_t)gain.size(), 0);
+  for (int32_t i = 0; i < cnt; ++i) n_of[(size_t)labels[i]] += 1;
+  int64_t top = (int64_t)gain.size() - 1;
+  double sum = 0.0;
+  for (int32_t j = 0; j < std::min(k, cnt); ++j) {
+    while (top > 0 && n_of[(size_t)top] <= 0) --top;
+    if (top < 0) break;
+    sum += disc[(size_t)j] * gain[(size_t)top];
+    n_of[(size_t)top] -= 1;
+  }
+  return sum;
+}
+}  // namespace
+
+extern "C" {
+
+int lgbm_hip_train_iter_binary(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_config* cfg,
+                               int32_t num_leaves, int32_t max_depth, double learning_rate,
+                               int32_t num_grad_quant_bins, int32_t stochastic,
+                               lgbm_tree_out* tree) {
+  return train_iter_single(c, LGBM_HIP_OBJECTIVE_BINARY, iter, cfg, num_leaves, max_depth,
+                           learning_rate, num_grad_quant_bins, stochastic, tree);
+}
+
+int lgbm_hip_train_iter(lgbm_hip_ctx* c, int32_t iter, const lgbm_gain_config* cfg,
+                        int32_t num_leaves, int32_t max_depth, double learning_rate,
+                        int32_t num_grad_quant_bins, int32_t stochastic, lgbm_tree_out* tree) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  return train_iter_single(c, c->objective, iter, cfg, num_leaves, max_depth, learning_rate,
+                           num_grad_quant_bins, stochastic, tree);
+}
+
+int lgbm_hip_set_objective(lgbm_hip_ctx* c, int32_t objective) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (objective != LGBM_HIP_OBJECTIVE_BINARY && objective != LGBM_HIP_OBJECTIVE_REGRESSION &&
+      objective != LGBM_HIP_OBJECTIVE_LAMBDARANK)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "unknown objective");
+  c->ahead = false;
+  c->objective = objective;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_set_lambdarank(lgbm_hip_ctx* c, const int32_t* query_boundaries, int32_t num_queries,
+                            double sigmoid, int32_t norm, int32_t truncation_level) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;
+  c->have_rank = false;
+  if (!c->have_labels || c->num_class != 1)
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "set the (single-score) labels first");
+  if (!query_boundaries || num_queries < 1)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "no query boundaries");
+  if (!(sigmoid > 0.0))
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "lambdarank sigmoid must be > 0");
+  // validate_query_boundaries (rank.rs:62-86)
+  if (query_boundaries[0] != 0 || query_boundaries[num_queries] != c->N)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "query boundaries must run from 0 to num_data");
+  int32_t max_q = 0;
+  for (int32_t q = 0; q < num_queries; ++q) {
+    const int32_t cnt = query_boundaries[q + 1] - query_boundaries[q];
+    if (cnt < 0)
+      return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "query boundaries must be non-decreasing");
+    max_q = std::max(max_q, cnt);
+  }
+  if (max_q > RANK_MAX_QUERY)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "a query holds more than " + std::to_string(RANK_MAX_QUERY) + " rows");
+  std::vector<float> lab((size_t)c->N);
+  HIPCHK(c, hipMemcpy(lab.data(), c->label, lab.size() * 4, hipMemcpyDeviceToHost));
+  // DefaultLabelGain and the discounts (dcg_calculator.rs:48-90); labels checked as
+  // DCGCalculator::check_labels does (integer, then in range)
+  std::vector<double> gain(31, 0.0), disc(RANK_DISCOUNTS);
+  for (int i = 1; i < 31; ++i) gain[(size_t)i] = (double)((1ll << i) - 1);
+  for (int i = 0; i < RANK_DISCOUNTS; ++i) disc[(size_t)i] = 1.0 / std::log2(2.0 + (double)i);
+  for (int64_t i = 0; i < c->N; ++i) {
+    const float l = lab[(size_t)i];
+    if (std::fabs(l - (float)(int32_t)l) > 1e-15f)
+      return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "ranking labels must be integers");
+    if (l < 0.0f || l >= 31.0f)
+      return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "ranking label outside the label gains");
+  }
+  std::vector<double> imd((size_t)num_queries);
+  for (int32_t q = 0; q < num_queries; ++q) {
+    const int32_t a = query_boundaries[q], cnt = query_boundaries[q + 1] - a;
+    double m = max_dcg_at_k(gain, disc, truncation_level, lab.data() + a, cnt);
+    imd[(size_t)q] = m > 0.0 ? 1.0 / m : m;
+  }
+  // ConstructSigmoidTable (rank.rs:170-182)
+  RankParams rp{};
+  rp.sigmoid = sigmoid;
+  rp.min_in = -50.0 / sigmoid / 2.0;
+  rp.max_in = -rp.min_in;
+  rp.idx_factor = (double)RANK_SIGMOID_BINS / (rp.max_in - rp.min_in);
+  rp.norm = norm ? 1 : 0;
+  rp.trunc = truncation_level;
+  std::vector<double> table(RANK_SIGMOID_BINS);
+  for (int32_t i = 0; i < RANK_SIGMOID_BINS; ++i) {
+    const double sc = (double)i / rp.idx_factor + rp.min_in;
+    table[(size_t)i] = 1.0 / (1.0 + std::exp(sc * sigmoid));
+  }
+  if ((rc = dalloc(c, &c->rk_qb, (size_t)num_queries + 1))) return rc;
+  if ((rc = dalloc(c, &c->rk_imd, (size_t)num_queries))) return rc;
+  if ((rc = dalloc(c, &c->rk_table, (size_t)RANK_SIGMOID_BINS))) return rc;
+  if ((rc = dalloc(c, &c->rk_disc, (size_t)RANK_DISCOUNTS))) return rc;
+  if ((rc = dalloc(c, &c->rk_gain, gain.size()))) return rc;
+  HIPCHK(c, hipMemcpy(c->rk_qb, query_boundaries, ((size_t)num_queries + 1) * 4, hipMemcpyHostToDevice));
+  HIPCHK(c, hipMemcpy(c->rk_imd, imd.data(), imd.size() * 8, hipMemcpyHostToDevice));
+  HIPCHK(c, hipMemcpy(c->rk_table, table.data(), table.size() * 8, hipMemcpyHostToDevice));
+  HIPCHK(c, hipMemcpy(c->rk_disc, disc.data(), disc.size() * 8, hipMemcpyHostToDevice));
+  HIPCHK(c, hipMemcpy(c->rk_gain, gain.data(), gain.size() * 8, hipMemcpyHostToDevice));
+  RankTables& t = c->rank;
+  t.qb = c->rk_qb;
+  t.inv_max_dcg = c->rk_imd;
+  t.table = c->rk_table;
+  t.discount = c->rk_disc;
+  t.gain = c->rk_gain;
+  t.p = rp;
+  t.num_queries = num_queries;
+  t.max_query = std::max(max_q, 1);
+  c->have_rank = true;
+  c->objective = LGBM_HIP_OBJECTIVE_LAMBDARANK;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_set_col_sampler(lgbm_hip_ctx* c, double feature_fraction,
+                             double feature_fraction_bynode, int32_t seed) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
+  if (!(feature_fraction_bynode >= 1.0))
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "feature_fraction_bynode < 1 is not supported");
+  if (!(feature_fraction > 0.0))
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "feature_fraction must be > 0");
+  c->ahead = false;
+  c->buf_gen++;  // the captured tree reads the mask pointer (or none)
+  if (!(feature_fraction < 1.0)) {  // no sampling: no draws (col_sampler.rs:98-103)
+    c->colsamp_on = false;
+    return LGBM_HIP_OK;
+  }
+  if ((rc = dalloc(c, &c->d_feat_used, (size_t)c->F))) return rc;
+  if (c->feat_used_host) (void)hipHostFree(c->feat_used_host);
+  c->feat_used_host = nullptr;
+  HIPCHK(c, hipHostMalloc((void**)&c->feat_used_host, (size_t)c->F, hipHostMallocDefault));
+  c->colsamp.start(feature_fraction, seed, c->F);  // the construction draw
+  c->colsamp_on = true;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_boost_from_score(int32_t objective, const float* label, int64_t n, double* out) {
+  if (!out || n < 0 || (n > 0 && !label)) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  if (objective == LGBM_HIP_OBJECTIVE_BINARY)
+    return lgbm_hip_binary_boost_from_score(label, n, 1.0, out);
+  if (objective == LGBM_HIP_OBJECTIVE_LAMBDARANK) {  // no init score (boosting objective.rs:112-116)
+    *out = 0.0;
+    return LGBM_HIP_OK;
+  }
+  if (objective != LGBM_HIP_OBJECTIVE_REGRESSION) return LGBM_HIP_ERR_INVALID_ARGUMENT;
+  // Objective::Regression::boost_from_score (regression.rs:563-575): the ordered
+  // f64 label mean
+  double sum = 0.0;
+  for (int64_t i = 0; i < n; ++i) sum += (double)label[i];
+  *out = n > 0 ? sum / (double)n : 0.0;
+  return LGBM_HIP_OK;
 }
 
 int lgbm_hip_set_labels_multiclass(lgbm_hip_ctx* c, const float* labels, int64_t n,
@@ -1976,6 +2251,7 @@ int lgbm_hip_set_labels_multiclass(lgbm_hip_ctx* c, const float* labels, int64_t
   HIPCHK(c, hipMemcpy(c->score, s.data(), kn * 8, hipMemcpyHostToDevice));
   c->num_class = num_class;
   c->have_labels = true;
+  c->have_rank = false;
   return LGBM_HIP_OK;
 }
 

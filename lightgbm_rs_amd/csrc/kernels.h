@@ -118,6 +118,7 @@ struct DevLearner {
   int32_t acc_cells;          // cells per accumulator: total_cells, + 1 (row totals) when wide
   const uint8_t* binmat;      // wide layout: row-major bins [N][row_stride]
   int64_t row_stride;
+  const uint8_t* feat_used;   // per feature position: the tree's column sample (NULL: all)
   unsigned long long* part_slots;  // [part blocks + SPEC_MAX][total_cells] packed (block, job) cells
   // f32-gradient training: 64-bit fixed-point (g, h) cells
   int64_t* hist_part64;       // [HIST_SLOTS][total_cells][2]
@@ -140,6 +141,26 @@ struct DevLearner {
   DevLeaves leaves;
   DevTree tree;
   RowBufs bufs;
+};
+
+// LambdaRank on the device (objective.hip): one RANK_THREADS block per query of at
+// most RANK_MAX_QUERY rows; the tables are built on the host.
+#define RANK_THREADS 128
+#define RANK_SIGMOID_BINS (1024 * 1024)
+#define RANK_MAX_QUERY 2048
+#define RANK_DISCOUNTS 10000
+struct RankParams {
+  double sigmoid, min_in, max_in, idx_factor;
+  int32_t norm, trunc;
+};
+struct RankTables {
+  const int32_t* qb;           // [num_queries + 1] query boundaries
+  const double* inv_max_dcg;   // [num_queries]
+  const double* table;         // [RANK_SIGMOID_BINS] 1 / (1 + exp(score * sigmoid))
+  const double* discount;      // [RANK_DISCOUNTS] 1 / log2(2 + i)
+  const double* gain;          // label gains (31)
+  RankParams p;
+  int32_t num_queries, max_query;
 };
 
 namespace lgbm {
@@ -182,6 +203,10 @@ void launch_bin_records(const void* x, int32_t f64, int32_t col_major, int64_t n
 void launch_absmax(const float* g, const float* h, int64_t n, uint4* partials, hipStream_t s);
 void launch_grad_binary(const double* score, const float* label, float* g, float* h, int64_t n,
                         uint4* partials, hipStream_t s);
+void launch_grad_l2(const double* score, const float* label, float* g, float* h, int64_t n,
+                    hipStream_t s);
+void launch_grad_lambdarank(const double* score, const float* label, const RankTables& t,
+                            float* g, float* h, hipStream_t s);
 void launch_grad_softmax(const double* score, const float* label, float* g, float* h, int64_t n,
                          int32_t K, double factor, hipStream_t s);
 void launch_quant_scales(Ctl* ctl, const uint4* partials, int64_t n, int32_t bins,

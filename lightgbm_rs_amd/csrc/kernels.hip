@@ -845,7 +845,9 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
   for (int i = tid; i < 2 * nb; i += SCAN_THREADS) L.slots[ft.slot_off + i] = cs[i];
   if (tid >= LGBM_WAVE) return;
   lgbm_split_info* out = L.feat_split + f;
-  if (ctl->root_skip || !(sh > 0.0 && nrows > 0)) {
+  // a feature outside the tree's column sample is never scanned (learner.rs:1932-1990)
+  const bool sampled_out = L.feat_used && !L.feat_used[f];
+  if (ctl->root_skip || !(sh > 0.0 && nrows > 0) || sampled_out) {
     if (lane_id() == 0) {
       split_set_none(out);
       L.splittable[f] = 0;
