@@ -19,6 +19,8 @@ default_bin, missing type and the offset rule come from the mappers.  With `devi
 set to a torch CUDA device the generation and a quantile binning run there (same
 recipe, torch's generator).
 """
+import os
+
 import numpy as np
 
 from ._abi import FeatureMeta
@@ -218,9 +220,10 @@ def config2_raw_host(n, seed=0x5EED0002, F=2000, informative=50):
     x * U(-1, 1) + N(0, 0.5)."""
     rng = np.random.default_rng(seed)
     X = np.zeros((F, n), dtype=np.float32)
-    for f in range(F):
-        nz = rng.random(n) < 0.1
-        X[f, nz] = np.exp(rng.standard_normal(int(nz.sum()))).astype(np.float32)
+    for f0 in range(0, F, 64):  # 64 features per draw
+        blk = X[f0:f0 + 64]
+        nz = rng.random(blk.shape, dtype=np.float32) < 0.1
+        blk[nz] = np.exp(rng.standard_normal(int(nz.sum()), dtype=np.float32))
     feats = rng.choice(F, size=informative, replace=False)
     w = rng.uniform(-1.0, 1.0, informative)
     y = (X[feats].astype(np.float64).T @ w + rng.normal(0.0, 0.5, n)).astype(np.float32)
@@ -233,6 +236,21 @@ def config2_binned(n, seed=0x5EED0002, F=2000, max_bin=255):
     return bins, meta, upper, y
 
 
+def sample_mappers(X, max_bin, min_data_in_leaf=20):
+    """One BinMapper per feature row of X [F, n] from find_bin_from_column's
+    200000-row sample (data_random_seed 1): the mappers lgbm_hip_upload_raw bins with."""
+    from concurrent.futures import ThreadPoolExecutor
+    from .binning import BinMapper, sample_indices
+    F, n = X.shape
+    idx = sample_indices(n, 200000, 1)
+
+    def one(f):  # the C++ mapper construction runs without the GIL
+        return BinMapper.from_sampled_column(X[f, idx].astype(np.float64), n, max_bin=max_bin,
+                                             min_data_in_leaf=min_data_in_leaf)
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+        return list(ex.map(one, range(F)))
+
+
 def config4_raw_host(n, seed=0x5EED0004, F=700, mean_group=120):
     """configs[4]'s raw table: X float32 [F, n] ~U(0, 1) with 30% zeros, query groups of
     Poisson(mean_group) sizes (at least 1; the last one cut at n), graded relevance 0-4
@@ -240,7 +258,9 @@ def config4_raw_host(n, seed=0x5EED0004, F=700, mean_group=120):
     float32, group sizes int32)."""
     rng = np.random.default_rng(seed)
     X = rng.random((F, n), dtype=np.float32)
-    X[rng.random((F, n)) < 0.3] = 0.0
+    for f0 in range(0, F, 64):  # 30% zeros, 64 features per draw
+        blk = X[f0:f0 + 64]
+        blk[rng.random(blk.shape, dtype=np.float32) < 0.3] = 0.0
     w = rng.standard_normal(F)
     s = X.astype(np.float64).T @ w
     s += rng.normal(0.0, float(np.std(s)) * 0.5 + 1e-12, n)

@@ -237,3 +237,64 @@ def test_feature_fraction_real_binary_on_device(cell):
     for t, w in zip(trees, want):
         assert sorted(set(int(v) for v in t["split_feature"][:t["num_leaves"] - 1])) == w
     np.testing.assert_allclose(scores, z["pred_bits"][cell].view(np.float64), rtol=1e-9, atol=1e-12)
+
+
+# --- configs[2] and configs[4] at their full sizes ------------------------------------
+def _full_chain(X, ms, y, objective, nl, qbins, feature_fraction=1.0, qb=None):
+    """The library's own chain: device binning of the raw table (lgbm_hip_upload_raw,
+    wide layout) -> one resident boosting iteration; returns the device's bins too."""
+    init = boost_from_score(objective, y)
+    cfg = GainConfig.make(min_data_in_leaf=20)
+    b = HipBackend(0)
+    try:
+        b.upload_raw(X, ms, col_major=True)
+        bins = b.get_bins()
+        b.set_labels(y, init if abs(init) > float(np.float32(1e-15)) else 0.0)
+        if objective == "lambdarank":
+            b.set_lambdarank(qb)
+        else:
+            b.set_objective(objective)
+        if feature_fraction < 1.0:
+            b.set_col_sampler(feature_fraction, 1.0, 2)
+        trees = [b.train_iter(0, cfg, nl, -1, 0.1, qbins, True)]
+        scores = b.scores()
+    finally:
+        b.close()
+    meta = [feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f)
+            for f, m in enumerate(ms)]
+    ub = np.concatenate([m.upper_bounds for m in ms])
+    return trees, scores, init, bins, meta, ub, cfg
+
+
+def test_config2_full_size():
+    """1,000,000 x 2,000 (90% zeros, LogNormal nonzeros), L2, f32
+    gradients, feature_fraction 0.8, max_bin 255, 127 leaves: one iteration."""
+    from lightgbm_rs_amd.synth import config2_raw_host, sample_mappers
+    n, F, nl = 1_000_000, 2000, 127
+    X, y = config2_raw_host(n, F=F)
+    ms = sample_mappers(X, 255)
+    say(f"configs[2] full size {n} x {F}: {sum(m.num_bin for m in ms)} cells")
+    trees, scores, init, bins, meta, ub, cfg = _full_chain(X, ms, y, "regression", nl, 0, 0.8)
+    del X
+    say("device done")
+    oscores, otrees = oracle.train(bins, meta, ub, y, cfg, oracle.OBJECTIVE_REGRESSION, nl, -1, 1,
+                                   0.1, quantized=False, feature_fraction=0.8,
+                                   feature_fraction_seed=2)
+    compare(trees, scores, otrees, oscores, init, "configs[2] full", exact=False)
+
+
+def test_config4_full_size():
+    """2,000,000 x 700 (U(0,1), 30% zeros), Poisson(120) queries,
+    lambdarank, quantized int8 gradients, max_bin 255, 255 leaves: one iteration."""
+    from lightgbm_rs_amd.synth import config4_raw_host, sample_mappers
+    n, F, nl = 2_000_000, 700, 255
+    X, rel, groups = config4_raw_host(n, F=F)
+    qb = np.concatenate([[0], np.cumsum(groups)]).astype(np.int32)
+    ms = sample_mappers(X, 255)
+    say(f"configs[4] full size {n} x {F}, {len(groups)} queries")
+    trees, scores, init, bins, meta, ub, cfg = _full_chain(X, ms, rel, "lambdarank", nl, 4, qb=qb)
+    del X
+    say("device done")
+    oscores, otrees = oracle.train(bins, meta, ub, rel, cfg, oracle.OBJECTIVE_LAMBDARANK, nl, -1, 1,
+                                   0.1, quantized=True, query_boundaries=qb)
+    compare(trees, scores, otrees, oscores, 0.0, "configs[4] full", exact=True)
