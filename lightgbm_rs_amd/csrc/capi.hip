@@ -195,6 +195,7 @@ struct lgbm_hip_ctx {
   int32_t* hist_sum = nullptr;   // [cells][3]
   int32_t* hist_acc = nullptr;   // [SPEC_MAX][acc_cells][3]
   int64_t* hist_acc64 = nullptr;  // wide layout: [SPEC_MAX][acc_cells][2]
+  unsigned long long* wide_part = nullptr;  // wide layout: per-chunk partial cells
   int32_t acc_cells = 0;          // total_cells (+ 1 totals cell in the wide layout)
   unsigned long long* part_slots = nullptr;  // [part_blocks + SPEC_MAX][cells] packed
   int64_t* hist_part64 = nullptr;  // [HIST_SLOTS][cells][2]
@@ -365,6 +366,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.hist_sum = c->hist_sum;
   L.hist_acc = c->hist_acc;
   L.hist_acc64 = c->hist_acc64;
+  L.wide_part = c->wide_part;
   L.acc_cells = c->acc_cells;
   L.binmat = c->binmat;
   L.row_stride = c->row_stride;
@@ -976,12 +978,15 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
     if ((rc = dalloc(c, &c->binmat, (size_t)num_data * (size_t)c->row_stride))) return rc;
     if ((rc = dalloc(c, &c->hist_acc64, (size_t)SPEC_MAX * c->acc_cells * 2))) return rc;
     HIPCHK(c, hipMemset(c->hist_acc64, 0, (size_t)SPEC_MAX * c->acc_cells * 2 * 8));
+    if ((rc = dalloc(c, &c->wide_part, wide_part_words(F, num_data, (int32_t)acc)))) return rc;
   } else {
     c->row_stride = 0;
     if (c->binmat) (void)hipFree(c->binmat);
     if (c->hist_acc64) (void)hipFree(c->hist_acc64);
+    if (c->wide_part) (void)hipFree(c->wide_part);
     c->binmat = nullptr;
     c->hist_acc64 = nullptr;
+    c->wide_part = nullptr;
     if (acc > (uint32_t)(MAX_FGROUPS - 1) * (HIST_FP_CELLS - 256))
       return set_err(c, LGBM_HIP_ERR_CAPABILITY, "too many histogram cells for the f32 feature groups");
   }
@@ -1143,6 +1148,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->hist_sum);
   F(c->hist_acc);
   F(c->hist_acc64);
+  F(c->wide_part);
   F(c->binmat);
   F(c->rk_qb);
   F(c->rk_imd);

@@ -71,8 +71,8 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
   const int nthr = gridDim.x * blockDim.x;
   for (int i = tid; i < L.F; i += nthr) L.splittable[i] = 1;  // node slot 0
   if (rec_wide(L.fmt)) {
-    // the readers clear every cell they read; the totals cells only the root build
-    // writes (job 0), read by every root scan block
+    // the histogram cells go to per-chunk slots that every launch overwrites; the
+    // totals cells gather atomic adds of the root build (job 0)
     for (int j = tid; j < SPEC_MAX; j += nthr) {
       const size_t t = (size_t)j * L.acc_cells + L.total_cells;
       if (fp_mode) {
@@ -992,21 +992,21 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
   const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
   const bool wide = rec_wide(L.fmt);
   if (fp_mode) {
-    // f32 gradients: the smaller child from its k_hist_f32 partial slots (wide: its
-    // accumulator, read and cleared); the larger = parent - smaller, exact in 64-bit
+    // f32 gradients: the smaller child from its partial slots (k_hist_f32's, or the
+    // wide layout's per-chunk ones); the larger = parent - smaller, exact in 64-bit
     // fixed point
     const int32_t a0 = ctl->hjobs[j].a0, na = ctl->hjobs[j].nblk;
     const double gu = ldexp(1.0, -ctl->g_shift), hu = ldexp(1.0, -ctl->h_shift);
-    int64_t* acc64 = L.hist_acc64 + (size_t)j * L.acc_cells * 2;
     if (!gated) {
       for (int b = tid; b < nb; b += SCAN_THREADS) {
         const size_t ci = (size_t)(ft.cell_base + b);
-        long long SG, SH;
+        long long SG = 0, SH = 0;
         if (wide) {
-          SG = acc64[2 * ci];
-          SH = acc64[2 * ci + 1];
-          acc64[2 * ci] = 0;
-          acc64[2 * ci + 1] = 0;
+          for (int k = 0; k < na; ++k) {
+            const unsigned long long* wp = L.wide_part + ((size_t)(a0 + k) * cells + ci) * 2;
+            SG += (long long)wp[0];
+            SH += (long long)wp[1];
+          }
         } else {
           hist_part_sum64(L, a0, na, ci, &SG, &SH);
         }
@@ -1027,12 +1027,13 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
     // first tile to the one holding its last, slot = block + j; blocks without tiles
     // wrote nothing), plus the job's accumulator when a flush used it (read and
     // cleared even when the children are gated)
-    // (wide: k_hist_wide's accumulator)
+    // (wide: k_hist_wide's per-chunk slots)
     const int64_t s0 = jnt > 0 ? part_owner(jt0, T, part_grid) : 0;
     const int64_t s1 = jnt > 0 ? part_owner(jt0 + jnt - 1, T, part_grid) : -1;
     const bool use_slots =
         !wide && (jnt > 0 ? part_span_blocks(jt0, jnt, T, part_grid) <= PART_SLOT_MAX : true);
-    const bool read_acc = !use_slots || acc_used != 0;
+    const bool read_acc = !wide && (!use_slots || acc_used != 0);
+    const int32_t wa0 = ctl->hjobs[j].a0, wna = wide ? ctl->hjobs[j].nblk : 0;
     int32_t* acc = L.hist_acc + (size_t)j * L.acc_cells * 3;
     const unsigned long long* slots = L.part_slots;
 #pragma unroll
@@ -1049,6 +1050,13 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
         a[0] = 0;
         a[1] = 0;
         a[2] = 0;
+      }
+      for (int k = 0; k < wna; ++k) {
+        int32_t g_, h_, t_;
+        unpack_cell(L.wide_part[(size_t)(wa0 + k) * cells + ci], &g_, &h_, &t_);
+        AG += g_;
+        AH += h_;
+        AT += t_;
       }
       if (use_slots) {
         // at most PART_SLOT_MAX blocks, enumerated without a dependent chain so all

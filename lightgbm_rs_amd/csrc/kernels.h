@@ -115,6 +115,7 @@ struct DevLearner {
   int32_t* hist_sum;          // [total_cells][3] job 0's partials summed (k_hist_reduce)
   int32_t* hist_acc;          // [SPEC_MAX][acc_cells][3] per-job accumulators
   int64_t* hist_acc64;        // wide layout, f32 gradients: [SPEC_MAX][acc_cells][2]
+  unsigned long long* wide_part;  // wide layout: per-chunk partial cells [chunks][cells][1 or 2]
   int32_t acc_cells;          // cells per accumulator: total_cells, + 1 (row totals) when wide
   const uint8_t* binmat;      // wide layout: row-major bins [N][row_stride]
   int64_t row_stride;
@@ -255,6 +256,8 @@ void launch_pack_wide(const uint8_t* bins, int64_t n, int32_t F, int64_t stride,
                       uint4* rec, hipStream_t s);
 // Opts the wide histogram kernels into their LDS size (outside graph capture); 0 = ok.
 int wide_prepare();
+// u64 words of the wide layout's per-chunk partial histogram slots
+size_t wide_part_words(int32_t F, int64_t N, int32_t cells);
 // ConstructHistogram of the launch's histogram jobs into the per-job accumulators
 void launch_hist_wide(const DevLearner& L, int fp, hipStream_t s, const KernelEvents* ev = nullptr);
 // raw values -> the row-major matrix (ValueToBin per feature group, bounds in LDS)

@@ -713,8 +713,8 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_f32(DevLearner L) {
 //                   (exact, from the integer totals), FixHistogram, compaction, and
 //                   the root's FindBestThreshold (wave 0).
 //   mode 2 (build): per-op build into `explicit_out` (no scan).
-// The integer cells are the sum of histogram job 0's partial slots; in the wide layout
-// job 0's accumulator (read and cleared), whose totals cell holds the root sums (its
+// The integer cells are the sum of histogram job 0's partial slots (the wide layout's
+// per-chunk slots); the wide layout's root sums come from its totals cell (its
 // most-frequent-bin cells are not accumulated).
 // ===========================================================================
 __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t mode,
@@ -738,10 +738,11 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
     if (fp) {
       long long G = 0, H = 0;
       if (wide) {
-        G = L.hist_acc64[2 * ci];
-        H = L.hist_acc64[2 * ci + 1];
-        L.hist_acc64[2 * ci] = 0;
-        L.hist_acc64[2 * ci + 1] = 0;
+        for (int k = 0; k < na; ++k) {
+          const unsigned long long* wp = L.wide_part + ((size_t)(a0 + k) * L.total_cells + ci) * 2;
+          G += (long long)wp[0];
+          H += (long long)wp[1];
+        }
       } else {
         hist_part_sum64(L, a0, na, ci, &G, &H);
       }
@@ -756,12 +757,19 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
       th += H;
       continue;
     }
-    int32_t* hs = (wide ? L.hist_acc : L.hist_sum) + ci * 3;
-    const int32_t G = hs[0], H = hs[1], T = hs[2];
+    int32_t G = 0, H = 0, T = 0;
     if (wide) {
-      hs[0] = 0;
-      hs[1] = 0;
-      hs[2] = 0;
+      for (int k = 0; k < na; ++k) {
+        int32_t g_, h_, t_;
+        unpack_cell(L.wide_part[(size_t)(a0 + k) * L.total_cells + ci], &g_, &h_, &t_);
+        G += g_;
+        H += h_;
+        T += t_;
+      }
+    } else {
+      G = L.hist_sum[ci * 3];
+      H = L.hist_sum[ci * 3 + 1];
+      T = L.hist_sum[ci * 3 + 2];
     }
     if (mode == 1) {
       int32_t* ps = L.int_slots + ci * 3;  // node slot 0

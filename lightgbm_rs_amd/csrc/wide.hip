@@ -13,9 +13,10 @@
 // WIDE_GF_F = 32 with 64-bit fixed-point (g, h) cells: 128 KiB of LDS either way)
 // and a contiguous chunk of one job's rows.  Each thread takes a row at a time: its
 // index, its pair, and the group's bytes of its binmat row in 16-byte loads; then one
-// LDS atomic per (row, feature).  The block's cells go to the job's accumulator with
-// global atomic adds (zero cells skipped); the reader (k_fixscan for the root,
-// k_pair_scan for the children) clears them.
+// LDS atomic per (row, feature).  The block stores its group's cells, as they are in
+// LDS, into its chunk's partial slot (plain stores; the launch's chunk a owns slot a);
+// the reader (k_fixscan for the root, k_pair_scan for the children) sums the job's
+// chunks (HistJob a0 / nblk).
 //
 // The most frequent bin of a feature is never accumulated.  The scans never read
 // that cell's own sum: FixHistogram (fix_histogram.rs:50-80) overwrites it with the
@@ -76,6 +77,11 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
   int32_t j = -1;
   for (int k = 0; k < nj; ++k)
     if (a >= s_a0[k] && a < s_a0[k] + s_nb[k]) j = k;
+  if (tid == 0 && blockIdx.x == 0 && blockIdx.y == 0)
+    for (int k = 0; k < nj; ++k) {  // the readers' chunk ranges
+      ctl->hjobs[k].a0 = s_a0[k];
+      ctl->hjobs[k].nblk = s_nb[k];
+    }
   if (j < 0) return;
   const int f1 = min(f0 + GF, F);
   const int gbase = (int)L.feats[f0].cell_base;
@@ -175,24 +181,10 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
   }
   __syncthreads();
   const size_t ac = (size_t)L.acc_cells;
-  if constexpr (FP) {
-    unsigned long long* acc = (unsigned long long*)L.hist_acc64 + ((size_t)j * ac + gbase) * 2;
-    for (int c = tid; c < gcells; c += WIDE_THREADS) {
-      const unsigned long long G = lds[2 * c], H = lds[2 * c + 1];
-      if (G) atomicAdd(&acc[2 * c], G);
-      if (H) atomicAdd(&acc[2 * c + 1], H);
-    }
-  } else {
-    int32_t* acc = L.hist_acc + ((size_t)j * ac + gbase) * 3;
-    for (int c = tid; c < gcells; c += WIDE_THREADS) {
-      const unsigned long long p = lds[c];
-      if (p == 0ull) continue;
-      int32_t g, h, t;
-      unpack_cell(p, &g, &h, &t);
-      if (g) atomicAdd(&acc[3 * c], g);
-      if (h) atomicAdd(&acc[3 * c + 1], h);
-      if (t) atomicAdd(&acc[3 * c + 2], t);
-    }
+  {
+    constexpr int CW = FP ? 2 : 1;  // u64 words per cell
+    unsigned long long* dst = L.wide_part + ((size_t)a * cells + gbase) * CW;
+    for (int c = tid; c < gcells * CW; c += WIDE_THREADS) dst[c] = lds[c];
   }
   if (totals) {
 #pragma unroll
@@ -252,6 +244,20 @@ size_t wide_lds_bytes(int fp) {
   return (size_t)(fp ? WIDE_GF_F * 256 * 16 : WIDE_GF_Q * 256 * 8);
 }
 
+// Blocks per feature group of a launch (row chunks + one per job at most): rows per
+// chunk stay <= WIDE_MAX_ROWS, and the grid fills the chip.
+int64_t wide_grid_x(int32_t F, int64_t N, int fp) {
+  const int GF = fp ? WIDE_GF_F : WIDE_GF_Q;
+  const int ng = (F + GF - 1) / GF;
+  int64_t chunks = std::max<int64_t>(WIDE_GRID / ng, (N + WIDE_MAX_ROWS - 1) / WIDE_MAX_ROWS);
+  return std::max<int64_t>(chunks, 1) + SPEC_MAX;
+}
+
+// u64 words of the partial slots: every chunk of either gradient mode's launch
+size_t wide_part_words(int32_t F, int64_t N, int32_t cells) {
+  return std::max((size_t)wide_grid_x(F, N, 1) * 2, (size_t)wide_grid_x(F, N, 0)) * (size_t)cells;
+}
+
 // Opt the histogram kernels into their LDS size (outside any graph capture).
 int wide_prepare() {
   if (hipFuncSetAttribute((const void*)k_hist_wide<0>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -266,9 +272,7 @@ int wide_prepare() {
 void launch_hist_wide(const DevLearner& L, int fp, hipStream_t s, const KernelEvents* ev) {
   const int GF = fp ? WIDE_GF_F : WIDE_GF_Q;
   const int ng = (L.F + GF - 1) / GF;
-  int64_t chunks = std::max<int64_t>(WIDE_GRID / ng, (L.N + WIDE_MAX_ROWS - 1) / WIDE_MAX_ROWS);
-  chunks = std::max<int64_t>(chunks, 1);
-  const dim3 g((unsigned)(chunks + SPEC_MAX), (unsigned)ng), blk(WIDE_THREADS);
+  const dim3 g((unsigned)wide_grid_x(L.F, L.N, fp), (unsigned)ng), blk(WIDE_THREADS);
   if (fp)
     KLAUNCH(ev, k_hist_wide<1>, g, blk, wide_lds_bytes(1), s, L);
   else
