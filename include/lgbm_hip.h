@@ -525,8 +525,20 @@ int lgbm_hip_upload_raw(lgbm_hip_ctx* ctx, const void* values, int32_t dtype, in
                         int64_t num_rows, int32_t num_cols,
                         const lgbm_hip_bin_mapper* const* mappers);
 /* The resident bins, feature-major [num_features][num_data] (no reference
- * counterpart: the reference's FeatureColumn.bins are host data). */
+ * counterpart: the reference's FeatureColumn.bins are host data); refused when a
+ * feature holds more than 256 bins (lgbm_hip_get_bins16). */
 int lgbm_hip_get_bins(lgbm_hip_ctx* ctx, uint8_t* out, int64_t num_data);
+/* The same as 2-byte bins (any resident layout). */
+int lgbm_hip_get_bins16(lgbm_hip_ctx* ctx, uint16_t* out, int64_t num_data);
+
+/* 2-byte bin columns (`BinColumn::U16`, lgbm-compute/src/lib.rs:75-211;
+ * `resident_bin_width`, :3752): like lgbm_hip_upload_bins for features of up to 4096
+ * bins (categorical ones at most 256).  A feature of more than 256 bins selects the
+ * wide row layout with 2-byte bins; otherwise the columns are stored as 1-byte bins.
+ * lgbm_hip_upload_raw[_device] take mappers of up to 4096 bins the same way. */
+int lgbm_hip_upload_bins16(lgbm_hip_ctx* ctx, const uint16_t* bins, int32_t num_features,
+                           int64_t num_data, const lgbm_feature_meta* meta,
+                           const double* bin_upper_bound);
 
 /* ---- models and batch prediction ------------------------------------------ */
 

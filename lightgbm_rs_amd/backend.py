@@ -88,13 +88,20 @@ class HipBackend:
 
     # ---- resident data -------------------------------------------------------
     def upload_resident_bins(self, bins_feature_major, meta, bin_upper_bound=None):
-        """`Backend::upload_resident_bins` (lib.rs:1564): bins [F, N] u8."""
-        b = np.ascontiguousarray(bins_feature_major, dtype=np.uint8)
-        F, N = b.shape
+        """`Backend::upload_resident_bins` (lib.rs:1564): bins [F, N] u8, or u16
+        (lgbm_hip_upload_bins16) when given as uint16."""
         marr = _feature_meta_array(meta)
         ub = None if bin_upper_bound is None else np.ascontiguousarray(bin_upper_bound, np.float64)
-        self._check(self.lib.lgbm_hip_upload_bins(self.ctx, ptr(b, C.c_uint8), C.c_int32(F),
-                                                  C.c_int64(N), marr, ptr(ub, C.c_double)))
+        if np.asarray(bins_feature_major).dtype == np.uint16:
+            b = np.ascontiguousarray(bins_feature_major, dtype=np.uint16)
+            F, N = b.shape
+            self._check(self.lib.lgbm_hip_upload_bins16(self.ctx, ptr(b, C.c_uint16), C.c_int32(F),
+                                                        C.c_int64(N), marr, ptr(ub, C.c_double)))
+        else:
+            b = np.ascontiguousarray(bins_feature_major, dtype=np.uint8)
+            F, N = b.shape
+            self._check(self.lib.lgbm_hip_upload_bins(self.ctx, ptr(b, C.c_uint8), C.c_int32(F),
+                                                      C.c_int64(N), marr, ptr(ub, C.c_double)))
         self.num_data, self.num_features = N, F
         self.slot_len = 2 * sum(m.num_bin for m in meta)
 

@@ -208,6 +208,15 @@ def _get_bins(self):
     return out
 
 
+def _get_bins16(self):
+    """The resident bins as uint16 [features, rows] (any bin width)."""
+    out = np.zeros((self.num_features, self.num_data), np.uint16)
+    self._check(self.lib.lgbm_hip_get_bins16(self.ctx, out.ctypes.data_as(C.c_void_p),
+                                             C.c_int64(self.num_data)))
+    return out
+
+
+HipBackend.get_bins16 = _get_bins16
 HipBackend.upload_raw = _upload_raw
 HipBackend.upload_raw_device = _upload_raw_device
 HipBackend.get_bins = _get_bins

@@ -23,6 +23,7 @@ __device__ __forceinline__ int32_t sat_i32(double x) {
   return (int32_t)x;
 }
 
+template <int TOP = 128>  // the largest binary-lifting step: num_bin <= 2 * TOP
 __device__ __forceinline__ uint32_t bin_of(const DevBinFeature& f, const double* ub,
                                            const int2* __restrict__ cats, double v) {
   if (v != v) {
@@ -39,7 +40,7 @@ __device__ __forceinline__ uint32_t bin_of(const DevBinFeature& f, const double*
     const double* u = ub + f.off;
     int32_t pos = 0;
 #pragma unroll
-    for (int32_t step = 128; step > 0; step >>= 1)
+    for (int32_t step = TOP; step > 0; step >>= 1)
       if (pos + step <= f.last && u[pos + step - 1] < v) pos += step;
     return (uint32_t)pos;
   }
@@ -155,16 +156,51 @@ __global__ __launch_bounds__(256) void k_bin_wide(const T* __restrict__ x, int64
   }
 }
 
+// 2-byte bins (a feature of more than 256 bins): block (row chunk, 8-feature word),
+// bounds read through the caches (a word's can exceed LDS), 12 lifting steps.
+template <typename T, bool COL_MAJOR>
+__global__ __launch_bounds__(256) void k_bin_wide16(const T* __restrict__ x, int64_t n, int32_t F,
+                                                    int64_t stride,
+                                                    const DevBinFeature* __restrict__ feats,
+                                                    const double* __restrict__ ub,
+                                                    const int2* __restrict__ cats,
+                                                    uint8_t* __restrict__ binmat,
+                                                    uint32_t* __restrict__ rec) {
+  __shared__ DevBinFeature s_f[8];
+  const int f0 = (int)blockIdx.y * 8;
+  const int nf = min(8, F - f0);
+  if (threadIdx.x < (unsigned)max(nf, 0)) s_f[threadIdx.x] = feats[f0 + threadIdx.x];
+  __syncthreads();
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += step) {
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k < nf) {
+        const int f = f0 + k;
+        const double val = (double)(COL_MAJOR ? x[(int64_t)f * n + r] : x[r * F + f]);
+        v[k >> 1] |= bin_of<WIDE_MAX_BIN / 2>(s_f[k], ub, cats, val) << (16 * (k & 1));
+      }
+    }
+    *(uint4*)(binmat + r * stride + 2 * f0) = make_uint4(v[0], v[1], v[2], v[3]);
+    if (blockIdx.y == 0) rec[r] = (uint32_t)r;
+  }
+}
+
 template <typename T, bool CM>
 void launch_wide_typed(const void* x, int64_t n, int32_t F, int64_t stride, const DevBinFeature* feats,
-                       const double* ub, const int2* cats, uint8_t* binmat, uint4* rec, hipStream_t s,
-                       const KernelEvents* ev) {
+                       const double* ub, const int2* cats, uint8_t* binmat, uint4* rec, int bin16,
+                       hipStream_t s, const KernelEvents* ev) {
   const int64_t want = (n + 255) / 256;
   const unsigned blocks = (unsigned)std::min<int64_t>(std::max<int64_t>(want, 1), 1024);
   // every 16-byte word of a row, the padding words too (zeros)
-  const unsigned words = (unsigned)(stride / BIN_WIDE_F);
-  KLAUNCH(ev, (k_bin_wide<T, CM>), dim3(blocks, words), dim3(256), 0, s, (const T*)x, n, F, stride,
-          feats, ub, cats, binmat, (uint32_t*)rec);
+  const unsigned words = (unsigned)(stride / 16);  // 16-byte words of a row
+  if (bin16)
+    KLAUNCH(ev, (k_bin_wide16<T, CM>), dim3(blocks, words), dim3(256), 0, s, (const T*)x, n, F,
+            stride, feats, ub, cats, binmat, (uint32_t*)rec);
+  else
+    KLAUNCH(ev, (k_bin_wide<T, CM>), dim3(blocks, words), dim3(256), 0, s, (const T*)x, n, F,
+            stride, feats, ub, cats, binmat, (uint32_t*)rec);
 }
 
 template <typename T, bool CM>
@@ -182,19 +218,19 @@ void launch_typed(const void* x, int64_t n, int32_t F, int32_t fmt, const DevBin
 
 void launch_bin_wide(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
                      int64_t stride, const DevBinFeature* feats, const double* ub,
-                     const int2* cats, uint8_t* binmat, uint4* rec, hipStream_t s,
+                     const int2* cats, uint8_t* binmat, uint4* rec, int32_t bin16, hipStream_t s,
                      const KernelEvents* ev) {
   if (n <= 0) return;
   if (f64) {
     if (col_major)
-      launch_wide_typed<double, true>(x, n, F, stride, feats, ub, cats, binmat, rec, s, ev);
+      launch_wide_typed<double, true>(x, n, F, stride, feats, ub, cats, binmat, rec, bin16, s, ev);
     else
-      launch_wide_typed<double, false>(x, n, F, stride, feats, ub, cats, binmat, rec, s, ev);
+      launch_wide_typed<double, false>(x, n, F, stride, feats, ub, cats, binmat, rec, bin16, s, ev);
   } else {
     if (col_major)
-      launch_wide_typed<float, true>(x, n, F, stride, feats, ub, cats, binmat, rec, s, ev);
+      launch_wide_typed<float, true>(x, n, F, stride, feats, ub, cats, binmat, rec, bin16, s, ev);
     else
-      launch_wide_typed<float, false>(x, n, F, stride, feats, ub, cats, binmat, rec, s, ev);
+      launch_wide_typed<float, false>(x, n, F, stride, feats, ub, cats, binmat, rec, bin16, s, ev);
   }
 }
 

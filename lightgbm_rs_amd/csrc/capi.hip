@@ -154,6 +154,10 @@ struct lgbm_hip_ctx {
   int64_t N = 0;
   int32_t F = 0, fmt = 1, total_cells = 0;  // fmt: row record format (lgbm_device.h)
   int32_t records_env = 0;  // LGBM_HIP_RECORDS: 0 automatic, 1 legacy (8-bit records), 2 wide
+  int32_t max_bins = 0;     // the widest feature's num_bin
+  bool bin16 = false;       // wide layout with 2-byte bins
+  int32_t n_wgroups = 0;    // 2-byte bins: feature groups of the histogram kernel
+  int32_t* d_wgroups = nullptr;  // [n_wgroups + 1] first feature of each group
   uint8_t* binmat = nullptr;  // wide layout: row-major bins [N][row_stride]
   int64_t row_stride = 0;
   uint64_t slot_len = 0;
@@ -370,6 +374,10 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.acc_cells = c->acc_cells;
   L.binmat = c->binmat;
   L.row_stride = c->row_stride;
+  L.max_bins = c->max_bins;
+  L.bin16 = c->bin16 ? 1 : 0;
+  L.n_wgroups = c->n_wgroups;
+  L.wgroups = c->d_wgroups;
   L.feat_used = c->colsamp_on ? c->d_feat_used : nullptr;
   L.part_slots = c->part_slots;
   L.hist_part64 = c->hist_part64;
@@ -896,8 +904,11 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   uint32_t acc = 0, uacc = 0;
   for (int f = 0; f < F; ++f) {
     const lgbm_feature_meta& m = meta[f];
-    if (m.num_bin == 0 || m.num_bin > 256)
-      return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be in 1..=256 (u8 bin storage)");
+    if (m.num_bin == 0 || m.num_bin > WIDE_MAX_BIN)
+      return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                     "num_bin must be in 1..=" + std::to_string(WIDE_MAX_BIN));
+    if (m.bin_type == LGBM_BIN_CATEGORICAL && m.num_bin > 256)
+      return set_err(c, LGBM_HIP_ERR_CAPABILITY, "categorical features hold at most 256 bins");
     DevFeature& d = feats[f];
     d.num_bin = m.num_bin;
     d.offset = m.offset;
@@ -925,16 +936,22 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   // when the records cannot hold the features or the quantized builds' LDS cannot
   // hold the cells; else 6-bit bins with the quantized pair inside when every feature
   // has at most 64 bins and fits (F <= 39), else 8-bit bins and the row index
-  const bool wide = c->records_env == 2 || F > 16 * LGBM_MAX_W - 4 || acc > QUANT_LDS_CELLS;
+  uint32_t max_nb = 0;
+  for (int f = 0; f < F; ++f) max_nb = std::max(max_nb, meta[f].num_bin);
+  const bool bin16 = max_nb > 256;  // 2-byte bins: the wide layout only
+  const bool wide =
+      bin16 || c->records_env == 2 || F > 16 * LGBM_MAX_W - 4 || acc > QUANT_LDS_CELLS;
   if (!wide && acc > HIST_WAVE_CELLS && num_data > (int64_t)HIST_GRID_Q * HIST_BLOCK_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "rows per histogram block exceed the packed LDS cell fields");
   if (wide && wide_prepare())
     return set_err(c, LGBM_HIP_ERR_HIP, "the wide histogram kernels' LDS size was refused");
+  if (bin16 && (scan_prepare() || fixscan_prepare()))
+    return set_err(c, LGBM_HIP_ERR_HIP, "the scans' LDS size was refused");
   c->F = F;
   c->N = num_data;
-  uint32_t max_nb = 0;
-  for (int f = 0; f < F; ++f) max_nb = std::max(max_nb, meta[f].num_bin);
+  c->max_bins = (int32_t)max_nb;
+  c->bin16 = bin16;
   c->fmt = (F + 4 + 15) / 16;
   if (wide) {
     c->fmt = REC_FMT_WIDE;
@@ -974,11 +991,30 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   if ((rc = dalloc(c, &c->hist_sum, (size_t)acc * 3))) return rc;
   if ((rc = dalloc(c, &c->hist_part64, (size_t)HIST_SLOTS * pc * 2))) return rc;
   if (wide) {
-    c->row_stride = ((int64_t)F + WIDE_GF_Q - 1) / WIDE_GF_Q * WIDE_GF_Q;
+    // row stride in bytes: F rounded up to a 64-feature group, times the bin width
+    c->row_stride = ((int64_t)F + WIDE_GF_Q - 1) / WIDE_GF_Q * WIDE_GF_Q * (bin16 ? 2 : 1);
     if ((rc = dalloc(c, &c->binmat, (size_t)num_data * (size_t)c->row_stride))) return rc;
+    // 2-byte bins: feature groups of at most WIDE16_GROUP_F consecutive features whose
+    // cells fit WIDE16_GROUP_CELLS
+    std::vector<int32_t> groups(1, 0);
+    uint32_t gc = 0;
+    for (int f = 0; f < F; ++f) {
+      const int32_t nf = f - groups.back();
+      if (nf > 0 && (nf >= WIDE16_GROUP_F || gc + meta[f].num_bin > WIDE16_GROUP_CELLS)) {
+        groups.push_back(f);
+        gc = 0;
+      }
+      gc += meta[f].num_bin;
+    }
+    groups.push_back(F);
+    c->n_wgroups = (int32_t)groups.size() - 1;
+    if ((rc = dalloc(c, &c->d_wgroups, groups.size()))) return rc;
+    HIPCHK(c, hipMemcpy(c->d_wgroups, groups.data(), groups.size() * 4, hipMemcpyHostToDevice));
     if ((rc = dalloc(c, &c->hist_acc64, (size_t)SPEC_MAX * c->acc_cells * 2))) return rc;
     HIPCHK(c, hipMemset(c->hist_acc64, 0, (size_t)SPEC_MAX * c->acc_cells * 2 * 8));
-    if ((rc = dalloc(c, &c->wide_part, wide_part_words(F, num_data, (int32_t)acc)))) return rc;
+    if ((rc = dalloc(c, &c->wide_part,
+                     wide_part_words(F, num_data, (int32_t)acc, bin16 ? c->n_wgroups : 0))))
+      return rc;
   } else {
     c->row_stride = 0;
     if (c->binmat) (void)hipFree(c->binmat);
@@ -1149,6 +1185,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->hist_acc);
   F(c->hist_acc64);
   F(c->wide_part);
+  F(c->d_wgroups);
   F(c->binmat);
   F(c->rk_qb);
   F(c->rk_imd);
@@ -1398,8 +1435,9 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
   for (int32_t f = 0; f < F; ++f) {
     const lgbm_hip_bin_mapper* m = mappers[f];
     if (!m) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null mapper");
-    if (m->num_bin < 1 || m->num_bin > 256)
-      return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be in 1..=256 (u8 bin storage)");
+    if (m->num_bin < 1 || m->num_bin > WIDE_MAX_BIN)
+      return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                     "num_bin must be in 1..=" + std::to_string(WIDE_MAX_BIN));
     const bool cat = m->bin_type == LGBM_BIN_CATEGORICAL;
     lgbm_feature_meta& d = meta[(size_t)f];
     d.num_bin = (uint32_t)m->num_bin;
@@ -1448,8 +1486,8 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
     KernelEvents ke;
     if (rec_wide(c->fmt))
       launch_bin_wide(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->row_stride,
-                      d_bf, c->d_ub, d_cats, c->binmat, c->rec[BUF_ORIG], c->stream,
-                      ev_kernel(c, FAM_BIN, &ke));
+                      d_bf, c->d_ub, d_cats, c->binmat, c->rec[BUF_ORIG], c->bin16 ? 1 : 0,
+                      c->stream, ev_kernel(c, FAM_BIN, &ke));
     else
       launch_bin_records(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->fmt,
                          d_bf, c->d_ub, (int32_t)ub.size(), d_cats, c->rec[BUF_ORIG], c->stream,
@@ -1492,6 +1530,8 @@ int lgbm_hip_get_bins(lgbm_hip_ctx* c, uint8_t* out, int64_t n) {
   if (rc) return rc;
   if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "no resident bins");
   if (!out || n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_data");
+  if (c->bin16)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "the resident bins are 2-byte: lgbm_hip_get_bins16");
   if (rec_wide(c->fmt)) {
     const size_t st = (size_t)c->row_stride;
     std::vector<uint8_t> m((size_t)c->N * st);
@@ -1512,6 +1552,83 @@ int lgbm_hip_get_bins(lgbm_hip_ctx* c, uint8_t* out, int64_t n) {
       out[(size_t)f * c->N + r] = (uint8_t)((rec[(size_t)r * U + wi] >> sh) & mask);
   }
   return LGBM_HIP_OK;
+}
+
+int lgbm_hip_get_bins16(lgbm_hip_ctx* c, uint16_t* out, int64_t n) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "no resident bins");
+  if (!out || n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "n != num_data");
+  if (!c->bin16) {
+    std::vector<uint8_t> b8((size_t)c->F * (size_t)c->N);
+    if ((rc = lgbm_hip_get_bins(c, b8.data(), n))) return rc;
+    for (size_t i = 0; i < b8.size(); ++i) out[i] = b8[i];
+    return LGBM_HIP_OK;
+  }
+  const size_t st = (size_t)c->row_stride;
+  std::vector<uint8_t> m((size_t)c->N * st);
+  HIPCHK(c, hipMemcpy(m.data(), c->binmat, m.size(), hipMemcpyDeviceToHost));
+  for (int32_t f = 0; f < c->F; ++f)
+    for (int64_t r = 0; r < c->N; ++r) {
+      uint16_t v;
+      std::memcpy(&v, m.data() + (size_t)r * st + 2 * (size_t)f, 2);
+      out[(size_t)f * c->N + r] = v;
+    }
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_upload_bins16(lgbm_hip_ctx* c, const uint16_t* bins, int32_t num_features,
+                           int64_t num_data, const lgbm_feature_meta* meta,
+                           const double* bin_upper_bound) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
+  if (!bins || !meta || num_features <= 0 || num_data <= 0)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null bins/meta or empty shape");
+  const int32_t F = num_features;
+  for (int f = 0; f < F; ++f)
+    if (meta[f].num_bin == 0 || meta[f].num_bin > WIDE_MAX_BIN)
+      return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                     "num_bin must be in 1..=" + std::to_string(WIDE_MAX_BIN));
+  // bin-range gate (learner.rs:1161-1187): first offending bin, feature order
+  for (int f = 0; f < F; ++f) {
+    const uint16_t* col = bins + (size_t)f * (size_t)num_data;
+    const uint32_t nb = meta[f].num_bin;
+    for (int64_t r = 0; r < num_data; ++r)
+      if (col[r] >= nb)
+        return set_err(c, LGBM_HIP_ERR_BIN_OUT_OF_RANGE,
+                       "bin " + std::to_string(col[r]) + " >= num_bin " + std::to_string(nb) +
+                           " (feature " + std::to_string(f) + ", row " + std::to_string(r) + ")");
+  }
+  if ((rc = resident_setup(c, F, num_data, meta, bin_upper_bound))) return rc;
+  hipError_t e = hipSuccess;
+  if (c->bin16) {
+    uint16_t* tmp = nullptr;
+    HIPCHK(c, hipMalloc((void**)&tmp, (size_t)F * num_data * 2));
+    e = hipMemcpy(tmp, bins, (size_t)F * num_data * 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+      launch_pack_wide16(tmp, num_data, F, c->row_stride, c->binmat, c->rec[BUF_ORIG], c->stream);
+      e = hipStreamSynchronize(c->stream);
+    }
+    (void)hipFree(tmp);
+  } else {
+    // every feature fits a byte: the 1-byte layouts
+    std::vector<uint8_t> b8((size_t)F * (size_t)num_data);
+    for (size_t i = 0; i < b8.size(); ++i) b8[i] = (uint8_t)bins[i];
+    uint8_t* tmp = nullptr;
+    HIPCHK(c, hipMalloc((void**)&tmp, b8.size()));
+    e = hipMemcpy(tmp, b8.data(), b8.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+      if (rec_wide(c->fmt))
+        launch_pack_wide(tmp, num_data, F, c->row_stride, c->binmat, c->rec[BUF_ORIG], c->stream);
+      else
+        launch_pack_records(tmp, num_data, F, c->fmt, c->rec[BUF_ORIG], c->stream);
+      e = hipStreamSynchronize(c->stream);
+    }
+    (void)hipFree(tmp);
+  }
+  if (e != hipSuccess) return set_err(c, LGBM_HIP_ERR_HIP, hipGetErrorString(e));
+  return resident_done(c);
 }
 
 int lgbm_hip_set_gradients(lgbm_hip_ctx* c, const float* grad, const float* hess, int64_t n) {

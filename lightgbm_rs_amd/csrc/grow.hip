@@ -720,10 +720,17 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     rec_field_pos(FMT, J.fbyte, &fwi, &fsh);
     int32_t wbin[PR];
     if constexpr (WIDE) {
-      const uint8_t* __restrict__ col = L.binmat + J.fbyte;
       const int64_t stride = L.row_stride;
+      if (L.bin16) {
+        const uint8_t* __restrict__ col = L.binmat + 2 * (int64_t)J.fbyte;
 #pragma unroll
-      for (int k = 0; k < PR; ++k) wbin[k] = col[(int64_t)w[k][0] * stride];
+        for (int k = 0; k < PR; ++k)
+          wbin[k] = *(const uint16_t*)(col + (int64_t)w[k][0] * stride);
+      } else {
+        const uint8_t* __restrict__ col = L.binmat + J.fbyte;
+#pragma unroll
+        for (int k = 0; k < PR; ++k) wbin[k] = col[(int64_t)w[k][0] * stride];
+      }
     }
 #pragma unroll
     for (int k = 0; k < PR; ++k) {
@@ -946,8 +953,10 @@ __global__ __launch_bounds__(1024) void k_tile_scan(DevLearner L) {
 // ===========================================================================
 __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_t part_grid) {
   static_assert(SCAN_THREADS == 128, "two bins and four f64 cells per thread cover 256 bins");
-  __shared__ double cs[2 * 256];
-  __shared__ double cp[2 * 256];
+  // the smaller child's and the larger child's f64 cells, sized for the widest feature
+  extern __shared__ double scan_lds[];
+  double* cs = scan_lds;
+  double* cp = scan_lds + 2 * L.max_bins;
   Ctl* ctl = L.ctl;
   const int f = blockIdx.x, j = blockIdx.y;
   const int tid = threadIdx.x, F = L.F, cells = L.total_cells;
@@ -1036,9 +1045,10 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
     const int32_t wa0 = ctl->hjobs[j].a0, wna = wide ? ctl->hjobs[j].nblk : 0;
     int32_t* acc = L.hist_acc + (size_t)j * L.acc_cells * 3;
     const unsigned long long* slots = L.part_slots;
+    for (int b0 = 0; b0 < nb; b0 += 2 * SCAN_THREADS)  // one pass below 257 bins
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int b = tid + SCAN_THREADS * q;
+      const int b = b0 + tid + SCAN_THREADS * q;
       if (b >= nb) continue;
       const size_t ci = (size_t)(ft.cell_base + b);
       int32_t AG = 0, AH = 0, AT = 0;
@@ -1115,6 +1125,13 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
     if (i >= 2 * nb) continue;
     const double v = cs[i];
     const double d = pv[k] - v;
+    cp[i] = d;
+    s_sm[i] = v;
+    s_lg[i] = d;
+  }
+  for (int i = tid + 4 * SCAN_THREADS; i < 2 * nb; i += SCAN_THREADS) {  // past 256 bins
+    const double v = cs[i];
+    const double d = s_par[i] - v;
     cp[i] = d;
     s_sm[i] = v;
     s_lg[i] = d;
@@ -1323,9 +1340,19 @@ void launch_partition_stable(const DevLearner& L, int64_t ntiles, int64_t blocks
   const size_t lds = (size_t)(std::max(L.total_cells, 1) + LDS_TRASH_CELLS) * sizeof(unsigned long long);
   k_partition<1, 0, true><<<dim3((unsigned)blocks), dim3(PART_THREADS), lds, s>>>(L);
 }
+// Lets the scans take LDS rows for the widest feature (2-byte bins: 4096 bins, 128 KiB
+// for k_pair_scan's two children); called outside graph capture.
+int scan_prepare() {
+  if (hipFuncSetAttribute((const void*)k_pair_scan, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          4 * WIDE_MAX_BIN * (int)sizeof(double)) != hipSuccess)
+    return 1;
+  return 0;
+}
+
 void launch_pair_scan(const DevLearner& L, int32_t spec_max, int32_t part_grid, hipStream_t s,
                       const KernelEvents* ev) {
-  KLAUNCH(ev, k_pair_scan, dim3((unsigned)L.F, (unsigned)spec_max), dim3(SCAN_THREADS), 0, s, L,
+  const size_t lds = (size_t)4 * std::max(L.max_bins, 1) * sizeof(double);
+  KLAUNCH(ev, k_pair_scan, dim3((unsigned)L.F, (unsigned)spec_max), dim3(SCAN_THREADS), lds, s, L,
           part_grid);
 }
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {

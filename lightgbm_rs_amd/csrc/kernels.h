@@ -108,6 +108,10 @@ struct DevLearner {
   const double* ub;
   int32_t F;
   int32_t total_cells;
+  int32_t max_bins;           // the widest feature's num_bin (scan LDS rows)
+  int32_t bin16;              // wide layout: 2-byte bins (a feature has more than 256)
+  int32_t n_wgroups;          // 2-byte bins: feature groups of k_hist_wide
+  const int32_t* wgroups;     // [n_wgroups + 1] their first features
   int32_t fmt;                // row record format (rec_words / rec_packed)
   int64_t N;
   uint64_t slot_len;
@@ -144,9 +148,9 @@ struct DevLearner {
   RowBufs bufs;
 };
 
-// LambdaRank on the device (objective.hip): one RANK_THREADS block per query of at
+// LambdaRank on the device (objective.hip): one LAMBDARANK_THREADS block per query of at
 // most RANK_MAX_QUERY rows; the tables are built on the host.
-#define RANK_THREADS 128
+#define LAMBDARANK_THREADS 128
 #define RANK_SIGMOID_BINS (1024 * 1024)
 #define RANK_MAX_QUERY 2048
 #define RANK_DISCOUNTS 10000
@@ -256,14 +260,20 @@ void launch_pack_wide(const uint8_t* bins, int64_t n, int32_t F, int64_t stride,
                       uint4* rec, hipStream_t s);
 // Opts the wide histogram kernels into their LDS size (outside graph capture); 0 = ok.
 int wide_prepare();
+// The same for the scans' LDS rows of features wider than 256 bins.
+int scan_prepare();
+int fixscan_prepare();
 // u64 words of the wide layout's per-chunk partial histogram slots
-size_t wide_part_words(int32_t F, int64_t N, int32_t cells);
+size_t wide_part_words(int32_t F, int64_t N, int32_t cells, int32_t n_groups16);
+// feature-major 2-byte bins -> the row-major matrix (2-byte bins)
+void launch_pack_wide16(const uint16_t* bins, int64_t n, int32_t F, int64_t stride,
+                        uint8_t* binmat, uint4* rec, hipStream_t s);
 // ConstructHistogram of the launch's histogram jobs into the per-job accumulators
 void launch_hist_wide(const DevLearner& L, int fp, hipStream_t s, const KernelEvents* ev = nullptr);
 // raw values -> the row-major matrix (ValueToBin per feature group, bounds in LDS)
 void launch_bin_wide(const void* x, int32_t f64, int32_t col_major, int64_t n, int32_t F,
                      int64_t stride, const DevBinFeature* feats, const double* ub,
-                     const int2* cats, uint8_t* binmat, uint4* rec, hipStream_t s,
+                     const int2* cats, uint8_t* binmat, uint4* rec, int32_t bin16, hipStream_t s,
                      const KernelEvents* ev);
 void launch_pack_partition(const uint32_t* bins, int64_t n, uint4* rec, hipStream_t s);
 }  // namespace lgbm

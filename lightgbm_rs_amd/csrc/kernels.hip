@@ -719,7 +719,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_f32(DevLearner L) {
 // ===========================================================================
 __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t mode,
                                                           double* __restrict__ explicit_out) {
-  __shared__ double cs[2 * 256];
+  extern __shared__ double cs[];  // [2 * max_bins] f64 cells of the feature
   __shared__ long long tot[3][SCAN_THREADS / LGBM_WAVE];
   Ctl* ctl = L.ctl;
   const int f = blockIdx.x;
@@ -940,7 +940,20 @@ __global__ __launch_bounds__(256) void k_walk(DevLearner L, double lr, double* _
       const uint32_t u = s_node[node];
       uint32_t bin;
       if constexpr (WIDE) {
-        bin = bm[r * rstride + s_wf[node]];
+        if (L.bin16) {
+          // 2-byte bins: the node's router, not the 256-bin route set (categorical
+          // features keep at most 256 bins)
+          bin = *(const uint16_t*)(bm + r * rstride + 2 * s_wf[node]);
+          const NodeRoute nr = L.tree.nodes[node];
+          if (!(nr.flags & ROUTE_CAT)) {
+            const bool right =
+                route_right((int32_t)bin, nr.pmin, nr.max_bin, nr.th, nr.na_bin, nr.flags);
+            node = right ? ((int32_t)u >> 20) : ((int32_t)(u << 12) >> 20);
+            continue;
+          }
+        } else {
+          bin = bm[r * rstride + s_wf[node]];
+        }
       } else {
         const uint32_t f = u & 0xffu;
         const uint32_t wi = f / BPW;
@@ -1058,6 +1071,10 @@ void launch_fp_prep(const DevLearner& L, const float* g, const float* h, int64_t
   k_fp_scales<<<1, 256, 0, s>>>(L.ctl, partials, stat_blocks(n), n);
   k_pack_g32<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(g, h, n, L.bufs.g32[BUF_ORIG]);
 }
+int fixscan_prepare() {
+  return hipFuncSetAttribute((const void*)k_fixscan, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             2 * WIDE_MAX_BIN * (int)sizeof(double)) != hipSuccess;
+}
 void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hipStream_t s,
                     const KernelEvents* ev) {
   // quantized: the partial slots summed into hist_sum first (f32 cells are summed by
@@ -1065,7 +1082,8 @@ void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hip
   const int64_t cols = (int64_t)L.total_cells * 3;
   if (!rec_wide(L.fmt))
     k_hist_reduce<<<dim3((unsigned)((cols + 15) / 16)), dim3(256), 0, s>>>(L);
-  KLAUNCH(ev, k_fixscan, dim3((unsigned)L.F), dim3(SCAN_THREADS), 0, s, L, mode, explicit_out);
+  KLAUNCH(ev, k_fixscan, dim3((unsigned)L.F), dim3(SCAN_THREADS),
+          (size_t)2 * std::max(L.max_bins, 1) * sizeof(double), s, L, mode, explicit_out);
 }
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,

@@ -34,6 +34,9 @@
 #define WIDE_MIN_ROWS 16384             // rows per chunk (at least): a flush costs a group
 #define WIDE_MAX_ROWS ((1 << 19) - 1)   // packed LDS cell field limit (quantized)
 #define WIDE_MAX_F 4096
+#define WIDE_MAX_BIN 4096               // 2-byte bins (a feature of more than 256 bins)
+#define WIDE16_GROUP_CELLS 8192         // 2-byte bins: cells of a feature group (LDS)
+#define WIDE16_GROUP_F 64               // 2-byte bins: features of a group (at most)
 #ifndef PART_THREADS
 #define PART_THREADS 512                // partition block (two per CU)
 #endif

@@ -41,7 +41,7 @@ __device__ __forceinline__ double rank_sigmoid(const RankParams& p, const double
   return tab[(size_t)((s - p.min_in) * p.idx_factor)];
 }
 
-__global__ __launch_bounds__(RANK_THREADS) void k_grad_lambdarank(
+__global__ __launch_bounds__(LAMBDARANK_THREADS) void k_grad_lambdarank(
     const double* __restrict__ score, const float* __restrict__ label,
     const int32_t* __restrict__ qb, const double* __restrict__ inv_max_dcg,
     const double* __restrict__ tab, const double* __restrict__ discount,
@@ -63,7 +63,7 @@ __global__ __launch_bounds__(RANK_THREADS) void k_grad_lambdarank(
   float* s_hes = s_lam + cnt;
   int8_t* s_dir = (int8_t*)(s_hes + cnt);  // row i's pair j: +1 i high, -1 i low, 0 none
   const double kmin = -__builtin_inf();
-  for (int i = tid; i < cnt; i += RANK_THREADS) {
+  for (int i = tid; i < cnt; i += LAMBDARANK_THREADS) {
     s_sc[i] = score[st + i];
     s_lab[i] = label[st + i];
     s_lam[i] = 0.0f;
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(RANK_THREADS) void k_grad_lambdarank(
   // stable sort by descending score: the rank of document i among the query's (a
   // NaN score, which the reference's comparison leaves unordered, sorts last so the
   // ranks stay a permutation)
-  for (int i = tid; i < cnt; i += RANK_THREADS) {
+  for (int i = tid; i < cnt; i += LAMBDARANK_THREADS) {
     const double si = s_sc[i];
     const bool ni = si != si;
     int32_t r = 0;
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(RANK_THREADS) void k_grad_lambdarank(
     const double si = s_sc[di];
     if (si == kmin) continue;  // block-uniform
     const float li = s_lab[di];
-    for (int32_t j = i + 1 + tid; j < cnt; j += RANK_THREADS) {
+    for (int32_t j = i + 1 + tid; j < cnt; j += LAMBDARANK_THREADS) {
       const int32_t dj = s_ord[j];
       const double sj = s_sc[dj];
       const float lj = s_lab[dj];
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(RANK_THREADS) void k_grad_lambdarank(
   if (tid == 0) s_nf = (p.norm && sum_lambdas > 0.0) ? log2(1.0 + sum_lambdas) / sum_lambdas : 0.0;
   __syncthreads();
   const double nf = s_nf;
-  for (int i = tid; i < cnt; i += RANK_THREADS) {
+  for (int i = tid; i < cnt; i += LAMBDARANK_THREADS) {
     float lam = s_lam[i], hes = s_hes[i];
     if (nf != 0.0) {
       lam = (float)((double)lam * nf);
@@ -184,7 +184,7 @@ void launch_grad_l2(const double* score, const float* label, float* g, float* h,
 void launch_grad_lambdarank(const double* score, const float* label, const RankTables& t,
                             float* g, float* h, hipStream_t s) {
   if (t.num_queries <= 0) return;
-  k_grad_lambdarank<<<dim3((unsigned)t.num_queries), dim3(RANK_THREADS),
+  k_grad_lambdarank<<<dim3((unsigned)t.num_queries), dim3(LAMBDARANK_THREADS),
                       rank_lds_bytes(t.max_query), s>>>(score, label, t.qb, t.inv_max_dcg, t.table,
                                                         t.discount, t.gain, t.p, g, h);
 }

@@ -184,7 +184,7 @@ __device__ __forceinline__ void prefix_in_order(double g, double h, int32_t c, i
   *sc = ac;
 }
 
-static __device__ void wave_scan(const double* hist, const DevFeature& ft, const ScanCfg& c,
+static __device__ __attribute__((unused)) void wave_scan(const double* hist, const DevFeature& ft, const ScanCfg& c,
                           double sum_gradient, double sum_hessian, int32_t num_data, double po,
                           lgbm_split_info* out) {
   const int lane = (int)lane_id();
@@ -380,7 +380,7 @@ __device__ __forceinline__ double leaf_gain_given_output(bool use_l1, double g, 
   return -__builtin_fma(2.0 * gg, out, (h + l2) * out * out);
 }
 
-static __device__ void wave_scan_cat(const double* hist, const DevFeature& ft, const ScanCfg& c,
+static __device__ __attribute__((unused)) void wave_scan_cat(const double* hist, const DevFeature& ft, const ScanCfg& c,
                                      const lgbm_gain_config& cfg, double sum_gradient,
                                      double sum_hessian, int32_t num_data, double po,
                                      lgbm_split_info* out, uint32_t* bits) {
@@ -641,18 +641,34 @@ __device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* 
   __syncthreads();
   if (ft.offset > 0) {
     const int off = ft.offset;
-    double a[256 / SCAN_THREADS], b2[256 / SCAN_THREADS];
-    int k = 0;
-    for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
-      const int src = c + off;
-      a[k] = src < nb ? cs[2 * src] : 0.0;
-      b2[k] = src < nb ? cs[2 * src + 1] : 0.0;
-    }
-    __syncthreads();
-    k = 0;
-    for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
-      cs[2 * c] = a[k];
-      cs[2 * c + 1] = b2[k];
+    if (nb <= 256) {
+      double a[256 / SCAN_THREADS], b2[256 / SCAN_THREADS];
+      int k = 0;
+      for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
+        const int src = c + off;
+        a[k] = src < nb ? cs[2 * src] : 0.0;
+        b2[k] = src < nb ? cs[2 * src + 1] : 0.0;
+      }
+      __syncthreads();
+      k = 0;
+      for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
+        cs[2 * c] = a[k];
+        cs[2 * c + 1] = b2[k];
+      }
+    } else {
+      // wider features shift down chunk by chunk: a chunk reads only cells the
+      // earlier chunks did not write
+      for (int c0 = 0; c0 < nb; c0 += SCAN_THREADS) {
+        const int c = c0 + tid, src = c + off;
+        const double a = (c < nb && src < nb) ? cs[2 * src] : 0.0;
+        const double b2 = (c < nb && src < nb) ? cs[2 * src + 1] : 0.0;
+        __syncthreads();
+        if (c < nb) {
+          cs[2 * c] = a;
+          cs[2 * c + 1] = b2;
+        }
+        __syncthreads();
+      }
     }
   }
   __syncthreads();

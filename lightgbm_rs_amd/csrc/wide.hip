@@ -53,14 +53,16 @@ __device__ __forceinline__ void wide_assign(const Ctl* ctl, int32_t nj, int32_t*
   *s_R = R;
 }
 
-template <int FP>
+template <int FP, bool B16>
 __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
-  constexpr int GF = FP ? WIDE_GF_F : WIDE_GF_Q;
+  // B16: 2-byte bins, feature groups from the host's table (cells <= WIDE16_GROUP_CELLS)
+  constexpr int GF = B16 ? WIDE16_GROUP_F : FP ? WIDE_GF_F : WIDE_GF_Q;
   constexpr int NV = GF / 16;      // 16-byte words of a row's group bytes
   constexpr int RU = FP ? 4 : 2;   // rows per thread in flight
   constexpr int NW = WIDE_THREADS / LGBM_WAVE;
   extern __shared__ unsigned long long lds[];
   __shared__ uint32_t s_fd[GF];    // per feature: (first cell - group base) << 8 | mfb
+                                   // (2-byte bins: << 16)
   __shared__ int32_t s_a0[SPEC_MAX], s_nb[SPEC_MAX];
   __shared__ int64_t s_R;
   __shared__ long long s_tot[3][NW];
@@ -69,7 +71,7 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
   if (nj <= 0) return;
   const int tid = threadIdx.x, wave = tid >> 6;
   const int F = L.F, cells = L.total_cells;
-  const int f0 = (int)blockIdx.y * GF;
+  const int f0 = B16 ? L.wgroups[blockIdx.y] : (int)blockIdx.y * GF;
   if (f0 >= F) return;
   if (tid == 0) wide_assign(ctl, nj, s_a0, s_nb, &s_R, (int64_t)gridDim.x - SPEC_MAX);
   __syncthreads();
@@ -83,14 +85,15 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
       ctl->hjobs[k].nblk = s_nb[k];
     }
   if (j < 0) return;
-  const int f1 = min(f0 + GF, F);
+  const int f1 = B16 ? L.wgroups[blockIdx.y + 1] : min(f0 + GF, F);
   const int gbase = (int)L.feats[f0].cell_base;
   const int gcells = (f1 < F ? (int)L.feats[f1].cell_base : cells) - gbase;
   for (int k = tid; k < GF; k += WIDE_THREADS) {
     uint32_t d = 0u;  // padding bytes: bin 0 == "mfb" 0, never added
-    if (f0 + k < F) {
+    if (f0 + k < f1) {
       const DevFeature& ft = L.feats[f0 + k];
-      d = ((ft.cell_base - (uint32_t)gbase) << 8) | (ft.mfb & 0xffu);
+      d = B16 ? ((ft.cell_base - (uint32_t)gbase) << 16) | (ft.mfb & 0xffffu)
+              : ((ft.cell_base - (uint32_t)gbase) << 8) | (ft.mfb & 0xffu);
     }
     s_fd[k] = d;
   }
@@ -104,7 +107,8 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
   const int64_t jb = J.begin;
   const bool orig = J.buf == BUF_ORIG;
   const uint32_t* __restrict__ rows = (const uint32_t*)rec_buf(L.bufs, J.buf) + jb;
-  const uint8_t* __restrict__ bm = L.binmat + f0;
+  const uint8_t* __restrict__ bm = L.binmat + (B16 ? 2 : 1) * f0;
+  const int nfeat = f1 - f0;
   const int64_t stride = L.row_stride;
   const bool totals = (J._pad & 1) != 0 && blockIdx.y == 0;
   const uint16_t* __restrict__ ghq = L.bufs.gh[0];
@@ -126,13 +130,18 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
       row[u] = rr;
     }
     uint4 w[RU][NV];
+    const uint16_t* src16[RU];
     unsigned long long va[RU], vb[RU];  // quantized: packed cell add; f32: g, h fixed point
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const int64_t src_row = orig ? jb + row[u] : (int64_t)rows[row[u]];
-      const uint4* src = (const uint4*)(bm + src_row * stride);
+      if constexpr (B16) {
+        src16[u] = (const uint16_t*)(bm + src_row * stride);
+      } else {
+        const uint4* src = (const uint4*)(bm + src_row * stride);
 #pragma unroll
-      for (int i = 0; i < NV; ++i) w[u][i] = src[i];
+        for (int i = 0; i < NV; ++i) w[u][i] = src[i];
+      }
       if constexpr (FP) {
         const float2 v = gh32[row[u]];
         const long long gi = (long long)rint((double)v.x * gm);
@@ -153,26 +162,49 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
         t3 += qh == 3 ? 1 : 0;
       }
     }
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      uint32_t fd[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) fd[k] = __builtin_amdgcn_readfirstlane(s_fd[16 * i + k]);
+    if constexpr (B16) {
+      // one 2-byte load per (row, feature) of the group
 #pragma unroll
       for (int u = 0; u < RU; ++u) {
         const bool live = FP ? ok[u] : va[u] != 0ull;
         if (!live) continue;
-        const uint32_t word[4] = {w[u][i].x, w[u][i].y, w[u][i].z, w[u][i].w};
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          const uint32_t bin = (word[k >> 2] >> (8 * (k & 3))) & 0xffu;
-          if (bin != (fd[k] & 0xffu)) {
-            const int c = (int)(fd[k] >> 8) + (int)bin;
+        for (int k = 0; k < nfeat; ++k) {
+          const uint32_t d = s_fd[k];
+          const uint32_t bin = src16[u][k];
+          if (bin != (d & 0xffffu)) {
+            const int c = (int)(d >> 16) + (int)bin;
             if constexpr (FP) {
               __hip_atomic_fetch_add(&lds[2 * c], va[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
               __hip_atomic_fetch_add(&lds[2 * c + 1], vb[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             } else {
               __hip_atomic_fetch_add(&lds[c], va[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+          }
+        }
+      }
+    }
+    if constexpr (!B16) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        uint32_t fd[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) fd[k] = __builtin_amdgcn_readfirstlane(s_fd[16 * i + k]);
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+          const bool live = FP ? ok[u] : va[u] != 0ull;
+          if (!live) continue;
+          const uint32_t word[4] = {w[u][i].x, w[u][i].y, w[u][i].z, w[u][i].w};
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            const uint32_t bin = (word[k >> 2] >> (8 * (k & 3))) & 0xffu;
+            if (bin != (fd[k] & 0xffu)) {
+              const int c = (int)(fd[k] >> 8) + (int)bin;
+              if constexpr (FP) {
+                __hip_atomic_fetch_add(&lds[2 * c], va[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_fetch_add(&lds[2 * c + 1], vb[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+              } else {
+                __hip_atomic_fetch_add(&lds[c], va[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+              }
             }
           }
         }
@@ -238,45 +270,84 @@ __global__ void k_pack_wide(const uint8_t* __restrict__ bins, int64_t n, int32_t
   if (wd == 0) rec[r] = (uint32_t)r;
 }
 
+// Feature-major 2-byte bins -> the row-major matrix: thread = (8-feature word, row).
+__global__ void k_pack_wide16(const uint16_t* __restrict__ bins, int64_t n, int32_t F,
+                              int64_t stride, uint8_t* __restrict__ binmat,
+                              uint32_t* __restrict__ rec) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t words = stride / 16;
+  if (i >= n * words) return;
+  const int64_t wd = i / n, r = i - wd * n;
+  uint32_t v[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int64_t f = wd * 8 + k;
+    if (f < F) v[k >> 1] |= (uint32_t)bins[f * n + r] << (16 * (k & 1));
+  }
+  ((uint4*)(binmat + r * stride))[wd] = make_uint4(v[0], v[1], v[2], v[3]);
+  if (wd == 0) rec[r] = (uint32_t)r;
+}
+
 }  // namespace
 
-size_t wide_lds_bytes(int fp) {
+void launch_pack_wide16(const uint16_t* bins, int64_t n, int32_t F, int64_t stride,
+                        uint8_t* binmat, uint4* rec, hipStream_t s) {
+  const int64_t total = n * (stride / 16);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks < 1) return;
+  k_pack_wide16<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(bins, n, F, stride, binmat,
+                                                            (uint32_t*)rec);
+}
+
+size_t wide_lds_bytes(int fp) {  // the same for both bin widths
   return (size_t)(fp ? WIDE_GF_F * 256 * 16 : WIDE_GF_Q * 256 * 8);
+}
+
+// Feature groups of a launch: fixed 1-byte groups, or the host's 2-byte-bin table.
+int wide_groups(int32_t F, int fp, int32_t n_groups16) {
+  if (n_groups16 > 0) return n_groups16;
+  const int GF = fp ? WIDE_GF_F : WIDE_GF_Q;
+  return (F + GF - 1) / GF;
 }
 
 // Blocks per feature group of a launch (row chunks + one per job at most): rows per
 // chunk stay <= WIDE_MAX_ROWS, and the grid fills the chip.
-int64_t wide_grid_x(int32_t F, int64_t N, int fp) {
-  const int GF = fp ? WIDE_GF_F : WIDE_GF_Q;
-  const int ng = (F + GF - 1) / GF;
+int64_t wide_grid_x(int ng, int64_t N) {
   int64_t chunks = std::max<int64_t>(WIDE_GRID / ng, (N + WIDE_MAX_ROWS - 1) / WIDE_MAX_ROWS);
   return std::max<int64_t>(chunks, 1) + SPEC_MAX;
 }
 
 // u64 words of the partial slots: every chunk of either gradient mode's launch
-size_t wide_part_words(int32_t F, int64_t N, int32_t cells) {
-  return std::max((size_t)wide_grid_x(F, N, 1) * 2, (size_t)wide_grid_x(F, N, 0)) * (size_t)cells;
+size_t wide_part_words(int32_t F, int64_t N, int32_t cells, int32_t n_groups16) {
+  const int64_t gf = wide_grid_x(wide_groups(F, 1, n_groups16), N);
+  const int64_t gq = wide_grid_x(wide_groups(F, 0, n_groups16), N);
+  return std::max((size_t)gf * 2, (size_t)gq) * (size_t)cells;
 }
 
 // Opt the histogram kernels into their LDS size (outside any graph capture).
 int wide_prepare() {
-  if (hipFuncSetAttribute((const void*)k_hist_wide<0>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)wide_lds_bytes(0)) != hipSuccess)
-    return 1;
-  if (hipFuncSetAttribute((const void*)k_hist_wide<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)wide_lds_bytes(1)) != hipSuccess)
-    return 1;
+  const void* k[4] = {(const void*)k_hist_wide<0, false>, (const void*)k_hist_wide<1, false>,
+                      (const void*)k_hist_wide<0, true>, (const void*)k_hist_wide<1, true>};
+  for (int i = 0; i < 4; ++i)
+    if (hipFuncSetAttribute(k[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)wide_lds_bytes(i & 1)) != hipSuccess)
+      return 1;
   return 0;
 }
 
 void launch_hist_wide(const DevLearner& L, int fp, hipStream_t s, const KernelEvents* ev) {
-  const int GF = fp ? WIDE_GF_F : WIDE_GF_Q;
-  const int ng = (L.F + GF - 1) / GF;
-  const dim3 g((unsigned)wide_grid_x(L.F, L.N, fp), (unsigned)ng), blk(WIDE_THREADS);
-  if (fp)
-    KLAUNCH(ev, k_hist_wide<1>, g, blk, wide_lds_bytes(1), s, L);
-  else
-    KLAUNCH(ev, k_hist_wide<0>, g, blk, wide_lds_bytes(0), s, L);
+  const int ng = wide_groups(L.F, fp, L.bin16 ? L.n_wgroups : 0);
+  const dim3 g((unsigned)wide_grid_x(ng, L.N), (unsigned)ng), blk(WIDE_THREADS);
+  if (L.bin16) {
+    if (fp)
+      KLAUNCH(ev, (k_hist_wide<1, true>), g, blk, wide_lds_bytes(1), s, L);
+    else
+      KLAUNCH(ev, (k_hist_wide<0, true>), g, blk, wide_lds_bytes(0), s, L);
+  } else if (fp) {
+    KLAUNCH(ev, (k_hist_wide<1, false>), g, blk, wide_lds_bytes(1), s, L);
+  } else {
+    KLAUNCH(ev, (k_hist_wide<0, false>), g, blk, wide_lds_bytes(0), s, L);
+  }
 }
 
 void launch_pack_wide(const uint8_t* bins, int64_t n, int32_t F, int64_t stride, uint8_t* binmat,
