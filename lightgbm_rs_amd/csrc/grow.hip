@@ -954,7 +954,7 @@ __global__ __launch_bounds__(1024) void k_tile_scan(DevLearner L) {
 __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_t part_grid) {
   static_assert(SCAN_THREADS == 128, "two bins and four f64 cells per thread cover 256 bins");
   // the smaller child's and the larger child's f64 cells, sized for the widest feature
-  extern __shared__ double scan_lds[];
+  extern __shared__ __align__(16) double scan_lds[];
   double* cs = scan_lds;
   double* cp = scan_lds + 2 * L.max_bins;
   Ctl* ctl = L.ctl;
@@ -973,6 +973,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
   const int64_t T = ctl->tile_total;
   const int32_t md = ctl->max_depth, min2 = ctl->cfg.min_data_in_leaf * 2;
   const int32_t fp_mode = ctl->fp_mode;
+  const ScanCfg sc = make_scan_cfg(ctl->cfg);
   if (j >= n_jobs) return;  // only after the job's fields are known to be live
   const DevNodes& nd = L.nodes;
   const int32_t lcnt = nd.count[cl], rcnt = nd.count[cr], dcl = nd.depth[cl];
@@ -1149,17 +1150,16 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
       L.splittable[(size_t)leaf * F + f] = 0;
     }
   } else {
-    const ScanCfg sc = make_scan_cfg(ctl->cfg);
-    if (ft.categorical)  // bin_type dispatch (learner.rs:3103-3118)
-      wave_scan_cat(wv == 0 ? cs : cp, ft, sc, ctl->cfg, ls.sg, ls.sh, ls.n, ls.weight, out,
-                    L.cat_bits + ((size_t)leaf * F + f) * 8);
-    else
-      wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
+    const double gain =
+        ft.categorical  // bin_type dispatch (learner.rs:3103-3118)
+            ? wave_scan_cat(wv == 0 ? cs : cp, ft, sc, ctl->cfg, ls.sg, ls.sh, ls.n, ls.weight,
+                            out, L.cat_bits + ((size_t)leaf * F + f) * 8)
+            : wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
     if (lane_id() == 0) {
       // splittability from the raw scan, then feature_contri scales the gain the
       // ArgMax compares (learner.rs:3235-3252)
-      L.splittable[(size_t)leaf * F + f] = out->gain > -__builtin_inf() ? 1 : 0;
-      out->gain *= ft.penalty;
+      L.splittable[(size_t)leaf * F + f] = gain > -__builtin_inf() ? 1 : 0;
+      out->gain = gain * ft.penalty;
     }
   }
 }

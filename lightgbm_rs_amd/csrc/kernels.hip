@@ -719,7 +719,7 @@ __global__ __launch_bounds__(HIST_THREADS) void k_hist_f32(DevLearner L) {
 // ===========================================================================
 __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t mode,
                                                           double* __restrict__ explicit_out) {
-  extern __shared__ double cs[];  // [2 * max_bins] f64 cells of the feature
+  extern __shared__ __align__(16) double cs[];  // [2 * max_bins] f64 cells of the feature
   __shared__ long long tot[3][SCAN_THREADS / LGBM_WAVE];
   Ctl* ctl = L.ctl;
   const int f = blockIdx.x;
@@ -863,13 +863,14 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
     return;
   }
   const ScanCfg sc = make_scan_cfg(ctl->cfg);
-  if (ft.categorical)  // bin_type dispatch (learner.rs:3103-3118)
-    wave_scan_cat(cs, ft, sc, ctl->cfg, sg, sh, nrows, weight, out, L.cat_bits + (size_t)f * 8);
-  else
-    wave_scan(cs, ft, sc, sg, sh, nrows, weight, out);
+  const double gain =
+      ft.categorical  // bin_type dispatch (learner.rs:3103-3118)
+          ? wave_scan_cat(cs, ft, sc, ctl->cfg, sg, sh, nrows, weight, out,
+                          L.cat_bits + (size_t)f * 8)
+          : wave_scan(cs, ft, sc, sg, sh, nrows, weight, out);
   if (lane_id() == 0) {
-    L.splittable[f] = out->gain > -__builtin_inf() ? 1 : 0;
-    out->gain *= ft.penalty;  // feature_contri (learner.rs:3235-3252)
+    L.splittable[f] = gain > -__builtin_inf() ? 1 : 0;
+    out->gain = gain * ft.penalty;  // feature_contri (learner.rs:3235-3252)
   }
 }
 
@@ -881,7 +882,7 @@ __global__ __launch_bounds__(LGBM_WAVE) void k_scan_explicit(const double* __res
                                                              lgbm_gain_config cfg, double sg,
                                                              double sh, int32_t n,
                                                              lgbm_split_info* out) {
-  __shared__ double cs[2 * 256];
+  __shared__ __align__(16) double cs[2 * 256];
   const int f = blockIdx.x;
   if (f >= n_feats) return;
   const DevFeature ft = feats[f];

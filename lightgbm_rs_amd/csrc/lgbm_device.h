@@ -364,6 +364,43 @@ __device__ __forceinline__ int32_t readlane_i32(int32_t v, int lane) {
   return __builtin_amdgcn_readlane(v, lane);
 }
 
+// A DPP move of an f64 register (GFX9 data-parallel primitives, both halves moved
+// alike); lanes outside ROW_MASK, or whose source lane is invalid, keep their own value.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const int lo = (int)(uint32_t)b, hi = (int)(uint32_t)(b >> 32);
+  const uint32_t nlo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xf, false);
+  const uint32_t nhi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xf, false);
+  return __longlong_as_double((long long)(((unsigned long long)nhi << 32) | nlo));
+}
+
+// Inclusive prefix sum of an int32 over the wave's lanes (lane k: lanes 0..k):
+// row_shr 1, 2, 4, 8 within each 16-lane row (invalid sources add 0), then the row
+// broadcasts 15 and 31 carry the earlier rows' totals.
+__device__ __forceinline__ int32_t wave_incl_sum_i32(int32_t v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+
+// The maximum of the wave's f64 values (no NaN), in every lane: quad butterflies, the
+// half-row and row mirrors, then the row broadcasts 15 and 31 carry rows 0-2 into row
+// 3, whose lane 63 is read out.  max is exact and order-free.
+__device__ __forceinline__ double wave_max_f64(double v) {
+  v = fmax(v, dpp_f64<0xB1, 0xf>(v));   // quad_perm [1,0,3,2]
+  v = fmax(v, dpp_f64<0x4E, 0xf>(v));   // quad_perm [2,3,0,1]
+  v = fmax(v, dpp_f64<0x141, 0xf>(v));  // row_half_mirror
+  v = fmax(v, dpp_f64<0x140, 0xf>(v));  // row_mirror
+  v = fmax(v, dpp_f64<0x142, 0xa>(v));  // row_bcast:15 into rows 1, 3
+  v = fmax(v, dpp_f64<0x143, 0xc>(v));  // row_bcast:31 into rows 2, 3
+  return readlane_f64(v, LGBM_WAVE - 1);
+}
+
 __device__ __forceinline__ uint64_t lanemask_lt() {
   uint32_t l = lane_id();
   return l == 0 ? 0ull : ((1ull << l) - 1ull);

@@ -138,53 +138,63 @@ __device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int3
 // break becomes "first candidate with active && !cont && brk" (ballot), and the
 // sequential strict-> best becomes a max-gain, lowest-index wave reduction.
 // ===========================================================================
-// Per lane k < cnt: (sg, sh, sc) += the lanes' (g, h, c) of lanes 0..k, added one at a
-// time in lane order — the reference's sequential f64 accumulation, so every prefix
-// rounds exactly as its loop does.  Lanes that hold no bin pass (+0.0, +0.0, 0):
-// adding +0.0 to an accumulation that started at a value other than -0.0 never
-// changes it.  The values go through a per-wave LDS row so the chain reads them as
-// uniform (broadcast) loads, eight candidates per batch so a batch's loads are all in
-// flight before its adds (lanes at or past cnt store zeros, so a batch may run past
-// cnt); the loop has no branch and no cross-lane move.
+// Per lane k < cnt: (sg, sh) += the lanes' (g, h) of lanes 0..k, added one at a time in
+// lane order — the reference's sequential f64 accumulation, so every prefix rounds
+// exactly as its loop does; sc += the integer counts of lanes 0..k (exact in any
+// order: a DPP inclusive scan).  The f64 values go through a per-wave LDS row behind
+// 64 cells of -0.0 (x + (-0.0) == x for every x, signed zeros included).  The loop
+// runs n8 = cnt rounded up to 8 steps and lane k reads cell 65 + j + k - n8 at step j,
+// so it adds only padding until step n8 - 1 - k and then its values 0..k in order:
+// per-lane consecutive addresses, no masking; each batch of eight cells is loaded
+// while the previous one is added.
 __device__ __forceinline__ void prefix_in_order(double g, double h, int32_t c, int32_t cnt,
                                                 int lane, double* sg, double* sh, int32_t* sc) {
-  __shared__ double pf_g[SCAN_THREADS / LGBM_WAVE][LGBM_WAVE];
-  __shared__ double pf_h[SCAN_THREADS / LGBM_WAVE][LGBM_WAVE];
-  __shared__ int32_t pf_c[SCAN_THREADS / LGBM_WAVE][LGBM_WAVE];
+  constexpr int kRow = 2 * LGBM_WAVE + 8;  // padding, values, one batch of overrun
+  __shared__ double2 pf_gh[SCAN_THREADS / LGBM_WAVE][kRow];
   const int w = (int)(threadIdx.x / LGBM_WAVE);
   const bool in = lane < cnt;
-  pf_g[w][lane] = in ? g : 0.0;
-  pf_h[w][lane] = in ? h : 0.0;
-  pf_c[w][lane] = in ? c : 0;
+  const double nz = -0.0;
+  pf_gh[w][lane] = make_double2(nz, nz);
+  pf_gh[w][LGBM_WAVE + lane] = in ? make_double2(g, h) : make_double2(nz, nz);
+  if (lane < 8) pf_gh[w][2 * LGBM_WAVE + lane] = make_double2(nz, nz);
   __builtin_amdgcn_wave_barrier();
+  *sc += wave_incl_sum_i32(in ? c : 0);
   double ag = *sg, ah = *sh;
-  int32_t ac = *sc;
   const int32_t n8 = (cnt + 7) & ~7;
-  for (int32_t i0 = 0; i0 < n8; i0 += 8) {
-    double vg[8], vh[8];
-    int32_t vc[8];
+  const double2* r = &pf_gh[w][LGBM_WAVE + 1 + lane - n8];
+  double2 cur[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) cur[u] = r[u];
+  for (int32_t j0 = 0; j0 < n8; j0 += 8) {
+    double2 nxt[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) nxt[u] = r[j0 + 8 + u];  // <= cell 135 of the row
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      vg[u] = pf_g[w][i0 + u];
-      vh[u] = pf_h[w][i0 + u];
-      vc[u] = pf_c[w][i0 + u];
+      ag += cur[u].x;
+      ah += cur[u].y;
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      // lanes before i add +0.0 (all-zero bits): a mask, not a select
-      const unsigned long long m = i0 + u <= lane ? ~0ull : 0ull;
-      ag += __longlong_as_double((long long)((unsigned long long)__double_as_longlong(vg[u]) & m));
-      ah += __longlong_as_double((long long)((unsigned long long)__double_as_longlong(vh[u]) & m));
-      ac += vc[u] & (int32_t)(uint32_t)m;
-    }
+    for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
   }
   __builtin_amdgcn_wave_barrier();  // the row is rewritten by the next call
   *sg = ag;
   *sh = ah;
-  *sc = ac;
 }
 
-static __device__ __attribute__((unused)) void wave_scan(const double* hist, const DevFeature& ft, const ScanCfg& c,
+// The best candidate of one batch of a threshold scan: the highest gain, the lowest
+// lane among equal gains (the reference's strict-> scan in candidate order); -1 when
+// no lane is a candidate.  `best` receives the gain.
+__device__ __forceinline__ int wave_best_lane(bool cand, double gain, double* best) {
+  const double g = wave_max_f64(cand ? gain : -__builtin_inf());
+  const unsigned long long m = __ballot(cand && gain == g);
+  *best = g;
+  return m ? (int)__builtin_ctzll(m) : -1;
+}
+
+// FindBestThresholdNumerical for one (leaf, feature) by one wave over the compacted
+// histogram; returns the gain written to `out` (-inf for none), in every lane.
+static __device__ __attribute__((unused)) double wave_scan(const double* hist, const DevFeature& ft, const ScanCfg& c,
                           double sum_gradient, double sum_hessian, int32_t num_data, double po,
                           lgbm_split_info* out) {
   const int lane = (int)lane_id();
@@ -225,7 +235,8 @@ static __device__ __attribute__((unused)) void wave_scan(const double* hist, con
       const bool valid = lane < cnt;
       const int32_t t = t_start - (base + lane);
       const bool act = valid && (t >= 1 - offset) && !(skip_def && t + offset == defb);
-      const double mg = act ? hist[2 * t] : 0.0, mh = act ? hist[2 * t + 1] : 0.0;
+      const double2 m2 = act ? ((const double2*)hist)[t] : make_double2(0.0, 0.0);
+      const double mg = m2.x, mh = m2.y;
       const int32_t mc = act ? round_int(mh * cf) : 0;
       double sg = cg, sh = ch;
       int32_t rc = cc;
@@ -239,30 +250,23 @@ static __device__ __attribute__((unused)) void wave_scan(const double* hist, con
       const bool consider = act && !cont && lane < first_brk;
       double gain = ninf;
       if (consider) gain = split_gain_of(c, slg, slh, sg, sh, lc, rc, po);
-      const bool cand = consider && gain > mgs;
-      if (__ballot(cand)) any_split = true;
-      double rg = cand ? gain : ninf;
-      int32_t rl = cand ? lane : LGBM_WAVE;
-      for (int off = 32; off >= 1; off >>= 1) {
-        const double og = __shfl_xor(rg, off);
-        const int32_t ol = __shfl_xor(rl, off);
-        if (og > rg || (og == rg && ol < rl)) {
-          rg = og;
-          rl = ol;
+      double bg;
+      const int rl = wave_best_lane(consider && gain > mgs, gain, &bg);
+      if (rl >= 0) {
+        any_split = true;
+        if (bg > best_gain) {
+          best_gain = bg;
+          best_lc = readlane_i32(lc, rl);
+          best_lg = readlane_f64(slg, rl);
+          best_lh = readlane_f64(slh, rl);
+          best_thr = readlane_i32(t, rl) - 1 + offset;
+          best_dl = true;
         }
       }
-      if (rl < LGBM_WAVE && rg > best_gain) {
-        best_gain = rg;
-        best_lc = __shfl(lc, rl);
-        best_lg = __shfl(slg, rl);
-        best_lh = __shfl(slh, rl);
-        best_thr = __shfl(t, rl) - 1 + offset;
-        best_dl = true;
-      }
       if (bm) break;
-      cg = __shfl(sg, cnt - 1);
-      ch = __shfl(sh, cnt - 1);
-      cc = __shfl(rc, cnt - 1);
+      cg = readlane_f64(sg, cnt - 1);
+      ch = readlane_f64(sh, cnt - 1);
+      cc = readlane_i32(rc, cnt - 1);
     }
   }
   {  // FORWARD (split.rs:9178-9277)
@@ -292,7 +296,8 @@ static __device__ __attribute__((unused)) void wave_scan(const double* hist, con
       const int32_t t = fwd_start + base + lane;
       const bool act = valid && !(skip_def && t + offset == defb);
       const bool addl = act && t >= 0;
-      const double mg = addl ? hist[2 * t] : 0.0, mh = addl ? hist[2 * t + 1] : 0.0;
+      const double2 m2 = addl ? ((const double2*)hist)[t] : make_double2(0.0, 0.0);
+      const double mg = m2.x, mh = m2.y;
       const int32_t mc = addl ? round_int(mh * cf) : 0;
       double sg = cg, sh = ch;
       int32_t lcn = cc;
@@ -306,30 +311,23 @@ static __device__ __attribute__((unused)) void wave_scan(const double* hist, con
       const bool consider = act && !cont && lane < first_brk;
       double gain = ninf;
       if (consider) gain = split_gain_of(c, sg, sh, srg, srh, lcn, rc, po);
-      const bool cand = consider && gain > mgs;
-      if (__ballot(cand)) any_split = true;
-      double rg = cand ? gain : ninf;
-      int32_t rl = cand ? lane : LGBM_WAVE;
-      for (int off = 32; off >= 1; off >>= 1) {
-        const double og = __shfl_xor(rg, off);
-        const int32_t ol = __shfl_xor(rl, off);
-        if (og > rg || (og == rg && ol < rl)) {
-          rg = og;
-          rl = ol;
+      double bg;
+      const int rl = wave_best_lane(consider && gain > mgs, gain, &bg);
+      if (rl >= 0) {
+        any_split = true;
+        if (bg > best_gain) {
+          best_gain = bg;
+          best_lc = readlane_i32(lcn, rl);
+          best_lg = readlane_f64(sg, rl);
+          best_lh = readlane_f64(sh, rl);
+          best_thr = readlane_i32(t, rl) + offset;
+          best_dl = false;
         }
       }
-      if (rl < LGBM_WAVE && rg > best_gain) {
-        best_gain = rg;
-        best_lc = __shfl(lcn, rl);
-        best_lg = __shfl(sg, rl);
-        best_lh = __shfl(sh, rl);
-        best_thr = __shfl(t, rl) + offset;
-        best_dl = false;
-      }
       if (bm) break;
-      cg = __shfl(sg, cnt - 1);
-      ch = __shfl(sh, cnt - 1);
-      cc = __shfl(lcn, cnt - 1);
+      cg = readlane_f64(sg, cnt - 1);
+      ch = readlane_f64(sh, cnt - 1);
+      cc = readlane_i32(lcn, cnt - 1);
     }
   }
   if (lane == 0) {
@@ -356,6 +354,7 @@ static __device__ __attribute__((unused)) void wave_scan(const double* hist, con
       split_set_none(out);
     }
   }
+  return any_split && best_gain > ninf ? best_gain - mgs : ninf;
 }
 
 // ===========================================================================
@@ -371,8 +370,9 @@ static __device__ __attribute__((unused)) void wave_scan(const double* hist, con
 //   wins ties (it runs first in the reference).
 // sum_hessian is the leaf's raw sum; the scan bumps it by 2 kEpsilon as the
 // categorical dispatch does (learner.rs:3103-3118).  `bits` (8 words) receives the
-// bins that go left.  A NaN sort key (cat_smooth <= 0 and an empty category) ranks
-// as 0.0: the reference's order for it depends on its sort algorithm.
+// bins that go left; the return value is the gain written to `out` (-inf for none).
+// A NaN sort key (cat_smooth <= 0 and an empty category) ranks as 0.0: the
+// reference's order for it depends on its sort algorithm.
 // ===========================================================================
 __device__ __forceinline__ double leaf_gain_given_output(bool use_l1, double g, double h,
                                                          double l1, double l2, double out) {
@@ -380,7 +380,7 @@ __device__ __forceinline__ double leaf_gain_given_output(bool use_l1, double g, 
   return -__builtin_fma(2.0 * gg, out, (h + l2) * out * out);
 }
 
-static __device__ __attribute__((unused)) void wave_scan_cat(const double* hist, const DevFeature& ft, const ScanCfg& c,
+static __device__ __attribute__((unused)) double wave_scan_cat(const double* hist, const DevFeature& ft, const ScanCfg& c,
                                      const lgbm_gain_config& cfg, double sum_gradient,
                                      double sum_hessian, int32_t num_data, double po,
                                      lgbm_split_info* out, uint32_t* bits) {
@@ -567,6 +567,7 @@ static __device__ __attribute__((unused)) void wave_scan_cat(const double* hist,
       out->threshold = 0;
     }
   }
+  return any ? best_gain - mgs : ninf;
 }
 
 struct BestKey {
@@ -614,25 +615,32 @@ __device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* 
   if (tid < LGBM_WAVE && mfb > 0 && mfb < nb) {
     // leaf sum minus the other bins in ascending order (the sequential f64 chain),
     // every lane of wave 0 the same chain over broadcast LDS reads, eight bins per
-    // batch; the skipped bin and bins past num_bin subtract +0.0 (an exact no-op)
+    // batch.  The skipped bin is parked at +0.0 first (x - (+0.0) == x for every x)
+    // and overwritten with the result.
+    if (tid == 0) {
+      cs[2 * mfb] = 0.0;
+      cs[2 * mfb + 1] = 0.0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const double2* c2 = (const double2*)cs;
     double g = sg, h = sh;
-    const int n8 = (nb + 7) & ~7;
-    for (int i0 = 0; i0 < n8; i0 += 8) {
-      double vg[8], vh[8];
+    int i = 0;
+    for (; i + 8 <= nb; i += 8) {
+      double2 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = c2[i + u];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int i = i0 + u;
-        const bool use = i < nb && i != mfb;
-        const double a = cs[2 * i], b = cs[2 * i + 1];
-        vg[u] = use ? a : 0.0;
-        vh[u] = use ? b : 0.0;
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        g -= vg[u];
-        h -= vh[u];
+        g -= v[u].x;
+        h -= v[u].y;
       }
     }
+    for (; i < nb; ++i) {
+      const double2 v = c2[i];
+      g -= v.x;
+      h -= v.y;
+    }
+    __builtin_amdgcn_wave_barrier();
     if (tid == 0) {
       cs[2 * mfb] = g;
       cs[2 * mfb + 1] = h;
