@@ -195,7 +195,8 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   __shared__ int4 s_pick[SPEC_MAX];        // (leaf, node slot, left slot, right slot)
   __shared__ int32_t s_red[2 * SPEC_MAX + 2];
   __shared__ int32_t s_ntiles[SPEC_MAX];
-  __shared__ int32_t s_nc, s_nj, s_nl, s_done, s_nslots, s_nS, s_ncand;
+  __shared__ int32_t s_nc, s_nj, s_nl, s_done, s_nslots, s_nS, s_ncand, s_nsurv;
+  __shared__ int32_t s_surv[MAX_LEAVES];   //   the candidates that survive pass A
   __shared__ unsigned long long s_uhi, s_ulo;  // best unsplit leaf key at the start
   __shared__ LKey s_key[MAX_LEAVES];       // per leaf: its ArgMax key
   __shared__ LKey s_ck[MAX_LEAVES];        //   the same for selection candidates, else 0
@@ -216,9 +217,16 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   const int32_t nred = ctl->n_reduce, spec = ctl->spec_max, cerr = ctl->error;
   const bool fp = ctl->fp_mode != 0;
   if (tid < 2 * SPEC_MAX + 2) s_red[tid] = ctl->reduce_list[tid];
+  // this wave's first slot of phase 1 and its first chunk of feature gains, loaded
+  // with the prefetch
+  static_assert(PLAN_WAVES <= 2 * SPEC_MAX + 2, "reduce_list covers a slot per wave");
+  const bool red0 = wave < nred;
+  const int32_t s_w = ctl->reduce_list[wave];
+  const double g_w = (red0 && lane < F) ? L.feat_split[(size_t)s_w * F + lane].gain : ninf;
   if (tid == 0) {
     s_nS = 0;
     s_ncand = 0;
+    s_nsurv = 0;
     s_uhi = 0ull;
     s_ulo = 0ull;
   }
@@ -241,11 +249,11 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     const int32_t s = s_red[i];
     BestKey k{ninf, -1, INT_MAX32};
     for (int f = lane; f < F; f += LGBM_WAVE) {
-      const double g = L.feat_split[(size_t)s * F + f].gain;
+      const double g = (i == wave && f == lane) ? g_w : L.feat_split[(size_t)s * F + f].gain;
       const BestKey c{g, fts[f].real_index, f};
       if (g > ninf && key_better(c, k)) k = c;
     }
-    k = wave_best(k);
+    k = wave_best_fast(k);
     const bool have = k.idx != INT_MAX32 && k.gain > ninf;
     if (lane == 0) {
       const double kg = have ? k.gain : ninf;
@@ -388,8 +396,11 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   // ---- 3. selection ------------------------------------------------------------
   // The ArgMax leaf, then the next best-ranked unsplit leaves with gain > 0, up to
   // spec_max; beyond the first, two node slots stay in reserve for every split the
-  // tree may still need, so the ArgMax leaf of every later round can be split.  Each
-  // candidate's rank (number of better candidates) is counted by 4 threads.
+  // tree may still need, so the ArgMax leaf of every later round can be split.  A
+  // candidate's rank is the number of better candidates (keys of non-candidates are
+  // 0, below every candidate), found in two passes.
+  static_assert(PLAN_THREADS == 4 * MAX_LEAVES && MAX_LEAVES % 32 == 0,
+                "selection: four threads per leaf, groups of 32 leaves");
   if (!s_done) {
     const int32_t nl = nl_;
     if (tid < MAX_LEAVES) {  // whole waves, one LDS atomic per wave
@@ -399,6 +410,8 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
         const LKey k = s_key[l];
         cand = s_lc[l].x < 0 && k.hi != 0ull;
         s_ck[l] = cand ? k : LKey{0ull, 0ull};
+      } else {
+        s_ck[l] = LKey{0ull, 0ull};
       }
       const unsigned long long cm = __ballot(cand);
       if (lane == 0 && cm) atomicAdd(&s_ncand, (int32_t)__popcll(cm));
@@ -409,17 +422,41 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
       const int32_t extra = (slot_cap - ns0 - 2 - 2 * (maxl - nl)) / 2;
       allowed = min(spec, 1 + max(extra, 0));
     }
-    const int32_t l = tid >> 2, q = tid & 3;
-    const LKey c = l < nl ? s_ck[l] : LKey{0ull, 0ull};
-    int32_t r = 0;
-    if (c.hi != 0ull) {
-#pragma unroll 4
-      for (int m = q; m < nl; m += 4) r += lk_gt(s_ck[m], c) ? 1 : 0;
+    // pass A: a candidate's rank within its group of 32 leaves (4 threads, 8 keys
+    // each); the group's best `allowed` survive.  Every candidate of the overall best
+    // `allowed` survives (all better ones are better in their groups too), so pass B,
+    // which ranks the survivors among themselves, gives the exact ranks of those.
+    {
+      const int l = tid >> 2, q = tid & 3, gb = l & ~31;
+      const LKey c = s_ck[l];
+      int32_t ra = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ra += lk_gt(s_ck[gb + q + 4 * i], c) ? 1 : 0;
+      ra += __builtin_amdgcn_update_dpp(0, ra, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+      ra += __builtin_amdgcn_update_dpp(0, ra, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+      const bool surv = q == 0 && c.hi != 0ull && ra < allowed;
+      const unsigned long long sm = __ballot(surv);
+      int32_t base = 0;
+      if (lane == 0 && sm) base = atomicAdd(&s_nsurv, (int32_t)__popcll(sm));
+      base = __builtin_amdgcn_readfirstlane(base);
+      if (surv) s_surv[base + (int32_t)__popcll(sm & lanemask_lt())] = l;
     }
-    r += __shfl_xor(r, 1);
-    r += __shfl_xor(r, 2);
-    if (q == 0 && c.hi != 0ull && r < allowed)
-      s_pick[r] = make_int4(l, s_ps[PS_LEAF_SLOT][l], ns0 + 2 * r, ns0 + 2 * r + 1);
+    __syncthreads();
+    // pass B: 16 threads per survivor (one DPP row), 64 survivors per step
+    const int32_t nsv = s_nsurv;
+    for (int32_t u0 = 0; u0 < nsv; u0 += PLAN_THREADS / 16) {
+      const int32_t u = u0 + (tid >> 4), sub = tid & 15;
+      const int32_t l = u < nsv ? s_surv[u] : 0;
+      const LKey c = u < nsv ? s_ck[l] : LKey{0ull, 0ull};
+      int32_t rb = 0;
+      for (int32_t v = sub; v < nsv; v += 16) rb += lk_gt(s_ck[s_surv[v]], c) ? 1 : 0;
+      rb += __builtin_amdgcn_update_dpp(0, rb, 0xB1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
+      rb += __builtin_amdgcn_update_dpp(0, rb, 0x4E, 0xf, 0xf, false);   // quad_perm [2,3,0,1]
+      rb += __builtin_amdgcn_update_dpp(0, rb, 0x141, 0xf, 0xf, false);  // row_half_mirror
+      rb += __builtin_amdgcn_update_dpp(0, rb, 0x140, 0xf, 0xf, false);  // row_mirror
+      if (sub == 0 && c.hi != 0ull && rb < allowed)
+        s_pick[rb] = make_int4(l, s_ps[PS_LEAF_SLOT][l], ns0 + 2 * rb, ns0 + 2 * rb + 1);
+    }
     if (tid == 0) {
       const int32_t nj = min(s_ncand, allowed);
       s_nj = nj;

@@ -595,6 +595,21 @@ __device__ __forceinline__ BestKey wave_best(BestKey k) {
   return k;
 }
 
+// wave_best with the common case fast: the highest gain by a DPP maximum, and when
+// one lane alone holds it, that lane's key; ties (or no key) take the exact order.
+__device__ __forceinline__ BestKey wave_best_fast(BestKey k) {
+  const double ninf = -__builtin_inf();
+  const bool valid = k.idx != 0x7fffffff;  // no key
+  const double gm = wave_max_f64(valid ? k.gain : ninf);
+  if (!(gm > ninf)) return BestKey{ninf, -1, 0x7fffffff};
+  const unsigned long long m = __ballot(valid && k.gain == gm);
+  if (__popcll(m) == 1) {
+    const int r = (int)__builtin_ctzll(m);
+    return BestKey{gm, readlane_i32(k.feat, r), readlane_i32(k.idx, r)};
+  }
+  return wave_best(k);
+}
+
 // FixHistogram (fix_histogram.rs:50-80) on the RAW leaf sums, then compaction
 // (compact_histogram, learner.rs:4460-4492), on one feature's cells in LDS.  The fix
 // is the reference's sequential f64 subtraction in ascending bin order: each lane of
