@@ -194,7 +194,6 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   __shared__ int2 s_lcf[MAX_LEAVES];
   __shared__ int4 s_pick[SPEC_MAX];        // (leaf, node slot, left slot, right slot)
   __shared__ int32_t s_red[2 * SPEC_MAX + 2];
-  __shared__ int32_t s_ntiles[SPEC_MAX];
   __shared__ int32_t s_nc, s_nj, s_nl, s_done, s_nslots, s_nS, s_ncand, s_nsurv;
   __shared__ int32_t s_surv[MAX_LEAVES];   //   the candidates that survive pass A
   __shared__ unsigned long long s_uhi, s_ulo;  // best unsplit leaf key at the start
@@ -526,78 +525,89 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     L.plan_state[PS_NODE_LEFT * MAX_LEAVES + n] = s_ps[PS_NODE_LEFT][n];
     L.plan_state[PS_NODE_RIGHT * MAX_LEAVES + n] = s_ps[PS_NODE_RIGHT][n];
   }
-  for (int j = tid; j < nj; j += PLAN_THREADS) {
-    const int4 pk = s_pick[j];
-    const int32_t p = pk.y, cl = pk.z, cr = pk.w, fpos = s_fpos[p];
-    const lgbm_split_info b = L.feat_split[(size_t)p * F + fpos];
-    const DevFeature ft = fts[fpos];
+  // the picks on wave PICK_WAVE, one lane each, beside the commits (waves 0-3): their
+  // loads overlap, and the wave's prefix sum places each job's tiles
+  constexpr int PICK_WAVE = PLAN_WAVES / 2;
+  static_assert(SPEC_MAX <= LGBM_WAVE && PICK_WAVE * LGBM_WAVE >= MAX_LEAVES,
+                "picks: one lane each on a wave of their own");
+  if (wave == PICK_WAVE) {
+    const int j = lane;
+    const bool pick = j < nj;
     PartJob J;
-    J.parent = p;
-    J.cl = cl;
-    J.cr = cr;
-    J.src_buf = nd.buf[p];
-    J.rev = nd.rev[p];
-    J.begin = nd.begin[p];
-    J.count = nd.count[p];
-    const int32_t d = nd.depth[p] + 1;
-    J.dst_buf = J.src_buf == BUF_A ? BUF_B : BUF_A;
-    J.fbyte = fpos;
-    router_of(ft, b, &J.pmin, &J.th, &J.flags);
-    J.max_bin = (int32_t)ft.max_bin;
-    J.na_bin = (int32_t)ft.num_bin - 1;
-    if (ft.categorical) {
-      // bit 8: the SplitInfo counts make the left child the smaller one
-      J.flags = ROUTE_CAT | (b.left_count < b.right_count ? 1 << 8 : 0);
-      const uint32_t* cb = L.cat_bits + ((size_t)p * F + fpos) * 8;
+    lgbm_split_info b;
+    int32_t d = 0;
+    if (pick) {
+      const int4 pk = s_pick[j];
+      const int32_t p = pk.y, fpos = s_fpos[p];
+      b = L.feat_split[(size_t)p * F + fpos];
+      const DevFeature ft = fts[fpos];
+      J.parent = p;
+      J.cl = pk.z;
+      J.cr = pk.w;
+      J.src_buf = nd.buf[p];
+      J.rev = nd.rev[p];
+      J.begin = nd.begin[p];
+      J.count = nd.count[p];
+      d = nd.depth[p] + 1;
+      J.dst_buf = J.src_buf == BUF_A ? BUF_B : BUF_A;
+      J.fbyte = fpos;
+      router_of(ft, b, &J.pmin, &J.th, &J.flags);
+      J.max_bin = (int32_t)ft.max_bin;
+      J.na_bin = (int32_t)ft.num_bin - 1;
+      if (ft.categorical) {
+        // bit 8: the SplitInfo counts make the left child the smaller one
+        J.flags = ROUTE_CAT | (b.left_count < b.right_count ? 1 << 8 : 0);
+        const uint32_t* cb = L.cat_bits + ((size_t)p * F + fpos) * 8;
 #pragma unroll
-      for (int w = 0; w < 8; ++w) J.cat[w] = cb[w];
+        for (int w = 0; w < 8; ++w) J.cat[w] = cb[w];
+      }
+      // quantized gradients: build the histogram of the side the scan expects to be
+      // smaller inside the partition pass (f32: k_hist_f32 builds the smaller child)
+      J.acc_right = fp ? -1 : (b.right_count < b.left_count ? 1 : 0);
+      J.ntiles = (int32_t)((J.count + part_tile(L.fmt) - 1) / part_tile(L.fmt));
     }
-    // quantized gradients: build the histogram of the side the scan expects to be
-    // smaller inside the partition pass (f32: k_hist_f32 builds the smaller child)
-    J.acc_right = fp ? -1 : (b.right_count < b.left_count ? 1 : 0);
-    J.ntiles = (int32_t)((J.count + part_tile(L.fmt) - 1) / part_tile(L.fmt));
-    J.tile0 = 0;
-    ctl->jobs[j] = J;
-    ctl->part_cur[j] = 0ull;
-    ctl->acc_used[j] = 0;
-    s_ntiles[j] = J.ntiles;
-    nd.child[2 * p] = cl;
-    nd.child[2 * p + 1] = cr;
-    nd.child[2 * cl] = -1;
-    nd.child[2 * cl + 1] = -1;
-    nd.child[2 * cr] = -1;
-    nd.child[2 * cr + 1] = -1;
-    nd.depth[cl] = d;
-    nd.depth[cr] = d;
-    // LeafSplits::init_from_split (leaf_splits.rs:162-173): sums and outputs of the
-    // SplitInfo; counts come from the partition.
-    nd.sums[cl] = LeafSums{b.left_sum_gradient, b.left_sum_hessian, b.left_output, 0, 0};
-    nd.sums[cr] = LeafSums{b.right_sum_gradient, b.right_sum_hessian, b.right_output, 0, 0};
-    nd.key_gain[cl] = ninf;
-    nd.key_gain[cr] = ninf;
-    nd.key_feat[cl] = -1;
-    nd.key_feat[cr] = -1;
-    L.best_fpos[cl] = -1;
-    L.best_fpos[cr] = -1;
-    ctl->reduce_list[2 * j] = cl;
-    ctl->reduce_list[2 * j + 1] = cr;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int64_t acc = 0;
-    for (int j = 0; j < nj; ++j) {
-      ctl->jobs[j].tile0 = acc;
-      acc += s_ntiles[j];
+    // each job's first tile: the exclusive prefix of the tile counts (all lanes)
+    const int32_t nt = pick ? J.ntiles : 0;
+    const int32_t incl = wave_incl_sum_i32(nt);
+    if (pick) {
+      const int32_t p = J.parent, cl = J.cl, cr = J.cr;
+      J.tile0 = incl - nt;
+      ctl->jobs[j] = J;
+      ctl->part_cur[j] = 0ull;
+      ctl->acc_used[j] = 0;
+      nd.child[2 * p] = cl;
+      nd.child[2 * p + 1] = cr;
+      nd.child[2 * cl] = -1;
+      nd.child[2 * cl + 1] = -1;
+      nd.child[2 * cr] = -1;
+      nd.child[2 * cr + 1] = -1;
+      nd.depth[cl] = d;
+      nd.depth[cr] = d;
+      // LeafSplits::init_from_split (leaf_splits.rs:162-173): sums and outputs of the
+      // SplitInfo; counts come from the partition.
+      nd.sums[cl] = LeafSums{b.left_sum_gradient, b.left_sum_hessian, b.left_output, 0, 0};
+      nd.sums[cr] = LeafSums{b.right_sum_gradient, b.right_sum_hessian, b.right_output, 0, 0};
+      nd.key_gain[cl] = ninf;
+      nd.key_gain[cr] = ninf;
+      nd.key_feat[cl] = -1;
+      nd.key_feat[cr] = -1;
+      L.best_fpos[cl] = -1;
+      L.best_fpos[cr] = -1;
+      ctl->reduce_list[2 * j] = cl;
+      ctl->reduce_list[2 * j + 1] = cr;
     }
-    ctl->tile_total = acc;
-    ctl->n_jobs = nj;
-    if (fp || rec_wide(L.fmt)) ctl->n_hjobs = nj;  // k_partition fills in each job's side
-    ctl->n_reduce = 2 * nj;
-    ctl->num_leaves = nl;
-    ctl->n_slots = s_nslots;
-    ctl->rounds += 1;
-    if (nj > 0) L.stats[1] += 1.0;
-    if (s_done) ctl->done = 1;
+    const int32_t total = readlane_i32(incl, LGBM_WAVE - 1);
+    if (lane == 0) {
+      ctl->tile_total = total;
+      ctl->n_jobs = nj;
+      if (fp || rec_wide(L.fmt)) ctl->n_hjobs = nj;  // k_partition fills in each job's side
+      ctl->n_reduce = 2 * nj;
+      ctl->num_leaves = nl;
+      ctl->n_slots = s_nslots;
+      ctl->rounds += 1;
+      if (nj > 0) L.stats[1] += 1.0;
+      if (s_done) ctl->done = 1;
+    }
   }
 }
 
