@@ -198,6 +198,7 @@ struct lgbm_hip_ctx {
   int32_t* hist_part = nullptr;  // [HIST_SLOTS][cells][3]
   int32_t* hist_sum = nullptr;   // [cells][3]
   int32_t* hist_acc = nullptr;   // [SPEC_MAX][acc_cells][3]
+  unsigned long long* hist_accp = nullptr;  // [SPEC_MAX][acc_cells] packed (small jobs)
   int64_t* hist_acc64 = nullptr;  // wide layout: [SPEC_MAX][acc_cells][2]
   unsigned long long* wide_part = nullptr;  // wide layout: per-chunk partial cells
   int32_t acc_cells = 0;          // total_cells (+ 1 totals cell in the wide layout)
@@ -370,6 +371,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.hist_sum = c->hist_sum;
   L.hist_acc = c->hist_acc;
   L.hist_acc64 = c->hist_acc64;
+  L.hist_accp = c->hist_accp;
   L.wide_part = c->wide_part;
   L.acc_cells = c->acc_cells;
   L.binmat = c->binmat;
@@ -1047,6 +1049,8 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   }
   if ((rc = dalloc(c, &c->hist_acc, (size_t)SPEC_MAX * c->acc_cells * 3))) return rc;
   HIPCHK(c, hipMemset(c->hist_acc, 0, (size_t)SPEC_MAX * c->acc_cells * 3 * 4));
+  if ((rc = dalloc(c, &c->hist_accp, (size_t)SPEC_MAX * c->acc_cells))) return rc;
+  HIPCHK(c, hipMemset(c->hist_accp, 0, (size_t)SPEC_MAX * c->acc_cells * 8));
   if ((rc = dalloc(c, &c->part_slots, ((size_t)c->part_blocks + SPEC_MAX) * pc))) return rc;
   if ((rc = ensure_tile_state(c, num_data))) return rc;
   return LGBM_HIP_OK;
@@ -1183,6 +1187,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->hist_part);
   F(c->hist_sum);
   F(c->hist_acc);
+  F(c->hist_accp);
   F(c->hist_acc64);
   F(c->wide_part);
   F(c->d_wgroups);

@@ -86,6 +86,7 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
     }
   } else {
     for (int i = tid; i < SPEC_MAX * L.acc_cells * 3; i += nthr) L.hist_acc[i] = 0;
+    for (int i = tid; i < SPEC_MAX * L.acc_cells; i += nthr) L.hist_accp[i] = 0ull;
   }
   if (tid == 0) {
     const int32_t N = (int32_t)L.N;
@@ -688,7 +689,9 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   // blocks gets one packed slot per block (slot block + job: unique, since blocks and
   // jobs both advance along the tile order), which k_pair_scan sums; a wider job, and
   // a block's second and later flush of one job, atomic adds into the job's
-  // accumulator and marks it used (k_pair_scan then reads and clears it).
+  // accumulator and marks it used (k_pair_scan then reads and clears it): one 64-bit
+  // add of the packed cell when the job has fewer than 2^19 rows (its sums fit the
+  // packed fields as a block's do), else three 32-bit adds.
   auto flush = [&]() {
     const PartJob& C = s_jobs[cur];
     if (!flushed && part_span_blocks(C.tile0, C.ntiles, total, G) <= PART_SLOT_MAX) {
@@ -696,7 +699,12 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
                            FLUSH_STORE);
     } else {
       if (tid == 0) ctl->acc_used[cur] = 1;
-      lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * L.acc_cells * 3, FLUSH_ATOMIC);
+      if (C.count <= PACKED_ACC_MAX_ROWS)
+        lds_hist_flush_clear(lds_hist, cells, L.hist_accp + (size_t)cur * L.acc_cells,
+                             FLUSH_ATOMIC64);
+      else
+        lds_hist_flush_clear(lds_hist, cells, L.hist_acc + (size_t)cur * L.acc_cells * 3,
+                             FLUSH_ATOMIC);
     }
   };
   struct TileBuf {
@@ -1090,6 +1098,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
     const bool use_slots =
         !wide && (jnt > 0 ? part_span_blocks(jt0, jnt, T, part_grid) <= PART_SLOT_MAX : true);
     const bool read_acc = !wide && (!use_slots || acc_used != 0);
+    const bool acc_packed = J.count <= PACKED_ACC_MAX_ROWS;
+    unsigned long long* accp = L.hist_accp + (size_t)j * L.acc_cells;
     const int32_t wa0 = ctl->hjobs[j].a0, wna = wide ? ctl->hjobs[j].nblk : 0;
     int32_t* acc = L.hist_acc + (size_t)j * L.acc_cells * 3;
     const unsigned long long* slots = L.part_slots;
@@ -1100,7 +1110,10 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
       if (b >= nb) continue;
       const size_t ci = (size_t)(ft.cell_base + b);
       int32_t AG = 0, AH = 0, AT = 0;
-      if (read_acc) {
+      if (read_acc && acc_packed) {
+        unpack_cell(accp[ci], &AG, &AH, &AT);
+        accp[ci] = 0ull;
+      } else if (read_acc) {
         int32_t* a = acc + ci * 3;
         AG = a[0];
         AH = a[1];

@@ -118,6 +118,7 @@ struct DevLearner {
   int32_t* hist_part;         // [HIST_SLOTS][total_cells][3] root / per-op partials
   int32_t* hist_sum;          // [total_cells][3] job 0's partials summed (k_hist_reduce)
   int32_t* hist_acc;          // [SPEC_MAX][acc_cells][3] per-job accumulators
+  unsigned long long* hist_accp;  // [SPEC_MAX][acc_cells] packed accumulators (small jobs)
   int64_t* hist_acc64;        // wide layout, f32 gradients: [SPEC_MAX][acc_cells][2]
   unsigned long long* wide_part;  // wide layout: per-chunk partial cells [chunks][cells][1 or 2]
   int32_t acc_cells;          // cells per accumulator: total_cells, + 1 (row totals) when wide

@@ -48,6 +48,7 @@
 #endif
 #define PART_WAVES (PART_THREADS / LGBM_WAVE)
 #define PART_SLOT_MAX 8                 // blocks per job whose cells go to per-block slots
+#define PACKED_ACC_MAX_ROWS ((1 << 19) - 1)  // jobs whose accumulator takes packed 64-bit adds
 #define QUANT_MAX_ROWS (1ll << 29)      // int32 cells: sum of q_h <= 4 N < 2^31
 #define QUANT_LDS_CELLS 8192            // quantized builds: every cell in LDS (8 B, 64 KiB)
 #define PART_MIN_TILE 1024                // smallest tile of any partition launch shape

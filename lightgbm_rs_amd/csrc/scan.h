@@ -711,12 +711,15 @@ __device__ __forceinline__ void unpack_cell(unsigned long long p, int32_t* g, in
 
 // Moves a block's packed LDS histogram into integer cells (G, H, T) and clears it (the
 // trash cells too).  mode FLUSH_ATOMIC: atomic adds into a shared int32 [cells][3]
-// accumulator (zero cells skipped); FLUSH_STORE: the packed cells as they are into
+// accumulator (zero cells skipped); FLUSH_ATOMIC64: 64-bit atomic adds of the packed
+// cells into a u64 [cells] accumulator (the caller bounds the summed rows below 2^19,
+// so no field carries); FLUSH_STORE: the packed cells as they are into
 // the block's own u64 [cells] slot (one flush per slot: a slot holds fewer than 2^19
 // rows per cell, as the LDS histogram does).  The caller has synchronised the block
 // after the last accumulation.
 #define FLUSH_ATOMIC 0
 #define FLUSH_STORE 1
+#define FLUSH_ATOMIC64 2
 __device__ __forceinline__ void lds_hist_flush_clear(unsigned long long* lds, int cells,
                                                      void* __restrict__ out, int mode) {
   for (int c = threadIdx.x; c < cells + 4; c += blockDim.x) {
@@ -725,6 +728,12 @@ __device__ __forceinline__ void lds_hist_flush_clear(unsigned long long* lds, in
     if (c >= cells) continue;  // trash cells
     if (mode == FLUSH_STORE) {
       ((unsigned long long*)out)[c] = p;
+      continue;
+    }
+    if (mode == FLUSH_ATOMIC64) {
+      if (p != 0ull)
+        __hip_atomic_fetch_add((unsigned long long*)out + c, p, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
       continue;
     }
     int32_t gsum, hsum, n3;
