@@ -673,15 +673,78 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   if (tid < SPEC_MAX) s_jobs[tid] = ctl->jobs[tid];
   if (nj <= 0 || t_lo >= t_hi) return;
   const int F = L.F, cells = L.total_cells, nw = (F + BPW - 1) / BPW;
+  // the bin slots' cell bases, loaded before the first tile so that waiting for them
+  // does not wait for the tile's loads (the load counter drains in issue order)
+  static_assert(NS <= PT, "a slot per thread");
+  const int32_t cb_v = tid < NS ? (tid < F ? (int32_t)L.feats[tid].cell_base : cells) : 0;
+  struct TileBuf {
+    uint32_t w[PR][U];
+    GhT q[PR];
+    bool valid[PR];
+    bool q_in_rec;  // q still sits in the records (taken out when the tile is processed)
+  };
+  // Issues every load of tile t of a job (first tile tile0, `count` rows from `begin`,
+  // stored reversed when rev) at once: positions past the job's end re-read its last
+  // row (a job that owns a tile has count >= 1).
+  auto load_job = [&](int64_t t, TileBuf& B, int64_t tile0, int64_t count, int64_t begin,
+                      int32_t rev, int32_t src_buf) {
+    const int64_t base = (t - tile0) * kTile;
+    const uint4* __restrict__ src = rec_buf(L.bufs, src_buf);
+    const GhT* __restrict__ sgh = gh_buf<GhT>(L.bufs, src_buf);
+    const bool from_rec = EMBED && src_buf != BUF_ORIG;
+#pragma unroll
+    for (int k = 0; k < PR; ++k) {
+      const int64_t p = base + (int64_t)k * PT + tid;
+      B.valid[k] = p < count;
+      const int64_t pc = B.valid[k] ? p : count - 1;
+      const int64_t phys = rev ? begin + count - 1 - pc : begin + pc;
+      rec_load<FMT>(src, phys, B.w[k]);
+      if constexpr (EMBED) {
+        if (!from_rec) B.q[k] = sgh[phys];
+      } else {
+        B.q[k] = sgh[phys];
+      }
+    }
+    // the pairs embedded in the records are taken out in process(): reading them here
+    // would wait for the loads and void the overlap with the current tile
+    B.q_in_rec = from_rec;
+  };
+  int32_t jl = 0;  // job of the last tile loaded
+  // tile t's job from the LDS job records; returns it
+  auto load = [&](int64_t t, TileBuf& B) -> int32_t {
+    while (jl + 1 < nj && s_jobs[jl + 1].tile0 <= t) ++jl;
+    const PartJob& J = s_jobs[jl];
+    load_job(t, B, J.tile0, J.count, J.begin, J.rev, J.src_buf);
+    return jl;
+  };
+  // The first tile's job from the job records in registers (lane k: job k; jobs are in
+  // tile order, an empty job shares the next one's first tile), so its loads are in
+  // flight while the block sets up its LDS.
+  TileBuf cur_b, next_b;
+  int32_t jc = 0, jn = 0;
+  {
+    const bool lj = lane < nj;
+    const PartJob& gj = ctl->jobs[lj ? lane : 0];
+    const int64_t t0k = lj ? gj.tile0 : INT64_MAX;
+    const int64_t cntk = gj.count, begk = gj.begin;
+    const int32_t revk = gj.rev, srck = gj.src_buf;
+    jc = (int32_t)__popcll(__ballot(t0k <= t_lo)) - 1;  // job 0 starts at tile 0
+    jl = jc;
+    auto rl64 = [&](int64_t v) {
+      return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), jc) << 32) |
+                       (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)v, jc));
+    };
+    load_job(t_lo, cur_b, rl64(t0k), rl64(cntk), rl64(begk), __builtin_amdgcn_readlane(revk, jc),
+             __builtin_amdgcn_readlane(srck, jc));
+  }
   if constexpr (HIST)
     for (int c = tid; c < cells + LDS_TRASH_CELLS; c += PT) lds_hist[c] = 0ull;
-  for (int f = tid; f < NS; f += PT) cb[f] = f < F ? (int32_t)L.feats[f].cell_base : cells;
+  if (tid < NS) cb[tid] = cb_v;
   __syncthreads();
   // bin-slot cell bases in scalar registers (slots beyond F map to the trash cell)
   int32_t cbr[NS];
 #pragma unroll
   for (int f = 0; f < NS; ++f) cbr[f] = __builtin_amdgcn_readfirstlane(cb[f]);
-  int32_t jl = 0;         // job of the last tile loaded
   int32_t cur = -1;       // job whose rows the LDS histogram holds
   int32_t held = 0;       // tiles of that job in the LDS histogram
   bool flushed = false;   // this block already flushed part of that job
@@ -707,42 +770,6 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
                              FLUSH_ATOMIC);
     }
   };
-  struct TileBuf {
-    uint32_t w[PR][U];
-    GhT q[PR];
-    bool valid[PR];
-  };
-  // Issues every load of tile t at once (positions past the job's end re-read its
-  // last row; a job that owns a tile has count >= 1).  Returns the tile's job.
-  auto load = [&](int64_t t, TileBuf& B) -> int32_t {
-    while (jl + 1 < nj && s_jobs[jl + 1].tile0 <= t) ++jl;
-    const PartJob& J = s_jobs[jl];
-    const int64_t count = J.count, begin = J.begin;
-    const int64_t base = (t - J.tile0) * kTile;
-    const uint4* __restrict__ src = rec_buf(L.bufs, J.src_buf);
-    const GhT* __restrict__ sgh = gh_buf<GhT>(L.bufs, J.src_buf);
-    const bool from_rec = EMBED && J.src_buf != BUF_ORIG;
-#pragma unroll
-    for (int k = 0; k < PR; ++k) {
-      const int64_t p = base + (int64_t)k * PT + tid;
-      B.valid[k] = p < count;
-      const int64_t pc = B.valid[k] ? p : count - 1;
-      const int64_t phys = J.rev ? begin + count - 1 - pc : begin + pc;
-      rec_load<FMT>(src, phys, B.w[k]);
-      if constexpr (EMBED) {
-        if (!from_rec) B.q[k] = sgh[phys];
-      } else {
-        B.q[k] = sgh[phys];
-      }
-    }
-    if constexpr (EMBED) {
-      if (from_rec) {
-#pragma unroll
-        for (int k = 0; k < PR; ++k) B.q[k] = (GhT)rec_gh<FMT>(B.w[k]);
-      }
-    }
-    return jl;
-  };
   // Shared-state hand-off per tile: s_cnt is written after the loads and read by
   // wave 0 before barrier B; s_pref / s_lbase / s_rbase / s_total / s_last are
   // written by wave 0 between barriers A and B and read after B; the next tile's
@@ -759,6 +786,12 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
       }
       cur = j;
       held = 0;
+    }
+    if constexpr (EMBED) {
+      if (B.q_in_rec) {
+#pragma unroll
+        for (int k = 0; k < PR; ++k) B.q[k] = (GhT)rec_gh<FMT>(B.w[k]);
+      }
     }
     const PartJob& J = s_jobs[j];
     const int64_t count = J.count, begin = J.begin;
@@ -921,8 +954,6 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   // ranked, histogrammed and scattered (its stores queue behind those loads).  One
   // copy of the per-tile code (the buffers swap by register moves) keeps the kernel
   // small enough to stay in the instruction cache next to the round's other kernels.
-  TileBuf cur_b, next_b;
-  int32_t jc = load(t_lo, cur_b), jn = 0;
   for (int64_t t = t_lo; t < t_hi; ++t) {
     const bool more = t + 1 < t_hi;
     if (more) jn = load(t + 1, next_b);
