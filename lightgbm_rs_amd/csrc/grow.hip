@@ -663,6 +663,11 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
   __shared__ int32_t s_cnt[kSlots];
   __shared__ int32_t s_pref[kSlots];
   __shared__ int32_t s_lbase, s_rbase, s_total, s_last;
+  // packed records: each wave stages its rows of the built side densely (a ring of 128
+  // records + pairs) so that the histogram adds run on full waves
+  constexpr bool STAGE = HIST && EMBED;
+  constexpr int kRing = 128;
+  __shared__ uint32_t s_stage[STAGE ? kWaves * kRing * (U + 1) : 1];
   Ctl* ctl = L.ctl;
   const int tid = threadIdx.x, wave = tid >> 6, lane = (int)lane_id();
   const int32_t nj = ctl->n_jobs;
@@ -854,7 +859,45 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
                                                  ((unsigned long long)(uint32_t)(trows - acc) << 32));
     }
     // histogram adds (every wave, wave 0 while its reservation is in flight)
-    if constexpr (HIST) {
+    if constexpr (STAGE) {
+      if (J.acc_right >= 0) {
+        // LDS atomics cost per instruction more than per active lane: the rows to add
+        // (a fraction of the tile) go through the wave's ring and are added 64 at a
+        // time, then the remainder
+        const bool want_left = J.acc_right == 0;
+        uint32_t* ring = s_stage + (size_t)wave * kRing * (U + 1);
+        int staged = 0, consumed = 0;  // wave-uniform
+        auto add_batch = [&](int n) {
+          __builtin_amdgcn_wave_barrier();
+          if (lane < n) {
+            const uint32_t* e = ring + ((consumed + lane) & (kRing - 1)) * (U + 1);
+            uint32_t rw[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) rw[u] = e[u];
+            lds_hist_add<FMT>(lds_hist, cbr, nw, F, cells + 4 + lane, rw, e[U]);
+          }
+          __builtin_amdgcn_wave_barrier();
+          consumed += n;
+          staged -= n;
+        };
+#pragma unroll
+        for (int k = 0; k < PR; ++k) {
+          const bool act = valid[k] && isleft[k] == want_left && gh_bits(q[k]) != 0u;
+          const unsigned long long am = __ballot(act);
+          if (act) {
+            uint32_t* e = ring + ((consumed + staged + (int)__popcll(am & lanemask_lt())) &
+                                  (kRing - 1)) * (U + 1);
+#pragma unroll
+            for (int u = 0; u < U; ++u) e[u] = w[k][u];
+            e[U] = gh_bits(q[k]);
+          }
+          staged += (int)__popcll(am);
+          if (staged >= LGBM_WAVE) add_batch(LGBM_WAVE);
+        }
+        if (staged > 0) add_batch(staged);
+        ++held;
+      }
+    } else if constexpr (HIST) {
       if (J.acc_right >= 0) {
         const bool want_left = J.acc_right == 0;
 #pragma unroll
