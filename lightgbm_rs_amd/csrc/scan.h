@@ -54,20 +54,35 @@ __device__ __forceinline__ void rec_load(const uint4* __restrict__ base, int64_t
     }
   }
 }
+// The partition's record stores are non-temporal: the next reader is the next round's
+// pass, long after they would have left the L2, and stores that stay dirty in the L2
+// are written back at the end of the kernel, on the round's critical path.
 template <int FMT>
 __device__ __forceinline__ void rec_store(uint4* __restrict__ base, int64_t r,
                                           const uint32_t (&w)[rec_words(FMT)]) {
   constexpr int U = rec_words(FMT);
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   if constexpr (U == 1) {
-    ((uint32_t*)base)[r] = w[0];
+    __builtin_nontemporal_store(w[0], (uint32_t*)base + r);
   } else if constexpr (U % 4 == 0) {
 #pragma unroll
-    for (int i = 0; i < U / 4; ++i)
-      base[r * (U / 4) + i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+    for (int i = 0; i < U / 4; ++i) {
+      u32x4 v;
+      v.x = w[4 * i];
+      v.y = w[4 * i + 1];
+      v.z = w[4 * i + 2];
+      v.w = w[4 * i + 3];
+      __builtin_nontemporal_store(v, (u32x4*)(base + r * (U / 4) + i));
+    }
   } else {
-    uint2* b2 = (uint2*)base;
 #pragma unroll
-    for (int i = 0; i < U / 2; ++i) b2[r * (U / 2) + i] = make_uint2(w[2 * i], w[2 * i + 1]);
+    for (int i = 0; i < U / 2; ++i) {
+      u32x2 v;
+      v.x = w[2 * i];
+      v.y = w[2 * i + 1];
+      __builtin_nontemporal_store(v, (u32x2*)base + r * (U / 2) + i);
+    }
   }
 }
 
