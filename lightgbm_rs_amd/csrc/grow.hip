@@ -151,9 +151,29 @@ __device__ __forceinline__ bool lk_gt(const LKey& a, const LKey& b) {
   return a.hi > b.hi || (a.hi == b.hi && a.lo > b.lo);
 }
 __device__ __forceinline__ LKey lk_max(const LKey& a, const LKey& b) { return lk_gt(a, b) ? a : b; }
-__device__ __forceinline__ LKey lk_shfl_up(const LKey& k, int off) {
-  return LKey{(uint64_t)__shfl_up((unsigned long long)k.hi, off),
-              (uint64_t)__shfl_up((unsigned long long)k.lo, off)};
+// A DPP move of a key (the four dwords alike); lanes outside ROW_MASK / BANK_MASK, or
+// whose source lane is invalid, keep their own key.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ LKey lk_dpp(const LKey& k) {
+  auto mv = [](uint64_t v) {
+    const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+    const uint32_t nlo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, BANK_MASK, false);
+    const uint32_t nhi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, BANK_MASK, false);
+    return ((uint64_t)nhi << 32) | nlo;
+  };
+  return LKey{mv(k.hi), mv(k.lo)};
+}
+// Inclusive prefix maximum of the wave's keys in lane order: row_shr 1, 2, 4, 8 within
+// each 16-lane row, then the row broadcasts 15 and 31 (max is idempotent, so lanes
+// that keep their own key change nothing).
+__device__ __forceinline__ LKey lk_prefix_max(LKey v) {
+  v = lk_max(v, lk_dpp<0x111, 0xf, 0xf>(v));  // row_shr:1
+  v = lk_max(v, lk_dpp<0x112, 0xf, 0xf>(v));  // row_shr:2
+  v = lk_max(v, lk_dpp<0x114, 0xf, 0xf>(v));  // row_shr:4
+  v = lk_max(v, lk_dpp<0x118, 0xf, 0xf>(v));  // row_shr:8
+  v = lk_max(v, lk_dpp<0x142, 0xa, 0xf>(v));  // row_bcast:15 into rows 1, 3
+  v = lk_max(v, lk_dpp<0x143, 0xc, 0xf>(v));  // row_bcast:31 into rows 2, 3
+  return v;
 }
 __device__ __forceinline__ LKey lk_readlane(const LKey& k, int lane) {
   auto rl = [&](uint64_t v) {
@@ -295,19 +315,16 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     const unsigned long long sm = __ballot(in_s);
     int32_t base = 0;
     if (lane == 0 && sm) base = atomicAdd(&s_nS, (int32_t)__popcll(sm));
-    base = __shfl(base, 0);
+    base = __builtin_amdgcn_readfirstlane(base);
     if (in_s) {
       const int32_t pos = base + (int32_t)__popcll(sm & lanemask_lt());
       s_S[pos] = l;
       s_SK[pos] = k;
     }
-    // the best unsplit key's high word: a wave maximum, one LDS atomic per wave
-    unsigned long long u = (live && ch.x < 0) ? k.hi : 0ull;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const unsigned long long o = __shfl_xor(u, off);
-      u = o > u ? o : u;
-    }
+    // the best unsplit key's high word: a wave maximum (the bits of a positive double,
+    // or 0, order like the double), one LDS atomic per wave
+    const unsigned long long u = (unsigned long long)__double_as_longlong(wave_max_f64(
+        __longlong_as_double((long long)((live && ch.x < 0) ? k.hi : 0ull))));
     if (lane == 0 && u != 0ull) atomicMax(&s_uhi, u);
   }
   __syncthreads();
@@ -339,13 +356,8 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
         e = s_key[l];
         M = lk_max(lkey(cg.x, cf.x, l), lkey(cg.y, cf.y, nl0 + i));  // Tree::split ids
       }
-      LKey inc = M;  // inclusive prefix maximum of the children keys
-#pragma unroll
-      for (int off = 1; off < LGBM_WAVE; off <<= 1) {
-        const LKey o = lk_shfl_up(inc, off);
-        if (lane >= off) inc = lk_max(inc, o);
-      }
-      LKey ex = lk_shfl_up(inc, 1);
+      const LKey inc = lk_prefix_max(M);  // inclusive prefix maximum of the children keys
+      LKey ex = lk_dpp<0x138, 0xf, 0xf>(inc);  // wave_shr:1: lane i - 1's
       if (lane == 0) ex = LKey{0ull, 0ull};
       ex = lk_max(ex, P);
       const bool ok = in && i < maxl - nl0 && lk_gt(e, ex);
