@@ -854,14 +854,9 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     if (wave == 0) {
       // exclusive prefix of the (row, wave) counts
       const int32_t c = lane < kSlots ? s_cnt[lane] : 0;
-      int32_t incl = c;
-#pragma unroll
-      for (int off = 1; off < kSlots; off <<= 1) {
-        const int32_t v = __shfl_up(incl, off);
-        if (lane >= off) incl += v;
-      }
+      const int32_t incl = wave_incl_sum_i32(c);
       if (lane < kSlots) s_pref[lane] = incl - c;
-      acc = __shfl(incl, kSlots - 1);
+      acc = readlane_i32(incl, kSlots - 1);
       trows = (int32_t)min((int64_t)kTile, count - base);
       // the reservation is issued here and its result used after this wave's
       // histogram adds, so the atomic's round trip overlaps them
