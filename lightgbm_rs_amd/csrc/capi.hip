@@ -2884,6 +2884,8 @@ int predict_sparse(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t* indp
                            &it1, &width);
   if (rc) return rc;
   if (nnz < 0) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "negative nnz");
+  if (csc && nnz >= (int64_t)UINT32_MAX)  // the densify claims cells with k + 1 in 32 bits
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "csc input of 2^32 - 1 entries or more");
   if (!indptr || (nnz > 0 && (!indices || !values)))
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null indptr/indices/values");
   if (num_rows == 0 || width == 0) return LGBM_HIP_OK;
@@ -2921,8 +2923,8 @@ int predict_sparse(lgbm_hip_ctx* c, const lgbm_hip_model* m, const int64_t* indp
     HIPCHK(c, hipMemcpy(d_idx, indices, ib, hipMemcpyHostToDevice));
     HIPCHK(c, hipMemcpy(d_val, values, ib, hipMemcpyHostToDevice));
   }
+  HIPCHK(c, hipMemsetAsync(c->pm_x, 0, (size_t)num_rows * (size_t)fw * 4, c->stream));
   if (csc) {
-    HIPCHK(c, hipMemsetAsync(c->pm_x, 0, (size_t)num_rows * (size_t)fw * 4, c->stream));
     launch_csc_dense(d_ptr, d_idx, d_val, nnz, num_rows, num_cols, fw, c->pm_x, d_err, c->stream);
   } else {
     launch_csr_dense(d_ptr, d_idx, d_val, nnz, num_rows, num_cols, fw, c->pm_x, d_err, c->stream);

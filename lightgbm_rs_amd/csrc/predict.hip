@@ -439,9 +439,9 @@ void launch_contrib(const PredNode* nodes, const PredTree* trees, const double* 
 
 // ---- sparse rows ------------------------------------------------------------------
 // scatter_csr_row + validate_indptr_pair (predict.rs:772-870): one thread per row
-// zeroes its dense row of `width` (= max_feature_idx + 1) floats and writes its
-// entries in order (a repeated column keeps the last value; columns in [width, cols)
-// are dropped).  A row whose indptr pair leaves [0, nnz] or runs backwards sets bit 0
+// writes its entries in order into its zeroed dense row of `width` (=
+// max_feature_idx + 1) floats (a repeated column keeps the last value; columns in
+// [width, cols) are dropped).  A row whose indptr pair leaves [0, nnz] or runs backwards sets bit 0
 // of *err, a column outside [0, cols) bit 1; the host refuses the call on either.
 __global__ __launch_bounds__(256) void k_csr_dense(const int64_t* __restrict__ indptr,
                                                    const int32_t* __restrict__ indices,
@@ -452,7 +452,6 @@ __global__ __launch_bounds__(256) void k_csr_dense(const int64_t* __restrict__ i
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows) return;
   float* row = dense + r * width;
-  for (int32_t c = 0; c < width; ++c) row[c] = 0.0f;
   const int64_t lo = indptr[r], hi = indptr[r + 1];
   if (lo < 0 || hi < lo || hi > nnz) {
     atomicOr(err, 1u);
@@ -468,39 +467,68 @@ __global__ __launch_bounds__(256) void k_csr_dense(const int64_t* __restrict__ i
   }
 }
 
-// scatter_csc_dense (predict.rs:868-894): one thread per column writes its entries
-// into the zeroed dense rows (a repeated row keeps the last value; columns past
-// `width` are only checked).  Bit 0 of *err: a bad indptr pair; bit 1: a row index
-// outside [0, rows).
-__global__ __launch_bounds__(256) void k_csc_dense(const int64_t* __restrict__ indptr,
-                                                   const int32_t* __restrict__ indices,
-                                                   const float* __restrict__ values, int64_t nnz,
-                                                   int64_t rows, int32_t cols, int32_t width,
-                                                   float* __restrict__ dense,
+// scatter_csc_dense (predict.rs:868-894) over the entries in parallel.  The dense
+// rows are zeroed; a repeated row of a column keeps the column's last value; columns
+// past `width` are only checked.  Bit 0 of *err: a column's indptr pair leaves
+// [0, nnz] or runs backwards; bit 1: a row index outside [0, rows) (the host refuses
+// the call on either, so the dense rows are then never read).
+//   k_csc_check: one thread per column checks its indptr pair;
+//   k_csc_claim: one thread per entry finds its column (the last c with indptr[c] <=
+//     k; entries outside every column's range are skipped), checks its row and takes
+//     its dense cell with a 32-bit atomic maximum of k + 1, so the last entry wins;
+//     the claims live in the dense buffer itself (zeroed first);
+//   k_csc_fill: one thread per cell replaces its claim by the claimed value (0: none).
+__global__ __launch_bounds__(256) void k_csc_check(const int64_t* __restrict__ indptr,
+                                                   int64_t nnz, int32_t cols,
                                                    uint32_t* __restrict__ err) {
   const int32_t c = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x);
   if (c >= cols) return;
   const int64_t lo = indptr[c], hi = indptr[c + 1];
-  if (lo < 0 || hi < lo || hi > nnz) {
-    atomicOr(err, 1u);
+  if (lo < 0 || hi < lo || hi > nnz) atomicOr(err, 1u);
+}
+__global__ __launch_bounds__(256) void k_csc_claim(const int64_t* __restrict__ indptr,
+                                                   const int32_t* __restrict__ indices,
+                                                   int64_t nnz, int64_t rows, int32_t cols,
+                                                   int32_t width, uint32_t* __restrict__ claim,
+                                                   uint32_t* __restrict__ err) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= nnz) return;
+  int32_t lo = 0, hi = cols + 1;  // first position in [0, cols] with indptr > k
+  while (lo < hi) {
+    const int32_t mid = lo + (hi - lo) / 2;
+    if (indptr[mid] > k)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  const int32_t c = lo - 1;
+  if (c < 0 || c >= cols || k < indptr[c] || k >= indptr[c + 1]) return;
+  const int32_t r = indices[k];
+  if (r < 0 || (int64_t)r >= rows) {
+    atomicOr(err, 2u);
     return;
   }
-  for (int64_t k = lo; k < hi; ++k) {
-    const int32_t r = indices[k];
-    if (r < 0 || (int64_t)r >= rows) {
-      atomicOr(err, 2u);
-      return;
-    }
-    if (c < width) dense[(int64_t)r * width + c] = values[k];
-  }
+  if (c < width) atomicMax(&claim[(int64_t)r * width + c], (uint32_t)(k + 1));
+}
+__global__ __launch_bounds__(256) void k_csc_fill(const float* __restrict__ values, int64_t cells,
+                                                  float* dense) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= cells) return;
+  const uint32_t u = ((const uint32_t*)dense)[i];
+  dense[i] = u ? values[u - 1] : 0.0f;
 }
 
 void launch_csc_dense(const int64_t* indptr, const int32_t* indices, const float* values,
                       int64_t nnz, int64_t rows, int32_t cols, int32_t width, float* dense,
                       uint32_t* err, hipStream_t s) {
   if (cols <= 0) return;
-  k_csc_dense<<<dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s>>>(
-      indptr, indices, values, nnz, rows, cols, width, dense, err);
+  k_csc_check<<<dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s>>>(indptr, nnz, cols, err);
+  if (nnz > 0)
+    k_csc_claim<<<dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, s>>>(
+        indptr, indices, nnz, rows, cols, width, (uint32_t*)dense, err);
+  const int64_t cells = rows * (int64_t)width;
+  if (cells > 0)
+    k_csc_fill<<<dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, s>>>(values, cells, dense);
 }
 
 void launch_csr_dense(const int64_t* indptr, const int32_t* indices, const float* values,

@@ -123,3 +123,40 @@ def test_csc_errors(be):
     got = be.predict_csc(m, np.array([0, 2, 3], np.int64), rows, val, 3)
     X = np.array([[1, 0], [1, 0], [0, 1]], np.float32)
     assert np.array_equal(got, be.predict(m, X, "raw"))
+
+
+def test_csc_repeated_rows_keep_the_last_entry(be):
+    """Entries of a column are placed in parallel; a row repeated anywhere in its
+    column (not only next to itself) keeps the column's last value."""
+    print("csc repeated rows", flush=True)
+    m = Model(open(os.path.join(MT, "binary_spine.txt")).read())
+    cptr = np.array([0, 3, 5], np.int64)
+    rows = np.array([2, 0, 2, 1, 1], np.int32)
+    vals = np.array([5, 1, 7, 3, 9], np.float32)
+    got = be.predict_csc(m, cptr, rows, vals, 3)
+    X = np.array([[1, 0], [0, 9], [7, 0]], np.float32)
+    assert np.array_equal(got, be.predict(m, X, "raw"))
+
+
+def test_csc_tall_columns_equal_dense(be):
+    """A tall input of few columns (the shape a per-column pass serialises): random
+    entries with repeated rows, against the dense prediction of the same values."""
+    print("csc tall", flush=True)
+    m = Model(open(os.path.join(MT, "binary_spine.txt")).read())
+    rng = np.random.default_rng(31)
+    n, cols = 300_000, 3
+    cptr = [0]
+    rows_l, vals_l = [], []
+    X = np.zeros((n, 2), np.float32)
+    for c in range(cols):
+        k = int(rng.integers(n // 2, n))
+        r = rng.integers(0, n, size=k).astype(np.int32)  # repeats in any order
+        v = rng.standard_normal(k).astype(np.float32)
+        if c < 2:
+            X[r, c] = v  # numpy keeps the last assignment of a repeated index
+        rows_l.append(r)
+        vals_l.append(v)
+        cptr.append(cptr[-1] + k)
+    got = be.predict_csc(m, np.array(cptr, np.int64), np.concatenate(rows_l),
+                         np.concatenate(vals_l), n)
+    assert np.array_equal(got, be.predict(m, X, "raw"))
