@@ -17,6 +17,12 @@ those bytes over the kernels that perform them.  `cpu_baseline` times the CPU
 restatement of the reference learner (oracle/) on a bounded sample of the same
 workload and bins (all cores and one thread), and `parity` compares the device's
 first iterations with that run's trees and scores, bit for bit.
+
+`--workload config2|config4` instead times BASELINE.json configs[2] (1M x 2000 sparse
+LogNormal features, L2 regression, f32 gradients, feature_fraction 0.8, 127 leaves)
+or configs[4] (2M x 700, lambdarank over query groups, quantized, 255 leaves) on the
+wide row layout, as a secondary line (no roofline or CPU leg); the default
+`config1` is the headline above.
 """
 import argparse
 import json
@@ -124,6 +130,68 @@ def compare_iterations(trees, scores, otrees, oscores, init):
             "leaves": [int(t["num_leaves"]) for t in trees]}
 
 
+def secondary(args):
+    """the wide row layout's paths (column sampling and L2
+    regression with f32 gradients; lambdarank with quantized gradients)."""
+    import numpy as np
+    from lightgbm_rs_amd import GainConfig, HipBackend, boost_from_score
+    from lightgbm_rs_amd.synth import config2_raw_host, config4_raw_host, sample_mappers
+
+    t0 = time.perf_counter()
+    if args.workload == "config2":
+        n, F = 1_000_000, 2000
+        X, y = config2_raw_host(n, F=F)
+        obj, nl, ff, qbins, qb = "regression", 127, 0.8, 0, None
+        workload = ("configs[2]: L2 regression, 1M rows x 2000 sparse LogNormal features, "
+                    "max_bin 255, num_leaves 127, feature_fraction 0.8, f32 gradients")
+        dtype = "f32 grad/hess, 64-bit fixed-point histogram, f64 split math"
+    else:
+        n, F = 2_000_000, 700
+        X, y, groups = config4_raw_host(n, F=F)
+        qb = np.concatenate([[0], np.cumsum(groups)]).astype(np.int32)
+        obj, nl, ff, qbins = "lambdarank", 255, 1.0, 4
+        workload = ("configs[4]: lambdarank, 2M rows x 700 features in query groups, "
+                    "max_bin 255, num_leaves 255, quantized int8 grads (4 bins, stochastic)")
+        dtype = "int8 grad/hess, int32 histogram, f64 split math"
+    mappers = sample_mappers(X, 255)
+    log(f"{args.workload}: data + mappers {time.perf_counter() - t0:.1f}s")
+    init = boost_from_score(obj, y)
+    cfg = GainConfig.make(min_data_in_leaf=20)
+    be = HipBackend(0)
+    be.upload_raw(X, mappers, col_major=True)
+    del X
+    be.set_labels(y, init if abs(init) > 1e-15 else 0.0)
+    if obj == "lambdarank":
+        be.set_lambdarank(qb)
+    else:
+        be.set_objective(obj)
+    if ff < 1.0:
+        be.set_col_sampler(ff, 1.0, 2)
+    for i in range(max(args.warmup, 1)):
+        be.train_iter(i, cfg, nl, -1, 0.1, qbins, True)
+    t1 = time.perf_counter()
+    for i in range(args.warmup, args.warmup + args.steps):
+        be.train_iter(i, cfg, nl, -1, 0.1, qbins, True)
+    elapsed = time.perf_counter() - t1
+    be.set_timing(True)
+    for i in range(args.warmup + args.steps, args.warmup + args.steps + max(args.prof_steps, 1)):
+        be.train_iter(i, cfg, nl, -1, 0.1, qbins, True)
+    tm = be.timing()
+    be.close()
+    ps = max(args.prof_steps, 1)
+    ms = elapsed / args.steps * 1e3
+    print(json.dumps({
+        "metric": f"sec per 100 trees, {args.workload} (wide row layout), 1 MI355X",
+        "value": round(ms / 10.0, 4), "unit": "s/100 trees", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic (BASELINE.json recipe), binned by the library's BinMapper",
+        "config": {"workload": workload, "rows": n, "features": F, "num_leaves": nl},
+        "phase_ms_per_step": {k: round(v / ps, 4) for k, v in tm.items()
+                              if k.endswith("_ms")},
+        "rounds_per_tree": round(tm["rounds"] / max(tm["trees"], 1.0), 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,6 +211,8 @@ def main():
                          "of all is reported beside it")
     ap.add_argument("--prof-steps", type=int, default=3,
                     help="extra iterations timed per kernel with HIP events")
+    ap.add_argument("--workload", default="config1", choices=["config1", "config2", "config4"],
+                    help="config1: the headline; config2 / config4: a secondary wide-layout line")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB device-to-device "
                          "(3 times): the known-size kernel that scales rocprofv3 "
@@ -153,6 +223,8 @@ def main():
               "has no multi-GPU path; see DESIGN.md for how the path would shard.",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload != "config1":
+        return secondary(args)
 
     import numpy as np
     import torch
