@@ -31,7 +31,7 @@
 #define WIDE_GF_F 32
 #define WIDE_THREADS 1024
 #define WIDE_GRID 1024                  // row-chunk blocks over all groups (at least)
-#define WIDE_MIN_ROWS 16384             // rows per chunk (at least): a flush costs a group
+#define WIDE_MIN_ROWS 4096              // rows per chunk (at least): a flush costs a group
 #define WIDE_MAX_ROWS ((1 << 19) - 1)   // packed LDS cell field limit (quantized)
 #define WIDE_MAX_F 4096
 #define WIDE_MAX_BIN 4096               // 2-byte bins (a feature of more than 256 bins)
