@@ -268,10 +268,23 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   for (int i = wave; i < nred; i += PLAN_WAVES) {
     const int32_t s = s_red[i];
     BestKey k{ninf, -1, INT_MAX32};
-    for (int f = lane; f < F; f += LGBM_WAVE) {
-      const double g = (i == wave && f == lane) ? g_w : L.feat_split[(size_t)s * F + f].gain;
-      const BestKey c{g, fts[f].real_index, f};
-      if (g > ninf && key_better(c, k)) k = c;
+    // eight features a lane in flight: with thousands of features one load round
+    // trip per 64 features would set the phase's time
+    constexpr int KU = 8;
+    for (int f0 = lane; f0 < F; f0 += KU * LGBM_WAVE) {
+      double gv[KU];
+      int32_t rv[KU];
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        const int f = f0 + u * LGBM_WAVE;
+        gv[u] = f < F ? ((i == wave && f == lane) ? g_w : L.feat_split[(size_t)s * F + f].gain) : ninf;
+        rv[u] = f < F ? fts[f].real_index : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        const BestKey c{gv[u], rv[u], f0 + u * LGBM_WAVE};
+        if (gv[u] > ninf && key_better(c, k)) k = c;
+      }
     }
     k = wave_best_fast(k);
     const bool have = k.idx != INT_MAX32 && k.gain > ninf;
@@ -1137,6 +1150,19 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
   const int32_t sm = right_small ? cr : cl, lg = right_small ? cl : cr;
   const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
   const bool wide = rec_wide(L.fmt);
+  if (pgate && !gated && (fp_mode || wide)) {
+    // The parent cannot split on this feature (outside the column sample, or no
+    // valid threshold), so neither child scans it and no descendant reads its cells;
+    // these layouts hold no accumulator to clear (their partial slots are rewritten
+    // every round).  The children get what the scan below would give them.
+    if (tid == 0 || tid == LGBM_WAVE) {
+      const int32_t leaf = tid == 0 ? sm : lg;
+      const LeafSums ls = (tid == 0) == right_small ? scr : scl;
+      split_set_none(&L.feat_split[(size_t)leaf * F + f]);
+      if (ls.sh > 0.0 && ls.n > 0) L.splittable[(size_t)leaf * F + f] = 0;
+    }
+    return;
+  }
   if (fp_mode) {
     // f32 gradients: the smaller child from its partial slots (k_hist_f32's, or the
     // wide layout's per-chunk ones); the larger = parent - smaller, exact in 64-bit
@@ -1148,10 +1174,23 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
         const size_t ci = (size_t)(ft.cell_base + b);
         long long SG = 0, SH = 0;
         if (wide) {
-          for (int k = 0; k < na; ++k) {
-            const unsigned long long* wp = L.wide_part + ((size_t)(a0 + k) * cells + ci) * 2;
-            SG += (long long)wp[0];
-            SH += (long long)wp[1];
+          // the job's chunks, four loads in flight at a time (integer sums: any order)
+          const ulonglong2* wp = (const ulonglong2*)L.wide_part + (size_t)a0 * cells + ci;
+          int k = 0;
+          for (; k + 4 <= na; k += 4) {
+            ulonglong2 x[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] = wp[(size_t)(k + u) * cells];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              SG += (long long)x[u].x;
+              SH += (long long)x[u].y;
+            }
+          }
+          for (; k < na; ++k) {
+            const ulonglong2 x = wp[(size_t)k * cells];
+            SG += (long long)x.x;
+            SH += (long long)x.y;
           }
         } else {
           hist_part_sum64(L, a0, na, ci, &SG, &SH);
@@ -1203,12 +1242,30 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
         a[1] = 0;
         a[2] = 0;
       }
-      for (int k = 0; k < wna; ++k) {
-        int32_t g_, h_, t_;
-        unpack_cell(L.wide_part[(size_t)(wa0 + k) * cells + ci], &g_, &h_, &t_);
-        AG += g_;
-        AH += h_;
-        AT += t_;
+      {
+        // the job's chunks (wide layout), four loads in flight at a time
+        const unsigned long long* wp = L.wide_part + (size_t)wa0 * cells + ci;
+        int k = 0;
+        for (; k + 4 <= wna; k += 4) {
+          unsigned long long x[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) x[u] = wp[(size_t)(k + u) * cells];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            int32_t g_, h_, t_;
+            unpack_cell(x[u], &g_, &h_, &t_);
+            AG += g_;
+            AH += h_;
+            AT += t_;
+          }
+        }
+        for (; k < wna; ++k) {
+          int32_t g_, h_, t_;
+          unpack_cell(wp[(size_t)k * cells], &g_, &h_, &t_);
+          AG += g_;
+          AH += h_;
+          AT += t_;
+        }
       }
       if (use_slots) {
         // at most PART_SLOT_MAX blocks, enumerated without a dependent chain so all

@@ -36,21 +36,23 @@ namespace {
 // Rows per chunk R and the first chunk of every job: jobs get ceil(count / R) chunks,
 // R = the launch's rows / `chunks` (at least WIDE_MIN_ROWS); the host sizes `chunks`
 // so that R <= WIDE_MAX_ROWS, and launches chunks + SPEC_MAX blocks per group.
+// Wave 0, lane j = job j (nj <= SPEC_MAX): the counts load in parallel.
 __device__ __forceinline__ void wide_assign(const Ctl* ctl, int32_t nj, int32_t* s_a0,
-                                            int32_t* s_nb, int64_t* s_R, int64_t chunks) {
-  int64_t S = 0;
-  for (int j = 0; j < nj; ++j) S += max(ctl->hjobs[j].count, (int64_t)0);
+                                            int32_t* s_nb, int64_t* s_R, int64_t chunks,
+                                            int lane) {
+  const int64_t c = lane < nj ? max(ctl->hjobs[lane].count, (int64_t)0) : 0;
+  int64_t S = c;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) S += __shfl_xor(S, off);
   int64_t R = (S + chunks - 1) / chunks;
   if (R < WIDE_MIN_ROWS) R = WIDE_MIN_ROWS;
-  int32_t acc = 0;
-  for (int j = 0; j < nj; ++j) {
-    const int64_t c = ctl->hjobs[j].count;
-    const int32_t nb = c > 0 ? (int32_t)((c + R - 1) / R) : 0;
-    s_a0[j] = acc;
-    s_nb[j] = nb;
-    acc += nb;
+  const int32_t nb = c > 0 ? (int32_t)((c + R - 1) / R) : 0;
+  const int32_t incl = wave_incl_sum_i32(nb);
+  if (lane < nj) {
+    s_a0[lane] = incl - nb;
+    s_nb[lane] = nb;
   }
-  *s_R = R;
+  if (lane == 0) *s_R = R;
 }
 
 template <int FP, bool B16>
@@ -73,7 +75,7 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
   const int F = L.F, cells = L.total_cells;
   const int f0 = B16 ? L.wgroups[blockIdx.y] : (int)blockIdx.y * GF;
   if (f0 >= F) return;
-  if (tid == 0) wide_assign(ctl, nj, s_a0, s_nb, &s_R, (int64_t)gridDim.x - SPEC_MAX);
+  if (wave == 0) wide_assign(ctl, nj, s_a0, s_nb, &s_R, (int64_t)gridDim.x - SPEC_MAX, (int)lane_id());
   __syncthreads();
   const int32_t a = (int32_t)blockIdx.x;
   int32_t j = -1;
