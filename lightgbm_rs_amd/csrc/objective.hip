@@ -52,16 +52,17 @@ __global__ __launch_bounds__(LAMBDARANK_THREADS) void k_grad_lambdarank(
   const int tid = threadIdx.x;
   const int32_t st = qb[q], cnt = qb[q + 1] - qb[q];
   if (cnt <= 0) return;
-  // LDS: score, pair term and hessian term (f64) per position; label, sorted
-  // document, lambda, hessian (32-bit) per position
+  // LDS: score and row i's pair j's normalisation term (f64) per position; label,
+  // sorted document, lambda, hessian, row i's pair j's lambda and hessian terms
+  // (32-bit) per position
   double* s_sc = lds;
-  double* s_pl = s_sc + cnt;
-  double* s_ph = s_pl + cnt;
-  float* s_lab = (float*)(s_ph + cnt);
+  double* s_nt = s_sc + cnt;
+  float* s_lab = (float*)(s_nt + cnt);
   int32_t* s_ord = (int32_t*)(s_lab + cnt);
   float* s_lam = (float*)(s_ord + cnt);
   float* s_hes = s_lam + cnt;
-  int8_t* s_dir = (int8_t*)(s_hes + cnt);  // row i's pair j: +1 i high, -1 i low, 0 none
+  float* s_lt = s_hes + cnt;
+  float* s_ht = s_lt + cnt;
   const double kmin = -__builtin_inf();
   for (int i = tid; i < cnt; i += LAMBDARANK_THREADS) {
     s_sc[i] = score[st + i];
@@ -106,9 +107,13 @@ __global__ __launch_bounds__(LAMBDARANK_THREADS) void k_grad_lambdarank(
       const int32_t dj = s_ord[j];
       const double sj = s_sc[dj];
       const float lj = s_lab[dj];
-      int8_t dir = 0;
-      double pl = 0.0, ph = 0.0;
+      // row i's side of the pair as addends: a pair without a term adds -0.0f to
+      // the f32 sums and subtracts +0.0 from the f64 one, which leaves every value
+      // (signed zeros included) as skipping it does; x - y is x + (-y) exactly
+      float lt = -0.0f, ht = -0.0f;
+      double nt = 0.0;
       if (sj != kmin && li != lj) {
+        double pl, ph;
         const bool ihigh = li > lj;
         const int32_t hr = ihigh ? i : j, lr = ihigh ? j : i;
         const int32_t hd = ihigh ? di : dj, ld = ihigh ? dj : di;
@@ -127,27 +132,27 @@ __global__ __launch_bounds__(LAMBDARANK_THREADS) void k_grad_lambdarank(
         else
           s_lam[dj] += (float)pl;
         s_hes[dj] += (float)ph;
-        dir = ihigh ? 1 : -1;
+        lt = ihigh ? (float)pl : -(float)pl;
+        ht = (float)ph;
+        nt = 2.0 * pl;
       }
-      s_pl[j] = pl;
-      s_ph[j] = ph;
-      s_dir[j] = dir;
+      s_lt[j] = lt;
+      s_ht[j] = ht;
+      s_nt[j] = nt;
     }
     __syncthreads();
     if (tid == 0) {
-      // the i side and the normalisation sum, in j order
+      // the i side and the normalisation sum, in j order: three independent chains
+      // over branch-free addends, so the LDS reads run ahead of the adds
       float lam = s_lam[di], hes = s_hes[di];
+      double sl = sum_lambdas;
+#pragma unroll 8
       for (int32_t j = i + 1; j < cnt; ++j) {
-        const int8_t dir = s_dir[j];
-        if (dir == 0) continue;
-        const double pl = s_pl[j];
-        if (dir > 0)
-          lam += (float)pl;
-        else
-          lam -= (float)pl;
-        hes += (float)s_ph[j];
-        sum_lambdas -= 2.0 * pl;
+        lam += s_lt[j];
+        hes += s_ht[j];
+        sl -= s_nt[j];
       }
+      sum_lambdas = sl;
       s_lam[di] = lam;
       s_hes[di] = hes;
     }
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(LAMBDARANK_THREADS) void k_grad_lambdarank(
 }  // namespace
 
 size_t rank_lds_bytes(int32_t max_query) {
-  return (size_t)max_query * (3 * sizeof(double) + 4 * 4 + 1) + 16;
+  return (size_t)max_query * (2 * sizeof(double) + 6 * 4) + 16;
 }
 
 void launch_grad_l2(const double* score, const float* label, float* g, float* h, int64_t n,
