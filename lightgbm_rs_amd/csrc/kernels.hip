@@ -540,16 +540,15 @@ __global__ __launch_bounds__(HIST_THREADS, 2) void k_hist_jobs(DevLearner L) {
         const int32_t qg = (int32_t)(int8_t)(q[u] & 0xffu);
         const int32_t qh = (int32_t)(int8_t)((q[u] >> 8) & 0xffu);
         const uint32_t v = (uint32_t)qg + ((uint32_t)qh << 11) + ((qh == 3 ? 1u : 0u) << 22);
-        // slots past F go to the lane's own trash cell (no conflicts, no branch)
+        // slots past F hold no feature: skipped by a uniform branch
 #pragma unroll
         for (int k = 0; k < (NS + BPW - 1) / BPW; ++k) {
           if (k < nw) {
             const uint32_t word = w[u][k];
 #pragma unroll
             for (int bb = 0; bb < BPW; ++bb)
-              if (BPW * k + bb < NS) {
-                const int ad = BPW * k + bb < F ? cbr[BPW * k + bb] + (int)((word >> (BB * bb)) & BM)
-                                                : cells + 4 + lane;
+              if (BPW * k + bb < NS && BPW * k + bb < F) {
+                const int ad = cbr[BPW * k + bb] + (int)((word >> (BB * bb)) & BM);
                 __hip_atomic_fetch_add(&my[ad], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
               }
           }

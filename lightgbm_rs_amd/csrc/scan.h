@@ -115,9 +115,9 @@ __device__ __forceinline__ void rec_set_gh(uint32_t (&w)[rec_words(FMT)], uint32
 
 // Accumulate one row (quantized pair q in the u16 form) into the packed u64 LDS
 // histogram of all features: every bin slot of the record words 0 .. nw-1; cbr[s] is
-// slot s's first cell.  Slots at or past F (wave-uniform) hold no feature: they go to
-// the lane's own trash cell tl (cells + 4 + lane), so they cost no address conflicts
-// and no branch.  Callers skip a (0, 0) pair: it adds nothing.
+// slot s's first cell.  Slots at or past F hold no feature and are skipped by a
+// uniform branch (an LDS atomic costs far more than the branch).  Callers skip a
+// (0, 0) pair: it adds nothing.
 #define LDS_TRASH_CELLS (4 + LGBM_WAVE)
 template <int FMT>
 __device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int32_t* cbr, int nw,
@@ -125,6 +125,7 @@ __device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int3
                                              uint32_t q) {
   constexpr int BPW = rec_bpw(FMT), BB = rec_bits(FMT), NS = rec_slots(FMT);
   constexpr uint32_t M = (1u << BB) - 1u;
+  (void)tl;  // the trash cell: unused since the slots past F are skipped
   const int32_t qg = (int32_t)(int8_t)(q & 0xffu);
   const int32_t qh = (int32_t)(int8_t)(q >> 8);
   const unsigned long long v = (unsigned long long)(long long)qg +
@@ -136,8 +137,8 @@ __device__ __forceinline__ void lds_hist_add(unsigned long long* lds, const int3
       const uint32_t word = w[k];
 #pragma unroll
       for (int bb = 0; bb < BPW; ++bb)
-        if (BPW * k + bb < NS) {
-          const int a = BPW * k + bb < F ? cbr[BPW * k + bb] + (int)((word >> (BB * bb)) & M) : tl;
+        if (BPW * k + bb < NS && BPW * k + bb < F) {  // F: a uniform branch
+          const int a = cbr[BPW * k + bb] + (int)((word >> (BB * bb)) & M);
           __hip_atomic_fetch_add(&lds[a], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
