@@ -267,8 +267,9 @@ int lgbm_hip_find_best_splits(lgbm_hip_ctx* ctx, const double* hist, int64_t his
  * (hist_len doubles), feats (n_feats lgbm_batched_feature) and out (n_feats
  * lgbm_split_info) are device memory of the context's device; cfg is a host struct.
  * No counterpart in the reference: this is for callers that cannot allocate device
- * memory (code under HIP graph capture, serving loops, harnesses that forbid
- * hipMalloc).  Its working memory is one fixed library-owned device array per GPU
+ * memory (serving loops, harnesses that forbid hipMalloc).  It is not capturable in a
+ * HIP graph: it copies its status word to the host and waits for the context stream.
+ * Its working memory is one fixed library-owned device array per GPU
  * (LGBM_HIP_NOALLOC_MAX_FEATURES feature descriptors), held until the process ends
  * and shared by every context on that GPU: calls that overlap on one GPU race.
  * n_feats above the maximum returns LGBM_HIP_ERR_CAPABILITY before any work; a
@@ -308,6 +309,14 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* ctx, const uint32_t* bins, int64_t n, 
  * `layout` may be NULL (else indices has num_data entries). */
 int lgbm_hip_grow_tree(lgbm_hip_ctx* ctx, const lgbm_gain_config* cfg, int32_t num_leaves,
                        int32_t max_depth, lgbm_tree_out* tree, lgbm_layout_out* layout);
+
+/* Capacity (32-bit words) a tree output's cat_threshold needs for a tree of
+ * num_leaves leaves over the resident bins: (num_leaves - 1) x (largest category
+ * value / 32 + 1) when some feature is categorical, else 0.  No counterpart in the
+ * reference (its Tree grows its Vec); lgbm_hip_grow_tree and the train_iter entries
+ * return LGBM_HIP_ERR_LENGTH_MISMATCH before any work when a non-NULL tree output
+ * holds less. */
+int lgbm_hip_cat_threshold_words(lgbm_hip_ctx* ctx, int32_t num_leaves, int64_t* out);
 
 /* ---- boosting loop on device (binary objective) ----------------------------- */
 

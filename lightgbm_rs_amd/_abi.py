@@ -183,7 +183,9 @@ CAT_WORDS_PER_NODE = 64  # category bitset capacity per categorical node (2048 c
 class TreeBuffers:
     """Host arrays backing one TreeOut (capacity num_leaves)."""
 
-    def __init__(self, num_leaves):
+    def __init__(self, num_leaves, cat_words=None):
+        """cat_words: capacity of cat_threshold in 32-bit words (default
+        CAT_WORDS_PER_NODE per internal node)."""
         self.cap = num_leaves
         self.arrays = {}
         self.out = TreeOut()
@@ -193,7 +195,9 @@ class TreeBuffers:
             self.arrays[name] = a
             setattr(self.out, name, ptr(a, ct))
         self.cat_boundaries = np.zeros(max(num_leaves, 2), dtype=np.int32)
-        self.cat_threshold = np.zeros(max(num_leaves - 1, 1) * CAT_WORDS_PER_NODE, dtype=np.uint32)
+        if cat_words is None:
+            cat_words = max(num_leaves - 1, 1) * CAT_WORDS_PER_NODE
+        self.cat_threshold = np.zeros(max(int(cat_words), 1), dtype=np.uint32)
         self.out.cat_boundaries = ptr(self.cat_boundaries, C.c_int32)
         self.out.cat_threshold = ptr(self.cat_threshold, C.c_uint32)
         self.out.cat_threshold_cap = len(self.cat_threshold)

@@ -56,15 +56,26 @@ class HipBackend:
         self.num_features = 0
         self.slot_len = 0
 
+    def cat_threshold_words(self, num_leaves):
+        """cat_threshold capacity a tree of num_leaves needs over the resident bins
+        (lgbm_hip_cat_threshold_words)."""
+        out = C.c_int64(0)
+        self._check(self.lib.lgbm_hip_cat_threshold_words(self.ctx, C.c_int32(num_leaves),
+                                                          C.byref(out)))
+        return int(out.value)
+
     def _tree_buffers(self, num_leaves, fresh=False):
         """Host arrays for one grown tree, reused across calls (to_dict copies);
-        fresh=True: new arrays (several trees filled by one call)."""
+        fresh=True: new arrays (several trees filled by one call).  The categorical
+        bitset capacity covers the resident bins' widest category set per node."""
+        words = max(self.cat_threshold_words(num_leaves), max(num_leaves - 1, 1) * 64)
         if fresh:
-            return TreeBuffers(num_leaves)
+            return TreeBuffers(num_leaves, words)
         cache = self.__dict__.setdefault("_tb_cache", {})
-        if num_leaves not in cache:
-            cache[num_leaves] = TreeBuffers(num_leaves)
-        return cache[num_leaves]
+        key = (num_leaves, words)
+        if key not in cache:
+            cache[key] = TreeBuffers(num_leaves, words)
+        return cache[key]
 
     def _err(self, ctx):
         buf = C.create_string_buffer(1024)

@@ -163,6 +163,9 @@ struct lgbm_hip_ctx {
   uint64_t slot_len = 0;
   std::vector<DevFeature> feats;
   std::vector<double> ub_host;  // per-bin values (numerical: upper bounds, categorical: categories)
+  // words of one categorical node's bitset at most (largest category value / 32 + 1);
+  // 0 without categorical features
+  int64_t cat_words_node = 0;
   bool have_bins = false, have_grad = false, quant_ready = false, have_labels = false;
   int32_t quant_bins = 0;
   // lookahead (lgbm_hip_set_lookahead): the next iteration's objective + quantizer
@@ -741,6 +744,24 @@ int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_le
   return finish_rounds(c, num_leaves, rounds, fp);
 }
 
+// cat_threshold words a tree of num_leaves leaves may need: every internal node
+// categorical with the widest bitset.
+int64_t cat_words_needed(const lgbm_hip_ctx* c, int32_t num_leaves) {
+  return c->cat_words_node * (int64_t)std::max(num_leaves - 1, 0);
+}
+// Refuses, before any work is enqueued, a tree output whose categorical arrays could
+// not hold the tree (a later refusal would come after the score update).
+int check_cat_capacity(lgbm_hip_ctx* c, const lgbm_tree_out* out, int32_t num_leaves) {
+  if (!out || c->cat_words_node == 0) return LGBM_HIP_OK;
+  const int64_t need = cat_words_needed(c, num_leaves);
+  if (!out->cat_boundaries || !out->cat_threshold || (int64_t)out->cat_threshold_cap < need)
+    return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH,
+                   "categorical features: cat_threshold needs capacity for " + std::to_string(need) +
+                       " words (lgbm_hip_cat_threshold_words), got " +
+                       std::to_string(out->cat_threshold_cap));
+  return LGBM_HIP_OK;
+}
+
 // `copied`: the caller has enqueued the blob copy and waited for it (the stream may
 // still be busy with later work).
 int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, double shrink,
@@ -971,6 +992,17 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   HIPCHK(c, hipMemcpy(c->d_feats, feats.data(), F * sizeof(DevFeature), hipMemcpyHostToDevice));
   c->ub_host.assign(bin_upper_bound ? bin_upper_bound : nullptr,
                     bin_upper_bound ? bin_upper_bound + uacc : nullptr);
+  // the widest bitset finish_tree can write for one categorical node (its category
+  // values converted as there)
+  c->cat_words_node = 0;
+  for (const DevFeature& d : c->feats) {
+    if (!d.categorical) continue;
+    for (uint32_t b = 0; b < d.num_bin; ++b) {
+      const size_t k = d.ub_off + (size_t)b;
+      const double v = k < c->ub_host.size() ? c->ub_host[k] : (double)b;
+      c->cat_words_node = std::max<int64_t>(c->cat_words_node, (int64_t)((uint32_t)(int32_t)v / 32) + 1);
+    }
+  }
   if (bin_upper_bound) {
     if ((rc = dalloc(c, &c->d_ub, (size_t)uacc))) return rc;
     HIPCHK(c, hipMemcpy(c->d_ub, bin_upper_bound, uacc * 8, hipMemcpyHostToDevice));
@@ -1643,6 +1675,9 @@ int lgbm_hip_set_gradients(lgbm_hip_ctx* c, const float* grad, const float* hess
   if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
   if (!grad || !hess) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null gradients");
   if (n != c->N) return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "gradient length != num_data");
+  // the context stream does not wait on the null stream's copies: a lookahead left
+  // queued by train_iter (the next objective and quantizer) writes these buffers
+  HIPCHK(c, hipStreamSynchronize(c->stream));
   HIPCHK(c, hipMemcpy(c->g, grad, (size_t)n * 4, hipMemcpyHostToDevice));
   HIPCHK(c, hipMemcpy(c->h, hess, (size_t)n * 4, hipMemcpyHostToDevice));
   c->have_grad = true;
@@ -1712,6 +1747,8 @@ int lgbm_hip_set_dequantized_gradients(lgbm_hip_ctx* c, const float* grad, const
                      "no scales given and no lgbm_hip_quantize with these bins to take them from");
   }
   c->quant_ready = false;
+  // as in lgbm_hip_set_gradients: a queued lookahead writes g, h and the scales
+  HIPCHK(c, hipStreamSynchronize(c->stream));
   HIPCHK(c, hipMemcpy(c->g, grad, (size_t)n * 4, hipMemcpyHostToDevice));
   HIPCHK(c, hipMemcpy(c->h, hess, (size_t)n * 4, hipMemcpyHostToDevice));
   c->have_grad = true;
@@ -2088,6 +2125,7 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num
   if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
+  if ((rc = check_cat_capacity(c, tree, num_leaves))) return rc;
   if (fp) {
     if ((rc = ensure_fp(c))) return rc;
     if ((rc = ensure_leaves(c, num_leaves))) return rc;
@@ -2096,6 +2134,15 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num
   }
   if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
   return finish_tree(c, tree, layout, 1.0);
+}
+
+int lgbm_hip_cat_threshold_words(lgbm_hip_ctx* c, int32_t num_leaves, int64_t* out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
+  *out = cat_words_needed(c, num_leaves);
+  return LGBM_HIP_OK;
 }
 
 int lgbm_hip_set_labels(lgbm_hip_ctx* c, const float* labels, int64_t n, double init_score) {
@@ -2143,6 +2190,7 @@ int train_iter_single(lgbm_hip_ctx* c, int32_t objective, int32_t iter, const lg
   if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
+  if ((rc = check_cat_capacity(c, tree, num_leaves))) return rc;
   if (fp) {
     if ((rc = ensure_fp(c))) return rc;
     if ((rc = ensure_leaves(c, num_leaves))) return rc;
@@ -2176,11 +2224,24 @@ int train_iter_single(lgbm_hip_ctx* c, int32_t objective, int32_t iter, const lg
   return finish_tree(c, tree, nullptr, learning_rate);
 }
 
-// DCGCalculator::cal_max_dcg_at_k (lgbm-metric/src/dcg_calculator.rs:142-165)
+// Rust's saturating float -> integer casts (`l as i32`, `l as usize`): truncation
+// toward zero, NaN -> 0, values past the type's range clamped.  A NaN ranking label
+// passes DCGCalculator::check_labels (dcg_calculator.rs:112-137, every comparison with
+// NaN is false) and then indexes the label gains as 0.
+int32_t rust_as_i32(float l) {
+  if (!(l == l)) return 0;
+  if (l <= -2147483648.0f) return INT32_MIN;
+  if (l >= 2147483648.0f) return INT32_MAX;
+  return (int32_t)l;
+}
+size_t rust_as_usize(float l) { return l == l && l > 0.0f ? (size_t)rust_as_i32(l) : 0; }
+
+// DCGCalculator::cal_max_dcg_at_k (lgbm-metric/src/dcg_calculator.rs:142-165); labels
+// already checked to be NaN or integers in [0, gain.size())
 double max_dcg_at_k(const std::vector<double>& gain, const std::vector<double>& disc, int32_t k,
                     const float* labels, int32_t cnt) {
   std::vector<int64_t> n_of((size_t)gain.size(), 0);
-  for (int32_t i = 0; i < cnt; ++i) n_of[(size_t)labels[i]] += 1;
+  for (int32_t i = 0; i < cnt; ++i) n_of[rust_as_usize(labels[i])] += 1;
   int64_t top = (int64_t)gain.size() - 1;
   double sum = 0.0;
   for (int32_t j = 0; j < std::min(k, cnt); ++j) {
@@ -2248,6 +2309,8 @@ int lgbm_hip_set_lambdarank(lgbm_hip_ctx* c, const int32_t* query_boundaries, in
   if (max_q > RANK_MAX_QUERY)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "a query holds more than " + std::to_string(RANK_MAX_QUERY) + " rows");
+  if (lambdarank_prepare(std::max(max_q, 1)))
+    return set_err(c, LGBM_HIP_ERR_HIP, "the lambdarank kernel's LDS size was refused");
   std::vector<float> lab((size_t)c->N);
   HIPCHK(c, hipMemcpy(lab.data(), c->label, lab.size() * 4, hipMemcpyDeviceToHost));
   // DefaultLabelGain and the discounts (dcg_calculator.rs:48-90); labels checked as
@@ -2257,9 +2320,9 @@ int lgbm_hip_set_lambdarank(lgbm_hip_ctx* c, const int32_t* query_boundaries, in
   for (int i = 0; i < RANK_DISCOUNTS; ++i) disc[(size_t)i] = 1.0 / std::log2(2.0 + (double)i);
   for (int64_t i = 0; i < c->N; ++i) {
     const float l = lab[(size_t)i];
-    if (std::fabs(l - (float)(int32_t)l) > 1e-15f)
+    if (std::fabs(l - (float)rust_as_i32(l)) > 1e-15f)
       return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "ranking labels must be integers");
-    if (l < 0.0f || l >= 31.0f)
+    if (l < 0.0f || rust_as_usize(l) >= gain.size())
       return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "ranking label outside the label gains");
   }
   std::vector<double> imd((size_t)num_queries);
@@ -2404,6 +2467,11 @@ int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gai
   if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
+  if (trees)
+    for (int32_t k = 0; k < c->num_class; ++k)
+      if (!(class_need_train && !class_need_train[k]) &&
+          (rc = check_cat_capacity(c, &trees[k], num_leaves)))
+        return rc;
   if ((rc = ensure_leaves(c, num_leaves))) return rc;
   if (fp && (rc = ensure_fp(c))) return rc;
   const int32_t K = c->num_class;

@@ -213,6 +213,8 @@ void launch_grad_l2(const double* score, const float* label, float* g, float* h,
                     hipStream_t s);
 void launch_grad_lambdarank(const double* score, const float* label, const RankTables& t,
                             float* g, float* h, hipStream_t s);
+// Opts the lambdarank kernel into the LDS of a query of max_query rows; 0 = ok.
+int lambdarank_prepare(int32_t max_query);
 void launch_grad_softmax(const double* score, const float* label, float* g, float* h, int64_t n,
                          int32_t K, double factor, hipStream_t s);
 void launch_quant_scales(Ctl* ctl, const uint4* partials, int64_t n, int32_t bins,

@@ -118,7 +118,10 @@ __global__ __launch_bounds__(LAMBDARANK_THREADS) void k_grad_lambdarank(
         const int32_t hr = ihigh ? i : j, lr = ihigh ? j : i;
         const int32_t hd = ihigh ? di : dj, ld = ihigh ? dj : di;
         const double delta = s_sc[hd] - s_sc[ld];
-        const double gap = gain[(int32_t)s_lab[hd]] - gain[(int32_t)s_lab[ld]];
+        // a NaN label indexes gain 0 (Rust's saturating `as usize`); the host checked
+        // every other label to be an integer in [0, 31)
+        const float lh = s_lab[hd], ll = s_lab[ld];
+        const double gap = gain[lh == lh ? (int32_t)lh : 0] - gain[ll == ll ? (int32_t)ll : 0];
         const double paired = fabs(discount[hr] - discount[lr]);
         double dpn = gap * paired * imd;
         if (scale) dpn /= (double)0.01f + fabs(delta);
@@ -177,6 +180,16 @@ __global__ __launch_bounds__(LAMBDARANK_THREADS) void k_grad_lambdarank(
 
 size_t rank_lds_bytes(int32_t max_query) {
   return (size_t)max_query * (2 * sizeof(double) + 6 * 4) + 16;
+}
+
+// Opts the lambdarank kernel into the LDS of its longest query (above 64 KiB from
+// 1639 rows on); outside any graph capture.  0 = ok.
+int lambdarank_prepare(int32_t max_query) {
+  return hipFuncSetAttribute((const void*)k_grad_lambdarank,
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)rank_lds_bytes(max_query)) == hipSuccess
+             ? 0
+             : 1;
 }
 
 void launch_grad_l2(const double* score, const float* label, float* g, float* h, int64_t n,

@@ -1506,9 +1506,9 @@ struct Lambdarank {
     for (int i = 1; i < 31; ++i) gain.push_back((double)((1ll << i) - 1));
     for (int64_t i = 0; i < n; ++i) {  // DCGCalculator::check_labels order
       const float l = labels[i];
-      if (std::fabs(l - (float)(int32_t)l) > (float)1e-15f)
+      if (std::fabs(l - (float)as_i32(l)) > (float)1e-15f)
         return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "ranking labels must be integers");
-      if (l < 0.0f || (size_t)l >= gain.size())
+      if (l < 0.0f || as_usize(l) >= gain.size())
         return fail(LGBM_HIP_ERR_INVALID_ARGUMENT, "ranking label out of the label gain table");
     }
     discount.resize(kMaxPosition);
@@ -1530,9 +1530,20 @@ struct Lambdarank {
     }
     return LGBM_HIP_OK;
   }
+  // Rust's saturating `l as i32` / `l as usize` (dcg_calculator.rs:118,128; rank.rs:329,
+  // 334): NaN -> 0, truncation toward zero, clamped to the type's range.  A NaN label
+  // passes check_labels (its comparisons are all false) and indexes gain 0, while the
+  // pair loop still compares the f32 labels themselves.
+  static int32_t as_i32(float l) {
+    if (!(l == l)) return 0;
+    if (l <= -2147483648.0f) return INT32_MIN;
+    if (l >= 2147483648.0f) return INT32_MAX;
+    return (int32_t)l;
+  }
+  static size_t as_usize(float l) { return l == l && l > 0.0f ? (size_t)as_i32(l) : 0; }
   double cal_max_dcg_at_k(int32_t k, const float* labels, int32_t cnt) const {
     std::vector<int64_t> lc(gain.size(), 0);
-    for (int32_t i = 0; i < cnt; ++i) lc[(size_t)labels[i]] += 1;
+    for (int32_t i = 0; i < cnt; ++i) lc[as_usize(labels[i])] += 1;
     int64_t top = (int64_t)gain.size() - 1;
     double ret = 0.0;
     const int32_t kk = std::min(k, cnt);
@@ -1583,7 +1594,7 @@ struct Lambdarank {
           const int32_t hr = ihigh ? i : j, lr = ihigh ? j : i;
           const int32_t hi = si[hr], lo = si[lr];
           const double delta_score = s[hi] - s[lo];
-          const double dcg_gap = gain[(size_t)ql[hi]] - gain[(size_t)ql[lo]];
+          const double dcg_gap = gain[as_usize(ql[hi])] - gain[as_usize(ql[lo])];
           const double paired = std::fabs(discount[hr] - discount[lr]);
           double dpn = dcg_gap * paired * imd;
           if (norm && best != worst) dpn /= (double)0.01f + std::fabs(delta_score);

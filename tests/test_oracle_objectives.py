@@ -186,6 +186,37 @@ def test_lambdarank_gradients_at_distinct_scores():
         np.testing.assert_allclose(g[a:b], lam, rtol=1e-4, atol=1e-5)
 
 
+def test_lambdarank_nan_label_follows_rust_casts():
+    """A NaN relevance label passes check_labels (dcg_calculator.rs:112-137: NaN - 0 is
+    NaN, and `NaN > eps`, `NaN < 0` are false), indexes the label gains as 0 (Rust's
+    saturating `as usize`), and in the pair loop (rank.rs:317-336) compares neither
+    equal to nor greater than the other label, so the later-ranked document of the
+    pair is taken as the high one.  Two documents, scores (1, 0), labels (2, NaN):
+    high = doc 1 (gain 0), low = doc 0 (gain 3), so dcg_gap = -3 and the pair's
+    hessian term is negative (a NaN read as label 0 would give a positive one)."""
+    s = np.array([1.0, 0.0])
+    y = np.array([2.0, np.nan], np.float32)
+    qb = np.array([0, 2], np.int32)
+    g, h = oracle.lambdarank_gradients(s, y, qb, 1.0, True, 30)
+    # max DCG of labels (2, 0) at k = 2: gain 3 at discount 1; pair at ranks (1, 0)
+    paired = abs(1.0 / np.log2(3.0) - 1.0)
+    dpn = (-3.0 * paired * (1.0 / 3.0)) / (float(np.float32(0.01)) + 1.0)
+    # the sigmoid table entry of delta = s[1] - s[0] = -1 (2^20 bins over [-25, 25])
+    f = 2.0 ** 20 / 50.0
+    sc = int((-1.0 + 25.0) * f) / f - 25.0
+    p = 1.0 / (1.0 + np.exp(sc))
+    pl = p * -(1.0 * dpn)
+    ph = p * (1.0 - p) * dpn
+    assert g[0] == np.float32(-np.float32(pl)) and g[1] == np.float32(pl), (g, pl)
+    assert h[0] == np.float32(ph) and h[1] == np.float32(ph) and h[0] < 0, (h, ph)
+    # NaN labels in a larger query: every label's f32 comparisons stay the reference's
+    rng = np.random.default_rng(1)
+    y2 = rng.integers(0, 5, 50).astype(np.float32)
+    y2[[3, 17, 18]] = np.nan
+    g2, h2 = oracle.lambdarank_gradients(rng.normal(size=50), y2, np.array([0, 50], np.int32))
+    assert np.all(np.isfinite(g2)) and np.all(np.isfinite(h2))
+
+
 def test_lambdarank_model_matches_real_binary():
     d = _rank()
     X = np.array(d["X"], dtype=np.float64)
