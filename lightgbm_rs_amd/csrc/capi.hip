@@ -831,6 +831,8 @@ int finish_tree(lgbm_hip_ctx* c, lgbm_tree_out* out, lgbm_layout_out* layout, do
         const double v = fpos >= 0 && ft.ub_off + (size_t)b < c->ub_host.size()
                              ? c->ub_host[ft.ub_off + (size_t)b]
                              : (double)b;
+        if (!(v >= 0.0 && v < 2147483648.0))  // the NaN dummy bin never wins a set
+          return set_err(c, LGBM_HIP_ERR_RUNTIME, "a categorical split sent a negative category left");
         const uint32_t cat = (uint32_t)(int32_t)v;
         if (bits.size() <= cat / 32) bits.resize(cat / 32 + 1, 0u);
         bits[cat / 32] |= 1u << (cat % 32);
@@ -993,13 +995,15 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   c->ub_host.assign(bin_upper_bound ? bin_upper_bound : nullptr,
                     bin_upper_bound ? bin_upper_bound + uacc : nullptr);
   // the widest bitset finish_tree can write for one categorical node (its category
-  // values converted as there)
+  // values converted as there); a bin of negative category (the NaN dummy bin 0) is
+  // never in a winning set (learner.rs:4120-4124)
   c->cat_words_node = 0;
   for (const DevFeature& d : c->feats) {
     if (!d.categorical) continue;
     for (uint32_t b = 0; b < d.num_bin; ++b) {
       const size_t k = d.ub_off + (size_t)b;
       const double v = k < c->ub_host.size() ? c->ub_host[k] : (double)b;
+      if (!(v >= 0.0 && v < 2147483648.0)) continue;
       c->cat_words_node = std::max<int64_t>(c->cat_words_node, (int64_t)((uint32_t)(int32_t)v / 32) + 1);
     }
   }
