@@ -13,6 +13,28 @@ import numpy as np
 from lightgbm_rs_amd._abi import (BatchedFeature, FeatureMeta, GainConfig, LayoutBuffers,
                                   SplitInfo, TreeBuffers, ptr)
 
+def _cat_words(meta, upper, num_leaves):
+    """cat_threshold capacity for a tree: (num_leaves - 1) x the widest category
+    bitset of one node (largest non-negative category value / 32 + 1), at least the
+    default 64 words a node."""
+    per = 64
+    if upper is not None:
+        off = 0
+        for m in meta:
+            nb = int(m.num_bin)
+            if int(m.bin_type) != 0:
+                v = np.asarray(upper[off:off + nb], np.float64)
+                v = v[(v >= 0) & (v < 2.0 ** 31)]
+                if len(v):
+                    per = max(per, int(v.max()) // 32 + 1)
+            off += nb
+    return max(num_leaves - 1, 1) * per
+
+
+def _tree_buffers(num_leaves, meta, upper):
+    return TreeBuffers(num_leaves, _cat_words(meta, upper, num_leaves))
+
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liblgbm_oracle.so")
 
@@ -184,7 +206,7 @@ def train_tree(bins_fm, meta, upper, grad, hess, cfg, num_leaves, max_depth=-1,
     ub = None if upper is None else np.ascontiguousarray(upper, dtype=np.float64)
     g = np.ascontiguousarray(grad, dtype=np.float32)
     h = np.ascontiguousarray(hess, dtype=np.float32)
-    tb = TreeBuffers(num_leaves)
+    tb = _tree_buffers(num_leaves, meta, upper)
     lb = LayoutBuffers(N, num_leaves)
     _check(lib().oracle_train_tree(b.ctypes.data_as(C.c_void_p), C.c_int32(width), C.c_int32(F),
                                    C.c_int64(N), marr, ptr(ub, C.c_double), ptr(g, C.c_float),
@@ -223,7 +245,7 @@ def train_binary(bins_fm, meta, upper, label, cfg, num_leaves, max_depth, iters,
     ub = None if upper is None else np.ascontiguousarray(upper, dtype=np.float64)
     lab = np.ascontiguousarray(label, dtype=np.float32)
     scores = np.zeros(N, dtype=np.float64)
-    trees = [TreeBuffers(num_leaves) for _ in range(iters)] if want_trees else []
+    trees = [_tree_buffers(num_leaves, meta, upper) for _ in range(iters)] if want_trees else []
     tarr = (type(trees[0].out) * iters)(*[t.out for t in trees]) if want_trees else None
     nt = C.c_int32(0)
     _check(lib().oracle_train_binary(
@@ -267,7 +289,7 @@ def train_multiclass(bins_fm, meta, upper, label, num_class, cfg, num_leaves, ma
     lab = np.ascontiguousarray(label, dtype=np.float32)
     scores = np.zeros(N * num_class, dtype=np.float64)
     cap = iters * num_class
-    trees = [TreeBuffers(num_leaves) for _ in range(cap)] if want_trees else []
+    trees = [_tree_buffers(num_leaves, meta, upper) for _ in range(cap)] if want_trees else []
     tarr = (type(trees[0].out) * cap)(*[t.out for t in trees]) if want_trees else None
     nt = C.c_int32(0)
     _check(lib().oracle_train_multiclass(
@@ -322,7 +344,7 @@ def train(bins_fm, meta, upper, label, cfg, objective, num_leaves, max_depth, it
     p.num_queries = 0 if qb is None else len(qb) - 1
     p.query_boundaries = ptr(qb, C.c_int32) if qb is not None else None
     scores = np.zeros(N, dtype=np.float64)
-    trees = [TreeBuffers(num_leaves) for _ in range(iters)] if want_trees else []
+    trees = [_tree_buffers(num_leaves, meta, upper) for _ in range(iters)] if want_trees else []
     tarr = (type(trees[0].out) * iters)(*[t.out for t in trees]) if want_trees else None
     nt = C.c_int32(0)
     _check(lib().oracle_train(b.ctypes.data_as(C.c_void_p), C.c_int32(width), C.c_int32(F),

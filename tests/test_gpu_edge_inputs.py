@@ -26,7 +26,7 @@ def say(*a):
     print(*a, flush=True)
 
 
-def _rank_grads_at_trained_scores(bins, meta, ub, rel, qb, iters=2):
+def _rank_grads_at_trained_scores(bins, meta, ub, rel, qb, iters=2, qbins=4):
     b = HipBackend(0)
     try:
         b.upload_resident_bins(bins, meta, ub)
@@ -34,9 +34,9 @@ def _rank_grads_at_trained_scores(bins, meta, ub, rel, qb, iters=2):
         b.set_lambdarank(qb)
         cfg = GainConfig.make(min_data_in_leaf=20)
         for i in range(iters):
-            b.train_iter(i, cfg, 31, -1, 0.1, 4, True)
+            b.train_iter(i, cfg, 31, -1, 0.1, qbins, True)
         s = b.scores()
-        b.train_iter(iters, cfg, 31, -1, 0.1, 4, True)  # evaluates the gradients at s
+        b.train_iter(iters, cfg, 31, -1, 0.1, qbins, True)  # evaluates the gradients at s
         g, h = b.gradients()
     finally:
         b.close()
@@ -56,11 +56,14 @@ def test_lambdarank_nan_labels_match_oracle():
     rel[qb[5]:qb[6]] = np.nan
     rel[qb[5]] = 3.0
     say(f"lambdarank NaN labels n={n} nan={int(np.isnan(rel).sum())}")
-    s, g, h = _rank_grads_at_trained_scores(bins, meta, ub, rel, qb)
+    # a NaN-labelled pair can carry a negative hessian term (the quantized learner
+    # refuses those): the trees grow from f32 gradients
+    s, g, h = _rank_grads_at_trained_scores(bins, meta, ub, rel, qb, qbins=0)
     og, oh = oracle.lambdarank_gradients(s, rel, qb)
     assert np.array_equal(g.view(np.uint32), og.view(np.uint32))
     assert np.array_equal(h.view(np.uint32), oh.view(np.uint32))
     assert np.any(g[nan_rows] != 0.0), "NaN-labelled documents take part in pairs"
+    assert np.any(h < 0.0), "the reference's NaN pairs give negative hessian terms"
 
 
 @pytest.mark.parametrize("qlen", [1639, 2048])
