@@ -192,6 +192,45 @@ def secondary(args):
         "rounds_per_tree": round(tm["rounds"] / max(tm["trees"], 1.0), 1)}), flush=True)
 
 
+def lds_probe(args):
+    """LDS-atomic ceiling of the quantized histogram adds (lgbm_hip_probe_lds_atomics):
+    one packed-cell add per (row, feature) into 28 x 64 LDS cells, with nothing else in
+    the loop, on configs[1]-shaped bins; prints one JSON line of lane adds per CU-cycle
+    per mode and the root build's LDS-only floor at that rate."""
+    import ctypes as C
+    import numpy as np
+    from lightgbm_rs_amd import load_library
+    from lightgbm_rs_amd.synth import config1_like
+
+    lib = load_library()
+    n = 262_144  # one row per thread of the probe's 2 x 256 blocks x 512 threads
+    bins, _, _, _ = config1_like(n)
+    bins = np.ascontiguousarray(bins, np.uint8)
+    F = bins.shape[0]
+    modes = {"u32 distinct": 0, "u32 config1 bins": 1, "u32 one address": 2,
+             "u64 distinct": 4, "u64 config1 bins": 5, "u64 one address": 6,
+             "u32 wave-private distinct": 8, "u32 wave-private config1 bins": 9}
+    rows = {}
+    for name, mode in modes.items():
+        out = (C.c_double * 5)()
+        rc = lib.lgbm_hip_probe_lds_atomics(C.c_int(0), bins.ctypes.data_as(C.c_void_p),
+                                            C.c_int64(n), C.c_int32(F), C.c_int32(mode),
+                                            C.c_int32(args.probe_reps), out)
+        if rc != 0:
+            sys.exit(f"lds probe mode {mode}: status {rc}")
+        rows[name] = {"ms": round(out[0], 4), "lane_adds": int(out[1]),
+                      "lane_adds_per_cu_cycle": round(out[2], 3)}
+        clock_mhz, cus = out[3], int(out[4])
+        log(f"lds probe {name}: {out[2]:.3f} lane adds / CU-cycle ({out[0]:.3f} ms)")
+    root_adds = 10_500_000 * 28
+    floor = {k: round(root_adds / (v["lane_adds_per_cu_cycle"] * cus * clock_mhz * 1e6) * 1e6, 1)
+             for k, v in rows.items()}
+    print(json.dumps({"probe": "lds atomics", "rows_per_launch": n, "features": F,
+                      "reps": args.probe_reps, "clock_mhz": clock_mhz, "cus": cus,
+                      "modes": rows,
+                      "root_build_lds_floor_us (10.5M rows x 28 adds)": floor}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -217,7 +256,12 @@ def main():
                     help="after the run, copy a buffer of this many MiB device-to-device "
                          "(3 times): the known-size kernel that scales rocprofv3 "
                          "FETCH_SIZE/WRITE_SIZE readings to bytes")
+    ap.add_argument("--lds-probe", action="store_true",
+                    help="measure the LDS-atomic ceiling of the histogram adds instead")
+    ap.add_argument("--probe-reps", type=int, default=64)
     args = ap.parse_args()
+    if args.lds_probe:
+        return lds_probe(args)
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (--gpus {args.gpus} requested): this build "
               "has no multi-GPU path; see DESIGN.md for how the path would shard.",

@@ -654,6 +654,21 @@ int lgbm_hip_predict_early_stop(lgbm_hip_ctx* ctx, const lgbm_hip_model* model, 
                                 int32_t num_iteration, int32_t freq, double margin, double* out,
                                 int32_t* iterations);
 
+/* ---- measurement ------------------------------------------------------------ */
+
+/* LDS-atomic throughput probe (no counterpart in the reference: the ceiling that
+ * ConstructHistogram's packed-cell adds run against).  2 x CUs blocks of 512 threads;
+ * each thread holds one row's num_features (<= 32) bins and adds `reps` times one cell
+ * per feature to an LDS histogram of num_features x 64 cells.  mode bits 0-1: the
+ * bin of each add (0: the lane's index, 64 distinct cells; 1: the row's bin from
+ * bins, host u8 feature-major [num_features][n]; 2: bin 0 for every lane), bit
+ * 2: u64 cells (else u32), bit 3: one histogram per wave (u32 only; else one per
+ * block).  out[5]: ms of the timed launch, lane adds, lane adds per CU-cycle at the
+ * device's reported peak clock, that clock in MHz, CUs.  Allocates its own stream,
+ * events and an 8-byte sink. */
+int lgbm_hip_probe_lds_atomics(int device, const uint8_t* bins, int64_t n,
+                               int32_t num_features, int32_t mode, int32_t reps, double* out);
+
 #ifdef __cplusplus
 }
 #endif
