@@ -364,6 +364,23 @@ def test_xorshift_transition_has_full_period():
     assert np.array_equal(u, (st >> np.uint64(11)).astype(np.float64) / 2.0 ** 53)
 
 
+def test_xorshift_matches_the_published_13_7_17_stream():
+    """Known answer for the shift triple itself: Marsaglia's xor64 generator
+    ("Xorshift RNGs", J. Stat. Softw. 8(14), 2003: x ^= x << 13; x ^= x >> 7;
+    x ^= x << 17) from its example seed 88172645463325252 emits 8748534153485358512,
+    3040900993826735515, 3453997556048239312.  The full-period check above cannot tell
+    (13, 7, 17) from its mirror (17, 7, 13), which is also full period; this does."""
+    st = oracle.xorshift_states(88172645463325252, 3)
+    assert [int(v) for v in st] == [8748534153485358512, 3040900993826735515,
+                                     3453997556048239312]
+    mirror = 88172645463325252
+    m = (1 << 64) - 1
+    mirror ^= (mirror << 17) & m
+    mirror ^= mirror >> 7
+    mirror ^= (mirror << 13) & m
+    assert mirror != int(st[0])
+
+
 def test_xorshift_period_check_has_teeth():
     """The same period check rejects a transition with one shift direction flipped."""
     def step(x):
