@@ -211,4 +211,4 @@ def test_config3_workload_matches_oracle(be):
 
 
 def test_config3_full_size_matches_oracle(be):
-    _config3_case(be, 2_000_000, 1, 0x5EED0003)
+    _config3_case(be, 2_000_000, 2, 0x5EED0003)

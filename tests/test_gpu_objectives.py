@@ -62,6 +62,12 @@ def compare(trees, scores, otrees, oscores, init, tag, exact):
                 assert np.array_equal(bits(a), bits(b)), (tag, i, k)
             else:
                 np.testing.assert_allclose(a, b, rtol=1e-9, atol=1e-300, err_msg=f"{tag} {i} {k}")
+        if exact:  # every other field of the tree too
+            for k in o:
+                if k in STRUCT or k in VALUES or k == "num_leaves":
+                    continue
+                a, b = np.ascontiguousarray(t[k]), np.ascontiguousarray(o[k])
+                assert a.shape == b.shape and a.tobytes() == b.tobytes(), (tag, i, k)
     if exact:
         assert np.array_equal(bits(scores), bits(oscores)), tag
     else:
@@ -240,9 +246,10 @@ def test_feature_fraction_real_binary_on_device(cell):
 
 
 # --- configs[2] and configs[4] at their full sizes ------------------------------------
-def _full_chain(X, ms, y, objective, nl, qbins, feature_fraction=1.0, qb=None):
+def _full_chain(X, ms, y, objective, nl, qbins, feature_fraction=1.0, qb=None, iters=1):
     """The library's own chain: device binning of the raw table (lgbm_hip_upload_raw,
-    wide layout) -> one resident boosting iteration; returns the device's bins too."""
+    wide layout) -> `iters` resident boosting iterations; returns the device's bins
+    too."""
     init = boost_from_score(objective, y)
     cfg = GainConfig.make(min_data_in_leaf=20)
     b = HipBackend(0)
@@ -256,7 +263,7 @@ def _full_chain(X, ms, y, objective, nl, qbins, feature_fraction=1.0, qb=None):
             b.set_objective(objective)
         if feature_fraction < 1.0:
             b.set_col_sampler(feature_fraction, 1.0, 2)
-        trees = [b.train_iter(0, cfg, nl, -1, 0.1, qbins, True)]
+        trees = [b.train_iter(i, cfg, nl, -1, 0.1, qbins, True) for i in range(iters)]
         scores = b.scores()
     finally:
         b.close()
@@ -285,16 +292,18 @@ def test_config2_full_size():
 
 def test_config4_full_size():
     """2,000,000 x 700 (U(0,1), 30% zeros), Poisson(120) queries,
-    lambdarank, quantized int8 gradients, max_bin 255, 255 leaves: one iteration."""
+    lambdarank, quantized int8 gradients, max_bin 255, 255 leaves: three iterations,
+    every tree field and every score bit-exact."""
     from lightgbm_rs_amd.synth import config4_raw_host, sample_mappers
-    n, F, nl = 2_000_000, 700, 255
+    n, F, nl, iters = 2_000_000, 700, 255, 3
     X, rel, groups = config4_raw_host(n, F=F)
     qb = np.concatenate([[0], np.cumsum(groups)]).astype(np.int32)
     ms = sample_mappers(X, 255)
-    say(f"configs[4] full size {n} x {F}, {len(groups)} queries")
-    trees, scores, init, bins, meta, ub, cfg = _full_chain(X, ms, rel, "lambdarank", nl, 4, qb=qb)
+    say(f"configs[4] full size {n} x {F}, {len(groups)} queries, {iters} iterations")
+    trees, scores, init, bins, meta, ub, cfg = _full_chain(X, ms, rel, "lambdarank", nl, 4, qb=qb,
+                                                           iters=iters)
     del X
     say("device done")
-    oscores, otrees = oracle.train(bins, meta, ub, rel, cfg, oracle.OBJECTIVE_LAMBDARANK, nl, -1, 1,
-                                   0.1, quantized=True, query_boundaries=qb)
+    oscores, otrees = oracle.train(bins, meta, ub, rel, cfg, oracle.OBJECTIVE_LAMBDARANK, nl, -1,
+                                   iters, 0.1, quantized=True, query_boundaries=qb)
     compare(trees, scores, otrees, oscores, 0.0, "configs[4] full", exact=True)
