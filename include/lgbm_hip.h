@@ -297,6 +297,52 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* ctx, const uint32_t* bins, int64_t n, 
                             uint32_t most_freq_bin, int32_t na_as_missing, int32_t default_left,
                             uint32_t* order_out, int64_t* left_count_out);
 
+/* ---- device-resident histogram slots ----------------------------------------- */
+/* The reference's resident pool (lib.rs:1940-2058): each leaf's f64 histogram
+ * (slot_len doubles, the concatenated stride-2 layout of the resident features)
+ * stays in a device slot owned by the context; only SplitInfos come back.  Every
+ * entry runs on the context stream and returns after it completes.  Slots are
+ * invalidated by a new bins upload (reset again). */
+
+/* `Backend::reset_resident_pool(num_slots, slot_len)` (lib.rs:1940): size the pool;
+ * slot_len must equal the resident layout's (2 x the features' bin counts). */
+int lgbm_hip_resident_reset(lgbm_hip_ctx* ctx, int32_t num_slots, int64_t slot_len);
+
+/* `Backend::build_resident_leaf` (lib.rs:1953-1972): build the leaf's histogram from
+ * the resident bins and the current gradients (quantized after lgbm_hip_quantize,
+ * else f32), FixHistogram on its RAW sums, compaction, into `slot`.  leaf_rows (host,
+ * n_rows entries) NULL = every row. */
+int lgbm_hip_resident_build(lgbm_hip_ctx* ctx, int32_t slot, const uint32_t* leaf_rows,
+                            int64_t n_rows, double sum_gradient, double sum_hessian);
+
+/* `Backend::move_resident(src, dst)` (lib.rs:1978): dst receives src's histogram. */
+int lgbm_hip_resident_move(lgbm_hip_ctx* ctx, int32_t src_slot, int32_t dst_slot);
+
+/* `Backend::subtract_resident` (lib.rs:1988-2000): larger = parent - smaller in f64
+ * (histogram_pool.rs:249; not re-fixed).  larger_slot may be parent_slot. */
+int lgbm_hip_resident_subtract(lgbm_hip_ctx* ctx, int32_t parent_slot, int32_t smaller_slot,
+                               int32_t larger_slot);
+
+/* `Backend::scan_resident_leaf` (lib.rs:2012-2027): FindBestThreshold of every
+ * `feats` entry over slot's histogram (cfg->parent_output as given); out has n_feats
+ * entries, in input order. */
+int lgbm_hip_resident_scan(lgbm_hip_ctx* ctx, int32_t slot, const lgbm_batched_feature* feats,
+                           int32_t n_feats, const lgbm_gain_config* cfg, double sum_gradient,
+                           double sum_hessian, int32_t num_data, lgbm_split_info* out);
+
+/* `Backend::scan_resident_siblings` (lib.rs:2043-2058): both siblings of a split with
+ * one wait and readback; each side's totals carry its own parent_output (`weight`),
+ * which replaces cfg->parent_output for that side. */
+int lgbm_hip_resident_scan_siblings(lgbm_hip_ctx* ctx, int32_t smaller_slot, int32_t larger_slot,
+                                    const lgbm_batched_feature* feats, int32_t n_feats,
+                                    const lgbm_gain_config* cfg, const lgbm_leaf_sums* smaller,
+                                    const lgbm_leaf_sums* larger, lgbm_split_info* out_smaller,
+                                    lgbm_split_info* out_larger);
+
+/* Copy a slot's histogram to host memory (slot_len doubles); no counterpart in the
+ * reference (its handles are read only by its own scans), for checks. */
+int lgbm_hip_resident_read(lgbm_hip_ctx* ctx, int32_t slot, double* out);
+
 /* ---- coarse seam: one whole tree per call ----------------------------------- */
 
 /* Grow one tree on device from the resident bins and the CURRENT gradients:

@@ -142,6 +142,12 @@ class TreeOut(C.Structure):
     ]
 
 
+class LeafSums(C.Structure):
+    """lgbm_leaf_sums: a leaf's raw totals and its parent_output (LeafSplits)."""
+    _fields_ = [("sum_gradient", C.c_double), ("sum_hessian", C.c_double),
+                ("num_data", C.c_int32), ("_pad", C.c_int32), ("weight", C.c_double)]
+
+
 class LayoutOut(C.Structure):
     _fields_ = [
         ("indices", C.POINTER(C.c_uint32)),

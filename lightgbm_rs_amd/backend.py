@@ -10,8 +10,8 @@ import os
 
 import numpy as np
 
-from ._abi import (STATUS, BatchedFeature, FeatureMeta, GainConfig, LayoutBuffers, SplitInfo,
-                   TreeBuffers, ptr)
+from ._abi import (STATUS, BatchedFeature, FeatureMeta, GainConfig, LayoutBuffers, LeafSums,
+                   SplitInfo, TreeBuffers, ptr)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liblgbm_hip.so")
@@ -173,9 +173,63 @@ class HipBackend:
             ptr(out, C.c_int64)))
         return out
 
-    def build_resident_leaf(self, leaf_rows, sum_gradient, sum_hessian):
-        """`Backend::build_resident_leaf` (lib.rs:1953-1972): build + fix + compact."""
+    # ---- device-resident histogram slots (lib.rs:1940-2058) -------------------------
+    def reset_resident_pool(self, num_slots, slot_len=None):
+        """`Backend::reset_resident_pool`: num_slots device slots of slot_len doubles."""
+        self._check(self.lib.lgbm_hip_resident_reset(
+            self.ctx, C.c_int32(num_slots), C.c_int64(self.slot_len if slot_len is None else slot_len)))
+
+    def move_resident(self, src_slot, dst_slot):
+        """`Backend::move_resident`."""
+        self._check(self.lib.lgbm_hip_resident_move(self.ctx, C.c_int32(src_slot), C.c_int32(dst_slot)))
+
+    def subtract_resident(self, parent_slot, smaller_slot, larger_slot):
+        """`Backend::subtract_resident`: larger = parent - smaller on the device."""
+        self._check(self.lib.lgbm_hip_resident_subtract(self.ctx, C.c_int32(parent_slot),
+                                                        C.c_int32(smaller_slot),
+                                                        C.c_int32(larger_slot)))
+
+    def scan_resident_leaf(self, slot, feats, cfg, sum_gradient, sum_hessian, num_data):
+        """`Backend::scan_resident_leaf`: per-feature SplitInfos of a resident slot."""
+        farr = (BatchedFeature * len(feats))(*feats)
+        out = (SplitInfo * len(feats))()
+        self._check(self.lib.lgbm_hip_resident_scan(
+            self.ctx, C.c_int32(slot), farr, C.c_int32(len(feats)), C.byref(cfg),
+            C.c_double(sum_gradient), C.c_double(sum_hessian), C.c_int32(num_data), out))
+        return list(out)
+
+    def scan_resident_siblings(self, smaller_slot, larger_slot, feats, cfg, smaller_totals,
+                               larger_totals):
+        """`Backend::scan_resident_siblings`; totals = (sum_g, sum_h, num_data,
+        parent_output) of each sibling.  Returns (smaller splits, larger splits)."""
+        farr = (BatchedFeature * len(feats))(*feats)
+        o1 = (SplitInfo * len(feats))()
+        o2 = (SplitInfo * len(feats))()
+        st, lt = LeafSums(), LeafSums()
+        st.sum_gradient, st.sum_hessian, st.num_data, st.weight = smaller_totals
+        lt.sum_gradient, lt.sum_hessian, lt.num_data, lt.weight = larger_totals
+        self._check(self.lib.lgbm_hip_resident_scan_siblings(
+            self.ctx, C.c_int32(smaller_slot), C.c_int32(larger_slot), farr, C.c_int32(len(feats)),
+            C.byref(cfg), C.byref(st), C.byref(lt), o1, o2))
+        return list(o1), list(o2)
+
+    def read_resident(self, slot):
+        """A slot's histogram as host doubles (lgbm_hip_resident_read)."""
+        out = np.zeros(self.slot_len, np.float64)
+        self._check(self.lib.lgbm_hip_resident_read(self.ctx, C.c_int32(slot), ptr(out, C.c_double)))
+        return out
+
+    def build_resident_leaf(self, leaf_rows, sum_gradient, sum_hessian, slot=None):
+        """`Backend::build_resident_leaf` (lib.rs:1953-1972): build + fix + compact.
+        slot given: into that resident slot (nothing returned); else the histogram is
+        returned as host doubles."""
         rows = None if leaf_rows is None else np.ascontiguousarray(leaf_rows, np.uint32)
+        if slot is not None:
+            self._check(self.lib.lgbm_hip_resident_build(
+                self.ctx, C.c_int32(slot), ptr(rows, C.c_uint32),
+                C.c_int64(0 if rows is None else len(rows)), C.c_double(sum_gradient),
+                C.c_double(sum_hessian)))
+            return None
         out = np.zeros(self.slot_len, np.float64)
         self._check(self.lib.lgbm_hip_build_leaf_histogram(
             self.ctx, ptr(rows, C.c_uint32), C.c_int64(0 if rows is None else len(rows)),

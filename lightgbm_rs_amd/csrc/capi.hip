@@ -236,6 +236,10 @@ struct lgbm_hip_ctx {
   void* scratch = nullptr;
   size_t scratch_cap = 0;
   double* slot_tmp = nullptr;
+  // device-resident histogram slots (lgbm_hip_resident_*)
+  double* res_slots = nullptr;
+  int32_t res_num = 0;
+  int64_t res_len = 0, res_cap = 0;
   uint32_t* d_indices = nullptr;
   int64_t indices_cap = 0;
   // captured per-tree launch sequence (all parameters live in device memory)
@@ -1289,6 +1293,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(T.route_node);
   F(c->scratch);
   F(c->slot_tmp);
+  F(c->res_slots);
   F(c->d_indices);
   for (auto& p : c->ev_pool) {
     (void)hipEventDestroy(p.a);
@@ -1862,11 +1867,14 @@ int lgbm_hip_build_int_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int
   return LGBM_HIP_OK;
 }
 
-int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int64_t n_rows,
-                                  double sum_gradient, double sum_hessian, double* out) {
-  int rc = check_ctx(c);
-  if (rc) return rc;
-  c->ahead = false;  // device inputs change: a pending lookahead is stale
+}  // extern "C"
+
+// build_resident_leaf's body (lib.rs:1953-1972): gather the leaf's rows, build its
+// histogram (quantized or f32 gradients), FixHistogram + compaction on the leaf's RAW
+// sums, into the device slot d_out (slot_len doubles); enqueued on the context stream.
+static int build_leaf_into(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int64_t n_rows,
+                           double sum_gradient, double sum_hessian, double* d_out) {
+  int rc;
   if (rec_wide(c->fmt))
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "per-op histogram builds need the record layouts (F <= 124, cells <= 8192)");
@@ -1881,7 +1889,6 @@ int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, in
   if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "quantized histograms hold every cell in LDS: at most 8192 (feature, bin) cells");
-  if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
   DevLearner L0 = make_learner(c);
   if (fp) {
     if ((rc = ensure_fp(c))) return rc;
@@ -1892,14 +1899,27 @@ int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, in
   LeafSums s{sum_gradient, sum_hessian, 0.0, (int32_t)(leaf_rows ? n_rows : c->N), 0};
   if ((rc = ctl_write(c, CTL_OFF(sm), s))) return rc;
   if ((rc = ctl_write(c, CTL_OFF(fp_mode), fp))) return rc;
-  if ((rc = dalloc(c, &c->slot_tmp, (size_t)c->slot_len))) return rc;
   DevLearner L = make_learner(c);
   if (fp)
     launch_hist_f32(L, c->stream);
   else
     launch_hist(L, c->stream);
-  launch_fixscan(L, 2, c->slot_tmp, c->stream);
+  launch_fixscan(L, 2, d_out, c->stream);
   HIPCHK(c, hipGetLastError());
+  return LGBM_HIP_OK;
+}
+
+extern "C" {
+
+int lgbm_hip_build_leaf_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int64_t n_rows,
+                                  double sum_gradient, double sum_hessian, double* out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;  // device inputs change: a pending lookahead is stale
+  if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  if ((rc = dalloc(c, &c->slot_tmp, (size_t)c->slot_len))) return rc;
+  if ((rc = build_leaf_into(c, leaf_rows, n_rows, sum_gradient, sum_hessian, c->slot_tmp)))
+    return rc;
   HIPCHK(c, hipStreamSynchronize(c->stream));
   HIPCHK(c, hipMemcpy(out, c->slot_tmp, (size_t)c->slot_len * 8, hipMemcpyDeviceToHost));
   return LGBM_HIP_OK;
@@ -2107,6 +2127,191 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* c, const uint32_t* bins, int64_t n, ui
   *left_count_out = lc;
   // the scratch rows were sized for W=1 here; force a re-size for the next gather
   c->buf_rows[BUF_S0] = c->buf_rows[BUF_S1] = 0;
+  return LGBM_HIP_OK;
+}
+
+// ---- device-resident histogram slots ----------------------------------------------
+// The reference's resident arm keeps each leaf's f64 histogram in a device slot that
+// never crosses to the host (Backend::reset_resident_pool, build_resident_leaf,
+// move_resident, subtract_resident, scan_resident_leaf, scan_resident_siblings;
+// lib.rs:1940-2058).  Here the slots are one context-owned array of num_slots x
+// slot_len doubles; every entry runs on the context stream and returns after it.
+
+}  // extern "C"
+
+static int res_slot_ok(lgbm_hip_ctx* c, int32_t s) {
+  if (!c->res_slots || c->res_num == 0)
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "reset the resident pool first");
+  if (c->res_len != (int64_t)c->slot_len)
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "the resident pool predates the current bins: reset it");
+  if (s < 0 || s >= c->res_num)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT,
+                   "resident slot " + std::to_string(s) + " outside [0, " +
+                       std::to_string(c->res_num) + ")");
+  return LGBM_HIP_OK;
+}
+
+// The host entry's feature checks and table (find_best_splits), the table staged in
+// the scratch buffer after `reserve` bytes; returns the device table in *d_f.
+static int res_feature_table(lgbm_hip_ctx* c, const lgbm_batched_feature* feats, int32_t n_feats,
+                             size_t reserve, DevFeature** d_f) {
+  std::vector<DevFeature> df((size_t)n_feats);
+  for (int i = 0; i < n_feats; ++i) {
+    if (feats[i].num_bin == 0) return set_err(c, LGBM_HIP_ERR_RUNTIME, "num_bin must be > 0");
+    if (feats[i].num_bin > 256) return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_bin must be <= 256");
+    if (feats[i].slot_off + 2ull * feats[i].num_bin > (uint64_t)c->res_len)
+      return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH, "feature region beyond the slot");
+    df[(size_t)i] = feature_from_batched(feats[i]);
+  }
+  const size_t tab = (size_t)n_feats * sizeof(DevFeature);
+  int rc = ensure_scratch_bytes(c, reserve + tab);
+  if (rc) return rc;
+  *d_f = (DevFeature*)((char*)c->scratch + reserve);
+  HIPCHK(c, hipMemcpy(*d_f, df.data(), tab, hipMemcpyHostToDevice));
+  return LGBM_HIP_OK;
+}
+
+extern "C" {
+
+int lgbm_hip_resident_reset(lgbm_hip_ctx* c, int32_t num_slots, int64_t slot_len) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
+  if (num_slots < 1) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_slots must be >= 1");
+  if (slot_len != (int64_t)c->slot_len)
+    return set_err(c, LGBM_HIP_ERR_LENGTH_MISMATCH,
+                   "slot_len " + std::to_string(slot_len) + " != the resident layout's " +
+                       std::to_string(c->slot_len));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (!c->res_slots || (int64_t)num_slots * slot_len > c->res_cap) {
+    c->res_num = 0;
+    if ((rc = dalloc(c, &c->res_slots, (size_t)num_slots * (size_t)slot_len))) {
+      c->res_cap = 0;
+      return rc;
+    }
+    c->res_cap = (int64_t)num_slots * slot_len;
+  }
+  c->res_num = num_slots;
+  c->res_len = slot_len;
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_resident_build(lgbm_hip_ctx* c, int32_t slot, const uint32_t* leaf_rows,
+                            int64_t n_rows, double sum_gradient, double sum_hessian) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;
+  if ((rc = res_slot_ok(c, slot))) return rc;
+  if (leaf_rows && n_rows < 0) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "negative n_rows");
+  if ((rc = build_leaf_into(c, leaf_rows, n_rows, sum_gradient, sum_hessian,
+                            c->res_slots + (size_t)slot * (size_t)c->res_len)))
+    return rc;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_resident_move(lgbm_hip_ctx* c, int32_t src_slot, int32_t dst_slot) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if ((rc = res_slot_ok(c, src_slot)) || (rc = res_slot_ok(c, dst_slot))) return rc;
+  if (src_slot == dst_slot) return LGBM_HIP_OK;
+  const size_t L = (size_t)c->res_len;
+  HIPCHK(c, hipMemcpyAsync(c->res_slots + (size_t)dst_slot * L, c->res_slots + (size_t)src_slot * L,
+                           L * 8, hipMemcpyDeviceToDevice, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_resident_subtract(lgbm_hip_ctx* c, int32_t parent_slot, int32_t smaller_slot,
+                               int32_t larger_slot) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if ((rc = res_slot_ok(c, parent_slot)) || (rc = res_slot_ok(c, smaller_slot)) ||
+      (rc = res_slot_ok(c, larger_slot)))
+    return rc;
+  if (smaller_slot == larger_slot)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "smaller and larger slots coincide");
+  const size_t L = (size_t)c->res_len;
+  // elementwise: larger may be the parent's slot (each cell is read, then written)
+  launch_subtract(c->res_slots + (size_t)parent_slot * L, c->res_slots + (size_t)smaller_slot * L,
+                  (int64_t)L, c->res_slots + (size_t)larger_slot * L, c->stream);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_resident_read(lgbm_hip_ctx* c, int32_t slot, double* out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  if ((rc = res_slot_ok(c, slot))) return rc;
+  if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipMemcpy(out, c->res_slots + (size_t)slot * (size_t)c->res_len,
+                      (size_t)c->res_len * 8, hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_resident_scan(lgbm_hip_ctx* c, int32_t slot, const lgbm_batched_feature* feats,
+                           int32_t n_feats, const lgbm_gain_config* cfg, double sum_gradient,
+                           double sum_hessian, int32_t num_data, lgbm_split_info* out) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;
+  if ((rc = res_slot_ok(c, slot))) return rc;
+  if (!feats || !cfg || !out || n_feats < 0)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  if (n_feats == 0) return LGBM_HIP_OK;
+  if (!(sum_hessian > 0.0))
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "find_best_split: sum_hessian must be > 0");
+  const size_t outb = ((size_t)n_feats * sizeof(lgbm_split_info) + 255) / 256 * 256;
+  DevFeature* d_f = nullptr;
+  if ((rc = res_feature_table(c, feats, n_feats, outb, &d_f))) return rc;
+  lgbm_split_info* d_out = (lgbm_split_info*)c->scratch;
+  launch_scan_explicit(c->res_slots + (size_t)slot * (size_t)c->res_len, d_f, n_feats, *cfg,
+                       sum_gradient, sum_hessian, num_data, d_out, c->stream);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipMemcpy(out, d_out, (size_t)n_feats * sizeof(lgbm_split_info), hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_resident_scan_siblings(lgbm_hip_ctx* c, int32_t smaller_slot, int32_t larger_slot,
+                                    const lgbm_batched_feature* feats, int32_t n_feats,
+                                    const lgbm_gain_config* cfg, const lgbm_leaf_sums* smaller,
+                                    const lgbm_leaf_sums* larger, lgbm_split_info* out_smaller,
+                                    lgbm_split_info* out_larger) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;
+  if ((rc = res_slot_ok(c, smaller_slot)) || (rc = res_slot_ok(c, larger_slot))) return rc;
+  if (!feats || !cfg || !smaller || !larger || !out_smaller || !out_larger || n_feats < 0)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  if (n_feats == 0) return LGBM_HIP_OK;
+  if (!(smaller->sum_hessian > 0.0) || !(larger->sum_hessian > 0.0))
+    return set_err(c, LGBM_HIP_ERR_RUNTIME, "find_best_split: sum_hessian must be > 0");
+  const size_t one = ((size_t)n_feats * sizeof(lgbm_split_info) + 255) / 256 * 256;
+  DevFeature* d_f = nullptr;
+  if ((rc = res_feature_table(c, feats, n_feats, 2 * one, &d_f))) return rc;
+  lgbm_split_info* d_out = (lgbm_split_info*)c->scratch;
+  lgbm_split_info* d_out2 = (lgbm_split_info*)((char*)c->scratch + one);
+  // each sibling's own parent_output (LeafSplits::weight) rides in its totals
+  lgbm_gain_config cs = *cfg, cl = *cfg;
+  cs.parent_output = smaller->weight;
+  cl.parent_output = larger->weight;
+  const size_t L = (size_t)c->res_len;
+  launch_scan_explicit(c->res_slots + (size_t)smaller_slot * L, d_f, n_feats, cs,
+                       smaller->sum_gradient, smaller->sum_hessian, smaller->num_data, d_out,
+                       c->stream);
+  launch_scan_explicit(c->res_slots + (size_t)larger_slot * L, d_f, n_feats, cl,
+                       larger->sum_gradient, larger->sum_hessian, larger->num_data, d_out2,
+                       c->stream);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipMemcpy(out_smaller, d_out, (size_t)n_feats * sizeof(lgbm_split_info),
+                      hipMemcpyDeviceToHost));
+  HIPCHK(c, hipMemcpy(out_larger, d_out2, (size_t)n_feats * sizeof(lgbm_split_info),
+                      hipMemcpyDeviceToHost));
   return LGBM_HIP_OK;
 }
 
