@@ -21,7 +21,8 @@ first iterations with that run's trees and scores, bit for bit.
 `--workload config2|config4` instead times BASELINE.json configs[2] (1M x 2000 sparse
 LogNormal features, L2 regression, f32 gradients, feature_fraction 0.8, 127 leaves)
 or configs[4] (2M x 700, lambdarank over query groups, quantized, 255 leaves) on the
-wide row layout, as a secondary line (no roofline or CPU leg); the default
+wide row layout, as a secondary line with the roofline of its dominant kernel
+(k_hist_wide) and the CPU restatement timed on its first iteration; the default
 `config1` is the headline above.
 """
 import argparse
@@ -156,17 +157,24 @@ def secondary(args):
     mappers = sample_mappers(X, 255)
     log(f"{args.workload}: data + mappers {time.perf_counter() - t0:.1f}s")
     init = boost_from_score(obj, y)
+    init = init if abs(init) > 1e-15 else 0.0
     cfg = GainConfig.make(min_data_in_leaf=20)
     be = HipBackend(0)
     be.upload_raw(X, mappers, col_major=True)
     del X
-    be.set_labels(y, init if abs(init) > 1e-15 else 0.0)
-    if obj == "lambdarank":
-        be.set_lambdarank(qb)
-    else:
-        be.set_objective(obj)
-    if ff < 1.0:
-        be.set_col_sampler(ff, 1.0, 2)
+    cpu_iters = min(args.cpu_iters, 1)
+    bins = be.get_bins() if cpu_iters > 0 else None  # the CPU baseline's input
+
+    def start():
+        be.set_labels(y, init)
+        if obj == "lambdarank":
+            be.set_lambdarank(qb)
+        else:
+            be.set_objective(obj)
+        if ff < 1.0:
+            be.set_col_sampler(ff, 1.0, 2)
+
+    start()
     for i in range(max(args.warmup, 1)):
         be.train_iter(i, cfg, nl, -1, 0.1, qbins, True)
     t1 = time.perf_counter()
@@ -177,9 +185,52 @@ def secondary(args):
     for i in range(args.warmup + args.steps, args.warmup + args.steps + max(args.prof_steps, 1)):
         be.train_iter(i, cfg, nl, -1, 0.1, qbins, True)
     tm = be.timing()
+    be.set_timing(False)
+    gpu_first = None
+    if cpu_iters > 0:  # the parity leg's device iterations, from a fresh start
+        start()
+        gpu_first = [be.train_iter(i, cfg, nl, -1, 0.1, qbins, True) for i in range(cpu_iters)]
+        gpu_scores = be.scores()
     be.close()
     ps = max(args.prof_steps, 1)
     ms = elapsed / args.steps * 1e3
+    # k_hist_wide, the dominant kernel: the survey's algorithmic bytes, u8 bins (F per
+    # row), the pair (2 B quantized, 8 B f32) and the row index of a child build
+    w_gh = 2 if qbins else 8
+    cell_b = 8 if qbins else 16
+    hist_bytes = (tm["root_rows"] * (F + w_gh) + tm["hist_child_rows"] * (F + w_gh + 4)
+                  + (tm["hist_launches"] + tm["partition_launches"]) * tm["cells"] * cell_b)
+    hist_launches = tm["hist_launches"] + tm["partition_launches"]
+    hist_gbs = hist_bytes / (tm["hist_ms"] * 1e-3) / 1e9 if tm["hist_ms"] > 0 else 0.0
+    cpu, parity = None, None
+    if cpu_iters > 0:
+        from oracle import oracle
+        from lightgbm_rs_amd import feature_meta
+        meta = [feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f)
+                for f, m in enumerate(mappers)]
+        ub = np.concatenate([m.upper_bounds for m in mappers])
+        env_threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+        threads = oracle.set_threads(args.cpu_threads or env_threads or len(os.sched_getaffinity(0)))
+        okind = oracle.OBJECTIVE_LAMBDARANK if obj == "lambdarank" else oracle.OBJECTIVE_REGRESSION
+        tc = time.perf_counter()
+        oscores, otrees = oracle.train(bins, meta, ub, y, cfg, okind, nl, -1, cpu_iters, 0.1,
+                                       quantized=qbins > 0, feature_fraction=ff,
+                                       feature_fraction_seed=2, query_boundaries=qb)
+        cs = time.perf_counter() - tc
+        log(f"cpu: {cs:.1f}s for {cpu_iters} iteration(s) on {threads} threads")
+        model_name, phys = cpu_info()
+        cpu = {"value": round(cs / cpu_iters * 100.0, 3), "unit": "s/100 trees", "cores": threads,
+               "kind": "port",
+               "sample": f"the first {cpu_iters} boosting iteration(s) of the same workload and "
+                         f"bins (C++ restatement of the reference CpuBackend learner, OpenMP, "
+                         f"{threads} threads: {cs:.1f}s), scaled to 100 trees",
+               "cpu_model": model_name, "physical_cores": phys,
+               "gpu_speedup": round((cs / cpu_iters) / (elapsed / args.steps), 1)}
+        parity = compare_iterations(gpu_first, gpu_scores, otrees, oscores, init)
+        if not qbins:  # f32 gradients: fixed-point cells vs the f64 fold (stated bar 1e-5)
+            parity["scores_max_rel_diff"] = float(
+                np.max(np.abs(gpu_scores - oscores) / np.maximum(np.abs(oscores), 1e-300)))
+        log(f"parity: {parity}")
     print(json.dumps({
         "metric": f"sec per 100 trees, {args.workload} (wide row layout), 1 MI355X",
         "value": round(ms / 10.0, 4), "unit": "s/100 trees", "n_gpus": 1, "steps": args.steps,
@@ -189,7 +240,14 @@ def secondary(args):
         "config": {"workload": workload, "rows": n, "features": F, "num_leaves": nl},
         "phase_ms_per_step": {k: round(v / ps, 4) for k, v in tm.items()
                               if k.endswith("_ms")},
-        "rounds_per_tree": round(tm["rounds"] / max(tm["trees"], 1.0), 1)}), flush=True)
+        "rounds_per_tree": round(tm["rounds"] / max(tm["trees"], 1.0), 1),
+        "roofline": {"bound": "hbm", "achieved": round(hist_gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(hist_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_hist_wide (ConstructHistogram, root and child builds)",
+                     "bytes_per_launch": round(hist_bytes / max(hist_launches, 1), 1),
+                     "launches": int(hist_launches),
+                     "avg_launch_us": round(tm["hist_ms"] * 1e3 / max(hist_launches, 1), 3)},
+        "cpu_baseline": cpu, "parity": parity}), flush=True)
 
 
 def lds_probe(args):

@@ -1003,10 +1003,12 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
           hj.a0 = 0;
           hj.nblk = 0;
           ctl->hjobs[j] = hj;
+          atomicAdd(&L.stats[5], (double)hj.count);  // rows of the child builds
         }
         atomicAdd(&L.stats[0], (double)count);
         atomicAdd(&L.stats[4], 1.0);
-        // rows whose histogram this pass built (the side predicted smaller)
+        // rows whose histogram this pass built (the side predicted smaller; the f32 and
+        // wide paths count their separate child builds above)
         if (HIST && J.acc_right >= 0) atomicAdd(&L.stats[5], (double)(J.acc_right ? rc : lc));
       } else {
         ctl->part_left_count = lc;
