@@ -297,6 +297,16 @@ int lgbm_hip_data_partition(lgbm_hip_ctx* ctx, const uint32_t* bins, int64_t n, 
                             uint32_t most_freq_bin, int32_t na_as_missing, int32_t default_left,
                             uint32_t* order_out, int64_t* left_count_out);
 
+/* `quant_train_renew_leaf` (Gbdt::with_quant_renew_leaf, gbdt.rs:472-477; applied at
+ * gbdt.rs:1194-1212 through renew_tree_output, learner.rs:4411-4429): with quantized
+ * gradients, every tree the train_iter entries grow gets its leaf outputs recomputed
+ * from the original f32 gradients, -ThresholdL1(sum_g, lambda_l1) / (sum_h +
+ * lambda_l2) of the cfg, the sums an ordered f64 fold over each leaf's rows in
+ * partition order; before shrinkage and the score update.  No effect on f32-gradient
+ * training.  Set after the bins upload (an upload of another row count needs it set
+ * again). */
+int lgbm_hip_set_quant_renew_leaf(lgbm_hip_ctx* ctx, int32_t enable);
+
 /* ---- device-resident histogram slots ----------------------------------------- */
 /* The reference's resident pool (lib.rs:1940-2058): each leaf's f64 histogram
  * (slot_len doubles, the concatenated stride-2 layout of the resident features)

@@ -381,6 +381,11 @@ class HipBackend:
                                                     C.c_int64(self.num_data)))
         return g, h
 
+    def set_quant_renew_leaf(self, enable=True):
+        """quant_train_renew_leaf: quantized trees' leaf outputs from the original
+        gradients (lgbm_hip_set_quant_renew_leaf)."""
+        self._check(self.lib.lgbm_hip_set_quant_renew_leaf(self.ctx, C.c_int32(int(enable))))
+
     def set_lookahead(self, enable=True):
         """Enqueue the next iteration's gradients + quantization inside
         train_iter_binary (lgbm_hip_set_lookahead); results are unchanged."""

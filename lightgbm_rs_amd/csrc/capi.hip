@@ -236,6 +236,12 @@ struct lgbm_hip_ctx {
   void* scratch = nullptr;
   size_t scratch_cap = 0;
   double* slot_tmp = nullptr;
+  // quant_train_renew_leaf (lgbm_hip_set_quant_renew_leaf): the exported layout and
+  // its scratch, sized for num_data rows and MAX_LEAVES leaves
+  bool renew_leaf = false;
+  int64_t renew_rows = 0;
+  uint32_t* renew_idx = nullptr;
+  void* renew_scratch = nullptr;
   // device-resident histogram slots (lgbm_hip_resident_*)
   double* res_slots = nullptr;
   int32_t res_num = 0;
@@ -1294,6 +1300,8 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->scratch);
   F(c->slot_tmp);
   F(c->res_slots);
+  F(c->renew_idx);
+  F(c->renew_scratch);
   F(c->d_indices);
   for (auto& p : c->ev_pool) {
     (void)hipEventDestroy(p.a);
@@ -2375,6 +2383,21 @@ int lgbm_hip_set_labels(lgbm_hip_ctx* c, const float* labels, int64_t n, double 
 }  // extern "C"
 
 namespace {
+// quant_train_renew_leaf after a quantized tree (gbdt.rs:1194-1212): the tree's layout
+// exported on the device, then every leaf's output from the original gradients g, h
+// (the tree blob's leaf values, read by the score update and the host copy).
+int renew_leaves(lgbm_hip_ctx* c, int32_t num_leaves, const float* g, const float* h,
+                 const lgbm_gain_config* cfg) {
+  if (!c->renew_idx || !c->renew_scratch || c->renew_rows != c->N)
+    return set_err(c, LGBM_HIP_ERR_RUNTIME,
+                   "quant_train_renew_leaf was set for other bins: set it again after the upload");
+  DevLearner L = make_learner(c);
+  launch_export_layout(L, num_leaves, c->renew_idx, c->renew_scratch, c->stream);
+  launch_renew_leaves(L, c->renew_idx, g, h, cfg->lambda_l1, cfg->lambda_l2, c->stream);
+  HIPCHK(c, hipGetLastError());
+  return LGBM_HIP_OK;
+}
+
 // One resident boosting iteration of a one-tree-per-iteration objective.
 int train_iter_single(lgbm_hip_ctx* c, int32_t objective, int32_t iter, const lgbm_gain_config* cfg,
                       int32_t num_leaves, int32_t max_depth, double learning_rate,
@@ -2409,6 +2432,7 @@ int train_iter_single(lgbm_hip_ctx* c, int32_t objective, int32_t iter, const lg
   c->ahead = false;
   if (!pro) enqueue_objective(c, objective, iter, num_grad_quant_bins, stochastic);
   if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
+  if (!fp && c->renew_leaf && (rc = renew_leaves(c, num_leaves, c->g, c->h, cfg))) return rc;
   DevLearner L = make_learner(c);
   KernelEvents ke;
   launch_score_update(L, learning_rate, c->score, c->stream, ev_kernel(c, FAM_OBJ, &ke));
@@ -2721,6 +2745,7 @@ int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gai
     HIPCHK(c, hipGetLastError());
     c->have_grad = false;  // c->g / c->h do not hold this class's gradients
     if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
+    if (!fp && c->renew_leaf && (rc = renew_leaves(c, num_leaves, gk, hk, cfg))) return rc;
     DevLearner L = make_learner(c);
     KernelEvents ke;
     launch_score_update(L, learning_rate, c->score + (size_t)k * N, c->stream,
@@ -2741,6 +2766,25 @@ int lgbm_hip_get_multiclass_gradients(lgbm_hip_ctx* c, float* grad, float* hess,
   HIPCHK(c, hipStreamSynchronize(c->stream));
   if (grad) HIPCHK(c, hipMemcpy(grad, c->gk, (size_t)n * 4, hipMemcpyDeviceToHost));
   if (hess) HIPCHK(c, hipMemcpy(hess, c->hk, (size_t)n * 4, hipMemcpyDeviceToHost));
+  return LGBM_HIP_OK;
+}
+
+int lgbm_hip_set_quant_renew_leaf(lgbm_hip_ctx* c, int32_t enable) {
+  int rc = check_ctx(c);
+  if (rc) return rc;
+  c->ahead = false;
+  if (!enable) {
+    c->renew_leaf = false;
+    return LGBM_HIP_OK;
+  }
+  if (!c->have_bins) return set_err(c, LGBM_HIP_ERR_RUNTIME, "upload bins first");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  c->renew_leaf = false;
+  if ((rc = dalloc(c, &c->renew_idx, (size_t)c->N))) return rc;
+  if ((rc = dalloc(c, (char**)&c->renew_scratch, export_layout_scratch_bytes(c->N, MAX_LEAVES))))
+    return rc;
+  c->renew_rows = c->N;
+  c->renew_leaf = true;
   return LGBM_HIP_OK;
 }
 

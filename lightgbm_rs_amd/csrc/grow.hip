@@ -1507,6 +1507,49 @@ __global__ __launch_bounds__(1024) void k_leaf_rank_offsets(DevLearner L, int64_
 }
 
 // ===========================================================================
+// quant_train_renew_leaf (gbdt.rs:936-943,1194-1212; renew_tree_output,
+// learner.rs:4411-4429): after a quantized tree, every leaf's output from the ORIGINAL
+// f32 gradients, -ThresholdL1(sum_g, l1) / (sum_h + l2), the sums an ordered f64 fold
+// over the leaf's rows in partition order (the exported layout: each leaf's rows
+// ascending, DataPartition::split's order).  One thread per leaf walks its rows
+// sequentially (the fold's order is its value); the loads run eight rows ahead.
+// ===========================================================================
+__global__ __launch_bounds__(256) void k_renew_leaves(DevLearner L, const uint32_t* __restrict__ indices,
+                                                      const float* __restrict__ g,
+                                                      const float* __restrict__ h, double l1,
+                                                      double l2) {
+  const int32_t nl = L.ctl->num_leaves;
+  const int l = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (nl <= 1 || l >= nl) return;  // renew_tree_output skips a single-leaf tree
+  const int32_t c = L.leaves.count[l];
+  const uint32_t* __restrict__ rows = indices + L.leaves.begin[l];
+  double sg = 0.0, sh = 0.0;
+  int32_t k = 0;
+  for (; k + 8 <= c; k += 8) {
+    uint32_t r[8];
+    float gv[8], hv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) r[u] = rows[k + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      gv[u] = g[r[u]];
+      hv[u] = h[r[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      sg += (double)gv[u];
+      sh += (double)hv[u];
+    }
+  }
+  for (; k < c; ++k) {
+    const uint32_t r = rows[k];
+    sg += (double)g[r];
+    sh += (double)h[r];
+  }
+  L.tree.leaf_value[l] = -threshold_l1(sg, l1) / (sh + l2);
+}
+
+// ===========================================================================
 // launchers
 // ===========================================================================
 void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth, int32_t slot_cap,
@@ -1557,6 +1600,10 @@ void launch_pair_scan(const DevLearner& L, int32_t spec_max, int32_t part_grid, 
 }
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
   KLAUNCH(ev, k_tree_finalize, dim3(1), dim3(256), 0, s, L);
+}
+void launch_renew_leaves(const DevLearner& L, const uint32_t* indices, const float* g,
+                         const float* h, double l1, double l2, hipStream_t s) {
+  k_renew_leaves<<<dim3(1), dim3(256), 0, s>>>(L, indices, g, h, l1, l2);
 }
 size_t export_layout_scratch_bytes(int64_t n, int32_t num_leaves) {
   const int64_t nblk = (n + RANK_ROWS - 1) / RANK_ROWS;

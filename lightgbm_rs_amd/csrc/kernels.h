@@ -251,6 +251,10 @@ void launch_score_update(const DevLearner& L, double lr, double* score, hipStrea
 void launch_leaf_of(const DevLearner& L, uint8_t* leaf_of, hipStream_t s);
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
 size_t export_layout_scratch_bytes(int64_t n, int32_t num_leaves);
+// quant_train_renew_leaf: the grown tree's leaf outputs from the original gradients
+// over the exported layout (indices as launch_export_layout leaves them)
+void launch_renew_leaves(const DevLearner& L, const uint32_t* indices, const float* g,
+                         const float* h, double l1, double l2, hipStream_t s);
 void launch_export_layout(const DevLearner& L, int32_t num_leaves, uint32_t* indices,
                           void* scratch, hipStream_t s);
 void launch_gather_rows(int fmt, const uint32_t* rows, int64_t n, const uint4* rec,

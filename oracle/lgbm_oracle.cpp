@@ -1836,13 +1836,32 @@ int oracle_multiclass_gradients(const double* score, const float* label, int64_t
 // iteration, else 0).  A round in which no class splits ends training (after the
 // first iteration its trees are dropped: gbdt.rs:1330-1349).  `scores` (K * n,
 // class-major) receives the final scores; trees_out (optional) holds iters * K trees.
+// RenewIntGradTreeOutput through renew_tree_output (learner.rs:4411-4429;
+// gbdt.rs:1194-1212): every leaf's output from the ordered f64 fold of the original
+// gradients og, oh over its rows in partition order, -ThresholdL1(sum_g, l1) /
+// (sum_h + l2), before shrinkage.
+void renew_leaf_outputs(Tree& t, const DataPartition& dp, const float* og, const float* oh,
+                        const lgbm_gain_config& cfg) {
+  if (t.num_leaves <= 1) return;
+  for (int32_t leaf = 0; leaf < t.num_leaves; ++leaf) {
+    const uint32_t* rows = dp.indices.data() + dp.leaf_begin[leaf];
+    const int32_t c = dp.leaf_count[leaf];
+    double sg = 0.0, sh = 0.0;
+    for (int32_t k = 0; k < c; ++k) {
+      sg += (double)og[rows[k]];
+      sh += (double)oh[rows[k]];
+    }
+    t.leaf_value[leaf] = -threshold_l1(sg, cfg.lambda_l1) / (sh + cfg.lambda_l2);
+  }
+}
+
 int oracle_train_multiclass(const void* bins, int32_t width, int32_t F, int64_t N,
                             const lgbm_feature_meta* meta, const double* ub, const float* label,
                             int32_t num_class, const lgbm_gain_config* cfg, int32_t num_leaves,
                             int32_t max_depth, int32_t iters, double lr,
                             int32_t boost_from_average, int32_t quantized, int32_t quant_bins,
                             int32_t stochastic, double* scores, lgbm_tree_out* trees_out,
-                            int32_t* n_trees) {
+                            int32_t* n_trees, int32_t quant_renew_leaf) {
   if (num_class > 256) return fail(LGBM_HIP_ERR_CAPABILITY, "num_class must be <= 256");
   Learner L;
   int rc = make_learner(L, bins, width, F, N, meta, ub, cfg, num_leaves, max_depth);
@@ -1858,9 +1877,15 @@ int oracle_train_multiclass(const void* bins, int32_t width, int32_t F, int64_t 
         for (int64_t i = 0; i < N; ++i) score[(size_t)k * N + i] += init[k];
     }
   std::vector<float> g((size_t)K * N), h((size_t)K * N);
+  const bool renew = quantized && quant_renew_leaf;
+  std::vector<float> og, oh;  // the original gradients of the iteration (renew)
   int32_t nt = 0;
   for (int32_t it = 0; it < iters; ++it) {
     M.gradients(score.data(), N, g.data(), h.data());
+    if (renew) {
+      og = g;
+      oh = h;
+    }
     if (quantized)
       for (int32_t k = 0; k < K; ++k) {
         const uint64_t seed = ((uint64_t)it << 20) ^ (uint64_t)k ^ 0x51702010ull;
@@ -1879,6 +1904,8 @@ int oracle_train_multiclass(const void* bins, int32_t width, int32_t F, int64_t 
         if (t.num_leaves > 1) {
           trained = true;
           any_split = true;
+          if (renew)
+            renew_leaf_outputs(t, dp, og.data() + (size_t)k * N, oh.data() + (size_t)k * N, *cfg);
           t.shrinkage(lr);
           double* sk = score.data() + (size_t)k * N;
           for (int32_t leaf = 0; leaf < t.num_leaves; ++leaf) {
@@ -1923,6 +1950,9 @@ typedef struct {
   double sigmoid;
   int32_t truncation_level, num_queries;
   const int32_t* query_boundaries;  // num_queries + 1 (lambdarank)
+  // quant_train_renew_leaf (gbdt.rs:936-943,1194-1212): with quantized gradients, each
+  // tree's leaf outputs are recomputed from the original gradients
+  int32_t quant_renew_leaf, _pad;
 } oracle_train_params;
 
 int oracle_train(const void* bins, int32_t width, int32_t F, int64_t N,
@@ -1963,11 +1993,17 @@ int oracle_train(const void* bins, int32_t width, int32_t F, int64_t N,
       for (int64_t i = 0; i < N; ++i) score[i] += init;
   }
   std::vector<float> g(N), h(N);
+  const bool renew = p->quantized && p->quant_renew_leaf;
+  std::vector<float> og, oh;  // the original gradients of the iteration (renew)
   int32_t nt = 0;
   for (int32_t it = 0; it < p->iters; ++it) {
     if (p->objective == 0) binary_gradients(score.data(), label, g.data(), h.data(), N, 1.0);
     if (p->objective == 1) l2_gradients(score.data(), label, g.data(), h.data(), N);
     if (p->objective == 2) rank.gradients(score.data(), g.data(), h.data());
+    if (renew) {
+      og = g;
+      oh = h;
+    }
     if (p->quantized) {
       uint64_t seed = ((uint64_t)it << 20) ^ 0ull ^ 0x51702010ull;
       quantize_in_place(g.data(), h.data(), N, p->quant_bins, p->stochastic != 0, seed, nullptr,
@@ -1993,6 +2029,7 @@ int oracle_train(const void* bins, int32_t width, int32_t F, int64_t N,
       }
       break;
     }
+    if (renew) renew_leaf_outputs(t, dp, og.data(), oh.data(), *cfg);
     {
       t.shrinkage(p->learning_rate);
       for (int32_t leaf = 0; leaf < t.num_leaves; ++leaf) {

@@ -279,7 +279,7 @@ def multiclass_gradients(score, label, num_class):
 
 def train_multiclass(bins_fm, meta, upper, label, num_class, cfg, num_leaves, max_depth, iters,
                      lr, boost_from_average=True, quantized=False, quant_bins=4, stochastic=True,
-                     want_trees=True):
+                     want_trees=True, quant_renew_leaf=False):
     """Softmax boosting: (class-major final scores [K * n], trees in iteration-major,
     class-minor order)."""
     b, width = _bins_arg(bins_fm)
@@ -297,7 +297,8 @@ def train_multiclass(bins_fm, meta, upper, label, num_class, cfg, num_leaves, ma
         ptr(ub, C.c_double), ptr(lab, C.c_float), C.c_int32(num_class), C.byref(cfg),
         C.c_int32(num_leaves), C.c_int32(max_depth), C.c_int32(iters), C.c_double(lr),
         C.c_int32(int(boost_from_average)), C.c_int32(int(quantized)), C.c_int32(quant_bins),
-        C.c_int32(int(stochastic)), ptr(scores, C.c_double), tarr, C.byref(nt)))
+        C.c_int32(int(stochastic)), ptr(scores, C.c_double), tarr, C.byref(nt),
+        C.c_int32(int(quant_renew_leaf))))
     out_trees = []
     if want_trees:
         for i in range(nt.value):
@@ -318,16 +319,18 @@ class TrainParams(C.Structure):
                 ("feature_fraction", C.c_double), ("feature_fraction_seed", C.c_int32),
                 ("lambdarank_norm", C.c_int32), ("sigmoid", C.c_double),
                 ("truncation_level", C.c_int32), ("num_queries", C.c_int32),
-                ("query_boundaries", C.POINTER(C.c_int32))]
+                ("query_boundaries", C.POINTER(C.c_int32)),
+                ("quant_renew_leaf", C.c_int32), ("_pad", C.c_int32)]
 
 
 def train(bins_fm, meta, upper, label, cfg, objective, num_leaves, max_depth, iters, lr,
           boost_from_average=True, quantized=False, quant_bins=4, stochastic=True,
           feature_fraction=1.0, feature_fraction_seed=2, query_boundaries=None, sigmoid=1.0,
-          lambdarank_norm=True, truncation_level=30, want_trees=True):
+          lambdarank_norm=True, truncation_level=30, want_trees=True, quant_renew_leaf=False):
     """The one-tree-per-iteration boosting loop for binary logloss (0), L2 regression
-    (1) or lambdarank (2, over `query_boundaries`), with the optional quantizer and
-    per-tree column sampling.  Returns (final scores, trees)."""
+    (1) or lambdarank (2, over `query_boundaries`), with the optional quantizer (and its
+    quant_train_renew_leaf) and per-tree column sampling.  Returns (final scores,
+    trees)."""
     b, width = _bins_arg(bins_fm)
     F, N = b.shape
     marr = _meta_arr(meta)
@@ -343,6 +346,7 @@ def train(bins_fm, meta, upper, label, cfg, objective, num_leaves, max_depth, it
     p.lambdarank_norm, p.sigmoid, p.truncation_level = int(lambdarank_norm), sigmoid, truncation_level
     p.num_queries = 0 if qb is None else len(qb) - 1
     p.query_boundaries = ptr(qb, C.c_int32) if qb is not None else None
+    p.quant_renew_leaf = int(quant_renew_leaf)
     scores = np.zeros(N, dtype=np.float64)
     trees = [_tree_buffers(num_leaves, meta, upper) for _ in range(iters)] if want_trees else []
     tarr = (type(trees[0].out) * iters)(*[t.out for t in trees]) if want_trees else None
