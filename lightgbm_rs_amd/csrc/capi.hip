@@ -240,6 +240,10 @@ struct lgbm_hip_ctx {
   // its scratch, sized for num_data rows and MAX_LEAVES leaves
   bool renew_leaf = false;
   int64_t renew_rows = 0;
+  // dequantized gradients of a bin count other than 2 or 4 ([2][N] f32), fed to the
+  // fixed-point learner path with exact scales
+  float* dq = nullptr;
+  int64_t dq_rows = 0;
   uint32_t* renew_idx = nullptr;
   void* renew_scratch = nullptr;
   // device-resident histogram slots (lgbm_hip_resident_*)
@@ -547,6 +551,18 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
 }
 
 // f32-gradient training: the (g, h) pair buffers that move with the rows.
+// num_grad_quant_bins other than 2 and 4: the dequantized values go through the
+// fixed-point path (its scales set from the quantizer's, exact); 2 and 4 take the
+// packed integer cells.
+bool gen_bins(int32_t bins) { return bins > 0 && bins != 2 && bins != 4; }
+int ensure_dq(lgbm_hip_ctx* c) {
+  if (c->dq && c->dq_rows >= c->N) return LGBM_HIP_OK;
+  int rc = dalloc(c, &c->dq, 2 * (size_t)c->N);
+  if (rc) return rc;
+  c->dq_rows = c->N;
+  return LGBM_HIP_OK;
+}
+
 int ensure_fp(lgbm_hip_ctx* c) {
   for (int b : {BUF_ORIG, BUF_A, BUF_B}) {
     if (c->g32[b] && c->g32_rows[b] >= c->N) continue;
@@ -1126,11 +1142,16 @@ void enqueue_objective(lgbm_hip_ctx* c, int32_t objective, int32_t iter, int32_t
     c->quant_ready = false;
   } else {
     const uint64_t seed = ((uint64_t)(uint32_t)iter << 20) ^ 0ull ^ 0x51702010ull;  // gbdt.rs:950
+    const bool gen = gen_bins(qbins);  // the caller allocated c->dq
     ev_begin(c, FAM_QUANT);
     launch_quant_scales(c->ctl, c->partials, c->N, qbins, -1, c->stream);
     launch_quantize(c->g, c->h, c->N, c->ctl, c->wave_mats, c->lane_mats,
-                    seed ^ 0x9E3779B97F4A7C15ull, stochastic, c->gh[BUF_ORIG], nullptr, nullptr,
-                    c->stream);
+                    seed ^ 0x9E3779B97F4A7C15ull, stochastic, c->gh[BUF_ORIG],
+                    gen ? c->dq : nullptr, gen ? c->dq + c->N : nullptr, c->stream);
+    if (gen) {
+      DevLearner L0 = make_learner(c);
+      launch_exact_prep(L0, c->dq, c->dq + c->N, c->N, c->stream);
+    }
     ev_end(c);
     c->quant_ready = true;
     c->quant_bins = qbins;
@@ -1302,6 +1323,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->res_slots);
   F(c->renew_idx);
   F(c->renew_scratch);
+  F(c->dq);
   F(c->d_indices);
   for (auto& p : c->ev_pool) {
     (void)hipEventDestroy(p.a);
@@ -1711,7 +1733,12 @@ int lgbm_hip_quantize(lgbm_hip_ctx* c, int32_t bins, int32_t stochastic, uint64_
   if (bins < 1 || bins > 254)
     return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_grad_quant_bins must be in 1..=254");
   float *dg = nullptr, *dh = nullptr;
-  if (dg_out || dh_out) {
+  if (gen_bins(bins)) {
+    // the learner reads these dequantized values (the fixed-point path)
+    if ((rc = ensure_dq(c))) return rc;
+    dg = c->dq;
+    dh = c->dq + c->N;
+  } else if (dg_out || dh_out) {
     if ((rc = ensure_scratch_bytes(c, (size_t)c->N * 8))) return rc;
     dg = (float*)c->scratch;
     dh = dg + c->N;
@@ -1769,6 +1796,12 @@ int lgbm_hip_set_dequantized_gradients(lgbm_hip_ctx* c, const float* grad, const
   HIPCHK(c, hipMemcpy(c->g, grad, (size_t)n * 4, hipMemcpyHostToDevice));
   HIPCHK(c, hipMemcpy(c->h, hess, (size_t)n * 4, hipMemcpyHostToDevice));
   c->have_grad = true;
+  if (gen_bins(bins)) {
+    // the learner's input for these bin counts: the dequantized values themselves
+    if ((rc = ensure_dq(c))) return rc;
+    HIPCHK(c, hipMemcpy(c->dq, grad, (size_t)n * 4, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(c->dq + n, hess, (size_t)n * 4, hipMemcpyHostToDevice));
+  }
   if (given) {
     // the quantizer header of the control block, as compute_scales leaves it
     // (gradient_discretizer.rs:145-165); the packed cells need q_h >= 0 (hmin 0)
@@ -1845,6 +1878,9 @@ int lgbm_hip_build_int_histogram(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int
   c->ahead = false;  // device inputs change: a pending lookahead is stale
   if (!c->quant_ready) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize first");
   if (!out) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null out");
+  if (gen_bins(c->quant_bins))
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
+                   "integer (sum q) histograms need num_grad_quant_bins 2 or 4 (the packed cells)");
   if (rec_wide(c->fmt))
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "per-op histogram builds need the record layouts (F <= 124, cells <= 8192)");
@@ -1886,12 +1922,12 @@ static int build_leaf_into(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int64_t n
   if (rec_wide(c->fmt))
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "per-op histogram builds need the record layouts (F <= 124, cells <= 8192)");
-  // quantized gradients (after lgbm_hip_quantize) or the f32 gradients as uploaded
-  const int32_t fp = c->quant_ready ? 0 : 1;
-  if (fp && !c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set gradients first");
-  if (!fp && c->quant_bins != 2 && c->quant_bins != 4)
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
-                   "exact f64 histogram requires num_grad_quant_bins in {2, 4}");
+  // quantized gradients (after lgbm_hip_quantize; bin counts other than 2 and 4 as their
+  // dequantized values through the exact fixed-point path) or the f32 gradients
+  const bool gen = c->quant_ready && gen_bins(c->quant_bins);
+  const int32_t fp = c->quant_ready && !gen ? 0 : 1;
+  if (fp && !gen && !c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set gradients first");
+  if (gen && !c->dq) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize again");
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
   if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
@@ -1901,7 +1937,10 @@ static int build_leaf_into(lgbm_hip_ctx* c, const uint32_t* leaf_rows, int64_t n
   if (fp) {
     if ((rc = ensure_fp(c))) return rc;
     L0 = make_learner(c);
-    launch_fp_prep(L0, c->g, c->h, c->N, c->partials, c->stream);
+    if (gen)
+      launch_exact_prep(L0, c->dq, c->dq + c->N, c->N, c->stream);
+    else
+      launch_fp_prep(L0, c->g, c->h, c->N, c->partials, c->stream);
   }
   if ((rc = set_hist_job(c, leaf_rows, n_rows))) return rc;
   LeafSums s{sum_gradient, sum_hessian, 0.0, (int32_t)(leaf_rows ? n_rows : c->N), 0};
@@ -2331,12 +2370,14 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num
   if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
   if (num_leaves < 1) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_leaves must be >= 1");
   if (num_leaves > 256) return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_leaves must be <= 256");
-  // quantized gradients (after lgbm_hip_quantize) or the f32 gradients as uploaded
-  const int32_t fp = c->quant_ready ? 0 : 1;
-  if (fp && !c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set gradients first");
-  if (!fp && c->quant_bins != 2 && c->quant_bins != 4)
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
-                   "device learner requires num_grad_quant_bins in {2, 4}");
+  // quantized gradients (after lgbm_hip_quantize; bin counts other than 2 and 4 as their
+  // dequantized values through the exact fixed-point path) or the f32 gradients
+  const bool gen = c->quant_ready && gen_bins(c->quant_bins);
+  const int32_t fp = c->quant_ready && !gen ? 0 : 1;
+  if (fp && !gen && !c->have_grad) return set_err(c, LGBM_HIP_ERR_RUNTIME, "set gradients first");
+  if (gen && !c->dq) return set_err(c, LGBM_HIP_ERR_RUNTIME, "quantize again");
+  if (gen && c->quant_bins == 1)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_grad_quant_bins 1 gives no gradient scale");
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
   if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
@@ -2347,7 +2388,10 @@ int lgbm_hip_grow_tree(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num
     if ((rc = ensure_fp(c))) return rc;
     if ((rc = ensure_leaves(c, num_leaves))) return rc;
     DevLearner L = make_learner(c);
-    launch_fp_prep(L, c->g, c->h, c->N, c->partials, c->stream);
+    if (gen)
+      launch_exact_prep(L, c->dq, c->dq + c->N, c->N, c->stream);
+    else
+      launch_fp_prep(L, c->g, c->h, c->N, c->partials, c->stream);
   }
   if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
   return finish_tree(c, tree, layout, 1.0);
@@ -2412,11 +2456,14 @@ int train_iter_single(lgbm_hip_ctx* c, int32_t objective, int32_t iter, const lg
   if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
   if (num_leaves < 1 || num_leaves > 256)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_leaves must be in 1..=256");
-  // num_grad_quant_bins = 0: use_quantized_grad = false (f32 gradients)
-  const int32_t fp = num_grad_quant_bins == 0 ? 1 : 0;
-  if (!fp && num_grad_quant_bins != 2 && num_grad_quant_bins != 4)
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
-                   "device learner requires num_grad_quant_bins in {0, 2, 4}");
+  // num_grad_quant_bins = 0: use_quantized_grad = false (f32 gradients); 2 and 4: packed
+  // integer cells; other counts: the dequantized values through the exact fixed-point path
+  if (num_grad_quant_bins < 0 || num_grad_quant_bins > 254)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_grad_quant_bins must be in 0..=254");
+  if (num_grad_quant_bins == 1)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_grad_quant_bins 1 gives no gradient scale");
+  const bool gen = gen_bins(num_grad_quant_bins);
+  const int32_t fp = num_grad_quant_bins == 0 || gen ? 1 : 0;
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
   if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
@@ -2427,12 +2474,15 @@ int train_iter_single(lgbm_hip_ctx* c, int32_t objective, int32_t iter, const lg
     if ((rc = ensure_fp(c))) return rc;
     if ((rc = ensure_leaves(c, num_leaves))) return rc;
   }
+  if (gen && (rc = ensure_dq(c))) return rc;
   const bool pro = c->ahead && c->ahead_iter == iter && c->ahead_qbins == num_grad_quant_bins &&
                    c->ahead_stoch == stochastic && c->ahead_obj == objective;
   c->ahead = false;
   if (!pro) enqueue_objective(c, objective, iter, num_grad_quant_bins, stochastic);
   if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
-  if (!fp && c->renew_leaf && (rc = renew_leaves(c, num_leaves, c->g, c->h, cfg))) return rc;
+  if (num_grad_quant_bins > 0 && c->renew_leaf &&
+      (rc = renew_leaves(c, num_leaves, c->g, c->h, cfg)))
+    return rc;
   DevLearner L = make_learner(c);
   KernelEvents ke;
   launch_score_update(L, learning_rate, c->score, c->stream, ev_kernel(c, FAM_OBJ, &ke));
@@ -2691,10 +2741,12 @@ int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gai
   if (!cfg) return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "null cfg");
   if (num_leaves < 1 || num_leaves > 256)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_leaves must be in 1..=256");
-  const int32_t fp = num_grad_quant_bins == 0 ? 1 : 0;
-  if (!fp && num_grad_quant_bins != 2 && num_grad_quant_bins != 4)
-    return set_err(c, LGBM_HIP_ERR_CAPABILITY,
-                   "device learner requires num_grad_quant_bins in {0, 2, 4}");
+  if (num_grad_quant_bins < 0 || num_grad_quant_bins > 254)
+    return set_err(c, LGBM_HIP_ERR_INVALID_ARGUMENT, "num_grad_quant_bins must be in 0..=254");
+  if (num_grad_quant_bins == 1)
+    return set_err(c, LGBM_HIP_ERR_CAPABILITY, "num_grad_quant_bins 1 gives no gradient scale");
+  const bool gen = gen_bins(num_grad_quant_bins);
+  const int32_t fp = num_grad_quant_bins == 0 || gen ? 1 : 0;
   if (!fp && c->N >= QUANT_MAX_ROWS)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY, "quantized int32 histogram cells need N < 2^29");
   if (!fp && !rec_wide(c->fmt) && c->total_cells > QUANT_LDS_CELLS)
@@ -2707,6 +2759,7 @@ int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gai
         return rc;
   if ((rc = ensure_leaves(c, num_leaves))) return rc;
   if (fp && (rc = ensure_fp(c))) return rc;
+  if (gen && (rc = ensure_dq(c))) return rc;
   const int32_t K = c->num_class;
   const int64_t N = c->N;
   // factor = K / (K - 1) (multiclass.rs:84)
@@ -2725,7 +2778,7 @@ int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gai
     const float* gk = c->gk + (size_t)k * N;
     const float* hk = c->hk + (size_t)k * N;
     DevLearner L0 = make_learner(c);
-    if (fp) {
+    if (num_grad_quant_bins == 0) {
       ev_begin(c, FAM_QUANT);
       launch_fp_prep(L0, gk, hk, N, c->partials, c->stream);
       ev_end(c);
@@ -2737,7 +2790,9 @@ int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gai
       launch_absmax(gk, hk, N, c->partials, c->stream);
       launch_quant_scales(c->ctl, c->partials, N, num_grad_quant_bins, -1, c->stream);
       launch_quantize(gk, hk, N, c->ctl, c->wave_mats, c->lane_mats, seed ^ 0x9E3779B97F4A7C15ull,
-                      stochastic, c->gh[BUF_ORIG], nullptr, nullptr, c->stream);
+                      stochastic, c->gh[BUF_ORIG], gen ? c->dq : nullptr,
+                      gen ? c->dq + N : nullptr, c->stream);
+      if (gen) launch_exact_prep(L0, c->dq, c->dq + N, N, c->stream);
       ev_end(c);
       c->quant_ready = true;
       c->quant_bins = num_grad_quant_bins;
@@ -2745,7 +2800,9 @@ int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gai
     HIPCHK(c, hipGetLastError());
     c->have_grad = false;  // c->g / c->h do not hold this class's gradients
     if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
-    if (!fp && c->renew_leaf && (rc = renew_leaves(c, num_leaves, gk, hk, cfg))) return rc;
+    if (num_grad_quant_bins > 0 && c->renew_leaf &&
+        (rc = renew_leaves(c, num_leaves, gk, hk, cfg)))
+      return rc;
     DevLearner L = make_learner(c);
     KernelEvents ke;
     launch_score_update(L, learning_rate, c->score + (size_t)k * N, c->stream,

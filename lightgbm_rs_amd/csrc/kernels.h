@@ -242,6 +242,10 @@ void launch_partition_stable(const DevLearner& L, int64_t ntiles, int64_t blocks
 void launch_hist_f32(const DevLearner& L, hipStream_t s, const KernelEvents* ev = nullptr);
 void launch_fp_prep(const DevLearner& L, const float* g, const float* h, int64_t n,
                     const uint4* partials, hipStream_t s);
+// quantized gradients of a bin count other than 2 or 4: the dequantized values dg, dh
+// through the fixed-point path with the exact scales of the quantizer's header
+void launch_exact_prep(const DevLearner& L, const float* dg, const float* dh, int64_t n,
+                       hipStream_t s);
 void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth,
                       int32_t slot_cap, int32_t spec_max, int32_t fp_mode, hipStream_t s,
                       const KernelEvents* ev = nullptr);

@@ -260,6 +260,27 @@ __global__ __launch_bounds__(256) void k_fp_scales(Ctl* ctl, const uint4* __rest
   ctl->h_shift = fp_shift(__uint_as_float(s.ah), n);
 }
 
+// Quantized gradients of any bin count (num_grad_quant_bins other than 2 and 4) go
+// through the fixed-point path above with exact scales.  Every dequantized value
+// f32(q * scale) with |q| >= 1 has at least f32(1 * scale)'s magnitude, so its ulp is a
+// multiple of u = ulp(f32(1 * scale)) and the value an integer multiple of u: with
+// shift = -log2(u) each row's fixed-point value is that integer exactly (below 2^32),
+// cells, leaf totals and parent - child are exact, and (double)sum * u equals the
+// reference's f64 fold of the dequantized values whenever that fold is exact (every
+// partial sum below 2^53 u).
+__device__ __forceinline__ int32_t exact_shift(float v1) {
+  if (!(v1 > 0.0f) || !(v1 < __builtin_inff())) return 0;  // no nonzero value
+  if (v1 < 1.17549435e-38f) return 149;                      // subnormal: u = 2^-149
+  int e = 0;
+  (void)frexpf(v1, &e);  // v1 = f * 2^e, f in [0.5, 1): ulp = 2^(e - 24)
+  return 24 - e;
+}
+__global__ void k_exact_shifts(Ctl* ctl) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  ctl->g_shift = exact_shift(ctl->vg1);
+  ctl->h_shift = exact_shift(ctl->vh1);
+}
+
 __global__ void k_pack_g32(const float* __restrict__ g, const float* __restrict__ h, int64_t n,
                            float2* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1064,6 +1085,11 @@ void launch_hist_f32(const DevLearner& L, hipStream_t s, const KernelEvents* ev)
   const dim3 g(HIST_GRID + SPEC_MAX, (unsigned)std::max(L.n_fgroups, 1)), blk(HIST_THREADS);
   const size_t lds = (size_t)2 * HIST_FP_CELLS * sizeof(unsigned long long);
   DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_hist_f32<kF>), g, blk, lds, s, L));
+}
+void launch_exact_prep(const DevLearner& L, const float* dg, const float* dh, int64_t n,
+                       hipStream_t s) {
+  k_exact_shifts<<<1, 1, 0, s>>>(L.ctl);
+  k_pack_g32<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s>>>(dg, dh, n, L.bufs.g32[BUF_ORIG]);
 }
 void launch_fp_prep(const DevLearner& L, const float* g, const float* h, int64_t n,
                     const uint4* partials, hipStream_t s) {
