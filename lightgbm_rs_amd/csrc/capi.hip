@@ -252,10 +252,21 @@ struct lgbm_hip_ctx {
   int64_t res_len = 0, res_cap = 0;
   uint32_t* d_indices = nullptr;
   int64_t indices_cap = 0;
-  // captured per-tree launch sequence (all parameters live in device memory)
-  hipGraphExec_t graph_exec = nullptr;
-  int32_t graph_nl = -1, graph_md = 0, graph_rounds = 0, graph_spec = 0, graph_fp = -1;
+  // Captured per-tree launch sequences (all parameters live in device memory): one per
+  // round count in use (the round count follows the trees, a re-instantiation costs
+  // more than a tree's round), and a tail of TAIL_ROUNDS rounds launched when a tree
+  // needs more rounds than its sequence holds.  Keyed together by the tree shape.
+  static constexpr int GRAPH_CACHE = 8, TAIL_ROUNDS = 4, ROUND_HIST = 16;
+  hipGraphExec_t graph_exec[GRAPH_CACHE] = {};
+  int32_t graph_rounds[GRAPH_CACHE] = {};
+  uint64_t graph_used[GRAPH_CACHE] = {};  // last use (LRU eviction)
+  uint64_t graph_clock = 0;
+  hipGraphExec_t tail_exec = nullptr;
+  int32_t graph_nl = -1, graph_md = 0, graph_spec = 0, graph_fp = -1;
   int32_t round_cap = 24;     // partition rounds in the captured sequence
+  bool round_fixed = false;   // LGBM_HIP_ROUNDS: a fixed round count
+  int32_t round_hist[ROUND_HIST] = {};  // rounds the last trees used (ring)
+  int32_t round_hist_n = 0;
   int32_t spec_max = SPEC_DEFAULT;
   int32_t part_blocks = 256 * PART_BLOCKS_PER_CU;  // partition grid (set from the CU count)
   int32_t* done_host = nullptr;  // pinned: ctl->done after the captured rounds
@@ -631,6 +642,16 @@ void ev_collect(lgbm_hip_ctx* c) {
 enum { FAM_HIST = 0, FAM_PART = 1, FAM_SCAN = 2, FAM_QUANT = 3, FAM_OBJ = 4, FAM_BIN = 5,
        FAM_PRED = 6 };
 
+void drop_graphs(lgbm_hip_ctx* c) {
+  for (int i = 0; i < lgbm_hip_ctx::GRAPH_CACHE; ++i) {
+    if (c->graph_exec[i]) (void)hipGraphExecDestroy(c->graph_exec[i]);
+    c->graph_exec[i] = nullptr;
+    c->graph_rounds[i] = 0;
+  }
+  if (c->tail_exec) (void)hipGraphExecDestroy(c->tail_exec);
+  c->tail_exec = nullptr;
+}
+
 int check_ctx(lgbm_hip_ctx* c) {
   if (!c) return LGBM_HIP_ERR_INVALID_ARGUMENT;
   HIPCHK(c, hipSetDevice(c->device));
@@ -686,10 +707,53 @@ void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth, int32_
   enqueue_rounds(c, rounds, fp);
 }
 
+// The round count of the next trees' captured sequence: the 75th percentile of the
+// rounds the last trees used (ROUND_HIST of them).  The rounds a tree needs follow the
+// training (more in later iterations) and vary from tree to tree; a round past the
+// tree's end costs a near-empty plan / partition / scan, a tree that needs more runs
+// the tail sequence after one host check.
+void update_round_cap(lgbm_hip_ctx* c, int32_t used, int32_t num_leaves) {
+  constexpr int H = lgbm_hip_ctx::ROUND_HIST;
+  c->round_hist[c->round_hist_n % H] = used;
+  c->round_hist_n += 1;
+  if (c->round_fixed) return;
+  const int n = std::min(c->round_hist_n, H);
+  int32_t v[H];
+  std::copy(c->round_hist, c->round_hist + n, v);
+  std::sort(v, v + n);
+  const int q = (3 * n + 3) / 4 - 1;  // ceil(0.75 n) - 1
+  c->round_cap = std::max(1, std::min(num_leaves + 1, v[q]));
+}
+
+// The tail sequence: TAIL_ROUNDS more rounds (captured once per tree shape), else the
+// same rounds launched one by one.
+int launch_tail(lgbm_hip_ctx* c, int32_t fp) {
+  constexpr int32_t T = lgbm_hip_ctx::TAIL_ROUNDS;
+  if (c->timing || !c->use_graphs) {
+    enqueue_rounds(c, T, fp);
+    HIPCHK(c, hipGetLastError());
+    return LGBM_HIP_OK;
+  }
+  if (!c->tail_exec) {
+    hipGraph_t g = nullptr;
+    HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    enqueue_rounds(c, T, fp);
+    HIPCHK(c, hipStreamEndCapture(c->stream, &g));
+    hipError_t e = hipGraphInstantiate(&c->tail_exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+      c->tail_exec = nullptr;
+      return set_err(c, LGBM_HIP_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    }
+  }
+  HIPCHK(c, hipGraphLaunch(c->tail_exec, c->stream));
+  return LGBM_HIP_OK;
+}
+
 // After the enqueued rounds: rounds commit at least one split each once the first
-// leaf is picked, so a tree needs at most num_leaves + 1 plans.  Runs further rounds
-// (checked after every chunk) until the plan reports the tree complete, then the
-// finalize kernel.
+// leaf is picked, so a tree needs at most num_leaves + 1 plans.  Runs the tail
+// (checked after each) until the plan reports the tree complete, then the finalize
+// kernel.
 int finish_rounds(lgbm_hip_ctx* c, int32_t num_leaves, int32_t rounds, int32_t fp) {
   static_assert(offsetof(Ctl, rounds) - offsetof(Ctl, done) < 64, "ctl readback window");
   const size_t r_off = (offsetof(Ctl, rounds) - offsetof(Ctl, done)) / 4;
@@ -699,19 +763,15 @@ int finish_rounds(lgbm_hip_ctx* c, int32_t num_leaves, int32_t rounds, int32_t f
                              hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     if (c->done_host[0]) {
-      // Plans this tree ran; a longer captured sequence serves the next trees (later
-      // boosting iterations tend to need more rounds).
-      const int32_t used = c->done_host[r_off];
-      if (used > c->round_cap) c->round_cap = std::min(num_leaves + 1, used + 2);
+      update_round_cap(c, c->done_host[r_off], num_leaves);
       break;
     }
     if (done_rounds > num_leaves + 2)
       return set_err(c, LGBM_HIP_ERR_RUNTIME, "tree driver did not complete");
-    const int32_t chunk = 4;
-    enqueue_rounds(c, chunk, fp);
-    HIPCHK(c, hipGetLastError());
-    done_rounds += chunk;
-    c->extra_rounds += chunk;
+    int rc = launch_tail(c, fp);
+    if (rc) return rc;
+    done_rounds += lgbm_hip_ctx::TAIL_ROUNDS;
+    c->extra_rounds += lgbm_hip_ctx::TAIL_ROUNDS;
   }
   DevLearner L = make_learner(c);
   KernelEvents ke;
@@ -742,31 +802,44 @@ int grow_tree_async(lgbm_hip_ctx* c, const lgbm_gain_config* cfg, int32_t num_le
     HIPCHK(c, hipGetLastError());
     return finish_rounds(c, num_leaves, rounds, fp);
   }
-  if (!(c->graph_exec && c->graph_nl == num_leaves && c->graph_md == max_depth &&
-        c->graph_gen == c->buf_gen && c->graph_rounds == rounds && c->graph_spec == c->spec_max &&
-        c->graph_fp == fp)) {
-    if (c->graph_exec) {
-      (void)hipGraphExecDestroy(c->graph_exec);
-      c->graph_exec = nullptr;
+  if (!(c->graph_nl == num_leaves && c->graph_md == max_depth && c->graph_gen == c->buf_gen &&
+        c->graph_spec == c->spec_max && c->graph_fp == fp)) {
+    drop_graphs(c);  // another tree shape: every cached sequence is stale
+    c->graph_nl = num_leaves;
+    c->graph_md = max_depth;
+    c->graph_gen = c->buf_gen;
+    c->graph_spec = c->spec_max;
+    c->graph_fp = fp;
+  }
+  constexpr int GC = lgbm_hip_ctx::GRAPH_CACHE;
+  int slot = -1;
+  for (int i = 0; i < GC; ++i)
+    if (c->graph_exec[i] && c->graph_rounds[i] == rounds) slot = i;
+  if (slot < 0) {
+    slot = 0;  // a free entry, else the least recently used
+    for (int i = 0; i < GC; ++i) {
+      if (!c->graph_exec[i]) {
+        slot = i;
+        break;
+      }
+      if (c->graph_used[i] < c->graph_used[slot]) slot = i;
     }
+    if (c->graph_exec[slot]) (void)hipGraphExecDestroy(c->graph_exec[slot]);
+    c->graph_exec[slot] = nullptr;
     hipGraph_t g = nullptr;
     HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
     enqueue_tree(c, num_leaves, max_depth, rounds, fp);
     HIPCHK(c, hipStreamEndCapture(c->stream, &g));
-    hipError_t e = hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0);
+    hipError_t e = hipGraphInstantiate(&c->graph_exec[slot], g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) {
-      c->graph_exec = nullptr;
+      c->graph_exec[slot] = nullptr;
       return set_err(c, LGBM_HIP_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
     }
-    c->graph_nl = num_leaves;
-    c->graph_md = max_depth;
-    c->graph_gen = c->buf_gen;
-    c->graph_rounds = rounds;
-    c->graph_spec = c->spec_max;
-    c->graph_fp = fp;
+    c->graph_rounds[slot] = rounds;
   }
-  HIPCHK(c, hipGraphLaunch(c->graph_exec, c->stream));
+  c->graph_used[slot] = ++c->graph_clock;
+  HIPCHK(c, hipGraphLaunch(c->graph_exec[slot], c->stream));
   return finish_rounds(c, num_leaves, rounds, fp);
 }
 
@@ -942,10 +1015,7 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   c->colsamp_on = false;
   c->have_rank = false;
   c->buf_gen++;
-  if (c->graph_exec) {
-    (void)hipGraphExecDestroy(c->graph_exec);
-    c->graph_exec = nullptr;
-  }
+  drop_graphs(c);
   if (F > WIDE_MAX_F)
     return set_err(c, LGBM_HIP_ERR_CAPABILITY,
                    "more than " + std::to_string(WIDE_MAX_F) + " features");
@@ -1222,7 +1292,10 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   if (const char* e = std::getenv("LGBM_HIP_GRAPHS")) c->use_graphs = std::strcmp(e, "0") != 0;
   if (const char* e = std::getenv("LGBM_HIP_RECORDS"))
     c->records_env = std::strcmp(e, "legacy") == 0 ? 1 : std::strcmp(e, "wide") == 0 ? 2 : 0;
-  if (const char* e = std::getenv("LGBM_HIP_ROUNDS")) c->round_cap = std::max(1, std::atoi(e));
+  if (const char* e = std::getenv("LGBM_HIP_ROUNDS")) {
+    c->round_cap = std::max(1, std::atoi(e));
+    c->round_fixed = true;
+  }
   if (const char* e = std::getenv("LGBM_HIP_SPEC"))
     c->spec_max = std::max(1, std::min(SPEC_MAX, std::atoi(e)));
   *out = c;
@@ -1233,7 +1306,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   if (!c) return LGBM_HIP_OK;
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
-  if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+  drop_graphs(c);
   auto F = [](void* p) {
     if (p) (void)hipFree(p);
   };
