@@ -20,7 +20,11 @@
 #define HIST_MIN_ROWS 4096              // rows per chunk (at least)
 #define HIST_WAVE_CELLS 1792            // wave-private scheme: 28 cells per lane
 #define HIST_FOLD_STEPS 7               // 7 x 64 rows <= 511 per 11-bit field
-#define HIST_ROWS_PER_LANE 2            // rows per lane in flight per step
+#ifndef HIST_ROWS_PER_LANE
+#define HIST_ROWS_PER_LANE 1            // rows per lane in flight per step (1: 114 us root
+                                        // build, 2: 117, 3: 138, 4: 156; 16 waves a CU
+                                        // hide the loads, fewer folds pay)
+#endif
 #define HIST_BLOCK_MAX_ROWS ((1 << 19) - 1)  // block-shared scheme field limit
 #define HIST_FP_CELLS 3584              // f32 gradients: cells per feature group (16 B each)
 #define MAX_FGROUPS 32
