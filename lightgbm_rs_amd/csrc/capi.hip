@@ -278,6 +278,7 @@ struct lgbm_hip_ctx {
   bool use_graphs = true;
   // timing
   bool timing = false;
+  uint64_t hold_ticks = 0;  // the timing pass's device wait ahead of each kernel sequence
   std::vector<EventPair> ev_pool;
   size_t ev_used = 0;
   // Per-tree event list: every timed kernel gets a (start, stop) pair bound to its own
@@ -639,6 +640,14 @@ void ev_collect(lgbm_hip_ctx* c) {
   }
   c->chain_used = 0;
 }
+// Timing pass: the host launches a timed kernel (and its two events) more slowly than
+// a small round runs, so a device that has caught up with the host would stamp a start
+// event while the kernel is not yet submitted.  A bounded device-side wait ahead of each
+// kernel sequence lets the host enqueue the whole sequence first; the events then span
+// each kernel's own execution.
+void timing_hold(lgbm_hip_ctx* c) {
+  if (c->timing) launch_hold(c->hold_ticks, c->stream);
+}
 enum { FAM_HIST = 0, FAM_PART = 1, FAM_SCAN = 2, FAM_QUANT = 3, FAM_OBJ = 4, FAM_BIN = 5,
        FAM_PRED = 6 };
 
@@ -730,6 +739,7 @@ void update_round_cap(lgbm_hip_ctx* c, int32_t used, int32_t num_leaves) {
 int launch_tail(lgbm_hip_ctx* c, int32_t fp) {
   constexpr int32_t T = lgbm_hip_ctx::TAIL_ROUNDS;
   if (c->timing || !c->use_graphs) {
+    timing_hold(c);
     enqueue_rounds(c, T, fp);
     HIPCHK(c, hipGetLastError());
     return LGBM_HIP_OK;
@@ -2551,6 +2561,7 @@ int train_iter_single(lgbm_hip_ctx* c, int32_t objective, int32_t iter, const lg
   const bool pro = c->ahead && c->ahead_iter == iter && c->ahead_qbins == num_grad_quant_bins &&
                    c->ahead_stoch == stochastic && c->ahead_obj == objective;
   c->ahead = false;
+  timing_hold(c);
   if (!pro) enqueue_objective(c, objective, iter, num_grad_quant_bins, stochastic);
   if ((rc = grow_tree_async(c, cfg, num_leaves, max_depth, fp))) return rc;
   if (num_grad_quant_bins > 0 && c->renew_leaf &&
@@ -2837,6 +2848,7 @@ int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gai
   const int64_t N = c->N;
   // factor = K / (K - 1) (multiclass.rs:84)
   const double factor = (double)K / ((double)K - 1.0);
+  timing_hold(c);
   ev_begin(c, FAM_OBJ);
   launch_grad_softmax(c->score, c->label, c->gk, c->hk, N, K, factor, c->stream);
   ev_end(c);
@@ -2850,6 +2862,7 @@ int lgbm_hip_train_iter_multiclass(lgbm_hip_ctx* c, int32_t iter, const lgbm_gai
     }
     const float* gk = c->gk + (size_t)k * N;
     const float* hk = c->hk + (size_t)k * N;
+    if (k > 0) timing_hold(c);
     DevLearner L0 = make_learner(c);
     if (num_grad_quant_bins == 0) {
       ev_begin(c, FAM_QUANT);
@@ -2972,6 +2985,11 @@ int lgbm_hip_set_timing(lgbm_hip_ctx* c, int32_t enable) {
   HIPCHK(c, hipStreamSynchronize(c->stream));
   ev_collect(c);
   c->timing = enable != 0;
+  if (c->timing && !c->hold_ticks) {
+    int khz = 0;
+    HIPCHK(c, hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, c->device));
+    c->hold_ticks = (uint64_t)std::max(khz, 1) * 10;  // 10 ms
+  }
   for (double& m : c->ms) m = 0.0;
   HIPCHK(c, hipMemset(c->stats, 0, 64));
   c->tree_rounds = c->trees = c->extra_rounds = c->part_launches = 0.0;

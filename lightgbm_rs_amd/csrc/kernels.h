@@ -246,6 +246,8 @@ void launch_fp_prep(const DevLearner& L, const float* g, const float* h, int64_t
 // through the fixed-point path with the exact scales of the quantizer's header
 void launch_exact_prep(const DevLearner& L, const float* dg, const float* dh, int64_t n,
                        hipStream_t s);
+// timing pass: a device-side wait of `ticks` wall-clock ticks ahead of a kernel sequence
+void launch_hold(uint64_t ticks, hipStream_t s);
 void launch_tree_init(const DevLearner& L, int32_t max_leaves, int32_t max_depth,
                       int32_t slot_cap, int32_t spec_max, int32_t fp_mode, hipStream_t s,
                       const KernelEvents* ev = nullptr);

@@ -1018,6 +1018,15 @@ __global__ void k_pack_partition(const uint32_t* __restrict__ bins, int64_t n,
   if (i < n) rec[i] = make_uint4(bins[i] & 0xffu, 0u, 0u, (uint32_t)i);
 }
 
+// Timing pass only: one wave that waits `ticks` of the constant-rate wall clock (a
+// second bound, 2^20 sleeps of ~3 us, ends it whatever the clock reads), so that the
+// host has enqueued the whole kernel sequence behind it before the device starts it.
+__global__ void k_hold(uint64_t ticks) {
+  const uint64_t t0 = wall_clock64();
+  for (uint32_t i = 0; i < (1u << 20) && wall_clock64() - t0 < ticks; ++i)
+    __builtin_amdgcn_s_sleep(127);
+}
+
 // ===========================================================================
 // launchers
 // ===========================================================================
@@ -1155,6 +1164,10 @@ void launch_pack_partition(const uint32_t* bins, int64_t n, uint4* rec, hipStrea
   const int64_t blocks = (n + 255) / 256;
   if (blocks < 1) return;
   k_pack_partition<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(bins, n, rec);
+}
+
+void launch_hold(uint64_t ticks, hipStream_t s) {
+  k_hold<<<dim3(1), dim3(64), 0, s>>>(ticks);
 }
 
 }  // namespace lgbm

@@ -34,7 +34,9 @@
 #define WIDE_GF_Q 64
 #define WIDE_GF_F 32
 #define WIDE_THREADS 1024
+#ifndef WIDE_GRID
 #define WIDE_GRID 1024                  // row-chunk blocks over all groups (at least)
+#endif
 #define WIDE_MIN_ROWS 4096              // rows per chunk (at least): a flush costs a group
 #define WIDE_MAX_ROWS ((1 << 19) - 1)   // packed LDS cell field limit (quantized)
 #define WIDE_MAX_F 4096
