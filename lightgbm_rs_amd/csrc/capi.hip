@@ -155,6 +155,7 @@ struct lgbm_hip_ctx {
   int32_t F = 0, fmt = 1, total_cells = 0;  // fmt: row record format (lgbm_device.h)
   int32_t records_env = 0;  // LGBM_HIP_RECORDS: 0 automatic, 1 legacy (8-bit records), 2 wide
   int32_t max_bins = 0;     // the widest feature's num_bin
+  int32_t has_cat = 0;      // some feature is categorical
   bool bin16 = false;       // wide layout with 2-byte bins
   int32_t n_wgroups = 0;    // 2-byte bins: feature groups of the histogram kernel
   int32_t* d_wgroups = nullptr;  // [n_wgroups + 1] first feature of each group
@@ -406,6 +407,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.binmat = c->binmat;
   L.row_stride = c->row_stride;
   L.max_bins = c->max_bins;
+  L.has_cat = c->has_cat;
   L.bin16 = c->bin16 ? 1 : 0;
   L.n_wgroups = c->n_wgroups;
   L.wgroups = c->d_wgroups;
@@ -1082,6 +1084,9 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   c->F = F;
   c->N = num_data;
   c->max_bins = (int32_t)max_nb;
+  c->has_cat = 0;
+  for (int f = 0; f < F; ++f)
+    if (meta[f].bin_type == LGBM_BIN_CATEGORICAL) c->has_cat = 1;
   c->bin16 = bin16;
   c->fmt = (F + 4 + 15) / 16;
   if (wide) {

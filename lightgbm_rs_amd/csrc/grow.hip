@@ -1102,7 +1102,13 @@ __global__ __launch_bounds__(1024) void k_tile_scan(DevLearner L) {
 //   (before_find_best_split, learner.rs:1808-1839: max_depth reached, or both below
 //   2 * min_data_in_leaf rows) are not built or scanned.
 // ===========================================================================
-__global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_t part_grid) {
+// CAT: the dataset has categorical features (the categorical scan's LDS rows are
+// allocated only then: without them more blocks fit a CU).  A round of the wide layout
+// runs F x jobs blocks of ~15-20 us each, more than the chip holds at once, so blocks a
+// CU can hold set its time: six waves a SIMD (at most 80 VGPRs) and 12.5 KB of LDS at
+// 256 bins give 12 blocks a CU where 89 VGPRs and the categorical rows gave 8.
+template <bool CAT>
+__global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int32_t part_grid) {
   static_assert(SCAN_THREADS == 128, "two bins and four f64 cells per thread cover 256 bins");
   // the smaller child's and the larger child's f64 cells, sized for the widest feature
   extern __shared__ __align__(16) double scan_lds[];
@@ -1350,11 +1356,14 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_pair_scan(DevLearner L, int32_
       L.splittable[(size_t)leaf * F + f] = 0;
     }
   } else {
-    const double gain =
-        ft.categorical  // bin_type dispatch (learner.rs:3103-3118)
-            ? wave_scan_cat(wv == 0 ? cs : cp, ft, sc, ctl->cfg, ls.sg, ls.sh, ls.n, ls.weight,
-                            out, L.cat_bits + ((size_t)leaf * F + f) * 8)
-            : wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
+    double gain;
+    if constexpr (CAT)
+      gain = ft.categorical  // bin_type dispatch (learner.rs:3103-3118)
+                 ? wave_scan_cat(wv == 0 ? cs : cp, ft, sc, ctl->cfg, ls.sg, ls.sh, ls.n,
+                                 ls.weight, out, L.cat_bits + ((size_t)leaf * F + f) * 8)
+                 : wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
+    else
+      gain = wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
     if (lane_id() == 0) {
       // splittability from the raw scan, then feature_contri scales the gain the
       // ArgMax compares (learner.rs:3235-3252)
@@ -1586,7 +1595,11 @@ void launch_partition_stable(const DevLearner& L, int64_t ntiles, int64_t blocks
 // Lets the scans take LDS rows for the widest feature (2-byte bins: 4096 bins, 128 KiB
 // for k_pair_scan's two children); called outside graph capture.
 int scan_prepare() {
-  if (hipFuncSetAttribute((const void*)k_pair_scan, hipFuncAttributeMaxDynamicSharedMemorySize,
+  if (hipFuncSetAttribute((const void*)k_pair_scan<false>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          4 * WIDE_MAX_BIN * (int)sizeof(double)) != hipSuccess ||
+      hipFuncSetAttribute((const void*)k_pair_scan<true>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
                           4 * WIDE_MAX_BIN * (int)sizeof(double)) != hipSuccess)
     return 1;
   return 0;
@@ -1595,8 +1608,12 @@ int scan_prepare() {
 void launch_pair_scan(const DevLearner& L, int32_t spec_max, int32_t part_grid, hipStream_t s,
                       const KernelEvents* ev) {
   const size_t lds = (size_t)4 * std::max(L.max_bins, 1) * sizeof(double);
-  KLAUNCH(ev, k_pair_scan, dim3((unsigned)L.F, (unsigned)spec_max), dim3(SCAN_THREADS), lds, s, L,
-          part_grid);
+  if (L.has_cat)
+    KLAUNCH(ev, k_pair_scan<true>, dim3((unsigned)L.F, (unsigned)spec_max), dim3(SCAN_THREADS),
+            lds, s, L, part_grid);
+  else
+    KLAUNCH(ev, k_pair_scan<false>, dim3((unsigned)L.F, (unsigned)spec_max), dim3(SCAN_THREADS),
+            lds, s, L, part_grid);
 }
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
   KLAUNCH(ev, k_tree_finalize, dim3(1), dim3(256), 0, s, L);

@@ -109,6 +109,7 @@ struct DevLearner {
   int32_t F;
   int32_t total_cells;
   int32_t max_bins;           // the widest feature's num_bin (scan LDS rows)
+  int32_t has_cat;            // some feature is categorical (the scans' categorical path)
   int32_t bin16;              // wide layout: 2-byte bins (a feature has more than 256)
   int32_t n_wgroups;          // 2-byte bins: feature groups of k_hist_wide
   const int32_t* wgroups;     // [n_wgroups + 1] their first features
