@@ -221,6 +221,7 @@ struct lgbm_hip_ctx {
   int32_t lcap = 0;
   double* slots = nullptr;
   lgbm_split_info *feat_split = nullptr, *best = nullptr;
+  double* gain_dense = nullptr;  // [slot_cap][F] feat_split's gains, contiguous
   int32_t* best_fpos = nullptr;
   int32_t* int_slots = nullptr;
   uint8_t* splittable = nullptr;
@@ -419,6 +420,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   for (int i = 0; i <= MAX_FGROUPS; ++i) L.fgroup_first[i] = c->fgroup_first[i];
   L.slots = c->slots;
   L.feat_split = c->feat_split;
+  L.gain_dense = c->gain_dense;
   L.best = c->best;
   L.best_fpos = c->best_fpos;
   L.int_slots = c->int_slots;
@@ -502,6 +504,7 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   const size_t P = (size_t)SLOT_CAP(L);  // node slots
   if ((rc = dalloc(c, &c->slots, P * c->slot_len))) return rc;
   if ((rc = dalloc(c, &c->feat_split, P * F))) return rc;
+  if ((rc = dalloc(c, &c->gain_dense, P * F))) return rc;
   if ((rc = dalloc(c, &c->best, P))) return rc;
   if ((rc = dalloc(c, &c->splittable, P * F))) return rc;
   if ((rc = dalloc(c, &c->cat_bits, P * F * 8))) return rc;
@@ -1370,6 +1373,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   if (c->tree_host) (void)hipHostFree(c->tree_host);
   F(c->slots);
   F(c->feat_split);
+  F(c->gain_dense);
   F(c->best);
   F(c->splittable);
   F(c->plan_state);

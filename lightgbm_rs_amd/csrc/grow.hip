@@ -242,7 +242,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   static_assert(PLAN_WAVES <= 2 * SPEC_MAX + 2, "reduce_list covers a slot per wave");
   const bool red0 = wave < nred;
   const int32_t s_w = ctl->reduce_list[wave];
-  const double g_w = (red0 && lane < F) ? L.feat_split[(size_t)s_w * F + lane].gain : ninf;
+  const double g_w = (red0 && lane < F) ? L.gain_dense[(size_t)s_w * F + lane] : ninf;
   if (tid == 0) {
     s_nS = 0;
     s_ncand = 0;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
 #pragma unroll
       for (int u = 0; u < KU; ++u) {
         const int f = f0 + u * LGBM_WAVE;
-        gv[u] = f < F ? ((i == wave && f == lane) ? g_w : L.feat_split[(size_t)s * F + f].gain) : ninf;
+        gv[u] = f < F ? ((i == wave && f == lane) ? g_w : L.gain_dense[(size_t)s * F + f]) : ninf;
         rv[u] = f < F ? fts[f].real_index : -1;
       }
 #pragma unroll
@@ -1167,6 +1167,7 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
       const int32_t leaf = tid == 0 ? sm : lg;
       const LeafSums ls = (tid == 0) == right_small ? scr : scl;
       split_set_none(&L.feat_split[(size_t)leaf * F + f]);
+      L.gain_dense[(size_t)leaf * F + f] = -__builtin_inf();
       if (ls.sh > 0.0 && ls.n > 0) L.splittable[(size_t)leaf * F + f] = 0;
     }
     return;
@@ -1319,6 +1320,8 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
     if (tid == 0) {
       split_set_none(&L.feat_split[(size_t)cl * F + f]);
       split_set_none(&L.feat_split[(size_t)cr * F + f]);
+      L.gain_dense[(size_t)cl * F + f] = -__builtin_inf();
+      L.gain_dense[(size_t)cr * F + f] = -__builtin_inf();
     }
     return;
   }
@@ -1348,11 +1351,16 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
   const int32_t leaf = wv == 0 ? sm : lg;
   const LeafSums ls = wv == 0 ? ss : gs;
   lgbm_split_info* out = L.feat_split + (size_t)leaf * F + f;
+  double* out_gain = L.gain_dense + (size_t)leaf * F + f;
   if (!(ls.sh > 0.0 && ls.n > 0)) {
-    if (lane_id() == 0) split_set_none(out);
+    if (lane_id() == 0) {
+      split_set_none(out);
+      *out_gain = -__builtin_inf();
+    }
   } else if (pgate) {
     if (lane_id() == 0) {
       split_set_none(out);
+      *out_gain = -__builtin_inf();
       L.splittable[(size_t)leaf * F + f] = 0;
     }
   } else {
@@ -1369,6 +1377,7 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
       // ArgMax compares (learner.rs:3235-3252)
       L.splittable[(size_t)leaf * F + f] = gain > -__builtin_inf() ? 1 : 0;
       out->gain = gain * ft.penalty;
+      *out_gain = gain * ft.penalty;
     }
   }
 }

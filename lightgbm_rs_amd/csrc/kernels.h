@@ -135,6 +135,7 @@ struct DevLearner {
   int32_t* int_slots;         // [slot_cap][total_cells][3] per-node integer histograms
   double* slots;              // [slot_cap][slot_len] per-node f64 histograms
   lgbm_split_info* feat_split;  // [slot_cap][F]
+  double* gain_dense;           // [slot_cap][F] the same gains, contiguous (the plan's ArgMax)
   lgbm_split_info* best;        // [slot_cap]
   int32_t* best_fpos;           // [slot_cap] feature position of best
   uint8_t* splittable;          // [slot_cap][F]

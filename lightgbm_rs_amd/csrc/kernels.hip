@@ -878,6 +878,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
   if (ctl->root_skip || !(sh > 0.0 && nrows > 0) || sampled_out) {
     if (lane_id() == 0) {
       split_set_none(out);
+      L.gain_dense[f] = -__builtin_inf();
       L.splittable[f] = 0;
     }
     return;
@@ -891,6 +892,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
   if (lane_id() == 0) {
     L.splittable[f] = gain > -__builtin_inf() ? 1 : 0;
     out->gain = gain * ft.penalty;  // feature_contri (learner.rs:3235-3252)
+    L.gain_dense[f] = gain * ft.penalty;
   }
 }
 
