@@ -73,11 +73,14 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
   if (nj <= 0) return;
   const int tid = threadIdx.x, wave = tid >> 6;
   const int F = L.F, cells = L.total_cells;
-  const int f0 = B16 ? L.wgroups[blockIdx.y] : (int)blockIdx.y * GF;
+  // grid (feature group, row chunk): chunk-major launch order, so the chunks a round
+  // uses (the first ones of every group) start before the idle tail
+  const int grp = (int)blockIdx.x;
+  const int f0 = B16 ? L.wgroups[grp] : grp * GF;
   if (f0 >= F) return;
-  if (wave == 0) wide_assign(ctl, nj, s_a0, s_nb, &s_R, (int64_t)gridDim.x - SPEC_MAX, (int)lane_id());
+  if (wave == 0) wide_assign(ctl, nj, s_a0, s_nb, &s_R, (int64_t)gridDim.y - SPEC_MAX, (int)lane_id());
   __syncthreads();
-  const int32_t a = (int32_t)blockIdx.x;
+  const int32_t a = (int32_t)blockIdx.y;
   int32_t j = -1;
   for (int k = 0; k < nj; ++k)
     if (a >= s_a0[k] && a < s_a0[k] + s_nb[k]) j = k;
@@ -87,7 +90,7 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
       ctl->hjobs[k].nblk = s_nb[k];
     }
   if (j < 0) return;
-  const int f1 = B16 ? L.wgroups[blockIdx.y + 1] : min(f0 + GF, F);
+  const int f1 = B16 ? L.wgroups[grp + 1] : min(f0 + GF, F);
   const int gbase = (int)L.feats[f0].cell_base;
   const int gcells = (f1 < F ? (int)L.feats[f1].cell_base : cells) - gbase;
   for (int k = tid; k < GF; k += WIDE_THREADS) {
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
   const uint8_t* __restrict__ bm = L.binmat + (B16 ? 2 : 1) * f0;
   const int nfeat = f1 - f0;
   const int64_t stride = L.row_stride;
-  const bool totals = (J._pad & 1) != 0 && blockIdx.y == 0;
+  const bool totals = (J._pad & 1) != 0 && grp == 0;
   const uint16_t* __restrict__ ghq = L.bufs.gh[0];
   const float2* __restrict__ gh32 = L.bufs.g32[0];
   if constexpr (FP)
@@ -339,7 +342,7 @@ int wide_prepare() {
 
 void launch_hist_wide(const DevLearner& L, int fp, hipStream_t s, const KernelEvents* ev) {
   const int ng = wide_groups(L.F, fp, L.bin16 ? L.n_wgroups : 0);
-  const dim3 g((unsigned)wide_grid_x(ng, L.N), (unsigned)ng), blk(WIDE_THREADS);
+  const dim3 g((unsigned)ng, (unsigned)wide_grid_x(ng, L.N)), blk(WIDE_THREADS);
   if (L.bin16) {
     if (fp)
       KLAUNCH(ev, (k_hist_wide<1, true>), g, blk, wide_lds_bytes(1), s, L);
