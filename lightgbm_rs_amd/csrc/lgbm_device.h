@@ -31,9 +31,15 @@
 // wide layout (REC_FMT_WIDE): ConstructHistogram per (row chunk, feature group); a
 // group is WIDE_GF_Q (quantized, 8-byte LDS cells) or WIDE_GF_F (f32, two 8-byte
 // cells) consecutive features, at most 256 bins each: 128 KiB of LDS either way
+#ifndef WIDE_GF_Q
 #define WIDE_GF_Q 64
+#endif
+#ifndef WIDE_GF_F
 #define WIDE_GF_F 32
+#endif
+#ifndef WIDE_THREADS
 #define WIDE_THREADS 1024
+#endif
 #ifndef WIDE_GRID
 #define WIDE_GRID 1024                  // row-chunk blocks over all groups (at least)
 #endif

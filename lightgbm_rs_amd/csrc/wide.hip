@@ -304,8 +304,10 @@ void launch_pack_wide16(const uint16_t* bins, int64_t n, int32_t F, int64_t stri
                                                             (uint32_t*)rec);
 }
 
-size_t wide_lds_bytes(int fp) {  // the same for both bin widths
-  return (size_t)(fp ? WIDE_GF_F * 256 * 16 : WIDE_GF_Q * 256 * 8);
+// LDS of a block: its group's cells, 8 bytes each (quantized) or 16 (f32 gradients)
+size_t wide_lds_bytes(int fp, bool b16) {
+  const size_t cells = b16 ? (size_t)WIDE16_GROUP_CELLS : (size_t)(fp ? WIDE_GF_F : WIDE_GF_Q) * 256;
+  return cells * (fp ? 16 : 8);
 }
 
 // Feature groups of a launch: fixed 1-byte groups, or the host's 2-byte-bin table.
@@ -335,7 +337,7 @@ int wide_prepare() {
                       (const void*)k_hist_wide<0, true>, (const void*)k_hist_wide<1, true>};
   for (int i = 0; i < 4; ++i)
     if (hipFuncSetAttribute(k[i], hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)wide_lds_bytes(i & 1)) != hipSuccess)
+                            (int)wide_lds_bytes(i & 1, i >= 2)) != hipSuccess)
       return 1;
   return 0;
 }
@@ -345,13 +347,13 @@ void launch_hist_wide(const DevLearner& L, int fp, hipStream_t s, const KernelEv
   const dim3 g((unsigned)ng, (unsigned)wide_grid_x(ng, L.N)), blk(WIDE_THREADS);
   if (L.bin16) {
     if (fp)
-      KLAUNCH(ev, (k_hist_wide<1, true>), g, blk, wide_lds_bytes(1), s, L);
+      KLAUNCH(ev, (k_hist_wide<1, true>), g, blk, wide_lds_bytes(1, true), s, L);
     else
-      KLAUNCH(ev, (k_hist_wide<0, true>), g, blk, wide_lds_bytes(0), s, L);
+      KLAUNCH(ev, (k_hist_wide<0, true>), g, blk, wide_lds_bytes(0, true), s, L);
   } else if (fp) {
-    KLAUNCH(ev, (k_hist_wide<1, false>), g, blk, wide_lds_bytes(1), s, L);
+    KLAUNCH(ev, (k_hist_wide<1, false>), g, blk, wide_lds_bytes(1, false), s, L);
   } else {
-    KLAUNCH(ev, (k_hist_wide<0, false>), g, blk, wide_lds_bytes(0), s, L);
+    KLAUNCH(ev, (k_hist_wide<0, false>), g, blk, wide_lds_bytes(0, false), s, L);
   }
 }
 
