@@ -156,6 +156,10 @@ struct DevLearner {
 #define LAMBDARANK_THREADS 128
 #define RANK_SIGMOID_BINS (1024 * 1024)
 #define RANK_MAX_QUERY 2048
+#ifndef RANK_BATCH
+#define RANK_BATCH 4                   // rows of the lambdarank loop per batch (2-5 measured alike, 8 and 16 slower)
+#endif
+#define RANK_LDS_BUDGET (150 * 1024)   // the lambdarank block's LDS at most
 #define RANK_DISCOUNTS 10000
 struct RankParams {
   double sigmoid, min_in, max_in, idx_factor;
