@@ -209,6 +209,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   __shared__ int2 s_child[SLOT_CAP(MAX_LEAVES)];
   __shared__ int32_t s_ps[5][MAX_LEAVES];  // PS_* linkage
   __shared__ DevFeature s_ft[16 * LGBM_MAX_W];  // the record layouts' features (wide: global)
+  __shared__ int32_t s_ri[WIDE_MAX_F];     // per feature position: its real index (ArgMax ties)
   __shared__ int4 s_commit[MAX_LEAVES];    // (leaf, node slot, node, new right leaf)
   __shared__ int2 s_lc[MAX_LEAVES];        // per leaf: speculated children slots
   __shared__ double2 s_lcg[MAX_LEAVES];    //   and their keys
@@ -254,6 +255,11 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   const DevFeature* __restrict__ fts = ft_lds ? s_ft : L.feats;
   if (ft_lds)
     for (int f = tid; f < F; f += PLAN_THREADS) s_ft[f] = L.feats[f];
+  // wide layouts: the tie-break indices of every feature, once; the per-slot ArgMax
+  // below reads them for every slot, which from global memory is a cache line per
+  // feature and slot
+  if (!ft_lds)
+    for (int f = tid; f < F; f += PLAN_THREADS) s_ri[f] = L.feats[f].real_index;
   for (int s = tid; s < slot_cap; s += PLAN_THREADS) {
     s_gain[s] = nd.key_gain[s];
     s_feat[s] = nd.key_feat[s];
@@ -278,7 +284,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
       for (int u = 0; u < KU; ++u) {
         const int f = f0 + u * LGBM_WAVE;
         gv[u] = f < F ? ((i == wave && f == lane) ? g_w : L.gain_dense[(size_t)s * F + f]) : ninf;
-        rv[u] = f < F ? fts[f].real_index : -1;
+        rv[u] = f < F ? (ft_lds ? fts[f].real_index : s_ri[f]) : -1;
       }
 #pragma unroll
       for (int u = 0; u < KU; ++u) {
