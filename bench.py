@@ -126,7 +126,13 @@ def compare_iterations(trees, scores, otrees, oscores, init):
                 bad.append(f"tree {i} {k}")
     same_scores = bool(np.ascontiguousarray(scores).tobytes() ==
                        np.ascontiguousarray(oscores).tobytes())
+    # the tree structure (what splits where, and the partition counts)
+    structural = ("num_leaves", "split_feature", "threshold_in_bin", "threshold",
+                  "decision_type", "left_child", "right_child", "leaf_count",
+                  "internal_count", "leaf_depth", "leaf_parent", "cat_boundaries",
+                  "cat_threshold", "num_cat")
     return {"iterations": len(trees), "trees_bit_exact": not bad, "mismatches": bad[:8],
+            "structure_equal": not any(m.split()[-1] in structural for m in bad),
             "scores_bit_exact": same_scores,
             "leaves": [int(t["num_leaves"]) for t in trees]}
 
@@ -230,6 +236,9 @@ def secondary(args):
         if not qbins:  # f32 gradients: fixed-point cells vs the f64 fold (stated bar 1e-5)
             parity["scores_max_rel_diff"] = float(
                 np.max(np.abs(gpu_scores - oscores) / np.maximum(np.abs(oscores), 1e-300)))
+            # the tree structure must match exactly; the f64 values within the bar
+            parity["within_1e-5"] = bool(parity["structure_equal"] and
+                                         parity["scores_max_rel_diff"] <= 1e-5)
         log(f"parity: {parity}")
     print(json.dumps({
         "metric": f"sec per 100 trees, {args.workload} (wide row layout), 1 MI355X",
