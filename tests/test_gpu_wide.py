@@ -9,6 +9,9 @@ moving row indices) on the device against the oracle and against the record layo
     and the layout export (partition order) equal to DataPartition::split's;
   * configs[2]'s shape (2000 sparse LogNormal columns, 90% zeros, f32 gradients) and
     configs[4]'s shape (700 U(0,1) columns with 30% zeros, quantized) at reduced rows;
+  * configs[3]'s mix (numerical and categorical columns, softmax multiclass) forced
+    onto the wide layout: the categorical scan and the bitset routing of the 1-byte
+    wide layout, trees and scores bit-exact with the oracle;
   * device binning of a wide raw table (lgbm_hip_upload_raw) against the host mappers.
 The most frequent bin of every feature is never accumulated in this layout
 (FixHistogram rebuilds it, compaction drops it); these trees pin that it changes
@@ -20,7 +23,8 @@ import numpy as np
 import pytest
 
 from lightgbm_rs_amd import GainConfig, HipBackend
-from lightgbm_rs_amd.synth import config1_like, config2_binned, config4_binned, _bin_columns
+from lightgbm_rs_amd.synth import (config1_like, config2_binned, config3_binned,
+                                   config4_binned, _bin_columns)
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -210,3 +214,41 @@ def test_wide_device_binning_matches_mappers():
         finally:
             b.close()
         assert np.array_equal(got, bins), col_major
+
+
+def test_wide_forced_categorical_multiclass_matches_oracle():
+    n, K, nl, iters = 60_000, 10, 31, 2
+    bins, meta, vals, y, cat, _, _ = config3_binned(n, seed=0x5EED0063)
+    assert cat, "the data must hold categorical columns"
+    cfg = GainConfig.make(min_data_in_leaf=20)
+    prior = np.bincount(y.astype(np.int64), minlength=K) / n
+    init = np.log(np.maximum(prior, 1e-15))
+    applied = np.where(np.abs(init) > 1e-15, init, 0.0)
+    say(f"wide categorical multiclass n={n} K={K}")
+    b = backend("wide")
+    try:
+        b.upload_resident_bins(bins, meta, vals)
+        b.set_labels_multiclass(y, K, applied)
+        trees = []
+        for it in range(iters):
+            for k, t in enumerate(b.train_iter_multiclass(it, cfg, nl, -1, 0.1, 4, True, [1] * K)):
+                t = dict(t)
+                if it == 0 and abs(init[k]) > 1e-15:
+                    t["leaf_value"] = _mrz(t["leaf_value"] + init[k])
+                    t["internal_value"] = _mrz(t["internal_value"] + init[k])
+                trees.append(t)
+        scores = b.scores()
+    finally:
+        b.close()
+    oscores, otrees = oracle.train_multiclass(bins, meta, vals, y, K, cfg, nl, -1, iters, 0.1,
+                                              quantized=True, quant_bins=4, stochastic=True)
+    assert len(trees) == len(otrees) == K * iters
+    assert any(int(t["num_cat"]) > 0 for t in trees), "no categorical split was exercised"
+    for i, (t, o) in enumerate(zip(trees, otrees)):
+        assert t["num_leaves"] == o["num_leaves"], i
+        for k in o:
+            if k == "num_leaves":
+                continue
+            a, c = np.ascontiguousarray(t[k]), np.ascontiguousarray(o[k])
+            assert a.shape == c.shape and a.tobytes() == c.tobytes(), (i, k)
+    assert np.array_equal(bits(scores), bits(oscores))
