@@ -331,8 +331,8 @@ def main():
         return lds_probe(args)
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (--gpus {args.gpus} requested): this build "
-              "has no multi-GPU path; see DESIGN.md for how the path would shard.",
-              file=sys.stderr)
+              "has no multi-GPU path (rows would shard by range, one all-reduce of each "
+              "round's built integer histograms; not built).", file=sys.stderr)
         sys.exit(2)
     if args.workload != "config1":
         return secondary(args)
