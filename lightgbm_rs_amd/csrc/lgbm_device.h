@@ -43,7 +43,9 @@
 #ifndef WIDE_GRID
 #define WIDE_GRID 1024                  // row-chunk blocks over all groups (at least)
 #endif
+#ifndef WIDE_MIN_ROWS
 #define WIDE_MIN_ROWS 4096              // rows per chunk (at least): a flush costs a group
+#endif
 #define WIDE_MAX_ROWS ((1 << 19) - 1)   // packed LDS cell field limit (quantized)
 #define WIDE_MAX_F 4096
 #define WIDE_MAX_BIN 4096               // 2-byte bins (a feature of more than 256 bins)
