@@ -222,6 +222,8 @@ struct lgbm_hip_ctx {
   double* slots = nullptr;
   lgbm_split_info *feat_split = nullptr, *best = nullptr;
   double* gain_dense = nullptr;  // [slot_cap][F] feat_split's gains, contiguous
+  double2* mfbv = nullptr;       // [slot_cap][F] quantized: the fixed cell's f64 pair
+  int32_t* fmat = nullptr;       // [slot_cap] quantized: f64 cells held in `slots`
   int32_t* best_fpos = nullptr;
   int32_t* int_slots = nullptr;
   uint8_t* splittable = nullptr;
@@ -421,6 +423,8 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.slots = c->slots;
   L.feat_split = c->feat_split;
   L.gain_dense = c->gain_dense;
+  L.mfbv = c->mfbv;
+  L.fmat = c->fmat;
   L.best = c->best;
   L.best_fpos = c->best_fpos;
   L.int_slots = c->int_slots;
@@ -505,6 +509,8 @@ int ensure_leaves(lgbm_hip_ctx* c, int32_t L) {
   if ((rc = dalloc(c, &c->slots, P * c->slot_len))) return rc;
   if ((rc = dalloc(c, &c->feat_split, P * F))) return rc;
   if ((rc = dalloc(c, &c->gain_dense, P * F))) return rc;
+  if ((rc = dalloc(c, &c->mfbv, P * F))) return rc;
+  if ((rc = dalloc(c, &c->fmat, P))) return rc;
   if ((rc = dalloc(c, &c->best, P))) return rc;
   if ((rc = dalloc(c, &c->splittable, P * F))) return rc;
   if ((rc = dalloc(c, &c->cat_bits, P * F * 8))) return rc;
@@ -700,7 +706,7 @@ void enqueue_rounds(lgbm_hip_ctx* c, int32_t rounds, int32_t fp) {
       launch_hist_wide(L, fp, c->stream, ev_kernel(c, FAM_HIST, &ke));
     else if (fp)
       launch_hist_f32(L, c->stream, ev_kernel(c, FAM_HIST, &ke));
-    launch_pair_scan(L, c->spec_max, c->part_blocks, c->stream, ev_kernel(c, FAM_SCAN, &ke));
+    launch_pair_scan(L, fp, c->spec_max, c->part_blocks, c->stream, ev_kernel(c, FAM_SCAN, &ke));
   }
 }
 
@@ -1374,6 +1380,8 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->slots);
   F(c->feat_split);
   F(c->gain_dense);
+  F(c->mfbv);
+  F(c->fmat);
   F(c->best);
   F(c->splittable);
   F(c->plan_state);

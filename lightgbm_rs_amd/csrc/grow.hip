@@ -122,6 +122,7 @@ __global__ void k_tree_init(DevLearner L, int32_t max_leaves, int32_t max_depth,
     nd.sums[0] = LeafSums{0.0, 0.0, 0.0, N, 0};
     nd.key_gain[0] = -__builtin_inf();
     nd.key_feat[0] = -1;
+    L.fmat[0] = 0;
     split_set_none(&L.best[0]);
     L.best_fpos[0] = -1;
     L.plan_state[PS_LEAF_SLOT * MAX_LEAVES] = 0;
@@ -1113,7 +1114,8 @@ __global__ __launch_bounds__(1024) void k_tile_scan(DevLearner L) {
 // runs F x jobs blocks of ~15-20 us each, more than the chip holds at once, so blocks a
 // CU can hold set its time: six waves a SIMD (at most 80 VGPRs) and 12.5 KB of LDS at
 // 256 bins give 12 blocks a CU where 89 VGPRs and the categorical rows gave 8.
-template <bool CAT>
+// FP: f32 gradients (64-bit fixed-point cells, f64 cells kept in the node slots).
+template <bool CAT, bool FP>
 __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int32_t part_grid) {
   static_assert(SCAN_THREADS == 128, "two bins and four f64 cells per thread cover 256 bins");
   // the smaller child's and the larger child's f64 cells, sized for the widest feature
@@ -1135,7 +1137,7 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
   const DevFeature ft = L.feats[f];
   const int64_t T = ctl->tile_total;
   const int32_t md = ctl->max_depth, min2 = ctl->cfg.min_data_in_leaf * 2;
-  const int32_t fp_mode = ctl->fp_mode;
+  constexpr bool fp_mode = FP;
   const ScanCfg sc = make_scan_cfg(ctl->cfg);
   if (j >= n_jobs) return;  // only after the job's fields are known to be live
   const DevNodes& nd = L.nodes;
@@ -1153,15 +1155,32 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
   const int nb = (int)ft.num_bin;
   const size_t sl = L.slot_len;
   const double* s_par = L.slots + (size_t)p * sl + ft.slot_off;
-  double pv[4];  // the parent's f64 cells i = tid + 128 k
+  // Quantized gradients derive both children's f64 cells from their integer cells
+  // (fix_compact_pair); only a parent whose cells are materialised (pmat) is read.
+  constexpr bool derive = !FP;
+  const bool pmat = derive && L.fmat[p] != 0;
+  const double2 pm = derive ? L.mfbv[(size_t)p * F + f] : make_double2(0.0, 0.0);
+  double pv[4];  // f32 mode: the parent's f64 cells i = tid + 128 k
+  if constexpr (!derive) {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int i = tid + SCAN_THREADS * k;
-    pv[k] = i < 2 * nb ? s_par[i] : 0.0;
+    for (int k = 0; k < 4; ++k) {
+      const int i = tid + SCAN_THREADS * k;
+      pv[k] = i < 2 * nb ? s_par[i] : 0.0;
+    }
   }
   const bool gated = (md > 0 && dcl >= md) || (lcnt < min2 && rcnt < min2);
   const bool right_small = !(lcnt < rcnt);
   const int32_t sm = right_small ? cr : cl, lg = right_small ? cl : cr;
+  const LeafSums ss = right_small ? scr : scl, gs = right_small ? scl : scr;
+  // A smaller child without rows or hessian has its cells cleared, so the reference's
+  // larger child is the parent's cells (not its own integers): it is materialised, as
+  // is every larger child of a materialised parent.
+  const bool sm_zero = !(ss.sh > 0.0 && ss.n > 0);
+  const bool lg_mat = pmat || sm_zero;
+  if (derive && f == 0 && tid == 0) {
+    L.fmat[sm] = 0;
+    L.fmat[lg] = lg_mat ? 1 : 0;
+  }
   const double vg1 = (double)ctl->vg1, vh1 = (double)ctl->vh1, vh3 = (double)ctl->vh3;
   const bool wide = rec_wide(L.fmt);
   if (pgate && !gated && (fp_mode || wide)) {
@@ -1178,7 +1197,7 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
     }
     return;
   }
-  if (fp_mode) {
+  if constexpr (fp_mode) {
     // f32 gradients: the smaller child from its partial slots (k_hist_f32's, or the
     // wide layout's per-chunk ones); the larger = parent - smaller, exact in 64-bit
     // fixed point
@@ -1305,7 +1324,8 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
       }
       if (gated) continue;
       const int32_t* ps = L.int_slots + ((size_t)p * cells + ci) * 3;
-      const int32_t OG = ps[0] - AG, OH = ps[1] - AH, OT = ps[2] - AT;  // exact
+      const int32_t PG = ps[0], PH = ps[1], PT = ps[2];
+      const int32_t OG = PG - AG, OH = PH - AH, OT = PT - AT;  // exact
       int32_t* ls = L.int_slots + ((size_t)cl * cells + ci) * 3;
       int32_t* rs = L.int_slots + ((size_t)cr * cells + ci) * 3;
       const int32_t LG_ = acc_right ? OG : AG, LH = acc_right ? OH : AH, LT = acc_right ? OT : AT;
@@ -1320,6 +1340,15 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
         int_cell_to_f64(RG, RH, RT, vg1, vh1, vh3, &cs[2 * b], &cs[2 * b + 1]);
       else
         int_cell_to_f64(LG_, LH, LT, vg1, vh1, vh3, &cs[2 * b], &cs[2 * b + 1]);
+      if constexpr (derive) {
+        // the larger child's cells, or the parent's when the larger is materialised
+        if (lg_mat)
+          int_cell_to_f64(PG, PH, PT, vg1, vh1, vh3, &cp[2 * b], &cp[2 * b + 1]);
+        else if (right_small)
+          int_cell_to_f64(LG_, LH, LT, vg1, vh1, vh3, &cp[2 * b], &cp[2 * b + 1]);
+        else
+          int_cell_to_f64(RG, RH, RT, vg1, vh1, vh3, &cp[2 * b], &cp[2 * b + 1]);
+      }
     }
   }
   if (gated) {
@@ -1331,28 +1360,45 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
     }
     return;
   }
-  const LeafSums ss = right_small ? scr : scl, gs = right_small ? scl : scr;
-  fix_compact_block(ft, cs, ss.sg, ss.sh, pgate || !(ss.sh > 0.0 && ss.n > 0));
   double* s_sm = L.slots + (size_t)sm * sl + ft.slot_off;
   double* s_lg = L.slots + (size_t)lg * sl + ft.slot_off;
+  if constexpr (derive) {
+    fix_compact_pair(ft, cs, cp, ss.sg, ss.sh, pgate || sm_zero, pm, !lg_mat);
+    if (lg_mat) {
+      // larger = parent - smaller cell by cell, kept in the node's f64 slot
+      for (int i = tid; i < 2 * nb; i += SCAN_THREADS) {
+        const double d = (pmat ? s_par[i] : cp[i]) - cs[i];
+        cp[i] = d;
+        s_lg[i] = d;
+      }
+    }
+    __syncthreads();
+    const int mfb = (int)ft.mfb, tm = mfb - ft.offset;
+    if (tid == 0 && mfb > 0 && mfb < nb && tm >= 0) {
+      L.mfbv[(size_t)sm * F + f] = make_double2(cs[2 * tm], cs[2 * tm + 1]);
+      L.mfbv[(size_t)lg * F + f] = make_double2(cp[2 * tm], cp[2 * tm + 1]);
+    }
+  } else {
+    fix_compact_block(ft, cs, ss.sg, ss.sh, pgate || sm_zero);
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int i = tid + SCAN_THREADS * k;
-    if (i >= 2 * nb) continue;
-    const double v = cs[i];
-    const double d = pv[k] - v;
-    cp[i] = d;
-    s_sm[i] = v;
-    s_lg[i] = d;
+    for (int k = 0; k < 4; ++k) {
+      const int i = tid + SCAN_THREADS * k;
+      if (i >= 2 * nb) continue;
+      const double v = cs[i];
+      const double d = pv[k] - v;
+      cp[i] = d;
+      s_sm[i] = v;
+      s_lg[i] = d;
+    }
+    for (int i = tid + 4 * SCAN_THREADS; i < 2 * nb; i += SCAN_THREADS) {  // past 256 bins
+      const double v = cs[i];
+      const double d = s_par[i] - v;
+      cp[i] = d;
+      s_sm[i] = v;
+      s_lg[i] = d;
+    }
+    __syncthreads();
   }
-  for (int i = tid + 4 * SCAN_THREADS; i < 2 * nb; i += SCAN_THREADS) {  // past 256 bins
-    const double v = cs[i];
-    const double d = s_par[i] - v;
-    cp[i] = d;
-    s_sm[i] = v;
-    s_lg[i] = d;
-  }
-  __syncthreads();
   const int wv = tid >> 6;
   const int32_t leaf = wv == 0 ? sm : lg;
   const LeafSums ls = wv == 0 ? ss : gs;
@@ -1610,25 +1656,29 @@ void launch_partition_stable(const DevLearner& L, int64_t ntiles, int64_t blocks
 // Lets the scans take LDS rows for the widest feature (2-byte bins: 4096 bins, 128 KiB
 // for k_pair_scan's two children); called outside graph capture.
 int scan_prepare() {
-  if (hipFuncSetAttribute((const void*)k_pair_scan<false>,
-                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                          4 * WIDE_MAX_BIN * (int)sizeof(double)) != hipSuccess ||
-      hipFuncSetAttribute((const void*)k_pair_scan<true>,
-                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                          4 * WIDE_MAX_BIN * (int)sizeof(double)) != hipSuccess)
-    return 1;
+  const void* k[4] = {(const void*)k_pair_scan<false, false>, (const void*)k_pair_scan<true, false>,
+                      (const void*)k_pair_scan<false, true>, (const void*)k_pair_scan<true, true>};
+  for (int i = 0; i < 4; ++i)
+    if (hipFuncSetAttribute(k[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                            4 * WIDE_MAX_BIN * (int)sizeof(double)) != hipSuccess)
+      return 1;
   return 0;
 }
 
-void launch_pair_scan(const DevLearner& L, int32_t spec_max, int32_t part_grid, hipStream_t s,
-                      const KernelEvents* ev) {
+void launch_pair_scan(const DevLearner& L, int fp, int32_t spec_max, int32_t part_grid,
+                      hipStream_t s, const KernelEvents* ev) {
   const size_t lds = (size_t)4 * std::max(L.max_bins, 1) * sizeof(double);
-  if (L.has_cat)
-    KLAUNCH(ev, k_pair_scan<true>, dim3((unsigned)L.F, (unsigned)spec_max), dim3(SCAN_THREADS),
-            lds, s, L, part_grid);
-  else
-    KLAUNCH(ev, k_pair_scan<false>, dim3((unsigned)L.F, (unsigned)spec_max), dim3(SCAN_THREADS),
-            lds, s, L, part_grid);
+  const dim3 g((unsigned)L.F, (unsigned)spec_max), b(SCAN_THREADS);
+  if (L.has_cat) {
+    if (fp)
+      KLAUNCH(ev, (k_pair_scan<true, true>), g, b, lds, s, L, part_grid);
+    else
+      KLAUNCH(ev, (k_pair_scan<true, false>), g, b, lds, s, L, part_grid);
+  } else if (fp) {
+    KLAUNCH(ev, (k_pair_scan<false, true>), g, b, lds, s, L, part_grid);
+  } else {
+    KLAUNCH(ev, (k_pair_scan<false, false>), g, b, lds, s, L, part_grid);
+  }
 }
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {
   KLAUNCH(ev, k_tree_finalize, dim3(1), dim3(256), 0, s, L);

@@ -133,7 +133,13 @@ struct DevLearner {
   int32_t n_fgroups;          // feature groups of k_hist_f32 (cells of a group fit LDS)
   int32_t fgroup_first[MAX_FGROUPS + 1];
   int32_t* int_slots;         // [slot_cap][total_cells][3] per-node integer histograms
-  double* slots;              // [slot_cap][slot_len] per-node f64 histograms
+  double* slots;              // [slot_cap][slot_len] per-node f64 histograms (f32 mode,
+                              // and quantized nodes with fmat set)
+  // Quantized gradients: a node's f64 cells are its integer cells through
+  // int_cell_to_f64, except the cell FixHistogram writes (its f64 pair in mfbv); a
+  // node whose cells cannot be derived that way (fmat = 1) holds them in `slots`.
+  double2* mfbv;              // [slot_cap][F] the fixed most-frequent-bin cell
+  int32_t* fmat;              // [slot_cap] 1: the node's f64 cells are in `slots`
   lgbm_split_info* feat_split;  // [slot_cap][F]
   double* gain_dense;           // [slot_cap][F] the same gains, contiguous (the plan's ArgMax)
   lgbm_split_info* best;        // [slot_cap]
@@ -235,8 +241,8 @@ void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hip
                     const KernelEvents* ev = nullptr);
 void launch_plan(const DevLearner& L, int32_t slot_cap, hipStream_t s,
                  const KernelEvents* ev = nullptr);
-void launch_pair_scan(const DevLearner& L, int32_t spec_max, int32_t part_grid, hipStream_t s,
-                      const KernelEvents* ev = nullptr);
+void launch_pair_scan(const DevLearner& L, int fp, int32_t spec_max, int32_t part_grid,
+                      hipStream_t s, const KernelEvents* ev = nullptr);
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,
                           lgbm_split_info* out, hipStream_t s);

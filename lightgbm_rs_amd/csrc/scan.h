@@ -626,12 +626,89 @@ __device__ __forceinline__ BestKey wave_best_fast(BestKey k) {
   return wave_best(k);
 }
 
-// FixHistogram (fix_histogram.rs:50-80) on the RAW leaf sums, then compaction
-// (compact_histogram, learner.rs:4460-4492), on one feature's cells in LDS.  The fix
-// is the reference's sequential f64 subtraction in ascending bin order: each lane of
-// wave 0 holds one bin and broadcasts it in turn.  `zero` (a leaf with no rows or no
-// hessian, or a feature masked out by the parent) clears the cells instead.  Called by
-// every thread of a SCAN_THREADS block.
+// FixHistogram (fix_histogram.rs:50-80) on the RAW leaf sums: the most frequent bin's
+// cell = leaf sum minus the other bins in ascending order (the sequential f64 chain),
+// every lane of wave 0 the same chain over broadcast LDS reads, eight bins per batch.
+// The skipped bin is parked at +0.0 first (x - (+0.0) == x for every x) and
+// overwritten with the result, which every lane of wave 0 also returns in (g, h).
+// Called by wave 0 when 0 < mfb < num_bin.
+__device__ __forceinline__ void fix_mfb_wave(double* cs, int nb, int mfb, double sg, double sh,
+                                             double* fg, double* fh) {
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    cs[2 * mfb] = 0.0;
+    cs[2 * mfb + 1] = 0.0;
+  }
+  __builtin_amdgcn_wave_barrier();
+  const double2* c2 = (const double2*)cs;
+  double g = sg, h = sh;
+  int i = 0;
+  for (; i + 8 <= nb; i += 8) {
+    double2 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = c2[i + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      g -= v[u].x;
+      h -= v[u].y;
+    }
+  }
+  for (; i < nb; ++i) {
+    const double2 v = c2[i];
+    g -= v.x;
+    h -= v.y;
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (tid == 0) {
+    cs[2 * mfb] = g;
+    cs[2 * mfb + 1] = h;
+  }
+  *fg = g;
+  *fh = h;
+}
+
+// Compaction (compact_histogram, learner.rs:4460-4492): the cells shift down by the
+// feature's offset, zeros enter at the top.  Every thread of a SCAN_THREADS block;
+// the caller has synchronised the cells.
+__device__ __forceinline__ void compact_shift(const DevFeature& ft, double* cs) {
+  const int tid = threadIdx.x;
+  const int nb = (int)ft.num_bin;
+  const int off = ft.offset;
+  if (off <= 0) return;
+  if (nb <= 256) {
+    double a[256 / SCAN_THREADS], b2[256 / SCAN_THREADS];
+    int k = 0;
+    for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
+      const int src = c + off;
+      a[k] = src < nb ? cs[2 * src] : 0.0;
+      b2[k] = src < nb ? cs[2 * src + 1] : 0.0;
+    }
+    __syncthreads();
+    k = 0;
+    for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
+      cs[2 * c] = a[k];
+      cs[2 * c + 1] = b2[k];
+    }
+  } else {
+    // wider features shift down chunk by chunk: a chunk reads only cells the
+    // earlier chunks did not write
+    for (int c0 = 0; c0 < nb; c0 += SCAN_THREADS) {
+      const int c = c0 + tid, src = c + off;
+      const double a = (c < nb && src < nb) ? cs[2 * src] : 0.0;
+      const double b2 = (c < nb && src < nb) ? cs[2 * src + 1] : 0.0;
+      __syncthreads();
+      if (c < nb) {
+        cs[2 * c] = a;
+        cs[2 * c + 1] = b2;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// FixHistogram, then compaction, on one feature's cells in LDS.  `zero` (a leaf with
+// no rows or no hessian, or a feature masked out by the parent) clears the cells
+// instead.  Called by every thread of a SCAN_THREADS block.
 __device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* cs, double sg,
                                                   double sh, bool zero) {
   const int tid = threadIdx.x;
@@ -644,72 +721,47 @@ __device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* 
   }
   const int mfb = (int)ft.mfb;
   if (tid < LGBM_WAVE && mfb > 0 && mfb < nb) {
-    // leaf sum minus the other bins in ascending order (the sequential f64 chain),
-    // every lane of wave 0 the same chain over broadcast LDS reads, eight bins per
-    // batch.  The skipped bin is parked at +0.0 first (x - (+0.0) == x for every x)
-    // and overwritten with the result.
+    double fg, fh;
+    fix_mfb_wave(cs, nb, mfb, sg, sh, &fg, &fh);
+  }
+  __syncthreads();
+  compact_shift(ft, cs);
+  __syncthreads();
+}
+
+// The same for both children of a quantized split.  `cs` holds the smaller child's
+// cells (fixed with its sums as above, or cleared by `zero`), `cp` the larger child's
+// (or the parent's) cells from integers.  The reference's larger child is
+// parent - smaller cell by cell, never re-fixed: integer-derived cells subtract
+// exactly, so only its most-frequent-bin cell differs from its integers: the parent's
+// fixed pair `pm` minus the smaller's fixed cell (`sub`), or `pm` itself (`cp` then
+// holds the parent, from which the caller subtracts).  Both arrays are compacted.
+__device__ __forceinline__ void fix_compact_pair(const DevFeature& ft, double* cs, double* cp,
+                                                 double sg, double sh, bool zero, double2 pm,
+                                                 bool sub) {
+  const int tid = threadIdx.x;
+  const int nb = (int)ft.num_bin;
+  const int mfb = (int)ft.mfb;
+  const bool has_fix = mfb > 0 && mfb < nb;
+  __syncthreads();
+  if (zero) {
+    for (int i = tid; i < 2 * nb; i += SCAN_THREADS) cs[i] = 0.0;
+    if (tid == 0 && has_fix) {
+      cp[2 * mfb] = sub ? pm.x - 0.0 : pm.x;
+      cp[2 * mfb + 1] = sub ? pm.y - 0.0 : pm.y;
+    }
+  } else if (tid < LGBM_WAVE && has_fix) {
+    double fg, fh;
+    fix_mfb_wave(cs, nb, mfb, sg, sh, &fg, &fh);
     if (tid == 0) {
-      cs[2 * mfb] = 0.0;
-      cs[2 * mfb + 1] = 0.0;
-    }
-    __builtin_amdgcn_wave_barrier();
-    const double2* c2 = (const double2*)cs;
-    double g = sg, h = sh;
-    int i = 0;
-    for (; i + 8 <= nb; i += 8) {
-      double2 v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = c2[i + u];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        g -= v[u].x;
-        h -= v[u].y;
-      }
-    }
-    for (; i < nb; ++i) {
-      const double2 v = c2[i];
-      g -= v.x;
-      h -= v.y;
-    }
-    __builtin_amdgcn_wave_barrier();
-    if (tid == 0) {
-      cs[2 * mfb] = g;
-      cs[2 * mfb + 1] = h;
+      cp[2 * mfb] = sub ? pm.x - fg : pm.x;
+      cp[2 * mfb + 1] = sub ? pm.y - fh : pm.y;
     }
   }
   __syncthreads();
-  if (ft.offset > 0) {
-    const int off = ft.offset;
-    if (nb <= 256) {
-      double a[256 / SCAN_THREADS], b2[256 / SCAN_THREADS];
-      int k = 0;
-      for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
-        const int src = c + off;
-        a[k] = src < nb ? cs[2 * src] : 0.0;
-        b2[k] = src < nb ? cs[2 * src + 1] : 0.0;
-      }
-      __syncthreads();
-      k = 0;
-      for (int c = tid; c < nb; c += SCAN_THREADS, ++k) {
-        cs[2 * c] = a[k];
-        cs[2 * c + 1] = b2[k];
-      }
-    } else {
-      // wider features shift down chunk by chunk: a chunk reads only cells the
-      // earlier chunks did not write
-      for (int c0 = 0; c0 < nb; c0 += SCAN_THREADS) {
-        const int c = c0 + tid, src = c + off;
-        const double a = (c < nb && src < nb) ? cs[2 * src] : 0.0;
-        const double b2 = (c < nb && src < nb) ? cs[2 * src + 1] : 0.0;
-        __syncthreads();
-        if (c < nb) {
-          cs[2 * c] = a;
-          cs[2 * c + 1] = b2;
-        }
-        __syncthreads();
-      }
-    }
-  }
+  compact_shift(ft, cs);
+  __syncthreads();
+  compact_shift(ft, cp);
   __syncthreads();
 }
 
