@@ -40,8 +40,13 @@
 #ifndef WIDE_THREADS
 #define WIDE_THREADS 1024
 #endif
-#ifndef WIDE_GRID
-#define WIDE_GRID 1024                  // row-chunk blocks over all groups (at least)
+// row-chunk blocks over all groups (at least), per gradient mode: more chunks spread
+// the large builds over more blocks, fewer leave the scans fewer partial slots to sum
+#ifndef WIDE_GRID_Q
+#define WIDE_GRID_Q 512                 // quantized: 64-feature groups, 8-byte cells
+#endif
+#ifndef WIDE_GRID_F
+#define WIDE_GRID_F 1024                // f32: 32-feature groups, 16-byte cells
 #endif
 #ifndef WIDE_MIN_ROWS
 #define WIDE_MIN_ROWS 4096              // rows per chunk (at least): a flush costs a group

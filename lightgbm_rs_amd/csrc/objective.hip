@@ -38,7 +38,11 @@ __device__ __forceinline__ double rank_sigmoid(const RankParams& p, const double
                                                double s) {
   if (s <= p.min_in) return tab[0];
   if (s >= p.max_in) return tab[RANK_SIGMOID_BINS - 1];
-  return tab[(size_t)((s - p.min_in) * p.idx_factor)];
+  // a NaN score indexes bin 0 (Rust's saturating `as usize`); the index stays inside
+  // the table whatever the rounding
+  const double x = (s - p.min_in) * p.idx_factor;
+  const size_t i = x == x ? (size_t)x : 0;
+  return tab[i < (size_t)RANK_SIGMOID_BINS ? i : (size_t)RANK_SIGMOID_BINS - 1];
 }
 
 // Rows i of the reference's loop are taken RANK_BATCH (`nbat`) at a time.  A batch's

@@ -319,15 +319,16 @@ int wide_groups(int32_t F, int fp, int32_t n_groups16) {
 
 // Blocks per feature group of a launch (row chunks + one per job at most): rows per
 // chunk stay <= WIDE_MAX_ROWS, and the grid fills the chip.
-int64_t wide_grid_x(int ng, int64_t N) {
-  int64_t chunks = std::max<int64_t>(WIDE_GRID / ng, (N + WIDE_MAX_ROWS - 1) / WIDE_MAX_ROWS);
+int64_t wide_grid_x(int ng, int64_t N, int fp) {
+  int64_t chunks = std::max<int64_t>((fp ? WIDE_GRID_F : WIDE_GRID_Q) / ng,
+                                     (N + WIDE_MAX_ROWS - 1) / WIDE_MAX_ROWS);
   return std::max<int64_t>(chunks, 1) + SPEC_MAX;
 }
 
 // u64 words of the partial slots: every chunk of either gradient mode's launch
 size_t wide_part_words(int32_t F, int64_t N, int32_t cells, int32_t n_groups16) {
-  const int64_t gf = wide_grid_x(wide_groups(F, 1, n_groups16), N);
-  const int64_t gq = wide_grid_x(wide_groups(F, 0, n_groups16), N);
+  const int64_t gf = wide_grid_x(wide_groups(F, 1, n_groups16), N, 1);
+  const int64_t gq = wide_grid_x(wide_groups(F, 0, n_groups16), N, 0);
   return std::max((size_t)gf * 2, (size_t)gq) * (size_t)cells;
 }
 
@@ -344,7 +345,7 @@ int wide_prepare() {
 
 void launch_hist_wide(const DevLearner& L, int fp, hipStream_t s, const KernelEvents* ev) {
   const int ng = wide_groups(L.F, fp, L.bin16 ? L.n_wgroups : 0);
-  const dim3 g((unsigned)ng, (unsigned)wide_grid_x(ng, L.N)), blk(WIDE_THREADS);
+  const dim3 g((unsigned)ng, (unsigned)wide_grid_x(ng, L.N, fp)), blk(WIDE_THREADS);
   if (L.bin16) {
     if (fp)
       KLAUNCH(ev, (k_hist_wide<1, true>), g, blk, wide_lds_bytes(1, true), s, L);
