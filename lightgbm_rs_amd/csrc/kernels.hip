@@ -1127,6 +1127,57 @@ void launch_fixscan(const DevLearner& L, int32_t mode, double* explicit_out, hip
   KLAUNCH(ev, k_fixscan, dim3((unsigned)L.F), dim3(SCAN_THREADS),
           (size_t)2 * std::max(L.max_bins, 1) * sizeof(double), s, L, mode, explicit_out);
 }
+// The wide layout's score update (ScoreUpdater::add_score over the partition,
+// score_updater.rs:133-209): its records are row indices, and every committed leaf's
+// rows are its range of the row buffer its partition wrote (the leaf ranges
+// k_tree_finalize records), so each row gets its leaf's shrunk value from that range
+// without walking the tree through the row's binmat bytes.  Block b takes
+// LEAF_SCORE_ROWS positions of one leaf, found from the prefix of the leaves' block
+// counts; every row belongs to exactly one leaf range, so the adds do not overlap.
+#define LEAF_SCORE_ROWS 2048
+__global__ __launch_bounds__(256) void k_leaf_score(DevLearner L, double lr,
+                                                    double* __restrict__ score) {
+  __shared__ int32_t s_leaf, s_blk0;
+  const int32_t nl = L.ctl->num_leaves;
+  if (nl <= 1) return;
+  const int tid = threadIdx.x;
+  const int32_t b = (int32_t)blockIdx.x;
+  if (tid < LGBM_WAVE) {
+    if (tid == 0) s_leaf = -1;
+    int32_t run = 0;
+    for (int32_t l0 = 0; l0 < nl; l0 += LGBM_WAVE) {
+      const int32_t l = l0 + tid;
+      const int32_t c = l < nl ? L.leaves.count[l] : 0;
+      const int32_t nbk = (c + LEAF_SCORE_ROWS - 1) / LEAF_SCORE_ROWS;
+      const int32_t incl = wave_incl_sum_i32(nbk);
+      const int32_t ex = run + incl - nbk;
+      if (l < nl && b >= ex && b < ex + nbk) {
+        s_leaf = l;
+        s_blk0 = ex;
+      }
+      run += readlane_i32(incl, LGBM_WAVE - 1);
+    }
+  }
+  __syncthreads();
+  const int32_t l = s_leaf;
+  if (l < 0) return;
+  const int64_t off = (int64_t)(b - s_blk0) * LEAF_SCORE_ROWS;
+  const int64_t cnt = L.leaves.count[l], beg = L.leaves.begin[l];
+  const int32_t buf = L.leaves.buf[l];
+  const double v = maybe_round_to_zero(L.tree.leaf_value[l] * lr);
+  const uint32_t* __restrict__ idx = (const uint32_t*)rec_buf(L.bufs, buf) + beg;
+  constexpr int K = LEAF_SCORE_ROWS / 256;
+  int64_t row[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int64_t p = off + k * 256 + tid;
+    row[k] = p < cnt ? (buf == BUF_ORIG ? beg + p : (int64_t)idx[p]) : -1;
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (row[k] >= 0) score[row[k]] += v;
+}
+
 void launch_scan_explicit(const double* hist, const DevFeature* feats, int32_t n_feats,
                           const lgbm_gain_config& cfg, double sg, double sh, int32_t n,
                           lgbm_split_info* out, hipStream_t s) {
@@ -1137,10 +1188,11 @@ void launch_score_update(const DevLearner& L, double lr, double* score, hipStrea
                          const KernelEvents* ev) {
   int64_t blocks = std::min<int64_t>((L.N + 255) / 256, 2048);
   if (blocks < 1) blocks = 1;
-  if (rec_wide(L.fmt))
-    KLAUNCH(ev, (k_walk<REC_FMT_WIDE, false>), dim3((unsigned)blocks), dim3(256), 0, s, L, lr,
-            score, (uint8_t*)nullptr);
-  else
+  if (rec_wide(L.fmt)) {
+    // leaves' blocks: at most N / LEAF_SCORE_ROWS rounded up, plus one per leaf
+    const int64_t lb = (L.N + LEAF_SCORE_ROWS - 1) / LEAF_SCORE_ROWS + MAX_LEAVES;
+    KLAUNCH(ev, k_leaf_score, dim3((unsigned)lb), dim3(256), 0, s, L, lr, score);
+  } else
     DISPATCH_FMT(L.fmt, KLAUNCH(ev, (k_walk<kF, false>), dim3((unsigned)blocks), dim3(256), 0, s, L,
                                 lr, score, (uint8_t*)nullptr));
 }
