@@ -160,6 +160,7 @@ struct lgbm_hip_ctx {
   int32_t n_wgroups = 0;    // 2-byte bins: feature groups of the histogram kernel
   int32_t* d_wgroups = nullptr;  // [n_wgroups + 1] first feature of each group
   uint8_t* binmat = nullptr;  // wide layout: row-major bins [N][row_stride]
+  uint8_t* bincol = nullptr;  // wide layout: feature-major copy [F][N] (optional)
   int64_t row_stride = 0;
   uint64_t slot_len = 0;
   std::vector<DevFeature> feats;
@@ -408,6 +409,7 @@ DevLearner make_learner(lgbm_hip_ctx* c) {
   L.wide_part = c->wide_part;
   L.acc_cells = c->acc_cells;
   L.binmat = c->binmat;
+  L.bincol = c->bincol;
   L.row_stride = c->row_stride;
   L.max_bins = c->max_bins;
   L.has_cat = c->has_cat;
@@ -1152,6 +1154,14 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
     // row stride in bytes: F rounded up to a 64-feature group, times the bin width
     c->row_stride = ((int64_t)F + WIDE_GF_Q - 1) / WIDE_GF_Q * WIDE_GF_Q * (bin16 ? 2 : 1);
     if ((rc = dalloc(c, &c->binmat, (size_t)num_data * (size_t)c->row_stride))) return rc;
+    // the feature-major copy is optional: without it the router reads binmat rows
+    if (c->bincol) (void)hipFree(c->bincol);
+    c->bincol = nullptr;
+    if (hipMalloc((void**)&c->bincol, (size_t)num_data * (size_t)F * (bin16 ? 2 : 1)) !=
+        hipSuccess) {
+      c->bincol = nullptr;
+      (void)hipGetLastError();
+    }
     // 2-byte bins: feature groups of at most WIDE16_GROUP_F consecutive features whose
     // cells fit WIDE16_GROUP_CELLS
     std::vector<int32_t> groups(1, 0);
@@ -1176,9 +1186,11 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
   } else {
     c->row_stride = 0;
     if (c->binmat) (void)hipFree(c->binmat);
+    if (c->bincol) (void)hipFree(c->bincol);
     if (c->hist_acc64) (void)hipFree(c->hist_acc64);
     if (c->wide_part) (void)hipFree(c->wide_part);
     c->binmat = nullptr;
+    c->bincol = nullptr;
     c->hist_acc64 = nullptr;
     c->wide_part = nullptr;
     if (acc > (uint32_t)(MAX_FGROUPS - 1) * (HIST_FP_CELLS - 256))
@@ -1356,6 +1368,7 @@ int lgbm_hip_ctx_destroy(lgbm_hip_ctx* c) {
   F(c->wide_part);
   F(c->d_wgroups);
   F(c->binmat);
+  F(c->bincol);
   F(c->rk_qb);
   F(c->rk_imd);
   F(c->rk_table);
@@ -1472,10 +1485,12 @@ int lgbm_hip_upload_bins(lgbm_hip_ctx* c, const uint8_t* bins, int32_t num_featu
   HIPCHK(c, hipMalloc((void**)&tmp, (size_t)F * num_data));
   hipError_t e = hipMemcpy(tmp, bins, (size_t)F * num_data, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
-    if (rec_wide(c->fmt))
+    if (rec_wide(c->fmt)) {
       launch_pack_wide(tmp, num_data, F, c->row_stride, c->binmat, c->rec[BUF_ORIG], c->stream);
-    else
+      launch_wide_cols(c->binmat, num_data, F, c->row_stride, 0, c->bincol, c->stream);
+    } else {
       launch_pack_records(tmp, num_data, F, c->fmt, c->rec[BUF_ORIG], c->stream);
+    }
     e = hipStreamSynchronize(c->stream);
   }
   (void)hipFree(tmp);
@@ -1660,11 +1675,13 @@ int lgbm_hip_upload_raw_device(lgbm_hip_ctx* c, const void* d_values, int32_t dt
   if (e == hipSuccess) {
     // c->d_ub holds the same bounds, concatenated in feature order
     KernelEvents ke;
-    if (rec_wide(c->fmt))
+    if (rec_wide(c->fmt)) {
       launch_bin_wide(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->row_stride,
                       d_bf, c->d_ub, d_cats, c->binmat, c->rec[BUF_ORIG], c->bin16 ? 1 : 0,
                       c->stream, ev_kernel(c, FAM_BIN, &ke));
-    else
+      launch_wide_cols(c->binmat, num_rows, F, c->row_stride, c->bin16 ? 1 : 0, c->bincol,
+                       c->stream);
+    } else
       launch_bin_records(d_values, dtype == LGBM_HIP_DTYPE_F64, col_major, num_rows, F, c->fmt,
                          d_bf, c->d_ub, (int32_t)ub.size(), d_cats, c->rec[BUF_ORIG], c->stream,
                          ev_kernel(c, FAM_BIN, &ke));
@@ -1784,6 +1801,7 @@ int lgbm_hip_upload_bins16(lgbm_hip_ctx* c, const uint16_t* bins, int32_t num_fe
     e = hipMemcpy(tmp, bins, (size_t)F * num_data * 2, hipMemcpyHostToDevice);
     if (e == hipSuccess) {
       launch_pack_wide16(tmp, num_data, F, c->row_stride, c->binmat, c->rec[BUF_ORIG], c->stream);
+      launch_wide_cols(c->binmat, num_data, F, c->row_stride, 1, c->bincol, c->stream);
       e = hipStreamSynchronize(c->stream);
     }
     (void)hipFree(tmp);
@@ -1795,10 +1813,12 @@ int lgbm_hip_upload_bins16(lgbm_hip_ctx* c, const uint16_t* bins, int32_t num_fe
     HIPCHK(c, hipMalloc((void**)&tmp, b8.size()));
     e = hipMemcpy(tmp, b8.data(), b8.size(), hipMemcpyHostToDevice);
     if (e == hipSuccess) {
-      if (rec_wide(c->fmt))
+      if (rec_wide(c->fmt)) {
         launch_pack_wide(tmp, num_data, F, c->row_stride, c->binmat, c->rec[BUF_ORIG], c->stream);
-      else
+        launch_wide_cols(c->binmat, num_data, F, c->row_stride, 0, c->bincol, c->stream);
+      } else {
         launch_pack_records(tmp, num_data, F, c->fmt, c->rec[BUF_ORIG], c->stream);
+      }
       e = hipStreamSynchronize(c->stream);
     }
     (void)hipFree(tmp);

@@ -846,7 +846,18 @@ __global__ __launch_bounds__(PART_THREADS) void k_partition(DevLearner L) {
     int32_t wbin[PR];
     if constexpr (WIDE) {
       const int64_t stride = L.row_stride;
-      if (L.bin16) {
+      if (L.bincol) {
+        // the feature-major copy: the job's rows share the feature's column
+        if (L.bin16) {
+          const uint16_t* __restrict__ col = (const uint16_t*)L.bincol + (int64_t)J.fbyte * L.N;
+#pragma unroll
+          for (int k = 0; k < PR; ++k) wbin[k] = col[w[k][0]];
+        } else {
+          const uint8_t* __restrict__ col = L.bincol + (int64_t)J.fbyte * L.N;
+#pragma unroll
+          for (int k = 0; k < PR; ++k) wbin[k] = col[w[k][0]];
+        }
+      } else if (L.bin16) {
         const uint8_t* __restrict__ col = L.binmat + 2 * (int64_t)J.fbyte;
 #pragma unroll
         for (int k = 0; k < PR; ++k)

@@ -124,6 +124,8 @@ struct DevLearner {
   unsigned long long* wide_part;  // wide layout: per-chunk partial cells [chunks][cells][1 or 2]
   int32_t acc_cells;          // cells per accumulator: total_cells, + 1 (row totals) when wide
   const uint8_t* binmat;      // wide layout: row-major bins [N][row_stride]
+  const uint8_t* bincol;      // wide layout: the same bins feature-major [F][N] (1 or 2
+                              // bytes each; NULL if it did not fit), the partition's router
   int64_t row_stride;
   const uint8_t* feat_used;   // per feature position: the tree's column sample (NULL: all)
   unsigned long long* part_slots;  // [part blocks + SPEC_MAX][total_cells] packed (block, job) cells
@@ -291,6 +293,8 @@ int fixscan_prepare();
 // u64 words of the wide layout's per-chunk partial histogram slots
 size_t wide_part_words(int32_t F, int64_t N, int32_t cells, int32_t n_groups16);
 // feature-major 2-byte bins -> the row-major matrix (2-byte bins)
+void launch_wide_cols(const uint8_t* binmat, int64_t n, int32_t F, int64_t stride, int bin16,
+                      uint8_t* bincol, hipStream_t s);
 void launch_pack_wide16(const uint16_t* bins, int64_t n, int32_t F, int64_t stride,
                         uint8_t* binmat, uint4* rec, hipStream_t s);
 // ConstructHistogram of the launch's histogram jobs into the per-job accumulators

@@ -293,7 +293,42 @@ __global__ void k_pack_wide16(const uint16_t* __restrict__ bins, int64_t n, int3
   if (wd == 0) rec[r] = (uint32_t)r;
 }
 
+// Row-major matrix -> feature-major copy (the partition's router reads one feature of
+// many rows): thread = (16-byte word, row), rows fastest, so each feature's stores
+// of a wave are 64 consecutive rows.
+__global__ void k_wide_cols(const uint8_t* __restrict__ binmat, int64_t n, int32_t F,
+                            int64_t stride, int32_t bin16, uint8_t* __restrict__ bincol) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t words = stride / 16;
+  if (i >= n * words) return;
+  const int64_t wd = i / n, r = i - wd * n;
+  const uint4 v = ((const uint4*)(binmat + r * stride))[wd];
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+  if (bin16) {
+    uint16_t* col = (uint16_t*)bincol;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int64_t f = wd * 8 + k;
+      if (f < F) col[f * n + r] = (uint16_t)(u[k >> 1] >> (16 * (k & 1)));
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int64_t f = wd * 16 + k;
+      if (f < F) bincol[f * n + r] = (uint8_t)(u[k >> 2] >> (8 * (k & 3)));
+    }
+  }
+}
+
 }  // namespace
+
+void launch_wide_cols(const uint8_t* binmat, int64_t n, int32_t F, int64_t stride, int bin16,
+                      uint8_t* bincol, hipStream_t s) {
+  const int64_t total = n * (stride / 16);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks < 1 || !bincol) return;
+  k_wide_cols<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(binmat, n, F, stride, bin16, bincol);
+}
 
 void launch_pack_wide16(const uint16_t* bins, int64_t n, int32_t F, int64_t stride,
                         uint8_t* binmat, uint4* rec, hipStream_t s) {
