@@ -1126,7 +1126,8 @@ __global__ __launch_bounds__(1024) void k_tile_scan(DevLearner L) {
 // CU can hold set its time: six waves a SIMD (at most 80 VGPRs) and 12.5 KB of LDS at
 // 256 bins give 12 blocks a CU where 89 VGPRs and the categorical rows gave 8.
 // FP: f32 gradients (64-bit fixed-point cells, f64 cells kept in the node slots).
-template <bool CAT, bool FP>
+// GRID: quantized cells below 2^53 units, scanned with prefix_grid.
+template <bool CAT, bool FP, bool GRID>
 __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int32_t part_grid) {
   static_assert(SCAN_THREADS == 128, "two bins and four f64 cells per thread cover 256 bins");
   // the smaller child's and the larger child's f64 cells, sized for the widest feature
@@ -1432,9 +1433,9 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
       gain = ft.categorical  // bin_type dispatch (learner.rs:3103-3118)
                  ? wave_scan_cat(wv == 0 ? cs : cp, ft, sc, ctl->cfg, ls.sg, ls.sh, ls.n,
                                  ls.weight, out, L.cat_bits + ((size_t)leaf * F + f) * 8)
-                 : wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
+                 : wave_scan<GRID>(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
     else
-      gain = wave_scan(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
+      gain = wave_scan<GRID>(wv == 0 ? cs : cp, ft, sc, ls.sg, ls.sh, ls.n, ls.weight, out);
     if (lane_id() == 0) {
       // splittability from the raw scan, then feature_contri scales the gain the
       // ArgMax compares (learner.rs:3235-3252)
@@ -1667,9 +1668,13 @@ void launch_partition_stable(const DevLearner& L, int64_t ntiles, int64_t blocks
 // Lets the scans take LDS rows for the widest feature (2-byte bins: 4096 bins, 128 KiB
 // for k_pair_scan's two children); called outside graph capture.
 int scan_prepare() {
-  const void* k[4] = {(const void*)k_pair_scan<false, false>, (const void*)k_pair_scan<true, false>,
-                      (const void*)k_pair_scan<false, true>, (const void*)k_pair_scan<true, true>};
-  for (int i = 0; i < 4; ++i)
+  const void* k[6] = {(const void*)k_pair_scan<false, false, false>,
+                      (const void*)k_pair_scan<true, false, false>,
+                      (const void*)k_pair_scan<false, true, false>,
+                      (const void*)k_pair_scan<true, true, false>,
+                      (const void*)k_pair_scan<false, false, true>,
+                      (const void*)k_pair_scan<true, false, true>};
+  for (int i = 0; i < 6; ++i)
     if (hipFuncSetAttribute(k[i], hipFuncAttributeMaxDynamicSharedMemorySize,
                             4 * WIDE_MAX_BIN * (int)sizeof(double)) != hipSuccess)
       return 1;
@@ -1680,15 +1685,23 @@ void launch_pair_scan(const DevLearner& L, int fp, int32_t spec_max, int32_t par
                       hipStream_t s, const KernelEvents* ev) {
   const size_t lds = (size_t)4 * std::max(L.max_bins, 1) * sizeof(double);
   const dim3 g((unsigned)L.F, (unsigned)spec_max), b(SCAN_THREADS);
+  // quantized cells are exact unit multiples while every sum stays below 2^53 units
+  // (fewer than 2^24 rows); the grid prefix pays where a scan spans several 64-candidate
+  // batches (at most 64 candidates: one batch, as cheap in order)
+  const bool grid = !fp && L.N < (int64_t(1) << 24) && L.max_bins > LGBM_WAVE + 1;
   if (L.has_cat) {
     if (fp)
-      KLAUNCH(ev, (k_pair_scan<true, true>), g, b, lds, s, L, part_grid);
+      KLAUNCH(ev, (k_pair_scan<true, true, false>), g, b, lds, s, L, part_grid);
+    else if (grid)
+      KLAUNCH(ev, (k_pair_scan<true, false, true>), g, b, lds, s, L, part_grid);
     else
-      KLAUNCH(ev, (k_pair_scan<true, false>), g, b, lds, s, L, part_grid);
+      KLAUNCH(ev, (k_pair_scan<true, false, false>), g, b, lds, s, L, part_grid);
   } else if (fp) {
-    KLAUNCH(ev, (k_pair_scan<false, true>), g, b, lds, s, L, part_grid);
+    KLAUNCH(ev, (k_pair_scan<false, true, false>), g, b, lds, s, L, part_grid);
+  } else if (grid) {
+    KLAUNCH(ev, (k_pair_scan<false, false, true>), g, b, lds, s, L, part_grid);
   } else {
-    KLAUNCH(ev, (k_pair_scan<false, false>), g, b, lds, s, L, part_grid);
+    KLAUNCH(ev, (k_pair_scan<false, false, false>), g, b, lds, s, L, part_grid);
   }
 }
 void launch_tree_finalize(const DevLearner& L, hipStream_t s, const KernelEvents* ev) {

@@ -198,6 +198,79 @@ __device__ __forceinline__ void prefix_in_order(double g, double h, int32_t c, i
   *sh = ah;
 }
 
+// A DPP move of an f64 (both halves alike); lanes without a source lane get +0.0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const int lo = (int)(uint32_t)b, hi = (int)(uint32_t)(b >> 32);
+  const uint32_t nlo = (uint32_t)__builtin_amdgcn_update_dpp(0, lo, CTRL, ROW_MASK, 0xf, false);
+  const uint32_t nhi = (uint32_t)__builtin_amdgcn_update_dpp(0, hi, CTRL, ROW_MASK, 0xf, false);
+  return __longlong_as_double((long long)(((unsigned long long)nhi << 32) | nlo));
+}
+// Inclusive prefix sum of the wave's values in lane order, as a DPP tree (row_shr 1, 2,
+// 4, 8, then the row broadcasts 15 and 31): exact only when every partial sum is a
+// double, as for multiples of one unit well below 2^53 units.
+__device__ __forceinline__ double wave_incl_sum_f64_exact(double v) {
+  v += dpp_f64<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_f64<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_f64<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_f64<0x118, 0xf>(v);  // row_shr:8
+  v += dpp_f64<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+  v += dpp_f64<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+// s == fl(a + b): true when the sum is exact (TwoSum's error term is zero).
+__device__ __forceinline__ bool sum_is_exact(double a, double b, double s) {
+  const double bv = s - a, av = s - bv;
+  return ((a - av) + (b - bv)) == 0.0;
+}
+
+// prefix_in_order's result for cells that are exact multiples of one unit (quantized
+// gradients: integer cells through int_cell_to_f64), except the lane `odd` (the
+// FixHistogram cell; out of range: none).  The reference's sums S_k = fl(S_{k-1} +
+// v_k) start from the carry (any double).  The unit cells' prefix P is exact in any
+// order, so from the last step t that rounded, S_{k-1} = S_t + (P_{k-1} - P_t) exactly
+// as long as no step in between rounds; every lane forms its own step from that and
+// tests it with TwoSum, and the first lane whose step rounds (or holds the odd cell)
+// takes the rounded sum, which is the reference's, as the next t.  The loop runs once
+// per rounding step, plus once: a step rounds only where the sum changes binade or
+// carries bits below the unit (the kEpsilon start, absorbed within a few binades).
+__device__ __forceinline__ void prefix_grid(double g, double h, int32_t c, int32_t cnt, int lane,
+                                            int odd, double* sg, double* sh, int32_t* sc) {
+  const bool in = lane < cnt;
+  *sc += wave_incl_sum_i32(in ? c : 0);
+  const bool unit = in && lane != odd;
+  const double pg = wave_incl_sum_f64_exact(unit ? g : 0.0);
+  const double ph = wave_incl_sum_f64_exact(unit ? h : 0.0);
+  const double qg = dpp_f64<0x138, 0xf>(pg), qh = dpp_f64<0x138, 0xf>(ph);  // wave_shr:1
+  const double vg = in ? g : 0.0, vh = in ? h : 0.0;
+  double tg = *sg, th = *sh, ptg = 0.0, pth = 0.0;
+  double og = 0.0, oh = 0.0;
+  int t = -1;
+  for (;;) {
+    // this lane's S_{k-1}, unchanged (signed zeros included) while P has not moved
+    const double ag = qg == ptg ? tg : tg + (qg - ptg);
+    const double ah = qh == pth ? th : th + (qh - pth);
+    const double ng = ag + vg, nh = ah + vh;
+    const bool live = in && lane > t;
+    const bool bad = live && (lane == odd || !sum_is_exact(ag, vg, ng) || !sum_is_exact(ah, vh, nh));
+    const unsigned long long m = __ballot(bad);
+    const int j = m ? (int)__builtin_ctzll(m) : LGBM_WAVE;
+    if (live && lane <= j) {
+      og = ng;
+      oh = nh;
+    }
+    if (!m) break;
+    tg = readlane_f64(ng, j);
+    th = readlane_f64(nh, j);
+    ptg = readlane_f64(pg, j);
+    pth = readlane_f64(ph, j);
+    t = j;
+  }
+  *sg = og;
+  *sh = oh;
+}
+
 // The best candidate of one batch of a threshold scan: the highest gain, the lowest
 // lane among equal gains (the reference's strict-> scan in candidate order); -1 when
 // no lane is a candidate.  `best` receives the gain.
@@ -210,7 +283,9 @@ __device__ __forceinline__ int wave_best_lane(bool cand, double gain, double* be
 
 // FindBestThresholdNumerical for one (leaf, feature) by one wave over the compacted
 // histogram; returns the gain written to `out` (-inf for none), in every lane.
-static __device__ __attribute__((unused)) double wave_scan(const double* hist, const DevFeature& ft, const ScanCfg& c,
+// GRID: the cells are unit multiples but for the FixHistogram cell (prefix_grid).
+template <bool GRID = false>
+__device__ __attribute__((unused)) double wave_scan(const double* hist, const DevFeature& ft, const ScanCfg& c,
                           double sum_gradient, double sum_hessian, int32_t num_data, double po,
                           lgbm_split_info* out) {
   const int lane = (int)lane_id();
@@ -236,6 +311,10 @@ static __device__ __attribute__((unused)) double wave_scan(const double* hist, c
     fwd_count = na_pre ? base + 1 : base;
   }
   const double cf = (double)num_data / shb;
+  // the FixHistogram cell's compacted index (-1: none)
+  const int32_t tm = (ft.mfb > 0 && (int32_t)ft.mfb < nb && (int32_t)ft.mfb >= offset)
+                         ? (int32_t)ft.mfb - offset
+                         : -1;
 
   bool any_split = false;
   double best_gain = ninf, best_lg = 0.0, best_lh = 0.0;
@@ -256,7 +335,10 @@ static __device__ __attribute__((unused)) double wave_scan(const double* hist, c
       const int32_t mc = act ? round_int(mh * cf) : 0;
       double sg = cg, sh = ch;
       int32_t rc = cc;
-      prefix_in_order(mg, mh, mc, cnt, lane, &sg, &sh, &rc);
+      if constexpr (GRID)
+        prefix_grid(mg, mh, mc, cnt, lane, tm >= 0 ? t_start - base - tm : -1, &sg, &sh, &rc);
+      else
+        prefix_in_order(mg, mh, mc, cnt, lane, &sg, &sh, &rc);
       const int32_t lc = num_data - rc;
       const double slh = shb - sh, slg = sum_gradient - sg;
       const bool cont = rc < c.min_d || sh < c.min_h;
@@ -317,7 +399,10 @@ static __device__ __attribute__((unused)) double wave_scan(const double* hist, c
       const int32_t mc = addl ? round_int(mh * cf) : 0;
       double sg = cg, sh = ch;
       int32_t lcn = cc;
-      prefix_in_order(mg, mh, mc, cnt, lane, &sg, &sh, &lcn);
+      if constexpr (GRID)
+        prefix_grid(mg, mh, mc, cnt, lane, tm >= 0 ? tm - fwd_start - base : -1, &sg, &sh, &lcn);
+      else
+        prefix_in_order(mg, mh, mc, cnt, lane, &sg, &sh, &lcn);
       const int32_t rc = num_data - lcn;
       const double srh = shb - sh, srg = sum_gradient - sg;
       const bool cont = lcn < c.min_d || sh < c.min_h;
