@@ -51,6 +51,15 @@
 #ifndef WIDE_MIN_ROWS
 #define WIDE_MIN_ROWS 4096              // rows per chunk (at least): a flush costs a group
 #endif
+#ifndef WIDE_MIN_ROWS_SMALL_Q
+#define WIDE_MIN_ROWS_SMALL_Q 2048      // ... and in rounds too small to fill the chip
+#endif                                  //     (quantized; f32 keeps WIDE_MIN_ROWS)
+#ifndef WIDE_MIN_ROWS_SMALL_F
+#define WIDE_MIN_ROWS_SMALL_F 4096
+#endif
+#ifndef WIDE_FILL
+#define WIDE_FILL 256                   // blocks a small round aims at
+#endif
 #define WIDE_MAX_ROWS ((1 << 19) - 1)   // packed LDS cell field limit (quantized)
 #define WIDE_MAX_F 4096
 #define WIDE_MAX_BIN 4096               // 2-byte bins (a feature of more than 256 bins)

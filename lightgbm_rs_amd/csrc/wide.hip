@@ -39,13 +39,17 @@ namespace {
 // Wave 0, lane j = job j (nj <= SPEC_MAX): the counts load in parallel.
 __device__ __forceinline__ void wide_assign(const Ctl* ctl, int32_t nj, int32_t* s_a0,
                                             int32_t* s_nb, int64_t* s_R, int64_t chunks,
-                                            int lane) {
+                                            int64_t groups, int64_t min_small, int lane) {
   const int64_t c = lane < nj ? max(ctl->hjobs[lane].count, (int64_t)0) : 0;
   int64_t S = c;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) S += __shfl_xor(S, off);
   int64_t R = (S + chunks - 1) / chunks;
-  if (R < WIDE_MIN_ROWS) R = WIDE_MIN_ROWS;
+  // at least WIDE_MIN_ROWS rows a chunk (a chunk's flush costs its group's cells),
+  // fewer down to `min_small` when the round is too small to give every CU a block
+  // (about WIDE_FILL blocks over the groups)
+  const int64_t rmin = min((int64_t)WIDE_MIN_ROWS, max(min_small, S * groups / WIDE_FILL));
+  if (R < rmin) R = rmin;
   const int32_t nb = c > 0 ? (int32_t)((c + R - 1) / R) : 0;
   const int32_t incl = wave_incl_sum_i32(nb);
   if (lane < nj) {
@@ -78,7 +82,10 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
   const int grp = (int)blockIdx.x;
   const int f0 = B16 ? L.wgroups[grp] : grp * GF;
   if (f0 >= F) return;
-  if (wave == 0) wide_assign(ctl, nj, s_a0, s_nb, &s_R, (int64_t)gridDim.y - SPEC_MAX, (int)lane_id());
+  if (wave == 0) wide_assign(ctl, nj, s_a0, s_nb, &s_R, (int64_t)gridDim.y - SPEC_MAX,
+                              (int64_t)gridDim.x,
+                              (int64_t)(FP ? WIDE_MIN_ROWS_SMALL_F : WIDE_MIN_ROWS_SMALL_Q),
+                              (int)lane_id());
   __syncthreads();
   const int32_t a = (int32_t)blockIdx.y;
   int32_t j = -1;
