@@ -91,11 +91,17 @@ __global__ __launch_bounds__(LAMBDARANK_THREADS) void k_grad_lambdarank(
     const double si = s_sc[i];
     const bool ni = si != si;
     int32_t r = 0;
-    for (int j = 0; j < cnt; ++j) {
-      const double sj = s_sc[j];
-      const bool nj = sj != sj;
-      const bool before = (ni || nj) ? (ni && (!nj || j < i)) : (sj > si || (sj == si && j < i));
-      r += before ? 1 : 0;
+    if (!ni) {
+      // before i: higher or equal scores (a NaN compares false); after i: higher
+#pragma unroll 4
+      for (int j = 0; j < i; ++j) r += s_sc[j] >= si ? 1 : 0;
+#pragma unroll 4
+      for (int j = i + 1; j < cnt; ++j) r += s_sc[j] > si ? 1 : 0;
+    } else {
+      for (int j = 0; j < cnt; ++j) {
+        const bool nj = s_sc[j] != s_sc[j];
+        r += (!nj || j < i) ? 1 : 0;
+      }
     }
     s_ord[r] = i;
   }
