@@ -353,12 +353,27 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     if (s_lc[l].x < 0 && k.hi != 0ull && k.hi == s_uhi) atomicMax(&s_ulo, (unsigned long long)k.lo);
   }
   const int32_t nS = s_nS;
-  for (int i = tid; i < nS; i += PLAN_THREADS) {  // rank of each S leaf within S
-    const LKey c = s_SK[i];
-    int32_t r = 0;
+  {
+    // rank of each S leaf within S (the leaves split ahead of their turn can number
+    // well over a hundred): T consecutive threads per leaf (at most a DPP row), each
+    // counting the better keys among every T-th entry, summed across the group
+    int T = 1;
+    while (T < 16 && nS * T * 2 <= PLAN_THREADS) T *= 2;
+    for (int i0 = 0; i0 < nS * T; i0 += PLAN_THREADS) {
+      const int idx = i0 + tid, i = idx / T, sub = idx - i * T;
+      const bool valid = i < nS;
+      int32_t r = 0;
+      if (valid) {
+        const LKey c = s_SK[i];
 #pragma unroll 4
-    for (int k = 0; k < nS; ++k) r += lk_gt(s_SK[k], c) ? 1 : 0;
-    s_sorted[r] = s_S[i];
+        for (int k = sub; k < nS; k += T) r += lk_gt(s_SK[k], c) ? 1 : 0;
+      }
+      if (T >= 2) r += __builtin_amdgcn_update_dpp(0, r, 0xB1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
+      if (T >= 4) r += __builtin_amdgcn_update_dpp(0, r, 0x4E, 0xf, 0xf, false);   // quad_perm [2,3,0,1]
+      if (T >= 8) r += __builtin_amdgcn_update_dpp(0, r, 0x141, 0xf, 0xf, false);  // row_half_mirror
+      if (T >= 16) r += __builtin_amdgcn_update_dpp(0, r, 0x140, 0xf, 0xf, false); // row_mirror
+      if (valid && sub == 0) s_sorted[r] = s_S[i];
+    }
   }
   __syncthreads();
   if (wave == 0) {
