@@ -468,6 +468,13 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
     if (ns0 + 2 <= slot_cap) {
       const int32_t extra = (slot_cap - ns0 - 2 - 2 * (maxl - nl)) / 2;
       allowed = min(spec, 1 + max(extra, 0));
+      // Where a job's scans are costly next to a round's fixed latency (many features,
+      // f32 cells twice the work), speculate beyond the ArgMax leaf only while the
+      // leaves already split ahead of their turn are fewer than the splits the tree
+      // can still take; with fewer features the rounds the cap adds cost more than
+      // the jobs it saves
+      if (F * (fp ? 2 : 1) >= PLAN_CAP_WORK)
+        allowed = min(allowed, max(1, (maxl - nl) - (s_nS - s_nc)));
     }
     // pass A: a candidate's rank within its group of 32 leaves (4 threads, 8 keys
     // each); the group's best `allowed` survive.  Every candidate of the overall best

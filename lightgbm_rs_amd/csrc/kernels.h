@@ -164,6 +164,9 @@ struct DevLearner {
 #define LAMBDARANK_THREADS 128
 #define RANK_SIGMOID_BINS (1024 * 1024)
 #define RANK_MAX_QUERY 2048
+#ifndef PLAN_CAP_WORK
+#define PLAN_CAP_WORK 2048             // features x (2 for f32 cells) from which k_plan caps speculation
+#endif
 #ifndef RANK_BATCH
 #define RANK_BATCH 4                   // rows of the lambdarank loop per batch (2-5 measured alike, 8 and 16 slower)
 #endif
