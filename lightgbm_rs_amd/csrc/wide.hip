@@ -131,6 +131,74 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
     ghq = buf_sel(L.bufs.gh, J.buf) + jb;
   const double gm = FP ? ldexp(1.0, ctl->g_shift) : 0.0, hm = FP ? ldexp(1.0, ctl->h_shift) : 0.0;
   long long tg = 0, th = 0, t3 = 0;
+  if constexpr (!FP && !B16) {
+    // Quantized 1-byte bins: a row whose pair quantized to (0, 0) adds nothing (there
+    // is no count field), and with 4 quantization bins that is most rows of a ranking
+    // objective.  Each wave queues its live rows (source row, pair) in an LDS ring and
+    // adds them 64 at a time, so the atomics and the row's binmat bytes are spent on
+    // live rows only: LDS atomics cost per instruction more than per active lane.
+    constexpr int kRing = 2 * LGBM_WAVE;
+    __shared__ uint32_t s_rrow[NW * kRing], s_rq[NW * kRing];
+    uint32_t* rrow = s_rrow + wave * kRing;
+    uint32_t* rq = s_rq + wave * kRing;
+    const int lane = (int)lane_id();
+    int staged = 0, consumed = 0;  // wave-uniform
+    auto add_batch = [&](int n) {
+      __builtin_amdgcn_wave_barrier();  // the ring's stores come first (in-order LDS)
+      if (lane < n) {
+        const int e = (consumed + lane) & (kRing - 1);
+        const uint32_t q = rq[e];
+        const int64_t src_row = (int64_t)rrow[e];
+        const int32_t qg = (int32_t)(int8_t)(q & 0xffu);
+        const int32_t qh = (int32_t)(int8_t)(q >> 8);
+        const unsigned long long v = (unsigned long long)(long long)qg +
+                                     ((unsigned long long)(uint32_t)qh << 22) +
+                                     ((unsigned long long)(qh == 3 ? 1u : 0u) << 43);
+        const uint4* src = (const uint4*)(bm + src_row * stride);
+        uint4 w4[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) w4[i] = src[i];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const uint32_t word[4] = {w4[i].x, w4[i].y, w4[i].z, w4[i].w};
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            const uint32_t fd = __builtin_amdgcn_readfirstlane(s_fd[16 * i + k]);
+            const uint32_t bin = (word[k >> 2] >> (8 * (k & 3))) & 0xffu;
+            if (bin != (fd & 0xffu))
+              __hip_atomic_fetch_add(&lds[(int)(fd >> 8) + (int)bin], v, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();  // the ring's loads complete before it is refilled
+      consumed += n;
+    };
+    for (int64_t b0 = lo; b0 < hi; b0 += (int64_t)WIDE_THREADS * RU) {
+#pragma unroll
+      for (int u = 0; u < RU; ++u) {
+        const int64_t r = b0 + (int64_t)u * WIDE_THREADS + tid;
+        const bool ok = r < hi;
+        const uint32_t q = ok ? (uint32_t)ghq[r] : 0u;
+        const uint32_t srow = ok ? (orig ? (uint32_t)(jb + r) : rows[r]) : 0u;
+        const int32_t qg = (int32_t)(int8_t)(q & 0xffu);
+        const int32_t qh = (int32_t)(int8_t)(q >> 8);
+        tg += qg;
+        th += qh;
+        t3 += qh == 3 ? 1 : 0;
+        const bool live = q != 0u;
+        const unsigned long long m = __ballot(live);
+        if (live) {
+          const int e = (staged + (int)__popcll(m & lanemask_lt())) & (kRing - 1);
+          rrow[e] = srow;
+          rq[e] = q;
+        }
+        staged += (int)__popcll(m);
+        if (staged - consumed >= LGBM_WAVE) add_batch(LGBM_WAVE);
+      }
+    }
+    if (staged > consumed) add_batch(staged - consumed);
+  } else
   for (int64_t b0 = lo; b0 < hi; b0 += (int64_t)WIDE_THREADS * RU) {
     int64_t row[RU];
     bool ok[RU];
