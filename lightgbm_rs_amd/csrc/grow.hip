@@ -1147,7 +1147,7 @@ __global__ __launch_bounds__(1024) void k_tile_scan(DevLearner L) {
 // runs F x jobs blocks of ~15-20 us each, more than the chip holds at once, so blocks a
 // CU can hold set its time: six waves a SIMD (at most 80 VGPRs) and 12.5 KB of LDS at
 // 256 bins give 12 blocks a CU where 89 VGPRs and the categorical rows gave 8.
-// FP: f32 gradients (64-bit fixed-point cells, f64 cells kept in the node slots).
+// FP: f32 gradients (64-bit fixed-point integer cells).
 // GRID: quantized cells below 2^53 units, scanned with prefix_grid.
 template <bool CAT, bool FP, bool GRID>
 __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int32_t part_grid) {
@@ -1189,19 +1189,10 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
   const int nb = (int)ft.num_bin;
   const size_t sl = L.slot_len;
   const double* s_par = L.slots + (size_t)p * sl + ft.slot_off;
-  // Quantized gradients derive both children's f64 cells from their integer cells
-  // (fix_compact_pair); only a parent whose cells are materialised (pmat) is read.
-  constexpr bool derive = !FP;
-  const bool pmat = derive && L.fmat[p] != 0;
-  const double2 pm = derive ? L.mfbv[(size_t)p * F + f] : make_double2(0.0, 0.0);
-  double pv[4];  // f32 mode: the parent's f64 cells i = tid + 128 k
-  if constexpr (!derive) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = tid + SCAN_THREADS * k;
-      pv[k] = i < 2 * nb ? s_par[i] : 0.0;
-    }
-  }
+  // Both children's f64 cells come from their integer cells (fix_compact_pair); only
+  // a parent whose cells are materialised (pmat) is read.
+  const bool pmat = L.fmat[p] != 0;
+  const double2 pm = L.mfbv[(size_t)p * F + f];
   const bool gated = (md > 0 && dcl >= md) || (lcnt < min2 && rcnt < min2);
   const bool right_small = !(lcnt < rcnt);
   const int32_t sm = right_small ? cr : cl, lg = right_small ? cl : cr;
@@ -1211,7 +1202,7 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
   // is every larger child of a materialised parent.
   const bool sm_zero = !(ss.sh > 0.0 && ss.n > 0);
   const bool lg_mat = pmat || sm_zero;
-  if (derive && f == 0 && tid == 0) {
+  if (f == 0 && tid == 0) {
     L.fmat[sm] = 0;
     L.fmat[lg] = lg_mat ? 1 : 0;
   }
@@ -1264,14 +1255,19 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
           hist_part_sum64(L, a0, na, ci, &SG, &SH);
         }
         const int64_t* ps = L.int_slots64 + ((size_t)p * cells + ci) * 2;
-        int64_t* ss = L.int_slots64 + ((size_t)sm * cells + ci) * 2;
-        int64_t* gs_ = L.int_slots64 + ((size_t)lg * cells + ci) * 2;
-        ss[0] = SG;
-        ss[1] = SH;
-        gs_[0] = ps[0] - SG;
-        gs_[1] = ps[1] - SH;
+        int64_t* sp_ = L.int_slots64 + ((size_t)sm * cells + ci) * 2;
+        int64_t* gp_ = L.int_slots64 + ((size_t)lg * cells + ci) * 2;
+        const int64_t PG = ps[0], PH = ps[1];
+        sp_[0] = SG;
+        sp_[1] = SH;
+        gp_[0] = PG - SG;
+        gp_[1] = PH - SH;
         cs[2 * b] = (double)SG * gu;
         cs[2 * b + 1] = (double)SH * hu;
+        // the larger child's cells from its exact integers (or the parent's, when the
+        // larger is materialised): one rounding instead of one per subtraction level
+        cp[2 * b] = (double)(lg_mat ? PG : PG - SG) * gu;
+        cp[2 * b + 1] = (double)(lg_mat ? PH : PH - SH) * hu;
       }
     }
   } else {
@@ -1374,7 +1370,7 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
         int_cell_to_f64(RG, RH, RT, vg1, vh1, vh3, &cs[2 * b], &cs[2 * b + 1]);
       else
         int_cell_to_f64(LG_, LH, LT, vg1, vh1, vh3, &cs[2 * b], &cs[2 * b + 1]);
-      if constexpr (derive) {
+      {
         // the larger child's cells, or the parent's when the larger is materialised
         if (lg_mat)
           int_cell_to_f64(PG, PH, PT, vg1, vh1, vh3, &cp[2 * b], &cp[2 * b + 1]);
@@ -1394,44 +1390,21 @@ __global__ __launch_bounds__(SCAN_THREADS, 6) void k_pair_scan(DevLearner L, int
     }
     return;
   }
-  double* s_sm = L.slots + (size_t)sm * sl + ft.slot_off;
   double* s_lg = L.slots + (size_t)lg * sl + ft.slot_off;
-  if constexpr (derive) {
-    fix_compact_pair(ft, cs, cp, ss.sg, ss.sh, pgate || sm_zero, pm, !lg_mat);
-    if (lg_mat) {
-      // larger = parent - smaller cell by cell, kept in the node's f64 slot
-      for (int i = tid; i < 2 * nb; i += SCAN_THREADS) {
-        const double d = (pmat ? s_par[i] : cp[i]) - cs[i];
-        cp[i] = d;
-        s_lg[i] = d;
-      }
-    }
-    __syncthreads();
-    const int mfb = (int)ft.mfb, tm = mfb - ft.offset;
-    if (tid == 0 && mfb > 0 && mfb < nb && tm >= 0) {
-      L.mfbv[(size_t)sm * F + f] = make_double2(cs[2 * tm], cs[2 * tm + 1]);
-      L.mfbv[(size_t)lg * F + f] = make_double2(cp[2 * tm], cp[2 * tm + 1]);
-    }
-  } else {
-    fix_compact_block(ft, cs, ss.sg, ss.sh, pgate || sm_zero);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = tid + SCAN_THREADS * k;
-      if (i >= 2 * nb) continue;
-      const double v = cs[i];
-      const double d = pv[k] - v;
+  fix_compact_pair(ft, cs, cp, ss.sg, ss.sh, pgate || sm_zero, pm, !lg_mat);
+  if (lg_mat) {
+    // larger = parent - smaller cell by cell, kept in the node's f64 slot
+    for (int i = tid; i < 2 * nb; i += SCAN_THREADS) {
+      const double d = (pmat ? s_par[i] : cp[i]) - cs[i];
       cp[i] = d;
-      s_sm[i] = v;
       s_lg[i] = d;
     }
-    for (int i = tid + 4 * SCAN_THREADS; i < 2 * nb; i += SCAN_THREADS) {  // past 256 bins
-      const double v = cs[i];
-      const double d = s_par[i] - v;
-      cp[i] = d;
-      s_sm[i] = v;
-      s_lg[i] = d;
-    }
-    __syncthreads();
+  }
+  __syncthreads();
+  const int mfb = (int)ft.mfb, tm = mfb - ft.offset;
+  if (tid == 0 && mfb > 0 && mfb < nb && tm >= 0) {
+    L.mfbv[(size_t)sm * F + f] = make_double2(cs[2 * tm], cs[2 * tm + 1]);
+    L.mfbv[(size_t)lg * F + f] = make_double2(cp[2 * tm], cp[2 * tm + 1]);
   }
   const int wv = tid >> 6;
   const int32_t leaf = wv == 0 ? sm : lg;

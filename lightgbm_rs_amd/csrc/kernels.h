@@ -135,10 +135,10 @@ struct DevLearner {
   int32_t n_fgroups;          // feature groups of k_hist_f32 (cells of a group fit LDS)
   int32_t fgroup_first[MAX_FGROUPS + 1];
   int32_t* int_slots;         // [slot_cap][total_cells][3] per-node integer histograms
-  double* slots;              // [slot_cap][slot_len] per-node f64 histograms (f32 mode,
-                              // and quantized nodes with fmat set)
-  // Quantized gradients: a node's f64 cells are its integer cells through
-  // int_cell_to_f64, except the cell FixHistogram writes (its f64 pair in mfbv); a
+  double* slots;              // [slot_cap][slot_len] per-node f64 histograms (nodes with
+                              // fmat set, and the root)
+  // A node's f64 cells are its integer cells converted (int_cell_to_f64, or the
+  // fixed-point scale), except the cell FixHistogram writes (its f64 pair in mfbv); a
   // node whose cells cannot be derived that way (fmat = 1) holds them in `slots`.
   double2* mfbv;              // [slot_cap][F] the fixed most-frequent-bin cell
   int32_t* fmat;              // [slot_cap] 1: the node's f64 cells are in `slots`

@@ -871,8 +871,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_fixscan(DevLearner L, int32_t 
     return;
   }
   for (int i = tid; i < 2 * nb; i += SCAN_THREADS) L.slots[ft.slot_off + i] = cs[i];
-  if (!fp && tid == 0) {
-    // quantized: the root's fixed cell (its other f64 cells are its integer cells)
+  if (tid == 0) {
+    // the root's fixed cell (its other f64 cells are its integer cells)
     const int mfb = (int)ft.mfb, tm = mfb - ft.offset;
     if (mfb > 0 && mfb < nb && tm >= 0) L.mfbv[f] = make_double2(cs[2 * tm], cs[2 * tm + 1]);
   }

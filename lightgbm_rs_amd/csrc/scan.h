@@ -814,13 +814,14 @@ __device__ __forceinline__ void fix_compact_block(const DevFeature& ft, double* 
   __syncthreads();
 }
 
-// The same for both children of a quantized split.  `cs` holds the smaller child's
-// cells (fixed with its sums as above, or cleared by `zero`), `cp` the larger child's
-// (or the parent's) cells from integers.  The reference's larger child is
-// parent - smaller cell by cell, never re-fixed: integer-derived cells subtract
-// exactly, so only its most-frequent-bin cell differs from its integers: the parent's
-// fixed pair `pm` minus the smaller's fixed cell (`sub`), or `pm` itself (`cp` then
-// holds the parent, from which the caller subtracts).  Both arrays are compacted.
+// The same for both children of a split.  `cs` holds the smaller child's cells
+// (fixed with its sums as above, or cleared by `zero`), `cp` the larger child's (or
+// the parent's) cells from integers.  The reference's larger child is parent - smaller
+// cell by cell, never re-fixed: quantized integer-derived cells subtract exactly (f32
+// fixed-point ones within one rounding), so only its most-frequent-bin cell differs
+// from its integers: the parent's fixed pair `pm` minus the smaller's fixed cell
+// (`sub`), or `pm` itself (`cp` then holds the parent, from which the caller
+// subtracts).  Both arrays are compacted.
 __device__ __forceinline__ void fix_compact_pair(const DevFeature& ft, double* cs, double* cp,
                                                  double sg, double sh, bool zero, double2 pm,
                                                  bool sub) {
