@@ -131,7 +131,41 @@ __global__ __launch_bounds__(WIDE_THREADS) void k_hist_wide(DevLearner L) {
     ghq = buf_sel(L.bufs.gh, J.buf) + jb;
   const double gm = FP ? ldexp(1.0, ctl->g_shift) : 0.0, hm = FP ? ldexp(1.0, ctl->h_shift) : 0.0;
   long long tg = 0, th = 0, t3 = 0;
-  if constexpr (!FP && !B16) {
+  if (FP && !B16 && orig && L.bincol) {
+    // f32 root build: rows in their original order, so each feature's bytes of a
+    // wave's rows are 64 consecutive bytes of the feature-major copy; a group of 32
+    // features is half of each row's 64-byte sector of binmat, which every group
+    // would fetch whole
+    const uint8_t* __restrict__ colbase = L.bincol + (size_t)f0 * (size_t)L.N;
+    const size_t cstride = (size_t)L.N;
+    for (int64_t b0 = lo; b0 < hi; b0 += (int64_t)WIDE_THREADS) {
+      const int64_t r = b0 + tid;
+      if (r >= hi) continue;
+      const int64_t src_row = jb + r;
+      const float2 v = gh32[r];
+      const long long gi = (long long)rint((double)v.x * gm);
+      const long long hi_ = (long long)rint((double)v.y * hm);
+      tg += gi;
+      th += hi_;
+      for (int k0 = 0; k0 < GF; k0 += 8) {  // eight features' bytes in flight
+        uint32_t bins[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          bins[k] = k0 + k < nfeat ? colbase[(size_t)(k0 + k) * cstride + src_row] : 0u;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t fd = __builtin_amdgcn_readfirstlane(s_fd[k0 + k]);
+          if (bins[k] != (fd & 0xffu)) {
+            const int c = (int)(fd >> 8) + (int)bins[k];
+            __hip_atomic_fetch_add(&lds[2 * c], (unsigned long long)gi, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_add(&lds[2 * c + 1], (unsigned long long)hi_, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
+        }
+      }
+    }
+  } else if constexpr (!FP && !B16) {
     // Quantized 1-byte bins: a row whose pair quantized to (0, 0) adds nothing (there
     // is no count field), and with 4 quantization bins that is most rows of a ranking
     // objective.  Each wave queues its live rows (source row, pair) in an LDS ring and
