@@ -154,6 +154,7 @@ struct lgbm_hip_ctx {
   int64_t N = 0;
   int32_t F = 0, fmt = 1, total_cells = 0;  // fmt: row record format (lgbm_device.h)
   int32_t records_env = 0;  // LGBM_HIP_RECORDS: 0 automatic, 1 legacy (8-bit records), 2 wide
+  bool no_bincol = false;   // LGBM_HIP_BINCOL=0: the wide layout without its feature-major copy
   int32_t max_bins = 0;     // the widest feature's num_bin
   int32_t has_cat = 0;      // some feature is categorical
   bool bin16 = false;       // wide layout with 2-byte bins
@@ -1157,8 +1158,9 @@ int resident_setup(lgbm_hip_ctx* c, int32_t F_in, int64_t num_data, const lgbm_f
     // the feature-major copy is optional: without it the router reads binmat rows
     if (c->bincol) (void)hipFree(c->bincol);
     c->bincol = nullptr;
-    if (hipMalloc((void**)&c->bincol, (size_t)num_data * (size_t)F * (bin16 ? 2 : 1)) !=
-        hipSuccess) {
+    if (c->no_bincol ||
+        hipMalloc((void**)&c->bincol, (size_t)num_data * (size_t)F * (bin16 ? 2 : 1)) !=
+            hipSuccess) {
       c->bincol = nullptr;
       (void)hipGetLastError();
     }
@@ -1334,6 +1336,7 @@ int lgbm_hip_ctx_create(int device, lgbm_hip_ctx** out) {
   }
   if (const char* e = std::getenv("LGBM_HIP_SPEC"))
     c->spec_max = std::max(1, std::min(SPEC_MAX, std::atoi(e)));
+  if (const char* e = std::getenv("LGBM_HIP_BINCOL")) c->no_bincol = std::strcmp(e, "0") == 0;
   *out = c;
   return LGBM_HIP_OK;
 }

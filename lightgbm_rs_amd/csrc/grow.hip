@@ -272,6 +272,60 @@ __global__ __launch_bounds__(PLAN_THREADS) void k_plan(DevLearner L, int32_t slo
   __syncthreads();
 
   // ---- 1. per-slot feature ArgMax -------------------------------------------
+  if (nred > 0 && nred * 2 <= PLAN_WAVES) {
+    // few slots (the late rounds): W waves a slot, each over every W-th 64-feature
+    // chunk, then the slot's first wave combines their keys (one load round trip per
+    // wave instead of F / 512)
+    __shared__ double s_bkg[PLAN_WAVES];
+    __shared__ int32_t s_bkf[PLAN_WAVES], s_bki[PLAN_WAVES];
+    int W = 2;
+    while (W * 2 * nred <= PLAN_WAVES) W *= 2;
+    const int i = wave / W, part = wave - i * W;
+    BestKey k{ninf, -1, INT_MAX32};
+    if (i < nred) {
+      const int32_t s = s_red[i];
+      constexpr int KU = 4;
+      for (int f0 = part * LGBM_WAVE + lane; f0 < F; f0 += KU * W * LGBM_WAVE) {
+        double gv[KU];
+        int32_t rv[KU];
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+          const int f = f0 + u * W * LGBM_WAVE;
+          gv[u] = f < F ? L.gain_dense[(size_t)s * F + f] : ninf;
+          rv[u] = f < F ? (ft_lds ? fts[f].real_index : s_ri[f]) : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+          const BestKey c{gv[u], rv[u], f0 + u * W * LGBM_WAVE};
+          if (gv[u] > ninf && key_better(c, k)) k = c;
+        }
+      }
+      k = wave_best_fast(k);
+    }
+    if (lane == 0) {
+      s_bkg[wave] = k.gain;
+      s_bkf[wave] = k.feat;
+      s_bki[wave] = k.idx;
+    }
+    __syncthreads();
+    if (i < nred && part == 0) {
+      BestKey c{ninf, -1, INT_MAX32};
+      if (lane < W) c = BestKey{s_bkg[wave + lane], s_bkf[wave + lane], s_bki[wave + lane]};
+      c = wave_best_fast(c);
+      const int32_t s = s_red[i];
+      const bool have = c.idx != INT_MAX32 && c.gain > ninf;
+      if (lane == 0) {
+        const double kg = have ? c.gain : ninf;
+        const int32_t kf = have ? c.feat : -1, kp = have ? c.idx : -1;
+        nd.key_gain[s] = kg;
+        nd.key_feat[s] = kf;
+        L.best_fpos[s] = kp;
+        s_gain[s] = kg;
+        s_feat[s] = kf;
+        s_fpos[s] = kp;
+      }
+    }
+  } else
   for (int i = wave; i < nred; i += PLAN_WAVES) {
     const int32_t s = s_red[i];
     BestKey k{ninf, -1, INT_MAX32};

@@ -252,3 +252,32 @@ def test_wide_forced_categorical_multiclass_matches_oracle():
             a, c = np.ascontiguousarray(t[k]), np.ascontiguousarray(o[k])
             assert a.shape == c.shape and a.tobytes() == c.tobytes(), (i, k)
     assert np.array_equal(bits(scores), bits(oscores))
+
+
+def _train_env(env, bins, meta, ub, y, nl, iters, qbins):
+    """train() with extra environment switches read at context creation."""
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return train(bins, meta, ub, y, nl, iters, qbins)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("qbins", [4, 0])
+def test_wide_without_feature_major_copy_matches(qbins):
+    """The wide layout routes partitions (and builds an f32 root histogram) from its
+    feature-major copy of the bins when that copy fits; without it (LGBM_HIP_BINCOL=0,
+    as when the allocation fails) the router reads the row's binmat byte.  Both give
+    the same trees and scores, bit for bit."""
+    n, F, iters, nl = 50_000, 300, 2, 63
+    say(f"wide F={F} n={n} qbins={qbins} with and without the feature-major copy")
+    X, y, bins, meta, ub, ms = _wide_data(n, F, 37)
+    ta, sa, _ = train(bins, meta, ub, y, nl, iters, qbins)
+    tb, sb, _ = _train_env({"LGBM_HIP_BINCOL": "0"}, bins, meta, ub, y, nl, iters, qbins)
+    assert_same_trees(ta, tb, "bincol vs binmat router")
+    assert np.array_equal(bits(sa), bits(sb))
