@@ -18,10 +18,11 @@ restatement of the reference learner (oracle/) on a bounded sample of the same
 workload and bins (all cores and one thread), and `parity` compares the device's
 first iterations with that run's trees and scores, bit for bit.
 
-`--workload config2|config4` instead times BASELINE.json configs[2] (1M x 2000 sparse
-LogNormal features, L2 regression, f32 gradients, feature_fraction 0.8, 127 leaves)
-or configs[4] (2M x 700, lambdarank over query groups, quantized, 255 leaves) on the
-wide row layout, as a secondary line with the roofline of its dominant kernel
+`--workload config2|config3|config4` instead times BASELINE.json configs[2] (1M x 2000
+sparse LogNormal features, L2 regression, f32 gradients, feature_fraction 0.8, 127
+leaves), configs[3] (2M x 100 with 20 categorical features, softmax over 10 classes:
+10 trees per iteration, f32 gradients, 127 leaves) or configs[4] (2M x 700,
+lambdarank over query groups, quantized, 255 leaves) on the wide row layout, as a secondary line with the roofline of its dominant kernel
 (k_hist_wide) and the CPU restatement timed on its first iteration; the default
 `config1` is the headline above.
 """
@@ -138,14 +139,26 @@ def compare_iterations(trees, scores, otrees, oscores, init):
 
 
 def secondary(args):
-    """the wide row layout's paths (column sampling and L2
-    regression with f32 gradients; lambdarank with quantized gradients)."""
+    """configs[2] / [3] / [4]: the wide row layout's paths (column sampling and L2
+    regression with f32 gradients; softmax over 10 classes with categorical splits and
+    f32 gradients; lambdarank with quantized gradients)."""
     import numpy as np
-    from lightgbm_rs_amd import GainConfig, HipBackend, boost_from_score
-    from lightgbm_rs_amd.synth import config2_raw_host, config4_raw_host, sample_mappers
+    from lightgbm_rs_amd import GainConfig, HipBackend, boost_from_score, feature_meta
+    from lightgbm_rs_amd.synth import (config2_raw_host, config3_mappers, config3_raw_host,
+                                       config4_raw_host, sample_mappers)
 
     t0 = time.perf_counter()
-    if args.workload == "config2":
+    K, cat = 1, []  # trees per iteration, categorical features
+    if args.workload == "config3":
+        n, K = 2_000_000, 10
+        X, y, cat = config3_raw_host(n, num_class=K)
+        F = X.shape[0]
+        obj, nl, ff, qbins, qb = "multiclass", 127, 1.0, 0, None
+        workload = ("configs[3]: softmax, 10 classes, 2M rows x 100 features (80 N(0,1), "
+                    "20 categorical of 32 levels), max_bin 255, num_leaves 127, categorical "
+                    "splits, f32 gradients, one step = one iteration = 10 trees")
+        dtype = "f32 grad/hess, 64-bit fixed-point histogram, f64 split math"
+    elif args.workload == "config2":
         n, F = 1_000_000, 2000
         X, y = config2_raw_host(n, F=F)
         obj, nl, ff, qbins, qb = "regression", 127, 0.8, 0, None
@@ -160,10 +173,24 @@ def secondary(args):
         workload = ("configs[4]: lambdarank, 2M rows x 700 features in query groups, "
                     "max_bin 255, num_leaves 255, quantized int8 grads (4 bins, stochastic)")
         dtype = "int8 grad/hess, int32 histogram, f64 split math"
-    mappers = sample_mappers(X, 255)
+    if cat:
+        mappers, meta, ub = config3_mappers(X, cat)
+    else:
+        mappers = sample_mappers(X, 255)
+        meta = [feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f)
+                for f, m in enumerate(mappers)]
+        ub = np.concatenate([m.upper_bounds for m in mappers])
     log(f"{args.workload}: data + mappers {time.perf_counter() - t0:.1f}s")
-    init = boost_from_score(obj, y)
-    init = init if abs(init) > 1e-15 else 0.0
+    if K > 1:  # BoostFromAverage per class (gbdt.rs:691-1373), classes that need trees
+        k_eps = float(np.float32(1e-15))
+        prior = np.bincount(y.astype(np.int64), minlength=K) / n
+        init_k = np.log(np.maximum(prior, k_eps))
+        init_k = np.where(np.abs(init_k) > k_eps, init_k, 0.0)
+        need = [0 if (p <= k_eps or p >= 1.0 - k_eps) else 1 for p in prior]
+        init = 0.0
+    else:
+        init = boost_from_score(obj, y)
+        init = init if abs(init) > 1e-15 else 0.0
     cfg = GainConfig.make(min_data_in_leaf=20)
     be = HipBackend(0)
     be.upload_raw(X, mappers, col_major=True)
@@ -172,6 +199,9 @@ def secondary(args):
     bins = be.get_bins() if cpu_iters > 0 else None  # the CPU baseline's input
 
     def start():
+        if K > 1:
+            be.set_labels_multiclass(y, K, init_k)
+            return
         be.set_labels(y, init)
         if obj == "lambdarank":
             be.set_lambdarank(qb)
@@ -180,26 +210,51 @@ def secondary(args):
         if ff < 1.0:
             be.set_col_sampler(ff, 1.0, 2)
 
+    def step(i):  # one boosting iteration: its K trees, read back
+        if K > 1:
+            return be.train_iter_multiclass(i, cfg, nl, -1, 0.1, qbins, True, need)
+        return [be.train_iter(i, cfg, nl, -1, 0.1, qbins, True)]
+
+    # configs[3] times its first iterations from a fresh score (at most 10 = 100 trees):
+    # the reference's categorical child seeding (learner.rs:4191-4229, kept bit for bit)
+    # hands a child its sibling's sums whenever the SplitInfo and partition counts order
+    # the two differently, which on this data drives the softmax scores to saturation and
+    # a class's root sum_hessian to 0 (InvalidLeafHessian, learner.rs:1331-1334) after
+    # about 14 iterations, in the CPU restatement as on the device
+    steps = min(args.steps, 10) if K > 1 else args.steps
+    first = 0 if K > 1 else args.warmup
     start()
     for i in range(max(args.warmup, 1)):
-        be.train_iter(i, cfg, nl, -1, 0.1, qbins, True)
+        step(i)
+    if K > 1:
+        start()
     t1 = time.perf_counter()
-    for i in range(args.warmup, args.warmup + args.steps):
-        be.train_iter(i, cfg, nl, -1, 0.1, qbins, True)
+    for i in range(first, first + steps):
+        step(i)
     elapsed = time.perf_counter() - t1
+    if K > 1:
+        start()
     be.set_timing(True)
-    for i in range(args.warmup + args.steps, args.warmup + args.steps + max(args.prof_steps, 1)):
-        be.train_iter(i, cfg, nl, -1, 0.1, qbins, True)
+    p0 = 0 if K > 1 else first + steps
+    for i in range(p0, p0 + max(args.prof_steps, 1)):
+        step(i)
     tm = be.timing()
     be.set_timing(False)
     gpu_first = None
     if cpu_iters > 0:  # the parity leg's device iterations, from a fresh start
         start()
-        gpu_first = [be.train_iter(i, cfg, nl, -1, 0.1, qbins, True) for i in range(cpu_iters)]
+        gpu_first = [t for i in range(cpu_iters) for t in step(i)]
         gpu_scores = be.scores()
+        if K > 1:  # the first iteration's trees carry the class's init (add_bias)
+            z = float(np.float32(1e-35))
+            for k, t in enumerate(gpu_first[:K]):
+                if abs(init_k[k]) > 0.0 and t["num_leaves"] > 1:
+                    for key in ("leaf_value", "internal_value"):
+                        v = t[key] + init_k[k]
+                        t[key] = np.where((v >= -z) & (v <= z), 0.0, v)
     be.close()
     ps = max(args.prof_steps, 1)
-    ms = elapsed / args.steps * 1e3
+    ms = elapsed / steps * 1e3
     # k_hist_wide, the dominant kernel: the survey's algorithmic bytes, u8 bins (F per
     # row), the pair (2 B quantized, 8 B f32) and the row index of a child build
     w_gh = 2 if qbins else 8
@@ -211,27 +266,29 @@ def secondary(args):
     cpu, parity = None, None
     if cpu_iters > 0:
         from oracle import oracle
-        from lightgbm_rs_amd import feature_meta
-        meta = [feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f)
-                for f, m in enumerate(mappers)]
-        ub = np.concatenate([m.upper_bounds for m in mappers])
         env_threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
         threads = oracle.set_threads(args.cpu_threads or env_threads or len(os.sched_getaffinity(0)))
         okind = oracle.OBJECTIVE_LAMBDARANK if obj == "lambdarank" else oracle.OBJECTIVE_REGRESSION
         tc = time.perf_counter()
-        oscores, otrees = oracle.train(bins, meta, ub, y, cfg, okind, nl, -1, cpu_iters, 0.1,
-                                       quantized=qbins > 0, feature_fraction=ff,
-                                       feature_fraction_seed=2, query_boundaries=qb)
+        if K > 1:
+            oscores, otrees = oracle.train_multiclass(bins, meta, ub, y, K, cfg, nl, -1,
+                                                      cpu_iters, 0.1)
+        else:
+            oscores, otrees = oracle.train(bins, meta, ub, y, cfg, okind, nl, -1, cpu_iters,
+                                           0.1, quantized=qbins > 0, feature_fraction=ff,
+                                           feature_fraction_seed=2, query_boundaries=qb)
         cs = time.perf_counter() - tc
         log(f"cpu: {cs:.1f}s for {cpu_iters} iteration(s) on {threads} threads")
         model_name, phys = cpu_info()
-        cpu = {"value": round(cs / cpu_iters * 100.0, 3), "unit": "s/100 trees", "cores": threads,
+        cpu = {"value": round(cs / (cpu_iters * K) * 100.0, 3), "unit": "s/100 trees",
+               "cores": threads,
                "kind": "port",
-               "sample": f"the first {cpu_iters} boosting iteration(s) of the same workload and "
+               "sample": f"the first {cpu_iters} boosting iteration(s) ({cpu_iters * K} trees) "
+                         f"of the same workload and "
                          f"bins (C++ restatement of the reference CpuBackend learner, OpenMP, "
                          f"{threads} threads: {cs:.1f}s), scaled to 100 trees",
                "cpu_model": model_name, "physical_cores": phys,
-               "gpu_speedup": round((cs / cpu_iters) / (elapsed / args.steps), 1)}
+               "gpu_speedup": round((cs / cpu_iters) / (elapsed / steps), 1)}
         parity = compare_iterations(gpu_first, gpu_scores, otrees, oscores, init)
         if not qbins:  # f32 gradients: fixed-point cells vs the f64 fold (stated bar 1e-5)
             parity["scores_max_rel_diff"] = float(
@@ -242,13 +299,14 @@ def secondary(args):
         log(f"parity: {parity}")
     print(json.dumps({
         "metric": f"sec per 100 trees, {args.workload} (wide row layout), 1 MI355X",
-        "value": round(ms / 10.0, 4), "unit": "s/100 trees", "n_gpus": 1, "steps": args.steps,
+        "value": round(ms / K / 10.0, 4), "unit": "s/100 trees", "n_gpus": 1, "steps": steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (BASELINE.json recipe), binned by the library's BinMapper",
         "config": {"workload": workload, "rows": n, "features": F, "num_leaves": nl},
         "phase_ms_per_step": {k: round(v / ps, 4) for k, v in tm.items()
                               if k.endswith("_ms")},
+        "trees_per_step": K,
         "rounds_per_tree": round(tm["rounds"] / max(tm["trees"], 1.0), 1),
         "roofline": {"bound": "hbm", "achieved": round(hist_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(hist_gbs / HBM_PEAK_GBS, 4), "traffic": None,
@@ -317,8 +375,10 @@ def main():
                          "of all is reported beside it")
     ap.add_argument("--prof-steps", type=int, default=3,
                     help="extra iterations timed per kernel with HIP events")
-    ap.add_argument("--workload", default="config1", choices=["config1", "config2", "config4"],
-                    help="config1: the headline; config2 / config4: a secondary wide-layout line")
+    ap.add_argument("--workload", default="config1",
+                    choices=["config1", "config2", "config3", "config4"],
+                    help="config1: the headline; config2 / config3 / config4: a secondary "
+                         "wide-layout line")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB device-to-device "
                          "(3 times): the known-size kernel that scales rocprofv3 "

@@ -169,15 +169,15 @@ def config3_raw_host(n, seed=0x5EED0003, num_class=10, n_num=80, n_cat=20, level
     return X, y, list(range(n_num, F))
 
 
-def config3_binned(n, seed=0x5EED0003, max_bin=255, min_data_in_leaf=20, **kw):
-    """configs[3] binned: (bins u8 [F, n], feature meta, per-bin values (numerical upper
-    bounds, categorical category codes), labels, categorical positions, raw X)."""
+def config3_mappers(X, cat, max_bin=255, min_data_in_leaf=20):
+    """configs[3]'s mappers for X [F, n]: categorical features binned whole
+    (find_bin_categorical), numerical ones from find_bin_from_column's 200000-row
+    sample.  Returns (mappers, feature meta, per-bin values: numerical upper bounds,
+    categorical category codes)."""
     from .backend import feature_meta
     from .binning import BinMapper, sample_indices
-    X, y, cat = config3_raw_host(n, seed, **kw)
-    F = X.shape[0]
+    F, n = X.shape
     idx = sample_indices(n, 200000, 1)
-    bins = np.zeros((F, n), dtype=np.uint8)
     meta, vals, mappers = [], [], []
     for f in range(F):
         if f in cat:
@@ -188,11 +188,21 @@ def config3_binned(n, seed=0x5EED0003, max_bin=255, min_data_in_leaf=20, **kw):
             m = BinMapper.from_sampled_column(X[f, idx].astype(np.float64), n, max_bin=max_bin,
                                               min_data_in_leaf=min_data_in_leaf)
             vals.extend(m.upper_bounds.tolist())
-        bins[f] = m.value_to_bin(X[f]).astype(np.uint8)
         meta.append(feature_meta(m.num_bin, m.most_freq_bin, m.missing_type, m.default_bin, f,
                                  bin_type=m.bin_type))
         mappers.append(m)
-    return bins, meta, np.array(vals, dtype=np.float64), y, cat, X, mappers
+    return mappers, meta, np.array(vals, dtype=np.float64)
+
+
+def config3_binned(n, seed=0x5EED0003, max_bin=255, min_data_in_leaf=20, **kw):
+    """configs[3] binned: (bins u8 [F, n], feature meta, per-bin values (numerical upper
+    bounds, categorical category codes), labels, categorical positions, raw X)."""
+    X, y, cat = config3_raw_host(n, seed, **kw)
+    mappers, meta, vals = config3_mappers(X, cat, max_bin, min_data_in_leaf)
+    bins = np.zeros(X.shape, dtype=np.uint8)
+    for f, m in enumerate(mappers):
+        bins[f] = m.value_to_bin(X[f]).astype(np.uint8)
+    return bins, meta, vals, y, cat, X, mappers
 
 
 def _bin_columns(X, max_bin, min_data_in_leaf=20):
