@@ -730,22 +730,60 @@ void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth, int32_
   enqueue_rounds(c, rounds, fp);
 }
 
-// The round count of the next trees' captured sequence: the 75th percentile of the
-// rounds the last trees used (ROUND_HIST of them).  The rounds a tree needs follow the
-// training (more in later iterations) and vary from tree to tree; a round past the
-// tree's end costs a near-empty plan / partition / scan, a tree that needs more runs
-// the tail sequence after one host check.
+// The round count of the next trees' captured sequence, from the rounds the last trees
+// used (ROUND_HIST of them).  The rounds a tree needs follow the training (more in
+// later iterations) and vary from tree to tree (widely across the classes of a
+// softmax iteration).  A round past the tree's end costs a near-empty plan /
+// partition / scan; a tree that needs more runs a tail sequence of TAIL_ROUNDS after
+// one host check, which costs about as much.  ROUND_POLICY 1 takes the multiple of
+// ROUND_QUANT that minimises (empty rounds + ROUND_W_TAIL x tail checks) over the
+// history; the multiples bound the distinct captured sequences (each a graph
+// instantiation).  ROUND_POLICY 0: the 75th percentile.
+#ifndef ROUND_POLICY
+#define ROUND_POLICY 1
+#endif
+#ifndef ROUND_QUANT
+#define ROUND_QUANT 8
+#endif
+#ifndef ROUND_W_TAIL
+#define ROUND_W_TAIL 1
+#endif
 void update_round_cap(lgbm_hip_ctx* c, int32_t used, int32_t num_leaves) {
   constexpr int H = lgbm_hip_ctx::ROUND_HIST;
   c->round_hist[c->round_hist_n % H] = used;
   c->round_hist_n += 1;
   if (c->round_fixed) return;
   const int n = std::min(c->round_hist_n, H);
+  const int32_t top = num_leaves + 1;  // no tree needs more rounds than this
+#if ROUND_POLICY == 1
+  constexpr int32_t T = lgbm_hip_ctx::TAIL_ROUNDS;
+  int32_t best = top;
+  int64_t best_cost = INT64_MAX;
+  for (int32_t q = ROUND_QUANT; q < top + ROUND_QUANT; q += ROUND_QUANT) {
+    const int32_t cap = std::min(q, top);
+    int64_t cost = 0;
+    for (int i = 0; i < n; ++i) {
+      const int32_t r = c->round_hist[i];
+      if (r <= cap) {
+        cost += cap - r;
+      } else {
+        const int32_t tails = (r - cap + T - 1) / T;
+        cost += (int64_t)tails * T - (r - cap) + (int64_t)ROUND_W_TAIL * tails;
+      }
+    }
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = cap;
+    }
+  }
+  c->round_cap = std::max(1, best);
+#else
   int32_t v[H];
   std::copy(c->round_hist, c->round_hist + n, v);
   std::sort(v, v + n);
   const int q = (3 * n + 3) / 4 - 1;  // ceil(0.75 n) - 1
-  c->round_cap = std::max(1, std::min(num_leaves + 1, v[q]));
+  c->round_cap = std::max(1, std::min(top, v[q]));
+#endif
 }
 
 // The tail sequence: TAIL_ROUNDS more rounds (captured once per tree shape), else the
