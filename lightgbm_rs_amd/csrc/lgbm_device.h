@@ -225,6 +225,7 @@ struct PartJob {
 
 #define SPEC_MAX 32        // partition jobs per round
 #define SPEC_DEFAULT 8
+#define SPEC_SCAN_HEAVY 4  // speculation width where one job's scans are costly (PLAN_CAP_WORK)
 
 // A histogram job: a physical row range of one row buffer.  nblk partial slots from
 // a0 hold its histogram after k_hist_jobs.
