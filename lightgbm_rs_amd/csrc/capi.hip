@@ -736,13 +736,11 @@ void enqueue_tree(lgbm_hip_ctx* c, int32_t num_leaves, int32_t max_depth, int32_
 // later iterations) and vary from tree to tree (widely across the classes of a
 // softmax iteration).  A round past the tree's end costs a near-empty plan /
 // partition / scan; a tree that needs more runs a tail sequence of TAIL_ROUNDS after
-// one host check, which costs about as much.  ROUND_POLICY 1 takes the multiple of
+// one host check, which costs about as much.  The count is the multiple of
 // ROUND_QUANT that minimises (empty rounds + ROUND_W_TAIL x tail checks) over the
 // history; the multiples bound the distinct captured sequences (each a graph
-// instantiation).  ROUND_POLICY 0: the 75th percentile.
-#ifndef ROUND_POLICY
-#define ROUND_POLICY 1
-#endif
+// instantiation).  (The 75th percentile of the history carried too many empty rounds
+// where the trees' round counts spread.)
 #ifndef ROUND_QUANT
 #define ROUND_QUANT 8
 #endif
@@ -756,7 +754,6 @@ void update_round_cap(lgbm_hip_ctx* c, int32_t used, int32_t num_leaves) {
   if (c->round_fixed) return;
   const int n = std::min(c->round_hist_n, H);
   const int32_t top = num_leaves + 1;  // no tree needs more rounds than this
-#if ROUND_POLICY == 1
   constexpr int32_t T = lgbm_hip_ctx::TAIL_ROUNDS;
   int32_t best = top;
   int64_t best_cost = INT64_MAX;
@@ -778,13 +775,6 @@ void update_round_cap(lgbm_hip_ctx* c, int32_t used, int32_t num_leaves) {
     }
   }
   c->round_cap = std::max(1, best);
-#else
-  int32_t v[H];
-  std::copy(c->round_hist, c->round_hist + n, v);
-  std::sort(v, v + n);
-  const int q = (3 * n + 3) / 4 - 1;  // ceil(0.75 n) - 1
-  c->round_cap = std::max(1, std::min(top, v[q]));
-#endif
 }
 
 // The tail sequence: TAIL_ROUNDS more rounds (captured once per tree shape), else the
